@@ -1,0 +1,82 @@
+"""Writes the golden fixtures of tests/golden/ from the reference's own kernel code.
+
+Run in a checkout where the reference tree is mounted (it is absent on the GPU box):
+    make -C oracle ref && python tests/golden/make_vectors.py
+The inputs are SplitMix64 normals (candle-core/src/accel/turbo.rs:150-176, the generator of
+the reference's own tests); the outputs come from oracle/_ref/accel_host_test, i.e. the
+reference's tq_quant / tq_attn / tq_combine kernels run on its host emulator. The reference's
+test candle-core/tests/accel_kernels_host.rs:960-1070 asserts that this tq_quant is bit-exact
+with the CPU codec RowCodec::quantize_row for the FP8 / MX formats.
+"""
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+
+from oracle import oracle as O  # noqa: E402
+from tests.golden import ref_harness as H  # noqa: E402
+
+
+def quant_case(name, mode, bits, d, rows, seed):
+    l = O.row_layout(mode, bits, d)
+    x = O.normal(seed, (rows, d)) * np.float32(2.0)
+    x[0, 3] = 0.0
+    x[1, :] = 0.0  # an all-zero row
+    x[2, 5] = 40.0  # an outlier
+    x[3, :32] = 1e-30  # a subnormal-scale block
+    if mode == O.TURBO_MSE:
+        c, b = O.lloyd_max(d, bits)
+        tab = H.tq_tab(c, b)
+    else:
+        tab = H.tq_tab()
+    got = H.tq_quant(x.astype(np.float32), mode, l.code_bits, l.code_words, l.aux_words,
+                     l.row_words, tab)
+    np.savez_compressed(os.path.join(HERE, f"ref_quant_{name}.npz"), x=x, rows=got,
+                        mode=mode, bits=bits, d=d)
+    print(name, got.shape)
+
+
+def attn_case():
+    # GQA pack G = 4 FP8 rows (the decode path of BASELINE config 2 at a small size)
+    B, Hq, Hkv, D, Lk = 2, 8, 2, 64, 200
+    q = O.normal(101, (B, Hq, 1, D))
+    k = O.normal(102, (B, Hkv, Lk, D))
+    v = O.normal(103, (B, Hkv, Lk, D))
+    kd = O.quantize_rows(O.FP8, 0, k)
+    vd = O.quantize_rows(O.FP8, 0, v)
+    l = O.row_layout(O.FP8, 0, D)
+    side = (O.FP8, 8, l.code_words, l.code_words + l.aux_words)
+    tab = np.zeros(64, dtype=np.float32)
+    out = H.tq_attn(q, kd, vd, side, side, tab, 0.125, splits=4, group=4, fp8=True)
+    np.savez_compressed(os.path.join(HERE, "ref_attn_fp8.npz"), q=q, kd=kd, vd=vd, out=out,
+                        scale=0.125)
+    print("attn", out.shape)
+
+
+def combine_case():
+    splits, rows, d = 5, 7, 32
+    po = O.normal(201, (splits, rows, d))
+    pl = O.normal(202, (splits, rows)) * np.float32(3.0)
+    pl[1, 2] = -np.inf
+    pl[:, 4] = -np.inf  # a row without keys
+    t = H.combine(po, pl)
+    np.savez_compressed(os.path.join(HERE, "ref_combine.npz"), part_o=po, part_lse=pl, o=t)
+    print("combine", t.shape)
+
+
+if __name__ == "__main__":
+    if not H.available():
+        sys.exit("oracle/_ref/accel_host_test missing: run `make -C oracle ref` first")
+    quant_case("fp8_d128", O.FP8, 0, 128, 37, 11)
+    quant_case("fp8_d80", O.FP8, 0, 80, 19, 12)
+    quant_case("mxfp4_d128", O.MXFP4, 0, 128, 37, 13)
+    quant_case("mxfp4_d64", O.MXFP4, 0, 64, 19, 14)
+    quant_case("turbo4_d128", O.TURBO_MSE, 4, 128, 37, 15)
+    quant_case("nvfp4_d128", O.NVFP4, 0, 128, 11, 16)
+    attn_case()
+    combine_case()

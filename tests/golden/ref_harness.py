@@ -1,0 +1,112 @@
+"""Driver of the reference's host-emulator kernel harness (oracle/_ref/accel_host_test).
+
+The harness is the reference's own tq_quant / tq_attn / combine kernel code compiled for the
+CPU by oracle/Makefile (`make -C oracle ref`) from the reference tree. File protocol
+(candle-core/kernels/tests/accel_host_test.cpp:1-5): repeated
+[u32 name_len][name][u8 kind][u64 bytes][bytes], kinds 0 f32, 1 u32, 2 u64, 3 i32, 4 bytes.
+"""
+from __future__ import annotations
+
+import os
+import struct
+import subprocess
+import tempfile
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+BIN = os.path.join(REPO, "oracle", "_ref", "accel_host_test")
+
+_KINDS = {0: np.float32, 1: np.uint32, 2: np.uint64, 3: np.int32}
+
+
+def available() -> bool:
+    return os.path.exists(BIN) and os.access(BIN, os.X_OK)
+
+
+def _write(path: str, arrays: dict) -> None:
+    with open(path, "wb") as f:
+        for name, val in arrays.items():
+            if isinstance(val, str):
+                kind, data = 4, val.encode()
+            else:
+                a = np.ascontiguousarray(val)
+                kind = {np.dtype(np.float32): 0, np.dtype(np.uint32): 1,
+                        np.dtype(np.uint64): 2, np.dtype(np.int32): 3}[a.dtype]
+                data = a.tobytes()
+            nb = name.encode()
+            f.write(struct.pack("<I", len(nb)) + nb + struct.pack("<BQ", kind, len(data)) + data)
+
+
+def _read(path: str) -> dict:
+    out = {}
+    with open(path, "rb") as f:
+        buf = f.read()
+    pos = 0
+    while pos < len(buf):
+        (nl,) = struct.unpack_from("<I", buf, pos)
+        pos += 4
+        name = buf[pos:pos + nl].decode()
+        pos += nl
+        kind, nb = struct.unpack_from("<BQ", buf, pos)
+        pos += 9
+        raw = buf[pos:pos + nb]
+        pos += nb
+        out[name] = np.frombuffer(raw, dtype=_KINDS[kind]).copy() if kind in _KINDS else raw
+    return out
+
+
+def run(arrays: dict) -> dict:
+    with tempfile.TemporaryDirectory() as d:
+        pin, pout = os.path.join(d, "in"), os.path.join(d, "out")
+        _write(pin, arrays)
+        subprocess.run([BIN, pin, pout], check=True, capture_output=True)
+        return _read(pout)
+
+
+def tq_tab(centroids=None, boundaries=None) -> np.ndarray:
+    """The 32-float table of the kernels: [centroids; 16][boundaries; 16], unused = +inf
+    (candle-core/src/accel/turbo.rs:47-55)."""
+    t = np.zeros(32, dtype=np.float32)
+    if centroids is not None:
+        t[: len(centroids)] = centroids
+        t[16: 16 + len(boundaries)] = boundaries
+        t[16 + len(boundaries):] = np.inf
+    return t
+
+
+def tq_quant(x: np.ndarray, mode: int, code_bits: int, code_words: int, aux_words: int,
+             row_words: int, tab: np.ndarray, gx: int = 5) -> np.ndarray:
+    """Reference `tq_quant_f32` over rows x (rows, D) f32 -> (rows, row_words) u32."""
+    rows, d = x.shape
+    p = np.array([rows, d, mode, code_bits, code_words, aux_words, row_words, gx, 0], dtype=np.uint32)
+    out = run({"op": "tq_quant", "x": x.astype(np.float32), "tab": tab, "params": p})
+    return out["out"].reshape(rows, row_words)
+
+
+def tq_attn(q: np.ndarray, kd: np.ndarray, vd: np.ndarray, k_side, v_side, tab64: np.ndarray,
+            scale: float, splits: int = 1, wl: int = -1, wr: int = -1, group: int = 1,
+            fp8: bool = False) -> np.ndarray:
+    """Reference `tq_attn*` + `tq_combine`: q (B, Hq, Lq, D) f32 rotated queries, kd / vd
+    (B, Hkv, Lk, words) u32 rows; sides (mode, code_bits, code_words, rsc_offset)."""
+    B, Hq, Lq, D = q.shape
+    _, Hkv, Lk, kw = kd.shape
+    vw = vd.shape[3]
+    u = np.array([B, Lq, Lk, Hq, Hkv, D, *k_side, *v_side, splits, 3, 0, int(fp8), group],
+                 dtype=np.uint32)
+    s = np.array([Hq * Lq * D, Lq * D, D, Hkv * Lk * kw, Lk * kw, kw, Hkv * Lk * vw, Lk * vw, vw],
+                 dtype=np.uint64)
+    out = run({"op": "tq_attn", "uparams": u, "strides": s,
+               "fparams": np.array([scale, 0.0], dtype=np.float32),
+               "iparams": np.array([wl, wr], dtype=np.int32), "q": q.astype(np.float32),
+               "kd": kd.astype(np.uint32), "vd": vd.astype(np.uint32), "tab": tab64})
+    return out["o"].reshape(B, Hq, Lq, D)
+
+
+def combine(part_o: np.ndarray, part_lse: np.ndarray) -> np.ndarray:
+    """Reference `tq_combine` (output `t`)."""
+    splits, rows, d = part_o.shape
+    out = run({"op": "combine", "part_o": part_o.astype(np.float32),
+               "part_lse": part_lse.astype(np.float32),
+               "params": np.array([rows, d, splits], dtype=np.uint32)})
+    return out["t"].reshape(rows, d)

@@ -1,0 +1,455 @@
+"""Pins the CPU oracle before it is trusted as the checker of the HIP path.
+
+Each check is one of: a known-answer test of the reference's own test suite (cited), a golden
+fixture written by the reference's own kernel code (tests/golden/, see make_vectors.py), or an
+independent mathematical fact (brute-force nearest-value rounding, Sylvester Hadamard matrices,
+Lloyd-Max optimality conditions by numerical integration, float64 attention).
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.golden import ref_harness as H
+
+GOLD = __import__("os").path.join(__import__("os").path.dirname(__file__), "golden")
+
+
+def gold(name):
+    return np.load(f"{GOLD}/{name}.npz")
+
+
+# ---------------------------------------------------------------------------------------------
+# E4M3 (OCP FN)
+# ---------------------------------------------------------------------------------------------
+def e4m3_value_table():
+    """Closed form of OCP E4M3FN: (-1)^s 2^(e-7)(1 + m/8), subnormals m 2^-9, S.1111.111 NaN."""
+    vals = np.zeros(256, dtype=np.float64)
+    for c in range(256):
+        s, e, m = c >> 7, (c >> 3) & 15, c & 7
+        if e == 15 and m == 7:
+            vals[c] = np.nan
+            continue
+        v = m * 2.0 ** -9 if e == 0 else 2.0 ** (e - 7) * (1 + m / 8)
+        vals[c] = -v if s else v
+    return vals
+
+
+def test_e4m3_decode_all_codes_closed_form():
+    table = e4m3_value_table()
+    for c in range(256):
+        got = O.e4m3_to_f32(c)
+        if np.isnan(table[c]):
+            assert math.isnan(got)
+        else:
+            assert got == table[c], hex(c)
+            assert math.copysign(1, got) == (-1 if c & 0x80 else 1)
+
+
+def test_e4m3_reference_known_answers():
+    # candle-core/src/accel/formats.rs:413-432
+    for c in range(256):
+        v = O.e4m3_to_f32(c)
+        if math.isnan(v):
+            continue
+        back = O.f32_to_e4m3(v)
+        if v == 0.0:
+            assert back & 0x7F == 0
+        else:
+            assert back == c
+    assert O.e4m3_to_f32(0x7E) == 448.0
+    assert O.f32_to_e4m3(1000.0) == 0x7E
+    assert O.f32_to_e4m3(-1000.0) == 0xFE
+    assert O.e4m3_to_f32(0x01) == 0.001953125
+    # candle-nn/tests/accel_rocm.rs:483-507
+    known = [(0x00, 0.0), (0x80, -0.0), (0x01, 0.001953125), (0x81, -0.001953125),
+             (0x07, 0.013671875), (0x08, 0.015625), (0x38, 1.0), (0xB8, -1.0), (0x40, 2.0),
+             (0x78, 256.0), (0x7D, 416.0), (0x7E, 448.0), (0xFE, -448.0), (0x77, 240.0)]
+    for c, v in known:
+        got = O.e4m3_to_f32(c)
+        assert got == v and math.copysign(1, got) == math.copysign(1, v), hex(c)
+    assert math.isnan(O.e4m3_to_f32(0x7F)) and math.isnan(O.e4m3_to_f32(0xFF))
+
+
+def brute_e4m3(x: np.ndarray) -> np.ndarray:
+    """Nearest E4M3FN value, ties to the even code, saturation to +-448, NaN -> 0x7f|s."""
+    pos = e4m3_value_table()[:0x7F]  # codes 0..0x7e ascending
+    with np.errstate(invalid="ignore"):
+        a = np.abs(x.astype(np.float64))
+    s = (np.signbit(x).astype(np.uint8)) << 7
+    i = np.clip(np.searchsorted(pos, a), 1, 0x7E)
+    lo, hi = i - 1, i
+    dl, dh = a - pos[lo], pos[hi] - a
+    pick = np.where(dl < dh, lo, np.where(dh < dl, hi, np.where(lo % 2 == 0, lo, hi)))
+    pick = np.where(a >= pos[0x7E], 0x7E, pick)
+    out = (pick.astype(np.uint8) | s)
+    return np.where(np.isnan(x), 0x7F | s, out).astype(np.uint8)
+
+
+def test_e4m3_encode_matches_brute_force():
+    # every f32 with the low 11 mantissa bits clear (2^21 patterns incl. both signs, inf, NaN)
+    bits = (np.arange(1 << 21, dtype=np.uint64) << 11).astype(np.uint32)
+    x = bits.view(np.float32)
+    np.testing.assert_array_equal(O.e4m3_encode(x), brute_e4m3(x))
+    # every midpoint between adjacent codes and its two f32 neighbours
+    pos = e4m3_value_table()[:0x7F].astype(np.float32)
+    mids = ((pos[:-1].astype(np.float64) + pos[1:]) / 2).astype(np.float32)
+    near = np.concatenate([mids, np.nextafter(mids, 0), np.nextafter(mids, 1000), pos])
+    near = np.concatenate([near, -near])
+    np.testing.assert_array_equal(O.e4m3_encode(near), brute_e4m3(near))
+
+
+def test_e4m3_encode_matches_torch_below_saturation():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.uniform(-448, 448, 200000), rng.normal(0, 0.01, 200000)]).astype(np.float32)
+    t = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    ours = O.e4m3_encode(x)
+    # torch keeps -0 for tiny negatives like the reference
+    np.testing.assert_array_equal(ours, t)
+
+
+# ---------------------------------------------------------------------------------------------
+# E2M1, E8M0
+# ---------------------------------------------------------------------------------------------
+FP4 = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
+
+
+def test_fp4_reference_known_answers():
+    # candle-core/src/accel/formats.rs:446-458
+    for c, v in enumerate(FP4):
+        assert O.fp4_to_f32(c) == v
+        assert O.fp4_to_f32(c | 8) == -v
+        assert O.f32_to_fp4(v) == c
+    assert O.f32_to_fp4(0.75) == 2
+    assert O.f32_to_fp4(2.5) == 4
+    assert O.f32_to_fp4(5.0) == 6
+    assert O.f32_to_fp4(100.0) == 7
+
+
+def test_fp4_encode_matches_brute_force():
+    vals = np.array(FP4)
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.uniform(-8, 8, 100000), (vals[:-1] + vals[1:]) / 2, vals,
+                        -(vals[:-1] + vals[1:]) / 2]).astype(np.float32)
+    x = np.concatenate([x, np.nextafter(x, 10), np.nextafter(x, -10)]).astype(np.float32)
+    a = np.abs(x.astype(np.float64))
+    i = np.clip(np.searchsorted(vals, a), 1, 7)
+    lo, hi = i - 1, i
+    dl, dh = a - vals[lo], vals[hi] - a
+    pick = np.where(dl < dh, lo, np.where(dh < dl, hi, np.where(lo % 2 == 0, lo, hi)))
+    pick = np.where(a >= 6.0, 7, pick)
+    want = (pick | (np.signbit(x) * 8)).astype(np.uint8)
+    np.testing.assert_array_equal(O.fp4_encode(x), want)
+
+
+def test_mx_scale_known_answers():
+    # candle-core/src/accel/formats.rs:460-465
+    assert O.mx_scale_code(6.0, 2) == 127
+    assert O.e8m0_to_f32(O.mx_scale_code(12.0, 2)) == 2.0
+    assert O.mx_scale_code(0.0, 2) == 0
+    # the OCP rule: scale = 2^(floor(log2 amax) - emax)
+    for amax in [1e-3, 0.3, 1.0, 5.9, 6.0, 7.99, 1e6]:
+        assert O.e8m0_to_f32(O.mx_scale_code(amax, 2)) == 2.0 ** (math.floor(math.log2(amax)) - 2)
+    assert O.mx_scale_code(float("inf"), 2) == 0 and O.mx_scale_code(float("nan"), 2) == 0
+    assert O.e8m0_to_f32(0) == 2.0 ** -127
+
+
+# ---------------------------------------------------------------------------------------------
+# layouts, bit streams
+# ---------------------------------------------------------------------------------------------
+def test_row_layouts():
+    # candle-core/src/accel/formats.rs:467-477
+    l = O.row_layout(O.TURBO_MSE, 3, 128)
+    assert (l.code_words, l.aux_words, l.row_words) == (12, 0, 14)
+    l = O.row_layout(O.TURBO_PROD, 4, 128)
+    assert (l.code_words, l.aux_words, l.row_words) == (12, 4, 18)
+    l = O.row_layout(O.MXFP4, 0, 64)
+    assert (l.code_words, l.aux_words) == (8, 1)
+    l = O.row_layout(O.NVFP4, 0, 128)
+    assert (l.code_words, l.aux_words) == (16, 2)
+    with pytest.raises(ValueError):
+        O.row_layout(O.MXFP8, 0, 48)
+    # the BASELINE formats at head_dim 128
+    assert O.row_layout(O.FP8, 0, 128).row_words == 34
+    assert O.row_layout(O.MXFP4, 0, 128).row_words == 19
+    assert O.row_layout(O.TURBO_MSE, 4, 128).row_words == 18
+
+
+def test_bit_stream():
+    # candle-core/src/accel/formats.rs:496-504
+    import ctypes
+    w = (ctypes.c_uint32 * 4)()
+    for j in range(40):
+        O.lib().orc_put_bits(w, j * 3, 3, j % 8)
+    O.lib().orc_get_bits.restype = ctypes.c_uint32
+    for j in range(40):
+        assert O.lib().orc_get_bits(w, ctypes.c_size_t(j * 3), 3) == j % 8
+
+
+# ---------------------------------------------------------------------------------------------
+# SplitMix64, rotations, codebooks
+# ---------------------------------------------------------------------------------------------
+def test_splitmix64_published_vector():
+    # the published SplitMix64 output for seed 0 (Steele, Lea, Flood 2014; used by xoshiro seeding)
+    assert O.splitmix_u64(0, 3) == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F]
+
+
+def test_box_muller_moments():
+    x = O.normal(7, (400000,)).astype(np.float64)
+    assert abs(x.mean()) < 0.01 and abs(x.var() - 1) < 0.01
+    assert abs((x ** 4).mean() - 3) < 0.05
+
+
+def test_hadamard_rotation_structure():
+    import scipy.linalg
+    for d, seed in [(64, 7), (128, 42), (128, 44)]:
+        m = O.rotation_matrix(d, O.ROT_HADAMARD, seed).astype(np.float64)
+        signs = np.array([1.0 if (u & 1) == 0 else -1.0
+                          for u in O.splitmix_u64(seed ^ 0x484144414D415244, d)])
+        h = scipy.linalg.hadamard(d)
+        np.testing.assert_allclose(m * math.sqrt(d), h * signs[None, :], rtol=1e-6)
+        np.testing.assert_allclose(m @ m.T, np.eye(d), atol=1e-5)
+
+
+def test_rotations_orthogonal():
+    # candle-core/src/accel/turbo.rs:599-615
+    for d, kind in [(64, O.ROT_HADAMARD), (48, O.ROT_DENSE), (16, O.ROT_NONE)]:
+        m = O.rotation_matrix(d, kind, 7).astype(np.float64)
+        np.testing.assert_allclose(m @ m.T, np.eye(d), atol=1e-4)
+
+
+def test_codebook_reference_bounds():
+    # candle-core/src/accel/turbo.rs:584-597
+    d = 128
+    s = math.sqrt(d)
+    c, _ = O.lloyd_max(d, 2)
+    assert abs(c[2] * s - 0.4528) < 0.01 and abs(c[3] * s - 1.5104) < 0.02
+    assert abs(c[0] + c[3]) < 1e-6
+    c1, _ = O.lloyd_max(d, 1)
+    assert abs(c1[1] * s - 0.7979) < 0.01
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+def test_codebook_lloyd_max_conditions(bits):
+    """Centroids are the conditional means of their cells under the density (1 - x^2)^((d-3)/2)
+    on [-1, 1] (integrated independently with scipy), boundaries are the midpoints."""
+    from scipy import integrate
+    d = 128
+    c, b = O.lloyd_max(d, bits)
+    c = c.astype(np.float64)
+    b64 = b.astype(np.float64)
+    np.testing.assert_allclose(b64, (c[:-1] + c[1:]) / 2, rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(c, -c[::-1], atol=0)
+    expo = (d - 3) / 2
+    f = lambda x: (1 - x * x) ** expo
+    edges = np.concatenate([[-1.0], (c[:-1] + c[1:]) / 2, [1.0]])
+    for i in range(len(c)):
+        mass = integrate.quad(f, edges[i], edges[i + 1], epsabs=1e-14, limit=200)[0]
+        mom = integrate.quad(lambda x: x * f(x), edges[i], edges[i + 1], epsabs=1e-14, limit=200)[0]
+        # the reference integrates on a 2^16-point grid: cell boundaries snap to grid points,
+        # which moves a centroid by up to ~one grid step h = 2 / 2^16; a wrong density
+        # exponent or a dropped term moves them by ~1e-3
+        assert abs(mom / mass - c[i]) < 2.0 / 65536, (i, mom / mass, c[i])
+
+
+def test_codebook_close_to_gaussian_lloyd_max():
+    # 16-level Lloyd-Max quantizer of N(0, 1) (Max 1960): for d = 128 the coordinates are close
+    # to N(0, 1/d) with slightly lighter tails
+    gauss = np.array([0.1284, 0.3881, 0.6568, 0.9424, 1.2562, 1.6181, 2.0690, 2.7326])
+    c, _ = O.lloyd_max(128, 4)
+    np.testing.assert_allclose(c[8:] * math.sqrt(128), gauss, rtol=0.03)
+
+
+# ---------------------------------------------------------------------------------------------
+# row codecs against the reference's own kernel (golden fixtures)
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("name", ["fp8_d128", "fp8_d80", "mxfp4_d128", "mxfp4_d64", "nvfp4_d128"])
+def test_quantize_rows_bit_exact_with_reference_kernel(name):
+    g = gold(f"ref_quant_{name}")
+    mode, bits = int(g["mode"]), int(g["bits"])
+    got = O.quantize_rows(mode, bits, g["x"])
+    np.testing.assert_array_equal(got, g["rows"])
+
+
+def test_turbo_quantize_rows_vs_reference_kernel():
+    # the reference kernel sums the norm in a tree: codes may flip at a boundary (<= 0.1 %) and
+    # the norm differs in the last bits (candle-core/tests/accel_kernels_host.rs:1000-1027)
+    g = gold("ref_quant_turbo4_d128")
+    got = O.quantize_rows(O.TURBO_MSE, 4, g["x"])
+    want = g["rows"]
+    l = O.row_layout(O.TURBO_MSE, 4, 128)
+    gn = got[:, l.code_words].view(np.float32)
+    wn = want[:, l.code_words].view(np.float32)
+    np.testing.assert_allclose(gn, wn, rtol=1e-5, atol=1e-6)
+    gc = np.stack([(got[:, :16] >> (4 * i)) & 15 for i in range(8)])
+    wc = np.stack([(want[:, :16] >> (4 * i)) & 15 for i in range(8)])
+    assert (gc != wc).sum() <= got.shape[0] * 128 // 1000
+
+
+def test_fp8_row_properties():
+    x = O.normal(5, (64, 128)) * np.float32(3)
+    rows = O.quantize_rows(O.FP8, 0, x)
+    s = rows[:, 32].view(np.float32)
+    np.testing.assert_array_equal(s, (np.abs(x).max(1) / np.float32(448)).astype(np.float32))
+    assert (rows[:, 33] == 0).all()
+    codes = rows[:, :32].view(np.uint8).reshape(64, 128)
+    table = e4m3_value_table()
+    dec = table[codes] * s[:, None]
+    # the largest element lands on +-448; every element within half an E4M3 step
+    amax_pos = np.abs(x).argmax(1)
+    assert ((codes[np.arange(64), amax_pos] & 0x7F) == 0x7E).all()
+    rel = np.abs(dec - x) / np.maximum(np.abs(x), 2.0 ** -6 * s[:, None])
+    assert rel.max() <= 2.0 ** -4 + 1e-6
+
+
+def test_mxfp4_row_properties():
+    x = O.normal(6, (64, 128))
+    rows = O.quantize_rows(O.MXFP4, 0, x)
+    dq = O.dequantize_rows(O.MXFP4, 0, 128, rows)
+    for b in range(4):
+        blk = x[:, 32 * b: 32 * b + 32]
+        sc = (rows[:, 16] >> (8 * b)) & 0xFF
+        amax = np.abs(blk).max(1)
+        np.testing.assert_array_equal(sc, np.floor(np.log2(amax)).astype(int) - 2 + 127)
+        # the block maximum / scale lies in [4, 8): it encodes to 4 or 6
+        top = np.abs(dq[:, 32 * b: 32 * b + 32]).max(1) / 2.0 ** (sc.astype(float) - 127)
+        assert np.isin(top, [4.0, 6.0]).all()
+    assert (rows[:, 17].view(np.float32) == 1.0).all() and (rows[:, 18] == 0).all()
+
+
+# ---------------------------------------------------------------------------------------------
+# attention, masks, combine
+# ---------------------------------------------------------------------------------------------
+def test_key_ranges():
+    # candle-core/src/accel/attention.rs:741-753
+    assert O.key_range(0, 4, 4, -1, 0) == (0, 1)
+    assert O.key_range(3, 4, 4, -1, 0) == (0, 4)
+    assert O.key_range(0, 1, 10, -1, 0) == (0, 10)
+    assert O.key_range(5, 8, 8, 2, 0) == (3, 6)
+    assert O.key_range(1, 3, 7, -1, -1) == (0, 7)
+    assert O.key_range(0, 4, 2, -1, 0) == (0, 0)
+
+
+def attention_f64(q, k, v, scale, wl=-1, wr=-1, kv_lens=None):
+    b, hq, lq, d = q.shape
+    hkv = k.shape[1]
+    g = hq // hkv
+    out = np.zeros(q.shape)
+    for bi in range(b):
+        lk = k.shape[2] if kv_lens is None else int(kv_lens[bi])
+        for h in range(hq):
+            kk = k[bi, h // g, :lk].astype(np.float64)
+            vv = v[bi, h // g, :lk].astype(np.float64)
+            for i in range(lq):
+                pos = i + lk - lq
+                lo = max(pos - wl, 0) if wl >= 0 else 0
+                hi = min(pos + wr + 1, lk) if wr >= 0 else lk
+                lo = min(lo, lk)
+                if lo >= hi:
+                    continue
+                s = kk[lo:hi] @ q[bi, h, i].astype(np.float64) * scale
+                p = np.exp(s - s.max())
+                out[bi, h, i] = p @ vv[lo:hi] / p.sum()
+    return out
+
+
+@pytest.mark.parametrize("wl,wr", [(-1, -1), (-1, 0), (3, 0), (2, 1)])
+def test_attention_unfused_vs_float64(wl, wr):
+    q = O.normal(1, (2, 4, 5, 32))
+    k = O.normal(2, (2, 2, 9, 32))
+    v = O.normal(3, (2, 2, 9, 32))
+    got = O.attention_unfused(q, k, v, 0.2, wl=wl, wr=wr)
+    np.testing.assert_allclose(got, attention_f64(q, k, v, 0.2, wl, wr), atol=2e-6)
+
+
+def test_attention_ragged_lengths_vs_float64():
+    q = O.normal(11, (3, 4, 1, 16))
+    k = O.normal(12, (3, 2, 40, 16))
+    v = O.normal(13, (3, 2, 40, 16))
+    lens = np.array([40, 1, 17], dtype=np.int32)
+    got = O.attention_unfused(q, k, v, 0.25, kv_lens=lens)
+    np.testing.assert_allclose(got, attention_f64(q, k, v, 0.25, kv_lens=lens), atol=2e-6)
+
+
+def test_attention_vs_reference_tq_attn_fixture():
+    # the reference's tq_attng4_fp8 + tq_combine over FP8 rows vs the oracle's attention over the
+    # dequantized rows (tolerance of candle-core/tests/accel_kernels_host.rs:1097-1313)
+    g = gold("ref_attn_fp8")
+    k = O.dequantize_rows(O.FP8, 0, 64, g["kd"])
+    v = O.dequantize_rows(O.FP8, 0, 64, g["vd"])
+    got = O.attention_unfused(g["q"], k, v, float(g["scale"]))
+    np.testing.assert_allclose(got, g["out"], atol=3e-5, rtol=2e-4)
+
+
+def test_combine_bit_exact_with_reference_kernel():
+    g = gold("ref_combine")
+    np.testing.assert_array_equal(O.combine(g["part_o"], g["part_lse"]), g["o"])
+
+
+def test_combine_of_key_splits_equals_full_attention():
+    q = O.normal(21, (1, 2, 1, 16))
+    k = O.normal(22, (1, 2, 60, 16))
+    v = O.normal(23, (1, 2, 60, 16))
+    full = O.attention_unfused(q, k, v, 0.3)[0, :, 0]
+    cuts = [0, 7, 30, 30, 60]
+    po, pl = [], []
+    for a, b in zip(cuts[:-1], cuts[1:]):
+        if a == b:
+            po.append(np.zeros((2, 16), np.float32))
+            pl.append(np.full(2, -np.inf, np.float32))
+            continue
+        o = O.attention_unfused(q, k[:, :, a:b], v[:, :, a:b], 0.3)[0, :, 0]
+        s = np.einsum("hd,hkd->hk", q[0, :, 0].astype(np.float64), k[0, :, a:b].astype(np.float64)) * 0.3
+        m = s.max(1)
+        pl.append((m + np.log(np.exp(s - m[:, None]).sum(1))).astype(np.float32))
+        po.append(o)
+    np.testing.assert_allclose(O.combine(np.stack(po), np.stack(pl)), full, atol=2e-6)
+
+
+def test_split_rules_known_answers():
+    # candle-core/src/accel/attention.rs:799-807, 854-857
+    assert O.split_count_grouped(8, 1, 8192, 60) == 64
+    assert O.split_count_grouped(8, 1, 1000, 60) == 8
+    assert O.split_count_grouped(64, 1, 2048, 16) == 16
+    assert O.split_count_grouped(4096, 1, 2048, 16) == 1
+    assert O.split_count_grouped(16, 4, 1024, 16) == 16
+    assert O.split_count_grouped(16, 4, 8192, 16) == 64
+    assert O.split_count_grouped(4096, 4, 2048, 16) == 1
+    assert (O.row_group(16, 8), O.row_group(32, 2), O.row_group(12, 4), O.row_group(8, 8)) == (2, 8, 1, 1)
+
+
+def test_cache_attention_fp8_matches_dequantized_bf16_path():
+    """orc_cache_attention = dequantize -> bf16 -> unfused attention (turbo_quant.rs:948-990)."""
+    b, hq, hkv, d, lk = 1, 4, 2, 64, 33
+    kx = O.normal(31, (b, hkv, lk, d))
+    vx = O.normal(32, (b, hkv, lk, d))
+    q = O.normal(33, (b, hq, 1, d))
+    qb = O.f32_to_bf16_bits(q)
+    kr = O.quantize_rows(O.FP8, 0, kx)
+    vr = O.quantize_rows(O.FP8, 0, vx)
+    got = O.cache_attention(qb, kr, vr, (O.FP8, 0), (O.FP8, 0), None, None, lk, 0.125)
+    kd = O.round_bf16(O.dequantize_rows(O.FP8, 0, d, kr))
+    vd = O.round_bf16(O.dequantize_rows(O.FP8, 0, d, vr))
+    want = attention_f64(O.bf16_bits_to_f32(qb), kd, vd, 0.125)
+    np.testing.assert_allclose(got, want, atol=2e-6)
+
+
+def test_turbo_cache_roundtrip_error_bound():
+    # candle-core/src/accel/turbo.rs:621-656: relative mse of TurboMse-4 < 0.012 at d = 128
+    d = 128
+    x = O.normal(3, (64, d))
+    pi = O.rotation_matrix(d, O.ROT_HADAMARD, 11)
+    rows = O.quantize_rows(O.TURBO_MSE, 4, O.rotate_rows(pi, x))
+    back = O.unrotate_rows(pi, O.dequantize_rows(O.TURBO_MSE, 4, d, rows))
+    rel = ((back.astype(np.float64) - x) ** 2).sum() / (x.astype(np.float64) ** 2).sum()
+    assert rel < 0.012
+
+
+@pytest.mark.skipif(not H.available(), reason="reference harness not built (make -C oracle ref)")
+def test_live_reference_harness_fp8_rows():
+    x = O.normal(99, (23, 128))
+    l = O.row_layout(O.FP8, 0, 128)
+    want = H.tq_quant(x, O.FP8, 8, l.code_words, l.aux_words, l.row_words, H.tq_tab())
+    np.testing.assert_array_equal(O.quantize_rows(O.FP8, 0, x), want)
