@@ -1,0 +1,316 @@
+"""ctypes front end of libcqkv.so (the C ABI of include/cqkv.h) over torch device tensors.
+
+torch supplies device memory and the current stream; every computation runs in the HIP kernels
+of libcqkv.so. There is no fallback: when the library is missing or the device is not a GPU,
+the calls raise.
+
+Names follow the reference's candle-nn API (paths relative to the reference repository root):
+TurboKvCache (candle-nn/src/turbo_quant.rs:793-991), flash_attn
+(candle-flash-attn/src/lib.rs:149-157).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libcqkv.so")
+
+# formats: the reference's kernel mode ids (candle-core/src/accel/formats.rs:41-48)
+TURBO4, MXFP4, FP8 = 0, 2, 5
+FORMAT_NAMES = {"fp8": FP8, "mxfp4": MXFP4, "turbo4": TURBO4}
+BF16, F16, F32 = 0, 1, 2
+_DTYPES = {torch.bfloat16: BF16, torch.float16: F16, torch.float32: F32}
+
+OK, ERR_ARG, ERR_HIP, ERR_WORKSPACE = 0, -1, -2, -3
+
+
+class CqkvError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"cqkv error {code}: {msg}")
+        self.code = code
+
+
+class Side(ctypes.Structure):
+    _fields_ = [("format", ctypes.c_int32), ("is_value", ctypes.c_int32),
+                ("head_dim", ctypes.c_int32), ("kv_heads", ctypes.c_int32),
+                ("capacity", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("seed", ctypes.c_uint64), ("codes", ctypes.c_void_p),
+                ("scales", ctypes.c_void_p)]
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Loads libcqkv.so (built by __graft_entry__.build() / `make -C <pkg>/csrc`)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -C {HERE}/csrc`")
+        L = ctypes.CDLL(LIB_PATH)
+        P, i32, sz, f32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_size_t, ctypes.c_float
+        I64P = ctypes.POINTER(ctypes.c_int64)
+        SP = ctypes.POINTER(Side)
+        L.cqkv_codes_plane_bytes.argtypes = [i32, i32, i32]
+        L.cqkv_codes_plane_bytes.restype = sz
+        L.cqkv_scales_plane_bytes.argtypes = [i32, i32, i32]
+        L.cqkv_scales_plane_bytes.restype = sz
+        L.cqkv_quant_append.argtypes = [SP, P, i32, I64P, i32, i32, P, i32, P]
+        L.cqkv_decode_workspace_bytes.argtypes = [i32, i32, i32, i32, i32]
+        L.cqkv_decode_workspace_bytes.restype = sz
+        L.cqkv_decode_splits.argtypes = [i32, i32, i32]
+        L.cqkv_decode_splits.restype = i32
+        L.cqkv_decode_attention.argtypes = [P, i32, I64P, SP, SP, i32, i32, i32, P, i32, f32,
+                                            i32, i32, P, i32, I64P, i32, P, sz, P]
+        L.cqkv_flash_attn.argtypes = [P, I64P, P, I64P, P, I64P, P, I64P, i32, i32, i32, i32,
+                                      i32, i32, f32, i32, i32, SP, SP, i32, P]
+        L.cqkv_reference_row_words.argtypes = [i32, i32]
+        L.cqkv_reference_row_words.restype = i32
+        L.cqkv_rows_import.argtypes = [SP, P, i32, i32, i32, P]
+        L.cqkv_rows_export.argtypes = [SP, P, i32, i32, i32, P]
+        L.cqkv_turbo_codebook.argtypes = [i32, i32, P, P]
+        L.cqkv_turbo_signs.argtypes = [i32, ctypes.c_uint64, P]
+        L.cqkv_last_error.restype = ctypes.c_char_p
+        L.cqkv_version.restype = ctypes.c_char_p
+        _lib = L
+    return _lib
+
+
+EXPORTED = ["cqkv_codes_plane_bytes", "cqkv_scales_plane_bytes", "cqkv_quant_append",
+            "cqkv_decode_workspace_bytes", "cqkv_decode_splits", "cqkv_decode_attention",
+            "cqkv_flash_attn", "cqkv_reference_row_words", "cqkv_rows_import",
+            "cqkv_rows_export", "cqkv_turbo_codebook", "cqkv_turbo_signs", "cqkv_last_error",
+            "cqkv_version"]
+
+
+def _check(rc: int) -> None:
+    if rc != OK:
+        raise CqkvError(rc, lib().cqkv_last_error().decode())
+
+
+def _strides3(t: torch.Tensor, dims) -> ctypes.Array:
+    return (ctypes.c_int64 * 3)(*[t.stride(i) for i in dims])
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _need_gpu(t: torch.Tensor, what: str) -> None:
+    if t.device.type != "cuda":
+        raise CqkvError(ERR_ARG, f"{what} must be a GPU tensor (got {t.device})")
+
+
+# ------------------------------------------------------------------------------------------
+# cache sides
+# ------------------------------------------------------------------------------------------
+@dataclass
+class CacheSide:
+    """One side (keys or values) of a quantized cache: codes + scales planes for
+    (batch, kv_heads) at `capacity` tokens each (layout in include/cqkv.h)."""
+    fmt: int
+    is_value: bool
+    batch: int
+    kv_heads: int
+    head_dim: int
+    capacity: int
+    codes: torch.Tensor
+    scales: torch.Tensor
+    seed: int = 0
+
+    @staticmethod
+    def empty(fmt: int, is_value: bool, batch: int, kv_heads: int, head_dim: int,
+              capacity: int, device, seed: int = 0) -> "CacheSide":
+        capacity = (capacity + 31) // 32 * 32
+        cb = lib().cqkv_codes_plane_bytes(fmt, head_dim, capacity)
+        sb = lib().cqkv_scales_plane_bytes(fmt, head_dim, capacity)
+        if cb == 0:
+            raise CqkvError(ERR_ARG, f"format {fmt} / head_dim {head_dim} not supported")
+        codes = torch.zeros(batch * kv_heads * cb, dtype=torch.uint8, device=device)
+        scales = torch.zeros(batch * kv_heads * sb, dtype=torch.uint8, device=device)
+        return CacheSide(fmt, is_value, batch, kv_heads, head_dim, capacity, codes, scales, seed)
+
+    def struct(self) -> Side:
+        return Side(self.fmt, int(self.is_value), self.head_dim, self.kv_heads, self.capacity, 0,
+                    self.seed, self.codes.data_ptr(), self.scales.data_ptr())
+
+    def nbytes(self) -> int:
+        return self.codes.numel() + self.scales.numel()
+
+
+def quant_append(side: CacheSide, x: torch.Tensor, position: int = 0,
+                 positions: torch.Tensor | None = None) -> None:
+    """Quantize x (batch, kv_heads, tokens, D) and write it at `position` (or the per-batch
+    device int32 `positions`)."""
+    _need_gpu(x, "x")
+    if x.dim() != 4 or x.stride(3) != 1:
+        raise CqkvError(ERR_ARG, "x must be (batch, kv_heads, tokens, D) with contiguous D")
+    b, h, t, d = x.shape
+    if h != side.kv_heads or d != side.head_dim or b != side.batch:
+        raise CqkvError(ERR_ARG, f"x {tuple(x.shape)} does not match the cache side")
+    s = side.struct()
+    _check(lib().cqkv_quant_append(ctypes.byref(s), _ptr(x), _DTYPES[x.dtype],
+                                   _strides3(x, (0, 1, 2)), b, t, _ptr(positions), position,
+                                   _stream(x.device)))
+
+
+def decode_workspace_bytes(batch, q_heads, q_len, head_dim, splits) -> int:
+    return lib().cqkv_decode_workspace_bytes(batch, q_heads, q_len, head_dim, splits)
+
+
+def decode_splits(batch, kv_heads, kv_len) -> int:
+    return lib().cqkv_decode_splits(batch, kv_heads, kv_len)
+
+
+def decode_attention(q: torch.Tensor, k: CacheSide, v: CacheSide, kv_len: int,
+                     softmax_scale: float, kv_lens: torch.Tensor | None = None,
+                     window_left: int = -1, window_right: int = -1,
+                     out: torch.Tensor | None = None, splits: int = 0,
+                     workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """q (batch, q_heads, q_len, D) -> out of the same shape (dtype of q unless `out` given)."""
+    _need_gpu(q, "q")
+    b, hq, lq, d = q.shape
+    if q.stride(3) != 1:
+        raise CqkvError(ERR_ARG, "q must have a contiguous head dim")
+    if b != k.batch or b != v.batch or d != k.head_dim:
+        raise CqkvError(ERR_ARG, f"q {tuple(q.shape)} does not match the cache sides")
+    if kv_lens is not None and (kv_lens.numel() != b or kv_lens.dtype != torch.int32):
+        raise CqkvError(ERR_ARG, "kv_lens must be int32 with one length per batch entry")
+    if out is None:
+        out = torch.empty_like(q)
+    elif tuple(out.shape) != tuple(q.shape) or out.stride(3) != 1:
+        raise CqkvError(ERR_ARG, f"out {tuple(out.shape)} does not match q")
+    ks, vs = k.struct(), v.struct()
+    _check(lib().cqkv_decode_attention(
+        _ptr(q), _DTYPES[q.dtype], _strides3(q, (0, 1, 2)), ctypes.byref(ks), ctypes.byref(vs), b,
+        hq, lq, _ptr(kv_lens), kv_len, softmax_scale, window_left, window_right, _ptr(out),
+        _DTYPES[out.dtype], _strides3(out, (0, 1, 2)), splits, _ptr(workspace),
+        0 if workspace is None else workspace.numel() * workspace.element_size(),
+        _stream(q.device)))
+    return out
+
+
+def flash_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, softmax_scale: float,
+               causal: bool, window_left: int = -1, window_right: int = -1,
+               k_cache: CacheSide | None = None, v_cache: CacheSide | None = None,
+               position: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """candle_flash_attn::flash_attn layout: q (b, s_q, h_q, d), k / v (b, s_kv, h_kv, d), bf16.
+    With k_cache / v_cache (FP8 sides) K / V are also quantized into the cache at `position`."""
+    _need_gpu(q, "q")
+    b, sq, hq, d = q.shape
+    _, sk, hkv, _ = k.shape
+    if out is None:
+        out = torch.empty_like(q)
+    if causal:
+        window_right = 0
+    kc = None if k_cache is None else ctypes.byref(k_cache.struct())
+    vc = None if v_cache is None else ctypes.byref(v_cache.struct())
+    _check(lib().cqkv_flash_attn(
+        _ptr(q), _strides3(q, (0, 1, 2)), _ptr(k), _strides3(k, (0, 1, 2)), _ptr(v),
+        _strides3(v, (0, 1, 2)), _ptr(out), _strides3(out, (0, 1, 2)), b, sq, sk, hq, hkv, d,
+        softmax_scale, window_left, window_right, kc, vc, position, _stream(q.device)))
+    return out
+
+
+def reference_row_words(fmt: int, head_dim: int) -> int:
+    return lib().cqkv_reference_row_words(fmt, head_dim)
+
+
+def rows_import(side: CacheSide, rows: torch.Tensor, position: int = 0) -> None:
+    """Reference rows (batch, kv_heads, tokens, row_words) u32 (as int32) -> cache."""
+    _need_gpu(rows, "rows")
+    b, h, t, w = rows.shape
+    if (b, h, w) != (side.batch, side.kv_heads, reference_row_words(side.fmt, side.head_dim)):
+        raise CqkvError(ERR_ARG, f"rows {tuple(rows.shape)} do not match the cache side")
+    if rows.dtype not in (torch.int32, torch.uint32):
+        raise CqkvError(ERR_ARG, "rows must be 32-bit words")
+    s = side.struct()
+    _check(lib().cqkv_rows_import(ctypes.byref(s), _ptr(rows.contiguous()), b, t, position,
+                                  _stream(rows.device)))
+
+
+def rows_export(side: CacheSide, tokens: int, position: int = 0) -> torch.Tensor:
+    w = reference_row_words(side.fmt, side.head_dim)
+    rows = torch.zeros((side.batch, side.kv_heads, tokens, w), dtype=torch.int32,
+                       device=side.codes.device)
+    s = side.struct()
+    _check(lib().cqkv_rows_export(ctypes.byref(s), _ptr(rows), side.batch, tokens, position,
+                                  _stream(rows.device)))
+    return rows
+
+
+def turbo_codebook(head_dim: int, bits: int = 4):
+    import numpy as np
+    c = np.zeros(16, dtype=np.float32)
+    bnd = np.zeros(16, dtype=np.float32)
+    _check(lib().cqkv_turbo_codebook(head_dim, bits, c.ctypes.data, bnd.ctypes.data))
+    k = 1 << bits
+    return c[:k].copy(), bnd[:k - 1].copy()
+
+
+def turbo_signs(head_dim: int, seed: int):
+    import numpy as np
+    s = np.zeros(head_dim, dtype=np.float32)
+    _check(lib().cqkv_turbo_signs(head_dim, seed, s.ctypes.data))
+    return s
+
+
+# ------------------------------------------------------------------------------------------
+# host-side mirror of candle-nn's TurboKvCache (candle-nn/src/turbo_quant.rs:793-991)
+# ------------------------------------------------------------------------------------------
+class TurboKvCache:
+    """A quantized KV cache of fixed capacity for (batch, kv_heads, head_dim), keys and values
+    in `key_format` / `value_format` (FP8, MXFP4 or TURBO4; TurboQuant seeds: keys `seed`,
+    values `seed + 2` as TurboKvCache::with_formats does)."""
+
+    def __init__(self, key_format: int, value_format: int, batch: int, kv_heads: int,
+                 head_dim: int, capacity: int, device="cuda", seed: int = 42):
+        if key_format != value_format:
+            raise CqkvError(ERR_ARG, "key and value formats must match")
+        self.k = CacheSide.empty(key_format, False, batch, kv_heads, head_dim, capacity, device,
+                                 seed)
+        self.v = CacheSide.empty(value_format, True, batch, kv_heads, head_dim, capacity, device,
+                                 seed + 2)
+        self._len = 0
+        self.dim = head_dim
+
+    def formats(self):
+        return self.k.fmt, self.v.fmt
+
+    def seq_len(self) -> int:
+        return self._len
+
+    def reset(self) -> None:
+        self._len = 0
+
+    def storage_bytes(self) -> int:
+        return self.k.nbytes() + self.v.nbytes()
+
+    def append(self, k: torch.Tensor, v: torch.Tensor) -> None:
+        """k, v: (batch, kv_heads, tokens, head_dim)."""
+        if k.shape != v.shape or k.dim() != 4 or k.shape[3] != self.dim:
+            raise CqkvError(ERR_ARG, f"turbo-quant cache: k {tuple(k.shape)} / v {tuple(v.shape)}"
+                                     f" do not match head dim {self.dim}")
+        t = k.shape[2]
+        if self._len + t > self.k.capacity:
+            raise CqkvError(ERR_ARG, f"cache full: {self._len} + {t} > {self.k.capacity}")
+        quant_append(self.k, k, self._len)
+        quant_append(self.v, v, self._len)
+        self._len += t
+
+    def attention(self, q: torch.Tensor, softmax_scale: float, window_left: int = -1,
+                  window_right: int = -1, splits: int = 0) -> torch.Tensor:
+        """q (batch, q_heads, q_len, head_dim), bottom-right aligned over the cached tokens."""
+        if self._len == 0:
+            raise CqkvError(ERR_ARG, "turbo-quant cache: attention on an empty cache")
+        return decode_attention(q, self.k, self.v, self._len, softmax_scale,
+                                window_left=window_left, window_right=window_right,
+                                splits=splits)

@@ -1,0 +1,182 @@
+// Converters between the cache layout of include/cqkv.h and the reference's packed rows
+// [codes][aux][rsc0][rsc1] (u32 words; candle-core/src/accel/formats.rs:206-242, written by
+// RowCodec::quantize_row, candle-core/src/accel/turbo.rs:366-381):
+//   FP8    D/4 code words (byte j = element j), rsc0 = f32 scale, rsc1 = 0
+//   MXFP4  D/8 code words (nibble j = element j), ceil(D/32 / 4) aux words (byte b = E8M0 of
+//          block b), rsc0 = 1.0, rsc1 = 0
+//   TURBO4 D/8 code words, rsc0 = f32 norm, rsc1 = 0
+// One wavefront per 8-token tile of a (batch, head) plane; lane l owns elements 2l, 2l+1, so
+// the value tiles are read and written whole by one lane (no cross-lane read-modify-write).
+#include "cqkv_device.h"
+#include "cqkv_host.h"
+
+namespace cqkv {
+
+struct ConvertArgs {
+    uint32_t *rows;  // (batch, kv_heads, tokens, row_words)
+    uint8_t *codes, *scales;
+    uint32_t codes_plane, scales_plane;
+    int32_t kv_heads, tokens, position, row_words, format, is_value, head_dim;
+};
+
+template <bool EXPORT>
+__global__ __launch_bounds__(64) void convert_kernel(ConvertArgs a) {
+    const int lane = threadIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int D = a.head_dim;
+    const int tile = a.position / 8 + (int)blockIdx.x;
+    const int t_lo = max(tile * 8, a.position), t_hi = min(tile * 8 + 8, a.position + a.tokens);
+    if (t_lo >= t_hi) return;
+    const bool active = lane < D / 2;
+    const bool fp8 = a.format == CQKV_FMT_FP8;
+    const int64_t plane = (int64_t)b * a.kv_heads + h;
+    uint8_t *codes = a.codes + plane * a.codes_plane;
+    uint8_t *scales = a.scales + plane * a.scales_plane;
+    const int code_words = fp8 ? D / 4 : D / 8;
+    const int aux_words = a.format == CQKV_FMT_MXFP4 ? (D / 32 + 3) / 4 : 0;
+
+    // value tile words of this lane (elements 2l, 2l+1)
+    uint64_t vw0 = 0, vw1 = 0;
+    uint32_t vn0 = 0, vn1 = 0;
+    if (a.is_value && active) {
+        if (fp8) {
+            const uint64_t *src = (const uint64_t *)(codes + (int64_t)tile * D * 8 + 2 * lane * 8);
+            vw0 = src[0];
+            vw1 = src[1];
+        } else {
+            const uint32_t *src = (const uint32_t *)(codes + (int64_t)tile * D * 4 + 2 * lane * 4);
+            vn0 = src[0];
+            vn1 = src[1];
+        }
+    }
+    for (int t = t_lo; t < t_hi; ++t) {
+        uint32_t *row = a.rows + ((plane * a.tokens) + (t - a.position)) * (int64_t)a.row_words;
+        uint8_t *rowb = (uint8_t *)row;
+        const int s = t & 7;
+        if (active) {
+            if (EXPORT) {
+                uint32_t c0, c1;
+                if (!a.is_value) {
+                    if (fp8) {
+                        c0 = codes[(int64_t)t * D + 2 * lane];
+                        c1 = codes[(int64_t)t * D + 2 * lane + 1];
+                    } else {
+                        const uint32_t by = codes[(int64_t)t * (D / 2) + lane];
+                        c0 = by & 15u;
+                        c1 = by >> 4;
+                    }
+                } else if (fp8) {
+                    c0 = (uint32_t)(vw0 >> (8 * s)) & 0xffu;
+                    c1 = (uint32_t)(vw1 >> (8 * s)) & 0xffu;
+                } else {
+                    c0 = (vn0 >> (4 * s)) & 15u;
+                    c1 = (vn1 >> (4 * s)) & 15u;
+                }
+                if (fp8) {
+                    rowb[2 * lane] = (uint8_t)c0;
+                    rowb[2 * lane + 1] = (uint8_t)c1;
+                } else {
+                    rowb[lane] = (uint8_t)(c0 | (c1 << 4));
+                }
+            } else {
+                uint32_t c0, c1;
+                if (fp8) {
+                    c0 = rowb[2 * lane];
+                    c1 = rowb[2 * lane + 1];
+                } else {
+                    c0 = rowb[lane] & 15u;
+                    c1 = rowb[lane] >> 4;
+                }
+                if (!a.is_value) {
+                    if (fp8) {
+                        codes[(int64_t)t * D + 2 * lane] = (uint8_t)c0;
+                        codes[(int64_t)t * D + 2 * lane + 1] = (uint8_t)c1;
+                    } else {
+                        codes[(int64_t)t * (D / 2) + lane] = (uint8_t)(c0 | (c1 << 4));
+                    }
+                } else if (fp8) {
+                    vw0 = (vw0 & ~(0xffull << (8 * s))) | ((uint64_t)c0 << (8 * s));
+                    vw1 = (vw1 & ~(0xffull << (8 * s))) | ((uint64_t)c1 << (8 * s));
+                } else {
+                    vn0 = (vn0 & ~(15u << (4 * s))) | (c0 << (4 * s));
+                    vn1 = (vn1 & ~(15u << (4 * s))) | (c1 << (4 * s));
+                }
+            }
+        }
+        if (lane == 0) {
+            uint32_t *aux = row + code_words;
+            uint32_t *rsc = aux + aux_words;
+            if (EXPORT) {
+                if (a.format == CQKV_FMT_MXFP4) {
+                    for (int w = 0; w < aux_words; ++w) aux[w] = 0;
+                    for (int k = 0; k < D / 32; ++k)
+                        aux[k >> 2] |= (uint32_t)scales[(int64_t)t * (D / 32) + k] << (8 * (k & 3));
+                    rsc[0] = __float_as_uint(1.0f);
+                } else {
+                    rsc[0] = ((const uint32_t *)scales)[t];
+                }
+                rsc[1] = 0;
+            } else {
+                if (a.format == CQKV_FMT_MXFP4) {
+                    for (int k = 0; k < D / 32; ++k)
+                        scales[(int64_t)t * (D / 32) + k] = (uint8_t)(aux[k >> 2] >> (8 * (k & 3)));
+                } else {
+                    ((uint32_t *)scales)[t] = rsc[0];
+                }
+            }
+        }
+    }
+    if (!EXPORT && a.is_value && active) {
+        if (fp8) {
+            uint64_t *dst = (uint64_t *)(codes + (int64_t)tile * D * 8 + 2 * lane * 8);
+            dst[0] = vw0;
+            dst[1] = vw1;
+        } else {
+            uint32_t *dst = (uint32_t *)(codes + (int64_t)tile * D * 4 + 2 * lane * 4);
+            dst[0] = vn0;
+            dst[1] = vn1;
+        }
+    }
+}
+
+static int convert(const cqkv_side *side, uint32_t *rows, int32_t batch, int32_t tokens,
+                   int32_t position, hipStream_t st, bool to_rows, const char *what) {
+    clear_error();
+    if (int rc = check_side(side, what)) return rc;
+    if (!rows) return fail(CQKV_ERR_ARG, "%s: null rows", what);
+    if (batch <= 0 || tokens < 0 || position < 0 || (int64_t)position + tokens > side->capacity)
+        return fail(CQKV_ERR_ARG, "%s: batch %d, tokens [%d, %d) outside the capacity %d", what,
+                    batch, position, position + tokens, side->capacity);
+    if (tokens == 0) return CQKV_OK;
+    ConvertArgs a = {};
+    a.rows = rows;
+    a.codes = (uint8_t *)side->codes;
+    a.scales = (uint8_t *)side->scales;
+    a.codes_plane = (uint32_t)cqkv_codes_plane_bytes(side->format, side->head_dim, side->capacity);
+    a.scales_plane = (uint32_t)cqkv_scales_plane_bytes(side->format, side->head_dim, side->capacity);
+    a.kv_heads = side->kv_heads;
+    a.tokens = tokens;
+    a.position = position;
+    a.row_words = cqkv_reference_row_words(side->format, side->head_dim);
+    a.format = side->format;
+    a.is_value = side->is_value;
+    a.head_dim = side->head_dim;
+    dim3 grid((tokens + 7) / 8 + 1, side->kv_heads, batch);
+    if (to_rows) hipLaunchKernelGGL(convert_kernel<true>, grid, dim3(64), 0, st, a);
+    else hipLaunchKernelGGL(convert_kernel<false>, grid, dim3(64), 0, st, a);
+    CQKV_HIP_CHECK(hipGetLastError());
+    return CQKV_OK;
+}
+
+}  // namespace cqkv
+
+extern "C" int cqkv_rows_import(const cqkv_side *side, const uint32_t *rows, int32_t batch,
+                                int32_t tokens, int32_t position, cqkv_stream_t stream) {
+    return cqkv::convert(side, const_cast<uint32_t *>(rows), batch, tokens, position,
+                         (hipStream_t)stream, false, "cqkv_rows_import");
+}
+
+extern "C" int cqkv_rows_export(const cqkv_side *side, uint32_t *rows, int32_t batch,
+                                int32_t tokens, int32_t position, cqkv_stream_t stream) {
+    return cqkv::convert(side, rows, batch, tokens, position, (hipStream_t)stream, true,
+                         "cqkv_rows_export");
+}

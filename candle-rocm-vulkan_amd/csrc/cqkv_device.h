@@ -1,0 +1,229 @@
+// Device-side building blocks of the cqkv kernels (gfx950 only): vector types, bounds-checked
+// buffer loads, the cache element codecs, and wavefront reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cqkv {
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// ---------------------------------------------------------------------------------------------
+// Buffer resources: a base pointer plus a byte range. Loads past the range return zeros, so a
+// plane read never leaves its plane whatever the lengths say.
+// ---------------------------------------------------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ inline rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    // word 3 = 0x00020000: 32-bit data format, raw (untyped) access
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+__device__ inline u32x4 ld128(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+__device__ inline u32x2 ld64(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+}
+__device__ inline uint32_t ld32(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+
+// ---------------------------------------------------------------------------------------------
+// 16-bit floats
+// ---------------------------------------------------------------------------------------------
+__device__ inline float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+__device__ inline float f16_bits_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+// f32 -> bf16 bits, round to nearest even (v_cvt_pk_bf16_f32)
+__device__ inline uint32_t f32_to_bf16_bits(float f) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
+}
+__device__ inline uint32_t pack_bf16x2(float lo, float hi) {
+    bf16x2 v;
+    v.x = (__bf16)lo;
+    v.y = (__bf16)hi;
+    return __builtin_bit_cast(uint32_t, v);
+}
+__device__ inline uint32_t pack_f16x2(float lo, float hi) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+}
+
+// Element dtype of q / k / v / out: 0 bf16, 1 f16, 2 f32 (the CQKV_* ids of cqkv.h).
+__device__ inline float load_elem(const void *p, int64_t idx, int dtype) {
+    if (dtype == 0) return bf16_bits_to_f32(((const uint16_t *)p)[idx]);
+    if (dtype == 1) return f16_bits_to_f32(((const uint16_t *)p)[idx]);
+    return ((const float *)p)[idx];
+}
+__device__ inline void store_elem(void *p, int64_t idx, int dtype, float v) {
+    if (dtype == 0) ((uint16_t *)p)[idx] = (uint16_t)f32_to_bf16_bits(v);
+    else if (dtype == 1) ((uint16_t *)p)[idx] = __builtin_bit_cast(uint16_t, (_Float16)v);
+    else ((float *)p)[idx] = v;
+}
+
+// ---------------------------------------------------------------------------------------------
+// E4M3 (OCP E4M3FN) and E2M1 / E8M0 codecs. The encoders are the reference's integer
+// algorithms (candle-core/src/accel/formats.rs:288-308, 329-350, 354-372): codes must be bit
+// for bit those of RowCodec::quantize_row.
+// ---------------------------------------------------------------------------------------------
+__device__ inline uint32_t e4m3_encode(float f) {
+    const uint32_t x = __float_as_uint(f);
+    const uint32_t s = (x >> 24) & 0x80u;
+    const uint32_t ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return s | 0x7fu;              // NaN
+    const float a = __uint_as_float(ax);
+    if (a >= 448.0f) return s | 0x7eu;                    // saturate (incl. inf)
+    if (a < 0.015625f) return s | (uint32_t)__builtin_rintf(a * 512.0f);  // subnormals, RNE
+    const uint32_t r = ax + 0x7ffffu + ((ax >> 20) & 1u);  // RNE at 3 mantissa bits
+    uint32_t code = (((r >> 23) - 120u) << 3) | ((r >> 20) & 7u);
+    return s | (code > 0x7eu ? 0x7eu : code);
+}
+
+__device__ inline uint32_t fp4_encode(float f) {
+    const uint32_t s = (__float_as_uint(f) >> 28) & 8u;
+    const float a = __builtin_fabsf(f);
+    uint32_t c;
+    if (!(a > 0.25f)) c = 0;  // also NaN
+    else if (a < 0.75f) c = 1;
+    else if (a <= 1.25f) c = 2;
+    else if (a < 1.75f) c = 3;
+    else if (a <= 2.5f) c = 4;
+    else if (a < 3.5f) c = 5;
+    else if (a <= 5.0f) c = 6;
+    else c = 7;
+    return s | c;
+}
+
+// E8M0 block-scale code of a block maximum: floor(log2 amax) - emax_elem + 127, clamped; 0 when
+// amax is zero, subnormal-exponent or not finite.
+__device__ inline uint32_t mx_scale_code(float amax, int emax_elem) {
+    const int be = (int)((__float_as_uint(amax) >> 23) & 0xffu);
+    int e = (amax > 0.0f && be != 0xff) ? (be == 0 ? -127 : be - 127) - emax_elem : -127;
+    e = e < -127 ? -127 : (e > 127 ? 127 : e);
+    return (uint32_t)(e + 127);
+}
+__device__ inline float e8m0_to_f32(uint32_t c) {
+    return c == 0 ? __uint_as_float(0x00400000u) : __uint_as_float(c << 23);
+}
+
+// Two E4M3 codes of `w` (bytes 0,1 when !hi, bytes 2,3 when hi) -> bf16x2, exact.
+__device__ inline uint32_t fp8x2_to_bf16x2(uint32_t w, bool hi) {
+    bf16x2 v = hi ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true)
+                  : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+    return __builtin_bit_cast(uint32_t, v);
+}
+// 8 E4M3 codes (two words, byte order) -> bf16x8.
+__device__ inline bf16x8 fp8x8_to_bf16x8(uint32_t w0, uint32_t w1) {
+    u32x4 r;
+    r.x = fp8x2_to_bf16x2(w0, false);
+    r.y = fp8x2_to_bf16x2(w0, true);
+    r.z = fp8x2_to_bf16x2(w1, false);
+    r.w = fp8x2_to_bf16x2(w1, true);
+    return __builtin_bit_cast(bf16x8, r);
+}
+
+// 8 E4M3 codes times a scale, rounded to bf16: bf16(scale * e4m3) in f32 arithmetic, the very
+// values of the reference's dequantized bf16 cache (RowCodec::dequantize_row then to_dtype,
+// candle-core/src/accel/turbo.rs:404-409, candle-nn/src/turbo_quant.rs:948-966).
+__device__ inline bf16x8 fp8x8_scaled_bf16x8(uint32_t w0, uint32_t w1, float scale) {
+    const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(w0, false);
+    const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8(w0, true);
+    const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8(w1, false);
+    const f32x2 d = __builtin_amdgcn_cvt_pk_f32_fp8(w1, true);
+    u32x4 r;
+    r.x = pack_bf16x2(a.x * scale, a.y * scale);
+    r.y = pack_bf16x2(b.x * scale, b.y * scale);
+    r.z = pack_bf16x2(c.x * scale, c.y * scale);
+    r.w = pack_bf16x2(d.x * scale, d.y * scale);
+    return __builtin_bit_cast(bf16x8, r);
+}
+// Same with one scale per code (value operands: 8 keys of one head dim).
+__device__ inline bf16x8 fp8x8_scaled_bf16x8(uint32_t w0, uint32_t w1, const float *sc) {
+    const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(w0, false);
+    const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8(w0, true);
+    const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8(w1, false);
+    const f32x2 d = __builtin_amdgcn_cvt_pk_f32_fp8(w1, true);
+    u32x4 r;
+    r.x = pack_bf16x2(a.x * sc[0], a.y * sc[1]);
+    r.y = pack_bf16x2(b.x * sc[2], b.y * sc[3]);
+    r.z = pack_bf16x2(c.x * sc[4], c.y * sc[5]);
+    r.w = pack_bf16x2(d.x * sc[6], d.y * sc[7]);
+    return __builtin_bit_cast(bf16x8, r);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Cross-lane helpers (ds_bpermute based shuffles; wave64)
+// ---------------------------------------------------------------------------------------------
+__device__ inline float shfl_xor(float v, int m) { return __shfl_xor(v, m, kWave); }
+__device__ inline float group16_max(float v) {  // max over lanes sharing lane % 16
+    v = fmaxf(v, shfl_xor(v, 16));
+    return fmaxf(v, shfl_xor(v, 32));
+}
+__device__ inline float group16_sum(float v) {
+    v += shfl_xor(v, 16);
+    return v + shfl_xor(v, 32);
+}
+__device__ inline float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));
+    return v;
+}
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
+    return v;
+}
+// max over aligned groups of `w` lanes (w a power of two <= 64)
+__device__ inline float group_max(float v, int w) {
+    for (int m = w >> 1; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));
+    return v;
+}
+
+// 8 floats -> bf16 hi + bf16 lo operands with hi + lo = x to 16 significant bits.
+__device__ inline void split_bf16x8(const float *x, bf16x8 &hi, bf16x8 &lo) {
+    u32x4 h, l;
+    uint32_t *hp = (uint32_t *)&h, *lp = (uint32_t *)&l;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        hp[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+        const float r0 = x[2 * i] - __uint_as_float(hp[i] << 16);
+        const float r1 = x[2 * i + 1] - __uint_as_float(hp[i] & 0xffff0000u);
+        lp[i] = pack_bf16x2(r0, r1);
+    }
+    hi = __builtin_bit_cast(bf16x8, h);
+    lo = __builtin_bit_cast(bf16x8, l);
+}
+
+// 8 floats -> f16 hi + f16 lo operands (22 significant bits for normal values).
+__device__ inline void split_f16x8(const float *x, f16x8 &hi, f16x8 &lo) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        hi[i] = (_Float16)x[i];
+        lo[i] = (_Float16)(x[i] - (float)hi[i]);
+    }
+}
+__device__ inline void split8(const float *x, bf16x8 &hi, bf16x8 &lo) { split_bf16x8(x, hi, lo); }
+__device__ inline void split8(const float *x, f16x8 &hi, f16x8 &lo) { split_f16x8(x, hi, lo); }
+
+__device__ inline f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ inline f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+}  // namespace cqkv

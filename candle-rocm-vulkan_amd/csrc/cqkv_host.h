@@ -1,0 +1,46 @@
+// Host-side helpers shared by the C-ABI entry points: per-thread error text, side checks,
+// plane sizes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/cqkv.h"
+
+namespace cqkv {
+
+void set_error(const std::string &msg);
+void clear_error();
+
+// Formats an error, stores it for cqkv_last_error() and returns `code`.
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+
+#define CQKV_HIP_CHECK(expr)                                                                   \
+    do {                                                                                       \
+        hipError_t e_ = (expr);                                                                \
+        if (e_ != hipSuccess)                                                                  \
+            return ::cqkv::fail(CQKV_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+// Code bits per element, or 0 for an unknown format.
+inline int code_bits(int32_t format) {
+    switch (format) {
+    case CQKV_FMT_FP8: return 8;
+    case CQKV_FMT_MXFP4:
+    case CQKV_FMT_TURBO4: return 4;
+    default: return 0;
+    }
+}
+
+inline bool supported_dim(int32_t d) { return d == 64 || d == 128; }
+
+// Validates a cache side; returns CQKV_OK or an error (message set).
+int check_side(const cqkv_side *s, const char *what);
+
+// Host tables of the TurboQuant format (see cqkv.h).
+int turbo_codebook(int dim, int bits, float *centroids, float *boundaries);
+void turbo_signs(int dim, uint64_t seed, float *signs);
+
+}  // namespace cqkv

@@ -1,0 +1,766 @@
+// Split-K flash-decode over the quantized cache, and the split combine (gfx950).
+//
+// Reference behaviour (paths relative to the reference repository root): TqAttn / tq_attention
+// (candle-core/src/rocm_backend/accel.rs:425-571; kernels tq_attng_core and tq_combine_impl in
+// candle-core/kernels/turbo_quant_impl.h:403-619, 659-685), masks of key_range
+// (candle-core/src/accel/attention.rs:80-92), the q rotation / o unrotation of the fused
+// TurboQuant path (candle-nn/src/turbo_quant.rs:1162-1167, 1263). Numerics follow the reference's
+// CPU path (softmax(scale q k^T) v over the dequantized cache, f32 accumulation) within the bf16
+// tolerance, not bit for bit.
+//
+// Kernel shape: one workgroup = 8 wavefronts = one (key split, kv head, batch).
+//  * Both products run on v_mfma_f32_16x16x32_bf16. MFMA columns are the (query, head) pairs of
+//    the GQA group (q_len * group <= 16); rows are keys (S^T = K Q^T) or head dims
+//    (O^T = V^T P^T).
+//  * A wavefront streams 32-key tiles with buffer loads straight into operand registers (two
+//    register sets, A/B, no copies) and decodes codes in registers: E4M3 -> bf16 exactly, E2M1
+//    with its E8M0 block scale exactly, TurboQuant nibbles through an LDS table of f16 pairs
+//    (TurboQuant runs its MFMAs in f16: codebook values are not bf16-exact).
+//    Loads of tiles past the split's end are aimed past the buffer range, so the hardware
+//    returns zeros without touching memory and the load schedule stays branch-free.
+//  * Key rows are row-major, so lane (r, g) loads the codes of key r for head-dim group g.
+//    Value codes are stored in 8-token transposed tiles, so lane (r, g) loads keys 8g..8g+7 of
+//    one head dim - the A operand of V^T P^T with no shuffle.
+//  * Online softmax runs in the exp2 domain on the S^T accumulator; lane (n, g) holds column n
+//    for keys 8g..8g+7, which is the B operand layout P^T needs. Only the running maximum is
+//    reduced across lanes. P^T enters the MFMA as a hi + lo pair of 16-bit operands.
+//  * The wavefronts of a workgroup interleave tiles and merge through LDS. With one split the
+//    workgroup writes the output; otherwise it writes its (o, lse) partial and combine_kernel
+//    merges the splits (tq_combine's formula), unrotating TurboQuant values. (A fused "last
+//    workgroup combines" variant needs agent-scope release fences, which write back the L2 of
+//    the XCD each time; measured at 6x the whole decode time, so the kernel boundary is used.)
+#include "cqkv_device.h"
+#include "cqkv_host.h"
+
+#include <type_traits>
+
+namespace cqkv {
+
+constexpr uint32_t kOOB = 0x80000000u;  // past every plane (planes are < 2 GiB)
+
+struct DecodeArgs {
+    const void *q;
+    int64_t q_sb, q_sh, q_si;
+    const uint8_t *kc, *ks, *vc, *vs;
+    uint32_t kc_plane, ks_plane, vc_plane, vs_plane;
+    const int32_t *kv_lens;
+    int32_t kv_len, q_dtype;
+    int32_t q_heads, kv_heads, group, q_len, ncols;
+    float scale_log2;  // softmax scale * log2(e)
+    int32_t wl, wr;
+    int32_t tiles_per_split, splits;
+    float *part_o;       // (splits, rows, D) f32, normalised partial outputs
+    float *part_lse;     // (splits, rows) f32, log2-domain lse of each split
+    void *out;
+    int32_t out_dtype, q_split;  // q_split: queries need a bf16 lo part (not bf16 inputs)
+    int64_t o_sb, o_sh, o_si;
+    uint32_t ksign_bits[4], vsign_bits[4];  // TURBO4 rotation signs (bit set -> -1)
+    float rot_scale;
+    float cent[16];  // TURBO4 codebook (the same for keys and values at one head dim)
+};
+
+// Visible keys [lo, hi) of query i of lq over lk keys (bottom-right aligned).
+__device__ inline void key_range(int i, int lq, int lk, int wl, int wr, int &lo, int &hi) {
+    const int pos = i + lk - lq;
+    lo = wl >= 0 ? max(pos - wl, 0) : 0;
+    hi = wr >= 0 ? min(pos + wr + 1, lk) : lk;
+    lo = min(lo, lk);
+    hi = max(hi, lo);
+}
+
+template <int D>
+__device__ inline void fwht_pairs_dec(float &v0, float &v1, int lane) {
+    float a = v0 + v1, b = v0 - v1;
+    v0 = a;
+    v1 = b;
+#pragma unroll
+    for (int m = 1; m < D / 2; m <<= 1) {
+        const float p0 = shfl_xor(v0, m), p1 = shfl_xor(v1, m);
+        const bool upper = (lane & m) != 0;
+        v0 = upper ? p0 - v0 : v0 + p0;
+        v1 = upper ? p1 - v1 : v1 + p1;
+    }
+}
+
+__device__ inline bool sign_bit(const uint32_t *bits, int j) { return (bits[j >> 5] >> (j & 31)) & 1u; }
+
+// Head dim held in k-slot e of MFMA chunk j by lane group g (the same for K and Q operands).
+template <int FMT, int D>
+__device__ inline int qdim(int j, int g, int e) {
+    if constexpr (FMT == CQKV_FMT_FP8) return 64 * (j >> 1) + 16 * g + 8 * (j & 1) + e;
+    else return (D / 4) * g + 8 * j + e;
+}
+
+// ---------------------------------------------------------------------------------------------
+// per-format tile registers, loads and decoders
+// ---------------------------------------------------------------------------------------------
+template <int FMT, int D>
+struct Tile {
+    // keys: 2 sub-tiles x D/32 code words (FP8: D/32 words = 4 per 16-key row chunk pair)
+    uint32_t k[2][FMT == CQKV_FMT_FP8 ? D / 16 : D / 32];
+    // values: D/32 chunks of 2 head dims x 8 keys (FP8 4 words, 4-bit 2 words)
+    uint32_t v[D / 32][FMT == CQKV_FMT_FP8 ? 4 : 2];
+    uint32_t kscale[2];  // per sub-tile, this lane's key: MXFP4 E8M0 block byte, FP8 f32 scale
+    uint32_t ks, vs;     // key lane % 32: TURBO4 norms, FP8 value scale, MXFP4 value block bytes
+};
+
+template <int FMT, int D>
+__device__ inline void load_tile(Tile<FMT, D> &r, int tile, bool live, int lane, rsrc_t kr,
+                                 rsrc_t ksr, rsrc_t vr, rsrc_t vsr) {
+    const int n = lane & 15, g = lane >> 4;
+    const uint32_t t0 = (uint32_t)tile * 32u;
+    const uint32_t oob = live ? 0u : kOOB;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        const uint32_t key = t0 + 8 * (n >> 2) + 4 * s + (n & 3);
+        if constexpr (FMT == CQKV_FMT_FP8) {
+#pragma unroll
+            for (int i = 0; i < D / 64; ++i) {
+                const u32x4 w = ld128(kr, (key * D + 16 * g + 64 * i) | oob);
+                r.k[s][4 * i + 0] = w.x;
+                r.k[s][4 * i + 1] = w.y;
+                r.k[s][4 * i + 2] = w.z;
+                r.k[s][4 * i + 3] = w.w;
+            }
+            r.kscale[s] = ld32(ksr, (key * 4) | oob);
+        } else {
+            if constexpr (D == 128) {
+                const u32x4 w = ld128(kr, (key * 64 + 16 * g) | oob);
+                r.k[s][0] = w.x;
+                r.k[s][1] = w.y;
+                r.k[s][2] = w.z;
+                r.k[s][3] = w.w;
+            } else {
+                const u32x2 w = ld64(kr, (key * 32 + 8 * g) | oob);
+                r.k[s][0] = w.x;
+                r.k[s][1] = w.y;
+            }
+            if constexpr (FMT == CQKV_FMT_MXFP4)
+                r.kscale[s] = __builtin_amdgcn_raw_buffer_load_b8(
+                    ksr, (key * (D / 32) + (D == 128 ? g : g >> 1)) | oob, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < D / 32; ++u) {
+        if constexpr (FMT == CQKV_FMT_FP8) {
+            const u32x4 w = ld128(vr, (((t0 / 8 + g) * D + 32 * u + 2 * n) * 8) | oob);
+            r.v[u][0] = w.x;
+            r.v[u][1] = w.y;
+            r.v[u][2] = w.z;
+            r.v[u][3] = w.w;
+        } else {
+            const u32x2 w = ld64(vr, (((t0 / 8 + g) * D + 32 * u + 2 * n) * 4) | oob);
+            r.v[u][0] = w.x;
+            r.v[u][1] = w.y;
+        }
+    }
+    const uint32_t kl = t0 + (lane & 31);
+    if constexpr (FMT == CQKV_FMT_MXFP4) {
+        r.vs = D == 128 ? ld32(vsr, (kl * 4) | oob)
+                        : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(vsr, (kl * 2) | oob, 0, 0);
+    } else if constexpr (FMT == CQKV_FMT_FP8) {
+        r.vs = ld32(vsr, (kl * 4) | oob);
+    } else {
+        r.ks = ld32(ksr, (kl * 4) | oob);
+        r.vs = ld32(vsr, (kl * 4) | oob);
+    }
+}
+
+__device__ inline uint32_t fp4x2_to_bf16x2(uint32_t w, int byte_sel, float scale) {
+    bf16x2 v;
+    switch (byte_sel) {  // the selector must be an immediate
+    case 0: v = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0); break;
+    case 1: v = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1); break;
+    case 2: v = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2); break;
+    default: v = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3); break;
+    }
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// MFMA operand type: bf16 for FP8 / MXFP4 (their codes decode exactly), f16 for TurboQuant
+// (codebook values, rotated queries: 11 significant bits instead of 8).
+template <int FMT>
+using op_t = typename std::conditional<FMT == CQKV_FMT_TURBO4, f16x8, bf16x8>::type;
+
+// 8 codes of one code word (4-bit) or two words (FP8) -> 8 operand values.
+template <int FMT>
+__device__ inline op_t<FMT> decode8(uint32_t w0, uint32_t w1, float scale, const uint32_t *tab) {
+    u32x4 r;
+    if constexpr (FMT == CQKV_FMT_FP8) {
+        return fp8x8_to_bf16x8(w0, w1);
+    } else if constexpr (FMT == CQKV_FMT_MXFP4) {
+        r.x = fp4x2_to_bf16x2(w0, 0, scale);
+        r.y = fp4x2_to_bf16x2(w0, 1, scale);
+        r.z = fp4x2_to_bf16x2(w0, 2, scale);
+        r.w = fp4x2_to_bf16x2(w0, 3, scale);
+    } else {
+        r.x = tab[w0 & 0xffu];
+        r.y = tab[(w0 >> 8) & 0xffu];
+        r.z = tab[(w0 >> 16) & 0xffu];
+        r.w = tab[w0 >> 24];
+    }
+    return __builtin_bit_cast(op_t<FMT>, r);
+}
+
+__device__ inline float e8m0_scale(uint32_t code) {  // code 0 marks an all-zero block
+    return code == 0 ? 0.0f : __uint_as_float(code << 23);
+}
+
+template <int FMT, int D>
+__device__ inline void compute_tile(Tile<FMT, D> &cur, int tile, const DecodeArgs &a,
+                                    const op_t<FMT> *qhi, const op_t<FMT> *qlo, bool q_split, int lane,
+                                    int lo, int hi, int lo_max, int hi_min, int L,
+                                    const uint32_t *tab, float &m_run, float &l_run,
+                                    f32x4 *acc) {
+    constexpr int NCH = D / 32;
+    const int g = lane >> 4;
+    const int t0 = tile * 32;
+    const bool full = t0 >= lo_max && t0 + 32 <= hi_min;
+
+    // S^T = K Q^T for the two 16-key sub-tiles
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+        op_t<FMT> k0, k1;
+        if constexpr (FMT == CQKV_FMT_FP8) {
+            k0 = fp8x8_scaled_bf16x8(cur.k[0][2 * j], cur.k[0][2 * j + 1], __uint_as_float(cur.kscale[0]));
+            k1 = fp8x8_scaled_bf16x8(cur.k[1][2 * j], cur.k[1][2 * j + 1], __uint_as_float(cur.kscale[1]));
+        } else {
+            float sc0 = 1.0f, sc1 = 1.0f;
+            if constexpr (FMT == CQKV_FMT_MXFP4) {
+                sc0 = cur.kscale[0] ? __uint_as_float(cur.kscale[0] << 23) : 1.0f;
+                sc1 = cur.kscale[1] ? __uint_as_float(cur.kscale[1] << 23) : 1.0f;
+            }
+            k0 = decode8<FMT>(cur.k[0][j], 0, sc0, tab);
+            k1 = decode8<FMT>(cur.k[1][j], 0, sc1, tab);
+        }
+        s0 = mfma16x16x32(k0, qhi[j], s0);
+        s1 = mfma16x16x32(k1, qhi[j], s1);
+        if (q_split) {
+            s0 = mfma16x16x32(k0, qlo[j], s0);
+            s1 = mfma16x16x32(k1, qlo[j], s1);
+        }
+    }
+    float x[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    const int kbase = t0 + 8 * g;  // x[e] is key kbase + e
+    if constexpr (FMT != CQKV_FMT_TURBO4) {  // scales are inside the operands
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] *= a.scale_log2;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            x[e] = x[e] * __uint_as_float((uint32_t)__shfl((int)cur.ks, 8 * g + e)) * a.scale_log2;
+    }
+    if (!full) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int key = kbase + e;
+            if (!(key >= lo && key < hi)) x[e] = -__builtin_inff();
+        }
+    }
+    float mx = x[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) mx = fmaxf(mx, x[e]);
+    mx = group16_max(mx);
+    const float m_new = fmaxf(m_run, mx);
+    const bool none = m_new == -__builtin_inff();
+    const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+    float p[8], psum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        p[e] = none ? 0.0f : __builtin_amdgcn_exp2f(x[e] - m_new);
+        psum += p[e];
+    }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int t = 0; t < 2 * NCH; ++t) acc[t] *= alpha;
+    }
+    // keys past the written length may hold any bytes: keep them out of PV
+    const int nv = min(max(L - kbase, 0), 8);
+    if (t0 + 32 > L) {  // uniform: only the tile holding the end of the keys
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) {
+            if constexpr (FMT == CQKV_FMT_FP8) {
+                const uint64_t keep = nv == 0 ? 0ull : (~0ull >> (64 - 8 * nv));
+                const uint64_t w0 = (((uint64_t)cur.v[u][1] << 32) | cur.v[u][0]) & keep;
+                const uint64_t w1 = (((uint64_t)cur.v[u][3] << 32) | cur.v[u][2]) & keep;
+                cur.v[u][0] = (uint32_t)w0;
+                cur.v[u][1] = (uint32_t)(w0 >> 32);
+                cur.v[u][2] = (uint32_t)w1;
+                cur.v[u][3] = (uint32_t)(w1 >> 32);
+            } else {
+                const uint32_t keep = nv == 0 ? 0u : (~0u >> (32 - 4 * nv));
+                cur.v[u][0] &= keep;
+                cur.v[u][1] &= keep;
+            }
+        }
+    }
+    // O^T += V^T P^T: d-tile 2u + h, row r <-> head dim 32u + 2r + h
+    if constexpr (FMT == CQKV_FMT_MXFP4) {
+        uint32_t vw[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vw[e] = (uint32_t)__shfl((int)cur.vs, 8 * g + e);
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) {  // value block u: P scaled by the keys' block-u scales
+            float pv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float sc = e8m0_scale((vw[e] >> (8 * u)) & 0xffu);
+                pv[e] = (e < nv && p[e] > 0.0f) ? p[e] * sc : 0.0f;
+            }
+            op_t<FMT> phi, plo;
+            split8(pv, phi, plo);
+            const op_t<FMT> v0 = decode8<FMT>(cur.v[u][0], 0, 1.0f, tab);
+            const op_t<FMT> v1 = decode8<FMT>(cur.v[u][1], 0, 1.0f, tab);
+            acc[2 * u] = mfma16x16x32(v0, phi, acc[2 * u]);
+            acc[2 * u + 1] = mfma16x16x32(v1, phi, acc[2 * u + 1]);
+            acc[2 * u] = mfma16x16x32(v0, plo, acc[2 * u]);
+            acc[2 * u + 1] = mfma16x16x32(v1, plo, acc[2 * u + 1]);
+        }
+    } else {
+        float pv[8], sv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            sv[e] = __uint_as_float((uint32_t)__shfl((int)cur.vs, 8 * g + e));
+            if (e >= nv) sv[e] = 0.0f;  // scales past the written length may be any bits
+            if constexpr (FMT == CQKV_FMT_FP8)  // the value scale is inside the V operand
+                pv[e] = (e < nv && p[e] > 0.0f) ? p[e] : 0.0f;
+            else
+                pv[e] = (e < nv && p[e] > 0.0f) ? p[e] * sv[e] : 0.0f;
+        }
+        op_t<FMT> phi, plo;
+        split8(pv, phi, plo);
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) {
+            op_t<FMT> v0, v1;
+            if constexpr (FMT == CQKV_FMT_FP8) {
+                v0 = fp8x8_scaled_bf16x8(cur.v[u][0], cur.v[u][1], sv);
+                v1 = fp8x8_scaled_bf16x8(cur.v[u][2], cur.v[u][3], sv);
+            } else {
+                v0 = decode8<FMT>(cur.v[u][0], 0, 1.0f, tab);
+                v1 = decode8<FMT>(cur.v[u][1], 0, 1.0f, tab);
+            }
+            acc[2 * u] = mfma16x16x32(v0, phi, acc[2 * u]);
+            acc[2 * u + 1] = mfma16x16x32(v1, phi, acc[2 * u + 1]);
+            acc[2 * u] = mfma16x16x32(v0, plo, acc[2 * u]);
+            acc[2 * u + 1] = mfma16x16x32(v1, plo, acc[2 * u + 1]);
+        }
+    }
+}
+
+template <int FMT, int D, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
+    constexpr int NCH = D / 32;
+    constexpr int NT = WAVES * 64;
+    constexpr bool kTurbo = FMT == CQKV_FMT_TURBO4;
+    __shared__ float sm_o[WAVES][16][D];
+    __shared__ float sm_fin[16][D];
+    __shared__ float sm_m[WAVES][16], sm_l[WAVES][16];
+    __shared__ uint32_t sm_tab[kTurbo ? 256 : 1];
+
+    const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+    // the wavefront index is uniform: keep it scalar so the tile loop stays a scalar loop
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 15, g = lane >> 4;
+    const int L = a.kv_lens ? __builtin_amdgcn_readfirstlane(min(max(a.kv_lens[b], 0), a.kv_len))
+                            : a.kv_len;
+
+    // visible key range of this lane's column, and the workgroup-wide bounds
+    const bool col_ok = n < a.ncols;
+    int lo, hi, lo_min, hi_max, lo_max, hi_min;
+    key_range(col_ok ? n / a.group : 0, a.q_len, L, a.wl, a.wr, lo, hi);
+    if (!col_ok) lo = hi = 0;
+    key_range(0, a.q_len, L, a.wl, a.wr, lo_min, hi_min);
+    key_range(a.q_len - 1, a.q_len, L, a.wl, a.wr, lo_max, hi_max);
+    const int tb = max(split * a.tiles_per_split, lo_min / 32);
+    const int te = min((split + 1) * a.tiles_per_split, (hi_max + 31) / 32);
+
+    // ---- queries (TURBO4: rotated, q Pi_k^T = sign-flip, Hadamard, 1/sqrt(D)) ----
+    float(*sm_q)[D] = sm_o[0];
+    for (int idx = threadIdx.x; idx < 16 * D; idx += NT) {
+        const int c = idx / D, d = idx % D;
+        float v = 0.0f;
+        if (c < a.ncols) {
+            const int head = hk * a.group + c % a.group, qi = c / a.group;
+            v = load_elem(a.q, (int64_t)b * a.q_sb + (int64_t)head * a.q_sh + (int64_t)qi * a.q_si + d,
+                          a.q_dtype);
+        }
+        sm_q[c][d] = v;
+    }
+    if constexpr (kTurbo) {
+        for (int i = threadIdx.x; i < 256; i += NT)  // byte i = code pair (i & 15, i >> 4)
+            sm_tab[i] = pack_f16x2(a.cent[i & 15], a.cent[i >> 4]);
+    }
+    __syncthreads();
+    if constexpr (kTurbo) {
+        for (int c = wave; c < a.ncols; c += WAVES) {
+            const bool act = lane < D / 2;
+            float v0 = act ? sm_q[c][2 * lane] : 0.0f, v1 = act ? sm_q[c][2 * lane + 1] : 0.0f;
+            if (act && sign_bit(a.ksign_bits, 2 * lane)) v0 = -v0;
+            if (act && sign_bit(a.ksign_bits, 2 * lane + 1)) v1 = -v1;
+            fwht_pairs_dec<D>(v0, v1, lane);
+            if (act) {
+                sm_q[c][2 * lane] = v0 * a.rot_scale;
+                sm_q[c][2 * lane + 1] = v1 * a.rot_scale;
+            }
+        }
+        __syncthreads();
+    }
+    op_t<FMT> qhi[NCH], qlo[NCH];
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+        float qv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qv[e] = sm_q[n][qdim<FMT, D>(j, g, e)];
+        split8(qv, qhi[j], qlo[j]);
+    }
+    const bool q_split = a.q_split != 0;
+    __syncthreads();
+
+    // ---- stream the tiles of this split ----
+    const int64_t plane = (int64_t)b * a.kv_heads + hk;
+    const rsrc_t kr = make_rsrc(a.kc + plane * a.kc_plane, a.kc_plane);
+    const rsrc_t ksr = make_rsrc(a.ks + plane * a.ks_plane, a.ks_plane);
+    const rsrc_t vr = make_rsrc(a.vc + plane * a.vc_plane, a.vc_plane);
+    const rsrc_t vsr = make_rsrc(a.vs + plane * a.vs_plane, a.vs_plane);
+
+    f32x4 acc[2 * NCH];
+#pragma unroll
+    for (int t = 0; t < 2 * NCH; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -__builtin_inff(), l_run = 0.0f;
+
+    // Register sets A and B alternate; the scheduling barriers keep every load of one set
+    // issued before the next set's, so each wait only covers the set about to be used.
+    Tile<FMT, D> ta, tb2;
+    int t = tb + wave;
+    load_tile<FMT, D>(ta, t, t < te, lane, kr, ksr, vr, vsr);
+    __builtin_amdgcn_sched_barrier(0);
+    load_tile<FMT, D>(tb2, t + WAVES, t + WAVES < te, lane, kr, ksr, vr, vsr);
+    __builtin_amdgcn_sched_barrier(0);
+    for (; t < te; t += 2 * WAVES) {
+        compute_tile<FMT, D>(ta, t, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min, L, sm_tab,
+                             m_run, l_run, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        load_tile<FMT, D>(ta, t + 2 * WAVES, t + 2 * WAVES < te, lane, kr, ksr, vr, vsr);
+        __builtin_amdgcn_sched_barrier(0);
+        if (t + WAVES < te)
+            compute_tile<FMT, D>(tb2, t + WAVES, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min,
+                                 L, sm_tab, m_run, l_run, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        load_tile<FMT, D>(tb2, t + 3 * WAVES, t + 3 * WAVES < te, lane, kr, ksr, vr, vsr);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- merge the wavefronts ----
+    const float l_col = group16_sum(l_run);
+#pragma unroll
+    for (int u = 0; u < NCH; ++u)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sm_o[wave][n][32 * u + 8 * g + 2 * i + h] = acc[2 * u + h][i];
+    if (g == 0) {
+        sm_m[wave][n] = m_run;
+        sm_l[wave][n] = l_col;
+    }
+    __syncthreads();
+    const int rows = (int)gridDim.z * a.q_heads * a.q_len;
+    const bool single = a.splits == 1;
+    for (int idx = threadIdx.x; idx < a.ncols * D; idx += NT) {
+        const int c = idx / D, d = idx % D;
+        float M = -__builtin_inff();
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) M = fmaxf(M, sm_m[w][c]);
+        float o = 0.0f, lse = -__builtin_inff();
+        if (M != -__builtin_inff()) {
+            float wsum = 0.0f, osum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) {
+                const float f = __builtin_amdgcn_exp2f(sm_m[w][c] - M);
+                wsum += sm_l[w][c] * f;
+                osum += sm_o[w][c][d] * f;
+            }
+            o = osum / wsum;
+            lse = M + __builtin_log2f(wsum);
+        }
+        const int head = hk * a.group + c % a.group, qi = c / a.group;
+        if (!single) {  // the partial of this split; combine_kernel merges the splits
+            const int64_t row = ((int64_t)b * a.q_heads + head) * a.q_len + qi;
+            a.part_o[((int64_t)split * rows + row) * D + d] = o;
+            if (d == 0) a.part_lse[(int64_t)split * rows + row] = lse;
+        } else if (kTurbo) {
+            sm_fin[c][d] = o;
+        } else {
+            store_elem(a.out, (int64_t)b * a.o_sb + (int64_t)head * a.o_sh + (int64_t)qi * a.o_si + d,
+                       a.out_dtype, o);
+        }
+    }
+    if (!single || !kTurbo) return;
+    __syncthreads();
+    // ---- single split, TURBO4: unrotate with the value rotation, x = sign * H o / sqrt(D) ----
+    for (int c = wave; c < a.ncols; c += WAVES) {
+        const bool act = lane < D / 2;
+        float v0 = act ? sm_fin[c][2 * lane] : 0.0f, v1 = act ? sm_fin[c][2 * lane + 1] : 0.0f;
+        fwht_pairs_dec<D>(v0, v1, lane);
+        v0 *= a.rot_scale;
+        v1 *= a.rot_scale;
+        if (act) {
+            if (sign_bit(a.vsign_bits, 2 * lane)) v0 = -v0;
+            if (sign_bit(a.vsign_bits, 2 * lane + 1)) v1 = -v1;
+            const int head = hk * a.group + c % a.group, qi = c / a.group;
+            const int64_t base =
+                (int64_t)b * a.o_sb + (int64_t)head * a.o_sh + (int64_t)qi * a.o_si + 2 * lane;
+            store_elem(a.out, base, a.out_dtype, v0);
+            store_elem(a.out, base + 1, a.out_dtype, v1);
+        }
+    }
+}
+
+struct CombineArgs {
+    const float *part_o, *part_lse;
+    int32_t splits, rows, q_heads, q_len, out_dtype, rotate;
+    void *out;
+    int64_t o_sb, o_sh, o_si;
+    uint32_t vsign_bits[4];
+    float rot_scale;
+};
+
+// Split combine (the formula of tq_combine_impl, candle-core/kernels/turbo_quant_impl.h:659-685,
+// in the log2 domain): o = sum_s w_s o_s / sum_s w_s, w_s = 2^(lse_s - max lse), empty splits
+// skipped; then, for TurboQuant values, x = sign * (H o) / sqrt(D) (the unrotation y Pi).
+// One wavefront per output row (lane l: head dims 2l, 2l+1), four rows per workgroup; the
+// split loop keeps up to 8 splits' loads in flight.
+template <int D>
+__global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= a.rows) return;
+    const bool active = lane < D / 2;
+    const float *lse = a.part_lse + row;
+    float M = -__builtin_inff();
+    for (int s = 0; s < a.splits; ++s) M = fmaxf(M, lse[(int64_t)s * a.rows]);
+    float o0 = 0.0f, o1 = 0.0f;
+    if (M != -__builtin_inff()) {
+        float wsum = 0.0f, a0 = 0.0f, a1 = 0.0f;
+        const float *po = a.part_o + (int64_t)row * D + 2 * (active ? lane : 0);
+        const int64_t step = (int64_t)a.rows * D;
+#pragma unroll 8
+        for (int s = 0; s < a.splits; ++s) {
+            const float e = lse[(int64_t)s * a.rows];
+            const f32x2 v = *(const f32x2 *)(po + s * step);
+            const float w = e == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(e - M);
+            wsum += w;
+            a0 += w * v.x;
+            a1 += w * v.y;
+        }
+        o0 = a0 / wsum;
+        o1 = a1 / wsum;
+    }
+    if (a.rotate) {
+        fwht_pairs_dec<D>(o0, o1, lane);
+        o0 *= a.rot_scale;
+        o1 *= a.rot_scale;
+        if (active && sign_bit(a.vsign_bits, 2 * lane)) o0 = -o0;
+        if (active && sign_bit(a.vsign_bits, 2 * lane + 1)) o1 = -o1;
+    }
+    if (!active) return;
+    const int qi = row % a.q_len, head = (row / a.q_len) % a.q_heads;
+    const int b = row / (a.q_len * a.q_heads);
+    const int64_t base = (int64_t)b * a.o_sb + (int64_t)head * a.o_sh + (int64_t)qi * a.o_si + 2 * lane;
+    store_elem(a.out, base, a.out_dtype, o0);
+    store_elem(a.out, base + 1, a.out_dtype, o1);
+}
+
+int fill_turbo_args(const cqkv_side *s, uint32_t sign_bits[4], float *rot_scale, float bnd[16]);
+
+static int tiles_of(int kv_len) { return (kv_len + 31) / 32; }
+
+// Key splits per (batch, kv head). One 8-wavefront workgroup per plane fills a CU of the
+// MI355X (256 CUs, two waves per SIMD at this register budget): split only when there are fewer
+// planes than CUs, and then into pieces of at least 16 tiles (two per wavefront). Ragged batches
+// (per-sequence lengths) are split into pieces of at most 128 tiles (4096 keys) so long and short
+// sequences even out across CUs.
+constexpr int kWaves = 8;
+constexpr int kCUs = 256;
+
+static int auto_splits(int batch, int kv_heads, int kv_len, bool ragged) {
+    const int planes = batch * kv_heads;
+    const int tiles = tiles_of(kv_len);
+    int s = (kCUs + planes - 1) / planes;
+    if (ragged) s = max(s, (tiles + 127) / 128);
+    s = min(s, max(1, tiles / 16));
+    s = max(1, min(s, 256));
+    const int tps = (tiles + s - 1) / s;
+    return max(1, (tiles + tps - 1) / tps);
+}
+
+template <int FMT>
+static void launch_decode(int d, dim3 grid, hipStream_t st, const DecodeArgs &a) {
+    if (d == 64)
+        hipLaunchKernelGGL((decode_kernel<FMT, 64, kWaves>), grid, dim3(kWaves * 64), 0, st, a);
+    else
+        hipLaunchKernelGGL((decode_kernel<FMT, 128, kWaves>), grid, dim3(kWaves * 64), 0, st, a);
+}
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Workspace: partial outputs (splits, rows, D) f32 | partial lse (splits, rows) f32.
+static size_t workspace_layout(int32_t batch, int32_t q_heads, int32_t q_len, int32_t head_dim,
+                               int32_t splits, size_t *lse_off) {
+    const size_t rows = (size_t)batch * q_heads * q_len;
+    *lse_off = align256((size_t)splits * rows * head_dim * 4);
+    return *lse_off + align256((size_t)splits * rows * 4);
+}
+
+}  // namespace cqkv
+
+using namespace cqkv;
+
+extern "C" int32_t cqkv_decode_splits(int32_t batch, int32_t kv_heads, int32_t kv_len) {
+    if (batch <= 0 || kv_heads <= 0 || kv_len <= 0) return 1;
+    return auto_splits(batch, kv_heads, kv_len, false);
+}
+
+extern "C" size_t cqkv_decode_workspace_bytes(int32_t batch, int32_t q_heads, int32_t q_len,
+                                              int32_t head_dim, int32_t splits) {
+    if (batch <= 0 || q_heads <= 0 || q_len <= 0 || head_dim <= 0 || splits <= 0) return 0;
+    size_t lse_off;
+    return workspace_layout(batch, q_heads, q_len, head_dim, splits, &lse_off);
+}
+
+extern "C" int cqkv_decode_attention(const void *q, int32_t q_dtype, const int64_t q_strides[3],
+                                     const cqkv_side *k, const cqkv_side *v, int32_t batch,
+                                     int32_t q_heads, int32_t q_len, const int32_t *kv_lens,
+                                     int32_t kv_len, float softmax_scale, int32_t window_left,
+                                     int32_t window_right, void *out, int32_t out_dtype,
+                                     const int64_t out_strides[3], int32_t splits,
+                                     void *workspace, size_t workspace_bytes,
+                                     cqkv_stream_t stream) {
+    clear_error();
+    if (int rc = check_side(k, "cqkv_decode_attention (keys)")) return rc;
+    if (int rc = check_side(v, "cqkv_decode_attention (values)")) return rc;
+    if (k->is_value != 0 || v->is_value != 1)
+        return fail(CQKV_ERR_ARG, "cqkv_decode_attention: expected a key side and a value side");
+    if (k->format != v->format || k->head_dim != v->head_dim || k->kv_heads != v->kv_heads ||
+        k->capacity != v->capacity)
+        return fail(CQKV_ERR_ARG, "cqkv_decode_attention: key / value sides differ in format, D, heads or capacity");
+    if (!q || !out || !q_strides || !out_strides)
+        return fail(CQKV_ERR_ARG, "cqkv_decode_attention: null q / out / strides");
+    if (q_dtype < CQKV_BF16 || q_dtype > CQKV_F32 || out_dtype < CQKV_BF16 || out_dtype > CQKV_F32)
+        return fail(CQKV_ERR_ARG, "cqkv_decode_attention: dtypes q %d out %d", q_dtype, out_dtype);
+    const int hkv = k->kv_heads, d = k->head_dim;
+    if (batch <= 0 || q_heads <= 0 || q_len <= 0 || q_heads % hkv != 0)
+        return fail(CQKV_ERR_ARG, "cqkv_decode_attention: batch %d q_heads %d q_len %d kv_heads %d",
+                    batch, q_heads, q_len, hkv);
+    const int group = q_heads / hkv;
+    if (group * q_len > 16)
+        return fail(CQKV_ERR_ARG, "cqkv_decode_attention: q_len * q_heads / kv_heads = %d > 16",
+                    group * q_len);
+    if (kv_len < 0 || kv_len > k->capacity)
+        return fail(CQKV_ERR_ARG, "cqkv_decode_attention: kv_len %d outside [0, capacity %d]",
+                    kv_len, k->capacity);
+    if (splits < 0) return fail(CQKV_ERR_ARG, "cqkv_decode_attention: splits %d", splits);
+
+    const int tiles = max(1, tiles_of(kv_len));
+    int s = splits > 0 ? min(splits, tiles)
+                       : auto_splits(batch, hkv, max(kv_len, 1), kv_lens != nullptr);
+    const int tps = (tiles + s - 1) / s;
+    s = (tiles + tps - 1) / tps;
+
+    DecodeArgs a = {};
+    a.q = q;
+    a.q_sb = q_strides[0];
+    a.q_sh = q_strides[1];
+    a.q_si = q_strides[2];
+    a.q_dtype = q_dtype;
+    a.kc = (const uint8_t *)k->codes;
+    a.ks = (const uint8_t *)k->scales;
+    a.vc = (const uint8_t *)v->codes;
+    a.vs = (const uint8_t *)v->scales;
+    a.kc_plane = (uint32_t)cqkv_codes_plane_bytes(k->format, d, k->capacity);
+    a.ks_plane = (uint32_t)cqkv_scales_plane_bytes(k->format, d, k->capacity);
+    a.vc_plane = (uint32_t)cqkv_codes_plane_bytes(v->format, d, v->capacity);
+    a.vs_plane = (uint32_t)cqkv_scales_plane_bytes(v->format, d, v->capacity);
+    a.kv_lens = kv_lens;
+    a.kv_len = kv_len;
+    a.q_heads = q_heads;
+    a.kv_heads = hkv;
+    a.group = group;
+    a.q_len = q_len;
+    a.ncols = group * q_len;
+    a.scale_log2 = softmax_scale * kLog2e;
+    a.wl = window_left;
+    a.wr = window_right;
+    a.tiles_per_split = tps;
+    a.splits = s;
+    a.out = out;
+    a.out_dtype = out_dtype;
+    a.q_split = (q_dtype != CQKV_BF16 || k->format == CQKV_FMT_TURBO4) ? 1 : 0;
+    a.o_sb = out_strides[0];
+    a.o_sh = out_strides[1];
+    a.o_si = out_strides[2];
+    const bool rotate = k->format == CQKV_FMT_TURBO4;
+    if (rotate) {
+        float bnd[16], cent[16];
+        if (int rc = fill_turbo_args(k, a.ksign_bits, &a.rot_scale, bnd)) return rc;
+        if (int rc = fill_turbo_args(v, a.vsign_bits, &a.rot_scale, bnd)) return rc;
+        if (turbo_codebook(d, 4, cent, bnd) != 0)
+            return fail(CQKV_ERR_ARG, "cqkv_decode_attention: turbo codebook D=%d", d);
+        for (int i = 0; i < 16; ++i) a.cent[i] = cent[i];
+    }
+
+    hipStream_t st = (hipStream_t)stream;
+    void *ws = workspace;
+    bool owned = false;
+    if (s > 1) {
+        size_t lse_off;
+        const size_t need = workspace_layout(batch, q_heads, q_len, d, s, &lse_off);
+        if (ws && workspace_bytes < need)
+            return fail(CQKV_ERR_WORKSPACE, "cqkv_decode_attention: workspace %zu < %zu bytes",
+                        workspace_bytes, need);
+        if (!ws) {
+            CQKV_HIP_CHECK(hipMallocAsync(&ws, need, st));
+            owned = true;
+        }
+        a.part_o = (float *)ws;
+        a.part_lse = (float *)((char *)ws + lse_off);
+    }
+
+    dim3 grid(s, hkv, batch);
+    switch (k->format) {
+    case CQKV_FMT_FP8: launch_decode<CQKV_FMT_FP8>(d, grid, st, a); break;
+    case CQKV_FMT_MXFP4: launch_decode<CQKV_FMT_MXFP4>(d, grid, st, a); break;
+    default: launch_decode<CQKV_FMT_TURBO4>(d, grid, st, a); break;
+    }
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && s > 1) {
+        CombineArgs c = {};
+        c.part_o = a.part_o;
+        c.part_lse = a.part_lse;
+        c.splits = s;
+        c.rows = batch * q_heads * q_len;
+        c.q_heads = q_heads;
+        c.q_len = q_len;
+        c.out_dtype = out_dtype;
+        c.rotate = rotate ? 1 : 0;
+        c.out = out;
+        c.o_sb = a.o_sb;
+        c.o_sh = a.o_sh;
+        c.o_si = a.o_si;
+        for (int i = 0; i < 4; ++i) c.vsign_bits[i] = a.vsign_bits[i];
+        c.rot_scale = a.rot_scale;
+        const dim3 cg((c.rows + 3) / 4);
+        if (d == 64) hipLaunchKernelGGL(combine_kernel<64>, cg, dim3(256), 0, st, c);
+        else hipLaunchKernelGGL(combine_kernel<128>, cg, dim3(256), 0, st, c);
+        e = hipGetLastError();
+    }
+    if (owned) {
+        hipError_t fe = hipFreeAsync(ws, st);
+        if (e == hipSuccess) e = fe;
+    }
+    if (e != hipSuccess)
+        return fail(CQKV_ERR_HIP, "cqkv_decode_attention: launch failed: %s", hipGetErrorString(e));
+    return CQKV_OK;
+}

@@ -1,0 +1,166 @@
+// Host side of the C ABI that launches nothing: error text, plane sizes, side checks and the
+// TurboQuant tables (Lloyd-Max codebook, Hadamard signs).
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "cqkv_host.h"
+
+namespace cqkv {
+
+static thread_local std::string g_error;
+
+void set_error(const std::string &msg) { g_error = msg; }
+void clear_error() { g_error.clear(); }
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return code;
+}
+
+int check_side(const cqkv_side *s, const char *what) {
+    if (!s) return fail(CQKV_ERR_ARG, "%s: null cache side", what);
+    if (!code_bits(s->format)) return fail(CQKV_ERR_ARG, "%s: unknown format %d", what, s->format);
+    if (!supported_dim(s->head_dim))
+        return fail(CQKV_ERR_ARG, "%s: head_dim %d not supported (64, 128)", what, s->head_dim);
+    if (s->kv_heads <= 0) return fail(CQKV_ERR_ARG, "%s: kv_heads %d", what, s->kv_heads);
+    if (s->capacity <= 0 || s->capacity % 32 != 0)
+        return fail(CQKV_ERR_ARG, "%s: capacity %d is not a positive multiple of 32", what,
+                    s->capacity);
+    if (!s->codes || !s->scales) return fail(CQKV_ERR_ARG, "%s: null codes / scales", what);
+    if (s->is_value != 0 && s->is_value != 1)
+        return fail(CQKV_ERR_ARG, "%s: is_value must be 0 or 1", what);
+    const size_t cb = cqkv_codes_plane_bytes(s->format, s->head_dim, s->capacity);
+    if (cb > 0x7fffffffull)
+        return fail(CQKV_ERR_ARG, "%s: a plane of %zu bytes exceeds 2 GiB", what, cb);
+    return CQKV_OK;
+}
+
+// Lloyd-Max quantizer of one coordinate of a uniform random unit vector in R^dim, whose density
+// is proportional to (1 - x^2)^((dim - 3) / 2). Same algorithm and constants as the reference
+// (candle-core/src/accel/turbo.rs:58-129): a 2^16-point midpoint grid over
+// |x| < min(1, 12 / sqrt(dim)), quantile initialisation, at most 2000 Lloyd iterations stopped
+// at a 1e-12 centroid move, exact symmetrisation, f32 centroids and midpoint boundaries. The
+// float64 sums run in index order so that the f32 tables come out identical.
+int turbo_codebook(int dim, int bits, float *centroids, float *boundaries) {
+    if (bits < 1 || bits > 4 || dim < 2) return -1;
+    const int k = 1 << bits;
+    const size_t n = size_t(1) << 16;
+    const double lim = std::min(1.0, 12.0 / sqrt((double)dim));
+    const double step = 2.0 * lim / (double)n;
+    const double expo = ((double)dim - 3.0) / 2.0;
+    std::vector<double> grid(n), mass(n), cmass(n + 1, 0.0), cmom(n + 1, 0.0);
+    double total = 0.0;
+    for (size_t i = 0; i < n; ++i) {
+        grid[i] = -lim + ((double)i + 0.5) * step;
+        mass[i] = exp(expo * log(std::max(1.0 - grid[i] * grid[i], 1e-300)));
+    }
+    for (size_t i = 0; i < n; ++i) total += mass[i];
+    for (size_t i = 0; i < n; ++i) mass[i] /= total;
+    for (size_t i = 0; i < n; ++i) {
+        cmass[i + 1] = cmass[i] + mass[i];
+        cmom[i + 1] = cmom[i] + mass[i] * grid[i];
+    }
+    auto first_not_below = [](const std::vector<double> &v, size_t len, double x) {
+        return (size_t)(std::lower_bound(v.begin(), v.begin() + len, x) - v.begin());
+    };
+    double c[16], b[16];
+    for (int i = 0; i < k; ++i) {
+        const double p = ((double)i + 0.5) / (double)k;
+        size_t j = first_not_below(cmass, n + 1, p);
+        j = std::min(std::max(j, (size_t)1), n);
+        c[i] = grid[j - 1];
+    }
+    for (int it = 0; it < 2000; ++it) {
+        for (int i = 0; i + 1 < k; ++i) b[i] = 0.5 * (c[i] + c[i + 1]);
+        double moved = 0.0;
+        size_t lo = 0;
+        for (int i = 0; i < k; ++i) {
+            const size_t hi = i + 1 < k ? first_not_below(grid, n, b[i]) : n;
+            const double m = cmass[hi] - cmass[lo];
+            if (m > 0.0) {
+                const double mean = (cmom[hi] - cmom[lo]) / m;
+                moved = std::max(moved, fabs(mean - c[i]));
+                c[i] = mean;
+            }
+            lo = hi;
+        }
+        if (moved < 1e-12) break;
+    }
+    for (int i = 0; i < k / 2; ++i) {
+        const double h = 0.5 * (c[k - 1 - i] - c[i]);
+        c[i] = -h;
+        c[k - 1 - i] = h;
+    }
+    for (int i = 0; i < k; ++i) centroids[i] = (float)c[i];
+    for (int i = 0; i + 1 < k; ++i) boundaries[i] = (float)(0.5 * (c[i] + c[i + 1]));
+    return 0;
+}
+
+// Column signs of the seeded Hadamard rotation: SplitMix64 seeded with seed ^ "HADAMARD"
+// (0x484144414d415244 in ASCII), one draw per column, even draw -> +1
+// (candle-core/src/accel/turbo.rs:150-163, 188-196).
+void turbo_signs(int dim, uint64_t seed, float *signs) {
+    uint64_t state = seed ^ 0x484144414d415244ull;
+    for (int j = 0; j < dim; ++j) {
+        state += 0x9e3779b97f4a7c15ull;
+        uint64_t z = state;
+        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+        z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+        z ^= z >> 31;
+        signs[j] = (z & 1) == 0 ? 1.0f : -1.0f;
+    }
+}
+
+}  // namespace cqkv
+
+extern "C" {
+
+size_t cqkv_codes_plane_bytes(int32_t format, int32_t head_dim, int32_t capacity) {
+    const int bits = cqkv::code_bits(format);
+    if (!bits || !cqkv::supported_dim(head_dim) || capacity <= 0) return 0;
+    return (size_t)capacity * (size_t)head_dim * (size_t)bits / 8;
+}
+
+size_t cqkv_scales_plane_bytes(int32_t format, int32_t head_dim, int32_t capacity) {
+    if (!cqkv::code_bits(format) || !cqkv::supported_dim(head_dim) || capacity <= 0) return 0;
+    if (format == CQKV_FMT_MXFP4) return (size_t)capacity * (size_t)(head_dim / 32);
+    return (size_t)capacity * 4;
+}
+
+int32_t cqkv_reference_row_words(int32_t format, int32_t head_dim) {
+    const int bits = cqkv::code_bits(format);
+    if (!bits || !cqkv::supported_dim(head_dim)) return 0;
+    const int code_words = (head_dim * bits + 31) / 32;
+    const int aux_words = format == CQKV_FMT_MXFP4 ? (head_dim / 32 + 3) / 4 : 0;
+    return code_words + aux_words + 2;
+}
+
+int cqkv_turbo_codebook(int32_t head_dim, int32_t bits, float *centroids, float *boundaries) {
+    if (!centroids || !boundaries)
+        return cqkv::fail(CQKV_ERR_ARG, "cqkv_turbo_codebook: null output");
+    if (cqkv::turbo_codebook(head_dim, bits, centroids, boundaries) != 0)
+        return cqkv::fail(CQKV_ERR_ARG, "cqkv_turbo_codebook: bits %d / dim %d", bits, head_dim);
+    return CQKV_OK;
+}
+
+int cqkv_turbo_signs(int32_t head_dim, uint64_t seed, float *signs) {
+    if (!signs || head_dim <= 0 || (head_dim & (head_dim - 1)) != 0)
+        return cqkv::fail(CQKV_ERR_ARG, "cqkv_turbo_signs: head_dim %d", head_dim);
+    cqkv::turbo_signs(head_dim, seed, signs);
+    return CQKV_OK;
+}
+
+const char *cqkv_last_error(void) { return cqkv::g_error.c_str(); }
+
+const char *cqkv_version(void) { return "cqkv 0.1 gfx950"; }
+
+}  // extern "C"

@@ -1,0 +1,147 @@
+/*
+ * cqkv: MI355X (gfx950) quantized-KV fused attention, C ABI.
+ *
+ * This is the drop-in boundary of the quantized-KV attention path of the candle fork
+ * Qntology/candle-rocm-vulkan. Every entry point is a host function taking device pointers,
+ * explicit sizes / strides and a hipStream_t (NULL = the legacy stream the reference launches on),
+ * and returning CQKV_OK or a negative status; cqkv_last_error() gives the message of the last
+ * failure of the calling thread. No call allocates device memory except cqkv_decode_attention when
+ * it is given no workspace. Nothing here holds torch or candle types.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository root):
+ *   cqkv_quant_append      RocmStorage::tq_quantize + Cache::append
+ *                          (candle-core/src/rocm_backend/accel.rs:269-303,
+ *                           candle-nn/src/turbo_quant.rs:916-945, candle-nn/src/kv_cache.rs:68-99)
+ *   cqkv_decode_attention  RocmStorage::tq_attention (+ tq_combine)
+ *                          (candle-core/src/rocm_backend/accel.rs:425-571,
+ *                           candle-nn/src/turbo_quant.rs:1143-1264)
+ *   cqkv_flash_attn        RocmStorage::flash_attn (candle-core/src/rocm_backend/accel.rs:54-158),
+ *                          behind candle_flash_attn::flash_attn (candle-flash-attn/src/lib.rs:149)
+ *   cqkv_rows_import /     the reference's packed row layout [codes][aux][rsc0][rsc1]
+ *   cqkv_rows_export       (candle-core/src/accel/formats.rs:206-242)
+ *
+ * Cache layout in HBM (one "plane" per (batch, kv head), planes batch-major, `capacity` tokens):
+ *   format        codes plane (bytes)                  scales plane (bytes)
+ *   FP8   keys    capacity * D      row-major          capacity * 4   f32 absmax/448 per token
+ *   FP8   values  capacity * D      8-token tiles      capacity * 4   f32 per token
+ *   MXFP4 keys    capacity * D/2    row-major nibbles  capacity * D/32  E8M0 per 32-element block
+ *   MXFP4 values  capacity * D/2    8-token tiles      capacity * D/32  E8M0
+ *   TURBO4 keys   capacity * D/2    row-major nibbles  capacity * 4   f32 norm per token
+ *   TURBO4 values capacity * D/2    8-token tiles      capacity * 4   f32 norm
+ * Row-major: token t's codes at t * row_bytes, element j at byte j (FP8) or nibble j (bits 4(j%2)
+ * of byte j/2), i.e. the reference's code stream. 8-token tiles (values): token t, element j at
+ * tile t/8, offset j*8 + t%8 bytes (FP8) or bits 4(t%8) of the little-endian u32 j (4-bit). The
+ * code values are the reference encoders' codes bit for bit; only their positions differ.
+ */
+#ifndef CQKV_H
+#define CQKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *cqkv_stream_t; /* == hipStream_t */
+
+/* Status codes. */
+enum {
+    CQKV_OK = 0,
+    CQKV_ERR_ARG = -1,      /* invalid argument / unsupported shape (the reference's bail!) */
+    CQKV_ERR_HIP = -2,      /* a HIP runtime call failed (the reference's RocmError::Hip) */
+    CQKV_ERR_WORKSPACE = -3 /* workspace too small */
+};
+
+/* Cache formats: the reference's kernel mode ids (candle-core/src/accel/formats.rs:41-48).
+ * TURBO4 = TurboQuant MSE, 4 bits, Hadamard rotation (QuantFormat::TurboMse{bits: 4}). */
+enum { CQKV_FMT_TURBO4 = 0, CQKV_FMT_MXFP4 = 2, CQKV_FMT_FP8 = 5 };
+
+/* Element types of q / k / v / outputs. */
+enum { CQKV_BF16 = 0, CQKV_F16 = 1, CQKV_F32 = 2 };
+
+/* One side (keys or values) of a quantized cache. */
+typedef struct cqkv_side {
+    int32_t format;    /* CQKV_FMT_* */
+    int32_t is_value;  /* 0 keys (row-major codes), 1 values (8-token tiles) */
+    int32_t head_dim;  /* D: 64 or 128 */
+    int32_t kv_heads;  /* Hkv */
+    int32_t capacity;  /* tokens per plane, a multiple of 32 */
+    int32_t reserved;
+    uint64_t seed;     /* TURBO4 rotation seed (keys 42, values 44 by default); else unused */
+    void *codes;       /* device, batch * kv_heads planes of cqkv_codes_plane_bytes() */
+    void *scales;      /* device, batch * kv_heads planes of cqkv_scales_plane_bytes() */
+} cqkv_side;
+
+/* Bytes of one (batch, head) plane of codes / scales; 0 for an invalid format or D. */
+size_t cqkv_codes_plane_bytes(int32_t format, int32_t head_dim, int32_t capacity);
+size_t cqkv_scales_plane_bytes(int32_t format, int32_t head_dim, int32_t capacity);
+
+/* Quantize-and-append (RowCodec::quantize_row per (token, head) row, turbo.rs:293-381, then the
+ * Cache::append copy): x is (batch, kv_heads, tokens, D) with element strides x_strides[0..2] for
+ * batch, head and token (D contiguous), dtype CQKV_BF16 / F16 / F32. Token i of batch b lands at
+ * position positions[b] + i (device int32 array of `batch`) or, when positions is NULL, at
+ * `position` + i. Positions past the capacity are an error when positions is NULL and are
+ * skipped otherwise (the device array is not read on the host). */
+int cqkv_quant_append(const cqkv_side *side, const void *x, int32_t x_dtype,
+                      const int64_t x_strides[3], int32_t batch, int32_t tokens,
+                      const int32_t *positions, int32_t position, cqkv_stream_t stream);
+
+/* Decode attention over a quantized cache (TqAttn + tq_combine, bottom-right aligned masks of
+ * candle-core/src/accel/attention.rs:80-92):
+ *   q   (batch, q_heads, q_len, D), element strides q_strides[0..2] for batch, head, query;
+ *   out same shape, strides out_strides, dtype out_dtype;
+ *   keys [0, kv_lens[b]) of plane b are attended (device int32 array; NULL: kv_len for all),
+ *   kv_len = the largest length (host), used to size the launch;
+ *   window_left / window_right: -1 = unbounded (causal = (-1, 0));
+ *   q head h reads kv head h / (q_heads / kv_heads); q_len * (q_heads / kv_heads) <= 16.
+ * splits: key splits per (batch, kv head); 0 = automatic. workspace: device scratch of at least
+ * cqkv_decode_workspace_bytes(); NULL = allocated (and freed) by the call. */
+size_t cqkv_decode_workspace_bytes(int32_t batch, int32_t q_heads, int32_t q_len, int32_t head_dim,
+                                   int32_t splits);
+int32_t cqkv_decode_splits(int32_t batch, int32_t kv_heads, int32_t kv_len);
+int cqkv_decode_attention(const void *q, int32_t q_dtype, const int64_t q_strides[3],
+                          const cqkv_side *k, const cqkv_side *v, int32_t batch, int32_t q_heads,
+                          int32_t q_len, const int32_t *kv_lens, int32_t kv_len,
+                          float softmax_scale, int32_t window_left, int32_t window_right,
+                          void *out, int32_t out_dtype, const int64_t out_strides[3],
+                          int32_t splits, void *workspace, size_t workspace_bytes,
+                          cqkv_stream_t stream);
+
+/* Dense bf16 flash attention (FlashAttnOp / candle_flash_attn::flash_attn):
+ *   q (batch, q_len, q_heads, D), k / v (batch, kv_len, kv_heads, D), out like q, all bf16 with
+ *   element strides {batch, token, head} (D contiguous); bottom-right aligned windows;
+ *   causal = window (-1, 0). When k_cache / v_cache are non-NULL (FP8 sides) the same call also
+ *   quantizes and appends k / v at positions [position, position + kv_len) of the cache. */
+int cqkv_flash_attn(const void *q, const int64_t q_strides[3], const void *k,
+                    const int64_t k_strides[3], const void *v, const int64_t v_strides[3],
+                    void *out, const int64_t out_strides[3], int32_t batch, int32_t q_len,
+                    int32_t kv_len, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                    float softmax_scale, int32_t window_left, int32_t window_right,
+                    const cqkv_side *k_cache, const cqkv_side *v_cache, int32_t position,
+                    cqkv_stream_t stream);
+
+/* Reference row layout interop (candle-core/src/accel/formats.rs:206-242): rows are
+ * (batch, kv_heads, tokens, row_words) u32 on the device, row_words = code + aux + 2 words.
+ * import: rows -> cache positions [position, position + tokens); export: the reverse. */
+int32_t cqkv_reference_row_words(int32_t format, int32_t head_dim);
+int cqkv_rows_import(const cqkv_side *side, const uint32_t *rows, int32_t batch, int32_t tokens,
+                     int32_t position, cqkv_stream_t stream);
+int cqkv_rows_export(const cqkv_side *side, uint32_t *rows, int32_t batch, int32_t tokens,
+                     int32_t position, cqkv_stream_t stream);
+
+/* TurboQuant tables the kernels use (host): the Lloyd-Max codebook of TurboMse{bits} at head
+ * dim D (candle-core/src/accel/turbo.rs:58-129; 2^bits centroids, 2^bits - 1 boundaries) and
+ * the Hadamard sign vector of `seed` (turbo.rs:188-203; +1 / -1 per column). */
+int cqkv_turbo_codebook(int32_t head_dim, int32_t bits, float *centroids, float *boundaries);
+int cqkv_turbo_signs(int32_t head_dim, uint64_t seed, float *signs);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *cqkv_last_error(void);
+/* Library version string, e.g. "cqkv 0.1 gfx950". */
+const char *cqkv_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,113 @@
+"""The C-ABI library on the CPU: it loads, exports every entry point include/cqkv.h declares,
+its host-only functions agree with the oracle, and argument errors come back as status codes
+(no GPU call is made by any of these)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "cqkv.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(cqkv_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(cq):
+    names = declared_symbols()
+    assert len(names) >= 14
+    lib = ctypes.CDLL(cq.LIB_PATH)
+    for n in names:
+        assert hasattr(lib, n), n
+    assert sorted(cq.EXPORTED) == names
+
+
+def test_version(cq):
+    assert cq.lib().cqkv_version().decode().startswith("cqkv")
+
+
+def test_plane_sizes(cq):
+    L = cq.lib()
+    assert L.cqkv_codes_plane_bytes(cq.FP8, 128, 8192) == 8192 * 128
+    assert L.cqkv_scales_plane_bytes(cq.FP8, 128, 8192) == 8192 * 4
+    assert L.cqkv_codes_plane_bytes(cq.MXFP4, 128, 64) == 64 * 64
+    assert L.cqkv_scales_plane_bytes(cq.MXFP4, 128, 64) == 64 * 4
+    assert L.cqkv_scales_plane_bytes(cq.MXFP4, 64, 64) == 64 * 2
+    assert L.cqkv_codes_plane_bytes(cq.TURBO4, 128, 32) == 32 * 64
+    assert L.cqkv_codes_plane_bytes(cq.FP8, 96, 32) == 0
+    assert L.cqkv_codes_plane_bytes(7, 128, 32) == 0
+
+
+@pytest.mark.parametrize("fmt,bits", [(5, 0), (2, 0), (0, 4)])
+@pytest.mark.parametrize("d", [64, 128])
+def test_reference_row_words_match_oracle_layout(cq, fmt, bits, d):
+    # candle-core/src/accel/formats.rs:224-242, restated by the oracle
+    assert cq.reference_row_words(fmt, d) == O.row_layout(fmt, bits, d).row_words
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_turbo_codebook_identical_to_oracle(cq, d):
+    c, b = cq.turbo_codebook(d, 4)
+    oc, ob = O.lloyd_max(d, 4)
+    np.testing.assert_array_equal(c, oc)
+    np.testing.assert_array_equal(b, ob)
+
+
+@pytest.mark.parametrize("d,seed", [(64, 7), (128, 42), (128, 44)])
+def test_turbo_signs_match_oracle_rotation(cq, d, seed):
+    s = cq.turbo_signs(d, seed)
+    m = O.rotation_matrix(d, O.ROT_HADAMARD, seed)
+    # row 0 of the Sylvester matrix is all +1: Pi[0][j] = sign_j / sqrt(d)
+    np.testing.assert_array_equal(np.sign(m[0]), s)
+
+
+def test_workspace_and_split_plan(cq):
+    assert cq.decode_workspace_bytes(32, 32, 1, 128, 8) >= 8 * 1024 * 129 * 4
+    assert cq.decode_workspace_bytes(0, 32, 1, 128, 8) == 0
+    s = cq.decode_splits(32, 8, 8192)
+    assert 1 <= s <= 256
+    assert cq.decode_splits(1, 8, 512) >= 1
+
+
+def test_argument_errors_are_status_codes(cq):
+    L = cq.lib()
+    x = (ctypes.c_int64 * 3)(1, 1, 1)
+    assert L.cqkv_quant_append(None, None, 0, x, 1, 1, None, 0, None) == cq.ERR_ARG
+    assert b"null cache side" in L.cqkv_last_error()
+    side = cq.Side(cq.FP8, 0, 96, 8, 64, 0, 0, 1, 1)
+    assert L.cqkv_quant_append(ctypes.byref(side), ctypes.c_void_p(1), 0, x, 1, 1, None, 0,
+                               None) == cq.ERR_ARG
+    assert b"head_dim 96" in L.cqkv_last_error()
+    side = cq.Side(cq.FP8, 0, 128, 8, 48, 0, 0, 1, 1)
+    assert L.cqkv_quant_append(ctypes.byref(side), ctypes.c_void_p(1), 0, x, 1, 1, None, 0,
+                               None) == cq.ERR_ARG
+    assert b"multiple of 32" in L.cqkv_last_error()
+    side = cq.Side(cq.FP8, 0, 128, 8, 64, 0, 0, 1, 1)
+    # appending past the capacity is refused before any launch
+    assert L.cqkv_quant_append(ctypes.byref(side), ctypes.c_void_p(1), 0, x, 1, 10, None, 60,
+                               None) == cq.ERR_ARG
+    assert b"exceed the capacity" in L.cqkv_last_error()
+    # decode: a key side given twice, GQA groups too wide, kv_len past the capacity
+    vs = cq.Side(cq.FP8, 1, 128, 8, 64, 0, 0, 1, 1)
+    args = lambda k, v, hq, lq, kvlen: L.cqkv_decode_attention(
+        ctypes.c_void_p(1), 0, x, ctypes.byref(k), ctypes.byref(v), 1, hq, lq, None, kvlen,
+        0.1, -1, -1, ctypes.c_void_p(1), 0, x, 0, None, 0, None)
+    assert args(side, side, 8, 1, 10) == cq.ERR_ARG
+    assert args(side, vs, 8 * 32, 1, 10) == cq.ERR_ARG
+    assert args(side, vs, 8 * 4, 5, 10) == cq.ERR_ARG
+    assert args(side, vs, 8, 1, 65) == cq.ERR_ARG
+    assert b"capacity" in L.cqkv_last_error()
+
+
+def test_gpu_entry_points_refuse_cpu_tensors(cq):
+    torch = pytest.importorskip("torch")
+    side = cq.CacheSide(cq.FP8, False, 1, 1, 64, 32, torch.zeros(1, dtype=torch.uint8),
+                        torch.zeros(1, dtype=torch.uint8))
+    with pytest.raises(cq.CqkvError):
+        cq.quant_append(side, torch.zeros(1, 1, 1, 64))
