@@ -5,6 +5,8 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <map>
+#include <mutex>
 #include <vector>
 
 #include "cqkv_host.h"
@@ -50,8 +52,7 @@ int check_side(const cqkv_side *s, const char *what) {
 // |x| < min(1, 12 / sqrt(dim)), quantile initialisation, at most 2000 Lloyd iterations stopped
 // at a 1e-12 centroid move, exact symmetrisation, f32 centroids and midpoint boundaries. The
 // float64 sums run in index order so that the f32 tables come out identical.
-int turbo_codebook(int dim, int bits, float *centroids, float *boundaries) {
-    if (bits < 1 || bits > 4 || dim < 2) return -1;
+static int turbo_codebook_compute(int dim, int bits, float *centroids, float *boundaries) {
     const int k = 1 << bits;
     const size_t n = size_t(1) << 16;
     const double lim = std::min(1.0, 12.0 / sqrt((double)dim));
@@ -102,6 +103,29 @@ int turbo_codebook(int dim, int bits, float *centroids, float *boundaries) {
     }
     for (int i = 0; i < k; ++i) centroids[i] = (float)c[i];
     for (int i = 0; i + 1 < k; ++i) boundaries[i] = (float)(0.5 * (c[i] + c[i + 1]));
+    return 0;
+}
+
+// The codebook of (dim, bits), computed once per process and cached (the reference caches it
+// per (dim, bits) too, candle-core/src/accel/turbo.rs:131-146): every quantize / decode call
+// needs it, and computing it takes milliseconds.
+int turbo_codebook(int dim, int bits, float *centroids, float *boundaries) {
+    if (bits < 1 || bits > 4 || dim < 2 || dim > 1024) return -1;
+    struct Entry {
+        float c[16], b[16];
+    };
+    static std::mutex mu;
+    static std::map<std::pair<int, int>, Entry> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find({dim, bits});
+    if (it == cache.end()) {
+        Entry e;
+        if (turbo_codebook_compute(dim, bits, e.c, e.b) != 0) return -1;
+        it = cache.emplace(std::make_pair(dim, bits), e).first;
+    }
+    const int k = 1 << bits;
+    for (int i = 0; i < k; ++i) centroids[i] = it->second.c[i];
+    for (int i = 0; i + 1 < k; ++i) boundaries[i] = it->second.b[i];
     return 0;
 }
 
