@@ -9,7 +9,8 @@
 // windows (causal = (-1, 0), candle-core/src/accel/attention.rs:80-92), bf16 in / out, f32
 // accumulation; rows with no visible key give zeros.
 //
-// Kernel shape (one workgroup = 4 wavefronts = 64 queries of 4 query heads sharing a kv head):
+// Kernel shape (one workgroup = 8 wavefronts = 64 queries x 4 query heads sharing a kv head, 32
+// queries per wavefront):
 //  * Both products run on v_mfma_f32_32x32x16_bf16. S^T = K Q^T: K (32 keys x 16 dims) comes
 //    from LDS with ds_read_b128, Q^T stays in registers for the whole key loop. The S^T
 //    accumulator of a lane holds one query column, so the row-wise online softmax needs one
@@ -18,9 +19,10 @@
 //  * V^T operands come from the row-major V tile in LDS through ds_read_b64_tr_b16: in each
 //    16-lane group, source lane 4p+q points at V[key0 + p][d0 + 4q .. +3], and lane i receives
 //    V[key0 .. key0 + 3][d0 + i] - four keys of one head dim, the k-slots the MFMA needs.
-//  * K / V tiles of 64 keys are double-buffered in LDS (rows padded to 288 B so the row reads of
-//    ds_read_b128 and the 4-row groups of the transposing reads hit distinct banks); the next
-//    tile's global loads are in flight while the current one is computed, one barrier per tile.
+//  * K / V tiles of 64 keys stream through a 4-stage LDS ring with asynchronous global -> LDS
+//    copies (global_load_lds_dwordx4), issued three tiles ahead; one barrier per tile. Chunks of
+//    a row are XOR-swizzled so both LDS read patterns are free of bank conflicts.
+//  * Two wavefronts per SIMD: one's softmax (VALU) overlaps the other's MFMAs.
 //  * Causal work is uneven: the workgroups with the most key tiles are dispatched first.
 #include "cqkv_device.h"
 #include "cqkv_host.h"
@@ -32,10 +34,8 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 constexpr int kPfD = 128;          // head dim
-constexpr int kPfBQ = 64;          // queries per wavefront (and per workgroup)
+constexpr int kPfBQ = 64;          // queries per workgroup (two wavefronts of 32 per head)
 constexpr int kPfBK = 64;          // keys per tile
-constexpr int kPfPitch = 288;      // LDS bytes per key row (256 + 32 padding)
-constexpr int kPfTile = kPfBK * kPfPitch;  // one K or V tile in LDS
 
 struct PrefillArgs {
     const uint16_t *q, *k, *v;
@@ -44,7 +44,7 @@ struct PrefillArgs {
     int64_t k_sb, k_st, k_sh;
     int64_t v_sb, v_st, v_sh;
     int64_t o_sb, o_st, o_sh;
-    int32_t q_len, kv_len, q_heads, kv_heads, group, heads_per_wg, q_blocks;
+    int32_t q_len, kv_len, q_heads, kv_heads, group, heads_per_wg, q_blocks, batch;
     int32_t wl, wr;
     float scale_log2;
 };
@@ -64,201 +64,263 @@ __device__ inline void pf_key_range(int i, int lq, int lk, int wl, int wr, int &
     hi = max(hi, lo);
 }
 
-__global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // 2 stages x (K, V)
+// LDS tile layout: 64 rows (keys) x 256 B (128 bf16 dims), no padding; the 16-byte chunk c of
+// row r sits at chunk position c ^ swz(r). swz takes 16 distinct values over any 16 consecutive
+// rows (the 16 rows of one ds_read_b128 pass) and 4 distinct even offsets over 4 consecutive
+// rows (the 4 rows x 2 chunks of one ds_read_b64_tr_b16 group), so both read patterns are
+// conflict-free.
+__device__ inline int swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+constexpr int kPfWaves = 8;               // 4 query heads x 2 halves of the 64 queries
+constexpr int kPfRow = 256;
+constexpr int kPfHalf = kPfBK * kPfRow;   // one K or V tile: 16 KB
+constexpr int kPfStage = 2 * kPfHalf;     // K then V
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+#define PF_INLINE __device__ __attribute__((always_inline)) inline
+
+// Asynchronous global -> LDS copy of key tile kt (K and V) into `stage`: wavefront w copies rows
+// 8w .. 8w+7 of each, 4 rows (1 KB) per global_load_lds_dwordx4. Lane l writes chunk position
+// l % 16 of row l / 16, so it loads logical chunk (l % 16) ^ swz(row). Rows past the keys repeat
+// the last key (finite values; they are masked out).
+PF_INLINE void pf_issue_tile(uint8_t *stage, const uint16_t *kplane, const uint16_t *vplane,
+                             int64_t k_st, int64_t v_st, int kt, int kv_len, int wave, int lane) {
+#pragma unroll
+    for (int r4 = 0; r4 < 2; ++r4) {
+        const int row = 8 * wave + 4 * r4 + (lane >> 4);
+        const int key = min(kt * kPfBK + row, kv_len - 1);
+        const int c = (lane & 15) ^ swz(row);
+        __builtin_amdgcn_global_load_lds((const void *)(kplane + (int64_t)key * k_st + 8 * c),
+                                         (lds_void *)(stage + (8 * wave + 4 * r4) * kPfRow), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void *)(vplane + (int64_t)key * v_st + 8 * c),
+                                         (lds_void *)(stage + kPfHalf + (8 * wave + 4 * r4) * kPfRow),
+                                         16, 0, 0);
+    }
+}
+constexpr int kPfCopiesPerTile = 4;  // global_load_lds per wavefront per tile
+
+// s_waitcnt vmcnt(n) (gfx9 encoding; expcnt and lgkmcnt left at their maxima)
+#define PF_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | 0x0f70)
+
+struct PfState {
+    bf16x8 qop[8];   // Q^T operands (16-dim steps ks) of this wavefront's 32 queries
+    f32x16 acc[4];   // O^T: 32-dim block md
+    float m_run, l_run;
+    int qlo, qhi;    // visible keys of this lane's query
+};
+
+// S^T (64 keys x 32 queries) = K Q^T for the tile at k_lds.
+PF_INLINE void pf_qk(f32x16 (&s)[2], const PfState &st, const uint8_t *k_lds, int lane) {
+    const int qr = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+        s[mb] = f32x16{};
+        const int row = 32 * mb + qr;
+        const uint8_t *rbase = k_lds + row * kPfRow;
+        const int sw = swz(row);
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            const bf16x8 kop =
+                __builtin_bit_cast(bf16x8, *(const u32x4 *)(rbase + (((2 * ks + h) ^ sw) << 4)));
+            s[mb] = mfma32x32x16(kop, st.qop[ks], s[mb]);
+        }
+    }
+}
+
+// masks scores of keys outside the lane's visible range (tiles that cross a range end only)
+PF_INLINE void pf_mask(f32x16 (&s)[2], const PfState &st, int k0, int lane) {
+    const int h = lane >> 5;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int key = k0 + 32 * mb + 8 * (j >> 2) + 4 * h + (j & 3);
+            if (!(key >= st.qlo && key < st.qhi)) s[mb][j] = -__builtin_inff();
+        }
+}
+
+// Online softmax over the tile: P^T operands of the four 16-key steps, running maximum (lazy:
+// kept unless exceeded by more than 2^8, so p < 2^8 and rescaling is rare) and row sum.
+PF_INLINE void pf_softmax(bf16x8 (&pop)[4], const f32x16 (&s)[2], PfState &st, float scale_log2) {
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[mb][j]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
+    const float m_new = mx > st.m_run + 8.0f ? mx : st.m_run;
+    const bool none = m_new == -__builtin_inff();
+    const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(st.m_run - m_new);
+    const float mneg = none ? 0.0f : m_new;
+    float psum = 0.0f;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            float p[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                p[e] = __builtin_amdgcn_exp2f(s[mb][8 * half + e] * scale_log2 - mneg);
+                psum += p[e];
+            }
+            u32x4 w;
+            w.x = pack_bf16x2(p[0], p[1]);
+            w.y = pack_bf16x2(p[2], p[3]);
+            w.z = pack_bf16x2(p[4], p[5]);
+            w.w = pack_bf16x2(p[6], p[7]);
+            pop[2 * mb + half] = __builtin_bit_cast(bf16x8, w);
+        }
+    st.l_run = st.l_run * alpha + psum;
+    st.m_run = m_new;
+    if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int md = 0; md < 4; ++md) st.acc[md] *= alpha;
+    }
+}
+
+// O^T += V^T P^T over the tile at v_lds; 16-key step kk = keys 32 (kk / 2) + 16 (kk % 2) +
+// [0, 16), whose k order matches the S^T accumulator registers 8 (kk % 2) .. +7 of block kk / 2.
+PF_INLINE void pf_pv(PfState &st, const bf16x8 (&pop)[4], const uint8_t *v_lds, int lane) {
+    const int h = lane >> 5, g16 = lane >> 4, idx = lane & 15, sp = idx >> 2, sq = idx & 3;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+        const int r0 = 32 * (kk >> 1) + 16 * (kk & 1) + 4 * h + sp;
+        const int r1 = r0 + 8;
+        const int sw0 = swz(r0), sw1 = swz(r1);
+#pragma unroll
+        for (int md = 0; md < 4; ++md) {
+            const int d = 32 * md + 16 * (g16 & 1) + 4 * sq;
+            const int c = d >> 3, sub = (d & 7) * 2;
+            const s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4 *)(v_lds + r0 * kPfRow + ((c ^ sw0) << 4) + sub));
+            const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4 *)(v_lds + r1 * kPfRow + ((c ^ sw1) << 4) + sub));
+            const u32x2 l2 = __builtin_bit_cast(u32x2, lo4), h2 = __builtin_bit_cast(u32x2, hi4);
+            const bf16x8 vt = __builtin_bit_cast(bf16x8, u32x4{l2.x, l2.y, h2.x, h2.y});
+            st.acc[md] = mfma32x32x16(vt, pop[kk], st.acc[md]);
+        }
+    }
+}
+
+PF_INLINE void pf_tile(PfState &st, const uint8_t *stage, int k0, bool full, float scale_log2,
+                       int lane) {
+    f32x16 s[2];
+    bf16x8 pop[4];
+    pf_qk(s, st, stage, lane);
+    if (!full) pf_mask(s, st, k0, lane);
+    pf_softmax(pop, s, st, scale_log2);
+    pf_pv(st, pop, stage + kPfHalf, lane);
+}
+
+// Two wavefronts per SIMD (8 per workgroup, ~200 registers each): while one runs its softmax on
+// the VALU, the other's MFMAs run.
+__global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a) {
+    // four K/V stages as distinct arrays, each named statically below, so the compiler can tell
+    // the asynchronous copy into one stage from the reads of another (a dynamically selected
+    // stage makes it wait for every copy before every LDS read)
+    __shared__ __attribute__((aligned(1024))) uint8_t stage0[kPfStage];
+    __shared__ __attribute__((aligned(1024))) uint8_t stage1[kPfStage];
+    __shared__ __attribute__((aligned(1024))) uint8_t stage2[kPfStage];
+    __shared__ __attribute__((aligned(1024))) uint8_t stage3[kPfStage];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int qr = lane & 31, h = lane >> 5;  // MFMA column / half
+    const int qr = lane & 31, h = lane >> 5;
 
-    // heaviest query blocks first
-    const int qb = a.q_blocks - 1 - (int)blockIdx.x;
-    const int hk = blockIdx.y % a.kv_heads;
-    const int hgrp = blockIdx.y / a.kv_heads;
-    const int b = blockIdx.z;
-    const int head = hk * a.group + hgrp * a.heads_per_wg + wave;
-    const bool wave_live = wave < a.heads_per_wg;
+    // 1-D grid: consecutive workgroup ids walk the planes (batch, kv head, head group) first, so
+    // the workgroups of one plane share an XCD (ids are dealt round-robin to the 8 XCDs) and its
+    // L2; the query blocks with the most key tiles come first.
+    const int hgroups = a.group / a.heads_per_wg;
+    const int nplanes = a.kv_heads * hgroups * a.batch;
+    const int plane = (int)blockIdx.x % nplanes;
+    const int qb = a.q_blocks - 1 - (int)blockIdx.x / nplanes;
+    const int b = plane / (a.kv_heads * hgroups);
+    const int rem = plane % (a.kv_heads * hgroups);
+    const int hk = rem % a.kv_heads, hgrp = rem / a.kv_heads;
+    const int hslot = wave & 3, qhalf = wave >> 2;
+    const int head = hk * a.group + hgrp * a.heads_per_wg + hslot;
+    const bool wave_live = hslot < a.heads_per_wg;
     const int q0 = qb * kPfBQ;
 
-    // key tiles this workgroup visits
     int lo_first, hi_first, lo_last, hi_last;
     pf_key_range(q0, a.q_len, a.kv_len, a.wl, a.wr, lo_first, hi_first);
     pf_key_range(min(q0 + kPfBQ, a.q_len) - 1, a.q_len, a.kv_len, a.wl, a.wr, lo_last, hi_last);
     const int kt_begin = lo_first / kPfBK;
-    const int kt_end = (hi_last + kPfBK - 1) / kPfBK;
+    const int ntiles = (hi_last + kPfBK - 1) / kPfBK - kt_begin;
 
-    // ---- Q^T operands (B of S^T = K Q^T): lane (qr, h), N-block nb, k-step ks -> 8 dims ----
-    bf16x8 qop[2][8];
-    const uint16_t *qbase = a.q + (int64_t)b * a.q_sb + (int64_t)min(head, a.q_heads - 1) * a.q_sh;
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-        const int qi = q0 + 32 * nb + qr;
+    PfState st;
+    {
+        const int qi = q0 + 32 * qhalf + qr;
         const bool ok = wave_live && qi < a.q_len;
-        const uint16_t *row = qbase + (int64_t)min(qi, a.q_len - 1) * a.q_st;
+        const uint16_t *row = a.q + (int64_t)b * a.q_sb + (int64_t)min(head, a.q_heads - 1) * a.q_sh +
+                              (int64_t)min(qi, a.q_len - 1) * a.q_st;
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
             u32x4 w = ok ? ldg128(row + 16 * ks + 8 * h) : u32x4{0u, 0u, 0u, 0u};
-            qop[nb][ks] = __builtin_bit_cast(bf16x8, w);
+            st.qop[ks] = __builtin_bit_cast(bf16x8, w);
         }
+        if (qi < a.q_len) pf_key_range(qi, a.q_len, a.kv_len, a.wl, a.wr, st.qlo, st.qhi);
+        else st.qlo = st.qhi = 0;
+        st.m_run = -__builtin_inff();
+        st.l_run = 0.0f;
+#pragma unroll
+        for (int md = 0; md < 4; ++md) st.acc[md] = f32x16{};
     }
 
-    // per-lane query rows of the two N-blocks and their visible key ranges
-    int qlo[2], qhi[2];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-        const int qi = q0 + 32 * nb + qr;
-        if (qi < a.q_len) pf_key_range(qi, a.q_len, a.kv_len, a.wl, a.wr, qlo[nb], qhi[nb]);
-        else qlo[nb] = qhi[nb] = 0;
+    const uint16_t *kplane = a.k + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh;
+    const uint16_t *vplane = a.v + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
+    PF_WAIT_VMCNT(0);  // the Q loads above must not be counted by the copy waits below
+
+    // tile t lives in stage t % 4; its copy is issued at step t - 3, after the barrier that ends
+    // the use of tile t - 4 (same stage)
+#define PF_STG(k) ((k) == 0 ? stage0 : (k) == 1 ? stage1 : (k) == 2 ? stage2 : stage3)
+#define PF_ISSUE(k, t) \
+    pf_issue_tile(PF_STG(k), kplane, vplane, a.k_st, a.v_st, kt_begin + (t), a.kv_len, wave, lane)
+    if (ntiles > 0) PF_ISSUE(0, 0);
+    if (ntiles > 1) PF_ISSUE(1, 1);
+    if (ntiles > 2) PF_ISSUE(2, 2);
+#define PF_STEP(k)                                                                          \
+    {                                                                                       \
+        if (t >= ntiles) break;                                                             \
+        /* this wave's copies of tile t done (those of t+1, t+2 may still be in flight) */  \
+        const int ahead = min(ntiles - 1, t + 2) - t;                                       \
+        if (ahead == 2) PF_WAIT_VMCNT(2 * kPfCopiesPerTile);                                \
+        else if (ahead == 1) PF_WAIT_VMCNT(kPfCopiesPerTile);                               \
+        else PF_WAIT_VMCNT(0);                                                              \
+        __builtin_amdgcn_s_barrier();                                                       \
+        if (t + 3 < ntiles) PF_ISSUE(((k) + 3) & 3, t + 3);                                 \
+        if (wave_live) {                                                                    \
+            const int k0 = (kt_begin + t) * kPfBK;                                          \
+            pf_tile(st, PF_STG(k), k0, k0 >= lo_last && k0 + kPfBK <= hi_first,             \
+                    a.scale_log2, lane);                                                    \
+        }                                                                                   \
+        ++t;                                                                                \
     }
-
-    f32x16 acc[4][2];  // O^T: d-block md (32 dims), query block nb
-#pragma unroll
-    for (int md = 0; md < 4; ++md)
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) acc[md][nb] = f32x16{};
-    float m_run[2] = {-__builtin_inff(), -__builtin_inff()}, l_run[2] = {0.f, 0.f};
-
-    // ---- K / V staging: thread t copies key t / 4, dims 32 (t % 4) .. +31 of both tiles ----
-    const int skey = threadIdx.x >> 2, spart = threadIdx.x & 3;
-    const uint16_t *kbase = a.k + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh + 32 * spart;
-    const uint16_t *vbase = a.v + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh + 32 * spart;
-    u32x4 stk[4], stv[4];
-    auto fetch = [&](int kt) {
-        const int key = kt * kPfBK + skey;
-        const bool ok = key < a.kv_len;
-        const uint16_t *kr = kbase + (int64_t)min(key, a.kv_len - 1) * a.k_st;
-        const uint16_t *vr = vbase + (int64_t)min(key, a.kv_len - 1) * a.v_st;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            stk[i] = ok ? ldg128(kr + 8 * i) : u32x4{0u, 0u, 0u, 0u};
-            stv[i] = ok ? ldg128(vr + 8 * i) : u32x4{0u, 0u, 0u, 0u};
-        }
-    };
-    auto stash = [&](int stage) {
-        uint8_t *kt_lds = smem + stage * 2 * kPfTile;
-        uint8_t *vt_lds = kt_lds + kPfTile;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            *(u32x4 *)(kt_lds + skey * kPfPitch + (32 * spart + 8 * i) * 2) = stk[i];
-            *(u32x4 *)(vt_lds + skey * kPfPitch + (32 * spart + 8 * i) * 2) = stv[i];
-        }
-    };
-
-    if (kt_begin < kt_end) fetch(kt_begin);
-    for (int kt = kt_begin; kt < kt_end; ++kt) {
-        const int stage = (kt - kt_begin) & 1;
-        stash(stage);
-        __syncthreads();
-        if (kt + 1 < kt_end) fetch(kt + 1);
-        if (!wave_live) continue;
-        const uint8_t *k_lds = smem + stage * 2 * kPfTile;
-        const uint8_t *v_lds = k_lds + kPfTile;
-        const int k0 = kt * kPfBK;
-
-        // S^T = K Q^T: key block mb (32 keys), query block nb
-        f32x16 s[2][2];
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
-            s[mb][0] = f32x16{};
-            s[mb][1] = f32x16{};
-#pragma unroll
-            for (int ks = 0; ks < 8; ++ks) {
-                const bf16x8 kop = __builtin_bit_cast(
-                    bf16x8, *(const u32x4 *)(k_lds + (32 * mb + qr) * kPfPitch + (16 * ks + 8 * h) * 2));
-                s[mb][0] = mfma32x32x16(kop, qop[0][ks], s[mb][0]);
-                s[mb][1] = mfma32x32x16(kop, qop[1][ks], s[mb][1]);
-            }
-        }
-        // masks: only tiles that cross some query's visible range
-        const bool full = k0 >= lo_last && k0 + kPfBK <= hi_first;
-        if (!full) {
-#pragma unroll
-            for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-                for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                    for (int j = 0; j < 16; ++j) {
-                        const int key = k0 + 32 * mb + 8 * (j >> 2) + 4 * h + (j & 3);
-                        if (!(key >= qlo[nb] && key < qhi[nb])) s[mb][nb][j] = -__builtin_inff();
-                    }
-        }
-        // online softmax per query column (exp2 domain)
-        bf16x8 pop[2][4];  // P^T operands: query block nb, 16-key step kk
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-            float mx = -__builtin_inff();
-#pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[mb][nb][j]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float m_new = fmaxf(m_run[nb], mx * a.scale_log2);
-            const bool none = m_new == -__builtin_inff();
-            const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(m_run[nb] - m_new);
-            const float mneg = none ? 0.0f : m_new;
-            float psum = 0.0f;
-#pragma unroll
-            for (int mb = 0; mb < 2; ++mb) {
-                float p[16];
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    p[j] = __builtin_amdgcn_exp2f(s[mb][nb][j] * a.scale_log2 - mneg);
-                    psum += p[j];
-                }
-#pragma unroll
-                for (int half = 0; half < 2; ++half) {
-                    u32x4 w;
-                    w.x = pack_bf16x2(p[8 * half + 0], p[8 * half + 1]);
-                    w.y = pack_bf16x2(p[8 * half + 2], p[8 * half + 3]);
-                    w.z = pack_bf16x2(p[8 * half + 4], p[8 * half + 5]);
-                    w.w = pack_bf16x2(p[8 * half + 6], p[8 * half + 7]);
-                    pop[nb][2 * mb + half] = __builtin_bit_cast(bf16x8, w);
-                }
-            }
-            l_run[nb] = l_run[nb] * alpha + psum;
-            m_run[nb] = m_new;
-            if (__any(alpha != 1.0f)) {
-#pragma unroll
-                for (int md = 0; md < 4; ++md) acc[md][nb] *= alpha;
-            }
-        }
-        // O^T += V^T P^T: 16-key step kk = keys 32 mb + 16 i + [0, 16), mb = kk / 2, i = kk % 2
-        const int g16 = lane >> 4, idx = lane & 15, sp = idx >> 2, sq = idx & 3;
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            const int key0 = 32 * (kk >> 1) + 16 * (kk & 1) + 4 * h + sp;
-#pragma unroll
-            for (int md = 0; md < 4; ++md) {
-                const int d0 = 32 * md + 16 * (g16 & 1) + 4 * sq;
-                const uint8_t *src = v_lds + key0 * kPfPitch + d0 * 2;
-                const s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)src);
-                const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(src + 8 * kPfPitch));
-                const u32x2 l2 = __builtin_bit_cast(u32x2, lo4), h2 = __builtin_bit_cast(u32x2, hi4);
-                const bf16x8 vt = __builtin_bit_cast(bf16x8, u32x4{l2.x, l2.y, h2.x, h2.y});
-                acc[md][0] = mfma32x32x16(vt, pop[0][kk], acc[md][0]);
-                acc[md][1] = mfma32x32x16(vt, pop[1][kk], acc[md][1]);
-            }
-        }
+    for (int t = 0; t < ntiles;) {
+        PF_STEP(0)
+        PF_STEP(1)
+        PF_STEP(2)
+        PF_STEP(3)
     }
+#undef PF_STEP
+#undef PF_ISSUE
+#undef PF_STG
     if (!wave_live) return;
 
     // ---- normalise and write O (bf16): lane (qr, h), d = 32 md + 8 (j / 4) + 4 h + j % 4 ----
+    const float l = st.l_run + __shfl_xor(st.l_run, 32, 64);
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const int qi = q0 + 32 * qhalf + qr;
+    if (qi >= a.q_len) return;
+    uint16_t *orow = a.out + (int64_t)b * a.o_sb + (int64_t)qi * a.o_st + (int64_t)head * a.o_sh;
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-        const float l = l_run[nb] + __shfl_xor(l_run[nb], 32, 64);
-        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        const int qi = q0 + 32 * nb + qr;
-        if (qi >= a.q_len) continue;
-        uint16_t *orow = a.out + (int64_t)b * a.o_sb + (int64_t)qi * a.o_st + (int64_t)head * a.o_sh;
+    for (int md = 0; md < 4; ++md)
 #pragma unroll
-        for (int md = 0; md < 4; ++md)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                u32x2 w;
-                w.x = pack_bf16x2(acc[md][nb][4 * i + 0] * inv, acc[md][nb][4 * i + 1] * inv);
-                w.y = pack_bf16x2(acc[md][nb][4 * i + 2] * inv, acc[md][nb][4 * i + 3] * inv);
-                *(u32x2 *)(orow + 32 * md + 8 * i + 4 * h) = w;
-            }
-    }
+        for (int j = 0; j < 4; ++j) {
+            u32x2 w;
+            w.x = pack_bf16x2(st.acc[md][4 * j + 0] * inv, st.acc[md][4 * j + 1] * inv);
+            w.y = pack_bf16x2(st.acc[md][4 * j + 2] * inv, st.acc[md][4 * j + 3] * inv);
+            *(u32x2 *)(orow + 32 * md + 8 * j + 4 * h) = w;
+        }
 }
 
 int quant_append_launch(const cqkv_side *side, const void *x, int32_t x_dtype,
@@ -332,15 +394,9 @@ extern "C" int cqkv_flash_attn(const void *q, const int64_t q_strides[3], const 
     a.wl = window_left;
     a.wr = window_right;
     a.scale_log2 = softmax_scale * kLog2e;
-    const dim3 grid(a.q_blocks, kv_heads * (a.group / a.heads_per_wg), batch);
-    const size_t lds = 4 * (size_t)kPfTile;
-    static bool lds_set = false;
-    if (!lds_set) {
-        CQKV_HIP_CHECK(hipFuncSetAttribute((const void *)prefill_kernel,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        lds_set = true;
-    }
-    hipLaunchKernelGGL(prefill_kernel, grid, dim3(256), lds, st, a);
+    a.batch = batch;
+    const dim3 grid(a.q_blocks * kv_heads * (a.group / a.heads_per_wg) * batch);
+    hipLaunchKernelGGL(prefill_kernel, grid, dim3(kPfWaves * 64), 0, st, a);
     CQKV_HIP_CHECK(hipGetLastError());
     if (k_cache) {
         // K / V are (batch, kv_len, kv_heads, D): the append kernel's (batch, head, token)
