@@ -3,23 +3,33 @@
 Headline workload: FP8-E4M3 KV-cache flash-decode, batch 32,
 32 query / 8 KV heads, head_dim 128, every sequence at context 8192, bf16 queries and outputs;
 cached K/V from bf16 N(0,1) with 1 % of channels x8, per-(token, head) absmax/448 scales.
-A step is one decode call (split-K attention + split combine) over the whole batch, with the
-cache resident in HBM. Two cache copies (554 MB each, both larger than the 256 MB MALL) are
-used alternately so every call streams from HBM.
+A step is one decode call over the whole batch with the cache resident in HBM. At this shape the
+split rule picks one split, so one call is one launch of the decode kernel (no combine pass).
+Two cache copies (554 MB each, both larger than the 256 MB MALL) are used alternately so every
+call streams from HBM.
 
-value = algorithmic HBM bytes per call (codes + scales + q + out) / measured seconds per call.
-roofline.achieved = the same bytes / the decode kernel's average duration, timed with HIP events
-on the stream the library launches on (torch's current stream). cpu_baseline = the oracle's
+value = algorithmic HBM bytes per call (codes + scales + q + out) / measured seconds per call,
+timed with HIP events on the stream the library launches on (torch's current stream);
+roofline.achieved = the same bytes / the decode kernel's average duration (the same figure, as
+one call is one launch). roofline.traffic = HBM bytes per launch read by rocprofv3's FETCH_SIZE
+and WRITE_SIZE counters, scaled by what they read for a plain copy of known size; it is taken
+from the committed counter summary when that file is present. cpu_baseline = the oracle's
 restatement of the reference CPU path (dequantize -> bf16 -> f32 unfused attention), timed on the
 host on a bounded sample of the same workload.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--extra]
+"other_configs" reports BASELINE configs 3 (MXFP4, ragged), 4 (causal bf16 prefill with fused
+FP8 append) and 5 (TurboQuant-4, context 128K) with the same timing method; they are secondary
+figures, not the headline value.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+                       [--only c2,c3,c4,c5] [--calibration-copy]
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -28,6 +38,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "decode_fp8_b32_ctx8192_traffic.md")
 
 
 def load_cqkv():
@@ -40,6 +51,10 @@ def load_cqkv():
     return mod
 
 
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def kv_gpu(shape, seed, dev, outliers=True):
     import torch
     g = torch.Generator(device=dev).manual_seed(seed)
@@ -50,12 +65,12 @@ def kv_gpu(shape, seed, dev, outliers=True):
     return x.to(torch.bfloat16)
 
 
-def build_cache(cq, fmt, b, hkv, d, ctx, dev, seed):
+def build_cache(cq, fmt, b, hkv, d, ctx, dev, seed, chunk=2048):
     cache = cq.TurboKvCache(fmt, fmt, b, hkv, d, ctx, device=dev)
-    chunk = max(1, 2048 // 1)
     for t0 in range(0, ctx, chunk):
         t = min(chunk, ctx - t0)
-        cache.append(kv_gpu((b, hkv, t, d), seed + t0, dev), kv_gpu((b, hkv, t, d), seed + 7 + t0, dev))
+        cache.append(kv_gpu((b, hkv, t, d), seed + t0, dev),
+                     kv_gpu((b, hkv, t, d), seed + 7 + t0, dev))
     return cache
 
 
@@ -74,9 +89,24 @@ def time_calls(fn, steps, warmup, stream):
     return start.elapsed_time(stop) / steps  # ms per call
 
 
-def decode_bytes(b, hq, hkv, d, ctx, fmt):
-    per_row = {5: d + 4, 2: d // 2 + d // 32, 0: d // 2 + 4}[fmt]
-    return 2 * b * hkv * ctx * per_row + 2 * b * hq * d * 2
+def row_bytes(fmt, d):
+    """Packed cache bytes of one (token, head) row: codes + its scales."""
+    return {5: d + 4, 2: d // 2 + d // 32, 0: d // 2 + 4}[fmt]
+
+
+def decode_bytes(b, hq, hkv, d, total_tokens, fmt):
+    """K + V rows over `total_tokens` (summed over the batch) for every kv head, plus q and out."""
+    return 2 * hkv * total_tokens * row_bytes(fmt, d) + 2 * b * hq * d * 2
+
+
+def read_traffic():
+    """HBM bytes per decode launch from the committed counter summary, or None."""
+    try:
+        with open(TRAFFIC_SUMMARY) as f:
+            m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", f.read())
+        return int(m.group(1)) if m else None
+    except OSError:
+        return None
 
 
 def cpu_baseline_decode(cq, cache, q, b_sample, ctx, scale, threads):
@@ -97,70 +127,191 @@ def cpu_baseline_decode(cq, cache, q, b_sample, ctx, scale, threads):
     return t_total / reps * (b / b_sample), reps
 
 
+def decode_case(cq, dev, stream, fmt, b, hq, hkv, d, ctx, steps, warmup, lens=None, chunk=2048):
+    """Build two cache copies, time `steps` decode calls alternating between them."""
+    import torch
+    scale = 1.0 / d ** 0.5
+    caches = [build_cache(cq, fmt, b, hkv, d, ctx, dev, 1000 * i + 11 * fmt, chunk)
+              for i in range(2)]
+    q = kv_gpu((b, hq, 1, d), 5, dev, outliers=False)
+    out = torch.empty_like(q)
+    kv_lens = None if lens is None else torch.tensor(lens, dtype=torch.int32, device=dev)
+    # the split rule picks at most 256 splits; size the workspace for that so ragged calls
+    # (whose split count depends on the longest sequence) never allocate inside the timing
+    splits = cq.decode_splits(b, hkv, ctx) if lens is None else 256
+    ws = torch.zeros(max(1, cq.decode_workspace_bytes(b, hq, 1, d, splits)), dtype=torch.uint8,
+                     device=dev)
+
+    def step(i):
+        c = caches[i & 1]
+        cq.decode_attention(q, c.k, c.v, ctx, scale, kv_lens=kv_lens, out=out, splits=0,
+                            workspace=ws)
+
+    ms = time_calls(step, steps, warmup, stream)
+    total = b * ctx if lens is None else int(sum(lens))
+    nbytes = decode_bytes(b, hq, hkv, d, total, fmt)
+    return caches, q, ms, nbytes
+
+
+def prefill_case(cq, dev, stream, steps, warmup):
+    """causal bf16 prefill, B=4, S=4096, 32/8 heads, d=128, fused FP8
+    append of K and V into a cache."""
+    import torch
+    b, s, hq, hkv, d = 4, 4096, 32, 8, 128
+    g = torch.Generator(device=dev).manual_seed(7)
+    q = torch.randn(b, s, hq, d, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(b, s, hkv, d, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(b, s, hkv, d, generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    kc = cq.CacheSide.empty(cq.FP8, False, b, hkv, d, s, dev)
+    vc = cq.CacheSide.empty(cq.FP8, True, b, hkv, d, s, dev)
+
+    def step(i):
+        cq.flash_attn(q, k, v, 1.0 / d ** 0.5, True, out=out, k_cache=kc, v_cache=vc)
+
+    ms = time_calls(step, steps, warmup, stream)
+    flops = 2 * b * hq * s * s * d  # causal: half of 4*B*H*S^2*D
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"workload": "BASELINE config 4: causal bf16 prefill + fused FP8 K/V append",
+            "batch": b, "seq_len": s, "q_heads": hq, "kv_heads": hkv, "head_dim": d,
+            "us_per_call": round(ms * 1e3, 2), "flop_per_call": flops,
+            "achieved_tflops": round(tflops, 1), "peak_tflops": BF16_PEAK_TFLOPS,
+            "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "bound": "mfma",
+            "timed": "whole call: prefill kernel + K and V append kernels"}
+
+
+def decode_summary(name, ms, nbytes, extra):
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    res = {"workload": name, "us_per_call": round(ms * 1e3, 2), "bytes_per_call": nbytes,
+           "achieved_gbs": round(gbs, 1), "peak_gbs": HBM_PEAK_GBS,
+           "frac": round(gbs / HBM_PEAK_GBS, 4), "bound": "hbm"}
+    res.update(extra)
+    return res
+
+
+def calibration_copy(dev, reps=3):
+    """A plain device copy of 1 GiB, `reps` times: the counter scale of FETCH_SIZE/WRITE_SIZE."""
+    import torch
+    n = 1 << 30
+    src = torch.ones(n, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"calibration copy: {reps} x {n} bytes read and written")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--splits", type=int, default=0)
+    ap.add_argument("--no-extra", action="store_true", help="headline workload only")
+    ap.add_argument("--only", default="", help="comma list of c2,c3,c4,c5 (default: all)")
+    ap.add_argument("--calibration-copy", action="store_true",
+                    help="also run a plain 1 GiB copy (for counter scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "the path shards by batch / kv head with no exchange, see DESIGN.md", file=sys.stderr)
+              "the path would shard by sequence / kv head with no exchange between GPUs",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
     cq = load_cqkv()
+    cq.lib()
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream(dev)
+    only = set(x for x in args.only.split(",") if x)
+    want = (lambda c: c in only) if only else (lambda c: c == "c2" or not args.no_extra)
+    if args.calibration_copy:
+        calibration_copy(dev)
 
-    B, HQ, HKV, D, CTX = 32, 32, 8, 128, 8192
-    scale = 1.0 / D ** 0.5
-    caches = [build_cache(cq, cq.FP8, B, HKV, D, CTX, dev, 1000 * i) for i in range(2)]
-    q = kv_gpu((B, HQ, 1, D), 5, dev, outliers=False)
-    out = torch.empty_like(q)
-    splits = args.splits or cq.decode_splits(B, HKV, CTX)
-    ws = torch.zeros(cq.decode_workspace_bytes(B, HQ, 1, D, splits), dtype=torch.uint8, device=dev)
+    res = None
+    if want("c2"):
+        B, HQ, HKV, D, CTX = 32, 32, 8, 128, 8192
+        log("config 2: FP8 decode B=32 32/8 d=128 ctx 8192")
+        caches, q, ms, nbytes = decode_case(cq, dev, stream, cq.FP8, B, HQ, HKV, D, CTX,
+                                            args.steps, args.warmup)
+        splits = cq.decode_splits(B, HKV, CTX)
+        achieved = nbytes / (ms * 1e-3) / 1e9  # GB/s
+        log(f"config 2: {ms * 1e3:.2f} us/call, {achieved:.1f} GB/s")
+        cores = min(16, os.cpu_count() or 1)
+        cpu = None
+        if not args.no_cpu:
+            sec, reps = cpu_baseline_decode(cq, caches[0], q, 2, CTX, 1.0 / D ** 0.5, cores)
+            cpu = {"value": round(nbytes / sec / 1e12, 6), "unit": "TB/s", "cores": cores,
+                   "kind": "port", "us_per_call": round(sec * 1e6, 1),
+                   "sample": f"oracle cache_attention (reference CPU path restated in C) on 2 "
+                             f"of the 32 sequences, {reps} reps, scaled x16 to the full call"}
+            log(f"cpu baseline: {sec * 1e6:.0f} us/call on {cores} threads")
+        del caches
+        traffic = read_traffic()
+        res = {
+            "metric": "quant-KV flash-decode µs/call + achieved HBM TB/s; bf16 prefill TFLOP/s",
+            "value": round(achieved / 1000.0, 4),
+            "unit": "TB/s",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": round(ms, 5),
+            "us_per_call": round(ms * 1e3, 2),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "fp8-e4m3 cache codes, bf16 q/out, f32 accumulate",
+            "data": "synthetic (torch N(0,1) bf16, 1% channels x8)",
+            "config": {"workload": "BASELINE config 2: FP8-KV GQA flash-decode", "batch": B,
+                       "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "context": CTX,
+                       "splits": splits, "cache_copies": 2, "parallelism": "single GPU"},
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                         "traffic": traffic, "bytes_per_call": nbytes,
+                         "timed": "decode kernel (one launch per call at this shape)"},
+            "cpu_baseline": cpu,
+        }
+        torch.cuda.empty_cache()
 
-    def step(i):
-        c = caches[i & 1]
-        cq.decode_attention(q, c.k, c.v, CTX, scale, out=out, splits=splits, workspace=ws)
+    other = {}
+    steps_x = max(5, args.steps // 5)
+    warm_x = max(2, args.warmup // 2)
+    if want("c4"):
+        log("config 4: causal prefill + fused FP8 append")
+        other["c4_prefill"] = prefill_case(cq, dev, stream, steps_x, warm_x)
+        log(f"config 4: {other['c4_prefill']['us_per_call']} us/call")
+        torch.cuda.empty_cache()
+    if want("c3"):
+        import random
+        rng = random.Random(3)
+        lens = [rng.randint(1024, 32768) for _ in range(64)]
+        log("config 3: MXFP4 ragged decode B=64 32/8 d=128")
+        caches, _, ms, nbytes = decode_case(cq, dev, stream, cq.MXFP4, 64, 32, 8, 128, 32768,
+                                            steps_x, warm_x, lens=lens)
+        del caches
+        other["c3_mxfp4_ragged"] = decode_summary(
+            "BASELINE config 3: MXFP4-KV ragged decode", ms, nbytes,
+            {"batch": 64, "q_heads": 32, "kv_heads": 8, "head_dim": 128,
+             "lens": "uniform [1024, 32768], random.Random(3)", "sum_len": int(sum(lens)),
+             "timed": "whole call (split-K decode + combine)"})
+        log(f"config 3: {ms * 1e3:.2f} us/call")
+        torch.cuda.empty_cache()
+    if want("c5"):
+        log("config 5: TurboQuant-4 decode B=8 64/8 d=128 ctx 131072")
+        caches, _, ms, nbytes = decode_case(cq, dev, stream, cq.TURBO4, 8, 64, 8, 128, 131072,
+                                            steps_x, warm_x, chunk=8192)
+        del caches
+        other["c5_turbo4"] = decode_summary(
+            "BASELINE config 5: TurboQuant-4 KV decode", ms, nbytes,
+            {"batch": 8, "q_heads": 64, "kv_heads": 8, "head_dim": 128, "context": 131072,
+             "timed": "whole call (split-K decode + combine with unrotation)"})
+        log(f"config 5: {ms * 1e3:.2f} us/call")
+        torch.cuda.empty_cache()
 
-    ms = time_calls(step, args.steps, args.warmup, stream)
-    nbytes = decode_bytes(B, HQ, HKV, D, CTX, cq.FP8)
-    achieved = nbytes / (ms * 1e-3) / 1e9  # GB/s
-    cores = min(16, os.cpu_count() or 1)
-    cpu = None
-    if not args.no_cpu:
-        sec, reps = cpu_baseline_decode(cq, caches[0], q, 2, CTX, scale, cores)
-        cpu = {"value": round(nbytes / sec / 1e12, 6), "unit": "TB/s", "cores": cores,
-               "kind": "port", "us_per_call": round(sec * 1e6, 1),
-               "sample": f"oracle cache_attention (reference CPU path restated in C) on 2 of the "
-                         f"32 sequences, {reps} reps, scaled x16 to the full call"}
-    res = {
-        "metric": "quant-KV flash-decode µs/call + achieved HBM TB/s; bf16 prefill TFLOP/s",
-        "value": round(achieved / 1000.0, 4),
-        "unit": "TB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
-        "us_per_call": round(ms * 1e3, 2),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "fp8-e4m3 cache, bf16 q/out, f32 accumulate",
-        "data": "synthetic (torch N(0,1) bf16, 1% channels x8)",
-        "config": {"workload": "BASELINE config 2: FP8-KV GQA flash-decode", "batch": B,
-                   "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "context": CTX,
-                   "splits": splits, "cache_copies": 2, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "bytes_per_call": nbytes,
-                     "timed": "whole call (decode + combine kernels)"},
-        "cpu_baseline": cpu,
-    }
+    if res is None:
+        res = {"metric": "partial run", "value": None, "note": "headline workload not selected"}
+    if other:
+        res["other_configs"] = other
     print(json.dumps(res), flush=True)
 
 

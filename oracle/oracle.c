@@ -3,6 +3,13 @@
  * check and bench.py's cpu_baseline leg use it, as the checker). Restates the reference's CPU
  * algorithms in plain C; every function cites the reference file:line it follows. Built with
  * -ffp-contract=off so that a*b+c is never fused, matching the reference's Rust arithmetic.
+ *
+ * Parity unpinned: the f32 bits of orc_rotate_rows / orc_unrotate_rows. The reference rotates
+ * with the CPU `gemm` crate (0.18.2 / 0.19.0, not part of the reference tree), whose summation
+ * order is not restated here (this sums in index order); the rotation is pinned by its structure
+ * (Hadamard signs, orthogonality) and TurboQuant codes by the reference's own flip criterion, not
+ * bit for bit. Likewise the last bits of orc_attention_unfused / orc_cache_attention (gemm and
+ * SIMD sum order) are pinned against float64 attention within tolerance, not bit for bit.
  */
 #include "oracle.h"
 
