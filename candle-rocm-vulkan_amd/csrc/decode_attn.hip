@@ -12,8 +12,8 @@
 //  * Both products run on v_mfma_f32_16x16x32_bf16. MFMA columns are the (query, head) pairs of
 //    the GQA group (q_len * group <= 16); rows are keys (S^T = K Q^T) or head dims
 //    (O^T = V^T P^T).
-//  * A wavefront streams 32-key tiles with buffer loads straight into operand registers (two
-//    register sets, A/B, no copies) and decodes codes in registers: E4M3 -> bf16 exactly, E2M1
+//  * A wavefront streams 32-key tiles with nontemporal buffer loads straight into operand
+//    registers (two register sets, A/B, no copies) and decodes codes in registers: E4M3 -> bf16 exactly, E2M1
 //    with its E8M0 block scale exactly, TurboQuant nibbles through an LDS table of f16 pairs
 //    (TurboQuant runs its MFMAs in f16: codebook values are not bf16-exact).
 //    Loads of tiles past the split's end are aimed past the buffer range, so the hardware
@@ -116,7 +116,7 @@ __device__ inline void load_tile(Tile<FMT, D> &r, int tile, bool live, int lane,
         if constexpr (FMT == CQKV_FMT_FP8) {
 #pragma unroll
             for (int i = 0; i < D / 64; ++i) {
-                const u32x4 w = ld128(kr, (key * D + 16 * g + 64 * i) | oob);
+                const u32x4 w = ld128_stream(kr, (key * D + 16 * g + 64 * i) | oob);
                 r.k[s][4 * i + 0] = w.x;
                 r.k[s][4 * i + 1] = w.y;
                 r.k[s][4 * i + 2] = w.z;
@@ -125,13 +125,13 @@ __device__ inline void load_tile(Tile<FMT, D> &r, int tile, bool live, int lane,
             r.kscale[s] = ld32(ksr, (key * 4) | oob);
         } else {
             if constexpr (D == 128) {
-                const u32x4 w = ld128(kr, (key * 64 + 16 * g) | oob);
+                const u32x4 w = ld128_stream(kr, (key * 64 + 16 * g) | oob);
                 r.k[s][0] = w.x;
                 r.k[s][1] = w.y;
                 r.k[s][2] = w.z;
                 r.k[s][3] = w.w;
             } else {
-                const u32x2 w = ld64(kr, (key * 32 + 8 * g) | oob);
+                const u32x2 w = ld64_stream(kr, (key * 32 + 8 * g) | oob);
                 r.k[s][0] = w.x;
                 r.k[s][1] = w.y;
             }
@@ -143,13 +143,13 @@ __device__ inline void load_tile(Tile<FMT, D> &r, int tile, bool live, int lane,
 #pragma unroll
     for (int u = 0; u < D / 32; ++u) {
         if constexpr (FMT == CQKV_FMT_FP8) {
-            const u32x4 w = ld128(vr, (((t0 / 8 + g) * D + 32 * u + 2 * n) * 8) | oob);
+            const u32x4 w = ld128_stream(vr, (((t0 / 8 + g) * D + 32 * u + 2 * n) * 8) | oob);
             r.v[u][0] = w.x;
             r.v[u][1] = w.y;
             r.v[u][2] = w.z;
             r.v[u][3] = w.w;
         } else {
-            const u32x2 w = ld64(vr, (((t0 / 8 + g) * D + 32 * u + 2 * n) * 4) | oob);
+            const u32x2 w = ld64_stream(vr, (((t0 / 8 + g) * D + 32 * u + 2 * n) * 4) | oob);
             r.v[u][0] = w.x;
             r.v[u][1] = w.y;
         }
