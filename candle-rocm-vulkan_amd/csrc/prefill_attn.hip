@@ -44,6 +44,12 @@ struct PrefillArgs {
     int64_t k_sb, k_st, k_sh;
     int64_t v_sb, v_st, v_sh;
     int64_t o_sb, o_st, o_sh;
+    const uint16_t *vt;  // V transposed: (batch, kv head, D, vt_len), keys in S^T register order
+    int32_t vt_len;      // keys per row of vt: kv_len rounded up to the key tile
+    // fused FP8 append (append != 0): codes / scales planes of the key and value cache sides
+    uint8_t *kc, *ks, *vc, *vs;
+    uint32_t kc_plane, ks_plane, vc_plane, vs_plane;
+    int32_t append, position;
     int32_t q_len, kv_len, q_heads, kv_heads, group, heads_per_wg, q_blocks, batch;
     int32_t wl, wr;
     float scale_log2;
@@ -70,6 +76,11 @@ __device__ inline void pf_key_range(int i, int lq, int lk, int wl, int wr, int &
 // rows (the 4 rows x 2 chunks of one ds_read_b64_tr_b16 group), so both read patterns are
 // conflict-free.
 __device__ inline int swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+// V^T tile layout in LDS: 128 rows (head dims) x 128 B (64 keys); the 16-byte chunk j (8 keys) of
+// row d sits at position j ^ swz_vt(d). Over any 16 consecutive rows, (d % 2, position) takes 16
+// distinct values, so a ds_read_b128 of one chunk across 16 rows is conflict-free.
+__device__ inline int swz_vt(int d) { return (d >> 1) & 7; }
+constexpr int kPfVtRow = 128;
 constexpr int kPfWaves = 8;               // 4 query heads x 2 halves of the 64 queries
 constexpr int kPfRow = 256;
 constexpr int kPfHalf = kPfBK * kPfRow;   // one K or V tile: 16 KB
@@ -79,22 +90,53 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 #define PF_INLINE __device__ __attribute__((always_inline)) inline
 
-// Asynchronous global -> LDS copy of key tile kt (K and V) into `stage`: wavefront w copies rows
-// 8w .. 8w+7 of each, 4 rows (1 KB) per global_load_lds_dwordx4. Lane l writes chunk position
-// l % 16 of row l / 16, so it loads logical chunk (l % 16) ^ swz(row). Rows past the keys repeat
-// the last key (finite values; they are masked out).
-PF_INLINE void pf_issue_tile(uint8_t *stage, const uint16_t *kplane, const uint16_t *vplane,
-                             int64_t k_st, int64_t v_st, int kt, int kv_len, int wave, int lane) {
+// Asynchronous global -> LDS copy of key tile kt into `stage`: K rows (keys) and V^T rows (head
+// dims), one global_load_lds_dwordx4 (1 KB) per 4 K rows / 8 V^T rows. Wavefront w copies K rows
+// 8w .. 8w+7 and V^T rows 16w .. 16w+15. K: lane l writes chunk position l % 16 of row l / 16,
+// so it loads logical chunk (l % 16) ^ swz(row); rows past the keys repeat the last key. V^T:
+// lane l writes chunk position l % 8 of row l / 8 (the pre-pass zero-fills keys past the end).
+PF_INLINE void pf_issue_tile(uint8_t *stage, const uint16_t *kplane, const uint16_t *vtplane,
+                             int64_t k_st, int vt_len, const uint32_t (&koff)[2],
+                             const uint32_t (&voff)[2], int kt, int kv_len, int wave, int lane) {
+    const int row0 = kt * kPfBK;
+    if (row0 + kPfBK <= kv_len) {
+        // a wave-uniform tile address plus a fixed per-lane byte offset
+        const uint8_t *ktile = (const uint8_t *)(kplane + (int64_t)row0 * k_st);
+#pragma unroll
+        for (int r4 = 0; r4 < 2; ++r4)
+            __builtin_amdgcn_global_load_lds((const void *)(ktile + koff[r4]),
+                                             (lds_void *)(stage + (8 * wave + 4 * r4) * kPfRow),
+                                             16, 0, 0);
+    } else {
+#pragma unroll
+        for (int r4 = 0; r4 < 2; ++r4) {
+            const int row = 8 * wave + 4 * r4 + (lane >> 4);
+            const int key = min(row0 + row, kv_len - 1);
+            const int c = (lane & 15) ^ swz(row);
+            __builtin_amdgcn_global_load_lds((const void *)(kplane + (int64_t)key * k_st + 8 * c),
+                                             (lds_void *)(stage + (8 * wave + 4 * r4) * kPfRow),
+                                             16, 0, 0);
+        }
+    }
+    const uint8_t *vtile = (const uint8_t *)(vtplane + row0);
+#pragma unroll
+    for (int r8 = 0; r8 < 2; ++r8)
+        __builtin_amdgcn_global_load_lds((const void *)(vtile + voff[r8]),
+                                         (lds_void *)(stage + kPfHalf + (16 * wave + 8 * r8) * kPfVtRow),
+                                         16, 0, 0);
+}
+// byte offsets of this lane's copy sources from a tile's first K row / first V^T key
+PF_INLINE void pf_copy_offsets(uint32_t (&koff)[2], uint32_t (&voff)[2], int64_t k_st, int vt_len,
+                               int wave, int lane) {
 #pragma unroll
     for (int r4 = 0; r4 < 2; ++r4) {
         const int row = 8 * wave + 4 * r4 + (lane >> 4);
-        const int key = min(kt * kPfBK + row, kv_len - 1);
-        const int c = (lane & 15) ^ swz(row);
-        __builtin_amdgcn_global_load_lds((const void *)(kplane + (int64_t)key * k_st + 8 * c),
-                                         (lds_void *)(stage + (8 * wave + 4 * r4) * kPfRow), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void *)(vplane + (int64_t)key * v_st + 8 * c),
-                                         (lds_void *)(stage + kPfHalf + (8 * wave + 4 * r4) * kPfRow),
-                                         16, 0, 0);
+        koff[r4] = (uint32_t)(((int64_t)row * k_st + 8 * ((lane & 15) ^ swz(row))) * 2);
+    }
+#pragma unroll
+    for (int r8 = 0; r8 < 2; ++r8) {
+        const int d = 16 * wave + 8 * r8 + (lane >> 3);
+        voff[r8] = (uint32_t)(((int64_t)d * vt_len + 8 * ((lane & 7) ^ swz_vt(d))) * 2);
     }
 }
 constexpr int kPfCopiesPerTile = 4;  // global_load_lds per wavefront per tile
@@ -152,23 +194,26 @@ PF_INLINE void pf_softmax(bf16x8 (&pop)[4], const f32x16 (&s)[2], PfState &st, f
     const bool none = m_new == -__builtin_inff();
     const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(st.m_run - m_new);
     const float mneg = none ? 0.0f : m_new;
+    // p = exp2(s * scale - m), packed to bf16; the row sum adds the bf16 values the product
+    // uses, two per dot2 instruction
+    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
     float psum = 0.0f;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
-            float p[8];
+            uint32_t w[4];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                p[e] = __builtin_amdgcn_exp2f(s[mb][8 * half + e] * scale_log2 - mneg);
-                psum += p[e];
+            for (int e = 0; e < 4; ++e) {
+                const float p0 = __builtin_amdgcn_exp2f(
+                    __builtin_fmaf(s[mb][8 * half + 2 * e], scale_log2, -mneg));
+                const float p1 = __builtin_amdgcn_exp2f(
+                    __builtin_fmaf(s[mb][8 * half + 2 * e + 1], scale_log2, -mneg));
+                const bf16x2 pp = {(__bf16)p0, (__bf16)p1};
+                psum = __builtin_amdgcn_fdot2_f32_bf16(pp, ones, psum, false);
+                w[e] = __builtin_bit_cast(uint32_t, pp);
             }
-            u32x4 w;
-            w.x = pack_bf16x2(p[0], p[1]);
-            w.y = pack_bf16x2(p[2], p[3]);
-            w.z = pack_bf16x2(p[4], p[5]);
-            w.w = pack_bf16x2(p[6], p[7]);
-            pop[2 * mb + half] = __builtin_bit_cast(bf16x8, w);
+            pop[2 * mb + half] = __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
         }
     st.l_run = st.l_run * alpha + psum;
     st.m_run = m_new;
@@ -178,42 +223,35 @@ PF_INLINE void pf_softmax(bf16x8 (&pop)[4], const f32x16 (&s)[2], PfState &st, f
     }
 }
 
-// O^T += V^T P^T over the tile at v_lds; 16-key step kk = keys 32 (kk / 2) + 16 (kk % 2) +
-// [0, 16), whose k order matches the S^T accumulator registers 8 (kk % 2) .. +7 of block kk / 2.
+// O^T += V^T P^T over the V^T tile at v_lds. 16-key step kk = keys 16 kk + [0, 16): the P^T
+// operand holds S^T registers 8 (kk % 2) .. +7 of key block kk / 2, i.e. lane half h holds keys
+// 16 kk + 8 (e / 4) + 4 h + e % 4 in k-slot 8 h + e; the pre-pass stores V^T keys in that order
+// (bits 2 and 3 of the key swapped), so the A operand of lane (d, h) is chunk 2 kk + h of row d.
 PF_INLINE void pf_pv(PfState &st, const bf16x8 (&pop)[4], const uint8_t *v_lds, int lane) {
-    const int h = lane >> 5, g16 = lane >> 4, idx = lane & 15, sp = idx >> 2, sq = idx & 3;
+    const int qr = lane & 31, h = lane >> 5;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-        const int r0 = 32 * (kk >> 1) + 16 * (kk & 1) + 4 * h + sp;
-        const int r1 = r0 + 8;
-        const int sw0 = swz(r0), sw1 = swz(r1);
+        const uint32_t off = qr * kPfVtRow + (((2 * kk + h) ^ swz_vt(qr)) << 4);
 #pragma unroll
         for (int md = 0; md < 4; ++md) {
-            const int d = 32 * md + 16 * (g16 & 1) + 4 * sq;
-            const int c = d >> 3, sub = (d & 7) * 2;
-            const s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_s16x4 *)(v_lds + r0 * kPfRow + ((c ^ sw0) << 4) + sub));
-            const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_s16x4 *)(v_lds + r1 * kPfRow + ((c ^ sw1) << 4) + sub));
-            const u32x2 l2 = __builtin_bit_cast(u32x2, lo4), h2 = __builtin_bit_cast(u32x2, hi4);
-            const bf16x8 vt = __builtin_bit_cast(bf16x8, u32x4{l2.x, l2.y, h2.x, h2.y});
+            const bf16x8 vt =
+                __builtin_bit_cast(bf16x8, *(const u32x4 *)(v_lds + off + md * 32 * kPfVtRow));
             st.acc[md] = mfma32x32x16(vt, pop[kk], st.acc[md]);
         }
     }
 }
 
-PF_INLINE void pf_tile(PfState &st, const uint8_t *stage, int k0, bool full, float scale_log2,
-                       int lane) {
+// S^T of the tile, mask (tiles that cross a range end only) and online softmax into pop
+PF_INLINE void pf_qk_softmax(PfState &st, bf16x8 (&pop)[4], const uint8_t *stage, int k0,
+                             bool full, float scale_log2, int lane) {
     f32x16 s[2];
-    bf16x8 pop[4];
     pf_qk(s, st, stage, lane);
     if (!full) pf_mask(s, st, k0, lane);
     pf_softmax(pop, s, st, scale_log2);
-    pf_pv(st, pop, stage + kPfHalf, lane);
 }
 
 // Two wavefronts per SIMD (8 per workgroup, ~200 registers each): while one runs its softmax on
-// the VALU, the other's MFMAs run.
+// the VALU, the other's MFMAs can run.
 __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a) {
     // four K/V stages as distinct arrays, each named statically below, so the compiler can tell
     // the asynchronous copy into one stage from the reads of another (a dynamically selected
@@ -267,31 +305,39 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     }
 
     const uint16_t *kplane = a.k + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh;
-    const uint16_t *vplane = a.v + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
+    const uint16_t *vtplane = a.vt + ((int64_t)b * a.kv_heads + hk) * kPfD * a.vt_len;
     PF_WAIT_VMCNT(0);  // the Q loads above must not be counted by the copy waits below
 
-    // tile t lives in stage t % 4; its copy is issued at step t - 3, after the barrier that ends
-    // the use of tile t - 4 (same stage)
+    // Tile t lives in stage t % 4; its copy is issued in step t - 3, after that step's barrier
+    // (which ends step t - 4, the last reader of the stage) and after its S / softmax, so the
+    // copy's issue overlaps the other wavefronts' work.
 #define PF_STG(k) ((k) == 0 ? stage0 : (k) == 1 ? stage1 : (k) == 2 ? stage2 : stage3)
-#define PF_ISSUE(k, t) \
-    pf_issue_tile(PF_STG(k), kplane, vplane, a.k_st, a.v_st, kt_begin + (t), a.kv_len, wave, lane)
+    uint32_t koff[2], voff[2];
+    pf_copy_offsets(koff, voff, a.k_st, a.vt_len, wave, lane);
+#define PF_ISSUE(k, t)                                                                      \
+    pf_issue_tile(PF_STG(k), kplane, vtplane, a.k_st, a.vt_len, koff, voff, kt_begin + (t), \
+                  a.kv_len, wave, lane)
     if (ntiles > 0) PF_ISSUE(0, 0);
     if (ntiles > 1) PF_ISSUE(1, 1);
     if (ntiles > 2) PF_ISSUE(2, 2);
+    bf16x8 pop[4];
 #define PF_STEP(k)                                                                          \
     {                                                                                       \
         if (t >= ntiles) break;                                                             \
-        /* this wave's copies of tile t done (those of t+1, t+2 may still be in flight) */  \
+        /* this wave's copies of tile t done (those of t + 1, t + 2 may be in flight) */    \
         const int ahead = min(ntiles - 1, t + 2) - t;                                       \
         if (ahead == 2) PF_WAIT_VMCNT(2 * kPfCopiesPerTile);                                \
         else if (ahead == 1) PF_WAIT_VMCNT(kPfCopiesPerTile);                               \
         else PF_WAIT_VMCNT(0);                                                              \
         __builtin_amdgcn_s_barrier();                                                       \
-        if (t + 3 < ntiles) PF_ISSUE(((k) + 3) & 3, t + 3);                                 \
         if (wave_live) {                                                                    \
             const int k0 = (kt_begin + t) * kPfBK;                                          \
-            pf_tile(st, PF_STG(k), k0, k0 >= lo_last && k0 + kPfBK <= hi_first,             \
-                    a.scale_log2, lane);                                                    \
+            const bool full = k0 >= lo_last && k0 + kPfBK <= hi_first;                      \
+            pf_qk_softmax(st, pop, PF_STG(k), k0, full, a.scale_log2, lane);                \
+            if (t + 3 < ntiles) PF_ISSUE(((k) + 3) & 3, t + 3);                             \
+            pf_pv(st, pop, PF_STG(k) + kPfHalf, lane);                                      \
+        } else if (t + 3 < ntiles) {                                                        \
+            PF_ISSUE(((k) + 3) & 3, t + 3);                                                 \
         }                                                                                   \
         ++t;                                                                                \
     }
@@ -321,6 +367,128 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
             w.y = pack_bf16x2(st.acc[md][4 * j + 2] * inv, st.acc[md][4 * j + 3] * inv);
             *(u32x2 *)(orow + 32 * md + 8 * j + 4 * h) = w;
         }
+}
+
+// Pre-pass, one workgroup per 64-key tile of a (batch, kv head) plane, through LDS:
+//  * V (batch, kv_len, kv heads, D) -> V^T (batch, kv head, D, vt_len) with the keys of each
+//    16-key group in S^T register order (key bits 2 and 3 swapped) and zeros past kv_len;
+//  * with a.append, the FP8 quantize-and-append of K and V into the cache at a.position (a
+//    multiple of 8): per token s = absmax / 448 (1 for an all-zero row), codes e4m3(x / s) -
+//    RowCodec::quantize_row's FP8 branch (candle-core/src/accel/turbo.rs:366-374) as in
+//    cqkv_quant_append - key codes row-major, value codes in 8-token transposed tiles.
+PF_INLINE float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+PF_INLINE float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+constexpr int kStRow = 68;  // LDS row stride of the pre-pass tiles in 32-bit words (272 B)
+
+__global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) uint32_t vtile[kPfBK * kStRow];
+    __shared__ __attribute__((aligned(16))) uint32_t ktile[kPfBK * kStRow];
+    __shared__ float vscale[kPfBK];
+    const int kt = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x;
+    const uint16_t *vplane = a.v + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
+    const uint16_t *kplane = a.k + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int id = tid + 256 * i, row = id >> 4, c = id & 15;
+        const int key = kt * kPfBK + row;
+        u32x4 w = {0u, 0u, 0u, 0u};
+        if (key < a.kv_len) w = *(const u32x4 *)(vplane + (int64_t)key * a.v_st + 8 * c);
+        *(u32x4 *)&vtile[row * kStRow + 4 * c] = w;
+        if (a.append) {
+            u32x4 wk = {0u, 0u, 0u, 0u};
+            if (key < a.kv_len) wk = *(const u32x4 *)(kplane + (int64_t)key * a.k_st + 8 * c);
+            *(u32x4 *)&ktile[row * kStRow + 4 * c] = wk;
+        }
+    }
+    __syncthreads();
+    // V^T: thread (d, j) writes keys 8j .. 8j+7 (in register order) of head dim d
+    uint16_t *out = (uint16_t *)a.vt + ((int64_t)b * a.kv_heads + hk) * kPfD * a.vt_len;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int id = tid + 256 * i, d = id >> 3, j = id & 7;
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int p0 = 8 * j + 2 * e, p1 = p0 + 1;  // positions -> keys: swap bits 2 and 3
+            const int k0 = (p0 & ~12) | ((p0 & 4) << 1) | ((p0 & 8) >> 1);
+            const int k1 = (p1 & ~12) | ((p1 & 4) << 1) | ((p1 & 8) >> 1);
+            const uint32_t w0 = vtile[k0 * kStRow + (d >> 1)], w1 = vtile[k1 * kStRow + (d >> 1)];
+            w[e] = (d & 1) ? ((w0 >> 16) | (w1 & 0xffff0000u)) : ((w0 & 0xffffu) | (w1 << 16));
+        }
+        *(u32x4 *)(out + (int64_t)d * a.vt_len + kt * kPfBK + 8 * j) = u32x4{w[0], w[1], w[2], w[3]};
+    }
+    if (!a.append) return;
+    const int64_t plane = (int64_t)b * a.kv_heads + hk;
+    // ---- per-token scales: 4 threads per token, 32 head dims each ----
+    const int r = tid >> 2, qd = tid & 3, t = kt * kPfBK + r;
+    const bool live = t < a.kv_len;
+    float kmax = 0.0f, vmax = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+        const uint32_t kw = ktile[r * kStRow + 16 * qd + w], vw = vtile[r * kStRow + 16 * qd + w];
+        kmax = fmaxf(kmax, fmaxf(__builtin_fabsf(bf16_lo(kw)), __builtin_fabsf(bf16_hi(kw))));
+        vmax = fmaxf(vmax, fmaxf(__builtin_fabsf(bf16_lo(vw)), __builtin_fabsf(bf16_hi(vw))));
+    }
+    kmax = fmaxf(kmax, __shfl_xor(kmax, 1, 64));
+    kmax = fmaxf(kmax, __shfl_xor(kmax, 2, 64));
+    vmax = fmaxf(vmax, __shfl_xor(vmax, 1, 64));
+    vmax = fmaxf(vmax, __shfl_xor(vmax, 2, 64));
+    const float ksc = kmax > 0.0f ? kmax / 448.0f : 1.0f;
+    const float vsc = vmax > 0.0f ? vmax / 448.0f : 1.0f;
+    if (qd == 0) {
+        vscale[r] = vsc;
+        if (live) {
+            ((float *)(a.ks + plane * a.ks_plane))[a.position + t] = ksc;
+            ((float *)(a.vs + plane * a.vs_plane))[a.position + t] = vsc;
+        }
+    }
+    // ---- key codes: the thread's 32 dims of its token, row-major ----
+    if (live) {
+        uint32_t cw[8];
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            const uint32_t x01 = ktile[r * kStRow + 16 * qd + 2 * w];
+            const uint32_t x23 = ktile[r * kStRow + 16 * qd + 2 * w + 1];
+            cw[w] = e4m3_encode(bf16_lo(x01) / ksc) | (e4m3_encode(bf16_hi(x01) / ksc) << 8) |
+                    (e4m3_encode(bf16_lo(x23) / ksc) << 16) | (e4m3_encode(bf16_hi(x23) / ksc) << 24);
+        }
+        uint8_t *dst = a.kc + plane * a.kc_plane + (int64_t)(a.position + t) * kPfD + 32 * qd;
+        *(u32x4 *)dst = u32x4{cw[0], cw[1], cw[2], cw[3]};
+        *(u32x4 *)(dst + 16) = u32x4{cw[4], cw[5], cw[6], cw[7]};
+    }
+    __syncthreads();
+    // ---- value codes: thread (dim pair dp, groups g, g + 4) of 8 tokens, 8-token tiles ----
+    const int dp = tid & 63;
+    uint8_t *vc = a.vc + plane * a.vc_plane;
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+        const int g = (tid >> 6) + 4 * gi, t0 = kt * kPfBK + 8 * g;
+        if (t0 >= a.kv_len) continue;
+        uint64_t vw0 = 0, vw1 = 0;
+        uint32_t mask = 0;
+#pragma unroll
+        for (int sl = 0; sl < 8; ++sl) {
+            if (t0 + sl < a.kv_len) {
+                const uint32_t x = vtile[(8 * g + sl) * kStRow + dp];
+                const float sc = vscale[8 * g + sl];
+                vw0 |= (uint64_t)e4m3_encode(bf16_lo(x) / sc) << (8 * sl);
+                vw1 |= (uint64_t)e4m3_encode(bf16_hi(x) / sc) << (8 * sl);
+                mask |= 1u << sl;
+            }
+        }
+        // (position + t0) is a multiple of 8: the group is one value tile of the cache
+        uint64_t *dst = (uint64_t *)(vc + (int64_t)((a.position + t0) >> 3) * kPfD * 8 + dp * 16);
+        if (mask != 0xffu) {  // keep the codes of the tokens past the end
+            uint64_t keep = 0;
+            for (int sl = 0; sl < 8; ++sl)
+                if (!((mask >> sl) & 1u)) keep |= 0xffull << (8 * sl);
+            vw0 |= dst[0] & keep;
+            vw1 |= dst[1] & keep;
+        }
+        *(u32x4 *)dst = u32x4{(uint32_t)vw0, (uint32_t)(vw0 >> 32), (uint32_t)vw1, (uint32_t)(vw1 >> 32)};
+    }
 }
 
 int quant_append_launch(const cqkv_side *side, const void *x, int32_t x_dtype,
@@ -395,10 +563,36 @@ extern "C" int cqkv_flash_attn(const void *q, const int64_t q_strides[3], const 
     a.wr = window_right;
     a.scale_log2 = softmax_scale * kLog2e;
     a.batch = batch;
+    // V^T scratch (stream-ordered: freed after the launches that use it)
+    a.vt_len = (kv_len + kPfBK - 1) / kPfBK * kPfBK;
+    void *vt = nullptr;
+    const size_t vt_bytes = (size_t)batch * kv_heads * kPfD * a.vt_len * 2;
+    CQKV_HIP_CHECK(hipMallocAsync(&vt, vt_bytes, st));
+    a.vt = (const uint16_t *)vt;
+    // the FP8 append runs inside the pre-pass when value tiles line up (position % 8 == 0),
+    // else as two cqkv_quant_append launches after the attention
+    const bool fused = k_cache != nullptr && position % 8 == 0;
+    if (fused) {
+        a.append = 1;
+        a.position = position;
+        a.kc = (uint8_t *)k_cache->codes;
+        a.ks = (uint8_t *)k_cache->scales;
+        a.vc = (uint8_t *)v_cache->codes;
+        a.vs = (uint8_t *)v_cache->scales;
+        a.kc_plane = (uint32_t)cqkv_codes_plane_bytes(CQKV_FMT_FP8, kPfD, k_cache->capacity);
+        a.ks_plane = (uint32_t)cqkv_scales_plane_bytes(CQKV_FMT_FP8, kPfD, k_cache->capacity);
+        a.vc_plane = (uint32_t)cqkv_codes_plane_bytes(CQKV_FMT_FP8, kPfD, v_cache->capacity);
+        a.vs_plane = (uint32_t)cqkv_scales_plane_bytes(CQKV_FMT_FP8, kPfD, v_cache->capacity);
+    }
+    hipLaunchKernelGGL(prefill_stage_kernel, dim3(a.vt_len / kPfBK, kv_heads, batch), dim3(256),
+                       0, st, a);
     const dim3 grid(a.q_blocks * kv_heads * (a.group / a.heads_per_wg) * batch);
     hipLaunchKernelGGL(prefill_kernel, grid, dim3(kPfWaves * 64), 0, st, a);
-    CQKV_HIP_CHECK(hipGetLastError());
-    if (k_cache) {
+    hipError_t le = hipGetLastError();
+    hipError_t fe = hipFreeAsync(vt, st);
+    if (le != hipSuccess) return fail(CQKV_ERR_HIP, "cqkv_flash_attn: launch: %s", hipGetErrorString(le));
+    CQKV_HIP_CHECK(fe);
+    if (k_cache && !fused) {
         // K / V are (batch, kv_len, kv_heads, D): the append kernel's (batch, head, token)
         const int64_t ks[3] = {k_strides[0], k_strides[2], k_strides[1]};
         const int64_t vs[3] = {v_strides[0], v_strides[2], v_strides[1]};

@@ -60,8 +60,11 @@ def test_prefill_rows_without_keys_are_zero(cq, dev):
     assert_close_bf16(got, want)
 
 
-def test_prefill_fused_fp8_append(cq, dev):
-    b, s, hq, hkv, d, pos = 2, 150, 8, 2, 128, 37
+@pytest.mark.parametrize("pos", [37, 40, 0])
+def test_prefill_fused_fp8_append(cq, dev, pos):
+    """Positions that are multiples of 8 take the in-pre-pass append (150 tokens: a partial last
+    8-token group keeps the cache bytes past it), others the separate append launches."""
+    b, s, hq, hkv, d = 2, 150, 8, 2, 128
     q = bf16_randn(11, (b, s, hq, d))
     k = bf16_randn(12, (b, s, hkv, d))
     v = bf16_randn(13, (b, s, hkv, d))
@@ -102,6 +105,14 @@ def test_prefill_config4_full_size_sampled_rows(cq, dev):
         want.append(O.round_bf16((p @ vv / p.sum()).astype(np.float32)))
         got.append(on[bi, i, h])
     assert_close_bf16(np.array(got), np.array(want))
-    # fused append: per-row FP8 scales equal absmax / 448 of the bf16 rows (all rows)
+    # fused append: per-row FP8 scales equal absmax / 448 of the bf16 rows (all rows), and the
+    # codes of batch 0's first 512 tokens and last 64 tokens equal the reference encoder's
     ks = kc.scales.view(torch.float32).view(b, hkv, s).cpu().numpy()
     np.testing.assert_array_equal(ks, (np.abs(kn).max(-1).transpose(0, 2, 1) / np.float32(448)))
+    vs = vc.scales.view(torch.float32).view(b, hkv, s).cpu().numpy()
+    np.testing.assert_array_equal(vs, (np.abs(vn).max(-1).transpose(0, 2, 1) / np.float32(448)))
+    for side, x in ((kc, k), (vc, v)):
+        rows = cq.rows_export(side, s).cpu().numpy().view(np.uint32)
+        xs = x[:1].permute(0, 2, 1, 3).cpu()
+        for lo, hi in ((0, 512), (s - 64, s)):
+            np.testing.assert_array_equal(rows[:1, :, lo:hi], oracle_rows(cq.FP8, xs[:, :, lo:hi]))
