@@ -101,6 +101,35 @@ __device__ inline uint32_t e4m3_encode(float f) {
     return s | (code > 0x7eu ? 0x7eu : code);
 }
 
+// The quotient x / s of the FP8 row encoder, correctly rounded, from r = 1 / s (correctly
+// rounded, computed once per row): q0 = x r, then one FMA correction q0 + r (x - q0 s) - the
+// correctly rounded quotient when the residual does not underflow (Markstein's theorem on
+// FMA-based division, P. Markstein, "IA-64 and Elementary Functions", 2000). Below |x| = 2^-96
+// the residual may underflow and the IEEE division is used. Where the quotient itself
+// underflows it can differ from x / s in its last bits, but every such quotient encodes to the
+// same E4M3 code (signed zero).
+__device__ inline float fp8_row_quotient(float x, float s, float r) {
+    const float q0 = x * r;
+    const float q = __builtin_fmaf(__builtin_fmaf(-q0, s, x), r, q0);
+    return __builtin_fabsf(x) < 0x1p-96f ? x / s : q;
+}
+
+// E4M3 codes of two quotients (|q| <= 448 * (1 + 2^-23)): the gfx950 conversion rounds to
+// nearest-even with the same subnormal and signed-zero results as e4m3_encode on that range
+// (all 2^31 - 2^23 f32 values with |q| <= 449 compared).
+__device__ inline uint32_t e4m3_encode2(float q0, float q1) {
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q0, q1, 0, false) & 0xffffu;
+}
+
+// Codes of x0 / s and x1 / s (low byte: x0) for the FP8 row encoder, r = 1 / s. Non-finite
+// inputs or scales take the division and the software encoder (the reference's NaN / infinity
+// results); finite ones the fast path above.
+__device__ inline uint32_t fp8_row_codes(float x0, float x1, float s, float r) {
+    if (__builtin_isfinite(x0) && __builtin_isfinite(x1) && __builtin_isfinite(s))
+        return e4m3_encode2(fp8_row_quotient(x0, s, r), fp8_row_quotient(x1, s, r));
+    return e4m3_encode(x0 / s) | (e4m3_encode(x1 / s) << 8);
+}
+
 __device__ inline uint32_t fp4_encode(float f) {
     const uint32_t s = (__float_as_uint(f) >> 28) & 8u;
     const float a = __builtin_fabsf(f);

@@ -384,7 +384,7 @@ constexpr int kStRow = 68;  // LDS row stride of the pre-pass tiles in 32-bit wo
 __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t vtile[kPfBK * kStRow];
     __shared__ __attribute__((aligned(16))) uint32_t ktile[kPfBK * kStRow];
-    __shared__ float vscale[kPfBK];
+    __shared__ float vscale[kPfBK], vrcp[kPfBK];
     const int kt = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x;
     const uint16_t *vplane = a.v + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
@@ -439,6 +439,7 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
     const float vsc = vmax > 0.0f ? vmax / 448.0f : 1.0f;
     if (qd == 0) {
         vscale[r] = vsc;
+        vrcp[r] = 1.0f / vsc;
         if (live) {
             ((float *)(a.ks + plane * a.ks_plane))[a.position + t] = ksc;
             ((float *)(a.vs + plane * a.vs_plane))[a.position + t] = vsc;
@@ -446,13 +447,14 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
     }
     // ---- key codes: the thread's 32 dims of its token, row-major ----
     if (live) {
+        const float kr = 1.0f / ksc;
         uint32_t cw[8];
 #pragma unroll
         for (int w = 0; w < 8; ++w) {
             const uint32_t x01 = ktile[r * kStRow + 16 * qd + 2 * w];
             const uint32_t x23 = ktile[r * kStRow + 16 * qd + 2 * w + 1];
-            cw[w] = e4m3_encode(bf16_lo(x01) / ksc) | (e4m3_encode(bf16_hi(x01) / ksc) << 8) |
-                    (e4m3_encode(bf16_lo(x23) / ksc) << 16) | (e4m3_encode(bf16_hi(x23) / ksc) << 24);
+            cw[w] = fp8_row_codes(bf16_lo(x01), bf16_hi(x01), ksc, kr) |
+                    (fp8_row_codes(bf16_lo(x23), bf16_hi(x23), ksc, kr) << 16);
         }
         uint8_t *dst = a.kc + plane * a.kc_plane + (int64_t)(a.position + t) * kPfD + 32 * qd;
         *(u32x4 *)dst = u32x4{cw[0], cw[1], cw[2], cw[3]};
@@ -472,9 +474,10 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
         for (int sl = 0; sl < 8; ++sl) {
             if (t0 + sl < a.kv_len) {
                 const uint32_t x = vtile[(8 * g + sl) * kStRow + dp];
-                const float sc = vscale[8 * g + sl];
-                vw0 |= (uint64_t)e4m3_encode(bf16_lo(x) / sc) << (8 * sl);
-                vw1 |= (uint64_t)e4m3_encode(bf16_hi(x) / sc) << (8 * sl);
+                const float sc = vscale[8 * g + sl], rc = vrcp[8 * g + sl];
+                const uint32_t c01 = fp8_row_codes(bf16_lo(x), bf16_hi(x), sc, rc);
+                vw0 |= (uint64_t)(c01 & 0xffu) << (8 * sl);
+                vw1 |= (uint64_t)(c01 >> 8) << (8 * sl);
                 mask |= 1u << sl;
             }
         }

@@ -28,7 +28,27 @@ struct AppendArgs {
     uint32_t sign_bits[4];  // TURBO4: bit j set -> column j of the rotation has sign -1
     float rot_scale;        // TURBO4: 1 / sqrt(D) in f32
     float bnd[16];          // TURBO4: the 15 codebook boundaries (+inf padded)
+    int32_t pair_loads;     // elements 2l, 2l+1 of every row are one aligned 4 / 8-byte word
 };
+
+// elements idx, idx + 1 of x as floats (one load when `pair` says they form an aligned word)
+__device__ inline void load_pair(const void *p, int64_t idx, int dtype, bool pair, float &x0,
+                                 float &x1) {
+    if (pair) {
+        if (dtype == 2) {
+            const f32x2 w = *(const f32x2 *)((const float *)p + idx);
+            x0 = w.x;
+            x1 = w.y;
+        } else {
+            const uint32_t w = *(const uint32_t *)((const uint16_t *)p + idx);
+            x0 = dtype == 0 ? bf16_bits_to_f32(w & 0xffffu) : f16_bits_to_f32(w & 0xffffu);
+            x1 = dtype == 0 ? bf16_bits_to_f32(w >> 16) : f16_bits_to_f32(w >> 16);
+        }
+    } else {
+        x0 = load_elem(p, idx, dtype);
+        x1 = load_elem(p, idx + 1, dtype);
+    }
+}
 
 // In-register Walsh-Hadamard transform over 2 * `lanes` elements held as (v0, v1) = elements
 // (2l, 2l+1): y_i = sum_j (-1)^popcount(i & j) x_j (Sylvester order, unnormalised).
@@ -69,18 +89,18 @@ __global__ __launch_bounds__(256) void quant_append_kernel(AppendArgs a) {
 
     for (int t = t_lo; t < t_hi; ++t) {
         float x0 = 0.0f, x1 = 0.0f;
-        if (active) {
-            const int64_t xi = xrow0 + (int64_t)(t - pos) * a.st + 2 * lane;
-            x0 = load_elem(a.x, xi, a.x_dtype);
-            x1 = load_elem(a.x, xi + 1, a.x_dtype);
-        }
+        if (active)
+            load_pair(a.x, xrow0 + (int64_t)(t - pos) * a.st + 2 * lane, a.x_dtype,
+                      a.pair_loads != 0, x0, x1);
         uint32_t c0, c1;
         float row_scale = 0.0f;
         if constexpr (FMT == CQKV_FMT_FP8) {
             const float amax = wave_max(fmaxf(__builtin_fabsf(x0), __builtin_fabsf(x1)));
             const float s = amax > 0.0f ? amax / 448.0f : 1.0f;
-            c0 = e4m3_encode(x0 / s);
-            c1 = e4m3_encode(x1 / s);
+            const float r = 1.0f / s;
+            const uint32_t c01 = fp8_row_codes(x0, x1, s, r);
+            c0 = c01 & 0xffu;
+            c1 = c01 >> 8;
             row_scale = s;
         } else if constexpr (FMT == CQKV_FMT_MXFP4) {
             const float amax = group_max(fmaxf(__builtin_fabsf(x0), __builtin_fabsf(x1)), 16);
@@ -197,6 +217,11 @@ int quant_append_launch(const cqkv_side *side, const void *x, int32_t x_dtype,
     a.sb = xs[0];
     a.sh = xs[1];
     a.st = xs[2];
+    {
+        const size_t esz = x_dtype == CQKV_F32 ? 4 : 2;
+        a.pair_loads = (xs[0] % 2 == 0 && xs[1] % 2 == 0 && xs[2] % 2 == 0 &&
+                        ((uintptr_t)x % (2 * esz)) == 0) ? 1 : 0;
+    }
     a.codes = (uint8_t *)side->codes;
     a.scales = (uint8_t *)side->scales;
     a.codes_plane = (uint32_t)cqkv_codes_plane_bytes(side->format, side->head_dim, side->capacity);

@@ -47,6 +47,31 @@ def test_append_codes_bit_exact(cq, dev, fmt, is_value, d):
     np.testing.assert_array_equal(got, want)
 
 
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp4"])
+@pytest.mark.parametrize("layout", ["f32", "f16", "bf16_odd_stride"])
+def test_append_input_dtypes_and_strides(cq, dev, fmt, layout):
+    """f32 / f16 rows (paired loads of one 8- / 4-byte word) and bf16 rows whose element pairs
+    are not word-aligned (token stride 129: single-element loads) encode bit-exactly."""
+    f = FMTS[fmt]
+    b, h, t, d = 2, 2, 21, 128
+    x = kv_source(23, (b, h, t, d), outliers=True)
+    if layout == "f32":
+        xin = x.float() * 1.001  # values off the bf16 grid
+        xref = xin
+    elif layout == "f16":
+        xin = x.to(torch.float16)
+        xref = xin.float()
+    else:
+        big = torch.zeros(b, h, t, d + 1, dtype=torch.bfloat16)
+        big[..., :d] = x
+        xin = big[..., :d]
+        xref = x
+    side = cq.CacheSide.empty(f, fmt == "fp8", b, h, d, 32, dev)
+    cq.quant_append(side, xin.to(dev) if layout != "bf16_odd_stride" else big.to(dev)[..., :d])
+    rows = O.quantize_rows(f, 0, xref.float().numpy())
+    np.testing.assert_array_equal(export_np(cq, side, t), rows)
+
+
 @pytest.mark.parametrize("is_value", [False, True])
 def test_append_per_batch_positions(cq, dev, is_value):
     b, h, d = 4, 2, 128
