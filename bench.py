@@ -136,9 +136,8 @@ def decode_case(cq, dev, stream, fmt, b, hq, hkv, d, ctx, steps, warmup, lens=No
     q = kv_gpu((b, hq, 1, d), 5, dev, outliers=False)
     out = torch.empty_like(q)
     kv_lens = None if lens is None else torch.tensor(lens, dtype=torch.int32, device=dev)
-    # the split rule picks at most 256 splits; size the workspace for that so ragged calls
-    # (whose split count depends on the longest sequence) never allocate inside the timing
-    splits = cq.decode_splits(b, hkv, ctx) if lens is None else 256
+    # workspace for the split count the call will pick, so no call allocates inside the timing
+    splits = cq.decode_splits(b, hkv, ctx, fmt, ragged=lens is not None)
     ws = torch.zeros(max(1, cq.decode_workspace_bytes(b, hq, 1, d, splits)), dtype=torch.uint8,
                      device=dev)
 

@@ -62,7 +62,7 @@ def lib() -> ctypes.CDLL:
         L.cqkv_quant_append.argtypes = [SP, P, i32, I64P, i32, i32, P, i32, P]
         L.cqkv_decode_workspace_bytes.argtypes = [i32, i32, i32, i32, i32]
         L.cqkv_decode_workspace_bytes.restype = sz
-        L.cqkv_decode_splits.argtypes = [i32, i32, i32]
+        L.cqkv_decode_splits.argtypes = [i32, i32, i32, i32, i32]
         L.cqkv_decode_splits.restype = i32
         L.cqkv_decode_attention.argtypes = [P, i32, I64P, SP, SP, i32, i32, i32, P, i32, f32,
                                             i32, i32, P, i32, I64P, i32, P, sz, P]
@@ -166,8 +166,9 @@ def decode_workspace_bytes(batch, q_heads, q_len, head_dim, splits) -> int:
     return lib().cqkv_decode_workspace_bytes(batch, q_heads, q_len, head_dim, splits)
 
 
-def decode_splits(batch, kv_heads, kv_len) -> int:
-    return lib().cqkv_decode_splits(batch, kv_heads, kv_len)
+def decode_splits(batch, kv_heads, kv_len, fmt: int = FP8, ragged: bool = False) -> int:
+    """Key splits decode_attention uses with splits=0 (size the workspace with it)."""
+    return lib().cqkv_decode_splits(fmt, batch, kv_heads, kv_len, int(ragged))
 
 
 def decode_attention(q: torch.Tensor, k: CacheSide, v: CacheSide, kv_len: int,

@@ -578,30 +578,37 @@ int fill_turbo_args(const cqkv_side *s, uint32_t sign_bits[4], float *rot_scale,
 static int tiles_of(int kv_len) { return (kv_len + 31) / 32; }
 
 // Key splits per (batch, kv head). One 8-wavefront workgroup per plane fills a CU of the
-// MI355X (256 CUs, two waves per SIMD at this register budget): split only when there are fewer
-// planes than CUs, and then into pieces of at least 16 tiles (two per wavefront). Ragged batches
-// (per-sequence lengths) are split into pieces of at most 128 tiles (4096 keys) so long and short
-// sequences even out across CUs.
+// MI355X (256 CUs, two waves per SIMD at this register budget; twice as many workgroups of 4
+// wavefronts): split only when there are fewer planes than that, and then into pieces of at
+// least two tiles per wavefront. Ragged batches (per-sequence lengths) are split into pieces of
+// at most 128 tiles (4096 keys) so long and short sequences even out across CUs.
 constexpr int kWaves = 8;
 constexpr int kCUs = 256;
 
-static int auto_splits(int batch, int kv_heads, int kv_len, bool ragged) {
+static int auto_splits(int batch, int kv_heads, int kv_len, bool ragged, int waves = kWaves) {
     const int planes = batch * kv_heads;
     const int tiles = tiles_of(kv_len);
-    int s = (kCUs + planes - 1) / planes;
+    const int wgs = kCUs * (kWaves / waves);  // workgroups that fill the chip
+    int s = (wgs + planes - 1) / planes;
     if (ragged) s = max(s, (tiles + 127) / 128);
-    s = min(s, max(1, tiles / 16));
+    s = min(s, max(1, tiles / (2 * waves)));
     s = max(1, min(s, 256));
     const int tps = (tiles + s - 1) / s;
     return max(1, (tiles + tps - 1) / tps);
 }
 
+// Wavefronts per workgroup: 8 for FP8 (HBM-bound: one workgroup per plane fills a CU), 4 for
+// the 4-bit formats (their decode is VALU-heavy; two or three independent workgroups per CU
+// hide each other's latencies better than one of 8 wavefronts: 10 % faster on BASELINE config 3).
+constexpr int waves_of(int format) { return format == CQKV_FMT_FP8 ? kWaves : 4; }
+
 template <int FMT>
 static void launch_decode(int d, dim3 grid, hipStream_t st, const DecodeArgs &a) {
+    constexpr int W = waves_of(FMT);
     if (d == 64)
-        hipLaunchKernelGGL((decode_kernel<FMT, 64, kWaves>), grid, dim3(kWaves * 64), 0, st, a);
+        hipLaunchKernelGGL((decode_kernel<FMT, 64, W>), grid, dim3(W * 64), 0, st, a);
     else
-        hipLaunchKernelGGL((decode_kernel<FMT, 128, kWaves>), grid, dim3(kWaves * 64), 0, st, a);
+        hipLaunchKernelGGL((decode_kernel<FMT, 128, W>), grid, dim3(W * 64), 0, st, a);
 }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -618,9 +625,10 @@ static size_t workspace_layout(int32_t batch, int32_t q_heads, int32_t q_len, in
 
 using namespace cqkv;
 
-extern "C" int32_t cqkv_decode_splits(int32_t batch, int32_t kv_heads, int32_t kv_len) {
+extern "C" int32_t cqkv_decode_splits(int32_t format, int32_t batch, int32_t kv_heads,
+                                      int32_t kv_len, int32_t ragged) {
     if (batch <= 0 || kv_heads <= 0 || kv_len <= 0) return 1;
-    return auto_splits(batch, kv_heads, kv_len, false);
+    return auto_splits(batch, kv_heads, kv_len, ragged != 0, waves_of(format));
 }
 
 extern "C" size_t cqkv_decode_workspace_bytes(int32_t batch, int32_t q_heads, int32_t q_len,
@@ -665,7 +673,8 @@ extern "C" int cqkv_decode_attention(const void *q, int32_t q_dtype, const int64
 
     const int tiles = max(1, tiles_of(kv_len));
     int s = splits > 0 ? min(splits, tiles)
-                       : auto_splits(batch, hkv, max(kv_len, 1), kv_lens != nullptr);
+                       : auto_splits(batch, hkv, max(kv_len, 1), kv_lens != nullptr,
+                                     waves_of(k->format));
     const int tps = (tiles + s - 1) / s;
     s = (tiles + tps - 1) / tps;
 

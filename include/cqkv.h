@@ -99,7 +99,11 @@ int cqkv_quant_append(const cqkv_side *side, const void *x, int32_t x_dtype,
  * cqkv_decode_workspace_bytes(); NULL = allocated (and freed) by the call. */
 size_t cqkv_decode_workspace_bytes(int32_t batch, int32_t q_heads, int32_t q_len, int32_t head_dim,
                                    int32_t splits);
-int32_t cqkv_decode_splits(int32_t batch, int32_t kv_heads, int32_t kv_len);
+/* The key splits cqkv_decode_attention uses with splits = 0 for a cache of `format`, `batch`
+ * sequences, `kv_heads` heads and largest length kv_len, with (ragged != 0) or without per-
+ * sequence lengths: size the workspace with it. */
+int32_t cqkv_decode_splits(int32_t format, int32_t batch, int32_t kv_heads, int32_t kv_len,
+                           int32_t ragged);
 int cqkv_decode_attention(const void *q, int32_t q_dtype, const int64_t q_strides[3],
                           const cqkv_side *k, const cqkv_side *v, int32_t batch, int32_t q_heads,
                           int32_t q_len, const int32_t *kv_lens, int32_t kv_len,

@@ -73,6 +73,10 @@ def test_workspace_and_split_plan(cq):
     s = cq.decode_splits(32, 8, 8192)
     assert 1 <= s <= 256
     assert cq.decode_splits(1, 8, 512) >= 1
+    # 4-bit formats run 4-wavefront workgroups: twice the workgroups, so at least as many splits
+    for fmt in (cq.MXFP4, cq.TURBO4):
+        assert cq.decode_splits(8, 8, 131072, fmt) >= cq.decode_splits(8, 8, 131072, cq.FP8)
+    assert cq.decode_splits(64, 8, 32768, cq.MXFP4, ragged=True) >= 8  # pieces of <= 4096 keys
 
 
 def test_argument_errors_are_status_codes(cq):
