@@ -299,25 +299,32 @@ __device__ inline void compute_tile(Tile<FMT, D> &cur, int tile, const DecodeArg
     }
     // O^T += V^T P^T: d-tile 2u + h, row r <-> head dim 32u + 2r + h
     if constexpr (FMT == CQKV_FMT_MXFP4) {
+        // value block u: P scaled by the keys' block-u scales, one bf16 operand (the E2M1 codes
+        // and E8M0 scales are exact; P rounds to 8 significant bits, as in a bf16 flash
+        // attention). The scale of E8M0 code c is the float with exponent field c (code 0: 0).
         uint32_t vw[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) vw[e] = (uint32_t)__shfl((int)cur.vs, 8 * g + e);
+        if (t0 + 32 > L) {  // uniform: keys past the written length may hold any scale bytes
 #pragma unroll
-        for (int u = 0; u < NCH; ++u) {  // value block u: P scaled by the keys' block-u scales
-            float pv[8];
+            for (int e = 0; e < 8; ++e)
+                if (e >= nv) vw[e] = 0u;
+        }
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float sc = e8m0_scale((vw[e] >> (8 * u)) & 0xffu);
-                pv[e] = (e < nv && p[e] > 0.0f) ? p[e] * sc : 0.0f;
+        for (int u = 0; u < NCH; ++u) {
+            u32x4 pw;
+            uint32_t *pwp = (uint32_t *)&pw;
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const float s0 = __uint_as_float(((vw[e] >> (8 * u)) & 0xffu) << 23);
+                const float s1 = __uint_as_float(((vw[e + 1] >> (8 * u)) & 0xffu) << 23);
+                pwp[e / 2] = pack_bf16x2(p[e] * s0, p[e + 1] * s1);
             }
-            op_t<FMT> phi, plo;
-            split8(pv, phi, plo);
+            const op_t<FMT> pb = __builtin_bit_cast(op_t<FMT>, pw);
             const op_t<FMT> v0 = decode8<FMT>(cur.v[u][0], 0, 1.0f, tab);
             const op_t<FMT> v1 = decode8<FMT>(cur.v[u][1], 0, 1.0f, tab);
-            acc[2 * u] = mfma16x16x32(v0, phi, acc[2 * u]);
-            acc[2 * u + 1] = mfma16x16x32(v1, phi, acc[2 * u + 1]);
-            acc[2 * u] = mfma16x16x32(v0, plo, acc[2 * u]);
-            acc[2 * u + 1] = mfma16x16x32(v1, plo, acc[2 * u + 1]);
+            acc[2 * u] = mfma16x16x32(v0, pb, acc[2 * u]);
+            acc[2 * u + 1] = mfma16x16x32(v1, pb, acc[2 * u + 1]);
         }
     } else {
         float pv[8], sv[8];
