@@ -48,7 +48,7 @@ struct DecodeArgs {
     int32_t q_heads, kv_heads, group, q_len, ncols;
     float scale_log2;  // softmax scale * log2(e)
     int32_t wl, wr;
-    int32_t tiles_per_split, splits;
+    int32_t tiles_per_split, splits, batch;
     float *part_o;       // (splits, rows, D) f32, normalised partial outputs
     float *part_lse;     // (splits, rows) f32, log2-domain lse of each split
     void *out;
@@ -367,7 +367,13 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     __shared__ float sm_m[WAVES][16], sm_l[WAVES][16];
     __shared__ uint32_t sm_tab[kTurbo ? 256 : 1];
 
-    const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+    // 1-D grid, plane fastest: workgroup ids are dealt round-robin to the 8 XCDs, so with
+    // kv_heads a multiple of 8 each XCD takes whole planes of one kv head from every sequence -
+    // the same length mix everywhere (a split-fastest order would send split i of every plane to
+    // one XCD, and in a ragged batch the high splits are mostly empty)
+    const int planes = a.batch * a.kv_heads;
+    const int split = (int)blockIdx.x / planes, plane_id = (int)blockIdx.x % planes;
+    const int hk = plane_id % a.kv_heads, b = plane_id / a.kv_heads;
     // the wavefront index is uniform: keep it scalar so the tile loop stays a scalar loop
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, g = lane >> 4;
@@ -473,7 +479,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
         sm_l[wave][n] = l_col;
     }
     __syncthreads();
-    const int rows = (int)gridDim.z * a.q_heads * a.q_len;
+    const int rows = a.batch * a.q_heads * a.q_len;
     const bool single = a.splits == 1;
     for (int idx = threadIdx.x; idx < a.ncols * D; idx += NT) {
         const int c = idx / D, d = idx % D;
@@ -711,6 +717,7 @@ extern "C" int cqkv_decode_attention(const void *q, int32_t q_dtype, const int64
     a.wr = window_right;
     a.tiles_per_split = tps;
     a.splits = s;
+    a.batch = batch;
     a.out = out;
     a.out_dtype = out_dtype;
     a.q_split = (q_dtype != CQKV_BF16 || k->format == CQKV_FMT_TURBO4) ? 1 : 0;
@@ -744,7 +751,7 @@ extern "C" int cqkv_decode_attention(const void *q, int32_t q_dtype, const int64
         a.part_lse = (float *)((char *)ws + lse_off);
     }
 
-    dim3 grid(s, hkv, batch);
+    const dim3 grid(s * hkv * batch);
     switch (k->format) {
     case CQKV_FMT_FP8: launch_decode<CQKV_FMT_FP8>(d, grid, st, a); break;
     case CQKV_FMT_MXFP4: launch_decode<CQKV_FMT_MXFP4>(d, grid, st, a); break;
