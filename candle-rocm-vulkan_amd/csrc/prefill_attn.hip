@@ -12,17 +12,18 @@
 // Kernel shape (one workgroup = 8 wavefronts = 64 queries x 4 query heads sharing a kv head, 32
 // queries per wavefront):
 //  * Both products run on v_mfma_f32_32x32x16_bf16. S^T = K Q^T: K (32 keys x 16 dims) comes
-//    from LDS with ds_read_b128, Q^T stays in registers for the whole key loop. The S^T
-//    accumulator of a lane holds one query column, so the row-wise online softmax needs one
-//    cross-lane step, and its registers 4i0..4i0+7 are directly the P^T operand of a 16-key
-//    step of O^T = V^T P^T (the k order inside a step is permuted to match).
-//  * V^T operands come from the row-major V tile in LDS through ds_read_b64_tr_b16: in each
-//    16-lane group, source lane 4p+q points at V[key0 + p][d0 + 4q .. +3], and lane i receives
-//    V[key0 .. key0 + 3][d0 + i] - four keys of one head dim, the k-slots the MFMA needs.
-//  * K / V tiles of 64 keys stream through a 4-stage LDS ring with asynchronous global -> LDS
-//    copies (global_load_lds_dwordx4), issued three tiles ahead; one barrier per tile. Chunks of
-//    a row are XOR-swizzled so both LDS read patterns are free of bank conflicts.
-//  * Two wavefronts per SIMD: one's softmax (VALU) overlaps the other's MFMAs.
+//    from LDS with ds_read_b128, Q^T (pre-scaled by scale * log2(e), rounded to bf16) stays in
+//    registers for the whole key loop. The S^T accumulator of a lane holds one query column, so
+//    the row-wise online softmax needs one cross-lane step, and its registers 4i0..4i0+7 are
+//    directly the P^T operand of a 16-key step of O^T = V^T P^T (the k order inside a step is
+//    permuted to match).
+//  * V^T operands come by ds_read_b128 from a V^T tile written by the pre-pass
+//    (prefill_stage_kernel) with its keys already in that permuted order.
+//  * K and V^T tiles of 64 keys stream through two 4-stage LDS rings, filled by asynchronous
+//    buffer_load_dwordx4 ... lds copies issued two tiles ahead; one barrier per tile. Chunks of a
+//    row are XOR-swizzled so the reads are free of bank conflicts.
+//  * The two wavefronts of a SIMD ping-pong: between two barriers one runs its MFMAs (P V of the
+//    previous tile, S of this one) while the other runs its softmax on the VALU, then they swap.
 //  * Causal work is uneven: the workgroups with the most key tiles are dispatched first.
 #include "cqkv_device.h"
 #include "cqkv_host.h"
@@ -84,46 +85,35 @@ constexpr int kPfVtRow = 128;
 constexpr int kPfWaves = 8;               // 4 query heads x 2 halves of the 64 queries
 constexpr int kPfRow = 256;
 constexpr int kPfHalf = kPfBK * kPfRow;   // one K or V tile: 16 KB
-constexpr int kPfStage = 2 * kPfHalf;     // K then V
 
 typedef __attribute__((address_space(3))) void lds_void;
 
 #define PF_INLINE __device__ __attribute__((always_inline)) inline
 
-// Asynchronous global -> LDS copy of key tile kt into `stage`: K rows (keys) and V^T rows (head
-// dims), one global_load_lds_dwordx4 (1 KB) per 4 K rows / 8 V^T rows. Wavefront w copies K rows
-// 8w .. 8w+7 and V^T rows 16w .. 16w+15. K: lane l writes chunk position l % 16 of row l / 16,
-// so it loads logical chunk (l % 16) ^ swz(row); rows past the keys repeat the last key. V^T:
-// lane l writes chunk position l % 8 of row l / 8 (the pre-pass zero-fills keys past the end).
-PF_INLINE void pf_issue_tile(uint8_t *stage, const uint16_t *kplane, const uint16_t *vtplane,
-                             int64_t k_st, int vt_len, const uint32_t (&koff)[2],
-                             const uint32_t (&voff)[2], int kt, int kv_len, int wave, int lane) {
+// Asynchronous global -> LDS copy of key tile kt into the stages kstage / vstage: K rows (keys)
+// and V^T rows (head dims), one buffer_load_dwordx4 ... lds (1 KB) per 4 K rows / 8 V^T rows.
+// Wavefront w copies K rows 8w .. 8w+7 and V^T rows 16w .. 16w+15. K: lane l writes chunk
+// position l % 16 of row l / 16, so it loads logical chunk (l % 16) ^ swz(row); the buffer
+// range ends at the last key, so rows past it read zeros. V^T: lane l writes chunk position
+// l % 8 of row l / 8 (the pre-pass zero-fills keys past the end). Buffer loads count on vmcnt
+// only, so the LDS reads of other stages need no wait on these copies.
+PF_INLINE void pf_issue_tile(uint8_t *kstage, uint8_t *vstage, const uint16_t *kplane,
+                             const uint16_t *vtplane, int64_t k_st, int vt_len,
+                             const uint32_t (&koff)[2], const uint32_t (&voff)[2], int kt,
+                             int kv_len, int wave) {
     const int row0 = kt * kPfBK;
-    if (row0 + kPfBK <= kv_len) {
-        // a wave-uniform tile address plus a fixed per-lane byte offset
-        const uint8_t *ktile = (const uint8_t *)(kplane + (int64_t)row0 * k_st);
+    const int nvalid = min(kPfBK, kv_len - row0);
+    const rsrc_t kr = make_rsrc(kplane + (int64_t)row0 * k_st,
+                                (uint32_t)((int64_t)(nvalid - 1) * k_st * 2 + kPfRow));
 #pragma unroll
-        for (int r4 = 0; r4 < 2; ++r4)
-            __builtin_amdgcn_global_load_lds((const void *)(ktile + koff[r4]),
-                                             (lds_void *)(stage + (8 * wave + 4 * r4) * kPfRow),
-                                             16, 0, 0);
-    } else {
-#pragma unroll
-        for (int r4 = 0; r4 < 2; ++r4) {
-            const int row = 8 * wave + 4 * r4 + (lane >> 4);
-            const int key = min(row0 + row, kv_len - 1);
-            const int c = (lane & 15) ^ swz(row);
-            __builtin_amdgcn_global_load_lds((const void *)(kplane + (int64_t)key * k_st + 8 * c),
-                                             (lds_void *)(stage + (8 * wave + 4 * r4) * kPfRow),
-                                             16, 0, 0);
-        }
-    }
-    const uint8_t *vtile = (const uint8_t *)(vtplane + row0);
+    for (int r4 = 0; r4 < 2; ++r4)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void *)(kstage + (8 * wave + 4 * r4) * kPfRow),
+                                                 16, koff[r4], 0, 0, 0);
+    const rsrc_t vr = make_rsrc(vtplane + row0, (uint32_t)(((int64_t)kPfD * vt_len - row0) * 2));
 #pragma unroll
     for (int r8 = 0; r8 < 2; ++r8)
-        __builtin_amdgcn_global_load_lds((const void *)(vtile + voff[r8]),
-                                         (lds_void *)(stage + kPfHalf + (16 * wave + 8 * r8) * kPfVtRow),
-                                         16, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_void *)(vstage + (16 * wave + 8 * r8) * kPfVtRow),
+                                                 16, voff[r8], 0, 0, 0);
 }
 // byte offsets of this lane's copy sources from a tile's first K row / first V^T key
 PF_INLINE void pf_copy_offsets(uint32_t (&koff)[2], uint32_t (&voff)[2], int64_t k_st, int vt_len,
@@ -147,55 +137,103 @@ constexpr int kPfCopiesPerTile = 4;  // global_load_lds per wavefront per tile
 struct PfState {
     bf16x8 qop[8];   // Q^T operands (16-dim steps ks) of this wavefront's 32 queries
     f32x16 acc[4];   // O^T: 32-dim block md
+    f32x16 negm;     // -m_run (0 before the first key) in every register: the S^T accumulator seed
     float m_run, l_run;
     int qlo, qhi;    // visible keys of this lane's query
 };
 
-// S^T (64 keys x 32 queries) = K Q^T for the tile at k_lds.
+// Orders the 16 LDS reads and 16 MFMAs of a product block: kPfReadAhead reads first, then one
+// MFMA per read, so each MFMA's operand was requested kPfReadAhead MFMAs earlier (left to
+// itself, the scheduler waits for every read before each pair of MFMAs).
+constexpr int kPfReadAhead = 4;
+PF_INLINE void pf_pipe_schedule() {
+    constexpr int kDsRead = 0x100, kMfma = 0x008;  // sched_group_barrier instruction classes
+#pragma unroll
+    for (int i = 0; i < kPfReadAhead; ++i) __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+#pragma unroll
+    for (int i = 0; i < 16 - kPfReadAhead; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < kPfReadAhead; ++i) __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+}
+
+// S^T (64 keys x 32 queries) = K Q^T for the tile at k_lds; the two 32-key blocks alternate.
 PF_INLINE void pf_qk(f32x16 (&s)[2], const PfState &st, const uint8_t *k_lds, int lane) {
     const int qr = lane & 31, h = lane >> 5;
+    const int sw = swz(qr);  // swz(32 + qr) == swz(qr)
+    bf16x8 kop[16];
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-        s[mb] = f32x16{};
-        const int row = 32 * mb + qr;
-        const uint8_t *rbase = k_lds + row * kPfRow;
-        const int sw = swz(row);
+    for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-            const bf16x8 kop =
-                __builtin_bit_cast(bf16x8, *(const u32x4 *)(rbase + (((2 * ks + h) ^ sw) << 4)));
-            s[mb] = mfma32x32x16(kop, st.qop[ks], s[mb]);
-        }
-    }
+        for (int mb = 0; mb < 2; ++mb)
+            kop[2 * ks + mb] = __builtin_bit_cast(
+                bf16x8, *(const u32x4 *)(k_lds + (32 * mb + qr) * kPfRow + (((2 * ks + h) ^ sw) << 4)));
+    s[0] = st.negm;
+    s[1] = st.negm;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) s[mb] = mfma32x32x16(kop[2 * ks + mb], st.qop[ks], s[mb]);
+    pf_pipe_schedule();
 }
 
 // masks scores of keys outside the lane's visible range (tiles that cross a range end only)
 PF_INLINE void pf_mask(f32x16 (&s)[2], const PfState &st, int k0, int lane) {
     const int h = lane >> 5;
+    // key - qlo of register 0, made opaque so the per-register offsets stay immediates
+    int u = k0 + 4 * h - st.qlo;
+    asm volatile("" : "+v"(u));
+    const uint32_t w = (uint32_t)(st.qhi - st.qlo);
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const int key = k0 + 32 * mb + 8 * (j >> 2) + 4 * h + (j & 3);
-            if (!(key >= st.qlo && key < st.qhi)) s[mb][j] = -__builtin_inff();
-        }
+        for (int j = 0; j < 16; ++j)
+            if ((uint32_t)(u + 32 * mb + 8 * (j >> 2) + (j & 3)) >= w) s[mb][j] = -__builtin_inff();
 }
 
-// Online softmax over the tile: P^T operands of the four 16-key steps, running maximum (lazy:
-// kept unless exceeded by more than 2^8, so p < 2^8 and rescaling is rare) and row sum.
-PF_INLINE void pf_softmax(bf16x8 (&pop)[4], const f32x16 (&s)[2], PfState &st, float scale_log2) {
+PF_INLINE float pf_max_halves(float x) {  // max of lanes l and l ^ 32
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+PF_INLINE float pf_sum_halves(float x) {  // sum of lanes l and l ^ 32
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Online softmax over the tile. Q carries scale * log2(e) and the S^T accumulators start at
+// -m_run, so s already is the exponent of p = exp2(s) relative to the running maximum m_run.
+// The maximum is lazy: it moves (s is shifted, O and the row sum rescaled) only when a score
+// exceeds it by more than 2^8, or on a row's first keys; otherwise p < 2^8 and the step costs
+// one exp2 per score.
+PF_INLINE void pf_softmax(bf16x8 (&pop)[4], f32x16 (&s)[2], PfState &st) {
     float mx = -__builtin_inff();
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[mb][j]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
-    const float m_new = mx > st.m_run + 8.0f ? mx : st.m_run;
-    const bool none = m_new == -__builtin_inff();
-    const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(st.m_run - m_new);
-    const float mneg = none ? 0.0f : m_new;
-    // p = exp2(s * scale - m), packed to bf16; the row sum adds the bf16 values the product
-    // uses, two per dot2 instruction
+    mx = pf_max_halves(mx);
+    const bool fresh = st.m_run == -__builtin_inff();
+    const bool need = fresh ? mx != -__builtin_inff() : mx > 8.0f;
+    if (__builtin_expect(__any(need), 0)) {
+        const float shift = need ? mx : 0.0f;
+        const float m_new = need ? (fresh ? 0.0f : st.m_run) + mx : st.m_run;
+        const float alpha = need ? __builtin_amdgcn_exp2f(st.m_run - m_new) : 1.0f;
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) s[mb][j] -= shift;
+#pragma unroll
+        for (int md = 0; md < 4; ++md) st.acc[md] *= alpha;
+        st.l_run *= alpha;
+        st.m_run = m_new;
+        const float nm = m_new == -__builtin_inff() ? 0.0f : -m_new;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) st.negm[j] = nm;
+    }
+    // p = exp2(s), packed to bf16; the row sum adds the bf16 values the product uses, two per
+    // dot2 instruction
     const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
     float psum = 0.0f;
 #pragma unroll
@@ -205,22 +243,15 @@ PF_INLINE void pf_softmax(bf16x8 (&pop)[4], const f32x16 (&s)[2], PfState &st, f
             uint32_t w[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float p0 = __builtin_amdgcn_exp2f(
-                    __builtin_fmaf(s[mb][8 * half + 2 * e], scale_log2, -mneg));
-                const float p1 = __builtin_amdgcn_exp2f(
-                    __builtin_fmaf(s[mb][8 * half + 2 * e + 1], scale_log2, -mneg));
+                const float p0 = __builtin_amdgcn_exp2f(s[mb][8 * half + 2 * e]);
+                const float p1 = __builtin_amdgcn_exp2f(s[mb][8 * half + 2 * e + 1]);
                 const bf16x2 pp = {(__bf16)p0, (__bf16)p1};
                 psum = __builtin_amdgcn_fdot2_f32_bf16(pp, ones, psum, false);
                 w[e] = __builtin_bit_cast(uint32_t, pp);
             }
             pop[2 * mb + half] = __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
         }
-    st.l_run = st.l_run * alpha + psum;
-    st.m_run = m_new;
-    if (__any(alpha != 1.0f)) {
-#pragma unroll
-        for (int md = 0; md < 4; ++md) st.acc[md] *= alpha;
-    }
+    st.l_run += psum;
 }
 
 // O^T += V^T P^T over the V^T tile at v_lds. 16-key step kk = keys 16 kk + [0, 16): the P^T
@@ -229,37 +260,36 @@ PF_INLINE void pf_softmax(bf16x8 (&pop)[4], const f32x16 (&s)[2], PfState &st, f
 // (bits 2 and 3 of the key swapped), so the A operand of lane (d, h) is chunk 2 kk + h of row d.
 PF_INLINE void pf_pv(PfState &st, const bf16x8 (&pop)[4], const uint8_t *v_lds, int lane) {
     const int qr = lane & 31, h = lane >> 5;
+    bf16x8 vt[16];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
         const uint32_t off = qr * kPfVtRow + (((2 * kk + h) ^ swz_vt(qr)) << 4);
 #pragma unroll
-        for (int md = 0; md < 4; ++md) {
-            const bf16x8 vt =
+        for (int md = 0; md < 4; ++md)
+            vt[4 * kk + md] =
                 __builtin_bit_cast(bf16x8, *(const u32x4 *)(v_lds + off + md * 32 * kPfVtRow));
-            st.acc[md] = mfma32x32x16(vt, pop[kk], st.acc[md]);
-        }
     }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int md = 0; md < 4; ++md) st.acc[md] = mfma32x32x16(vt[4 * kk + md], pop[kk], st.acc[md]);
+    pf_pipe_schedule();
 }
 
-// S^T of the tile, mask (tiles that cross a range end only) and online softmax into pop
-PF_INLINE void pf_qk_softmax(PfState &st, bf16x8 (&pop)[4], const uint8_t *stage, int k0,
-                             bool full, float scale_log2, int lane) {
-    f32x16 s[2];
-    pf_qk(s, st, stage, lane);
-    if (!full) pf_mask(s, st, k0, lane);
-    pf_softmax(pop, s, st, scale_log2);
-}
-
-// Two wavefronts per SIMD (8 per workgroup, ~200 registers each): while one runs its softmax on
-// the VALU, the other's MFMAs can run.
+// Two wavefronts per SIMD (8 per workgroup, ~240 registers each).
 __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a) {
-    // four K/V stages as distinct arrays, each named statically below, so the compiler can tell
-    // the asynchronous copy into one stage from the reads of another (a dynamically selected
-    // stage makes it wait for every copy before every LDS read)
-    __shared__ __attribute__((aligned(1024))) uint8_t stage0[kPfStage];
-    __shared__ __attribute__((aligned(1024))) uint8_t stage1[kPfStage];
-    __shared__ __attribute__((aligned(1024))) uint8_t stage2[kPfStage];
-    __shared__ __attribute__((aligned(1024))) uint8_t stage3[kPfStage];
+    // the K and V^T rings: four stages each, as distinct arrays named statically below, so the
+    // compiler can tell the asynchronous copy into one stage from the reads of another (a
+    // dynamically selected stage makes it wait for every copy before every LDS read); K stages
+    // first, so a K read address plus any stage offset fits the 16-bit LDS offset field
+    __shared__ __attribute__((aligned(1024))) uint8_t ks0[kPfHalf];
+    __shared__ __attribute__((aligned(1024))) uint8_t ks1[kPfHalf];
+    __shared__ __attribute__((aligned(1024))) uint8_t ks2[kPfHalf];
+    __shared__ __attribute__((aligned(1024))) uint8_t ks3[kPfHalf];
+    __shared__ __attribute__((aligned(1024))) uint8_t vs0[kPfHalf];
+    __shared__ __attribute__((aligned(1024))) uint8_t vs1[kPfHalf];
+    __shared__ __attribute__((aligned(1024))) uint8_t vs2[kPfHalf];
+    __shared__ __attribute__((aligned(1024))) uint8_t vs3[kPfHalf];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int qr = lane & 31, h = lane >> 5;
@@ -294,12 +324,18 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
             u32x4 w = ok ? ldg128(row + 16 * ks + 8 * h) : u32x4{0u, 0u, 0u, 0u};
+            // q * scale * log2(e), rounded to bf16
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                w[e] = pack_bf16x2(__uint_as_float(w[e] << 16) * a.scale_log2,
+                                   __uint_as_float(w[e] & 0xffff0000u) * a.scale_log2);
             st.qop[ks] = __builtin_bit_cast(bf16x8, w);
         }
         if (qi < a.q_len) pf_key_range(qi, a.q_len, a.kv_len, a.wl, a.wr, st.qlo, st.qhi);
         else st.qlo = st.qhi = 0;
         st.m_run = -__builtin_inff();
         st.l_run = 0.0f;
+        st.negm = f32x16{};
 #pragma unroll
         for (int md = 0; md < 4; ++md) st.acc[md] = f32x16{};
     }
@@ -308,40 +344,53 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     const uint16_t *vtplane = a.vt + ((int64_t)b * a.kv_heads + hk) * kPfD * a.vt_len;
     PF_WAIT_VMCNT(0);  // the Q loads above must not be counted by the copy waits below
 
-    // Tile t lives in stage t % 4; its copy is issued in step t - 3, after that step's barrier
-    // (which ends step t - 4, the last reader of the stage) and after its S / softmax, so the
-    // copy's issue overlaps the other wavefronts' work.
-#define PF_STG(k) ((k) == 0 ? stage0 : (k) == 1 ? stage1 : (k) == 2 ? stage2 : stage3)
+    // Tile t lives in stage t % 4 of both rings; its copies are issued right after barrier t - 2.
+#define PF_KS(k) ((k) == 0 ? ks0 : (k) == 1 ? ks1 : (k) == 2 ? ks2 : ks3)
+#define PF_VS(k) ((k) == 0 ? vs0 : (k) == 1 ? vs1 : (k) == 2 ? vs2 : vs3)
     uint32_t koff[2], voff[2];
     pf_copy_offsets(koff, voff, a.k_st, a.vt_len, wave, lane);
-#define PF_ISSUE(k, t)                                                                      \
-    pf_issue_tile(PF_STG(k), kplane, vtplane, a.k_st, a.vt_len, koff, voff, kt_begin + (t), \
-                  a.kv_len, wave, lane)
+#define PF_ISSUE(k, t)                                                                       \
+    pf_issue_tile(PF_KS(k), PF_VS(k), kplane, vtplane, a.k_st, a.vt_len, koff, voff,         \
+                  kt_begin + (t), a.kv_len, wave)
+    // Barrier j: this wave's copies of tile j are done (those of tile j + 1 may be in flight);
+    // once every wave has passed it, tile j - 2 has no reader left and tile j + 2 is copied
+    // into its stage.
+#define PF_BARRIER(j, kst)                                                                   \
+    {                                                                                        \
+        if ((j) + 1 < ntiles) PF_WAIT_VMCNT(kPfCopiesPerTile);                               \
+        else PF_WAIT_VMCNT(0);                                                               \
+        __builtin_amdgcn_s_barrier();                                                        \
+        if ((j) + 2 < ntiles) PF_ISSUE(kst, (j) + 2);                                        \
+    }
     if (ntiles > 0) PF_ISSUE(0, 0);
     if (ntiles > 1) PF_ISSUE(1, 1);
-    if (ntiles > 2) PF_ISSUE(2, 2);
     bf16x8 pop[4];
-#define PF_STEP(k)                                                                          \
-    {                                                                                       \
-        if (t >= ntiles) break;                                                             \
-        /* this wave's copies of tile t done (those of t + 1, t + 2 may be in flight) */    \
-        const int ahead = min(ntiles - 1, t + 2) - t;                                       \
-        if (ahead == 2) PF_WAIT_VMCNT(2 * kPfCopiesPerTile);                                \
-        else if (ahead == 1) PF_WAIT_VMCNT(kPfCopiesPerTile);                               \
-        else PF_WAIT_VMCNT(0);                                                              \
-        __builtin_amdgcn_s_barrier();                                                       \
-        if (wave_live) {                                                                    \
-            const int k0 = (kt_begin + t) * kPfBK;                                          \
-            const bool full = k0 >= lo_last && k0 + kPfBK <= hi_first;                      \
-            pf_qk_softmax(st, pop, PF_STG(k), k0, full, a.scale_log2, lane);                \
-            if (t + 3 < ntiles) PF_ISSUE(((k) + 3) & 3, t + 3);                             \
-            pf_pv(st, pop, PF_STG(k) + kPfHalf, lane);                                      \
-        } else if (t + 3 < ntiles) {                                                        \
-            PF_ISSUE(((k) + 3) & 3, t + 3);                                                 \
-        }                                                                                   \
-        ++t;                                                                                \
+    f32x16 s[2];
+    // Ping-pong between the two wavefronts of a SIMD (w and w + 4). Both run the same sequence
+    // softmax(t - 1), P V(t - 1), S(t), but wavefronts 0-3 take barrier t between softmax(t - 1)
+    // and P V(t - 1), wavefronts 4-7 after S(t - 1). Between two barriers one wavefront of each
+    // SIMD runs P V, S (MFMA) and then softmax (VALU), the other softmax and then P V, S.
+    const bool lead = qhalf == 0;
+    if (!lead) PF_BARRIER(0, 2)
+#define PF_STEP(k)                                                                           \
+    {                                                                                        \
+        if (t > ntiles) break;                                                               \
+        if (wave_live && t > 0) pf_softmax(pop, s, st);                                      \
+        if (lead) PF_BARRIER(t, ((k) + 2) & 3)                                               \
+        if (wave_live) {                                                                     \
+            __builtin_amdgcn_s_setprio(1); /* the MFMA block goes first at issue */          \
+            if (t > 0) pf_pv(st, pop, PF_VS(((k) + 3) & 3), lane);                           \
+            if (t < ntiles) {                                                                \
+                const int k0 = (kt_begin + t) * kPfBK;                                       \
+                pf_qk(s, st, PF_KS(k), lane);                                                \
+                if (!(k0 >= lo_last && k0 + kPfBK <= hi_first)) pf_mask(s, st, k0, lane);    \
+            }                                                                                \
+            __builtin_amdgcn_s_setprio(0);                                                   \
+        }                                                                                    \
+        if (!lead && t < ntiles) PF_BARRIER(t + 1, ((k) + 3) & 3)                            \
+        ++t;                                                                                 \
     }
-    for (int t = 0; t < ntiles;) {
+    for (int t = 0; t <= ntiles;) {
         PF_STEP(0)
         PF_STEP(1)
         PF_STEP(2)
@@ -349,11 +398,13 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     }
 #undef PF_STEP
 #undef PF_ISSUE
-#undef PF_STG
+#undef PF_KS
+#undef PF_VS
+#undef PF_BARRIER
     if (!wave_live) return;
 
     // ---- normalise and write O (bf16): lane (qr, h), d = 32 md + 8 (j / 4) + 4 h + j % 4 ----
-    const float l = st.l_run + __shfl_xor(st.l_run, 32, 64);
+    const float l = pf_sum_halves(st.l_run);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     const int qi = q0 + 32 * qhalf + qr;
     if (qi >= a.q_len) return;
@@ -521,6 +572,12 @@ extern "C" int cqkv_flash_attn(const void *q, const int64_t q_strides[3], const 
                     batch, q_len, kv_len, q_heads, kv_heads);
     if ((k_cache == nullptr) != (v_cache == nullptr))
         return fail(CQKV_ERR_ARG, "cqkv_flash_attn: give both cache sides or neither");
+    // 32-bit byte offsets inside a key tile (64 token rows) and inside a V^T plane
+    if (k_strides && (k_strides[1] <= 0 || k_strides[1] >= (1 << 25)))
+        return fail(CQKV_ERR_ARG, "cqkv_flash_attn: key token stride %lld outside [1, 2^25)",
+                    (long long)k_strides[1]);
+    if (kv_len > (1 << 23))
+        return fail(CQKV_ERR_ARG, "cqkv_flash_attn: kv_len %d above 2^23", kv_len);
     hipStream_t st = (hipStream_t)stream;
     if (k_cache) {
         if (int rc = check_side(k_cache, "cqkv_flash_attn (key cache)")) return rc;
