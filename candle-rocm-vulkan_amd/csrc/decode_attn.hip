@@ -14,8 +14,8 @@
 //    (O^T = V^T P^T).
 //  * A wavefront streams 32-key tiles with nontemporal buffer loads straight into operand
 //    registers (two register sets, A/B, no copies) and decodes codes in registers: E4M3 -> bf16 exactly, E2M1
-//    with its E8M0 block scale exactly, TurboQuant nibbles through an LDS table of f16 pairs
-//    (TurboQuant runs its MFMAs in f16: codebook values are not bf16-exact).
+//    with its E8M0 block scale exactly, TurboQuant code bytes through a per-lane LDS table of
+//    f16 pairs (TurboQuant runs its MFMAs in f16: codebook values are not bf16-exact).
 //    Loads of tiles past the split's end are aimed past the buffer range, so the hardware
 //    returns zeros without touching memory and the load schedule stays branch-free.
 //  * Key rows are row-major, so lane (r, g) loads the codes of key r for head-dim group g.
@@ -182,9 +182,22 @@ __device__ inline uint32_t fp4x2_to_bf16x2(uint32_t w, int byte_sel, float scale
 template <int FMT>
 using op_t = typename std::conditional<FMT == CQKV_FMT_TURBO4, f16x8, bf16x8>::type;
 
+// TurboQuant codebook lookups: code byte b (codes b & 15, b >> 4) of lane l reads the f16 pair of
+// entry (b, l) at byte 256 b + 4 l of a 64 KB LDS table, a copy per lane, so every lane reads
+// its own bank (random codes through one shared 1 KB table cost several passes per read in bank
+// conflicts). The table is 64 KB-aligned and tab = its address + 4 l, so the address of byte I
+// of code word w is tab with w's byte I as byte 1: one byte permute.
+typedef __attribute__((address_space(3))) const uint32_t lds_u32;
+template <int I>
+__device__ inline uint32_t turbo_pair(uint32_t tab, uint32_t w) {
+    // v_perm_b32 selector bytes: 0-3 pick bytes of the second operand (tab), 4-7 of the first (w)
+    constexpr uint32_t sel = 0x03020000u | ((4u + I) << 8);
+    return *(lds_u32 *)(size_t)__builtin_amdgcn_perm(w, tab, sel);
+}
+
 // 8 codes of one code word (4-bit) or two words (FP8) -> 8 operand values.
 template <int FMT>
-__device__ inline op_t<FMT> decode8(uint32_t w0, uint32_t w1, float scale, const uint32_t *tab) {
+__device__ inline op_t<FMT> decode8(uint32_t w0, uint32_t w1, float scale, uint32_t tab) {
     u32x4 r;
     if constexpr (FMT == CQKV_FMT_FP8) {
         return fp8x8_to_bf16x8(w0, w1);
@@ -194,10 +207,10 @@ __device__ inline op_t<FMT> decode8(uint32_t w0, uint32_t w1, float scale, const
         r.z = fp4x2_to_bf16x2(w0, 2, scale);
         r.w = fp4x2_to_bf16x2(w0, 3, scale);
     } else {
-        r.x = tab[w0 & 0xffu];
-        r.y = tab[(w0 >> 8) & 0xffu];
-        r.z = tab[(w0 >> 16) & 0xffu];
-        r.w = tab[w0 >> 24];
+        r.x = turbo_pair<0>(tab, w0);
+        r.y = turbo_pair<1>(tab, w0);
+        r.z = turbo_pair<2>(tab, w0);
+        r.w = turbo_pair<3>(tab, w0);
     }
     return __builtin_bit_cast(op_t<FMT>, r);
 }
@@ -210,7 +223,7 @@ template <int FMT, int D>
 __device__ inline void compute_tile(Tile<FMT, D> &cur, int tile, const DecodeArgs &a,
                                     const op_t<FMT> *qhi, const op_t<FMT> *qlo, bool q_split, int lane,
                                     int lo, int hi, int lo_max, int hi_min, int L,
-                                    const uint32_t *tab, float &m_run, float &l_run,
+                                    uint32_t tab, float &m_run, float &l_run,
                                     f32x4 *acc) {
     constexpr int NCH = D / 32;
     const int g = lane >> 4;
@@ -362,10 +375,15 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     constexpr int NCH = D / 32;
     constexpr int NT = WAVES * 64;
     constexpr bool kTurbo = FMT == CQKV_FMT_TURBO4;
-    __shared__ float sm_o[WAVES][16][D];
+    // the per-wavefront outputs (and, before the tile loop, the queries) share their LDS with the
+    // TurboQuant code table (64 KB-aligned, see turbo_pair), which is live only during the tile
+    // loop
+    constexpr int kOWords = WAVES * 16 * D, kTabWords = kTurbo ? 256 * 64 : 0;
+    __shared__ __attribute__((aligned(65536))) float sm_buf[kOWords > kTabWords ? kOWords : kTabWords];
+    float(*sm_o)[16][D] = (float(*)[16][D])sm_buf;
+    uint32_t *sm_tab = (uint32_t *)sm_buf;
     __shared__ float sm_fin[16][D];
     __shared__ float sm_m[WAVES][16], sm_l[WAVES][16];
-    __shared__ uint32_t sm_tab[kTurbo ? 256 : 1];
 
     // 1-D grid, plane fastest: workgroup ids are dealt round-robin to the 8 XCDs, so with
     // kv_heads a multiple of 8 each XCD takes whole planes of one kv head from every sequence -
@@ -402,10 +420,6 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
         }
         sm_q[c][d] = v;
     }
-    if constexpr (kTurbo) {
-        for (int i = threadIdx.x; i < 256; i += NT)  // byte i = code pair (i & 15, i >> 4)
-            sm_tab[i] = pack_f16x2(a.cent[i & 15], a.cent[i >> 4]);
-    }
     __syncthreads();
     if constexpr (kTurbo) {
         for (int c = wave; c < a.ncols; c += WAVES) {
@@ -431,6 +445,11 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     }
     const bool q_split = a.q_split != 0;
     __syncthreads();
+    if constexpr (kTurbo) {  // entry (b, l) at word 64 b + l: code pair (b & 15, b >> 4)
+        for (int i = threadIdx.x; i < 256 * 64; i += NT)
+            sm_tab[i] = pack_f16x2(a.cent[(i >> 6) & 15], a.cent[i >> 10]);
+        __syncthreads();
+    }
 
     // ---- stream the tiles of this split ----
     const int64_t plane = (int64_t)b * a.kv_heads + hk;
@@ -442,6 +461,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     f32x4 acc[2 * NCH];
 #pragma unroll
     for (int t = 0; t < 2 * NCH; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint32_t tab = (uint32_t)(size_t)sm_tab + 4 * lane;
     float m_run = -__builtin_inff(), l_run = 0.0f;
 
     // Register sets A and B alternate; the scheduling barriers keep every load of one set
@@ -453,20 +473,21 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     load_tile<FMT, D>(tb2, t + WAVES, t + WAVES < te, lane, kr, ksr, vr, vsr);
     __builtin_amdgcn_sched_barrier(0);
     for (; t < te; t += 2 * WAVES) {
-        compute_tile<FMT, D>(ta, t, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min, L, sm_tab,
+        compute_tile<FMT, D>(ta, t, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min, L, tab,
                              m_run, l_run, acc);
         __builtin_amdgcn_sched_barrier(0);
         load_tile<FMT, D>(ta, t + 2 * WAVES, t + 2 * WAVES < te, lane, kr, ksr, vr, vsr);
         __builtin_amdgcn_sched_barrier(0);
         if (t + WAVES < te)
             compute_tile<FMT, D>(tb2, t + WAVES, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min,
-                                 L, sm_tab, m_run, l_run, acc);
+                                 L, tab, m_run, l_run, acc);
         __builtin_amdgcn_sched_barrier(0);
         load_tile<FMT, D>(tb2, t + 3 * WAVES, t + 3 * WAVES < te, lane, kr, ksr, vr, vsr);
         __builtin_amdgcn_sched_barrier(0);
     }
 
     // ---- merge the wavefronts ----
+    if constexpr (kTurbo) __syncthreads();  // every wavefront is done with the code table
     const float l_col = group16_sum(l_run);
 #pragma unroll
     for (int u = 0; u < NCH; ++u)
