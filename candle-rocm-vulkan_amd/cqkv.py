@@ -42,6 +42,12 @@ class Side(ctypes.Structure):
                 ("scales", ctypes.c_void_p)]
 
 
+class KvBlock(ctypes.Structure):
+    """cqkv_kv_block: a key side, a value side and the valid rows at the start of their planes."""
+    _fields_ = [("k", ctypes.POINTER(Side)), ("v", ctypes.POINTER(Side)),
+                ("rows", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+
 _lib = None
 
 
@@ -66,6 +72,11 @@ def lib() -> ctypes.CDLL:
         L.cqkv_decode_splits.restype = i32
         L.cqkv_decode_attention.argtypes = [P, i32, I64P, SP, SP, i32, i32, i32, P, i32, f32,
                                             i32, i32, P, i32, I64P, i32, P, sz, P]
+        BP = ctypes.POINTER(KvBlock)
+        L.cqkv_decode_paged_workspace_bytes.argtypes = [BP, i32, i32, i32, i32]
+        L.cqkv_decode_paged_workspace_bytes.restype = sz
+        L.cqkv_decode_attention_paged.argtypes = [P, i32, I64P, BP, i32, i32, i32, i32, f32, i32,
+                                                  i32, P, i32, I64P, P, sz, P]
         L.cqkv_flash_attn.argtypes = [P, I64P, P, I64P, P, I64P, P, I64P, i32, i32, i32, i32,
                                       i32, i32, f32, i32, i32, SP, SP, i32, P]
         L.cqkv_reference_row_words.argtypes = [i32, i32]
@@ -82,6 +93,7 @@ def lib() -> ctypes.CDLL:
 
 EXPORTED = ["cqkv_codes_plane_bytes", "cqkv_scales_plane_bytes", "cqkv_quant_append",
             "cqkv_decode_workspace_bytes", "cqkv_decode_splits", "cqkv_decode_attention",
+            "cqkv_decode_paged_workspace_bytes", "cqkv_decode_attention_paged",
             "cqkv_flash_attn", "cqkv_reference_row_words", "cqkv_rows_import",
             "cqkv_rows_export", "cqkv_turbo_codebook", "cqkv_turbo_signs", "cqkv_last_error",
             "cqkv_version"]
@@ -194,6 +206,51 @@ def decode_attention(q: torch.Tensor, k: CacheSide, v: CacheSide, kv_len: int,
         _ptr(q), _DTYPES[q.dtype], _strides3(q, (0, 1, 2)), ctypes.byref(ks), ctypes.byref(vs), b,
         hq, lq, _ptr(kv_lens), kv_len, softmax_scale, window_left, window_right, _ptr(out),
         _DTYPES[out.dtype], _strides3(out, (0, 1, 2)), splits, _ptr(workspace),
+        0 if workspace is None else workspace.numel() * workspace.element_size(),
+        _stream(q.device)))
+    return out
+
+
+def _blocks_struct(blocks):
+    """[(k_side, v_side, rows), ...] -> (ctypes array of KvBlock, the Side structs it points to)."""
+    sides = [(k.struct(), v.struct()) for k, v, _ in blocks]
+    arr = (KvBlock * len(blocks))()
+    for i, ((ks, vs), (_, _, rows)) in enumerate(zip(sides, blocks)):
+        arr[i].k = ctypes.pointer(ks)
+        arr[i].v = ctypes.pointer(vs)
+        arr[i].rows = rows
+    return arr, sides
+
+
+def decode_paged_workspace_bytes(blocks, batch: int, q_heads: int, q_len: int) -> int:
+    arr, _sides = _blocks_struct(blocks)
+    return lib().cqkv_decode_paged_workspace_bytes(arr, len(blocks), batch, q_heads, q_len)
+
+
+def decode_attention_paged(q: torch.Tensor, blocks, softmax_scale: float, window_left: int = -1,
+                           window_right: int = -1, out: torch.Tensor | None = None,
+                           workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode over paged cache blocks [(k_side, v_side, rows), ...]: the keys are the blocks'
+    first `rows` tokens concatenated (attention_packed_blocks, candle-nn/src/turbo_quant.rs:
+    1082-1114). q (batch, q_heads, q_len, D) -> out of the same shape."""
+    _need_gpu(q, "q")
+    b, hq, lq, d = q.shape
+    if q.stride(3) != 1:
+        raise CqkvError(ERR_ARG, "q must have a contiguous head dim")
+    if not blocks:
+        raise CqkvError(ERR_ARG, "no blocks")
+    for k, v, _ in blocks:
+        if b != k.batch or b != v.batch or d != k.head_dim:
+            raise CqkvError(ERR_ARG, f"q {tuple(q.shape)} does not match a block's sides")
+    if out is None:
+        out = torch.empty_like(q)
+    elif tuple(out.shape) != tuple(q.shape) or out.stride(3) != 1:
+        raise CqkvError(ERR_ARG, f"out {tuple(out.shape)} does not match q")
+    arr, _sides = _blocks_struct(blocks)
+    _check(lib().cqkv_decode_attention_paged(
+        _ptr(q), _DTYPES[q.dtype], _strides3(q, (0, 1, 2)), arr, len(blocks), b, hq, lq,
+        softmax_scale, window_left, window_right, _ptr(out), _DTYPES[out.dtype],
+        _strides3(out, (0, 1, 2)), _ptr(workspace),
         0 if workspace is None else workspace.numel() * workspace.element_size(),
         _stream(q.device)))
     return out

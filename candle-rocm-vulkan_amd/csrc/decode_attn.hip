@@ -29,6 +29,8 @@
 //    merges the splits (tq_combine's formula), unrotating TurboQuant values. (A fused "last
 //    workgroup combines" variant needs agent-scope release fences, which write back the L2 of
 //    the XCD each time; measured at 6x the whole decode time, so the kernel boundary is used.)
+#include <vector>
+
 #include "cqkv_device.h"
 #include "cqkv_host.h"
 
@@ -37,6 +39,18 @@
 namespace cqkv {
 
 constexpr uint32_t kOOB = 0x80000000u;  // past every plane (planes are < 2 GiB)
+
+// Paged decode: a run of whole 32-key tiles of one cache block, decoded by one split. The keys
+// of the call are the blocks' valid rows concatenated (the reference's block table, PageTable
+// in candle-core/src/accel/attention.rs:307-366, walked by attention_packed_blocks,
+// candle-nn/src/turbo_quant.rs:1082-1114).
+struct PagedSeg {
+    const uint8_t *kc, *ks, *vc, *vs;                  // the block's planes
+    uint32_t kc_plane, ks_plane, vc_plane, vs_plane;   // bytes per (sequence, kv head) plane
+    int32_t tile_begin, tile_end;                      // tiles [begin, end) of the block
+    int32_t key_offset;                                // key index of the block's row 0
+    int32_t rows;                                      // valid rows of the block
+};
 
 struct DecodeArgs {
     const void *q;
@@ -57,6 +71,7 @@ struct DecodeArgs {
     uint32_t ksign_bits[4], vsign_bits[4];  // TURBO4 rotation signs (bit set -> -1)
     float rot_scale;
     float cent[16];  // TURBO4 codebook (the same for keys and values at one head dim)
+    const PagedSeg *segs;  // paged: one segment per split (the planes above are unused)
 };
 
 // Visible keys [lo, hi) of query i of lq over lk keys (bottom-right aligned).
@@ -222,13 +237,15 @@ __device__ inline float e8m0_scale(uint32_t code) {  // code 0 marks an all-zero
 template <int FMT, int D>
 __device__ inline void compute_tile(Tile<FMT, D> &cur, int tile, const DecodeArgs &a,
                                     const op_t<FMT> *qhi, const op_t<FMT> *qlo, bool q_split, int lane,
-                                    int lo, int hi, int lo_max, int hi_min, int L,
+                                    int lo, int hi, int lo_max, int hi_min, int L, int koff,
                                     uint32_t tab, float &m_run, float &l_run,
                                     f32x4 *acc) {
     constexpr int NCH = D / 32;
     const int g = lane >> 4;
+    // tile and L are rows of the current block (the whole cache when not paged); keys of the
+    // call, for the masks, are koff further
     const int t0 = tile * 32;
-    const bool full = t0 >= lo_max && t0 + 32 <= hi_min;
+    const bool full = koff + t0 >= lo_max && koff + t0 + 32 <= hi_min && t0 + 32 <= L;
 
     // S^T = K Q^T for the two 16-key sub-tiles
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
@@ -267,8 +284,8 @@ __device__ inline void compute_tile(Tile<FMT, D> &cur, int tile, const DecodeArg
     if (!full) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int key = kbase + e;
-            if (!(key >= lo && key < hi)) x[e] = -__builtin_inff();
+            const int key = koff + kbase + e;  // rows past the block's valid rows are masked too
+            if (!(key >= lo && key < hi && kbase + e < L)) x[e] = -__builtin_inff();
         }
     }
     float mx = x[0];
@@ -405,8 +422,29 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     if (!col_ok) lo = hi = 0;
     key_range(0, a.q_len, L, a.wl, a.wr, lo_min, hi_min);
     key_range(a.q_len - 1, a.q_len, L, a.wl, a.wr, lo_max, hi_max);
-    const int tb = max(split * a.tiles_per_split, lo_min / 32);
-    const int te = min((split + 1) * a.tiles_per_split, (hi_max + 31) / 32);
+    // the split's tiles and the planes they live in: a segment of one block (paged) or a range of
+    // the cache's tiles
+    const uint8_t *kc = a.kc, *ks = a.ks, *vc = a.vc, *vs = a.vs;
+    uint32_t kc_plane = a.kc_plane, ks_plane = a.ks_plane, vc_plane = a.vc_plane, vs_plane = a.vs_plane;
+    int koff = 0, Lb = L, tb, te;
+    if (a.segs) {
+        const PagedSeg sg = a.segs[split];
+        kc = sg.kc;
+        ks = sg.ks;
+        vc = sg.vc;
+        vs = sg.vs;
+        kc_plane = sg.kc_plane;
+        ks_plane = sg.ks_plane;
+        vc_plane = sg.vc_plane;
+        vs_plane = sg.vs_plane;
+        koff = sg.key_offset;
+        Lb = sg.rows;
+        tb = max(sg.tile_begin, max(lo_min - koff, 0) / 32);
+        te = min(sg.tile_end, (max(hi_max - koff, 0) + 31) / 32);
+    } else {
+        tb = max(split * a.tiles_per_split, lo_min / 32);
+        te = min((split + 1) * a.tiles_per_split, (hi_max + 31) / 32);
+    }
 
     // ---- queries (TURBO4: rotated, q Pi_k^T = sign-flip, Hadamard, 1/sqrt(D)) ----
     float(*sm_q)[D] = sm_o[0];
@@ -453,10 +491,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
 
     // ---- stream the tiles of this split ----
     const int64_t plane = (int64_t)b * a.kv_heads + hk;
-    const rsrc_t kr = make_rsrc(a.kc + plane * a.kc_plane, a.kc_plane);
-    const rsrc_t ksr = make_rsrc(a.ks + plane * a.ks_plane, a.ks_plane);
-    const rsrc_t vr = make_rsrc(a.vc + plane * a.vc_plane, a.vc_plane);
-    const rsrc_t vsr = make_rsrc(a.vs + plane * a.vs_plane, a.vs_plane);
+    const rsrc_t kr = make_rsrc(kc + plane * kc_plane, kc_plane);
+    const rsrc_t ksr = make_rsrc(ks + plane * ks_plane, ks_plane);
+    const rsrc_t vr = make_rsrc(vc + plane * vc_plane, vc_plane);
+    const rsrc_t vsr = make_rsrc(vs + plane * vs_plane, vs_plane);
 
     f32x4 acc[2 * NCH];
 #pragma unroll
@@ -473,14 +511,14 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     load_tile<FMT, D>(tb2, t + WAVES, t + WAVES < te, lane, kr, ksr, vr, vsr);
     __builtin_amdgcn_sched_barrier(0);
     for (; t < te; t += 2 * WAVES) {
-        compute_tile<FMT, D>(ta, t, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min, L, tab,
+        compute_tile<FMT, D>(ta, t, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min, Lb, koff, tab,
                              m_run, l_run, acc);
         __builtin_amdgcn_sched_barrier(0);
         load_tile<FMT, D>(ta, t + 2 * WAVES, t + 2 * WAVES < te, lane, kr, ksr, vr, vsr);
         __builtin_amdgcn_sched_barrier(0);
         if (t + WAVES < te)
             compute_tile<FMT, D>(tb2, t + WAVES, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min,
-                                 L, tab, m_run, l_run, acc);
+                                 Lb, koff, tab, m_run, l_run, acc);
         __builtin_amdgcn_sched_barrier(0);
         load_tile<FMT, D>(tb2, t + 3 * WAVES, t + 3 * WAVES < te, lane, kr, ksr, vr, vsr);
         __builtin_amdgcn_sched_barrier(0);
@@ -672,6 +710,96 @@ extern "C" size_t cqkv_decode_workspace_bytes(int32_t batch, int32_t q_heads, in
     return workspace_layout(batch, q_heads, q_len, head_dim, splits, &lse_off);
 }
 
+// Checks and fills what the dense and the paged calls share: queries, output, heads, scale,
+// window, TurboQuant rotation and codebook. k / v give the format, head dim and kv heads.
+static int decode_prepare(DecodeArgs &a, const char *who, const void *q, int32_t q_dtype,
+                          const int64_t q_strides[3], const cqkv_side *k, const cqkv_side *v,
+                          int32_t batch, int32_t q_heads, int32_t q_len, float softmax_scale,
+                          int32_t window_left, int32_t window_right, void *out, int32_t out_dtype,
+                          const int64_t out_strides[3]) {
+    if (int rc = check_side(k, who)) return rc;
+    if (int rc = check_side(v, who)) return rc;
+    if (k->is_value != 0 || v->is_value != 1)
+        return fail(CQKV_ERR_ARG, "%s: expected a key side and a value side", who);
+    if (k->format != v->format || k->head_dim != v->head_dim || k->kv_heads != v->kv_heads)
+        return fail(CQKV_ERR_ARG, "%s: key / value sides differ in format, D or heads", who);
+    if (!q || !out || !q_strides || !out_strides)
+        return fail(CQKV_ERR_ARG, "%s: null q / out / strides", who);
+    if (q_dtype < CQKV_BF16 || q_dtype > CQKV_F32 || out_dtype < CQKV_BF16 || out_dtype > CQKV_F32)
+        return fail(CQKV_ERR_ARG, "%s: dtypes q %d out %d", who, q_dtype, out_dtype);
+    const int hkv = k->kv_heads, d = k->head_dim;
+    if (batch <= 0 || q_heads <= 0 || q_len <= 0 || q_heads % hkv != 0)
+        return fail(CQKV_ERR_ARG, "%s: batch %d q_heads %d q_len %d kv_heads %d", who, batch,
+                    q_heads, q_len, hkv);
+    const int group = q_heads / hkv;
+    if (group * q_len > 16)
+        return fail(CQKV_ERR_ARG, "%s: q_len * q_heads / kv_heads = %d > 16", who, group * q_len);
+    a = DecodeArgs{};
+    a.q = q;
+    a.q_sb = q_strides[0];
+    a.q_sh = q_strides[1];
+    a.q_si = q_strides[2];
+    a.q_dtype = q_dtype;
+    a.q_heads = q_heads;
+    a.kv_heads = hkv;
+    a.group = group;
+    a.q_len = q_len;
+    a.ncols = group * q_len;
+    a.scale_log2 = softmax_scale * kLog2e;
+    a.wl = window_left;
+    a.wr = window_right;
+    a.batch = batch;
+    a.out = out;
+    a.out_dtype = out_dtype;
+    a.q_split = (q_dtype != CQKV_BF16 || k->format == CQKV_FMT_TURBO4) ? 1 : 0;
+    a.o_sb = out_strides[0];
+    a.o_sh = out_strides[1];
+    a.o_si = out_strides[2];
+    if (k->format == CQKV_FMT_TURBO4) {
+        float bnd[16], cent[16];
+        if (int rc = fill_turbo_args(k, a.ksign_bits, &a.rot_scale, bnd)) return rc;
+        if (int rc = fill_turbo_args(v, a.vsign_bits, &a.rot_scale, bnd)) return rc;
+        if (turbo_codebook(d, 4, cent, bnd) != 0)
+            return fail(CQKV_ERR_ARG, "%s: turbo codebook D=%d", who, d);
+        for (int i = 0; i < 16; ++i) a.cent[i] = cent[i];
+    }
+    return CQKV_OK;
+}
+
+// Launches the decode kernel over a.splits splits and, for more than one, the combine
+// (partials at a.part_o / a.part_lse).
+static hipError_t decode_launch(const DecodeArgs &a, int format, int d, hipStream_t st) {
+    const dim3 grid(a.splits * a.kv_heads * a.batch);
+    switch (format) {
+    case CQKV_FMT_FP8: launch_decode<CQKV_FMT_FP8>(d, grid, st, a); break;
+    case CQKV_FMT_MXFP4: launch_decode<CQKV_FMT_MXFP4>(d, grid, st, a); break;
+    default: launch_decode<CQKV_FMT_TURBO4>(d, grid, st, a); break;
+    }
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && a.splits > 1) {
+        CombineArgs c = {};
+        c.part_o = a.part_o;
+        c.part_lse = a.part_lse;
+        c.splits = a.splits;
+        c.rows = a.batch * a.q_heads * a.q_len;
+        c.q_heads = a.q_heads;
+        c.q_len = a.q_len;
+        c.out_dtype = a.out_dtype;
+        c.rotate = format == CQKV_FMT_TURBO4 ? 1 : 0;
+        c.out = a.out;
+        c.o_sb = a.o_sb;
+        c.o_sh = a.o_sh;
+        c.o_si = a.o_si;
+        for (int i = 0; i < 4; ++i) c.vsign_bits[i] = a.vsign_bits[i];
+        c.rot_scale = a.rot_scale;
+        const dim3 cg((c.rows + 3) / 4);
+        if (d == 64) hipLaunchKernelGGL(combine_kernel<64>, cg, dim3(256), 0, st, c);
+        else hipLaunchKernelGGL(combine_kernel<128>, cg, dim3(256), 0, st, c);
+        e = hipGetLastError();
+    }
+    return e;
+}
+
 extern "C" int cqkv_decode_attention(const void *q, int32_t q_dtype, const int64_t q_strides[3],
                                      const cqkv_side *k, const cqkv_side *v, int32_t batch,
                                      int32_t q_heads, int32_t q_len, const int32_t *kv_lens,
@@ -681,29 +809,19 @@ extern "C" int cqkv_decode_attention(const void *q, int32_t q_dtype, const int64
                                      void *workspace, size_t workspace_bytes,
                                      cqkv_stream_t stream) {
     clear_error();
-    if (int rc = check_side(k, "cqkv_decode_attention (keys)")) return rc;
-    if (int rc = check_side(v, "cqkv_decode_attention (values)")) return rc;
-    if (k->is_value != 0 || v->is_value != 1)
-        return fail(CQKV_ERR_ARG, "cqkv_decode_attention: expected a key side and a value side");
-    if (k->format != v->format || k->head_dim != v->head_dim || k->kv_heads != v->kv_heads ||
-        k->capacity != v->capacity)
-        return fail(CQKV_ERR_ARG, "cqkv_decode_attention: key / value sides differ in format, D, heads or capacity");
-    if (!q || !out || !q_strides || !out_strides)
-        return fail(CQKV_ERR_ARG, "cqkv_decode_attention: null q / out / strides");
-    if (q_dtype < CQKV_BF16 || q_dtype > CQKV_F32 || out_dtype < CQKV_BF16 || out_dtype > CQKV_F32)
-        return fail(CQKV_ERR_ARG, "cqkv_decode_attention: dtypes q %d out %d", q_dtype, out_dtype);
-    const int hkv = k->kv_heads, d = k->head_dim;
-    if (batch <= 0 || q_heads <= 0 || q_len <= 0 || q_heads % hkv != 0)
-        return fail(CQKV_ERR_ARG, "cqkv_decode_attention: batch %d q_heads %d q_len %d kv_heads %d",
-                    batch, q_heads, q_len, hkv);
-    const int group = q_heads / hkv;
-    if (group * q_len > 16)
-        return fail(CQKV_ERR_ARG, "cqkv_decode_attention: q_len * q_heads / kv_heads = %d > 16",
-                    group * q_len);
+    DecodeArgs a;
+    if (int rc = decode_prepare(a, "cqkv_decode_attention", q, q_dtype, q_strides, k, v, batch,
+                                q_heads, q_len, softmax_scale, window_left, window_right, out,
+                                out_dtype, out_strides))
+        return rc;
+    if (k->capacity != v->capacity)
+        return fail(CQKV_ERR_ARG, "cqkv_decode_attention: key / value capacities %d / %d differ",
+                    k->capacity, v->capacity);
     if (kv_len < 0 || kv_len > k->capacity)
         return fail(CQKV_ERR_ARG, "cqkv_decode_attention: kv_len %d outside [0, capacity %d]",
                     kv_len, k->capacity);
     if (splits < 0) return fail(CQKV_ERR_ARG, "cqkv_decode_attention: splits %d", splits);
+    const int hkv = k->kv_heads, d = k->head_dim;
 
     const int tiles = max(1, tiles_of(kv_len));
     int s = splits > 0 ? min(splits, tiles)
@@ -712,12 +830,6 @@ extern "C" int cqkv_decode_attention(const void *q, int32_t q_dtype, const int64
     const int tps = (tiles + s - 1) / s;
     s = (tiles + tps - 1) / tps;
 
-    DecodeArgs a = {};
-    a.q = q;
-    a.q_sb = q_strides[0];
-    a.q_sh = q_strides[1];
-    a.q_si = q_strides[2];
-    a.q_dtype = q_dtype;
     a.kc = (const uint8_t *)k->codes;
     a.ks = (const uint8_t *)k->scales;
     a.vc = (const uint8_t *)v->codes;
@@ -728,32 +840,8 @@ extern "C" int cqkv_decode_attention(const void *q, int32_t q_dtype, const int64
     a.vs_plane = (uint32_t)cqkv_scales_plane_bytes(v->format, d, v->capacity);
     a.kv_lens = kv_lens;
     a.kv_len = kv_len;
-    a.q_heads = q_heads;
-    a.kv_heads = hkv;
-    a.group = group;
-    a.q_len = q_len;
-    a.ncols = group * q_len;
-    a.scale_log2 = softmax_scale * kLog2e;
-    a.wl = window_left;
-    a.wr = window_right;
     a.tiles_per_split = tps;
     a.splits = s;
-    a.batch = batch;
-    a.out = out;
-    a.out_dtype = out_dtype;
-    a.q_split = (q_dtype != CQKV_BF16 || k->format == CQKV_FMT_TURBO4) ? 1 : 0;
-    a.o_sb = out_strides[0];
-    a.o_sh = out_strides[1];
-    a.o_si = out_strides[2];
-    const bool rotate = k->format == CQKV_FMT_TURBO4;
-    if (rotate) {
-        float bnd[16], cent[16];
-        if (int rc = fill_turbo_args(k, a.ksign_bits, &a.rot_scale, bnd)) return rc;
-        if (int rc = fill_turbo_args(v, a.vsign_bits, &a.rot_scale, bnd)) return rc;
-        if (turbo_codebook(d, 4, cent, bnd) != 0)
-            return fail(CQKV_ERR_ARG, "cqkv_decode_attention: turbo codebook D=%d", d);
-        for (int i = 0; i < 16; ++i) a.cent[i] = cent[i];
-    }
 
     hipStream_t st = (hipStream_t)stream;
     void *ws = workspace;
@@ -771,40 +859,155 @@ extern "C" int cqkv_decode_attention(const void *q, int32_t q_dtype, const int64
         a.part_o = (float *)ws;
         a.part_lse = (float *)((char *)ws + lse_off);
     }
-
-    const dim3 grid(s * hkv * batch);
-    switch (k->format) {
-    case CQKV_FMT_FP8: launch_decode<CQKV_FMT_FP8>(d, grid, st, a); break;
-    case CQKV_FMT_MXFP4: launch_decode<CQKV_FMT_MXFP4>(d, grid, st, a); break;
-    default: launch_decode<CQKV_FMT_TURBO4>(d, grid, st, a); break;
-    }
-    hipError_t e = hipGetLastError();
-    if (e == hipSuccess && s > 1) {
-        CombineArgs c = {};
-        c.part_o = a.part_o;
-        c.part_lse = a.part_lse;
-        c.splits = s;
-        c.rows = batch * q_heads * q_len;
-        c.q_heads = q_heads;
-        c.q_len = q_len;
-        c.out_dtype = out_dtype;
-        c.rotate = rotate ? 1 : 0;
-        c.out = out;
-        c.o_sb = a.o_sb;
-        c.o_sh = a.o_sh;
-        c.o_si = a.o_si;
-        for (int i = 0; i < 4; ++i) c.vsign_bits[i] = a.vsign_bits[i];
-        c.rot_scale = a.rot_scale;
-        const dim3 cg((c.rows + 3) / 4);
-        if (d == 64) hipLaunchKernelGGL(combine_kernel<64>, cg, dim3(256), 0, st, c);
-        else hipLaunchKernelGGL(combine_kernel<128>, cg, dim3(256), 0, st, c);
-        e = hipGetLastError();
-    }
+    hipError_t e = decode_launch(a, k->format, d, st);
     if (owned) {
         hipError_t fe = hipFreeAsync(ws, st);
         if (e == hipSuccess) e = fe;
     }
     if (e != hipSuccess)
         return fail(CQKV_ERR_HIP, "cqkv_decode_attention: launch failed: %s", hipGetErrorString(e));
+    return CQKV_OK;
+}
+
+// ---- paged decode ----
+// Segments of a block list: each block's valid rows, cut into runs of at most tps whole tiles;
+// the run length is the dense split rule's for the total key count.
+static int paged_segments(const cqkv_kv_block *blocks, int32_t n_blocks, int32_t batch,
+                          std::vector<PagedSeg> *segs) {
+    const cqkv_side *k0 = blocks[0].k;
+    int64_t total = 0, tiles = 0;
+    for (int i = 0; i < n_blocks; ++i) {
+        total += blocks[i].rows;
+        tiles += tiles_of(blocks[i].rows);
+    }
+    const int s = auto_splits(batch, k0->kv_heads, (int)std::max<int64_t>(total, 1), false,
+                              waves_of(k0->format));
+    const int tps = (int)std::max<int64_t>(1, (tiles + s - 1) / s);
+    int key = 0, n = 0;
+    for (int i = 0; i < n_blocks; ++i) {
+        const cqkv_kv_block &bl = blocks[i];
+        const int bt = tiles_of(bl.rows);
+        for (int t = 0; t < bt; t += tps) {
+            if (segs) {
+                PagedSeg g = {};
+                const int d = bl.k->head_dim;
+                g.kc = (const uint8_t *)bl.k->codes;
+                g.ks = (const uint8_t *)bl.k->scales;
+                g.vc = (const uint8_t *)bl.v->codes;
+                g.vs = (const uint8_t *)bl.v->scales;
+                g.kc_plane = (uint32_t)cqkv_codes_plane_bytes(bl.k->format, d, bl.k->capacity);
+                g.ks_plane = (uint32_t)cqkv_scales_plane_bytes(bl.k->format, d, bl.k->capacity);
+                g.vc_plane = (uint32_t)cqkv_codes_plane_bytes(bl.v->format, d, bl.v->capacity);
+                g.vs_plane = (uint32_t)cqkv_scales_plane_bytes(bl.v->format, d, bl.v->capacity);
+                g.tile_begin = t;
+                g.tile_end = min(t + tps, bt);
+                g.key_offset = key;
+                g.rows = bl.rows;
+                segs->push_back(g);
+            }
+            ++n;
+        }
+        key += bl.rows;
+    }
+    return n;
+}
+
+// workspace: the segment table, then (more than one segment) the partials
+static size_t paged_workspace(int nseg, int32_t batch, int32_t q_heads, int32_t q_len,
+                              int32_t head_dim, size_t *part_off, size_t *lse_off) {
+    *part_off = align256((size_t)nseg * sizeof(PagedSeg));
+    size_t parts = 0;
+    *lse_off = 0;
+    if (nseg > 1) parts = workspace_layout(batch, q_heads, q_len, head_dim, nseg, lse_off);
+    return *part_off + parts;
+}
+
+static int check_blocks(const cqkv_kv_block *blocks, int32_t n_blocks, int32_t batch,
+                        const char *who) {
+    if (!blocks || n_blocks <= 0) return fail(CQKV_ERR_ARG, "%s: no blocks", who);
+    int64_t total = 0;
+    for (int i = 0; i < n_blocks; ++i) {
+        const cqkv_kv_block &bl = blocks[i];
+        if (!bl.k || !bl.v) return fail(CQKV_ERR_ARG, "%s: block %d has a null side", who, i);
+        if (int rc = check_side(bl.k, who)) return rc;
+        if (int rc = check_side(bl.v, who)) return rc;
+        if (bl.k->format != blocks[0].k->format || bl.k->head_dim != blocks[0].k->head_dim ||
+            bl.k->kv_heads != blocks[0].k->kv_heads || bl.v->format != blocks[0].k->format ||
+            bl.v->head_dim != blocks[0].k->head_dim || bl.v->kv_heads != blocks[0].k->kv_heads ||
+            bl.k->is_value != 0 || bl.v->is_value != 1 || bl.k->seed != blocks[0].k->seed ||
+            bl.v->seed != blocks[0].v->seed)
+            return fail(CQKV_ERR_ARG,
+                        "%s: block %d differs from block 0 in format, head dim, kv heads, side or seed",
+                        who, i);
+        if (bl.rows < 0 || bl.rows > bl.k->capacity || bl.rows > bl.v->capacity)
+            return fail(CQKV_ERR_ARG, "%s: block %d has %d rows but capacities %d / %d", who, i,
+                        bl.rows, bl.k->capacity, bl.v->capacity);
+        total += bl.rows;
+    }
+    if (total == 0) return fail(CQKV_ERR_ARG, "%s: the blocks hold no keys", who);
+    if (total > (1 << 30)) return fail(CQKV_ERR_ARG, "%s: %lld keys", who, (long long)total);
+    (void)batch;
+    return CQKV_OK;
+}
+
+extern "C" size_t cqkv_decode_paged_workspace_bytes(const cqkv_kv_block *blocks,
+                                                    int32_t n_blocks, int32_t batch,
+                                                    int32_t q_heads, int32_t q_len) {
+    clear_error();
+    if (check_blocks(blocks, n_blocks, batch, "cqkv_decode_paged_workspace_bytes") != CQKV_OK ||
+        batch <= 0 || q_heads <= 0 || q_len <= 0)
+        return 0;
+    const int nseg = paged_segments(blocks, n_blocks, batch, nullptr);
+    size_t part_off, lse_off;
+    return paged_workspace(nseg, batch, q_heads, q_len, blocks[0].k->head_dim, &part_off, &lse_off);
+}
+
+extern "C" int cqkv_decode_attention_paged(const void *q, int32_t q_dtype,
+                                           const int64_t q_strides[3], const cqkv_kv_block *blocks,
+                                           int32_t n_blocks, int32_t batch, int32_t q_heads,
+                                           int32_t q_len, float softmax_scale, int32_t window_left,
+                                           int32_t window_right, void *out, int32_t out_dtype,
+                                           const int64_t out_strides[3], void *workspace,
+                                           size_t workspace_bytes, cqkv_stream_t stream) {
+    clear_error();
+    const char *who = "cqkv_decode_attention_paged";
+    if (int rc = check_blocks(blocks, n_blocks, batch, who)) return rc;
+    DecodeArgs a;
+    if (int rc = decode_prepare(a, who, q, q_dtype, q_strides, blocks[0].k, blocks[0].v, batch,
+                                q_heads, q_len, softmax_scale, window_left, window_right, out,
+                                out_dtype, out_strides))
+        return rc;
+    std::vector<PagedSeg> segs;
+    const int nseg = paged_segments(blocks, n_blocks, batch, &segs);
+    int64_t total = 0;
+    for (int i = 0; i < n_blocks; ++i) total += blocks[i].rows;
+    const int d = blocks[0].k->head_dim;
+    a.kv_len = (int32_t)total;
+    a.splits = nseg;
+
+    hipStream_t st = (hipStream_t)stream;
+    size_t part_off, lse_off;
+    const size_t need = paged_workspace(nseg, batch, q_heads, q_len, d, &part_off, &lse_off);
+    void *ws = workspace;
+    bool owned = false;
+    if (ws && workspace_bytes < need)
+        return fail(CQKV_ERR_WORKSPACE, "%s: workspace %zu < %zu bytes", who, workspace_bytes, need);
+    if (!ws) {
+        CQKV_HIP_CHECK(hipMallocAsync(&ws, need, st));
+        owned = true;
+    }
+    hipError_t e = hipMemcpyAsync(ws, segs.data(), segs.size() * sizeof(PagedSeg),
+                                  hipMemcpyHostToDevice, st);
+    a.segs = (const PagedSeg *)ws;
+    if (nseg > 1) {
+        a.part_o = (float *)((char *)ws + part_off);
+        a.part_lse = (float *)((char *)ws + part_off + lse_off);
+    }
+    if (e == hipSuccess) e = decode_launch(a, blocks[0].k->format, d, st);
+    if (owned) {
+        hipError_t fe = hipFreeAsync(ws, st);
+        if (e == hipSuccess) e = fe;
+    }
+    if (e != hipSuccess) return fail(CQKV_ERR_HIP, "%s: %s", who, hipGetErrorString(e));
     return CQKV_OK;
 }

@@ -5,8 +5,9 @@
  * Qntology/candle-rocm-vulkan. Every entry point is a host function taking device pointers,
  * explicit sizes / strides and a hipStream_t (NULL = the legacy stream the reference launches on),
  * and returning CQKV_OK or a negative status; cqkv_last_error() gives the message of the last
- * failure of the calling thread. No call allocates device memory except cqkv_decode_attention when
- * it is given no workspace. Nothing here holds torch or candle types.
+ * failure of the calling thread. No call allocates device memory except cqkv_decode_attention and
+ * cqkv_decode_attention_paged when they are given no workspace. Nothing here holds torch or
+ * candle types.
  *
  * Reference interfaces replaced (paths relative to the reference repository root):
  *   cqkv_quant_append      RocmStorage::tq_quantize + Cache::append
@@ -15,6 +16,11 @@
  *   cqkv_decode_attention  RocmStorage::tq_attention (+ tq_combine)
  *                          (candle-core/src/rocm_backend/accel.rs:425-571,
  *                           candle-nn/src/turbo_quant.rs:1143-1264)
+ *   cqkv_decode_attention_paged
+ *                          RocmStorage::tq_attention_paged over a PageTable of cache blocks
+ *                          (candle-core/src/rocm_backend/accel.rs:425-571,
+ *                           candle-core/src/accel/attention.rs:293-366,
+ *                           candle-nn/src/turbo_quant.rs:1082-1114 attention_packed_blocks)
  *   cqkv_flash_attn        RocmStorage::flash_attn (candle-core/src/rocm_backend/accel.rs:54-158),
  *                          behind candle_flash_attn::flash_attn (candle-flash-attn/src/lib.rs:149)
  *   cqkv_rows_import /     the reference's packed row layout [codes][aux][rsc0][rsc1]
@@ -111,6 +117,34 @@ int cqkv_decode_attention(const void *q, int32_t q_dtype, const int64_t q_stride
                           void *out, int32_t out_dtype, const int64_t out_strides[3],
                           int32_t splits, void *workspace, size_t workspace_bytes,
                           cqkv_stream_t stream);
+
+/* One block of a paged cache (the reference's KvBlockRef, candle-nn/src/flash_attn.rs:609-613,
+ * packed into a PageTable, candle-core/src/accel/attention.rs:307-366): a key side and a value
+ * side holding `rows` valid tokens at the start of every (batch, kv head) plane. The keys of a
+ * paged call are the blocks' valid rows concatenated in block order; masks are bottom-right
+ * aligned over that concatenation. Every block has the format, head dim, kv heads and TURBO4
+ * seeds of block 0; capacities may differ. */
+typedef struct cqkv_kv_block {
+    const cqkv_side *k;
+    const cqkv_side *v;
+    int32_t rows;
+    int32_t reserved;
+} cqkv_kv_block;
+
+/* Device scratch a cqkv_decode_attention_paged call over these blocks needs (its block table and
+ * split partials); 0 if the blocks or sizes are invalid. */
+size_t cqkv_decode_paged_workspace_bytes(const cqkv_kv_block *blocks, int32_t n_blocks,
+                                         int32_t batch, int32_t q_heads, int32_t q_len);
+/* cqkv_decode_attention over the concatenated valid rows of n_blocks blocks, without copying
+ * them (any number of blocks; the reference's kernel takes at most 128 and concatenates beyond).
+ * Every sequence of the batch sees all the rows. Errors as the reference's check_blocks
+ * (flash_attn.rs:650-686): no blocks, mismatched blocks, rows above a capacity, no keys. */
+int cqkv_decode_attention_paged(const void *q, int32_t q_dtype, const int64_t q_strides[3],
+                                const cqkv_kv_block *blocks, int32_t n_blocks, int32_t batch,
+                                int32_t q_heads, int32_t q_len, float softmax_scale,
+                                int32_t window_left, int32_t window_right, void *out,
+                                int32_t out_dtype, const int64_t out_strides[3], void *workspace,
+                                size_t workspace_bytes, cqkv_stream_t stream);
 
 /* Dense bf16 flash attention (FlashAttnOp / candle_flash_attn::flash_attn):
  *   q (batch, q_len, q_heads, D), k / v (batch, kv_len, kv_heads, D), out like q, all bf16 with

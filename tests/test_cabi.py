@@ -109,6 +109,43 @@ def test_argument_errors_are_status_codes(cq):
     assert b"capacity" in L.cqkv_last_error()
 
 
+def test_paged_argument_errors_and_workspace(cq):
+    """cqkv_decode_attention_paged validates its blocks like the reference's check_blocks
+    (candle-nn/src/flash_attn.rs:650-686) before any launch, and sizes its scratch."""
+    L = cq.lib()
+    x = (ctypes.c_int64 * 3)(1, 1, 1)
+    k0 = cq.Side(cq.FP8, 0, 128, 8, 64, 0, 0, 1, 1)
+    v0 = cq.Side(cq.FP8, 1, 128, 8, 64, 0, 0, 1, 1)
+    k1 = cq.Side(cq.FP8, 0, 128, 8, 128, 0, 0, 1, 1)
+    v1 = cq.Side(cq.FP8, 1, 128, 8, 128, 0, 0, 1, 1)
+    kx = cq.Side(cq.MXFP4, 0, 128, 8, 64, 0, 0, 1, 1)
+
+    def blocks(*bl):
+        arr = (cq.KvBlock * len(bl))()
+        for i, (k, v, r) in enumerate(bl):
+            arr[i].k, arr[i].v, arr[i].rows = ctypes.pointer(k), ctypes.pointer(v), r
+        return arr
+
+    def call(arr, n, hq=8, lq=1):
+        return L.cqkv_decode_attention_paged(ctypes.c_void_p(1), 0, x, arr, n, 1, hq, lq, 0.1,
+                                             -1, -1, ctypes.c_void_p(1), 0, x, None, 0, None)
+    assert call(None, 0) == cq.ERR_ARG
+    assert b"no blocks" in L.cqkv_last_error()
+    assert call(blocks((k0, v0, 65)), 1) == cq.ERR_ARG  # rows above the capacity
+    assert b"capacities" in L.cqkv_last_error()
+    assert call(blocks((k0, v0, 0), (k1, v1, 0)), 2) == cq.ERR_ARG
+    assert b"no keys" in L.cqkv_last_error()
+    assert call(blocks((k0, v0, 10), (kx, v1, 10)), 2) == cq.ERR_ARG  # another format
+    assert b"differs from block 0" in L.cqkv_last_error()
+    assert call(blocks((k0, k0, 10)), 1) == cq.ERR_ARG  # a key side in the value slot
+    assert call(blocks((k0, v0, 10)), 1, hq=8 * 32) == cq.ERR_ARG  # GQA group too wide
+    # scratch: the block table plus, with several segments, the partials
+    one = L.cqkv_decode_paged_workspace_bytes(blocks((k0, v0, 10)), 1, 1, 8, 1)
+    many = L.cqkv_decode_paged_workspace_bytes(blocks((k1, v1, 128), (k1, v1, 128)), 2, 1, 8, 1)
+    assert 0 < one < many
+    assert L.cqkv_decode_paged_workspace_bytes(blocks((k0, v0, 65)), 1, 1, 8, 1) == 0
+
+
 def test_gpu_entry_points_refuse_cpu_tensors(cq):
     torch = pytest.importorskip("torch")
     side = cq.CacheSide(cq.FP8, False, 1, 1, 64, 32, torch.zeros(1, dtype=torch.uint8),
