@@ -20,10 +20,13 @@
 //  * V^T operands come by ds_read_b128 from a V^T tile written by the pre-pass
 //    (prefill_stage_kernel) with its keys already in that permuted order.
 //  * K and V^T tiles of 64 keys stream through two 4-stage LDS rings, filled by asynchronous
-//    buffer_load_dwordx4 ... lds copies issued two tiles ahead; one barrier per tile. Chunks of a
-//    row are XOR-swizzled so the reads are free of bank conflicts.
-//  * The two wavefronts of a SIMD ping-pong: between two barriers one runs its MFMAs (P V of the
-//    previous tile, S of this one) while the other runs its softmax on the VALU, then they swap.
+//    buffer_load_dwordx4 ... lds copies issued three tiles ahead; one barrier per tile. Chunks
+//    of a row are XOR-swizzled so the reads are free of bank conflicts.
+//  * Software-pipelined tile loop: each wavefront computes S of the next tile on the MFMA pipe
+//    while its VALU exponentiates this tile's scores, then runs P V of this tile on the MFMA
+//    pipe while its VALU sums P and takes the next tile's row maxima. The MFMA and VALU work of
+//    one wavefront are interleaved instruction by instruction (sched_group_barrier), and the two
+//    wavefronts of each SIMD fill each other's stalls.
 //  * Causal work is uneven: the workgroups with the most key tiles are dispatched first.
 #include "cqkv_device.h"
 #include "cqkv_host.h"
@@ -90,26 +93,36 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 #define PF_INLINE __device__ __attribute__((always_inline)) inline
 
+// A buffer resource from wavefront-uniform values, built in scalar registers (the compiler can
+// otherwise move the address to vector registers and wrap each copy in a per-lane loop).
+PF_INLINE rsrc_t pf_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t p = (uint64_t)base;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+    return make_rsrc((const void *)(((uint64_t)hi << 32) | lo), __builtin_amdgcn_readfirstlane(bytes));
+}
 // Asynchronous global -> LDS copy of key tile kt into the stages kstage / vstage: K rows (keys)
 // and V^T rows (head dims), one buffer_load_dwordx4 ... lds (1 KB) per 4 K rows / 8 V^T rows.
 // Wavefront w copies K rows 8w .. 8w+7 and V^T rows 16w .. 16w+15. K: lane l writes chunk
 // position l % 16 of row l / 16, so it loads logical chunk (l % 16) ^ swz(row); the buffer
 // range ends at the last key, so rows past it read zeros. V^T: lane l writes chunk position
-// l % 8 of row l / 8 (the pre-pass zero-fills keys past the end). Buffer loads count on vmcnt
-// only, so the LDS reads of other stages need no wait on these copies.
+// l % 8 of row l / 8 (the pre-pass zero-fills keys past the end). Tiles past the last one
+// (valid false) get a zero-size resource: no memory access, zeros into a stage nobody reads
+// again. Buffer loads count on vmcnt only, so the LDS reads of other stages need no wait on
+// these copies.
 PF_INLINE void pf_issue_tile(uint8_t *kstage, uint8_t *vstage, const uint16_t *kplane,
                              const uint16_t *vtplane, int64_t k_st, int vt_len,
                              const uint32_t (&koff)[2], const uint32_t (&voff)[2], int kt,
-                             int kv_len, int wave) {
-    const int row0 = kt * kPfBK;
+                             int kv_len, int wave, bool valid) {
+    const int row0 = valid ? kt * kPfBK : 0;
     const int nvalid = min(kPfBK, kv_len - row0);
-    const rsrc_t kr = make_rsrc(kplane + (int64_t)row0 * k_st,
-                                (uint32_t)((int64_t)(nvalid - 1) * k_st * 2 + kPfRow));
+    const rsrc_t kr = pf_rsrc(kplane + (int64_t)row0 * k_st,
+                              valid ? (uint32_t)((int64_t)(nvalid - 1) * k_st * 2 + kPfRow) : 0u);
 #pragma unroll
     for (int r4 = 0; r4 < 2; ++r4)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void *)(kstage + (8 * wave + 4 * r4) * kPfRow),
                                                  16, koff[r4], 0, 0, 0);
-    const rsrc_t vr = make_rsrc(vtplane + row0, (uint32_t)(((int64_t)kPfD * vt_len - row0) * 2));
+    const rsrc_t vr = pf_rsrc(vtplane + row0, valid ? (uint32_t)(((int64_t)kPfD * vt_len - row0) * 2) : 0u);
 #pragma unroll
     for (int r8 = 0; r8 < 2; ++r8)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_void *)(vstage + (16 * wave + 8 * r8) * kPfVtRow),
@@ -137,46 +150,73 @@ constexpr int kPfCopiesPerTile = 4;  // global_load_lds per wavefront per tile
 struct PfState {
     bf16x8 qop[8];   // Q^T operands (16-dim steps ks) of this wavefront's 32 queries
     f32x16 acc[4];   // O^T: 32-dim block md
-    f32x16 negm;     // -m_run (0 before the first key) in every register: the S^T accumulator seed
+    float negm;      // -m_run (0 before the first key), added to the raw scores
     float m_run, l_run;
+    float thr;       // the row maximum moves when a tile's maximum exceeds thr: -inf before the
+                     // row's first key, then 8 (p stays below 2^8)
     int qlo, qhi;    // visible keys of this lane's query
 };
 
-// Orders the 16 LDS reads and 16 MFMAs of a product block: kPfReadAhead reads first, then one
-// MFMA per read, so each MFMA's operand was requested kPfReadAhead MFMAs earlier (left to
-// itself, the scheduler waits for every read before each pair of MFMAs).
-constexpr int kPfReadAhead = 4;
-PF_INLINE void pf_pipe_schedule() {
-    constexpr int kDsRead = 0x100, kMfma = 0x008;  // sched_group_barrier instruction classes
+constexpr int kDsRead = 0x100, kMfma = 0x008, kValu = 0x402;  // sched_group_barrier classes (VALU + TRANS)
+
+// Orders a block of 16 MFMAs with its 16 LDS operand reads, VALU VALU instructions per MFMA
+// and the VMEM (tile copy) instructions: four reads first, then MFMA, read, copy, VALU x VALU,
+// so each MFMA's operand was requested four MFMAs earlier and the VALU work fills the MFMA
+// pipe's busy cycles.
+template <int VALU, int VMEM = 0>
+PF_INLINE void pf_block_schedule() {
 #pragma unroll
-    for (int i = 0; i < kPfReadAhead; ++i) __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+    for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
 #pragma unroll
-    for (int i = 0; i < 16 - kPfReadAhead; ++i) {
+    for (int i = 0; i < 16; ++i) {
         __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+        if (i < 12) __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+        if (i < VMEM) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+        if (VALU > 0) __builtin_amdgcn_sched_group_barrier(kValu, VALU, 0);
     }
-#pragma unroll
-    for (int i = 0; i < kPfReadAhead; ++i) __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
 }
 
-// S^T (64 keys x 32 queries) = K Q^T for the tile at k_lds; the two 32-key blocks alternate.
-PF_INLINE void pf_qk(f32x16 (&s)[2], const PfState &st, const uint8_t *k_lds, int lane) {
+// Per-lane LDS read offsets from the first stage of each ring, kept in registers and made opaque
+// at every step, so each read is one register plus a constant that fits the 16-bit DS offset
+// field (stage, key block, head-dim block); left alone, the compiler keeps a register per
+// (stage, offset) pair.
+struct PfAddr {
+    uint32_t k[8];  // K row qr, chunk 2 ks + h (swizzled), of key block 0
+    uint32_t v[4];  // kPfVBias + V^T row qr, chunk 2 kk + h (swizzled), of head-dim block 0
+};
+// The V^T stages follow the four 16 KB K stages; biasing the V^T offsets by 64 KB leaves
+// (stage address - 64 KB) + head-dim block offset, below 64 KB, as the constant part.
+constexpr uint32_t kPfVBias = 4 * kPfHalf;
+PF_INLINE void pf_addr_init(PfAddr &ad, int lane) {
     const int qr = lane & 31, h = lane >> 5;
-    const int sw = swz(qr);  // swz(32 + qr) == swz(qr)
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) ad.k[ks] = qr * kPfRow + (((2 * ks + h) ^ swz(qr)) << 4);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+        ad.v[kk] = kPfVBias + qr * kPfVtRow + (((2 * kk + h) ^ swz_vt(qr)) << 4);
+}
+PF_INLINE void pf_addr_opaque(PfAddr &ad) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(ad.k[i]));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(ad.v[i]));
+}
+
+// S^T (64 keys x 32 queries) = K Q^T for the tile at k_lds, key block 0 first.
+PF_INLINE void pf_qk(f32x16 (&s)[2], const PfState &st, const uint8_t *k_lds, const PfAddr &ad) {
     bf16x8 kop[16];
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
+    for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
-            kop[2 * ks + mb] = __builtin_bit_cast(
-                bf16x8, *(const u32x4 *)(k_lds + (32 * mb + qr) * kPfRow + (((2 * ks + h) ^ sw) << 4)));
-    s[0] = st.negm;
-    s[1] = st.negm;
+        for (int ks = 0; ks < 8; ++ks)
+            kop[8 * mb + ks] = __builtin_bit_cast(
+                bf16x8, *(const u32x4 *)(k_lds + ad.k[ks] + 32 * mb * kPfRow));
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
+    for (int mb = 0; mb < 2; ++mb) {
+        s[mb] = mfma32x32x16(kop[8 * mb], st.qop[0], f32x16{});
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb) s[mb] = mfma32x32x16(kop[2 * ks + mb], st.qop[ks], s[mb]);
-    pf_pipe_schedule();
+        for (int ks = 1; ks < 8; ++ks) s[mb] = mfma32x32x16(kop[8 * mb + ks], st.qop[ks], s[mb]);
+    }
 }
 
 // masks scores of keys outside the lane's visible range (tiles that cross a range end only)
@@ -202,40 +242,47 @@ PF_INLINE float pf_sum_halves(float x) {  // sum of lanes l and l ^ 32
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Online softmax over the tile. Q carries scale * log2(e) and the S^T accumulators start at
-// -m_run, so s already is the exponent of p = exp2(s) relative to the running maximum m_run.
-// The maximum is lazy: it moves (s is shifted, O and the row sum rescaled) only when a score
-// exceeds it by more than 2^8, or on a row's first keys; otherwise p < 2^8 and the step costs
-// one exp2 per score.
-PF_INLINE void pf_softmax(bf16x8 (&pop)[4], f32x16 (&s)[2], PfState &st) {
-    float mx = -__builtin_inff();
+// scores relative to the running maximum
+PF_INLINE void pf_shift(f32x16 (&s)[2], float negm) {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[mb][j]);
-    mx = pf_max_halves(mx);
-    const bool fresh = st.m_run == -__builtin_inff();
-    const bool need = fresh ? mx != -__builtin_inff() : mx > 8.0f;
-    if (__builtin_expect(__any(need), 0)) {
-        const float shift = need ? mx : 0.0f;
-        const float m_new = need ? (fresh ? 0.0f : st.m_run) + mx : st.m_run;
-        const float alpha = need ? __builtin_amdgcn_exp2f(st.m_run - m_new) : 1.0f;
+        for (int j = 0; j < 16; ++j) s[mb][j] += negm;
+}
+
+// this lane's maximum over the tile (two chains, block 0 first)
+PF_INLINE float pf_rowmax(const f32x16 (&s)[2]) {
+    float m0 = s[0][0], m1 = s[1][0];
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) s[mb][j] -= shift;
-#pragma unroll
-        for (int md = 0; md < 4; ++md) st.acc[md] *= alpha;
-        st.l_run *= alpha;
-        st.m_run = m_new;
-        const float nm = m_new == -__builtin_inff() ? 0.0f : -m_new;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) st.negm[j] = nm;
+    for (int j = 1; j < 16; ++j) {
+        m0 = fmaxf(m0, s[0][j]);
+        m1 = fmaxf(m1, s[1][j]);
     }
-    // p = exp2(s), packed to bf16; the row sum adds the bf16 values the product uses, two per
-    // dot2 instruction
-    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
-    float psum = 0.0f;
+    return fmaxf(m0, m1);
+}
+
+// The row maximum moves (rare): s is shifted to the new maximum, O and the row sum rescaled.
+// Q carries scale * log2(e) and pf_shift adds -m_run, so s is the exponent of p = exp2(s)
+// relative to m_run.
+PF_INLINE void pf_rescale(f32x16 (&s)[2], PfState &st, float mx, bool need) {
+    const bool fresh = st.m_run == -__builtin_inff();
+    const float shift = need ? mx : 0.0f;
+    const float m_new = need ? (fresh ? 0.0f : st.m_run) + mx : st.m_run;
+    const float alpha = need ? __builtin_amdgcn_exp2f(st.m_run - m_new) : 1.0f;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s[mb][j] -= shift;
+#pragma unroll
+    for (int md = 0; md < 4; ++md) st.acc[md] *= alpha;
+    st.l_run *= alpha;
+    st.m_run = m_new;
+    st.thr = m_new == -__builtin_inff() ? -__builtin_inff() : 8.0f;
+    st.negm -= shift;  // -m_new: 0 - mx for a row's first keys, -m_run - mx after
+}
+
+// p = exp2(s), packed to the bf16 P^T operands
+PF_INLINE void pf_exp(bf16x8 (&pop)[4], const f32x16 (&s)[2]) {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
@@ -246,34 +293,90 @@ PF_INLINE void pf_softmax(bf16x8 (&pop)[4], f32x16 (&s)[2], PfState &st) {
                 const float p0 = __builtin_amdgcn_exp2f(s[mb][8 * half + 2 * e]);
                 const float p1 = __builtin_amdgcn_exp2f(s[mb][8 * half + 2 * e + 1]);
                 const bf16x2 pp = {(__bf16)p0, (__bf16)p1};
-                psum = __builtin_amdgcn_fdot2_f32_bf16(pp, ones, psum, false);
                 w[e] = __builtin_bit_cast(uint32_t, pp);
             }
             pop[2 * mb + half] = __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
         }
-    st.l_run += psum;
+}
+
+// the row sum adds the bf16 values the product uses, two per dot2 instruction, in two chains
+// (each word goes through a scalar: clang's __builtin_bit_cast of a vector element reads
+// element 0)
+PF_INLINE float pf_dot2_ones(uint32_t w, float acc) {
+    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), ones, acc, false);
+}
+PF_INLINE void pf_psum(PfState &st, const bf16x8 (&pop)[4]) {
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const u32x4 w = __builtin_bit_cast(u32x4, pop[i]);
+        const uint32_t w0 = w.x, w1 = w.y, w2 = w.z, w3 = w.w;
+        a0 = pf_dot2_ones(w0, a0);
+        a1 = pf_dot2_ones(w1, a1);
+        a0 = pf_dot2_ones(w2, a0);
+        a1 = pf_dot2_ones(w3, a1);
+    }
+    st.l_run += a0 + a1;
 }
 
 // O^T += V^T P^T over the V^T tile at v_lds. 16-key step kk = keys 16 kk + [0, 16): the P^T
 // operand holds S^T registers 8 (kk % 2) .. +7 of key block kk / 2, i.e. lane half h holds keys
 // 16 kk + 8 (e / 4) + 4 h + e % 4 in k-slot 8 h + e; the pre-pass stores V^T keys in that order
 // (bits 2 and 3 of the key swapped), so the A operand of lane (d, h) is chunk 2 kk + h of row d.
-PF_INLINE void pf_pv(PfState &st, const bf16x8 (&pop)[4], const uint8_t *v_lds, int lane) {
-    const int qr = lane & 31, h = lane >> 5;
+PF_INLINE void pf_pv(PfState &st, const bf16x8 (&pop)[4], const uint8_t *v_lds, const PfAddr &ad) {
     bf16x8 vt[16];
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-        const uint32_t off = qr * kPfVtRow + (((2 * kk + h) ^ swz_vt(qr)) << 4);
+    for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
         for (int md = 0; md < 4; ++md)
             vt[4 * kk + md] =
-                __builtin_bit_cast(bf16x8, *(const u32x4 *)(v_lds + off + md * 32 * kPfVtRow));
-    }
+                __builtin_bit_cast(bf16x8, *(const u32x4 *)(v_lds + (ad.v[kk] - kPfVBias) + md * 32 * kPfVtRow));
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
         for (int md = 0; md < 4; ++md) st.acc[md] = mfma32x32x16(vt[4 * kk + md], pop[kk], st.acc[md]);
-    pf_pipe_schedule();
+}
+
+// One key tile t of a wavefront (not the last), with S(t) in `cur`:
+//  * block 1: S(t + 1) = K(t + 1) Q^T into `nxt` on the MFMA pipe while the VALU turns S(t)
+//    into P(t) = exp2(S(t));
+//  * on tiles that cross a range end, S(t + 1) is masked;
+//  * block 2: O += V(t)^T P(t) on the MFMA pipe while the VALU adds up the row sum of P(t),
+//    shifts S(t + 1) by -m_run and takes its row maximum; the copies of a later tile
+//    (issue_copies) are issued among its first MFMAs;
+//  * then, rarely, the row maximum moves (pf_rescale).
+template <typename IssueCopies>
+PF_INLINE void pf_tile(f32x16 (&cur)[2], f32x16 (&nxt)[2], bf16x8 (&pop)[4], PfState &st,
+                       const uint8_t *k_next, const uint8_t *v_cur, const PfAddr &ad,
+                       bool masked, int k1, int lane, IssueCopies &&issue_copies) {
+    pf_qk(nxt, st, k_next, ad);
+    pf_exp(pop, cur);
+    pf_block_schedule<3>();
+    __builtin_amdgcn_sched_barrier(0);
+    // P(t) is used only after the branch below: pin its computation to block 1
+#pragma unroll
+    for (int i = 0; i < 4; ++i) asm volatile("" ::"v"(pop[i]));
+    if (masked) pf_mask(nxt, st, k1, lane);
+    issue_copies();
+    pf_pv(st, pop, v_cur, ad);
+    pf_psum(st, pop);
+    pf_shift(nxt, st.negm);
+    float mx = pf_rowmax(nxt);
+    pf_block_schedule<4, 4>();
+    __builtin_amdgcn_sched_barrier(0);
+    mx = pf_max_halves(mx);
+    const bool need = mx > st.thr;
+    if (__builtin_expect(__any(need), 0)) pf_rescale(nxt, st, mx, need);
+}
+
+// The last key tile: P(t) and O += V(t)^T P(t).
+PF_INLINE void pf_last_tile(const f32x16 (&cur)[2], bf16x8 (&pop)[4], PfState &st,
+                            const uint8_t *v_cur, const PfAddr &ad) {
+    pf_exp(pop, cur);
+    pf_pv(st, pop, v_cur, ad);
+    pf_psum(st, pop);
+    pf_block_schedule<1>();
 }
 
 // Two wavefronts per SIMD (8 per workgroup, ~240 registers each).
@@ -334,8 +437,9 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
         if (qi < a.q_len) pf_key_range(qi, a.q_len, a.kv_len, a.wl, a.wr, st.qlo, st.qhi);
         else st.qlo = st.qhi = 0;
         st.m_run = -__builtin_inff();
+        st.thr = -__builtin_inff();
         st.l_run = 0.0f;
-        st.negm = f32x16{};
+        st.negm = 0.0f;
 #pragma unroll
         for (int md = 0; md < 4; ++md) st.acc[md] = f32x16{};
     }
@@ -344,64 +448,100 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     const uint16_t *vtplane = a.vt + ((int64_t)b * a.kv_heads + hk) * kPfD * a.vt_len;
     PF_WAIT_VMCNT(0);  // the Q loads above must not be counted by the copy waits below
 
-    // Tile t lives in stage t % 4 of both rings; its copies are issued right after barrier t - 2.
+    // Tile t lives in stage t % 4 of both rings. Its copies are issued in step t - 3, after
+    // barrier t - 3 (tiles 0-2 before the loop); barrier t (at the top of step t) follows this
+    // wavefront's copies of tile t + 1, so K(t + 1) and V(t) are in LDS for every wavefront
+    // after it, and stage (t + 3) % 4 has no reader left: K(t - 1) was read in step t - 2,
+    // V(t - 1) in step t - 1.
 #define PF_KS(k) ((k) == 0 ? ks0 : (k) == 1 ? ks1 : (k) == 2 ? ks2 : ks3)
 #define PF_VS(k) ((k) == 0 ? vs0 : (k) == 1 ? vs1 : (k) == 2 ? vs2 : vs3)
     uint32_t koff[2], voff[2];
     pf_copy_offsets(koff, voff, a.k_st, a.vt_len, wave, lane);
+    // Every step issues the copies of one tile; past the last tile they are dummies with a
+    // zero-size resource (no memory access; zeros land in a stage nobody reads again), so each
+    // wavefront always has the copies of exactly the next two tiles in flight at a barrier.
 #define PF_ISSUE(k, t)                                                                       \
     pf_issue_tile(PF_KS(k), PF_VS(k), kplane, vtplane, a.k_st, a.vt_len, koff, voff,         \
-                  kt_begin + (t), a.kv_len, wave)
-    // Barrier j: this wave's copies of tile j are done (those of tile j + 1 may be in flight);
-    // once every wave has passed it, tile j - 2 has no reader left and tile j + 2 is copied
-    // into its stage.
-#define PF_BARRIER(j, kst)                                                                   \
+                  kt_begin + (t), a.kv_len, wave, (t) < ntiles)
+    PF_ISSUE(0, 0);
+    PF_ISSUE(1, 1);
+    PF_ISSUE(2, 2);
+    PF_WAIT_VMCNT(2 * kPfCopiesPerTile);
+    __builtin_amdgcn_s_barrier();
+
+    // Barrier t: this wavefront's copies of tile t + 1 have landed (those of tile t + 2 may be
+    // in flight); the copies of tile t + 3 follow within the step.
+#define PF_SYNC(k, t)                                                                        \
     {                                                                                        \
-        if ((j) + 1 < ntiles) PF_WAIT_VMCNT(kPfCopiesPerTile);                               \
-        else PF_WAIT_VMCNT(0);                                                               \
+        PF_WAIT_VMCNT(kPfCopiesPerTile);                                                     \
         __builtin_amdgcn_s_barrier();                                                        \
-        if ((j) + 2 < ntiles) PF_ISSUE(kst, (j) + 2);                                        \
     }
-    if (ntiles > 0) PF_ISSUE(0, 0);
-    if (ntiles > 1) PF_ISSUE(1, 1);
+    if (!wave_live) {  // heads past the group: copies and barriers only
+        for (int t = 0; t < ntiles;) {
+            PF_SYNC(0, t) PF_ISSUE(3, t + 3); if (++t == ntiles) break;
+            PF_SYNC(1, t) PF_ISSUE(0, t + 3); if (++t == ntiles) break;
+            PF_SYNC(2, t) PF_ISSUE(1, t + 3); if (++t == ntiles) break;
+            PF_SYNC(3, t) PF_ISSUE(2, t + 3); ++t;
+        }
+        PF_WAIT_VMCNT(0);
+        return;
+    }
+
+    const auto tile_masked = [&](int kt) {
+        const int k0 = (kt_begin + kt) * kPfBK;
+        return !(k0 >= lo_last && k0 + kPfBK <= hi_first);
+    };
+    f32x16 sa[2], sb[2];
     bf16x8 pop[4];
-    f32x16 s[2];
-    // Ping-pong between the two wavefronts of a SIMD (w and w + 4). Both run the same sequence
-    // softmax(t - 1), P V(t - 1), S(t), but wavefronts 0-3 take barrier t between softmax(t - 1)
-    // and P V(t - 1), wavefronts 4-7 after S(t - 1). Between two barriers one wavefront of each
-    // SIMD runs P V, S (MFMA) and then softmax (VALU), the other softmax and then P V, S.
-    const bool lead = qhalf == 0;
-    if (!lead) PF_BARRIER(0, 2)
-#define PF_STEP(k)                                                                           \
+    PfAddr ad;
+    pf_addr_init(ad, lane);
+    if (ntiles > 0) {
+        pf_qk(sa, st, ks0, ad);
+        pf_shift(sa, st.negm);
+        if (tile_masked(0)) pf_mask(sa, st, kt_begin * kPfBK, lane);
+        const float mx = pf_max_halves(pf_rowmax(sa));
+        const bool need = mx > st.thr;
+        if (__any(need)) pf_rescale(sa, st, mx, need);
+    }
+    // Step t: S(t) in CUR, stage t % 4 holds V(t), stage (t + 1) % 4 holds K(t + 1); the
+    // copies of tile t + 3 go into stage (t + 3) % 4 in block 2. The last tile leaves the loop
+    // (its stage in `last`) and is finished after it.
+#define PF_STEP(k, CUR, NXT)                                                                 \
     {                                                                                        \
-        if (t > ntiles) break;                                                               \
-        if (wave_live && t > 0) pf_softmax(pop, s, st);                                      \
-        if (lead) PF_BARRIER(t, ((k) + 2) & 3)                                               \
-        if (wave_live) {                                                                     \
-            __builtin_amdgcn_s_setprio(1); /* the MFMA block goes first at issue */          \
-            if (t > 0) pf_pv(st, pop, PF_VS(((k) + 3) & 3), lane);                           \
-            if (t < ntiles) {                                                                \
-                const int k0 = (kt_begin + t) * kPfBK;                                       \
-                pf_qk(s, st, PF_KS(k), lane);                                                \
-                if (!(k0 >= lo_last && k0 + kPfBK <= hi_first)) pf_mask(s, st, k0, lane);    \
-            }                                                                                \
-            __builtin_amdgcn_s_setprio(0);                                                   \
+        pf_addr_opaque(ad);                                                                  \
+        PF_SYNC(k, t)                                                                        \
+        if (t + 1 == ntiles) {                                                               \
+            last = k;                                                                        \
+            break;                                                                           \
         }                                                                                    \
-        if (!lead && t < ntiles) PF_BARRIER(t + 1, ((k) + 3) & 3)                            \
+        pf_tile(CUR, NXT, pop, st, PF_KS(((k) + 1) & 3), PF_VS(k), ad, tile_masked(t + 1),   \
+                (kt_begin + t + 1) * kPfBK, lane, [&] {                                      \
+                    PF_ISSUE(((k) + 3) & 3, t + 3);                                          \
+                });                                                                          \
         ++t;                                                                                 \
     }
-    for (int t = 0; t <= ntiles;) {
-        PF_STEP(0)
-        PF_STEP(1)
-        PF_STEP(2)
-        PF_STEP(3)
+    int last = 0;
+    if (ntiles > 0) {
+        for (int t = 0;;) {
+            PF_STEP(0, sa, sb)
+            PF_STEP(1, sb, sa)
+            PF_STEP(2, sa, sb)
+            PF_STEP(3, sb, sa)
+        }
+        PF_WAIT_VMCNT(0);  // the dummy copies past the end
+        pf_addr_opaque(ad);
+        switch (last) {
+            case 0: pf_last_tile(sa, pop, st, vs0, ad); break;
+            case 1: pf_last_tile(sb, pop, st, vs1, ad); break;
+            case 2: pf_last_tile(sa, pop, st, vs2, ad); break;
+            default: pf_last_tile(sb, pop, st, vs3, ad); break;
+        }
     }
 #undef PF_STEP
+#undef PF_SYNC
 #undef PF_ISSUE
 #undef PF_KS
 #undef PF_VS
-#undef PF_BARRIER
-    if (!wave_live) return;
 
     // ---- normalise and write O (bf16): lane (qr, h), d = 32 md + 8 (j / 4) + 4 h + j % 4 ----
     const float l = pf_sum_halves(st.l_run);
