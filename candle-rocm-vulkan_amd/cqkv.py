@@ -79,6 +79,9 @@ def lib() -> ctypes.CDLL:
                                                   i32, P, i32, I64P, P, sz, P]
         L.cqkv_flash_attn.argtypes = [P, I64P, P, I64P, P, I64P, P, I64P, i32, i32, i32, i32,
                                       i32, i32, f32, i32, i32, SP, SP, i32, P]
+        L.cqkv_flash_attn_ext.argtypes = [P, I64P, P, I64P, P, I64P, P, I64P, i32, i32, i32,
+                                          i32, i32, i32, f32, i32, i32, f32, P, i32, P, P, i32,
+                                          i32, SP, SP, i32, P]
         L.cqkv_reference_row_words.argtypes = [i32, i32]
         L.cqkv_reference_row_words.restype = i32
         L.cqkv_rows_import.argtypes = [SP, P, i32, i32, i32, P]
@@ -94,7 +97,7 @@ def lib() -> ctypes.CDLL:
 EXPORTED = ["cqkv_codes_plane_bytes", "cqkv_scales_plane_bytes", "cqkv_quant_append",
             "cqkv_decode_workspace_bytes", "cqkv_decode_splits", "cqkv_decode_attention",
             "cqkv_decode_paged_workspace_bytes", "cqkv_decode_attention_paged",
-            "cqkv_flash_attn", "cqkv_reference_row_words", "cqkv_rows_import",
+            "cqkv_flash_attn", "cqkv_flash_attn_ext", "cqkv_reference_row_words", "cqkv_rows_import",
             "cqkv_rows_export", "cqkv_turbo_codebook", "cqkv_turbo_signs", "cqkv_last_error",
             "cqkv_version"]
 
@@ -256,12 +259,29 @@ def decode_attention_paged(q: torch.Tensor, blocks, softmax_scale: float, window
     return out
 
 
+def _alibi_arg(alibi_slopes, batch: int, q_heads: int):
+    """ALiBi slopes (q_heads) or (batch, q_heads) f32 on the device -> (pointer, batch stride)."""
+    if alibi_slopes is None:
+        return None, 0
+    _need_gpu(alibi_slopes, "alibi_slopes")
+    if alibi_slopes.dtype != torch.float32 or not alibi_slopes.is_contiguous():
+        raise CqkvError(ERR_ARG, "alibi_slopes must be contiguous float32")
+    if tuple(alibi_slopes.shape) == (q_heads,):
+        return _ptr(alibi_slopes), 0
+    if tuple(alibi_slopes.shape) == (batch, q_heads):
+        return _ptr(alibi_slopes), q_heads
+    raise CqkvError(ERR_ARG, f"alibi slopes must be ({q_heads}) or ({batch}, {q_heads}), "
+                             f"got {tuple(alibi_slopes.shape)}")
+
+
 def flash_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, softmax_scale: float,
                causal: bool, window_left: int = -1, window_right: int = -1,
                k_cache: CacheSide | None = None, v_cache: CacheSide | None = None,
-               position: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+               position: int = 0, out: torch.Tensor | None = None, softcap: float = 0.0,
+               alibi_slopes: torch.Tensor | None = None) -> torch.Tensor:
     """candle_flash_attn::flash_attn layout: q (b, s_q, h_q, d), k / v (b, s_kv, h_kv, d), bf16.
-    With k_cache / v_cache (FP8 sides) K / V are also quantized into the cache at `position`."""
+    With k_cache / v_cache (FP8 sides) K / V are also quantized into the cache at `position`.
+    softcap / alibi_slopes as flash_attn_alibi_windowed_softcap (candle-flash-attn/src/lib.rs)."""
     _need_gpu(q, "q")
     b, sq, hq, d = q.shape
     _, sk, hkv, _ = k.shape
@@ -271,10 +291,45 @@ def flash_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, softmax_scale:
         window_right = 0
     kc = None if k_cache is None else ctypes.byref(k_cache.struct())
     vc = None if v_cache is None else ctypes.byref(v_cache.struct())
-    _check(lib().cqkv_flash_attn(
+    al, al_bs = _alibi_arg(alibi_slopes, b, hq)
+    _check(lib().cqkv_flash_attn_ext(
         _ptr(q), _strides3(q, (0, 1, 2)), _ptr(k), _strides3(k, (0, 1, 2)), _ptr(v),
         _strides3(v, (0, 1, 2)), _ptr(out), _strides3(out, (0, 1, 2)), b, sq, sk, hq, hkv, d,
-        softmax_scale, window_left, window_right, kc, vc, position, _stream(q.device)))
+        softmax_scale, window_left, window_right, softcap, al, al_bs, None, None, 0, 0, kc, vc,
+        position, _stream(q.device)))
+    return out
+
+
+def flash_attn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                      cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, max_seqlen_q: int,
+                      max_seqlen_k: int, softmax_scale: float, causal: bool,
+                      window_left: int = -1, window_right: int = -1, softcap: float = 0.0,
+                      alibi_slopes: torch.Tensor | None = None,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """candle_flash_attn::flash_attn_varlen layout: q (total_q, h_q, d), k / v (total_k, h_kv,
+    d) bf16, cumulative sequence offsets cu_seqlens_q / cu_seqlens_k (batch + 1,) int32 on the
+    device (the reference takes u32)."""
+    _need_gpu(q, "q")
+    total_q, hq, d = q.shape
+    total_k, hkv, _ = k.shape
+    for name, c in (("cu_seqlens_q", cu_seqlens_q), ("cu_seqlens_k", cu_seqlens_k)):
+        _need_gpu(c, name)
+        if c.dtype != torch.int32 or c.dim() != 1 or not c.is_contiguous():
+            raise CqkvError(ERR_ARG, f"{name} must be a contiguous 1-D int32 tensor")
+    if cu_seqlens_q.shape != cu_seqlens_k.shape or cu_seqlens_q.numel() < 2:
+        raise CqkvError(ERR_ARG, "cu_seqlens_q / cu_seqlens_k must both have batch + 1 entries")
+    b = cu_seqlens_q.numel() - 1
+    if out is None:
+        out = torch.empty_like(q)
+    if causal:
+        window_right = 0
+    al, al_bs = _alibi_arg(alibi_slopes, b, hq)
+    strides = lambda t: (ctypes.c_int64 * 3)(0, t.stride(0), t.stride(1))
+    _check(lib().cqkv_flash_attn_ext(
+        _ptr(q), strides(q), _ptr(k), strides(k), _ptr(v), strides(v), _ptr(out), strides(out),
+        b, max_seqlen_q, max_seqlen_k, hq, hkv, d, softmax_scale, window_left, window_right,
+        softcap, al, al_bs, _ptr(cu_seqlens_q), _ptr(cu_seqlens_k), total_q, total_k, None, None,
+        0, _stream(q.device)))
     return out
 
 

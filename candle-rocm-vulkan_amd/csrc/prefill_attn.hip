@@ -57,7 +57,48 @@ struct PrefillArgs {
     int32_t q_len, kv_len, q_heads, kv_heads, group, heads_per_wg, q_blocks, batch;
     int32_t wl, wr;
     float scale_log2;
+    // score terms (candle-core/kernels/flash_attn_impl.h:42-47, fa_logit), in the exp2 units of
+    // the scores: softcap2 = softcap * log2(e) (0: off), slopes * log2(e) from alibi[b * alibi_bs
+    // + head] (null: off)
+    float softcap2;
+    const float *alibi;
+    int32_t alibi_bs;
+    // variable-length batches (flash_attn.rs varlen, cu_seqlens): sequence b is rows cu_q[b] ..
+    // cu_q[b + 1] - 1 of q / out and cu_k[b] .. of k / v (null: dense, batch strides); q_len /
+    // kv_len are the maximum lengths, total_q / total_k the row counts of the tensors
+    const int32_t *cu_q, *cu_k;
+    int32_t total_q, total_k;
 };
+
+// First rows and lengths of sequence b. Variable-length offsets are clamped into the tensors
+// and the lengths to q_len / kv_len, so inconsistent prefix sums cannot address memory outside
+// them (they give wrong rows, not faults).
+struct PfSeq {
+    int64_t q0, k0;  // element offsets of the sequence's first q / out row and k / v row
+    int64_t o0, v0;
+    int lq, lk;
+};
+__device__ inline PfSeq pf_sequence(const PrefillArgs &a, int b) {
+    PfSeq r;
+    if (a.cu_q) {
+        const int qa = min(max(a.cu_q[b], 0), a.total_q), qe = min(max(a.cu_q[b + 1], qa), a.total_q);
+        const int ka = min(max(a.cu_k[b], 0), a.total_k), ke = min(max(a.cu_k[b + 1], ka), a.total_k);
+        r.lq = min(qe - qa, a.q_len);
+        r.lk = min(ke - ka, a.kv_len);
+        r.q0 = (int64_t)qa * a.q_st;
+        r.o0 = (int64_t)qa * a.o_st;
+        r.k0 = (int64_t)ka * a.k_st;
+        r.v0 = (int64_t)ka * a.v_st;
+    } else {
+        r.lq = a.q_len;
+        r.lk = a.kv_len;
+        r.q0 = (int64_t)b * a.q_sb;
+        r.o0 = (int64_t)b * a.o_sb;
+        r.k0 = (int64_t)b * a.k_sb;
+        r.v0 = (int64_t)b * a.v_sb;
+    }
+    return r;
+}
 
 __device__ inline f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -219,6 +260,41 @@ PF_INLINE void pf_qk(f32x16 (&s)[2], const PfState &st, const uint8_t *k_lds, co
     }
 }
 
+// Soft-capping and ALiBi of the raw scores of a tile whose first key is k0 (exp2 units, in the
+// reference's order: cap * tanh(s / cap), then - slope * |pos - key|; fa_logit,
+// candle-core/kernels/flash_attn_impl.h:42-47). pos is the lane's query position in key
+// coordinates.
+struct PfLogit {
+    float cap2;   // softcap * log2(e) (0: off)
+    float e2;     // 2 log2(e) / cap2: exp2(s * e2) = e^(2 s / cap2)
+    float slope2; // ALiBi slope * log2(e) of the wavefront's head (0: off)
+    int pos;
+};
+// cap * tanh(x / cap) = cap - 2 cap / (e^(2x / cap) + 1): one exp2 and one reciprocal, exact
+// limits at both ends (e -> inf: cap; e -> 0: -cap), absolute error ~1e-7 cap
+PF_INLINE void pf_logit(f32x16 (&s)[2], const PfLogit &lg, int k0, int lane) {
+    if (lg.cap2 > 0.0f) {
+        const float two_cap = 2.0f * lg.cap2;
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const float e = __builtin_amdgcn_exp2f(s[mb][j] * lg.e2);
+                s[mb][j] = lg.cap2 - two_cap * __builtin_amdgcn_rcpf(e + 1.0f);
+            }
+    }
+    if (lg.slope2 != 0.0f) {
+        const int d0 = lg.pos - (k0 + 4 * (lane >> 5));  // pos - key of register 0
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int dist = d0 - (32 * mb + 8 * (j >> 2) + (j & 3));
+                s[mb][j] -= lg.slope2 * (float)(dist < 0 ? -dist : dist);
+            }
+    }
+}
+
 // masks scores of keys outside the lane's visible range (tiles that cross a range end only)
 PF_INLINE void pf_mask(f32x16 (&s)[2], const PfState &st, int k0, int lane) {
     const int h = lane >> 5;
@@ -346,10 +422,10 @@ PF_INLINE void pf_pv(PfState &st, const bf16x8 (&pop)[4], const uint8_t *v_lds, 
 //    shifts S(t + 1) by -m_run and takes its row maximum; the copies of a later tile
 //    (issue_copies) are issued among its first MFMAs;
 //  * then, rarely, the row maximum moves (pf_rescale).
-template <typename IssueCopies>
+template <bool LOGIT, typename IssueCopies>
 PF_INLINE void pf_tile(f32x16 (&cur)[2], f32x16 (&nxt)[2], bf16x8 (&pop)[4], PfState &st,
                        const uint8_t *k_next, const uint8_t *v_cur, const PfAddr &ad,
-                       bool masked, int k1, int lane, IssueCopies &&issue_copies) {
+                       bool masked, int k1, int lane, const PfLogit &lg, IssueCopies &&issue_copies) {
     pf_qk(nxt, st, k_next, ad);
     pf_exp(pop, cur);
     pf_block_schedule<3>();
@@ -357,6 +433,7 @@ PF_INLINE void pf_tile(f32x16 (&cur)[2], f32x16 (&nxt)[2], bf16x8 (&pop)[4], PfS
     // P(t) is used only after the branch below: pin its computation to block 1
 #pragma unroll
     for (int i = 0; i < 4; ++i) asm volatile("" ::"v"(pop[i]));
+    if (LOGIT) pf_logit(nxt, lg, k1, lane);
     if (masked) pf_mask(nxt, st, k1, lane);
     issue_copies();
     pf_pv(st, pop, v_cur, ad);
@@ -380,6 +457,8 @@ PF_INLINE void pf_last_tile(const f32x16 (&cur)[2], bf16x8 (&pop)[4], PfState &s
 }
 
 // Two wavefronts per SIMD (8 per workgroup, ~240 registers each).
+// LOGIT: soft-capping and / or ALiBi (a separate instantiation keeps them off the plain path)
+template <bool LOGIT>
 __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a) {
     // the K and V^T rings: four stages each, as distinct arrays named statically below, so the
     // compiler can tell the asynchronous copy into one stage from the reads of another (a
@@ -411,19 +490,22 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     const int head = hk * a.group + hgrp * a.heads_per_wg + hslot;
     const bool wave_live = hslot < a.heads_per_wg;
     const int q0 = qb * kPfBQ;
+    const PfSeq sq = pf_sequence(a, b);
+    const int lq = sq.lq, lk = sq.lk;
+    if (q0 >= lq) return;  // a shorter sequence of a variable-length batch: the whole workgroup
 
     int lo_first, hi_first, lo_last, hi_last;
-    pf_key_range(q0, a.q_len, a.kv_len, a.wl, a.wr, lo_first, hi_first);
-    pf_key_range(min(q0 + kPfBQ, a.q_len) - 1, a.q_len, a.kv_len, a.wl, a.wr, lo_last, hi_last);
+    pf_key_range(q0, lq, lk, a.wl, a.wr, lo_first, hi_first);
+    pf_key_range(min(q0 + kPfBQ, lq) - 1, lq, lk, a.wl, a.wr, lo_last, hi_last);
     const int kt_begin = lo_first / kPfBK;
     const int ntiles = (hi_last + kPfBK - 1) / kPfBK - kt_begin;
 
     PfState st;
     {
         const int qi = q0 + 32 * qhalf + qr;
-        const bool ok = wave_live && qi < a.q_len;
-        const uint16_t *row = a.q + (int64_t)b * a.q_sb + (int64_t)min(head, a.q_heads - 1) * a.q_sh +
-                              (int64_t)min(qi, a.q_len - 1) * a.q_st;
+        const bool ok = wave_live && qi < lq;
+        const uint16_t *row = a.q + sq.q0 + (int64_t)min(head, a.q_heads - 1) * a.q_sh +
+                              (int64_t)min(qi, lq - 1) * a.q_st;
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
             u32x4 w = ok ? ldg128(row + 16 * ks + 8 * h) : u32x4{0u, 0u, 0u, 0u};
@@ -434,7 +516,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
                                    __uint_as_float(w[e] & 0xffff0000u) * a.scale_log2);
             st.qop[ks] = __builtin_bit_cast(bf16x8, w);
         }
-        if (qi < a.q_len) pf_key_range(qi, a.q_len, a.kv_len, a.wl, a.wr, st.qlo, st.qhi);
+        if (qi < lq) pf_key_range(qi, lq, lk, a.wl, a.wr, st.qlo, st.qhi);
         else st.qlo = st.qhi = 0;
         st.m_run = -__builtin_inff();
         st.thr = -__builtin_inff();
@@ -444,8 +526,15 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
         for (int md = 0; md < 4; ++md) st.acc[md] = f32x16{};
     }
 
-    const uint16_t *kplane = a.k + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh;
+    const uint16_t *kplane = a.k + sq.k0 + (int64_t)hk * a.k_sh;
     const uint16_t *vtplane = a.vt + ((int64_t)b * a.kv_heads + hk) * kPfD * a.vt_len;
+    PfLogit lg = {};
+    if (LOGIT) {
+        lg.cap2 = a.softcap2;
+        lg.e2 = a.softcap2 > 0.0f ? 2.0f * kLog2e / a.softcap2 : 0.0f;
+        lg.slope2 = a.alibi && wave_live ? a.alibi[(int64_t)b * a.alibi_bs + head] * kLog2e : 0.0f;
+        lg.pos = q0 + 32 * qhalf + qr + lk - lq;
+    }
     PF_WAIT_VMCNT(0);  // the Q loads above must not be counted by the copy waits below
 
     // Tile t lives in stage t % 4 of both rings. Its copies are issued in step t - 3, after
@@ -462,7 +551,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     // wavefront always has the copies of exactly the next two tiles in flight at a barrier.
 #define PF_ISSUE(k, t)                                                                       \
     pf_issue_tile(PF_KS(k), PF_VS(k), kplane, vtplane, a.k_st, a.vt_len, koff, voff,         \
-                  kt_begin + (t), a.kv_len, wave, (t) < ntiles)
+                  kt_begin + (t), lk, wave, (t) < ntiles)
     PF_ISSUE(0, 0);
     PF_ISSUE(1, 1);
     PF_ISSUE(2, 2);
@@ -497,6 +586,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     pf_addr_init(ad, lane);
     if (ntiles > 0) {
         pf_qk(sa, st, ks0, ad);
+        if (LOGIT) pf_logit(sa, lg, kt_begin * kPfBK, lane);
         pf_shift(sa, st.negm);
         if (tile_masked(0)) pf_mask(sa, st, kt_begin * kPfBK, lane);
         const float mx = pf_max_halves(pf_rowmax(sa));
@@ -514,8 +604,8 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
             last = k;                                                                        \
             break;                                                                           \
         }                                                                                    \
-        pf_tile(CUR, NXT, pop, st, PF_KS(((k) + 1) & 3), PF_VS(k), ad, tile_masked(t + 1),   \
-                (kt_begin + t + 1) * kPfBK, lane, [&] {                                      \
+        pf_tile<LOGIT>(CUR, NXT, pop, st, PF_KS(((k) + 1) & 3), PF_VS(k), ad,                \
+                       tile_masked(t + 1), (kt_begin + t + 1) * kPfBK, lane, lg, [&] {       \
                     PF_ISSUE(((k) + 3) & 3, t + 3);                                          \
                 });                                                                          \
         ++t;                                                                                 \
@@ -547,8 +637,8 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     const float l = pf_sum_halves(st.l_run);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     const int qi = q0 + 32 * qhalf + qr;
-    if (qi >= a.q_len) return;
-    uint16_t *orow = a.out + (int64_t)b * a.o_sb + (int64_t)qi * a.o_st + (int64_t)head * a.o_sh;
+    if (qi >= lq) return;
+    uint16_t *orow = a.out + sq.o0 + (int64_t)qi * a.o_st + (int64_t)head * a.o_sh;
 #pragma unroll
     for (int md = 0; md < 4; ++md)
 #pragma unroll
@@ -578,18 +668,20 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
     __shared__ float vscale[kPfBK], vrcp[kPfBK];
     const int kt = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x;
-    const uint16_t *vplane = a.v + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
-    const uint16_t *kplane = a.k + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh;
+    const PfSeq sq = pf_sequence(a, b);
+    const int kv_len = sq.lk;  // this sequence's keys (the V^T row is zero-filled past them)
+    const uint16_t *vplane = a.v + sq.v0 + (int64_t)hk * a.v_sh;
+    const uint16_t *kplane = a.k + sq.k0 + (int64_t)hk * a.k_sh;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int id = tid + 256 * i, row = id >> 4, c = id & 15;
         const int key = kt * kPfBK + row;
         u32x4 w = {0u, 0u, 0u, 0u};
-        if (key < a.kv_len) w = *(const u32x4 *)(vplane + (int64_t)key * a.v_st + 8 * c);
+        if (key < kv_len) w = *(const u32x4 *)(vplane + (int64_t)key * a.v_st + 8 * c);
         *(u32x4 *)&vtile[row * kStRow + 4 * c] = w;
         if (a.append) {
             u32x4 wk = {0u, 0u, 0u, 0u};
-            if (key < a.kv_len) wk = *(const u32x4 *)(kplane + (int64_t)key * a.k_st + 8 * c);
+            if (key < kv_len) wk = *(const u32x4 *)(kplane + (int64_t)key * a.k_st + 8 * c);
             *(u32x4 *)&ktile[row * kStRow + 4 * c] = wk;
         }
     }
@@ -614,7 +706,7 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
     const int64_t plane = (int64_t)b * a.kv_heads + hk;
     // ---- per-token scales: 4 threads per token, 32 head dims each ----
     const int r = tid >> 2, qd = tid & 3, t = kt * kPfBK + r;
-    const bool live = t < a.kv_len;
+    const bool live = t < kv_len;
     float kmax = 0.0f, vmax = 0.0f;
 #pragma unroll
     for (int w = 0; w < 16; ++w) {
@@ -658,12 +750,12 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
         const int g = (tid >> 6) + 4 * gi, t0 = kt * kPfBK + 8 * g;
-        if (t0 >= a.kv_len) continue;
+        if (t0 >= kv_len) continue;
         uint64_t vw0 = 0, vw1 = 0;
         uint32_t mask = 0;
 #pragma unroll
         for (int sl = 0; sl < 8; ++sl) {
-            if (t0 + sl < a.kv_len) {
+            if (t0 + sl < kv_len) {
                 const uint32_t x = vtile[(8 * g + sl) * kStRow + dp];
                 const float sc = vscale[8 * g + sl], rc = vrcp[8 * g + sl];
                 const uint32_t c01 = fp8_row_codes(bf16_lo(x), bf16_hi(x), sc, rc);
@@ -693,14 +785,17 @@ int quant_append_launch(const cqkv_side *side, const void *x, int32_t x_dtype,
 
 using namespace cqkv;
 
-extern "C" int cqkv_flash_attn(const void *q, const int64_t q_strides[3], const void *k,
-                               const int64_t k_strides[3], const void *v,
-                               const int64_t v_strides[3], void *out,
-                               const int64_t out_strides[3], int32_t batch, int32_t q_len,
-                               int32_t kv_len, int32_t q_heads, int32_t kv_heads,
-                               int32_t head_dim, float softmax_scale, int32_t window_left,
-                               int32_t window_right, const cqkv_side *k_cache,
-                               const cqkv_side *v_cache, int32_t position, cqkv_stream_t stream) {
+extern "C" int cqkv_flash_attn_ext(const void *q, const int64_t q_strides[3], const void *k,
+                                   const int64_t k_strides[3], const void *v,
+                                   const int64_t v_strides[3], void *out,
+                                   const int64_t out_strides[3], int32_t batch, int32_t q_len,
+                                   int32_t kv_len, int32_t q_heads, int32_t kv_heads,
+                                   int32_t head_dim, float softmax_scale, int32_t window_left,
+                                   int32_t window_right, float softcap, const float *alibi_slopes,
+                                   int32_t alibi_batch_stride, const int32_t *cu_seqlens_q,
+                                   const int32_t *cu_seqlens_k, int32_t total_q, int32_t total_k,
+                                   const cqkv_side *k_cache, const cqkv_side *v_cache,
+                                   int32_t position, cqkv_stream_t stream) {
     clear_error();
     if (!q || !k || !v || !out || !q_strides || !k_strides || !v_strides || !out_strides)
         return fail(CQKV_ERR_ARG, "cqkv_flash_attn: null tensor or strides");
@@ -712,6 +807,20 @@ extern "C" int cqkv_flash_attn(const void *q, const int64_t q_strides[3], const 
                     batch, q_len, kv_len, q_heads, kv_heads);
     if ((k_cache == nullptr) != (v_cache == nullptr))
         return fail(CQKV_ERR_ARG, "cqkv_flash_attn: give both cache sides or neither");
+    if (!(softcap >= 0.0f) || softcap == __builtin_inff())
+        return fail(CQKV_ERR_ARG, "cqkv_flash_attn: softcap %g (finite, >= 0; 0 disables it)",
+                    (double)softcap);
+    if (alibi_slopes && alibi_batch_stride != 0 && alibi_batch_stride != q_heads)
+        return fail(CQKV_ERR_ARG, "cqkv_flash_attn: alibi slopes must be (%d) or (%d, %d) (batch stride %d)",
+                    q_heads, batch, q_heads, alibi_batch_stride);
+    const bool varlen = cu_seqlens_q != nullptr;
+    if ((cu_seqlens_k != nullptr) != varlen)
+        return fail(CQKV_ERR_ARG, "cqkv_flash_attn: give both cu_seqlens_q and cu_seqlens_k or neither");
+    if (varlen && (total_q <= 0 || total_k <= 0))
+        return fail(CQKV_ERR_ARG, "cqkv_flash_attn: variable-length rows total_q %d total_k %d",
+                    total_q, total_k);
+    if (varlen && k_cache)
+        return fail(CQKV_ERR_ARG, "cqkv_flash_attn: the fused cache append takes dense batches only");
     // 32-bit byte offsets inside a key tile (64 token rows) and inside a V^T plane
     if (k_strides && (k_strides[1] <= 0 || k_strides[1] >= (1 << 25)))
         return fail(CQKV_ERR_ARG, "cqkv_flash_attn: key token stride %lld outside [1, 2^25)",
@@ -763,6 +872,13 @@ extern "C" int cqkv_flash_attn(const void *q, const int64_t q_strides[3], const 
     a.wr = window_right;
     a.scale_log2 = softmax_scale * kLog2e;
     a.batch = batch;
+    a.softcap2 = softcap * kLog2e;
+    a.alibi = alibi_slopes;
+    a.alibi_bs = alibi_batch_stride;
+    a.cu_q = cu_seqlens_q;
+    a.cu_k = cu_seqlens_k;
+    a.total_q = total_q;
+    a.total_k = total_k;
     // V^T scratch (stream-ordered: freed after the launches that use it)
     a.vt_len = (kv_len + kPfBK - 1) / kPfBK * kPfBK;
     void *vt = nullptr;
@@ -787,7 +903,10 @@ extern "C" int cqkv_flash_attn(const void *q, const int64_t q_strides[3], const 
     hipLaunchKernelGGL(prefill_stage_kernel, dim3(a.vt_len / kPfBK, kv_heads, batch), dim3(256),
                        0, st, a);
     const dim3 grid(a.q_blocks * kv_heads * (a.group / a.heads_per_wg) * batch);
-    hipLaunchKernelGGL(prefill_kernel, grid, dim3(kPfWaves * 64), 0, st, a);
+    if (softcap > 0.0f || alibi_slopes)
+        hipLaunchKernelGGL(prefill_kernel<true>, grid, dim3(kPfWaves * 64), 0, st, a);
+    else
+        hipLaunchKernelGGL(prefill_kernel<false>, grid, dim3(kPfWaves * 64), 0, st, a);
     hipError_t le = hipGetLastError();
     hipError_t fe = hipFreeAsync(vt, st);
     if (le != hipSuccess) return fail(CQKV_ERR_HIP, "cqkv_flash_attn: launch: %s", hipGetErrorString(le));
@@ -802,4 +921,18 @@ extern "C" int cqkv_flash_attn(const void *q, const int64_t q_strides[3], const 
             return rc;
     }
     return CQKV_OK;
+}
+
+extern "C" int cqkv_flash_attn(const void *q, const int64_t q_strides[3], const void *k,
+                               const int64_t k_strides[3], const void *v,
+                               const int64_t v_strides[3], void *out,
+                               const int64_t out_strides[3], int32_t batch, int32_t q_len,
+                               int32_t kv_len, int32_t q_heads, int32_t kv_heads,
+                               int32_t head_dim, float softmax_scale, int32_t window_left,
+                               int32_t window_right, const cqkv_side *k_cache,
+                               const cqkv_side *v_cache, int32_t position, cqkv_stream_t stream) {
+    return cqkv_flash_attn_ext(q, q_strides, k, k_strides, v, v_strides, out, out_strides, batch,
+                               q_len, kv_len, q_heads, kv_heads, head_dim, softmax_scale,
+                               window_left, window_right, 0.0f, nullptr, 0, nullptr, nullptr, 0, 0,
+                               k_cache, v_cache, position, stream);
 }

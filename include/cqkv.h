@@ -23,6 +23,10 @@
  *                           candle-nn/src/turbo_quant.rs:1082-1114 attention_packed_blocks)
  *   cqkv_flash_attn        RocmStorage::flash_attn (candle-core/src/rocm_backend/accel.rs:54-158),
  *                          behind candle_flash_attn::flash_attn (candle-flash-attn/src/lib.rs:149)
+ *   cqkv_flash_attn_ext    the same with soft-capping, ALiBi and variable-length batches:
+ *                          flash_attn_alibi_windowed_softcap / flash_attn_varlen*
+ *                          (candle-flash-attn/src/lib.rs:41-511; FlashAttnParams.softcap,
+ *                          FaExtra.alibi, cu_seqlens in candle-core/src/accel/attention.rs)
  *   cqkv_rows_import /     the reference's packed row layout [codes][aux][rsc0][rsc1]
  *   cqkv_rows_export       (candle-core/src/accel/formats.rs:206-242)
  *
@@ -158,6 +162,27 @@ int cqkv_flash_attn(const void *q, const int64_t q_strides[3], const void *k,
                     float softmax_scale, int32_t window_left, int32_t window_right,
                     const cqkv_side *k_cache, const cqkv_side *v_cache, int32_t position,
                     cqkv_stream_t stream);
+
+/* cqkv_flash_attn plus the reference's optional score terms and variable-length batches
+ * (fa_logit, candle-core/kernels/flash_attn_impl.h:42-47; fa_tile_impl :330-443):
+ *   softcap > 0: score = softcap * tanh(score / softcap) (0 disables it);
+ *   alibi_slopes (device f32, NULL: none): score -= slope * |pos - key| with slope =
+ *     alibi_slopes[b * alibi_batch_stride + head], stride 0 (slopes per head) or q_heads;
+ *   cu_seqlens_q / cu_seqlens_k (device int32, batch + 1 prefix sums, NULL: dense): q / out are
+ *     (total_q, q_heads, D) and k / v (total_k, kv_heads, D) with element strides
+ *     {unused, token, head}; sequence b is rows cu[b] .. cu[b + 1] - 1; q_len / kv_len are the
+ *     maximum sequence lengths. Offsets are clamped into the totals and lengths to the maxima.
+ *     No fused cache append with variable-length batches.
+ * Soft-capping precedes ALiBi, and masked keys stay masked, as in the reference. */
+int cqkv_flash_attn_ext(const void *q, const int64_t q_strides[3], const void *k,
+                        const int64_t k_strides[3], const void *v, const int64_t v_strides[3],
+                        void *out, const int64_t out_strides[3], int32_t batch, int32_t q_len,
+                        int32_t kv_len, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                        float softmax_scale, int32_t window_left, int32_t window_right,
+                        float softcap, const float *alibi_slopes, int32_t alibi_batch_stride,
+                        const int32_t *cu_seqlens_q, const int32_t *cu_seqlens_k,
+                        int32_t total_q, int32_t total_k, const cqkv_side *k_cache,
+                        const cqkv_side *v_cache, int32_t position, cqkv_stream_t stream);
 
 /* Reference row layout interop (candle-core/src/accel/formats.rs:206-242): rows are
  * (batch, kv_heads, tokens, row_words) u32 on the device, row_words = code + aux + 2 words.

@@ -58,6 +58,28 @@ def attn_case():
     print("attn", out.shape)
 
 
+def fa_case():
+    # soft-capping, per-(batch, head) ALiBi slopes and a window through the reference's tile
+    # kernel, dense and variable-length (the score terms of candle-flash-attn's *_softcap / *_alibi
+    # / *_varlen entry points)
+    B, Lq, Lk, Hq, Hkv, D = 2, 37, 53, 4, 2, 32
+    q = O.normal(301, (B, Lq, Hq, D))
+    k = O.normal(302, (B, Lk, Hkv, D))
+    v = O.normal(303, (B, Lk, Hkv, D))
+    slopes = (0.05 * (1 + np.arange(B * Hq))).astype(np.float32).reshape(B, Hq)
+    dense = H.fa(q, k, v, 0.3, softcap=2.5, wl=20, wr=2, alibi=slopes, alibi_bs=Hq)
+    cu_q = np.array([0, 9, 9, 40], dtype=np.uint32)  # an empty second sequence
+    cu_k = np.array([0, 14, 20, 61], dtype=np.uint32)
+    qv = O.normal(304, (int(cu_q[-1]), Hq, D))
+    kv = O.normal(305, (int(cu_k[-1]), Hkv, D))
+    vv = O.normal(306, (int(cu_k[-1]), Hkv, D))
+    var = H.fa(qv, kv, vv, 0.25, softcap=4.0, wr=0, alibi=slopes[0], cu_q=cu_q, cu_k=cu_k,
+               max_q=31, max_k=41)
+    np.savez_compressed(os.path.join(HERE, "ref_fa_terms.npz"), q=q, k=k, v=v, slopes=slopes,
+                        dense=dense, cu_q=cu_q, cu_k=cu_k, qv=qv, kv=kv, vv=vv, var=var)
+    print("fa", dense.shape, var.shape)
+
+
 def combine_case():
     splits, rows, d = 5, 7, 32
     po = O.normal(201, (splits, rows, d))
@@ -78,5 +100,6 @@ if __name__ == "__main__":
     quant_case("mxfp4_d64", O.MXFP4, 0, 64, 19, 14)
     quant_case("turbo4_d128", O.TURBO_MSE, 4, 128, 37, 15)
     quant_case("nvfp4_d128", O.NVFP4, 0, 128, 11, 16)
+    fa_case()
     attn_case()
     combine_case()

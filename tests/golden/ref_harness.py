@@ -110,3 +110,38 @@ def combine(part_o: np.ndarray, part_lse: np.ndarray) -> np.ndarray:
                "part_lse": part_lse.astype(np.float32),
                "params": np.array([rows, d, splits], dtype=np.uint32)})
     return out["t"].reshape(rows, d)
+
+
+def fa(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, softcap: float = 0.0,
+       wl: int = -1, wr: int = -1, alibi: np.ndarray | None = None, alibi_bs: int = 0,
+       cu_q: np.ndarray | None = None, cu_k: np.ndarray | None = None,
+       max_q: int = 0, max_k: int = 0) -> np.ndarray:
+    """Reference `fa_tile_impl` (FA3 tiles, f32 q / k / v; flash_attn_impl.h:330-443).
+    Dense: q (B, Lq, Hq, D), k / v (B, Lk, Hkv, D) -> (B, Lq, Hq, D). Variable length
+    (cu_q / cu_k given): q (total_q, Hq, D), k / v (total_k, Hkv, D) -> (total_q, Hq, D), with
+    max_q / max_k as Lq / Lk. Slopes alibi[b * alibi_bs + h]."""
+    varlen = cu_q is not None
+    if varlen:
+        total_q, Hq, D = q.shape
+        _, Hkv, _ = k.shape
+        B, Lq, Lk = len(cu_q) - 1, max_q, max_k
+        st = [0, Hq * D, D, 0, Hkv * D, D, 0, Hkv * D, D]
+    else:
+        B, Lq, Hq, D = q.shape
+        _, Lk, Hkv, _ = k.shape
+        total_q = B * Lq
+        st = [Lq * Hq * D, Hq * D, D, Lk * Hkv * D, Hkv * D, D, Lk * Hkv * D, Hkv * D, D]
+    dmax = 64 if D <= 64 else 128
+    arrays = {"op": "fa", "dtypes": np.array([0, 0], dtype=np.uint32),
+              "dims": np.array([B, Lq, Lk, Hq, Hkv, D, total_q], dtype=np.uint32),
+              "strides": np.array(st, dtype=np.uint64),
+              "fparams": np.array([scale, softcap, 1.0, 1.0], dtype=np.float32),
+              "iparams": np.array([wl, wr], dtype=np.int32),
+              "cfg": np.array([1, dmax, 3, 1, int(varlen), 3, alibi_bs], dtype=np.uint32),
+              "q": q.astype(np.float32), "k": k.astype(np.float32), "v": v.astype(np.float32)}
+    if alibi is not None:
+        arrays["alibi"] = np.ascontiguousarray(alibi, dtype=np.float32)
+    if varlen:
+        arrays["cu_q"] = np.ascontiguousarray(cu_q, dtype=np.uint32)
+        arrays["cu_k"] = np.ascontiguousarray(cu_k, dtype=np.uint32)
+    return run(arrays)["o"].reshape(q.shape)

@@ -109,6 +109,33 @@ def test_argument_errors_are_status_codes(cq):
     assert b"capacity" in L.cqkv_last_error()
 
 
+def test_flash_attn_ext_argument_errors(cq):
+    """Soft-capping, ALiBi and variable-length arguments are checked before any launch."""
+    L = cq.lib()
+    x = (ctypes.c_int64 * 3)(1, 128, 128)
+    one = ctypes.c_void_p(1)
+
+    def call(softcap=0.0, alibi=None, alibi_bs=0, cu_q=None, cu_k=None, tq=0, tk=0, kc=None,
+             vc=None, hq=8, batch=2):
+        return L.cqkv_flash_attn_ext(one, x, one, x, one, x, one, x, batch, 16, 16, hq, 2, 128,
+                                     0.1, -1, 0, softcap, alibi, alibi_bs, cu_q, cu_k, tq, tk,
+                                     kc, vc, 0, None)
+    assert call(softcap=-1.0) == cq.ERR_ARG
+    assert b"softcap" in L.cqkv_last_error()
+    assert call(softcap=float("nan")) == cq.ERR_ARG
+    assert call(alibi=one, alibi_bs=3) == cq.ERR_ARG
+    assert b"alibi slopes" in L.cqkv_last_error()
+    assert call(cu_q=one) == cq.ERR_ARG
+    assert b"cu_seqlens" in L.cqkv_last_error()
+    assert call(cu_q=one, cu_k=one, tq=0, tk=5) == cq.ERR_ARG
+    assert b"total_q" in L.cqkv_last_error()
+    side = cq.Side(cq.FP8, 0, 128, 2, 64, 0, 0, 1, 1)
+    vside = cq.Side(cq.FP8, 1, 128, 2, 64, 0, 0, 1, 1)
+    assert call(cu_q=one, cu_k=one, tq=5, tk=5, kc=ctypes.byref(side),
+                vc=ctypes.byref(vside)) == cq.ERR_ARG
+    assert b"dense batches only" in L.cqkv_last_error()
+
+
 def test_paged_argument_errors_and_workspace(cq):
     """cqkv_decode_attention_paged validates its blocks like the reference's check_blocks
     (candle-nn/src/flash_attn.rs:650-686) before any launch, and sizes its scratch."""

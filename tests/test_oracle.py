@@ -332,7 +332,9 @@ def test_key_ranges():
     assert O.key_range(0, 4, 2, -1, 0) == (0, 0)
 
 
-def attention_f64(q, k, v, scale, wl=-1, wr=-1, kv_lens=None):
+def attention_f64(q, k, v, scale, wl=-1, wr=-1, kv_lens=None, softcap=0.0, alibi=None):
+    """Brute-force float64 attention; softcap and per-head ALiBi slopes as fa_logit
+    (candle-core/kernels/flash_attn_impl.h:42-47): cap * tanh(s / cap), then - slope * |pos - j|."""
     b, hq, lq, d = q.shape
     hkv = k.shape[1]
     g = hq // hkv
@@ -350,6 +352,10 @@ def attention_f64(q, k, v, scale, wl=-1, wr=-1, kv_lens=None):
                 if lo >= hi:
                     continue
                 s = kk[lo:hi] @ q[bi, h, i].astype(np.float64) * scale
+                if softcap > 0:
+                    s = softcap * np.tanh(s / softcap)
+                if alibi is not None:
+                    s = s - float(alibi[h]) * np.abs(pos - np.arange(lo, hi))
                 p = np.exp(s - s.max())
                 out[bi, h, i] = p @ vv[lo:hi] / p.sum()
     return out
@@ -371,6 +377,59 @@ def test_attention_ragged_lengths_vs_float64():
     lens = np.array([40, 1, 17], dtype=np.int32)
     got = O.attention_unfused(q, k, v, 0.25, kv_lens=lens)
     np.testing.assert_allclose(got, attention_f64(q, k, v, 0.25, kv_lens=lens), atol=2e-6)
+
+
+@pytest.mark.parametrize("wl,wr", [(-1, -1), (-1, 0), (4, 1)])
+def test_attention_softcap_alibi_vs_float64(wl, wr):
+    q = O.normal(21, (2, 4, 6, 32)) * np.float32(2.0)
+    k = O.normal(22, (2, 2, 11, 32))
+    v = O.normal(23, (2, 2, 11, 32))
+    slopes = np.array([0.0, 0.1, 0.35, 1.5], dtype=np.float32)
+    got = O.attention_unfused(q, k, v, 0.4, softcap=3.0, wl=wl, wr=wr, alibi=slopes)
+    want = attention_f64(q, k, v, 0.4, wl, wr, softcap=3.0, alibi=slopes)
+    np.testing.assert_allclose(got, want, atol=2e-6)
+    # a cap far above every score leaves the scores alone; zero slopes add nothing
+    big = O.attention_unfused(q, k, v, 0.4, softcap=1e6, wl=wl, wr=wr, alibi=np.zeros(4, np.float32))
+    np.testing.assert_allclose(big, O.attention_unfused(q, k, v, 0.4, wl=wl, wr=wr), atol=1e-6)
+
+
+def oracle_fa_dense(q, k, v, scale, softcap, wl, wr, slopes_bh):
+    """The oracle over (B, L, H, D) tensors with per-(batch, head) slopes, one sequence at a
+    time (the oracle takes per-head slopes)."""
+    out = np.zeros_like(q)
+    for bi in range(q.shape[0]):
+        qb = q[bi:bi + 1].transpose(0, 2, 1, 3)
+        kb = k[bi:bi + 1].transpose(0, 2, 1, 3)
+        vb = v[bi:bi + 1].transpose(0, 2, 1, 3)
+        al = None if slopes_bh is None else slopes_bh[bi]
+        o = O.attention_unfused(qb, kb, vb, scale, softcap=softcap, wl=wl, wr=wr, alibi=al)
+        out[bi] = o[0].transpose(1, 0, 2)
+    return out
+
+
+def oracle_fa_varlen(q, k, v, cu_q, cu_k, scale, softcap, wl, wr, slopes):
+    """The oracle over packed (total, H, D) sequences, one sequence at a time (the reference's
+    own varlen invariant, candle-flash-attn/tests/api.rs:86-140)."""
+    out = np.zeros_like(q)
+    for bi in range(len(cu_q) - 1):
+        qs, qe, ks, ke = int(cu_q[bi]), int(cu_q[bi + 1]), int(cu_k[bi]), int(cu_k[bi + 1])
+        if qe == qs:
+            continue
+        o = oracle_fa_dense(q[None, qs:qe], k[None, ks:ke], v[None, ks:ke], scale, softcap, wl,
+                            wr, None if slopes is None else slopes[None])
+        out[qs:qe] = o[0]
+    return out
+
+
+def test_attention_terms_vs_reference_tile_kernel_fixture():
+    # soft-capping, per-(batch, head) ALiBi, windows and variable-length batches through the
+    # reference's fa_tile_impl (tests/golden/make_vectors.py fa_case)
+    g = gold("ref_fa_terms")
+    dense = oracle_fa_dense(g["q"], g["k"], g["v"], 0.3, 2.5, 20, 2, g["slopes"])
+    np.testing.assert_allclose(dense, g["dense"], atol=2e-5)
+    var = oracle_fa_varlen(g["qv"], g["kv"], g["vv"], g["cu_q"], g["cu_k"], 0.25, 4.0, -1, 0,
+                           g["slopes"][0])
+    np.testing.assert_allclose(var, g["var"], atol=2e-5)
 
 
 def test_attention_vs_reference_tq_attn_fixture():
@@ -445,6 +504,17 @@ def test_turbo_cache_roundtrip_error_bound():
     back = O.unrotate_rows(pi, O.dequantize_rows(O.TURBO_MSE, 4, d, rows))
     rel = ((back.astype(np.float64) - x) ** 2).sum() / (x.astype(np.float64) ** 2).sum()
     assert rel < 0.012
+
+
+@pytest.mark.skipif(not H.available(), reason="reference harness not built (make -C oracle ref)")
+@pytest.mark.parametrize("softcap,wl,wr", [(0.0, -1, 0), (1.5, -1, -1), (6.0, 9, 0)])
+def test_live_reference_harness_fa_terms(softcap, wl, wr):
+    q = O.normal(401, (2, 19, 4, 64)) * np.float32(1.5)
+    k = O.normal(402, (2, 27, 1, 64))
+    v = O.normal(403, (2, 27, 1, 64))
+    slopes = np.array([[0.0, 0.2, 0.5, 1.0], [0.01, 0.02, 0.04, 0.08]], dtype=np.float32)
+    want = H.fa(q, k, v, 0.2, softcap=softcap, wl=wl, wr=wr, alibi=slopes, alibi_bs=4)
+    np.testing.assert_allclose(oracle_fa_dense(q, k, v, 0.2, softcap, wl, wr, slopes), want, atol=2e-5)
 
 
 @pytest.mark.skipif(not H.available(), reason="reference harness not built (make -C oracle ref)")
