@@ -19,10 +19,11 @@ host on a bounded sample of the same workload.
 
 "other_configs" reports BASELINE configs 3 (MXFP4, ragged), 4 (causal bf16 prefill with fused
 FP8 append) and 5 (TurboQuant-4, context 128K) with the same timing method; they are secondary
-figures, not the headline value.
+figures, not the headline value. "ra_*" time the fused RoPE + FP8 quantize-append at the
+config-4 prefill shape and at one config-2 decode step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
-                       [--only c2,c3,c4,c5] [--calibration-copy]
+                       [--only c2,c3,c4,c5,ra] [--calibration-copy]
 """
 from __future__ import annotations
 
@@ -179,6 +180,34 @@ def prefill_case(cq, dev, stream, steps, warmup):
             "timed": "whole call: pre-pass (V transpose + fused FP8 K/V append) + prefill kernel"}
 
 
+def rope_append_case(cq, dev, stream, fmt, b, hq, hkv, d, t, cap, steps, warmup):
+    """Fused RoPE + quantize-append from a (b, t, (hq + 2 hkv) d) bf16 QKV projection output:
+    rotated q written out (bf16), K rotated and V quantized into the cache at position 0."""
+    import torch
+    qkv = kv_gpu((b, t, 1, (hq + 2 * hkv) * d), 17, dev)[:, :, 0].contiguous()
+    q, k, v = cq.split_qkv(qkv, hq, hkv)
+    ang = torch.arange(cap, dtype=torch.float64, device=dev)[:, None] / \
+        10000.0 ** (torch.arange(0, d, 2, dtype=torch.float64, device=dev) / d)
+    cos, sin = ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
+    ks = cq.CacheSide.empty(fmt, False, b, hkv, d, cap, dev)
+    vs = cq.CacheSide.empty(fmt, True, b, hkv, d, cap, dev)
+    q_out = torch.empty(b, hq, t, d, dtype=torch.bfloat16, device=dev)
+
+    def step(i):
+        cq.rope_quant_append(ks, vs, q, k, v, cos, sin, cq.ROPE_HALVES, 0, q_out=q_out)
+    ms = time_calls(step, steps, warmup, stream)
+    rb = row_bytes(fmt, d)
+    nbytes = (qkv.numel() * 2 + 2 * t * (d // 2) * 2 + q_out.numel() * 2
+              + 2 * b * hkv * t * rb)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"workload": f"fused RoPE + {['TURBO4', '', 'MXFP4', '', '', 'FP8'][fmt]} append, "
+                        f"B={b} t={t} Hq={hq} Hkv={hkv} D={d}",
+            "us_per_call": round(ms * 1e3, 2), "bytes_per_call": nbytes,
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)},
+            "timed": "one cqkv_rope_quant_append launch"}
+
+
 def decode_summary(name, ms, nbytes, extra):
     gbs = nbytes / (ms * 1e-3) / 1e9
     res = {"workload": name, "us_per_call": round(ms * 1e3, 2), "bytes_per_call": nbytes,
@@ -207,7 +236,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
-    ap.add_argument("--only", default="", help="comma list of c2,c3,c4,c5 (default: all)")
+    ap.add_argument("--only", default="", help="comma list of c2,c3,c4,c5,ra (default: all)")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="also run a plain 1 GiB copy (for counter scaling)")
     args = ap.parse_args()
@@ -306,6 +335,16 @@ def main():
             {"batch": 8, "q_heads": 64, "kv_heads": 8, "head_dim": 128, "context": 131072,
              "timed": "whole call (split-K decode + combine with unrotation)"})
         log(f"config 5: {ms * 1e3:.2f} us/call")
+        torch.cuda.empty_cache()
+
+    if want("ra"):
+        log("fused RoPE + FP8 append: prefill shape (config 4) and one decode step (config 2)")
+        other["ra_prefill_c4"] = rope_append_case(cq, dev, stream, cq.FP8, 4, 32, 8, 128, 4096,
+                                                  4096, steps_x, warm_x)
+        other["ra_decode_step_c2"] = rope_append_case(cq, dev, stream, cq.FP8, 32, 32, 8, 128,
+                                                      1, 8192, steps_x, warm_x)
+        log(f"rope append: {other['ra_prefill_c4']['us_per_call']} us (prefill), "
+            f"{other['ra_decode_step_c2']['us_per_call']} us (decode step)")
         torch.cuda.empty_cache()
 
     if res is None:

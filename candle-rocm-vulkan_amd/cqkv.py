@@ -23,6 +23,8 @@ LIB_PATH = os.path.join(HERE, "libcqkv.so")
 TURBO4, MXFP4, FP8 = 0, 2, 5
 FORMAT_NAMES = {"fp8": FP8, "mxfp4": MXFP4, "turbo4": TURBO4}
 BF16, F16, F32 = 0, 1, 2
+# rotary layouts: rope (halves) and rope_i (interleaved) of candle-nn/src/rotary_emb.rs
+ROPE_HALVES, ROPE_INTERLEAVED = 1, 2
 _DTYPES = {torch.bfloat16: BF16, torch.float16: F16, torch.float32: F32}
 
 OK, ERR_ARG, ERR_HIP, ERR_WORKSPACE = 0, -1, -2, -3
@@ -66,6 +68,8 @@ def lib() -> ctypes.CDLL:
         L.cqkv_scales_plane_bytes.argtypes = [i32, i32, i32]
         L.cqkv_scales_plane_bytes.restype = sz
         L.cqkv_quant_append.argtypes = [SP, P, i32, I64P, i32, i32, P, i32, P]
+        L.cqkv_rope_quant_append.argtypes = [SP, SP, P, I64P, P, I64P, P, I64P, i32, i32, i32,
+                                             i32, P, P, i32, i32, P, i32, P, I64P, P]
         L.cqkv_decode_workspace_bytes.argtypes = [i32, i32, i32, i32, i32]
         L.cqkv_decode_workspace_bytes.restype = sz
         L.cqkv_decode_splits.argtypes = [i32, i32, i32, i32, i32]
@@ -95,6 +99,7 @@ def lib() -> ctypes.CDLL:
 
 
 EXPORTED = ["cqkv_codes_plane_bytes", "cqkv_scales_plane_bytes", "cqkv_quant_append",
+            "cqkv_rope_quant_append",
             "cqkv_decode_workspace_bytes", "cqkv_decode_splits", "cqkv_decode_attention",
             "cqkv_decode_paged_workspace_bytes", "cqkv_decode_attention_paged",
             "cqkv_flash_attn", "cqkv_flash_attn_ext", "cqkv_reference_row_words", "cqkv_rows_import",
@@ -175,6 +180,57 @@ def quant_append(side: CacheSide, x: torch.Tensor, position: int = 0,
     _check(lib().cqkv_quant_append(ctypes.byref(s), _ptr(x), _DTYPES[x.dtype],
                                    _strides3(x, (0, 1, 2)), b, t, _ptr(positions), position,
                                    _stream(x.device)))
+
+
+def rope_quant_append(k_side: CacheSide, v_side: CacheSide, q: torch.Tensor, k: torch.Tensor,
+                      v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                      kind: int = ROPE_HALVES, position: int = 0,
+                      positions: torch.Tensor | None = None,
+                      q_out: torch.Tensor | None = None) -> torch.Tensor:
+    """rope(q), rope(k) and TurboKvCache::append(k, v) in one launch.
+
+    q (batch, q_heads, tokens, D), k / v (batch, kv_heads, tokens, D), any strides with D
+    contiguous, one dtype; cos / sin (rows, D/2) contiguous tables of that dtype, row p holding
+    position p. Token i of batch b takes position `position` + i (or positions[b] + i). Returns
+    the rotated queries (q_out, or a new (batch, q_heads, tokens, D) tensor)."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (cos, "cos"), (sin, "sin")):
+        _need_gpu(t, n)
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4 or k.shape != v.shape:
+        raise CqkvError(ERR_ARG, "q / k / v must be 4-d and k, v of one shape")
+    if any(t.stride(3) != 1 for t in (q, k, v)):
+        raise CqkvError(ERR_ARG, "q / k / v need a contiguous head dim")
+    b, hq, t_, d = q.shape
+    if k.shape[0] != b or k.shape[2] != t_ or k.shape[3] != d:
+        raise CqkvError(ERR_ARG, f"q {tuple(q.shape)} and k {tuple(k.shape)} disagree")
+    if k.shape[1] != k_side.kv_heads or d != k_side.head_dim or b != k_side.batch:
+        raise CqkvError(ERR_ARG, f"k {tuple(k.shape)} does not match the cache side")
+    if len({q.dtype, k.dtype, v.dtype, cos.dtype, sin.dtype}) != 1 or q.dtype not in _DTYPES:
+        raise CqkvError(ERR_ARG, "q, k, v, cos and sin must share one float dtype")
+    if (cos.dim() != 2 or cos.shape != sin.shape or cos.shape[1] != d // 2
+            or not cos.is_contiguous() or not sin.is_contiguous()):
+        raise CqkvError(ERR_ARG, f"cos / sin must be contiguous (rows, {d // 2}) tables")
+    if q_out is None:
+        q_out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    elif q_out.shape != q.shape or q_out.dtype != q.dtype or q_out.stride(3) != 1:
+        raise CqkvError(ERR_ARG, "q_out must match q in shape and dtype, with a contiguous D")
+    ks, vs = k_side.struct(), v_side.struct()
+    _check(lib().cqkv_rope_quant_append(
+        ctypes.byref(ks), ctypes.byref(vs), _ptr(q), _strides3(q, (0, 1, 2)), _ptr(k),
+        _strides3(k, (0, 1, 2)), _ptr(v), _strides3(v, (0, 1, 2)), _DTYPES[q.dtype], b, t_, hq,
+        _ptr(cos), _ptr(sin), cos.shape[0], kind, _ptr(positions), position, _ptr(q_out),
+        _strides3(q_out, (0, 1, 2)), _stream(q.device)))
+    return q_out
+
+
+def split_qkv(qkv: torch.Tensor, q_heads: int, kv_heads: int):
+    """Views q (b, q_heads, t, D), k, v (b, kv_heads, t, D) of a QKV projection output
+    (b, t, (q_heads + 2 kv_heads) D), as the models reshape and transpose it."""
+    b, t, w = qkv.shape
+    d = w // (q_heads + 2 * kv_heads)
+    q = qkv[..., :q_heads * d].view(b, t, q_heads, d).transpose(1, 2)
+    k = qkv[..., q_heads * d:(q_heads + kv_heads) * d].view(b, t, kv_heads, d).transpose(1, 2)
+    v = qkv[..., (q_heads + kv_heads) * d:].view(b, t, kv_heads, d).transpose(1, 2)
+    return q, k, v
 
 
 def decode_workspace_bytes(batch, q_heads, q_len, head_dim, splits) -> int:
@@ -418,6 +474,17 @@ class TurboKvCache:
         quant_append(self.k, k, self._len)
         quant_append(self.v, v, self._len)
         self._len += t
+
+    def rope_append(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
+                    sin: torch.Tensor, kind: int = ROPE_HALVES) -> torch.Tensor:
+        """The model step rope(q), rope(k), append(k, v) in one launch, the new tokens taking
+        positions seq_len.. (their rows of cos / sin). Returns the rotated q."""
+        t = k.shape[2] if k.dim() == 4 else 0
+        if self._len + t > self.k.capacity:
+            raise CqkvError(ERR_ARG, f"cache full: {self._len} + {t} > {self.k.capacity}")
+        out = rope_quant_append(self.k, self.v, q, k, v, cos, sin, kind, self._len)
+        self._len += t
+        return out
 
     def attention(self, q: torch.Tensor, softmax_scale: float, window_left: int = -1,
                   window_right: int = -1, splits: int = 0) -> torch.Tensor:

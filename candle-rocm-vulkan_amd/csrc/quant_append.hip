@@ -29,25 +29,61 @@ struct AppendArgs {
     float rot_scale;        // TURBO4: 1 / sqrt(D) in f32
     float bnd[16];          // TURBO4: the 15 codebook boundaries (+inf padded)
     int32_t pair_loads;     // elements 2l, 2l+1 of every row are one aligned 4 / 8-byte word
+    const void *cos, *sin;  // rotary tables (cs_rows, D/2) in the dtype of x (fused RoPE only)
+    int32_t cs_rows;
+    int32_t cs_pair_loads;  // both tables aligned for paired loads
 };
 
-// elements idx, idx + 1 of x as floats (one load when `pair` says they form an aligned word)
+// Elements idx, idx + 1 of x in two steps: load_raw only issues the loads (one when `pair` says
+// they form an aligned word), raw_to_f32 converts. Batches of rows are loaded with load_raw
+// before any conversion, so no branch on dtype / pairing sits between a load and the next one
+// and the loads of a batch are in flight together.
+struct RawPair {
+    uint32_t w0, w1;
+};
+
+__device__ inline RawPair load_raw(const void *p, int64_t idx, int dtype, bool pair) {
+    RawPair r = {0u, 0u};
+    if (dtype == CQKV_F32) {
+        if (pair) {
+            const u32x2 w = *(const u32x2 *)((const float *)p + idx);
+            r.w0 = w.x;
+            r.w1 = w.y;
+        } else {
+            r.w0 = ((const uint32_t *)p)[idx];
+            r.w1 = ((const uint32_t *)p)[idx + 1];
+        }
+    } else if (pair) {
+        r.w0 = *(const uint32_t *)((const uint16_t *)p + idx);  // both halves
+    } else {
+        r.w0 = ((const uint16_t *)p)[idx];
+        r.w1 = ((const uint16_t *)p)[idx + 1];
+    }
+    return r;
+}
+
+__device__ inline void raw_to_f32(const RawPair &r, int dtype, bool pair, float &x0, float &x1) {
+    if (dtype == CQKV_F32) {
+        x0 = __uint_as_float(r.w0);
+        x1 = __uint_as_float(r.w1);
+        return;
+    }
+    const uint32_t lo = pair ? (r.w0 & 0xffffu) : r.w0, hi = pair ? (r.w0 >> 16) : r.w1;
+    x0 = dtype == CQKV_BF16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
+    x1 = dtype == CQKV_BF16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+}
+
 __device__ inline void load_pair(const void *p, int64_t idx, int dtype, bool pair, float &x0,
                                  float &x1) {
-    if (pair) {
-        if (dtype == 2) {
-            const f32x2 w = *(const f32x2 *)((const float *)p + idx);
-            x0 = w.x;
-            x1 = w.y;
-        } else {
-            const uint32_t w = *(const uint32_t *)((const uint16_t *)p + idx);
-            x0 = dtype == 0 ? bf16_bits_to_f32(w & 0xffffu) : f16_bits_to_f32(w & 0xffffu);
-            x1 = dtype == 0 ? bf16_bits_to_f32(w >> 16) : f16_bits_to_f32(w >> 16);
-        }
-    } else {
-        x0 = load_elem(p, idx, dtype);
-        x1 = load_elem(p, idx + 1, dtype);
-    }
+    raw_to_f32(load_raw(p, idx, dtype, pair), dtype, pair, x0, x1);
+}
+
+// W16: the launch guarantees a 16-bit dtype and pair-aligned rows (and tables), so every load is
+// one dword with no branch around it.
+template <bool W16>
+__device__ inline RawPair load_raw_t(const void *p, int64_t idx, int dtype, bool pair) {
+    if constexpr (W16) return RawPair{*(const uint32_t *)((const uint16_t *)p + idx), 0u};
+    else return load_raw(p, idx, dtype, pair);
 }
 
 // In-register Walsh-Hadamard transform over 2 * `lanes` elements held as (v0, v1) = elements
@@ -66,14 +102,82 @@ __device__ inline void fwht_pairs(float &v0, float &v1, int lane) {
     }
 }
 
-template <int FMT, int IS_VALUE, int D>
-__global__ __launch_bounds__(256) void quant_append_kernel(AppendArgs a) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int h = blockIdx.y, b = blockIdx.z;
+// Rotary embedding of the pair (x0, x1) = elements (2l, 2l+1) of a row at position `row` of the
+// cos / sin tables ((rows, D/2), dtype of x), then rounded to that dtype: the reference's rope
+// kernels (candle-core/kernels/nn.hip:107-148; candle-nn/src/rotary_emb.rs:585-611 `rope`,
+// :275-303 `rope_i`) write their output in the input dtype, and the cache quantizes that.
+//   CQKV_ROPE_HALVES:      y_i = x_i c_i - x_{i+D/2} s_i,  y_{i+D/2} = x_i s_i + x_{i+D/2} c_i
+//   CQKV_ROPE_INTERLEAVED: y_2i = x_2i c_i - x_2i+1 s_i,  y_2i+1 = x_2i s_i + x_2i+1 c_i
+// Products are rounded before the sum, as in the reference kernels (no fused multiply-add).
+// rope_load fetches a lane's table entries (issued ahead with the row loads); rope_apply is
+// called by every lane of the wave (the halves form exchanges pairs across lanes).
+struct RopeCS {
+    RawPair c, s;  // raw table words: interleaved one element each, halves a pair each
+};
+
+template <int D, int ROPE, bool W16>
+__device__ inline RopeCS rope_load(const void *cos, const void *sin, int dtype, bool pair,
+                                   int64_t row, int lane) {
+    RopeCS r;
+    if constexpr (ROPE == CQKV_ROPE_INTERLEAVED) {
+        const int64_t i = row * (D / 2) + lane;
+        if constexpr (W16) {
+            r.c = RawPair{((const uint16_t *)cos)[i], 0u};
+            r.s = RawPair{((const uint16_t *)sin)[i], 0u};
+        } else {
+            r.c = load_raw(cos, i, dtype, false);
+            r.s = load_raw(sin, i, dtype, false);
+        }
+    } else {
+        const int64_t i = row * (D / 2) + 2 * lane - (lane >= D / 4 ? D / 2 : 0);
+        r.c = load_raw_t<W16>(cos, i, dtype, pair);
+        r.s = load_raw_t<W16>(sin, i, dtype, pair);
+    }
+    return r;
+}
+
+template <int D, int ROPE>
+__device__ inline void rope_apply(float &x0, float &x1, const RopeCS &t, int dtype, bool pair,
+                                  int lane) {
+#pragma clang fp contract(off)
+    if constexpr (ROPE == CQKV_ROPE_INTERLEAVED) {
+        float c, s, unused;
+        raw_to_f32(RawPair{t.c.w0, t.c.w0}, dtype, false, c, unused);
+        raw_to_f32(RawPair{t.s.w0, t.s.w0}, dtype, false, s, unused);
+        const float y0 = x0 * c - x1 * s, y1 = x0 * s + x1 * c;
+        x0 = y0;
+        x1 = y1;
+    } else {
+        float c0, c1, s0, s1;
+        raw_to_f32(t.c, dtype, pair, c0, c1);
+        raw_to_f32(t.s, dtype, pair, s0, s1);
+        const float p0 = shfl_xor(x0, D / 4), p1 = shfl_xor(x1, D / 4);
+        if (lane < D / 4) {
+            x0 = x0 * c0 - p0 * s0;
+            x1 = x1 * c1 - p1 * s1;
+        } else {
+            x0 = p0 * s0 + x0 * c0;
+            x1 = p1 * s1 + x1 * c1;
+        }
+    }
+    if (dtype == CQKV_BF16) {
+        x0 = bf16_bits_to_f32(f32_to_bf16_bits(x0));
+        x1 = bf16_bits_to_f32(f32_to_bf16_bits(x1));
+    } else if (dtype == CQKV_F16) {
+        x0 = (float)(_Float16)x0;
+        x1 = (float)(_Float16)x1;
+    }
+}
+
+// One wave: the tokens of one 8-token cache tile of plane (b, h), bx / wave as in the grid of
+// quant_append_launch. ROPE != 0 rotates each row (position = its cache position) first.
+template <int FMT, int IS_VALUE, int D, int ROPE, bool W16>
+__device__ inline void append_tile(const AppendArgs &a, int h, int b, int bx, int wave, int lane) {
     const int pos = a.positions ? a.positions[b] : a.position;
-    const int tile = pos / 8 + (int)blockIdx.x * 4 + wave;
+    const int tile = pos / 8 + bx * 4 + wave;
     const int t_lo = max(tile * 8, pos);
-    const int t_hi = min(min(tile * 8 + 8, pos + a.tokens), a.capacity);
+    int t_hi = min(min(tile * 8 + 8, pos + a.tokens), a.capacity);
+    if constexpr (ROPE != 0) t_hi = min(t_hi, a.cs_rows);
     if (pos < 0 || t_lo >= t_hi) return;
 
     const bool active = lane < D / 2;
@@ -87,11 +191,29 @@ __global__ __launch_bounds__(256) void quant_append_kernel(AppendArgs a) {
     uint32_t vn0 = 0, vn1 = 0;      // 4-bit: 8 code nibbles per element
     uint32_t new_mask = 0;          // tokens of this tile written by this call (bit t % 8)
 
-    for (int t = t_lo; t < t_hi; ++t) {
-        float x0 = 0.0f, x1 = 0.0f;
-        if (active)
-            load_pair(a.x, xrow0 + (int64_t)(t - pos) * a.st + 2 * lane, a.x_dtype,
-                      a.pair_loads != 0, x0, x1);
+    // all rows of the tile (and their rotary entries) are loaded before the first is encoded
+    const bool pair = W16 || a.pair_loads != 0, cs_pair = W16 || a.cs_pair_loads != 0;
+    RawPair raw[8];
+    RopeCS cs[8];
+#pragma unroll
+    for (int slot = 0; slot < 8; ++slot) {
+        const int t = tile * 8 + slot;
+        raw[slot] = RawPair{0u, 0u};
+        cs[slot] = RopeCS{{0u, 0u}, {0u, 0u}};
+        if (active && t >= t_lo && t < t_hi) {
+            raw[slot] = load_raw_t<W16>(a.x, xrow0 + (int64_t)(t - pos) * a.st + 2 * lane,
+                                        a.x_dtype, pair);
+            if constexpr (ROPE != 0)
+                cs[slot] = rope_load<D, ROPE, W16>(a.cos, a.sin, a.x_dtype, cs_pair, t, lane);
+        }
+    }
+#pragma unroll
+    for (int slot = 0; slot < 8; ++slot) {
+        const int t = tile * 8 + slot;
+        if (t < t_lo || t >= t_hi) continue;
+        float x0, x1;
+        raw_to_f32(raw[slot], a.x_dtype, pair, x0, x1);
+        if constexpr (ROPE != 0) rope_apply<D, ROPE>(x0, x1, cs[slot], a.x_dtype, cs_pair, lane);
         uint32_t c0, c1;
         float row_scale = 0.0f;
         if constexpr (FMT == CQKV_FMT_FP8) {
@@ -133,7 +255,6 @@ __global__ __launch_bounds__(256) void quant_append_kernel(AppendArgs a) {
         if constexpr (FMT != CQKV_FMT_MXFP4) {
             if (lane == 0) ((float *)scales)[t] = row_scale;
         }
-        const int slot = t & 7;
         new_mask |= 1u << slot;
         if (!active) continue;
         if constexpr (!IS_VALUE) {
@@ -179,12 +300,24 @@ __global__ __launch_bounds__(256) void quant_append_kernel(AppendArgs a) {
     }
 }
 
+template <int FMT, int IS_VALUE, int D, bool W16>
+__global__ __launch_bounds__(256) void quant_append_kernel(AppendArgs a) {
+    append_tile<FMT, IS_VALUE, D, 0, W16>(a, blockIdx.y, blockIdx.z, blockIdx.x, threadIdx.x >> 6,
+                                     threadIdx.x & 63);
+}
+
+template <int FMT, int IS_VALUE, bool W16>
+static void launch_append_w(int d, dim3 grid, hipStream_t st, const AppendArgs &a) {
+    if (d == 64)
+        hipLaunchKernelGGL((quant_append_kernel<FMT, IS_VALUE, 64, W16>), grid, dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((quant_append_kernel<FMT, IS_VALUE, 128, W16>), grid, dim3(256), 0, st, a);
+}
+
 template <int FMT, int IS_VALUE>
 static void launch_append_dim(int d, dim3 grid, hipStream_t st, const AppendArgs &a) {
-    if (d == 64)
-        hipLaunchKernelGGL((quant_append_kernel<FMT, IS_VALUE, 64>), grid, dim3(256), 0, st, a);
-    else
-        hipLaunchKernelGGL((quant_append_kernel<FMT, IS_VALUE, 128>), grid, dim3(256), 0, st, a);
+    if (a.x_dtype != CQKV_F32 && a.pair_loads) launch_append_w<FMT, IS_VALUE, true>(d, grid, st, a);
+    else launch_append_w<FMT, IS_VALUE, false>(d, grid, st, a);
 }
 
 template <int FMT>
@@ -207,21 +340,22 @@ int fill_turbo_args(const cqkv_side *s, uint32_t sign_bits[4], float *rot_scale,
     return CQKV_OK;
 }
 
-// Launch used by cqkv_quant_append and by the prefill's fused append.
-int quant_append_launch(const cqkv_side *side, const void *x, int32_t x_dtype,
-                        const int64_t xs[3], int32_t batch, int32_t tokens,
-                        const int32_t *positions, int32_t position, hipStream_t stream) {
-    AppendArgs a = {};
+// Elements 2l, 2l+1 of every row form one aligned 4- / 8-byte word.
+static bool pair_aligned(const int64_t s[3], const void *p, int32_t dtype) {
+    const size_t esz = dtype == CQKV_F32 ? 4 : 2;
+    return s[0] % 2 == 0 && s[1] % 2 == 0 && s[2] % 2 == 0 && ((uintptr_t)p % (2 * esz)) == 0;
+}
+
+// Fills the append fields of `a` for one side and input x (shared by both entry points).
+static int fill_append_args(AppendArgs &a, const cqkv_side *side, const void *x,
+                            int32_t x_dtype, const int64_t xs[3], int32_t tokens,
+                            const int32_t *positions, int32_t position) {
     a.x = x;
     a.x_dtype = x_dtype;
     a.sb = xs[0];
     a.sh = xs[1];
     a.st = xs[2];
-    {
-        const size_t esz = x_dtype == CQKV_F32 ? 4 : 2;
-        a.pair_loads = (xs[0] % 2 == 0 && xs[1] % 2 == 0 && xs[2] % 2 == 0 &&
-                        ((uintptr_t)x % (2 * esz)) == 0) ? 1 : 0;
-    }
+    a.pair_loads = pair_aligned(xs, x, x_dtype) ? 1 : 0;
     a.codes = (uint8_t *)side->codes;
     a.scales = (uint8_t *)side->scales;
     a.codes_plane = (uint32_t)cqkv_codes_plane_bytes(side->format, side->head_dim, side->capacity);
@@ -231,10 +365,16 @@ int quant_append_launch(const cqkv_side *side, const void *x, int32_t x_dtype,
     a.tokens = tokens;
     a.capacity = side->capacity;
     a.kv_heads = side->kv_heads;
-    if (side->format == CQKV_FMT_TURBO4) {
-        const int rc = fill_turbo_args(side, a.sign_bits, &a.rot_scale, a.bnd);
-        if (rc) return rc;
-    }
+    if (side->format == CQKV_FMT_TURBO4) return fill_turbo_args(side, a.sign_bits, &a.rot_scale, a.bnd);
+    return CQKV_OK;
+}
+
+// Launch used by cqkv_quant_append and by the prefill's fused append.
+int quant_append_launch(const cqkv_side *side, const void *x, int32_t x_dtype,
+                        const int64_t xs[3], int32_t batch, int32_t tokens,
+                        const int32_t *positions, int32_t position, hipStream_t stream) {
+    AppendArgs a = {};
+    if (int rc = fill_append_args(a, side, x, x_dtype, xs, tokens, positions, position)) return rc;
     const int tiles = (tokens + 7) / 8 + 1;  // an unaligned start spans one more tile
     dim3 grid((tiles + 3) / 4, side->kv_heads, batch);
     switch (side->format) {
@@ -246,7 +386,176 @@ int quant_append_launch(const cqkv_side *side, const void *x, int32_t x_dtype,
     return CQKV_OK;
 }
 
+// ---------------------------------------------------------------------------------------------
+// Fused RoPE + quantize-append: one launch rotates the queries (written out in their dtype for
+// the attention call), rotates the keys and quantizes them into the key side, and quantizes the
+// values into the value side. Grid ((tiles / 4) * units, 1, batch) with units = 2 * kv_heads +
+// q_heads: unit y < kv_heads is a key plane, the next kv_heads value planes, the rest query heads.
+// ---------------------------------------------------------------------------------------------
+struct RopeAppendArgs {
+    AppendArgs k, v;  // k carries the cos / sin tables
+    const void *q;
+    void *q_out;
+    int64_t qsb, qsh, qst, osb, osh, ost;  // element strides: batch, head, token
+    int32_t q_pair_loads, o_pair_stores, q_heads;
+};
+
+template <int D, int ROPE, bool W16>
+__device__ inline void rope_query_rows(const RopeAppendArgs &r, int h, int b, int bx, int wave,
+                                       int lane) {
+    const AppendArgs &a = r.k;
+    const int pos = a.positions ? a.positions[b] : a.position;
+    const int i_lo = (bx * 4 + wave) * 8, i_hi = min(i_lo + 8, a.tokens);
+    if (pos < 0) return;
+    const bool active = lane < D / 2;
+    const int64_t in0 = (int64_t)b * r.qsb + (int64_t)h * r.qsh + 2 * lane;
+    const int64_t out0 = (int64_t)b * r.osb + (int64_t)h * r.osh + 2 * lane;
+    const int i_end = min(i_hi, a.cs_rows - pos);
+    const bool pair = W16 || r.q_pair_loads != 0, cs_pair = W16 || a.cs_pair_loads != 0;
+    RawPair raw[8];
+    RopeCS cs[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const int i = i_lo + s;
+        raw[s] = RawPair{0u, 0u};
+        cs[s] = RopeCS{{0u, 0u}, {0u, 0u}};
+        if (active && i < i_end) {
+            raw[s] = load_raw_t<W16>(r.q, in0 + (int64_t)i * r.qst, a.x_dtype, pair);
+            cs[s] = rope_load<D, ROPE, W16>(a.cos, a.sin, a.x_dtype, cs_pair, pos + i, lane);
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const int i = i_lo + s;
+        if (i >= i_end) break;
+        float x0, x1;
+        raw_to_f32(raw[s], a.x_dtype, pair, x0, x1);
+        rope_apply<D, ROPE>(x0, x1, cs[s], a.x_dtype, cs_pair, lane);
+        if (!active) continue;
+        const int64_t o = out0 + (int64_t)i * r.ost;
+        if (r.o_pair_stores && a.x_dtype != CQKV_F32) {
+            *(uint32_t *)((uint16_t *)r.q_out + o) =
+                a.x_dtype == CQKV_BF16 ? pack_bf16x2(x0, x1) : pack_f16x2(x0, x1);
+        } else {
+            store_elem(r.q_out, o, a.x_dtype, x0);
+            store_elem(r.q_out, o + 1, a.x_dtype, x1);
+        }
+    }
+}
+
+template <int FMT, int D, int ROPE, bool W16>
+__global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendArgs r) {
+    // head index fastest in dispatch order: the blocks in flight together read whole projection
+    // rows (all heads of the same tokens) instead of one head's 256-byte pieces 12 KB apart
+    const int hkv = r.k.kv_heads, units = 2 * hkv + r.q_heads;
+    const int y = (int)(blockIdx.x % (unsigned)units), bx = (int)(blockIdx.x / (unsigned)units);
+    const int b = blockIdx.z, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (y < hkv) append_tile<FMT, 0, D, ROPE, W16>(r.k, y, b, bx, wave, lane);
+    else if (y < 2 * hkv) append_tile<FMT, 1, D, 0, W16>(r.v, y - hkv, b, bx, wave, lane);
+    else rope_query_rows<D, ROPE, W16>(r, y - 2 * hkv, b, bx, wave, lane);
+}
+
+template <int FMT, int ROPE, bool W16>
+static void launch_rope_append_w(int d, dim3 grid, hipStream_t st, const RopeAppendArgs &r) {
+    if (d == 64)
+        hipLaunchKernelGGL((rope_append_kernel<FMT, 64, ROPE, W16>), grid, dim3(256), 0, st, r);
+    else
+        hipLaunchKernelGGL((rope_append_kernel<FMT, 128, ROPE, W16>), grid, dim3(256), 0, st, r);
+}
+
+template <int FMT, int ROPE>
+static void launch_rope_append(int d, dim3 grid, hipStream_t st, const RopeAppendArgs &r) {
+    const bool w16 = r.k.x_dtype != CQKV_F32 && r.k.pair_loads && r.v.pair_loads &&
+                     r.q_pair_loads && r.k.cs_pair_loads;
+    if (w16) launch_rope_append_w<FMT, ROPE, true>(d, grid, st, r);
+    else launch_rope_append_w<FMT, ROPE, false>(d, grid, st, r);
+}
+
+template <int FMT>
+static void launch_rope_append_fmt(int rope, int d, dim3 grid, hipStream_t st,
+                                   const RopeAppendArgs &r) {
+    if (rope == CQKV_ROPE_INTERLEAVED) launch_rope_append<FMT, CQKV_ROPE_INTERLEAVED>(d, grid, st, r);
+    else launch_rope_append<FMT, CQKV_ROPE_HALVES>(d, grid, st, r);
+}
+
 }  // namespace cqkv
+
+extern "C" int cqkv_rope_quant_append(const cqkv_side *k_side, const cqkv_side *v_side,
+                                      const void *q, const int64_t q_strides[3], const void *k,
+                                      const int64_t k_strides[3], const void *v,
+                                      const int64_t v_strides[3], int32_t dtype, int32_t batch,
+                                      int32_t tokens, int32_t q_heads, const void *cos,
+                                      const void *sin, int32_t cs_rows, int32_t rope_kind,
+                                      const int32_t *positions, int32_t position, void *q_out,
+                                      const int64_t q_out_strides[3], cqkv_stream_t stream) {
+    using namespace cqkv;
+    clear_error();
+    static const char *who = "cqkv_rope_quant_append";
+    if (int rc = check_side(k_side, who)) return rc;
+    if (int rc = check_side(v_side, who)) return rc;
+    if (k_side->is_value || !v_side->is_value)
+        return fail(CQKV_ERR_ARG, "%s: k_side must be a key side and v_side a value side", who);
+    if (k_side->format != v_side->format || k_side->head_dim != v_side->head_dim ||
+        k_side->kv_heads != v_side->kv_heads || k_side->capacity != v_side->capacity)
+        return fail(CQKV_ERR_ARG, "%s: key / value sides differ in format, D, heads or capacity", who);
+    if (!q || !k || !v || !q_out || !q_strides || !k_strides || !v_strides || !q_out_strides ||
+        !cos || !sin)
+        return fail(CQKV_ERR_ARG, "%s: null pointer argument", who);
+    if (dtype < CQKV_BF16 || dtype > CQKV_F32) return fail(CQKV_ERR_ARG, "%s: dtype %d", who, dtype);
+    if (rope_kind != CQKV_ROPE_HALVES && rope_kind != CQKV_ROPE_INTERLEAVED)
+        return fail(CQKV_ERR_ARG, "%s: rope kind %d", who, rope_kind);
+    const int hkv = k_side->kv_heads;
+    if (batch <= 0 || tokens < 0 || q_heads <= 0 || q_heads % hkv != 0)
+        return fail(CQKV_ERR_ARG, "%s: batch %d tokens %d q_heads %d kv_heads %d", who, batch,
+                    tokens, q_heads, hkv);
+    if (cs_rows <= 0) return fail(CQKV_ERR_ARG, "%s: cos / sin rows %d", who, cs_rows);
+    if (tokens == 0) return CQKV_OK;
+    if (!positions) {
+        const int64_t end = (int64_t)position + tokens;
+        if (position < 0 || end > k_side->capacity)
+            return fail(CQKV_ERR_ARG, "%s: positions [%d, %lld) exceed the capacity %d", who,
+                        position, (long long)end, k_side->capacity);
+        if (end > cs_rows)
+            return fail(CQKV_ERR_ARG, "%s: positions [%d, %lld) exceed the %d cos / sin rows", who,
+                        position, (long long)end, cs_rows);
+    }
+    RopeAppendArgs r = {};
+    if (int rc = fill_append_args(r.k, k_side, k, dtype, k_strides, tokens, positions, position)) return rc;
+    if (int rc = fill_append_args(r.v, v_side, v, dtype, v_strides, tokens, positions, position)) return rc;
+    r.k.cos = cos;
+    r.k.sin = sin;
+    r.k.cs_rows = cs_rows;
+    {
+        const uintptr_t al = dtype == CQKV_F32 ? 8 : 4;
+        r.k.cs_pair_loads = ((uintptr_t)cos % al == 0 && (uintptr_t)sin % al == 0) ? 1 : 0;
+    }
+    r.q = q;
+    r.q_out = q_out;
+    r.qsb = q_strides[0];
+    r.qsh = q_strides[1];
+    r.qst = q_strides[2];
+    r.osb = q_out_strides[0];
+    r.osh = q_out_strides[1];
+    r.ost = q_out_strides[2];
+    r.q_pair_loads = pair_aligned(q_strides, q, dtype) ? 1 : 0;
+    r.o_pair_stores = pair_aligned(q_out_strides, q_out, dtype) ? 1 : 0;
+    r.q_heads = q_heads;
+    const int64_t tiles = ((int64_t)tokens + 7) / 8 + 1;  // an unaligned start spans one more tile
+    const int64_t blocks = (tiles + 3) / 4 * (2 * hkv + q_heads);
+    if (blocks > INT32_MAX)
+        return fail(CQKV_ERR_ARG, "%s: %d tokens x %d heads exceed one launch", who, tokens,
+                    2 * hkv + q_heads);
+    dim3 grid((uint32_t)blocks, 1, batch);
+    const hipStream_t st = (hipStream_t)stream;
+    const int d = k_side->head_dim;
+    switch (k_side->format) {
+    case CQKV_FMT_FP8: launch_rope_append_fmt<CQKV_FMT_FP8>(rope_kind, d, grid, st, r); break;
+    case CQKV_FMT_MXFP4: launch_rope_append_fmt<CQKV_FMT_MXFP4>(rope_kind, d, grid, st, r); break;
+    default: launch_rope_append_fmt<CQKV_FMT_TURBO4>(rope_kind, d, grid, st, r); break;
+    }
+    CQKV_HIP_CHECK(hipGetLastError());
+    return CQKV_OK;
+}
 
 extern "C" int cqkv_quant_append(const cqkv_side *side, const void *x, int32_t x_dtype,
                                  const int64_t x_strides[3], int32_t batch, int32_t tokens,

@@ -13,6 +13,10 @@
  *   cqkv_quant_append      RocmStorage::tq_quantize + Cache::append
  *                          (candle-core/src/rocm_backend/accel.rs:269-303,
  *                           candle-nn/src/turbo_quant.rs:916-945, candle-nn/src/kv_cache.rs:68-99)
+ *   cqkv_rope_quant_append the model-side sequence rope(q), rope(k), TurboKvCache::append(k, v)
+ *                          in one launch: candle_nn::rotary_emb::rope / rope_i
+ *                          (candle-nn/src/rotary_emb.rs:275-303, 585-611; ROCm kernels
+ *                          candle-core/kernels/nn.hip:107-148) followed by the append above
  *   cqkv_decode_attention  RocmStorage::tq_attention (+ tq_combine)
  *                          (candle-core/src/rocm_backend/accel.rs:425-571,
  *                           candle-nn/src/turbo_quant.rs:1143-1264)
@@ -70,6 +74,10 @@ enum { CQKV_FMT_TURBO4 = 0, CQKV_FMT_MXFP4 = 2, CQKV_FMT_FP8 = 5 };
 /* Element types of q / k / v / outputs. */
 enum { CQKV_BF16 = 0, CQKV_F16 = 1, CQKV_F32 = 2 };
 
+/* Rotary embedding layouts: rope (halves, element i pairs with i + D/2) and rope_i (interleaved,
+ * element 2i pairs with 2i + 1) of candle-nn/src/rotary_emb.rs. */
+enum { CQKV_ROPE_HALVES = 1, CQKV_ROPE_INTERLEAVED = 2 };
+
 /* One side (keys or values) of a quantized cache. */
 typedef struct cqkv_side {
     int32_t format;    /* CQKV_FMT_* */
@@ -96,6 +104,25 @@ size_t cqkv_scales_plane_bytes(int32_t format, int32_t head_dim, int32_t capacit
 int cqkv_quant_append(const cqkv_side *side, const void *x, int32_t x_dtype,
                       const int64_t x_strides[3], int32_t batch, int32_t tokens,
                       const int32_t *positions, int32_t position, cqkv_stream_t stream);
+
+/* Fused RoPE + quantize-append from the QKV projection output. q (batch, q_heads, tokens, D),
+ * k / v (batch, kv_heads, tokens, D) with element strides *_strides[0..2] for batch, head, token
+ * (D contiguous; q, k and v may be views into one (batch, tokens, (q_heads + 2 kv_heads) D)
+ * projection output), all of `dtype`. cos / sin: (cs_rows, D/2) tables of `dtype`, row p = the
+ * rotary angles of position p. Token i of batch b sits at position p = positions[b] + i (device
+ * int32 array) or `position` + i: q is rotated with row p and written to q_out (strides
+ * q_out_strides, `dtype`); k is rotated with row p, rounded to `dtype` as the reference's rope
+ * output is, and quantized into k_side at cache position p; v is quantized into v_side as
+ * cqkv_quant_append does. The sides must share format, D, heads and capacity. Positions past the
+ * capacity (keys and values) or the tables (all three) are an error when positions is NULL and
+ * are skipped otherwise. */
+int cqkv_rope_quant_append(const cqkv_side *k_side, const cqkv_side *v_side, const void *q,
+                           const int64_t q_strides[3], const void *k, const int64_t k_strides[3],
+                           const void *v, const int64_t v_strides[3], int32_t dtype,
+                           int32_t batch, int32_t tokens, int32_t q_heads, const void *cos,
+                           const void *sin, int32_t cs_rows, int32_t rope_kind,
+                           const int32_t *positions, int32_t position, void *q_out,
+                           const int64_t q_out_strides[3], cqkv_stream_t stream);
 
 /* Decode attention over a quantized cache (TqAttn + tq_combine, bottom-right aligned masks of
  * candle-core/src/accel/attention.rs:80-92):

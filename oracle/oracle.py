@@ -229,6 +229,51 @@ def key_range(i: int, lq: int, lk: int, wl: int, wr: int) -> tuple[int, int]:
 
 
 # --------------------------------------------------------------------------------------------
+# rotary embeddings
+# --------------------------------------------------------------------------------------------
+ROPE_HALVES, ROPE_INTERLEAVED = 1, 2
+
+
+def round_to(x: np.ndarray, dtype: str) -> np.ndarray:
+    """x (f32) rounded to "bf16" / "f16" (round to nearest even) and back, or left as "f32"."""
+    if dtype == "bf16":
+        return round_bf16(x)
+    if dtype == "f16":
+        return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
+    return np.asarray(x, np.float32)
+
+
+def rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, kind: int, pos0: int) -> np.ndarray:
+    """Rotary embedding of x (..., t, d) f32, token i at table row pos0 + i of cos / sin
+    ((rows, d/2) f32); f32 result, before the rounding to the tensor dtype.
+
+    Follows the reference's ROCm kernels rope_impl / rope_i_impl
+    (candle-core/kernels/nn.hip:107-148: products rounded to f32 separately, then the difference
+    or sum) and its f32 CPU path (candle-nn/src/rotary_emb.rs:47-76, the same expressions):
+      halves:      y_i = x_i c_i - x_{i+d/2} s_i,   y_{i+d/2} = x_i s_i + x_{i+d/2} c_i
+      interleaved: y_2i = x_2i c_i - x_2i+1 s_i,   y_2i+1 = x_2i s_i + x_2i+1 c_i
+    numpy evaluates each product and sum in f32 with one rounding each, as those kernels do."""
+    x = np.asarray(x, np.float32)
+    t, d = x.shape[-2], x.shape[-1]
+    c = np.asarray(cos, np.float32)[pos0:pos0 + t]
+    s = np.asarray(sin, np.float32)[pos0:pos0 + t]
+    if c.shape[0] != t:
+        raise ValueError("rope: positions past the cos / sin table")
+    y = np.empty_like(x)
+    if kind == ROPE_HALVES:
+        a, b = x[..., :d // 2], x[..., d // 2:]
+        y[..., :d // 2] = a * c - b * s
+        y[..., d // 2:] = a * s + b * c
+    elif kind == ROPE_INTERLEAVED:
+        a, b = x[..., 0::2], x[..., 1::2]
+        y[..., 0::2] = a * c - b * s
+        y[..., 1::2] = a * s + b * c
+    else:
+        raise ValueError(f"rope kind {kind}")
+    return y
+
+
+# --------------------------------------------------------------------------------------------
 # attention
 # --------------------------------------------------------------------------------------------
 def attention_unfused(q, k, v, scale, kv_lens=None, softcap=0.0, wl=-1, wr=-1, alibi=None,

@@ -179,3 +179,29 @@ def test_gpu_entry_points_refuse_cpu_tensors(cq):
                         torch.zeros(1, dtype=torch.uint8))
     with pytest.raises(cq.CqkvError):
         cq.quant_append(side, torch.zeros(1, 1, 1, 64))
+
+
+def test_rope_quant_append_argument_errors(cq):
+    """The fused RoPE + append checks its sides, kinds and positions before any launch."""
+    L = cq.lib()
+    x = (ctypes.c_int64 * 3)(1, 128, 128)
+    one = ctypes.c_void_p(1)
+    k = cq.Side(cq.FP8, 0, 128, 2, 64, 0, 0, 1, 1)
+    v = cq.Side(cq.FP8, 1, 128, 2, 64, 0, 0, 1, 1)
+    vm = cq.Side(cq.MXFP4, 1, 128, 2, 64, 0, 0, 1, 1)
+
+    def call(ks=k, vs=v, kind=1, tokens=4, position=0, rows=100, hq=8, positions=None, cos=one):
+        return L.cqkv_rope_quant_append(ctypes.byref(ks), ctypes.byref(vs), one, x, one, x, one,
+                                        x, 0, 2, tokens, hq, cos, one, rows, kind, positions,
+                                        position, one, x, None)
+    assert call(kind=0) == cq.ERR_ARG
+    assert b"rope kind" in L.cqkv_last_error()
+    assert call(vs=vm) == cq.ERR_ARG
+    assert call(ks=v, vs=k) == cq.ERR_ARG
+    assert call(hq=5) == cq.ERR_ARG
+    assert call(position=62) == cq.ERR_ARG
+    assert b"capacity" in L.cqkv_last_error()
+    assert call(position=10, rows=12) == cq.ERR_ARG
+    assert b"cos / sin rows" in L.cqkv_last_error()
+    assert call(cos=None) == cq.ERR_ARG
+    assert call(tokens=0) == cq.OK  # nothing to do, nothing launched

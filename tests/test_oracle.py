@@ -523,3 +523,72 @@ def test_live_reference_harness_fp8_rows():
     l = O.row_layout(O.FP8, 0, 128)
     want = H.tq_quant(x, O.FP8, 8, l.code_words, l.aux_words, l.row_words, H.tq_tab())
     np.testing.assert_array_equal(O.quantize_rows(O.FP8, 0, x), want)
+
+
+# ---------------------------------------------------------------------------------------------
+# rotary embeddings
+# ---------------------------------------------------------------------------------------------
+def rope_tables(rows: int, d: int, base: float = 10000.0):
+    """cos / sin (rows, d/2) of the usual rotary angles p * base^(-2i/d), in f32."""
+    inv = 1.0 / base ** (np.arange(0, d, 2, dtype=np.float64) / d)
+    ang = np.arange(rows, dtype=np.float64)[:, None] * inv[None, :]
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+def test_rope_matches_rope_slow_bit_exact():
+    """candle-nn/tests/ops.rs:248-270 (and :199-220 for rope_i): on the CPU the fast rope equals
+    rope_slow bit for bit. rope_slow is x * cat(cos, cos) + rotate_half(x) * cat(sin, sin)
+    (candle-nn/src/rotary_emb.rs:614-630); rope_i_slow reshapes to (.., d/2, 2)
+    (rotary_emb.rs:305-324). Both are restated here with torch in f32, independently of the
+    oracle's index arithmetic, and must agree with it exactly (random tables as in the test)."""
+    import torch
+    g = np.random.default_rng(299792458)
+    b, h, t, d = 2, 5, 10, 16
+    x = g.random((b, h, t, d), dtype=np.float32)
+    cos = g.random((t, d // 2), dtype=np.float32)
+    sin = g.random((t, d // 2), dtype=np.float32)
+    xt, ct, st = torch.from_numpy(x), torch.from_numpy(cos), torch.from_numpy(sin)
+    rot_half = torch.cat([-xt[..., d // 2:], xt[..., :d // 2]], -1)
+    slow = xt * torch.cat([ct, ct], -1) + rot_half * torch.cat([st, st], -1)
+    np.testing.assert_array_equal(O.rope(x, cos, sin, O.ROPE_HALVES, 0), slow.numpy())
+    xr = xt.reshape(b, h, t, d // 2, 2)
+    x0, x1 = xr[..., 0], xr[..., 1]
+    c3, s3 = ct[:, :, None][..., 0], st[:, :, None][..., 0]
+    slow_i = torch.stack([x0 * c3 - x1 * s3, x0 * s3 + x1 * c3], -1).reshape(b, h, t, d)
+    np.testing.assert_array_equal(O.rope(x, cos, sin, O.ROPE_INTERLEAVED, 0), slow_i.numpy())
+    # the two layouts differ (a swapped layout would pass neither identity above)
+    assert not np.array_equal(O.rope(x, cos, sin, O.ROPE_HALVES, 0),
+                              O.rope(x, cos, sin, O.ROPE_INTERLEAVED, 0))
+
+
+@pytest.mark.parametrize("kind", [1, 2])
+def test_rope_is_a_rotation_by_position(kind):
+    """With real angle tables: each (pair) keeps its norm, rotating by -angle undoes it, and the
+    score <rope(q, m), rope(k, n)> depends only on m - n (the defining property); float64 checks
+    at f32 tolerance, so a wrong sign, pairing or table row fails them."""
+    d, rows = 64, 40
+    cos, sin = rope_tables(rows, d)
+    g = np.random.default_rng(3)
+    q = g.standard_normal((1, 1, 1, d)).astype(np.float32)
+    k = g.standard_normal((1, 1, 1, d)).astype(np.float32)
+    pairs = (lambda y: np.stack([y[..., :d // 2], y[..., d // 2:]], -1)) if kind == 1 else \
+        (lambda y: np.stack([y[..., 0::2], y[..., 1::2]], -1))
+    for p in (0, 7, 39):
+        y = O.rope(q, cos, sin, kind, p)
+        np.testing.assert_allclose(np.linalg.norm(pairs(y), axis=-1),
+                                   np.linalg.norm(pairs(q), axis=-1), rtol=1e-6)
+        back = O.rope(y, cos, -sin, kind, p)
+        np.testing.assert_allclose(back, q, atol=1e-5)
+    np.testing.assert_array_equal(O.rope(q, cos, sin, kind, 0), q)  # angle 0
+    dots = [float((O.rope(q, cos, sin, kind, m).astype(np.float64) *
+                   O.rope(k, cos, sin, kind, m - 5).astype(np.float64)).sum())
+            for m in (5, 12, 30, 39)]
+    np.testing.assert_allclose(dots, dots[0], rtol=1e-5, atol=1e-5)
+
+
+def test_round_to_dtypes():
+    x = np.array([1.0 + 2.0 ** -9, 1.0 + 3 * 2.0 ** -9, 65519.0, 1e-8], np.float32)
+    np.testing.assert_array_equal(O.round_to(x, "bf16")[:3], [1.0, 1.0 + 2.0 ** -7, 65536.0])
+    np.testing.assert_array_equal(O.round_to(x, "f16")[:2], [1.0 + 2.0 ** -9, 1.0 + 3 * 2.0 ** -9])
+    assert np.isinf(O.round_to(np.float32(65520.0), "f16"))
+    np.testing.assert_array_equal(O.round_to(x, "f32"), x)
