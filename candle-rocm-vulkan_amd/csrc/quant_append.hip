@@ -191,29 +191,9 @@ __device__ inline void append_tile(const AppendArgs &a, int h, int b, int bx, in
     uint32_t vn0 = 0, vn1 = 0;      // 4-bit: 8 code nibbles per element
     uint32_t new_mask = 0;          // tokens of this tile written by this call (bit t % 8)
 
-    // all rows of the tile (and their rotary entries) are loaded before the first is encoded
     const bool pair = W16 || a.pair_loads != 0, cs_pair = W16 || a.cs_pair_loads != 0;
-    RawPair raw[8];
-    RopeCS cs[8];
-#pragma unroll
-    for (int slot = 0; slot < 8; ++slot) {
-        const int t = tile * 8 + slot;
-        raw[slot] = RawPair{0u, 0u};
-        cs[slot] = RopeCS{{0u, 0u}, {0u, 0u}};
-        if (active && t >= t_lo && t < t_hi) {
-            raw[slot] = load_raw_t<W16>(a.x, xrow0 + (int64_t)(t - pos) * a.st + 2 * lane,
-                                        a.x_dtype, pair);
-            if constexpr (ROPE != 0)
-                cs[slot] = rope_load<D, ROPE, W16>(a.cos, a.sin, a.x_dtype, cs_pair, t, lane);
-        }
-    }
-#pragma unroll
-    for (int slot = 0; slot < 8; ++slot) {
-        const int t = tile * 8 + slot;
-        if (t < t_lo || t >= t_hi) continue;
-        float x0, x1;
-        raw_to_f32(raw[slot], a.x_dtype, pair, x0, x1);
-        if constexpr (ROPE != 0) rope_apply<D, ROPE>(x0, x1, cs[slot], a.x_dtype, cs_pair, lane);
+    // encodes one token (x0, x1) at cache position t, tile slot `slot`
+    auto encode = [&](float x0, float x1, int t, int slot) {
         uint32_t c0, c1;
         float row_scale = 0.0f;
         if constexpr (FMT == CQKV_FMT_FP8) {
@@ -256,7 +236,7 @@ __device__ inline void append_tile(const AppendArgs &a, int h, int b, int bx, in
             if (lane == 0) ((float *)scales)[t] = row_scale;
         }
         new_mask |= 1u << slot;
-        if (!active) continue;
+        if (!active) return;
         if constexpr (!IS_VALUE) {
             if constexpr (FMT == CQKV_FMT_FP8)
                 *(uint16_t *)(codes + (int64_t)t * D + 2 * lane) = (uint16_t)(c0 | (c1 << 8));
@@ -271,6 +251,20 @@ __device__ inline void append_tile(const AppendArgs &a, int h, int b, int bx, in
                 vn1 |= c1 << (4 * slot);
             }
         }
+    };
+    for (int t = t_lo; t < t_hi; ++t) {
+        RawPair raw = {0u, 0u};
+        RopeCS cs = {{0u, 0u}, {0u, 0u}};
+        if (active) {
+            raw = load_raw_t<W16>(a.x, xrow0 + (int64_t)(t - pos) * a.st + 2 * lane,
+                                  a.x_dtype, pair);
+            if constexpr (ROPE != 0)
+                cs = rope_load<D, ROPE, W16>(a.cos, a.sin, a.x_dtype, cs_pair, t, lane);
+        }
+        float x0, x1;
+        raw_to_f32(raw, a.x_dtype, pair, x0, x1);
+        if constexpr (ROPE != 0) rope_apply<D, ROPE>(x0, x1, cs, a.x_dtype, cs_pair, lane);
+        encode(x0, x1, t, t & 7);
     }
     if constexpr (IS_VALUE) {
         if (!active) return;
@@ -398,6 +392,8 @@ struct RopeAppendArgs {
     void *q_out;
     int64_t qsb, qsh, qst, osb, osh, ost;  // element strides: batch, head, token
     int32_t q_pair_loads, o_pair_stores, q_heads;
+    int32_t q_vec16;  // query rows by rope_query_rows16
+    int32_t q_units;  // grid units of the queries: q_heads, or head groups with q_vec16
 };
 
 template <int D, int ROPE, bool W16>
@@ -443,15 +439,111 @@ __device__ inline void rope_query_rows(const RopeAppendArgs &r, int h, int b, in
     }
 }
 
+// Query rows with 16-byte lanes (16-bit dtype, rows and tables 16-byte aligned): lane l holds
+// elements 8c..8c+7 (c = l % (D/8)) of head g * (64 / (D/8)) + l / (D/8), so one load covers
+// 4 heads (D = 128) or 8 heads (D = 64) of a token and a lane's table chunk serves 8 elements.
+// Halves: the partner chunk c ^ (D/16) sits in lane l ^ (D/16). A wave takes 8 tokens in two
+// batches of 4 (all loads of a batch issued before its first conversion).
+template <int D, int ROPE>
+__device__ inline void rope_query_rows16(const RopeAppendArgs &r, int g, int b, int bx, int wave,
+                                         int lane) {
+#pragma clang fp contract(off)
+    const AppendArgs &a = r.k;
+    constexpr int LPR = D / 8, RPW = 64 / LPR;
+    const int pos = a.positions ? a.positions[b] : a.position;
+    if (pos < 0) return;
+    const int h = g * RPW + lane / LPR, c = lane % LPR;
+    const bool live = h < r.q_heads;
+    const int i_lo = (bx * 4 + wave) * 8, i_end = min(min(i_lo + 8, a.tokens), a.cs_rows - pos);
+    if (i_lo >= i_end) return;
+    const uint16_t *qp = (const uint16_t *)r.q + (int64_t)b * r.qsb + (int64_t)h * r.qsh + 8 * c;
+    uint16_t *op = (uint16_t *)r.q_out + (int64_t)b * r.osb + (int64_t)h * r.osh + 8 * c;
+    const bool bf = a.x_dtype == CQKV_BF16;
+    const bool upper = c >= LPR / 2;
+    // table offset of this lane's elements in a row of D/2 entries
+    const int tofs = ROPE == CQKV_ROPE_HALVES ? 8 * (c % (LPR / 2)) : 4 * c;
+    auto f32_of = [bf](uint32_t bits16) {
+        return bf ? bf16_bits_to_f32(bits16) : f16_bits_to_f32(bits16);
+    };
+#pragma unroll
+    for (int s0 = 0; s0 < 8; s0 += 4) {
+        u32x4 xv[4], cv[4], sv[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int i = i_lo + s0 + s;
+            xv[s] = u32x4{0u, 0u, 0u, 0u};
+            cv[s] = sv[s] = u32x4{0u, 0u, 0u, 0u};
+            if (i < i_end) {
+                const int64_t trow = (int64_t)(pos + i) * (D / 2) + tofs;
+                if (live) xv[s] = *(const u32x4 *)(qp + (int64_t)i * r.qst);
+                if constexpr (ROPE == CQKV_ROPE_HALVES) {
+                    cv[s] = *(const u32x4 *)((const uint16_t *)a.cos + trow);
+                    sv[s] = *(const u32x4 *)((const uint16_t *)a.sin + trow);
+                } else {
+                    const u32x2 c2 = *(const u32x2 *)((const uint16_t *)a.cos + trow);
+                    const u32x2 s2 = *(const u32x2 *)((const uint16_t *)a.sin + trow);
+                    cv[s] = u32x4{c2.x, c2.y, 0u, 0u};
+                    sv[s] = u32x4{s2.x, s2.y, 0u, 0u};
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int i = i_lo + s0 + s;
+            if (i >= i_end) break;
+            float x[8], y[8];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                x[2 * w] = f32_of(xv[s][w] & 0xffffu);
+                x[2 * w + 1] = f32_of(xv[s][w] >> 16);
+            }
+            if constexpr (ROPE == CQKV_ROPE_HALVES) {
+                u32x4 pv;
+#pragma unroll
+                for (int w = 0; w < 4; ++w)
+                    pv[w] = (uint32_t)__shfl_xor((int)xv[s][w], LPR / 2, kWave);
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+#pragma unroll
+                    for (int k = 0; k < 2; ++k) {
+                        const uint32_t cb = k ? cv[s][w] >> 16 : cv[s][w] & 0xffffu;
+                        const uint32_t sb = k ? sv[s][w] >> 16 : sv[s][w] & 0xffffu;
+                        const float cc = f32_of(cb), ss = f32_of(sb);
+                        const float p = f32_of(k ? pv[w] >> 16 : pv[w] & 0xffffu);
+                        const float xe = x[2 * w + k];
+                        y[2 * w + k] = upper ? p * ss + xe * cc : xe * cc - p * ss;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const uint32_t cw = cv[s][m >> 1], sw = sv[s][m >> 1];
+                    const float cc = f32_of((m & 1) ? cw >> 16 : cw & 0xffffu);
+                    const float ss = f32_of((m & 1) ? sw >> 16 : sw & 0xffffu);
+                    y[2 * m] = x[2 * m] * cc - x[2 * m + 1] * ss;
+                    y[2 * m + 1] = x[2 * m] * ss + x[2 * m + 1] * cc;
+                }
+            }
+            if (!live) continue;
+            u32x4 ov;
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+                ov[w] = bf ? pack_bf16x2(y[2 * w], y[2 * w + 1]) : pack_f16x2(y[2 * w], y[2 * w + 1]);
+            *(u32x4 *)(op + (int64_t)i * r.ost) = ov;
+        }
+    }
+}
+
 template <int FMT, int D, int ROPE, bool W16>
 __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendArgs r) {
     // head index fastest in dispatch order: the blocks in flight together read whole projection
     // rows (all heads of the same tokens) instead of one head's 256-byte pieces 12 KB apart
-    const int hkv = r.k.kv_heads, units = 2 * hkv + r.q_heads;
+    const int hkv = r.k.kv_heads, units = 2 * hkv + r.q_units;
     const int y = (int)(blockIdx.x % (unsigned)units), bx = (int)(blockIdx.x / (unsigned)units);
     const int b = blockIdx.z, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (y < hkv) append_tile<FMT, 0, D, ROPE, W16>(r.k, y, b, bx, wave, lane);
     else if (y < 2 * hkv) append_tile<FMT, 1, D, 0, W16>(r.v, y - hkv, b, bx, wave, lane);
+    else if (W16 && r.q_vec16) rope_query_rows16<D, ROPE>(r, y - 2 * hkv, b, bx, wave, lane);
     else rope_query_rows<D, ROPE, W16>(r, y - 2 * hkv, b, bx, wave, lane);
 }
 
@@ -540,8 +632,17 @@ extern "C" int cqkv_rope_quant_append(const cqkv_side *k_side, const cqkv_side *
     r.q_pair_loads = pair_aligned(q_strides, q, dtype) ? 1 : 0;
     r.o_pair_stores = pair_aligned(q_out_strides, q_out, dtype) ? 1 : 0;
     r.q_heads = q_heads;
+    {
+        auto al16 = [](const void *p, const int64_t st[3]) {
+            return (uintptr_t)p % 16 == 0 && st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0;
+        };
+        r.q_vec16 = dtype != CQKV_F32 && al16(q, q_strides) && al16(q_out, q_out_strides) &&
+                    (uintptr_t)cos % 16 == 0 && (uintptr_t)sin % 16 == 0 ? 1 : 0;
+        const int rpw = 64 / (k_side->head_dim / 8);  // heads per 16-byte-lane load
+        r.q_units = r.q_vec16 ? (q_heads + rpw - 1) / rpw : q_heads;
+    }
     const int64_t tiles = ((int64_t)tokens + 7) / 8 + 1;  // an unaligned start spans one more tile
-    const int64_t blocks = (tiles + 3) / 4 * (2 * hkv + q_heads);
+    const int64_t blocks = (tiles + 3) / 4 * (2 * hkv + r.q_units);
     if (blocks > INT32_MAX)
         return fail(CQKV_ERR_ARG, "%s: %d tokens x %d heads exceed one launch", who, tokens,
                     2 * hkv + q_heads);

@@ -37,7 +37,8 @@ def expected_rope(x, cos, sin, kind, pos, dtype):
                              pos), dtype)
 
 
-def run_case(cq, dev, fmt, kind, d, dtype, b=2, hq=8, hkv=2, t=19, pos=5, cap=64):
+def run_case(cq, dev, fmt, kind, d, dtype, b=2, hq=8, hkv=2, t=19, pos=5, cap=64,
+             padded_out=False):
     f = FMTS[fmt]
     qkv = kv_source(7 + d + kind, (b, t, 1, (hq + 2 * hkv) * d), outliers=True)[:, :, 0]
     qkv = qkv.to(TORCH[dtype]).to(dev)
@@ -51,7 +52,11 @@ def run_case(cq, dev, fmt, kind, d, dtype, b=2, hq=8, hkv=2, t=19, pos=5, cap=64
     pre_v = oracle_rows(f, kv_source(92, (b, hkv, cap, d)), seed + 2)
     cq.rows_import(ks, torch.from_numpy(pre_k.view(np.int32)).to(dev), 0)
     cq.rows_import(vs, torch.from_numpy(pre_v.view(np.int32)).to(dev), 0)
-    q_out = cq.rope_quant_append(ks, vs, q, k, v, cos.to(dev), sin.to(dev), kind, pos)
+    q_out = None
+    if padded_out:  # odd row stride: the element-pair path instead of 16-byte lanes
+        q_out = torch.zeros(b, hq, t, d + 1, dtype=TORCH[dtype], device=dev)[..., :d]
+    q_out = cq.rope_quant_append(ks, vs, q, k, v, cos.to(dev), sin.to(dev), kind, pos,
+                                 q_out=q_out)
     torch.cuda.synchronize()
 
     want_q = expected_rope(q.cpu(), cos, sin, kind, pos, dtype)
@@ -89,6 +94,18 @@ def test_rope_append_bf16(cq, dev, fmt, kind, d):
 @pytest.mark.parametrize("kind", [1, 2])
 def test_rope_append_dtypes(cq, dev, dtype, kind):
     run_case(cq, dev, "fp8", kind, 128, dtype)
+
+
+@pytest.mark.parametrize("kind", [1, 2])
+@pytest.mark.parametrize("d,hq,hkv", [(128, 6, 2), (64, 12, 4), (64, 4, 4)])
+def test_rope_append_partial_head_groups(cq, dev, kind, d, hq, hkv):
+    """Query head counts that do not fill the last 4- (D=128) or 8-head (D=64) lane group."""
+    run_case(cq, dev, "fp8", kind, d, "bf16", hq=hq, hkv=hkv)
+
+
+@pytest.mark.parametrize("kind", [1, 2])
+def test_rope_append_padded_query_output(cq, dev, kind):
+    run_case(cq, dev, "mxfp4", kind, 128, "bf16", padded_out=True)
 
 
 def test_rope_append_single_token_decode_step(cq, dev):
