@@ -19,11 +19,12 @@ host on a bounded sample of the same workload.
 
 "other_configs" reports BASELINE configs 3 (MXFP4, ragged), 4 (causal bf16 prefill with fused
 FP8 append) and 5 (TurboQuant-4, context 128K) with the same timing method; they are secondary
-figures, not the headline value. "ra_*" time the fused RoPE + FP8 quantize-append at the
-config-4 prefill shape and at one config-2 decode step.
+figures, not the headline value. "c2_shape_mxfp8" / "c2_shape_nvfp4" time the decode of the
+other block-scaled formats at the config-2 shape; "ra_*" time the fused RoPE + FP8
+quantize-append at the config-4 prefill shape and at one config-2 decode step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
-                       [--only c2,c3,c4,c5,ra] [--calibration-copy]
+                       [--only c2,c3,c4,c5,fx,ra] [--calibration-copy]
 """
 from __future__ import annotations
 
@@ -92,7 +93,8 @@ def time_calls(fn, steps, warmup, stream):
 
 def row_bytes(fmt, d):
     """Packed cache bytes of one (token, head) row: codes + its scales."""
-    return {5: d + 4, 2: d // 2 + d // 32, 0: d // 2 + 4}[fmt]
+    return {5: d + 4, 2: d // 2 + d // 32, 0: d // 2 + 4, 4: d + d // 32,
+            3: d // 2 + d // 16 + 4}[fmt]
 
 
 def decode_bytes(b, hq, hkv, d, total_tokens, fmt):
@@ -220,7 +222,7 @@ def rope_append_case(cq, dev, stream, fmt, b, hq, hkv, d, t, cap, steps, warmup)
     nbytes = (qkv.numel() * 2 + 2 * t * (d // 2) * 2 + q_out.numel() * 2
               + 2 * b * hkv * t * rb)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"workload": f"fused RoPE + {['TURBO4', '', 'MXFP4', '', '', 'FP8'][fmt]} append, "
+    return {"workload": f"fused RoPE + {['TURBO4', '', 'MXFP4', 'NVFP4', 'MXFP8', 'FP8'][fmt]} append, "
                         f"B={b} t={t} Hq={hq} Hkv={hkv} D={d}",
             "us_per_call": round(ms * 1e3, 2), "bytes_per_call": nbytes,
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
@@ -256,7 +258,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
-    ap.add_argument("--only", default="", help="comma list of c2,c3,c4,c5,ra (default: all)")
+    ap.add_argument("--only", default="", help="comma list of c2,c3,c4,c5,fx,ra (default: all)")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="also run a plain 1 GiB copy (for counter scaling)")
     args = ap.parse_args()
@@ -357,6 +359,20 @@ def main():
         log(f"config 5: {ms * 1e3:.2f} us/call")
         torch.cuda.empty_cache()
 
+    if want("fx"):
+        # the block-scaled formats of the reference beyond the BASELINE configs, at the config-2
+        # decode shape
+        for fmt, name in ((cq.MXFP8, "mxfp8"), (cq.NVFP4, "nvfp4")):
+            log(f"{name} decode B=32 32/8 d=128 ctx 8192")
+            caches, _, ms, nbytes = decode_case(cq, dev, stream, fmt, 32, 32, 8, 128, 8192,
+                                                steps_x, warm_x)
+            del caches
+            other[f"c2_shape_{name}"] = decode_summary(
+                f"{name.upper()}-KV decode at the BASELINE config-2 shape", ms, nbytes,
+                {"batch": 32, "q_heads": 32, "kv_heads": 8, "head_dim": 128, "context": 8192,
+                 "timed": "whole call (split-K decode + combine)"})
+            log(f"{name}: {ms * 1e3:.2f} us/call")
+            torch.cuda.empty_cache()
     if want("ra"):
         log("fused RoPE + FP8 append: prefill shape (config 4) and one decode step (config 2)")
         other["ra_prefill_c4"] = rope_append_case(cq, dev, stream, cq.FP8, 4, 32, 8, 128, 4096,

@@ -20,8 +20,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libcqkv.so")
 
 # formats: the reference's kernel mode ids (candle-core/src/accel/formats.rs:41-48)
-TURBO4, MXFP4, FP8 = 0, 2, 5
-FORMAT_NAMES = {"fp8": FP8, "mxfp4": MXFP4, "turbo4": TURBO4}
+TURBO4, MXFP4, NVFP4, MXFP8, FP8 = 0, 2, 3, 4, 5
+FORMAT_NAMES = {"fp8": FP8, "mxfp4": MXFP4, "turbo4": TURBO4, "nvfp4": NVFP4, "mxfp8": MXFP8}
 BF16, F16, F32 = 0, 1, 2
 # rotary layouts: rope (halves) and rope_i (interleaved) of candle-nn/src/rotary_emb.rs
 ROPE_HALVES, ROPE_INTERLEAVED = 1, 2
@@ -437,7 +437,7 @@ def turbo_signs(head_dim: int, seed: int):
 # ------------------------------------------------------------------------------------------
 class TurboKvCache:
     """A quantized KV cache of fixed capacity for (batch, kv_heads, head_dim), keys and values
-    in `key_format` / `value_format` (FP8, MXFP4 or TURBO4; TurboQuant seeds: keys `seed`,
+    in `key_format` / `value_format` (FP8, MXFP4, MXFP8, NVFP4 or TURBO4; TurboQuant seeds: keys `seed`,
     values `seed + 2` as TurboKvCache::with_formats does)."""
 
     def __init__(self, key_format: int, value_format: int, batch: int, kv_heads: int,

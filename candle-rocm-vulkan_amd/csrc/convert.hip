@@ -5,6 +5,9 @@
 //   MXFP4  D/8 code words (nibble j = element j), ceil(D/32 / 4) aux words (byte b = E8M0 of
 //          block b), rsc0 = 1.0, rsc1 = 0
 //   TURBO4 D/8 code words, rsc0 = f32 norm, rsc1 = 0
+//   MXFP8  D/4 code words, ceil(D/32 / 4) aux words (E8M0 bytes), rsc0 = 1.0, rsc1 = 0
+//   NVFP4  D/8 code words, ceil(D/16 / 4) aux words (E4M3 block scales), rsc0 = f32 global
+//          scale, rsc1 = 0
 // One wavefront per 8-token tile of a (batch, head) plane; lane l owns elements 2l, 2l+1, so
 // the value tiles are read and written whole by one lane (no cross-lane read-modify-write).
 #include "cqkv_device.h"
@@ -17,6 +20,10 @@ struct ConvertArgs {
     uint8_t *codes, *scales;
     uint32_t codes_plane, scales_plane;
     int32_t kv_heads, tokens, position, row_words, format, is_value, head_dim;
+    int32_t b8;           // 8-bit codes (FP8, MXFP8), else 4-bit
+    int32_t nblk;         // block scale bytes per token (MX, NVFP4), else 0
+    int32_t tok_scale;    // an f32 per token (FP8, TURBO4, NVFP4), after the block bytes
+    int32_t capacity;
 };
 
 template <bool EXPORT>
@@ -27,12 +34,13 @@ __global__ __launch_bounds__(64) void convert_kernel(ConvertArgs a) {
     const int t_lo = max(tile * 8, a.position), t_hi = min(tile * 8 + 8, a.position + a.tokens);
     if (t_lo >= t_hi) return;
     const bool active = lane < D / 2;
-    const bool fp8 = a.format == CQKV_FMT_FP8;
+    const bool fp8 = a.b8 != 0;  // 8-bit code layout
     const int64_t plane = (int64_t)b * a.kv_heads + h;
     uint8_t *codes = a.codes + plane * a.codes_plane;
     uint8_t *scales = a.scales + plane * a.scales_plane;
     const int code_words = fp8 ? D / 4 : D / 8;
-    const int aux_words = a.format == CQKV_FMT_MXFP4 ? (D / 32 + 3) / 4 : 0;
+    const int nb = a.nblk, aux_words = (nb + 3) / 4;
+    float *tscale = (float *)(scales + (int64_t)a.capacity * nb);
 
     // value tile words of this lane (elements 2l, 2l+1)
     uint64_t vw0 = 0, vw1 = 0;
@@ -106,22 +114,15 @@ __global__ __launch_bounds__(64) void convert_kernel(ConvertArgs a) {
             uint32_t *aux = row + code_words;
             uint32_t *rsc = aux + aux_words;
             if (EXPORT) {
-                if (a.format == CQKV_FMT_MXFP4) {
-                    for (int w = 0; w < aux_words; ++w) aux[w] = 0;
-                    for (int k = 0; k < D / 32; ++k)
-                        aux[k >> 2] |= (uint32_t)scales[(int64_t)t * (D / 32) + k] << (8 * (k & 3));
-                    rsc[0] = __float_as_uint(1.0f);
-                } else {
-                    rsc[0] = ((const uint32_t *)scales)[t];
-                }
+                for (int w = 0; w < aux_words; ++w) aux[w] = 0;
+                for (int k = 0; k < nb; ++k)
+                    aux[k >> 2] |= (uint32_t)scales[(int64_t)t * nb + k] << (8 * (k & 3));
+                rsc[0] = a.tok_scale ? __float_as_uint(tscale[t]) : __float_as_uint(1.0f);
                 rsc[1] = 0;
             } else {
-                if (a.format == CQKV_FMT_MXFP4) {
-                    for (int k = 0; k < D / 32; ++k)
-                        scales[(int64_t)t * (D / 32) + k] = (uint8_t)(aux[k >> 2] >> (8 * (k & 3)));
-                } else {
-                    ((uint32_t *)scales)[t] = rsc[0];
-                }
+                for (int k = 0; k < nb; ++k)
+                    scales[(int64_t)t * nb + k] = (uint8_t)(aux[k >> 2] >> (8 * (k & 3)));
+                if (a.tok_scale) tscale[t] = __uint_as_float(rsc[0]);
             }
         }
     }
@@ -158,6 +159,10 @@ static int convert(const cqkv_side *side, uint32_t *rows, int32_t batch, int32_t
     a.position = position;
     a.row_words = cqkv_reference_row_words(side->format, side->head_dim);
     a.format = side->format;
+    a.b8 = code_bits(side->format) == 8 ? 1 : 0;
+    a.nblk = block_elems(side->format) ? side->head_dim / block_elems(side->format) : 0;
+    a.tok_scale = token_scale(side->format) ? 1 : 0;
+    a.capacity = side->capacity;
     a.is_value = side->is_value;
     a.head_dim = side->head_dim;
     dim3 grid((tokens + 7) / 8 + 1, side->kv_heads, batch);

@@ -27,11 +27,26 @@ int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 // Code bits per element, or 0 for an unknown format.
 inline int code_bits(int32_t format) {
     switch (format) {
-    case CQKV_FMT_FP8: return 8;
+    case CQKV_FMT_FP8:
+    case CQKV_FMT_MXFP8: return 8;
     case CQKV_FMT_MXFP4:
+    case CQKV_FMT_NVFP4:
     case CQKV_FMT_TURBO4: return 4;
     default: return 0;
     }
+}
+
+// Elements per block scale (MX: E8M0 per 32, NVFP4: E4M3 per 16), 0 without block scales.
+inline int block_elems(int32_t format) {
+    return format == CQKV_FMT_MXFP4 || format == CQKV_FMT_MXFP8 ? 32
+           : format == CQKV_FMT_NVFP4                           ? 16
+                                                                : 0;
+}
+
+// Formats with an f32 scale per token (FP8 absmax/448, TurboQuant norm, NVFP4 global scale);
+// in the scales plane it follows the block-scale bytes of all `capacity` tokens.
+inline bool token_scale(int32_t format) {
+    return format == CQKV_FMT_FP8 || format == CQKV_FMT_TURBO4 || format == CQKV_FMT_NVFP4;
 }
 
 inline bool supported_dim(int32_t d) { return d == 64 || d == 128; }

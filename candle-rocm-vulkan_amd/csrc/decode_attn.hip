@@ -99,10 +99,14 @@ __device__ inline void fwht_pairs_dec(float &v0, float &v1, int lane) {
 
 __device__ inline bool sign_bit(const uint32_t *bits, int j) { return (bits[j >> 5] >> (j & 31)) & 1u; }
 
+// Byte codes (FP8, MXFP8) or nibbles (MXFP4, NVFP4, TURBO4).
+template <int FMT>
+constexpr bool is8() { return FMT == CQKV_FMT_FP8 || FMT == CQKV_FMT_MXFP8; }
+
 // Head dim held in k-slot e of MFMA chunk j by lane group g (the same for K and Q operands).
 template <int FMT, int D>
 __device__ inline int qdim(int j, int g, int e) {
-    if constexpr (FMT == CQKV_FMT_FP8) return 64 * (j >> 1) + 16 * g + 8 * (j & 1) + e;
+    if constexpr (is8<FMT>()) return 64 * (j >> 1) + 16 * g + 8 * (j & 1) + e;
     else return (D / 4) * g + 8 * j + e;
 }
 
@@ -111,24 +115,30 @@ __device__ inline int qdim(int j, int g, int e) {
 // ---------------------------------------------------------------------------------------------
 template <int FMT, int D>
 struct Tile {
-    // keys: 2 sub-tiles x D/32 code words (FP8: D/32 words = 4 per 16-key row chunk pair)
-    uint32_t k[2][FMT == CQKV_FMT_FP8 ? D / 16 : D / 32];
-    // values: D/32 chunks of 2 head dims x 8 keys (FP8 4 words, 4-bit 2 words)
-    uint32_t v[D / 32][FMT == CQKV_FMT_FP8 ? 4 : 2];
-    uint32_t kscale[2];  // per sub-tile, this lane's key: MXFP4 E8M0 block byte, FP8 f32 scale
-    uint32_t ks, vs;     // key lane % 32: TURBO4 norms, FP8 value scale, MXFP4 value block bytes
+    // keys: 2 sub-tiles x D/32 code words (byte codes: D/16 words, 4 per 16-key row chunk pair)
+    uint32_t k[2][is8<FMT>() ? D / 16 : D / 32];
+    // values: D/32 chunks of 2 head dims x 8 keys (byte codes 4 words, 4-bit 2 words)
+    uint32_t v[D / 32][is8<FMT>() ? 4 : 2];
+    // per sub-tile, this lane's key: FP8 f32 scale; MXFP4 its E8M0 block byte; MXFP8 all its
+    // E8M0 block bytes; NVFP4 the E4M3 block bytes of its 32 (D=128) / 16 (D=64) head dims
+    uint32_t kscale[2];
+    uint32_t ktok[2];  // NVFP4: the key's f32 scale
+    // key lane % 32: TURBO4 norms, FP8 value scale, MX value block bytes, NVFP4 value block
+    // bytes (vs, vs2: D/16 bytes) and f32 scale (vtok)
+    uint32_t ks, vs, vs2, vtok;
 };
 
 template <int FMT, int D>
 __device__ inline void load_tile(Tile<FMT, D> &r, int tile, bool live, int lane, rsrc_t kr,
-                                 rsrc_t ksr, rsrc_t vr, rsrc_t vsr) {
+                                 rsrc_t ksr, rsrc_t vr, rsrc_t vsr, uint32_t ktok_off,
+                                 uint32_t vtok_off) {
     const int n = lane & 15, g = lane >> 4;
     const uint32_t t0 = (uint32_t)tile * 32u;
     const uint32_t oob = live ? 0u : kOOB;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
         const uint32_t key = t0 + 8 * (n >> 2) + 4 * s + (n & 3);
-        if constexpr (FMT == CQKV_FMT_FP8) {
+        if constexpr (is8<FMT>()) {
 #pragma unroll
             for (int i = 0; i < D / 64; ++i) {
                 const u32x4 w = ld128_stream(kr, (key * D + 16 * g + 64 * i) | oob);
@@ -137,7 +147,12 @@ __device__ inline void load_tile(Tile<FMT, D> &r, int tile, bool live, int lane,
                 r.k[s][4 * i + 2] = w.z;
                 r.k[s][4 * i + 3] = w.w;
             }
-            r.kscale[s] = ld32(ksr, (key * 4) | oob);
+            if constexpr (FMT == CQKV_FMT_FP8)
+                r.kscale[s] = ld32(ksr, (key * 4) | oob);
+            else if constexpr (D == 128)
+                r.kscale[s] = ld32(ksr, (key * 4) | oob);
+            else
+                r.kscale[s] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(ksr, (key * 2) | oob, 0, 0);
         } else {
             if constexpr (D == 128) {
                 const u32x4 w = ld128_stream(kr, (key * 64 + 16 * g) | oob);
@@ -153,11 +168,19 @@ __device__ inline void load_tile(Tile<FMT, D> &r, int tile, bool live, int lane,
             if constexpr (FMT == CQKV_FMT_MXFP4)
                 r.kscale[s] = __builtin_amdgcn_raw_buffer_load_b8(
                     ksr, (key * (D / 32) + (D == 128 ? g : g >> 1)) | oob, 0, 0);
+            if constexpr (FMT == CQKV_FMT_NVFP4) {
+                if constexpr (D == 128)
+                    r.kscale[s] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
+                        ksr, (key * 8 + 2 * g) | oob, 0, 0);
+                else
+                    r.kscale[s] = __builtin_amdgcn_raw_buffer_load_b8(ksr, (key * 4 + g) | oob, 0, 0);
+                r.ktok[s] = ld32(ksr, (ktok_off + key * 4) | oob);
+            }
         }
     }
 #pragma unroll
     for (int u = 0; u < D / 32; ++u) {
-        if constexpr (FMT == CQKV_FMT_FP8) {
+        if constexpr (is8<FMT>()) {
             const u32x4 w = ld128_stream(vr, (((t0 / 8 + g) * D + 32 * u + 2 * n) * 8) | oob);
             r.v[u][0] = w.x;
             r.v[u][1] = w.y;
@@ -170,9 +193,18 @@ __device__ inline void load_tile(Tile<FMT, D> &r, int tile, bool live, int lane,
         }
     }
     const uint32_t kl = t0 + (lane & 31);
-    if constexpr (FMT == CQKV_FMT_MXFP4) {
+    if constexpr (FMT == CQKV_FMT_MXFP4 || FMT == CQKV_FMT_MXFP8) {
         r.vs = D == 128 ? ld32(vsr, (kl * 4) | oob)
                         : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(vsr, (kl * 2) | oob, 0, 0);
+    } else if constexpr (FMT == CQKV_FMT_NVFP4) {
+        if constexpr (D == 128) {
+            const u32x2 w = ld64(vsr, (kl * 8) | oob);
+            r.vs = w.x;
+            r.vs2 = w.y;
+        } else {
+            r.vs = ld32(vsr, (kl * 4) | oob);
+        }
+        r.vtok = ld32(vsr, (vtok_off + kl * 4) | oob);
     } else if constexpr (FMT == CQKV_FMT_FP8) {
         r.vs = ld32(vsr, (kl * 4) | oob);
     } else {
@@ -234,6 +266,48 @@ __device__ inline float e8m0_scale(uint32_t code) {  // code 0 marks an all-zero
     return code == 0 ? 0.0f : __uint_as_float(code << 23);
 }
 
+// NVFP4: 8 E2M1 codes of one word times the scale sg = fl(cs * gs) of their (token, block):
+// the E4M3 block scale cs times the token's f32 scale gs, rounded once per block, then one
+// multiply per element before the bf16 rounding. The reference's dequantized cache rounds
+// fl(fl(fp4 * cs) * gs) instead (RowCodec::elem times rsc0, turbo.rs:383-395): the two agree
+// except where the f32 values straddle a bf16 rounding boundary (one bf16 ulp, rarely). The codes
+// are converted unscaled: the conversion's own scale operand is meant for the E8M0 powers of
+// two of the MX formats, not for E4M3 values.
+__device__ inline bf16x8 nvfp4x8_bf16x8(uint32_t w, float sg) {
+    u32x4 r;
+    uint32_t *rp = (uint32_t *)&r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f32x2 f;
+        switch (i) {  // the selector must be an immediate
+        case 0: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0); break;
+        case 1: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1); break;
+        case 2: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2); break;
+        default: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3); break;
+        }
+        rp[i] = pack_bf16x2(f.x * sg, f.y * sg);
+    }
+    return __builtin_bit_cast(bf16x8, r);
+}
+
+// The same for 8 codes of 8 keys, key e scaled by sg[e].
+__device__ inline bf16x8 nvfp4x8_keys_bf16x8(uint32_t w, const float *sg) {
+    u32x4 r;
+    uint32_t *rp = (uint32_t *)&r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f32x2 f;
+        switch (i) {
+        case 0: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0); break;
+        case 1: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1); break;
+        case 2: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2); break;
+        default: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3); break;
+        }
+        rp[i] = pack_bf16x2(f.x * sg[2 * i], f.y * sg[2 * i + 1]);
+    }
+    return __builtin_bit_cast(bf16x8, r);
+}
+
 template <int FMT, int D>
 __device__ inline void compute_tile(Tile<FMT, D> &cur, int tile, const DecodeArgs &a,
                                     const op_t<FMT> *qhi, const op_t<FMT> *qlo, bool q_split, int lane,
@@ -255,6 +329,22 @@ __device__ inline void compute_tile(Tile<FMT, D> &cur, int tile, const DecodeArg
         if constexpr (FMT == CQKV_FMT_FP8) {
             k0 = fp8x8_scaled_bf16x8(cur.k[0][2 * j], cur.k[0][2 * j + 1], __uint_as_float(cur.kscale[0]));
             k1 = fp8x8_scaled_bf16x8(cur.k[1][2 * j], cur.k[1][2 * j + 1], __uint_as_float(cur.kscale[1]));
+        } else if constexpr (FMT == CQKV_FMT_MXFP8) {
+            // chunk j holds head dims 64 (j >> 1) + 16 g + 8 (j & 1) + e: block 2 (j >> 1) + g / 2
+            const int bi = 2 * (j >> 1) + (g >> 1);
+            const float sc0 = e8m0_scale((cur.kscale[0] >> (8 * bi)) & 0xffu);
+            const float sc1 = e8m0_scale((cur.kscale[1] >> (8 * bi)) & 0xffu);
+            k0 = fp8x8_scaled_bf16x8(cur.k[0][2 * j], cur.k[0][2 * j + 1], sc0);
+            k1 = fp8x8_scaled_bf16x8(cur.k[1][2 * j], cur.k[1][2 * j + 1], sc1);
+        } else if constexpr (FMT == CQKV_FMT_NVFP4) {
+            // chunk j holds head dims (D/4) g + 8 j + e: the lane's block byte j / 2 (D = 128)
+            const int bi = D == 128 ? (j >> 1) : 0;
+            const float sg0 = __builtin_amdgcn_cvt_f32_fp8(cur.kscale[0] >> (8 * bi), 0) *
+                              __uint_as_float(cur.ktok[0]);
+            const float sg1 = __builtin_amdgcn_cvt_f32_fp8(cur.kscale[1] >> (8 * bi), 0) *
+                              __uint_as_float(cur.ktok[1]);
+            k0 = nvfp4x8_bf16x8(cur.k[0][j], sg0);
+            k1 = nvfp4x8_bf16x8(cur.k[1][j], sg1);
         } else {
             float sc0 = 1.0f, sc1 = 1.0f;
             if constexpr (FMT == CQKV_FMT_MXFP4) {
@@ -312,7 +402,7 @@ __device__ inline void compute_tile(Tile<FMT, D> &cur, int tile, const DecodeArg
     if (t0 + 32 > L) {  // uniform: only the tile holding the end of the keys
 #pragma unroll
         for (int u = 0; u < NCH; ++u) {
-            if constexpr (FMT == CQKV_FMT_FP8) {
+            if constexpr (is8<FMT>()) {
                 const uint64_t keep = nv == 0 ? 0ull : (~0ull >> (64 - 8 * nv));
                 const uint64_t w0 = (((uint64_t)cur.v[u][1] << 32) | cur.v[u][0]) & keep;
                 const uint64_t w1 = (((uint64_t)cur.v[u][3] << 32) | cur.v[u][2]) & keep;
@@ -357,15 +447,28 @@ __device__ inline void compute_tile(Tile<FMT, D> &cur, int tile, const DecodeArg
             acc[2 * u + 1] = mfma16x16x32(v1, pb, acc[2 * u + 1]);
         }
     } else {
+        // FP8 / MXFP8 / NVFP4: the value scales are inside the V operand (rounded to bf16 as the
+        // reference's dequantized cache), P goes in full precision as a bf16 hi + lo pair.
+        // TURBO4: the norm goes into P.
         float pv[8], sv[8];
+        uint32_t vw[8], vw2[8];  // MX / NVFP4: the keys' block scale bytes
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            sv[e] = __uint_as_float((uint32_t)__shfl((int)cur.vs, 8 * g + e));
-            if (e >= nv) sv[e] = 0.0f;  // scales past the written length may be any bits
-            if constexpr (FMT == CQKV_FMT_FP8)  // the value scale is inside the V operand
-                pv[e] = (e < nv && p[e] > 0.0f) ? p[e] : 0.0f;
-            else
+            // scales past the written length may be any bits
+            vw[e] = e < nv ? (uint32_t)__shfl((int)cur.vs, 8 * g + e) : 0u;
+            sv[e] = __uint_as_float(vw[e]);  // FP8 scale, TURBO4 norm
+            if constexpr (FMT == CQKV_FMT_NVFP4)
+                vw2[e] = D == 128 && e < nv ? (uint32_t)__shfl((int)cur.vs2, 8 * g + e) : 0u;
+            if constexpr (FMT == CQKV_FMT_TURBO4)
                 pv[e] = (e < nv && p[e] > 0.0f) ? p[e] * sv[e] : 0.0f;
+            else
+                pv[e] = (e < nv && p[e] > 0.0f) ? p[e] : 0.0f;
+        }
+        float gk[8];  // NVFP4: the keys' f32 scales
+        if constexpr (FMT == CQKV_FMT_NVFP4) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                gk[e] = e < nv ? __uint_as_float((uint32_t)__shfl((int)cur.vtok, 8 * g + e)) : 0.0f;
         }
         op_t<FMT> phi, plo;
         split8(pv, phi, plo);
@@ -375,6 +478,26 @@ __device__ inline void compute_tile(Tile<FMT, D> &cur, int tile, const DecodeArg
             if constexpr (FMT == CQKV_FMT_FP8) {
                 v0 = fp8x8_scaled_bf16x8(cur.v[u][0], cur.v[u][1], sv);
                 v1 = fp8x8_scaled_bf16x8(cur.v[u][2], cur.v[u][3], sv);
+            } else if constexpr (FMT == CQKV_FMT_MXFP8) {
+                // rows 32u + 2r + h: block u of every key
+                float su[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    su[e] = e8m0_scale((vw[e] >> (8 * u)) & 0xffu);
+                v0 = fp8x8_scaled_bf16x8(cur.v[u][0], cur.v[u][1], su);
+                v1 = fp8x8_scaled_bf16x8(cur.v[u][2], cur.v[u][3], su);
+            } else if constexpr (FMT == CQKV_FMT_NVFP4) {
+                // this lane's rows 32u + 2n + h lie in block 2u + n / 8 of every key
+                const int bi = 2 * u + ((lane & 15) >> 3);
+                float sg[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t w = bi < 4 ? vw[e] : vw2[e];
+                    sg[e] = __builtin_amdgcn_cvt_f32_fp8(w >> (8 * (bi & 3)), 0) * gk[e];
+                    if (e >= nv) sg[e] = 0.0f;
+                }
+                v0 = nvfp4x8_keys_bf16x8(cur.v[u][0], sg);
+                v1 = nvfp4x8_keys_bf16x8(cur.v[u][1], sg);
             } else {
                 v0 = decode8<FMT>(cur.v[u][0], 0, 1.0f, tab);
                 v1 = decode8<FMT>(cur.v[u][1], 0, 1.0f, tab);
@@ -495,6 +618,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     const rsrc_t ksr = make_rsrc(ks + plane * ks_plane, ks_plane);
     const rsrc_t vr = make_rsrc(vc + plane * vc_plane, vc_plane);
     const rsrc_t vsr = make_rsrc(vs + plane * vs_plane, vs_plane);
+    // NVFP4: the per-token f32 scales follow the block bytes of all the plane's tokens
+    uint32_t ktok_off = 0, vtok_off = 0;
+    if constexpr (FMT == CQKV_FMT_NVFP4) {
+        ktok_off = ks_plane / (D / 16 + 4) * (D / 16);
+        vtok_off = vs_plane / (D / 16 + 4) * (D / 16);
+    }
 
     f32x4 acc[2 * NCH];
 #pragma unroll
@@ -506,21 +635,21 @@ __global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs a) {
     // issued before the next set's, so each wait only covers the set about to be used.
     Tile<FMT, D> ta, tb2;
     int t = tb + wave;
-    load_tile<FMT, D>(ta, t, t < te, lane, kr, ksr, vr, vsr);
+    load_tile<FMT, D>(ta, t, t < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
     __builtin_amdgcn_sched_barrier(0);
-    load_tile<FMT, D>(tb2, t + WAVES, t + WAVES < te, lane, kr, ksr, vr, vsr);
+    load_tile<FMT, D>(tb2, t + WAVES, t + WAVES < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
     __builtin_amdgcn_sched_barrier(0);
     for (; t < te; t += 2 * WAVES) {
         compute_tile<FMT, D>(ta, t, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min, Lb, koff, tab,
                              m_run, l_run, acc);
         __builtin_amdgcn_sched_barrier(0);
-        load_tile<FMT, D>(ta, t + 2 * WAVES, t + 2 * WAVES < te, lane, kr, ksr, vr, vsr);
+        load_tile<FMT, D>(ta, t + 2 * WAVES, t + 2 * WAVES < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
         __builtin_amdgcn_sched_barrier(0);
         if (t + WAVES < te)
             compute_tile<FMT, D>(tb2, t + WAVES, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min,
                                  Lb, koff, tab, m_run, l_run, acc);
         __builtin_amdgcn_sched_barrier(0);
-        load_tile<FMT, D>(tb2, t + 3 * WAVES, t + 3 * WAVES < te, lane, kr, ksr, vr, vsr);
+        load_tile<FMT, D>(tb2, t + 3 * WAVES, t + 3 * WAVES < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
         __builtin_amdgcn_sched_barrier(0);
     }
 
@@ -672,7 +801,9 @@ static int auto_splits(int batch, int kv_heads, int kv_len, bool ragged, int wav
 // Wavefronts per workgroup: 8 for FP8 (HBM-bound: one workgroup per plane fills a CU), 4 for
 // the 4-bit formats (their decode is VALU-heavy; two or three independent workgroups per CU
 // hide each other's latencies better than one of 8 wavefronts: 10 % faster on BASELINE config 3).
-constexpr int waves_of(int format) { return format == CQKV_FMT_FP8 ? kWaves : 4; }
+constexpr int waves_of(int format) {
+    return format == CQKV_FMT_FP8 || format == CQKV_FMT_MXFP8 ? kWaves : 4;
+}
 
 template <int FMT>
 static void launch_decode(int d, dim3 grid, hipStream_t st, const DecodeArgs &a) {
@@ -773,6 +904,8 @@ static hipError_t decode_launch(const DecodeArgs &a, int format, int d, hipStrea
     switch (format) {
     case CQKV_FMT_FP8: launch_decode<CQKV_FMT_FP8>(d, grid, st, a); break;
     case CQKV_FMT_MXFP4: launch_decode<CQKV_FMT_MXFP4>(d, grid, st, a); break;
+    case CQKV_FMT_MXFP8: launch_decode<CQKV_FMT_MXFP8>(d, grid, st, a); break;
+    case CQKV_FMT_NVFP4: launch_decode<CQKV_FMT_NVFP4>(d, grid, st, a); break;
     default: launch_decode<CQKV_FMT_TURBO4>(d, grid, st, a); break;
     }
     hipError_t e = hipGetLastError();

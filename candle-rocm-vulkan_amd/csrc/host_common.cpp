@@ -156,15 +156,17 @@ size_t cqkv_codes_plane_bytes(int32_t format, int32_t head_dim, int32_t capacity
 
 size_t cqkv_scales_plane_bytes(int32_t format, int32_t head_dim, int32_t capacity) {
     if (!cqkv::code_bits(format) || !cqkv::supported_dim(head_dim) || capacity <= 0) return 0;
-    if (format == CQKV_FMT_MXFP4) return (size_t)capacity * (size_t)(head_dim / 32);
-    return (size_t)capacity * 4;
+    const int be = cqkv::block_elems(format);
+    const size_t blocks = be ? (size_t)capacity * (size_t)(head_dim / be) : 0;
+    return blocks + (cqkv::token_scale(format) ? (size_t)capacity * 4 : 0);
 }
 
 int32_t cqkv_reference_row_words(int32_t format, int32_t head_dim) {
     const int bits = cqkv::code_bits(format);
     if (!bits || !cqkv::supported_dim(head_dim)) return 0;
     const int code_words = (head_dim * bits + 31) / 32;
-    const int aux_words = format == CQKV_FMT_MXFP4 ? (head_dim / 32 + 3) / 4 : 0;
+    const int be = cqkv::block_elems(format);
+    const int aux_words = be ? (head_dim / be + 3) / 4 : 0;  // formats.rs:229-233
     return code_words + aux_words + 2;
 }
 

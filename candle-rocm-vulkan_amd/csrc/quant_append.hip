@@ -1,4 +1,4 @@
-// KV quantize-and-append into the FP8 / MXFP4 / TURBO4 cache layouts (gfx950).
+// KV quantize-and-append into the FP8 / MXFP4 / MXFP8 / NVFP4 / TURBO4 cache layouts (gfx950).
 //
 // Reference behaviour (paths relative to the reference repository root):
 //   RowCodec::quantize_row, candle-core/src/accel/turbo.rs:293-381 (FP8 366-374, MX 324-347,
@@ -192,6 +192,7 @@ __device__ inline void append_tile(const AppendArgs &a, int h, int b, int bx, in
     uint32_t new_mask = 0;          // tokens of this tile written by this call (bit t % 8)
 
     const bool pair = W16 || a.pair_loads != 0, cs_pair = W16 || a.cs_pair_loads != 0;
+    constexpr bool kB8 = FMT == CQKV_FMT_FP8 || FMT == CQKV_FMT_MXFP8;  // byte codes
     // encodes one token (x0, x1) at cache position t, tile slot `slot`
     auto encode = [&](float x0, float x1, int t, int slot) {
         uint32_t c0, c1;
@@ -204,13 +205,33 @@ __device__ inline void append_tile(const AppendArgs &a, int h, int b, int bx, in
             c0 = c01 & 0xffu;
             c1 = c01 >> 8;
             row_scale = s;
-        } else if constexpr (FMT == CQKV_FMT_MXFP4) {
+        } else if constexpr (FMT == CQKV_FMT_MXFP4 || FMT == CQKV_FMT_MXFP8) {
+            // E8M0 per 32 elements: floor_log2(amax) - emax of the element format (turbo.rs:324-347)
+            constexpr bool kFp4 = FMT == CQKV_FMT_MXFP4;
             const float amax = group_max(fmaxf(__builtin_fabsf(x0), __builtin_fabsf(x1)), 16);
-            const uint32_t sc = mx_scale_code(amax, 2);
+            const uint32_t sc = mx_scale_code(amax, kFp4 ? 2 : 8);
             const float scale = e8m0_to_f32(sc);
-            c0 = sc == 0 ? 0u : fp4_encode(x0 / scale);
-            c1 = sc == 0 ? 0u : fp4_encode(x1 / scale);
+            if constexpr (kFp4) {
+                c0 = sc == 0 ? 0u : fp4_encode(x0 / scale);
+                c1 = sc == 0 ? 0u : fp4_encode(x1 / scale);
+            } else {
+                c0 = sc == 0 ? 0u : e4m3_encode(x0 / scale);
+                c1 = sc == 0 ? 0u : e4m3_encode(x1 / scale);
+            }
             if (active && (lane & 15) == 0) scales[(int64_t)t * (D / 32) + lane / 16] = (uint8_t)sc;
+        } else if constexpr (FMT == CQKV_FMT_NVFP4) {
+            // g = row absmax / 2688 (= 448 * 6); per 16 elements an E4M3 scale of bmax / 6 / g;
+            // codes E2M1 of x / (e4m3(cs) * g) (turbo.rs:348-365)
+            const float ax = fmaxf(__builtin_fabsf(x0), __builtin_fabsf(x1));
+            const float amax = wave_max(ax);
+            const float gs = amax > 0.0f ? amax / 2688.0f : 1.0f;
+            const float bmax = group_max(ax, 8);
+            const uint32_t cs = e4m3_encode(bmax / 6.0f / gs);
+            const float eff = __builtin_amdgcn_cvt_f32_fp8(cs, 0) * gs;
+            c0 = eff > 0.0f ? fp4_encode(x0 / eff) : 0u;
+            c1 = eff > 0.0f ? fp4_encode(x1 / eff) : 0u;
+            if (active && (lane & 7) == 0) scales[(int64_t)t * (D / 16) + lane / 8] = (uint8_t)cs;
+            row_scale = gs;
         } else {  // TURBO4: y = H (sign * x) / sqrt(D), norm, codebook index of y / norm
             const int j0 = 2 * lane, j1 = 2 * lane + 1;
             if (active) {
@@ -232,18 +253,20 @@ __device__ inline void append_tile(const AppendArgs &a, int h, int b, int bx, in
             }
             row_scale = norm;
         }
-        if constexpr (FMT != CQKV_FMT_MXFP4) {
-            if (lane == 0) ((float *)scales)[t] = row_scale;
+        if constexpr (FMT == CQKV_FMT_FP8 || FMT == CQKV_FMT_TURBO4 || FMT == CQKV_FMT_NVFP4) {
+            // the per-token f32 follows the block bytes of all `capacity` tokens
+            constexpr int kBlockBytes = FMT == CQKV_FMT_NVFP4 ? D / 16 : 0;
+            if (lane == 0) ((float *)(scales + (int64_t)a.capacity * kBlockBytes))[t] = row_scale;
         }
         new_mask |= 1u << slot;
         if (!active) return;
         if constexpr (!IS_VALUE) {
-            if constexpr (FMT == CQKV_FMT_FP8)
+            if constexpr (kB8)
                 *(uint16_t *)(codes + (int64_t)t * D + 2 * lane) = (uint16_t)(c0 | (c1 << 8));
             else
                 codes[(int64_t)t * (D / 2) + lane] = (uint8_t)(c0 | (c1 << 4));
         } else {
-            if constexpr (FMT == CQKV_FMT_FP8) {
+            if constexpr (kB8) {
                 vw0 |= (uint64_t)c0 << (8 * slot);
                 vw1 |= (uint64_t)c1 << (8 * slot);
             } else {
@@ -268,7 +291,7 @@ __device__ inline void append_tile(const AppendArgs &a, int h, int b, int bx, in
     }
     if constexpr (IS_VALUE) {
         if (!active) return;
-        if constexpr (FMT == CQKV_FMT_FP8) {
+        if constexpr (kB8) {
             uint64_t *dst = (uint64_t *)(codes + (int64_t)tile * D * 8 + 2 * lane * 8);
             if (new_mask != 0xffu) {  // keep the codes of tokens this call does not write
                 uint64_t keep = 0;
@@ -374,6 +397,8 @@ int quant_append_launch(const cqkv_side *side, const void *x, int32_t x_dtype,
     switch (side->format) {
     case CQKV_FMT_FP8: launch_append<CQKV_FMT_FP8>(side, grid, stream, a); break;
     case CQKV_FMT_MXFP4: launch_append<CQKV_FMT_MXFP4>(side, grid, stream, a); break;
+    case CQKV_FMT_MXFP8: launch_append<CQKV_FMT_MXFP8>(side, grid, stream, a); break;
+    case CQKV_FMT_NVFP4: launch_append<CQKV_FMT_NVFP4>(side, grid, stream, a); break;
     default: launch_append<CQKV_FMT_TURBO4>(side, grid, stream, a); break;
     }
     CQKV_HIP_CHECK(hipGetLastError());
@@ -652,6 +677,8 @@ extern "C" int cqkv_rope_quant_append(const cqkv_side *k_side, const cqkv_side *
     switch (k_side->format) {
     case CQKV_FMT_FP8: launch_rope_append_fmt<CQKV_FMT_FP8>(rope_kind, d, grid, st, r); break;
     case CQKV_FMT_MXFP4: launch_rope_append_fmt<CQKV_FMT_MXFP4>(rope_kind, d, grid, st, r); break;
+    case CQKV_FMT_MXFP8: launch_rope_append_fmt<CQKV_FMT_MXFP8>(rope_kind, d, grid, st, r); break;
+    case CQKV_FMT_NVFP4: launch_rope_append_fmt<CQKV_FMT_NVFP4>(rope_kind, d, grid, st, r); break;
     default: launch_rope_append_fmt<CQKV_FMT_TURBO4>(rope_kind, d, grid, st, r); break;
     }
     CQKV_HIP_CHECK(hipGetLastError());

@@ -42,6 +42,11 @@
  *   MXFP4 values  capacity * D/2    8-token tiles      capacity * D/32  E8M0
  *   TURBO4 keys   capacity * D/2    row-major nibbles  capacity * 4   f32 norm per token
  *   TURBO4 values capacity * D/2    8-token tiles      capacity * 4   f32 norm
+ *   MXFP8 keys    capacity * D      row-major          capacity * D/32  E8M0 per 32-element block
+ *   MXFP8 values  capacity * D      8-token tiles      capacity * D/32  E8M0
+ *   NVFP4 keys    capacity * D/2    row-major nibbles  capacity * D/16  E4M3 per 16-element block,
+ *                                                      then capacity * 4  f32 per token
+ *   NVFP4 values  capacity * D/2    8-token tiles      the same
  * Row-major: token t's codes at t * row_bytes, element j at byte j (FP8) or nibble j (bits 4(j%2)
  * of byte j/2), i.e. the reference's code stream. 8-token tiles (values): token t, element j at
  * tile t/8, offset j*8 + t%8 bytes (FP8) or bits 4(t%8) of the little-endian u32 j (4-bit). The
@@ -68,8 +73,17 @@ enum {
 };
 
 /* Cache formats: the reference's kernel mode ids (candle-core/src/accel/formats.rs:41-48).
- * TURBO4 = TurboQuant MSE, 4 bits, Hadamard rotation (QuantFormat::TurboMse{bits: 4}). */
-enum { CQKV_FMT_TURBO4 = 0, CQKV_FMT_MXFP4 = 2, CQKV_FMT_FP8 = 5 };
+ * TURBO4 = TurboQuant MSE, 4 bits, Hadamard rotation (QuantFormat::TurboMse{bits: 4});
+ * NVFP4 = E2M1 codes, an E4M3 scale per 16 elements and an f32 scale per token
+ * (QuantFormat::Nvfp4); MXFP8 = E4M3 codes with an E8M0 scale per 32 elements
+ * (QuantFormat::Mxfp8). */
+enum {
+    CQKV_FMT_TURBO4 = 0,
+    CQKV_FMT_MXFP4 = 2,
+    CQKV_FMT_NVFP4 = 3,
+    CQKV_FMT_MXFP8 = 4,
+    CQKV_FMT_FP8 = 5
+};
 
 /* Element types of q / k / v / outputs. */
 enum { CQKV_BF16 = 0, CQKV_F16 = 1, CQKV_F32 = 2 };

@@ -100,6 +100,9 @@ if __name__ == "__main__":
     quant_case("mxfp4_d64", O.MXFP4, 0, 64, 19, 14)
     quant_case("turbo4_d128", O.TURBO_MSE, 4, 128, 37, 15)
     quant_case("nvfp4_d128", O.NVFP4, 0, 128, 11, 16)
+    quant_case("nvfp4_d64", O.NVFP4, 0, 64, 19, 18)
+    quant_case("mxfp8_d128", O.MXFP8, 0, 128, 37, 17)
+    quant_case("mxfp8_d64", O.MXFP8, 0, 64, 19, 19)
     fa_case()
     attn_case()
     combine_case()

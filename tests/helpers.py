@@ -6,7 +6,7 @@ import torch
 
 from oracle import oracle as O
 
-BITS = {5: 0, 2: 0, 0: 4}  # oracle (mode, bits) of the cqkv formats FP8, MXFP4, TURBO4
+BITS = {5: 0, 2: 0, 0: 4, 3: 0, 4: 0}  # oracle (mode, bits): FP8, MXFP4, TURBO4, NVFP4, MXFP8
 
 
 def kv_source(seed: int, shape, outliers: bool = False) -> torch.Tensor:
@@ -81,7 +81,7 @@ def exact_decode(fmt: int, q: torch.Tensor, k_rows: np.ndarray, v_rows: np.ndarr
 
 
 def assert_decode_parity(fmt: int, got: np.ndarray, ref: np.ndarray, exact: np.ndarray | None):
-    """FP8 / MXFP4: the BASELINE tolerance against the reference path. TurboQuant: the same
+    """FP8 / MX / NVFP4: the BASELINE tolerance against the reference path. TurboQuant: the same
     tolerance against the exact value of the same codes, and against the reference path within
     that path's own deviation from the exact value (its bf16 rounding of the unrotated cache
     alone moves outputs by up to ~4e-2 on outlier-heavy inputs) plus the tolerance."""

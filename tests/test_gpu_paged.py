@@ -17,7 +17,7 @@ from tests.helpers import (assert_close_bf16, assert_decode_parity, exact_decode
 
 pytestmark = pytest.mark.gpu
 
-FMTS = {"fp8": 5, "mxfp4": 2, "turbo4": 0}
+FMTS = {"fp8": 5, "mxfp4": 2, "turbo4": 0, "nvfp4": 3, "mxfp8": 4}
 
 
 def export_np(cq, side, tokens):
@@ -73,7 +73,7 @@ def paged_case(cq, dev, fmt, b, hq, hkv, d, sizes, caps, lq=1, wl=-1, wr=-1, see
     return got
 
 
-@pytest.mark.parametrize("fmt", ["fp8", "mxfp4", "turbo4"])
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp4", "turbo4", "nvfp4", "mxfp8"])
 def test_paged_blocks_of_uneven_sizes(cq, dev, fmt):
     """Blocks of 100, 37, 0, 256 and 5 rows with capacities 128, 64, 32, 256 and 32: tiles that
     cross a block's valid end, an empty block, a block filling its capacity."""

@@ -16,7 +16,7 @@ from tests.helpers import (assert_close_bf16, assert_decode_parity, exact_decode
 
 pytestmark = pytest.mark.gpu
 
-FMTS = {"fp8": 5, "mxfp4": 2, "turbo4": 0}
+FMTS = {"fp8": 5, "mxfp4": 2, "turbo4": 0, "nvfp4": 3, "mxfp8": 4}
 
 
 def export_np(cq, side, tokens, position=0):
@@ -26,7 +26,7 @@ def export_np(cq, side, tokens, position=0):
 # ---------------------------------------------------------------------------------------------
 # quantize-and-append
 # ---------------------------------------------------------------------------------------------
-@pytest.mark.parametrize("fmt", ["fp8", "mxfp4"])
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp4", "mxfp8", "nvfp4"])
 @pytest.mark.parametrize("is_value", [False, True])
 @pytest.mark.parametrize("d", [64, 128])
 def test_append_codes_bit_exact(cq, dev, fmt, is_value, d):
@@ -47,7 +47,7 @@ def test_append_codes_bit_exact(cq, dev, fmt, is_value, d):
     np.testing.assert_array_equal(got, want)
 
 
-@pytest.mark.parametrize("fmt", ["fp8", "mxfp4"])
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp4", "mxfp8", "nvfp4"])
 @pytest.mark.parametrize("layout", ["f32", "f16", "bf16_odd_stride"])
 def test_append_input_dtypes_and_strides(cq, dev, fmt, layout):
     """f32 / f16 rows (paired loads of one 8- / 4-byte word) and bf16 rows whose element pairs
@@ -112,11 +112,12 @@ def test_append_turbo4_vs_reference_criterion(cq, dev, is_value, d):
     assert (np.abs(gc.astype(int) - wc.astype(int)) <= 1).all()
 
 
-def test_rows_import_export_roundtrip(cq, dev):
+@pytest.mark.parametrize("d", [64, 128])
+def test_rows_import_export_roundtrip(cq, dev, d):
     for f in FMTS.values():
         for is_value in (False, True):
-            rows = oracle_rows(f, kv_source(3, (2, 2, 45, 128)), 42)
-            side = cq.CacheSide.empty(f, is_value, 2, 2, 128, 64, dev, seed=42)
+            rows = oracle_rows(f, kv_source(3, (2, 2, 45, d)), 42)
+            side = cq.CacheSide.empty(f, is_value, 2, 2, d, 64, dev, seed=42)
             cq.rows_import(side, torch.from_numpy(rows.view(np.int32)).to(dev), 9)
             np.testing.assert_array_equal(export_np(cq, side, 45, 9), rows)
 
@@ -161,21 +162,21 @@ def test_decode_fp8_config1(cq, dev):
     assert_close_bf16(got, want)
 
 
-@pytest.mark.parametrize("fmt", ["mxfp4", "turbo4"])
+@pytest.mark.parametrize("fmt", ["mxfp4", "turbo4", "nvfp4", "mxfp8"])
 @pytest.mark.parametrize("d", [64, 128])
-def test_decode_4bit_small(cq, dev, fmt, d):
+def test_decode_block_formats_small(cq, dev, fmt, d):
     got, want = run_decode(cq, dev, fmt, 1, 8, 8, d, 512, outliers=True)
     assert_close_bf16(got, want)
 
 
-@pytest.mark.parametrize("fmt", ["fp8", "mxfp4", "turbo4"])
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp4", "turbo4", "nvfp4", "mxfp8"])
 @pytest.mark.parametrize("splits", [1, 3, 0])
 def test_decode_gqa_splits(cq, dev, fmt, splits):
     got, want = run_decode(cq, dev, fmt, 2, 16, 4, 128, 1000, splits=splits, outliers=True)
     assert_close_bf16(got, want)
 
 
-@pytest.mark.parametrize("fmt", ["fp8", "mxfp4", "turbo4"])
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp4", "turbo4", "nvfp4", "mxfp8"])
 def test_decode_split_invariance(cq, dev, fmt):
     """Changing the split count changes only the f32 summation order (the reference checks its
     dense split kernels against unsplit ones within 4e-6, candle-nn/tests/accel_rocm.rs:749-752).
@@ -189,7 +190,7 @@ def test_decode_split_invariance(cq, dev, fmt):
         np.testing.assert_allclose(o, outs[0], atol=atol, rtol=rtol)
 
 
-@pytest.mark.parametrize("fmt", ["fp8", "mxfp4", "turbo4"])
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp4", "turbo4", "nvfp4", "mxfp8"])
 def test_decode_ragged_lengths(cq, dev, fmt):
     lens = [1000, 1, 0, 33, 517]
     got, want = run_decode(cq, dev, fmt, 5, 8, 2, 128, 1000, kv_lens=lens, cap=1024)
@@ -197,7 +198,7 @@ def test_decode_ragged_lengths(cq, dev, fmt):
     assert (got[2] == 0).all()  # a sequence without keys gives zeros
 
 
-@pytest.mark.parametrize("fmt", ["fp8", "mxfp4", "turbo4"])
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp4", "turbo4", "nvfp4", "mxfp8"])
 @pytest.mark.parametrize("wl,wr", [(-1, 0), (5, 0), (40, 2), (-1, -1)])
 def test_decode_multi_query_windows(cq, dev, fmt, wl, wr):
     got, want = run_decode(cq, dev, fmt, 2, 8, 2, 64, 300, lq=3, wl=wl, wr=wr)

@@ -265,7 +265,8 @@ def test_codebook_close_to_gaussian_lloyd_max():
 # ---------------------------------------------------------------------------------------------
 # row codecs against the reference's own kernel (golden fixtures)
 # ---------------------------------------------------------------------------------------------
-@pytest.mark.parametrize("name", ["fp8_d128", "fp8_d80", "mxfp4_d128", "mxfp4_d64", "nvfp4_d128"])
+@pytest.mark.parametrize("name", ["fp8_d128", "fp8_d80", "mxfp4_d128", "mxfp4_d64", "nvfp4_d128",
+                                  "nvfp4_d64", "mxfp8_d128", "mxfp8_d64"])
 def test_quantize_rows_bit_exact_with_reference_kernel(name):
     g = gold(f"ref_quant_{name}")
     mode, bits = int(g["mode"]), int(g["bits"])
