@@ -20,11 +20,12 @@ host on a bounded sample of the same workload.
 "other_configs" reports BASELINE configs 3 (MXFP4, ragged), 4 (causal bf16 prefill with fused
 FP8 append) and 5 (TurboQuant-4, context 128K) with the same timing method; they are secondary
 figures, not the headline value. "c2_shape_mxfp8" / "c2_shape_nvfp4" time the decode of the
-other block-scaled formats at the config-2 shape; "ra_*" time the fused RoPE + FP8
+other block-scaled formats at the config-2 shape; "c4_shape_fp8_kv" the attention over E4M3
+K / V with descales at the config-4 shape; "ra_*" time the fused RoPE + FP8
 quantize-append at the config-4 prefill shape and at one config-2 decode step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
-                       [--only c2,c3,c4,c5,fx,ra] [--calibration-copy]
+                       [--only c2,c3,c4,c5,f8,fx,ra] [--calibration-copy]
 """
 from __future__ import annotations
 
@@ -230,6 +231,31 @@ def rope_append_case(cq, dev, stream, fmt, b, hq, hkv, d, t, cap, steps, warmup)
             "timed": timed}
 
 
+def fp8_attn_case(cq, dev, stream, steps, warmup):
+    """Causal attention over E4M3 K / V with per-tensor descales (flash_attn_fp8's attention):
+    the E4M3 -> bf16 staging pass plus the MFMA prefill, B=4 S=4096 32/8 heads D=128."""
+    import torch
+    B, S, HQ, HKV, D = 4, 4096, 32, 8, 128
+    q = kv_gpu((B, S, HQ, D), 41, dev, outliers=False)
+    k = kv_gpu((B, S, HKV, D), 42, dev)
+    v = kv_gpu((B, S, HKV, D), 43, dev)
+    k8, ks = cq.fp8_quantize_tensor(k)
+    v8, vs = cq.fp8_quantize_tensor(v)
+    out = torch.empty_like(q)
+
+    def step(i):
+        cq.flash_attn_fp8_codes(q, k8, v8, 1.0 / D ** 0.5, True, 1.0, 1.0, k_scale=ks,
+                                v_scale=vs, out=out)
+    ms = time_calls(step, steps, warmup, stream)
+    flops = 2 * B * HQ * S * S * D
+    return {"workload": "FP8 (E4M3) K / V causal attention with descales, config-4 shape",
+            "us_per_call": round(ms * 1e3, 2), "flop_per_call": flops,
+            "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+            "peak_tflops": BF16_PEAK_TFLOPS,
+            "frac": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4), "bound": "mfma",
+            "timed": "whole call: E4M3 -> bf16 staging, V transpose pre-pass, prefill kernel"}
+
+
 def decode_summary(name, ms, nbytes, extra):
     gbs = nbytes / (ms * 1e-3) / 1e9
     res = {"workload": name, "us_per_call": round(ms * 1e3, 2), "bytes_per_call": nbytes,
@@ -258,7 +284,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
-    ap.add_argument("--only", default="", help="comma list of c2,c3,c4,c5,fx,ra (default: all)")
+    ap.add_argument("--only", default="", help="comma list of c2,c3,c4,c5,f8,fx,ra (default: all)")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="also run a plain 1 GiB copy (for counter scaling)")
     args = ap.parse_args()
@@ -329,7 +355,8 @@ def main():
     if want("c4"):
         # MFMA-bound: give the clocks time to settle after the HBM-bound decode workloads
         log("config 4: causal prefill + fused FP8 append")
-        other["c4_prefill"] = prefill_case(cq, dev, stream, max(steps_x, 20), max(warm_x, 20))
+        # the MFMA clocks settle over the first ~100 calls: a longer untimed warm-up
+        other["c4_prefill"] = prefill_case(cq, dev, stream, max(steps_x, 20), max(warm_x, 80))
         log(f"config 4: {other['c4_prefill']['us_per_call']} us/call")
         torch.cuda.empty_cache()
     if want("c3"):
@@ -359,6 +386,12 @@ def main():
         log(f"config 5: {ms * 1e3:.2f} us/call")
         torch.cuda.empty_cache()
 
+    if want("f8"):
+        # flash_attn_with_config on E4M3 K / V with descales at the config-4 shape
+        log("FP8 K/V attention at the config-4 shape")
+        other["c4_shape_fp8_kv"] = fp8_attn_case(cq, dev, stream, max(steps_x, 20), max(warm_x, 40))
+        log(f"fp8 kv: {other['c4_shape_fp8_kv']['us_per_call']} us/call")
+        torch.cuda.empty_cache()
     if want("fx"):
         # the block-scaled formats of the reference beyond the BASELINE configs, at the config-2
         # decode shape

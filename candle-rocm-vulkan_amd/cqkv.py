@@ -86,6 +86,9 @@ def lib() -> ctypes.CDLL:
         L.cqkv_flash_attn_ext.argtypes = [P, I64P, P, I64P, P, I64P, P, I64P, i32, i32, i32,
                                           i32, i32, i32, f32, i32, i32, f32, P, i32, P, P, i32,
                                           i32, SP, SP, i32, P]
+        L.cqkv_fp8_quantize_tensor.argtypes = [P, i32, ctypes.c_int64, P, P, P]
+        L.cqkv_flash_attn_fp8.argtypes = [P, I64P, P, I64P, P, I64P, P, I64P, i32, i32, i32, i32,
+                                          i32, i32, f32, i32, i32, f32, f32, P, P, P]
         L.cqkv_reference_row_words.argtypes = [i32, i32]
         L.cqkv_reference_row_words.restype = i32
         L.cqkv_rows_import.argtypes = [SP, P, i32, i32, i32, P]
@@ -102,7 +105,8 @@ EXPORTED = ["cqkv_codes_plane_bytes", "cqkv_scales_plane_bytes", "cqkv_quant_app
             "cqkv_rope_quant_append",
             "cqkv_decode_workspace_bytes", "cqkv_decode_splits", "cqkv_decode_attention",
             "cqkv_decode_paged_workspace_bytes", "cqkv_decode_attention_paged",
-            "cqkv_flash_attn", "cqkv_flash_attn_ext", "cqkv_reference_row_words", "cqkv_rows_import",
+            "cqkv_flash_attn", "cqkv_flash_attn_ext", "cqkv_fp8_quantize_tensor",
+            "cqkv_flash_attn_fp8", "cqkv_reference_row_words", "cqkv_rows_import",
             "cqkv_rows_export", "cqkv_turbo_codebook", "cqkv_turbo_signs", "cqkv_last_error",
             "cqkv_version"]
 
@@ -354,6 +358,66 @@ def flash_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, softmax_scale:
         softmax_scale, window_left, window_right, softcap, al, al_bs, None, None, 0, 0, kc, vc,
         position, _stream(q.device)))
     return out
+
+
+def fp8_quantize_tensor(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """The per-tensor FP8 quantization of flash_attn_fp8 (candle-nn/src/flash_attn.rs:882-887):
+    E4M3 codes (uint8, the shape of x) and a device f32 tensor whose element 0 is the scale
+    amax / 448 (1 for an all-zero tensor); element 1 is scratch."""
+    _need_gpu(x, "x")
+    if x.dtype not in _DTYPES or not x.is_contiguous():
+        raise CqkvError(ERR_ARG, "x must be a contiguous bf16 / f16 / f32 tensor")
+    codes = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    scale = torch.empty(2, dtype=torch.float32, device=x.device)
+    _check(lib().cqkv_fp8_quantize_tensor(_ptr(x), _DTYPES[x.dtype], x.numel(), _ptr(codes),
+                                          _ptr(scale), _stream(x.device)))
+    return codes, scale
+
+
+def _fp8_codes(t: torch.Tensor, name: str) -> torch.Tensor:
+    if getattr(torch, "float8_e4m3fn", None) is not None and t.dtype == torch.float8_e4m3fn:
+        return t.view(torch.uint8)
+    if t.dtype != torch.uint8:
+        raise CqkvError(ERR_ARG, f"{name} must hold E4M3 codes (uint8 or float8_e4m3fn)")
+    return t
+
+
+def flash_attn_fp8_codes(q: torch.Tensor, k8: torch.Tensor, v8: torch.Tensor,
+                         softmax_scale: float, causal: bool, k_descale: float = 1.0,
+                         v_descale: float = 1.0, window_left: int = -1, window_right: int = -1,
+                         k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None,
+                         out: torch.Tensor | None = None) -> torch.Tensor:
+    """flash_attn_with_config on F8E4M3 K / V with descale factors (FlashAttnConfig::descale,
+    candle-nn/src/flash_attn.rs:113-117): q (b, s_q, h_q, d) bf16, k8 / v8 (b, s_kv, h_kv, d) E4M3
+    codes; keys and values are k8 * k_descale * k_scale[0], v8 * v_descale * v_scale[0] (the
+    device scales optional)."""
+    _need_gpu(q, "q")
+    k8, v8 = _fp8_codes(k8, "k8"), _fp8_codes(v8, "v8")
+    b, sq, hq, d = q.shape
+    _, sk, hkv, _ = k8.shape
+    if out is None:
+        out = torch.empty_like(q)
+    if causal:
+        window_right = 0
+    _check(lib().cqkv_flash_attn_fp8(
+        _ptr(q), _strides3(q, (0, 1, 2)), _ptr(k8), _strides3(k8, (0, 1, 2)), _ptr(v8),
+        _strides3(v8, (0, 1, 2)), _ptr(out), _strides3(out, (0, 1, 2)), b, sq, sk, hq, hkv, d,
+        softmax_scale, window_left, window_right, k_descale, v_descale, _ptr(k_scale),
+        _ptr(v_scale), _stream(q.device)))
+    return out
+
+
+def flash_attn_fp8(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, softmax_scale: float,
+                   causal: bool, window_left: int = -1, window_right: int = -1,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """candle_nn::flash_attn::flash_attn_fp8 (candle-nn/src/flash_attn.rs:862-892, without its
+    optional Hadamard rotation): K and V quantized to E4M3 with per-tensor scales, then attention
+    with those scales as descale factors. Nothing waits on the host: the scales stay on the
+    device."""
+    k8, ks = fp8_quantize_tensor(k.contiguous())
+    v8, vs = fp8_quantize_tensor(v.contiguous())
+    return flash_attn_fp8_codes(q, k8, v8, softmax_scale, causal, 1.0, 1.0, window_left,
+                                window_right, ks, vs, out)
 
 
 def flash_attn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,

@@ -1,0 +1,214 @@
+// FP8 (E4M3) K / V with per-tensor descale factors: candle_nn::flash_attn::flash_attn_fp8 and the
+// F8E4M3 K / V branch of flash_attn_with_config (paths relative to the reference repository
+// root: candle-nn/src/flash_attn.rs:862-892 and FlashAttnConfig::descale :113-117; kernels
+// candle-core/kernels/flash_attn_impl.h:52-63, 153, 381, 434: scores dot * k_descale, outputs
+// times v_descale / l).
+//
+//  * cqkv_fp8_quantize_tensor: the per-tensor quantization of flash_attn_fp8 (:882-887):
+//    amax = max |x|, scale = amax > 0 ? amax / 448 : 1, codes E4M3(x * f32(1 / f64(scale)) + 0)
+//    (candle's `x / scale` is affine(1 / scale, 0), candle-core/src/tensor.rs:3124 and
+//    cpu_backend/mod.rs:313-315). The scale is written to device memory, so nothing waits on the
+//    host. Three launches: clear the maximum, the maximum (at most 512 workgroups, one atomic
+//    each on the float bits), the codes.
+//  * cqkv_flash_attn_fp8: K and V are E4M3 tensors; one pass writes their values to bf16 into
+//    stream-ordered scratch (E4M3 is exact in bf16), then the bf16 MFMA prefill runs on it with
+//    k_descale folded into the query pre-scale and v_descale into the output normalisation.
+#include "cqkv_device.h"
+#include "cqkv_host.h"
+
+namespace cqkv {
+
+struct Fp8QuantArgs {
+    const void *x;
+    int64_t n;
+    int32_t dtype;
+    uint8_t *codes;
+    float *scale;  // [0] the scale, [1] the maximum |x| as float bits (scratch)
+};
+
+__global__ __launch_bounds__(64) void fp8_clear_kernel(float *scale) {
+    if (threadIdx.x == 0) ((uint32_t *)scale)[1] = 0u;
+}
+
+__global__ __launch_bounds__(256) void fp8_amax_kernel(Fp8QuantArgs a) {
+    float m = 0.0f;
+    const int64_t t0 = (int64_t)blockIdx.x * 256 + threadIdx.x, step = (int64_t)gridDim.x * 256;
+    int64_t tail = 0;
+    if (a.dtype != CQKV_F32 && ((uintptr_t)a.x & 15) == 0) {
+        // 16-bit elements, 16-byte aligned: 8 per load
+        const int64_t n8 = a.n / 8;
+        const bool bf = a.dtype == CQKV_BF16;
+        auto fold = [&](const u32x4 &w) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float lo = bf ? bf16_bits_to_f32(w[e] & 0xffffu) : f16_bits_to_f32(w[e] & 0xffffu);
+                const float hi = bf ? bf16_bits_to_f32(w[e] >> 16) : f16_bits_to_f32(w[e] >> 16);
+                m = fmaxf(m, fmaxf(__builtin_fabsf(lo), __builtin_fabsf(hi)));
+            }
+        };
+        int64_t i = t0;
+        for (; i + 3 * step < n8; i += 4 * step) {  // four loads in flight
+            const u32x4 w0 = ((const u32x4 *)a.x)[i], w1 = ((const u32x4 *)a.x)[i + step];
+            const u32x4 w2 = ((const u32x4 *)a.x)[i + 2 * step], w3 = ((const u32x4 *)a.x)[i + 3 * step];
+            fold(w0);
+            fold(w1);
+            fold(w2);
+            fold(w3);
+        }
+        for (; i < n8; i += step) fold(((const u32x4 *)a.x)[i]);
+        tail = n8 * 8;
+    }
+    for (int64_t i = tail + t0; i < a.n; i += step)
+        m = fmaxf(m, __builtin_fabsf(load_elem(a.x, i, a.dtype)));
+    m = wave_max(m);
+    __shared__ float part[4];
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const float b = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+        // non-negative floats order as their bit patterns; fmaxf skips NaN inputs, as Rust's
+        // f32::max in candle's max_all does
+        atomicMax((uint32_t *)a.scale + 1, __float_as_uint(b));
+    }
+}
+
+__global__ __launch_bounds__(256) void fp8_quant_kernel(Fp8QuantArgs a) {
+    const float amax = __uint_as_float(((const uint32_t *)a.scale)[1]);
+    const float s = amax > 0.0f ? amax / 448.0f : 1.0f;
+    const float mul = (float)(1.0 / (double)s);
+    if (blockIdx.x == 0 && threadIdx.x == 0) a.scale[0] = s;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.n; i += (int64_t)gridDim.x * 256) {
+        const float q = load_elem(a.x, i, a.dtype) * mul + 0.0f;  // affine(mul, 0): -0 -> +0
+        a.codes[i] = (uint8_t)e4m3_encode(q);
+    }
+}
+
+struct Fp8StageArgs {
+    const uint8_t *k, *v;
+    int64_t k_sb, k_st, k_sh, v_sb, v_st, v_sh;  // element strides: batch, token, head
+    uint16_t *kb, *vb;                           // (batch, kv_heads, kv_len, D) bf16
+    int32_t kv_len, kv_heads;
+};
+
+// One thread per 8 head dims of one token: 8 code bytes in, their 8 bf16 values out, K and V.
+__global__ __launch_bounds__(256) void fp8_stage_kernel(Fp8StageArgs a) {
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int t = blockIdx.x * 16 + (threadIdx.x >> 4), c = threadIdx.x & 15;
+    if (t >= a.kv_len) return;
+    const int64_t dst = (((int64_t)b * a.kv_heads + h) * a.kv_len + t) * 128 + 8 * c;
+    const uint8_t *kp = a.k + (int64_t)b * a.k_sb + (int64_t)t * a.k_st + (int64_t)h * a.k_sh + 8 * c;
+    const uint8_t *vp = a.v + (int64_t)b * a.v_sb + (int64_t)t * a.v_st + (int64_t)h * a.v_sh + 8 * c;
+    const u32x2 kw = *(const u32x2 *)kp, vw = *(const u32x2 *)vp;
+    f32x2 kf[4], vf[4];  // code pairs (0,1) (2,3) of each word: the selector is an immediate
+    kf[0] = __builtin_amdgcn_cvt_pk_f32_fp8(kw.x, false);
+    kf[1] = __builtin_amdgcn_cvt_pk_f32_fp8(kw.x, true);
+    kf[2] = __builtin_amdgcn_cvt_pk_f32_fp8(kw.y, false);
+    kf[3] = __builtin_amdgcn_cvt_pk_f32_fp8(kw.y, true);
+    vf[0] = __builtin_amdgcn_cvt_pk_f32_fp8(vw.x, false);
+    vf[1] = __builtin_amdgcn_cvt_pk_f32_fp8(vw.x, true);
+    vf[2] = __builtin_amdgcn_cvt_pk_f32_fp8(vw.y, false);
+    vf[3] = __builtin_amdgcn_cvt_pk_f32_fp8(vw.y, true);
+    u32x4 ko, vo;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        ko[i] = pack_bf16x2(kf[i].x, kf[i].y);  // exact
+        vo[i] = pack_bf16x2(vf[i].x, vf[i].y);
+    }
+    *(u32x4 *)(a.kb + dst) = ko;
+    *(u32x4 *)(a.vb + dst) = vo;
+}
+
+int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
+                    const int64_t k_strides[3], const void *v, const int64_t v_strides[3],
+                    void *out, const int64_t out_strides[3], int32_t batch, int32_t q_len,
+                    int32_t kv_len, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                    float softmax_scale, int32_t window_left, int32_t window_right, float softcap,
+                    const float *alibi_slopes, int32_t alibi_batch_stride,
+                    const int32_t *cu_seqlens_q, const int32_t *cu_seqlens_k, int32_t total_q,
+                    int32_t total_k, const cqkv_side *k_cache, const cqkv_side *v_cache,
+                    int32_t position, cqkv_stream_t stream, float q_mul, const float *q_mul_dev,
+                    float o_mul, const float *o_mul_dev);
+
+}  // namespace cqkv
+
+using namespace cqkv;
+
+extern "C" int cqkv_fp8_quantize_tensor(const void *x, int32_t x_dtype, int64_t n, uint8_t *codes,
+                                        float *scale, cqkv_stream_t stream) {
+    clear_error();
+    if (!x || !codes || !scale) return fail(CQKV_ERR_ARG, "cqkv_fp8_quantize_tensor: null pointer");
+    if (x_dtype < CQKV_BF16 || x_dtype > CQKV_F32)
+        return fail(CQKV_ERR_ARG, "cqkv_fp8_quantize_tensor: dtype %d", x_dtype);
+    if (n < 0) return fail(CQKV_ERR_ARG, "cqkv_fp8_quantize_tensor: n %lld", (long long)n);
+    const hipStream_t st = (hipStream_t)stream;
+    Fp8QuantArgs a = {x, n, x_dtype, codes, scale};
+    const int64_t want = (n + 255) / 256;
+    const unsigned blocks = (unsigned)(want < 1 ? 1 : (want > 4096 ? 4096 : want));
+    // the maximum: few workgroups, since each ends with an atomic on the one address
+    const unsigned mblocks = blocks > 512 ? 512 : blocks;
+    hipLaunchKernelGGL(fp8_clear_kernel, dim3(1), dim3(64), 0, st, scale);
+    hipLaunchKernelGGL(fp8_amax_kernel, dim3(mblocks), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(fp8_quant_kernel, dim3(blocks), dim3(256), 0, st, a);
+    CQKV_HIP_CHECK(hipGetLastError());
+    return CQKV_OK;
+}
+
+extern "C" int cqkv_flash_attn_fp8(const void *q, const int64_t q_strides[3], const void *k8,
+                                   const int64_t k_strides[3], const void *v8,
+                                   const int64_t v_strides[3], void *out,
+                                   const int64_t out_strides[3], int32_t batch, int32_t q_len,
+                                   int32_t kv_len, int32_t q_heads, int32_t kv_heads,
+                                   int32_t head_dim, float softmax_scale, int32_t window_left,
+                                   int32_t window_right, float k_descale, float v_descale,
+                                   const float *k_scale, const float *v_scale,
+                                   cqkv_stream_t stream) {
+    clear_error();
+    static const char *who = "cqkv_flash_attn_fp8";
+    if (!q || !k8 || !v8 || !out || !q_strides || !k_strides || !v_strides || !out_strides)
+        return fail(CQKV_ERR_ARG, "%s: null tensor or strides", who);
+    if (head_dim != 128) return fail(CQKV_ERR_ARG, "%s: head_dim %d not supported (128)", who, head_dim);
+    if (batch <= 0 || q_len <= 0 || kv_len <= 0 || kv_heads <= 0)
+        return fail(CQKV_ERR_ARG, "%s: batch %d q_len %d kv_len %d kv_heads %d", who, batch, q_len,
+                    kv_len, kv_heads);
+    if (!(k_descale == k_descale) || !(v_descale == v_descale))
+        return fail(CQKV_ERR_ARG, "%s: NaN descale", who);
+    for (int i = 0; i < 3; ++i)
+        if (k_strides[i] % 8 != 0 || v_strides[i] % 8 != 0)
+            return fail(CQKV_ERR_ARG, "%s: K / V strides must be multiples of 8 bytes", who);
+    if ((uintptr_t)k8 % 8 != 0 || (uintptr_t)v8 % 8 != 0)
+        return fail(CQKV_ERR_ARG, "%s: K / V must be 8-byte aligned", who);
+    const hipStream_t st = (hipStream_t)stream;
+    const size_t plane = (size_t)batch * kv_heads * kv_len * 128;
+    void *scratch = nullptr;
+    CQKV_HIP_CHECK(hipMallocAsync(&scratch, plane * 4, st));
+    Fp8StageArgs s = {};
+    s.k = (const uint8_t *)k8;
+    s.v = (const uint8_t *)v8;
+    s.k_sb = k_strides[0];
+    s.k_st = k_strides[1];
+    s.k_sh = k_strides[2];
+    s.v_sb = v_strides[0];
+    s.v_st = v_strides[1];
+    s.v_sh = v_strides[2];
+    s.kb = (uint16_t *)scratch;
+    s.vb = (uint16_t *)scratch + plane;
+    s.kv_len = kv_len;
+    s.kv_heads = kv_heads;
+    hipLaunchKernelGGL(fp8_stage_kernel, dim3((kv_len + 15) / 16, kv_heads, batch), dim3(256), 0,
+                       st, s);
+    int rc = CQKV_OK;
+    if (hipGetLastError() != hipSuccess) {
+        rc = fail(CQKV_ERR_HIP, "%s: staging launch failed", who);
+    } else {
+        // the staged K / V are (batch, kv_heads, kv_len, D): (batch, token, head) strides
+        const int64_t ss[3] = {(int64_t)kv_heads * kv_len * 128, 128, (int64_t)kv_len * 128};
+        rc = flash_attn_impl(q, q_strides, s.kb, ss, s.vb, ss, out, out_strides, batch, q_len,
+                             kv_len, q_heads, kv_heads, head_dim, softmax_scale, window_left,
+                             window_right, 0.0f, nullptr, 0, nullptr, nullptr, 0, 0, nullptr,
+                             nullptr, 0, stream, k_descale, k_scale, v_descale, v_scale);
+    }
+    const hipError_t fe = hipFreeAsync(scratch, st);
+    if (rc != CQKV_OK) return rc;
+    CQKV_HIP_CHECK(fe);
+    return CQKV_OK;
+}

@@ -68,6 +68,11 @@ struct PrefillArgs {
     // kv_len are the maximum lengths, total_q / total_k the row counts of the tensors
     const int32_t *cu_q, *cu_k;
     int32_t total_q, total_k;
+    // FP8 K / V descales (flash_attn_impl.h:63, 434: scores dot * k_descale, outputs times
+    // v_descale / l): host factors times device factors (null: 1), folded into the query
+    // pre-scale and the output normalisation
+    float q_mul, o_mul;
+    const float *q_mul_dev, *o_mul_dev;
 };
 
 // First rows and lengths of sequence b. Variable-length offsets are clamped into the tensors
@@ -506,14 +511,15 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
         const bool ok = wave_live && qi < lq;
         const uint16_t *row = a.q + sq.q0 + (int64_t)min(head, a.q_heads - 1) * a.q_sh +
                               (int64_t)min(qi, lq - 1) * a.q_st;
+        const float qs = a.scale_log2 * a.q_mul * (a.q_mul_dev ? a.q_mul_dev[0] : 1.0f);
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
             u32x4 w = ok ? ldg128(row + 16 * ks + 8 * h) : u32x4{0u, 0u, 0u, 0u};
-            // q * scale * log2(e), rounded to bf16
+            // q * scale * log2(e) (* k_descale), rounded to bf16
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                w[e] = pack_bf16x2(__uint_as_float(w[e] << 16) * a.scale_log2,
-                                   __uint_as_float(w[e] & 0xffff0000u) * a.scale_log2);
+                w[e] = pack_bf16x2(__uint_as_float(w[e] << 16) * qs,
+                                   __uint_as_float(w[e] & 0xffff0000u) * qs);
             st.qop[ks] = __builtin_bit_cast(bf16x8, w);
         }
         if (qi < lq) pf_key_range(qi, lq, lk, a.wl, a.wr, st.qlo, st.qhi);
@@ -635,7 +641,8 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
 
     // ---- normalise and write O (bf16): lane (qr, h), d = 32 md + 8 (j / 4) + 4 h + j % 4 ----
     const float l = pf_sum_halves(st.l_run);
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const float om = a.o_mul * (a.o_mul_dev ? a.o_mul_dev[0] : 1.0f);
+    const float inv = l > 0.0f ? om / l : 0.0f;
     const int qi = q0 + 32 * qhalf + qr;
     if (qi >= lq) return;
     uint16_t *orow = a.out + sq.o0 + (int64_t)qi * a.o_st + (int64_t)head * a.o_sh;
@@ -785,18 +792,20 @@ int quant_append_launch(const cqkv_side *side, const void *x, int32_t x_dtype,
 
 using namespace cqkv;
 
-extern "C" int cqkv_flash_attn_ext(const void *q, const int64_t q_strides[3], const void *k,
-                                   const int64_t k_strides[3], const void *v,
-                                   const int64_t v_strides[3], void *out,
-                                   const int64_t out_strides[3], int32_t batch, int32_t q_len,
-                                   int32_t kv_len, int32_t q_heads, int32_t kv_heads,
-                                   int32_t head_dim, float softmax_scale, int32_t window_left,
-                                   int32_t window_right, float softcap, const float *alibi_slopes,
-                                   int32_t alibi_batch_stride, const int32_t *cu_seqlens_q,
-                                   const int32_t *cu_seqlens_k, int32_t total_q, int32_t total_k,
-                                   const cqkv_side *k_cache, const cqkv_side *v_cache,
-                                   int32_t position, cqkv_stream_t stream) {
-    clear_error();
+namespace cqkv {
+
+// The whole prefill call; descales (q_mul / o_mul and their device factors) are those of the FP8
+// K / V path (fp8_attn.hip), 1 / null for bf16 K / V.
+int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
+                    const int64_t k_strides[3], const void *v, const int64_t v_strides[3],
+                    void *out, const int64_t out_strides[3], int32_t batch, int32_t q_len,
+                    int32_t kv_len, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                    float softmax_scale, int32_t window_left, int32_t window_right, float softcap,
+                    const float *alibi_slopes, int32_t alibi_batch_stride,
+                    const int32_t *cu_seqlens_q, const int32_t *cu_seqlens_k, int32_t total_q,
+                    int32_t total_k, const cqkv_side *k_cache, const cqkv_side *v_cache,
+                    int32_t position, cqkv_stream_t stream, float q_mul, const float *q_mul_dev,
+                    float o_mul, const float *o_mul_dev) {
     if (!q || !k || !v || !out || !q_strides || !k_strides || !v_strides || !out_strides)
         return fail(CQKV_ERR_ARG, "cqkv_flash_attn: null tensor or strides");
     if (head_dim != kPfD)
@@ -879,6 +888,10 @@ extern "C" int cqkv_flash_attn_ext(const void *q, const int64_t q_strides[3], co
     a.cu_k = cu_seqlens_k;
     a.total_q = total_q;
     a.total_k = total_k;
+    a.q_mul = q_mul;
+    a.o_mul = o_mul;
+    a.q_mul_dev = q_mul_dev;
+    a.o_mul_dev = o_mul_dev;
     // V^T scratch (stream-ordered: freed after the launches that use it)
     a.vt_len = (kv_len + kPfBK - 1) / kPfBK * kPfBK;
     void *vt = nullptr;
@@ -921,6 +934,27 @@ extern "C" int cqkv_flash_attn_ext(const void *q, const int64_t q_strides[3], co
             return rc;
     }
     return CQKV_OK;
+}
+
+}  // namespace cqkv
+
+extern "C" int cqkv_flash_attn_ext(const void *q, const int64_t q_strides[3], const void *k,
+                                   const int64_t k_strides[3], const void *v,
+                                   const int64_t v_strides[3], void *out,
+                                   const int64_t out_strides[3], int32_t batch, int32_t q_len,
+                                   int32_t kv_len, int32_t q_heads, int32_t kv_heads,
+                                   int32_t head_dim, float softmax_scale, int32_t window_left,
+                                   int32_t window_right, float softcap, const float *alibi_slopes,
+                                   int32_t alibi_batch_stride, const int32_t *cu_seqlens_q,
+                                   const int32_t *cu_seqlens_k, int32_t total_q, int32_t total_k,
+                                   const cqkv_side *k_cache, const cqkv_side *v_cache,
+                                   int32_t position, cqkv_stream_t stream) {
+    clear_error();
+    return flash_attn_impl(q, q_strides, k, k_strides, v, v_strides, out, out_strides, batch,
+                           q_len, kv_len, q_heads, kv_heads, head_dim, softmax_scale, window_left,
+                           window_right, softcap, alibi_slopes, alibi_batch_stride, cu_seqlens_q,
+                           cu_seqlens_k, total_q, total_k, k_cache, v_cache, position, stream,
+                           1.0f, nullptr, 1.0f, nullptr);
 }
 
 extern "C" int cqkv_flash_attn(const void *q, const int64_t q_strides[3], const void *k,

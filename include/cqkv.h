@@ -31,6 +31,10 @@
  *                          flash_attn_alibi_windowed_softcap / flash_attn_varlen*
  *                          (candle-flash-attn/src/lib.rs:41-511; FlashAttnParams.softcap,
  *                          FaExtra.alibi, cu_seqlens in candle-core/src/accel/attention.rs)
+ *   cqkv_fp8_quantize_tensor / cqkv_flash_attn_fp8
+ *                          flash_attn_fp8 and the F8E4M3 K / V path of flash_attn_with_config
+ *                          with FlashAttnConfig::descale (candle-nn/src/flash_attn.rs:113-117,
+ *                          862-892; kernels candle-core/kernels/flash_attn_impl.h:52-63, 381, 434)
  *   cqkv_rows_import /     the reference's packed row layout [codes][aux][rsc0][rsc1]
  *   cqkv_rows_export       (candle-core/src/accel/formats.rs:206-242)
  *
@@ -224,6 +228,27 @@ int cqkv_flash_attn_ext(const void *q, const int64_t q_strides[3], const void *k
                         const int32_t *cu_seqlens_q, const int32_t *cu_seqlens_k,
                         int32_t total_q, int32_t total_k, const cqkv_side *k_cache,
                         const cqkv_side *v_cache, int32_t position, cqkv_stream_t stream);
+
+/* Per-tensor FP8 quantization (flash_attn_fp8, candle-nn/src/flash_attn.rs:882-887): over the n
+ * elements of x (dtype CQKV_BF16 / F16 / F32, contiguous), amax = max |x|, scale = amax > 0 ?
+ * amax / 448 : 1, codes[i] = E4M3(x[i] * f32(1 / f64(scale)) + 0) (candle's `x / scale`).
+ * scale: device float[2]; scale[0] receives the scale, scale[1] is scratch. Asynchronous. */
+int cqkv_fp8_quantize_tensor(const void *x, int32_t x_dtype, int64_t n, uint8_t *codes,
+                             float *scale, cqkv_stream_t stream);
+
+/* Attention over E4M3 K / V with descale factors (flash_attn_with_config on F8E4M3 tensors):
+ * shapes, strides and masks as cqkv_flash_attn (q, out bf16; k8 / v8 E4M3 bytes, strides
+ * multiples of 8, 8-byte aligned). Keys are e4m3(k8) * k_descale * (k_scale ? *k_scale : 1),
+ * values likewise with v_descale / v_scale (device floats, e.g. the scales written by
+ * cqkv_fp8_quantize_tensor, read on the device). The codes are dequantized to bf16 into
+ * stream-ordered scratch, then the bf16 MFMA prefill runs. */
+int cqkv_flash_attn_fp8(const void *q, const int64_t q_strides[3], const void *k8,
+                        const int64_t k_strides[3], const void *v8, const int64_t v_strides[3],
+                        void *out, const int64_t out_strides[3], int32_t batch, int32_t q_len,
+                        int32_t kv_len, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                        float softmax_scale, int32_t window_left, int32_t window_right,
+                        float k_descale, float v_descale, const float *k_scale,
+                        const float *v_scale, cqkv_stream_t stream);
 
 /* Reference row layout interop (candle-core/src/accel/formats.rs:206-242): rows are
  * (batch, kv_heads, tokens, row_words) u32 on the device, row_words = code + aux + 2 words.

@@ -229,6 +229,23 @@ def key_range(i: int, lq: int, lk: int, wl: int, wr: int) -> tuple[int, int]:
 
 
 # --------------------------------------------------------------------------------------------
+# per-tensor FP8 quantization
+# --------------------------------------------------------------------------------------------
+def fp8_quantize_tensor(x: np.ndarray) -> tuple[np.ndarray, np.float32]:
+    """flash_attn_fp8's K / V quantization (candle-nn/src/flash_attn.rs:882-887): amax = max |x|
+    over the f32 tensor, scale = amax / 448 (1 when amax is 0), codes = E4M3 of x / scale, where
+    candle's `tensor / f64` is affine(1 / rhs, 0) (candle-core/src/tensor.rs:3124) computed as
+    v * f32(mul) + f32(add) (candle-core/src/cpu_backend/mod.rs:313-315): the reciprocal in f64,
+    rounded to f32, one f32 multiply, then + 0 (which turns -0 into +0)."""
+    x = np.asarray(x, np.float32)
+    amax = np.float32(np.abs(x).max()) if x.size else np.float32(0.0)
+    scale = np.float32(amax / np.float32(448.0)) if amax > 0 else np.float32(1.0)
+    mul = np.float32(1.0 / np.float64(scale))
+    q = (x * mul + np.float32(0.0)).astype(np.float32)
+    return e4m3_encode(q).astype(np.uint8), scale
+
+
+# --------------------------------------------------------------------------------------------
 # rotary embeddings
 # --------------------------------------------------------------------------------------------
 ROPE_HALVES, ROPE_INTERLEAVED = 1, 2

@@ -205,3 +205,21 @@ def test_rope_quant_append_argument_errors(cq):
     assert b"cos / sin rows" in L.cqkv_last_error()
     assert call(cos=None) == cq.ERR_ARG
     assert call(tokens=0) == cq.OK  # nothing to do, nothing launched
+
+
+def test_fp8_attention_argument_errors(cq):
+    L = cq.lib()
+    one = ctypes.c_void_p(8)
+    x = (ctypes.c_int64 * 3)(8, 1024, 128)
+    odd = (ctypes.c_int64 * 3)(8, 1028, 130)
+
+    def attn(ks=x, hd=128, kd=1.0):
+        return L.cqkv_flash_attn_fp8(one, x, one, ks, one, x, one, x, 1, 16, 16, 8, 8, hd, 0.1,
+                                     -1, 0, kd, 1.0, None, None, None)
+    assert attn(hd=64) == cq.ERR_ARG
+    assert attn(ks=odd) == cq.ERR_ARG
+    assert b"multiples of 8" in L.cqkv_last_error()
+    assert attn(kd=float("nan")) == cq.ERR_ARG
+    assert L.cqkv_fp8_quantize_tensor(one, 7, 16, one, one, None) == cq.ERR_ARG
+    assert L.cqkv_fp8_quantize_tensor(None, 0, 16, one, one, None) == cq.ERR_ARG
+    assert L.cqkv_fp8_quantize_tensor(one, 0, -1, one, one, None) == cq.ERR_ARG

@@ -593,3 +593,51 @@ def test_round_to_dtypes():
     np.testing.assert_array_equal(O.round_to(x, "f16")[:2], [1.0 + 2.0 ** -9, 1.0 + 3 * 2.0 ** -9])
     assert np.isinf(O.round_to(np.float32(65520.0), "f16"))
     np.testing.assert_array_equal(O.round_to(x, "f32"), x)
+
+
+# ---------------------------------------------------------------------------------------------
+# per-tensor FP8 quantization (flash_attn_fp8)
+# ---------------------------------------------------------------------------------------------
+def test_fp8_tensor_quantize_semantics():
+    """flash_attn.rs:882-887 through candle's affine (tensor.rs:3124, cpu_backend/mod.rs:313-315):
+    the scale maps the largest magnitude to the E4M3 maximum 448; an all-zero tensor keeps
+    scale 1; -0 becomes +0 (the `+ 0` of affine); every code is the nearest E4M3 value of
+    x * f32(1 / f64(scale)) (brute force over the 127 positive finite codes)."""
+    codes, s = O.fp8_quantize_tensor(np.zeros(10, np.float32))
+    assert s == 1.0 and (codes == 0).all()
+    g = np.random.default_rng(5)
+    x = (g.standard_normal(4096) * 3).astype(np.float32)
+    x[7] = -0.0
+    x[9] = -x[np.argmax(np.abs(x))] * 1.0  # a second element at the maximum, negative
+    codes, s = O.fp8_quantize_tensor(x)
+    amax = np.abs(x).max()
+    assert s == np.float32(amax / np.float32(448.0))
+    assert codes[7] == 0x00
+    assert codes[np.argmax(np.abs(x))] & 0x7F == 0x7E and codes[9] & 0x7F == 0x7E
+    vals = np.array([e4m3_value_table()[c] for c in range(127)])  # positive finite codes
+    mul = np.float32(1.0 / np.float64(s))
+    q = (x * mul).astype(np.float64)
+    for i in range(0, 4096, 37):
+        d = np.abs(vals - abs(q[i]))
+        best = np.flatnonzero(d == d.min())
+        c = codes[i] & 0x7F
+        assert c in best if len(best) == 1 else (c in best and c % 2 == 0), (i, q[i], c)
+        if q[i] != 0:
+            assert (codes[i] >> 7) == (1 if q[i] < 0 else 0)
+
+
+def test_fp8_tensor_quantize_reciprocal_choice_only_matters_at_ties():
+    """x times f32(1 / f64(scale)) (candle's affine) and the f32 quotient x / scale differ in
+    the last f32 bit now and then, but an E4M3 code changes only where that bit crosses a
+    rounding tie of the 3-bit mantissa: over 400 000 random elements the codes agree. The oracle
+    follows the affine; a slip to the quotient would be immaterial at this bar."""
+    g = np.random.default_rng(11)
+    diff = quot = 0
+    for _ in range(20):
+        x = (g.standard_normal(20000) * g.uniform(0.1, 50)).astype(np.float32)
+        codes, s = O.fp8_quantize_tensor(x)
+        qa = (x * np.float32(1.0 / np.float64(s))).astype(np.float32)
+        qb = (x / s).astype(np.float32)
+        quot += int((qa != qb).sum())
+        diff += int((O.e4m3_encode(qb) != codes).sum())
+    assert quot > 0 and diff == 0
