@@ -87,6 +87,8 @@ def lib() -> ctypes.CDLL:
                                           i32, i32, i32, f32, i32, i32, f32, P, i32, P, P, i32,
                                           i32, SP, SP, i32, P]
         L.cqkv_fp8_quantize_tensor.argtypes = [P, i32, ctypes.c_int64, P, P, P]
+        L.cqkv_hadamard_rows.argtypes = [P, i32, ctypes.c_int64, ctypes.c_int64, i32,
+                                         ctypes.c_uint64, P, ctypes.c_int64, P]
         L.cqkv_flash_attn_fp8.argtypes = [P, I64P, P, I64P, P, I64P, P, I64P, i32, i32, i32, i32,
                                           i32, i32, f32, i32, i32, f32, f32, P, P, P]
         L.cqkv_reference_row_words.argtypes = [i32, i32]
@@ -106,7 +108,7 @@ EXPORTED = ["cqkv_codes_plane_bytes", "cqkv_scales_plane_bytes", "cqkv_quant_app
             "cqkv_decode_workspace_bytes", "cqkv_decode_splits", "cqkv_decode_attention",
             "cqkv_decode_paged_workspace_bytes", "cqkv_decode_attention_paged",
             "cqkv_flash_attn", "cqkv_flash_attn_ext", "cqkv_fp8_quantize_tensor",
-            "cqkv_flash_attn_fp8", "cqkv_reference_row_words", "cqkv_rows_import",
+            "cqkv_flash_attn_fp8", "cqkv_hadamard_rows", "cqkv_reference_row_words", "cqkv_rows_import",
             "cqkv_rows_export", "cqkv_turbo_codebook", "cqkv_turbo_signs", "cqkv_last_error",
             "cqkv_version"]
 
@@ -407,13 +409,31 @@ def flash_attn_fp8_codes(q: torch.Tensor, k8: torch.Tensor, v8: torch.Tensor,
     return out
 
 
+FP8_HADAMARD_SEED = 0x46413346  # flash_attn.rs:869
+
+
+def hadamard_rows(x: torch.Tensor, seed: int = FP8_HADAMARD_SEED) -> torch.Tensor:
+    """x (..., D) times rotation_matrix(D, Hadamard, seed)^T, in f32, rounded to x's dtype."""
+    _need_gpu(x, "x")
+    x = x.contiguous()
+    d = x.shape[-1]
+    out = torch.empty_like(x)
+    _check(lib().cqkv_hadamard_rows(_ptr(x), _DTYPES[x.dtype], x.numel() // d, d, d, seed,
+                                    _ptr(out), d, _stream(x.device)))
+    return out
+
+
 def flash_attn_fp8(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, softmax_scale: float,
                    causal: bool, window_left: int = -1, window_right: int = -1,
-                   out: torch.Tensor | None = None) -> torch.Tensor:
-    """candle_nn::flash_attn::flash_attn_fp8 (candle-nn/src/flash_attn.rs:862-892, without its
-    optional Hadamard rotation): K and V quantized to E4M3 with per-tensor scales, then attention
-    with those scales as descale factors. Nothing waits on the host: the scales stay on the
-    device."""
+                   out: torch.Tensor | None = None, hadamard: bool = False) -> torch.Tensor:
+    """candle_nn::flash_attn::flash_attn_fp8 (candle-nn/src/flash_attn.rs:862-892): K and V
+    quantized to E4M3 with per-tensor scales, then attention with those scales as descale
+    factors. hadamard=True is the reference's CANDLE_FLASH_ATTN_HADAMARD switch: q and k rotated
+    by the same Hadamard matrix first (Q K^T unchanged, outliers spread before the FP8 rounding).
+    Nothing waits on the host: the scales stay on the device."""
+    d = q.shape[-1]
+    if hadamard and d in (64, 128):
+        q, k = hadamard_rows(q), hadamard_rows(k)
     k8, ks = fp8_quantize_tensor(k.contiguous())
     v8, vs = fp8_quantize_tensor(v.contiguous())
     return flash_attn_fp8_codes(q, k8, v8, softmax_scale, causal, 1.0, 1.0, window_left,

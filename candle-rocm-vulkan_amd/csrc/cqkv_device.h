@@ -230,6 +230,22 @@ __device__ inline float group_max(float v, int w) {
     return v;
 }
 
+// In-register Walsh-Hadamard transform over 2 * `lanes` elements held as (v0, v1) = elements
+// (2l, 2l+1): y_i = sum_j (-1)^popcount(i & j) x_j (Sylvester order, unnormalised).
+template <int D>
+__device__ inline void fwht_pairs(float &v0, float &v1, int lane) {
+    float a = v0 + v1, b = v0 - v1;
+    v0 = a;
+    v1 = b;
+#pragma unroll
+    for (int m = 1; m < D / 2; m <<= 1) {
+        const float p0 = shfl_xor(v0, m), p1 = shfl_xor(v1, m);
+        const bool upper = (lane & m) != 0;
+        v0 = upper ? p0 - v0 : v0 + p0;
+        v1 = upper ? p1 - v1 : v1 + p1;
+    }
+}
+
 // 8 floats -> bf16 hi + bf16 lo operands with hi + lo = x to 16 significant bits.
 __device__ inline void split_bf16x8(const float *x, bf16x8 &hi, bf16x8 &lo) {
     u32x4 h, l;

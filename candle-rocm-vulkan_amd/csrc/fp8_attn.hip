@@ -212,3 +212,74 @@ extern "C" int cqkv_flash_attn_fp8(const void *q, const int64_t q_strides[3], co
     CQKV_HIP_CHECK(fe);
     return CQKV_OK;
 }
+
+// ---------------------------------------------------------------------------------------------
+// Hadamard rotation of rows (the incoherent processing of flash_attn_fp8, flash_attn.rs:868-880:
+// q and k times rotation_matrix(d, Hadamard, seed)^T in f32, cast back to their dtype; the
+// matrix is the sign-flipped Sylvester Hadamard / sqrt(d) of candle-core/src/accel/turbo.rs:
+// 180-203, signs from SplitMix64(seed ^ "HADAMARD")). One wavefront per row: sign flip, the
+// in-register transform, 1 / sqrt(d), the rounding to the dtype.
+// ---------------------------------------------------------------------------------------------
+namespace cqkv {
+
+struct HadamardArgs {
+    const void *x;
+    void *out;
+    int64_t rows, x_row, out_row;  // element strides between rows
+    int32_t dtype;
+    uint32_t sign_bits[4];
+    float scale;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void hadamard_rows_kernel(HadamardArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= a.rows) return;
+    const bool act = lane < D / 2;
+    const int j0 = 2 * lane, j1 = 2 * lane + 1;
+    float v0 = 0.0f, v1 = 0.0f;
+    if (act) {
+        v0 = load_elem(a.x, row * a.x_row + j0, a.dtype);
+        v1 = load_elem(a.x, row * a.x_row + j1, a.dtype);
+        if ((a.sign_bits[j0 >> 5] >> (j0 & 31)) & 1u) v0 = -v0;
+        if ((a.sign_bits[j1 >> 5] >> (j1 & 31)) & 1u) v1 = -v1;
+    }
+    fwht_pairs<D>(v0, v1, lane);
+    if (!act) return;
+    store_elem(a.out, row * a.out_row + j0, a.dtype, v0 * a.scale);
+    store_elem(a.out, row * a.out_row + j1, a.dtype, v1 * a.scale);
+}
+
+}  // namespace cqkv
+
+extern "C" int cqkv_hadamard_rows(const void *x, int32_t dtype, int64_t rows, int64_t x_row_stride,
+                                  int32_t head_dim, uint64_t seed, void *out,
+                                  int64_t out_row_stride, cqkv_stream_t stream) {
+    clear_error();
+    if (!x || !out) return fail(CQKV_ERR_ARG, "cqkv_hadamard_rows: null pointer");
+    if (dtype < CQKV_BF16 || dtype > CQKV_F32)
+        return fail(CQKV_ERR_ARG, "cqkv_hadamard_rows: dtype %d", dtype);
+    if (head_dim != 64 && head_dim != 128)
+        return fail(CQKV_ERR_ARG, "cqkv_hadamard_rows: head_dim %d (64 or 128)", head_dim);
+    if (rows < 0 || x_row_stride < head_dim || out_row_stride < head_dim)
+        return fail(CQKV_ERR_ARG, "cqkv_hadamard_rows: rows %lld / row strides", (long long)rows);
+    if (rows == 0) return CQKV_OK;
+    HadamardArgs a = {};
+    a.x = x;
+    a.out = out;
+    a.rows = rows;
+    a.x_row = x_row_stride;
+    a.out_row = out_row_stride;
+    a.dtype = dtype;
+    float signs[128];
+    turbo_signs(head_dim, seed, signs);
+    for (int j = 0; j < head_dim; ++j)
+        if (signs[j] < 0.0f) a.sign_bits[j >> 5] |= 1u << (j & 31);
+    a.scale = 1.0f / sqrtf((float)head_dim);
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    if (head_dim == 64) hipLaunchKernelGGL(hadamard_rows_kernel<64>, grid, dim3(256), 0, (hipStream_t)stream, a);
+    else hipLaunchKernelGGL(hadamard_rows_kernel<128>, grid, dim3(256), 0, (hipStream_t)stream, a);
+    CQKV_HIP_CHECK(hipGetLastError());
+    return CQKV_OK;
+}

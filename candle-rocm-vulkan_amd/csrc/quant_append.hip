@@ -86,21 +86,6 @@ __device__ inline RawPair load_raw_t(const void *p, int64_t idx, int dtype, bool
     else return load_raw(p, idx, dtype, pair);
 }
 
-// In-register Walsh-Hadamard transform over 2 * `lanes` elements held as (v0, v1) = elements
-// (2l, 2l+1): y_i = sum_j (-1)^popcount(i & j) x_j (Sylvester order, unnormalised).
-template <int D>
-__device__ inline void fwht_pairs(float &v0, float &v1, int lane) {
-    float a = v0 + v1, b = v0 - v1;
-    v0 = a;
-    v1 = b;
-#pragma unroll
-    for (int m = 1; m < D / 2; m <<= 1) {
-        const float p0 = shfl_xor(v0, m), p1 = shfl_xor(v1, m);
-        const bool upper = (lane & m) != 0;
-        v0 = upper ? p0 - v0 : v0 + p0;
-        v1 = upper ? p1 - v1 : v1 + p1;
-    }
-}
 
 // Rotary embedding of the pair (x0, x1) = elements (2l, 2l+1) of a row at position `row` of the
 // cos / sin tables ((rows, D/2), dtype of x), then rounded to that dtype: the reference's rope

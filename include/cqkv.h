@@ -31,7 +31,7 @@
  *                          flash_attn_alibi_windowed_softcap / flash_attn_varlen*
  *                          (candle-flash-attn/src/lib.rs:41-511; FlashAttnParams.softcap,
  *                          FaExtra.alibi, cu_seqlens in candle-core/src/accel/attention.rs)
- *   cqkv_fp8_quantize_tensor / cqkv_flash_attn_fp8
+ *   cqkv_fp8_quantize_tensor / cqkv_flash_attn_fp8 / cqkv_hadamard_rows
  *                          flash_attn_fp8 and the F8E4M3 K / V path of flash_attn_with_config
  *                          with FlashAttnConfig::descale (candle-nn/src/flash_attn.rs:113-117,
  *                          862-892; kernels candle-core/kernels/flash_attn_impl.h:52-63, 381, 434)
@@ -249,6 +249,15 @@ int cqkv_flash_attn_fp8(const void *q, const int64_t q_strides[3], const void *k
                         float softmax_scale, int32_t window_left, int32_t window_right,
                         float k_descale, float v_descale, const float *k_scale,
                         const float *v_scale, cqkv_stream_t stream);
+
+/* Hadamard rotation of rows (flash_attn_fp8's incoherent processing, candle-nn/src/flash_attn.rs:
+ * 868-880): out_r = x_r * rotation_matrix(D, Hadamard, seed)^T for each of `rows` rows of D
+ * contiguous elements (row strides in elements), computed in f32 and rounded to `dtype`
+ * (CQKV_BF16 / F16 / F32). D = 64 or 128. The matrix is the sign-flipped Sylvester Hadamard
+ * matrix / sqrt(D) of candle-core/src/accel/turbo.rs:180-203. */
+int cqkv_hadamard_rows(const void *x, int32_t dtype, int64_t rows, int64_t x_row_stride,
+                       int32_t head_dim, uint64_t seed, void *out, int64_t out_row_stride,
+                       cqkv_stream_t stream);
 
 /* Reference row layout interop (candle-core/src/accel/formats.rs:206-242): rows are
  * (batch, kv_heads, tokens, row_words) u32 on the device, row_words = code + aux + 2 words.

@@ -106,3 +106,44 @@ def test_flash_attn_fp8_decode_shape_and_float8_dtype(cq, dev):
     torch.cuda.synchronize()
     want = oracle_fp8_attention(q, k8, v8, 0.01, 0.01, 0.09, -1, 0)
     assert_close_bf16(out.float().cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_hadamard_rows_vs_oracle_rotation(cq, dev, d):
+    """The rotation of flash_attn_fp8's switch: rotation_matrix(d, Hadamard, 0x46413346) in f32.
+    The reference multiplies by the dense matrix (its f32 summation order is not pinned, as for
+    TurboQuant's rotation): within 2e-6 relative in f32 before the bf16 rounding, and at most
+    one bf16 ulp after it."""
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(3, 41, 4, d, generator=g)
+    pi = O.rotation_matrix(d, O.ROT_HADAMARD, cq.FP8_HADAMARD_SEED)
+    want = O.rotate_rows(pi, x.numpy().reshape(-1, d)).reshape(x.shape)
+    got = cq.hadamard_rows(x.to(dev)).cpu().numpy()
+    np.testing.assert_allclose(got, want, rtol=2e-6, atol=2e-6)
+    xb = x.to(torch.bfloat16)
+    gb = cq.hadamard_rows(xb.to(dev)).float().cpu().numpy()
+    wb = O.round_bf16(O.rotate_rows(pi, xb.float().numpy().reshape(-1, d)).reshape(x.shape))
+    ulp = np.abs(wb) * 2.0 ** -7 + 1e-30
+    assert (np.abs(gb - wb) <= ulp).all()
+    assert (gb == wb).mean() > 0.99
+
+
+def test_flash_attn_fp8_hadamard(cq, dev):
+    """With the switch: equal to the oracle pipeline (rotate q and k, round to bf16, per-tensor
+    FP8 of the rotated k, attention) to the tolerance, and to the unrotated bf16 attention to
+    the FP8 error (the rotation leaves Q K^T unchanged)."""
+    b, sq, sk, hq, hkv = 2, 96, 96, 8, 2
+    q, k, v = inputs(5, b, sq, sk, hq, hkv)
+    scale = 1 / 128 ** 0.5
+    out = cq.flash_attn_fp8(q.to(dev), k.to(dev), v.to(dev), scale, True, hadamard=True)
+    torch.cuda.synchronize()
+    pi = O.rotation_matrix(128, O.ROT_HADAMARD, cq.FP8_HADAMARD_SEED)
+    qr = O.round_bf16(O.rotate_rows(pi, q.float().numpy().reshape(-1, 128)).reshape(q.shape))
+    kr = O.round_bf16(O.rotate_rows(pi, k.float().numpy().reshape(-1, 128)).reshape(k.shape))
+    k8, ks = O.fp8_quantize_tensor(kr)
+    v8, vs = O.fp8_quantize_tensor(v.float().numpy())
+    want = oracle_fp8_attention(torch.from_numpy(qr), torch.from_numpy(k8), torch.from_numpy(v8),
+                                ks, vs, scale, -1, 0)
+    assert_close_bf16(out.float().cpu().numpy(), want)
+    full = cq.flash_attn(q.to(dev), k.to(dev), v.to(dev), scale, True).float().cpu().numpy()
+    assert np.abs(full - out.float().cpu().numpy()).mean() < 2e-2
