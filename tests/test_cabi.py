@@ -42,9 +42,24 @@ def test_plane_sizes(cq):
     assert L.cqkv_codes_plane_bytes(cq.TURBO4, 128, 32) == 32 * 64
     assert L.cqkv_codes_plane_bytes(cq.FP8, 96, 32) == 0
     assert L.cqkv_codes_plane_bytes(7, 128, 32) == 0
+    # MXFP8: byte codes + E8M0 per 32; NVFP4: nibbles + E4M3 per 16, then an f32 per token
+    assert L.cqkv_codes_plane_bytes(cq.MXFP8, 128, 64) == 64 * 128
+    assert L.cqkv_scales_plane_bytes(cq.MXFP8, 128, 64) == 64 * 4
+    assert L.cqkv_codes_plane_bytes(cq.NVFP4, 128, 64) == 64 * 64
+    assert L.cqkv_scales_plane_bytes(cq.NVFP4, 128, 64) == 64 * 8 + 64 * 4
+    assert L.cqkv_scales_plane_bytes(cq.NVFP4, 64, 64) == 64 * 4 + 64 * 4
 
 
-@pytest.mark.parametrize("fmt,bits", [(5, 0), (2, 0), (0, 4)])
+def test_reference_row_words_known_answers(cq):
+    """candle-core/src/accel/formats.rs:467-477: MXFP4 D=64 8 code + 1 aux words, NVFP4 D=128
+    16 + 2 (+ rsc0, rsc1); MXFP8 D=128 32 + 1 + 2 by the same rule (formats.rs:224-242)."""
+    assert cq.reference_row_words(cq.MXFP4, 64) == 8 + 1 + 2
+    assert cq.reference_row_words(cq.NVFP4, 128) == 16 + 2 + 2
+    assert cq.reference_row_words(cq.MXFP8, 128) == 32 + 1 + 2
+    assert cq.reference_row_words(cq.NVFP4, 64) == 8 + 1 + 2
+
+
+@pytest.mark.parametrize("fmt,bits", [(5, 0), (2, 0), (0, 4), (3, 0), (4, 0)])
 @pytest.mark.parametrize("d", [64, 128])
 def test_reference_row_words_match_oracle_layout(cq, fmt, bits, d):
     # candle-core/src/accel/formats.rs:224-242, restated by the oracle
