@@ -123,10 +123,30 @@ struct Tile {
     // E8M0 block bytes; NVFP4 the E4M3 block bytes of its 32 (D=128) / 16 (D=64) head dims
     uint32_t kscale[2];
     uint32_t ktok[2];  // NVFP4: the key's f32 scale
-    // key lane % 32: TURBO4 norms, FP8 value scale, MX value block bytes, NVFP4 value block
-    // bytes (vs, vs2: D/16 bytes) and f32 scale (vtok)
-    uint32_t ks, vs, vs2, vtok;
+    // key lane % 32 (broadcast across lanes): MX value block bytes, NVFP4 value block bytes
+    // (vs, vs2: D/16 bytes) and f32 scale (vtok)
+    uint32_t vs, vs2, vtok;
+    // FP8 / TURBO4: the scale words of keys 8 g .. 8 g + 7 of the tile (lane group g), the ones the
+    // lane's score and P rows need, read directly instead of broadcast across lanes
+    uint32_t ks8[8], vs8[8];
 };
+
+// Formats whose per-key scale words are read as ks8 / vs8 (one 32-bit word per key). Same-box
+// A/B against the cross-lane broadcast: TurboQuant-4 config 5 270-276 -> 257-264 us, FP8 config 2
+// 94.7-95.9 -> 94.3-94.6 us; MXFP4 config 3 got 2 % slower and keeps the broadcast.
+template <int FMT>
+constexpr bool direct_scales() {
+    return FMT == CQKV_FMT_FP8 || FMT == CQKV_FMT_TURBO4;
+}
+
+// The 32-bit scale words of keys kb .. kb + 7 (kb a multiple of 8: two aligned 16-byte loads).
+template <int BYTES>
+__device__ inline void load_scales8(uint32_t *out, rsrc_t r, uint32_t kb, uint32_t oob) {
+    static_assert(BYTES == 4, "32-bit scale words");
+    const u32x4 a = ld128(r, (kb * 4) | oob), b = ld128(r, (kb * 4 + 16) | oob);
+    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+    out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+}
 
 template <int FMT, int D>
 __device__ inline void load_tile(Tile<FMT, D> &r, int tile, bool live, int lane, rsrc_t kr,
@@ -193,7 +213,11 @@ __device__ inline void load_tile(Tile<FMT, D> &r, int tile, bool live, int lane,
         }
     }
     const uint32_t kl = t0 + (lane & 31);
-    if constexpr (FMT == CQKV_FMT_MXFP4 || FMT == CQKV_FMT_MXFP8) {
+    if constexpr (direct_scales<FMT>()) {
+        const uint32_t kb = t0 + 8 * g;
+        load_scales8<4>(r.vs8, vsr, kb, oob);
+        if constexpr (FMT == CQKV_FMT_TURBO4) load_scales8<4>(r.ks8, ksr, kb, oob);
+    } else if constexpr (FMT == CQKV_FMT_MXFP4 || FMT == CQKV_FMT_MXFP8) {
         r.vs = D == 128 ? ld32(vsr, (kl * 4) | oob)
                         : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(vsr, (kl * 2) | oob, 0, 0);
     } else if constexpr (FMT == CQKV_FMT_NVFP4) {
@@ -205,11 +229,6 @@ __device__ inline void load_tile(Tile<FMT, D> &r, int tile, bool live, int lane,
             r.vs = ld32(vsr, (kl * 4) | oob);
         }
         r.vtok = ld32(vsr, (vtok_off + kl * 4) | oob);
-    } else if constexpr (FMT == CQKV_FMT_FP8) {
-        r.vs = ld32(vsr, (kl * 4) | oob);
-    } else {
-        r.ks = ld32(ksr, (kl * 4) | oob);
-        r.vs = ld32(vsr, (kl * 4) | oob);
     }
 }
 
@@ -369,7 +388,7 @@ __device__ inline void compute_tile(Tile<FMT, D> &cur, int tile, const DecodeArg
     } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-            x[e] = x[e] * __uint_as_float((uint32_t)__shfl((int)cur.ks, 8 * g + e)) * a.scale_log2;
+            x[e] = x[e] * __uint_as_float(cur.ks8[e]) * a.scale_log2;
     }
     if (!full) {
 #pragma unroll
@@ -455,7 +474,10 @@ __device__ inline void compute_tile(Tile<FMT, D> &cur, int tile, const DecodeArg
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             // scales past the written length may be any bits
-            vw[e] = e < nv ? (uint32_t)__shfl((int)cur.vs, 8 * g + e) : 0u;
+            if constexpr (direct_scales<FMT>())
+                vw[e] = e < nv ? cur.vs8[e] : 0u;
+            else
+                vw[e] = e < nv ? (uint32_t)__shfl((int)cur.vs, 8 * g + e) : 0u;
             sv[e] = __uint_as_float(vw[e]);  // FP8 scale, TURBO4 norm
             if constexpr (FMT == CQKV_FMT_NVFP4)
                 vw2[e] = D == 128 && e < nv ? (uint32_t)__shfl((int)cur.vs2, 8 * g + e) : 0u;
