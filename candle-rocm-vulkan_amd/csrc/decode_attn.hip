@@ -468,7 +468,8 @@ __device__ inline void compute_tile(Tile<FMT, D> &cur, int tile, const DecodeArg
     } else {
         // FP8 / MXFP8 / NVFP4: the value scales are inside the V operand (rounded to bf16 as the
         // reference's dequantized cache), P goes in full precision as a bf16 hi + lo pair.
-        // TURBO4: the norm goes into P.
+        // TURBO4: the norm goes into P, which enters as one f16 operand (11 significant bits;
+        // the lo part cost 8 more MFMAs per tile: config 5 246-254 -> 236 us same-box).
         float pv[8], sv[8];
         uint32_t vw[8], vw2[8];  // MX / NVFP4: the keys' block scale bytes
 #pragma unroll
@@ -526,8 +527,10 @@ __device__ inline void compute_tile(Tile<FMT, D> &cur, int tile, const DecodeArg
             }
             acc[2 * u] = mfma16x16x32(v0, phi, acc[2 * u]);
             acc[2 * u + 1] = mfma16x16x32(v1, phi, acc[2 * u + 1]);
-            acc[2 * u] = mfma16x16x32(v0, plo, acc[2 * u]);
-            acc[2 * u + 1] = mfma16x16x32(v1, plo, acc[2 * u + 1]);
+            if constexpr (FMT != CQKV_FMT_TURBO4) {  // TURBO4: P (times the norms) as one f16
+                acc[2 * u] = mfma16x16x32(v0, plo, acc[2 * u]);
+                acc[2 * u + 1] = mfma16x16x32(v1, plo, acc[2 * u + 1]);
+            }
         }
     }
 }
