@@ -653,7 +653,7 @@ extern "C" int cqkv_rope_quant_append(const cqkv_side *k_side, const cqkv_side *
     }
     const int64_t tiles = ((int64_t)tokens + 7) / 8 + 1;  // an unaligned start spans one more tile
     const int64_t blocks = (tiles + 3) / 4 * (2 * hkv + r.q_units);
-    if (blocks > INT32_MAX)
+    if (blocks * 256 > (int64_t)UINT32_MAX)  // threads along x of one launch
         return fail(CQKV_ERR_ARG, "%s: %d tokens x %d heads exceed one launch", who, tokens,
                     2 * hkv + q_heads);
     dim3 grid((uint32_t)blocks, 1, batch);

@@ -220,6 +220,10 @@ def test_rope_quant_append_argument_errors(cq):
     assert b"cos / sin rows" in L.cqkv_last_error()
     assert call(cos=None) == cq.ERR_ARG
     assert call(tokens=0) == cq.OK  # nothing to do, nothing launched
+    # more blocks than one launch's 2^32 threads along x (device positions: no capacity check)
+    big = ctypes.c_void_p(16)
+    assert call(tokens=2_000_000_000, hq=2000, rows=100, positions=big) == cq.ERR_ARG
+    assert b"exceed one launch" in L.cqkv_last_error()
 
 
 def test_fp8_attention_argument_errors(cq):
