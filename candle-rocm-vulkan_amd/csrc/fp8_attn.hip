@@ -167,9 +167,11 @@ extern "C" int cqkv_flash_attn_fp8(const void *q, const int64_t q_strides[3], co
     if (!q || !k8 || !v8 || !out || !q_strides || !k_strides || !v_strides || !out_strides)
         return fail(CQKV_ERR_ARG, "%s: null tensor or strides", who);
     if (head_dim != 128) return fail(CQKV_ERR_ARG, "%s: head_dim %d not supported (128)", who, head_dim);
-    if (batch <= 0 || q_len <= 0 || kv_len <= 0 || kv_heads <= 0)
-        return fail(CQKV_ERR_ARG, "%s: batch %d q_len %d kv_len %d kv_heads %d", who, batch, q_len,
-                    kv_len, kv_heads);
+    // the prefill's own limits, checked before the staging pass is launched
+    if (batch <= 0 || q_len <= 0 || kv_len <= 0 || kv_heads <= 0 || q_heads <= 0 ||
+        q_heads % kv_heads != 0 || kv_len > (1 << 23))
+        return fail(CQKV_ERR_ARG, "%s: batch %d q_len %d kv_len %d heads %d / %d", who, batch,
+                    q_len, kv_len, q_heads, kv_heads);
     if (!(k_descale == k_descale) || !(v_descale == v_descale))
         return fail(CQKV_ERR_ARG, "%s: NaN descale", who);
     for (int i = 0; i < 3; ++i)
@@ -262,7 +264,9 @@ extern "C" int cqkv_hadamard_rows(const void *x, int32_t dtype, int64_t rows, in
         return fail(CQKV_ERR_ARG, "cqkv_hadamard_rows: dtype %d", dtype);
     if (head_dim != 64 && head_dim != 128)
         return fail(CQKV_ERR_ARG, "cqkv_hadamard_rows: head_dim %d (64 or 128)", head_dim);
-    if (rows < 0 || x_row_stride < head_dim || out_row_stride < head_dim)
+    // four rows per 256-thread workgroup along x: rows * 64 threads within one launch
+    if (rows < 0 || rows > (int64_t)(UINT32_MAX / 64) || x_row_stride < head_dim ||
+        out_row_stride < head_dim)
         return fail(CQKV_ERR_ARG, "cqkv_hadamard_rows: rows %lld / row strides", (long long)rows);
     if (rows == 0) return CQKV_OK;
     HadamardArgs a = {};

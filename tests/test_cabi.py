@@ -239,6 +239,15 @@ def test_fp8_attention_argument_errors(cq):
     assert attn(ks=odd) == cq.ERR_ARG
     assert b"multiples of 8" in L.cqkv_last_error()
     assert attn(kd=float("nan")) == cq.ERR_ARG
+
+    def attn2(kv_len=16, hq=8, hkv=8):
+        return L.cqkv_flash_attn_fp8(one, x, one, x, one, x, one, x, 1, 16, kv_len, hq, hkv, 128,
+                                     0.1, -1, 0, 1.0, 1.0, None, None, None)
+    assert attn2(kv_len=(1 << 23) + 1) == cq.ERR_ARG  # before any scratch or launch
+    assert attn2(hq=6, hkv=4) == cq.ERR_ARG
+    assert L.cqkv_hadamard_rows(one, 0, 1 << 27, 128, 128, 1, one, 128, None) == cq.ERR_ARG
+    assert L.cqkv_hadamard_rows(one, 0, 4, 64, 128, 1, one, 128, None) == cq.ERR_ARG
+    assert L.cqkv_hadamard_rows(one, 0, 4, 96, 96, 1, one, 96, None) == cq.ERR_ARG
     assert L.cqkv_fp8_quantize_tensor(one, 7, 16, one, one, None) == cq.ERR_ARG
     assert L.cqkv_fp8_quantize_tensor(None, 0, 16, one, one, None) == cq.ERR_ARG
     assert L.cqkv_fp8_quantize_tensor(one, 0, -1, one, one, None) == cq.ERR_ARG
