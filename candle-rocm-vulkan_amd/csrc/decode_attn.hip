@@ -123,12 +123,14 @@ struct Tile {
     // E8M0 block bytes; NVFP4 the E4M3 block bytes of its 32 (D=128) / 16 (D=64) head dims
     uint32_t kscale[2];
     uint32_t ktok[2];  // NVFP4: the key's f32 scale
-    // key lane % 32 (broadcast across lanes): MX value block bytes, NVFP4 value block bytes
-    // (vs, vs2: D/16 bytes) and f32 scale (vtok)
-    uint32_t vs, vs2, vtok;
+    // key lane % 32 (broadcast across lanes): the MX formats' value block bytes
+    uint32_t vs;
     // FP8 / TURBO4: the scale words of keys 8 g .. 8 g + 7 of the tile (lane group g), the ones the
     // lane's score and P rows need, read directly instead of broadcast across lanes
     uint32_t ks8[8], vs8[8];
+    // NVFP4: the value block bytes (two words per key at D = 128, one at D = 64) and f32 scales
+    // of keys 8 g .. 8 g + 7, read directly (config-2 shape 100-103 -> 99 us same-box)
+    uint32_t nvb[D == 128 ? 16 : 8], nvg[8];
 };
 
 // Formats whose per-key scale words are read as ks8 / vs8 (one 32-bit word per key). Same-box
@@ -221,14 +223,17 @@ __device__ inline void load_tile(Tile<FMT, D> &r, int tile, bool live, int lane,
         r.vs = D == 128 ? ld32(vsr, (kl * 4) | oob)
                         : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(vsr, (kl * 2) | oob, 0, 0);
     } else if constexpr (FMT == CQKV_FMT_NVFP4) {
-        if constexpr (D == 128) {
-            const u32x2 w = ld64(vsr, (kl * 8) | oob);
-            r.vs = w.x;
-            r.vs2 = w.y;
-        } else {
-            r.vs = ld32(vsr, (kl * 4) | oob);
+        const uint32_t kb = t0 + 8 * g;
+        constexpr uint32_t kBpk = D / 16;  // block bytes per key
+#pragma unroll
+        for (int i = 0; i < (int)(8 * kBpk / 16); ++i) {
+            const u32x4 w = ld128(vsr, (kb * kBpk + 16 * i) | oob);
+            r.nvb[4 * i + 0] = w.x;
+            r.nvb[4 * i + 1] = w.y;
+            r.nvb[4 * i + 2] = w.z;
+            r.nvb[4 * i + 3] = w.w;
         }
-        r.vtok = ld32(vsr, (vtok_off + kl * 4) | oob);
+        load_scales8<4>(r.nvg, vsr, kb + vtok_off / 4, oob);
     }
 }
 
@@ -477,11 +482,13 @@ __device__ inline void compute_tile(Tile<FMT, D> &cur, int tile, const DecodeArg
             // scales past the written length may be any bits
             if constexpr (direct_scales<FMT>())
                 vw[e] = e < nv ? cur.vs8[e] : 0u;
+            else if constexpr (FMT == CQKV_FMT_NVFP4)
+                vw[e] = e < nv ? cur.nvb[(D == 128 ? 2 : 1) * e] : 0u;
             else
                 vw[e] = e < nv ? (uint32_t)__shfl((int)cur.vs, 8 * g + e) : 0u;
             sv[e] = __uint_as_float(vw[e]);  // FP8 scale, TURBO4 norm
             if constexpr (FMT == CQKV_FMT_NVFP4)
-                vw2[e] = D == 128 && e < nv ? (uint32_t)__shfl((int)cur.vs2, 8 * g + e) : 0u;
+                vw2[e] = D == 128 && e < nv ? cur.nvb[2 * e + 1] : 0u;
             if constexpr (FMT == CQKV_FMT_TURBO4)
                 pv[e] = (e < nv && p[e] > 0.0f) ? p[e] * sv[e] : 0.0f;
             else
@@ -491,7 +498,7 @@ __device__ inline void compute_tile(Tile<FMT, D> &cur, int tile, const DecodeArg
         if constexpr (FMT == CQKV_FMT_NVFP4) {
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-                gk[e] = e < nv ? __uint_as_float((uint32_t)__shfl((int)cur.vtok, 8 * g + e)) : 0.0f;
+                gk[e] = e < nv ? __uint_as_float(cur.nvg[e]) : 0.0f;
         }
         op_t<FMT> phi, plo;
         split8(pv, phi, plo);
