@@ -158,3 +158,33 @@ def test_turbo_kv_cache_rope_append_then_decode(cq, dev):
     out = cache.attention(qr, 1.0 / d ** 0.5)
     want = ref.attention(qr_ref.to(dev), 1.0 / d ** 0.5)
     assert torch.equal(out, want)
+
+
+def test_rope_append_config4_full_size(cq, dev):
+    """At the BASELINE config-4 shape (B=4, 4096 tokens, 32 / 8 heads, D=128, FP8 cache): the
+    fused launch equals, bit for bit, torch's rope in f32 (separate elementwise kernels: products
+    rounded before the sum, as the reference's kernels) rounded to bf16, followed by this
+    library's plain quantize-append of the rotated keys and of the values."""
+    b, t, hq, hkv, d = 4, 4096, 32, 8, 128
+    g = torch.Generator(device=dev).manual_seed(4)
+    qkv = torch.randn(b, t, (hq + 2 * hkv) * d, generator=g, device=dev).to(torch.bfloat16)
+    q, k, v = cq.split_qkv(qkv, hq, hkv)
+    ang = torch.arange(t, dtype=torch.float64, device=dev)[:, None] / \
+        10000.0 ** (torch.arange(0, d, 2, dtype=torch.float64, device=dev) / d)
+    cos, sin = ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
+    ks = cq.CacheSide.empty(5, False, b, hkv, d, t, dev)
+    vs = cq.CacheSide.empty(5, True, b, hkv, d, t, dev)
+    q_out = cq.rope_quant_append(ks, vs, q, k, v, cos, sin, cq.ROPE_HALVES, 0)
+
+    def rope_ref(x):  # (b, h, t, d) bf16 -> bf16
+        xf, c, s = x.float(), cos.float()[None, None], sin.float()[None, None]
+        x1, x2 = xf[..., :d // 2], xf[..., d // 2:]
+        return torch.cat([x1 * c - x2 * s, x1 * s + x2 * c], -1).to(torch.bfloat16)
+    assert torch.equal(q_out, rope_ref(q))
+    ks2 = cq.CacheSide.empty(5, False, b, hkv, d, t, dev)
+    vs2 = cq.CacheSide.empty(5, True, b, hkv, d, t, dev)
+    cq.quant_append(ks2, rope_ref(k), 0)
+    cq.quant_append(vs2, v, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(ks.codes, ks2.codes) and torch.equal(ks.scales, ks2.scales)
+    assert torch.equal(vs.codes, vs2.codes) and torch.equal(vs.scales, vs2.scales)
