@@ -147,3 +147,21 @@ def test_flash_attn_fp8_hadamard(cq, dev):
     assert_close_bf16(out.float().cpu().numpy(), want)
     full = cq.flash_attn(q.to(dev), k.to(dev), v.to(dev), scale, True).float().cpu().numpy()
     assert np.abs(full - out.float().cpu().numpy()).mean() < 2e-2
+
+
+def test_flash_attn_fp8_config4_full_size_matches_bf16_path(cq, dev):
+    """At the config-4 shape with unit descales, the FP8 path is the bf16 prefill on the exact
+    bf16 values of the codes: its staging pass (E4M3 -> bf16, strided K / V) must give the same
+    output bit for bit as flash_attn on those values."""
+    b, s, hq, hkv, d = 4, 4096, 32, 8, 128
+    g = torch.Generator(device=dev).manual_seed(8)
+    q = torch.randn(b, s, hq, d, generator=g, device=dev).to(torch.bfloat16)
+    k8, _ = cq.fp8_quantize_tensor(torch.randn(b, s, hkv, d, generator=g, device=dev))
+    v8, _ = cq.fp8_quantize_tensor(torch.randn(b, s, hkv, d, generator=g, device=dev))
+    out = cq.flash_attn_fp8_codes(q, k8, v8, 1 / d ** 0.5, True)
+    vals = torch.from_numpy(e4m3_values()).to(dev)
+    kb = vals[k8.long()].to(torch.bfloat16)
+    vb = vals[v8.long()].to(torch.bfloat16)
+    ref = cq.flash_attn(q, kb, vb, 1 / d ** 0.5, True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)

@@ -315,3 +315,9 @@ def test_decode_mxfp4_config3_full_size(cq, dev):
 def test_decode_turbo4_config5_full_size(cq, dev):
     """B=8, 64 / 8 heads, D=128, TurboQuant-4, context 131072."""
     full_size_case(cq, dev, "turbo4", 8, 64, 8, 128, 131072, check=(0,))
+
+
+@pytest.mark.parametrize("fmt", ["mxfp8", "nvfp4"])
+def test_decode_block_formats_config2_shape_full_size(cq, dev, fmt):
+    """MXFP8 / NVFP4 caches at the config-2 shape (32 sequences x 8192 keys, 32 / 8 heads)."""
+    full_size_case(cq, dev, fmt, 32, 32, 8, 128, 8192, check=(0, 31))
