@@ -29,6 +29,7 @@
 //    merges the splits (tq_combine's formula), unrotating TurboQuant values. (A fused "last
 //    workgroup combines" variant needs agent-scope release fences, which write back the L2 of
 //    the XCD each time; measured at 6x the whole decode time, so the kernel boundary is used.)
+#include <algorithm>
 #include <vector>
 
 #include "cqkv_device.h"
@@ -1080,6 +1081,38 @@ static int paged_segments(const cqkv_kv_block *blocks, int32_t n_blocks, int32_t
     return n;
 }
 
+// The segment table is written into the workspace by kernels that carry the segments by value
+// in their arguments, kPagedSegsPerLaunch per launch: a captured HIP graph keeps kernel
+// arguments by value, so replays see this call's table (a host -> device copy would keep a
+// pointer to host memory freed when the call returns).
+constexpr int kPagedSegsPerLaunch = 32;  // 32 x 64 B of kernel arguments
+struct PagedTableArgs {
+    PagedSeg seg[kPagedSegsPerLaunch];
+    PagedSeg *dst;
+    int32_t n;
+};
+__global__ __launch_bounds__(64) void paged_table_kernel(PagedTableArgs a) {
+    // 16 words per segment; word w of segment i goes to lane w of iteration i
+    const int lane = threadIdx.x;
+    for (int i = lane / 16; i < a.n; i += 4)
+        ((uint32_t *)(a.dst + i))[lane % 16] = ((const uint32_t *)(a.seg + i))[lane % 16];
+}
+static_assert(sizeof(PagedSeg) == 64, "paged_table_kernel copies 16 words per segment");
+
+static hipError_t write_paged_table(const std::vector<PagedSeg> &segs, PagedSeg *dst,
+                                    hipStream_t st) {
+    for (size_t i0 = 0; i0 < segs.size(); i0 += kPagedSegsPerLaunch) {
+        PagedTableArgs t = {};
+        t.n = (int32_t)std::min<size_t>(kPagedSegsPerLaunch, segs.size() - i0);
+        for (int i = 0; i < t.n; ++i) t.seg[i] = segs[i0 + i];
+        t.dst = dst + i0;
+        hipLaunchKernelGGL(paged_table_kernel, dim3(1), dim3(64), 0, st, t);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 // workspace: the segment table, then (more than one segment) the partials
 static size_t paged_workspace(int nseg, int32_t batch, int32_t q_heads, int32_t q_len,
                               int32_t head_dim, size_t *part_off, size_t *lse_off) {
@@ -1164,8 +1197,7 @@ extern "C" int cqkv_decode_attention_paged(const void *q, int32_t q_dtype,
         CQKV_HIP_CHECK(hipMallocAsync(&ws, need, st));
         owned = true;
     }
-    hipError_t e = hipMemcpyAsync(ws, segs.data(), segs.size() * sizeof(PagedSeg),
-                                  hipMemcpyHostToDevice, st);
+    hipError_t e = write_paged_table(segs, (PagedSeg *)ws, st);
     a.segs = (const PagedSeg *)ws;
     if (nseg > 1) {
         a.part_o = (float *)((char *)ws + part_off);

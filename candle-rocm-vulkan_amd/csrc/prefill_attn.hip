@@ -484,7 +484,9 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     // 1-D grid: consecutive workgroup ids walk the planes (batch, kv head, head group) first, so
     // the workgroups of one plane share an XCD (ids are dealt round-robin to the 8 XCDs) and its
     // L2; the query blocks with the most key tiles come first.
-    const int hgroups = a.group / a.heads_per_wg;
+    // head groups of up to heads_per_wg heads; the last one of a group that is not a multiple
+    // (e.g. 7 = 4 + 3 for 28 / 4 heads) leaves its spare wavefronts idle
+    const int hgroups = (a.group + a.heads_per_wg - 1) / a.heads_per_wg;
     const int nplanes = a.kv_heads * hgroups * a.batch;
     const int plane = (int)blockIdx.x % nplanes;
     const int qb = a.q_blocks - 1 - (int)blockIdx.x / nplanes;
@@ -493,7 +495,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     const int hk = rem % a.kv_heads, hgrp = rem / a.kv_heads;
     const int hslot = wave & 3, qhalf = wave >> 2;
     const int head = hk * a.group + hgrp * a.heads_per_wg + hslot;
-    const bool wave_live = hslot < a.heads_per_wg;
+    const bool wave_live = hslot < a.heads_per_wg && hgrp * a.heads_per_wg + hslot < a.group;
     const int q0 = qb * kPfBQ;
     const PfSeq sq = pf_sequence(a, b);
     const int lq = sq.lq, lk = sq.lk;
@@ -873,9 +875,6 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
     a.kv_heads = kv_heads;
     a.group = q_heads / kv_heads;
     a.heads_per_wg = a.group < 4 ? a.group : 4;
-    if (a.group % a.heads_per_wg != 0)
-        return fail(CQKV_ERR_ARG, "cqkv_flash_attn: q_heads / kv_heads = %d not a multiple of 4 or below 4",
-                    a.group);
     a.q_blocks = (q_len + kPfBQ - 1) / kPfBQ;
     a.wl = window_left;
     a.wr = window_right;
@@ -915,7 +914,7 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
     }
     hipLaunchKernelGGL(prefill_stage_kernel, dim3(a.vt_len / kPfBK, kv_heads, batch), dim3(256),
                        0, st, a);
-    const dim3 grid(a.q_blocks * kv_heads * (a.group / a.heads_per_wg) * batch);
+    const dim3 grid(a.q_blocks * kv_heads * ((a.group + a.heads_per_wg - 1) / a.heads_per_wg) * batch);
     if (softcap > 0.0f || alibi_slopes)
         hipLaunchKernelGGL(prefill_kernel<true>, grid, dim3(kPfWaves * 64), 0, st, a);
     else

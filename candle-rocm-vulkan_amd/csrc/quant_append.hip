@@ -30,7 +30,8 @@ struct AppendArgs {
     float bnd[16];          // TURBO4: the 15 codebook boundaries (+inf padded)
     int32_t pair_loads;     // elements 2l, 2l+1 of every row are one aligned 4 / 8-byte word
     const void *cos, *sin;  // rotary tables (cs_rows, D/2) in the dtype of x (fused RoPE only)
-    int32_t cs_rows;
+    int32_t cs_rows;        // fused RoPE: rows of the tables, positions past them are skipped
+                            // (keys and values alike); 0 for a plain append
     int32_t cs_pair_loads;  // both tables aligned for paired loads
 };
 
@@ -162,7 +163,9 @@ __device__ inline void append_tile(const AppendArgs &a, int h, int b, int bx, in
     const int tile = pos / 8 + bx * 4 + wave;
     const int t_lo = max(tile * 8, pos);
     int t_hi = min(min(tile * 8 + 8, pos + a.tokens), a.capacity);
-    if constexpr (ROPE != 0) t_hi = min(t_hi, a.cs_rows);
+    // the fused RoPE call skips positions past its cos / sin tables on both sides, so a K / V
+    // slot is written for both or neither (cs_rows is 0 for a plain append)
+    if (a.cs_rows > 0) t_hi = min(t_hi, a.cs_rows);
     if (pos < 0 || t_lo >= t_hi) return;
 
     const bool active = lane < D / 2;
@@ -627,6 +630,7 @@ extern "C" int cqkv_rope_quant_append(const cqkv_side *k_side, const cqkv_side *
     r.k.cos = cos;
     r.k.sin = sin;
     r.k.cs_rows = cs_rows;
+    r.v.cs_rows = cs_rows;
     {
         const uintptr_t al = dtype == CQKV_F32 ? 8 : 4;
         r.k.cs_pair_loads = ((uintptr_t)cos % al == 0 && (uintptr_t)sin % al == 0) ? 1 : 0;

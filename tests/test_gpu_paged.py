@@ -125,3 +125,41 @@ def test_paged_caller_workspace(cq, dev):
     assert torch.equal(a, c)
     with pytest.raises(cq.CqkvError):
         cq.decode_attention_paged(q, blocks, 0.1, workspace=ws[:16])
+
+
+def test_paged_decode_graph_capture_replays(cq, dev):
+    """A paged decode captured into a HIP graph and replayed: its segment table travels in kernel
+    arguments (captured by value), so every replay matches the eager result, with eager paged
+    calls over other blocks between the replays (which rewrite the same workspace's table)."""
+    b, hq, hkv, d = 2, 8, 2, 128
+    blocks, others = [], []
+    for n, store in ((70, blocks), (130, blocks), (40, blocks), (90, others), (33, others)):
+        kc = cq.CacheSide.empty(5, False, b, hkv, d, 160, dev)
+        vc = cq.CacheSide.empty(5, True, b, hkv, d, 160, dev)
+        x = kv_source(n + 7, (b, hkv, n, d))
+        cq.quant_append(kc, x.to(dev), 0)
+        cq.quant_append(vc, (x * 0.5).to(dev), 0)
+        store.append((kc, vc, n))
+    q = kv_source(4, (b, hq, 1, d)).to(dev)
+    nbytes = max(cq.decode_paged_workspace_bytes(blocks, b, hq, 1),
+                 cq.decode_paged_workspace_bytes(others, b, hq, 1))
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    out = torch.empty_like(q)
+    cq.decode_attention_paged(q, blocks, 0.1, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    want = out.clone()
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            cq.decode_attention_paged(q, blocks, 0.1, out=out, workspace=ws)
+    torch.cuda.current_stream(dev).wait_stream(s)
+    for i in range(4):
+        other = cq.decode_attention_paged(q, others, 0.1, workspace=ws)  # rewrites the table
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {i} differs from the eager result"
+        assert not torch.equal(other, want)

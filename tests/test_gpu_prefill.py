@@ -39,7 +39,7 @@ def run_flash(cq, dev, b, sq, sk, hq, hkv, d=128, causal=True, wl=-1, wr=-1, see
     return got.float().cpu().numpy(), want
 
 
-@pytest.mark.parametrize("hq,hkv", [(8, 2), (4, 4), (8, 4), (16, 2)])
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (4, 4), (8, 4), (16, 2), (28, 4), (20, 4), (12, 2)])
 def test_prefill_causal_gqa(cq, dev, hq, hkv):
     got, want = run_flash(cq, dev, 2, 200, 200, hq, hkv)
     assert_close_bf16(got, want)

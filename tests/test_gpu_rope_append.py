@@ -188,3 +188,32 @@ def test_rope_append_config4_full_size(cq, dev):
     torch.cuda.synchronize()
     assert torch.equal(ks.codes, ks2.codes) and torch.equal(ks.scales, ks2.scales)
     assert torch.equal(vs.codes, vs2.codes) and torch.equal(vs.scales, vs2.scales)
+
+
+def test_rope_append_positions_past_table_skip_keys_and_values(cq, dev):
+    """Cos / sin tables shorter than the cache: a position past the table is skipped on both
+    sides, so no value row is written without its key row (and rows already there survive)."""
+    b, hq, hkv, d, t, cap, rows = 3, 4, 2, 128, 4, 64, 40
+    qkv = kv_source(5, (b, t, 1, (hq + 2 * hkv) * d))[:, :, 0].to(dev)
+    q, k, v = cq.split_qkv(qkv, hq, hkv)
+    cos, sin = tables(rows, d, "bf16")
+    pos = torch.tensor([0, 37, 50], dtype=torch.int32, device=dev)
+    ks = cq.CacheSide.empty(5, False, b, hkv, d, cap, dev)
+    vs = cq.CacheSide.empty(5, True, b, hkv, d, cap, dev)
+    pre_k = oracle_rows(5, kv_source(93, (b, hkv, cap, d)))
+    pre_v = oracle_rows(5, kv_source(94, (b, hkv, cap, d)))
+    cq.rows_import(ks, torch.from_numpy(pre_k.view(np.int32)).to(dev), 0)
+    cq.rows_import(vs, torch.from_numpy(pre_v.view(np.int32)).to(dev), 0)
+    cq.rope_quant_append(ks, vs, q, k, v, cos.to(dev), sin.to(dev), 1, positions=pos)
+    torch.cuda.synchronize()
+    got_k, got_v = export_np(cq, ks, cap), export_np(cq, vs, cap)
+    want_k, want_v = pre_k.copy(), pre_v.copy()
+    for bi, p in enumerate(pos.tolist()):
+        n = max(0, min(t, rows - p))  # positions below the table's rows only
+        if n == 0:
+            continue
+        k_rot = expected_rope(k[bi:bi + 1, :, :n].cpu(), cos, sin, 1, p, "bf16")
+        want_k[bi:bi + 1, :, p:p + n] = O.quantize_rows(5, 0, k_rot)
+        want_v[bi:bi + 1, :, p:p + n] = O.quantize_rows(5, 0, v[bi:bi + 1, :, :n].float().cpu().numpy())
+    np.testing.assert_array_equal(got_k, want_k)
+    np.testing.assert_array_equal(got_v, want_v)
