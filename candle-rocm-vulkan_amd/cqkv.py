@@ -76,6 +76,8 @@ def lib() -> ctypes.CDLL:
         L.cqkv_decode_splits.restype = i32
         L.cqkv_decode_attention.argtypes = [P, i32, I64P, SP, SP, i32, i32, i32, P, i32, f32,
                                             i32, i32, P, i32, I64P, i32, P, sz, P]
+        L.cqkv_decode_attention_noalloc.argtypes = [P, i32, I64P, SP, SP, i32, i32, i32, P, i32,
+                                                    f32, i32, i32, P, i32, I64P, i32, P]
         BP = ctypes.POINTER(KvBlock)
         L.cqkv_decode_paged_workspace_bytes.argtypes = [BP, i32, i32, i32, i32]
         L.cqkv_decode_paged_workspace_bytes.restype = sz
@@ -106,6 +108,7 @@ def lib() -> ctypes.CDLL:
 EXPORTED = ["cqkv_codes_plane_bytes", "cqkv_scales_plane_bytes", "cqkv_quant_append",
             "cqkv_rope_quant_append",
             "cqkv_decode_workspace_bytes", "cqkv_decode_splits", "cqkv_decode_attention",
+            "cqkv_decode_attention_noalloc",
             "cqkv_decode_paged_workspace_bytes", "cqkv_decode_attention_paged",
             "cqkv_flash_attn", "cqkv_flash_attn_ext", "cqkv_fp8_quantize_tensor",
             "cqkv_flash_attn_fp8", "cqkv_hadamard_rows", "cqkv_reference_row_words", "cqkv_rows_import",
@@ -273,6 +276,36 @@ def decode_attention(q: torch.Tensor, k: CacheSide, v: CacheSide, kv_len: int,
         _DTYPES[out.dtype], _strides3(out, (0, 1, 2)), splits, _ptr(workspace),
         0 if workspace is None else workspace.numel() * workspace.element_size(),
         _stream(q.device)))
+    return out
+
+
+DECODE_SCRATCH_BYTES = 32 << 20  # CQKV_DECODE_SCRATCH_BYTES
+
+
+def decode_attention_noalloc(q: torch.Tensor, k: CacheSide, v: CacheSide, kv_len: int,
+                             softmax_scale: float, kv_lens: torch.Tensor | None = None,
+                             window_left: int = -1, window_right: int = -1,
+                             out: torch.Tensor | None = None, splits: int = 0) -> torch.Tensor:
+    """decode_attention through cqkv_decode_attention_noalloc: no device allocation by the
+    library (split partials in its per-GPU device scratch array). `out` must be given for a call
+    that may not allocate at all (otherwise torch allocates it here)."""
+    _need_gpu(q, "q")
+    b, hq, lq, d = q.shape
+    if q.stride(3) != 1:
+        raise CqkvError(ERR_ARG, "q must have a contiguous head dim")
+    if b != k.batch or b != v.batch or d != k.head_dim:
+        raise CqkvError(ERR_ARG, f"q {tuple(q.shape)} does not match the cache sides")
+    if kv_lens is not None and (kv_lens.numel() != b or kv_lens.dtype != torch.int32):
+        raise CqkvError(ERR_ARG, "kv_lens must be int32 with one length per batch entry")
+    if out is None:
+        out = torch.empty_like(q)
+    elif tuple(out.shape) != tuple(q.shape) or out.stride(3) != 1:
+        raise CqkvError(ERR_ARG, f"out {tuple(out.shape)} does not match q")
+    ks, vs = k.struct(), v.struct()
+    _check(lib().cqkv_decode_attention_noalloc(
+        _ptr(q), _DTYPES[q.dtype], _strides3(q, (0, 1, 2)), ctypes.byref(ks), ctypes.byref(vs), b,
+        hq, lq, _ptr(kv_lens), kv_len, softmax_scale, window_left, window_right, _ptr(out),
+        _DTYPES[out.dtype], _strides3(out, (0, 1, 2)), splits, _stream(q.device)))
     return out
 
 

@@ -30,6 +30,7 @@
 //    workgroup combines" variant needs agent-scope release fences, which write back the L2 of
 //    the XCD each time; measured at 6x the whole decode time, so the kernel boundary is used.)
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 #include "cqkv_device.h"
@@ -969,33 +970,80 @@ static hipError_t decode_launch(const DecodeArgs &a, int format, int d, hipStrea
     return e;
 }
 
-extern "C" int cqkv_decode_attention(const void *q, int32_t q_dtype, const int64_t q_strides[3],
-                                     const cqkv_side *k, const cqkv_side *v, int32_t batch,
-                                     int32_t q_heads, int32_t q_len, const int32_t *kv_lens,
-                                     int32_t kv_len, float softmax_scale, int32_t window_left,
-                                     int32_t window_right, void *out, int32_t out_dtype,
-                                     const int64_t out_strides[3], int32_t splits,
-                                     void *workspace, size_t workspace_bytes,
-                                     cqkv_stream_t stream) {
-    clear_error();
+// ---- allocation-free decode: split partials in a library-owned device array ----
+// `scratch` is one array per GPU (each device that loads the library's code object holds its own
+// copy at its own address), kept until the process ends. In host code its name is only a
+// host-side stand-in: the device address comes from hipGetSymbolAddress, fetched once per device
+// with that device current, and only that address is ever handed to kernels. Every
+// cqkv_decode_attention_noalloc call on a GPU shares that GPU's array; calls that overlap on one
+// GPU (concurrent streams) race on it.
+static __device__ __attribute__((aligned(256))) uint8_t scratch[CQKV_DECODE_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kMaxDevices];
+
+static int scratch_address(void **out, const char *who) {
+    int dev = -1;
+    CQKV_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(CQKV_ERR_ARG, "%s: device ordinal %d above %d", who, dev, kMaxDevices - 1);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(CQKV_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", who,
+                        dev, hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return CQKV_OK;
+}
+
+// The dense decode of both entry points. noalloc: the partials go to the device `scratch` array
+// (automatic splits are lowered until they fit; explicit ones that do not fit are refused);
+// otherwise to `workspace`, or to a stream-ordered allocation when none is given.
+static int decode_dense(const char *who, const void *q, int32_t q_dtype,
+                        const int64_t q_strides[3], const cqkv_side *k, const cqkv_side *v,
+                        int32_t batch, int32_t q_heads, int32_t q_len, const int32_t *kv_lens,
+                        int32_t kv_len, float softmax_scale, int32_t window_left,
+                        int32_t window_right, void *out, int32_t out_dtype,
+                        const int64_t out_strides[3], int32_t splits, void *workspace,
+                        size_t workspace_bytes, bool noalloc, cqkv_stream_t stream) {
     DecodeArgs a;
-    if (int rc = decode_prepare(a, "cqkv_decode_attention", q, q_dtype, q_strides, k, v, batch,
-                                q_heads, q_len, softmax_scale, window_left, window_right, out,
-                                out_dtype, out_strides))
+    if (int rc = decode_prepare(a, who, q, q_dtype, q_strides, k, v, batch, q_heads, q_len,
+                                softmax_scale, window_left, window_right, out, out_dtype,
+                                out_strides))
         return rc;
     if (k->capacity != v->capacity)
-        return fail(CQKV_ERR_ARG, "cqkv_decode_attention: key / value capacities %d / %d differ",
-                    k->capacity, v->capacity);
+        return fail(CQKV_ERR_ARG, "%s: key / value capacities %d / %d differ", who, k->capacity,
+                    v->capacity);
     if (kv_len < 0 || kv_len > k->capacity)
-        return fail(CQKV_ERR_ARG, "cqkv_decode_attention: kv_len %d outside [0, capacity %d]",
-                    kv_len, k->capacity);
-    if (splits < 0) return fail(CQKV_ERR_ARG, "cqkv_decode_attention: splits %d", splits);
+        return fail(CQKV_ERR_ARG, "%s: kv_len %d outside [0, capacity %d]", who, kv_len,
+                    k->capacity);
+    if (splits < 0) return fail(CQKV_ERR_ARG, "%s: splits %d", who, splits);
     const int hkv = k->kv_heads, d = k->head_dim;
 
     const int tiles = max(1, tiles_of(kv_len));
     int s = splits > 0 ? min(splits, tiles)
                        : auto_splits(batch, hkv, max(kv_len, 1), kv_lens != nullptr,
                                      waves_of(k->format));
+    size_t lse_off = 0;
+    if (noalloc) {
+        if (s > 1 &&
+            workspace_layout(batch, q_heads, q_len, d, s, &lse_off) > CQKV_DECODE_SCRATCH_BYTES) {
+            if (splits > 0)
+                return fail(CQKV_ERR_WORKSPACE,
+                            "%s: %d splits need %zu bytes of partials, above the %zu-byte "
+                            "device scratch",
+                            who, s, workspace_layout(batch, q_heads, q_len, d, s, &lse_off),
+                            (size_t)CQKV_DECODE_SCRATCH_BYTES);
+            while (s > 1 && workspace_layout(batch, q_heads, q_len, d, s, &lse_off) >
+                                CQKV_DECODE_SCRATCH_BYTES)
+                --s;
+        }
+    }
     const int tps = (tiles + s - 1) / s;
     s = (tiles + tps - 1) / tps;
 
@@ -1016,12 +1064,13 @@ extern "C" int cqkv_decode_attention(const void *q, int32_t q_dtype, const int64
     void *ws = workspace;
     bool owned = false;
     if (s > 1) {
-        size_t lse_off;
         const size_t need = workspace_layout(batch, q_heads, q_len, d, s, &lse_off);
-        if (ws && workspace_bytes < need)
-            return fail(CQKV_ERR_WORKSPACE, "cqkv_decode_attention: workspace %zu < %zu bytes",
+        if (noalloc) {
+            if (int rc = scratch_address(&ws, who)) return rc;
+        } else if (ws && workspace_bytes < need) {
+            return fail(CQKV_ERR_WORKSPACE, "%s: workspace %zu < %zu bytes", who,
                         workspace_bytes, need);
-        if (!ws) {
+        } else if (!ws) {
             CQKV_HIP_CHECK(hipMallocAsync(&ws, need, st));
             owned = true;
         }
@@ -1033,9 +1082,38 @@ extern "C" int cqkv_decode_attention(const void *q, int32_t q_dtype, const int64
         hipError_t fe = hipFreeAsync(ws, st);
         if (e == hipSuccess) e = fe;
     }
-    if (e != hipSuccess)
-        return fail(CQKV_ERR_HIP, "cqkv_decode_attention: launch failed: %s", hipGetErrorString(e));
+    if (e != hipSuccess) return fail(CQKV_ERR_HIP, "%s: launch failed: %s", who, hipGetErrorString(e));
     return CQKV_OK;
+}
+
+extern "C" int cqkv_decode_attention(const void *q, int32_t q_dtype, const int64_t q_strides[3],
+                                     const cqkv_side *k, const cqkv_side *v, int32_t batch,
+                                     int32_t q_heads, int32_t q_len, const int32_t *kv_lens,
+                                     int32_t kv_len, float softmax_scale, int32_t window_left,
+                                     int32_t window_right, void *out, int32_t out_dtype,
+                                     const int64_t out_strides[3], int32_t splits,
+                                     void *workspace, size_t workspace_bytes,
+                                     cqkv_stream_t stream) {
+    clear_error();
+    return decode_dense("cqkv_decode_attention", q, q_dtype, q_strides, k, v, batch, q_heads,
+                        q_len, kv_lens, kv_len, softmax_scale, window_left, window_right, out,
+                        out_dtype, out_strides, splits, workspace, workspace_bytes, false, stream);
+}
+
+extern "C" int cqkv_decode_attention_noalloc(const void *q, int32_t q_dtype,
+                                             const int64_t q_strides[3], const cqkv_side *k,
+                                             const cqkv_side *v, int32_t batch, int32_t q_heads,
+                                             int32_t q_len, const int32_t *kv_lens,
+                                             int32_t kv_len, float softmax_scale,
+                                             int32_t window_left, int32_t window_right,
+                                             void *out, int32_t out_dtype,
+                                             const int64_t out_strides[3], int32_t splits,
+                                             cqkv_stream_t stream) {
+    clear_error();
+    return decode_dense("cqkv_decode_attention_noalloc", q, q_dtype, q_strides, k, v, batch,
+                        q_heads, q_len, kv_lens, kv_len, softmax_scale, window_left,
+                        window_right, out, out_dtype, out_strides, splits, nullptr, 0, true,
+                        stream);
 }
 
 // ---- paged decode ----

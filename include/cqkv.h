@@ -167,6 +167,25 @@ int cqkv_decode_attention(const void *q, int32_t q_dtype, const int64_t q_stride
                           int32_t splits, void *workspace, size_t workspace_bytes,
                           cqkv_stream_t stream);
 
+/* Allocation-free variant of cqkv_decode_attention. It has no counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same arguments and results as cqkv_decode_attention
+ * without the workspace; the split partials live in a library-owned device array of
+ * CQKV_DECODE_SCRATCH_BYTES per GPU (held until the process ends; its address is looked up once
+ * per device, with that device current). Automatic splits (splits = 0) are lowered until the
+ * partials fit that array; an explicit split count whose partials do not fit is refused with
+ * CQKV_ERR_WORKSPACE. Nothing is allocated or freed. Every call on one GPU shares that GPU's
+ * array, and the array keeps the last call's partials: calls that overlap on one GPU (on
+ * concurrent streams) race, so serialize them. */
+#define CQKV_DECODE_SCRATCH_BYTES (32u << 20)
+int cqkv_decode_attention_noalloc(const void *q, int32_t q_dtype, const int64_t q_strides[3],
+                                  const cqkv_side *k, const cqkv_side *v, int32_t batch,
+                                  int32_t q_heads, int32_t q_len, const int32_t *kv_lens,
+                                  int32_t kv_len, float softmax_scale, int32_t window_left,
+                                  int32_t window_right, void *out, int32_t out_dtype,
+                                  const int64_t out_strides[3], int32_t splits,
+                                  cqkv_stream_t stream);
+
 /* One block of a paged cache (the reference's KvBlockRef, candle-nn/src/flash_attn.rs:609-613,
  * packed into a PageTable, candle-core/src/accel/attention.rs:307-366): a key side and a value
  * side holding `rows` valid tokens at the start of every (batch, kv head) plane. The keys of a
