@@ -58,6 +58,49 @@ def attn_case():
     print("attn", out.shape)
 
 
+def attn_format_case(name, mode, bits):
+    """The reference's fused decode (tq_attn* + tq_combine on its host emulator) over rows of one
+    format, GQA group 4, three splits, outlier channels (1 % of the (head, dim) channels x8),
+    then the value unrotation of fused_attention_rows (candle-nn/src/turbo_quant.rs:1263) in f32.
+    TurboQuant-4 rows are the reference kernel's encoding of the Hadamard-rotated rows (keys seed
+    42, values 44), the query is rotated with the key rotation (turbo_quant.rs:1162)."""
+    B, Hq, Hkv, D, Lq, Lk = 2, 8, 2, 128, 2, 333
+    rng = np.random.default_rng(400 + mode)
+    mask = rng.random((Hkv, D)) < 0.01
+    mask[0, 5] = mask[1, 77] = True
+    q = O.round_bf16(O.normal(401 + mode, (B, Hq, Lq, D)))
+    k = O.normal(402 + mode, (B, Hkv, Lk, D))
+    v = O.normal(403 + mode, (B, Hkv, Lk, D))
+    k = O.round_bf16(np.where(mask[None, :, None, :], k * 8, k)).astype(np.float32)
+    v = O.round_bf16(np.where(mask[None, :, None, :], v * 8, v)).astype(np.float32)
+    l = O.row_layout(mode, bits, D)
+    turbo = mode == O.TURBO_MSE
+    if turbo:
+        c, b = O.lloyd_max(D, bits)
+        tab = H.tq_tab(c, b)
+        pk = O.rotation_matrix(D, O.ROT_HADAMARD, 42)
+        pv = O.rotation_matrix(D, O.ROT_HADAMARD, 44)
+        kx = O.rotate_rows(pk, k.reshape(-1, D))
+        vx = O.rotate_rows(pv, v.reshape(-1, D))
+        qx = O.rotate_rows(pk, q.reshape(-1, D)).reshape(q.shape)
+    else:
+        tab = H.tq_tab()
+        kx, vx, qx = k.reshape(-1, D), v.reshape(-1, D), q
+    enc = lambda x: H.tq_quant(x.astype(np.float32), mode, l.code_bits, l.code_words,
+                               l.aux_words, l.row_words, tab).reshape(B, Hkv, Lk, l.row_words)
+    kd, vd = enc(kx), enc(vx)
+    side = (mode, l.code_bits, l.code_words, l.code_words + l.aux_words)
+    tab64 = np.concatenate([tab, tab]).astype(np.float32)
+    scale = np.float32(1.0 / np.sqrt(D))
+    o = H.tq_attn(qx.astype(np.float32), kd, vd, side, side, tab64, float(scale), splits=3,
+                  group=4)
+    if turbo:
+        o = (o.reshape(-1, D) @ pv).reshape(o.shape).astype(np.float32)
+    np.savez_compressed(os.path.join(HERE, f"ref_decode_{name}.npz"), q=q.astype(np.float32),
+                        kd=kd, vd=vd, out=o, scale=scale, mode=mode, bits=bits)
+    print("decode", name, o.shape)
+
+
 def fa_case():
     # soft-capping, per-(batch, head) ALiBi slopes and a window through the reference's tile
     # kernel, dense and variable-length (the score terms of candle-flash-attn's *_softcap / *_alibi
@@ -105,4 +148,8 @@ if __name__ == "__main__":
     quant_case("mxfp8_d64", O.MXFP8, 0, 64, 19, 19)
     fa_case()
     attn_case()
+    attn_format_case("turbo4", O.TURBO_MSE, 4)
+    attn_format_case("mxfp4", O.MXFP4, 0)
+    attn_format_case("nvfp4", O.NVFP4, 0)
+    attn_format_case("mxfp8", O.MXFP8, 0)
     combine_case()
