@@ -22,10 +22,13 @@ FP8 append) and 5 (TurboQuant-4, context 128K) with the same timing method; they
 figures, not the headline value. "c2_shape_mxfp8" / "c2_shape_nvfp4" time the decode of the
 other block-scaled formats at the config-2 shape; "c4_shape_fp8_kv" the attention over E4M3
 K / V with descales at the config-4 shape; "ra_*" time the fused RoPE + FP8
-quantize-append at the config-4 prefill shape and at one config-2 decode step.
+quantize-append at the config-4 prefill shape and at one config-2 decode step; "append_c2_shape"
+the plain quantize-and-append of each format and side.
+Each "cpu_baseline" is the oracle's restatement of the reference CPU path, timed on this host's
+CPUs (all of those this process may use) on a bounded sample of the workload and scaled to it.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
-                       [--only c2,c3,c4,c5,f8,fx,ra] [--calibration-copy]
+                       [--only c2,c3,c4,c5,f8,fx,ap,ra] [--calibration-copy]
 """
 from __future__ import annotations
 
@@ -113,22 +116,90 @@ def read_traffic():
         return None
 
 
-def cpu_baseline_decode(cq, cache, q, b_sample, ctx, scale, threads):
-    """Oracle CPU path on the first b_sample sequences; returns seconds per full call."""
+def cpu_info():
+    """Threads the CPU baseline uses (every CPU this process may run on), the machine's logical
+    CPU count and model."""
+    threads = len(os.sched_getaffinity(0))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return threads, {"nproc": os.cpu_count(), "cpu_model": model}
+
+
+def side_rows(cq, side, b0, nb, tokens):
+    """Reference rows (nb, kv_heads, tokens, words) of sequences b0 .. b0 + nb - 1 of a cache side
+    (its planes are batch-major, so those sequences are one contiguous slice)."""
     import numpy as np
-    from oracle import oracle as O
-    b = q.shape[0]
-    kr = cq.rows_export(cache.k, ctx).cpu().numpy().view(np.uint32)[:b_sample]
-    vr = cq.rows_export(cache.v, ctx).cpu().numpy().view(np.uint32)[:b_sample]
-    qb = O.f32_to_bf16_bits(q[:b_sample].float().cpu().numpy())
+    cb, sb = side.codes.numel() // side.batch, side.scales.numel() // side.batch
+    view = cq.CacheSide(side.fmt, side.is_value, nb, side.kv_heads, side.head_dim, side.capacity,
+                        side.codes[b0 * cb:(b0 + nb) * cb], side.scales[b0 * sb:(b0 + nb) * sb],
+                        side.seed)
+    return cq.rows_export(view, tokens).cpu().numpy().view(np.uint32)
+
+
+def timed_reps(fn, budget_s=10.0, max_reps=20):
     reps, t_total = 0, 0.0
-    while t_total < 10.0 and reps < 20:
+    while t_total < budget_s and reps < max_reps:
         t0 = time.perf_counter()
-        O.cache_attention(qb, kr, vr, (O.FP8, 0), (O.FP8, 0), None, None, ctx, scale,
-                          threads=threads)
+        fn()
         t_total += time.perf_counter() - t0
         reps += 1
-    return t_total / reps * (b / b_sample), reps
+    return t_total / reps, reps
+
+
+def cpu_baseline_decode(cq, cache, q, fmt, seqs, tokens, scale, threads, kv_lens=None):
+    """The oracle's restatement of the reference CPU decode path (dequantize, unrotate, bf16
+    cache, unfused f32 attention) over the sequences `seqs` (a contiguous range); returns seconds
+    for that sample and the repetitions timed."""
+    import numpy as np
+    from oracle import oracle as O
+    b0, nb = seqs[0], len(seqs)
+    kr = side_rows(cq, cache.k, b0, nb, tokens)
+    vr = side_rows(cq, cache.v, b0, nb, tokens)
+    qb = O.f32_to_bf16_bits(q[b0:b0 + nb].float().cpu().numpy())
+    bits = 4 if fmt == O.TURBO_MSE else 0
+    pk = pv = None
+    if fmt == O.TURBO_MSE:
+        d = q.shape[-1]
+        pk = O.rotation_matrix(d, O.ROT_HADAMARD, cache.k.seed)
+        pv = O.rotation_matrix(d, O.ROT_HADAMARD, cache.v.seed)
+    lens = None if kv_lens is None else np.array(kv_lens[b0:b0 + nb], np.int32)
+    return timed_reps(lambda: O.cache_attention(qb, kr, vr, (fmt, bits), (fmt, bits), pk, pv,
+                                                tokens, scale, kv_lens=lens, threads=threads))
+
+
+def cpu_baseline_prefill(threads, heads=4):
+    """Config 4 on the CPU: the oracle's causal f32 attention (the reference's unfused CPU path)
+    for `heads` query heads (one kv head) of one sequence, plus the FP8 quantize_rows of that
+    sequence's K / V rows; returns seconds scaled to the whole call (4 sequences x 32 heads)."""
+    import numpy as np
+    from oracle import oracle as O
+    s, d = 4096, 128
+    rng = np.random.default_rng(7)
+    q = O.round_bf16(rng.standard_normal((1, heads, s, d), dtype=np.float32))
+    k = O.round_bf16(rng.standard_normal((1, 1, s, d), dtype=np.float32))
+    v = O.round_bf16(rng.standard_normal((1, 1, s, d), dtype=np.float32))
+    kv_rows = O.round_bf16(rng.standard_normal((8 * s, d), dtype=np.float32))
+    t_att, reps = timed_reps(lambda: O.attention_unfused(q, k, v, 1.0 / d ** 0.5, wl=-1, wr=0,
+                                                         threads=threads), max_reps=5)
+    t_app, _ = timed_reps(lambda: (O.quantize_rows(O.FP8, 0, kv_rows, threads=threads),
+                                   O.quantize_rows(O.FP8, 0, kv_rows, threads=threads)),
+                          budget_s=2.0, max_reps=5)
+    return t_att * (4 * 32 / heads) + t_app * 4, reps, heads
+
+
+def cpu_baseline_entry(value, unit, us_per_call, threads, info, sample, reps):
+    e = {"value": value, "unit": unit, "cores": threads, "kind": "port",
+         "us_per_call": round(us_per_call, 1), "reps": reps,
+         "sample": sample}
+    e.update(info)
+    return e
 
 
 def decode_case(cq, dev, stream, fmt, b, hq, hkv, d, ctx, steps, warmup, lens=None, chunk=2048):
@@ -256,6 +327,31 @@ def fp8_attn_case(cq, dev, stream, steps, warmup):
             "timed": "whole call: E4M3 -> bf16 staging, V transpose pre-pass, prefill kernel"}
 
 
+def append_case(cq, dev, stream, steps, warmup, b=32, hkv=8, d=128, t=2048):
+    """cqkv_quant_append alone: B=32 sequences x 8 kv heads x 2048 tokens (524,288 rows of the
+    config-2 cache shape) of bf16 K or V into FP8 / MXFP4 / TURBO4 / MXFP8 / NVFP4 sides at
+    position 0. Bytes = the bf16 rows read plus the codes and scales written."""
+    import torch
+    x = kv_gpu((b, hkv, t, d), 51, dev)
+    res = {}
+    names = {cq.FP8: "fp8", cq.MXFP4: "mxfp4", cq.TURBO4: "turbo4", cq.MXFP8: "mxfp8",
+             cq.NVFP4: "nvfp4"}
+    for fmt, name in names.items():
+        for is_value in (False, True):
+            side = cq.CacheSide.empty(fmt, is_value, b, hkv, d, t, dev, seed=44 if is_value else 42)
+            ms = time_calls(lambda i: cq.quant_append(side, x, 0), steps, warmup, stream)
+            nbytes = x.numel() * 2 + b * hkv * t * row_bytes(fmt, d)
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            res[f"{name}_{'values' if is_value else 'keys'}"] = {
+                "us_per_call": round(ms * 1e3, 2), "bytes_per_call": nbytes,
+                "achieved_gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+            del side
+    torch.cuda.empty_cache()
+    return {"workload": f"cqkv_quant_append of bf16 rows, B={b} x {hkv} kv heads x {t} tokens, "
+                        f"D={d}", "bound": "hbm", "peak_gbs": HBM_PEAK_GBS,
+            "timed": "one quant_append launch per call", "per_side": res}
+
+
 def decode_summary(name, ms, nbytes, extra):
     gbs = nbytes / (ms * 1e-3) / 1e9
     res = {"workload": name, "us_per_call": round(ms * 1e3, 2), "bytes_per_call": nbytes,
@@ -284,7 +380,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
-    ap.add_argument("--only", default="", help="comma list of c2,c3,c4,c5,f8,fx,ra (default: all)")
+    ap.add_argument("--only", default="", help="comma list of c2,c3,c4,c5,f8,fx,ap,ra (default: all)")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="also run a plain 1 GiB copy (for counter scaling)")
     args = ap.parse_args()
@@ -297,6 +393,7 @@ def main():
     import torch
     cq = load_cqkv()
     cq.lib()
+    threads, info = cpu_info()
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream(dev)
     only = set(x for x in args.only.split(",") if x)
@@ -313,15 +410,17 @@ def main():
         splits = cq.decode_splits(B, HKV, CTX)
         achieved = nbytes / (ms * 1e-3) / 1e9  # GB/s
         log(f"config 2: {ms * 1e3:.2f} us/call, {achieved:.1f} GB/s")
-        cores = min(16, os.cpu_count() or 1)
         cpu = None
         if not args.no_cpu:
-            sec, reps = cpu_baseline_decode(cq, caches[0], q, 2, CTX, 1.0 / D ** 0.5, cores)
-            cpu = {"value": round(nbytes / sec / 1e12, 6), "unit": "TB/s", "cores": cores,
-                   "kind": "port", "us_per_call": round(sec * 1e6, 1),
-                   "sample": f"oracle cache_attention (reference CPU path restated in C) on 2 "
-                             f"of the 32 sequences, {reps} reps, scaled x16 to the full call"}
-            log(f"cpu baseline: {sec * 1e6:.0f} us/call on {cores} threads")
+            sec, reps = cpu_baseline_decode(cq, caches[0], q, cq.FP8, range(2), CTX,
+                                            1.0 / D ** 0.5, threads)
+            sec *= B / 2
+            cpu = cpu_baseline_entry(
+                round(nbytes / sec / 1e12, 6), "TB/s", sec * 1e6, threads, info,
+                "oracle cache_attention (the reference CPU decode path restated in C: "
+                "dequantize, bf16 cache, unfused f32 attention) on 2 of the 32 sequences, "
+                "scaled x16 to the full call", reps)
+            log(f"cpu baseline: {sec * 1e6:.0f} us/call on {threads} threads")
         del caches
         traffic = read_traffic()
         res = {
@@ -358,32 +457,59 @@ def main():
         # the MFMA clocks settle over the first ~100 calls: a longer untimed warm-up
         other["c4_prefill"] = prefill_case(cq, dev, stream, max(steps_x, 20), max(warm_x, 80))
         log(f"config 4: {other['c4_prefill']['us_per_call']} us/call")
+        if not args.no_cpu:
+            sec, reps, heads = cpu_baseline_prefill(threads)
+            other["c4_prefill"]["cpu_baseline"] = cpu_baseline_entry(
+                round(other["c4_prefill"]["flop_per_call"] / sec / 1e12, 6), "TFLOP/s",
+                sec * 1e6, threads, info,
+                f"oracle attention_unfused (the reference CPU path: f32 q k^T, scale, mask, "
+                f"softmax, p v) causal on {heads} of the 32 query heads of sequence 0, plus the "
+                f"FP8 quantize_rows of its 8 x 4096 K and V rows, scaled to the 4 x 32 heads", reps)
+            log(f"config 4 cpu: {sec * 1e6:.0f} us/call")
         torch.cuda.empty_cache()
     if want("c3"):
         import random
         rng = random.Random(3)
         lens = [rng.randint(1024, 32768) for _ in range(64)]
         log("config 3: MXFP4 ragged decode B=64 32/8 d=128")
-        caches, _, ms, nbytes = decode_case(cq, dev, stream, cq.MXFP4, 64, 32, 8, 128, 32768,
-                                            steps_x, warm_x, lens=lens)
-        del caches
+        caches, q3, ms, nbytes = decode_case(cq, dev, stream, cq.MXFP4, 64, 32, 8, 128, 32768,
+                                             steps_x, warm_x, lens=lens)
         other["c3_mxfp4_ragged"] = decode_summary(
             "BASELINE config 3: MXFP4-KV ragged decode", ms, nbytes,
             {"batch": 64, "q_heads": 32, "kv_heads": 8, "head_dim": 128,
              "lens": "uniform [1024, 32768], random.Random(3)", "sum_len": int(sum(lens)),
              "timed": "whole call (split-K decode + combine)"})
         log(f"config 3: {ms * 1e3:.2f} us/call")
+        if not args.no_cpu:
+            sec, reps = cpu_baseline_decode(cq, caches[0], q3, cq.MXFP4, range(2), 32768,
+                                            1.0 / 128 ** 0.5, threads, kv_lens=lens)
+            sec *= sum(lens) / sum(lens[:2])  # the CPU path's work is linear in the keys
+            other["c3_mxfp4_ragged"]["cpu_baseline"] = cpu_baseline_entry(
+                round(nbytes / sec / 1e12, 6), "TB/s", sec * 1e6, threads, info,
+                f"oracle cache_attention on sequences 0-1 ({lens[0] + lens[1]} keys), scaled by "
+                f"the key count to the call's {sum(lens)}", reps)
+            log(f"config 3 cpu: {sec * 1e6:.0f} us/call")
+        del caches
         torch.cuda.empty_cache()
     if want("c5"):
         log("config 5: TurboQuant-4 decode B=8 64/8 d=128 ctx 131072")
-        caches, _, ms, nbytes = decode_case(cq, dev, stream, cq.TURBO4, 8, 64, 8, 128, 131072,
-                                            steps_x, warm_x, chunk=8192)
-        del caches
+        caches, q5, ms, nbytes = decode_case(cq, dev, stream, cq.TURBO4, 8, 64, 8, 128, 131072,
+                                             steps_x, warm_x, chunk=8192)
         other["c5_turbo4"] = decode_summary(
             "BASELINE config 5: TurboQuant-4 KV decode", ms, nbytes,
             {"batch": 8, "q_heads": 64, "kv_heads": 8, "head_dim": 128, "context": 131072,
              "timed": "whole call (split-K decode + combine with unrotation)"})
         log(f"config 5: {ms * 1e3:.2f} us/call")
+        if not args.no_cpu:
+            sec, reps = cpu_baseline_decode(cq, caches[0], q5, cq.TURBO4, range(1), 131072,
+                                            1.0 / 128 ** 0.5, threads)
+            sec *= 8
+            other["c5_turbo4"]["cpu_baseline"] = cpu_baseline_entry(
+                round(nbytes / sec / 1e12, 6), "TB/s", sec * 1e6, threads, info,
+                "oracle cache_attention (with the Hadamard unrotation of both sides) on 1 of the 8 "
+                "sequences, scaled x8", reps)
+            log(f"config 5 cpu: {sec * 1e6:.0f} us/call")
+        del caches
         torch.cuda.empty_cache()
 
     if want("f8"):
@@ -406,6 +532,11 @@ def main():
                  "timed": "whole call (split-K decode + combine)"})
             log(f"{name}: {ms * 1e3:.2f} us/call")
             torch.cuda.empty_cache()
+    if want("ap"):
+        log("append: B=32 x 8 kv heads x 2048 tokens, D=128, every format, keys and values")
+        other["append_c2_shape"] = append_case(cq, dev, stream, steps_x, warm_x)
+        log("append: " + ", ".join(f"{k} {v['us_per_call']} us"
+                                   for k, v in other["append_c2_shape"]["per_side"].items()))
     if want("ra"):
         log("fused RoPE + FP8 append: prefill shape (config 4) and one decode step (config 2)")
         other["ra_prefill_c4"] = rope_append_case(cq, dev, stream, cq.FP8, 4, 32, 8, 128, 4096,

@@ -130,6 +130,23 @@ __device__ inline uint32_t fp8_row_codes(float x0, float x1, float s, float r) {
     return e4m3_encode(x0 / s) | (e4m3_encode(x1 / s) << 8);
 }
 
+// The FMA-corrected quotient x / s from r = 1 / s with the sign of x: for x = -0 the correction
+// gives (+0) r + (-0) = +0, while x / s is -0 (for x != 0 the sign is already that of x).
+__device__ inline float signed_quotient(float x, float s, float r) {
+    const float q0 = x * r;
+    return __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-q0, s, x), r, q0), x);
+}
+
+// fp8_row_codes for a row known to be ordinary: finite scale s = amax / 448 with amax finite and
+// at least 2^-77, finite elements. Every element then takes the FMA-corrected quotient, also
+// below 2^-96: there |x / s| = 448 |x| / amax < 2^-10, both quotients encode to the signed zero
+// of x, and the division is never computed (checked against the IEEE quotient on 2^32 random
+// rows of finite bf16 values over the whole exponent range, signed zeros included).
+constexpr float kFp8FastRowMin = 0x1p-77f;
+__device__ inline uint32_t fp8_row_codes_fast(float x0, float x1, float s, float r) {
+    return e4m3_encode2(signed_quotient(x0, s, r), signed_quotient(x1, s, r));
+}
+
 __device__ inline uint32_t fp4_encode(float f) {
     const uint32_t s = (__float_as_uint(f) >> 28) & 8u;
     const float a = __builtin_fabsf(f);
@@ -143,6 +160,26 @@ __device__ inline uint32_t fp4_encode(float f) {
     else if (a <= 5.0f) c = 6;
     else c = 7;
     return s | c;
+}
+
+// E2M1 codes of two quotients (low nibble: q0) by the gfx950 conversion at scale 1 (its scale
+// operand divides, by the power of two of its exponent). It rounds to nearest-even, saturates to
+// +-6 and keeps signed zeros exactly as fp4_encode does on every f32 input but NaN (all 2^32 - 2^24
+// non-NaN patterns compared); a NaN gives code 7 here and 0 in fp4_encode, so NaN inputs need
+// fp4_encode.
+__device__ inline uint32_t fp4_encode_hw(float q0, float q1) {
+    return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, q0, q1, 1.0f, 0) & 0xffu;
+}
+
+// NVFP4 element codes of x0 / eff and x1 / eff (low nibble: x0), eff > 0 the block's effective
+// scale, r = 1 / eff, for a block known to be ordinary: finite elements and a block maximum of at
+// least 2^-60. The FMA-corrected quotient and the hardware conversion; below |x| = 2^-96 the
+// quotient may not be the IEEE one, but there |x / eff| < 2^-15 and both encode to the signed
+// zero of x. Equal to fp4_encode(x / eff) on 2^32 random NVFP4 rows (finite bf16 elements, row and
+// block maxima over the whole exponent range).
+constexpr float kNvfp4FastBlockMin = 0x1p-60f;
+__device__ inline uint32_t nvfp4_codes2_fast(float x0, float x1, float eff, float r) {
+    return fp4_encode_hw(signed_quotient(x0, eff, r), signed_quotient(x1, eff, r));
 }
 
 // E8M0 block-scale code of a block maximum: floor(log2 amax) - emax_elem + 127, clamped; 0 when

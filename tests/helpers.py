@@ -141,3 +141,22 @@ def e4m3_thresholds() -> np.ndarray:
                 lo = mid + 1
         thr.append(lo)
     return np.array(thr, dtype=np.uint32)
+
+
+FP4_SWEEP_END = 0x41000000  # f32 patterns [0, 8): every |q| the MXFP4 / NVFP4 encoders convert
+
+
+def fp4_thresholds() -> np.ndarray:
+    """thr[c - 1] = the first non-negative f32 bit pattern whose reference E2M1 code (the oracle's
+    f32_to_fp4, candle-core/src/accel/formats.rs:329-350) is at least c, c = 1 .. 7."""
+    thr = []
+    for c in range(1, 8):
+        lo, hi = 0, FP4_SWEEP_END
+        while lo < hi:
+            mid = (lo + hi) // 2
+            if O.f32_to_fp4(float(np.uint32(mid).view(np.float32))) >= c:
+                hi = mid
+            else:
+                lo = mid + 1
+        thr.append(lo)
+    return np.array(thr, dtype=np.uint32)

@@ -500,6 +500,21 @@ def test_e4m3_threshold_table_reproduces_the_encoder():
     np.testing.assert_array_equal(O.e4m3_encode(-x), want | 0x80)
 
 
+def test_fp4_threshold_table_reproduces_the_encoder():
+    """The 7 E2M1 code thresholds of the GPU sweep: strictly increasing, and equal to the oracle
+    encoder on 2,000,000 random non-NaN patterns (infinity included) and next to each threshold."""
+    from tests.helpers import fp4_thresholds
+    thr = fp4_thresholds()
+    assert (np.diff(thr.astype(np.int64)) > 0).all()
+    rng = np.random.default_rng(13)
+    u = np.concatenate([rng.integers(0, 0x7F800001, 2_000_000), thr.astype(np.int64),
+                        thr.astype(np.int64) - 1, [0, 0x7F800000]]).astype(np.uint32)
+    x = u.view(np.float32)
+    want = np.searchsorted(thr, u, side="right").astype(np.uint8)
+    np.testing.assert_array_equal(O.fp4_encode(x), want)
+    np.testing.assert_array_equal(O.fp4_encode(-x), want | 8)
+
+
 def test_combine_bit_exact_with_reference_kernel():
     g = gold("ref_combine")
     np.testing.assert_array_equal(O.combine(g["part_o"], g["part_lse"]), g["o"])
