@@ -44,7 +44,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6
-TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "decode_fp8_b32_ctx8192_traffic.md")
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "decode_fp8_c2_and_append_rows_traffic.md")
 
 
 def load_cqkv():
