@@ -23,6 +23,9 @@ LIB_PATH = os.path.join(HERE, "libcqkv.so")
 TURBO4, MXFP4, NVFP4, MXFP8, FP8 = 0, 2, 3, 4, 5
 FORMAT_NAMES = {"fp8": FP8, "mxfp4": MXFP4, "turbo4": TURBO4, "nvfp4": NVFP4, "mxfp8": MXFP8}
 BF16, F16, F32 = 0, 1, 2
+# cache-side rotations: DEFAULT rotates TURBO4 sides only; HADAMARD any format (the reference's
+# RotationKind::Hadamard, Auto at power-of-two head dims)
+ROT_DEFAULT, ROT_NONE, ROT_HADAMARD = 0, 1, 2
 # rotary layouts: rope (halves) and rope_i (interleaved) of candle-nn/src/rotary_emb.rs
 ROPE_HALVES, ROPE_INTERLEAVED = 1, 2
 _DTYPES = {torch.bfloat16: BF16, torch.float16: F16, torch.float32: F32}
@@ -39,7 +42,7 @@ class CqkvError(RuntimeError):
 class Side(ctypes.Structure):
     _fields_ = [("format", ctypes.c_int32), ("is_value", ctypes.c_int32),
                 ("head_dim", ctypes.c_int32), ("kv_heads", ctypes.c_int32),
-                ("capacity", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("capacity", ctypes.c_int32), ("rotation", ctypes.c_int32),
                 ("seed", ctypes.c_uint64), ("codes", ctypes.c_void_p),
                 ("scales", ctypes.c_void_p)]
 
@@ -72,7 +75,7 @@ def lib() -> ctypes.CDLL:
                                              i32, P, P, i32, i32, P, i32, P, I64P, P]
         L.cqkv_decode_workspace_bytes.argtypes = [i32, i32, i32, i32, i32]
         L.cqkv_decode_workspace_bytes.restype = sz
-        L.cqkv_decode_splits.argtypes = [i32, i32, i32, i32, i32]
+        L.cqkv_decode_splits.argtypes = [i32, i32, i32, i32, i32, i32]
         L.cqkv_decode_splits.restype = i32
         L.cqkv_decode_attention.argtypes = [P, i32, I64P, SP, SP, i32, i32, i32, P, i32, f32,
                                             i32, i32, P, i32, I64P, i32, P, sz, P]
@@ -97,6 +100,7 @@ def lib() -> ctypes.CDLL:
         L.cqkv_reference_row_words.restype = i32
         L.cqkv_rows_import.argtypes = [SP, P, i32, i32, i32, P]
         L.cqkv_rows_export.argtypes = [SP, P, i32, i32, i32, P]
+        L.cqkv_side_copy.argtypes = [SP, SP, i32, i32, P]
         L.cqkv_turbo_codebook.argtypes = [i32, i32, P, P]
         L.cqkv_turbo_signs.argtypes = [i32, ctypes.c_uint64, P]
         L.cqkv_last_error.restype = ctypes.c_char_p
@@ -112,7 +116,8 @@ EXPORTED = ["cqkv_codes_plane_bytes", "cqkv_scales_plane_bytes", "cqkv_quant_app
             "cqkv_decode_paged_workspace_bytes", "cqkv_decode_attention_paged",
             "cqkv_flash_attn", "cqkv_flash_attn_ext", "cqkv_fp8_quantize_tensor",
             "cqkv_flash_attn_fp8", "cqkv_hadamard_rows", "cqkv_reference_row_words", "cqkv_rows_import",
-            "cqkv_rows_export", "cqkv_turbo_codebook", "cqkv_turbo_signs", "cqkv_last_error",
+            "cqkv_rows_export", "cqkv_side_copy", "cqkv_turbo_codebook", "cqkv_turbo_signs",
+            "cqkv_last_error",
             "cqkv_version"]
 
 
@@ -154,10 +159,12 @@ class CacheSide:
     codes: torch.Tensor
     scales: torch.Tensor
     seed: int = 0
+    rotation: int = ROT_DEFAULT
 
     @staticmethod
     def empty(fmt: int, is_value: bool, batch: int, kv_heads: int, head_dim: int,
-              capacity: int, device, seed: int = 0) -> "CacheSide":
+              capacity: int, device, seed: int = 0,
+              rotation: int = ROT_DEFAULT) -> "CacheSide":
         capacity = (capacity + 31) // 32 * 32
         cb = lib().cqkv_codes_plane_bytes(fmt, head_dim, capacity)
         sb = lib().cqkv_scales_plane_bytes(fmt, head_dim, capacity)
@@ -165,11 +172,17 @@ class CacheSide:
             raise CqkvError(ERR_ARG, f"format {fmt} / head_dim {head_dim} not supported")
         codes = torch.zeros(batch * kv_heads * cb, dtype=torch.uint8, device=device)
         scales = torch.zeros(batch * kv_heads * sb, dtype=torch.uint8, device=device)
-        return CacheSide(fmt, is_value, batch, kv_heads, head_dim, capacity, codes, scales, seed)
+        return CacheSide(fmt, is_value, batch, kv_heads, head_dim, capacity, codes, scales, seed,
+                         rotation)
+
+    def rotates(self) -> bool:
+        """Whether rows are stored Hadamard-rotated (seeded by `seed`)."""
+        return self.rotation == ROT_HADAMARD or (self.rotation == ROT_DEFAULT and
+                                                 self.fmt == TURBO4)
 
     def struct(self) -> Side:
-        return Side(self.fmt, int(self.is_value), self.head_dim, self.kv_heads, self.capacity, 0,
-                    self.seed, self.codes.data_ptr(), self.scales.data_ptr())
+        return Side(self.fmt, int(self.is_value), self.head_dim, self.kv_heads, self.capacity,
+                    self.rotation, self.seed, self.codes.data_ptr(), self.scales.data_ptr())
 
     def nbytes(self) -> int:
         return self.codes.numel() + self.scales.numel()
@@ -246,9 +259,12 @@ def decode_workspace_bytes(batch, q_heads, q_len, head_dim, splits) -> int:
     return lib().cqkv_decode_workspace_bytes(batch, q_heads, q_len, head_dim, splits)
 
 
-def decode_splits(batch, kv_heads, kv_len, fmt: int = FP8, ragged: bool = False) -> int:
-    """Key splits decode_attention uses with splits=0 (size the workspace with it)."""
-    return lib().cqkv_decode_splits(fmt, batch, kv_heads, kv_len, int(ragged))
+def decode_splits(batch, kv_heads, kv_len, fmt: int = FP8, ragged: bool = False,
+                  v_fmt: int | None = None) -> int:
+    """Key splits decode_attention uses with splits=0 for keys in `fmt` and values in `v_fmt`
+    (default: `fmt`); size the workspace with it."""
+    return lib().cqkv_decode_splits(fmt, fmt if v_fmt is None else v_fmt, batch, kv_heads,
+                                    kv_len, int(ragged))
 
 
 def decode_attention(q: torch.Tensor, k: CacheSide, v: CacheSide, kv_len: int,
@@ -533,6 +549,22 @@ def rows_export(side: CacheSide, tokens: int, position: int = 0) -> torch.Tensor
     return rows
 
 
+def side_copy(dst: CacheSide, src: CacheSide, tokens: int) -> None:
+    """The first `tokens` positions of every plane of src into dst (a side of another capacity)."""
+    ds, ss = dst.struct(), src.struct()
+    _check(lib().cqkv_side_copy(ctypes.byref(ds), ctypes.byref(ss), src.batch, tokens,
+                                _stream(src.codes.device)))
+
+
+def grown_capacity(capacity: int, grow_by: int, need: int) -> int:
+    """Cache::grown_capacity (candle-nn/src/kv_cache.rs:60-66): the capacity plus
+    max(grow_by, capacity / 2, 1) until it holds `need`, here rounded up to 32 tokens."""
+    cap = capacity
+    while cap < need:
+        cap += max(grow_by, cap // 2, 1)
+    return (cap + 31) // 32 * 32
+
+
 def turbo_codebook(head_dim: int, bits: int = 4):
     import numpy as np
     c = np.zeros(16, dtype=np.float32)
@@ -553,20 +585,38 @@ def turbo_signs(head_dim: int, seed: int):
 # host-side mirror of candle-nn's TurboKvCache (candle-nn/src/turbo_quant.rs:793-991)
 # ------------------------------------------------------------------------------------------
 class TurboKvCache:
-    """A quantized KV cache of fixed capacity for (batch, kv_heads, head_dim), keys and values
-    in `key_format` / `value_format` (FP8, MXFP4, MXFP8, NVFP4 or TURBO4; TurboQuant seeds: keys `seed`,
-    values `seed + 2` as TurboKvCache::with_formats does)."""
+    """A quantized KV cache for (batch, kv_heads, head_dim), keys in `key_format` and values in
+    `value_format` (each FP8, MXFP4, MXFP8, NVFP4 or TURBO4), rotated per `rotation` with seeds
+    `seed` (keys) and `seed + 2` (values) as TurboKvCache::with_formats does
+    (candle-nn/src/turbo_quant.rs:858-879). It grows past `capacity` as Cache::append does."""
 
     def __init__(self, key_format: int, value_format: int, batch: int, kv_heads: int,
-                 head_dim: int, capacity: int, device="cuda", seed: int = 42):
-        if key_format != value_format:
-            raise CqkvError(ERR_ARG, "key and value formats must match")
+                 head_dim: int, capacity: int, device="cuda", seed: int = 42,
+                 grow_by: int | None = None, rotation: int = ROT_DEFAULT):
         self.k = CacheSide.empty(key_format, False, batch, kv_heads, head_dim, capacity, device,
-                                 seed)
+                                 seed, rotation)
         self.v = CacheSide.empty(value_format, True, batch, kv_heads, head_dim, capacity, device,
-                                 seed + 2)
+                                 seed + 2, rotation)
         self._len = 0
         self.dim = head_dim
+        # Cache::new(dim, max_seq_len) grows by max_seq_len (kv_cache.rs:19-27)
+        self.grow_by = capacity if grow_by is None else grow_by
+
+    def _reserve(self, need: int) -> None:
+        """Grows both sides to hold `need` tokens as Cache::append does: one new buffer at the
+        grown capacity and one copy of the tokens so far."""
+        if need <= self.k.capacity:
+            return
+        cap = grown_capacity(self.k.capacity, self.grow_by, need)
+        dev = self.k.codes.device
+        sides = []
+        for old in (self.k, self.v):
+            new = CacheSide.empty(old.fmt, old.is_value, old.batch, old.kv_heads, old.head_dim,
+                                  cap, dev, old.seed, old.rotation)
+            if self._len:
+                side_copy(new, old, self._len)
+            sides.append(new)
+        self.k, self.v = sides
 
     def formats(self):
         return self.k.fmt, self.v.fmt
@@ -586,8 +636,7 @@ class TurboKvCache:
             raise CqkvError(ERR_ARG, f"turbo-quant cache: k {tuple(k.shape)} / v {tuple(v.shape)}"
                                      f" do not match head dim {self.dim}")
         t = k.shape[2]
-        if self._len + t > self.k.capacity:
-            raise CqkvError(ERR_ARG, f"cache full: {self._len} + {t} > {self.k.capacity}")
+        self._reserve(self._len + t)
         quant_append(self.k, k, self._len)
         quant_append(self.v, v, self._len)
         self._len += t
@@ -597,8 +646,7 @@ class TurboKvCache:
         """The model step rope(q), rope(k), append(k, v) in one launch, the new tokens taking
         positions seq_len.. (their rows of cos / sin). Returns the rotated q."""
         t = k.shape[2] if k.dim() == 4 else 0
-        if self._len + t > self.k.capacity:
-            raise CqkvError(ERR_ARG, f"cache full: {self._len} + {t} > {self.k.capacity}")
+        self._reserve(self._len + t)
         out = rope_quant_append(self.k, self.v, q, k, v, cos, sin, kind, self._len)
         self._len += t
         return out

@@ -28,8 +28,9 @@ struct AppendArgs {
     uint32_t codes_plane, scales_plane;  // bytes per (batch, head) plane
     const int32_t *positions;            // device, per batch, or null
     int32_t position, tokens, capacity, kv_heads, x_dtype;
-    uint32_t sign_bits[4];  // TURBO4: bit j set -> column j of the rotation has sign -1
-    float rot_scale;        // TURBO4: 1 / sqrt(D) in f32
+    int32_t rotate;         // Hadamard-rotate each row before encoding (side_rotates)
+    uint32_t sign_bits[4];  // rotation: bit j set -> column j of the rotation has sign -1
+    float rot_scale;        // rotation: 1 / sqrt(D) in f32
     float bnd[16];          // TURBO4: the 15 codebook boundaries (+inf padded)
     int32_t turbo_sym;      // TURBO4: bnd[7] == 0 and bnd[14 - i] == -bnd[i] (a symmetric codebook)
     int32_t pair_loads;     // elements 2l, 2l+1 of every row are one aligned 4 / 8-byte word
@@ -324,6 +325,41 @@ __device__ inline void rope_row32(const AppendArgs &a, int64_t p, int q, bool li
     }
 }
 
+// y = H (sign * x) / sqrt(D) of this thread's 32 elements of a row (rotation_matrix(D, Hadamard,
+// seed), candle-core/src/accel/turbo.rs:180-203, applied as TurboQuantizer::rotate does,
+// candle-nn/src/turbo_quant.rs:182-189): the sign flip, the Walsh-Hadamard stages in element-stride
+// order 1, 2, ..., D / 2 (1..16 in the thread, 32 and 64 across the row's threads by DPP), then
+// 1 / sqrt(D).
+template <int D>
+__device__ inline void hadamard_row32(const AppendArgs &a, int q, float (&x)[32]) {
+    constexpr int R = D / 32;
+    const uint32_t sb = a.sign_bits[q];
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+        x[i] = __uint_as_float(__float_as_uint(x[i]) ^ ((sb << (31 - i)) & 0x80000000u));
+#pragma unroll
+    for (int m = 1; m < 32; m <<= 1)
+#pragma unroll
+        for (int i = 0; i < 32; ++i)
+            if (!(i & m)) {
+                const float u = x[i], v = x[i + m];
+                x[i] = u + v;
+                x[i + m] = u - v;
+            }
+    {
+        const float sg = (q & 1) ? -1.0f : 1.0f;  // stride 32: partner thread q ^ 1
+#pragma unroll
+        for (int i = 0; i < 32; ++i) x[i] = __builtin_fmaf(sg, x[i], quad_xor<1>(x[i]));
+    }
+    if constexpr (R == 4) {
+        const float sg = (q & 2) ? -1.0f : 1.0f;  // stride 64: partner thread q ^ 2
+#pragma unroll
+        for (int i = 0; i < 32; ++i) x[i] = __builtin_fmaf(sg, x[i], quad_xor<2>(x[i]));
+    }
+#pragma unroll
+    for (int i = 0; i < 32; ++i) x[i] *= a.rot_scale;
+}
+
 // NR token rows of plane (b, h) from cache position c0 = first tile of the range + bx * NR, by
 // the first NR * D / 32 threads of a 256-thread workgroup (all 256 threads must call it: the
 // value tiles pass through LDS). ROPE != 0 rotates each row first (the fused RoPE + append).
@@ -353,6 +389,7 @@ __device__ inline void rows_block(const AppendArgs &a, int h, int b, int bx) {
     load_row32<LOAD>(a, (int64_t)b * a.sb + (int64_t)h * a.sh + (int64_t)(t - pos) * a.st + 32 * q,
                      live, x);
     if constexpr (ROPE != 0) rope_row32<D, ROPE>(a, t, q, live, x);
+    if (a.rotate) hadamard_row32<D>(a, q, x);
 
     uint32_t cw[kB8 ? 8 : 4];  // this thread's 32 codes, element order
     float tok_scale = 0.0f;    // FP8 / TURBO4 / NVFP4: the token's f32
@@ -453,37 +490,10 @@ __device__ inline void rows_block(const AppendArgs &a, int h, int b, int bx) {
             }
         }
         tok_scale = gs;
-    } else {  // TURBO4: y = H (sign * x) / sqrt(D), norm, codebook index of y / norm
-        const uint32_t sb = a.sign_bits[q];
-#pragma unroll
-        for (int i = 0; i < 32; ++i)
-            x[i] = __uint_as_float(__float_as_uint(x[i]) ^ ((sb << (31 - i)) & 0x80000000u));
-        // the transform stages in element-stride order 1, 2, ..., D / 2 (as fwht_pairs runs them)
-#pragma unroll
-        for (int m = 1; m < 32; m <<= 1)
-#pragma unroll
-            for (int i = 0; i < 32; ++i)
-                if (!(i & m)) {
-                    const float u = x[i], v = x[i + m];
-                    x[i] = u + v;
-                    x[i + m] = u - v;
-                }
-        {
-            const float sg = (q & 1) ? -1.0f : 1.0f;  // stride 32: partner thread q ^ 1
-#pragma unroll
-            for (int i = 0; i < 32; ++i) x[i] = __builtin_fmaf(sg, x[i], quad_xor<1>(x[i]));
-        }
-        if constexpr (R == 4) {
-            const float sg = (q & 2) ? -1.0f : 1.0f;  // stride 64: partner thread q ^ 2
-#pragma unroll
-            for (int i = 0; i < 32; ++i) x[i] = __builtin_fmaf(sg, x[i], quad_xor<2>(x[i]));
-        }
+    } else {  // TURBO4: the (rotated) row's norm, codebook index of y / norm
         float ss = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            x[i] *= a.rot_scale;
-            ss += x[i] * x[i];
-        }
+        for (int i = 0; i < 32; ++i) ss += x[i] * x[i];
         const float norm = __builtin_sqrtf(row_sum<R>(ss));
         const float inv = norm > 0.0f ? 1.0f / norm : 0.0f;
         if (a.turbo_sym && norm <= 3.0e38f && inv <= 3.0e38f) {
@@ -643,8 +653,9 @@ inline void launch_rows(const cqkv_side *s, int32_t tokens, int32_t batch, hipSt
 // ---------------------------------------------------------------------------------------------
 // Fused RoPE + quantize-append: one launch rotates the queries (written out in their dtype for
 // the attention call), rotates the keys and quantizes them into the key side, and quantizes the
-// values into the value side. Grid ((tiles / 4) * units, 1, batch) with units = 2 * kv_heads +
-// q_heads: unit y < kv_heads is a key plane, the next kv_heads value planes, the rest query heads.
+// values into the value side. Grid ((tiles / 4) * units, 1, batch) with units = kv_heads +
+// v_units + q_units: unit y < kv_heads is a key plane, the next v_units (kv_heads, or 0 when the
+// value side has another format and its own launch) value planes, the rest query head units.
 // ---------------------------------------------------------------------------------------------
 struct RopeAppendArgs {
     AppendArgs k, v;  // k carries the cos / sin tables
@@ -654,6 +665,7 @@ struct RopeAppendArgs {
     int32_t q_pair_loads, o_pair_stores, q_heads;
     int32_t q_vec16;  // query rows by rope_query_rows16
     int32_t q_units;  // grid units of the queries: q_heads, or head groups with q_vec16
+    int32_t v_units;  // grid units of the values: kv_heads, or 0 (values appended separately)
 };
 
 template <int D, int ROPE, bool W16>
@@ -802,18 +814,18 @@ template <int FMT, int D, int ROPE, int LOAD>
 __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendArgs r) {
     // head index fastest in dispatch order: the blocks in flight together read whole projection
     // rows (all heads of the same tokens) instead of one head's pieces 12 KB apart
-    const int hkv = r.k.kv_heads, units = 2 * hkv + r.q_units;
+    const int hkv = r.k.kv_heads, qy = hkv + r.v_units, units = qy + r.q_units;
     const int y = (int)(blockIdx.x % (unsigned)units), bx = (int)(blockIdx.x / (unsigned)units);
     const int b = blockIdx.z, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (y < hkv) {
         rows_block<FMT, 0, D, LOAD, ROPE, kRopeBlockTokens>(r.k, y, b, bx);
-    } else if (y < 2 * hkv) {
+    } else if (y < qy) {
         rows_block<FMT, 1, D, LOAD, 0, kRopeBlockTokens>(r.v, y - hkv, b, bx);
     } else {
 #pragma unroll
         for (int k = 0; k < 2; ++k) {  // rope_query_rows* cover 32 tokens per block index
-            if (LOAD != kRowF32 && r.q_vec16) rope_query_rows16<D, ROPE>(r, y - 2 * hkv, b, 2 * bx + k, wave, lane);
-            else rope_query_rows<D, ROPE, false>(r, y - 2 * hkv, b, 2 * bx + k, wave, lane);
+            if (LOAD != kRowF32 && r.q_vec16) rope_query_rows16<D, ROPE>(r, y - qy, b, 2 * bx + k, wave, lane);
+            else rope_query_rows<D, ROPE, false>(r, y - qy, b, 2 * bx + k, wave, lane);
         }
     }
 }
@@ -829,7 +841,7 @@ inline void launch_rope_append_l(int d, dim3 grid, hipStream_t st, const RopeApp
 template <int FMT, int ROPE>
 inline void launch_rope_append(int d, dim3 grid, hipStream_t st, const RopeAppendArgs &r) {
     // one row-load form for both sides (the most general one when they differ)
-    const int load = r.k.row_loads == r.v.row_loads ? r.k.row_loads : kRowAny;
+    const int load = !r.v_units || r.k.row_loads == r.v.row_loads ? r.k.row_loads : kRowAny;
     if (load == kRowBF16) launch_rope_append_l<FMT, ROPE, kRowBF16>(d, grid, st, r);
     else if (load == kRowF16) launch_rope_append_l<FMT, ROPE, kRowF16>(d, grid, st, r);
     else if (load == kRowF32) launch_rope_append_l<FMT, ROPE, kRowF32>(d, grid, st, r);

@@ -10,6 +10,8 @@
 //          scale, rsc1 = 0
 // One wavefront per 8-token tile of a (batch, head) plane; lane l owns elements 2l, 2l+1, so
 // the value tiles are read and written whole by one lane (no cross-lane read-modify-write).
+#include <algorithm>
+
 #include "cqkv_device.h"
 #include "cqkv_host.h"
 
@@ -184,4 +186,52 @@ extern "C" int cqkv_rows_export(const cqkv_side *side, uint32_t *rows, int32_t b
                                 int32_t tokens, int32_t position, cqkv_stream_t stream) {
     return cqkv::convert(side, rows, batch, tokens, position, (hipStream_t)stream, true,
                          "cqkv_rows_export");
+}
+
+// ---------------------------------------------------------------------------------------------
+// Cache growth: the first `tokens` positions of every (batch, kv head) plane of src into dst,
+// sides of different capacities (Cache::append's copy of the old contents into the grown buffer,
+// candle-nn/src/kv_cache.rs:56-99). A codes plane is a prefix of whole rows (keys) or whole
+// 8-token tiles (values); a scales plane holds the block-scale bytes of all `capacity` tokens,
+// then the f32 token scales, so it is two prefixes at capacity-dependent offsets. Each region is
+// one strided device copy over all planes (no kernel, nothing allocated).
+// ---------------------------------------------------------------------------------------------
+extern "C" int cqkv_side_copy(const cqkv_side *dst, const cqkv_side *src, int32_t batch,
+                              int32_t tokens, cqkv_stream_t stream) {
+    using namespace cqkv;
+    clear_error();
+    static const char *who = "cqkv_side_copy";
+    if (int rc = check_side(dst, who)) return rc;
+    if (int rc = check_side(src, who)) return rc;
+    if (dst->format != src->format || dst->is_value != src->is_value ||
+        dst->head_dim != src->head_dim || dst->kv_heads != src->kv_heads ||
+        side_rotates(dst) != side_rotates(src) || (side_rotates(src) && dst->seed != src->seed))
+        return fail(CQKV_ERR_ARG,
+                    "%s: sides differ in format, side, head dim, kv heads, rotation or seed", who);
+    if (batch <= 0 || tokens < 0 || tokens > src->capacity || tokens > dst->capacity)
+        return fail(CQKV_ERR_ARG, "%s: batch %d, %d tokens for capacities %d -> %d", who, batch,
+                    tokens, src->capacity, dst->capacity);
+    if (tokens == 0) return CQKV_OK;
+    const int fmt = src->format, d = src->head_dim;
+    const size_t planes = (size_t)batch * src->kv_heads;
+    const size_t row_bytes = (size_t)d * code_bits(fmt) / 8;
+    // values: whole 8-token tiles, at most the smaller capacity (both are multiples of 32)
+    const int ctok = src->is_value ? std::min((tokens + 7) / 8 * 8, std::min(src->capacity, dst->capacity))
+                                   : tokens;
+    const size_t src_cp = cqkv_codes_plane_bytes(fmt, d, src->capacity);
+    const size_t dst_cp = cqkv_codes_plane_bytes(fmt, d, dst->capacity);
+    const size_t src_sp = cqkv_scales_plane_bytes(fmt, d, src->capacity);
+    const size_t dst_sp = cqkv_scales_plane_bytes(fmt, d, dst->capacity);
+    const size_t bb = block_elems(fmt) ? (size_t)d / block_elems(fmt) : 0;  // block bytes per token
+    const hipStream_t st = (hipStream_t)stream;
+    CQKV_HIP_CHECK(hipMemcpy2DAsync(dst->codes, dst_cp, src->codes, src_cp, row_bytes * ctok,
+                                    planes, hipMemcpyDeviceToDevice, st));
+    if (bb)
+        CQKV_HIP_CHECK(hipMemcpy2DAsync(dst->scales, dst_sp, src->scales, src_sp, bb * tokens,
+                                        planes, hipMemcpyDeviceToDevice, st));
+    if (token_scale(fmt))
+        CQKV_HIP_CHECK(hipMemcpy2DAsync((uint8_t *)dst->scales + bb * dst->capacity, dst_sp,
+                                        (const uint8_t *)src->scales + bb * src->capacity, src_sp,
+                                        (size_t)4 * tokens, planes, hipMemcpyDeviceToDevice, st));
+    return CQKV_OK;
 }

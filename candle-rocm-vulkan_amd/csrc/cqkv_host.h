@@ -51,6 +51,12 @@ inline bool token_scale(int32_t format) {
 
 inline bool supported_dim(int32_t d) { return d == 64 || d == 128; }
 
+// The side's rows are Hadamard-rotated before quantization (CQKV_ROT_DEFAULT: TURBO4 only).
+inline bool side_rotates(const cqkv_side *s) {
+    return s->rotation == CQKV_ROT_HADAMARD ||
+           (s->rotation == CQKV_ROT_DEFAULT && s->format == CQKV_FMT_TURBO4);
+}
+
 // Validates a cache side; returns CQKV_OK or an error (message set).
 int check_side(const cqkv_side *s, const char *what);
 

@@ -1,0 +1,789 @@
+// Split-K flash-decode kernels over the quantized cache (gfx950), templated on the key and the
+// value format (included by decode_inst.hip, one object per key format, and by decode_attn.hip
+// for the argument structs).
+//
+// Reference behaviour (paths relative to the reference repository root): TqAttn / tq_attention
+// (candle-core/src/rocm_backend/accel.rs:425-571; kernels tq_attng_core and tq_combine_impl in
+// candle-core/kernels/turbo_quant_impl.h:403-619, 659-685), masks of key_range
+// (candle-core/src/accel/attention.rs:80-92), the q rotation / o unrotation of the fused
+// TurboQuant path (candle-nn/src/turbo_quant.rs:1162-1167, 1263). Numerics follow the reference's
+// CPU path (softmax(scale q k^T) v over the dequantized cache, f32 accumulation) within the bf16
+// tolerance, not bit for bit.
+//
+// Kernel shape: one workgroup = 8 wavefronts = one (key split, kv head, batch).
+//  * Both products run on v_mfma_f32_16x16x32_bf16. MFMA columns are the (query, head) pairs of
+//    the GQA group, 16 per workgroup (more than 16 - chunked prefill or speculative decode over
+//    the cache - take more workgroups along a column-block index); rows are keys (S^T = K Q^T)
+//    or head dims (O^T = V^T P^T).
+//  * A wavefront streams 32-key tiles with nontemporal buffer loads straight into operand
+//    registers (two register sets, A/B, no copies) and decodes codes in registers: E4M3 -> bf16 exactly, E2M1
+//    with its E8M0 block scale exactly, TurboQuant code bytes through a per-lane LDS table of
+//    f16 pairs (TurboQuant runs its MFMAs in f16: codebook values are not bf16-exact).
+//    Loads of tiles past the split's end are aimed past the buffer range, so the hardware
+//    returns zeros without touching memory and the load schedule stays branch-free.
+//  * Key rows are row-major, so lane (r, g) loads the codes of key r for head-dim group g.
+//    Value codes are stored in 8-token transposed tiles, so lane (r, g) loads keys 8g..8g+7 of
+//    one head dim - the A operand of V^T P^T with no shuffle.
+//  * Online softmax runs in the exp2 domain on the S^T accumulator; lane (n, g) holds column n
+//    for keys 8g..8g+7, which is the B operand layout P^T needs. Only the running maximum is
+//    reduced across lanes. P^T enters the MFMA as a hi + lo pair of 16-bit operands.
+//  * The wavefronts of a workgroup interleave tiles and merge through LDS. With one split the
+//    workgroup writes the output; otherwise it writes its (o, lse) partial and combine_kernel
+//    merges the splits (tq_combine's formula), unrotating TurboQuant values. (A fused "last
+//    workgroup combines" variant needs agent-scope release fences, which write back the L2 of
+//    the XCD each time; measured at 6x the whole decode time, so the kernel boundary is used.)
+#pragma once
+
+#include <type_traits>
+
+#include "cqkv_device.h"
+#include "cqkv_host.h"
+
+namespace cqkv {
+
+constexpr uint32_t kOOB = 0x80000000u;  // past every plane (planes are < 2 GiB)
+
+// Paged decode: a run of whole 32-key tiles of one cache block, decoded by one split. The keys
+// of the call are the blocks' valid rows concatenated (the reference's block table, PageTable
+// in candle-core/src/accel/attention.rs:307-366, walked by attention_packed_blocks,
+// candle-nn/src/turbo_quant.rs:1082-1114).
+struct PagedSeg {
+    const uint8_t *kc, *ks, *vc, *vs;                  // the block's planes
+    uint32_t kc_plane, ks_plane, vc_plane, vs_plane;   // bytes per (sequence, kv head) plane
+    int32_t tile_begin, tile_end;                      // tiles [begin, end) of the block
+    int32_t key_offset;                                // key index of the block's row 0
+    int32_t rows;                                      // valid rows of the block
+};
+
+struct DecodeArgs {
+    const void *q;
+    int64_t q_sb, q_sh, q_si;
+    const uint8_t *kc, *ks, *vc, *vs;
+    uint32_t kc_plane, ks_plane, vc_plane, vs_plane;
+    const int32_t *kv_lens;
+    int32_t kv_len, q_dtype;
+    int32_t q_heads, kv_heads, group, q_len, ncols;
+    int32_t col_blocks;  // workgroups along the columns: ceil(ncols / 16)
+    float scale_log2;  // softmax scale * log2(e)
+    int32_t wl, wr;
+    int32_t tiles_per_split, splits, batch;
+    float *part_o;       // (splits, rows, D) f32, normalised partial outputs
+    float *part_lse;     // (splits, rows) f32, log2-domain lse of each split
+    void *out;
+    int32_t out_dtype, q_split;  // q_split: queries need a lo part (not bf16 inputs)
+    int64_t o_sb, o_sh, o_si;
+    int32_t rot_k, rot_v;                   // rotated key / value sides: rotate q, unrotate o
+    uint32_t ksign_bits[4], vsign_bits[4];  // their rotation signs (bit set -> -1)
+    float rot_scale;                        // 1 / sqrt(D)
+    float cent[16];  // TURBO4 codebook (the same for keys and values at one head dim)
+    const PagedSeg *segs;  // paged: one segment per split (the planes above are unused)
+};
+
+// Visible keys [lo, hi) of query i of lq over lk keys (bottom-right aligned).
+__device__ inline void key_range(int i, int lq, int lk, int wl, int wr, int &lo, int &hi) {
+    const int pos = i + lk - lq;
+    lo = wl >= 0 ? max(pos - wl, 0) : 0;
+    hi = wr >= 0 ? min(pos + wr + 1, lk) : lk;
+    lo = min(lo, lk);
+    hi = max(hi, lo);
+}
+
+template <int D>
+__device__ inline void fwht_pairs_dec(float &v0, float &v1, int lane) {
+    float a = v0 + v1, b = v0 - v1;
+    v0 = a;
+    v1 = b;
+#pragma unroll
+    for (int m = 1; m < D / 2; m <<= 1) {
+        const float p0 = shfl_xor(v0, m), p1 = shfl_xor(v1, m);
+        const bool upper = (lane & m) != 0;
+        v0 = upper ? p0 - v0 : v0 + p0;
+        v1 = upper ? p1 - v1 : v1 + p1;
+    }
+}
+
+__device__ inline bool sign_bit(const uint32_t *bits, int j) { return (bits[j >> 5] >> (j & 31)) & 1u; }
+
+// Byte codes (FP8, MXFP8) or nibbles (MXFP4, NVFP4, TURBO4).
+template <int FMT>
+constexpr bool is8() { return FMT == CQKV_FMT_FP8 || FMT == CQKV_FMT_MXFP8; }
+
+// Head dim held in k-slot e of MFMA chunk j by lane group g (the same for K and Q operands).
+template <int FMT, int D>
+__device__ inline int qdim(int j, int g, int e) {
+    if constexpr (is8<FMT>()) return 64 * (j >> 1) + 16 * g + 8 * (j & 1) + e;
+    else return (D / 4) * g + 8 * j + e;
+}
+
+// ---------------------------------------------------------------------------------------------
+// per-format tile registers, loads and decoders
+// ---------------------------------------------------------------------------------------------
+template <int KF, int VF, int D>
+struct Tile {
+    // keys: 2 sub-tiles x D/32 code words (byte codes: D/16 words, 4 per 16-key row chunk pair)
+    uint32_t k[2][is8<KF>() ? D / 16 : D / 32];
+    // values: D/32 chunks of 2 head dims x 8 keys (byte codes 4 words, 4-bit 2 words)
+    uint32_t v[D / 32][is8<VF>() ? 4 : 2];
+    // per sub-tile, this lane's key: FP8 f32 scale; MXFP4 its E8M0 block byte; MXFP8 all its
+    // E8M0 block bytes; NVFP4 the E4M3 block bytes of its 32 (D=128) / 16 (D=64) head dims
+    uint32_t kscale[2];
+    uint32_t ktok[2];  // NVFP4: the key's f32 scale
+    // key lane % 32 (broadcast across lanes): the MX formats' value block bytes
+    uint32_t vs;
+    // FP8 / TURBO4: the scale words of keys 8 g .. 8 g + 7 of the tile (lane group g), the ones the
+    // lane's score and P rows need, read directly instead of broadcast across lanes
+    uint32_t ks8[8], vs8[8];
+    // NVFP4: the value block bytes (two words per key at D = 128, one at D = 64) and f32 scales
+    // of keys 8 g .. 8 g + 7, read directly (config-2 shape 100-103 -> 99 us same-box)
+    uint32_t nvb[D == 128 ? 16 : 8], nvg[8];
+};
+
+// Formats whose per-key scale words are read as ks8 / vs8 (one 32-bit word per key). Same-box
+// A/B against the cross-lane broadcast: TurboQuant-4 config 5 270-276 -> 257-264 us, FP8 config 2
+// 94.7-95.9 -> 94.3-94.6 us; MXFP4 config 3 got 2 % slower and keeps the broadcast.
+template <int FMT>
+constexpr bool direct_scales() {
+    return FMT == CQKV_FMT_FP8 || FMT == CQKV_FMT_TURBO4;
+}
+
+// The 32-bit scale words of keys kb .. kb + 7 (kb a multiple of 8: two aligned 16-byte loads).
+template <int BYTES>
+__device__ inline void load_scales8(uint32_t *out, rsrc_t r, uint32_t kb, uint32_t oob) {
+    static_assert(BYTES == 4, "32-bit scale words");
+    const u32x4 a = ld128(r, (kb * 4) | oob), b = ld128(r, (kb * 4 + 16) | oob);
+    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+    out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+}
+
+template <int KF, int VF, int D>
+__device__ inline void load_tile(Tile<KF, VF, D> &r, int tile, bool live, int lane, rsrc_t kr,
+                                 rsrc_t ksr, rsrc_t vr, rsrc_t vsr, uint32_t ktok_off,
+                                 uint32_t vtok_off) {
+    const int n = lane & 15, g = lane >> 4;
+    const uint32_t t0 = (uint32_t)tile * 32u;
+    const uint32_t oob = live ? 0u : kOOB;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        const uint32_t key = t0 + 8 * (n >> 2) + 4 * s + (n & 3);
+        if constexpr (is8<KF>()) {
+#pragma unroll
+            for (int i = 0; i < D / 64; ++i) {
+                const u32x4 w = ld128_stream(kr, (key * D + 16 * g + 64 * i) | oob);
+                r.k[s][4 * i + 0] = w.x;
+                r.k[s][4 * i + 1] = w.y;
+                r.k[s][4 * i + 2] = w.z;
+                r.k[s][4 * i + 3] = w.w;
+            }
+            if constexpr (KF == CQKV_FMT_FP8)
+                r.kscale[s] = ld32(ksr, (key * 4) | oob);
+            else if constexpr (D == 128)
+                r.kscale[s] = ld32(ksr, (key * 4) | oob);
+            else
+                r.kscale[s] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(ksr, (key * 2) | oob, 0, 0);
+        } else {
+            if constexpr (D == 128) {
+                const u32x4 w = ld128_stream(kr, (key * 64 + 16 * g) | oob);
+                r.k[s][0] = w.x;
+                r.k[s][1] = w.y;
+                r.k[s][2] = w.z;
+                r.k[s][3] = w.w;
+            } else {
+                const u32x2 w = ld64_stream(kr, (key * 32 + 8 * g) | oob);
+                r.k[s][0] = w.x;
+                r.k[s][1] = w.y;
+            }
+            if constexpr (KF == CQKV_FMT_MXFP4)
+                r.kscale[s] = __builtin_amdgcn_raw_buffer_load_b8(
+                    ksr, (key * (D / 32) + (D == 128 ? g : g >> 1)) | oob, 0, 0);
+            if constexpr (KF == CQKV_FMT_NVFP4) {
+                if constexpr (D == 128)
+                    r.kscale[s] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
+                        ksr, (key * 8 + 2 * g) | oob, 0, 0);
+                else
+                    r.kscale[s] = __builtin_amdgcn_raw_buffer_load_b8(ksr, (key * 4 + g) | oob, 0, 0);
+                r.ktok[s] = ld32(ksr, (ktok_off + key * 4) | oob);
+            }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < D / 32; ++u) {
+        if constexpr (is8<VF>()) {
+            const u32x4 w = ld128_stream(vr, (((t0 / 8 + g) * D + 32 * u + 2 * n) * 8) | oob);
+            r.v[u][0] = w.x;
+            r.v[u][1] = w.y;
+            r.v[u][2] = w.z;
+            r.v[u][3] = w.w;
+        } else {
+            const u32x2 w = ld64_stream(vr, (((t0 / 8 + g) * D + 32 * u + 2 * n) * 4) | oob);
+            r.v[u][0] = w.x;
+            r.v[u][1] = w.y;
+        }
+    }
+    const uint32_t kl = t0 + (lane & 31);
+    if constexpr (KF == CQKV_FMT_TURBO4) load_scales8<4>(r.ks8, ksr, t0 + 8 * g, oob);
+    if constexpr (direct_scales<VF>()) {
+        load_scales8<4>(r.vs8, vsr, t0 + 8 * g, oob);
+    } else if constexpr (VF == CQKV_FMT_MXFP4 || VF == CQKV_FMT_MXFP8) {
+        r.vs = D == 128 ? ld32(vsr, (kl * 4) | oob)
+                        : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(vsr, (kl * 2) | oob, 0, 0);
+    } else if constexpr (VF == CQKV_FMT_NVFP4) {
+        const uint32_t kb = t0 + 8 * g;
+        constexpr uint32_t kBpk = D / 16;  // block bytes per key
+#pragma unroll
+        for (int i = 0; i < (int)(8 * kBpk / 16); ++i) {
+            const u32x4 w = ld128(vsr, (kb * kBpk + 16 * i) | oob);
+            r.nvb[4 * i + 0] = w.x;
+            r.nvb[4 * i + 1] = w.y;
+            r.nvb[4 * i + 2] = w.z;
+            r.nvb[4 * i + 3] = w.w;
+        }
+        load_scales8<4>(r.nvg, vsr, kb + vtok_off / 4, oob);
+    }
+}
+
+__device__ inline uint32_t fp4x2_to_bf16x2(uint32_t w, int byte_sel, float scale) {
+    bf16x2 v;
+    switch (byte_sel) {  // the selector must be an immediate
+    case 0: v = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0); break;
+    case 1: v = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1); break;
+    case 2: v = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2); break;
+    default: v = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3); break;
+    }
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// MFMA operand type: bf16 for FP8 / MXFP4 (their codes decode exactly), f16 for TurboQuant
+// (codebook values, rotated queries: 11 significant bits instead of 8).
+template <int FMT>
+using op_t = typename std::conditional<FMT == CQKV_FMT_TURBO4, f16x8, bf16x8>::type;
+
+// TurboQuant codebook lookups: code byte b (codes b & 15, b >> 4) of lane l reads the f16 pair of
+// entry (b, l) at byte 256 b + 4 l of a 64 KB LDS table, a copy per lane, so every lane reads
+// its own bank (random codes through one shared 1 KB table cost several passes per read in bank
+// conflicts). The table is 64 KB-aligned and tab = its address + 4 l, so the address of byte I
+// of code word w is tab with w's byte I as byte 1: one byte permute.
+typedef __attribute__((address_space(3))) const uint32_t lds_u32;
+template <int I>
+__device__ inline uint32_t turbo_pair(uint32_t tab, uint32_t w) {
+    // v_perm_b32 selector bytes: 0-3 pick bytes of the second operand (tab), 4-7 of the first (w)
+    constexpr uint32_t sel = 0x03020000u | ((4u + I) << 8);
+    return *(lds_u32 *)(size_t)__builtin_amdgcn_perm(w, tab, sel);
+}
+
+// 8 codes of one code word (4-bit) or two words (FP8) -> 8 operand values.
+template <int FMT>
+__device__ inline op_t<FMT> decode8(uint32_t w0, uint32_t w1, float scale, uint32_t tab) {
+    u32x4 r;
+    if constexpr (FMT == CQKV_FMT_FP8) {
+        return fp8x8_to_bf16x8(w0, w1);
+    } else if constexpr (FMT == CQKV_FMT_MXFP4) {
+        r.x = fp4x2_to_bf16x2(w0, 0, scale);
+        r.y = fp4x2_to_bf16x2(w0, 1, scale);
+        r.z = fp4x2_to_bf16x2(w0, 2, scale);
+        r.w = fp4x2_to_bf16x2(w0, 3, scale);
+    } else {
+        r.x = turbo_pair<0>(tab, w0);
+        r.y = turbo_pair<1>(tab, w0);
+        r.z = turbo_pair<2>(tab, w0);
+        r.w = turbo_pair<3>(tab, w0);
+    }
+    return __builtin_bit_cast(op_t<FMT>, r);
+}
+
+__device__ inline float e8m0_scale(uint32_t code) {  // code 0 marks an all-zero block
+    return code == 0 ? 0.0f : __uint_as_float(code << 23);
+}
+
+// NVFP4: 8 E2M1 codes of one word times the scale sg = fl(cs * gs) of their (token, block):
+// the E4M3 block scale cs times the token's f32 scale gs, rounded once per block, then one
+// multiply per element before the bf16 rounding. The reference's dequantized cache rounds
+// fl(fl(fp4 * cs) * gs) instead (RowCodec::elem times rsc0, turbo.rs:383-395): the two agree
+// except where the f32 values straddle a bf16 rounding boundary (one bf16 ulp, rarely). The codes
+// are converted unscaled: the conversion's own scale operand is meant for the E8M0 powers of
+// two of the MX formats, not for E4M3 values.
+__device__ inline bf16x8 nvfp4x8_bf16x8(uint32_t w, float sg) {
+    u32x4 r;
+    uint32_t *rp = (uint32_t *)&r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f32x2 f;
+        switch (i) {  // the selector must be an immediate
+        case 0: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0); break;
+        case 1: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1); break;
+        case 2: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2); break;
+        default: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3); break;
+        }
+        rp[i] = pack_bf16x2(f.x * sg, f.y * sg);
+    }
+    return __builtin_bit_cast(bf16x8, r);
+}
+
+// The same for 8 codes of 8 keys, key e scaled by sg[e].
+__device__ inline bf16x8 nvfp4x8_keys_bf16x8(uint32_t w, const float *sg) {
+    u32x4 r;
+    uint32_t *rp = (uint32_t *)&r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f32x2 f;
+        switch (i) {
+        case 0: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0); break;
+        case 1: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1); break;
+        case 2: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2); break;
+        default: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3); break;
+        }
+        rp[i] = pack_bf16x2(f.x * sg[2 * i], f.y * sg[2 * i + 1]);
+    }
+    return __builtin_bit_cast(bf16x8, r);
+}
+
+template <int KF, int VF, int D>
+__device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const DecodeArgs &a,
+                                    const op_t<KF> *qhi, const op_t<KF> *qlo, bool q_split, int lane,
+                                    int lo, int hi, int lo_max, int hi_min, int L, int koff,
+                                    uint32_t tab, float &m_run, float &l_run,
+                                    f32x4 *acc) {
+    constexpr int NCH = D / 32;
+    const int g = lane >> 4;
+    // tile and L are rows of the current block (the whole cache when not paged); keys of the
+    // call, for the masks, are koff further
+    const int t0 = tile * 32;
+    const bool full = koff + t0 >= lo_max && koff + t0 + 32 <= hi_min && t0 + 32 <= L;
+
+    // S^T = K Q^T for the two 16-key sub-tiles
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+        op_t<KF> k0, k1;
+        if constexpr (KF == CQKV_FMT_FP8) {
+            k0 = fp8x8_scaled_bf16x8(cur.k[0][2 * j], cur.k[0][2 * j + 1], __uint_as_float(cur.kscale[0]));
+            k1 = fp8x8_scaled_bf16x8(cur.k[1][2 * j], cur.k[1][2 * j + 1], __uint_as_float(cur.kscale[1]));
+        } else if constexpr (KF == CQKV_FMT_MXFP8) {
+            // chunk j holds head dims 64 (j >> 1) + 16 g + 8 (j & 1) + e: block 2 (j >> 1) + g / 2
+            const int bi = 2 * (j >> 1) + (g >> 1);
+            const float sc0 = e8m0_scale((cur.kscale[0] >> (8 * bi)) & 0xffu);
+            const float sc1 = e8m0_scale((cur.kscale[1] >> (8 * bi)) & 0xffu);
+            k0 = fp8x8_scaled_bf16x8(cur.k[0][2 * j], cur.k[0][2 * j + 1], sc0);
+            k1 = fp8x8_scaled_bf16x8(cur.k[1][2 * j], cur.k[1][2 * j + 1], sc1);
+        } else if constexpr (KF == CQKV_FMT_NVFP4) {
+            // chunk j holds head dims (D/4) g + 8 j + e: the lane's block byte j / 2 (D = 128)
+            const int bi = D == 128 ? (j >> 1) : 0;
+            const float sg0 = __builtin_amdgcn_cvt_f32_fp8(cur.kscale[0] >> (8 * bi), 0) *
+                              __uint_as_float(cur.ktok[0]);
+            const float sg1 = __builtin_amdgcn_cvt_f32_fp8(cur.kscale[1] >> (8 * bi), 0) *
+                              __uint_as_float(cur.ktok[1]);
+            k0 = nvfp4x8_bf16x8(cur.k[0][j], sg0);
+            k1 = nvfp4x8_bf16x8(cur.k[1][j], sg1);
+        } else {
+            float sc0 = 1.0f, sc1 = 1.0f;
+            if constexpr (KF == CQKV_FMT_MXFP4) {
+                sc0 = cur.kscale[0] ? __uint_as_float(cur.kscale[0] << 23) : 1.0f;
+                sc1 = cur.kscale[1] ? __uint_as_float(cur.kscale[1] << 23) : 1.0f;
+            }
+            k0 = decode8<KF>(cur.k[0][j], 0, sc0, tab);
+            k1 = decode8<KF>(cur.k[1][j], 0, sc1, tab);
+        }
+        s0 = mfma16x16x32(k0, qhi[j], s0);
+        s1 = mfma16x16x32(k1, qhi[j], s1);
+        if (q_split) {
+            s0 = mfma16x16x32(k0, qlo[j], s0);
+            s1 = mfma16x16x32(k1, qlo[j], s1);
+        }
+    }
+    float x[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    const int kbase = t0 + 8 * g;  // x[e] is key kbase + e
+    if constexpr (KF != CQKV_FMT_TURBO4) {  // scales are inside the operands
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] *= a.scale_log2;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            x[e] = x[e] * __uint_as_float(cur.ks8[e]) * a.scale_log2;
+    }
+    if (!full) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int key = koff + kbase + e;  // rows past the block's valid rows are masked too
+            if (!(key >= lo && key < hi && kbase + e < L)) x[e] = -__builtin_inff();
+        }
+    }
+    float mx = x[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) mx = fmaxf(mx, x[e]);
+    mx = group16_max(mx);
+    const float m_new = fmaxf(m_run, mx);
+    const bool none = m_new == -__builtin_inff();
+    const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+    float p[8], psum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        p[e] = none ? 0.0f : __builtin_amdgcn_exp2f(x[e] - m_new);
+        psum += p[e];
+    }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int t = 0; t < 2 * NCH; ++t) acc[t] *= alpha;
+    }
+    // keys past the written length may hold any bytes: keep them out of PV
+    const int nv = min(max(L - kbase, 0), 8);
+    if (t0 + 32 > L) {  // uniform: only the tile holding the end of the keys
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) {
+            if constexpr (is8<VF>()) {
+                const uint64_t keep = nv == 0 ? 0ull : (~0ull >> (64 - 8 * nv));
+                const uint64_t w0 = (((uint64_t)cur.v[u][1] << 32) | cur.v[u][0]) & keep;
+                const uint64_t w1 = (((uint64_t)cur.v[u][3] << 32) | cur.v[u][2]) & keep;
+                cur.v[u][0] = (uint32_t)w0;
+                cur.v[u][1] = (uint32_t)(w0 >> 32);
+                cur.v[u][2] = (uint32_t)w1;
+                cur.v[u][3] = (uint32_t)(w1 >> 32);
+            } else {
+                const uint32_t keep = nv == 0 ? 0u : (~0u >> (32 - 4 * nv));
+                cur.v[u][0] &= keep;
+                cur.v[u][1] &= keep;
+            }
+        }
+    }
+    // O^T += V^T P^T: d-tile 2u + h, row r <-> head dim 32u + 2r + h
+    if constexpr (VF == CQKV_FMT_MXFP4) {
+        // value block u: P scaled by the keys' block-u scales, one bf16 operand (the E2M1 codes
+        // and E8M0 scales are exact; P rounds to 8 significant bits, as in a bf16 flash
+        // attention). The scale of E8M0 code c is the float with exponent field c (code 0: 0).
+        uint32_t vw[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vw[e] = (uint32_t)__shfl((int)cur.vs, 8 * g + e);
+        if (t0 + 32 > L) {  // uniform: keys past the written length may hold any scale bytes
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (e >= nv) vw[e] = 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) {
+            u32x4 pw;
+            uint32_t *pwp = (uint32_t *)&pw;
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const float s0 = __uint_as_float(((vw[e] >> (8 * u)) & 0xffu) << 23);
+                const float s1 = __uint_as_float(((vw[e + 1] >> (8 * u)) & 0xffu) << 23);
+                pwp[e / 2] = pack_bf16x2(p[e] * s0, p[e + 1] * s1);
+            }
+            const op_t<VF> pb = __builtin_bit_cast(op_t<VF>, pw);
+            const op_t<VF> v0 = decode8<VF>(cur.v[u][0], 0, 1.0f, tab);
+            const op_t<VF> v1 = decode8<VF>(cur.v[u][1], 0, 1.0f, tab);
+            acc[2 * u] = mfma16x16x32(v0, pb, acc[2 * u]);
+            acc[2 * u + 1] = mfma16x16x32(v1, pb, acc[2 * u + 1]);
+        }
+    } else {
+        // FP8 / MXFP8 / NVFP4: the value scales are inside the V operand (rounded to bf16 as the
+        // reference's dequantized cache), P goes in full precision as a bf16 hi + lo pair.
+        // TURBO4: the norm goes into P, which enters as one f16 operand (11 significant bits;
+        // the lo part cost 8 more MFMAs per tile: config 5 246-254 -> 236 us same-box).
+        float pv[8], sv[8];
+        uint32_t vw[8], vw2[8];  // MX / NVFP4: the keys' block scale bytes
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            // scales past the written length may be any bits
+            if constexpr (direct_scales<VF>())
+                vw[e] = e < nv ? cur.vs8[e] : 0u;
+            else if constexpr (VF == CQKV_FMT_NVFP4)
+                vw[e] = e < nv ? cur.nvb[(D == 128 ? 2 : 1) * e] : 0u;
+            else
+                vw[e] = e < nv ? (uint32_t)__shfl((int)cur.vs, 8 * g + e) : 0u;
+            sv[e] = __uint_as_float(vw[e]);  // FP8 scale, TURBO4 norm
+            if constexpr (VF == CQKV_FMT_NVFP4)
+                vw2[e] = D == 128 && e < nv ? cur.nvb[2 * e + 1] : 0u;
+            if constexpr (VF == CQKV_FMT_TURBO4)
+                pv[e] = (e < nv && p[e] > 0.0f) ? p[e] * sv[e] : 0.0f;
+            else
+                pv[e] = (e < nv && p[e] > 0.0f) ? p[e] : 0.0f;
+        }
+        float gk[8];  // NVFP4: the keys' f32 scales
+        if constexpr (VF == CQKV_FMT_NVFP4) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                gk[e] = e < nv ? __uint_as_float(cur.nvg[e]) : 0.0f;
+        }
+        op_t<VF> phi, plo;
+        split8(pv, phi, plo);
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) {
+            op_t<VF> v0, v1;
+            if constexpr (VF == CQKV_FMT_FP8) {
+                v0 = fp8x8_scaled_bf16x8(cur.v[u][0], cur.v[u][1], sv);
+                v1 = fp8x8_scaled_bf16x8(cur.v[u][2], cur.v[u][3], sv);
+            } else if constexpr (VF == CQKV_FMT_MXFP8) {
+                // rows 32u + 2r + h: block u of every key
+                float su[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    su[e] = e8m0_scale((vw[e] >> (8 * u)) & 0xffu);
+                v0 = fp8x8_scaled_bf16x8(cur.v[u][0], cur.v[u][1], su);
+                v1 = fp8x8_scaled_bf16x8(cur.v[u][2], cur.v[u][3], su);
+            } else if constexpr (VF == CQKV_FMT_NVFP4) {
+                // this lane's rows 32u + 2n + h lie in block 2u + n / 8 of every key
+                const int bi = 2 * u + ((lane & 15) >> 3);
+                float sg[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t w = bi < 4 ? vw[e] : vw2[e];
+                    sg[e] = __builtin_amdgcn_cvt_f32_fp8(w >> (8 * (bi & 3)), 0) * gk[e];
+                    if (e >= nv) sg[e] = 0.0f;
+                }
+                v0 = nvfp4x8_keys_bf16x8(cur.v[u][0], sg);
+                v1 = nvfp4x8_keys_bf16x8(cur.v[u][1], sg);
+            } else {
+                v0 = decode8<VF>(cur.v[u][0], 0, 1.0f, tab);
+                v1 = decode8<VF>(cur.v[u][1], 0, 1.0f, tab);
+            }
+            acc[2 * u] = mfma16x16x32(v0, phi, acc[2 * u]);
+            acc[2 * u + 1] = mfma16x16x32(v1, phi, acc[2 * u + 1]);
+            if constexpr (VF != CQKV_FMT_TURBO4) {  // TURBO4: P (times the norms) as one f16
+                acc[2 * u] = mfma16x16x32(v0, plo, acc[2 * u]);
+                acc[2 * u + 1] = mfma16x16x32(v1, plo, acc[2 * u + 1]);
+            }
+        }
+    }
+}
+
+// Wavefronts per SIMD the register allocation must leave room for with MXFP4 keys and values:
+// 3 at D = 128 (168 VGPRs; at 176 only two fit and BASELINE config 3 runs 30 % slower), 4 at
+// D = 64; other formats take what the allocation gives.
+template <int KF, int VF, int D>
+constexpr int decode_min_waves() {
+    return KF == CQKV_FMT_MXFP4 && VF == CQKV_FMT_MXFP4 ? (D == 128 ? 3 : 4) : 1;
+}
+
+template <int KF, int VF, int D, int WAVES>
+__global__ __launch_bounds__(WAVES * 64)
+__attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_kernel(DecodeArgs a) {
+    constexpr int NCH = D / 32;
+    constexpr int NT = WAVES * 64;
+    constexpr bool kTurbo = KF == CQKV_FMT_TURBO4 || VF == CQKV_FMT_TURBO4;  // the code table
+    // the per-wavefront outputs (and, before the tile loop, the queries) share their LDS with the
+    // TurboQuant code table (64 KB-aligned, see turbo_pair), which is live only during the tile
+    // loop
+    constexpr int kOWords = WAVES * 16 * D, kTabWords = kTurbo ? 256 * 64 : 0;
+    __shared__ __attribute__((aligned(65536))) float sm_buf[kOWords > kTabWords ? kOWords : kTabWords];
+    float(*sm_o)[16][D] = (float(*)[16][D])sm_buf;
+    uint32_t *sm_tab = (uint32_t *)sm_buf;
+    __shared__ float sm_m[WAVES][16], sm_l[WAVES][16];
+
+    // 1-D grid, plane fastest: workgroup ids are dealt round-robin to the 8 XCDs, so with
+    // kv_heads a multiple of 8 each XCD takes whole planes of one kv head from every sequence -
+    // the same length mix everywhere (a split-fastest order would send split i of every plane to
+    // one XCD, and in a ragged batch the high splits are mostly empty)
+    const int planes = a.batch * a.kv_heads;
+    const int rest = (int)blockIdx.x / planes, plane_id = (int)blockIdx.x % planes;
+    const int split = rest / a.col_blocks, cb = rest % a.col_blocks;
+    // this workgroup's columns: global columns c0col .. c0col + ncb - 1 (query c / group, head
+    // c % group of the group)
+    const int c0col = 16 * cb, ncb = min(16, a.ncols - c0col);
+    const int hk = plane_id % a.kv_heads, b = plane_id / a.kv_heads;
+    // the wavefront index is uniform: keep it scalar so the tile loop stays a scalar loop
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 15, g = lane >> 4;
+    const int L = a.kv_lens ? __builtin_amdgcn_readfirstlane(min(max(a.kv_lens[b], 0), a.kv_len))
+                            : a.kv_len;
+
+    // visible key range of this lane's column, and the workgroup-wide bounds
+    const bool col_ok = n < ncb;
+    int lo, hi, lo_min, hi_max, lo_max, hi_min;
+    key_range(col_ok ? (c0col + n) / a.group : 0, a.q_len, L, a.wl, a.wr, lo, hi);
+    if (!col_ok) lo = hi = 0;
+    key_range(c0col / a.group, a.q_len, L, a.wl, a.wr, lo_min, hi_min);
+    key_range((c0col + ncb - 1) / a.group, a.q_len, L, a.wl, a.wr, lo_max, hi_max);
+    // the split's tiles and the planes they live in: a segment of one block (paged) or a range of
+    // the cache's tiles
+    const uint8_t *kc = a.kc, *ks = a.ks, *vc = a.vc, *vs = a.vs;
+    uint32_t kc_plane = a.kc_plane, ks_plane = a.ks_plane, vc_plane = a.vc_plane, vs_plane = a.vs_plane;
+    int koff = 0, Lb = L, tb, te;
+    if (a.segs) {
+        const PagedSeg sg = a.segs[split];
+        kc = sg.kc;
+        ks = sg.ks;
+        vc = sg.vc;
+        vs = sg.vs;
+        kc_plane = sg.kc_plane;
+        ks_plane = sg.ks_plane;
+        vc_plane = sg.vc_plane;
+        vs_plane = sg.vs_plane;
+        koff = sg.key_offset;
+        Lb = sg.rows;
+        tb = max(sg.tile_begin, max(lo_min - koff, 0) / 32);
+        te = min(sg.tile_end, (max(hi_max - koff, 0) + 31) / 32);
+    } else {
+        tb = max(split * a.tiles_per_split, lo_min / 32);
+        te = min((split + 1) * a.tiles_per_split, (hi_max + 31) / 32);
+    }
+
+    // ---- queries (rotated keys: q Pi_k^T = sign-flip, Hadamard, 1/sqrt(D)) ----
+    float(*sm_q)[D] = sm_o[0];
+    for (int idx = threadIdx.x; idx < 16 * D; idx += NT) {
+        const int c = idx / D, d = idx % D;
+        float v = 0.0f;
+        if (c < ncb) {
+            const int head = hk * a.group + (c0col + c) % a.group, qi = (c0col + c) / a.group;
+            v = load_elem(a.q, (int64_t)b * a.q_sb + (int64_t)head * a.q_sh + (int64_t)qi * a.q_si + d,
+                          a.q_dtype);
+        }
+        sm_q[c][d] = v;
+    }
+    __syncthreads();
+    if (a.rot_k) {
+        for (int c = wave; c < ncb; c += WAVES) {
+            const bool act = lane < D / 2;
+            float v0 = act ? sm_q[c][2 * lane] : 0.0f, v1 = act ? sm_q[c][2 * lane + 1] : 0.0f;
+            if (act && sign_bit(a.ksign_bits, 2 * lane)) v0 = -v0;
+            if (act && sign_bit(a.ksign_bits, 2 * lane + 1)) v1 = -v1;
+            fwht_pairs_dec<D>(v0, v1, lane);
+            if (act) {
+                sm_q[c][2 * lane] = v0 * a.rot_scale;
+                sm_q[c][2 * lane + 1] = v1 * a.rot_scale;
+            }
+        }
+        __syncthreads();
+    }
+    op_t<KF> qhi[NCH], qlo[NCH];
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+        float qv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qv[e] = sm_q[n][qdim<KF, D>(j, g, e)];
+        split8(qv, qhi[j], qlo[j]);
+    }
+    const bool q_split = a.q_split != 0;
+    __syncthreads();
+    if constexpr (kTurbo) {  // entry (b, l) at word 64 b + l: code pair (b & 15, b >> 4)
+        for (int i = threadIdx.x; i < 256 * 64; i += NT)
+            sm_tab[i] = pack_f16x2(a.cent[(i >> 6) & 15], a.cent[i >> 10]);
+        __syncthreads();
+    }
+
+    // ---- stream the tiles of this split ----
+    const int64_t plane = (int64_t)b * a.kv_heads + hk;
+    const rsrc_t kr = make_rsrc(kc + plane * kc_plane, kc_plane);
+    const rsrc_t ksr = make_rsrc(ks + plane * ks_plane, ks_plane);
+    const rsrc_t vr = make_rsrc(vc + plane * vc_plane, vc_plane);
+    const rsrc_t vsr = make_rsrc(vs + plane * vs_plane, vs_plane);
+    // NVFP4: the per-token f32 scales follow the block bytes of all the plane's tokens
+    uint32_t ktok_off = 0, vtok_off = 0;
+    if constexpr (KF == CQKV_FMT_NVFP4) ktok_off = ks_plane / (D / 16 + 4) * (D / 16);
+    if constexpr (VF == CQKV_FMT_NVFP4) vtok_off = vs_plane / (D / 16 + 4) * (D / 16);
+
+    f32x4 acc[2 * NCH];
+#pragma unroll
+    for (int t = 0; t < 2 * NCH; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint32_t tab = (uint32_t)(size_t)sm_tab + 4 * lane;
+    float m_run = -__builtin_inff(), l_run = 0.0f;
+
+    // Register sets A and B alternate; the scheduling barriers keep every load of one set
+    // issued before the next set's, so each wait only covers the set about to be used.
+    Tile<KF, VF, D> ta, tb2;
+    int t = tb + wave;
+    load_tile<KF, VF, D>(ta, t, t < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
+    __builtin_amdgcn_sched_barrier(0);
+    load_tile<KF, VF, D>(tb2, t + WAVES, t + WAVES < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
+    __builtin_amdgcn_sched_barrier(0);
+    for (; t < te; t += 2 * WAVES) {
+        compute_tile<KF, VF, D>(ta, t, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min, Lb, koff, tab,
+                             m_run, l_run, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        load_tile<KF, VF, D>(ta, t + 2 * WAVES, t + 2 * WAVES < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
+        __builtin_amdgcn_sched_barrier(0);
+        if (t + WAVES < te)
+            compute_tile<KF, VF, D>(tb2, t + WAVES, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min,
+                                 Lb, koff, tab, m_run, l_run, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        load_tile<KF, VF, D>(tb2, t + 3 * WAVES, t + 3 * WAVES < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- merge the wavefronts ----
+    if constexpr (kTurbo) __syncthreads();  // every wavefront is done with the code table
+    const float l_col = group16_sum(l_run);
+#pragma unroll
+    for (int u = 0; u < NCH; ++u)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sm_o[wave][n][32 * u + 8 * g + 2 * i + h] = acc[2 * u + h][i];
+    if (g == 0) {
+        sm_m[wave][n] = m_run;
+        sm_l[wave][n] = l_col;
+    }
+    __syncthreads();
+    const int rows = a.batch * a.q_heads * a.q_len;
+    // rotated values always leave partials: the combine unrotates them (an unrotation here costs
+    // the MXFP4 kernel three VGPRs and its third wavefront per SIMD)
+    const bool single = a.splits == 1 && !a.rot_v;
+    for (int idx = threadIdx.x; idx < ncb * D; idx += NT) {
+        const int c = idx / D, d = idx % D;
+        float M = -__builtin_inff();
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) M = fmaxf(M, sm_m[w][c]);
+        float o = 0.0f, lse = -__builtin_inff();
+        if (M != -__builtin_inff()) {
+            float wsum = 0.0f, osum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) {
+                const float f = __builtin_amdgcn_exp2f(sm_m[w][c] - M);
+                wsum += sm_l[w][c] * f;
+                osum += sm_o[w][c][d] * f;
+            }
+            o = osum / wsum;
+            lse = M + __builtin_log2f(wsum);
+        }
+        const int head = hk * a.group + (c0col + c) % a.group, qi = (c0col + c) / a.group;
+        if (!single) {  // the partial of this split; combine_kernel merges the splits
+            const int64_t row = ((int64_t)b * a.q_heads + head) * a.q_len + qi;
+            a.part_o[((int64_t)split * rows + row) * D + d] = o;
+            if (d == 0) a.part_lse[(int64_t)split * rows + row] = lse;
+        } else {
+            store_elem(a.out, (int64_t)b * a.o_sb + (int64_t)head * a.o_sh + (int64_t)qi * a.o_si + d,
+                       a.out_dtype, o);
+        }
+    }
+}
+
+// Wavefronts per workgroup: 8 when both formats have byte codes (HBM-bound: one workgroup per
+// plane fills a CU), 4 when either is a 4-bit format (its decode is VALU-heavy; two or three
+// independent workgroups per CU hide each other's latencies better than one of 8 wavefronts: 10 %
+// faster on BASELINE config 3).
+constexpr int kWaves = 8;
+constexpr int waves_of(int kf, int vf) {
+    return (kf == CQKV_FMT_FP8 || kf == CQKV_FMT_MXFP8) && (vf == CQKV_FMT_FP8 || vf == CQKV_FMT_MXFP8)
+               ? kWaves
+               : 4;
+}
+
+template <int KF, int VF>
+inline void launch_decode_kv(int d, dim3 grid, hipStream_t st, const DecodeArgs &a) {
+    constexpr int W = waves_of(KF, VF);
+    if (d == 64)
+        hipLaunchKernelGGL((decode_kernel<KF, VF, 64, W>), grid, dim3(W * 64), 0, st, a);
+    else
+        hipLaunchKernelGGL((decode_kernel<KF, VF, 128, W>), grid, dim3(W * 64), 0, st, a);
+}
+
+template <int KF>
+inline void launch_decode_k(int vf, int d, dim3 grid, hipStream_t st, const DecodeArgs &a) {
+    switch (vf) {
+    case CQKV_FMT_FP8: launch_decode_kv<KF, CQKV_FMT_FP8>(d, grid, st, a); break;
+    case CQKV_FMT_MXFP4: launch_decode_kv<KF, CQKV_FMT_MXFP4>(d, grid, st, a); break;
+    case CQKV_FMT_MXFP8: launch_decode_kv<KF, CQKV_FMT_MXFP8>(d, grid, st, a); break;
+    case CQKV_FMT_NVFP4: launch_decode_kv<KF, CQKV_FMT_NVFP4>(d, grid, st, a); break;
+    default: launch_decode_kv<KF, CQKV_FMT_TURBO4>(d, grid, st, a); break;
+    }
+}
+
+// Per-key-format launchers, defined in decode_inst.hip (one object per key format).
+#define CQKV_DECODE_LAUNCHER(F) \
+    void decode_launch_k##F(int vf, int d, dim3 grid, hipStream_t st, const DecodeArgs &a);
+CQKV_DECODE_LAUNCHER(0)
+CQKV_DECODE_LAUNCHER(2)
+CQKV_DECODE_LAUNCHER(3)
+CQKV_DECODE_LAUNCHER(4)
+CQKV_DECODE_LAUNCHER(5)
+
+}  // namespace cqkv

@@ -40,6 +40,8 @@ int check_side(const cqkv_side *s, const char *what) {
     if (!s->codes || !s->scales) return fail(CQKV_ERR_ARG, "%s: null codes / scales", what);
     if (s->is_value != 0 && s->is_value != 1)
         return fail(CQKV_ERR_ARG, "%s: is_value must be 0 or 1", what);
+    if (s->rotation < CQKV_ROT_DEFAULT || s->rotation > CQKV_ROT_HADAMARD)
+        return fail(CQKV_ERR_ARG, "%s: rotation %d (default, none or Hadamard)", what, s->rotation);
     const size_t cb = cqkv_codes_plane_bytes(s->format, s->head_dim, s->capacity);
     if (cb > 0x7fffffffull)
         return fail(CQKV_ERR_ARG, "%s: a plane of %zu bytes exceeds 2 GiB", what, cb);

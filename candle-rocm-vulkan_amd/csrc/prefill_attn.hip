@@ -788,7 +788,8 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
 
 int quant_append_launch(const cqkv_side *side, const void *x, int32_t x_dtype,
                         const int64_t xs[3], int32_t batch, int32_t tokens,
-                        const int32_t *positions, int32_t position, hipStream_t stream);
+                        const int32_t *positions, int32_t position, hipStream_t stream,
+                        int32_t clip_rows);
 
 }  // namespace cqkv
 
@@ -842,11 +843,10 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
     if (k_cache) {
         if (int rc = check_side(k_cache, "cqkv_flash_attn (key cache)")) return rc;
         if (int rc = check_side(v_cache, "cqkv_flash_attn (value cache)")) return rc;
-        if (k_cache->format != CQKV_FMT_FP8 || v_cache->format != CQKV_FMT_FP8 ||
-            k_cache->is_value != 0 || v_cache->is_value != 1 || k_cache->head_dim != head_dim ||
+        if (k_cache->is_value != 0 || v_cache->is_value != 1 || k_cache->head_dim != head_dim ||
             v_cache->head_dim != head_dim || k_cache->kv_heads != kv_heads ||
             v_cache->kv_heads != kv_heads)
-            return fail(CQKV_ERR_ARG, "cqkv_flash_attn: the fused append takes FP8 key / value sides of the same shape");
+            return fail(CQKV_ERR_ARG, "cqkv_flash_attn: the cache sides must be a key and a value side of the attention's head dim and kv heads");
         if (position < 0 || (int64_t)position + kv_len > k_cache->capacity ||
             (int64_t)position + kv_len > v_cache->capacity)
             return fail(CQKV_ERR_ARG, "cqkv_flash_attn: append [%d, %d) exceeds the cache capacity",
@@ -897,9 +897,11 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
     const size_t vt_bytes = (size_t)batch * kv_heads * kPfD * a.vt_len * 2;
     CQKV_HIP_CHECK(hipMallocAsync(&vt, vt_bytes, st));
     a.vt = (const uint16_t *)vt;
-    // the FP8 append runs inside the pre-pass when value tiles line up (position % 8 == 0),
-    // else as two cqkv_quant_append launches after the attention
-    const bool fused = k_cache != nullptr && position % 8 == 0;
+    // an FP8 append runs inside the pre-pass when value tiles line up (position % 8 == 0) and
+    // neither side rotates; any other append as two cqkv_quant_append launches after the attention
+    const bool fused = k_cache != nullptr && position % 8 == 0 && k_cache->format == CQKV_FMT_FP8 &&
+                       v_cache->format == CQKV_FMT_FP8 && !side_rotates(k_cache) &&
+                       !side_rotates(v_cache);
     if (fused) {
         a.append = 1;
         a.position = position;
@@ -927,9 +929,9 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
         // K / V are (batch, kv_len, kv_heads, D): the append kernel's (batch, head, token)
         const int64_t ks[3] = {k_strides[0], k_strides[2], k_strides[1]};
         const int64_t vs[3] = {v_strides[0], v_strides[2], v_strides[1]};
-        if (int rc = quant_append_launch(k_cache, k, CQKV_BF16, ks, batch, kv_len, nullptr, position, st))
+        if (int rc = quant_append_launch(k_cache, k, CQKV_BF16, ks, batch, kv_len, nullptr, position, st, 0))
             return rc;
-        if (int rc = quant_append_launch(v_cache, v, CQKV_BF16, vs, batch, kv_len, nullptr, position, st))
+        if (int rc = quant_append_launch(v_cache, v, CQKV_BF16, vs, batch, kv_len, nullptr, position, st, 0))
             return rc;
     }
     return CQKV_OK;

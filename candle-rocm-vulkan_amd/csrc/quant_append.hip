@@ -13,13 +13,22 @@ static int turbo_symmetric(const float bnd[16]) {
     return 1;
 }
 
-int fill_turbo_args(const cqkv_side *s, uint32_t sign_bits[4], float *rot_scale, float bnd[16]) {
-    float signs[128], cent[16];
-    turbo_signs(s->head_dim, s->seed, signs);
+// The Hadamard rotation of a side (its seed's sign vector as bits, bit j set -> column j has sign
+// -1, and 1 / sqrt(D)); zeros when the side does not rotate.
+void fill_rotation(const cqkv_side *s, uint32_t sign_bits[4], float *rot_scale) {
     for (int i = 0; i < 4; ++i) sign_bits[i] = 0;
+    *rot_scale = 1.0f;
+    if (!side_rotates(s)) return;
+    float signs[128];
+    turbo_signs(s->head_dim, s->seed, signs);
     for (int j = 0; j < s->head_dim; ++j)
         if (signs[j] < 0.0f) sign_bits[j >> 5] |= 1u << (j & 31);
     *rot_scale = 1.0f / sqrtf((float)s->head_dim);
+}
+
+// The TurboQuant-4 codebook boundaries of the side's head dim (+inf padded to 16).
+int fill_turbo_bounds(const cqkv_side *s, float bnd[16]) {
+    float cent[16];
     for (int i = 0; i < 16; ++i) bnd[i] = __builtin_inff();
     if (turbo_codebook(s->head_dim, 4, cent, bnd) != 0)
         return fail(CQKV_ERR_ARG, "turbo codebook for D=%d", s->head_dim);
@@ -60,19 +69,25 @@ static int fill_append_args(AppendArgs &a, const cqkv_side *side, const void *x,
                       : x_dtype == CQKV_BF16  ? kRowBF16
                                               : kRowF16;
     }
+    a.rotate = side_rotates(side) ? 1 : 0;
+    fill_rotation(side, a.sign_bits, &a.rot_scale);
     if (side->format == CQKV_FMT_TURBO4) {
-        if (int rc = fill_turbo_args(side, a.sign_bits, &a.rot_scale, a.bnd)) return rc;
+        if (int rc = fill_turbo_bounds(side, a.bnd)) return rc;
         a.turbo_sym = turbo_symmetric(a.bnd);
     }
     return CQKV_OK;
 }
 
-// Launch used by cqkv_quant_append and by the prefill's fused append.
+// Launch used by cqkv_quant_append, the prefill's unfused append and the value side of a fused
+// RoPE append whose sides differ in format; clip_rows > 0 skips positions at or past it (the
+// rotary table end of the fused RoPE append).
 int quant_append_launch(const cqkv_side *side, const void *x, int32_t x_dtype,
                         const int64_t xs[3], int32_t batch, int32_t tokens,
-                        const int32_t *positions, int32_t position, hipStream_t stream) {
+                        const int32_t *positions, int32_t position, hipStream_t stream,
+                        int32_t clip_rows) {
     AppendArgs a = {};
     if (int rc = fill_append_args(a, side, x, x_dtype, xs, tokens, positions, position)) return rc;
+    a.cs_rows = clip_rows;
     switch (side->format) {
     case CQKV_FMT_FP8: append_rows_launch_5(side, tokens, batch, stream, a); break;
     case CQKV_FMT_MXFP4: append_rows_launch_2(side, tokens, batch, stream, a); break;
@@ -101,9 +116,9 @@ extern "C" int cqkv_rope_quant_append(const cqkv_side *k_side, const cqkv_side *
     if (int rc = check_side(v_side, who)) return rc;
     if (k_side->is_value || !v_side->is_value)
         return fail(CQKV_ERR_ARG, "%s: k_side must be a key side and v_side a value side", who);
-    if (k_side->format != v_side->format || k_side->head_dim != v_side->head_dim ||
-        k_side->kv_heads != v_side->kv_heads || k_side->capacity != v_side->capacity)
-        return fail(CQKV_ERR_ARG, "%s: key / value sides differ in format, D, heads or capacity", who);
+    if (k_side->head_dim != v_side->head_dim || k_side->kv_heads != v_side->kv_heads ||
+        k_side->capacity != v_side->capacity)
+        return fail(CQKV_ERR_ARG, "%s: key / value sides differ in D, heads or capacity", who);
     if (!q || !k || !v || !q_out || !q_strides || !k_strides || !v_strides || !q_out_strides ||
         !cos || !sin)
         return fail(CQKV_ERR_ARG, "%s: null pointer argument", who);
@@ -157,9 +172,12 @@ extern "C" int cqkv_rope_quant_append(const cqkv_side *k_side, const cqkv_side *
         const int rpw = 64 / (k_side->head_dim / 8);  // heads per 16-byte-lane load
         r.q_units = r.q_vec16 ? (q_heads + rpw - 1) / rpw : q_heads;
     }
+    // values of another format than the keys: their own append launch after this one
+    const bool same = k_side->format == v_side->format;
+    r.v_units = same ? hkv : 0;
     // an unaligned start spans up to 7 more positions
     const int64_t blocks = ((int64_t)tokens + 7 + kRopeBlockTokens - 1) / kRopeBlockTokens *
-                           (2 * hkv + r.q_units);
+                           (hkv + r.v_units + r.q_units);
     if (blocks * 256 > (int64_t)UINT32_MAX)  // threads along x of one launch
         return fail(CQKV_ERR_ARG, "%s: %d tokens x %d heads exceed one launch", who, tokens,
                     2 * hkv + q_heads);
@@ -174,6 +192,9 @@ extern "C" int cqkv_rope_quant_append(const cqkv_side *k_side, const cqkv_side *
     default: rope_append_launch_0(rope_kind, d, grid, st, r); break;
     }
     CQKV_HIP_CHECK(hipGetLastError());
+    if (!same)
+        return quant_append_launch(v_side, v, dtype, v_strides, batch, tokens, positions, position,
+                                   st, cs_rows);
     return CQKV_OK;
 }
 
@@ -193,5 +214,5 @@ extern "C" int cqkv_quant_append(const cqkv_side *side, const void *x, int32_t x
         return fail(CQKV_ERR_ARG, "cqkv_quant_append: positions [%d, %d) exceed the capacity %d",
                     position, position + tokens, side->capacity);
     return quant_append_launch(side, x, x_dtype, x_strides, batch, tokens, positions, position,
-                               (hipStream_t)stream);
+                               (hipStream_t)stream, 0);
 }

@@ -5,9 +5,12 @@
  * Qntology/candle-rocm-vulkan. Every entry point is a host function taking device pointers,
  * explicit sizes / strides and a hipStream_t (NULL = the legacy stream the reference launches on),
  * and returning CQKV_OK or a negative status; cqkv_last_error() gives the message of the last
- * failure of the calling thread. No call allocates device memory except cqkv_decode_attention and
- * cqkv_decode_attention_paged when they are given no workspace. Nothing here holds torch or
- * candle types.
+ * failure of the calling thread. Device memory is allocated (stream-ordered, hipMallocAsync /
+ * hipFreeAsync on the call's stream) only by: cqkv_decode_attention and
+ * cqkv_decode_attention_paged when they are given no workspace; cqkv_flash_attn and
+ * cqkv_flash_attn_ext (a transposed copy of the values, batch * kv_heads * padded kv_len * D
+ * bf16); cqkv_flash_attn_fp8_codes (a per-plane staging buffer). cqkv_decode_attention_noalloc
+ * allocates nothing. Nothing here holds torch or candle types.
  *
  * Reference interfaces replaced (paths relative to the reference repository root):
  *   cqkv_quant_append      RocmStorage::tq_quantize + Cache::append
@@ -96,6 +99,15 @@ enum { CQKV_BF16 = 0, CQKV_F16 = 1, CQKV_F32 = 2 };
  * element 2i pairs with 2i + 1) of candle-nn/src/rotary_emb.rs. */
 enum { CQKV_ROPE_HALVES = 1, CQKV_ROPE_INTERLEAVED = 2 };
 
+/* Rotation of the rows before quantization (RotationKind of candle-core/src/accel/config.rs:
+ * 104-139, TurboQuantizer::rotate, candle-nn/src/turbo_quant.rs:182-189). DEFAULT is the format's
+ * own: Hadamard for TURBO4, none for the others. HADAMARD = the sign-flipped Sylvester matrix / sqrt(D)
+ * of `seed` (rotation_matrix, candle-core/src/accel/turbo.rs:180-203; what RotationKind::Auto
+ * resolves to for the power-of-two head dims here). The cache stores codes of the rotated rows;
+ * decode rotates the queries with the key side's rotation and unrotates the output with the
+ * value side's. */
+enum { CQKV_ROT_DEFAULT = 0, CQKV_ROT_NONE = 1, CQKV_ROT_HADAMARD = 2 };
+
 /* One side (keys or values) of a quantized cache. */
 typedef struct cqkv_side {
     int32_t format;    /* CQKV_FMT_* */
@@ -103,8 +115,8 @@ typedef struct cqkv_side {
     int32_t head_dim;  /* D: 64 or 128 */
     int32_t kv_heads;  /* Hkv */
     int32_t capacity;  /* tokens per plane, a multiple of 32 */
-    int32_t reserved;
-    uint64_t seed;     /* TURBO4 rotation seed (keys 42, values 44 by default); else unused */
+    int32_t rotation;  /* CQKV_ROT_* */
+    uint64_t seed;     /* rotation seed (keys 42, values 44 by default); unused without rotation */
     void *codes;       /* device, batch * kv_heads planes of cqkv_codes_plane_bytes() */
     void *scales;      /* device, batch * kv_heads planes of cqkv_scales_plane_bytes() */
 } cqkv_side;
@@ -131,7 +143,8 @@ int cqkv_quant_append(const cqkv_side *side, const void *x, int32_t x_dtype,
  * int32 array) or `position` + i: q is rotated with row p and written to q_out (strides
  * q_out_strides, `dtype`); k is rotated with row p, rounded to `dtype` as the reference's rope
  * output is, and quantized into k_side at cache position p; v is quantized into v_side as
- * cqkv_quant_append does. The sides must share format, D, heads and capacity. Positions past the
+ * cqkv_quant_append does. The sides must share D, heads and capacity; values of another format
+ * than the keys are appended by a second launch on the stream. Positions past the
  * capacity (keys and values) or the tables (all three) are an error when positions is NULL and
  * are skipped otherwise. */
 int cqkv_rope_quant_append(const cqkv_side *k_side, const cqkv_side *v_side, const void *q,
@@ -149,16 +162,22 @@ int cqkv_rope_quant_append(const cqkv_side *k_side, const cqkv_side *v_side, con
  *   keys [0, kv_lens[b]) of plane b are attended (device int32 array; NULL: kv_len for all),
  *   kv_len = the largest length (host), used to size the launch;
  *   window_left / window_right: -1 = unbounded (causal = (-1, 0));
- *   q head h reads kv head h / (q_heads / kv_heads); q_len * (q_heads / kv_heads) <= 16.
+ *   q head h reads kv head h / (q_heads / kv_heads); any q_len (chunked prefill or speculative
+ *   decode over the cache: the reference's grid (Lq * Hq / G, splits, B),
+ *   candle-core/kernels/turbo_quant_impl.h:621-627).
+ *   The key and value sides may differ in format; a side that rotates (CQKV_ROT_*) has the
+ *   queries rotated with the key rotation and the output unrotated with the value rotation.
  * splits: key splits per (batch, kv head); 0 = automatic. workspace: device scratch of at least
- * cqkv_decode_workspace_bytes(); NULL = allocated (and freed) by the call. */
+ * cqkv_decode_workspace_bytes() for the split count used (partials are written for more than
+ * one split, and at any split count when the value side rotates); NULL = allocated (and freed)
+ * by the call. */
 size_t cqkv_decode_workspace_bytes(int32_t batch, int32_t q_heads, int32_t q_len, int32_t head_dim,
                                    int32_t splits);
-/* The key splits cqkv_decode_attention uses with splits = 0 for a cache of `format`, `batch`
- * sequences, `kv_heads` heads and largest length kv_len, with (ragged != 0) or without per-
- * sequence lengths: size the workspace with it. */
-int32_t cqkv_decode_splits(int32_t format, int32_t batch, int32_t kv_heads, int32_t kv_len,
-                           int32_t ragged);
+/* The key splits cqkv_decode_attention uses with splits = 0 for a cache of key / value formats
+ * k_format / v_format, `batch` sequences, `kv_heads` heads and largest length kv_len, with
+ * (ragged != 0) or without per-sequence lengths: size the workspace with it. */
+int32_t cqkv_decode_splits(int32_t k_format, int32_t v_format, int32_t batch, int32_t kv_heads,
+                           int32_t kv_len, int32_t ragged);
 int cqkv_decode_attention(const void *q, int32_t q_dtype, const int64_t q_strides[3],
                           const cqkv_side *k, const cqkv_side *v, int32_t batch, int32_t q_heads,
                           int32_t q_len, const int32_t *kv_lens, int32_t kv_len,
@@ -217,8 +236,10 @@ int cqkv_decode_attention_paged(const void *q, int32_t q_dtype, const int64_t q_
 /* Dense bf16 flash attention (FlashAttnOp / candle_flash_attn::flash_attn):
  *   q (batch, q_len, q_heads, D), k / v (batch, kv_len, kv_heads, D), out like q, all bf16 with
  *   element strides {batch, token, head} (D contiguous); bottom-right aligned windows;
- *   causal = window (-1, 0). When k_cache / v_cache are non-NULL (FP8 sides) the same call also
- *   quantizes and appends k / v at positions [position, position + kv_len) of the cache. */
+ *   causal = window (-1, 0). When k_cache / v_cache are non-NULL (a key and a value side of any
+ *   formats and rotations) the same call also quantizes and appends k / v at positions
+ *   [position, position + kv_len) of the cache: inside the attention's pre-pass for unrotated
+ *   FP8 sides at a position that is a multiple of 8, else as two cqkv_quant_append launches. */
 int cqkv_flash_attn(const void *q, const int64_t q_strides[3], const void *k,
                     const int64_t k_strides[3], const void *v, const int64_t v_strides[3],
                     void *out, const int64_t out_strides[3], int32_t batch, int32_t q_len,
@@ -286,6 +307,15 @@ int cqkv_rows_import(const cqkv_side *side, const uint32_t *rows, int32_t batch,
                      int32_t position, cqkv_stream_t stream);
 int cqkv_rows_export(const cqkv_side *side, uint32_t *rows, int32_t batch, int32_t tokens,
                      int32_t position, cqkv_stream_t stream);
+
+/* Cache growth (the copy of Cache::append into a grown buffer, candle-nn/src/kv_cache.rs:56-99):
+ * the first `tokens` positions of every (batch, kv head) plane of src are copied into dst, a side
+ * of the same format, kind, head dim, kv heads and rotation (and seed, when it rotates) whose
+ * capacity may differ (at least `tokens`). Value sides copy whole 8-token tiles. Strided device copies on `stream`; no kernel,
+ * nothing allocated. The caller allocates dst (e.g. at the reference's grown capacity
+ * cap += max(grow_by, cap / 2) until it holds the new length, rounded up to 32). */
+int cqkv_side_copy(const cqkv_side *dst, const cqkv_side *src, int32_t batch, int32_t tokens,
+                   cqkv_stream_t stream);
 
 /* TurboQuant tables the kernels use (host): the Lloyd-Max codebook of TurboMse{bits} at head
  * dim D (candle-core/src/accel/turbo.rs:58-129; 2^bits centroids, 2^bits - 1 boundaries) and

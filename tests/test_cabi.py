@@ -112,14 +112,14 @@ def test_argument_errors_are_status_codes(cq):
     assert L.cqkv_quant_append(ctypes.byref(side), ctypes.c_void_p(1), 0, x, 1, 10, None, 60,
                                None) == cq.ERR_ARG
     assert b"exceed the capacity" in L.cqkv_last_error()
-    # decode: a key side given twice, GQA groups too wide, kv_len past the capacity
+    # decode: a key side given twice, more (query, head) columns than 2^24, kv_len past the
+    # capacity
     vs = cq.Side(cq.FP8, 1, 128, 8, 64, 0, 0, 1, 1)
     args = lambda k, v, hq, lq, kvlen: L.cqkv_decode_attention(
         ctypes.c_void_p(1), 0, x, ctypes.byref(k), ctypes.byref(v), 1, hq, lq, None, kvlen,
         0.1, -1, -1, ctypes.c_void_p(1), 0, x, 0, None, 0, None)
     assert args(side, side, 8, 1, 10) == cq.ERR_ARG
-    assert args(side, vs, 8 * 32, 1, 10) == cq.ERR_ARG
-    assert args(side, vs, 8 * 4, 5, 10) == cq.ERR_ARG
+    assert args(side, vs, 8 * 32, 1 << 20, 10) == cq.ERR_ARG
     assert args(side, vs, 8, 1, 65) == cq.ERR_ARG
     assert b"capacity" in L.cqkv_last_error()
 
@@ -180,7 +180,7 @@ def test_paged_argument_errors_and_workspace(cq):
     assert call(blocks((k0, v0, 10), (kx, v1, 10)), 2) == cq.ERR_ARG  # another format
     assert b"differs from block 0" in L.cqkv_last_error()
     assert call(blocks((k0, k0, 10)), 1) == cq.ERR_ARG  # a key side in the value slot
-    assert call(blocks((k0, v0, 10)), 1, hq=8 * 32) == cq.ERR_ARG  # GQA group too wide
+    assert call(blocks((k0, v0, 10)), 1, hq=8 * 32, lq=1 << 20) == cq.ERR_ARG  # 2^25 columns
     # scratch: the block table plus, with several segments, the partials
     one = L.cqkv_decode_paged_workspace_bytes(blocks((k0, v0, 10)), 1, 1, 8, 1)
     many = L.cqkv_decode_paged_workspace_bytes(blocks((k1, v1, 128), (k1, v1, 128)), 2, 1, 8, 1)
@@ -203,7 +203,8 @@ def test_rope_quant_append_argument_errors(cq):
     one = ctypes.c_void_p(1)
     k = cq.Side(cq.FP8, 0, 128, 2, 64, 0, 0, 1, 1)
     v = cq.Side(cq.FP8, 1, 128, 2, 64, 0, 0, 1, 1)
-    vm = cq.Side(cq.MXFP4, 1, 128, 2, 64, 0, 0, 1, 1)
+    vm = cq.Side(cq.MXFP4, 1, 128, 2, 96, 0, 0, 1, 1)  # another format is fine, capacity not
+    vr = cq.Side(cq.FP8, 1, 128, 2, 64, 7, 0, 1, 1)  # no rotation 7
 
     def call(ks=k, vs=v, kind=1, tokens=4, position=0, rows=100, hq=8, positions=None, cos=one):
         return L.cqkv_rope_quant_append(ctypes.byref(ks), ctypes.byref(vs), one, x, one, x, one,
@@ -212,6 +213,9 @@ def test_rope_quant_append_argument_errors(cq):
     assert call(kind=0) == cq.ERR_ARG
     assert b"rope kind" in L.cqkv_last_error()
     assert call(vs=vm) == cq.ERR_ARG
+    assert b"capacity" in L.cqkv_last_error()
+    assert call(vs=vr) == cq.ERR_ARG
+    assert b"rotation" in L.cqkv_last_error()
     assert call(ks=v, vs=k) == cq.ERR_ARG
     assert call(hq=5) == cq.ERR_ARG
     assert call(position=62) == cq.ERR_ARG
@@ -251,3 +255,41 @@ def test_fp8_attention_argument_errors(cq):
     assert L.cqkv_fp8_quantize_tensor(one, 7, 16, one, one, None) == cq.ERR_ARG
     assert L.cqkv_fp8_quantize_tensor(None, 0, 16, one, one, None) == cq.ERR_ARG
     assert L.cqkv_fp8_quantize_tensor(one, 0, -1, one, one, None) == cq.ERR_ARG
+
+
+def test_side_copy_argument_errors(cq):
+    """Cache growth copies only between sides of one format, kind, shape and rotation, and only
+    tokens both capacities hold; nothing is launched for zero tokens."""
+    L = cq.lib()
+    src = cq.Side(cq.MXFP4, 0, 128, 8, 64, 0, 42, 1, 1)
+
+    def copy(dst, tokens=40, batch=2):
+        return L.cqkv_side_copy(ctypes.byref(dst), ctypes.byref(src), batch, tokens, None)
+    assert copy(cq.Side(cq.FP8, 0, 128, 8, 128, 0, 42, 1, 1)) == cq.ERR_ARG
+    assert b"format" in L.cqkv_last_error()
+    assert copy(cq.Side(cq.MXFP4, 1, 128, 8, 128, 0, 42, 1, 1)) == cq.ERR_ARG  # value side
+    assert copy(cq.Side(cq.MXFP4, 0, 64, 8, 128, 0, 42, 1, 1)) == cq.ERR_ARG
+    assert copy(cq.Side(cq.MXFP4, 0, 128, 4, 128, 0, 42, 1, 1)) == cq.ERR_ARG
+    assert copy(cq.Side(cq.MXFP4, 0, 128, 8, 128, cq.ROT_HADAMARD, 42, 1, 1)) == cq.ERR_ARG
+    big = cq.Side(cq.MXFP4, 0, 128, 8, 128, 0, 42, 1, 1)
+    assert copy(big, tokens=65) == cq.ERR_ARG  # more than the source holds
+    assert b"capacities" in L.cqkv_last_error()
+    assert copy(cq.Side(cq.MXFP4, 0, 128, 8, 32, 0, 42, 1, 1)) == cq.ERR_ARG  # 40 > 32
+    assert copy(big, batch=0) == cq.ERR_ARG
+    assert copy(big, tokens=0) == cq.OK
+    # an unrotated side ignores the seed; a rotated one needs the same seed
+    assert copy(cq.Side(cq.MXFP4, 0, 128, 8, 128, 0, 7, 1, 1), tokens=0) == cq.OK
+    rsrc = cq.Side(cq.MXFP4, 0, 128, 8, 64, cq.ROT_HADAMARD, 42, 1, 1)
+    rdst = cq.Side(cq.MXFP4, 0, 128, 8, 128, cq.ROT_HADAMARD, 7, 1, 1)
+    assert L.cqkv_side_copy(ctypes.byref(rdst), ctypes.byref(rsrc), 2, 0, None) == cq.ERR_ARG
+    assert b"seed" in L.cqkv_last_error()
+
+
+def test_grown_capacity_follows_cache_append(cq):
+    """Cache::grown_capacity (candle-nn/src/kv_cache.rs:60-66): cap += max(grow_by, cap / 2, 1)
+    until the need fits, rounded up to 32 tokens here."""
+    assert cq.grown_capacity(64, 16, 64) == 64
+    assert cq.grown_capacity(64, 16, 65) == 96       # 64 + max(16, 32)
+    assert cq.grown_capacity(64, 100, 65) == 192     # 64 + 100 = 164 -> 192
+    assert cq.grown_capacity(32, 8, 100) == 128      # 32 -> 48 -> 72 -> 108 -> 128
+    assert cq.grown_capacity(0, 0, 1) == 32          # max(.., 1) makes progress

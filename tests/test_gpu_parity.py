@@ -362,3 +362,38 @@ def test_decode_vs_reference_fused_kernel_fixture(cq, dev, name, splits):
     own = np.abs(cpu - g["out"]).max()
     err = np.abs(got - cpu)
     assert err.max() <= own + 2e-2 and err.mean() <= 2e-3, (err.max(), own, err.mean())
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp4", "turbo4", "nvfp4", "mxfp8"])
+@pytest.mark.parametrize("lq,hq,hkv,wl,wr", [(10, 8, 2, -1, 0), (33, 4, 4, 20, 0), (7, 32, 8, -1, -1)])
+def test_decode_more_than_16_query_columns(cq, dev, fmt, lq, hq, hkv, wl, wr):
+    """q_len x group above 16 (chunked prefill / speculative decode over the cache: 40, 33 and
+    28 (query, head) columns per kv head), causal and windowed, against the oracle."""
+    got, want = run_decode(cq, dev, fmt, 2, hq, hkv, 128, 300, lq=lq, wl=wl, wr=wr)
+    assert_close_bf16(got, want)
+
+
+@pytest.mark.parametrize("splits", [1, 4])
+def test_decode_many_columns_split_and_paged(cq, dev, splits):
+    """64 columns (q_len 16 x group 4) with explicit splits, and the same through the paged
+    entry point over two blocks: the column blocks and the splits combine as the dense call."""
+    b, hq, hkv, d, n1, n2 = 1, 8, 2, 128, 200, 150
+    q = kv_source(61, (b, hq, 16, d)).to(dev)
+    k, v = kv_source(62, (b, hkv, n1 + n2, d)), kv_source(63, (b, hkv, n1 + n2, d))
+    dense = cq.TurboKvCache(5, 5, b, hkv, d, n1 + n2, device=dev)
+    dense.append(k.to(dev), v.to(dev))
+    want = cq.decode_attention(q, dense.k, dense.v, n1 + n2, 0.1, window_right=0, splits=splits,
+                               out=torch.empty(q.shape, dtype=torch.float32, device=dev))
+    blocks = []
+    for off, n in ((0, n1), (n1, n2)):
+        kc = cq.CacheSide.empty(5, False, b, hkv, d, 224, dev)
+        vc = cq.CacheSide.empty(5, True, b, hkv, d, 224, dev)
+        cq.quant_append(kc, k[:, :, off:off + n].to(dev), 0)
+        cq.quant_append(vc, v[:, :, off:off + n].to(dev), 0)
+        blocks.append((kc, vc, n))
+    got = cq.decode_attention_paged(q, blocks, 0.1, window_right=0,
+                                    out=torch.empty(q.shape, dtype=torch.float32, device=dev))
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(got.cpu().numpy(), want.cpu().numpy(), atol=1e-5, rtol=1e-4)
+    ref = oracle_decode(5, q.cpu(), oracle_rows(5, k), oracle_rows(5, v), n1 + n2, 0.1, wr=0)
+    assert_close_bf16(want.cpu().numpy(), ref)
