@@ -28,7 +28,7 @@ Each "cpu_baseline" is the oracle's restatement of the reference CPU path, timed
 CPUs (all of those this process may use) on a bounded sample of the workload and scaled to it.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
-                       [--only c2,c3,c4,c5,f8,fx,ap,ra] [--calibration-copy]
+                       [--only c2,c3,c4,c5,f8,fx,ap,ra,pd,pp] [--calibration-copy]
 """
 from __future__ import annotations
 
@@ -327,6 +327,50 @@ def fp8_attn_case(cq, dev, stream, steps, warmup):
             "timed": "whole call: E4M3 -> bf16 staging, V transpose pre-pass, prefill kernel"}
 
 
+def plain_decode_case(cq, dev, stream, steps, warmup, dtype, B=32, HQ=32, HKV=8, D=128,
+                      CTX=8192):
+    """flash_attn over plain K / V at the config-2 decode shape (one query per sequence): the
+    split-K row kernel; bytes = the K and V rows read (the queries and outputs are 0.02 %)."""
+    import torch
+    q = kv_gpu((B, 1, HQ, D), 61, dev, outliers=False).to(dtype)
+    k = kv_gpu((B, CTX, HKV, D), 62, dev).to(dtype)
+    v = kv_gpu((B, CTX, HKV, D), 63, dev).to(dtype)
+    out = torch.empty_like(q)
+    ws = torch.empty(max(cq.flash_attn_workspace_bytes(dtype, B, 1, CTX, HQ, HKV, D), 1),
+                     dtype=torch.uint8, device=dev)
+    ms = time_calls(lambda i: cq.flash_attn(q, k, v, 1.0 / D ** 0.5, True, out=out,
+                                            workspace=ws), steps, warmup, stream)
+    nbytes = 2 * B * CTX * HKV * D * 2
+    del q, k, v
+    torch.cuda.empty_cache()
+    return decode_summary(f"flash_attn decode over plain {str(dtype)[6:]} K / V, config-2 shape",
+                          ms, nbytes, {"batch": B, "q_heads": HQ, "kv_heads": HKV,
+                                       "head_dim": D, "context": CTX,
+                                       "timed": "whole call (split-K row kernel + combine)"})
+
+
+def plain_prefill_case(cq, dev, stream, steps, warmup, dtype, D, B=4, S=4096, HQ=32, HKV=8):
+    """Causal flash_attn on the plain-dtype kernel (f16, or a head dim other than 128)."""
+    import torch
+    q = kv_gpu((B, S, HQ, D), 71, dev, outliers=False).to(dtype)
+    k = kv_gpu((B, S, HKV, D), 72, dev).to(dtype)
+    v = kv_gpu((B, S, HKV, D), 73, dev).to(dtype)
+    out = torch.empty_like(q)
+    ws = torch.empty(max(cq.flash_attn_workspace_bytes(dtype, B, S, S, HQ, HKV, D), 1),
+                     dtype=torch.uint8, device=dev)
+    ms = time_calls(lambda i: cq.flash_attn(q, k, v, 1.0 / D ** 0.5, True, out=out,
+                                            workspace=ws), steps, warmup, stream)
+    flops = 2 * B * HQ * S * S * D  # causal: half of 4 B HQ S^2 D
+    del q, k, v
+    torch.cuda.empty_cache()
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"workload": f"causal flash_attn, {str(dtype)[6:]}, D={D}, B={B} S={S} {HQ}/{HKV} "
+                        "heads (plain-dtype kernel)",
+            "us_per_call": round(ms * 1e3, 2), "flop_per_call": flops,
+            "achieved_tflops": round(tf, 1), "peak_tflops": BF16_PEAK_TFLOPS,
+            "frac": round(tf / BF16_PEAK_TFLOPS, 4), "bound": "mfma", "timed": "whole call"}
+
+
 def append_case(cq, dev, stream, steps, warmup, b=32, hkv=8, d=128, t=2048):
     """cqkv_quant_append alone: B=32 sequences x 8 kv heads x 2048 tokens (524,288 rows of the
     config-2 cache shape) of bf16 K or V into FP8 / MXFP4 / TURBO4 / MXFP8 / NVFP4 sides at
@@ -380,7 +424,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
-    ap.add_argument("--only", default="", help="comma list of c2,c3,c4,c5,f8,fx,ap,ra (default: all)")
+    ap.add_argument("--only", default="",
+                    help="comma list of c2,c3,c4,c5,f8,fx,ap,ra,pd,pp (default: all)")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="also run a plain 1 GiB copy (for counter scaling)")
     args = ap.parse_args()
@@ -532,6 +577,21 @@ def main():
                  "timed": "whole call (split-K decode + combine)"})
             log(f"{name}: {ms * 1e3:.2f} us/call")
             torch.cuda.empty_cache()
+    if want("pd"):
+        for dt in (torch.bfloat16, torch.float16):
+            name = str(dt)[6:]
+            log(f"plain {name} K/V decode B=32 32/8 d=128 ctx 8192")
+            other[f"c2_shape_plain_{name}"] = plain_decode_case(cq, dev, stream, steps_x, warm_x,
+                                                                dt)
+            log(f"plain {name}: {other[f'c2_shape_plain_{name}']['us_per_call']} us/call")
+    if want("pp"):
+        for dt, d in ((torch.float16, 128), (torch.bfloat16, 64), (torch.bfloat16, 256)):
+            name = f"{str(dt)[6:]}_d{d}"
+            log(f"plain prefill {name} B=4 S=4096 32/8")
+            other[f"c4_shape_plain_{name}"] = plain_prefill_case(cq, dev, stream,
+                                                                 max(steps_x // 4, 5),
+                                                                 max(warm_x // 4, 3), dt, d)
+            log(f"plain prefill {name}: {other[f'c4_shape_plain_{name}']['us_per_call']} us/call")
     if want("ap"):
         log("append: B=32 x 8 kv heads x 2048 tokens, D=128, every format, keys and values")
         other["append_c2_shape"] = append_case(cq, dev, stream, steps_x, warm_x)

@@ -47,6 +47,14 @@ class Side(ctypes.Structure):
                 ("scales", ctypes.c_void_p)]
 
 
+class PlainBlock(ctypes.Structure):
+    """cqkv_plain_block: plain K / V (batch, kv_heads, capacity, D) with {batch, head, row}
+    strides and the valid rows at the start of their planes."""
+    _fields_ = [("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+                ("k_strides", ctypes.c_int64 * 3), ("v_strides", ctypes.c_int64 * 3),
+                ("rows", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+
 class KvBlock(ctypes.Structure):
     """cqkv_kv_block: a key side, a value side and the valid rows at the start of their planes."""
     _fields_ = [("k", ctypes.POINTER(Side)), ("v", ctypes.POINTER(Side)),
@@ -87,10 +95,17 @@ def lib() -> ctypes.CDLL:
         L.cqkv_decode_attention_paged.argtypes = [P, i32, I64P, BP, i32, i32, i32, i32, f32, i32,
                                                   i32, P, i32, I64P, P, sz, P]
         L.cqkv_flash_attn.argtypes = [P, I64P, P, I64P, P, I64P, P, I64P, i32, i32, i32, i32,
-                                      i32, i32, f32, i32, i32, SP, SP, i32, P]
+                                      i32, i32, i32, f32, i32, i32, SP, SP, i32, P]
         L.cqkv_flash_attn_ext.argtypes = [P, I64P, P, I64P, P, I64P, P, I64P, i32, i32, i32,
-                                          i32, i32, i32, f32, i32, i32, f32, P, i32, P, P, i32,
-                                          i32, SP, SP, i32, P]
+                                          i32, i32, i32, i32, f32, i32, i32, f32, P, i32, P, P,
+                                          i32, i32, SP, SP, i32, P, sz, P]
+        L.cqkv_flash_attn_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32, i32, i32]
+        L.cqkv_flash_attn_workspace_bytes.restype = sz
+        PBP = ctypes.POINTER(PlainBlock)
+        L.cqkv_flash_attn_blocks_workspace_bytes.argtypes = [PBP, i32, i32, i32, i32, i32, i32]
+        L.cqkv_flash_attn_blocks_workspace_bytes.restype = sz
+        L.cqkv_flash_attn_blocks.argtypes = [P, I64P, PBP, i32, i32, i32, i32, i32, i32, i32,
+                                             f32, i32, i32, f32, P, i32, P, I64P, P, sz, P]
         L.cqkv_fp8_quantize_tensor.argtypes = [P, i32, ctypes.c_int64, P, P, P]
         L.cqkv_hadamard_rows.argtypes = [P, i32, ctypes.c_int64, ctypes.c_int64, i32,
                                          ctypes.c_uint64, P, ctypes.c_int64, P]
@@ -114,7 +129,9 @@ EXPORTED = ["cqkv_codes_plane_bytes", "cqkv_scales_plane_bytes", "cqkv_quant_app
             "cqkv_decode_workspace_bytes", "cqkv_decode_splits", "cqkv_decode_attention",
             "cqkv_decode_attention_noalloc",
             "cqkv_decode_paged_workspace_bytes", "cqkv_decode_attention_paged",
-            "cqkv_flash_attn", "cqkv_flash_attn_ext", "cqkv_fp8_quantize_tensor",
+            "cqkv_flash_attn", "cqkv_flash_attn_ext", "cqkv_flash_attn_workspace_bytes",
+            "cqkv_flash_attn_blocks", "cqkv_flash_attn_blocks_workspace_bytes",
+            "cqkv_fp8_quantize_tensor",
             "cqkv_flash_attn_fp8", "cqkv_hadamard_rows", "cqkv_reference_row_words", "cqkv_rows_import",
             "cqkv_rows_export", "cqkv_side_copy", "cqkv_turbo_codebook", "cqkv_turbo_signs",
             "cqkv_last_error",
@@ -385,29 +402,92 @@ def _alibi_arg(alibi_slopes, batch: int, q_heads: int):
                              f"got {tuple(alibi_slopes.shape)}")
 
 
+def _attn_inputs(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> int:
+    """The dtype id of q / k / v (bf16 or f16, one dtype, head dim contiguous on the GPU)."""
+    for t, name in ((q, "q"), (k, "k"), (v, "v")):
+        _need_gpu(t, name)
+        if t.stride(-1) != 1:
+            raise CqkvError(ERR_ARG, f"{name} needs a contiguous head dim (stride {t.stride()})")
+    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise CqkvError(ERR_ARG, f"q / k / v must share bf16 or f16 (got {q.dtype}, {k.dtype}, "
+                                 f"{v.dtype})")
+    return _DTYPES[q.dtype]
+
+
+def flash_attn_workspace_bytes(dtype: torch.dtype, batch: int, q_len: int, kv_len: int,
+                               q_heads: int, kv_heads: int, head_dim: int,
+                               varlen: bool = False) -> int:
+    return lib().cqkv_flash_attn_workspace_bytes(_DTYPES[dtype], batch, q_len, kv_len, q_heads,
+                                                 kv_heads, head_dim, int(varlen))
+
+
 def flash_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, softmax_scale: float,
                causal: bool, window_left: int = -1, window_right: int = -1,
                k_cache: CacheSide | None = None, v_cache: CacheSide | None = None,
                position: int = 0, out: torch.Tensor | None = None, softcap: float = 0.0,
-               alibi_slopes: torch.Tensor | None = None) -> torch.Tensor:
-    """candle_flash_attn::flash_attn layout: q (b, s_q, h_q, d), k / v (b, s_kv, h_kv, d), bf16.
-    With k_cache / v_cache (FP8 sides) K / V are also quantized into the cache at `position`.
-    softcap / alibi_slopes as flash_attn_alibi_windowed_softcap (candle-flash-attn/src/lib.rs)."""
-    _need_gpu(q, "q")
+               alibi_slopes: torch.Tensor | None = None,
+               workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """candle_flash_attn::flash_attn layout: q (b, s_q, h_q, d), k / v (b, s_kv, h_kv, d), bf16 or
+    f16, d a multiple of 8 up to 256. With k_cache / v_cache K / V are also quantized into the
+    cache at `position`. softcap / alibi_slopes as flash_attn_alibi_windowed_softcap
+    (candle-flash-attn/src/lib.rs)."""
+    dt = _attn_inputs(q, k, v)
     b, sq, hq, d = q.shape
     _, sk, hkv, _ = k.shape
     if out is None:
-        out = torch.empty_like(q)
+        out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
+        raise CqkvError(ERR_ARG, "out must match q in shape and dtype, with a contiguous head dim")
     if causal:
         window_right = 0
     kc = None if k_cache is None else ctypes.byref(k_cache.struct())
     vc = None if v_cache is None else ctypes.byref(v_cache.struct())
     al, al_bs = _alibi_arg(alibi_slopes, b, hq)
+    ws = None if workspace is None else _ptr(workspace)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _check(lib().cqkv_flash_attn_ext(
         _ptr(q), _strides3(q, (0, 1, 2)), _ptr(k), _strides3(k, (0, 1, 2)), _ptr(v),
-        _strides3(v, (0, 1, 2)), _ptr(out), _strides3(out, (0, 1, 2)), b, sq, sk, hq, hkv, d,
+        _strides3(v, (0, 1, 2)), _ptr(out), _strides3(out, (0, 1, 2)), dt, b, sq, sk, hq, hkv, d,
         softmax_scale, window_left, window_right, softcap, al, al_bs, None, None, 0, 0, kc, vc,
-        position, _stream(q.device)))
+        position, ws, ws_bytes, _stream(q.device)))
+    return out
+
+
+def flash_attn_blocks(q: torch.Tensor, blocks, softmax_scale: float, window_left: int = -1,
+                      window_right: int = -1, softcap: float = 0.0,
+                      alibi_slopes: torch.Tensor | None = None,
+                      out: torch.Tensor | None = None,
+                      workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """flash_attn_blocks (candle-nn/src/flash_attn.rs:719-765): q (batch, q_heads, q_len, d) over
+    blocks [(k, v, rows)] of plain K / V (batch, kv_heads, capacity, d) - the valid rows of all
+    blocks in order are the keys of every sequence."""
+    _need_gpu(q, "q")
+    if not blocks:
+        raise CqkvError(ERR_ARG, "no blocks")
+    dt = _attn_inputs(q, blocks[0][0], blocks[0][1])
+    b, hq, lq, d = q.shape
+    hkv = blocks[0][0].shape[1]
+    arr = (PlainBlock * len(blocks))()
+    for i, (k, v, rows) in enumerate(blocks):
+        _attn_inputs(q, k, v)
+        if k.dim() != 4 or v.shape != k.shape or k.shape[0] != b or k.shape[1] != hkv or \
+                k.shape[3] != d:
+            raise CqkvError(ERR_ARG, f"block {i}: k {tuple(k.shape)} / v {tuple(v.shape)} do not "
+                                     f"match (batch {b}, {hkv} kv heads, head dim {d})")
+        if rows > k.shape[2]:
+            raise CqkvError(ERR_ARG, f"block {i}: {rows} rows above its capacity {k.shape[2]}")
+        arr[i].k, arr[i].v, arr[i].rows = _ptr(k), _ptr(v), int(rows)
+        arr[i].k_strides[:] = [k.stride(0), k.stride(1), k.stride(2)]
+        arr[i].v_strides[:] = [v.stride(0), v.stride(1), v.stride(2)]
+    if out is None:
+        out = torch.empty((b, hq, lq, d), dtype=q.dtype, device=q.device)
+    al, al_bs = _alibi_arg(alibi_slopes, b, hq)
+    ws = None if workspace is None else _ptr(workspace)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _check(lib().cqkv_flash_attn_blocks(
+        _ptr(q), _strides3(q, (0, 1, 2)), arr, len(blocks), dt, b, hq, lq, hkv, d, softmax_scale,
+        window_left, window_right, softcap, al, al_bs, _ptr(out), _strides3(out, (0, 1, 2)), ws,
+        ws_bytes, _stream(q.device)))
     return out
 
 
@@ -496,9 +576,9 @@ def flash_attn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                       alibi_slopes: torch.Tensor | None = None,
                       out: torch.Tensor | None = None) -> torch.Tensor:
     """candle_flash_attn::flash_attn_varlen layout: q (total_q, h_q, d), k / v (total_k, h_kv,
-    d) bf16, cumulative sequence offsets cu_seqlens_q / cu_seqlens_k (batch + 1,) int32 on the
-    device (the reference takes u32)."""
-    _need_gpu(q, "q")
+    d) bf16 or f16, cumulative sequence offsets cu_seqlens_q / cu_seqlens_k (batch + 1,) int32 on
+    the device (the reference takes u32)."""
+    dt = _attn_inputs(q, k, v)
     total_q, hq, d = q.shape
     total_k, hkv, _ = k.shape
     for name, c in (("cu_seqlens_q", cu_seqlens_q), ("cu_seqlens_k", cu_seqlens_k)):
@@ -516,9 +596,9 @@ def flash_attn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     strides = lambda t: (ctypes.c_int64 * 3)(0, t.stride(0), t.stride(1))
     _check(lib().cqkv_flash_attn_ext(
         _ptr(q), strides(q), _ptr(k), strides(k), _ptr(v), strides(v), _ptr(out), strides(out),
-        b, max_seqlen_q, max_seqlen_k, hq, hkv, d, softmax_scale, window_left, window_right,
+        dt, b, max_seqlen_q, max_seqlen_k, hq, hkv, d, softmax_scale, window_left, window_right,
         softcap, al, al_bs, _ptr(cu_seqlens_q), _ptr(cu_seqlens_k), total_q, total_k, None, None,
-        0, _stream(q.device)))
+        0, None, 0, _stream(q.device)))
     return out
 
 

@@ -120,14 +120,15 @@ __global__ __launch_bounds__(256) void fp8_stage_kernel(Fp8StageArgs a) {
 
 int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
                     const int64_t k_strides[3], const void *v, const int64_t v_strides[3],
-                    void *out, const int64_t out_strides[3], int32_t batch, int32_t q_len,
-                    int32_t kv_len, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
-                    float softmax_scale, int32_t window_left, int32_t window_right, float softcap,
-                    const float *alibi_slopes, int32_t alibi_batch_stride,
-                    const int32_t *cu_seqlens_q, const int32_t *cu_seqlens_k, int32_t total_q,
-                    int32_t total_k, const cqkv_side *k_cache, const cqkv_side *v_cache,
-                    int32_t position, cqkv_stream_t stream, float q_mul, const float *q_mul_dev,
-                    float o_mul, const float *o_mul_dev);
+                    void *out, const int64_t out_strides[3], int32_t dtype, int32_t batch,
+                    int32_t q_len, int32_t kv_len, int32_t q_heads, int32_t kv_heads,
+                    int32_t head_dim, float softmax_scale, int32_t window_left,
+                    int32_t window_right, float softcap, const float *alibi_slopes,
+                    int32_t alibi_batch_stride, const int32_t *cu_seqlens_q,
+                    const int32_t *cu_seqlens_k, int32_t total_q, int32_t total_k,
+                    const cqkv_side *k_cache, const cqkv_side *v_cache, int32_t position,
+                    void *workspace, size_t workspace_bytes, cqkv_stream_t stream, float q_mul,
+                    const float *q_mul_dev, float o_mul, const float *o_mul_dev);
 
 }  // namespace cqkv
 
@@ -204,10 +205,11 @@ extern "C" int cqkv_flash_attn_fp8(const void *q, const int64_t q_strides[3], co
     } else {
         // the staged K / V are (batch, kv_heads, kv_len, D): (batch, token, head) strides
         const int64_t ss[3] = {(int64_t)kv_heads * kv_len * 128, 128, (int64_t)kv_len * 128};
-        rc = flash_attn_impl(q, q_strides, s.kb, ss, s.vb, ss, out, out_strides, batch, q_len,
-                             kv_len, q_heads, kv_heads, head_dim, softmax_scale, window_left,
-                             window_right, 0.0f, nullptr, 0, nullptr, nullptr, 0, 0, nullptr,
-                             nullptr, 0, stream, k_descale, k_scale, v_descale, v_scale);
+        rc = flash_attn_impl(q, q_strides, s.kb, ss, s.vb, ss, out, out_strides, CQKV_BF16, batch,
+                             q_len, kv_len, q_heads, kv_heads, head_dim, softmax_scale,
+                             window_left, window_right, 0.0f, nullptr, 0, nullptr, nullptr, 0, 0,
+                             nullptr, nullptr, 0, nullptr, 0, stream, k_descale, k_scale,
+                             v_descale, v_scale);
     }
     const hipError_t fe = hipFreeAsync(scratch, st);
     if (rc != CQKV_OK) return rc;

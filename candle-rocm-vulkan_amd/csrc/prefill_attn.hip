@@ -28,8 +28,11 @@
 //    one wavefront are interleaved instruction by instruction (sched_group_barrier), and the two
 //    wavefronts of each SIMD fill each other's stalls.
 //  * Causal work is uneven: the workgroups with the most key tiles are dispatched first.
+#include <algorithm>
+
 #include "cqkv_device.h"
 #include "cqkv_host.h"
+#include "flash_plain.h"
 
 namespace cqkv {
 
@@ -786,6 +789,13 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
     }
 }
 
+int fa_plain_check(const char *who, int32_t dtype, int32_t head_dim, int64_t k_row_stride,
+                   int64_t v_row_stride, int64_t kv_len);
+int fa_plain_run(FaArgs a, const char *who, void *workspace, size_t workspace_bytes,
+                 hipStream_t st);
+size_t fa_plain_workspace_bytes(int32_t batch, int32_t q_len, int32_t kv_len, int32_t q_heads,
+                                int32_t kv_heads, int32_t head_dim, bool ragged);
+
 int quant_append_launch(const cqkv_side *side, const void *x, int32_t x_dtype,
                         const int64_t xs[3], int32_t batch, int32_t tokens,
                         const int32_t *positions, int32_t position, hipStream_t stream,
@@ -799,20 +809,62 @@ namespace cqkv {
 
 // The whole prefill call; descales (q_mul / o_mul and their device factors) are those of the FP8
 // K / V path (fp8_attn.hip), 1 / null for bf16 K / V.
+// Whether a call takes the MFMA prefill kernel (bf16, head dim 128, more than 16 queries);
+// every other call runs the plain-dtype kernel of flash_plain.h.
+static bool pf_fast_path(int32_t dtype, int32_t head_dim, int32_t q_len) {
+    return dtype == CQKV_BF16 && head_dim == kPfD && q_len > 16;
+}
+
+// V^T scratch of the MFMA prefill: (batch, kv heads, D, kv_len rounded up to the key tile) bf16.
+static size_t pf_vt_bytes(int32_t batch, int32_t kv_len, int32_t kv_heads) {
+    return (size_t)batch * kv_heads * kPfD * ((kv_len + kPfBK - 1) / kPfBK * kPfBK) * 2;
+}
+
+size_t flash_attn_workspace(int32_t dtype, int32_t batch, int32_t q_len, int32_t kv_len,
+                            int32_t q_heads, int32_t kv_heads, int32_t head_dim, bool varlen) {
+    if (batch <= 0 || q_len <= 0 || kv_len <= 0 || q_heads <= 0 || kv_heads <= 0 ||
+        q_heads % kv_heads != 0 || head_dim <= 0 || head_dim > 256)
+        return 0;
+    const size_t plain =
+        fa_plain_workspace_bytes(batch, q_len, kv_len, q_heads, kv_heads, head_dim, varlen);
+    // a call of the MFMA prefill's shape whose q / out rows are not aligned for it runs the
+    // plain kernel: size for either
+    if (pf_fast_path(dtype, head_dim, q_len))
+        return std::max(pf_vt_bytes(batch, kv_len, kv_heads), plain);
+    return plain;
+}
+
 int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
                     const int64_t k_strides[3], const void *v, const int64_t v_strides[3],
-                    void *out, const int64_t out_strides[3], int32_t batch, int32_t q_len,
-                    int32_t kv_len, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
-                    float softmax_scale, int32_t window_left, int32_t window_right, float softcap,
-                    const float *alibi_slopes, int32_t alibi_batch_stride,
-                    const int32_t *cu_seqlens_q, const int32_t *cu_seqlens_k, int32_t total_q,
-                    int32_t total_k, const cqkv_side *k_cache, const cqkv_side *v_cache,
-                    int32_t position, cqkv_stream_t stream, float q_mul, const float *q_mul_dev,
-                    float o_mul, const float *o_mul_dev) {
+                    void *out, const int64_t out_strides[3], int32_t dtype, int32_t batch,
+                    int32_t q_len, int32_t kv_len, int32_t q_heads, int32_t kv_heads,
+                    int32_t head_dim, float softmax_scale, int32_t window_left,
+                    int32_t window_right, float softcap, const float *alibi_slopes,
+                    int32_t alibi_batch_stride, const int32_t *cu_seqlens_q,
+                    const int32_t *cu_seqlens_k, int32_t total_q, int32_t total_k,
+                    const cqkv_side *k_cache, const cqkv_side *v_cache, int32_t position,
+                    void *workspace, size_t workspace_bytes, cqkv_stream_t stream, float q_mul,
+                    const float *q_mul_dev, float o_mul, const float *o_mul_dev) {
     if (!q || !k || !v || !out || !q_strides || !k_strides || !v_strides || !out_strides)
         return fail(CQKV_ERR_ARG, "cqkv_flash_attn: null tensor or strides");
-    if (head_dim != kPfD)
-        return fail(CQKV_ERR_ARG, "cqkv_flash_attn: head_dim %d not supported (128)", head_dim);
+    // 16-byte row loads of K / V in both kernels, of q in the MFMA prefill (which also stores
+    // 8-byte pieces of out rows); a batch stride is unused with variable-length batches
+    const bool vl = cu_seqlens_q != nullptr;
+    auto aligned = [vl](const void *p, const int64_t s[3], int bytes) {
+        const int64_t e = bytes / 2;  // elements per aligned piece
+        return (uintptr_t)p % bytes == 0 && (vl || s[0] % e == 0) && s[1] % e == 0 && s[2] % e == 0;
+    };
+    if (!aligned(k, k_strides, 16) || !aligned(v, v_strides, 16))
+        return fail(CQKV_ERR_ARG,
+                    "cqkv_flash_attn: K / V need 16-byte aligned rows (pointers and strides in "
+                    "whole 8-element chunks)");
+    const bool fast = pf_fast_path(dtype, head_dim, q_len) && aligned(q, q_strides, 16) &&
+                      aligned(out, out_strides, 8);
+    if (!fast) {
+        if (int rc = fa_plain_check("cqkv_flash_attn", dtype, head_dim, k_strides[1], v_strides[1],
+                                    kv_len))
+            return rc;
+    }
     if (batch <= 0 || q_len <= 0 || kv_len <= 0 || q_heads <= 0 || kv_heads <= 0 ||
         q_heads % kv_heads != 0)
         return fail(CQKV_ERR_ARG, "cqkv_flash_attn: batch %d q_len %d kv_len %d heads %d / %d",
@@ -832,7 +884,7 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
         return fail(CQKV_ERR_ARG, "cqkv_flash_attn: variable-length rows total_q %d total_k %d",
                     total_q, total_k);
     if (varlen && k_cache)
-        return fail(CQKV_ERR_ARG, "cqkv_flash_attn: the fused cache append takes dense batches only");
+        return fail(CQKV_ERR_ARG, "cqkv_flash_attn: the cache append takes dense batches only");
     // 32-bit byte offsets inside a key tile (64 token rows) and inside a V^T plane
     if (k_strides && (k_strides[1] <= 0 || k_strides[1] >= (1 << 25)))
         return fail(CQKV_ERR_ARG, "cqkv_flash_attn: key token stride %lld outside [1, 2^25)",
@@ -851,6 +903,57 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
             (int64_t)position + kv_len > v_cache->capacity)
             return fail(CQKV_ERR_ARG, "cqkv_flash_attn: append [%d, %d) exceeds the cache capacity",
                         position, position + kv_len);
+    }
+    if (!fast) {
+        FaArgs f = {};
+        f.q = (const uint16_t *)q;
+        f.q_sb = q_strides[0];
+        f.q_st = q_strides[1];
+        f.q_sh = q_strides[2];
+        f.out = out;
+        f.o_sb = out_strides[0];
+        f.o_st = out_strides[1];
+        f.o_sh = out_strides[2];
+        f.k = (const uint16_t *)k;
+        f.v = (const uint16_t *)v;
+        f.k_sb = k_strides[0];
+        f.k_st = k_strides[1];
+        f.k_sh = k_strides[2];
+        f.v_sb = v_strides[0];
+        f.v_st = v_strides[1];
+        f.v_sh = v_strides[2];
+        f.cu_q = cu_seqlens_q;
+        f.cu_k = cu_seqlens_k;
+        f.total_q = total_q;
+        f.total_k = total_k;
+        f.batch = batch;
+        f.q_len = q_len;
+        f.kv_len = kv_len;
+        f.q_heads = q_heads;
+        f.kv_heads = kv_heads;
+        f.group = q_heads / kv_heads;
+        f.head_dim = head_dim;
+        f.dtype = dtype;
+        f.wl = window_left;
+        f.wr = window_right;
+        f.scale_log2 = softmax_scale * q_mul * kLog2e;
+        f.softcap2 = softcap * kLog2e;
+        f.alibi = alibi_slopes;
+        f.alibi_bs = alibi_batch_stride;
+        f.o_mul = o_mul;
+        f.q_mul_dev = q_mul_dev;
+        f.o_mul_dev = o_mul_dev;
+        if (int rc = fa_plain_run(f, "cqkv_flash_attn", workspace, workspace_bytes, st)) return rc;
+        if (k_cache) {
+            // K / V are (batch, kv_len, kv_heads, D): the append kernel's (batch, head, token)
+            const int64_t ks[3] = {k_strides[0], k_strides[2], k_strides[1]};
+            const int64_t vs[3] = {v_strides[0], v_strides[2], v_strides[1]};
+            if (int rc = quant_append_launch(k_cache, k, dtype, ks, batch, kv_len, nullptr, position, st, 0))
+                return rc;
+            if (int rc = quant_append_launch(v_cache, v, dtype, vs, batch, kv_len, nullptr, position, st, 0))
+                return rc;
+        }
+        return CQKV_OK;
     }
     PrefillArgs a = {};
     a.q = (const uint16_t *)q;
@@ -893,9 +996,13 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
     a.o_mul_dev = o_mul_dev;
     // V^T scratch (stream-ordered: freed after the launches that use it)
     a.vt_len = (kv_len + kPfBK - 1) / kPfBK * kPfBK;
-    void *vt = nullptr;
-    const size_t vt_bytes = (size_t)batch * kv_heads * kPfD * a.vt_len * 2;
-    CQKV_HIP_CHECK(hipMallocAsync(&vt, vt_bytes, st));
+    void *vt = workspace;
+    const size_t vt_bytes = pf_vt_bytes(batch, kv_len, kv_heads);
+    if (workspace && workspace_bytes < vt_bytes)
+        return fail(CQKV_ERR_WORKSPACE, "cqkv_flash_attn: workspace %zu < %zu bytes",
+                    workspace_bytes, vt_bytes);
+    const bool vt_owned = workspace == nullptr;
+    if (vt_owned) CQKV_HIP_CHECK(hipMallocAsync(&vt, vt_bytes, st));
     a.vt = (const uint16_t *)vt;
     // an FP8 append runs inside the pre-pass when value tiles line up (position % 8 == 0) and
     // neither side rotates; any other append as two cqkv_quant_append launches after the attention
@@ -922,7 +1029,7 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
     else
         hipLaunchKernelGGL(prefill_kernel<false>, grid, dim3(kPfWaves * 64), 0, st, a);
     hipError_t le = hipGetLastError();
-    hipError_t fe = hipFreeAsync(vt, st);
+    hipError_t fe = vt_owned ? hipFreeAsync(vt, st) : hipSuccess;
     if (le != hipSuccess) return fail(CQKV_ERR_HIP, "cqkv_flash_attn: launch: %s", hipGetErrorString(le));
     CQKV_HIP_CHECK(fe);
     if (k_cache && !fused) {
@@ -939,35 +1046,45 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
 
 }  // namespace cqkv
 
+extern "C" size_t cqkv_flash_attn_workspace_bytes(int32_t dtype, int32_t batch, int32_t q_len,
+                                                  int32_t kv_len, int32_t q_heads,
+                                                  int32_t kv_heads, int32_t head_dim,
+                                                  int32_t varlen) {
+    return flash_attn_workspace(dtype, batch, q_len, kv_len, q_heads, kv_heads, head_dim,
+                                varlen != 0);
+}
+
 extern "C" int cqkv_flash_attn_ext(const void *q, const int64_t q_strides[3], const void *k,
                                    const int64_t k_strides[3], const void *v,
                                    const int64_t v_strides[3], void *out,
-                                   const int64_t out_strides[3], int32_t batch, int32_t q_len,
-                                   int32_t kv_len, int32_t q_heads, int32_t kv_heads,
-                                   int32_t head_dim, float softmax_scale, int32_t window_left,
-                                   int32_t window_right, float softcap, const float *alibi_slopes,
-                                   int32_t alibi_batch_stride, const int32_t *cu_seqlens_q,
-                                   const int32_t *cu_seqlens_k, int32_t total_q, int32_t total_k,
-                                   const cqkv_side *k_cache, const cqkv_side *v_cache,
-                                   int32_t position, cqkv_stream_t stream) {
+                                   const int64_t out_strides[3], int32_t dtype, int32_t batch,
+                                   int32_t q_len, int32_t kv_len, int32_t q_heads,
+                                   int32_t kv_heads, int32_t head_dim, float softmax_scale,
+                                   int32_t window_left, int32_t window_right, float softcap,
+                                   const float *alibi_slopes, int32_t alibi_batch_stride,
+                                   const int32_t *cu_seqlens_q, const int32_t *cu_seqlens_k,
+                                   int32_t total_q, int32_t total_k, const cqkv_side *k_cache,
+                                   const cqkv_side *v_cache, int32_t position, void *workspace,
+                                   size_t workspace_bytes, cqkv_stream_t stream) {
     clear_error();
-    return flash_attn_impl(q, q_strides, k, k_strides, v, v_strides, out, out_strides, batch,
-                           q_len, kv_len, q_heads, kv_heads, head_dim, softmax_scale, window_left,
-                           window_right, softcap, alibi_slopes, alibi_batch_stride, cu_seqlens_q,
-                           cu_seqlens_k, total_q, total_k, k_cache, v_cache, position, stream,
-                           1.0f, nullptr, 1.0f, nullptr);
+    return flash_attn_impl(q, q_strides, k, k_strides, v, v_strides, out, out_strides, dtype,
+                           batch, q_len, kv_len, q_heads, kv_heads, head_dim, softmax_scale,
+                           window_left, window_right, softcap, alibi_slopes, alibi_batch_stride,
+                           cu_seqlens_q, cu_seqlens_k, total_q, total_k, k_cache, v_cache,
+                           position, workspace, workspace_bytes, stream, 1.0f, nullptr, 1.0f,
+                           nullptr);
 }
 
 extern "C" int cqkv_flash_attn(const void *q, const int64_t q_strides[3], const void *k,
                                const int64_t k_strides[3], const void *v,
                                const int64_t v_strides[3], void *out,
-                               const int64_t out_strides[3], int32_t batch, int32_t q_len,
-                               int32_t kv_len, int32_t q_heads, int32_t kv_heads,
+                               const int64_t out_strides[3], int32_t dtype, int32_t batch,
+                               int32_t q_len, int32_t kv_len, int32_t q_heads, int32_t kv_heads,
                                int32_t head_dim, float softmax_scale, int32_t window_left,
                                int32_t window_right, const cqkv_side *k_cache,
                                const cqkv_side *v_cache, int32_t position, cqkv_stream_t stream) {
-    return cqkv_flash_attn_ext(q, q_strides, k, k_strides, v, v_strides, out, out_strides, batch,
-                               q_len, kv_len, q_heads, kv_heads, head_dim, softmax_scale,
+    return cqkv_flash_attn_ext(q, q_strides, k, k_strides, v, v_strides, out, out_strides, dtype,
+                               batch, q_len, kv_len, q_heads, kv_heads, head_dim, softmax_scale,
                                window_left, window_right, 0.0f, nullptr, 0, nullptr, nullptr, 0, 0,
-                               k_cache, v_cache, position, stream);
+                               k_cache, v_cache, position, nullptr, 0, stream);
 }

@@ -6,11 +6,11 @@
  * explicit sizes / strides and a hipStream_t (NULL = the legacy stream the reference launches on),
  * and returning CQKV_OK or a negative status; cqkv_last_error() gives the message of the last
  * failure of the calling thread. Device memory is allocated (stream-ordered, hipMallocAsync /
- * hipFreeAsync on the call's stream) only by: cqkv_decode_attention and
- * cqkv_decode_attention_paged when they are given no workspace; cqkv_flash_attn and
- * cqkv_flash_attn_ext (a transposed copy of the values, batch * kv_heads * padded kv_len * D
- * bf16); cqkv_flash_attn_fp8_codes (a per-plane staging buffer). cqkv_decode_attention_noalloc
- * allocates nothing. Nothing here holds torch or candle types.
+ * hipFreeAsync on the call's stream) only by: cqkv_decode_attention,
+ * cqkv_decode_attention_paged, cqkv_flash_attn_ext and cqkv_flash_attn_blocks when they are
+ * given no workspace (each has a *_workspace_bytes query); cqkv_flash_attn (its workspace);
+ * cqkv_flash_attn_fp8 (a bf16 staging copy of K / V). cqkv_decode_attention_noalloc allocates
+ * nothing. Nothing here holds torch or candle types.
  *
  * Reference interfaces replaced (paths relative to the reference repository root):
  *   cqkv_quant_append      RocmStorage::tq_quantize + Cache::append
@@ -233,20 +233,34 @@ int cqkv_decode_attention_paged(const void *q, int32_t q_dtype, const int64_t q_
                                 int32_t out_dtype, const int64_t out_strides[3], void *workspace,
                                 size_t workspace_bytes, cqkv_stream_t stream);
 
-/* Dense bf16 flash attention (FlashAttnOp / candle_flash_attn::flash_attn):
- *   q (batch, q_len, q_heads, D), k / v (batch, kv_len, kv_heads, D), out like q, all bf16 with
- *   element strides {batch, token, head} (D contiguous); bottom-right aligned windows;
- *   causal = window (-1, 0). When k_cache / v_cache are non-NULL (a key and a value side of any
- *   formats and rotations) the same call also quantizes and appends k / v at positions
- *   [position, position + kv_len) of the cache: inside the attention's pre-pass for unrotated
- *   FP8 sides at a position that is a multiple of 8, else as two cqkv_quant_append launches. */
+/* Dense flash attention (FlashAttnOp / candle_flash_attn::flash_attn):
+ *   q (batch, q_len, q_heads, D), k / v (batch, kv_len, kv_heads, D), out like q, all of
+ *   `dtype` (CQKV_BF16 or CQKV_F16), element strides {batch, token, head} (D contiguous);
+ *   head_dim any multiple of 8 up to 256 (the reference's FA_MAX_HEAD_DIM); any
+ *   q_heads % kv_heads == 0; bottom-right aligned windows; causal = window (-1, 0).
+ *   bf16 at head_dim 128 with more than 16 queries runs the MFMA prefill kernel; every other
+ *   call (f16, other head dims, decode-shaped calls of up to 16 queries) runs the plain-dtype
+ *   kernel: 16 (query, head) columns of a kv head per workgroup over split-K, the row kernels
+ *   fa_row_* / fa_rowg_* of the reference (candle-core/kernels/flash_attn_impl.h:49-328).
+ *   K / V of that kernel need 16-byte aligned rows (pointers and strides whole 8-element chunks).
+ *   When k_cache / v_cache are non-NULL (a key and a value side of any formats and rotations)
+ *   the same call also quantizes and appends k / v at positions [position, position + kv_len)
+ *   of the cache: inside the MFMA prefill's pre-pass for unrotated FP8 sides at a position that
+ *   is a multiple of 8, else as two cqkv_quant_append launches. Allocates its workspace. */
 int cqkv_flash_attn(const void *q, const int64_t q_strides[3], const void *k,
                     const int64_t k_strides[3], const void *v, const int64_t v_strides[3],
-                    void *out, const int64_t out_strides[3], int32_t batch, int32_t q_len,
-                    int32_t kv_len, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
-                    float softmax_scale, int32_t window_left, int32_t window_right,
-                    const cqkv_side *k_cache, const cqkv_side *v_cache, int32_t position,
-                    cqkv_stream_t stream);
+                    void *out, const int64_t out_strides[3], int32_t dtype, int32_t batch,
+                    int32_t q_len, int32_t kv_len, int32_t q_heads, int32_t kv_heads,
+                    int32_t head_dim, float softmax_scale, int32_t window_left,
+                    int32_t window_right, const cqkv_side *k_cache, const cqkv_side *v_cache,
+                    int32_t position, cqkv_stream_t stream);
+
+/* Device workspace cqkv_flash_attn_ext needs for a call of these sizes (varlen != 0: per-sequence
+ * lengths, q_len / kv_len their maxima): the MFMA prefill's V^T copy, or the plain kernel's split
+ * partials (0 when it does not split). */
+size_t cqkv_flash_attn_workspace_bytes(int32_t dtype, int32_t batch, int32_t q_len,
+                                       int32_t kv_len, int32_t q_heads, int32_t kv_heads,
+                                       int32_t head_dim, int32_t varlen);
 
 /* cqkv_flash_attn plus the reference's optional score terms and variable-length batches
  * (fa_logit, candle-core/kernels/flash_attn_impl.h:42-47; fa_tile_impl :330-443):
@@ -257,17 +271,49 @@ int cqkv_flash_attn(const void *q, const int64_t q_strides[3], const void *k,
  *     (total_q, q_heads, D) and k / v (total_k, kv_heads, D) with element strides
  *     {unused, token, head}; sequence b is rows cu[b] .. cu[b + 1] - 1; q_len / kv_len are the
  *     maximum sequence lengths. Offsets are clamped into the totals and lengths to the maxima.
- *     No fused cache append with variable-length batches.
+ *     No cache append with variable-length batches.
+ *   workspace: at least cqkv_flash_attn_workspace_bytes(); NULL = allocated (stream-ordered) and
+ *     freed by the call.
  * Soft-capping precedes ALiBi, and masked keys stay masked, as in the reference. */
 int cqkv_flash_attn_ext(const void *q, const int64_t q_strides[3], const void *k,
                         const int64_t k_strides[3], const void *v, const int64_t v_strides[3],
-                        void *out, const int64_t out_strides[3], int32_t batch, int32_t q_len,
-                        int32_t kv_len, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
-                        float softmax_scale, int32_t window_left, int32_t window_right,
-                        float softcap, const float *alibi_slopes, int32_t alibi_batch_stride,
-                        const int32_t *cu_seqlens_q, const int32_t *cu_seqlens_k,
-                        int32_t total_q, int32_t total_k, const cqkv_side *k_cache,
-                        const cqkv_side *v_cache, int32_t position, cqkv_stream_t stream);
+                        void *out, const int64_t out_strides[3], int32_t dtype, int32_t batch,
+                        int32_t q_len, int32_t kv_len, int32_t q_heads, int32_t kv_heads,
+                        int32_t head_dim, float softmax_scale, int32_t window_left,
+                        int32_t window_right, float softcap, const float *alibi_slopes,
+                        int32_t alibi_batch_stride, const int32_t *cu_seqlens_q,
+                        const int32_t *cu_seqlens_k, int32_t total_q, int32_t total_k,
+                        const cqkv_side *k_cache, const cqkv_side *v_cache, int32_t position,
+                        void *workspace, size_t workspace_bytes, cqkv_stream_t stream);
+
+/* One block of plain K / V for cqkv_flash_attn_blocks (the reference's KvBlockRef over dense
+ * tensors, candle-nn/src/flash_attn.rs:609-613): k / v of layout (batch, kv_heads, capacity, D)
+ * with element strides {batch, head, row} (D contiguous) and `rows` valid rows. */
+typedef struct cqkv_plain_block {
+    const void *k, *v;
+    int64_t k_strides[3], v_strides[3];
+    int32_t rows;
+    int32_t reserved;
+} cqkv_plain_block;
+
+/* flash_attn_blocks (candle-nn/src/flash_attn.rs:719-765, the paged row kernel fa_rowp_* of
+ * RocmStorage::flash_attn_paged): attention of q (batch, q_heads, q_len, D), element strides
+ * {batch, head, query}, over the concatenated valid rows of n_blocks blocks without copying them
+ * (any number of blocks; the reference's kernel takes at most 128 and concatenates beyond);
+ * every sequence sees all the rows; masks, soft-capping and ALiBi bottom-right aligned over
+ * them. q / K / V / out of `dtype` (bf16 or f16), K / V rows 16-byte aligned with one row stride
+ * per side across the blocks. out like q (strides {batch, head, query}). Errors as the
+ * reference's check_blocks (flash_attn.rs:650-686). */
+size_t cqkv_flash_attn_blocks_workspace_bytes(const cqkv_plain_block *blocks, int32_t n_blocks,
+                                              int32_t batch, int32_t q_heads, int32_t q_len,
+                                              int32_t kv_heads, int32_t head_dim);
+int cqkv_flash_attn_blocks(const void *q, const int64_t q_strides[3],
+                           const cqkv_plain_block *blocks, int32_t n_blocks, int32_t dtype,
+                           int32_t batch, int32_t q_heads, int32_t q_len, int32_t kv_heads,
+                           int32_t head_dim, float softmax_scale, int32_t window_left,
+                           int32_t window_right, float softcap, const float *alibi_slopes,
+                           int32_t alibi_batch_stride, void *out, const int64_t out_strides[3],
+                           void *workspace, size_t workspace_bytes, cqkv_stream_t stream);
 
 /* Per-tensor FP8 quantization (flash_attn_fp8, candle-nn/src/flash_attn.rs:882-887): over the n
  * elements of x (dtype CQKV_BF16 / F16 / F32, contiguous), amax = max |x|, scale = amax > 0 ?

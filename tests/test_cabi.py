@@ -127,14 +127,25 @@ def test_argument_errors_are_status_codes(cq):
 def test_flash_attn_ext_argument_errors(cq):
     """Soft-capping, ALiBi and variable-length arguments are checked before any launch."""
     L = cq.lib()
-    x = (ctypes.c_int64 * 3)(1, 128, 128)
-    one = ctypes.c_void_p(1)
+    x = (ctypes.c_int64 * 3)(8192, 256, 128)
+    one = ctypes.c_void_p(256)
 
     def call(softcap=0.0, alibi=None, alibi_bs=0, cu_q=None, cu_k=None, tq=0, tk=0, kc=None,
-             vc=None, hq=8, batch=2):
-        return L.cqkv_flash_attn_ext(one, x, one, x, one, x, one, x, batch, 16, 16, hq, 2, 128,
-                                     0.1, -1, 0, softcap, alibi, alibi_bs, cu_q, cu_k, tq, tk,
-                                     kc, vc, 0, None)
+             vc=None, hq=8, batch=2, dtype=0, d=128, kp=one, ks=x, ql=16):
+        return L.cqkv_flash_attn_ext(one, x, kp, ks, one, x, one, x, dtype, batch, ql, 16, hq, 2,
+                                     d, 0.1, -1, 0, softcap, alibi, alibi_bs, cu_q, cu_k, tq, tk,
+                                     kc, vc, 0, None, 0, None)
+    # K / V rows must be 16-byte aligned (the kernels' 16-byte row loads), dtypes bf16 / f16,
+    # head dims multiples of 8 up to 256
+    assert call(kp=ctypes.c_void_p(258)) == cq.ERR_ARG
+    assert b"16-byte aligned" in L.cqkv_last_error()
+    assert call(ks=(ctypes.c_int64 * 3)(8192, 260, 128)) == cq.ERR_ARG
+    assert call(ks=(ctypes.c_int64 * 3)(8192, 260, 128), ql=64) == cq.ERR_ARG
+    assert call(dtype=2) == cq.ERR_ARG
+    assert b"dtype" in L.cqkv_last_error()
+    assert call(d=100) == cq.ERR_ARG
+    assert call(d=264) == cq.ERR_ARG
+    assert b"head_dim" in L.cqkv_last_error()
     assert call(softcap=-1.0) == cq.ERR_ARG
     assert b"softcap" in L.cqkv_last_error()
     assert call(softcap=float("nan")) == cq.ERR_ARG
@@ -149,6 +160,12 @@ def test_flash_attn_ext_argument_errors(cq):
     assert call(cu_q=one, cu_k=one, tq=5, tk=5, kc=ctypes.byref(side),
                 vc=ctypes.byref(vside)) == cq.ERR_ARG
     assert b"dense batches only" in L.cqkv_last_error()
+    # the workspace query: the MFMA prefill's V^T copy (bf16, head dim 128, > 16 queries) or the
+    # plain kernel's split partials
+    vt = L.cqkv_flash_attn_workspace_bytes(0, 2, 4096, 4096, 32, 8, 128, 0)
+    assert vt >= 2 * 8 * 128 * 4096 * 2
+    assert L.cqkv_flash_attn_workspace_bytes(1, 2, 1, 8192, 32, 8, 128, 0) > 0  # f16 decode splits
+    assert L.cqkv_flash_attn_workspace_bytes(0, 2, 4096, 4096, 32, 7, 128, 0) == 0
 
 
 def test_paged_argument_errors_and_workspace(cq):
@@ -293,3 +310,41 @@ def test_grown_capacity_follows_cache_append(cq):
     assert cq.grown_capacity(64, 100, 65) == 192     # 64 + 100 = 164 -> 192
     assert cq.grown_capacity(32, 8, 100) == 128      # 32 -> 48 -> 72 -> 108 -> 128
     assert cq.grown_capacity(0, 0, 1) == 32          # max(.., 1) makes progress
+
+
+def test_flash_attn_blocks_argument_errors(cq):
+    """cqkv_flash_attn_blocks checks its blocks like the reference's check_blocks
+    (candle-nn/src/flash_attn.rs:650-686) before any launch."""
+    L = cq.lib()
+    qs = (ctypes.c_int64 * 3)(8 * 4 * 128, 4 * 128, 128)
+    one = ctypes.c_void_p(256)
+
+    def blk(rows=10, k=256, kr=128, vr=128):
+        b = cq.PlainBlock()
+        b.k, b.v, b.rows = k, 256, rows
+        b.k_strides[:] = [2 * 64 * kr, 64 * kr, kr]
+        b.v_strides[:] = [2 * 64 * vr, 64 * vr, vr]
+        return b
+
+    def call(*bl, dtype=0, d=128, softcap=0.0, hq=8):
+        arr = (cq.PlainBlock * max(len(bl), 1))(*bl)
+        return L.cqkv_flash_attn_blocks(one, qs, arr, len(bl), dtype, 1, hq, 1, 2, d, 0.1, -1, 0,
+                                        softcap, None, 0, one, qs, None, 0, None)
+    assert call() == cq.ERR_ARG
+    assert b"no blocks" in L.cqkv_last_error()
+    assert call(blk(rows=0), blk(rows=0)) == cq.ERR_ARG
+    assert b"no keys" in L.cqkv_last_error()
+    assert call(blk(rows=-1)) == cq.ERR_ARG
+    assert call(blk(), blk(kr=136)) == cq.ERR_ARG
+    assert b"row strides" in L.cqkv_last_error()
+    assert call(blk(k=264)) == cq.ERR_ARG
+    assert b"aligned" in L.cqkv_last_error()
+    assert call(blk(), dtype=2) == cq.ERR_ARG
+    assert call(blk(), d=300) == cq.ERR_ARG
+    assert call(blk(), softcap=-1.0) == cq.ERR_ARG
+    assert call(blk(), hq=5) == cq.ERR_ARG
+    # workspace: the segment table, plus partials once the keys are split
+    arr = (cq.PlainBlock * 1)(blk(rows=10))
+    small = L.cqkv_flash_attn_blocks_workspace_bytes(arr, 1, 1, 8, 1, 2, 128)
+    arr2 = (cq.PlainBlock * 2)(blk(rows=64), blk(rows=64))
+    assert 0 < small < L.cqkv_flash_attn_blocks_workspace_bytes(arr2, 2, 1, 8, 1, 2, 128)
