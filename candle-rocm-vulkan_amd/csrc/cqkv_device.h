@@ -66,9 +66,11 @@ __device__ inline uint32_t pack_bf16x2(float lo, float hi) {
     v.y = (__bf16)hi;
     return __builtin_bit_cast(uint32_t, v);
 }
+// f32 pair -> f16 pair, round to nearest even (one v_cvt_pk_f16_f32)
 __device__ inline uint32_t pack_f16x2(float lo, float hi) {
-    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 v = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, v);
 }
 
 // Element dtype of q / k / v / out: 0 bf16, 1 f16, 2 f32 (the CQKV_* ids of cqkv.h).

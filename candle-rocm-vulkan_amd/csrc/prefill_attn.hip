@@ -29,6 +29,7 @@
 //    wavefronts of each SIMD fill each other's stalls.
 //  * Causal work is uneven: the workgroups with the most key tiles are dispatched first.
 #include <algorithm>
+#include <type_traits>
 
 #include "cqkv_device.h"
 #include "cqkv_host.h"
@@ -111,6 +112,12 @@ __device__ inline PfSeq pf_sequence(const PrefillArgs &a, int b) {
 __device__ inline f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
+__device__ inline f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+// MFMA operands of the input dtype: q, K, V^T and P all in bf16, or all in f16
+template <bool F16>
+using pf_op_t = typename std::conditional<F16, f16x8, bf16x8>::type;
 
 __device__ inline u32x4 ldg128(const uint16_t *p) { return *(const u32x4 *)p; }
 
@@ -197,7 +204,7 @@ constexpr int kPfCopiesPerTile = 4;  // global_load_lds per wavefront per tile
 #define PF_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | 0x0f70)
 
 struct PfState {
-    bf16x8 qop[8];   // Q^T operands (16-dim steps ks) of this wavefront's 32 queries
+    u32x4 qop[8];    // Q^T operands (16-dim steps ks) of this wavefront's 32 queries, raw bits
     f32x16 acc[4];   // O^T: 32-dim block md
     float negm;      // -m_run (0 before the first key), added to the raw scores
     float m_run, l_run;
@@ -252,19 +259,22 @@ PF_INLINE void pf_addr_opaque(PfAddr &ad) {
 }
 
 // S^T (64 keys x 32 queries) = K Q^T for the tile at k_lds, key block 0 first.
+template <bool F16>
 PF_INLINE void pf_qk(f32x16 (&s)[2], const PfState &st, const uint8_t *k_lds, const PfAddr &ad) {
-    bf16x8 kop[16];
+    using op_t = pf_op_t<F16>;
+    op_t kop[16];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks)
             kop[8 * mb + ks] = __builtin_bit_cast(
-                bf16x8, *(const u32x4 *)(k_lds + ad.k[ks] + 32 * mb * kPfRow));
+                op_t, *(const u32x4 *)(k_lds + ad.k[ks] + 32 * mb * kPfRow));
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
-        s[mb] = mfma32x32x16(kop[8 * mb], st.qop[0], f32x16{});
+        s[mb] = mfma32x32x16(kop[8 * mb], __builtin_bit_cast(op_t, st.qop[0]), f32x16{});
 #pragma unroll
-        for (int ks = 1; ks < 8; ++ks) s[mb] = mfma32x32x16(kop[8 * mb + ks], st.qop[ks], s[mb]);
+        for (int ks = 1; ks < 8; ++ks)
+            s[mb] = mfma32x32x16(kop[8 * mb + ks], __builtin_bit_cast(op_t, st.qop[ks]), s[mb]);
     }
 }
 
@@ -365,8 +375,9 @@ PF_INLINE void pf_rescale(f32x16 (&s)[2], PfState &st, float mx, bool need) {
     st.negm -= shift;  // -m_new: 0 - mx for a row's first keys, -m_run - mx after
 }
 
-// p = exp2(s), packed to the bf16 P^T operands
-PF_INLINE void pf_exp(bf16x8 (&pop)[4], const f32x16 (&s)[2]) {
+// p = exp2(s), packed to the P^T operands of the dtype (raw bits)
+template <bool F16>
+PF_INLINE void pf_exp(u32x4 (&pop)[4], const f32x16 (&s)[2]) {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
@@ -376,30 +387,42 @@ PF_INLINE void pf_exp(bf16x8 (&pop)[4], const f32x16 (&s)[2]) {
             for (int e = 0; e < 4; ++e) {
                 const float p0 = __builtin_amdgcn_exp2f(s[mb][8 * half + 2 * e]);
                 const float p1 = __builtin_amdgcn_exp2f(s[mb][8 * half + 2 * e + 1]);
-                const bf16x2 pp = {(__bf16)p0, (__bf16)p1};
-                w[e] = __builtin_bit_cast(uint32_t, pp);
+                if constexpr (F16) {
+                    w[e] = pack_f16x2(p0, p1);
+                } else {
+                    const bf16x2 pp = {(__bf16)p0, (__bf16)p1};
+                    w[e] = __builtin_bit_cast(uint32_t, pp);
+                }
             }
-            pop[2 * mb + half] = __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
+            pop[2 * mb + half] = u32x4{w[0], w[1], w[2], w[3]};
         }
 }
 
 // the row sum adds the bf16 values the product uses, two per dot2 instruction, in two chains
 // (each word goes through a scalar: clang's __builtin_bit_cast of a vector element reads
 // element 0)
+template <bool F16>
 PF_INLINE float pf_dot2_ones(uint32_t w, float acc) {
-    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), ones, acc, false);
+    if constexpr (F16) {
+        typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+        const f16x2_t ones = {(_Float16)1.0f, (_Float16)1.0f};
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w), ones, acc, false);
+    } else {
+        const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), ones, acc, false);
+    }
 }
-PF_INLINE void pf_psum(PfState &st, const bf16x8 (&pop)[4]) {
+template <bool F16>
+PF_INLINE void pf_psum(PfState &st, const u32x4 (&pop)[4]) {
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const u32x4 w = __builtin_bit_cast(u32x4, pop[i]);
+        const u32x4 w = pop[i];
         const uint32_t w0 = w.x, w1 = w.y, w2 = w.z, w3 = w.w;
-        a0 = pf_dot2_ones(w0, a0);
-        a1 = pf_dot2_ones(w1, a1);
-        a0 = pf_dot2_ones(w2, a0);
-        a1 = pf_dot2_ones(w3, a1);
+        a0 = pf_dot2_ones<F16>(w0, a0);
+        a1 = pf_dot2_ones<F16>(w1, a1);
+        a0 = pf_dot2_ones<F16>(w2, a0);
+        a1 = pf_dot2_ones<F16>(w3, a1);
     }
     st.l_run += a0 + a1;
 }
@@ -408,18 +431,21 @@ PF_INLINE void pf_psum(PfState &st, const bf16x8 (&pop)[4]) {
 // operand holds S^T registers 8 (kk % 2) .. +7 of key block kk / 2, i.e. lane half h holds keys
 // 16 kk + 8 (e / 4) + 4 h + e % 4 in k-slot 8 h + e; the pre-pass stores V^T keys in that order
 // (bits 2 and 3 of the key swapped), so the A operand of lane (d, h) is chunk 2 kk + h of row d.
-PF_INLINE void pf_pv(PfState &st, const bf16x8 (&pop)[4], const uint8_t *v_lds, const PfAddr &ad) {
-    bf16x8 vt[16];
+template <bool F16>
+PF_INLINE void pf_pv(PfState &st, const u32x4 (&pop)[4], const uint8_t *v_lds, const PfAddr &ad) {
+    using op_t = pf_op_t<F16>;
+    op_t vt[16];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
         for (int md = 0; md < 4; ++md)
             vt[4 * kk + md] =
-                __builtin_bit_cast(bf16x8, *(const u32x4 *)(v_lds + (ad.v[kk] - kPfVBias) + md * 32 * kPfVtRow));
+                __builtin_bit_cast(op_t, *(const u32x4 *)(v_lds + (ad.v[kk] - kPfVBias) + md * 32 * kPfVtRow));
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-        for (int md = 0; md < 4; ++md) st.acc[md] = mfma32x32x16(vt[4 * kk + md], pop[kk], st.acc[md]);
+        for (int md = 0; md < 4; ++md)
+            st.acc[md] = mfma32x32x16(vt[4 * kk + md], __builtin_bit_cast(op_t, pop[kk]), st.acc[md]);
 }
 
 // One key tile t of a wavefront (not the last), with S(t) in `cur`:
@@ -430,12 +456,12 @@ PF_INLINE void pf_pv(PfState &st, const bf16x8 (&pop)[4], const uint8_t *v_lds, 
 //    shifts S(t + 1) by -m_run and takes its row maximum; the copies of a later tile
 //    (issue_copies) are issued among its first MFMAs;
 //  * then, rarely, the row maximum moves (pf_rescale).
-template <bool LOGIT, typename IssueCopies>
-PF_INLINE void pf_tile(f32x16 (&cur)[2], f32x16 (&nxt)[2], bf16x8 (&pop)[4], PfState &st,
+template <bool LOGIT, bool F16, typename IssueCopies>
+PF_INLINE void pf_tile(f32x16 (&cur)[2], f32x16 (&nxt)[2], u32x4 (&pop)[4], PfState &st,
                        const uint8_t *k_next, const uint8_t *v_cur, const PfAddr &ad,
                        bool masked, int k1, int lane, const PfLogit &lg, IssueCopies &&issue_copies) {
-    pf_qk(nxt, st, k_next, ad);
-    pf_exp(pop, cur);
+    pf_qk<F16>(nxt, st, k_next, ad);
+    pf_exp<F16>(pop, cur);
     pf_block_schedule<3>();
     __builtin_amdgcn_sched_barrier(0);
     // P(t) is used only after the branch below: pin its computation to block 1
@@ -444,8 +470,8 @@ PF_INLINE void pf_tile(f32x16 (&cur)[2], f32x16 (&nxt)[2], bf16x8 (&pop)[4], PfS
     if (LOGIT) pf_logit(nxt, lg, k1, lane);
     if (masked) pf_mask(nxt, st, k1, lane);
     issue_copies();
-    pf_pv(st, pop, v_cur, ad);
-    pf_psum(st, pop);
+    pf_pv<F16>(st, pop, v_cur, ad);
+    pf_psum<F16>(st, pop);
     pf_shift(nxt, st.negm);
     float mx = pf_rowmax(nxt);
     pf_block_schedule<4, 4>();
@@ -456,17 +482,18 @@ PF_INLINE void pf_tile(f32x16 (&cur)[2], f32x16 (&nxt)[2], bf16x8 (&pop)[4], PfS
 }
 
 // The last key tile: P(t) and O += V(t)^T P(t).
-PF_INLINE void pf_last_tile(const f32x16 (&cur)[2], bf16x8 (&pop)[4], PfState &st,
+template <bool F16>
+PF_INLINE void pf_last_tile(const f32x16 (&cur)[2], u32x4 (&pop)[4], PfState &st,
                             const uint8_t *v_cur, const PfAddr &ad) {
-    pf_exp(pop, cur);
-    pf_pv(st, pop, v_cur, ad);
-    pf_psum(st, pop);
+    pf_exp<F16>(pop, cur);
+    pf_pv<F16>(st, pop, v_cur, ad);
+    pf_psum<F16>(st, pop);
     pf_block_schedule<1>();
 }
 
 // Two wavefronts per SIMD (8 per workgroup, ~240 registers each).
 // LOGIT: soft-capping and / or ALiBi (a separate instantiation keeps them off the plain path)
-template <bool LOGIT>
+template <bool LOGIT, bool F16>
 __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a) {
     // the K and V^T rings: four stages each, as distinct arrays named statically below, so the
     // compiler can tell the asynchronous copy into one stage from the reads of another (a
@@ -520,12 +547,17 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
             u32x4 w = ok ? ldg128(row + 16 * ks + 8 * h) : u32x4{0u, 0u, 0u, 0u};
-            // q * scale * log2(e) (* k_descale), rounded to bf16
+            // q * scale * log2(e) (* k_descale), rounded to the dtype
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                w[e] = pack_bf16x2(__uint_as_float(w[e] << 16) * qs,
-                                   __uint_as_float(w[e] & 0xffff0000u) * qs);
-            st.qop[ks] = __builtin_bit_cast(bf16x8, w);
+            for (int e = 0; e < 4; ++e) {
+                if constexpr (F16)
+                    w[e] = pack_f16x2(f16_bits_to_f32(w[e] & 0xffffu) * qs,
+                                      f16_bits_to_f32(w[e] >> 16) * qs);
+                else
+                    w[e] = pack_bf16x2(__uint_as_float(w[e] << 16) * qs,
+                                       __uint_as_float(w[e] & 0xffff0000u) * qs);
+            }
+            st.qop[ks] = w;
         }
         if (qi < lq) pf_key_range(qi, lq, lk, a.wl, a.wr, st.qlo, st.qhi);
         else st.qlo = st.qhi = 0;
@@ -592,11 +624,11 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
         return !(k0 >= lo_last && k0 + kPfBK <= hi_first);
     };
     f32x16 sa[2], sb[2];
-    bf16x8 pop[4];
+    u32x4 pop[4];
     PfAddr ad;
     pf_addr_init(ad, lane);
     if (ntiles > 0) {
-        pf_qk(sa, st, ks0, ad);
+        pf_qk<F16>(sa, st, ks0, ad);
         if (LOGIT) pf_logit(sa, lg, kt_begin * kPfBK, lane);
         pf_shift(sa, st.negm);
         if (tile_masked(0)) pf_mask(sa, st, kt_begin * kPfBK, lane);
@@ -615,7 +647,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
             last = k;                                                                        \
             break;                                                                           \
         }                                                                                    \
-        pf_tile<LOGIT>(CUR, NXT, pop, st, PF_KS(((k) + 1) & 3), PF_VS(k), ad,                \
+        pf_tile<LOGIT, F16>(CUR, NXT, pop, st, PF_KS(((k) + 1) & 3), PF_VS(k), ad,           \
                        tile_masked(t + 1), (kt_begin + t + 1) * kPfBK, lane, lg, [&] {       \
                     PF_ISSUE(((k) + 3) & 3, t + 3);                                          \
                 });                                                                          \
@@ -632,10 +664,10 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
         PF_WAIT_VMCNT(0);  // the dummy copies past the end
         pf_addr_opaque(ad);
         switch (last) {
-            case 0: pf_last_tile(sa, pop, st, vs0, ad); break;
-            case 1: pf_last_tile(sb, pop, st, vs1, ad); break;
-            case 2: pf_last_tile(sa, pop, st, vs2, ad); break;
-            default: pf_last_tile(sb, pop, st, vs3, ad); break;
+            case 0: pf_last_tile<F16>(sa, pop, st, vs0, ad); break;
+            case 1: pf_last_tile<F16>(sb, pop, st, vs1, ad); break;
+            case 2: pf_last_tile<F16>(sa, pop, st, vs2, ad); break;
+            default: pf_last_tile<F16>(sb, pop, st, vs3, ad); break;
         }
     }
 #undef PF_STEP
@@ -656,8 +688,13 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             u32x2 w;
-            w.x = pack_bf16x2(st.acc[md][4 * j + 0] * inv, st.acc[md][4 * j + 1] * inv);
-            w.y = pack_bf16x2(st.acc[md][4 * j + 2] * inv, st.acc[md][4 * j + 3] * inv);
+            if constexpr (F16) {
+                w.x = pack_f16x2(st.acc[md][4 * j + 0] * inv, st.acc[md][4 * j + 1] * inv);
+                w.y = pack_f16x2(st.acc[md][4 * j + 2] * inv, st.acc[md][4 * j + 3] * inv);
+            } else {
+                w.x = pack_bf16x2(st.acc[md][4 * j + 0] * inv, st.acc[md][4 * j + 1] * inv);
+                w.y = pack_bf16x2(st.acc[md][4 * j + 2] * inv, st.acc[md][4 * j + 3] * inv);
+            }
             *(u32x2 *)(orow + 32 * md + 8 * j + 4 * h) = w;
         }
 }
@@ -812,7 +849,7 @@ namespace cqkv {
 // Whether a call takes the MFMA prefill kernel (bf16, head dim 128, more than 16 queries);
 // every other call runs the plain-dtype kernel of flash_plain.h.
 static bool pf_fast_path(int32_t dtype, int32_t head_dim, int32_t q_len) {
-    return dtype == CQKV_BF16 && head_dim == kPfD && q_len > 16;
+    return (dtype == CQKV_BF16 || dtype == CQKV_F16) && head_dim == kPfD && q_len > 16;
 }
 
 // V^T scratch of the MFMA prefill: (batch, kv heads, D, kv_len rounded up to the key tile) bf16.
@@ -1006,7 +1043,8 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
     a.vt = (const uint16_t *)vt;
     // an FP8 append runs inside the pre-pass when value tiles line up (position % 8 == 0) and
     // neither side rotates; any other append as two cqkv_quant_append launches after the attention
-    const bool fused = k_cache != nullptr && position % 8 == 0 && k_cache->format == CQKV_FMT_FP8 &&
+    const bool fused = k_cache != nullptr && dtype == CQKV_BF16 && position % 8 == 0 &&
+                       k_cache->format == CQKV_FMT_FP8 &&
                        v_cache->format == CQKV_FMT_FP8 && !side_rotates(k_cache) &&
                        !side_rotates(v_cache);
     if (fused) {
@@ -1024,10 +1062,14 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
     hipLaunchKernelGGL(prefill_stage_kernel, dim3(a.vt_len / kPfBK, kv_heads, batch), dim3(256),
                        0, st, a);
     const dim3 grid(a.q_blocks * kv_heads * ((a.group + a.heads_per_wg - 1) / a.heads_per_wg) * batch);
-    if (softcap > 0.0f || alibi_slopes)
-        hipLaunchKernelGGL(prefill_kernel<true>, grid, dim3(kPfWaves * 64), 0, st, a);
-    else
-        hipLaunchKernelGGL(prefill_kernel<false>, grid, dim3(kPfWaves * 64), 0, st, a);
+    const bool terms = softcap > 0.0f || alibi_slopes;
+    if (dtype == CQKV_F16) {
+        if (terms) hipLaunchKernelGGL((prefill_kernel<true, true>), grid, dim3(kPfWaves * 64), 0, st, a);
+        else hipLaunchKernelGGL((prefill_kernel<false, true>), grid, dim3(kPfWaves * 64), 0, st, a);
+    } else {
+        if (terms) hipLaunchKernelGGL((prefill_kernel<true, false>), grid, dim3(kPfWaves * 64), 0, st, a);
+        else hipLaunchKernelGGL((prefill_kernel<false, false>), grid, dim3(kPfWaves * 64), 0, st, a);
+    }
     hipError_t le = hipGetLastError();
     hipError_t fe = vt_owned ? hipFreeAsync(vt, st) : hipSuccess;
     if (le != hipSuccess) return fail(CQKV_ERR_HIP, "cqkv_flash_attn: launch: %s", hipGetErrorString(le));
@@ -1036,9 +1078,9 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
         // K / V are (batch, kv_len, kv_heads, D): the append kernel's (batch, head, token)
         const int64_t ks[3] = {k_strides[0], k_strides[2], k_strides[1]};
         const int64_t vs[3] = {v_strides[0], v_strides[2], v_strides[1]};
-        if (int rc = quant_append_launch(k_cache, k, CQKV_BF16, ks, batch, kv_len, nullptr, position, st, 0))
+        if (int rc = quant_append_launch(k_cache, k, dtype, ks, batch, kv_len, nullptr, position, st, 0))
             return rc;
-        if (int rc = quant_append_launch(v_cache, v, CQKV_BF16, vs, batch, kv_len, nullptr, position, st, 0))
+        if (int rc = quant_append_launch(v_cache, v, dtype, vs, batch, kv_len, nullptr, position, st, 0))
             return rc;
     }
     return CQKV_OK;
