@@ -164,8 +164,9 @@ __device__ inline float fa_logit2(float x, float cap2, float slope2, int dist) {
     return x;
 }
 
-// One 32-key tile of a wavefront: S^T, online softmax, O^T += V^T P^T.
-template <bool F16, int D>
+// One 32-key tile of a wavefront: S^T, online softmax, O^T += V^T P^T (PLO: P as a hi + lo
+// pair, else one operand of the dtype as the MFMA prefill does).
+template <bool F16, int D, bool PLO = true>
 __device__ inline void fa_tile(const uint8_t *kst, const uint8_t *vst, const fa_op_t<F16> *qop,
                                int t, int lane, int lo, int hi, int lo_max, int hi_min, int L,
                                int koff, float scale_log2, float cap2, float slope2, int pos,
@@ -224,6 +225,12 @@ __device__ inline void fa_tile(const uint8_t *kst, const uint8_t *vst, const fa_
     }
     op_t phi, plo;
     split8(p, phi, plo);
+    if constexpr (!PLO) {  // the row sum of the P the product uses
+        float r = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r += (float)phi[e];
+        l_run += r - psum;
+    }
     // V^T operands: lane (16-lane group g, index 4 pp + qq) points at key row 4 g + pp (then
     // 16 + 4 g + pp), head dims 16 u + 4 qq .. +3; lane i of the group receives those four keys
     // of head dim 16 u + i: k-slots 8 g .. 8 g + 3 and 8 g + 4 .. 8 g + 7, the keys of p[].
@@ -239,7 +246,7 @@ __device__ inline void fa_tile(const uint8_t *kst, const uint8_t *vst, const fa_
         const u32x2 w0 = __builtin_bit_cast(u32x2, a0), w1 = __builtin_bit_cast(u32x2, a1);
         const op_t va = __builtin_bit_cast(op_t, u32x4{w0.x, w0.y, w1.x, w1.y});
         acc[u] = mfma16x16x32(va, phi, acc[u]);
-        acc[u] = mfma16x16x32(va, plo, acc[u]);
+        if constexpr (PLO) acc[u] = mfma16x16x32(va, plo, acc[u]);
     }
 }
 
@@ -401,6 +408,190 @@ __global__ __launch_bounds__(W * 64) void fa_row_kernel(FaArgs a) {
             store_elem(a.out, sq.o0 + (int64_t)qc * a.o_st + (int64_t)hc * a.o_sh + d, a.dtype,
                        o * o_mul);
         }
+    }
+}
+
+// This wavefront's share of the copies of tile t (K and V) into a stage of the shared ring:
+// the 1 KB pieces wave, wave + 4, ... of each side; a tile past te copies nothing.
+template <int D, int NCPW>
+__device__ inline void fa_issue_shared(uint8_t *stage, int t, int te, const uint16_t *kplane,
+                                       const uint16_t *vplane, int64_t k_st, int64_t v_st, int L,
+                                       int head_dim, int wave, const uint32_t *koffs,
+                                       const uint32_t *voffs) {
+    using G = FaTileGeom<D>;
+    const bool valid = t < te;
+    const int row0 = valid ? t * 32 : 0;
+    const int nvalid = valid ? min(32, L - row0) : 0;
+#pragma unroll
+    for (int side = 0; side < 2; ++side) {
+        const uint16_t *plane = side ? vplane : kplane;
+        const int64_t rs = side ? v_st : k_st;
+        const uint64_t p = (uint64_t)(plane + (int64_t)row0 * rs);
+        const uint32_t plo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+        const uint32_t phi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+        const uint32_t bytes =
+            nvalid > 0 ? (uint32_t)((int64_t)(nvalid - 1) * rs * 2 + 2 * head_dim) : 0u;
+        const rsrc_t r = make_rsrc((const void *)(((uint64_t)phi << 32) | plo),
+                                   __builtin_amdgcn_readfirstlane(bytes));
+#pragma unroll
+        for (int j = 0; j < NCPW; ++j)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                r, (fa_lds_void *)(stage + side * G::TILE + 1024 * (wave + 4 * j)), 16,
+                side ? voffs[j] : koffs[j], 0, 0, 0);
+    }
+}
+
+// Prefill-shaped calls: one workgroup = 4 wavefronts on 4 consecutive 16-column blocks (64
+// columns of a kv head) over one split of the keys. The wavefronts share every K / V tile: each
+// issues a quarter of a tile's copies into a three-stage LDS ring, one barrier per tile, and
+// computes its own columns; no merge across wavefronts.
+template <bool F16, int D>
+__global__ __launch_bounds__(256) void fa_tile_kernel(FaArgs a) {
+    using op_t = fa_op_t<F16>;
+    using G = FaTileGeom<D>;
+    constexpr int NJ = D / 32, NU = D / 16, W = 4, NCPW = G::NCP / W;
+    static_assert(G::NCP % W == 0, "copies per wavefront");
+    __shared__ __attribute__((aligned(1024))) uint8_t st0[2 * G::TILE];
+    __shared__ __attribute__((aligned(1024))) uint8_t st1[2 * G::TILE];
+    __shared__ __attribute__((aligned(1024))) uint8_t st2[2 * G::TILE];
+
+    const int planes = a.batch * a.kv_heads;
+    const int rest = (int)blockIdx.x / planes, plane_id = (int)blockIdx.x % planes;
+    const int split = rest / a.col_blocks, cgrp = rest % a.col_blocks;
+    const int b = plane_id / a.kv_heads, hk = plane_id % a.kv_heads;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 15, g = lane >> 4;
+    const FaSeq sq = fa_sequence(a, b);
+    const int ncols = sq.lq * a.group, g0 = 64 * cgrp;
+    if (g0 >= ncols) return;  // the whole workgroup
+    const int c0 = g0 + 16 * wave;
+    const bool wave_live = c0 < ncols;
+    const int ncb = wave_live ? min(16, ncols - c0) : 0;
+    const bool col_ok = n < ncb;
+    const int col = col_ok ? c0 + n : g0;
+    const int qi = col / a.group, head = hk * a.group + col % a.group;
+    int lo, hi, lo_min, hi_min, lo_max, hi_max, wlo, whi;
+    fa_key_range(qi, sq.lq, sq.lk, a.wl, a.wr, lo, hi);
+    if (!col_ok) lo = hi = 0;
+    // the workgroup's keys: its first and last columns; the `full` bounds: this wavefront's
+    fa_key_range(g0 / a.group, sq.lq, sq.lk, a.wl, a.wr, lo_min, hi_min);
+    fa_key_range((min(g0 + 64, ncols) - 1) / a.group, sq.lq, sq.lk, a.wl, a.wr, lo_max, hi_max);
+    int wlo_max = 0, whi_min = 0;
+    if (wave_live) {
+        fa_key_range(c0 / a.group, sq.lq, sq.lk, a.wl, a.wr, wlo, whi_min);
+        fa_key_range((c0 + ncb - 1) / a.group, sq.lq, sq.lk, a.wl, a.wr, wlo_max, whi);
+    }
+    const uint16_t *kplane = a.k + sq.k0 + (int64_t)hk * a.k_sh;
+    const uint16_t *vplane = a.v + sq.v0 + (int64_t)hk * a.v_sh;
+    const int Lb = sq.lk;
+    const int tb = max(split * a.tiles_per_split, lo_min / 32);
+    const int te = min((split + 1) * a.tiles_per_split, (hi_max + 31) / 32);
+
+    op_t qop[NJ];
+    {
+        const uint16_t *qrow = a.q + sq.q0 + (int64_t)qi * a.q_st + (int64_t)head * a.q_sh;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int d0 = 32 * j + 8 * g;
+            u32x4 w = {0u, 0u, 0u, 0u};
+            if (col_ok && d0 < a.head_dim) {
+                if (a.q_vec) {
+                    w = *(const u32x4 *)(qrow + d0);
+                } else {
+                    uint32_t *wp = (uint32_t *)&w;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        wp[e] = (uint32_t)qrow[d0 + 2 * e] | ((uint32_t)qrow[d0 + 2 * e + 1] << 16);
+                }
+            }
+            qop[j] = __builtin_bit_cast(op_t, w);
+        }
+    }
+    float scale_log2 = a.scale_log2;
+    if (a.q_mul_dev) scale_log2 *= *a.q_mul_dev;
+    const float slope2 = a.alibi ? a.alibi[b * a.alibi_bs + head] * kLog2e : 0.0f;
+    const int pos = qi + sq.lk - sq.lq;
+
+    // this wavefront's copies of a tile: 1 KB pieces wave, wave + 4, ... of the K and the V tile
+    uint32_t koffs[NCPW], voffs[NCPW];
+    {
+        uint32_t ka[G::NCP], va[G::NCP];
+        fa_copy_offsets<D>(ka, a.k_st, a.head_dim, lane);
+        fa_copy_offsets<D>(va, a.v_st, a.head_dim, lane);
+#pragma unroll
+        for (int j = 0; j < NCPW; ++j) {
+            // wave is uniform: select with a switch-free expression on the unrolled copies
+            uint32_t kk = ka[0], vv = va[0];
+#pragma unroll
+            for (int i = 0; i < G::NCP; ++i)
+                if (i == wave + W * j) {
+                    kk = ka[i];
+                    vv = va[i];
+                }
+            koffs[j] = kk;
+            voffs[j] = vv;
+        }
+    }
+    f32x4 acc[NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -__builtin_inff(), l_run = 0.0f;
+
+    fa_issue_shared<D, NCPW>(st0, tb, te, kplane, vplane, a.k_st, a.v_st, Lb, a.head_dim, wave,
+                             koffs, voffs);
+    fa_issue_shared<D, NCPW>(st1, tb + 1, te, kplane, vplane, a.k_st, a.v_st, Lb, a.head_dim,
+                             wave, koffs, voffs);
+    // step t: stage t % 3 holds tile t; after the barrier every copy of tile t has landed and
+    // every wavefront is done with tile t - 1, whose stage takes tile t + 2
+#define FA_TSTEP(CUR, NEXT2)                                                                    \
+    {                                                                                          \
+        if (t >= te) break;                                                                    \
+        FA_WAIT_VMCNT(2 * NCPW);                                                               \
+        __syncthreads();                                                                       \
+        fa_issue_shared<D, NCPW>(NEXT2, t + 2, te, kplane, vplane, a.k_st, a.v_st, Lb,          \
+                                 a.head_dim, wave, koffs, voffs);                              \
+        if (wave_live)                                                                         \
+            fa_tile<F16, D, false>(CUR, CUR + G::TILE, qop, t, lane, lo, hi, wlo_max, whi_min,  \
+                                   Lb, 0, scale_log2, a.softcap2, slope2, pos, m_run, l_run,    \
+                                   acc);                                                        \
+        __builtin_amdgcn_sched_barrier(0);                                                     \
+        ++t;                                                                                   \
+    }
+    for (int t = tb;;) {
+        FA_TSTEP(st0, st2)
+        FA_TSTEP(st1, st0)
+        FA_TSTEP(st2, st1)
+    }
+#undef FA_TSTEP
+    FA_WAIT_VMCNT(0);
+    if (!wave_live) return;
+
+    // ---- outputs of this wavefront's columns, straight from the accumulators ----
+    const float l_col = group16_sum(l_run);
+    if (!col_ok) return;
+    const int rows = a.batch * a.q_heads * a.q_len;
+    float o_mul = a.o_mul;
+    if (a.o_mul_dev) o_mul *= *a.o_mul_dev;
+    const float inv = l_col > 0.0f ? 1.0f / l_col : 0.0f;
+    if (a.splits == 1) {
+        const int64_t base = sq.o0 + (int64_t)qi * a.o_st + (int64_t)head * a.o_sh;
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = 16 * u + 4 * g + i;
+                if (d < a.head_dim) store_elem(a.out, base + d, a.dtype, acc[u][i] * inv * o_mul);
+            }
+    } else {
+        const int64_t row = ((int64_t)b * a.q_heads + head) * a.q_len + qi;
+        float *po = a.part_o + ((int64_t)split * rows + row) * D;
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) po[16 * u + 4 * g + i] = acc[u][i] * inv;
+        if (g == 0)
+            a.part_lse[(int64_t)split * rows + row] =
+                l_col > 0.0f ? m_run + __builtin_log2f(l_col) : -__builtin_inff();
     }
 }
 

@@ -9,19 +9,20 @@ namespace cqkv {
 
 static int fa_dmax(int head_dim) { return head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256; }
 
-// Workgroups of the row kernel one CU holds (LDS: two stages of a K and a V tile per wavefront).
-static int fa_wgs_per_cu(int dmax) {
+// Workgroups one CU holds: the row kernel keeps two stages of a K and a V tile per wavefront,
+// the tile kernel three stages shared by its four wavefronts.
+static int fa_wgs_per_cu(int dmax, bool tile = false) {
     const int w = dmax == 256 ? 2 : 4;
-    const int lds = 2 * w * 2 * 32 * 2 * dmax;
+    const int lds = tile ? 3 * 2 * 32 * 2 * dmax : 2 * w * 2 * 32 * 2 * dmax;
     return std::max(1, (160 * 1024) / lds);
 }
 
 // Key splits: enough workgroups to fill the chip (256 CUs), at least two tiles per wavefront and
 // split; with per-sequence lengths, pieces of at most 4096 keys.
-static int fa_auto_splits(int planes_cols, int kv_len, int dmax, bool ragged) {
-    const int w = dmax == 256 ? 2 : 4;
+static int fa_auto_splits(int planes_cols, int kv_len, int dmax, bool ragged, bool tile = false) {
+    const int w = tile ? 1 : dmax == 256 ? 2 : 4;
     const int tiles = std::max(1, (kv_len + 31) / 32);
-    const int target = 256 * fa_wgs_per_cu(dmax);
+    const int target = 256 * fa_wgs_per_cu(dmax, tile);
     int s = (target + planes_cols - 1) / std::max(planes_cols, 1);
     if (ragged) s = std::max(s, (tiles + 127) / 128);
     s = std::min(s, std::max(1, tiles / (2 * w)));
@@ -39,10 +40,13 @@ static size_t fa_partials_bytes(int splits, int64_t rows, int dmax, size_t *lse_
 }
 
 template <bool F16, int D>
-static void fa_launch_d(const FaArgs &a, hipStream_t st) {
+static void fa_launch_d(const FaArgs &a, bool tile, hipStream_t st) {
     constexpr int W = fa_waves<D>();
     const int64_t wgs = (int64_t)a.splits * a.col_blocks * a.kv_heads * a.batch;
-    hipLaunchKernelGGL((fa_row_kernel<F16, D, W>), dim3((unsigned)wgs), dim3(W * 64), 0, st, a);
+    if (tile)
+        hipLaunchKernelGGL((fa_tile_kernel<F16, D>), dim3((unsigned)wgs), dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((fa_row_kernel<F16, D, W>), dim3((unsigned)wgs), dim3(W * 64), 0, st, a);
     if (a.splits > 1) {
         const int64_t rows = (int64_t)a.batch * a.q_heads * a.q_len;
         hipLaunchKernelGGL(fa_combine_kernel<D>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
@@ -50,11 +54,31 @@ static void fa_launch_d(const FaArgs &a, hipStream_t st) {
     }
 }
 
-static void fa_launch(const FaArgs &a, int dmax, hipStream_t st) {
+static void fa_launch(const FaArgs &a, int dmax, bool tile, hipStream_t st) {
     const bool f16 = a.dtype == CQKV_F16;
-    if (dmax == 64) f16 ? fa_launch_d<true, 64>(a, st) : fa_launch_d<false, 64>(a, st);
-    else if (dmax == 128) f16 ? fa_launch_d<true, 128>(a, st) : fa_launch_d<false, 128>(a, st);
-    else f16 ? fa_launch_d<true, 256>(a, st) : fa_launch_d<false, 256>(a, st);
+    if (dmax == 64) f16 ? fa_launch_d<true, 64>(a, tile, st) : fa_launch_d<false, 64>(a, tile, st);
+    else if (dmax == 128) f16 ? fa_launch_d<true, 128>(a, tile, st) : fa_launch_d<false, 128>(a, tile, st);
+    else f16 ? fa_launch_d<true, 256>(a, tile, st) : fa_launch_d<false, 256>(a, tile, st);
+}
+
+// The dense call's plan: the tile kernel (64 columns per workgroup) for more than 16 columns
+// per kv head, else the row kernel; column groups, splits, tiles per split.
+struct FaPlan {
+    bool tile;
+    int col_blocks, splits, tps;
+};
+static FaPlan fa_plan(int64_t batch, int64_t kv_heads, int64_t ncols, int kv_len, int dmax,
+                      bool ragged) {
+    FaPlan p;
+    p.tile = ncols > 16;
+    p.col_blocks = (int)std::min<int64_t>((ncols + (p.tile ? 63 : 15)) / (p.tile ? 64 : 16), 1 << 20);
+    const int64_t planes_cols = batch * kv_heads * p.col_blocks;
+    int s = fa_auto_splits((int)std::min<int64_t>(planes_cols, 1 << 30), kv_len, dmax, ragged,
+                           p.tile);
+    const int tiles = std::max(1, (kv_len + 31) / 32);
+    p.tps = (tiles + s - 1) / s;
+    p.splits = (tiles + p.tps - 1) / p.tps;
+    return p;
 }
 
 // Whether a 16-bit tensor's rows can be read as whole 16-byte chunks.
@@ -91,17 +115,14 @@ int fa_plain_run(FaArgs a, const char *who, void *workspace, size_t workspace_by
     const int64_t ncols = (int64_t)a.q_len * a.group;
     if ((ncols + 15) / 16 > (1 << 20))
         return fail(CQKV_ERR_ARG, "%s: %lld query columns per kv head", who, (long long)ncols);
-    a.col_blocks = (int)((ncols + 15) / 16);
+    const FaPlan plan = fa_plan(a.batch, a.kv_heads, ncols, a.kv_len, dmax, a.cu_k != nullptr);
+    a.col_blocks = plan.col_blocks;
     const int64_t planes_cols = (int64_t)a.batch * a.kv_heads * a.col_blocks;
-    int s = fa_auto_splits((int)std::min<int64_t>(planes_cols, 1 << 30), a.kv_len, dmax,
-                           a.cu_k != nullptr);
-    const int tiles = std::max(1, (a.kv_len + 31) / 32);
-    const int tps = (tiles + s - 1) / s;
-    s = (tiles + tps - 1) / tps;
+    const int s = plan.splits;
     if (planes_cols * s > 0x7fffffff)
         return fail(CQKV_ERR_ARG, "%s: %lld workgroups", who, (long long)(planes_cols * s));
     a.splits = s;
-    a.tiles_per_split = tps;
+    a.tiles_per_split = plan.tps;
     {
         const int64_t qs[3] = {a.cu_q ? 0 : a.q_sb, a.q_st, a.q_sh};
         a.q_vec = fa_vec_ok(a.q, qs) ? 1 : 0;
@@ -122,7 +143,7 @@ int fa_plain_run(FaArgs a, const char *who, void *workspace, size_t workspace_by
         a.part_o = (float *)ws;
         a.part_lse = (float *)((char *)ws + lse_off);
     }
-    fa_launch(a, dmax, st);
+    fa_launch(a, dmax, plan.tile, st);
     hipError_t e = hipGetLastError();
     if (owned) {
         const hipError_t fe = hipFreeAsync(ws, st);
@@ -135,15 +156,11 @@ int fa_plain_run(FaArgs a, const char *who, void *workspace, size_t workspace_by
 size_t fa_plain_workspace_bytes(int32_t batch, int32_t q_len, int32_t kv_len, int32_t q_heads,
                                 int32_t kv_heads, int32_t head_dim, bool ragged) {
     const int dmax = fa_dmax(head_dim);
-    const int64_t cb = ((int64_t)q_len * (q_heads / kv_heads) + 15) / 16;
-    const int64_t planes_cols = (int64_t)batch * kv_heads * cb;
-    int s = fa_auto_splits((int)std::min<int64_t>(planes_cols, 1 << 30), kv_len, dmax, ragged);
-    const int tiles = std::max(1, (kv_len + 31) / 32);
-    const int tps = (tiles + s - 1) / s;
-    s = (tiles + tps - 1) / tps;
-    if (s <= 1) return 0;
+    const FaPlan p = fa_plan(batch, kv_heads, (int64_t)q_len * (q_heads / kv_heads), kv_len, dmax,
+                             ragged);
+    if (p.splits <= 1) return 0;
     size_t lse_off;
-    return fa_partials_bytes(s, (int64_t)batch * q_heads * q_len, dmax, &lse_off);
+    return fa_partials_bytes(p.splits, (int64_t)batch * q_heads * q_len, dmax, &lse_off);
 }
 
 // ---- paged: blocks of plain K / V ----
@@ -331,7 +348,7 @@ extern "C" int cqkv_flash_attn_blocks(const void *q, const int64_t q_strides[3],
         a.part_lse = (float *)((char *)ws + table + lse_off);
     }
     if (e == hipSuccess) {
-        fa_launch(a, dmax, st);
+        fa_launch(a, dmax, false, st);
         e = hipGetLastError();
     }
     if (owned) {
