@@ -384,16 +384,23 @@ void orc_unrotate_rows(const float *pi, int dim, const float *y, size_t rows, fl
 }
 
 /* ------------------------------------------------------------------------------------------ */
-/* row codec: candle-core/src/accel/turbo.rs:293-424 (TurboProd's QJL stage not restated)      */
+/* row codec: candle-core/src/accel/turbo.rs:293-430                                           */
 /* ------------------------------------------------------------------------------------------ */
+void orc_qjl_matrix(int dim, uint64_t seed, float *s) { /* turbo.rs:236-239 */
+    orc_fill_normal((seed + 1) ^ 0x514a4c5f534b4554ull, s, (size_t)dim * dim);
+}
+
 int orc_codec_init(orc_codec *c, int mode, int bits, int dim) {
     memset(c, 0, sizeof(*c));
-    if (mode == ORC_TURBO_PROD) return -1;
     if (orc_row_layout(mode, bits, dim, &c->l) != 0) return -1;
     c->mode = mode;
     c->bits = bits;
     for (int i = 0; i < 16; ++i) c->boundaries[i] = INFINITY;
-    if (mode == ORC_TURBO_MSE && orc_lloyd_max(dim, bits, c->centroids, c->boundaries) != 0) return -1;
+    /* the MSE codebook of the code bits (bits for TurboMse, bits - 1 for TurboProd;
+       RowCodec::new, turbo.rs:252-258) */
+    if ((mode == ORC_TURBO_MSE || mode == ORC_TURBO_PROD) &&
+        orc_lloyd_max(dim, c->l.code_bits, c->centroids, c->boundaries) != 0)
+        return -1;
     return 0;
 }
 
@@ -402,19 +409,33 @@ void orc_quantize_row(const orc_codec *c, const float *y, uint32_t *out) {
     const int d = l->dim;
     memset(out, 0, sizeof(uint32_t) * l->row_words);
     float rsc0 = 1.0f, rsc1 = 0.0f;
-    if (c->mode == ORC_TURBO_MSE) { /* turbo.rs:299-323 */
-        const int nb = (1 << c->bits) - 1;
+    if (c->mode == ORC_TURBO_MSE || c->mode == ORC_TURBO_PROD) { /* turbo.rs:299-323 */
+        const int nb = (1 << l->code_bits) - 1;
         float ss = 0.0f;
         for (int j = 0; j < d; ++j) ss += y[j] * y[j];
         const float norm = sqrtf(ss);
         const float inv = norm > 0.0f ? 1.0f / norm : 0.0f;
+        float *resid = (float *)malloc(sizeof(float) * d);
         for (int j = 0; j < d; ++j) {
             const float u = y[j] * inv;
             uint32_t idx = 0;
             for (int b = 0; b < nb; ++b) idx += u >= c->boundaries[b] ? 1u : 0u;
             orc_put_bits(out, (size_t)j * l->code_bits, (uint32_t)l->code_bits, idx);
+            resid[j] = u - c->centroids[idx];
         }
         rsc0 = norm;
+        if (c->mode == ORC_TURBO_PROD && c->qjl) { /* turbo.rs:311-320 */
+            float rr = 0.0f;
+            for (int j = 0; j < d; ++j) rr += resid[j] * resid[j];
+            rsc1 = sqrtf(rr);
+            uint32_t *signs = out + l->code_words;
+            for (int i = 0; i < d; ++i) {
+                float pr = 0.0f;
+                for (int j = 0; j < d; ++j) pr += c->qjl[(size_t)i * d + j] * resid[j];
+                if (pr >= 0.0f) signs[i >> 5] |= 1u << (i & 31);
+            }
+        }
+        free(resid);
     } else if (c->mode == ORC_MXFP4 || c->mode == ORC_MXFP8) { /* turbo.rs:324-347 */
         const int fp4 = c->mode == ORC_MXFP4;
         for (int b = 0; b < d / 32; ++b) {
@@ -466,7 +487,8 @@ float orc_elem(const orc_codec *c, const uint32_t *row, int j) { /* turbo.rs:383
     const uint32_t code = orc_get_bits(row, (size_t)j * l->code_bits, (uint32_t)l->code_bits);
     const uint32_t *aux = row + l->code_words;
     switch (c->mode) {
-    case ORC_TURBO_MSE: return c->centroids[code];
+    case ORC_TURBO_MSE:
+    case ORC_TURBO_PROD: return c->centroids[code];
     case ORC_MXFP4: return orc_fp4_to_f32(code) * orc_e8m0_to_f32(get_byte(aux, (size_t)(j / 32)));
     case ORC_NVFP4: return orc_fp4_to_f32(code) * orc_e4m3_to_f32(get_byte(aux, (size_t)(j / 16)));
     case ORC_MXFP8: return orc_e4m3_to_f32((uint8_t)code) * orc_e8m0_to_f32(get_byte(aux, (size_t)(j / 32)));
@@ -474,9 +496,19 @@ float orc_elem(const orc_codec *c, const uint32_t *row, int j) { /* turbo.rs:383
     }
 }
 
-void orc_dequantize_row(const orc_codec *c, const uint32_t *row, float *out) { /* turbo.rs:404-409 */
+void orc_dequantize_row(const orc_codec *c, const uint32_t *row, float *out) { /* turbo.rs:401-424 */
+    const int d = c->l.dim;
     const float r0 = u2f(row[c->l.code_words + c->l.aux_words]);
-    for (int j = 0; j < c->l.dim; ++j) out[j] = r0 * orc_elem(c, row, j);
+    for (int j = 0; j < d; ++j) out[j] = r0 * orc_elem(c, row, j);
+    if (c->mode == ORC_TURBO_PROD && c->qjl) {
+        const float r1 = u2f(row[c->l.code_words + c->l.aux_words + 1]);
+        const float cq = r0 * r1 * 1.2533141f / (float)d; /* QJL_CONST, turbo.rs:26 */
+        const uint32_t *signs = row + c->l.code_words;
+        for (int i = 0; i < d; ++i) {
+            const float z = ((signs[i >> 5] >> (i & 31)) & 1u) ? cq : -cq;
+            for (int j = 0; j < d; ++j) out[j] += z * c->qjl[(size_t)i * d + j];
+        }
+    }
 }
 
 typedef struct {
@@ -510,6 +542,28 @@ int orc_quantize_rows(int mode, int bits, int dim, size_t rows, const float *y, 
 int orc_dequantize_rows(int mode, int bits, int dim, size_t rows, const uint32_t *words, float *out, int threads) {
     rows_ctx r;
     if (orc_codec_init(&r.c, mode, bits, dim) != 0) return -1;
+    r.w = words;
+    r.out_f = out;
+    orc_parallel(rows, threads, dequant_body, &r);
+    return 0;
+}
+
+int orc_quantize_rows_qjl(int bits, int dim, size_t rows, const float *y, const float *s, uint32_t *out,
+                          int threads) {
+    rows_ctx r;
+    if (orc_codec_init(&r.c, ORC_TURBO_PROD, bits, dim) != 0) return -1;
+    r.c.qjl = s;
+    r.y = y;
+    r.out_w = out;
+    orc_parallel(rows, threads, quant_body, &r);
+    return 0;
+}
+
+int orc_dequantize_rows_qjl(int bits, int dim, size_t rows, const uint32_t *words, const float *s,
+                            float *out, int threads) {
+    rows_ctx r;
+    if (orc_codec_init(&r.c, ORC_TURBO_PROD, bits, dim) != 0) return -1;
+    r.c.qjl = s;
     r.w = words;
     r.out_f = out;
     orc_parallel(rows, threads, dequant_body, &r);
@@ -642,12 +696,17 @@ static void deq_cache_body(void *p, size_t lo, size_t hi) {
 
 int orc_cache_attention(const uint16_t *q_bf16, const uint32_t *k_rows, const uint32_t *v_rows,
                         int k_mode, int k_bits, int v_mode, int v_bits, const float *pi_k,
-                        const float *pi_v, int b, int hq, int hkv, int lq, int cap, int d,
-                        const int32_t *kv_lens, int lk, float scale, int wl, int wr, float *out,
-                        int threads) {
+                        const float *pi_v, const float *qjl_k, int b, int hq, int hkv, int lq,
+                        int cap, int d, const int32_t *kv_lens, int lk, float scale, int wl, int wr,
+                        float *out, int threads) {
     deq_ctx kc, vc;
     if (orc_codec_init(&kc.c, k_mode, k_bits, d) != 0 || orc_codec_init(&vc.c, v_mode, v_bits, d) != 0)
         return -1;
+    if (k_mode == ORC_TURBO_PROD) {
+        if (!qjl_k) return -1;
+        kc.c.qjl = qjl_k;
+    }
+    if (v_mode == ORC_TURBO_PROD) return -1; /* values use the MSE codebooks (turbo_quant.rs:869-871) */
     const size_t kv_elems = (size_t)b * hkv * lk * d;
     float *k = (float *)malloc(sizeof(float) * kv_elems);
     float *v = (float *)malloc(sizeof(float) * kv_elems);

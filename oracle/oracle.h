@@ -61,13 +61,23 @@ void orc_rotate_rows(const float *pi, int dim, const float *x, size_t rows, floa
 /* x = y Π (turbo_quant.rs:191-196). */
 void orc_unrotate_rows(const float *pi, int dim, const float *y, size_t rows, float *x);
 
-/* ---- row codec (turbo.rs:293-424), TurboProd excluded (no QJL stage) ---- */
+/* ---- row codec (turbo.rs:293-424) ----
+ * TurboProd: qjl = the row-major dim x dim QJL matrix S (turbo.rs:236-239), or NULL for the
+ * codec without it (RowCodec::without_qjl, turbo.rs:273-286: codes and norm only). */
 typedef struct {
     int mode, bits;
     orc_layout l;
     float centroids[16];
     float boundaries[16];
+    const float *qjl;
 } orc_codec;
+/* S = SplitMix64((seed + 1) ^ 0x514a4c5f534b4554) normals, row-major dim x dim (turbo.rs:236-239). */
+void orc_qjl_matrix(int dim, uint64_t seed, float *s);
+/* TurboProd{bits} rows with the QJL matrix s (quantize: y already rotated). */
+int orc_quantize_rows_qjl(int bits, int dim, size_t rows, const float *y, const float *s, uint32_t *out,
+                          int threads);
+int orc_dequantize_rows_qjl(int bits, int dim, size_t rows, const uint32_t *words, const float *s,
+                            float *out, int threads);
 int orc_codec_init(orc_codec *c, int mode, int bits, int dim);
 void orc_quantize_row(const orc_codec *c, const float *y, uint32_t *out);
 float orc_elem(const orc_codec *c, const uint32_t *row, int j);
@@ -96,9 +106,9 @@ int orc_attention_unfused(const float *q, const float *k, const float *v, int b,
  * pi_k / pi_v: rotation matrices or NULL. Output f32 (b, hq, lq, d) (round to bf16 to compare). */
 int orc_cache_attention(const uint16_t *q_bf16, const uint32_t *k_rows, const uint32_t *v_rows,
                         int k_mode, int k_bits, int v_mode, int v_bits, const float *pi_k,
-                        const float *pi_v, int b, int hq, int hkv, int lq, int cap, int d,
-                        const int32_t *kv_lens, int lk, float scale, int wl, int wr, float *out,
-                        int threads);
+                        const float *pi_v, const float *qjl_k, int b, int hq, int hkv, int lq,
+                        int cap, int d, const int32_t *kv_lens, int lk, float scale, int wl, int wr,
+                        float *out, int threads);
 
 /* Split combine (candle-core/kernels/turbo_quant_impl.h:659-685). part_o (splits, rows, d),
  * part_lse (splits, rows). */

@@ -61,8 +61,11 @@ def lib() -> ctypes.CDLL:
                                     ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)]
         L.orc_attention_unfused.argtypes = [P, P, P, i32, i32, i32, i32, i32, i32, P, f32, f32,
                                             i32, i32, P, P, i32]
-        L.orc_cache_attention.argtypes = [P, P, P, i32, i32, i32, i32, P, P, i32, i32, i32, i32,
-                                          i32, i32, P, i32, f32, i32, i32, P, i32]
+        L.orc_cache_attention.argtypes = [P, P, P, i32, i32, i32, i32, P, P, P, i32, i32, i32,
+                                          i32, i32, i32, P, i32, f32, i32, i32, P, i32]
+        L.orc_qjl_matrix.argtypes = [i32, u64, P]
+        L.orc_quantize_rows_qjl.argtypes = [i32, i32, sz, P, P, P, i32]
+        L.orc_dequantize_rows_qjl.argtypes = [i32, i32, sz, P, P, P, i32]
         L.orc_combine.argtypes = [P, P, P, sz, i32, i32]
         L.orc_e4m3_encode_n.argtypes = [P, P, sz]
         L.orc_fp4_encode_n.argtypes = [P, P, sz]
@@ -222,6 +225,40 @@ def dequantize_rows(mode: int, bits: int, dim: int, words: np.ndarray, threads: 
     return out.reshape(words.shape[:-1] + (dim,))
 
 
+def qjl_matrix(dim: int, seed: int) -> np.ndarray:
+    """The QJL projection S (dim, dim) f32 of TurboProd (turbo.rs:236-239)."""
+    s = np.zeros((dim, dim), dtype=np.float32)
+    lib().orc_qjl_matrix(dim, seed, _p(s))
+    return s
+
+
+def quantize_rows_qjl(bits: int, y: np.ndarray, s: np.ndarray, threads: int = 8) -> np.ndarray:
+    """TurboProd{bits} rows (RowCodec::quantize_row with the QJL stage, turbo.rs:299-323) of
+    rotated rows y (.., dim) with the QJL matrix s."""
+    y = np.ascontiguousarray(y, dtype=np.float32)
+    s = np.ascontiguousarray(s, dtype=np.float32)
+    d = y.shape[-1]
+    l = row_layout(TURBO_PROD, bits, d)
+    rows = y.size // d
+    out = np.zeros(rows * l.row_words, dtype=np.uint32)
+    if lib().orc_quantize_rows_qjl(bits, d, rows, _p(y), _p(s), _p(out), threads) != 0:
+        raise ValueError("quantize_rows_qjl failed")
+    return out.reshape(y.shape[:-1] + (l.row_words,))
+
+
+def dequantize_rows_qjl(bits: int, dim: int, words: np.ndarray, s: np.ndarray,
+                        threads: int = 8) -> np.ndarray:
+    """RowCodec::dequantize_row with the QJL correction (turbo.rs:401-424), rotated domain."""
+    words = np.ascontiguousarray(words, dtype=np.uint32)
+    s = np.ascontiguousarray(s, dtype=np.float32)
+    l = row_layout(TURBO_PROD, bits, dim)
+    rows = words.size // l.row_words
+    out = np.zeros(rows * dim, dtype=np.float32)
+    if lib().orc_dequantize_rows_qjl(bits, dim, rows, _p(words), _p(s), _p(out), threads) != 0:
+        raise ValueError("dequantize_rows_qjl failed")
+    return out.reshape(words.shape[:-1] + (dim,))
+
+
 def key_range(i: int, lq: int, lk: int, wl: int, wr: int) -> tuple[int, int]:
     lo, hi = ctypes.c_int64(), ctypes.c_int64()
     lib().orc_key_range(i, lq, lk, wl, wr, ctypes.byref(lo), ctypes.byref(hi))
@@ -312,9 +349,10 @@ def attention_unfused(q, k, v, scale, kv_lens=None, softcap=0.0, wl=-1, wr=-1, a
 
 
 def cache_attention(q_bf16_bits, k_rows, v_rows, k_fmt, v_fmt, pi_k, pi_v, lk, scale,
-                    kv_lens=None, wl=-1, wr=-1, threads: int = 8) -> np.ndarray:
+                    kv_lens=None, wl=-1, wr=-1, threads: int = 8, qjl_k=None) -> np.ndarray:
     """The reference CPU decode path over packed rows. q_bf16_bits (b, hq, lq, d) u16,
-    k_rows / v_rows (b, hkv, cap, row_words) u32, formats (mode, bits). Output f32."""
+    k_rows / v_rows (b, hkv, cap, row_words) u32, formats (mode, bits); qjl_k: the QJL matrix
+    of TurboProd keys. Output f32."""
     q = np.ascontiguousarray(q_bf16_bits, dtype=np.uint16)
     k_rows = np.ascontiguousarray(k_rows, dtype=np.uint32)
     v_rows = np.ascontiguousarray(v_rows, dtype=np.uint32)
@@ -324,8 +362,9 @@ def cache_attention(q_bf16_bits, k_rows, v_rows, k_fmt, v_fmt, pi_k, pi_v, lk, s
     kl = None if kv_lens is None else np.ascontiguousarray(kv_lens, dtype=np.int32)
     pk = None if pi_k is None else np.ascontiguousarray(pi_k, dtype=np.float32)
     pv = None if pi_v is None else np.ascontiguousarray(pi_v, dtype=np.float32)
+    sk = None if qjl_k is None else np.ascontiguousarray(qjl_k, dtype=np.float32)
     rc = lib().orc_cache_attention(_p(q), _p(k_rows), _p(v_rows), k_fmt[0], k_fmt[1], v_fmt[0],
-                                   v_fmt[1], _p(pk), _p(pv), b, hq, hkv, lq, cap, d, _p(kl), lk,
+                                   v_fmt[1], _p(pk), _p(pv), _p(sk), b, hq, hkv, lq, cap, d, _p(kl), lk,
                                    scale, wl, wr, _p(out), threads)
     if rc != 0:
         raise ValueError(f"cache_attention failed ({rc})")

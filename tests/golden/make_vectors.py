@@ -123,6 +123,72 @@ def fa_case():
     print("fa", dense.shape, var.shape)
 
 
+def prod_rows(y: np.ndarray, s: np.ndarray, bits: int = 4) -> tuple[np.ndarray, np.ndarray]:
+    """TurboProd rows of rotated rows y through the reference's GPU pipeline
+    (TurboQuantizer::quantize_gpu, candle-nn/src/turbo_quant.rs:214-234): tq_quant (stage one:
+    codes and norm), the residual of tq_resid_impl (turbo_quant_impl.h:161-176, elementwise f32:
+    u = y * (1 / norm), u - centroid), proj = resid S^T (the reference's matmul; float64 here,
+    rounded to f32), tq_signs (signs of proj, rsc1 = |resid|). Returns (rows, proj)."""
+    d = y.shape[-1]
+    l = O.row_layout(O.TURBO_PROD, bits, d)
+    c, b = O.lloyd_max(d, bits - 1)
+    tab = H.tq_tab(c, b)
+    packed = H.tq_quant(y.astype(np.float32), O.TURBO_PROD, l.code_bits, l.code_words,
+                        l.aux_words, l.row_words, tab)
+    norm = packed[:, l.code_words + l.aux_words].view(np.float32)
+    inv = np.where(norm > 0, np.float32(1.0) / np.where(norm > 0, norm, 1), 0).astype(np.float32)
+    u = (y * inv[:, None]).astype(np.float32)
+    # 3-bit codes straddle words: read them bit by bit
+    codes = np.zeros((y.shape[0], d), dtype=np.int64)
+    for j in range(d):
+        for bit in range(l.code_bits):
+            pos = j * l.code_bits + bit
+            codes[:, j] |= ((packed[:, pos // 32] >> (pos % 32)) & 1).astype(np.int64) << bit
+    resid = (u - c[codes]).astype(np.float32)
+    proj = (resid.astype(np.float64) @ s.astype(np.float64).T).astype(np.float32)
+    return H.tq_signs(packed, proj, resid, l.code_words), proj
+
+
+def prod_case():
+    """TurboProd-4 keys (3-bit MSE codes + QJL signs) at D = 128: rows through the reference
+    kernels (prod_rows), and its fused decode (tq_attn with [q Pi^T, q Pi^T S^T] queries, then
+    the value unrotation) over them with TurboQuant-4 values."""
+    B, Hq, Hkv, D, Lq, Lk = 2, 8, 2, 128, 2, 300
+    rng = np.random.default_rng(700)
+    mask = rng.random((Hkv, D)) < 0.01
+    q = O.round_bf16(O.normal(701, (B, Hq, Lq, D)))
+    k = O.normal(702, (B, Hkv, Lk, D))
+    v = O.normal(703, (B, Hkv, Lk, D))
+    k = O.round_bf16(np.where(mask[None, :, None, :], k * 8, k)).astype(np.float32)
+    v = O.round_bf16(np.where(mask[None, :, None, :], v * 8, v)).astype(np.float32)
+    s = O.qjl_matrix(D, 42)
+    pk = O.rotation_matrix(D, O.ROT_HADAMARD, 42)
+    pv = O.rotation_matrix(D, O.ROT_HADAMARD, 44)
+    kx = O.rotate_rows(pk, k.reshape(-1, D))
+    vx = O.rotate_rows(pv, v.reshape(-1, D))
+    kd, proj = prod_rows(kx, s)
+    kd = kd.reshape(B, Hkv, Lk, -1)
+    lv = O.row_layout(O.TURBO_MSE, 4, D)
+    cv, bv = O.lloyd_max(D, 4)
+    vd = H.tq_quant(vx.astype(np.float32), O.TURBO_MSE, lv.code_bits, lv.code_words,
+                    lv.aux_words, lv.row_words, H.tq_tab(cv, bv)).reshape(B, Hkv, Lk, -1)
+    lk_ = O.row_layout(O.TURBO_PROD, 4, D)
+    ck, bk = O.lloyd_max(D, 3)
+    tab64 = np.concatenate([H.tq_tab(ck, bk), H.tq_tab(cv, bv)]).astype(np.float32)
+    qr = O.rotate_rows(pk, q.reshape(-1, D)).reshape(q.shape)
+    qs = (qr.reshape(-1, D).astype(np.float64) @ s.astype(np.float64).T).astype(np.float32)
+    qx = np.concatenate([qr, qs.reshape(q.shape)], -1).astype(np.float32)
+    scale = np.float32(1.0 / np.sqrt(D))
+    k_side = (O.TURBO_PROD, lk_.code_bits, lk_.code_words, lk_.code_words + lk_.aux_words)
+    v_side = (O.TURBO_MSE, lv.code_bits, lv.code_words, lv.code_words + lv.aux_words)
+    o = H.tq_attn(qx, kd, vd, k_side, v_side, tab64, float(scale), splits=3)
+    o = (o.reshape(-1, D) @ pv).reshape(o.shape).astype(np.float32)
+    # the inputs regenerate from the seeds above (prod_inputs in the tests); kept: the rows and
+    # the output
+    np.savez_compressed(os.path.join(HERE, "ref_prod4.npz"), kd=kd, vd=vd, out=o, scale=scale)
+    print("prod", kd.shape, o.shape)
+
+
 def combine_case():
     splits, rows, d = 5, 7, 32
     po = O.normal(201, (splits, rows, d))
@@ -152,4 +218,5 @@ if __name__ == "__main__":
     attn_format_case("mxfp4", O.MXFP4, 0)
     attn_format_case("nvfp4", O.NVFP4, 0)
     attn_format_case("mxfp8", O.MXFP8, 0)
+    prod_case()
     combine_case()

@@ -84,17 +84,31 @@ def tq_quant(x: np.ndarray, mode: int, code_bits: int, code_words: int, aux_word
     return out["out"].reshape(rows, row_words)
 
 
+def tq_signs(packed: np.ndarray, proj: np.ndarray, resid: np.ndarray, code_words: int,
+             gx: int = 5) -> np.ndarray:
+    """Reference `tq_signs`: packed prod rows (rows, row_words) with proj = S resid and resid
+    (rows, D) f32 -> rows with the QJL sign bits and rsc1 = |resid|."""
+    rows, rw = packed.shape
+    d = resid.shape[1]
+    p = np.array([rows, d, code_words, rw, gx], dtype=np.uint32)
+    out = run({"op": "tq_signs", "data": packed.astype(np.uint32),
+               "proj": proj.astype(np.float32), "resid": resid.astype(np.float32), "params": p})
+    return out["out"].reshape(rows, rw)
+
+
 def tq_attn(q: np.ndarray, kd: np.ndarray, vd: np.ndarray, k_side, v_side, tab64: np.ndarray,
             scale: float, splits: int = 1, wl: int = -1, wr: int = -1, group: int = 1,
             fp8: bool = False) -> np.ndarray:
-    """Reference `tq_attn*` + `tq_combine`: q (B, Hq, Lq, D) f32 rotated queries, kd / vd
-    (B, Hkv, Lk, words) u32 rows; sides (mode, code_bits, code_words, rsc_offset)."""
-    B, Hq, Lq, D = q.shape
+    """Reference `tq_attn*` + `tq_combine`: q (B, Hq, Lq, W) f32 rotated queries (W = D, or 2 D
+    with S q behind them for prod keys), kd / vd (B, Hkv, Lk, words) u32 rows; sides (mode,
+    code_bits, code_words, rsc_offset)."""
+    B, Hq, Lq, W = q.shape
+    D = W // 2 if k_side[0] == 1 else W
     _, Hkv, Lk, kw = kd.shape
     vw = vd.shape[3]
     u = np.array([B, Lq, Lk, Hq, Hkv, D, *k_side, *v_side, splits, 3, 0, int(fp8), group],
                  dtype=np.uint32)
-    s = np.array([Hq * Lq * D, Lq * D, D, Hkv * Lk * kw, Lk * kw, kw, Hkv * Lk * vw, Lk * vw, vw],
+    s = np.array([Hq * Lq * W, Lq * W, W, Hkv * Lk * kw, Lk * kw, kw, Hkv * Lk * vw, Lk * vw, vw],
                  dtype=np.uint64)
     out = run({"op": "tq_attn", "uparams": u, "strides": s,
                "fparams": np.array([scale, 0.0], dtype=np.float32),

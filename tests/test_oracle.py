@@ -713,3 +713,110 @@ def test_fp8_tensor_quantize_reciprocal_choice_only_matters_at_ties():
         quot += int((qa != qb).sum())
         diff += int((O.e4m3_encode(qb) != codes).sum())
     assert quot > 0 and diff == 0
+
+
+# ---------------------------------------------------------------------------------------------
+# TurboProd (QJL) keys
+# ---------------------------------------------------------------------------------------------
+def prod_inputs():
+    """The inputs of the ref_prod4 fixture (tests/golden/make_vectors.py prod_case)."""
+    B, Hq, Hkv, D, Lq, Lk = 2, 8, 2, 128, 2, 300
+    rng = np.random.default_rng(700)
+    mask = rng.random((Hkv, D)) < 0.01
+    q = O.round_bf16(O.normal(701, (B, Hq, Lq, D)))
+    k = O.normal(702, (B, Hkv, Lk, D))
+    v = O.normal(703, (B, Hkv, Lk, D))
+    k = O.round_bf16(np.where(mask[None, :, None, :], k * 8, k)).astype(np.float32)
+    v = O.round_bf16(np.where(mask[None, :, None, :], v * 8, v)).astype(np.float32)
+    return q, k, v
+
+
+def test_prod_rows_match_reference_kernels():
+    """RowCodec::quantize_row of TurboProd{4} (3-bit codes, QJL sign bits of S r, rsc1 = |r|;
+    turbo.rs:299-323) against the reference's GPU pipeline run on its host emulator (tq_quant,
+    the tq_resid residual, the S r projection, tq_signs): codes equal, norms and |r| within
+    rtol 1e-5 (their reduction orders differ), sign bits equal but for <= 0.1 % (a projection
+    within rounding of zero)."""
+    g = gold("ref_prod4")
+    q, k, v = prod_inputs()
+    D = 128
+    s = O.qjl_matrix(D, 42)
+    pk = O.rotation_matrix(D, O.ROT_HADAMARD, 42)
+    kx = O.rotate_rows(pk, k.reshape(-1, D)).reshape(k.shape)
+    mine, ref = O.quantize_rows_qjl(4, kx, s), g["kd"]
+    lay = O.row_layout(O.TURBO_PROD, 4, D)
+    cw, aw = lay.code_words, lay.aux_words
+    np.testing.assert_array_equal(mine[..., :cw], ref[..., :cw])
+    for w in (cw + aw, cw + aw + 1):
+        np.testing.assert_allclose(mine[..., w].view(np.float32), ref[..., w].view(np.float32),
+                                   rtol=1e-5)
+    ms = np.unpackbits(mine[..., cw:cw + aw].copy().view(np.uint8))
+    rs = np.unpackbits(ref[..., cw:cw + aw].copy().view(np.uint8))
+    assert (ms != rs).sum() <= ms.size // 1000
+
+
+def test_prod_decode_vs_reference_fused_kernel():
+    """The reference's fused decode over TurboProd keys (tq_attn with [q Pi^T, q Pi^T S^T],
+    turbo_quant_impl.h:259-279, then the value unrotation) equals float64 attention over the
+    oracle's dequantized rows (MSE part + QJL correction, turbo.rs:401-424) to 1e-5; the
+    reference CPU path (dequantize, unrotate, bf16, unfused attention) stays within 2e-2."""
+    g = gold("ref_prod4")
+    q, _, _ = prod_inputs()
+    B, Hq, Lq, D = q.shape
+    s = O.qjl_matrix(D, 42)
+    pk = O.rotation_matrix(D, O.ROT_HADAMARD, 42).astype(np.float64)
+    pv = O.rotation_matrix(D, O.ROT_HADAMARD, 44).astype(np.float64)
+    kd = O.dequantize_rows_qjl(4, D, g["kd"], s).astype(np.float64) @ pk
+    vd = O.dequantize_rows(O.TURBO_MSE, 4, D, g["vd"]).astype(np.float64) @ pv
+    scale = float(g["scale"])
+    ex = np.zeros((B, Hq, Lq, D))
+    for b in range(B):
+        for h in range(Hq):
+            sc = q[b, h].astype(np.float64) @ kd[b, h // 4].T * scale
+            p = np.exp(sc - sc.max(1, keepdims=True))
+            ex[b, h] = p @ vd[b, h // 4] / p.sum(1, keepdims=True)
+    assert np.abs(ex - g["out"]).max() < 1e-5
+    cpu = O.cache_attention(O.f32_to_bf16_bits(q), g["kd"], g["vd"], (O.TURBO_PROD, 4),
+                            (O.TURBO_MSE, 4), pk.astype(np.float32), pv.astype(np.float32),
+                            g["kd"].shape[2], scale, threads=8, qjl_k=s)
+    assert np.abs(O.round_bf16(cpu) - g["out"]).max() < 2e-2
+
+
+@pytest.mark.parametrize("qjl", [True, False])
+def test_prod_inner_products_are_unbiased(qjl):
+    """The reference's statistical test (turbo.rs:658-700) over 400 seeds of S: the TurboProd{2}
+    estimate of x . y is unbiased (within 0.06 |x| |y|). Dropping the QJL correction (a planted
+    mistake) leaves the 1-bit MSE estimate, shrunk by 2 / pi: it must fail."""
+    d, n = 64, 400
+    x = O.normal(5, (2, d))
+    # correlated vectors (x . y ~ 0.9 |x| |y|), so the 2 / pi shrink of the planted mistake
+    # stands well clear of the tolerance
+    y, xx = x[0], (x[0] + 0.5 * x[1]).astype(np.float32)
+    exact = float(xx @ y)
+    mean = 0.0
+    for seed in range(n):
+        pi = O.rotation_matrix(d, O.ROT_HADAMARD, seed)
+        rx = O.rotate_rows(pi, xx[None])[0]
+        ry = O.rotate_rows(pi, y[None])[0]
+        s = O.qjl_matrix(d, seed)
+        rows = O.quantize_rows_qjl(2, rx[None], s)
+        if qjl:
+            back = O.dequantize_rows_qjl(2, d, rows, s)[0]
+        else:
+            back = O.dequantize_rows(O.TURBO_PROD, 2, d, rows)[0]
+        mean += float(back @ ry) / n
+    scale = float(np.sqrt((xx @ xx) * (y @ y)))
+    if qjl:
+        assert abs(mean - exact) < 0.06 * scale, (mean, exact)
+    else:
+        assert abs(mean - exact) > 0.06 * scale and \
+            abs(mean - exact * 2 / np.pi) < 0.06 * scale, (mean, exact)
+
+
+def test_qjl_matrix_is_standard_normal_from_its_seed():
+    """S = SplitMix64((seed + 1) ^ "QJL_SKET") normals (turbo.rs:236-239): the stream of O.normal
+    at that seed, moments of N(0, 1), distinct seeds give distinct matrices."""
+    s = O.qjl_matrix(128, 42)
+    np.testing.assert_array_equal(s.ravel(), O.normal((42 + 1) ^ 0x514A4C5F534B4554, (128 * 128,)))
+    assert abs(s.mean()) < 0.02 and abs(s.var() - 1) < 0.03
+    assert not np.array_equal(s, O.qjl_matrix(128, 43))
