@@ -20,8 +20,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libcqkv.so")
 
 # formats: the reference's kernel mode ids (candle-core/src/accel/formats.rs:41-48)
-TURBO4, MXFP4, NVFP4, MXFP8, FP8 = 0, 2, 3, 4, 5
-FORMAT_NAMES = {"fp8": FP8, "mxfp4": MXFP4, "turbo4": TURBO4, "nvfp4": NVFP4, "mxfp8": MXFP8}
+TURBO4, TURBOPROD, MXFP4, NVFP4, MXFP8, FP8 = 0, 1, 2, 3, 4, 5
+FORMAT_NAMES = {"fp8": FP8, "mxfp4": MXFP4, "turbo4": TURBO4, "turboprod": TURBOPROD,
+                "nvfp4": NVFP4, "mxfp8": MXFP8}
 BF16, F16, F32 = 0, 1, 2
 # cache-side rotations: DEFAULT rotates TURBO4 sides only; HADAMARD any format (the reference's
 # RotationKind::Hadamard, Auto at power-of-two head dims)
@@ -44,7 +45,7 @@ class Side(ctypes.Structure):
                 ("head_dim", ctypes.c_int32), ("kv_heads", ctypes.c_int32),
                 ("capacity", ctypes.c_int32), ("rotation", ctypes.c_int32),
                 ("seed", ctypes.c_uint64), ("codes", ctypes.c_void_p),
-                ("scales", ctypes.c_void_p)]
+                ("scales", ctypes.c_void_p), ("qjl", ctypes.c_void_p)]
 
 
 class PlainBlock(ctypes.Structure):
@@ -118,6 +119,7 @@ def lib() -> ctypes.CDLL:
         L.cqkv_side_copy.argtypes = [SP, SP, i32, i32, P]
         L.cqkv_turbo_codebook.argtypes = [i32, i32, P, P]
         L.cqkv_turbo_signs.argtypes = [i32, ctypes.c_uint64, P]
+        L.cqkv_qjl_matrix.argtypes = [i32, ctypes.c_uint64, P]
         L.cqkv_last_error.restype = ctypes.c_char_p
         L.cqkv_version.restype = ctypes.c_char_p
         _lib = L
@@ -134,6 +136,7 @@ EXPORTED = ["cqkv_codes_plane_bytes", "cqkv_scales_plane_bytes", "cqkv_quant_app
             "cqkv_fp8_quantize_tensor",
             "cqkv_flash_attn_fp8", "cqkv_hadamard_rows", "cqkv_reference_row_words", "cqkv_rows_import",
             "cqkv_rows_export", "cqkv_side_copy", "cqkv_turbo_codebook", "cqkv_turbo_signs",
+            "cqkv_qjl_matrix",
             "cqkv_last_error",
             "cqkv_version"]
 
@@ -177,6 +180,7 @@ class CacheSide:
     scales: torch.Tensor
     seed: int = 0
     rotation: int = ROT_DEFAULT
+    qjl: torch.Tensor | None = None  # TURBOPROD: the (D, D) f32 QJL matrix on the device
 
     @staticmethod
     def empty(fmt: int, is_value: bool, batch: int, kv_heads: int, head_dim: int,
@@ -189,17 +193,19 @@ class CacheSide:
             raise CqkvError(ERR_ARG, f"format {fmt} / head_dim {head_dim} not supported")
         codes = torch.zeros(batch * kv_heads * cb, dtype=torch.uint8, device=device)
         scales = torch.zeros(batch * kv_heads * sb, dtype=torch.uint8, device=device)
+        qjl = qjl_matrix(head_dim, seed).to(device) if fmt == TURBOPROD else None
         return CacheSide(fmt, is_value, batch, kv_heads, head_dim, capacity, codes, scales, seed,
-                         rotation)
+                         rotation, qjl)
 
     def rotates(self) -> bool:
         """Whether rows are stored Hadamard-rotated (seeded by `seed`)."""
         return self.rotation == ROT_HADAMARD or (self.rotation == ROT_DEFAULT and
-                                                 self.fmt == TURBO4)
+                                                 self.fmt in (TURBO4, TURBOPROD))
 
     def struct(self) -> Side:
         return Side(self.fmt, int(self.is_value), self.head_dim, self.kv_heads, self.capacity,
-                    self.rotation, self.seed, self.codes.data_ptr(), self.scales.data_ptr())
+                    self.rotation, self.seed, self.codes.data_ptr(), self.scales.data_ptr(),
+                    None if self.qjl is None else self.qjl.data_ptr())
 
     def nbytes(self) -> int:
         return self.codes.numel() + self.scales.numel()
@@ -654,6 +660,13 @@ def turbo_codebook(head_dim: int, bits: int = 4):
     return c[:k].copy(), bnd[:k - 1].copy()
 
 
+def qjl_matrix(head_dim: int, seed: int) -> torch.Tensor:
+    """The QJL projection S (head_dim, head_dim) f32 of TurboProd (cqkv_qjl_matrix), on the host."""
+    s = torch.empty((head_dim, head_dim), dtype=torch.float32)
+    _check(lib().cqkv_qjl_matrix(head_dim, seed, ctypes.c_void_p(s.data_ptr())))
+    return s
+
+
 def turbo_signs(head_dim: int, seed: int):
     import numpy as np
     s = np.zeros(head_dim, dtype=np.float32)
@@ -665,14 +678,18 @@ def turbo_signs(head_dim: int, seed: int):
 # host-side mirror of candle-nn's TurboKvCache (candle-nn/src/turbo_quant.rs:793-991)
 # ------------------------------------------------------------------------------------------
 class TurboKvCache:
-    """A quantized KV cache for (batch, kv_heads, head_dim), keys in `key_format` and values in
-    `value_format` (each FP8, MXFP4, MXFP8, NVFP4 or TURBO4), rotated per `rotation` with seeds
-    `seed` (keys) and `seed + 2` (values) as TurboKvCache::with_formats does
-    (candle-nn/src/turbo_quant.rs:858-879). It grows past `capacity` as Cache::append does."""
+    """A quantized KV cache for (batch, kv_heads, head_dim), keys in `key_format` (FP8, MXFP4,
+    MXFP8, NVFP4, TURBO4 or TURBOPROD) and values in `value_format` (the same but TURBOPROD),
+    rotated per `rotation` with seeds `seed` (keys) and `seed + 2` (values) as
+    TurboKvCache::with_formats does (candle-nn/src/turbo_quant.rs:858-879). It grows past
+    `capacity` as Cache::append does."""
 
     def __init__(self, key_format: int, value_format: int, batch: int, kv_heads: int,
                  head_dim: int, capacity: int, device="cuda", seed: int = 42,
                  grow_by: int | None = None, rotation: int = ROT_DEFAULT):
+        if value_format == TURBOPROD:
+            raise CqkvError(ERR_ARG, "turbo-quant: values use the MSE codebooks, not the prod "
+                                     "(QJL) format")
         self.k = CacheSide.empty(key_format, False, batch, kv_heads, head_dim, capacity, device,
                                  seed, rotation)
         self.v = CacheSide.empty(value_format, True, batch, kv_heads, head_dim, capacity, device,
@@ -693,6 +710,7 @@ class TurboKvCache:
         for old in (self.k, self.v):
             new = CacheSide.empty(old.fmt, old.is_value, old.batch, old.kv_heads, old.head_dim,
                                   cap, dev, old.seed, old.rotation)
+            new.qjl = old.qjl
             if self._len:
                 side_copy(new, old, self._len)
             sides.append(new)

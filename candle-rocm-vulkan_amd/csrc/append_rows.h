@@ -31,8 +31,10 @@ struct AppendArgs {
     int32_t rotate;         // Hadamard-rotate each row before encoding (side_rotates)
     uint32_t sign_bits[4];  // rotation: bit j set -> column j of the rotation has sign -1
     float rot_scale;        // rotation: 1 / sqrt(D) in f32
-    float bnd[16];          // TURBO4: the 15 codebook boundaries (+inf padded)
+    float bnd[16];          // TURBO4: the 15 codebook boundaries (+inf padded); TURBOPROD: 7
     int32_t turbo_sym;      // TURBO4: bnd[7] == 0 and bnd[14 - i] == -bnd[i] (a symmetric codebook)
+    float cent[8];          // TURBOPROD: the 3-bit centroids
+    const float *qjl;       // TURBOPROD: device D x D QJL matrix S (row-major)
     int32_t pair_loads;     // elements 2l, 2l+1 of every row are one aligned 4 / 8-byte word
     int32_t row_loads;      // rows_block: kRowBF16 / kRowF16 / kRowF32 (16-byte loads) or kRowAny
     const void *cos, *sin;  // rotary tables (cs_rows, D/2) in the dtype of x (fused RoPE only)
@@ -363,6 +365,76 @@ __device__ inline void hadamard_row32(const AppendArgs &a, int q, float (&x)[32]
 // NR token rows of plane (b, h) from cache position c0 = first tile of the range + bx * NR, by
 // the first NR * D / 32 threads of a 256-thread workgroup (all 256 threads must call it: the
 // value tiles pass through LDS). ROPE != 0 rotates each row first (the fused RoPE + append).
+// TurboProd's QJL stage for the block's rows (RowCodec::quantize_row, candle-core/src/accel/
+// turbo.rs:311-320): residual r = u - centroid[code] of the unit row u = y / norm, rsc1 = |r|,
+// and the sign bits of p = S r. p runs on v_mfma_f32_16x16x4_f32 over the residuals staged in
+// LDS: P^T (D x 16 rows) = S (D x D) R^T per wavefront and 16 rows; k-step e of a group of four
+// takes column j = 16 kk + 4 g + e in lane group g, so A (S) and B (R) are 16-byte reads. Lane
+// (row n, group g) gets p of outputs 16 bi + 4 g + e: four bits, OR-ed across g into 16.
+template <int D, int NR>
+__device__ inline void prod_qjl(const AppendArgs &a, const float (&x)[32], float inv,
+                                const uint32_t (&cw)[4], bool live, int t, int r, int q,
+                                uint8_t *scales, float *sm_resid, float *sm_cent) {
+    constexpr int R = D / 32;
+    const int tid = threadIdx.x;
+    if (tid < 8) sm_cent[tid] = a.cent[tid];
+    __syncthreads();
+    float rr = 0.0f, res[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        const uint32_t code = (cw[i / 8] >> (4 * (i % 8))) & 7u;
+        res[i] = live ? x[i] * inv - sm_cent[code] : 0.0f;
+        rr += res[i] * res[i];
+    }
+    const float r1 = __builtin_sqrtf(row_sum<R>(rr));
+    if (r < NR) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            *(f32x4 *)(sm_resid + r * D + 32 * q + 4 * i) =
+                f32x4{res[4 * i], res[4 * i + 1], res[4 * i + 2], res[4 * i + 3]};
+    }
+    if (live && q == 0) ((float *)(scales + (int64_t)a.capacity * 4))[t] = r1;
+    __syncthreads();
+    const int lane = tid & 63, wave = tid >> 6, n = lane & 15, g = lane >> 4;
+    const int pos = a.positions ? a.positions[blockIdx.z] : a.position;
+    int end = min(pos + a.tokens, a.capacity);
+    if (a.cs_rows > 0) end = min(end, a.cs_rows);
+    const int c0 = t - r;  // the block's first cache position
+    uint32_t *signs = (uint32_t *)(scales + (int64_t)a.capacity * 8);
+    constexpr int RB = NR / 16;  // 16-row blocks, spread over the four wavefronts
+    for (int rb = wave; rb < RB; rb += 4) {
+        const float *rrow = sm_resid + (16 * rb + n) * D + 4 * g;
+        const int tr = c0 + 16 * rb + n;
+        const bool row_live = tr >= pos && tr < end;
+        uint32_t word = 0;
+#pragma unroll
+        for (int bi = 0; bi < D / 16; ++bi) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            const float *srow = a.qjl + (int64_t)(16 * bi + n) * D + 4 * g;
+#pragma unroll 4
+            for (int kk = 0; kk < D / 16; ++kk) {
+                const f32x4 sa = *(const f32x4 *)(srow + 16 * kk);
+                const f32x4 rb4 = *(const f32x4 *)(rrow + 16 * kk);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(sa[e], rb4[e], acc, 0, 0, 0);
+            }
+            // acc[e] = p of output 16 bi + 4 g + e, row n
+            uint32_t nib = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) nib |= (acc[e] >= 0.0f ? 1u : 0u) << e;
+            uint32_t chunk = nib << (4 * g);
+            chunk |= (uint32_t)__shfl_xor((int)chunk, 16, 64);
+            chunk |= (uint32_t)__shfl_xor((int)chunk, 32, 64);
+            word |= chunk << (16 * (bi & 1));
+            if (bi & 1) {
+                if (g == 0 && row_live) signs[(int64_t)tr * (D / 32) + bi / 2] = word;
+                word = 0;
+            }
+        }
+    }
+}
+
 template <int FMT, int IS_VALUE, int D, int LOAD, int ROPE, int NR>
 __device__ inline void rows_block(const AppendArgs &a, int h, int b, int bx) {
     constexpr int R = D / 32, ROWS = NR;
@@ -370,6 +442,11 @@ __device__ inline void rows_block(const AppendArgs &a, int h, int b, int bx) {
     constexpr bool kB8 = FMT == CQKV_FMT_FP8 || FMT == CQKV_FMT_MXFP8;
     constexpr int kRowBytes = kB8 ? D : D / 2;  // code bytes per token
     __shared__ __attribute__((aligned(16))) uint8_t sm_codes[IS_VALUE ? ROWS * kRowBytes : 16];
+    constexpr bool kProd = FMT == CQKV_FMT_TURBOPROD;
+    static_assert(!kProd || !IS_VALUE, "TurboProd is a key format");
+    // TurboProd: the rows' residuals (f32) for the S r projection, and the 3-bit centroids
+    __shared__ __attribute__((aligned(16))) float sm_resid[kProd ? ROWS * D : 4];
+    __shared__ float sm_cent[8];
 
     const int pos = a.positions ? a.positions[b] : a.position;
     if (pos < 0) return;
@@ -527,10 +604,11 @@ __device__ inline void rows_block(const AppendArgs &a, int h, int b, int bx) {
             }
         }
         tok_scale = norm;
+        if constexpr (kProd) prod_qjl<D, NR>(a, x, inv, cw, live, t, r, q, scales, sm_resid, sm_cent);
     }
 
     // ---- scales ----
-    if constexpr (FMT == CQKV_FMT_FP8 || FMT == CQKV_FMT_TURBO4 || FMT == CQKV_FMT_NVFP4) {
+    if constexpr (FMT == CQKV_FMT_FP8 || FMT == CQKV_FMT_TURBO4 || FMT == CQKV_FMT_NVFP4 || kProd) {
         constexpr int kBlockBytes = FMT == CQKV_FMT_NVFP4 ? D / 16 : 0;
         if (live && q == 0) ((float *)(scales + (int64_t)a.capacity * kBlockBytes))[t] = tok_scale;
     }
@@ -641,7 +719,10 @@ inline void launch_rows(const cqkv_side *s, int32_t tokens, int32_t batch, hipSt
                         const AppendArgs &a) {
     const int rows = 256 / (s->head_dim / 32);
     const dim3 grid((unsigned)(((int64_t)tokens + 7 + rows - 1) / rows), s->kv_heads, batch);
-    if (s->head_dim == 64) {
+    if constexpr (FMT == CQKV_FMT_TURBOPROD) {  // keys only (check_side refuses value sides)
+        if (s->head_dim == 64) launch_rows_d<FMT, 0, 64>(a.row_loads, grid, st, a);
+        else launch_rows_d<FMT, 0, 128>(a.row_loads, grid, st, a);
+    } else if (s->head_dim == 64) {
         if (s->is_value) launch_rows_d<FMT, 1, 64>(a.row_loads, grid, st, a);
         else launch_rows_d<FMT, 0, 64>(a.row_loads, grid, st, a);
     } else {
@@ -820,7 +901,9 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendArgs r) {
     if (y < hkv) {
         rows_block<FMT, 0, D, LOAD, ROPE, kRopeBlockTokens>(r.k, y, b, bx);
     } else if (y < qy) {
-        rows_block<FMT, 1, D, LOAD, 0, kRopeBlockTokens>(r.v, y - hkv, b, bx);
+        // TurboProd keys always take values of another format, appended by their own launch
+        if constexpr (FMT != CQKV_FMT_TURBOPROD)
+            rows_block<FMT, 1, D, LOAD, 0, kRopeBlockTokens>(r.v, y - hkv, b, bx);
     } else {
 #pragma unroll
         for (int k = 0; k < 2; ++k) {  // rope_query_rows* cover 32 tokens per block index
@@ -861,6 +944,7 @@ inline void launch_rope_append_fmt(int rope, int d, dim3 grid, hipStream_t st,
                                 const AppendArgs &a);                                              \
     void rope_append_launch_##F(int rope, int d, dim3 grid, hipStream_t st, const RopeAppendArgs &r);
 CQKV_APPEND_LAUNCHERS(0)
+CQKV_APPEND_LAUNCHERS(1)
 CQKV_APPEND_LAUNCHERS(2)
 CQKV_APPEND_LAUNCHERS(3)
 CQKV_APPEND_LAUNCHERS(4)

@@ -8,6 +8,8 @@
 //   MXFP8  D/4 code words, ceil(D/32 / 4) aux words (E8M0 bytes), rsc0 = 1.0, rsc1 = 0
 //   NVFP4  D/8 code words, ceil(D/16 / 4) aux words (E4M3 block scales), rsc0 = f32 global
 //          scale, rsc1 = 0
+//   TURBOPROD (keys) 3 D/32 code words (3-bit codes, LSB first), D/32 aux words (the QJL sign
+//          bits), rsc0 = f32 norm, rsc1 = f32 |r|
 // One wavefront per 8-token tile of a (batch, head) plane; lane l owns elements 2l, 2l+1, so
 // the value tiles are read and written whole by one lane (no cross-lane read-modify-write).
 #include <algorithm>
@@ -57,6 +59,49 @@ __global__ __launch_bounds__(64) void convert_kernel(ConvertArgs a) {
             vn0 = src[0];
             vn1 = src[1];
         }
+    }
+    if (a.format == CQKV_FMT_TURBOPROD) {  // keys: row-major nibble codes, norms, |r|, sign bits
+        const int cw = 3 * D / 32, sw = D / 32;
+        const float *r1 = (const float *)(scales + (int64_t)a.capacity * 4);
+        uint32_t *signs = (uint32_t *)(scales + (int64_t)a.capacity * 8);
+        for (int t = t_lo; t < t_hi; ++t) {
+            uint32_t *row = a.rows + ((plane * a.tokens) + (t - a.position)) * (int64_t)a.row_words;
+            const uint8_t *cp = codes + (int64_t)t * (D / 2);
+            if (EXPORT) {
+                if (lane < cw) {  // word `lane`: bits [32 lane, 32 lane + 32) of the 3-bit codes
+                    uint32_t w = 0;
+                    const int j0 = (32 * lane) / 3, j1 = min((32 * lane + 31) / 3, D - 1);
+                    for (int j = j0; j <= j1; ++j) {
+                        const uint32_t c = (cp[j >> 1] >> (4 * (j & 1))) & 7u;
+                        const int bit = 3 * j - 32 * lane;  // -2 .. 31
+                        w |= bit >= 0 ? c << bit : c >> (-bit);
+                    }
+                    row[lane] = w;
+                }
+                if (lane < sw) row[cw + lane] = signs[(int64_t)t * sw + lane];
+                if (lane == 0) {
+                    row[cw + sw] = __float_as_uint(tscale[t]);
+                    row[cw + sw + 1] = __float_as_uint(r1[t]);
+                }
+            } else {
+                if (active) {  // elements 2 lane, 2 lane + 1
+                    uint32_t c[2];
+                    for (int e = 0; e < 2; ++e) {
+                        const int pos = 3 * (2 * lane + e);
+                        const uint64_t two = (uint64_t)row[pos >> 5] |
+                                             ((pos >> 5) + 1 < cw ? (uint64_t)row[(pos >> 5) + 1] << 32 : 0ull);
+                        c[e] = (uint32_t)(two >> (pos & 31)) & 7u;
+                    }
+                    codes[(int64_t)t * (D / 2) + lane] = (uint8_t)(c[0] | (c[1] << 4));
+                }
+                if (lane < sw) signs[(int64_t)t * sw + lane] = row[cw + lane];
+                if (lane == 0) {
+                    tscale[t] = __uint_as_float(row[cw + sw]);
+                    ((float *)r1)[t] = __uint_as_float(row[cw + sw + 1]);
+                }
+            }
+        }
+        return;
     }
     for (int t = t_lo; t < t_hi; ++t) {
         uint32_t *row = a.rows + ((plane * a.tokens) + (t - a.position)) * (int64_t)a.row_words;
@@ -205,7 +250,8 @@ extern "C" int cqkv_side_copy(const cqkv_side *dst, const cqkv_side *src, int32_
     if (int rc = check_side(src, who)) return rc;
     if (dst->format != src->format || dst->is_value != src->is_value ||
         dst->head_dim != src->head_dim || dst->kv_heads != src->kv_heads ||
-        side_rotates(dst) != side_rotates(src) || (side_rotates(src) && dst->seed != src->seed))
+        side_rotates(dst) != side_rotates(src) ||
+        ((side_rotates(src) || src->format == CQKV_FMT_TURBOPROD) && dst->seed != src->seed))
         return fail(CQKV_ERR_ARG,
                     "%s: sides differ in format, side, head dim, kv heads, rotation or seed", who);
     if (batch <= 0 || tokens < 0 || tokens > src->capacity || tokens > dst->capacity)
@@ -233,5 +279,15 @@ extern "C" int cqkv_side_copy(const cqkv_side *dst, const cqkv_side *src, int32_
         CQKV_HIP_CHECK(hipMemcpy2DAsync((uint8_t *)dst->scales + bb * dst->capacity, dst_sp,
                                         (const uint8_t *)src->scales + bb * src->capacity, src_sp,
                                         (size_t)4 * tokens, planes, hipMemcpyDeviceToDevice, st));
+    if (fmt == CQKV_FMT_TURBOPROD) {  // |r| and the sign bits behind the norms
+        CQKV_HIP_CHECK(hipMemcpy2DAsync((uint8_t *)dst->scales + 4 * (size_t)dst->capacity, dst_sp,
+                                        (const uint8_t *)src->scales + 4 * (size_t)src->capacity,
+                                        src_sp, (size_t)4 * tokens, planes,
+                                        hipMemcpyDeviceToDevice, st));
+        CQKV_HIP_CHECK(hipMemcpy2DAsync((uint8_t *)dst->scales + 8 * (size_t)dst->capacity, dst_sp,
+                                        (const uint8_t *)src->scales + 8 * (size_t)src->capacity,
+                                        src_sp, (size_t)(d / 8) * tokens, planes,
+                                        hipMemcpyDeviceToDevice, st));
+    }
     return CQKV_OK;
 }

@@ -31,7 +31,8 @@ inline int code_bits(int32_t format) {
     case CQKV_FMT_MXFP8: return 8;
     case CQKV_FMT_MXFP4:
     case CQKV_FMT_NVFP4:
-    case CQKV_FMT_TURBO4: return 4;
+    case CQKV_FMT_TURBO4:
+    case CQKV_FMT_TURBOPROD: return 4;  // TURBOPROD: 3-bit codes stored as nibbles
     default: return 0;
     }
 }
@@ -46,7 +47,13 @@ inline int block_elems(int32_t format) {
 // Formats with an f32 scale per token (FP8 absmax/448, TurboQuant norm, NVFP4 global scale);
 // in the scales plane it follows the block-scale bytes of all `capacity` tokens.
 inline bool token_scale(int32_t format) {
-    return format == CQKV_FMT_FP8 || format == CQKV_FMT_TURBO4 || format == CQKV_FMT_NVFP4;
+    return format == CQKV_FMT_FP8 || format == CQKV_FMT_TURBO4 || format == CQKV_FMT_NVFP4 ||
+           format == CQKV_FMT_TURBOPROD;
+}
+
+// TurboQuant formats (codebook codes of the rotated unit row times its norm).
+inline bool is_turbo(int32_t format) {
+    return format == CQKV_FMT_TURBO4 || format == CQKV_FMT_TURBOPROD;
 }
 
 inline bool supported_dim(int32_t d) { return d == 64 || d == 128; }
@@ -54,7 +61,7 @@ inline bool supported_dim(int32_t d) { return d == 64 || d == 128; }
 // The side's rows are Hadamard-rotated before quantization (CQKV_ROT_DEFAULT: TURBO4 only).
 inline bool side_rotates(const cqkv_side *s) {
     return s->rotation == CQKV_ROT_HADAMARD ||
-           (s->rotation == CQKV_ROT_DEFAULT && s->format == CQKV_FMT_TURBO4);
+           (s->rotation == CQKV_ROT_DEFAULT && is_turbo(s->format));
 }
 
 // Validates a cache side; returns CQKV_OK or an error (message set).
@@ -63,5 +70,6 @@ int check_side(const cqkv_side *s, const char *what);
 // Host tables of the TurboQuant format (see cqkv.h).
 int turbo_codebook(int dim, int bits, float *centroids, float *boundaries);
 void turbo_signs(int dim, uint64_t seed, float *signs);
+void qjl_matrix(int dim, uint64_t seed, float *out);
 
 }  // namespace cqkv

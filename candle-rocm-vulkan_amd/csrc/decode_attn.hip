@@ -163,7 +163,7 @@ static int decode_prepare(DecodeArgs &a, const char *who, const void *q, int32_t
     // queries, for the bf16 key formats); TurboQuant keys take the rotated queries as one f16
     // operand (2^-12 relative rounding: config 5 216-225 -> 208-220 us same-box, its parity tests
     // unchanged)
-    a.q_split = k->format != CQKV_FMT_TURBO4 && (q_dtype != CQKV_BF16 || a.rot_k) ? 1 : 0;
+    a.q_split = !is_turbo(k->format) && (q_dtype != CQKV_BF16 || a.rot_k) ? 1 : 0;
     a.o_sb = out_strides[0];
     a.o_sh = out_strides[1];
     a.o_si = out_strides[2];
@@ -176,6 +176,13 @@ static int decode_prepare(DecodeArgs &a, const char *who, const void *q, int32_t
         if (turbo_codebook(d, 4, cent, bnd) != 0)
             return fail(CQKV_ERR_ARG, "%s: turbo codebook D=%d", who, d);
         for (int i = 0; i < 16; ++i) a.cent[i] = cent[i];
+    }
+    if (k->format == CQKV_FMT_TURBOPROD) {  // the 3-bit codebook and S of the keys
+        float bnd[16], cent[16];
+        if (turbo_codebook(d, 3, cent, bnd) != 0)
+            return fail(CQKV_ERR_ARG, "%s: turbo codebook D=%d", who, d);
+        for (int i = 0; i < 8; ++i) a.kcent[i] = cent[i];
+        a.qjl = k->qjl;
     }
     return CQKV_OK;
 }
@@ -191,6 +198,7 @@ static hipError_t decode_launch(const DecodeArgs &a, int kf, int vf, int d, hipS
     case CQKV_FMT_MXFP4: decode_launch_k2(vf, d, grid, st, a); break;
     case CQKV_FMT_MXFP8: decode_launch_k4(vf, d, grid, st, a); break;
     case CQKV_FMT_NVFP4: decode_launch_k3(vf, d, grid, st, a); break;
+    case CQKV_FMT_TURBOPROD: decode_launch_k1(vf, d, grid, st, a); break;
     default: decode_launch_k0(vf, d, grid, st, a); break;
     }
     hipError_t e = hipGetLastError();
@@ -476,10 +484,11 @@ static int check_blocks(const cqkv_kv_block *blocks, int32_t n_blocks, int32_t b
             bl.k->is_value != 0 || bl.v->is_value != 1 || side_rotates(bl.k) != side_rotates(b0.k) ||
             side_rotates(bl.v) != side_rotates(b0.v) ||
             (side_rotates(b0.k) && bl.k->seed != b0.k->seed) ||
-            (side_rotates(b0.v) && bl.v->seed != b0.v->seed))
+            (side_rotates(b0.v) && bl.v->seed != b0.v->seed) ||
+            (b0.k->format == CQKV_FMT_TURBOPROD && bl.k->qjl != b0.k->qjl))
             return fail(CQKV_ERR_ARG,
                         "%s: block %d differs from block 0 in format, head dim, kv heads, side, "
-                        "rotation or seed",
+                        "rotation, seed or QJL matrix",
                         who, i);
         if (bl.rows < 0 || bl.rows > bl.k->capacity || bl.rows > bl.v->capacity)
             return fail(CQKV_ERR_ARG, "%s: block %d has %d rows but capacities %d / %d", who, i,

@@ -77,7 +77,11 @@ struct DecodeArgs {
     float rot_scale;                        // 1 / sqrt(D)
     float cent[16];  // TURBO4 codebook (the same for keys and values at one head dim)
     const PagedSeg *segs;  // paged: one segment per split (the planes above are unused)
+    const float *qjl;      // TURBOPROD keys: the D x D QJL matrix S (device, row-major)
+    float kcent[8];        // TURBOPROD keys: the 3-bit codebook
 };
+
+constexpr float kQjlConst = 1.2533141f;  // sqrt(pi / 2) as the reference's QJL_CONST (turbo.rs:26)
 
 // Visible keys [lo, hi) of query i of lq over lk keys (bottom-right aligned).
 __device__ inline void key_range(int i, int lq, int lk, int wl, int wr, int &lo, int &hi) {
@@ -136,6 +140,9 @@ struct Tile {
     // NVFP4: the value block bytes (two words per key at D = 128, one at D = 64) and f32 scales
     // of keys 8 g .. 8 g + 7, read directly (config-2 shape 100-103 -> 99 us same-box)
     uint32_t nvb[D == 128 ? 16 : 8], nvg[8];
+    // TURBOPROD keys: |r| of keys 8 g .. 8 g + 7, and per sub-tile the lane key's sign bits of
+    // its head dims (D / 4 bits: dims (D / 4) g ..)
+    uint32_t kr1[8], ksg[2];
 };
 
 // Formats whose per-key scale words are read as ks8 / vs8 (one 32-bit word per key). Same-box
@@ -220,7 +227,21 @@ __device__ inline void load_tile(Tile<KF, VF, D> &r, int tile, bool live, int la
         }
     }
     const uint32_t kl = t0 + (lane & 31);
-    if constexpr (KF == CQKV_FMT_TURBO4) load_scales8<4>(r.ks8, ksr, t0 + 8 * g, oob);
+    if constexpr (KF == CQKV_FMT_TURBO4 || KF == CQKV_FMT_TURBOPROD)
+        load_scales8<4>(r.ks8, ksr, t0 + 8 * g, oob);
+    if constexpr (KF == CQKV_FMT_TURBOPROD) {
+        // the scales plane: norms, |r| (at cap * 4), sign bits (at cap * 8, D / 8 per key)
+        const uint32_t cap = ktok_off;  // load_tile's caller passes the capacity here
+        load_scales8<4>(r.kr1, ksr, cap + t0 + 8 * g, oob);
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            const uint32_t key = t0 + 8 * (n >> 2) + 4 * s2 + (n & 3);
+            if constexpr (D == 128)
+                r.ksg[s2] = ld32(ksr, (cap * 8 + key * 16 + 4 * g) | oob);
+            else
+                r.ksg[s2] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(ksr, (cap * 8 + key * 8 + 2 * g) | oob, 0, 0);
+        }
+    }
     if constexpr (direct_scales<VF>()) {
         load_scales8<4>(r.vs8, vsr, t0 + 8 * g, oob);
     } else if constexpr (VF == CQKV_FMT_MXFP4 || VF == CQKV_FMT_MXFP8) {
@@ -255,14 +276,34 @@ __device__ inline uint32_t fp4x2_to_bf16x2(uint32_t w, int byte_sel, float scale
 // MFMA operand type: bf16 for FP8 / MXFP4 (their codes decode exactly), f16 for TurboQuant
 // (codebook values, rotated queries: 11 significant bits instead of 8).
 template <int FMT>
-using op_t = typename std::conditional<FMT == CQKV_FMT_TURBO4, f16x8, bf16x8>::type;
+using op_t = typename std::conditional<FMT == CQKV_FMT_TURBO4 || FMT == CQKV_FMT_TURBOPROD, f16x8,
+                                      bf16x8>::type;
+
+typedef __attribute__((address_space(3))) const uint32_t lds_u32;
+
+// TurboProd key codes: the f16 pair of code byte b (codes b & 7, b >> 4 & 7) from a compact 16 KB
+// table, entry (lo + 8 hi, l) at byte 256 (lo + 8 hi) + 4 l (a copy per lane, as turbo_pair).
+template <int I>
+__device__ inline uint32_t prod_pair(uint32_t ktab, uint32_t w) {
+    const uint32_t b = (w >> (8 * I)) & 0xffu;
+    const uint32_t idx = (b & 7u) | ((b >> 1) & 0x38u);
+    return *(lds_u32 *)(size_t)(ktab + (idx << 8));
+}
+// 8 sign bits -> 8 f16 operands +1 (bit set) / -1
+__device__ inline f16x8 signs_f16x8(uint32_t bits8) {
+    u32x4 r;
+    uint32_t *rp = (uint32_t *)&r;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        rp[k] = 0xBC00BC00u ^ (((bits8 >> (2 * k)) & 1u) << 15) ^ (((bits8 >> (2 * k + 1)) & 1u) << 31);
+    return __builtin_bit_cast(f16x8, r);
+}
 
 // TurboQuant codebook lookups: code byte b (codes b & 15, b >> 4) of lane l reads the f16 pair of
 // entry (b, l) at byte 256 b + 4 l of a 64 KB LDS table, a copy per lane, so every lane reads
 // its own bank (random codes through one shared 1 KB table cost several passes per read in bank
 // conflicts). The table is 64 KB-aligned and tab = its address + 4 l, so the address of byte I
 // of code word w is tab with w's byte I as byte 1: one byte permute.
-typedef __attribute__((address_space(3))) const uint32_t lds_u32;
 template <int I>
 __device__ inline uint32_t turbo_pair(uint32_t tab, uint32_t w) {
     // v_perm_b32 selector bytes: 0-3 pick bytes of the second operand (tab), 4-7 of the first (w)
@@ -341,7 +382,7 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
                                     const op_t<KF> *qhi, const op_t<KF> *qlo, bool q_split, int lane,
                                     int lo, int hi, int lo_max, int hi_min, int L, int koff,
                                     uint32_t tab, float &m_run, float &l_run,
-                                    f32x4 *acc) {
+                                    f32x4 *acc, const op_t<KF> *qsop, uint32_t ktab) {
     constexpr int NCH = D / 32;
     const int g = lane >> 4;
     // tile and L are rows of the current block (the whole cache when not paged); keys of the
@@ -349,8 +390,9 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
     const int t0 = tile * 32;
     const bool full = koff + t0 >= lo_max && koff + t0 + 32 <= hi_min && t0 + 32 <= L;
 
-    // S^T = K Q^T for the two 16-key sub-tiles
+    // S^T = K Q^T for the two 16-key sub-tiles (TurboProd: and Z (S q)^T, the QJL sign dots)
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+    f32x4 z0 = {0.f, 0.f, 0.f, 0.f}, z1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
         op_t<KF> k0, k1;
@@ -379,11 +421,26 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
                 sc0 = cur.kscale[0] ? __uint_as_float(cur.kscale[0] << 23) : 1.0f;
                 sc1 = cur.kscale[1] ? __uint_as_float(cur.kscale[1] << 23) : 1.0f;
             }
-            k0 = decode8<KF>(cur.k[0][j], 0, sc0, tab);
-            k1 = decode8<KF>(cur.k[1][j], 0, sc1, tab);
+            if constexpr (KF == CQKV_FMT_TURBOPROD) {
+                k0 = __builtin_bit_cast(op_t<KF>, u32x4{prod_pair<0>(ktab, cur.k[0][j]),
+                                                        prod_pair<1>(ktab, cur.k[0][j]),
+                                                        prod_pair<2>(ktab, cur.k[0][j]),
+                                                        prod_pair<3>(ktab, cur.k[0][j])});
+                k1 = __builtin_bit_cast(op_t<KF>, u32x4{prod_pair<0>(ktab, cur.k[1][j]),
+                                                        prod_pair<1>(ktab, cur.k[1][j]),
+                                                        prod_pair<2>(ktab, cur.k[1][j]),
+                                                        prod_pair<3>(ktab, cur.k[1][j])});
+            } else {
+                k0 = decode8<KF>(cur.k[0][j], 0, sc0, tab);
+                k1 = decode8<KF>(cur.k[1][j], 0, sc1, tab);
+            }
         }
         s0 = mfma16x16x32(k0, qhi[j], s0);
         s1 = mfma16x16x32(k1, qhi[j], s1);
+        if constexpr (KF == CQKV_FMT_TURBOPROD) {  // byte j of the lane key's sign bits
+            z0 = mfma16x16x32(signs_f16x8((cur.ksg[0] >> (8 * j)) & 0xffu), qsop[j], z0);
+            z1 = mfma16x16x32(signs_f16x8((cur.ksg[1] >> (8 * j)) & 0xffu), qsop[j], z1);
+        }
         if (q_split) {
             s0 = mfma16x16x32(k0, qlo[j], s0);
             s1 = mfma16x16x32(k1, qlo[j], s1);
@@ -391,7 +448,15 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
     }
     float x[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
     const int kbase = t0 + 8 * g;  // x[e] is key kbase + e
-    if constexpr (KF != CQKV_FMT_TURBO4) {  // scales are inside the operands
+    if constexpr (KF == CQKV_FMT_TURBOPROD) {
+        // r0 (q . c + r1 sqrt(pi / 2) / D (S q) . z) (turbo_quant_impl.h:268-276)
+        const float zk[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
+        constexpr float kc = kQjlConst / D;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            x[e] = (x[e] + __uint_as_float(cur.kr1[e]) * kc * zk[e]) *
+                   __uint_as_float(cur.ks8[e]) * a.scale_log2;
+    } else if constexpr (KF != CQKV_FMT_TURBO4) {  // scales are inside the operands
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] *= a.scale_log2;
     } else {
@@ -568,6 +633,9 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
     float(*sm_o)[16][D] = (float(*)[16][D])sm_buf;
     uint32_t *sm_tab = (uint32_t *)sm_buf;
     __shared__ float sm_m[WAVES][16], sm_l[WAVES][16];
+    constexpr bool kProd = KF == CQKV_FMT_TURBOPROD;
+    // TurboProd keys: the compact 3-bit code-pair table (64 entries x 64 lanes)
+    __shared__ uint32_t sm_ktab[kProd ? 64 * 64 : 1];
 
     // 1-D grid, plane fastest: workgroup ids are dealt round-robin to the 8 XCDs, so with
     // kv_heads a multiple of 8 each XCD takes whole planes of one kv head from every sequence -
@@ -644,13 +712,44 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
         }
         __syncthreads();
     }
-    op_t<KF> qhi[NCH], qlo[NCH];
+    op_t<KF> qhi[NCH], qlo[NCH], qsop[kProd ? NCH : 1];
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
         float qv[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) qv[e] = sm_q[n][qdim<KF, D>(j, g, e)];
         split8(qv, qhi[j], qlo[j]);
+    }
+    if constexpr (kProd) {
+        // S q of the (rotated) queries on v_mfma_f32_16x16x4_f32: (S q)^T (D x 16) = S Q^T,
+        // 16 outputs per wavefront step; k-step e of a group of four takes column
+        // 16 kk + 4 g + e in lane group g (16-byte reads of S and of the queries)
+        float(*sm_qs)[D] = sm_o[1];
+        for (int bi = wave; bi < D / 16; bi += WAVES) {
+            f32x4 acc2 = {0.f, 0.f, 0.f, 0.f};
+            const float *srow = a.qjl + (int64_t)(16 * bi + n) * D + 4 * g;
+#pragma unroll 4
+            for (int kk = 0; kk < D / 16; ++kk) {
+                const f32x4 sa = *(const f32x4 *)(srow + 16 * kk);
+                const f32x4 qb = *(const f32x4 *)(&sm_q[n][16 * kk + 4 * g]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(sa[e], qb[e], acc2, 0, 0, 0);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sm_qs[n][16 * bi + 4 * g + e] = acc2[e];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) {
+            float qv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qv[e] = sm_qs[n][qdim<KF, D>(j, g, e)];
+            op_t<KF> lo_unused;
+            split8(qv, qsop[j], lo_unused);
+        }
+        for (int i = threadIdx.x; i < 64 * 64; i += NT)
+            sm_ktab[i] = pack_f16x2(a.kcent[(i >> 6) & 7], a.kcent[i >> 9]);
     }
     const bool q_split = a.q_split != 0;
     __syncthreads();
@@ -669,12 +768,14 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
     // NVFP4: the per-token f32 scales follow the block bytes of all the plane's tokens
     uint32_t ktok_off = 0, vtok_off = 0;
     if constexpr (KF == CQKV_FMT_NVFP4) ktok_off = ks_plane / (D / 16 + 4) * (D / 16);
+    if constexpr (kProd) ktok_off = ks_plane / (8 + D / 8);  // load_tile reads the capacity here
     if constexpr (VF == CQKV_FMT_NVFP4) vtok_off = vs_plane / (D / 16 + 4) * (D / 16);
 
     f32x4 acc[2 * NCH];
 #pragma unroll
     for (int t = 0; t < 2 * NCH; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     const uint32_t tab = (uint32_t)(size_t)sm_tab + 4 * lane;
+    const uint32_t ktab = (uint32_t)(size_t)sm_ktab + 4 * lane;
     float m_run = -__builtin_inff(), l_run = 0.0f;
 
     // Register sets A and B alternate; the scheduling barriers keep every load of one set
@@ -687,13 +788,13 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
     __builtin_amdgcn_sched_barrier(0);
     for (; t < te; t += 2 * WAVES) {
         compute_tile<KF, VF, D>(ta, t, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min, Lb, koff, tab,
-                             m_run, l_run, acc);
+                             m_run, l_run, acc, kProd ? qsop : qhi, ktab);
         __builtin_amdgcn_sched_barrier(0);
         load_tile<KF, VF, D>(ta, t + 2 * WAVES, t + 2 * WAVES < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
         __builtin_amdgcn_sched_barrier(0);
         if (t + WAVES < te)
             compute_tile<KF, VF, D>(tb2, t + WAVES, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min,
-                                 Lb, koff, tab, m_run, l_run, acc);
+                                 Lb, koff, tab, m_run, l_run, acc, kProd ? qsop : qhi, ktab);
         __builtin_amdgcn_sched_barrier(0);
         load_tile<KF, VF, D>(tb2, t + 3 * WAVES, t + 3 * WAVES < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
         __builtin_amdgcn_sched_barrier(0);
@@ -781,6 +882,7 @@ inline void launch_decode_k(int vf, int d, dim3 grid, hipStream_t st, const Deco
 #define CQKV_DECODE_LAUNCHER(F) \
     void decode_launch_k##F(int vf, int d, dim3 grid, hipStream_t st, const DecodeArgs &a);
 CQKV_DECODE_LAUNCHER(0)
+CQKV_DECODE_LAUNCHER(1)
 CQKV_DECODE_LAUNCHER(2)
 CQKV_DECODE_LAUNCHER(3)
 CQKV_DECODE_LAUNCHER(4)

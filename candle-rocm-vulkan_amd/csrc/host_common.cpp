@@ -42,6 +42,12 @@ int check_side(const cqkv_side *s, const char *what) {
         return fail(CQKV_ERR_ARG, "%s: is_value must be 0 or 1", what);
     if (s->rotation < CQKV_ROT_DEFAULT || s->rotation > CQKV_ROT_HADAMARD)
         return fail(CQKV_ERR_ARG, "%s: rotation %d (default, none or Hadamard)", what, s->rotation);
+    if (s->format == CQKV_FMT_TURBOPROD) {
+        if (s->is_value)
+            return fail(CQKV_ERR_ARG,
+                        "%s: TURBOPROD is a key format (values use the MSE codebooks)", what);
+        if (!s->qjl) return fail(CQKV_ERR_ARG, "%s: TURBOPROD side without its QJL matrix", what);
+    }
     const size_t cb = cqkv_codes_plane_bytes(s->format, s->head_dim, s->capacity);
     if (cb > 0x7fffffffull)
         return fail(CQKV_ERR_ARG, "%s: a plane of %zu bytes exceeds 2 GiB", what, cb);
@@ -146,6 +152,26 @@ void turbo_signs(int dim, uint64_t seed, float *signs) {
     }
 }
 
+// The QJL matrix: SplitMix64 at (seed + 1) ^ "QJL_SKET", one Box-Muller normal (two uniforms
+// ((u >> 11) + 0.5) / 2^53, f64 log / sqrt / cos) per entry, rounded to f32
+// (candle-core/src/accel/turbo.rs:150-176, 236-239).
+void qjl_matrix(int dim, uint64_t seed, float *out) {
+    uint64_t state = (seed + 1) ^ 0x514a4c5f534b4554ull;
+    auto next = [&state]() {
+        state += 0x9e3779b97f4a7c15ull;
+        uint64_t z = state;
+        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+        z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+        return z ^ (z >> 31);
+    };
+    const double two_pi = 2.0 * 3.141592653589793;
+    for (size_t i = 0; i < (size_t)dim * dim; ++i) {
+        const double u1 = ((double)(next() >> 11) + 0.5) / 9007199254740992.0;
+        const double u2 = ((double)(next() >> 11) + 0.5) / 9007199254740992.0;
+        out[i] = (float)(sqrt(-2.0 * log(u1)) * cos(two_pi * u2));
+    }
+}
+
 }  // namespace cqkv
 
 extern "C" {
@@ -158,6 +184,8 @@ size_t cqkv_codes_plane_bytes(int32_t format, int32_t head_dim, int32_t capacity
 
 size_t cqkv_scales_plane_bytes(int32_t format, int32_t head_dim, int32_t capacity) {
     if (!cqkv::code_bits(format) || !cqkv::supported_dim(head_dim) || capacity <= 0) return 0;
+    if (format == CQKV_FMT_TURBOPROD)  // norms, |r|, sign bits
+        return (size_t)capacity * (8 + (size_t)head_dim / 8);
     const int be = cqkv::block_elems(format);
     const size_t blocks = be ? (size_t)capacity * (size_t)(head_dim / be) : 0;
     return blocks + (cqkv::token_scale(format) ? (size_t)capacity * 4 : 0);
@@ -166,6 +194,8 @@ size_t cqkv_scales_plane_bytes(int32_t format, int32_t head_dim, int32_t capacit
 int32_t cqkv_reference_row_words(int32_t format, int32_t head_dim) {
     const int bits = cqkv::code_bits(format);
     if (!bits || !cqkv::supported_dim(head_dim)) return 0;
+    if (format == CQKV_FMT_TURBOPROD)  // 3-bit codes, D sign bits (formats.rs:226-240)
+        return (head_dim * 3 + 31) / 32 + (head_dim + 31) / 32 + 2;
     const int code_words = (head_dim * bits + 31) / 32;
     const int be = cqkv::block_elems(format);
     const int aux_words = be ? (head_dim / be + 3) / 4 : 0;  // formats.rs:229-233
@@ -184,6 +214,13 @@ int cqkv_turbo_signs(int32_t head_dim, uint64_t seed, float *signs) {
     if (!signs || head_dim <= 0 || (head_dim & (head_dim - 1)) != 0)
         return cqkv::fail(CQKV_ERR_ARG, "cqkv_turbo_signs: head_dim %d", head_dim);
     cqkv::turbo_signs(head_dim, seed, signs);
+    return CQKV_OK;
+}
+
+int cqkv_qjl_matrix(int32_t head_dim, uint64_t seed, float *out) {
+    if (!out || head_dim <= 0 || head_dim > 1024)
+        return cqkv::fail(CQKV_ERR_ARG, "cqkv_qjl_matrix: head_dim %d / null output", head_dim);
+    cqkv::qjl_matrix(head_dim, seed, out);
     return CQKV_OK;
 }
 

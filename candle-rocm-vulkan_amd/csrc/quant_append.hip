@@ -27,11 +27,15 @@ void fill_rotation(const cqkv_side *s, uint32_t sign_bits[4], float *rot_scale) 
 }
 
 // The TurboQuant-4 codebook boundaries of the side's head dim (+inf padded to 16).
-int fill_turbo_bounds(const cqkv_side *s, float bnd[16]) {
+int fill_turbo_bounds(const cqkv_side *s, float bnd[16], float *cent_out) {
     float cent[16];
     for (int i = 0; i < 16; ++i) bnd[i] = __builtin_inff();
-    if (turbo_codebook(s->head_dim, 4, cent, bnd) != 0)
+    // TurboMse{4}: the 4-bit codebook; TurboProd{4}: the 3-bit one (code bits = bits - 1)
+    const int bits = s->format == CQKV_FMT_TURBOPROD ? 3 : 4;
+    if (turbo_codebook(s->head_dim, bits, cent, bnd) != 0)
         return fail(CQKV_ERR_ARG, "turbo codebook for D=%d", s->head_dim);
+    if (cent_out)
+        for (int i = 0; i < (1 << bits); ++i) cent_out[i] = cent[i];
     return CQKV_OK;
 }
 
@@ -72,8 +76,12 @@ static int fill_append_args(AppendArgs &a, const cqkv_side *side, const void *x,
     a.rotate = side_rotates(side) ? 1 : 0;
     fill_rotation(side, a.sign_bits, &a.rot_scale);
     if (side->format == CQKV_FMT_TURBO4) {
-        if (int rc = fill_turbo_bounds(side, a.bnd)) return rc;
+        if (int rc = fill_turbo_bounds(side, a.bnd, nullptr)) return rc;
         a.turbo_sym = turbo_symmetric(a.bnd);
+    } else if (side->format == CQKV_FMT_TURBOPROD) {
+        if (int rc = fill_turbo_bounds(side, a.bnd, a.cent)) return rc;
+        a.turbo_sym = 0;  // 7 boundaries: the general count
+        a.qjl = side->qjl;
     }
     return CQKV_OK;
 }
@@ -93,6 +101,7 @@ int quant_append_launch(const cqkv_side *side, const void *x, int32_t x_dtype,
     case CQKV_FMT_MXFP4: append_rows_launch_2(side, tokens, batch, stream, a); break;
     case CQKV_FMT_MXFP8: append_rows_launch_4(side, tokens, batch, stream, a); break;
     case CQKV_FMT_NVFP4: append_rows_launch_3(side, tokens, batch, stream, a); break;
+    case CQKV_FMT_TURBOPROD: append_rows_launch_1(side, tokens, batch, stream, a); break;
     default: append_rows_launch_0(side, tokens, batch, stream, a); break;
     }
     CQKV_HIP_CHECK(hipGetLastError());
@@ -187,6 +196,7 @@ extern "C" int cqkv_rope_quant_append(const cqkv_side *k_side, const cqkv_side *
     switch (k_side->format) {
     case CQKV_FMT_FP8: rope_append_launch_5(rope_kind, d, grid, st, r); break;
     case CQKV_FMT_MXFP4: rope_append_launch_2(rope_kind, d, grid, st, r); break;
+    case CQKV_FMT_TURBOPROD: rope_append_launch_1(rope_kind, d, grid, st, r); break;
     case CQKV_FMT_MXFP8: rope_append_launch_4(rope_kind, d, grid, st, r); break;
     case CQKV_FMT_NVFP4: rope_append_launch_3(rope_kind, d, grid, st, r); break;
     default: rope_append_launch_0(rope_kind, d, grid, st, r); break;

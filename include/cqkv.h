@@ -81,11 +81,21 @@ enum {
 
 /* Cache formats: the reference's kernel mode ids (candle-core/src/accel/formats.rs:41-48).
  * TURBO4 = TurboQuant MSE, 4 bits, Hadamard rotation (QuantFormat::TurboMse{bits: 4});
+ * TURBOPROD = TurboQuant prod, 4 bits (QuantFormat::TurboProd{bits: 4}, keys only): 3-bit MSE
+ * codes of the rotated unit row, plus the sign bits of S r (r = the residual of the unit row to
+ * its centroids, S = cqkv_qjl_matrix(D, seed)) and |r| - an unbiased inner-product estimate
+ * (RowCodec::quantize_row, candle-core/src/accel/turbo.rs:299-323);
  * NVFP4 = E2M1 codes, an E4M3 scale per 16 elements and an f32 scale per token
  * (QuantFormat::Nvfp4); MXFP8 = E4M3 codes with an E8M0 scale per 32 elements
- * (QuantFormat::Mxfp8). */
+ * (QuantFormat::Mxfp8).
+ * Plane layouts (per (batch, kv head), `capacity` tokens): codes are D bytes (8-bit formats) or
+ * D/2 bytes (4-bit; TURBOPROD's 3-bit codes as nibbles) per token, keys row-major and values in
+ * 8-token tiles; scales are the block-scale bytes of every token, then an f32 per token (FP8
+ * scale, TurboQuant norm, NVFP4 global scale); TURBOPROD scales: the norms, then |r| (f32 per
+ * token), then D/8 sign-bit bytes per token (bit i of word i / 32 = sign of (S r)_i >= 0). */
 enum {
     CQKV_FMT_TURBO4 = 0,
+    CQKV_FMT_TURBOPROD = 1,
     CQKV_FMT_MXFP4 = 2,
     CQKV_FMT_NVFP4 = 3,
     CQKV_FMT_MXFP8 = 4,
@@ -103,7 +113,8 @@ enum { CQKV_ROPE_HALVES = 1, CQKV_ROPE_INTERLEAVED = 2 };
  * 104-139, TurboQuantizer::rotate, candle-nn/src/turbo_quant.rs:182-189). DEFAULT is the format's
  * own: Hadamard for TURBO4, none for the others. HADAMARD = the sign-flipped Sylvester matrix / sqrt(D)
  * of `seed` (rotation_matrix, candle-core/src/accel/turbo.rs:180-203; what RotationKind::Auto
- * resolves to for the power-of-two head dims here). The cache stores codes of the rotated rows;
+ * resolves to for the power-of-two head dims here; DEFAULT rotates TURBOPROD sides as well).
+ * The cache stores codes of the rotated rows;
  * decode rotates the queries with the key side's rotation and unrotates the output with the
  * value side's. */
 enum { CQKV_ROT_DEFAULT = 0, CQKV_ROT_NONE = 1, CQKV_ROT_HADAMARD = 2 };
@@ -119,7 +130,14 @@ typedef struct cqkv_side {
     uint64_t seed;     /* rotation seed (keys 42, values 44 by default); unused without rotation */
     void *codes;       /* device, batch * kv_heads planes of cqkv_codes_plane_bytes() */
     void *scales;      /* device, batch * kv_heads planes of cqkv_scales_plane_bytes() */
+    const float *qjl;  /* TURBOPROD: device D x D f32 QJL matrix S (row-major, cqkv_qjl_matrix
+                          of the side's seed); NULL for the other formats */
 } cqkv_side;
+
+/* The QJL projection S of TurboProd: D x D row-major f32 standard normals from SplitMix64 seeded
+ * with (seed + 1) ^ 0x514a4c5f534b4554, Box-Muller in f64 (qjl_matrix,
+ * candle-core/src/accel/turbo.rs:236-239). Host memory; upload it for cqkv_side.qjl. */
+int cqkv_qjl_matrix(int32_t head_dim, uint64_t seed, float *out);
 
 /* Bytes of one (batch, head) plane of codes / scales; 0 for an invalid format or D. */
 size_t cqkv_codes_plane_bytes(int32_t format, int32_t head_dim, int32_t capacity);

@@ -6,7 +6,8 @@ import torch
 
 from oracle import oracle as O
 
-BITS = {5: 0, 2: 0, 0: 4, 3: 0, 4: 0}  # oracle (mode, bits): FP8, MXFP4, TURBO4, NVFP4, MXFP8
+BITS = {5: 0, 2: 0, 0: 4, 3: 0, 4: 0, 1: 4}  # oracle (mode, bits): FP8, MXFP4, TURBO4, NVFP4,
+# MXFP8, TURBOPROD
 
 
 def kv_source(seed: int, shape, outliers: bool = False) -> torch.Tensor:
@@ -23,8 +24,8 @@ def kv_source(seed: int, shape, outliers: bool = False) -> torch.Tensor:
 
 def rotates(fmt: int, rotation: int = 0) -> bool:
     """Whether a cache side of `fmt` stores rotated rows under cqkv rotation `rotation`
-    (0 default: TURBO4 only, 1 none, 2 Hadamard)."""
-    return rotation == 2 or (rotation == 0 and fmt == 0)
+    (0 default: TurboQuant formats only, 1 none, 2 Hadamard)."""
+    return rotation == 2 or (rotation == 0 and fmt in (0, 1))
 
 
 def oracle_rows(fmt: int, x: torch.Tensor, seed: int = 0, rotation: int = 0) -> np.ndarray:
@@ -34,6 +35,8 @@ def oracle_rows(fmt: int, x: torch.Tensor, seed: int = 0, rotation: int = 0) -> 
     if rotates(fmt, rotation):
         pi = O.rotation_matrix(x.shape[-1], O.ROT_HADAMARD, seed)
         xf = O.rotate_rows(pi, xf.reshape(-1, x.shape[-1])).reshape(xf.shape)
+    if fmt == 1:
+        return O.quantize_rows_qjl(4, xf, O.qjl_matrix(x.shape[-1], seed))
     return O.quantize_rows(fmt, BITS[fmt], xf)
 
 
@@ -47,8 +50,9 @@ def oracle_decode(fmt: int, q: torch.Tensor, k_rows: np.ndarray, v_rows: np.ndar
     pk = O.rotation_matrix(d, O.ROT_HADAMARD, k_seed) if rotates(fmt, rotation) else None
     pv = O.rotation_matrix(d, O.ROT_HADAMARD, v_seed) if rotates(v_fmt, rotation) else None
     qb = O.f32_to_bf16_bits(q.float().numpy())
+    sk = O.qjl_matrix(d, k_seed) if fmt == 1 else None
     out = O.cache_attention(qb, k_rows, v_rows, (fmt, BITS[fmt]), (v_fmt, BITS[v_fmt]), pk, pv,
-                            lk, scale, kv_lens=kv_lens, wl=wl, wr=wr, threads=16)
+                            lk, scale, kv_lens=kv_lens, wl=wl, wr=wr, threads=16, qjl_k=sk)
     return O.round_bf16(out)
 
 
@@ -68,7 +72,11 @@ def exact_decode(fmt: int, q: torch.Tensor, k_rows: np.ndarray, v_rows: np.ndarr
     b, hq, lq, d = q.shape
     v_fmt = fmt if v_fmt is None else v_fmt
     hkv = k_rows.shape[1]
-    kd = O.dequantize_rows(fmt, BITS[fmt], d, k_rows[:, :, :lk]).astype(np.float64)
+    if fmt == 1:
+        kd = O.dequantize_rows_qjl(4, d, k_rows[:, :, :lk], O.qjl_matrix(d, k_seed))
+        kd = kd.astype(np.float64)
+    else:
+        kd = O.dequantize_rows(fmt, BITS[fmt], d, k_rows[:, :, :lk]).astype(np.float64)
     vd = O.dequantize_rows(v_fmt, BITS[v_fmt], d, v_rows[:, :, :lk]).astype(np.float64)
     if rotates(fmt, rotation):
         kd = kd @ O.rotation_matrix(d, O.ROT_HADAMARD, k_seed).astype(np.float64)
@@ -174,12 +182,44 @@ def assert_rotated_rows_close(fmt: int, got: np.ndarray, want: np.ndarray, d: in
     assert (np.abs(gc - wc)[same] <= 1).all()
 
 
+def assert_prod_rows_close(got: np.ndarray, want: np.ndarray, d: int):
+    """TurboProd{4} rows against the reference encoder's: the 3-bit codes and the norm by the
+    TurboQuant criterion (<= 0.1 % code flips to a neighbour, norms rtol 1e-5); in rows without a
+    code flip |r| within rtol 1e-4 and the QJL sign bits equal but for <= 0.1 % (a projection of
+    the residual within rounding of zero; the reference leaves the matmul's summation order
+    open)."""
+    lay = O.row_layout(1, 4, d)
+    cw, aw = lay.code_words, lay.aux_words
+
+    def codes(rows):
+        out = np.zeros(rows.shape[:-1] + (d,), dtype=np.int64)
+        for j in range(d):
+            for bit in range(3):
+                pos = 3 * j + bit
+                out[..., j] |= ((rows[..., pos // 32] >> (pos % 32)) & 1).astype(np.int64) << bit
+        return out
+    gc, wc = codes(got), codes(want)
+    flips = gc != wc
+    assert flips.sum() <= max(2, gc.size // 1000), flips.sum()
+    assert (np.abs(gc - wc) <= 1).all()
+    np.testing.assert_allclose(got[..., cw + aw].view(np.float32),
+                               want[..., cw + aw].view(np.float32), rtol=1e-5)
+    clean = ~flips.any(-1)
+    np.testing.assert_allclose(got[..., cw + aw + 1].view(np.float32)[clean],
+                               want[..., cw + aw + 1].view(np.float32)[clean], rtol=1e-4)
+    gs = np.unpackbits(got[..., cw:cw + aw].copy().view(np.uint8), axis=-1)[clean]
+    ws = np.unpackbits(want[..., cw:cw + aw].copy().view(np.uint8), axis=-1)[clean]
+    assert (gs != ws).sum() <= max(2, gs.size // 1000), (gs != ws).sum()
+
+
 def assert_rows_match_source(fmt: int, got: np.ndarray, src: torch.Tensor, seed: int,
                              rotation: int = 0):
     """Cache rows (exported in the reference layout) against the reference encoder applied to
     the source rows: bit for bit, TurboQuant-4 by the reference's flip criterion."""
     want = oracle_rows(fmt, src, seed, rotation)
-    if rotates(fmt, rotation):
+    if fmt == 1:
+        assert_prod_rows_close(got, want, src.shape[-1])
+    elif rotates(fmt, rotation):
         assert_rotated_rows_close(fmt, got, want, src.shape[-1])
     else:
         np.testing.assert_array_equal(got, want)

@@ -348,3 +348,23 @@ def test_flash_attn_blocks_argument_errors(cq):
     small = L.cqkv_flash_attn_blocks_workspace_bytes(arr, 1, 1, 8, 1, 2, 128)
     arr2 = (cq.PlainBlock * 2)(blk(rows=64), blk(rows=64))
     assert 0 < small < L.cqkv_flash_attn_blocks_workspace_bytes(arr2, 2, 1, 8, 1, 2, 128)
+
+
+def test_turboprod_sides_and_qjl_matrix(cq):
+    """TurboProd key sides: plane sizes (nibble codes; norms, |r|, D / 8 sign bytes per token),
+    the reference row of 3-bit codes + D sign bits + 2 (formats.rs:226-240), keys only, a QJL
+    matrix required; cqkv_qjl_matrix is the oracle's qjl_matrix bit for bit."""
+    L = cq.lib()
+    assert L.cqkv_codes_plane_bytes(cq.TURBOPROD, 128, 64) == 64 * 64
+    assert L.cqkv_scales_plane_bytes(cq.TURBOPROD, 128, 64) == 64 * (8 + 16)
+    assert L.cqkv_reference_row_words(cq.TURBOPROD, 128) == 12 + 4 + 2
+    assert L.cqkv_reference_row_words(cq.TURBOPROD, 64) == 6 + 2 + 2
+    np.testing.assert_array_equal(cq.qjl_matrix(128, 42).numpy(), O.qjl_matrix(128, 42))
+    x = (ctypes.c_int64 * 3)(1, 128, 128)
+    one = ctypes.c_void_p(256)
+    val = cq.Side(cq.TURBOPROD, 1, 128, 2, 64, 0, 44, 256, 256, 256)
+    assert L.cqkv_quant_append(ctypes.byref(val), one, 0, x, 1, 4, None, 0, None) == cq.ERR_ARG
+    assert b"key format" in L.cqkv_last_error()
+    noqjl = cq.Side(cq.TURBOPROD, 0, 128, 2, 64, 0, 42, 256, 256, None)
+    assert L.cqkv_quant_append(ctypes.byref(noqjl), one, 0, x, 1, 4, None, 0, None) == cq.ERR_ARG
+    assert b"QJL" in L.cqkv_last_error()
