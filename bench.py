@@ -28,7 +28,7 @@ Each "cpu_baseline" is the oracle's restatement of the reference CPU path, timed
 CPUs (all of those this process may use) on a bounded sample of the workload and scaled to it.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
-                       [--only c2,c3,c4,c5,f8,fx,ap,ra,pd,pp] [--calibration-copy]
+                       [--only c2,c3,c4,c5,tp,f8,fx,ap,ra,pd,pp] [--calibration-copy]
 """
 from __future__ import annotations
 
@@ -71,8 +71,8 @@ def kv_gpu(shape, seed, dev, outliers=True):
     return x.to(torch.bfloat16)
 
 
-def build_cache(cq, fmt, b, hkv, d, ctx, dev, seed, chunk=2048):
-    cache = cq.TurboKvCache(fmt, fmt, b, hkv, d, ctx, device=dev)
+def build_cache(cq, fmt, b, hkv, d, ctx, dev, seed, chunk=2048, vfmt=None):
+    cache = cq.TurboKvCache(fmt, fmt if vfmt is None else vfmt, b, hkv, d, ctx, device=dev)
     for t0 in range(0, ctx, chunk):
         t = min(chunk, ctx - t0)
         cache.append(kv_gpu((b, hkv, t, d), seed + t0, dev),
@@ -98,12 +98,14 @@ def time_calls(fn, steps, warmup, stream):
 def row_bytes(fmt, d):
     """Packed cache bytes of one (token, head) row: codes + its scales."""
     return {5: d + 4, 2: d // 2 + d // 32, 0: d // 2 + 4, 4: d + d // 32,
-            3: d // 2 + d // 16 + 4}[fmt]
+            3: d // 2 + d // 16 + 4, 1: d // 2 + 8 + d // 8}[fmt]
 
 
-def decode_bytes(b, hq, hkv, d, total_tokens, fmt):
+def decode_bytes(b, hq, hkv, d, total_tokens, fmt, vfmt=None):
     """K + V rows over `total_tokens` (summed over the batch) for every kv head, plus q and out."""
-    return 2 * hkv * total_tokens * row_bytes(fmt, d) + 2 * b * hq * d * 2
+    vfmt = fmt if vfmt is None else vfmt
+    return (hkv * total_tokens * (row_bytes(fmt, d) + row_bytes(vfmt, d))
+            + 2 * b * hq * d * 2)
 
 
 def read_traffic():
@@ -139,7 +141,7 @@ def side_rows(cq, side, b0, nb, tokens):
     cb, sb = side.codes.numel() // side.batch, side.scales.numel() // side.batch
     view = cq.CacheSide(side.fmt, side.is_value, nb, side.kv_heads, side.head_dim, side.capacity,
                         side.codes[b0 * cb:(b0 + nb) * cb], side.scales[b0 * sb:(b0 + nb) * sb],
-                        side.seed)
+                        side.seed, side.rotation, side.qjl)
     return cq.rows_export(view, tokens).cpu().numpy().view(np.uint32)
 
 
@@ -153,25 +155,28 @@ def timed_reps(fn, budget_s=10.0, max_reps=20):
     return t_total / reps, reps
 
 
-def cpu_baseline_decode(cq, cache, q, fmt, seqs, tokens, scale, threads, kv_lens=None):
+def cpu_baseline_decode(cq, cache, q, fmt, seqs, tokens, scale, threads, kv_lens=None,
+                        vfmt=None):
     """The oracle's restatement of the reference CPU decode path (dequantize, unrotate, bf16
     cache, unfused f32 attention) over the sequences `seqs` (a contiguous range); returns seconds
     for that sample and the repetitions timed."""
     import numpy as np
     from oracle import oracle as O
+    vfmt = fmt if vfmt is None else vfmt
     b0, nb = seqs[0], len(seqs)
     kr = side_rows(cq, cache.k, b0, nb, tokens)
     vr = side_rows(cq, cache.v, b0, nb, tokens)
     qb = O.f32_to_bf16_bits(q[b0:b0 + nb].float().cpu().numpy())
-    bits = 4 if fmt == O.TURBO_MSE else 0
-    pk = pv = None
-    if fmt == O.TURBO_MSE:
-        d = q.shape[-1]
-        pk = O.rotation_matrix(d, O.ROT_HADAMARD, cache.k.seed)
-        pv = O.rotation_matrix(d, O.ROT_HADAMARD, cache.v.seed)
+    turbo = (O.TURBO_MSE, O.TURBO_PROD)
+    bits = {f: (4 if f in turbo else 0) for f in (fmt, vfmt)}
+    d = q.shape[-1]
+    pk = O.rotation_matrix(d, O.ROT_HADAMARD, cache.k.seed) if fmt in turbo else None
+    pv = O.rotation_matrix(d, O.ROT_HADAMARD, cache.v.seed) if vfmt in turbo else None
+    sk = O.qjl_matrix(d, cache.k.seed) if fmt == O.TURBO_PROD else None
     lens = None if kv_lens is None else np.array(kv_lens[b0:b0 + nb], np.int32)
-    return timed_reps(lambda: O.cache_attention(qb, kr, vr, (fmt, bits), (fmt, bits), pk, pv,
-                                                tokens, scale, kv_lens=lens, threads=threads))
+    return timed_reps(lambda: O.cache_attention(qb, kr, vr, (fmt, bits[fmt]), (vfmt, bits[vfmt]),
+                                                pk, pv, tokens, scale, kv_lens=lens,
+                                                threads=threads, qjl_k=sk))
 
 
 def cpu_baseline_prefill(threads, heads=4):
@@ -202,17 +207,19 @@ def cpu_baseline_entry(value, unit, us_per_call, threads, info, sample, reps):
     return e
 
 
-def decode_case(cq, dev, stream, fmt, b, hq, hkv, d, ctx, steps, warmup, lens=None, chunk=2048):
+def decode_case(cq, dev, stream, fmt, b, hq, hkv, d, ctx, steps, warmup, lens=None, chunk=2048,
+                vfmt=None):
     """Build two cache copies, time `steps` decode calls alternating between them."""
     import torch
     scale = 1.0 / d ** 0.5
-    caches = [build_cache(cq, fmt, b, hkv, d, ctx, dev, 1000 * i + 11 * fmt, chunk)
+    caches = [build_cache(cq, fmt, b, hkv, d, ctx, dev, 1000 * i + 11 * fmt, chunk, vfmt)
               for i in range(2)]
     q = kv_gpu((b, hq, 1, d), 5, dev, outliers=False)
     out = torch.empty_like(q)
     kv_lens = None if lens is None else torch.tensor(lens, dtype=torch.int32, device=dev)
     # workspace for the split count the call will pick, so no call allocates inside the timing
-    splits = cq.decode_splits(b, hkv, ctx, fmt, ragged=lens is not None)
+    splits = cq.decode_splits(b, hkv, ctx, fmt, ragged=lens is not None,
+                              v_fmt=fmt if vfmt is None else vfmt)
     ws = torch.zeros(max(1, cq.decode_workspace_bytes(b, hq, 1, d, splits)), dtype=torch.uint8,
                      device=dev)
 
@@ -223,7 +230,7 @@ def decode_case(cq, dev, stream, fmt, b, hq, hkv, d, ctx, steps, warmup, lens=No
 
     ms = time_calls(step, steps, warmup, stream)
     total = b * ctx if lens is None else int(sum(lens))
-    nbytes = decode_bytes(b, hq, hkv, d, total, fmt)
+    nbytes = decode_bytes(b, hq, hkv, d, total, fmt, vfmt)
     return caches, q, ms, nbytes
 
 
@@ -373,15 +380,15 @@ def plain_prefill_case(cq, dev, stream, steps, warmup, dtype, D, B=4, S=4096, HQ
 
 def append_case(cq, dev, stream, steps, warmup, b=32, hkv=8, d=128, t=2048):
     """cqkv_quant_append alone: B=32 sequences x 8 kv heads x 2048 tokens (524,288 rows of the
-    config-2 cache shape) of bf16 K or V into FP8 / MXFP4 / TURBO4 / MXFP8 / NVFP4 sides at
+    config-2 cache shape) of bf16 K or V into FP8 / MXFP4 / TURBO4 / MXFP8 / NVFP4 sides (TurboProd: keys only) at
     position 0. Bytes = the bf16 rows read plus the codes and scales written."""
     import torch
     x = kv_gpu((b, hkv, t, d), 51, dev)
     res = {}
     names = {cq.FP8: "fp8", cq.MXFP4: "mxfp4", cq.TURBO4: "turbo4", cq.MXFP8: "mxfp8",
-             cq.NVFP4: "nvfp4"}
+             cq.NVFP4: "nvfp4", cq.TURBOPROD: "turboprod"}
     for fmt, name in names.items():
-        for is_value in (False, True):
+        for is_value in ((False,) if fmt == cq.TURBOPROD else (False, True)):
             side = cq.CacheSide.empty(fmt, is_value, b, hkv, d, t, dev, seed=44 if is_value else 42)
             ms = time_calls(lambda i: cq.quant_append(side, x, 0), steps, warmup, stream)
             nbytes = x.numel() * 2 + b * hkv * t * row_bytes(fmt, d)
@@ -425,7 +432,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--only", default="",
-                    help="comma list of c2,c3,c4,c5,f8,fx,ap,ra,pd,pp (default: all)")
+                    help="comma list of c2,c3,c4,c5,tp,f8,fx,ap,ra,pd,pp (default: all)")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="also run a plain 1 GiB copy (for counter scaling)")
     args = ap.parse_args()
@@ -554,6 +561,29 @@ def main():
                 "oracle cache_attention (with the Hadamard unrotation of both sides) on 1 of the 8 "
                 "sequences, scaled x8", reps)
             log(f"config 5 cpu: {sec * 1e6:.0f} us/call")
+        del caches
+        torch.cuda.empty_cache()
+
+    if want("tp"):
+        log("TurboProd keys + TurboQuant-4 values decode B=8 64/8 d=128 ctx 131072")
+        caches, qp, ms, nbytes = decode_case(cq, dev, stream, cq.TURBOPROD, 8, 64, 8, 128,
+                                             131072, steps_x, warm_x, chunk=8192,
+                                             vfmt=cq.TURBO4)
+        other["c5_shape_turboprod"] = decode_summary(
+            "TurboProd (QJL) keys + TurboQuant-4 values decode at the BASELINE config-5 shape",
+            ms, nbytes,
+            {"batch": 8, "q_heads": 64, "kv_heads": 8, "head_dim": 128, "context": 131072,
+             "timed": "whole call (split-K decode + combine with unrotation)"})
+        log(f"turboprod: {ms * 1e3:.2f} us/call")
+        if not args.no_cpu:
+            sec, reps = cpu_baseline_decode(cq, caches[0], qp, cq.TURBOPROD, range(1), 131072,
+                                            1.0 / 128 ** 0.5, threads, vfmt=cq.TURBO4)
+            sec *= 8
+            other["c5_shape_turboprod"]["cpu_baseline"] = cpu_baseline_entry(
+                round(nbytes / sec / 1e12, 6), "TB/s", sec * 1e6, threads, info,
+                "oracle cache_attention (QJL key scores, Hadamard unrotation) on 1 of the 8 "
+                "sequences, scaled x8", reps)
+            log(f"turboprod cpu: {sec * 1e6:.0f} us/call")
         del caches
         torch.cuda.empty_cache()
 

@@ -281,21 +281,24 @@ using op_t = typename std::conditional<FMT == CQKV_FMT_TURBO4 || FMT == CQKV_FMT
 
 typedef __attribute__((address_space(3))) const uint32_t lds_u32;
 
-// TurboProd key codes: the f16 pair of code byte b (codes b & 7, b >> 4 & 7) from a compact 16 KB
-// table, entry (lo + 8 hi, l) at byte 256 (lo + 8 hi) + 4 l (a copy per lane, as turbo_pair).
+// TurboProd key codes: the f16 pair of code byte b (codes b & 7, b >> 4 & 7; bits 3 and 7 are
+// zero) from a 15 KB table, entry (b, l) at byte 128 b + 4 (l % 32): a copy per half-wavefront
+// lane, so a 64 KB TurboQuant value table and this one leave room for two workgroups per CU.
+// The table is 16 KB-aligned, so the address is one shift-or of the code byte into ktab.
+constexpr int kProdTabWords = 120 * 32;
 template <int I>
 __device__ inline uint32_t prod_pair(uint32_t ktab, uint32_t w) {
     const uint32_t b = (w >> (8 * I)) & 0xffu;
-    const uint32_t idx = (b & 7u) | ((b >> 1) & 0x38u);
-    return *(lds_u32 *)(size_t)(ktab + (idx << 8));
+    return *(lds_u32 *)(size_t)(ktab | (b << 7));
 }
-// 8 sign bits -> 8 f16 operands +1 (bit set) / -1
-__device__ inline f16x8 signs_f16x8(uint32_t bits8) {
+// 8 sign bits (byte j of w) -> 8 f16 operands -1 (bit set) / +1: with t = u | u << 15, pair k
+// (bits 2k, 2k + 1 of u) sits at bits 15 and 31 of t << (15 - 2k), the f16 sign positions
+__device__ inline f16x8 signs_f16x8(uint32_t w, int j) {
+    const uint32_t u = (w >> (8 * j)) & 0xffu, t = u | (u << 15);
     u32x4 r;
     uint32_t *rp = (uint32_t *)&r;
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-        rp[k] = 0xBC00BC00u ^ (((bits8 >> (2 * k)) & 1u) << 15) ^ (((bits8 >> (2 * k + 1)) & 1u) << 31);
+    for (int k = 0; k < 4; ++k) rp[k] = ((t << (15 - 2 * k)) & 0x80008000u) | 0x3C003C00u;
     return __builtin_bit_cast(f16x8, r);
 }
 
@@ -438,8 +441,8 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
         s0 = mfma16x16x32(k0, qhi[j], s0);
         s1 = mfma16x16x32(k1, qhi[j], s1);
         if constexpr (KF == CQKV_FMT_TURBOPROD) {  // byte j of the lane key's sign bits
-            z0 = mfma16x16x32(signs_f16x8((cur.ksg[0] >> (8 * j)) & 0xffu), qsop[j], z0);
-            z1 = mfma16x16x32(signs_f16x8((cur.ksg[1] >> (8 * j)) & 0xffu), qsop[j], z1);
+            z0 = mfma16x16x32(signs_f16x8(cur.ksg[0], j), qsop[j], z0);
+            z1 = mfma16x16x32(signs_f16x8(cur.ksg[1], j), qsop[j], z1);
         }
         if (q_split) {
             s0 = mfma16x16x32(k0, qlo[j], s0);
@@ -449,9 +452,10 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
     float x[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
     const int kbase = t0 + 8 * g;  // x[e] is key kbase + e
     if constexpr (KF == CQKV_FMT_TURBOPROD) {
-        // r0 (q . c + r1 sqrt(pi / 2) / D (S q) . z) (turbo_quant_impl.h:268-276)
+        // r0 (q . c + r1 sqrt(pi / 2) / D (S q) . z) (turbo_quant_impl.h:268-276); zk holds
+        // -(S q) . z (the operands are -1 where the sign bit is set)
         const float zk[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
-        constexpr float kc = kQjlConst / D;
+        constexpr float kc = -kQjlConst / D;
 #pragma unroll
         for (int e = 0; e < 8; ++e)
             x[e] = (x[e] + __uint_as_float(cur.kr1[e]) * kc * zk[e]) *
@@ -634,8 +638,8 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
     uint32_t *sm_tab = (uint32_t *)sm_buf;
     __shared__ float sm_m[WAVES][16], sm_l[WAVES][16];
     constexpr bool kProd = KF == CQKV_FMT_TURBOPROD;
-    // TurboProd keys: the compact 3-bit code-pair table (64 entries x 64 lanes)
-    __shared__ uint32_t sm_ktab[kProd ? 64 * 64 : 1];
+    // TurboProd keys: the 3-bit code-pair table (120 code bytes x 32 lanes)
+    __shared__ __attribute__((aligned(16384))) uint32_t sm_ktab[kProd ? kProdTabWords : 1];
 
     // 1-D grid, plane fastest: workgroup ids are dealt round-robin to the 8 XCDs, so with
     // kv_heads a multiple of 8 each XCD takes whole planes of one kv head from every sequence -
@@ -748,8 +752,8 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
             op_t<KF> lo_unused;
             split8(qv, qsop[j], lo_unused);
         }
-        for (int i = threadIdx.x; i < 64 * 64; i += NT)
-            sm_ktab[i] = pack_f16x2(a.kcent[(i >> 6) & 7], a.kcent[i >> 9]);
+        for (int i = threadIdx.x; i < kProdTabWords; i += NT)
+            sm_ktab[i] = pack_f16x2(a.kcent[(i >> 5) & 7], a.kcent[(i >> 9) & 7]);
     }
     const bool q_split = a.q_split != 0;
     __syncthreads();
@@ -775,7 +779,7 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
 #pragma unroll
     for (int t = 0; t < 2 * NCH; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     const uint32_t tab = (uint32_t)(size_t)sm_tab + 4 * lane;
-    const uint32_t ktab = (uint32_t)(size_t)sm_ktab + 4 * lane;
+    const uint32_t ktab = (uint32_t)(size_t)sm_ktab + 4 * (lane & 31);
     float m_run = -__builtin_inff(), l_run = 0.0f;
 
     // Register sets A and B alternate; the scheduling barriers keep every load of one set
