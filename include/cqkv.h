@@ -38,8 +38,14 @@
  *                          flash_attn_fp8 and the F8E4M3 K / V path of flash_attn_with_config
  *                          with FlashAttnConfig::descale (candle-nn/src/flash_attn.rs:113-117,
  *                          862-892; kernels candle-core/kernels/flash_attn_impl.h:52-63, 381, 434)
+ *   cqkv_flash_attn_blocks flash_attn_blocks over blocks of plain K / V, the paged row kernels
+ *                          fa_rowp_* (candle-nn/src/flash_attn.rs:705-836,
+ *                          candle-core/src/accel/attention.rs:293-366)
  *   cqkv_rows_import /     the reference's packed row layout [codes][aux][rsc0][rsc1]
  *   cqkv_rows_export       (candle-core/src/accel/formats.rs:206-242)
+ *   cqkv_side_copy         the grown-buffer copy of Cache::append (candle-nn/src/kv_cache.rs:56-99)
+ *   cqkv_qjl_matrix / cqkv_turbo_codebook / cqkv_turbo_signs
+ *                          qjl_matrix, Codebook, the Hadamard signs (candle-core/src/accel/turbo.rs)
  *
  * Cache layout in HBM (one "plane" per (batch, kv head), planes batch-major, `capacity` tokens):
  *   format        codes plane (bytes)                  scales plane (bytes)
@@ -54,6 +60,8 @@
  *   NVFP4 keys    capacity * D/2    row-major nibbles  capacity * D/16  E4M3 per 16-element block,
  *                                                      then capacity * 4  f32 per token
  *   NVFP4 values  capacity * D/2    8-token tiles      the same
+ *   TURBOPROD keys capacity * D/2   row-major nibbles  capacity * (8 + D/8): f32 norms, f32 |r|,
+ *                  (3-bit codes)                       then D/8 QJL sign-bit bytes per token
  * Row-major: token t's codes at t * row_bytes, element j at byte j (FP8) or nibble j (bits 4(j%2)
  * of byte j/2), i.e. the reference's code stream. 8-token tiles (values): token t, element j at
  * tile t/8, offset j*8 + t%8 bytes (FP8) or bits 4(t%8) of the little-endian u32 j (4-bit). The
@@ -227,8 +235,8 @@ int cqkv_decode_attention_noalloc(const void *q, int32_t q_dtype, const int64_t 
  * packed into a PageTable, candle-core/src/accel/attention.rs:307-366): a key side and a value
  * side holding `rows` valid tokens at the start of every (batch, kv head) plane. The keys of a
  * paged call are the blocks' valid rows concatenated in block order; masks are bottom-right
- * aligned over that concatenation. Every block has the format, head dim, kv heads and TURBO4
- * seeds of block 0; capacities may differ. */
+ * aligned over that concatenation. Every block has the formats, head dim, kv heads, rotations,
+ * seeds (and TURBOPROD QJL matrix) of block 0; capacities may differ. */
 typedef struct cqkv_kv_block {
     const cqkv_side *k;
     const cqkv_side *v;
@@ -256,11 +264,12 @@ int cqkv_decode_attention_paged(const void *q, int32_t q_dtype, const int64_t q_
  *   `dtype` (CQKV_BF16 or CQKV_F16), element strides {batch, token, head} (D contiguous);
  *   head_dim any multiple of 8 up to 256 (the reference's FA_MAX_HEAD_DIM); any
  *   q_heads % kv_heads == 0; bottom-right aligned windows; causal = window (-1, 0).
- *   bf16 at head_dim 128 with more than 16 queries runs the MFMA prefill kernel; every other
- *   call (f16, other head dims, decode-shaped calls of up to 16 queries) runs the plain-dtype
- *   kernel: 16 (query, head) columns of a kv head per workgroup over split-K, the row kernels
- *   fa_row_* / fa_rowg_* of the reference (candle-core/kernels/flash_attn_impl.h:49-328).
- *   K / V of that kernel need 16-byte aligned rows (pointers and strides whole 8-element chunks).
+ *   bf16 / f16 at head_dim 128 with more than 16 queries runs the MFMA prefill kernel; every
+ *   other call runs the plain-dtype kernels over split-K: up to 16 (query, head) columns per kv
+ *   head the row kernel (the reference's fa_row_* / fa_rowg_*,
+ *   candle-core/kernels/flash_attn_impl.h:49-328), more the shared-tile kernel (its tile
+ *   kernels, :330-443). K / V need 16-byte aligned rows (pointers and strides whole 8-element
+ *   chunks).
  *   When k_cache / v_cache are non-NULL (a key and a value side of any formats and rotations)
  *   the same call also quantizes and appends k / v at positions [position, position + kv_len)
  *   of the cache: inside the MFMA prefill's pre-pass for unrotated FP8 sides at a position that
