@@ -367,15 +367,28 @@ __device__ inline void hadamard_row32(const AppendArgs &a, int q, float (&x)[32]
 // value tiles pass through LDS). ROPE != 0 rotates each row first (the fused RoPE + append).
 // TurboProd's QJL stage for the block's rows (RowCodec::quantize_row, candle-core/src/accel/
 // turbo.rs:311-320): residual r = u - centroid[code] of the unit row u = y / norm, rsc1 = |r|,
-// and the sign bits of p = S r. p runs on v_mfma_f32_16x16x4_f32 over the residuals staged in
-// LDS: P^T (D x 16 rows) = S (D x D) R^T per wavefront and 16 rows; k-step e of a group of four
-// takes column j = 16 kk + 4 g + e in lane group g, so A (S) and B (R) are 16-byte reads. Lane
-// (row n, group g) gets p of outputs 16 bi + 4 g + e: four bits, OR-ed across g into 16.
+// and the sign bits of p = S r. Only signs are kept, so r is scaled by 64 (exact) into the range
+// where its f16 hi + lo split keeps 22 significant bits; p = S_hi r_hi + S_hi r_lo + S_lo r_hi
+// on v_mfma_f32_16x16x32_f16 (products exact, f32 sums; the dropped S_lo r_lo is 2^-22 of a
+// term). Wavefront w owns outputs [w D / 4, (w + 1) D / 4): its rows of S stay in registers as
+// A operands, the rows' r (hi, lo) come from LDS as B operands, and lane (row n, group g) gets p
+// of outputs 16 bo + 4 g + i: bits OR-ed across g into the wavefront's D / 4 bits of the row.
+constexpr int kProdResidStride = 8;  // f16 padding per LDS row: conflict-free 16-byte reads
+__device__ inline void f16_split8(const float *v, f16x8 &hi, f16x8 &lo) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const _Float16 h = (_Float16)v[e];
+        hi[e] = h;
+        lo[e] = (_Float16)(v[e] - (float)h);
+    }
+}
 template <int D, int NR>
 __device__ inline void prod_qjl(const AppendArgs &a, const float (&x)[32], float inv,
                                 const uint32_t (&cw)[4], bool live, int t, int r, int q,
-                                uint8_t *scales, float *sm_resid, float *sm_cent) {
-    constexpr int R = D / 32;
+                                uint8_t *scales, uint16_t *sm_r, float *sm_cent) {
+    constexpr int R = D / 32, LD = D + kProdResidStride;  // f16 per LDS row
+    constexpr int NB = D / 64;                            // 16-output blocks per wavefront
+    constexpr int NC = D / 32;                            // 32-wide k chunks
     const int tid = threadIdx.x;
     if (tid < 8) sm_cent[tid] = a.cent[tid];
     __syncthreads();
@@ -388,49 +401,69 @@ __device__ inline void prod_qjl(const AppendArgs &a, const float (&x)[32], float
     }
     const float r1 = __builtin_sqrtf(row_sum<R>(rr));
     if (r < NR) {
+        uint16_t *hrow = sm_r + r * LD + 32 * q, *lrow = sm_r + (NR + r) * LD + 32 * q;
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            *(f32x4 *)(sm_resid + r * D + 32 * q + 4 * i) =
-                f32x4{res[4 * i], res[4 * i + 1], res[4 * i + 2], res[4 * i + 3]};
+        for (int j = 0; j < 4; ++j) {
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = 64.0f * res[8 * j + e];
+            f16x8 hi, lo;
+            f16_split8(v, hi, lo);
+            *(f16x8 *)(hrow + 8 * j) = hi;
+            *(f16x8 *)(lrow + 8 * j) = lo;
+        }
     }
     if (live && q == 0) ((float *)(scales + (int64_t)a.capacity * 4))[t] = r1;
-    __syncthreads();
     const int lane = tid & 63, wave = tid >> 6, n = lane & 15, g = lane >> 4;
+    // this wavefront's rows of S as A operands: lane (m, g) of block bo, chunk c holds
+    // S[o0 + 16 bo + m][32 c + 8 g .. + 7]
+    f16x8 shi[NB][NC], slo[NB][NC];
+    const int o0 = wave * (D / 4);
+#pragma unroll
+    for (int bo = 0; bo < NB; ++bo)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const float *src = a.qjl + (int64_t)(o0 + 16 * bo + n) * D + 32 * c + 8 * g;
+            const f32x4 v0 = *(const f32x4 *)src, v1 = *(const f32x4 *)(src + 4);
+            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            f16_split8(v, shi[bo][c], slo[bo][c]);
+        }
+    __syncthreads();
     const int pos = a.positions ? a.positions[blockIdx.z] : a.position;
     int end = min(pos + a.tokens, a.capacity);
     if (a.cs_rows > 0) end = min(end, a.cs_rows);
     const int c0 = t - r;  // the block's first cache position
-    uint32_t *signs = (uint32_t *)(scales + (int64_t)a.capacity * 8);
-    constexpr int RB = NR / 16;  // 16-row blocks, spread over the four wavefronts
-    for (int rb = wave; rb < RB; rb += 4) {
-        const float *rrow = sm_resid + (16 * rb + n) * D + 4 * g;
-        const int tr = c0 + 16 * rb + n;
-        const bool row_live = tr >= pos && tr < end;
+    uint8_t *signs = scales + (int64_t)a.capacity * 8;
+#pragma unroll 1
+    for (int rb = 0; rb < NR / 16; ++rb) {
+        f32x4 acc[NB];
+#pragma unroll
+        for (int bo = 0; bo < NB; ++bo) acc[bo] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const uint16_t *hrow = sm_r + (16 * rb + n) * LD + 8 * g;
+        const uint16_t *lrow = sm_r + (NR + 16 * rb + n) * LD + 8 * g;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const f16x8 rhi = *(const f16x8 *)(hrow + 32 * c), rlo = *(const f16x8 *)(lrow + 32 * c);
+#pragma unroll
+            for (int bo = 0; bo < NB; ++bo) {
+                acc[bo] = mfma16x16x32(shi[bo][c], rhi, acc[bo]);
+                acc[bo] = mfma16x16x32(shi[bo][c], rlo, acc[bo]);
+                acc[bo] = mfma16x16x32(slo[bo][c], rhi, acc[bo]);
+            }
+        }
+        // acc[bo][i] = p of output o0 + 16 bo + 4 g + i, row 16 rb + n
         uint32_t word = 0;
 #pragma unroll
-        for (int bi = 0; bi < D / 16; ++bi) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            const float *srow = a.qjl + (int64_t)(16 * bi + n) * D + 4 * g;
-#pragma unroll 4
-            for (int kk = 0; kk < D / 16; ++kk) {
-                const f32x4 sa = *(const f32x4 *)(srow + 16 * kk);
-                const f32x4 rb4 = *(const f32x4 *)(rrow + 16 * kk);
+        for (int bo = 0; bo < NB; ++bo)
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(sa[e], rb4[e], acc, 0, 0, 0);
-            }
-            // acc[e] = p of output 16 bi + 4 g + e, row n
-            uint32_t nib = 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) nib |= (acc[e] >= 0.0f ? 1u : 0u) << e;
-            uint32_t chunk = nib << (4 * g);
-            chunk |= (uint32_t)__shfl_xor((int)chunk, 16, 64);
-            chunk |= (uint32_t)__shfl_xor((int)chunk, 32, 64);
-            word |= chunk << (16 * (bi & 1));
-            if (bi & 1) {
-                if (g == 0 && row_live) signs[(int64_t)tr * (D / 32) + bi / 2] = word;
-                word = 0;
-            }
+            for (int i = 0; i < 4; ++i) word |= (acc[bo][i] >= 0.0f ? 1u : 0u) << (16 * bo + 4 * g + i);
+        word |= (uint32_t)__shfl_xor((int)word, 16, 64);
+        word |= (uint32_t)__shfl_xor((int)word, 32, 64);
+        const int tr = c0 + 16 * rb + n;
+        if (g == 0 && tr >= pos && tr < end) {
+            uint8_t *dst = signs + (int64_t)tr * (D / 8) + wave * (D / 32);
+            if constexpr (D == 128) *(uint32_t *)dst = word;
+            else *(uint16_t *)dst = (uint16_t)word;
         }
     }
 }
@@ -444,8 +477,10 @@ __device__ inline void rows_block(const AppendArgs &a, int h, int b, int bx) {
     __shared__ __attribute__((aligned(16))) uint8_t sm_codes[IS_VALUE ? ROWS * kRowBytes : 16];
     constexpr bool kProd = FMT == CQKV_FMT_TURBOPROD;
     static_assert(!kProd || !IS_VALUE, "TurboProd is a key format");
-    // TurboProd: the rows' residuals (f32) for the S r projection, and the 3-bit centroids
-    __shared__ __attribute__((aligned(16))) float sm_resid[kProd ? ROWS * D : 4];
+    // TurboProd: the rows' scaled residuals (f16 hi rows, then lo rows) for the S r projection,
+    // and the 3-bit centroids
+    __shared__ __attribute__((aligned(16))) uint16_t
+        sm_resid[kProd ? 2 * ROWS * (D + kProdResidStride) : 8];
     __shared__ float sm_cent[8];
 
     const int pos = a.positions ? a.positions[b] : a.position;
