@@ -44,6 +44,7 @@ class Side(ctypes.Structure):
     _fields_ = [("format", ctypes.c_int32), ("is_value", ctypes.c_int32),
                 ("head_dim", ctypes.c_int32), ("kv_heads", ctypes.c_int32),
                 ("capacity", ctypes.c_int32), ("rotation", ctypes.c_int32),
+                ("bits", ctypes.c_int32), ("reserved", ctypes.c_int32),
                 ("seed", ctypes.c_uint64), ("codes", ctypes.c_void_p),
                 ("scales", ctypes.c_void_p), ("qjl", ctypes.c_void_p)]
 
@@ -112,7 +113,7 @@ def lib() -> ctypes.CDLL:
                                          ctypes.c_uint64, P, ctypes.c_int64, P]
         L.cqkv_flash_attn_fp8.argtypes = [P, I64P, P, I64P, P, I64P, P, I64P, i32, i32, i32, i32,
                                           i32, i32, f32, i32, i32, f32, f32, P, P, P]
-        L.cqkv_reference_row_words.argtypes = [i32, i32]
+        L.cqkv_reference_row_words.argtypes = [i32, i32, i32]
         L.cqkv_reference_row_words.restype = i32
         L.cqkv_rows_import.argtypes = [SP, P, i32, i32, i32, P]
         L.cqkv_rows_export.argtypes = [SP, P, i32, i32, i32, P]
@@ -181,11 +182,13 @@ class CacheSide:
     seed: int = 0
     rotation: int = ROT_DEFAULT
     qjl: torch.Tensor | None = None  # TURBOPROD: the (D, D) f32 QJL matrix on the device
+    # TurboQuant width (TURBO4: TurboMse{bits} 1-4, TURBOPROD: TurboProd{bits} 2-4; 0 = 4)
+    bits: int = 0
 
     @staticmethod
     def empty(fmt: int, is_value: bool, batch: int, kv_heads: int, head_dim: int,
               capacity: int, device, seed: int = 0,
-              rotation: int = ROT_DEFAULT) -> "CacheSide":
+              rotation: int = ROT_DEFAULT, bits: int = 0) -> "CacheSide":
         capacity = (capacity + 31) // 32 * 32
         cb = lib().cqkv_codes_plane_bytes(fmt, head_dim, capacity)
         sb = lib().cqkv_scales_plane_bytes(fmt, head_dim, capacity)
@@ -195,7 +198,7 @@ class CacheSide:
         scales = torch.zeros(batch * kv_heads * sb, dtype=torch.uint8, device=device)
         qjl = qjl_matrix(head_dim, seed).to(device) if fmt == TURBOPROD else None
         return CacheSide(fmt, is_value, batch, kv_heads, head_dim, capacity, codes, scales, seed,
-                         rotation, qjl)
+                         rotation, qjl, bits)
 
     def rotates(self) -> bool:
         """Whether rows are stored Hadamard-rotated (seeded by `seed`)."""
@@ -204,7 +207,8 @@ class CacheSide:
 
     def struct(self) -> Side:
         return Side(self.fmt, int(self.is_value), self.head_dim, self.kv_heads, self.capacity,
-                    self.rotation, self.seed, self.codes.data_ptr(), self.scales.data_ptr(),
+                    self.rotation, self.bits, 0, self.seed, self.codes.data_ptr(),
+                    self.scales.data_ptr(),
                     None if self.qjl is None else self.qjl.data_ptr())
 
     def nbytes(self) -> int:
@@ -608,15 +612,17 @@ def flash_attn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     return out
 
 
-def reference_row_words(fmt: int, head_dim: int) -> int:
-    return lib().cqkv_reference_row_words(fmt, head_dim)
+def reference_row_words(fmt: int, head_dim: int, bits: int = 0) -> int:
+    """u32 words of one reference row (formats.rs:206-242); `bits` as CacheSide.bits."""
+    return lib().cqkv_reference_row_words(fmt, bits, head_dim)
 
 
 def rows_import(side: CacheSide, rows: torch.Tensor, position: int = 0) -> None:
     """Reference rows (batch, kv_heads, tokens, row_words) u32 (as int32) -> cache."""
     _need_gpu(rows, "rows")
     b, h, t, w = rows.shape
-    if (b, h, w) != (side.batch, side.kv_heads, reference_row_words(side.fmt, side.head_dim)):
+    if (b, h, w) != (side.batch, side.kv_heads,
+                     reference_row_words(side.fmt, side.head_dim, side.bits)):
         raise CqkvError(ERR_ARG, f"rows {tuple(rows.shape)} do not match the cache side")
     if rows.dtype not in (torch.int32, torch.uint32):
         raise CqkvError(ERR_ARG, "rows must be 32-bit words")
@@ -626,7 +632,7 @@ def rows_import(side: CacheSide, rows: torch.Tensor, position: int = 0) -> None:
 
 
 def rows_export(side: CacheSide, tokens: int, position: int = 0) -> torch.Tensor:
-    w = reference_row_words(side.fmt, side.head_dim)
+    w = reference_row_words(side.fmt, side.head_dim, side.bits)
     rows = torch.zeros((side.batch, side.kv_heads, tokens, w), dtype=torch.int32,
                        device=side.codes.device)
     s = side.struct()
@@ -680,20 +686,21 @@ def turbo_signs(head_dim: int, seed: int):
 class TurboKvCache:
     """A quantized KV cache for (batch, kv_heads, head_dim), keys in `key_format` (FP8, MXFP4,
     MXFP8, NVFP4, TURBO4 or TURBOPROD) and values in `value_format` (the same but TURBOPROD),
-    rotated per `rotation` with seeds `seed` (keys) and `seed + 2` (values) as
-    TurboKvCache::with_formats does (candle-nn/src/turbo_quant.rs:858-879). It grows past
-    `capacity` as Cache::append does."""
+    TurboQuant widths `key_bits` / `value_bits` (0: 4), rotated per `rotation` with seeds `seed`
+    (keys) and `seed + 2` (values) as TurboKvCache::with_formats does
+    (candle-nn/src/turbo_quant.rs:858-879). It grows past `capacity` as Cache::append does."""
 
     def __init__(self, key_format: int, value_format: int, batch: int, kv_heads: int,
                  head_dim: int, capacity: int, device="cuda", seed: int = 42,
-                 grow_by: int | None = None, rotation: int = ROT_DEFAULT):
+                 grow_by: int | None = None, rotation: int = ROT_DEFAULT, key_bits: int = 0,
+                 value_bits: int = 0):
         if value_format == TURBOPROD:
             raise CqkvError(ERR_ARG, "turbo-quant: values use the MSE codebooks, not the prod "
                                      "(QJL) format")
         self.k = CacheSide.empty(key_format, False, batch, kv_heads, head_dim, capacity, device,
-                                 seed, rotation)
+                                 seed, rotation, key_bits)
         self.v = CacheSide.empty(value_format, True, batch, kv_heads, head_dim, capacity, device,
-                                 seed + 2, rotation)
+                                 seed + 2, rotation, value_bits)
         self._len = 0
         self.dim = head_dim
         # Cache::new(dim, max_seq_len) grows by max_seq_len (kv_cache.rs:19-27)
@@ -709,7 +716,7 @@ class TurboKvCache:
         sides = []
         for old in (self.k, self.v):
             new = CacheSide.empty(old.fmt, old.is_value, old.batch, old.kv_heads, old.head_dim,
-                                  cap, dev, old.seed, old.rotation)
+                                  cap, dev, old.seed, old.rotation, old.bits)
             new.qjl = old.qjl
             if self._len:
                 side_copy(new, old, self._len)

@@ -8,8 +8,11 @@
 //   MXFP8  D/4 code words, ceil(D/32 / 4) aux words (E8M0 bytes), rsc0 = 1.0, rsc1 = 0
 //   NVFP4  D/8 code words, ceil(D/16 / 4) aux words (E4M3 block scales), rsc0 = f32 global
 //          scale, rsc1 = 0
-//   TURBOPROD (keys) 3 D/32 code words (3-bit codes, LSB first), D/32 aux words (the QJL sign
-//          bits), rsc0 = f32 norm, rsc1 = f32 |r|
+//   TURBO4 at bits b < 4 (TurboMse{b}): ceil(b D / 32) code words (b-bit codes, LSB first),
+//          rsc0 = f32 norm, rsc1 = 0
+//   TURBOPROD{b} (keys) ceil((b - 1) D / 32) code words ((b - 1)-bit codes, LSB first), D/32 aux
+//          words (the QJL sign bits), rsc0 = f32 norm, rsc1 = f32 |r|
+// The cache keeps TurboQuant codes of every width as nibbles.
 // One wavefront per 8-token tile of a (batch, head) plane; lane l owns elements 2l, 2l+1, so
 // the value tiles are read and written whole by one lane (no cross-lane read-modify-write).
 #include <algorithm>
@@ -28,6 +31,7 @@ struct ConvertArgs {
     int32_t nblk;         // block scale bytes per token (MX, NVFP4), else 0
     int32_t tok_scale;    // an f32 per token (FP8, TURBO4, NVFP4), after the block bytes
     int32_t capacity;
+    int32_t cbits;        // TurboQuant codes packed at cbits < 4 per element, or TURBOPROD; else 0
 };
 
 template <bool EXPORT>
@@ -60,46 +64,75 @@ __global__ __launch_bounds__(64) void convert_kernel(ConvertArgs a) {
             vn1 = src[1];
         }
     }
-    if (a.format == CQKV_FMT_TURBOPROD) {  // keys: row-major nibble codes, norms, |r|, sign bits
-        const int cw = 3 * D / 32, sw = D / 32;
+    if (a.cbits) {  // TurboQuant codes of cbits < 4 bits, or TURBOPROD: nibbles <-> packed bits
+        __shared__ uint8_t sm_c[256];
+        const int cb = a.cbits, cw = (D * cb + 31) / 32;
+        const bool prod = a.format == CQKV_FMT_TURBOPROD;
+        const int sw = prod ? D / 32 : 0;
         const float *r1 = (const float *)(scales + (int64_t)a.capacity * 4);
         uint32_t *signs = (uint32_t *)(scales + (int64_t)a.capacity * 8);
+        const uint32_t mask = (1u << cb) - 1u;
         for (int t = t_lo; t < t_hi; ++t) {
             uint32_t *row = a.rows + ((plane * a.tokens) + (t - a.position)) * (int64_t)a.row_words;
-            const uint8_t *cp = codes + (int64_t)t * (D / 2);
+            const int s = t & 7;
             if (EXPORT) {
-                if (lane < cw) {  // word `lane`: bits [32 lane, 32 lane + 32) of the 3-bit codes
+                if (active) {  // this lane's codes of elements 2 lane, 2 lane + 1
+                    uint32_t c0, c1;
+                    if (!a.is_value) {
+                        const uint32_t by = codes[(int64_t)t * (D / 2) + lane];
+                        c0 = by & 15u;
+                        c1 = by >> 4;
+                    } else {
+                        c0 = (vn0 >> (4 * s)) & 15u;
+                        c1 = (vn1 >> (4 * s)) & 15u;
+                    }
+                    sm_c[2 * lane] = (uint8_t)(c0 & mask);
+                    sm_c[2 * lane + 1] = (uint8_t)(c1 & mask);
+                }
+                __syncthreads();
+                if (lane < cw) {  // word `lane`: bits [32 lane, 32 lane + 32) of the packed codes
                     uint32_t w = 0;
-                    const int j0 = (32 * lane) / 3, j1 = min((32 * lane + 31) / 3, D - 1);
+                    const int j0 = (32 * lane) / cb, j1 = min((32 * lane + 31) / cb, D - 1);
                     for (int j = j0; j <= j1; ++j) {
-                        const uint32_t c = (cp[j >> 1] >> (4 * (j & 1))) & 7u;
-                        const int bit = 3 * j - 32 * lane;  // -2 .. 31
+                        const uint32_t c = sm_c[j];
+                        const int bit = cb * j - 32 * lane;  // -(cb - 1) .. 31
                         w |= bit >= 0 ? c << bit : c >> (-bit);
                     }
                     row[lane] = w;
                 }
+                __syncthreads();
                 if (lane < sw) row[cw + lane] = signs[(int64_t)t * sw + lane];
                 if (lane == 0) {
                     row[cw + sw] = __float_as_uint(tscale[t]);
-                    row[cw + sw + 1] = __float_as_uint(r1[t]);
+                    row[cw + sw + 1] = prod ? __float_as_uint(r1[t]) : 0u;
                 }
             } else {
                 if (active) {  // elements 2 lane, 2 lane + 1
                     uint32_t c[2];
                     for (int e = 0; e < 2; ++e) {
-                        const int pos = 3 * (2 * lane + e);
+                        const int pos = cb * (2 * lane + e);
                         const uint64_t two = (uint64_t)row[pos >> 5] |
                                              ((pos >> 5) + 1 < cw ? (uint64_t)row[(pos >> 5) + 1] << 32 : 0ull);
-                        c[e] = (uint32_t)(two >> (pos & 31)) & 7u;
+                        c[e] = (uint32_t)(two >> (pos & 31)) & mask;
                     }
-                    codes[(int64_t)t * (D / 2) + lane] = (uint8_t)(c[0] | (c[1] << 4));
+                    if (!a.is_value) {
+                        codes[(int64_t)t * (D / 2) + lane] = (uint8_t)(c[0] | (c[1] << 4));
+                    } else {
+                        vn0 = (vn0 & ~(15u << (4 * s))) | (c[0] << (4 * s));
+                        vn1 = (vn1 & ~(15u << (4 * s))) | (c[1] << (4 * s));
+                    }
                 }
                 if (lane < sw) signs[(int64_t)t * sw + lane] = row[cw + lane];
                 if (lane == 0) {
                     tscale[t] = __uint_as_float(row[cw + sw]);
-                    ((float *)r1)[t] = __uint_as_float(row[cw + sw + 1]);
+                    if (prod) ((float *)r1)[t] = __uint_as_float(row[cw + sw + 1]);
                 }
             }
+        }
+        if (!EXPORT && a.is_value && active) {
+            uint32_t *dst = (uint32_t *)(codes + (int64_t)tile * D * 4 + 2 * lane * 4);
+            dst[0] = vn0;
+            dst[1] = vn1;
         }
         return;
     }
@@ -204,7 +237,7 @@ static int convert(const cqkv_side *side, uint32_t *rows, int32_t batch, int32_t
     a.kv_heads = side->kv_heads;
     a.tokens = tokens;
     a.position = position;
-    a.row_words = cqkv_reference_row_words(side->format, side->head_dim);
+    a.row_words = cqkv_reference_row_words(side->format, side->bits, side->head_dim);
     a.format = side->format;
     a.b8 = code_bits(side->format) == 8 ? 1 : 0;
     a.nblk = block_elems(side->format) ? side->head_dim / block_elems(side->format) : 0;
@@ -212,6 +245,7 @@ static int convert(const cqkv_side *side, uint32_t *rows, int32_t batch, int32_t
     a.capacity = side->capacity;
     a.is_value = side->is_value;
     a.head_dim = side->head_dim;
+    a.cbits = side->format == CQKV_FMT_TURBOPROD || turbo_code_bits(side) < 4 ? turbo_code_bits(side) : 0;
     dim3 grid((tokens + 7) / 8 + 1, side->kv_heads, batch);
     if (to_rows) hipLaunchKernelGGL(convert_kernel<true>, grid, dim3(64), 0, st, a);
     else hipLaunchKernelGGL(convert_kernel<false>, grid, dim3(64), 0, st, a);
@@ -250,10 +284,10 @@ extern "C" int cqkv_side_copy(const cqkv_side *dst, const cqkv_side *src, int32_
     if (int rc = check_side(src, who)) return rc;
     if (dst->format != src->format || dst->is_value != src->is_value ||
         dst->head_dim != src->head_dim || dst->kv_heads != src->kv_heads ||
-        side_rotates(dst) != side_rotates(src) ||
+        side_rotates(dst) != side_rotates(src) || side_bits(dst) != side_bits(src) ||
         ((side_rotates(src) || src->format == CQKV_FMT_TURBOPROD) && dst->seed != src->seed))
         return fail(CQKV_ERR_ARG,
-                    "%s: sides differ in format, side, head dim, kv heads, rotation or seed", who);
+                    "%s: sides differ in format, bits, side, head dim, kv heads, rotation or seed", who);
     if (batch <= 0 || tokens < 0 || tokens > src->capacity || tokens > dst->capacity)
         return fail(CQKV_ERR_ARG, "%s: batch %d, %d tokens for capacities %d -> %d", who, batch,
                     tokens, src->capacity, dst->capacity);

@@ -58,6 +58,17 @@ inline bool is_turbo(int32_t format) {
 
 inline bool supported_dim(int32_t d) { return d == 64 || d == 128; }
 
+// TurboQuant width of a side (QuantFormat::TurboMse{bits} / TurboProd{bits}; 0 selects 4), 0 for
+// the other formats.
+inline int side_bits(const cqkv_side *s) {
+    return is_turbo(s->format) ? (s->bits ? s->bits : 4) : 0;
+}
+// Bits of a TurboQuant side's codebook codes (TurboProd: bits - 1), 0 for the other formats.
+// The cache stores them as nibbles whatever the width.
+inline int turbo_code_bits(const cqkv_side *s) {
+    return s->format == CQKV_FMT_TURBOPROD ? side_bits(s) - 1 : side_bits(s);
+}
+
 // The side's rows are Hadamard-rotated before quantization (CQKV_ROT_DEFAULT: TURBO4 only).
 inline bool side_rotates(const cqkv_side *s) {
     return s->rotation == CQKV_ROT_HADAMARD ||

@@ -171,19 +171,32 @@ static int decode_prepare(DecodeArgs &a, const char *who, const void *q, int32_t
     fill_rotation(k, a.ksign_bits, &rs);
     fill_rotation(v, a.vsign_bits, &rs);
     a.rot_scale = 1.0f / sqrtf((float)d);
-    if (k->format == CQKV_FMT_TURBO4 || v->format == CQKV_FMT_TURBO4) {
-        float bnd[16], cent[16];
-        if (turbo_codebook(d, 4, cent, bnd) != 0)
+    // kernel formats: TurboMse keys and values of different widths cannot share the 64 KB code
+    // table, so the side with the narrower (at most 3-bit) codes takes a compact table of its own
+    const int kb = turbo_code_bits(k), vb = turbo_code_bits(v);
+    a.kfmt = k->format;
+    a.vfmt = v->format;
+    if (k->format == CQKV_FMT_TURBO4 && v->format == CQKV_FMT_TURBO4 && kb != vb) {
+        if (kb <= 3) a.kfmt = kFmtTurboC;
+        else a.vfmt = kFmtTurboC;
+    }
+    float bnd[16], cent[16];
+    if (a.kfmt == CQKV_FMT_TURBO4 || a.vfmt == CQKV_FMT_TURBO4) {  // the 64 KB table's codebook
+        if (turbo_codebook(d, a.kfmt == CQKV_FMT_TURBO4 ? kb : vb, cent, bnd) != 0)
             return fail(CQKV_ERR_ARG, "%s: turbo codebook D=%d", who, d);
         for (int i = 0; i < 16; ++i) a.cent[i] = cent[i];
     }
-    if (k->format == CQKV_FMT_TURBOPROD) {  // the 3-bit codebook and S of the keys
-        float bnd[16], cent[16];
-        if (turbo_codebook(d, 3, cent, bnd) != 0)
+    if (a.kfmt == CQKV_FMT_TURBOPROD || a.kfmt == kFmtTurboC) {  // compact key codebook
+        if (turbo_codebook(d, kb, cent, bnd) != 0)
             return fail(CQKV_ERR_ARG, "%s: turbo codebook D=%d", who, d);
-        for (int i = 0; i < 8; ++i) a.kcent[i] = cent[i];
-        a.qjl = k->qjl;
+        for (int i = 0; i < (1 << kb); ++i) a.kcent[i] = cent[i];
     }
+    if (a.vfmt == kFmtTurboC) {  // compact value codebook
+        if (turbo_codebook(d, vb, cent, bnd) != 0)
+            return fail(CQKV_ERR_ARG, "%s: turbo codebook D=%d", who, d);
+        for (int i = 0; i < (1 << vb); ++i) a.vcent[i] = cent[i];
+    }
+    if (k->format == CQKV_FMT_TURBOPROD) a.qjl = k->qjl;
     return CQKV_OK;
 }
 
@@ -199,6 +212,7 @@ static hipError_t decode_launch(const DecodeArgs &a, int kf, int vf, int d, hipS
     case CQKV_FMT_MXFP8: decode_launch_k4(vf, d, grid, st, a); break;
     case CQKV_FMT_NVFP4: decode_launch_k3(vf, d, grid, st, a); break;
     case CQKV_FMT_TURBOPROD: decode_launch_k1(vf, d, grid, st, a); break;
+    case kFmtTurboC: decode_launch_k6(vf, d, grid, st, a); break;
     default: decode_launch_k0(vf, d, grid, st, a); break;
     }
     hipError_t e = hipGetLastError();
@@ -343,7 +357,7 @@ static int decode_dense(const char *who, const void *q, int32_t q_dtype,
         a.part_o = (float *)ws;
         a.part_lse = (float *)((char *)ws + lse_off);
     }
-    hipError_t e = decode_launch(a, k->format, v->format, d, st);
+    hipError_t e = decode_launch(a, a.kfmt, a.vfmt, d, st);
     if (owned) {
         hipError_t fe = hipFreeAsync(ws, st);
         if (e == hipSuccess) e = fe;
@@ -479,6 +493,7 @@ static int check_blocks(const cqkv_kv_block *blocks, int32_t n_blocks, int32_t b
         if (int rc = check_side(bl.v, who)) return rc;
         const cqkv_kv_block &b0 = blocks[0];
         if (bl.k->format != b0.k->format || bl.v->format != b0.v->format ||
+            side_bits(bl.k) != side_bits(b0.k) || side_bits(bl.v) != side_bits(b0.v) ||
             bl.k->head_dim != b0.k->head_dim || bl.v->head_dim != b0.k->head_dim ||
             bl.k->kv_heads != b0.k->kv_heads || bl.v->kv_heads != b0.k->kv_heads ||
             bl.k->is_value != 0 || bl.v->is_value != 1 || side_rotates(bl.k) != side_rotates(b0.k) ||
@@ -555,7 +570,7 @@ extern "C" int cqkv_decode_attention_paged(const void *q, int32_t q_dtype,
         a.part_o = (float *)((char *)ws + part_off);
         a.part_lse = (float *)((char *)ws + part_off + lse_off);
     }
-    if (e == hipSuccess) e = decode_launch(a, blocks[0].k->format, blocks[0].v->format, d, st);
+    if (e == hipSuccess) e = decode_launch(a, a.kfmt, a.vfmt, d, st);
     if (owned) {
         hipError_t fe = hipFreeAsync(ws, st);
         if (e == hipSuccess) e = fe;

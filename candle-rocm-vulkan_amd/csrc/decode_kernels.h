@@ -75,10 +75,12 @@ struct DecodeArgs {
     int32_t rot_k, rot_v;                   // rotated key / value sides: rotate q, unrotate o
     uint32_t ksign_bits[4], vsign_bits[4];  // their rotation signs (bit set -> -1)
     float rot_scale;                        // 1 / sqrt(D)
-    float cent[16];  // TURBO4 codebook (the same for keys and values at one head dim)
+    float cent[16];  // the TURBO4 code table's codebook (keys', else values'; one per kernel)
     const PagedSeg *segs;  // paged: one segment per split (the planes above are unused)
     const float *qjl;      // TURBOPROD keys: the D x D QJL matrix S (device, row-major)
-    float kcent[8];        // TURBOPROD keys: the 3-bit codebook
+    float kcent[8];        // compact key table (TURBOPROD, kFmtTurboC keys): their codebook
+    float vcent[8];        // compact value table (kFmtTurboC values): their codebook
+    int32_t kfmt, vfmt;    // host: the kernel formats of the call (kFmtTurboC where it applies)
 };
 
 constexpr float kQjlConst = 1.2533141f;  // sqrt(pi / 2) as the reference's QJL_CONST (turbo.rs:26)
@@ -108,7 +110,19 @@ __device__ inline void fwht_pairs_dec(float &v0, float &v1, int lane) {
 
 __device__ inline bool sign_bit(const uint32_t *bits, int j) { return (bits[j >> 5] >> (j & 31)) & 1u; }
 
-// Byte codes (FP8, MXFP8) or nibbles (MXFP4, NVFP4, TURBO4).
+// Kernel-internal format id: TurboMse values or keys whose codes have at most 3 bits, decoded
+// through a compact per-side table (as TurboProd keys' codes are) when the other side's
+// TurboMse codebook occupies the 64 KB code table (TurboKvCache::with_formats(TurboMse{4},
+// TurboMse{3}, ..)).
+constexpr int kFmtTurboC = 6;
+// TurboMse codes (either table).
+template <int FMT>
+constexpr bool turbo_mse() { return FMT == CQKV_FMT_TURBO4 || FMT == kFmtTurboC; }
+// Codes of at most 3 bits through the compact byte-indexed table.
+template <int FMT>
+constexpr bool compact_tab() { return FMT == CQKV_FMT_TURBOPROD || FMT == kFmtTurboC; }
+
+// Byte codes (FP8, MXFP8) or nibbles (MXFP4, NVFP4, TurboQuant).
 template <int FMT>
 constexpr bool is8() { return FMT == CQKV_FMT_FP8 || FMT == CQKV_FMT_MXFP8; }
 
@@ -150,7 +164,7 @@ struct Tile {
 // 94.7-95.9 -> 94.3-94.6 us; MXFP4 config 3 got 2 % slower and keeps the broadcast.
 template <int FMT>
 constexpr bool direct_scales() {
-    return FMT == CQKV_FMT_FP8 || FMT == CQKV_FMT_TURBO4;
+    return FMT == CQKV_FMT_FP8 || turbo_mse<FMT>();
 }
 
 // The 32-bit scale words of keys kb .. kb + 7 (kb a multiple of 8: two aligned 16-byte loads).
@@ -227,7 +241,7 @@ __device__ inline void load_tile(Tile<KF, VF, D> &r, int tile, bool live, int la
         }
     }
     const uint32_t kl = t0 + (lane & 31);
-    if constexpr (KF == CQKV_FMT_TURBO4 || KF == CQKV_FMT_TURBOPROD)
+    if constexpr (turbo_mse<KF>() || KF == CQKV_FMT_TURBOPROD)
         load_scales8<4>(r.ks8, ksr, t0 + 8 * g, oob);
     if constexpr (KF == CQKV_FMT_TURBOPROD) {
         // the scales plane: norms, |r| (at cap * 4), sign bits (at cap * 8, D / 8 per key)
@@ -276,7 +290,7 @@ __device__ inline uint32_t fp4x2_to_bf16x2(uint32_t w, int byte_sel, float scale
 // MFMA operand type: bf16 for FP8 / MXFP4 (their codes decode exactly), f16 for TurboQuant
 // (codebook values, rotated queries: 11 significant bits instead of 8).
 template <int FMT>
-using op_t = typename std::conditional<FMT == CQKV_FMT_TURBO4 || FMT == CQKV_FMT_TURBOPROD, f16x8,
+using op_t = typename std::conditional<turbo_mse<FMT>() || FMT == CQKV_FMT_TURBOPROD, f16x8,
                                       bf16x8>::type;
 
 typedef __attribute__((address_space(3))) const uint32_t lds_u32;
@@ -325,6 +339,11 @@ __device__ inline op_t<FMT> decode8(uint32_t w0, uint32_t w1, float scale, uint3
         r.y = fp4x2_to_bf16x2(w0, 1, scale);
         r.z = fp4x2_to_bf16x2(w0, 2, scale);
         r.w = fp4x2_to_bf16x2(w0, 3, scale);
+    } else if constexpr (compact_tab<FMT>()) {  // tab: the side's compact table
+        r.x = prod_pair<0>(tab, w0);
+        r.y = prod_pair<1>(tab, w0);
+        r.z = prod_pair<2>(tab, w0);
+        r.w = prod_pair<3>(tab, w0);
     } else {
         r.x = turbo_pair<0>(tab, w0);
         r.y = turbo_pair<1>(tab, w0);
@@ -385,7 +404,8 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
                                     const op_t<KF> *qhi, const op_t<KF> *qlo, bool q_split, int lane,
                                     int lo, int hi, int lo_max, int hi_min, int L, int koff,
                                     uint32_t tab, float &m_run, float &l_run,
-                                    f32x4 *acc, const op_t<KF> *qsop, uint32_t ktab) {
+                                    f32x4 *acc, const op_t<KF> *qsop, uint32_t ktab,
+                                    uint32_t vtab) {
     constexpr int NCH = D / 32;
     const int g = lane >> 4;
     // tile and L are rows of the current block (the whole cache when not paged); keys of the
@@ -424,7 +444,7 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
                 sc0 = cur.kscale[0] ? __uint_as_float(cur.kscale[0] << 23) : 1.0f;
                 sc1 = cur.kscale[1] ? __uint_as_float(cur.kscale[1] << 23) : 1.0f;
             }
-            if constexpr (KF == CQKV_FMT_TURBOPROD) {
+            if constexpr (compact_tab<KF>()) {
                 k0 = __builtin_bit_cast(op_t<KF>, u32x4{prod_pair<0>(ktab, cur.k[0][j]),
                                                         prod_pair<1>(ktab, cur.k[0][j]),
                                                         prod_pair<2>(ktab, cur.k[0][j]),
@@ -460,7 +480,7 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
         for (int e = 0; e < 8; ++e)
             x[e] = (x[e] + __uint_as_float(cur.kr1[e]) * kc * zk[e]) *
                    __uint_as_float(cur.ks8[e]) * a.scale_log2;
-    } else if constexpr (KF != CQKV_FMT_TURBO4) {  // scales are inside the operands
+    } else if constexpr (!turbo_mse<KF>()) {  // scales are inside the operands
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] *= a.scale_log2;
     } else {
@@ -562,7 +582,7 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
             sv[e] = __uint_as_float(vw[e]);  // FP8 scale, TURBO4 norm
             if constexpr (VF == CQKV_FMT_NVFP4)
                 vw2[e] = D == 128 && e < nv ? cur.nvb[2 * e + 1] : 0u;
-            if constexpr (VF == CQKV_FMT_TURBO4)
+            if constexpr (turbo_mse<VF>())
                 pv[e] = (e < nv && p[e] > 0.0f) ? p[e] * sv[e] : 0.0f;
             else
                 pv[e] = (e < nv && p[e] > 0.0f) ? p[e] : 0.0f;
@@ -602,12 +622,12 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
                 v0 = nvfp4x8_keys_bf16x8(cur.v[u][0], sg);
                 v1 = nvfp4x8_keys_bf16x8(cur.v[u][1], sg);
             } else {
-                v0 = decode8<VF>(cur.v[u][0], 0, 1.0f, tab);
-                v1 = decode8<VF>(cur.v[u][1], 0, 1.0f, tab);
+                v0 = decode8<VF>(cur.v[u][0], 0, 1.0f, compact_tab<VF>() ? vtab : tab);
+                v1 = decode8<VF>(cur.v[u][1], 0, 1.0f, compact_tab<VF>() ? vtab : tab);
             }
             acc[2 * u] = mfma16x16x32(v0, phi, acc[2 * u]);
             acc[2 * u + 1] = mfma16x16x32(v1, phi, acc[2 * u + 1]);
-            if constexpr (VF != CQKV_FMT_TURBO4) {  // TURBO4: P (times the norms) as one f16
+            if constexpr (!turbo_mse<VF>()) {  // TurboMse: P (times the norms) as one f16
                 acc[2 * u] = mfma16x16x32(v0, plo, acc[2 * u]);
                 acc[2 * u + 1] = mfma16x16x32(v1, plo, acc[2 * u + 1]);
             }
@@ -638,8 +658,10 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
     uint32_t *sm_tab = (uint32_t *)sm_buf;
     __shared__ float sm_m[WAVES][16], sm_l[WAVES][16];
     constexpr bool kProd = KF == CQKV_FMT_TURBOPROD;
-    // TurboProd keys: the 3-bit code-pair table (120 code bytes x 32 lanes)
-    __shared__ __attribute__((aligned(16384))) uint32_t sm_ktab[kProd ? kProdTabWords : 1];
+    // compact code-pair tables (120 code bytes x 32 lanes) of keys (TurboProd, kFmtTurboC) and of
+    // kFmtTurboC values
+    __shared__ __attribute__((aligned(16384))) uint32_t sm_ktab[compact_tab<KF>() ? kProdTabWords : 1];
+    __shared__ __attribute__((aligned(16384))) uint32_t sm_vtab[compact_tab<VF>() ? kProdTabWords : 1];
 
     // 1-D grid, plane fastest: workgroup ids are dealt round-robin to the 8 XCDs, so with
     // kv_heads a multiple of 8 each XCD takes whole planes of one kv head from every sequence -
@@ -752,8 +774,14 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
             op_t<KF> lo_unused;
             split8(qv, qsop[j], lo_unused);
         }
+    }
+    if constexpr (compact_tab<KF>()) {
         for (int i = threadIdx.x; i < kProdTabWords; i += NT)
             sm_ktab[i] = pack_f16x2(a.kcent[(i >> 5) & 7], a.kcent[(i >> 9) & 7]);
+    }
+    if constexpr (compact_tab<VF>()) {
+        for (int i = threadIdx.x; i < kProdTabWords; i += NT)
+            sm_vtab[i] = pack_f16x2(a.vcent[(i >> 5) & 7], a.vcent[(i >> 9) & 7]);
     }
     const bool q_split = a.q_split != 0;
     __syncthreads();
@@ -780,6 +808,7 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
     for (int t = 0; t < 2 * NCH; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     const uint32_t tab = (uint32_t)(size_t)sm_tab + 4 * lane;
     const uint32_t ktab = (uint32_t)(size_t)sm_ktab + 4 * (lane & 31);
+    const uint32_t vtab = (uint32_t)(size_t)sm_vtab + 4 * (lane & 31);
     float m_run = -__builtin_inff(), l_run = 0.0f;
 
     // Register sets A and B alternate; the scheduling barriers keep every load of one set
@@ -792,13 +821,13 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
     __builtin_amdgcn_sched_barrier(0);
     for (; t < te; t += 2 * WAVES) {
         compute_tile<KF, VF, D>(ta, t, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min, Lb, koff, tab,
-                             m_run, l_run, acc, kProd ? qsop : qhi, ktab);
+                             m_run, l_run, acc, kProd ? qsop : qhi, ktab, vtab);
         __builtin_amdgcn_sched_barrier(0);
         load_tile<KF, VF, D>(ta, t + 2 * WAVES, t + 2 * WAVES < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
         __builtin_amdgcn_sched_barrier(0);
         if (t + WAVES < te)
             compute_tile<KF, VF, D>(tb2, t + WAVES, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min,
-                                 Lb, koff, tab, m_run, l_run, acc, kProd ? qsop : qhi, ktab);
+                                 Lb, koff, tab, m_run, l_run, acc, kProd ? qsop : qhi, ktab, vtab);
         __builtin_amdgcn_sched_barrier(0);
         load_tile<KF, VF, D>(tb2, t + 3 * WAVES, t + 3 * WAVES < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
         __builtin_amdgcn_sched_barrier(0);
@@ -873,12 +902,19 @@ inline void launch_decode_kv(int d, dim3 grid, hipStream_t st, const DecodeArgs 
 
 template <int KF>
 inline void launch_decode_k(int vf, int d, dim3 grid, hipStream_t st, const DecodeArgs &a) {
-    switch (vf) {
-    case CQKV_FMT_FP8: launch_decode_kv<KF, CQKV_FMT_FP8>(d, grid, st, a); break;
-    case CQKV_FMT_MXFP4: launch_decode_kv<KF, CQKV_FMT_MXFP4>(d, grid, st, a); break;
-    case CQKV_FMT_MXFP8: launch_decode_kv<KF, CQKV_FMT_MXFP8>(d, grid, st, a); break;
-    case CQKV_FMT_NVFP4: launch_decode_kv<KF, CQKV_FMT_NVFP4>(d, grid, st, a); break;
-    default: launch_decode_kv<KF, CQKV_FMT_TURBO4>(d, grid, st, a); break;
+    if constexpr (KF == kFmtTurboC) {  // compact keys come with TURBO4-table values only
+        launch_decode_kv<KF, CQKV_FMT_TURBO4>(d, grid, st, a);
+    } else {
+        switch (vf) {
+        case CQKV_FMT_FP8: launch_decode_kv<KF, CQKV_FMT_FP8>(d, grid, st, a); break;
+        case CQKV_FMT_MXFP4: launch_decode_kv<KF, CQKV_FMT_MXFP4>(d, grid, st, a); break;
+        case CQKV_FMT_MXFP8: launch_decode_kv<KF, CQKV_FMT_MXFP8>(d, grid, st, a); break;
+        case CQKV_FMT_NVFP4: launch_decode_kv<KF, CQKV_FMT_NVFP4>(d, grid, st, a); break;
+        case kFmtTurboC:  // compact values come with TURBO4-table keys only
+            if constexpr (KF == CQKV_FMT_TURBO4) launch_decode_kv<KF, kFmtTurboC>(d, grid, st, a);
+            break;
+        default: launch_decode_kv<KF, CQKV_FMT_TURBO4>(d, grid, st, a); break;
+        }
     }
 }
 
@@ -891,5 +927,6 @@ CQKV_DECODE_LAUNCHER(2)
 CQKV_DECODE_LAUNCHER(3)
 CQKV_DECODE_LAUNCHER(4)
 CQKV_DECODE_LAUNCHER(5)
+CQKV_DECODE_LAUNCHER(6)
 
 }  // namespace cqkv

@@ -42,6 +42,13 @@ int check_side(const cqkv_side *s, const char *what) {
         return fail(CQKV_ERR_ARG, "%s: is_value must be 0 or 1", what);
     if (s->rotation < CQKV_ROT_DEFAULT || s->rotation > CQKV_ROT_HADAMARD)
         return fail(CQKV_ERR_ARG, "%s: rotation %d (default, none or Hadamard)", what, s->rotation);
+    if (s->format == CQKV_FMT_TURBO4 && (s->bits < 0 || s->bits > 4))
+        return fail(CQKV_ERR_ARG, "%s: TurboMse bits %d (1-4, 0: 4)", what, s->bits);
+    if (s->format == CQKV_FMT_TURBOPROD && (s->bits < 0 || s->bits == 1 || s->bits > 4))
+        return fail(CQKV_ERR_ARG, "%s: TurboProd bits %d (2-4, 0: 4)", what, s->bits);
+    if (!is_turbo(s->format) && s->bits != 0)
+        return fail(CQKV_ERR_ARG, "%s: bits %d given for a format without a width (0)", what,
+                    s->bits);
     if (s->format == CQKV_FMT_TURBOPROD) {
         if (s->is_value)
             return fail(CQKV_ERR_ARG,
@@ -191,12 +198,19 @@ size_t cqkv_scales_plane_bytes(int32_t format, int32_t head_dim, int32_t capacit
     return blocks + (cqkv::token_scale(format) ? (size_t)capacity * 4 : 0);
 }
 
-int32_t cqkv_reference_row_words(int32_t format, int32_t head_dim) {
-    const int bits = cqkv::code_bits(format);
-    if (!bits || !cqkv::supported_dim(head_dim)) return 0;
-    if (format == CQKV_FMT_TURBOPROD)  // 3-bit codes, D sign bits (formats.rs:226-240)
-        return (head_dim * 3 + 31) / 32 + (head_dim + 31) / 32 + 2;
-    const int code_words = (head_dim * bits + 31) / 32;
+int32_t cqkv_reference_row_words(int32_t format, int32_t bits, int32_t head_dim) {
+    const int cb = cqkv::code_bits(format);
+    if (!cb || !cqkv::supported_dim(head_dim)) return 0;
+    if (cqkv::is_turbo(format)) {  // formats.rs:226-240: b-bit (prod: b - 1) codes, prod signs
+        const int b = bits ? bits : 4;
+        if (format == CQKV_FMT_TURBO4 && (b < 1 || b > 4)) return 0;
+        if (format == CQKV_FMT_TURBOPROD && (b < 2 || b > 4)) return 0;
+        const int code = format == CQKV_FMT_TURBOPROD ? b - 1 : b;
+        return (head_dim * code + 31) / 32 +
+               (format == CQKV_FMT_TURBOPROD ? (head_dim + 31) / 32 : 0) + 2;
+    }
+    if (bits != 0) return 0;
+    const int code_words = (head_dim * cb + 31) / 32;
     const int be = cqkv::block_elems(format);
     const int aux_words = be ? (head_dim / be + 3) / 4 : 0;  // formats.rs:229-233
     return code_words + aux_words + 2;

@@ -30,8 +30,9 @@ void fill_rotation(const cqkv_side *s, uint32_t sign_bits[4], float *rot_scale) 
 int fill_turbo_bounds(const cqkv_side *s, float bnd[16], float *cent_out) {
     float cent[16];
     for (int i = 0; i < 16; ++i) bnd[i] = __builtin_inff();
-    // TurboMse{4}: the 4-bit codebook; TurboProd{4}: the 3-bit one (code bits = bits - 1)
-    const int bits = s->format == CQKV_FMT_TURBOPROD ? 3 : 4;
+    // TurboMse{b}: the b-bit codebook; TurboProd{b}: the (b - 1)-bit one; boundaries past the
+    // codebook's stay +inf, so the general count never passes them
+    const int bits = turbo_code_bits(s);
     if (turbo_codebook(s->head_dim, bits, cent, bnd) != 0)
         return fail(CQKV_ERR_ARG, "turbo codebook for D=%d", s->head_dim);
     if (cent_out)
@@ -80,7 +81,7 @@ static int fill_append_args(AppendArgs &a, const cqkv_side *side, const void *x,
         a.turbo_sym = turbo_symmetric(a.bnd);
     } else if (side->format == CQKV_FMT_TURBOPROD) {
         if (int rc = fill_turbo_bounds(side, a.bnd, a.cent)) return rc;
-        a.turbo_sym = 0;  // 7 boundaries: the general count
+        a.turbo_sym = 0;  // at most 7 boundaries: the general count
         a.qjl = side->qjl;
     }
     return CQKV_OK;

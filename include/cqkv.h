@@ -88,16 +88,17 @@ enum {
 };
 
 /* Cache formats: the reference's kernel mode ids (candle-core/src/accel/formats.rs:41-48).
- * TURBO4 = TurboQuant MSE, 4 bits, Hadamard rotation (QuantFormat::TurboMse{bits: 4});
- * TURBOPROD = TurboQuant prod, 4 bits (QuantFormat::TurboProd{bits: 4}, keys only): 3-bit MSE
- * codes of the rotated unit row, plus the sign bits of S r (r = the residual of the unit row to
- * its centroids, S = cqkv_qjl_matrix(D, seed)) and |r| - an unbiased inner-product estimate
- * (RowCodec::quantize_row, candle-core/src/accel/turbo.rs:299-323);
+ * TURBO4 = TurboQuant MSE, Hadamard rotation (QuantFormat::TurboMse{bits}, cqkv_side.bits 1-4,
+ * default 4); TURBOPROD = TurboQuant prod (QuantFormat::TurboProd{bits}, bits 2-4, default 4;
+ * keys only): (bits - 1)-bit MSE codes of the rotated unit row, plus the sign bits of S r (r =
+ * the residual of the unit row to its centroids, S = cqkv_qjl_matrix(D, seed)) and |r| - an
+ * unbiased inner-product estimate (RowCodec::quantize_row, candle-core/src/accel/turbo.rs:
+ * 299-323);
  * NVFP4 = E2M1 codes, an E4M3 scale per 16 elements and an f32 scale per token
  * (QuantFormat::Nvfp4); MXFP8 = E4M3 codes with an E8M0 scale per 32 elements
  * (QuantFormat::Mxfp8).
  * Plane layouts (per (batch, kv head), `capacity` tokens): codes are D bytes (8-bit formats) or
- * D/2 bytes (4-bit; TURBOPROD's 3-bit codes as nibbles) per token, keys row-major and values in
+ * D/2 bytes (4-bit; TurboQuant codes of every width as nibbles) per token, keys row-major and values in
  * 8-token tiles; scales are the block-scale bytes of every token, then an f32 per token (FP8
  * scale, TurboQuant norm, NVFP4 global scale); TURBOPROD scales: the norms, then |r| (f32 per
  * token), then D/8 sign-bit bytes per token (bit i of word i / 32 = sign of (S r)_i >= 0). */
@@ -135,6 +136,11 @@ typedef struct cqkv_side {
     int32_t kv_heads;  /* Hkv */
     int32_t capacity;  /* tokens per plane, a multiple of 32 */
     int32_t rotation;  /* CQKV_ROT_* */
+    int32_t bits;      /* TurboQuant width: TURBO4 = TurboMse{bits} 1-4, TURBOPROD = TurboProd{bits}
+                          2-4 (QuantFormat bits, formats.rs:22-29); 0 = 4. The codes (bits, or
+                          bits - 1 for TURBOPROD) are stored as nibbles at every width. 0 for the
+                          other formats. */
+    int32_t reserved;  /* 0 */
     uint64_t seed;     /* rotation seed (keys 42, values 44 by default); unused without rotation */
     void *codes;       /* device, batch * kv_heads planes of cqkv_codes_plane_bytes() */
     void *scales;      /* device, batch * kv_heads planes of cqkv_scales_plane_bytes() */
@@ -373,9 +379,11 @@ int cqkv_hadamard_rows(const void *x, int32_t dtype, int64_t rows, int64_t x_row
                        cqkv_stream_t stream);
 
 /* Reference row layout interop (candle-core/src/accel/formats.rs:206-242): rows are
- * (batch, kv_heads, tokens, row_words) u32 on the device, row_words = code + aux + 2 words.
- * import: rows -> cache positions [position, position + tokens); export: the reverse. */
-int32_t cqkv_reference_row_words(int32_t format, int32_t head_dim);
+ * (batch, kv_heads, tokens, row_words) u32 on the device, row_words = code + aux + 2 words
+ * (TurboQuant codes packed at their width, LSB first). `bits` as cqkv_side.bits (0 for the
+ * formats without a width). import: rows -> cache positions [position, position + tokens);
+ * export: the reverse. */
+int32_t cqkv_reference_row_words(int32_t format, int32_t bits, int32_t head_dim);
 int cqkv_rows_import(const cqkv_side *side, const uint32_t *rows, int32_t batch, int32_t tokens,
                      int32_t position, cqkv_stream_t stream);
 int cqkv_rows_export(const cqkv_side *side, uint32_t *rows, int32_t batch, int32_t tokens,

@@ -189,6 +189,61 @@ def prod_case():
     print("prod", kd.shape, o.shape)
 
 
+def widths_case():
+    """TurboQuant widths other than 4 (QuantFormat::TurboMse{1..3}, TurboProd{2, 3}): rows
+    through the reference kernels, and its fused decode over TurboMse{4} keys with TurboMse{3}
+    values (TurboKvCache::with_formats(TurboMse{4}, TurboMse{3}, ..), the pairing of the
+    reference's turbo_kv_cache_fused_matches_unfused test) and over TurboProd{3} keys with
+    TurboMse{2} values."""
+    quant_case("turbo3_d128", O.TURBO_MSE, 3, 128, 37, 21)
+    quant_case("turbo2_d64", O.TURBO_MSE, 2, 64, 19, 22)
+    quant_case("turbo1_d64", O.TURBO_MSE, 1, 64, 19, 23)
+    prods = {}
+    for bits, d, seed in ((3, 128, 24), (2, 64, 25)):
+        y = O.normal(seed, (33, d)) * np.float32(2.0)
+        y[1, :] = 0.0
+        rows, _ = prod_rows(y, O.qjl_matrix(d, 42), bits)
+        prods[f"x{bits}"], prods[f"rows{bits}"] = y, rows
+    np.savez_compressed(os.path.join(HERE, "ref_prod_widths.npz"), **prods)
+    B, Hq, Hkv, D, Lq, Lk = 2, 8, 2, 128, 2, 300
+    q = O.round_bf16(O.normal(801, (B, Hq, Lq, D)))
+    k = O.round_bf16(O.normal(802, (B, Hkv, Lk, D))).astype(np.float32)
+    v = O.round_bf16(O.normal(803, (B, Hkv, Lk, D))).astype(np.float32)
+    pk = O.rotation_matrix(D, O.ROT_HADAMARD, 42)
+    pv = O.rotation_matrix(D, O.ROT_HADAMARD, 44)
+    kx = O.rotate_rows(pk, k.reshape(-1, D))
+    vx = O.rotate_rows(pv, v.reshape(-1, D))
+    qr = O.rotate_rows(pk, q.reshape(-1, D)).reshape(q.shape)
+    scale = np.float32(1.0 / np.sqrt(D))
+    out = {"scale": scale}
+    for name, kmode, kbits, vbits in (("mse4_mse3", O.TURBO_MSE, 4, 3),
+                                      ("prod3_mse2", O.TURBO_PROD, 3, 2)):
+        lk_ = O.row_layout(kmode, kbits, D)
+        lv = O.row_layout(O.TURBO_MSE, vbits, D)
+        ck, bk = O.lloyd_max(D, lk_.code_bits)
+        cv, bv = O.lloyd_max(D, vbits)
+        if kmode == O.TURBO_PROD:
+            s = O.qjl_matrix(D, 42)
+            kd, _ = prod_rows(kx, s, kbits)
+            qs = (qr.reshape(-1, D).astype(np.float64) @ s.astype(np.float64).T).astype(np.float32)
+            qx = np.concatenate([qr, qs.reshape(q.shape)], -1).astype(np.float32)
+        else:
+            kd = H.tq_quant(kx.astype(np.float32), kmode, lk_.code_bits, lk_.code_words,
+                            lk_.aux_words, lk_.row_words, H.tq_tab(ck, bk))
+            qx = qr.astype(np.float32)
+        kd = kd.reshape(B, Hkv, Lk, -1)
+        vd = H.tq_quant(vx.astype(np.float32), O.TURBO_MSE, lv.code_bits, lv.code_words,
+                        lv.aux_words, lv.row_words, H.tq_tab(cv, bv)).reshape(B, Hkv, Lk, -1)
+        tab64 = np.concatenate([H.tq_tab(ck, bk), H.tq_tab(cv, bv)]).astype(np.float32)
+        k_side = (kmode, lk_.code_bits, lk_.code_words, lk_.code_words + lk_.aux_words)
+        v_side = (O.TURBO_MSE, lv.code_bits, lv.code_words, lv.code_words + lv.aux_words)
+        o = H.tq_attn(qx, kd, vd, k_side, v_side, tab64, float(scale), splits=3, group=4)
+        o = (o.reshape(-1, D) @ pv).reshape(o.shape).astype(np.float32)
+        out[f"kd_{name}"], out[f"vd_{name}"], out[f"out_{name}"] = kd, vd, o
+        print("decode", name, o.shape)
+    np.savez_compressed(os.path.join(HERE, "ref_decode_widths.npz"), **out)
+
+
 def combine_case():
     splits, rows, d = 5, 7, 32
     po = O.normal(201, (splits, rows, d))
@@ -203,6 +258,9 @@ def combine_case():
 if __name__ == "__main__":
     if not H.available():
         sys.exit("oracle/_ref/accel_host_test missing: run `make -C oracle ref` first")
+    if sys.argv[1:] == ["widths"]:  # only the TurboQuant widths fixtures
+        widths_case()
+        sys.exit(0)
     quant_case("fp8_d128", O.FP8, 0, 128, 37, 11)
     quant_case("fp8_d80", O.FP8, 0, 80, 19, 12)
     quant_case("mxfp4_d128", O.MXFP4, 0, 128, 37, 13)
@@ -219,4 +277,5 @@ if __name__ == "__main__":
     attn_format_case("nvfp4", O.NVFP4, 0)
     attn_format_case("mxfp8", O.MXFP8, 0)
     prod_case()
+    widths_case()
     combine_case()

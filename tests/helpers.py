@@ -28,21 +28,29 @@ def rotates(fmt: int, rotation: int = 0) -> bool:
     return rotation == 2 or (rotation == 0 and fmt in (0, 1))
 
 
-def oracle_rows(fmt: int, x: torch.Tensor, seed: int = 0, rotation: int = 0) -> np.ndarray:
+def obits(fmt: int, bits: int = 0) -> int:
+    """The oracle's (mode, bits) width of a cache side of cqkv width `bits` (0: 4)."""
+    return (bits or 4) if fmt in (0, 1) else BITS[fmt]
+
+
+def oracle_rows(fmt: int, x: torch.Tensor, seed: int = 0, rotation: int = 0,
+                bits: int = 0) -> np.ndarray:
     """Reference rows of x (.., d) bf16, rotated by the seed's Hadamard first when the side
-    rotates (TurboQuantizer::quantize_rows, candle-nn/src/turbo_quant.rs:180-215)."""
+    rotates (TurboQuantizer::quantize_rows, candle-nn/src/turbo_quant.rs:180-215); `bits` the
+    TurboQuant width (0: 4)."""
     xf = x.float().numpy()
     if rotates(fmt, rotation):
         pi = O.rotation_matrix(x.shape[-1], O.ROT_HADAMARD, seed)
         xf = O.rotate_rows(pi, xf.reshape(-1, x.shape[-1])).reshape(xf.shape)
     if fmt == 1:
-        return O.quantize_rows_qjl(4, xf, O.qjl_matrix(x.shape[-1], seed))
-    return O.quantize_rows(fmt, BITS[fmt], xf)
+        return O.quantize_rows_qjl(obits(1, bits), xf, O.qjl_matrix(x.shape[-1], seed))
+    return O.quantize_rows(fmt, obits(fmt, bits), xf)
 
 
 def oracle_decode(fmt: int, q: torch.Tensor, k_rows: np.ndarray, v_rows: np.ndarray, lk: int,
                   scale: float, kv_lens=None, wl=-1, wr=-1, k_seed=42, v_seed=44,
-                  v_fmt: int | None = None, rotation: int = 0) -> np.ndarray:
+                  v_fmt: int | None = None, rotation: int = 0, k_bits: int = 0,
+                  v_bits: int = 0) -> np.ndarray:
     """The reference CPU decode path (dequantize, unrotate, bf16, unfused f32 attention),
     rounded to bf16 like the reference's output; keys in `fmt`, values in `v_fmt`."""
     d = q.shape[-1]
@@ -51,7 +59,8 @@ def oracle_decode(fmt: int, q: torch.Tensor, k_rows: np.ndarray, v_rows: np.ndar
     pv = O.rotation_matrix(d, O.ROT_HADAMARD, v_seed) if rotates(v_fmt, rotation) else None
     qb = O.f32_to_bf16_bits(q.float().numpy())
     sk = O.qjl_matrix(d, k_seed) if fmt == 1 else None
-    out = O.cache_attention(qb, k_rows, v_rows, (fmt, BITS[fmt]), (v_fmt, BITS[v_fmt]), pk, pv,
+    out = O.cache_attention(qb, k_rows, v_rows, (fmt, obits(fmt, k_bits)),
+                            (v_fmt, obits(v_fmt, v_bits)), pk, pv,
                             lk, scale, kv_lens=kv_lens, wl=wl, wr=wr, threads=16, qjl_k=sk)
     return O.round_bf16(out)
 
@@ -66,18 +75,20 @@ def assert_close_bf16(got: np.ndarray, want: np.ndarray, max_abs=2e-2, mean_abs=
 
 def exact_decode(fmt: int, q: torch.Tensor, k_rows: np.ndarray, v_rows: np.ndarray, lk: int,
                  scale: float, kv_lens=None, wl=-1, wr=-1, k_seed=42, v_seed=44,
-                 v_fmt: int | None = None, rotation: int = 0) -> np.ndarray:
+                 v_fmt: int | None = None, rotation: int = 0, k_bits: int = 0,
+                 v_bits: int = 0) -> np.ndarray:
     """float64 attention over the dequantized (and unrotated) codes, without the reference
     path's bf16 rounding of the cache: the mathematical value both paths approximate."""
     b, hq, lq, d = q.shape
     v_fmt = fmt if v_fmt is None else v_fmt
     hkv = k_rows.shape[1]
     if fmt == 1:
-        kd = O.dequantize_rows_qjl(4, d, k_rows[:, :, :lk], O.qjl_matrix(d, k_seed))
+        kd = O.dequantize_rows_qjl(obits(1, k_bits), d, k_rows[:, :, :lk],
+                                   O.qjl_matrix(d, k_seed))
         kd = kd.astype(np.float64)
     else:
-        kd = O.dequantize_rows(fmt, BITS[fmt], d, k_rows[:, :, :lk]).astype(np.float64)
-    vd = O.dequantize_rows(v_fmt, BITS[v_fmt], d, v_rows[:, :, :lk]).astype(np.float64)
+        kd = O.dequantize_rows(fmt, obits(fmt, k_bits), d, k_rows[:, :, :lk]).astype(np.float64)
+    vd = O.dequantize_rows(v_fmt, obits(v_fmt, v_bits), d, v_rows[:, :, :lk]).astype(np.float64)
     if rotates(fmt, rotation):
         kd = kd @ O.rotation_matrix(d, O.ROT_HADAMARD, k_seed).astype(np.float64)
     if rotates(v_fmt, rotation):
@@ -127,19 +138,29 @@ def assert_decode_parity(fmt: int, got: np.ndarray, ref: np.ndarray, exact: np.n
                                                                     err.mean())
 
 
-def assert_turbo_rows_close(got: np.ndarray, want: np.ndarray, d: int):
-    """TurboQuant-4 rows against the reference encoder's rows under the reference's own
-    end-to-end criterion (candle-core/tests/accel_kernels_host.rs:998-1027): norms within rtol
-    1e-5, at most 0.1 % of the codes flipped, each flip to a neighbouring code."""
-    cw = d // 8
+def packed_codes(rows: np.ndarray, bits: int, d: int) -> np.ndarray:
+    """The `bits`-bit codes of reference rows (LSB first across the code words)."""
+    out = np.zeros(rows.shape[:-1] + (d,), dtype=np.int64)
+    for j in range(d):
+        for bit in range(bits):
+            pos = bits * j + bit
+            out[..., j] |= ((rows[..., pos // 32] >> (pos % 32)) & 1).astype(np.int64) << bit
+    return out
+
+
+def assert_turbo_rows_close(got: np.ndarray, want: np.ndarray, d: int, bits: int = 4):
+    """TurboQuant (TurboMse{bits}) rows against the reference encoder's rows under the
+    reference's own end-to-end criterion (candle-core/tests/accel_kernels_host.rs:998-1027):
+    norms within rtol 1e-5, at most 0.1 % of the codes flipped, each flip to a neighbouring
+    code."""
+    cw = (d * bits + 31) // 32
     np.testing.assert_allclose(got[..., cw].view(np.float32), want[..., cw].view(np.float32),
                                rtol=1e-5)
     assert (got[..., cw + 1] == 0).all()
-    gc = np.stack([(got[..., :cw] >> (4 * i)) & 15 for i in range(8)])
-    wc = np.stack([(want[..., :cw] >> (4 * i)) & 15 for i in range(8)])
+    gc, wc = packed_codes(got, bits, d), packed_codes(want, bits, d)
     flips = (gc != wc).sum()
-    assert flips <= gc.size // 1000, flips
-    assert (np.abs(gc.astype(int) - wc.astype(int)) <= 1).all()
+    assert flips <= max(2, gc.size // 1000), flips
+    assert (np.abs(gc - wc) <= 1).all()
 
 
 def assert_rotated_rows_close(fmt: int, got: np.ndarray, want: np.ndarray, d: int):
@@ -182,23 +203,15 @@ def assert_rotated_rows_close(fmt: int, got: np.ndarray, want: np.ndarray, d: in
     assert (np.abs(gc - wc)[same] <= 1).all()
 
 
-def assert_prod_rows_close(got: np.ndarray, want: np.ndarray, d: int):
-    """TurboProd{4} rows against the reference encoder's: the 3-bit codes and the norm by the
+def assert_prod_rows_close(got: np.ndarray, want: np.ndarray, d: int, bits: int = 4):
+    """TurboProd{bits} rows against the reference encoder's: the (bits - 1)-bit codes and the norm by the
     TurboQuant criterion (<= 0.1 % code flips to a neighbour, norms rtol 1e-5); in rows without a
     code flip |r| within rtol 1e-4 and the QJL sign bits equal but for <= 0.1 % (a projection of
     the residual within rounding of zero; the reference leaves the matmul's summation order
     open)."""
-    lay = O.row_layout(1, 4, d)
+    lay = O.row_layout(1, bits, d)
     cw, aw = lay.code_words, lay.aux_words
-
-    def codes(rows):
-        out = np.zeros(rows.shape[:-1] + (d,), dtype=np.int64)
-        for j in range(d):
-            for bit in range(3):
-                pos = 3 * j + bit
-                out[..., j] |= ((rows[..., pos // 32] >> (pos % 32)) & 1).astype(np.int64) << bit
-        return out
-    gc, wc = codes(got), codes(want)
+    gc, wc = packed_codes(got, bits - 1, d), packed_codes(want, bits - 1, d)
     flips = gc != wc
     assert flips.sum() <= max(2, gc.size // 1000), flips.sum()
     assert (np.abs(gc - wc) <= 1).all()
@@ -213,12 +226,14 @@ def assert_prod_rows_close(got: np.ndarray, want: np.ndarray, d: int):
 
 
 def assert_rows_match_source(fmt: int, got: np.ndarray, src: torch.Tensor, seed: int,
-                             rotation: int = 0):
+                             rotation: int = 0, bits: int = 0):
     """Cache rows (exported in the reference layout) against the reference encoder applied to
-    the source rows: bit for bit, TurboQuant-4 by the reference's flip criterion."""
-    want = oracle_rows(fmt, src, seed, rotation)
+    the source rows: bit for bit, TurboQuant by the reference's flip criterion."""
+    want = oracle_rows(fmt, src, seed, rotation, bits)
     if fmt == 1:
-        assert_prod_rows_close(got, want, src.shape[-1])
+        assert_prod_rows_close(got, want, src.shape[-1], obits(1, bits))
+    elif fmt == 0 and rotates(fmt, rotation):
+        assert_turbo_rows_close(got, want, src.shape[-1], obits(0, bits))
     elif rotates(fmt, rotation):
         assert_rotated_rows_close(fmt, got, want, src.shape[-1])
     else:

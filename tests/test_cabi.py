@@ -51,19 +51,30 @@ def test_plane_sizes(cq):
 
 
 def test_reference_row_words_known_answers(cq):
-    """candle-core/src/accel/formats.rs:467-477: MXFP4 D=64 8 code + 1 aux words, NVFP4 D=128
-    16 + 2 (+ rsc0, rsc1); MXFP8 D=128 32 + 1 + 2 by the same rule (formats.rs:224-242)."""
+    """candle-core/src/accel/formats.rs:467-477: TurboMse{3} D=128 12 code words + rsc0, rsc1,
+    TurboProd{4} D=128 12 + 4 aux + 2, MXFP4 D=64 8 code + 1 aux words, NVFP4 D=128 16 + 2
+    (+ rsc0, rsc1); MXFP8 D=128 32 + 1 + 2 by the same rule (formats.rs:224-242). Widths outside
+    TurboMse 1-4 / TurboProd 2-4, or a width for another format, give 0."""
+    assert cq.reference_row_words(cq.TURBO4, 128, 3) == 12 + 2
+    assert cq.reference_row_words(cq.TURBOPROD, 128, 4) == 12 + 4 + 2
+    assert cq.reference_row_words(cq.TURBO4, 128, 1) == 4 + 2
+    assert cq.reference_row_words(cq.TURBOPROD, 64, 2) == 2 + 2 + 2
+    assert cq.reference_row_words(cq.TURBO4, 128, 5) == 0
+    assert cq.reference_row_words(cq.TURBOPROD, 128, 1) == 0
+    assert cq.reference_row_words(cq.FP8, 128, 4) == 0
     assert cq.reference_row_words(cq.MXFP4, 64) == 8 + 1 + 2
     assert cq.reference_row_words(cq.NVFP4, 128) == 16 + 2 + 2
     assert cq.reference_row_words(cq.MXFP8, 128) == 32 + 1 + 2
     assert cq.reference_row_words(cq.NVFP4, 64) == 8 + 1 + 2
 
 
-@pytest.mark.parametrize("fmt,bits", [(5, 0), (2, 0), (0, 4), (3, 0), (4, 0)])
+@pytest.mark.parametrize("fmt,bits", [(5, 0), (2, 0), (0, 4), (3, 0), (4, 0), (0, 1), (0, 2),
+                                      (0, 3), (1, 2), (1, 3), (1, 4)])
 @pytest.mark.parametrize("d", [64, 128])
 def test_reference_row_words_match_oracle_layout(cq, fmt, bits, d):
     # candle-core/src/accel/formats.rs:224-242, restated by the oracle
-    assert cq.reference_row_words(fmt, d) == O.row_layout(fmt, bits, d).row_words
+    cbits = bits if fmt in (0, 1) else 0
+    assert cq.reference_row_words(fmt, d, cbits) == O.row_layout(fmt, bits, d).row_words
 
 
 @pytest.mark.parametrize("d", [64, 128])
@@ -99,22 +110,22 @@ def test_argument_errors_are_status_codes(cq):
     x = (ctypes.c_int64 * 3)(1, 1, 1)
     assert L.cqkv_quant_append(None, None, 0, x, 1, 1, None, 0, None) == cq.ERR_ARG
     assert b"null cache side" in L.cqkv_last_error()
-    side = cq.Side(cq.FP8, 0, 96, 8, 64, 0, 0, 1, 1)
+    side = cq.Side(cq.FP8, 0, 96, 8, 64, 0, 0, 0, 0, 1, 1)
     assert L.cqkv_quant_append(ctypes.byref(side), ctypes.c_void_p(1), 0, x, 1, 1, None, 0,
                                None) == cq.ERR_ARG
     assert b"head_dim 96" in L.cqkv_last_error()
-    side = cq.Side(cq.FP8, 0, 128, 8, 48, 0, 0, 1, 1)
+    side = cq.Side(cq.FP8, 0, 128, 8, 48, 0, 0, 0, 0, 1, 1)
     assert L.cqkv_quant_append(ctypes.byref(side), ctypes.c_void_p(1), 0, x, 1, 1, None, 0,
                                None) == cq.ERR_ARG
     assert b"multiple of 32" in L.cqkv_last_error()
-    side = cq.Side(cq.FP8, 0, 128, 8, 64, 0, 0, 1, 1)
+    side = cq.Side(cq.FP8, 0, 128, 8, 64, 0, 0, 0, 0, 1, 1)
     # appending past the capacity is refused before any launch
     assert L.cqkv_quant_append(ctypes.byref(side), ctypes.c_void_p(1), 0, x, 1, 10, None, 60,
                                None) == cq.ERR_ARG
     assert b"exceed the capacity" in L.cqkv_last_error()
     # decode: a key side given twice, more (query, head) columns than 2^24, kv_len past the
     # capacity
-    vs = cq.Side(cq.FP8, 1, 128, 8, 64, 0, 0, 1, 1)
+    vs = cq.Side(cq.FP8, 1, 128, 8, 64, 0, 0, 0, 0, 1, 1)
     args = lambda k, v, hq, lq, kvlen: L.cqkv_decode_attention(
         ctypes.c_void_p(1), 0, x, ctypes.byref(k), ctypes.byref(v), 1, hq, lq, None, kvlen,
         0.1, -1, -1, ctypes.c_void_p(1), 0, x, 0, None, 0, None)
@@ -155,8 +166,8 @@ def test_flash_attn_ext_argument_errors(cq):
     assert b"cu_seqlens" in L.cqkv_last_error()
     assert call(cu_q=one, cu_k=one, tq=0, tk=5) == cq.ERR_ARG
     assert b"total_q" in L.cqkv_last_error()
-    side = cq.Side(cq.FP8, 0, 128, 2, 64, 0, 0, 1, 1)
-    vside = cq.Side(cq.FP8, 1, 128, 2, 64, 0, 0, 1, 1)
+    side = cq.Side(cq.FP8, 0, 128, 2, 64, 0, 0, 0, 0, 1, 1)
+    vside = cq.Side(cq.FP8, 1, 128, 2, 64, 0, 0, 0, 0, 1, 1)
     assert call(cu_q=one, cu_k=one, tq=5, tk=5, kc=ctypes.byref(side),
                 vc=ctypes.byref(vside)) == cq.ERR_ARG
     assert b"dense batches only" in L.cqkv_last_error()
@@ -173,11 +184,11 @@ def test_paged_argument_errors_and_workspace(cq):
     (candle-nn/src/flash_attn.rs:650-686) before any launch, and sizes its scratch."""
     L = cq.lib()
     x = (ctypes.c_int64 * 3)(1, 1, 1)
-    k0 = cq.Side(cq.FP8, 0, 128, 8, 64, 0, 0, 1, 1)
-    v0 = cq.Side(cq.FP8, 1, 128, 8, 64, 0, 0, 1, 1)
-    k1 = cq.Side(cq.FP8, 0, 128, 8, 128, 0, 0, 1, 1)
-    v1 = cq.Side(cq.FP8, 1, 128, 8, 128, 0, 0, 1, 1)
-    kx = cq.Side(cq.MXFP4, 0, 128, 8, 64, 0, 0, 1, 1)
+    k0 = cq.Side(cq.FP8, 0, 128, 8, 64, 0, 0, 0, 0, 1, 1)
+    v0 = cq.Side(cq.FP8, 1, 128, 8, 64, 0, 0, 0, 0, 1, 1)
+    k1 = cq.Side(cq.FP8, 0, 128, 8, 128, 0, 0, 0, 0, 1, 1)
+    v1 = cq.Side(cq.FP8, 1, 128, 8, 128, 0, 0, 0, 0, 1, 1)
+    kx = cq.Side(cq.MXFP4, 0, 128, 8, 64, 0, 0, 0, 0, 1, 1)
 
     def blocks(*bl):
         arr = (cq.KvBlock * len(bl))()
@@ -218,10 +229,10 @@ def test_rope_quant_append_argument_errors(cq):
     L = cq.lib()
     x = (ctypes.c_int64 * 3)(1, 128, 128)
     one = ctypes.c_void_p(1)
-    k = cq.Side(cq.FP8, 0, 128, 2, 64, 0, 0, 1, 1)
-    v = cq.Side(cq.FP8, 1, 128, 2, 64, 0, 0, 1, 1)
-    vm = cq.Side(cq.MXFP4, 1, 128, 2, 96, 0, 0, 1, 1)  # another format is fine, capacity not
-    vr = cq.Side(cq.FP8, 1, 128, 2, 64, 7, 0, 1, 1)  # no rotation 7
+    k = cq.Side(cq.FP8, 0, 128, 2, 64, 0, 0, 0, 0, 1, 1)
+    v = cq.Side(cq.FP8, 1, 128, 2, 64, 0, 0, 0, 0, 1, 1)
+    vm = cq.Side(cq.MXFP4, 1, 128, 2, 96, 0, 0, 0, 0, 1, 1)  # another format is fine, capacity not
+    vr = cq.Side(cq.FP8, 1, 128, 2, 64, 7, 0, 0, 0, 1, 1)  # no rotation 7
 
     def call(ks=k, vs=v, kind=1, tokens=4, position=0, rows=100, hq=8, positions=None, cos=one):
         return L.cqkv_rope_quant_append(ctypes.byref(ks), ctypes.byref(vs), one, x, one, x, one,
@@ -278,26 +289,26 @@ def test_side_copy_argument_errors(cq):
     """Cache growth copies only between sides of one format, kind, shape and rotation, and only
     tokens both capacities hold; nothing is launched for zero tokens."""
     L = cq.lib()
-    src = cq.Side(cq.MXFP4, 0, 128, 8, 64, 0, 42, 1, 1)
+    src = cq.Side(cq.MXFP4, 0, 128, 8, 64, 0, 0, 0, 42, 1, 1)
 
     def copy(dst, tokens=40, batch=2):
         return L.cqkv_side_copy(ctypes.byref(dst), ctypes.byref(src), batch, tokens, None)
-    assert copy(cq.Side(cq.FP8, 0, 128, 8, 128, 0, 42, 1, 1)) == cq.ERR_ARG
+    assert copy(cq.Side(cq.FP8, 0, 128, 8, 128, 0, 0, 0, 42, 1, 1)) == cq.ERR_ARG
     assert b"format" in L.cqkv_last_error()
-    assert copy(cq.Side(cq.MXFP4, 1, 128, 8, 128, 0, 42, 1, 1)) == cq.ERR_ARG  # value side
-    assert copy(cq.Side(cq.MXFP4, 0, 64, 8, 128, 0, 42, 1, 1)) == cq.ERR_ARG
-    assert copy(cq.Side(cq.MXFP4, 0, 128, 4, 128, 0, 42, 1, 1)) == cq.ERR_ARG
-    assert copy(cq.Side(cq.MXFP4, 0, 128, 8, 128, cq.ROT_HADAMARD, 42, 1, 1)) == cq.ERR_ARG
-    big = cq.Side(cq.MXFP4, 0, 128, 8, 128, 0, 42, 1, 1)
+    assert copy(cq.Side(cq.MXFP4, 1, 128, 8, 128, 0, 0, 0, 42, 1, 1)) == cq.ERR_ARG  # value side
+    assert copy(cq.Side(cq.MXFP4, 0, 64, 8, 128, 0, 0, 0, 42, 1, 1)) == cq.ERR_ARG
+    assert copy(cq.Side(cq.MXFP4, 0, 128, 4, 128, 0, 0, 0, 42, 1, 1)) == cq.ERR_ARG
+    assert copy(cq.Side(cq.MXFP4, 0, 128, 8, 128, cq.ROT_HADAMARD, 0, 0, 42, 1, 1)) == cq.ERR_ARG
+    big = cq.Side(cq.MXFP4, 0, 128, 8, 128, 0, 0, 0, 42, 1, 1)
     assert copy(big, tokens=65) == cq.ERR_ARG  # more than the source holds
     assert b"capacities" in L.cqkv_last_error()
-    assert copy(cq.Side(cq.MXFP4, 0, 128, 8, 32, 0, 42, 1, 1)) == cq.ERR_ARG  # 40 > 32
+    assert copy(cq.Side(cq.MXFP4, 0, 128, 8, 32, 0, 0, 0, 42, 1, 1)) == cq.ERR_ARG  # 40 > 32
     assert copy(big, batch=0) == cq.ERR_ARG
     assert copy(big, tokens=0) == cq.OK
     # an unrotated side ignores the seed; a rotated one needs the same seed
-    assert copy(cq.Side(cq.MXFP4, 0, 128, 8, 128, 0, 7, 1, 1), tokens=0) == cq.OK
-    rsrc = cq.Side(cq.MXFP4, 0, 128, 8, 64, cq.ROT_HADAMARD, 42, 1, 1)
-    rdst = cq.Side(cq.MXFP4, 0, 128, 8, 128, cq.ROT_HADAMARD, 7, 1, 1)
+    assert copy(cq.Side(cq.MXFP4, 0, 128, 8, 128, 0, 0, 0, 7, 1, 1), tokens=0) == cq.OK
+    rsrc = cq.Side(cq.MXFP4, 0, 128, 8, 64, cq.ROT_HADAMARD, 0, 0, 42, 1, 1)
+    rdst = cq.Side(cq.MXFP4, 0, 128, 8, 128, cq.ROT_HADAMARD, 0, 0, 7, 1, 1)
     assert L.cqkv_side_copy(ctypes.byref(rdst), ctypes.byref(rsrc), 2, 0, None) == cq.ERR_ARG
     assert b"seed" in L.cqkv_last_error()
 
@@ -357,14 +368,14 @@ def test_turboprod_sides_and_qjl_matrix(cq):
     L = cq.lib()
     assert L.cqkv_codes_plane_bytes(cq.TURBOPROD, 128, 64) == 64 * 64
     assert L.cqkv_scales_plane_bytes(cq.TURBOPROD, 128, 64) == 64 * (8 + 16)
-    assert L.cqkv_reference_row_words(cq.TURBOPROD, 128) == 12 + 4 + 2
-    assert L.cqkv_reference_row_words(cq.TURBOPROD, 64) == 6 + 2 + 2
+    assert L.cqkv_reference_row_words(cq.TURBOPROD, 0, 128) == 12 + 4 + 2
+    assert L.cqkv_reference_row_words(cq.TURBOPROD, 4, 64) == 6 + 2 + 2
     np.testing.assert_array_equal(cq.qjl_matrix(128, 42).numpy(), O.qjl_matrix(128, 42))
     x = (ctypes.c_int64 * 3)(1, 128, 128)
     one = ctypes.c_void_p(256)
-    val = cq.Side(cq.TURBOPROD, 1, 128, 2, 64, 0, 44, 256, 256, 256)
+    val = cq.Side(cq.TURBOPROD, 1, 128, 2, 64, 0, 0, 0, 44, 256, 256, 256)
     assert L.cqkv_quant_append(ctypes.byref(val), one, 0, x, 1, 4, None, 0, None) == cq.ERR_ARG
     assert b"key format" in L.cqkv_last_error()
-    noqjl = cq.Side(cq.TURBOPROD, 0, 128, 2, 64, 0, 42, 256, 256, None)
+    noqjl = cq.Side(cq.TURBOPROD, 0, 128, 2, 64, 0, 0, 0, 42, 256, 256, None)
     assert L.cqkv_quant_append(ctypes.byref(noqjl), one, 0, x, 1, 4, None, 0, None) == cq.ERR_ARG
     assert b"QJL" in L.cqkv_last_error()

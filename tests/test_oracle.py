@@ -274,19 +274,97 @@ def test_quantize_rows_bit_exact_with_reference_kernel(name):
     np.testing.assert_array_equal(got, g["rows"])
 
 
-def test_turbo_quantize_rows_vs_reference_kernel():
+def turbo_codes(rows: np.ndarray, bits: int, d: int) -> np.ndarray:
+    """The b-bit codes of packed reference rows (LSB first across words)."""
+    out = np.zeros(rows.shape[:-1] + (d,), dtype=np.int64)
+    for j in range(d):
+        for bit in range(bits):
+            pos = bits * j + bit
+            out[..., j] |= ((rows[..., pos // 32] >> (pos % 32)) & 1).astype(np.int64) << bit
+    return out
+
+
+@pytest.mark.parametrize("name,bits,d", [("turbo4_d128", 4, 128), ("turbo3_d128", 3, 128),
+                                         ("turbo2_d64", 2, 64), ("turbo1_d64", 1, 64)])
+def test_turbo_quantize_rows_vs_reference_kernel(name, bits, d):
     # the reference kernel sums the norm in a tree: codes may flip at a boundary (<= 0.1 %) and
-    # the norm differs in the last bits (candle-core/tests/accel_kernels_host.rs:1000-1027)
-    g = gold("ref_quant_turbo4_d128")
-    got = O.quantize_rows(O.TURBO_MSE, 4, g["x"])
+    # the norm differs in the last bits (candle-core/tests/accel_kernels_host.rs:1000-1027);
+    # TurboMse{1..4} (row layouts of formats.rs:224-242, b-bit codes packed LSB first)
+    g = gold(f"ref_quant_{name}")
+    got = O.quantize_rows(O.TURBO_MSE, bits, g["x"])
     want = g["rows"]
-    l = O.row_layout(O.TURBO_MSE, 4, 128)
+    l = O.row_layout(O.TURBO_MSE, bits, d)
+    assert got.shape == want.shape == (want.shape[0], l.row_words)
     gn = got[:, l.code_words].view(np.float32)
     wn = want[:, l.code_words].view(np.float32)
     np.testing.assert_allclose(gn, wn, rtol=1e-5, atol=1e-6)
-    gc = np.stack([(got[:, :16] >> (4 * i)) & 15 for i in range(8)])
-    wc = np.stack([(want[:, :16] >> (4 * i)) & 15 for i in range(8)])
-    assert (gc != wc).sum() <= got.shape[0] * 128 // 1000
+    gc, wc = turbo_codes(got, bits, d), turbo_codes(want, bits, d)
+    assert (gc != wc).sum() <= max(1, got.shape[0] * d // 1000)
+    assert (np.abs(gc - wc) <= 1).all()
+
+
+@pytest.mark.parametrize("bits,d", [(3, 128), (2, 64)])
+def test_prod_width_rows_match_reference_kernels(bits, d):
+    """TurboProd{3} / {2} rows ((bits - 1)-bit codes, QJL signs, |r|) against the reference's
+    pipeline (tq_quant, tq_resid, S r, tq_signs): codes equal, norms and |r| to 1e-5, signs but
+    for <= 0.1 %."""
+    g = gold("ref_prod_widths")
+    y, want = g[f"x{bits}"], g[f"rows{bits}"]
+    mine = O.quantize_rows_qjl(bits, y, O.qjl_matrix(d, 42))
+    l = O.row_layout(O.TURBO_PROD, bits, d)
+    cw, aw = l.code_words, l.aux_words
+    np.testing.assert_array_equal(turbo_codes(mine, bits - 1, d), turbo_codes(want, bits - 1, d))
+    for w in (cw + aw, cw + aw + 1):
+        np.testing.assert_allclose(mine[..., w].view(np.float32), want[..., w].view(np.float32),
+                                   rtol=1e-5)
+    ms = np.unpackbits(mine[..., cw:cw + aw].copy().view(np.uint8))
+    rs = np.unpackbits(want[..., cw:cw + aw].copy().view(np.uint8))
+    assert (ms != rs).sum() <= max(1, ms.size // 1000)
+
+
+def widths_inputs():
+    """The inputs of the ref_decode_widths fixture (tests/golden/make_vectors.py widths_case)."""
+    B, Hq, Hkv, D, Lq, Lk = 2, 8, 2, 128, 2, 300
+    q = O.round_bf16(O.normal(801, (B, Hq, Lq, D)))
+    k = O.round_bf16(O.normal(802, (B, Hkv, Lk, D))).astype(np.float32)
+    v = O.round_bf16(O.normal(803, (B, Hkv, Lk, D))).astype(np.float32)
+    return q, k, v
+
+
+WIDTH_DECODES = {"mse4_mse3": (O.TURBO_MSE, 4, 3), "prod3_mse2": (O.TURBO_PROD, 3, 2)}
+
+
+@pytest.mark.parametrize("name", sorted(WIDTH_DECODES))
+def test_width_decode_vs_reference_fused_kernel(name):
+    """The reference's fused decode over TurboMse{4} keys + TurboMse{3} values and TurboProd{3}
+    keys + TurboMse{2} values (tq_attn with a codebook table per side) equals float64 attention
+    over the oracle's dequantized rows to 1e-5; the reference CPU path stays within 2e-2."""
+    g = gold("ref_decode_widths")
+    kmode, kbits, vbits = WIDTH_DECODES[name]
+    kd, vd, want = g[f"kd_{name}"], g[f"vd_{name}"], g[f"out_{name}"]
+    q, _, _ = widths_inputs()
+    B, Hq, Lq, D = q.shape
+    pk = O.rotation_matrix(D, O.ROT_HADAMARD, 42).astype(np.float64)
+    pv = O.rotation_matrix(D, O.ROT_HADAMARD, 44).astype(np.float64)
+    s = O.qjl_matrix(D, 42) if kmode == O.TURBO_PROD else None
+    if kmode == O.TURBO_PROD:
+        kq = O.dequantize_rows_qjl(kbits, D, kd, s)
+    else:
+        kq = O.dequantize_rows(kmode, kbits, D, kd)
+    kx = kq.astype(np.float64) @ pk
+    vx = O.dequantize_rows(O.TURBO_MSE, vbits, D, vd).astype(np.float64) @ pv
+    scale = float(g["scale"])
+    ex = np.zeros((B, Hq, Lq, D))
+    for b in range(B):
+        for h in range(Hq):
+            sc = q[b, h].astype(np.float64) @ kx[b, h // 4].T * scale
+            p = np.exp(sc - sc.max(1, keepdims=True))
+            ex[b, h] = p @ vx[b, h // 4] / p.sum(1, keepdims=True)
+    assert np.abs(ex - want).max() < 1e-5
+    cpu = O.cache_attention(O.f32_to_bf16_bits(q), kd, vd, (kmode, kbits), (O.TURBO_MSE, vbits),
+                            pk.astype(np.float32), pv.astype(np.float32), kd.shape[2], scale,
+                            threads=8, qjl_k=s)
+    assert np.abs(O.round_bf16(cpu) - want).max() < 2e-2
 
 
 def test_fp8_row_properties():
