@@ -106,10 +106,14 @@ struct FaTileGeom {
     static constexpr int ROWS_PER_CP = 1024 / RB;
 };
 
-// Byte offset in LDS of 16-byte chunk c of tile row r (chunks XOR-swizzled by the row).
+// Byte offset in LDS of 16-byte chunk c of tile row r (chunks XOR-swizzled by the row: by its
+// low 3 bits for the 8-chunk rows of D = 64, 4 bits for longer rows, so that the 16 rows a
+// 16-lane group reads hit 16 different 16-byte bank groups).
+template <int D>
+__device__ inline int fa_swz(int r) { return r & (D >= 128 ? 15 : 7); }
 template <int D>
 __device__ inline uint32_t fa_chunk_off(int r, int c) {
-    return (uint32_t)(r * FaTileGeom<D>::RB + ((c ^ (r & 7)) << 4));
+    return (uint32_t)(r * FaTileGeom<D>::RB + ((c ^ fa_swz<D>(r)) << 4));
 }
 
 // The source offsets (bytes from a tile's row 0) of this lane's part of each 1 KB copy: copy i
@@ -123,7 +127,7 @@ __device__ inline void fa_copy_offsets(uint32_t (&off)[FaTileGeom<D>::NCP], int6
     for (int i = 0; i < G::NCP; ++i) {
         const int o = 1024 * i + 16 * lane;
         const int r = o / G::RB, ph = (o % G::RB) >> 4;
-        const int c = ph ^ (r & 7);
+        const int c = ph ^ fa_swz<D>(r);
         off[i] = 8 * c < head_dim ? (uint32_t)(r * row_stride * 2 + 16 * c) : kFaOOB;
     }
 }
