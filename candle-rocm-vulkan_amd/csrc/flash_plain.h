@@ -168,8 +168,29 @@ __device__ inline float fa_logit2(float x, float cap2, float slope2, int dist) {
     return x;
 }
 
+// Sum of the 8 elements of a bf16 / f16 operand (four dot2 with ones).
+template <bool F16>
+__device__ inline float fa_sum8(fa_op_t<F16> v) {
+    const u32x4 w = __builtin_bit_cast(u32x4, v);
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t x = w[i];
+        if constexpr (F16) {
+            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+            const h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+            a = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, x), ones, a, false);
+        } else {
+            const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+            a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x), ones, a, false);
+        }
+    }
+    return a;
+}
+
 // One 32-key tile of a wavefront: S^T, online softmax, O^T += V^T P^T (PLO: P as a hi + lo
-// pair, else one operand of the dtype as the MFMA prefill does).
+// pair and the scores scaled here; else, as the MFMA prefill does, one P operand of the dtype
+// and queries pre-scaled by scale * log2(e) before they were rounded to the dtype).
 template <bool F16, int D, bool PLO = true>
 __device__ inline void fa_tile(const uint8_t *kst, const uint8_t *vst, const fa_op_t<F16> *qop,
                                int t, int lane, int lo, int hi, int lo_max, int hi_min, int L,
@@ -190,8 +211,10 @@ __device__ inline void fa_tile(const uint8_t *kst, const uint8_t *vst, const fa_
     // x[e]: key 4 g + e (e < 4) or 16 + 4 g + e - 4 of the tile, for this lane's column
     float x[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
     const int t0 = t * 32;
+    if constexpr (PLO) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] *= scale_log2;
+        for (int e = 0; e < 8; ++e) x[e] *= scale_log2;
+    }
     if (cap2 > 0.0f || slope2 != 0.0f) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -219,9 +242,8 @@ __device__ inline void fa_tile(const uint8_t *kst, const uint8_t *vst, const fa_
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         p[e] = none ? 0.0f : __builtin_amdgcn_exp2f(x[e] - m_new);
-        psum += p[e];
+        if constexpr (PLO) psum += p[e];
     }
-    l_run = l_run * alpha + psum;
     m_run = m_new;
     if (__any(alpha != 1.0f)) {
 #pragma unroll
@@ -229,12 +251,8 @@ __device__ inline void fa_tile(const uint8_t *kst, const uint8_t *vst, const fa_
     }
     op_t phi, plo;
     split8(p, phi, plo);
-    if constexpr (!PLO) {  // the row sum of the P the product uses
-        float r = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) r += (float)phi[e];
-        l_run += r - psum;
-    }
+    // the row sum of the P the product uses (hi + lo: p itself)
+    l_run = l_run * alpha + (PLO ? psum : fa_sum8<F16>(phi));
     // V^T operands: lane (16-lane group g, index 4 pp + qq) points at key row 4 g + pp (then
     // 16 + 4 g + pp), head dims 16 u + 4 qq .. +3; lane i of the group receives those four keys
     // of head dim 16 u + i: k-slots 8 g .. 8 g + 3 and 8 g + 4 .. 8 g + 7, the keys of p[].
@@ -308,7 +326,10 @@ __global__ __launch_bounds__(W * 64) void fa_row_kernel(FaArgs a) {
         te = min((split + 1) * a.tiles_per_split, (hi_max + 31) / 32);
     }
 
-    // Q^T operands: chunk j holds head dims 32 j + 8 g .. + 7 of this lane's column
+    // Q^T operands: chunk j holds head dims 32 j + 8 g .. + 7 of this lane's column (exact; the
+    // scores are scaled in f32)
+    float scale_log2 = a.scale_log2;
+    if (a.q_mul_dev) scale_log2 *= *a.q_mul_dev;
     op_t qop[NJ];
     {
         const uint16_t *qrow = a.q + sq.q0 + (int64_t)qi * a.q_st + (int64_t)head * a.q_sh;
@@ -329,8 +350,6 @@ __global__ __launch_bounds__(W * 64) void fa_row_kernel(FaArgs a) {
             qop[j] = __builtin_bit_cast(op_t, w);
         }
     }
-    float scale_log2 = a.scale_log2;
-    if (a.q_mul_dev) scale_log2 *= *a.q_mul_dev;
     const float slope2 = a.alibi ? a.alibi[b * a.alibi_bs + head] * kLog2e : 0.0f;
     const int pos = qi + sq.lk - sq.lq;  // the column's query position in key coordinates
 
@@ -491,6 +510,10 @@ __global__ __launch_bounds__(256) void fa_tile_kernel(FaArgs a) {
     const int tb = max(split * a.tiles_per_split, lo_min / 32);
     const int te = min((split + 1) * a.tiles_per_split, (hi_max + 31) / 32);
 
+    float scale_log2 = a.scale_log2;
+    if (a.q_mul_dev) scale_log2 *= *a.q_mul_dev;
+    // queries pre-scaled by scale * log2(e) and rounded to the dtype (the MFMA prefill's order,
+    // and the reference tile kernel's, which scales q first: flash_attn_impl.h:364)
     op_t qop[NJ];
     {
         const uint16_t *qrow = a.q + sq.q0 + (int64_t)qi * a.q_st + (int64_t)head * a.q_sh;
@@ -508,11 +531,18 @@ __global__ __launch_bounds__(256) void fa_tile_kernel(FaArgs a) {
                         wp[e] = (uint32_t)qrow[d0 + 2 * e] | ((uint32_t)qrow[d0 + 2 * e + 1] << 16);
                 }
             }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if constexpr (F16)
+                    w[e] = pack_f16x2(f16_bits_to_f32(w[e] & 0xffffu) * scale_log2,
+                                      f16_bits_to_f32(w[e] >> 16) * scale_log2);
+                else
+                    w[e] = pack_bf16x2(__uint_as_float(w[e] << 16) * scale_log2,
+                                       __uint_as_float(w[e] & 0xffff0000u) * scale_log2);
+            }
             qop[j] = __builtin_bit_cast(op_t, w);
         }
     }
-    float scale_log2 = a.scale_log2;
-    if (a.q_mul_dev) scale_log2 *= *a.q_mul_dev;
     const float slope2 = a.alibi ? a.alibi[b * a.alibi_bs + head] * kLog2e : 0.0f;
     const int pos = qi + sq.lk - sq.lq;
 
