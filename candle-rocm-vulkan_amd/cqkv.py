@@ -112,7 +112,9 @@ def lib() -> ctypes.CDLL:
         L.cqkv_hadamard_rows.argtypes = [P, i32, ctypes.c_int64, ctypes.c_int64, i32,
                                          ctypes.c_uint64, P, ctypes.c_int64, P]
         L.cqkv_flash_attn_fp8.argtypes = [P, I64P, P, I64P, P, I64P, P, I64P, i32, i32, i32, i32,
-                                          i32, i32, f32, i32, i32, f32, f32, P, P, P]
+                                          i32, i32, i32, f32, i32, i32, f32, f32, P, P, P, sz, P]
+        L.cqkv_flash_attn_fp8_workspace_bytes.argtypes = [i32] * 7
+        L.cqkv_flash_attn_fp8_workspace_bytes.restype = sz
         L.cqkv_reference_row_words.argtypes = [i32, i32, i32]
         L.cqkv_reference_row_words.restype = i32
         L.cqkv_rows_import.argtypes = [SP, P, i32, i32, i32, P]
@@ -135,7 +137,7 @@ EXPORTED = ["cqkv_codes_plane_bytes", "cqkv_scales_plane_bytes", "cqkv_quant_app
             "cqkv_flash_attn", "cqkv_flash_attn_ext", "cqkv_flash_attn_workspace_bytes",
             "cqkv_flash_attn_blocks", "cqkv_flash_attn_blocks_workspace_bytes",
             "cqkv_fp8_quantize_tensor",
-            "cqkv_flash_attn_fp8", "cqkv_hadamard_rows", "cqkv_reference_row_words", "cqkv_rows_import",
+            "cqkv_flash_attn_fp8", "cqkv_flash_attn_fp8_workspace_bytes", "cqkv_hadamard_rows", "cqkv_reference_row_words", "cqkv_rows_import",
             "cqkv_rows_export", "cqkv_side_copy", "cqkv_turbo_codebook", "cqkv_turbo_signs",
             "cqkv_qjl_matrix",
             "cqkv_last_error",
@@ -527,12 +529,16 @@ def flash_attn_fp8_codes(q: torch.Tensor, k8: torch.Tensor, v8: torch.Tensor,
                          softmax_scale: float, causal: bool, k_descale: float = 1.0,
                          v_descale: float = 1.0, window_left: int = -1, window_right: int = -1,
                          k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None,
-                         out: torch.Tensor | None = None) -> torch.Tensor:
+                         out: torch.Tensor | None = None,
+                         workspace: torch.Tensor | None = None) -> torch.Tensor:
     """flash_attn_with_config on F8E4M3 K / V with descale factors (FlashAttnConfig::descale,
-    candle-nn/src/flash_attn.rs:113-117): q (b, s_q, h_q, d) bf16, k8 / v8 (b, s_kv, h_kv, d) E4M3
-    codes; keys and values are k8 * k_descale * k_scale[0], v8 * v_descale * v_scale[0] (the
-    device scales optional)."""
+    candle-nn/src/flash_attn.rs:113-117): q (b, s_q, h_q, d) bf16 or f16, k8 / v8
+    (b, s_kv, h_kv, d) E4M3 codes; keys and values are k8 * k_descale * k_scale[0],
+    v8 * v_descale * v_scale[0] (the device scales optional). workspace: a device byte tensor
+    of flash_attn_fp8_workspace_bytes (None: allocated by the call)."""
     _need_gpu(q, "q")
+    if q.dtype not in (torch.bfloat16, torch.float16):
+        raise CqkvError(ERR_ARG, f"q must be bfloat16 or float16, got {q.dtype}")
     k8, v8 = _fp8_codes(k8, "k8"), _fp8_codes(v8, "v8")
     b, sq, hq, d = q.shape
     _, sk, hkv, _ = k8.shape
@@ -540,12 +546,20 @@ def flash_attn_fp8_codes(q: torch.Tensor, k8: torch.Tensor, v8: torch.Tensor,
         out = torch.empty_like(q)
     if causal:
         window_right = 0
+    ws, wsb = (None, 0) if workspace is None else (_ptr(workspace), workspace.numel())
     _check(lib().cqkv_flash_attn_fp8(
         _ptr(q), _strides3(q, (0, 1, 2)), _ptr(k8), _strides3(k8, (0, 1, 2)), _ptr(v8),
-        _strides3(v8, (0, 1, 2)), _ptr(out), _strides3(out, (0, 1, 2)), b, sq, sk, hq, hkv, d,
-        softmax_scale, window_left, window_right, k_descale, v_descale, _ptr(k_scale),
-        _ptr(v_scale), _stream(q.device)))
+        _strides3(v8, (0, 1, 2)), _ptr(out), _strides3(out, (0, 1, 2)), _DTYPES[q.dtype], b, sq,
+        sk, hq, hkv, d, softmax_scale, window_left, window_right, k_descale, v_descale,
+        _ptr(k_scale), _ptr(v_scale), ws, wsb, _stream(q.device)))
     return out
+
+
+def flash_attn_fp8_workspace_bytes(dtype, batch: int, q_len: int, kv_len: int, q_heads: int,
+                                   kv_heads: int, head_dim: int) -> int:
+    """Device bytes flash_attn_fp8_codes needs for a call of these sizes."""
+    return lib().cqkv_flash_attn_fp8_workspace_bytes(_DTYPES[dtype], batch, q_len, kv_len,
+                                                     q_heads, kv_heads, head_dim)
 
 
 FP8_HADAMARD_SEED = 0x46413346  # flash_attn.rs:869

@@ -86,16 +86,18 @@ __global__ __launch_bounds__(256) void fp8_quant_kernel(Fp8QuantArgs a) {
 struct Fp8StageArgs {
     const uint8_t *k, *v;
     int64_t k_sb, k_st, k_sh, v_sb, v_st, v_sh;  // element strides: batch, token, head
-    uint16_t *kb, *vb;                           // (batch, kv_heads, kv_len, D) bf16
-    int32_t kv_len, kv_heads;
+    uint16_t *kb, *vb;                           // (batch, kv_heads, kv_len, D) of the dtype
+    int32_t kv_len, kv_heads, head_dim, f16;
 };
 
-// One thread per 8 head dims of one token: 8 code bytes in, their 8 bf16 values out, K and V.
+// One thread per 8 head dims of one token: 8 code bytes in, their 8 bf16 / f16 values out (exact
+// in either: E4M3 has 4 significant bits and its range inside both), K and V.
 __global__ __launch_bounds__(256) void fp8_stage_kernel(Fp8StageArgs a) {
     const int h = blockIdx.y, b = blockIdx.z;
-    const int t = blockIdx.x * 16 + (threadIdx.x >> 4), c = threadIdx.x & 15;
-    if (t >= a.kv_len) return;
-    const int64_t dst = (((int64_t)b * a.kv_heads + h) * a.kv_len + t) * 128 + 8 * c;
+    const int cpt = a.head_dim / 8, tpb = 256 / cpt;  // chunks per token, tokens per block
+    const int t = blockIdx.x * tpb + (int)threadIdx.x / cpt, c = (int)threadIdx.x % cpt;
+    if ((int)threadIdx.x >= tpb * cpt || t >= a.kv_len) return;
+    const int64_t dst = (((int64_t)b * a.kv_heads + h) * a.kv_len + t) * a.head_dim + 8 * c;
     const uint8_t *kp = a.k + (int64_t)b * a.k_sb + (int64_t)t * a.k_st + (int64_t)h * a.k_sh + 8 * c;
     const uint8_t *vp = a.v + (int64_t)b * a.v_sb + (int64_t)t * a.v_st + (int64_t)h * a.v_sh + 8 * c;
     const u32x2 kw = *(const u32x2 *)kp, vw = *(const u32x2 *)vp;
@@ -111,8 +113,8 @@ __global__ __launch_bounds__(256) void fp8_stage_kernel(Fp8StageArgs a) {
     u32x4 ko, vo;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        ko[i] = pack_bf16x2(kf[i].x, kf[i].y);  // exact
-        vo[i] = pack_bf16x2(vf[i].x, vf[i].y);
+        ko[i] = a.f16 ? pack_f16x2(kf[i].x, kf[i].y) : pack_bf16x2(kf[i].x, kf[i].y);
+        vo[i] = a.f16 ? pack_f16x2(vf[i].x, vf[i].y) : pack_bf16x2(vf[i].x, vf[i].y);
     }
     *(u32x4 *)(a.kb + dst) = ko;
     *(u32x4 *)(a.vb + dst) = vo;
@@ -129,6 +131,8 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
                     const cqkv_side *k_cache, const cqkv_side *v_cache, int32_t position,
                     void *workspace, size_t workspace_bytes, cqkv_stream_t stream, float q_mul,
                     const float *q_mul_dev, float o_mul, const float *o_mul_dev);
+size_t flash_attn_workspace(int32_t dtype, int32_t batch, int32_t q_len, int32_t kv_len,
+                            int32_t q_heads, int32_t kv_heads, int32_t head_dim, bool varlen);
 
 }  // namespace cqkv
 
@@ -154,21 +158,41 @@ extern "C" int cqkv_fp8_quantize_tensor(const void *x, int32_t x_dtype, int64_t 
     return CQKV_OK;
 }
 
+// Workspace of cqkv_flash_attn_fp8: the staged K / V (dtype copies of the codes), 256-aligned,
+// then the attention's own (flash_attn_workspace); 0 for invalid sizes.
+static size_t fp8_stage_bytes(int32_t batch, int32_t kv_len, int32_t kv_heads, int32_t head_dim) {
+    return ((size_t)batch * kv_heads * kv_len * head_dim * 2 * 2 + 255) / 256 * 256;
+}
+
+extern "C" size_t cqkv_flash_attn_fp8_workspace_bytes(int32_t dtype, int32_t batch, int32_t q_len,
+                                                      int32_t kv_len, int32_t q_heads,
+                                                      int32_t kv_heads, int32_t head_dim) {
+    if ((dtype != CQKV_BF16 && dtype != CQKV_F16) || batch <= 0 || q_len <= 0 || kv_len <= 0 ||
+        q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0 || head_dim <= 0 ||
+        head_dim > 256 || head_dim % 8 != 0)
+        return 0;
+    return fp8_stage_bytes(batch, kv_len, kv_heads, head_dim) +
+           flash_attn_workspace(dtype, batch, q_len, kv_len, q_heads, kv_heads, head_dim, false);
+}
+
 extern "C" int cqkv_flash_attn_fp8(const void *q, const int64_t q_strides[3], const void *k8,
                                    const int64_t k_strides[3], const void *v8,
                                    const int64_t v_strides[3], void *out,
-                                   const int64_t out_strides[3], int32_t batch, int32_t q_len,
-                                   int32_t kv_len, int32_t q_heads, int32_t kv_heads,
-                                   int32_t head_dim, float softmax_scale, int32_t window_left,
-                                   int32_t window_right, float k_descale, float v_descale,
-                                   const float *k_scale, const float *v_scale,
-                                   cqkv_stream_t stream) {
+                                   const int64_t out_strides[3], int32_t dtype, int32_t batch,
+                                   int32_t q_len, int32_t kv_len, int32_t q_heads,
+                                   int32_t kv_heads, int32_t head_dim, float softmax_scale,
+                                   int32_t window_left, int32_t window_right, float k_descale,
+                                   float v_descale, const float *k_scale, const float *v_scale,
+                                   void *workspace, size_t workspace_bytes, cqkv_stream_t stream) {
     clear_error();
     static const char *who = "cqkv_flash_attn_fp8";
     if (!q || !k8 || !v8 || !out || !q_strides || !k_strides || !v_strides || !out_strides)
         return fail(CQKV_ERR_ARG, "%s: null tensor or strides", who);
-    if (head_dim != 128) return fail(CQKV_ERR_ARG, "%s: head_dim %d not supported (128)", who, head_dim);
-    // the prefill's own limits, checked before the staging pass is launched
+    if (dtype != CQKV_BF16 && dtype != CQKV_F16)
+        return fail(CQKV_ERR_ARG, "%s: dtype %d (bf16 or f16 q / out)", who, dtype);
+    if (head_dim <= 0 || head_dim > 256 || head_dim % 8 != 0)
+        return fail(CQKV_ERR_ARG, "%s: head_dim %d (a multiple of 8 up to 256)", who, head_dim);
+    // the attention's own limits, checked before the staging pass is launched
     if (batch <= 0 || q_len <= 0 || kv_len <= 0 || kv_heads <= 0 || q_heads <= 0 ||
         q_heads % kv_heads != 0 || kv_len > (1 << 23))
         return fail(CQKV_ERR_ARG, "%s: batch %d q_len %d kv_len %d heads %d / %d", who, batch,
@@ -181,9 +205,18 @@ extern "C" int cqkv_flash_attn_fp8(const void *q, const int64_t q_strides[3], co
     if ((uintptr_t)k8 % 8 != 0 || (uintptr_t)v8 % 8 != 0)
         return fail(CQKV_ERR_ARG, "%s: K / V must be 8-byte aligned", who);
     const hipStream_t st = (hipStream_t)stream;
-    const size_t plane = (size_t)batch * kv_heads * kv_len * 128;
-    void *scratch = nullptr;
-    CQKV_HIP_CHECK(hipMallocAsync(&scratch, plane * 4, st));
+    const size_t stage = fp8_stage_bytes(batch, kv_len, kv_heads, head_dim);
+    const size_t need = cqkv_flash_attn_fp8_workspace_bytes(dtype, batch, q_len, kv_len, q_heads,
+                                                            kv_heads, head_dim);
+    void *ws = workspace;
+    if (ws) {
+        if (workspace_bytes < need)
+            return fail(CQKV_ERR_WORKSPACE, "%s: workspace %zu bytes, need %zu", who,
+                        workspace_bytes, need);
+    } else {
+        CQKV_HIP_CHECK(hipMallocAsync(&ws, need, st));
+    }
+    const size_t plane = (size_t)batch * kv_heads * kv_len * head_dim;
     Fp8StageArgs s = {};
     s.k = (const uint8_t *)k8;
     s.v = (const uint8_t *)v8;
@@ -193,28 +226,34 @@ extern "C" int cqkv_flash_attn_fp8(const void *q, const int64_t q_strides[3], co
     s.v_sb = v_strides[0];
     s.v_st = v_strides[1];
     s.v_sh = v_strides[2];
-    s.kb = (uint16_t *)scratch;
-    s.vb = (uint16_t *)scratch + plane;
+    s.kb = (uint16_t *)ws;
+    s.vb = (uint16_t *)ws + plane;
     s.kv_len = kv_len;
     s.kv_heads = kv_heads;
-    hipLaunchKernelGGL(fp8_stage_kernel, dim3((kv_len + 15) / 16, kv_heads, batch), dim3(256), 0,
-                       st, s);
+    s.head_dim = head_dim;
+    s.f16 = dtype == CQKV_F16 ? 1 : 0;
+    const int tpb = 256 / (head_dim / 8);
+    hipLaunchKernelGGL(fp8_stage_kernel, dim3((kv_len + tpb - 1) / tpb, kv_heads, batch),
+                       dim3(256), 0, st, s);
     int rc = CQKV_OK;
     if (hipGetLastError() != hipSuccess) {
         rc = fail(CQKV_ERR_HIP, "%s: staging launch failed", who);
     } else {
         // the staged K / V are (batch, kv_heads, kv_len, D): (batch, token, head) strides
-        const int64_t ss[3] = {(int64_t)kv_heads * kv_len * 128, 128, (int64_t)kv_len * 128};
-        rc = flash_attn_impl(q, q_strides, s.kb, ss, s.vb, ss, out, out_strides, CQKV_BF16, batch,
+        const int64_t ss[3] = {(int64_t)kv_heads * kv_len * head_dim, head_dim,
+                               (int64_t)kv_len * head_dim};
+        rc = flash_attn_impl(q, q_strides, s.kb, ss, s.vb, ss, out, out_strides, dtype, batch,
                              q_len, kv_len, q_heads, kv_heads, head_dim, softmax_scale,
                              window_left, window_right, 0.0f, nullptr, 0, nullptr, nullptr, 0, 0,
-                             nullptr, nullptr, 0, nullptr, 0, stream, k_descale, k_scale,
-                             v_descale, v_scale);
+                             nullptr, nullptr, 0, (uint8_t *)ws + stage, need - stage, stream,
+                             k_descale, k_scale, v_descale, v_scale);
     }
-    const hipError_t fe = hipFreeAsync(scratch, st);
-    if (rc != CQKV_OK) return rc;
-    CQKV_HIP_CHECK(fe);
-    return CQKV_OK;
+    if (!workspace) {
+        const hipError_t fe = hipFreeAsync(ws, st);
+        if (rc != CQKV_OK) return rc;
+        CQKV_HIP_CHECK(fe);
+    }
+    return rc;
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -9,8 +9,8 @@
  * hipFreeAsync on the call's stream) only by: cqkv_decode_attention,
  * cqkv_decode_attention_paged, cqkv_flash_attn_ext and cqkv_flash_attn_blocks when they are
  * given no workspace (each has a *_workspace_bytes query); cqkv_flash_attn (its workspace);
- * cqkv_flash_attn_fp8 (a bf16 staging copy of K / V). cqkv_decode_attention_noalloc allocates
- * nothing. Nothing here holds torch or candle types.
+ * cqkv_flash_attn_fp8 given no workspace (the staged K / V and the attention's workspace).
+ * cqkv_decode_attention_noalloc allocates nothing. Nothing here holds torch or candle types.
  *
  * Reference interfaces replaced (paths relative to the reference repository root):
  *   cqkv_quant_append      RocmStorage::tq_quantize + Cache::append
@@ -356,18 +356,24 @@ int cqkv_fp8_quantize_tensor(const void *x, int32_t x_dtype, int64_t n, uint8_t 
                              float *scale, cqkv_stream_t stream);
 
 /* Attention over E4M3 K / V with descale factors (flash_attn_with_config on F8E4M3 tensors):
- * shapes, strides and masks as cqkv_flash_attn (q, out bf16; k8 / v8 E4M3 bytes, strides
- * multiples of 8, 8-byte aligned). Keys are e4m3(k8) * k_descale * (k_scale ? *k_scale : 1),
- * values likewise with v_descale / v_scale (device floats, e.g. the scales written by
- * cqkv_fp8_quantize_tensor, read on the device). The codes are dequantized to bf16 into
- * stream-ordered scratch, then the bf16 MFMA prefill runs. */
+ * shapes, strides, head dims and masks as cqkv_flash_attn (q, out of `dtype`, bf16 or f16; k8 /
+ * v8 E4M3 bytes, strides multiples of 8, 8-byte aligned). Keys are e4m3(k8) * k_descale *
+ * (k_scale ? *k_scale : 1), values likewise with v_descale / v_scale (device floats, e.g. the
+ * scales written by cqkv_fp8_quantize_tensor, read on the device). The codes are converted to
+ * the dtype (exactly) into the workspace, then the attention runs with the descales folded into
+ * the query scale and the output normalisation. workspace: at least
+ * cqkv_flash_attn_fp8_workspace_bytes(); NULL = allocated (stream-ordered) and freed by the call. */
+size_t cqkv_flash_attn_fp8_workspace_bytes(int32_t dtype, int32_t batch, int32_t q_len,
+                                           int32_t kv_len, int32_t q_heads, int32_t kv_heads,
+                                           int32_t head_dim);
 int cqkv_flash_attn_fp8(const void *q, const int64_t q_strides[3], const void *k8,
                         const int64_t k_strides[3], const void *v8, const int64_t v_strides[3],
-                        void *out, const int64_t out_strides[3], int32_t batch, int32_t q_len,
-                        int32_t kv_len, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
-                        float softmax_scale, int32_t window_left, int32_t window_right,
-                        float k_descale, float v_descale, const float *k_scale,
-                        const float *v_scale, cqkv_stream_t stream);
+                        void *out, const int64_t out_strides[3], int32_t dtype, int32_t batch,
+                        int32_t q_len, int32_t kv_len, int32_t q_heads, int32_t kv_heads,
+                        int32_t head_dim, float softmax_scale, int32_t window_left,
+                        int32_t window_right, float k_descale, float v_descale,
+                        const float *k_scale, const float *v_scale, void *workspace,
+                        size_t workspace_bytes, cqkv_stream_t stream);
 
 /* Hadamard rotation of rows (flash_attn_fp8's incoherent processing, candle-nn/src/flash_attn.rs:
  * 868-880): out_r = x_r * rotation_matrix(D, Hadamard, seed)^T for each of `rows` rows of D

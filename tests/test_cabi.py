@@ -264,17 +264,22 @@ def test_fp8_attention_argument_errors(cq):
     x = (ctypes.c_int64 * 3)(8, 1024, 128)
     odd = (ctypes.c_int64 * 3)(8, 1028, 130)
 
-    def attn(ks=x, hd=128, kd=1.0):
-        return L.cqkv_flash_attn_fp8(one, x, one, ks, one, x, one, x, 1, 16, 16, 8, 8, hd, 0.1,
-                                     -1, 0, kd, 1.0, None, None, None)
-    assert attn(hd=64) == cq.ERR_ARG
+    def attn(ks=x, hd=128, kd=1.0, dtype=0, ws=None, wsb=0):
+        return L.cqkv_flash_attn_fp8(one, x, one, ks, one, x, one, x, dtype, 1, 16, 16, 8, 8, hd,
+                                     0.1, -1, 0, kd, 1.0, None, None, ws, wsb, None)
+    assert attn(hd=260) == cq.ERR_ARG  # head dims: multiples of 8 up to 256
+    assert attn(hd=100) == cq.ERR_ARG
+    assert attn(dtype=2) == cq.ERR_ARG  # bf16 / f16 queries
+    assert attn(ws=one, wsb=16) == cq.ERR_WORKSPACE  # a workspace below the query's size
+    assert L.cqkv_flash_attn_fp8_workspace_bytes(0, 1, 16, 16, 8, 8, 128) > 0
+    assert L.cqkv_flash_attn_fp8_workspace_bytes(2, 1, 16, 16, 8, 8, 128) == 0
     assert attn(ks=odd) == cq.ERR_ARG
     assert b"multiples of 8" in L.cqkv_last_error()
     assert attn(kd=float("nan")) == cq.ERR_ARG
 
     def attn2(kv_len=16, hq=8, hkv=8):
-        return L.cqkv_flash_attn_fp8(one, x, one, x, one, x, one, x, 1, 16, kv_len, hq, hkv, 128,
-                                     0.1, -1, 0, 1.0, 1.0, None, None, None)
+        return L.cqkv_flash_attn_fp8(one, x, one, x, one, x, one, x, 0, 1, 16, kv_len, hq, hkv,
+                                     128, 0.1, -1, 0, 1.0, 1.0, None, None, None, 0, None)
     assert attn2(kv_len=(1 << 23) + 1) == cq.ERR_ARG  # before any scratch or launch
     assert attn2(hq=6, hkv=4) == cq.ERR_ARG
     assert L.cqkv_hadamard_rows(one, 0, 1 << 27, 128, 128, 1, one, 128, None) == cq.ERR_ARG

@@ -108,6 +108,34 @@ def test_flash_attn_fp8_decode_shape_and_float8_dtype(cq, dev):
     assert_close_bf16(out.float().cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("d,dtype,sq", [(64, torch.bfloat16, 150), (256, torch.float16, 77),
+                                         (96, torch.float16, 3), (128, torch.float16, 200)])
+def test_flash_attn_fp8_head_dims_f16_and_workspace(cq, dev, d, dtype, sq):
+    """The reference's FP8 K / V path takes every head dim of its tile kernels and f16 queries
+    (flash_attn.rs:862-892; kernels fa_*_f16_f8 of flash_attn_impl.h): head dims 64 / 96 / 256,
+    f16 queries and outputs, prefill and decode shapes; a caller workspace of
+    flash_attn_fp8_workspace_bytes gives the same output as the allocating call, and a smaller
+    one is refused."""
+    b, sk, hq, hkv = 2, 301, 8, 2
+    q, k, v = inputs(7 + d, b, sq, sk, hq, hkv, d)
+    q = q.to(dtype)
+    k8 = torch.from_numpy(O.e4m3_encode(k.float().numpy() * 40.0))
+    v8 = torch.from_numpy(O.e4m3_encode(v.float().numpy() * 60.0))
+    kd, vd, scale = 1 / 40.0, 1 / 60.0, 1 / d ** 0.5
+    qd, k8d, v8d = q.to(dev), k8.to(dev), v8.to(dev)
+    out = cq.flash_attn_fp8_codes(qd, k8d, v8d, scale, True, kd, vd)
+    n = cq.flash_attn_fp8_workspace_bytes(dtype, b, sq, sk, hq, hkv, d)
+    assert n > 0
+    ws = torch.empty(n, dtype=torch.uint8, device=dev)
+    out2 = cq.flash_attn_fp8_codes(qd, k8d, v8d, scale, True, kd, vd, workspace=ws)
+    torch.cuda.synchronize()
+    assert out.dtype == dtype and torch.equal(out, out2)
+    want = oracle_fp8_attention(q, k8, v8, kd, vd, scale, -1, 0)
+    assert_close_bf16(out.float().cpu().numpy(), want)
+    with pytest.raises(cq.CqkvError):
+        cq.flash_attn_fp8_codes(qd, k8d, v8d, scale, True, kd, vd, workspace=ws[:n - 256])
+
+
 @pytest.mark.parametrize("d", [64, 128])
 def test_hadamard_rows_vs_oracle_rotation(cq, dev, d):
     """The rotation of flash_attn_fp8's switch: rotation_matrix(d, Hadamard, 0x46413346) in f32.
