@@ -28,7 +28,7 @@ Each "cpu_baseline" is the oracle's restatement of the reference CPU path, timed
 CPUs (all of those this process may use) on a bounded sample of the workload and scaled to it.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
-                       [--only c2,c3,c4,c5,tp,f8,fx,ap,ra,pd,pp] [--calibration-copy]
+                       [--only c2,c3,c4,c5,tp,f8,fx,ap,ra,pd,pp,fq] [--calibration-copy]
 """
 from __future__ import annotations
 
@@ -44,6 +44,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6
+F32_PEAK_TFLOPS = 157.3  # dense f32 MFMA
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "decode_fp8_c2_and_append_rows_traffic.md")
 
 
@@ -335,35 +336,41 @@ def fp8_attn_case(cq, dev, stream, steps, warmup):
 
 
 def plain_decode_case(cq, dev, stream, steps, warmup, dtype, B=32, HQ=32, HKV=8, D=128,
-                      CTX=8192):
+                      CTX=8192, q_dtype=None):
     """flash_attn over plain K / V at the config-2 decode shape (one query per sequence): the
-    split-K row kernel; bytes = the K and V rows read (the queries and outputs are 0.02 %)."""
+    split-K row kernel (f32 queries: the f32 kernel); bytes = the K and V rows read (the queries
+    and outputs are 0.02 %)."""
     import torch
-    q = kv_gpu((B, 1, HQ, D), 61, dev, outliers=False).to(dtype)
+    q_dtype = q_dtype or dtype
+    q = kv_gpu((B, 1, HQ, D), 61, dev, outliers=False).to(q_dtype)
     k = kv_gpu((B, CTX, HKV, D), 62, dev).to(dtype)
     v = kv_gpu((B, CTX, HKV, D), 63, dev).to(dtype)
     out = torch.empty_like(q)
-    ws = torch.empty(max(cq.flash_attn_workspace_bytes(dtype, B, 1, CTX, HQ, HKV, D), 1),
+    ws = torch.empty(max(cq.flash_attn_workspace_bytes(q_dtype, B, 1, CTX, HQ, HKV, D), 1),
                      dtype=torch.uint8, device=dev)
     ms = time_calls(lambda i: cq.flash_attn(q, k, v, 1.0 / D ** 0.5, True, out=out,
                                             workspace=ws), steps, warmup, stream)
-    nbytes = 2 * B * CTX * HKV * D * 2
+    nbytes = 2 * B * CTX * HKV * D * k.element_size()
     del q, k, v
     torch.cuda.empty_cache()
-    return decode_summary(f"flash_attn decode over plain {str(dtype)[6:]} K / V, config-2 shape",
+    qn = "" if q_dtype == dtype else f"{str(q_dtype)[6:]} queries, "
+    return decode_summary(f"flash_attn decode, {qn}plain {str(dtype)[6:]} K / V, config-2 shape",
                           ms, nbytes, {"batch": B, "q_heads": HQ, "kv_heads": HKV,
                                        "head_dim": D, "context": CTX,
                                        "timed": "whole call (split-K row kernel + combine)"})
 
 
-def plain_prefill_case(cq, dev, stream, steps, warmup, dtype, D, B=4, S=4096, HQ=32, HKV=8):
-    """Causal flash_attn on the plain-dtype kernel (f16, or a head dim other than 128)."""
+def plain_prefill_case(cq, dev, stream, steps, warmup, dtype, D, B=4, S=4096, HQ=32, HKV=8,
+                       q_dtype=None):
+    """Causal flash_attn on the plain-dtype kernel (f16, or a head dim other than 128), or with
+    f32 queries on the f32 kernel (roofline: the f32 MFMA peak)."""
     import torch
-    q = kv_gpu((B, S, HQ, D), 71, dev, outliers=False).to(dtype)
+    q_dtype = q_dtype or dtype
+    q = kv_gpu((B, S, HQ, D), 71, dev, outliers=False).to(q_dtype)
     k = kv_gpu((B, S, HKV, D), 72, dev).to(dtype)
     v = kv_gpu((B, S, HKV, D), 73, dev).to(dtype)
     out = torch.empty_like(q)
-    ws = torch.empty(max(cq.flash_attn_workspace_bytes(dtype, B, S, S, HQ, HKV, D), 1),
+    ws = torch.empty(max(cq.flash_attn_workspace_bytes(q_dtype, B, S, S, HQ, HKV, D), 1),
                      dtype=torch.uint8, device=dev)
     ms = time_calls(lambda i: cq.flash_attn(q, k, v, 1.0 / D ** 0.5, True, out=out,
                                             workspace=ws), steps, warmup, stream)
@@ -371,11 +378,15 @@ def plain_prefill_case(cq, dev, stream, steps, warmup, dtype, D, B=4, S=4096, HQ
     del q, k, v
     torch.cuda.empty_cache()
     tf = flops / (ms * 1e-3) / 1e12
-    return {"workload": f"causal flash_attn, {str(dtype)[6:]}, D={D}, B={B} S={S} {HQ}/{HKV} "
-                        "heads (plain-dtype kernel)",
+    f32 = q_dtype == torch.float32
+    peak = F32_PEAK_TFLOPS if f32 else BF16_PEAK_TFLOPS
+    kind = "f32 kernel, f32 MFMA" if f32 else "plain-dtype kernel"
+    qn = "" if q_dtype == dtype else f"{str(q_dtype)[6:]} queries over "
+    return {"workload": f"causal flash_attn, {qn}{str(dtype)[6:]}, D={D}, B={B} S={S} "
+                        f"{HQ}/{HKV} heads ({kind})",
             "us_per_call": round(ms * 1e3, 2), "flop_per_call": flops,
-            "achieved_tflops": round(tf, 1), "peak_tflops": BF16_PEAK_TFLOPS,
-            "frac": round(tf / BF16_PEAK_TFLOPS, 4), "bound": "mfma", "timed": "whole call"}
+            "achieved_tflops": round(tf, 1), "peak_tflops": peak,
+            "frac": round(tf / peak, 4), "bound": "mfma", "timed": "whole call"}
 
 
 def append_case(cq, dev, stream, steps, warmup, b=32, hkv=8, d=128, t=2048):
@@ -432,7 +443,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--only", default="",
-                    help="comma list of c2,c3,c4,c5,tp,f8,fx,ap,ra,pd,pp (default: all)")
+                    help="comma list of c2,c3,c4,c5,tp,f8,fx,ap,ra,pd,pp,fq (default: all)")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="also run a plain 1 GiB copy (for counter scaling)")
     args = ap.parse_args()
@@ -622,6 +633,18 @@ def main():
                                                                  max(steps_x // 4, 5),
                                                                  max(warm_x // 4, 3), dt, d)
             log(f"plain prefill {name}: {other[f'c4_shape_plain_{name}']['us_per_call']} us/call")
+    if want("fq"):
+        f32 = torch.float32
+        for dt in (torch.bfloat16, f32):
+            name = str(dt)[6:]
+            log(f"f32 queries over {name} K/V decode B=32 32/8 d=128 ctx 8192")
+            other[f"c2_shape_f32q_{name}"] = plain_decode_case(cq, dev, stream, steps_x, warm_x,
+                                                               dt, q_dtype=f32)
+            log(f"f32q {name}: {other[f'c2_shape_f32q_{name}']['us_per_call']} us/call")
+        log("f32 queries over bf16 K/V causal prefill B=4 S=4096 32/8 d=128")
+        other["c4_shape_f32q_bfloat16"] = plain_prefill_case(cq, dev, stream, 5, 2,
+                                                             torch.bfloat16, 128, q_dtype=f32)
+        log(f"f32q prefill: {other['c4_shape_f32q_bfloat16']['us_per_call']} us/call")
     if want("ap"):
         log("append: B=32 x 8 kv heads x 2048 tokens, D=128, every format, keys and values")
         other["append_c2_shape"] = append_case(cq, dev, stream, steps_x, warm_x)

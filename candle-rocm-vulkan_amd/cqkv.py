@@ -99,15 +99,15 @@ def lib() -> ctypes.CDLL:
         L.cqkv_flash_attn.argtypes = [P, I64P, P, I64P, P, I64P, P, I64P, i32, i32, i32, i32,
                                       i32, i32, i32, f32, i32, i32, SP, SP, i32, P]
         L.cqkv_flash_attn_ext.argtypes = [P, I64P, P, I64P, P, I64P, P, I64P, i32, i32, i32,
-                                          i32, i32, i32, i32, f32, i32, i32, f32, P, i32, P, P,
-                                          i32, i32, SP, SP, i32, P, sz, P]
+                                          i32, i32, i32, i32, i32, f32, i32, i32, f32, P, i32,
+                                          P, P, i32, i32, SP, SP, i32, P, sz, P]
         L.cqkv_flash_attn_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32, i32, i32]
         L.cqkv_flash_attn_workspace_bytes.restype = sz
         PBP = ctypes.POINTER(PlainBlock)
         L.cqkv_flash_attn_blocks_workspace_bytes.argtypes = [PBP, i32, i32, i32, i32, i32, i32]
         L.cqkv_flash_attn_blocks_workspace_bytes.restype = sz
         L.cqkv_flash_attn_blocks.argtypes = [P, I64P, PBP, i32, i32, i32, i32, i32, i32, i32,
-                                             f32, i32, i32, f32, P, i32, P, I64P, P, sz, P]
+                                             i32, f32, i32, i32, f32, P, i32, P, I64P, P, sz, P]
         L.cqkv_fp8_quantize_tensor.argtypes = [P, i32, ctypes.c_int64, P, P, P]
         L.cqkv_hadamard_rows.argtypes = [P, i32, ctypes.c_int64, ctypes.c_int64, i32,
                                          ctypes.c_uint64, P, ctypes.c_int64, P]
@@ -414,16 +414,21 @@ def _alibi_arg(alibi_slopes, batch: int, q_heads: int):
                              f"got {tuple(alibi_slopes.shape)}")
 
 
-def _attn_inputs(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> int:
-    """The dtype id of q / k / v (bf16 or f16, one dtype, head dim contiguous on the GPU)."""
+def _attn_inputs(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> tuple[int, int]:
+    """The dtype ids of q and of k / v (head dim contiguous on the GPU): one of bf16, f16, f32
+    for all three, or f32 q over f16 / bf16 k / v (kv_dtype_supported,
+    candle-core/src/accel/attention.rs:569-576)."""
     for t, name in ((q, "q"), (k, "k"), (v, "v")):
         _need_gpu(t, name)
         if t.stride(-1) != 1:
             raise CqkvError(ERR_ARG, f"{name} needs a contiguous head dim (stride {t.stride()})")
-    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
-        raise CqkvError(ERR_ARG, f"q / k / v must share bf16 or f16 (got {q.dtype}, {k.dtype}, "
-                                 f"{v.dtype})")
-    return _DTYPES[q.dtype]
+    ok = q.dtype in _DTYPES and k.dtype == v.dtype and (
+        k.dtype == q.dtype or (q.dtype == torch.float32 and k.dtype in (torch.bfloat16,
+                                                                         torch.float16)))
+    if not ok:
+        raise CqkvError(ERR_ARG, f"flash-attn: k/v dtype {k.dtype} / {v.dtype} must match q "
+                                 f"{q.dtype}, or be f16 / bf16 with f32 queries")
+    return _DTYPES[q.dtype], _DTYPES[k.dtype]
 
 
 def flash_attn_workspace_bytes(dtype: torch.dtype, batch: int, q_len: int, kv_len: int,
@@ -439,11 +444,11 @@ def flash_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, softmax_scale:
                position: int = 0, out: torch.Tensor | None = None, softcap: float = 0.0,
                alibi_slopes: torch.Tensor | None = None,
                workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """candle_flash_attn::flash_attn layout: q (b, s_q, h_q, d), k / v (b, s_kv, h_kv, d), bf16 or
-    f16, d a multiple of 8 up to 256. With k_cache / v_cache K / V are also quantized into the
-    cache at `position`. softcap / alibi_slopes as flash_attn_alibi_windowed_softcap
-    (candle-flash-attn/src/lib.rs)."""
-    dt = _attn_inputs(q, k, v)
+    """candle_flash_attn::flash_attn layout: q (b, s_q, h_q, d), k / v (b, s_kv, h_kv, d), all
+    bf16, f16 or f32, or f32 q over f16 / bf16 k / v; d a multiple of 8 up to 256; out in q's
+    dtype. With k_cache / v_cache K / V are also quantized into the cache at `position`.
+    softcap / alibi_slopes as flash_attn_alibi_windowed_softcap (candle-flash-attn/src/lib.rs)."""
+    dt, kvt = _attn_inputs(q, k, v)
     b, sq, hq, d = q.shape
     _, sk, hkv, _ = k.shape
     if out is None:
@@ -459,8 +464,8 @@ def flash_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, softmax_scale:
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _check(lib().cqkv_flash_attn_ext(
         _ptr(q), _strides3(q, (0, 1, 2)), _ptr(k), _strides3(k, (0, 1, 2)), _ptr(v),
-        _strides3(v, (0, 1, 2)), _ptr(out), _strides3(out, (0, 1, 2)), dt, b, sq, sk, hq, hkv, d,
-        softmax_scale, window_left, window_right, softcap, al, al_bs, None, None, 0, 0, kc, vc,
+        _strides3(v, (0, 1, 2)), _ptr(out), _strides3(out, (0, 1, 2)), dt, kvt, b, sq, sk, hq, hkv,
+        d, softmax_scale, window_left, window_right, softcap, al, al_bs, None, None, 0, 0, kc, vc,
         position, ws, ws_bytes, _stream(q.device)))
     return out
 
@@ -476,12 +481,14 @@ def flash_attn_blocks(q: torch.Tensor, blocks, softmax_scale: float, window_left
     _need_gpu(q, "q")
     if not blocks:
         raise CqkvError(ERR_ARG, "no blocks")
-    dt = _attn_inputs(q, blocks[0][0], blocks[0][1])
+    dt, kvt = _attn_inputs(q, blocks[0][0], blocks[0][1])
     b, hq, lq, d = q.shape
     hkv = blocks[0][0].shape[1]
     arr = (PlainBlock * len(blocks))()
     for i, (k, v, rows) in enumerate(blocks):
         _attn_inputs(q, k, v)
+        if k.dtype != blocks[0][0].dtype:
+            raise CqkvError(ERR_ARG, f"block {i}: K / V dtype {k.dtype} differs from block 0's")
         if k.dim() != 4 or v.shape != k.shape or k.shape[0] != b or k.shape[1] != hkv or \
                 k.shape[3] != d:
             raise CqkvError(ERR_ARG, f"block {i}: k {tuple(k.shape)} / v {tuple(v.shape)} do not "
@@ -497,7 +504,8 @@ def flash_attn_blocks(q: torch.Tensor, blocks, softmax_scale: float, window_left
     ws = None if workspace is None else _ptr(workspace)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _check(lib().cqkv_flash_attn_blocks(
-        _ptr(q), _strides3(q, (0, 1, 2)), arr, len(blocks), dt, b, hq, lq, hkv, d, softmax_scale,
+        _ptr(q), _strides3(q, (0, 1, 2)), arr, len(blocks), dt, kvt, b, hq, lq, hkv, d,
+        softmax_scale,
         window_left, window_right, softcap, al, al_bs, _ptr(out), _strides3(out, (0, 1, 2)), ws,
         ws_bytes, _stream(q.device)))
     return out
@@ -532,13 +540,13 @@ def flash_attn_fp8_codes(q: torch.Tensor, k8: torch.Tensor, v8: torch.Tensor,
                          out: torch.Tensor | None = None,
                          workspace: torch.Tensor | None = None) -> torch.Tensor:
     """flash_attn_with_config on F8E4M3 K / V with descale factors (FlashAttnConfig::descale,
-    candle-nn/src/flash_attn.rs:113-117): q (b, s_q, h_q, d) bf16 or f16, k8 / v8
+    candle-nn/src/flash_attn.rs:113-117): q (b, s_q, h_q, d) bf16, f16 or f32, k8 / v8
     (b, s_kv, h_kv, d) E4M3 codes; keys and values are k8 * k_descale * k_scale[0],
     v8 * v_descale * v_scale[0] (the device scales optional). workspace: a device byte tensor
     of flash_attn_fp8_workspace_bytes (None: allocated by the call)."""
     _need_gpu(q, "q")
-    if q.dtype not in (torch.bfloat16, torch.float16):
-        raise CqkvError(ERR_ARG, f"q must be bfloat16 or float16, got {q.dtype}")
+    if q.dtype not in _DTYPES:
+        raise CqkvError(ERR_ARG, f"q must be bfloat16, float16 or float32, got {q.dtype}")
     k8, v8 = _fp8_codes(k8, "k8"), _fp8_codes(v8, "v8")
     b, sq, hq, d = q.shape
     _, sk, hkv, _ = k8.shape
@@ -600,9 +608,9 @@ def flash_attn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                       alibi_slopes: torch.Tensor | None = None,
                       out: torch.Tensor | None = None) -> torch.Tensor:
     """candle_flash_attn::flash_attn_varlen layout: q (total_q, h_q, d), k / v (total_k, h_kv,
-    d) bf16 or f16, cumulative sequence offsets cu_seqlens_q / cu_seqlens_k (batch + 1,) int32 on
-    the device (the reference takes u32)."""
-    dt = _attn_inputs(q, k, v)
+    d) with the dtypes of flash_attn, cumulative sequence offsets cu_seqlens_q / cu_seqlens_k
+    (batch + 1,) int32 on the device (the reference takes u32)."""
+    dt, kvt = _attn_inputs(q, k, v)
     total_q, hq, d = q.shape
     total_k, hkv, _ = k.shape
     for name, c in (("cu_seqlens_q", cu_seqlens_q), ("cu_seqlens_k", cu_seqlens_k)):
@@ -620,7 +628,8 @@ def flash_attn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     strides = lambda t: (ctypes.c_int64 * 3)(0, t.stride(0), t.stride(1))
     _check(lib().cqkv_flash_attn_ext(
         _ptr(q), strides(q), _ptr(k), strides(k), _ptr(v), strides(v), _ptr(out), strides(out),
-        dt, b, max_seqlen_q, max_seqlen_k, hq, hkv, d, softmax_scale, window_left, window_right,
+        dt, kvt, b, max_seqlen_q, max_seqlen_k, hq, hkv, d, softmax_scale, window_left,
+        window_right,
         softcap, al, al_bs, _ptr(cu_seqlens_q), _ptr(cu_seqlens_k), total_q, total_k, None, None,
         0, None, 0, _stream(q.device)))
     return out

@@ -60,6 +60,10 @@ inline bool supported_dim(int32_t d) { return d == 64 || d == 128; }
 
 // TurboQuant width of a side (QuantFormat::TurboMse{bits} / TurboProd{bits}; 0 selects 4), 0 for
 // the other formats.
+// K / V element type of the f32-query attention beyond the CQKV_* dtypes: E4M3 codes (the FP8
+// K / V path with f32 queries).
+constexpr int kKvE4M3 = 3;
+
 inline int side_bits(const cqkv_side *s) {
     return is_turbo(s->format) ? (s->bits ? s->bits : 4) : 0;
 }
@@ -82,5 +86,30 @@ int check_side(const cqkv_side *s, const char *what);
 int turbo_codebook(int dim, int bits, float *centroids, float *boundaries);
 void turbo_signs(int dim, uint64_t seed, float *signs);
 void qjl_matrix(int dim, uint64_t seed, float *out);
+
+// The dense / variable-length flash attention (prefill_attn.hip) behind cqkv_flash_attn_ext and
+// the FP8 K / V path: dtype is q's and out's, kv_dtype K's and V's (dtype itself, or with f32
+// queries CQKV_F16 / CQKV_BF16 / kKvE4M3); q_mul / o_mul and their device factors are the FP8
+// descales (1 / null otherwise).
+int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
+                    const int64_t k_strides[3], const void *v, const int64_t v_strides[3],
+                    void *out, const int64_t out_strides[3], int32_t dtype, int32_t kv_dtype,
+                    int32_t batch, int32_t q_len, int32_t kv_len, int32_t q_heads,
+                    int32_t kv_heads, int32_t head_dim, float softmax_scale, int32_t window_left,
+                    int32_t window_right, float softcap, const float *alibi_slopes,
+                    int32_t alibi_batch_stride, const int32_t *cu_seqlens_q,
+                    const int32_t *cu_seqlens_k, int32_t total_q, int32_t total_k,
+                    const cqkv_side *k_cache, const cqkv_side *v_cache, int32_t position,
+                    void *workspace, size_t workspace_bytes, cqkv_stream_t stream, float q_mul,
+                    const float *q_mul_dev, float o_mul, const float *o_mul_dev);
+size_t flash_attn_workspace(int32_t dtype, int32_t batch, int32_t q_len, int32_t kv_len,
+                            int32_t q_heads, int32_t kv_heads, int32_t head_dim, bool varlen);
+
+// Plain-dtype attention (flash_plain.hip): argument checks, workspace, bytes per K / V element.
+int fa_plain_check(const char *who, int32_t dtype, int32_t kv_dtype, int32_t head_dim,
+                   int64_t k_row_stride, int64_t v_row_stride, int64_t kv_len);
+size_t fa_plain_workspace_bytes(int32_t batch, int32_t q_len, int32_t kv_len, int32_t q_heads,
+                                int32_t kv_heads, int32_t head_dim, bool ragged);
+int fa_kv_esz(int32_t kv_dtype);
 
 }  // namespace cqkv

@@ -43,9 +43,11 @@ struct FaArgs {
     const FaSeg *segs;  // paged calls: one segment per split (null: dense)
     float *part_o, *part_lse;
     int32_t batch, q_len, kv_len, q_heads, kv_heads, group, head_dim, dtype;
+    int32_t kv_dtype;  // K / V element type: dtype, or with f32 queries f16 / bf16 / E4M3 (3)
     int32_t splits, tiles_per_split, col_blocks;
     int32_t wl, wr;
-    int32_t q_vec;  // q rows 16-byte aligned with strides of whole 8-element chunks
+    int32_t q_vec;  // q rows 16-byte aligned with strides of whole 16-byte chunks
+    int32_t o_vec;  // f32 out rows likewise (f32 kernel, column mode)
     float scale_log2;  // softmax scale * log2(e) (times the host query factor)
     float softcap2;    // softcap * log2(e), 0: off
     const float *alibi;

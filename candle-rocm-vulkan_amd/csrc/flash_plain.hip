@@ -39,6 +39,9 @@ static size_t fa_partials_bytes(int splits, int64_t rows, int dmax, size_t *lse_
     return *lse_off + fa_align256((size_t)splits * rows * 4);
 }
 
+// The f32-query kernels (flash_f32.hip).
+void fa32_launch(const FaArgs &a, int dmax, bool tile, hipStream_t st);
+
 template <bool F16, int D>
 static void fa_launch_d(const FaArgs &a, bool tile, hipStream_t st) {
     constexpr int W = fa_waves<D>();
@@ -55,6 +58,10 @@ static void fa_launch_d(const FaArgs &a, bool tile, hipStream_t st) {
 }
 
 static void fa_launch(const FaArgs &a, int dmax, bool tile, hipStream_t st) {
+    if (a.dtype == CQKV_F32) {
+        fa32_launch(a, dmax, tile, st);
+        return;
+    }
     const bool f16 = a.dtype == CQKV_F16;
     if (dmax == 64) f16 ? fa_launch_d<true, 64>(a, tile, st) : fa_launch_d<false, 64>(a, tile, st);
     else if (dmax == 128) f16 ? fa_launch_d<true, 128>(a, tile, st) : fa_launch_d<false, 128>(a, tile, st);
@@ -81,23 +88,38 @@ static FaPlan fa_plan(int64_t batch, int64_t kv_heads, int64_t ncols, int kv_len
     return p;
 }
 
-// Whether a 16-bit tensor's rows can be read as whole 16-byte chunks.
-static bool fa_vec_ok(const void *p, const int64_t s[3]) {
-    return (uintptr_t)p % 16 == 0 && s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0;
+// Whether a tensor's rows can be read as whole 16-byte chunks (`esz`-byte elements).
+static bool fa_vec_ok(const void *p, const int64_t s[3], int esz = 2) {
+    const int64_t e = 16 / esz;
+    return (uintptr_t)p % 16 == 0 && s[0] % e == 0 && s[1] % e == 0 && s[2] % e == 0;
 }
 
-// Checks shared by the dense and the paged calls.
-int fa_plain_check(const char *who, int32_t dtype, int32_t head_dim, int64_t k_row_stride,
-                   int64_t v_row_stride, int64_t kv_len) {
-    if (dtype != CQKV_BF16 && dtype != CQKV_F16)
-        return fail(CQKV_ERR_ARG, "%s: dtype %d (bf16 or f16 q / k / v / out)", who, dtype);
+// Bytes per K / V element of a dtype pair.
+int fa_kv_esz(int32_t kv_dtype) {
+    return kv_dtype == CQKV_F32 ? 4 : kv_dtype == kKvE4M3 ? 1 : 2;
+}
+
+// Checks shared by the dense and the paged calls. The dtype pairs are the reference's
+// (kv_dtype_supported, candle-core/src/accel/attention.rs:569-576): q / out and K / V of one
+// dtype, or f32 queries over f16 / bf16 / E4M3 K / V.
+int fa_plain_check(const char *who, int32_t dtype, int32_t kv_dtype, int32_t head_dim,
+                   int64_t k_row_stride, int64_t v_row_stride, int64_t kv_len) {
+    const bool same = (dtype == CQKV_BF16 || dtype == CQKV_F16 || dtype == CQKV_F32) &&
+                      kv_dtype == dtype;
+    const bool wide = dtype == CQKV_F32 &&
+                      (kv_dtype == CQKV_F16 || kv_dtype == CQKV_BF16 || kv_dtype == kKvE4M3);
+    if (!same && !wide)
+        return fail(CQKV_ERR_ARG,
+                    "%s: dtypes q %d, k / v %d (q / k / v of one of bf16, f16, f32, or f32 q with "
+                    "f16 / bf16 k / v)", who, dtype, kv_dtype);
     if (head_dim <= 0 || head_dim > 256 || head_dim % 8 != 0)
         return fail(CQKV_ERR_ARG, "%s: head_dim %d (a multiple of 8 up to 256)", who, head_dim);
-    // 32-bit byte offsets of the copies inside a 32-row tile
-    if (k_row_stride < head_dim || v_row_stride < head_dim || k_row_stride >= (1 << 25) ||
-        v_row_stride >= (1 << 25))
-        return fail(CQKV_ERR_ARG, "%s: K / V row strides %lld / %lld (head_dim .. 2^25)", who,
-                    (long long)k_row_stride, (long long)v_row_stride);
+    // 32-bit byte offsets inside a 32-row tile (16-bit copies) or a 16-row tile (f32 kernel)
+    const int64_t lim = dtype == CQKV_F32 ? (1 << 24) : (1 << 25);
+    if (k_row_stride < head_dim || v_row_stride < head_dim || k_row_stride >= lim ||
+        v_row_stride >= lim)
+        return fail(CQKV_ERR_ARG, "%s: K / V row strides %lld / %lld (head_dim .. %lld)", who,
+                    (long long)k_row_stride, (long long)v_row_stride, (long long)lim);
     if (kv_len > (1 << 30)) return fail(CQKV_ERR_ARG, "%s: %lld keys", who, (long long)kv_len);
     return CQKV_OK;
 }
@@ -106,11 +128,17 @@ int fa_plain_check(const char *who, int32_t dtype, int32_t head_dim, int64_t k_r
 // prefill does not take): `a` carries tensors, lengths, masks and terms.
 int fa_plain_run(FaArgs a, const char *who, void *workspace, size_t workspace_bytes,
                  hipStream_t st) {
-    if ((uintptr_t)a.k % 16 != 0 || (uintptr_t)a.v % 16 != 0 || a.k_st % 8 != 0 ||
-        a.v_st % 8 != 0 || a.k_sh % 8 != 0 || a.v_sh % 8 != 0 || (!a.cu_k && (a.k_sb % 8 != 0 || a.v_sb % 8 != 0)))
+    // 16-bit kernels: 16-byte copies; f32 kernel: loads of 4 elements
+    const bool f32 = a.dtype == CQKV_F32;
+    const int esz = fa_kv_esz(a.kv_dtype);
+    const int64_t ce = f32 ? 4 : 8;  // elements per aligned piece
+    const uintptr_t cb = (uintptr_t)(ce * esz);
+    if ((uintptr_t)a.k % cb != 0 || (uintptr_t)a.v % cb != 0 || a.k_st % ce != 0 ||
+        a.v_st % ce != 0 || a.k_sh % ce != 0 || a.v_sh % ce != 0 ||
+        (!a.cu_k && (a.k_sb % ce != 0 || a.v_sb % ce != 0)))
         return fail(CQKV_ERR_ARG,
-                    "%s: K / V need 16-byte aligned rows (pointers and strides in whole 8-element chunks)",
-                    who);
+                    "%s: K / V need %d-byte aligned rows (pointers and strides in whole %d-element "
+                    "chunks)", who, (int)cb, (int)ce);
     const int dmax = fa_dmax(a.head_dim);
     const int64_t ncols = (int64_t)a.q_len * a.group;
     if ((ncols + 15) / 16 > (1 << 20))
@@ -125,7 +153,9 @@ int fa_plain_run(FaArgs a, const char *who, void *workspace, size_t workspace_by
     a.tiles_per_split = plan.tps;
     {
         const int64_t qs[3] = {a.cu_q ? 0 : a.q_sb, a.q_st, a.q_sh};
-        a.q_vec = fa_vec_ok(a.q, qs) ? 1 : 0;
+        const int64_t os[3] = {a.cu_q ? 0 : a.o_sb, a.o_st, a.o_sh};
+        a.q_vec = fa_vec_ok(a.q, qs, f32 ? 4 : 2) ? 1 : 0;
+        a.o_vec = f32 && fa_vec_ok(a.out, os, 4) ? 1 : 0;
     }
     void *ws = workspace;
     bool owned = false;
@@ -242,7 +272,8 @@ extern "C" size_t cqkv_flash_attn_blocks_workspace_bytes(const cqkv_plain_block 
 
 extern "C" int cqkv_flash_attn_blocks(const void *q, const int64_t q_strides[3],
                                       const cqkv_plain_block *blocks, int32_t n_blocks,
-                                      int32_t dtype, int32_t batch, int32_t q_heads,
+                                      int32_t dtype, int32_t kv_dtype, int32_t batch,
+                                      int32_t q_heads,
                                       int32_t q_len, int32_t kv_heads, int32_t head_dim,
                                       float softmax_scale, int32_t window_left,
                                       int32_t window_right, float softcap,
@@ -263,6 +294,10 @@ extern "C" int cqkv_flash_attn_blocks(const void *q, const int64_t q_strides[3],
         return fail(CQKV_ERR_ARG, "%s: alibi batch stride %d (0 or q_heads)", who,
                     alibi_batch_stride);
     const int64_t k_row = blocks[0].k_strides[2], v_row = blocks[0].v_strides[2];
+    if (int rc = fa_plain_check(who, dtype, kv_dtype, head_dim, k_row, v_row, 0)) return rc;
+    // 16-bit kernels: 16-byte copies; f32 kernel: loads of 4 elements
+    const int64_t ce = dtype == CQKV_F32 ? 4 : 8;
+    const uintptr_t cb = (uintptr_t)(ce * fa_kv_esz(kv_dtype));
     int64_t total = 0;
     for (int i = 0; i < n_blocks; ++i) {
         const cqkv_plain_block &bl = blocks[i];
@@ -270,15 +305,17 @@ extern "C" int cqkv_flash_attn_blocks(const void *q, const int64_t q_strides[3],
         if (bl.rows < 0) return fail(CQKV_ERR_ARG, "%s: block %d rows %d", who, i, bl.rows);
         if (bl.k_strides[2] != k_row || bl.v_strides[2] != v_row)
             return fail(CQKV_ERR_ARG, "%s: block %d row strides differ from block 0's", who, i);
-        if ((uintptr_t)bl.k % 16 || (uintptr_t)bl.v % 16 || bl.k_strides[0] % 8 ||
-            bl.k_strides[1] % 8 || bl.v_strides[0] % 8 || bl.v_strides[1] % 8)
-            return fail(CQKV_ERR_ARG, "%s: block %d K / V need 16-byte aligned rows", who, i);
+        if ((uintptr_t)bl.k % cb || (uintptr_t)bl.v % cb || bl.k_strides[0] % ce ||
+            bl.k_strides[1] % ce || bl.v_strides[0] % ce || bl.v_strides[1] % ce)
+            return fail(CQKV_ERR_ARG, "%s: block %d K / V need %d-byte aligned rows", who, i,
+                        (int)cb);
         total += bl.rows;
     }
     if (total == 0) return fail(CQKV_ERR_ARG, "%s: the blocks hold no keys", who);
-    if (k_row % 8 || v_row % 8)
-        return fail(CQKV_ERR_ARG, "%s: K / V row strides must be whole 8-element chunks", who);
-    if (int rc = fa_plain_check(who, dtype, head_dim, k_row, v_row, total)) return rc;
+    if (k_row % ce || v_row % ce)
+        return fail(CQKV_ERR_ARG, "%s: K / V row strides must be whole %d-element chunks", who,
+                    (int)ce);
+    if (int rc = fa_plain_check(who, dtype, kv_dtype, head_dim, k_row, v_row, total)) return rc;
     const int dmax = fa_dmax(head_dim);
     const int cols = (int)(((int64_t)q_len * (q_heads / kv_heads) + 15) / 16);
     FaPagedPlan p;
@@ -306,6 +343,7 @@ extern "C" int cqkv_flash_attn_blocks(const void *q, const int64_t q_strides[3],
     a.group = q_heads / kv_heads;
     a.head_dim = head_dim;
     a.dtype = dtype;
+    a.kv_dtype = kv_dtype;
     a.splits = nseg;
     a.tiles_per_split = 0;
     a.col_blocks = cols;
@@ -316,8 +354,8 @@ extern "C" int cqkv_flash_attn_blocks(const void *q, const int64_t q_strides[3],
     a.alibi = alibi_slopes;
     a.alibi_bs = alibi_batch_stride;
     a.o_mul = 1.0f;
-    a.q_vec = (uintptr_t)q % 16 == 0 && q_strides[0] % 8 == 0 && q_strides[1] % 8 == 0 &&
-              q_strides[2] % 8 == 0;
+    a.q_vec = fa_vec_ok(q, q_strides, dtype == CQKV_F32 ? 4 : 2) ? 1 : 0;
+    a.o_vec = dtype == CQKV_F32 && fa_vec_ok(out, out_strides, 4) ? 1 : 0;
 
     const hipStream_t st = (hipStream_t)stream;
     const size_t table = fa_align256((size_t)nseg * sizeof(FaSeg));

@@ -120,20 +120,6 @@ __global__ __launch_bounds__(256) void fp8_stage_kernel(Fp8StageArgs a) {
     *(u32x4 *)(a.vb + dst) = vo;
 }
 
-int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
-                    const int64_t k_strides[3], const void *v, const int64_t v_strides[3],
-                    void *out, const int64_t out_strides[3], int32_t dtype, int32_t batch,
-                    int32_t q_len, int32_t kv_len, int32_t q_heads, int32_t kv_heads,
-                    int32_t head_dim, float softmax_scale, int32_t window_left,
-                    int32_t window_right, float softcap, const float *alibi_slopes,
-                    int32_t alibi_batch_stride, const int32_t *cu_seqlens_q,
-                    const int32_t *cu_seqlens_k, int32_t total_q, int32_t total_k,
-                    const cqkv_side *k_cache, const cqkv_side *v_cache, int32_t position,
-                    void *workspace, size_t workspace_bytes, cqkv_stream_t stream, float q_mul,
-                    const float *q_mul_dev, float o_mul, const float *o_mul_dev);
-size_t flash_attn_workspace(int32_t dtype, int32_t batch, int32_t q_len, int32_t kv_len,
-                            int32_t q_heads, int32_t kv_heads, int32_t head_dim, bool varlen);
-
 }  // namespace cqkv
 
 using namespace cqkv;
@@ -167,11 +153,13 @@ static size_t fp8_stage_bytes(int32_t batch, int32_t kv_len, int32_t kv_heads, i
 extern "C" size_t cqkv_flash_attn_fp8_workspace_bytes(int32_t dtype, int32_t batch, int32_t q_len,
                                                       int32_t kv_len, int32_t q_heads,
                                                       int32_t kv_heads, int32_t head_dim) {
-    if ((dtype != CQKV_BF16 && dtype != CQKV_F16) || batch <= 0 || q_len <= 0 || kv_len <= 0 ||
-        q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0 || head_dim <= 0 ||
-        head_dim > 256 || head_dim % 8 != 0)
+    if ((dtype != CQKV_BF16 && dtype != CQKV_F16 && dtype != CQKV_F32) || batch <= 0 ||
+        q_len <= 0 || kv_len <= 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0 ||
+        head_dim <= 0 || head_dim > 256 || head_dim % 8 != 0)
         return 0;
-    return fp8_stage_bytes(batch, kv_len, kv_heads, head_dim) +
+    // f32 queries read the codes directly (no staged copy)
+    const size_t stage = dtype == CQKV_F32 ? 0 : fp8_stage_bytes(batch, kv_len, kv_heads, head_dim);
+    return stage +
            flash_attn_workspace(dtype, batch, q_len, kv_len, q_heads, kv_heads, head_dim, false);
 }
 
@@ -188,8 +176,8 @@ extern "C" int cqkv_flash_attn_fp8(const void *q, const int64_t q_strides[3], co
     static const char *who = "cqkv_flash_attn_fp8";
     if (!q || !k8 || !v8 || !out || !q_strides || !k_strides || !v_strides || !out_strides)
         return fail(CQKV_ERR_ARG, "%s: null tensor or strides", who);
-    if (dtype != CQKV_BF16 && dtype != CQKV_F16)
-        return fail(CQKV_ERR_ARG, "%s: dtype %d (bf16 or f16 q / out)", who, dtype);
+    if (dtype != CQKV_BF16 && dtype != CQKV_F16 && dtype != CQKV_F32)
+        return fail(CQKV_ERR_ARG, "%s: dtype %d (bf16, f16 or f32 q / out)", who, dtype);
     if (head_dim <= 0 || head_dim > 256 || head_dim % 8 != 0)
         return fail(CQKV_ERR_ARG, "%s: head_dim %d (a multiple of 8 up to 256)", who, head_dim);
     // the attention's own limits, checked before the staging pass is launched
@@ -204,6 +192,15 @@ extern "C" int cqkv_flash_attn_fp8(const void *q, const int64_t q_strides[3], co
             return fail(CQKV_ERR_ARG, "%s: K / V strides must be multiples of 8 bytes", who);
     if ((uintptr_t)k8 % 8 != 0 || (uintptr_t)v8 % 8 != 0)
         return fail(CQKV_ERR_ARG, "%s: K / V must be 8-byte aligned", who);
+    if (dtype == CQKV_F32) {
+        // the f32-query kernel reads the E4M3 codes and widens them exactly, with k_descale in the
+        // scores' scale and v_descale in the output, as the reference's fa_row_f32_fp8 does
+        return flash_attn_impl(q, q_strides, k8, k_strides, v8, v_strides, out, out_strides, dtype,
+                               kKvE4M3, batch, q_len, kv_len, q_heads, kv_heads, head_dim,
+                               softmax_scale, window_left, window_right, 0.0f, nullptr, 0, nullptr,
+                               nullptr, 0, 0, nullptr, nullptr, 0, workspace, workspace_bytes,
+                               stream, k_descale, k_scale, v_descale, v_scale);
+    }
     const hipStream_t st = (hipStream_t)stream;
     const size_t stage = fp8_stage_bytes(batch, kv_len, kv_heads, head_dim);
     const size_t need = cqkv_flash_attn_fp8_workspace_bytes(dtype, batch, q_len, kv_len, q_heads,
@@ -242,7 +239,7 @@ extern "C" int cqkv_flash_attn_fp8(const void *q, const int64_t q_strides[3], co
         // the staged K / V are (batch, kv_heads, kv_len, D): (batch, token, head) strides
         const int64_t ss[3] = {(int64_t)kv_heads * kv_len * head_dim, head_dim,
                                (int64_t)kv_len * head_dim};
-        rc = flash_attn_impl(q, q_strides, s.kb, ss, s.vb, ss, out, out_strides, dtype, batch,
+        rc = flash_attn_impl(q, q_strides, s.kb, ss, s.vb, ss, out, out_strides, dtype, dtype, batch,
                              q_len, kv_len, q_heads, kv_heads, head_dim, softmax_scale,
                              window_left, window_right, 0.0f, nullptr, 0, nullptr, nullptr, 0, 0,
                              nullptr, nullptr, 0, (uint8_t *)ws + stage, need - stage, stream,

@@ -826,12 +826,8 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
     }
 }
 
-int fa_plain_check(const char *who, int32_t dtype, int32_t head_dim, int64_t k_row_stride,
-                   int64_t v_row_stride, int64_t kv_len);
 int fa_plain_run(FaArgs a, const char *who, void *workspace, size_t workspace_bytes,
                  hipStream_t st);
-size_t fa_plain_workspace_bytes(int32_t batch, int32_t q_len, int32_t kv_len, int32_t q_heads,
-                                int32_t kv_heads, int32_t head_dim, bool ragged);
 
 int quant_append_launch(const cqkv_side *side, const void *x, int32_t x_dtype,
                         const int64_t xs[3], int32_t batch, int32_t tokens,
@@ -873,9 +869,9 @@ size_t flash_attn_workspace(int32_t dtype, int32_t batch, int32_t q_len, int32_t
 
 int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
                     const int64_t k_strides[3], const void *v, const int64_t v_strides[3],
-                    void *out, const int64_t out_strides[3], int32_t dtype, int32_t batch,
-                    int32_t q_len, int32_t kv_len, int32_t q_heads, int32_t kv_heads,
-                    int32_t head_dim, float softmax_scale, int32_t window_left,
+                    void *out, const int64_t out_strides[3], int32_t dtype, int32_t kv_dtype,
+                    int32_t batch, int32_t q_len, int32_t kv_len, int32_t q_heads,
+                    int32_t kv_heads, int32_t head_dim, float softmax_scale, int32_t window_left,
                     int32_t window_right, float softcap, const float *alibi_slopes,
                     int32_t alibi_batch_stride, const int32_t *cu_seqlens_q,
                     const int32_t *cu_seqlens_k, int32_t total_q, int32_t total_k,
@@ -891,15 +887,16 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
         const int64_t e = bytes / 2;  // elements per aligned piece
         return (uintptr_t)p % bytes == 0 && (vl || s[0] % e == 0) && s[1] % e == 0 && s[2] % e == 0;
     };
-    if (!aligned(k, k_strides, 16) || !aligned(v, v_strides, 16))
+    // (the f32-query kernel checks its own, 4-element, alignment)
+    if (dtype != CQKV_F32 && (!aligned(k, k_strides, 16) || !aligned(v, v_strides, 16)))
         return fail(CQKV_ERR_ARG,
                     "cqkv_flash_attn: K / V need 16-byte aligned rows (pointers and strides in "
                     "whole 8-element chunks)");
-    const bool fast = pf_fast_path(dtype, head_dim, q_len) && aligned(q, q_strides, 16) &&
-                      aligned(out, out_strides, 8);
+    const bool fast = kv_dtype == dtype && pf_fast_path(dtype, head_dim, q_len) &&
+                      aligned(q, q_strides, 16) && aligned(out, out_strides, 8);
     if (!fast) {
-        if (int rc = fa_plain_check("cqkv_flash_attn", dtype, head_dim, k_strides[1], v_strides[1],
-                                    kv_len))
+        if (int rc = fa_plain_check("cqkv_flash_attn", dtype, kv_dtype, head_dim, k_strides[1],
+                                    v_strides[1], kv_len))
             return rc;
     }
     if (batch <= 0 || q_len <= 0 || kv_len <= 0 || q_heads <= 0 || kv_heads <= 0 ||
@@ -971,6 +968,7 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
         f.group = q_heads / kv_heads;
         f.head_dim = head_dim;
         f.dtype = dtype;
+        f.kv_dtype = kv_dtype;
         f.wl = window_left;
         f.wr = window_right;
         f.scale_log2 = softmax_scale * q_mul * kLog2e;
@@ -985,9 +983,9 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
             // K / V are (batch, kv_len, kv_heads, D): the append kernel's (batch, head, token)
             const int64_t ks[3] = {k_strides[0], k_strides[2], k_strides[1]};
             const int64_t vs[3] = {v_strides[0], v_strides[2], v_strides[1]};
-            if (int rc = quant_append_launch(k_cache, k, dtype, ks, batch, kv_len, nullptr, position, st, 0))
+            if (int rc = quant_append_launch(k_cache, k, kv_dtype, ks, batch, kv_len, nullptr, position, st, 0))
                 return rc;
-            if (int rc = quant_append_launch(v_cache, v, dtype, vs, batch, kv_len, nullptr, position, st, 0))
+            if (int rc = quant_append_launch(v_cache, v, kv_dtype, vs, batch, kv_len, nullptr, position, st, 0))
                 return rc;
         }
         return CQKV_OK;
@@ -1099,18 +1097,22 @@ extern "C" size_t cqkv_flash_attn_workspace_bytes(int32_t dtype, int32_t batch, 
 extern "C" int cqkv_flash_attn_ext(const void *q, const int64_t q_strides[3], const void *k,
                                    const int64_t k_strides[3], const void *v,
                                    const int64_t v_strides[3], void *out,
-                                   const int64_t out_strides[3], int32_t dtype, int32_t batch,
-                                   int32_t q_len, int32_t kv_len, int32_t q_heads,
-                                   int32_t kv_heads, int32_t head_dim, float softmax_scale,
-                                   int32_t window_left, int32_t window_right, float softcap,
+                                   const int64_t out_strides[3], int32_t dtype,
+                                   int32_t kv_dtype, int32_t batch, int32_t q_len,
+                                   int32_t kv_len, int32_t q_heads, int32_t kv_heads,
+                                   int32_t head_dim, float softmax_scale, int32_t window_left,
+                                   int32_t window_right, float softcap,
                                    const float *alibi_slopes, int32_t alibi_batch_stride,
                                    const int32_t *cu_seqlens_q, const int32_t *cu_seqlens_k,
                                    int32_t total_q, int32_t total_k, const cqkv_side *k_cache,
                                    const cqkv_side *v_cache, int32_t position, void *workspace,
                                    size_t workspace_bytes, cqkv_stream_t stream) {
     clear_error();
+    // E4M3 K / V come through cqkv_flash_attn_fp8 (which carries their descales)
+    if (kv_dtype == kKvE4M3)
+        return fail(CQKV_ERR_ARG, "cqkv_flash_attn_ext: kv_dtype %d (bf16, f16 or f32)", kv_dtype);
     return flash_attn_impl(q, q_strides, k, k_strides, v, v_strides, out, out_strides, dtype,
-                           batch, q_len, kv_len, q_heads, kv_heads, head_dim, softmax_scale,
+                           kv_dtype, batch, q_len, kv_len, q_heads, kv_heads, head_dim, softmax_scale,
                            window_left, window_right, softcap, alibi_slopes, alibi_batch_stride,
                            cu_seqlens_q, cu_seqlens_k, total_q, total_k, k_cache, v_cache,
                            position, workspace, workspace_bytes, stream, 1.0f, nullptr, 1.0f,
@@ -1126,7 +1128,7 @@ extern "C" int cqkv_flash_attn(const void *q, const int64_t q_strides[3], const 
                                int32_t window_right, const cqkv_side *k_cache,
                                const cqkv_side *v_cache, int32_t position, cqkv_stream_t stream) {
     return cqkv_flash_attn_ext(q, q_strides, k, k_strides, v, v_strides, out, out_strides, dtype,
-                               batch, q_len, kv_len, q_heads, kv_heads, head_dim, softmax_scale,
+                               dtype, batch, q_len, kv_len, q_heads, kv_heads, head_dim, softmax_scale,
                                window_left, window_right, 0.0f, nullptr, 0, nullptr, nullptr, 0, 0,
                                k_cache, v_cache, position, nullptr, 0, stream);
 }

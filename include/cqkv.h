@@ -267,15 +267,17 @@ int cqkv_decode_attention_paged(const void *q, int32_t q_dtype, const int64_t q_
 
 /* Dense flash attention (FlashAttnOp / candle_flash_attn::flash_attn):
  *   q (batch, q_len, q_heads, D), k / v (batch, kv_len, kv_heads, D), out like q, all of
- *   `dtype` (CQKV_BF16 or CQKV_F16), element strides {batch, token, head} (D contiguous);
- *   head_dim any multiple of 8 up to 256 (the reference's FA_MAX_HEAD_DIM); any
+ *   `dtype` (CQKV_BF16, CQKV_F16 or CQKV_F32), element strides {batch, token, head} (D
+ *   contiguous); head_dim any multiple of 8 up to 256 (the reference's FA_MAX_HEAD_DIM); any
  *   q_heads % kv_heads == 0; bottom-right aligned windows; causal = window (-1, 0).
  *   bf16 / f16 at head_dim 128 with more than 16 queries runs the MFMA prefill kernel; every
- *   other call runs the plain-dtype kernels over split-K: up to 16 (query, head) columns per kv
- *   head the row kernel (the reference's fa_row_* / fa_rowg_*,
+ *   other bf16 / f16 call runs the plain-dtype kernels over split-K: up to 16 (query, head)
+ *   columns per kv head the row kernel (the reference's fa_row_* / fa_rowg_*,
  *   candle-core/kernels/flash_attn_impl.h:49-328), more the shared-tile kernel (its tile
  *   kernels, :330-443). K / V need 16-byte aligned rows (pointers and strides whole 8-element
- *   chunks).
+ *   chunks). f32 runs the f32 kernels (f32 math on the f32 MFMA, as the reference's
+ *   fa_row_f32_* / fa*_f32_*); their K / V need rows aligned to 4 elements (pointers and
+ *   strides whole 4-element chunks), row strides below 2^24 elements.
  *   When k_cache / v_cache are non-NULL (a key and a value side of any formats and rotations)
  *   the same call also quantizes and appends k / v at positions [position, position + kv_len)
  *   of the cache: inside the MFMA prefill's pre-pass for unrotated FP8 sides at a position that
@@ -289,14 +291,18 @@ int cqkv_flash_attn(const void *q, const int64_t q_strides[3], const void *k,
                     int32_t position, cqkv_stream_t stream);
 
 /* Device workspace cqkv_flash_attn_ext needs for a call of these sizes (varlen != 0: per-sequence
- * lengths, q_len / kv_len their maxima): the MFMA prefill's V^T copy, or the plain kernel's split
- * partials (0 when it does not split). */
+ * lengths, q_len / kv_len their maxima; dtype is q's, the K / V dtype does not change it): the
+ * MFMA prefill's V^T copy, or the plain kernel's split partials (0 when it does not split). */
 size_t cqkv_flash_attn_workspace_bytes(int32_t dtype, int32_t batch, int32_t q_len,
                                        int32_t kv_len, int32_t q_heads, int32_t kv_heads,
                                        int32_t head_dim, int32_t varlen);
 
-/* cqkv_flash_attn plus the reference's optional score terms and variable-length batches
- * (fa_logit, candle-core/kernels/flash_attn_impl.h:42-47; fa_tile_impl :330-443):
+/* cqkv_flash_attn plus mixed dtypes, the reference's optional score terms and variable-length
+ * batches (fa_logit, candle-core/kernels/flash_attn_impl.h:42-47; fa_tile_impl :330-443):
+ *   dtype is q's and out's, kv_dtype k's and v's: equal, or f32 queries over CQKV_F16 /
+ *     CQKV_BF16 K / V (the reference's kv_dtype_supported, candle-core/src/accel/attention.rs:
+ *     569-576; the K / V elements are widened exactly, then f32 math; E4M3 K / V go through
+ *     cqkv_flash_attn_fp8). A cache append quantizes k / v from kv_dtype;
  *   softcap > 0: score = softcap * tanh(score / softcap) (0 disables it);
  *   alibi_slopes (device f32, NULL: none): score -= slope * |pos - key| with slope =
  *     alibi_slopes[b * alibi_batch_stride + head], stride 0 (slopes per head) or q_heads;
@@ -310,9 +316,9 @@ size_t cqkv_flash_attn_workspace_bytes(int32_t dtype, int32_t batch, int32_t q_l
  * Soft-capping precedes ALiBi, and masked keys stay masked, as in the reference. */
 int cqkv_flash_attn_ext(const void *q, const int64_t q_strides[3], const void *k,
                         const int64_t k_strides[3], const void *v, const int64_t v_strides[3],
-                        void *out, const int64_t out_strides[3], int32_t dtype, int32_t batch,
-                        int32_t q_len, int32_t kv_len, int32_t q_heads, int32_t kv_heads,
-                        int32_t head_dim, float softmax_scale, int32_t window_left,
+                        void *out, const int64_t out_strides[3], int32_t dtype, int32_t kv_dtype,
+                        int32_t batch, int32_t q_len, int32_t kv_len, int32_t q_heads,
+                        int32_t kv_heads, int32_t head_dim, float softmax_scale, int32_t window_left,
                         int32_t window_right, float softcap, const float *alibi_slopes,
                         int32_t alibi_batch_stride, const int32_t *cu_seqlens_q,
                         const int32_t *cu_seqlens_k, int32_t total_q, int32_t total_k,
@@ -334,15 +340,18 @@ typedef struct cqkv_plain_block {
  * {batch, head, query}, over the concatenated valid rows of n_blocks blocks without copying them
  * (any number of blocks; the reference's kernel takes at most 128 and concatenates beyond);
  * every sequence sees all the rows; masks, soft-capping and ALiBi bottom-right aligned over
- * them. q / K / V / out of `dtype` (bf16 or f16), K / V rows 16-byte aligned with one row stride
+ * them. q / out of `dtype`, K / V of `kv_dtype`, the pairs of cqkv_flash_attn_ext (bf16 / bf16,
+ * f16 / f16, f32 / f32, f32 / f16, f32 / bf16), K / V rows aligned as there with one row stride
  * per side across the blocks. out like q (strides {batch, head, query}). Errors as the
- * reference's check_blocks (flash_attn.rs:650-686). */
+ * reference's check_blocks (flash_attn.rs:650-686). The workspace does not depend on the
+ * dtypes. */
 size_t cqkv_flash_attn_blocks_workspace_bytes(const cqkv_plain_block *blocks, int32_t n_blocks,
                                               int32_t batch, int32_t q_heads, int32_t q_len,
                                               int32_t kv_heads, int32_t head_dim);
 int cqkv_flash_attn_blocks(const void *q, const int64_t q_strides[3],
                            const cqkv_plain_block *blocks, int32_t n_blocks, int32_t dtype,
-                           int32_t batch, int32_t q_heads, int32_t q_len, int32_t kv_heads,
+                           int32_t kv_dtype, int32_t batch, int32_t q_heads, int32_t q_len,
+                           int32_t kv_heads,
                            int32_t head_dim, float softmax_scale, int32_t window_left,
                            int32_t window_right, float softcap, const float *alibi_slopes,
                            int32_t alibi_batch_stride, void *out, const int64_t out_strides[3],
@@ -356,12 +365,14 @@ int cqkv_fp8_quantize_tensor(const void *x, int32_t x_dtype, int64_t n, uint8_t 
                              float *scale, cqkv_stream_t stream);
 
 /* Attention over E4M3 K / V with descale factors (flash_attn_with_config on F8E4M3 tensors):
- * shapes, strides, head dims and masks as cqkv_flash_attn (q, out of `dtype`, bf16 or f16; k8 /
- * v8 E4M3 bytes, strides multiples of 8, 8-byte aligned). Keys are e4m3(k8) * k_descale *
+ * shapes, strides, head dims and masks as cqkv_flash_attn (q, out of `dtype`, bf16, f16 or f32;
+ * k8 / v8 E4M3 bytes, strides multiples of 8, 8-byte aligned). Keys are e4m3(k8) * k_descale *
  * (k_scale ? *k_scale : 1), values likewise with v_descale / v_scale (device floats, e.g. the
- * scales written by cqkv_fp8_quantize_tensor, read on the device). The codes are converted to
- * the dtype (exactly) into the workspace, then the attention runs with the descales folded into
- * the query scale and the output normalisation. workspace: at least
+ * scales written by cqkv_fp8_quantize_tensor, read on the device). bf16 / f16: the codes are
+ * converted to the dtype (exactly) into the workspace, then the attention runs with the descales
+ * folded into the query scale and the output normalisation. f32 (the reference's
+ * fa_row_f32_fp8): the f32 kernels read the codes directly, widen them exactly and compute in
+ * f32, the descales folded the same way. workspace: at least
  * cqkv_flash_attn_fp8_workspace_bytes(); NULL = allocated (stream-ordered) and freed by the call. */
 size_t cqkv_flash_attn_fp8_workspace_bytes(int32_t dtype, int32_t batch, int32_t q_len,
                                            int32_t kv_len, int32_t q_heads, int32_t kv_heads,

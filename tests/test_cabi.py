@@ -142,18 +142,26 @@ def test_flash_attn_ext_argument_errors(cq):
     one = ctypes.c_void_p(256)
 
     def call(softcap=0.0, alibi=None, alibi_bs=0, cu_q=None, cu_k=None, tq=0, tk=0, kc=None,
-             vc=None, hq=8, batch=2, dtype=0, d=128, kp=one, ks=x, ql=16):
-        return L.cqkv_flash_attn_ext(one, x, kp, ks, one, x, one, x, dtype, batch, ql, 16, hq, 2,
-                                     d, 0.1, -1, 0, softcap, alibi, alibi_bs, cu_q, cu_k, tq, tk,
-                                     kc, vc, 0, None, 0, None)
-    # K / V rows must be 16-byte aligned (the kernels' 16-byte row loads), dtypes bf16 / f16,
-    # head dims multiples of 8 up to 256
+             vc=None, hq=8, batch=2, dtype=0, kvd=None, d=128, kp=one, ks=x, ql=16):
+        kvd = dtype if kvd is None else kvd
+        return L.cqkv_flash_attn_ext(one, x, kp, ks, one, x, one, x, dtype, kvd, batch, ql, 16,
+                                     hq, 2, d, 0.1, -1, 0, softcap, alibi, alibi_bs, cu_q, cu_k,
+                                     tq, tk, kc, vc, 0, None, 0, None)
+    # K / V rows must be 16-byte aligned (the kernels' 16-byte row loads) for bf16 / f16, rows of
+    # whole 4-element pieces for f32 queries; head dims multiples of 8 up to 256
     assert call(kp=ctypes.c_void_p(258)) == cq.ERR_ARG
     assert b"16-byte aligned" in L.cqkv_last_error()
     assert call(ks=(ctypes.c_int64 * 3)(8192, 260, 128)) == cq.ERR_ARG
     assert call(ks=(ctypes.c_int64 * 3)(8192, 260, 128), ql=64) == cq.ERR_ARG
-    assert call(dtype=2) == cq.ERR_ARG
-    assert b"dtype" in L.cqkv_last_error()
+    assert call(dtype=2, kp=ctypes.c_void_p(260)) == cq.ERR_ARG  # f32 rows: 16-byte pieces
+    assert b"aligned" in L.cqkv_last_error()
+    assert call(dtype=2, kvd=0, kp=ctypes.c_void_p(252)) == cq.ERR_ARG  # bf16 rows: 8-byte pieces
+    assert call(dtype=2, kvd=1, ks=(ctypes.c_int64 * 3)(8192, 258, 128)) == cq.ERR_ARG
+    # the reference's dtype pairs only (kv_dtype_supported): no f16 / bf16 mix, no f32 K / V
+    # under half queries, no E4M3 here (cqkv_flash_attn_fp8 takes it), no unknown ids
+    for dt, kvd in ((0, 1), (1, 0), (0, 2), (1, 2), (2, 3), (3, 3), (-1, -1)):
+        assert call(dtype=dt, kvd=kvd) == cq.ERR_ARG, (dt, kvd)
+        assert b"dtype" in L.cqkv_last_error()
     assert call(d=100) == cq.ERR_ARG
     assert call(d=264) == cq.ERR_ARG
     assert b"head_dim" in L.cqkv_last_error()
@@ -269,10 +277,14 @@ def test_fp8_attention_argument_errors(cq):
                                      0.1, -1, 0, kd, 1.0, None, None, ws, wsb, None)
     assert attn(hd=260) == cq.ERR_ARG  # head dims: multiples of 8 up to 256
     assert attn(hd=100) == cq.ERR_ARG
-    assert attn(dtype=2) == cq.ERR_ARG  # bf16 / f16 queries
+    assert attn(dtype=3) == cq.ERR_ARG  # bf16 / f16 / f32 queries
     assert attn(ws=one, wsb=16) == cq.ERR_WORKSPACE  # a workspace below the query's size
     assert L.cqkv_flash_attn_fp8_workspace_bytes(0, 1, 16, 16, 8, 8, 128) > 0
-    assert L.cqkv_flash_attn_fp8_workspace_bytes(2, 1, 16, 16, 8, 8, 128) == 0
+    assert L.cqkv_flash_attn_fp8_workspace_bytes(3, 1, 16, 16, 8, 8, 128) == 0
+    # f32 queries read the codes directly: only the attention's own split partials
+    f32_ws = L.cqkv_flash_attn_fp8_workspace_bytes(2, 1, 1, 8192, 32, 8, 128)
+    assert f32_ws == L.cqkv_flash_attn_workspace_bytes(2, 1, 1, 8192, 32, 8, 128, 0) > 0
+    assert f32_ws < L.cqkv_flash_attn_fp8_workspace_bytes(0, 1, 1, 8192, 32, 8, 128)
     assert attn(ks=odd) == cq.ERR_ARG
     assert b"multiples of 8" in L.cqkv_last_error()
     assert attn(kd=float("nan")) == cq.ERR_ARG
@@ -342,10 +354,11 @@ def test_flash_attn_blocks_argument_errors(cq):
         b.v_strides[:] = [2 * 64 * vr, 64 * vr, vr]
         return b
 
-    def call(*bl, dtype=0, d=128, softcap=0.0, hq=8):
+    def call(*bl, dtype=0, kvd=None, d=128, softcap=0.0, hq=8):
         arr = (cq.PlainBlock * max(len(bl), 1))(*bl)
-        return L.cqkv_flash_attn_blocks(one, qs, arr, len(bl), dtype, 1, hq, 1, 2, d, 0.1, -1, 0,
-                                        softcap, None, 0, one, qs, None, 0, None)
+        kvd = dtype if kvd is None else kvd
+        return L.cqkv_flash_attn_blocks(one, qs, arr, len(bl), dtype, kvd, 1, hq, 1, 2, d, 0.1,
+                                        -1, 0, softcap, None, 0, one, qs, None, 0, None)
     assert call() == cq.ERR_ARG
     assert b"no blocks" in L.cqkv_last_error()
     assert call(blk(rows=0), blk(rows=0)) == cq.ERR_ARG
@@ -355,7 +368,11 @@ def test_flash_attn_blocks_argument_errors(cq):
     assert b"row strides" in L.cqkv_last_error()
     assert call(blk(k=264)) == cq.ERR_ARG
     assert b"aligned" in L.cqkv_last_error()
-    assert call(blk(), dtype=2) == cq.ERR_ARG
+    assert call(blk(), dtype=0, kvd=1) == cq.ERR_ARG
+    assert b"dtype" in L.cqkv_last_error()
+    assert call(blk(), dtype=1, kvd=2) == cq.ERR_ARG
+    assert call(blk(k=260), dtype=2, kvd=1) == cq.ERR_ARG  # 4-element (8-byte) pieces
+    assert b"aligned" in L.cqkv_last_error()
     assert call(blk(), d=300) == cq.ERR_ARG
     assert call(blk(), softcap=-1.0) == cq.ERR_ARG
     assert call(blk(), hq=5) == cq.ERR_ARG

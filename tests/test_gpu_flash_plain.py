@@ -153,8 +153,8 @@ def test_explicit_workspace_matches_allocated(cq, dev):
 
 def test_refused_inputs(cq, dev):
     q = randn(91, (1, 8, 4, 128), "bf16").to(dev)
-    with pytest.raises(cq.CqkvError):  # f32
-        cq.flash_attn(q.float(), q.float(), q.float(), 0.1, True)
+    with pytest.raises(cq.CqkvError):  # f32 K / V under bf16 queries (f32 queries take them)
+        cq.flash_attn(q, q.float(), q.float(), 0.1, True)
     with pytest.raises(cq.CqkvError):  # mixed dtypes
         cq.flash_attn(q, q.half(), q, 0.1, True)
     with pytest.raises(cq.CqkvError):  # head dim not contiguous

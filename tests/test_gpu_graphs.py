@@ -44,7 +44,9 @@ def randn(seed, shape, dtype=torch.bfloat16, dev="cuda"):
 
 @pytest.mark.parametrize("dtype,d,sq,sk", [(torch.bfloat16, 128, 200, 200),  # MFMA prefill
                                            (torch.float16, 64, 100, 900),    # tile kernel
-                                           (torch.bfloat16, 128, 1, 3000)])  # row kernel, splits
+                                           (torch.bfloat16, 128, 1, 3000),   # row kernel, splits
+                                           (torch.float32, 64, 100, 900),    # f32, column mode
+                                           (torch.float32, 128, 1, 3000)])   # f32 rows, splits
 def test_flash_attn_capture(cq, dev, dtype, d, sq, sk):
     b, hq, hkv = 2, 8, 2
     q, k, v = (randn(i, s, dtype, dev) for i, s in
