@@ -468,6 +468,61 @@ __device__ inline void prod_qjl(const AppendArgs &a, const float (&x)[32], float
     }
 }
 
+// The 8-token value tiles of ROWS rows starting at cache position c0 (a multiple of 8), from
+// their row-major codes in LDS (kRowBytes per row): a 16-byte piece of a tile holds 2 (byte
+// codes) or 4 (nibble codes) elements of all 8 tokens. Positions outside [pos, end) keep the
+// codes already in the cache. All NT threads of the workgroup take part.
+template <bool kB8, int D, int ROWS, int NT = 256>
+__device__ inline void write_value_tiles(uint8_t *codes, const uint8_t *sm_codes, int c0, int pos,
+                                         int end, int tid) {
+    constexpr int kRowBytes = kB8 ? D : D / 2;
+    constexpr int kPer = kB8 ? 2 : 4;           // elements per piece
+    constexpr int kPieces = ROWS / 8 * (D / kPer);
+    for (int i = tid; i < kPieces; i += NT) {
+        const int T = i / (D / kPer), e = i % (D / kPer);
+        const int tt = c0 + 8 * T;  // first cache position of the tile
+        uint32_t mask = 0;
+#pragma unroll
+        for (int s2 = 0; s2 < 8; ++s2) mask |= (tt + s2 >= pos && tt + s2 < end) ? 1u << s2 : 0u;
+        if (!mask) continue;
+        uint32_t wv[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int s2 = 0; s2 < 8; ++s2) {
+            const uint32_t c2 = *(const uint16_t *)(sm_codes + (8 * T + s2) * kRowBytes + 2 * e);
+            if constexpr (kB8) {  // elements 2e (low byte), 2e + 1: bytes e*16 + s2, + 8
+                wv[s2 / 4] |= (c2 & 0xffu) << (8 * (s2 % 4));
+                wv[2 + s2 / 4] |= (c2 >> 8) << (8 * (s2 % 4));
+            } else {  // elements 4e .. 4e + 3: nibble k of c2, word k, nibble s2
+#pragma unroll
+                for (int k = 0; k < 4; ++k) wv[k] |= ((c2 >> (4 * k)) & 15u) << (4 * s2);
+            }
+        }
+        u32x4 *dst = (u32x4 *)(codes + (int64_t)(tt / 8) * (kB8 ? D * 8 : D * 4) + 16 * e);
+        if (mask != 0xffu) {  // keep the codes of tokens this call does not write
+            uint32_t keep[4];
+            if constexpr (kB8) {
+                uint32_t kb = 0;
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2) kb |= ((mask >> s2) & 1u) ? 0u : 0xffu << (8 * s2);
+                uint32_t kh = 0;
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2) kh |= ((mask >> (s2 + 4)) & 1u) ? 0u : 0xffu << (8 * s2);
+                keep[0] = keep[2] = kb;
+                keep[1] = keep[3] = kh;
+            } else {
+                uint32_t kn = 0;
+#pragma unroll
+                for (int s2 = 0; s2 < 8; ++s2) kn |= ((mask >> s2) & 1u) ? 0u : 0xfu << (4 * s2);
+                keep[0] = keep[1] = keep[2] = keep[3] = kn;
+            }
+            const u32x4 old = *dst;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) wv[k] = (wv[k] & ~keep[k]) | (old[k] & keep[k]);
+        }
+        *dst = u32x4{wv[0], wv[1], wv[2], wv[3]};
+    }
+}
+
 template <int FMT, int IS_VALUE, int D, int LOAD, int ROPE, int NR>
 __device__ inline void rows_block(const AppendArgs &a, int h, int b, int bx) {
     constexpr int R = D / 32, ROWS = NR;
@@ -682,53 +737,7 @@ __device__ inline void rows_block(const AppendArgs &a, int h, int b, int bx) {
             if constexpr (kB8) *(u32x4 *)(row + 16) = u32x4{cw[4], cw[5], cw[6], cw[7]};
         }
         __syncthreads();
-        // value tiles: 8 tokens x D elements; a 16-byte piece holds 2 (byte codes) or 4 (nibble
-        // codes) elements of all 8 tokens
-        constexpr int kPer = kB8 ? 2 : 4;           // elements per piece
-        constexpr int kPieces = ROWS / 8 * (D / kPer);
-        for (int i = tid; i < kPieces; i += 256) {
-            const int T = i / (D / kPer), e = i % (D / kPer);
-            const int tt = c0 + 8 * T;  // first cache position of the tile
-            uint32_t mask = 0;
-#pragma unroll
-            for (int s2 = 0; s2 < 8; ++s2) mask |= (tt + s2 >= pos && tt + s2 < end) ? 1u << s2 : 0u;
-            if (!mask) continue;
-            uint32_t wv[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-            for (int s2 = 0; s2 < 8; ++s2) {
-                const uint32_t c2 = *(const uint16_t *)(sm_codes + (8 * T + s2) * kRowBytes + 2 * e);
-                if constexpr (kB8) {  // elements 2e (low byte), 2e + 1: bytes e*16 + s2, + 8
-                    wv[s2 / 4] |= (c2 & 0xffu) << (8 * (s2 % 4));
-                    wv[2 + s2 / 4] |= (c2 >> 8) << (8 * (s2 % 4));
-                } else {  // elements 4e .. 4e + 3: nibble k of c2, word k, nibble s2
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) wv[k] |= ((c2 >> (4 * k)) & 15u) << (4 * s2);
-                }
-            }
-            u32x4 *dst = (u32x4 *)(codes + (int64_t)(tt / 8) * (kB8 ? D * 8 : D * 4) + 16 * e);
-            if (mask != 0xffu) {  // keep the codes of tokens this call does not write
-                uint32_t keep[4];
-                if constexpr (kB8) {
-                    uint32_t kb = 0;
-#pragma unroll
-                    for (int s2 = 0; s2 < 4; ++s2) kb |= ((mask >> s2) & 1u) ? 0u : 0xffu << (8 * s2);
-                    uint32_t kh = 0;
-#pragma unroll
-                    for (int s2 = 0; s2 < 4; ++s2) kh |= ((mask >> (s2 + 4)) & 1u) ? 0u : 0xffu << (8 * s2);
-                    keep[0] = keep[2] = kb;
-                    keep[1] = keep[3] = kh;
-                } else {
-                    uint32_t kn = 0;
-#pragma unroll
-                    for (int s2 = 0; s2 < 8; ++s2) kn |= ((mask >> s2) & 1u) ? 0u : 0xfu << (4 * s2);
-                    keep[0] = keep[1] = keep[2] = keep[3] = kn;
-                }
-                const u32x4 old = *dst;
-#pragma unroll
-                for (int k = 0; k < 4; ++k) wv[k] = (wv[k] & ~keep[k]) | (old[k] & keep[k]);
-            }
-            *dst = u32x4{wv[0], wv[1], wv[2], wv[3]};
-        }
+        write_value_tiles<kB8, D, ROWS>(codes, sm_codes, c0, pos, end, tid);
     }
 }
 
@@ -749,9 +758,17 @@ inline void launch_rows_d(int load, dim3 grid, hipStream_t st, const AppendArgs 
         hipLaunchKernelGGL((append_rows_kernel<FMT, IS_VALUE, D, kRowAny>), grid, dim3(256), 0, st, a);
 }
 
+// The MFMA-rotation form of the TurboMse append (append_turbo.hip); false when the case is not
+// one it takes (then the row-parallel encoder runs).
+bool turbo_mfma_launch(const cqkv_side *s, int32_t tokens, int32_t batch, hipStream_t st,
+                       const AppendArgs &a);
+
 template <int FMT>
 inline void launch_rows(const cqkv_side *s, int32_t tokens, int32_t batch, hipStream_t st,
                         const AppendArgs &a) {
+    if constexpr (FMT == CQKV_FMT_TURBO4) {
+        if (turbo_mfma_launch(s, tokens, batch, st, a)) return;
+    }
     const int rows = 256 / (s->head_dim / 32);
     const dim3 grid((unsigned)(((int64_t)tokens + 7 + rows - 1) / rows), s->kv_heads, batch);
     if constexpr (FMT == CQKV_FMT_TURBOPROD) {  // keys only (check_side refuses value sides)
