@@ -184,7 +184,7 @@ class CacheSide:
     seed: int = 0
     rotation: int = ROT_DEFAULT
     qjl: torch.Tensor | None = None  # TURBOPROD: the (D, D) f32 QJL matrix on the device
-    # TurboQuant width (TURBO4: TurboMse{bits} 1-4, TURBOPROD: TurboProd{bits} 2-4; 0 = 4)
+    # TurboQuant width (TURBO4: TurboMse{bits} 1-4, TURBOPROD: TurboProd{bits} 2-5; 0 = 4)
     bits: int = 0
 
     @staticmethod

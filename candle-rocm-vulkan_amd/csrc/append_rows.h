@@ -33,7 +33,7 @@ struct AppendArgs {
     float rot_scale;        // rotation: 1 / sqrt(D) in f32
     float bnd[16];          // TURBO4: the 15 codebook boundaries (+inf padded); TURBOPROD: 7
     int32_t turbo_sym;      // TURBO4: bnd[7] == 0 and bnd[14 - i] == -bnd[i] (a symmetric codebook)
-    float cent[8];          // TURBOPROD: the 3-bit centroids
+    float cent[16];         // TURBOPROD: the centroids of its (bits - 1)-bit codebook
     const float *qjl;       // TURBOPROD: device D x D QJL matrix S (row-major)
     int32_t pair_loads;     // elements 2l, 2l+1 of every row are one aligned 4 / 8-byte word
     int32_t row_loads;      // rows_block: kRowBF16 / kRowF16 / kRowF32 (16-byte loads) or kRowAny
@@ -390,12 +390,12 @@ __device__ inline void prod_qjl(const AppendArgs &a, const float (&x)[32], float
     constexpr int NB = D / 64;                            // 16-output blocks per wavefront
     constexpr int NC = D / 32;                            // 32-wide k chunks
     const int tid = threadIdx.x;
-    if (tid < 8) sm_cent[tid] = a.cent[tid];
+    if (tid < 16) sm_cent[tid] = a.cent[tid];
     __syncthreads();
     float rr = 0.0f, res[32];
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-        const uint32_t code = (cw[i / 8] >> (4 * (i % 8))) & 7u;
+        const uint32_t code = (cw[i / 8] >> (4 * (i % 8))) & 15u;
         res[i] = live ? x[i] * inv - sm_cent[code] : 0.0f;
         rr += res[i] * res[i];
     }
@@ -533,10 +533,10 @@ __device__ inline void rows_block(const AppendArgs &a, int h, int b, int bx) {
     constexpr bool kProd = FMT == CQKV_FMT_TURBOPROD;
     static_assert(!kProd || !IS_VALUE, "TurboProd is a key format");
     // TurboProd: the rows' scaled residuals (f16 hi rows, then lo rows) for the S r projection,
-    // and the 3-bit centroids
+    // and the centroids of its MSE codebook
     __shared__ __attribute__((aligned(16))) uint16_t
         sm_resid[kProd ? 2 * ROWS * (D + kProdResidStride) : 8];
-    __shared__ float sm_cent[8];
+    __shared__ float sm_cent[16];
 
     const int pos = a.positions ? a.positions[b] : a.position;
     if (pos < 0) return;

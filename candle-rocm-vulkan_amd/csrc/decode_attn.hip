@@ -173,16 +173,19 @@ static int decode_prepare(DecodeArgs &a, const char *who, const void *q, int32_t
     a.rot_scale = 1.0f / sqrtf((float)d);
     // kernel formats: TurboMse keys and values of different widths cannot share the 64 KB code
     // table, so the side with the narrower (at most 3-bit) codes takes a compact table of its own
+    // TurboProd{5} keys (4-bit MSE codes) decode their codes through the 64 KB table
     const int kb = turbo_code_bits(k), vb = turbo_code_bits(v);
-    a.kfmt = k->format;
+    a.kfmt = k->format == CQKV_FMT_TURBOPROD && kb == 4 ? kFmtProd4 : k->format;
     a.vfmt = v->format;
-    if (k->format == CQKV_FMT_TURBO4 && v->format == CQKV_FMT_TURBO4 && kb != vb) {
+    const bool k_tab = a.kfmt == CQKV_FMT_TURBO4 || a.kfmt == kFmtProd4;  // keys on the 64 KB table
+    if (k_tab && v->format == CQKV_FMT_TURBO4 && kb != vb) {
         if (kb <= 3) a.kfmt = kFmtTurboC;
         else a.vfmt = kFmtTurboC;
     }
     float bnd[16], cent[16];
-    if (a.kfmt == CQKV_FMT_TURBO4 || a.vfmt == CQKV_FMT_TURBO4) {  // the 64 KB table's codebook
-        if (turbo_codebook(d, a.kfmt == CQKV_FMT_TURBO4 ? kb : vb, cent, bnd) != 0)
+    const bool k_tab2 = a.kfmt == CQKV_FMT_TURBO4 || a.kfmt == kFmtProd4;
+    if (k_tab2 || a.vfmt == CQKV_FMT_TURBO4) {  // the 64 KB table's codebook
+        if (turbo_codebook(d, k_tab2 ? kb : vb, cent, bnd) != 0)
             return fail(CQKV_ERR_ARG, "%s: turbo codebook D=%d", who, d);
         for (int i = 0; i < 16; ++i) a.cent[i] = cent[i];
     }
@@ -213,6 +216,7 @@ static hipError_t decode_launch(const DecodeArgs &a, int kf, int vf, int d, hipS
     case CQKV_FMT_NVFP4: decode_launch_k3(vf, d, grid, st, a); break;
     case CQKV_FMT_TURBOPROD: decode_launch_k1(vf, d, grid, st, a); break;
     case kFmtTurboC: decode_launch_k6(vf, d, grid, st, a); break;
+    case kFmtProd4: decode_launch_k7(vf, d, grid, st, a); break;
     default: decode_launch_k0(vf, d, grid, st, a); break;
     }
     hipError_t e = hipGetLastError();

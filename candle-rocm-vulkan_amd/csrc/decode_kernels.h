@@ -115,9 +115,15 @@ __device__ inline bool sign_bit(const uint32_t *bits, int j) { return (bits[j >>
 // TurboMse codebook occupies the 64 KB code table (TurboKvCache::with_formats(TurboMse{4},
 // TurboMse{3}, ..)).
 constexpr int kFmtTurboC = 6;
+// Kernel-internal format id: TurboProd{5} keys, whose 4-bit MSE codes go through the 64 KB code
+// table (the TurboMse{4} codebook of the head dim) while the QJL part is TurboProd's.
+constexpr int kFmtProd4 = 7;
 // TurboMse codes (either table).
 template <int FMT>
 constexpr bool turbo_mse() { return FMT == CQKV_FMT_TURBO4 || FMT == kFmtTurboC; }
+// TurboProd keys (either code table).
+template <int FMT>
+constexpr bool is_prod() { return FMT == CQKV_FMT_TURBOPROD || FMT == kFmtProd4; }
 // Codes of at most 3 bits through the compact byte-indexed table.
 template <int FMT>
 constexpr bool compact_tab() { return FMT == CQKV_FMT_TURBOPROD || FMT == kFmtTurboC; }
@@ -241,9 +247,9 @@ __device__ inline void load_tile(Tile<KF, VF, D> &r, int tile, bool live, int la
         }
     }
     const uint32_t kl = t0 + (lane & 31);
-    if constexpr (turbo_mse<KF>() || KF == CQKV_FMT_TURBOPROD)
+    if constexpr (turbo_mse<KF>() || is_prod<KF>())
         load_scales8<4>(r.ks8, ksr, t0 + 8 * g, oob);
-    if constexpr (KF == CQKV_FMT_TURBOPROD) {
+    if constexpr (is_prod<KF>()) {
         // the scales plane: norms, |r| (at cap * 4), sign bits (at cap * 8, D / 8 per key)
         const uint32_t cap = ktok_off;  // load_tile's caller passes the capacity here
         load_scales8<4>(r.kr1, ksr, cap + t0 + 8 * g, oob);
@@ -290,7 +296,7 @@ __device__ inline uint32_t fp4x2_to_bf16x2(uint32_t w, int byte_sel, float scale
 // MFMA operand type: bf16 for FP8 / MXFP4 (their codes decode exactly), f16 for TurboQuant
 // (codebook values, rotated queries: 11 significant bits instead of 8).
 template <int FMT>
-using op_t = typename std::conditional<turbo_mse<FMT>() || FMT == CQKV_FMT_TURBOPROD, f16x8,
+using op_t = typename std::conditional<turbo_mse<FMT>() || is_prod<FMT>(), f16x8,
                                       bf16x8>::type;
 
 typedef __attribute__((address_space(3))) const uint32_t lds_u32;
@@ -460,7 +466,7 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
         }
         s0 = mfma16x16x32(k0, qhi[j], s0);
         s1 = mfma16x16x32(k1, qhi[j], s1);
-        if constexpr (KF == CQKV_FMT_TURBOPROD) {  // byte j of the lane key's sign bits
+        if constexpr (is_prod<KF>()) {  // byte j of the lane key's sign bits
             z0 = mfma16x16x32(signs_f16x8(cur.ksg[0], j), qsop[j], z0);
             z1 = mfma16x16x32(signs_f16x8(cur.ksg[1], j), qsop[j], z1);
         }
@@ -471,7 +477,7 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
     }
     float x[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
     const int kbase = t0 + 8 * g;  // x[e] is key kbase + e
-    if constexpr (KF == CQKV_FMT_TURBOPROD) {
+    if constexpr (is_prod<KF>()) {
         // r0 (q . c + r1 sqrt(pi / 2) / D (S q) . z) (turbo_quant_impl.h:268-276); zk holds
         // -(S q) . z (the operands are -1 where the sign bit is set)
         const float zk[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
@@ -648,7 +654,8 @@ __global__ __launch_bounds__(WAVES * 64)
 __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_kernel(DecodeArgs a) {
     constexpr int NCH = D / 32;
     constexpr int NT = WAVES * 64;
-    constexpr bool kTurbo = KF == CQKV_FMT_TURBO4 || VF == CQKV_FMT_TURBO4;  // the code table
+    constexpr bool kTurbo =
+        KF == CQKV_FMT_TURBO4 || KF == kFmtProd4 || VF == CQKV_FMT_TURBO4;  // the code table
     // the per-wavefront outputs (and, before the tile loop, the queries) share their LDS with the
     // TurboQuant code table (64 KB-aligned, see turbo_pair), which is live only during the tile
     // loop
@@ -657,7 +664,7 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
     float(*sm_o)[16][D] = (float(*)[16][D])sm_buf;
     uint32_t *sm_tab = (uint32_t *)sm_buf;
     __shared__ float sm_m[WAVES][16], sm_l[WAVES][16];
-    constexpr bool kProd = KF == CQKV_FMT_TURBOPROD;
+    constexpr bool kProd = is_prod<KF>();
     // compact code-pair tables (120 code bytes x 32 lanes) of keys (TurboProd, kFmtTurboC) and of
     // kFmtTurboC values
     __shared__ __attribute__((aligned(16384))) uint32_t sm_ktab[compact_tab<KF>() ? kProdTabWords : 1];
@@ -910,8 +917,9 @@ inline void launch_decode_k(int vf, int d, dim3 grid, hipStream_t st, const Deco
         case CQKV_FMT_MXFP4: launch_decode_kv<KF, CQKV_FMT_MXFP4>(d, grid, st, a); break;
         case CQKV_FMT_MXFP8: launch_decode_kv<KF, CQKV_FMT_MXFP8>(d, grid, st, a); break;
         case CQKV_FMT_NVFP4: launch_decode_kv<KF, CQKV_FMT_NVFP4>(d, grid, st, a); break;
-        case kFmtTurboC:  // compact values come with TURBO4-table keys only
-            if constexpr (KF == CQKV_FMT_TURBO4) launch_decode_kv<KF, kFmtTurboC>(d, grid, st, a);
+        case kFmtTurboC:  // compact values come with 64 KB-table keys only
+            if constexpr (KF == CQKV_FMT_TURBO4 || KF == kFmtProd4)
+                launch_decode_kv<KF, kFmtTurboC>(d, grid, st, a);
             break;
         default: launch_decode_kv<KF, CQKV_FMT_TURBO4>(d, grid, st, a); break;
         }
@@ -928,5 +936,6 @@ CQKV_DECODE_LAUNCHER(3)
 CQKV_DECODE_LAUNCHER(4)
 CQKV_DECODE_LAUNCHER(5)
 CQKV_DECODE_LAUNCHER(6)
+CQKV_DECODE_LAUNCHER(7)
 
 }  // namespace cqkv

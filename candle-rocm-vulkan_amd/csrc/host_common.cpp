@@ -44,8 +44,8 @@ int check_side(const cqkv_side *s, const char *what) {
         return fail(CQKV_ERR_ARG, "%s: rotation %d (default, none or Hadamard)", what, s->rotation);
     if (s->format == CQKV_FMT_TURBO4 && (s->bits < 0 || s->bits > 4))
         return fail(CQKV_ERR_ARG, "%s: TurboMse bits %d (1-4, 0: 4)", what, s->bits);
-    if (s->format == CQKV_FMT_TURBOPROD && (s->bits < 0 || s->bits == 1 || s->bits > 4))
-        return fail(CQKV_ERR_ARG, "%s: TurboProd bits %d (2-4, 0: 4)", what, s->bits);
+    if (s->format == CQKV_FMT_TURBOPROD && (s->bits < 0 || s->bits == 1 || s->bits > 5))
+        return fail(CQKV_ERR_ARG, "%s: TurboProd bits %d (2-5, 0: 4)", what, s->bits);
     if (!is_turbo(s->format) && s->bits != 0)
         return fail(CQKV_ERR_ARG, "%s: bits %d given for a format without a width (0)", what,
                     s->bits);
@@ -204,7 +204,7 @@ int32_t cqkv_reference_row_words(int32_t format, int32_t bits, int32_t head_dim)
     if (cqkv::is_turbo(format)) {  // formats.rs:226-240: b-bit (prod: b - 1) codes, prod signs
         const int b = bits ? bits : 4;
         if (format == CQKV_FMT_TURBO4 && (b < 1 || b > 4)) return 0;
-        if (format == CQKV_FMT_TURBOPROD && (b < 2 || b > 4)) return 0;
+        if (format == CQKV_FMT_TURBOPROD && (b < 2 || b > 5)) return 0;
         const int code = format == CQKV_FMT_TURBOPROD ? b - 1 : b;
         return (head_dim * code + 31) / 32 +
                (format == CQKV_FMT_TURBOPROD ? (head_dim + 31) / 32 : 0) + 2;

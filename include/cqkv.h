@@ -89,7 +89,7 @@ enum {
 
 /* Cache formats: the reference's kernel mode ids (candle-core/src/accel/formats.rs:41-48).
  * TURBO4 = TurboQuant MSE, Hadamard rotation (QuantFormat::TurboMse{bits}, cqkv_side.bits 1-4,
- * default 4); TURBOPROD = TurboQuant prod (QuantFormat::TurboProd{bits}, bits 2-4, default 4;
+ * default 4); TURBOPROD = TurboQuant prod (QuantFormat::TurboProd{bits}, bits 2-5, default 4;
  * keys only): (bits - 1)-bit MSE codes of the rotated unit row, plus the sign bits of S r (r =
  * the residual of the unit row to its centroids, S = cqkv_qjl_matrix(D, seed)) and |r| - an
  * unbiased inner-product estimate (RowCodec::quantize_row, candle-core/src/accel/turbo.rs:
@@ -137,7 +137,7 @@ typedef struct cqkv_side {
     int32_t capacity;  /* tokens per plane, a multiple of 32 */
     int32_t rotation;  /* CQKV_ROT_* */
     int32_t bits;      /* TurboQuant width: TURBO4 = TurboMse{bits} 1-4, TURBOPROD = TurboProd{bits}
-                          2-4 (QuantFormat bits, formats.rs:22-29); 0 = 4. The codes (bits, or
+                          2-5 (QuantFormat bits, formats.rs:22-29); 0 = 4. The codes (bits, or
                           bits - 1 for TURBOPROD) are stored as nibbles at every width. 0 for the
                           other formats. */
     int32_t reserved;  /* 0 */

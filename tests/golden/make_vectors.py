@@ -244,6 +244,51 @@ def widths_case():
     np.savez_compressed(os.path.join(HERE, "ref_decode_widths.npz"), **out)
 
 
+def prod5_case():
+    """TurboProd{5} (4-bit MSE codes plus the QJL sketch, QuantFormat::TurboProd { bits: 5 },
+    candle-core/src/accel/formats.rs:26-29): rows through the reference kernels at D 128 and 64,
+    and the reference's fused decode over TurboProd{5} keys with TurboMse{4} and TurboMse{3}
+    values (the inputs of widths_case)."""
+    out = {}
+    for d, seed in ((128, 26), (64, 27)):
+        y = O.normal(seed, (33, d)) * np.float32(2.0)
+        y[1, :] = 0.0
+        rows, _ = prod_rows(y, O.qjl_matrix(d, 42), 5)
+        out[f"x_d{d}"], out[f"rows_d{d}"] = y, rows
+    B, Hq, Hkv, D, Lq, Lk = 2, 8, 2, 128, 2, 300
+    q = O.round_bf16(O.normal(801, (B, Hq, Lq, D)))
+    k = O.round_bf16(O.normal(802, (B, Hkv, Lk, D))).astype(np.float32)
+    v = O.round_bf16(O.normal(803, (B, Hkv, Lk, D))).astype(np.float32)
+    pk = O.rotation_matrix(D, O.ROT_HADAMARD, 42)
+    pv = O.rotation_matrix(D, O.ROT_HADAMARD, 44)
+    kx = O.rotate_rows(pk, k.reshape(-1, D))
+    vx = O.rotate_rows(pv, v.reshape(-1, D))
+    qr = O.rotate_rows(pk, q.reshape(-1, D)).reshape(q.shape)
+    scale = np.float32(1.0 / np.sqrt(D))
+    out["scale"] = scale
+    s = O.qjl_matrix(D, 42)
+    lk_ = O.row_layout(O.TURBO_PROD, 5, D)
+    ck, bk = O.lloyd_max(D, lk_.code_bits)
+    kd, _ = prod_rows(kx, s, 5)
+    qs = (qr.reshape(-1, D).astype(np.float64) @ s.astype(np.float64).T).astype(np.float32)
+    qx = np.concatenate([qr, qs.reshape(q.shape)], -1).astype(np.float32)
+    kd = kd.reshape(B, Hkv, Lk, -1)
+    out["kd"] = kd
+    for vbits in (4, 3):
+        lv = O.row_layout(O.TURBO_MSE, vbits, D)
+        cv, bv = O.lloyd_max(D, vbits)
+        vd = H.tq_quant(vx.astype(np.float32), O.TURBO_MSE, lv.code_bits, lv.code_words,
+                        lv.aux_words, lv.row_words, H.tq_tab(cv, bv)).reshape(B, Hkv, Lk, -1)
+        tab64 = np.concatenate([H.tq_tab(ck, bk), H.tq_tab(cv, bv)]).astype(np.float32)
+        k_side = (O.TURBO_PROD, lk_.code_bits, lk_.code_words, lk_.code_words + lk_.aux_words)
+        v_side = (O.TURBO_MSE, lv.code_bits, lv.code_words, lv.code_words + lv.aux_words)
+        o = H.tq_attn(qx, kd, vd, k_side, v_side, tab64, float(scale), splits=3, group=4)
+        o = (o.reshape(-1, D) @ pv).reshape(o.shape).astype(np.float32)
+        out[f"vd_mse{vbits}"], out[f"out_mse{vbits}"] = vd, o
+        print("decode prod5 mse", vbits, o.shape)
+    np.savez_compressed(os.path.join(HERE, "ref_prod5.npz"), **out)
+
+
 def combine_case():
     splits, rows, d = 5, 7, 32
     po = O.normal(201, (splits, rows, d))
@@ -260,6 +305,9 @@ if __name__ == "__main__":
         sys.exit("oracle/_ref/accel_host_test missing: run `make -C oracle ref` first")
     if sys.argv[1:] == ["widths"]:  # only the TurboQuant widths fixtures
         widths_case()
+        sys.exit(0)
+    if sys.argv[1:] == ["prod5"]:  # only the TurboProd{5} fixture
+        prod5_case()
         sys.exit(0)
     quant_case("fp8_d128", O.FP8, 0, 128, 37, 11)
     quant_case("fp8_d80", O.FP8, 0, 80, 19, 12)
@@ -278,4 +326,5 @@ if __name__ == "__main__":
     attn_format_case("mxfp8", O.MXFP8, 0)
     prod_case()
     widths_case()
+    prod5_case()
     combine_case()

@@ -61,6 +61,8 @@ def test_reference_row_words_known_answers(cq):
     assert cq.reference_row_words(cq.TURBOPROD, 64, 2) == 2 + 2 + 2
     assert cq.reference_row_words(cq.TURBO4, 128, 5) == 0
     assert cq.reference_row_words(cq.TURBOPROD, 128, 1) == 0
+    assert cq.reference_row_words(cq.TURBOPROD, 128, 5) == 16 + 4 + 2  # 4-bit MSE codes
+    assert cq.reference_row_words(cq.TURBOPROD, 128, 6) == 0
     assert cq.reference_row_words(cq.FP8, 128, 4) == 0
     assert cq.reference_row_words(cq.MXFP4, 64) == 8 + 1 + 2
     assert cq.reference_row_words(cq.NVFP4, 128) == 16 + 2 + 2

@@ -1,5 +1,5 @@
 """GPU parity of the TurboQuant widths other than 4: QuantFormat::TurboMse{1, 2, 3} on keys and
-values and TurboProd{2, 3} on keys (candle-core/src/accel/formats.rs:22-29, code widths of
+values and TurboProd{2, 3, 5} on keys (candle-core/src/accel/formats.rs:22-29, code widths of
 formats.rs:138-160; Lloyd-Max codebooks of turbo.rs:58-146 at those widths), cqkv_side.bits.
 
 The cache keeps the codes as nibbles at every width; rows are compared in the reference layout
@@ -33,7 +33,8 @@ def export_np(cq, side, tokens, position=0):
 @pytest.mark.parametrize("fmt,bits,is_value", [(TURBO, 3, False), (TURBO, 3, True),
                                                (TURBO, 2, False), (TURBO, 2, True),
                                                (TURBO, 1, False), (TURBO, 1, True),
-                                               (PROD, 3, False), (PROD, 2, False)])
+                                               (PROD, 3, False), (PROD, 2, False),
+                                               (PROD, 5, False)])
 @pytest.mark.parametrize("d", [64, 128])
 def test_width_append_rows(cq, dev, fmt, bits, is_value, d):
     b, h, t, pos = 2, 3, 77, 5
@@ -84,9 +85,11 @@ def test_width_decode_vs_reference_fused_kernel(cq, dev, name, kfmt, kbits, vbit
 
 # (key format, key bits, value format, value bits): equal and different TurboMse widths (the
 # narrower side on its compact table), TurboMse with the other formats, TurboProd widths
+# (TurboProd{5}: 4-bit MSE codes on the 64 KB table, values sharing it or on their own)
 PAIRS = [(TURBO, 4, TURBO, 3), (TURBO, 2, TURBO, 4), (TURBO, 3, TURBO, 3), (TURBO, 1, FP8, 0),
          (FP8, 0, TURBO, 2), (MXFP4, 0, TURBO, 1), (PROD, 3, TURBO, 2), (PROD, 2, MXFP4, 0),
-         (PROD, 3, TURBO, 4)]
+         (PROD, 3, TURBO, 4), (PROD, 5, TURBO, 4), (PROD, 5, TURBO, 2), (PROD, 5, FP8, 0),
+         (PROD, 5, MXFP4, 0), (PROD, 5, NVFP4, 0)]
 
 
 @pytest.mark.parametrize("kf,kb,vf,vb", PAIRS)
@@ -150,12 +153,47 @@ def test_width_paged_equals_dense_and_growth(cq, dev):
         np.testing.assert_array_equal(export_np(cq, gs, n1 + n2), export_np(cq, ds, n1 + n2))
 
 
+@pytest.mark.parametrize("d", [128, 64])
+def test_prod5_rows_import_export_roundtrip(cq, dev, d):
+    """TurboProd{5} rows of the reference kernels in, the same rows out, bit for bit."""
+    rows = np.load(os.path.join(GOLD, "ref_prod5.npz"))[f"rows_d{d}"]
+    n = rows.shape[0]
+    side = cq.CacheSide.empty(PROD, False, 1, 1, d, 64, dev, seed=42, bits=5)
+    cq.rows_import(side, torch.from_numpy(rows.view(np.int32)).reshape(1, 1, n, -1).to(dev), 3)
+    np.testing.assert_array_equal(export_np(cq, side, n, 3).reshape(n, -1), rows)
+
+
+@pytest.mark.parametrize("vbits", [4, 3])
+@pytest.mark.parametrize("splits", [1, 3, 0])
+def test_prod5_decode_vs_reference_fused_kernel(cq, dev, vbits, splits):
+    """The reference's TurboProd{5} rows (imported) with TurboMse{4} values (sharing the 64 KB
+    code table) or TurboMse{3} values (on their compact table), decoded by the HIP kernel,
+    against the reference's fused kernel over them."""
+    g = np.load(os.path.join(GOLD, "ref_prod5.npz"))
+    q, _, _ = widths_inputs()
+    b, hq, lq, d = q.shape
+    kd, vd = g["kd"], g[f"vd_mse{vbits}"]
+    hkv, lk = kd.shape[1], kd.shape[2]
+    ks = cq.CacheSide.empty(PROD, False, b, hkv, d, 320, dev, seed=42, bits=5)
+    vs = cq.CacheSide.empty(TURBO, True, b, hkv, d, 320, dev, seed=44, bits=vbits)
+    cq.rows_import(ks, torch.from_numpy(kd.view(np.int32)).to(dev))
+    cq.rows_import(vs, torch.from_numpy(vd.view(np.int32)).to(dev))
+    out = torch.empty((b, hq, lq, d), dtype=torch.float32, device=dev)
+    got = cq.decode_attention(torch.from_numpy(q).to(torch.bfloat16).to(dev), ks, vs, lk,
+                              float(g["scale"]), splits=splits, out=out).cpu().numpy()
+    err = np.abs(got - g[f"out_mse{vbits}"])
+    assert err.max() <= 5e-3 and err.mean() <= 2e-3, (err.max(), err.mean())
+
+
 def test_width_arguments_refused(cq, dev):
     with pytest.raises(cq.CqkvError):  # TurboMse 5 bits
         side = cq.CacheSide.empty(TURBO, False, 1, 1, 128, 32, dev, bits=5)
         cq.quant_append(side, torch.zeros(1, 1, 4, 128, dtype=torch.bfloat16, device=dev))
     with pytest.raises(cq.CqkvError):  # TurboProd 1 bit
         side = cq.CacheSide.empty(PROD, False, 1, 1, 128, 32, dev, seed=42, bits=1)
+        cq.quant_append(side, torch.zeros(1, 1, 4, 128, dtype=torch.bfloat16, device=dev))
+    with pytest.raises(cq.CqkvError):  # TurboProd 6 bits
+        side = cq.CacheSide.empty(PROD, False, 1, 1, 128, 32, dev, seed=42, bits=6)
         cq.quant_append(side, torch.zeros(1, 1, 4, 128, dtype=torch.bfloat16, device=dev))
     with pytest.raises(cq.CqkvError):  # a width for a format without one
         side = cq.CacheSide.empty(FP8, False, 1, 1, 128, 32, dev, bits=4)

@@ -322,6 +322,53 @@ def test_prod_width_rows_match_reference_kernels(bits, d):
     assert (ms != rs).sum() <= max(1, ms.size // 1000)
 
 
+@pytest.mark.parametrize("d", [128, 64])
+def test_prod5_rows_match_reference_kernels(d):
+    """TurboProd{5} rows (4-bit MSE codes, QJL signs, |r|) against the reference's pipeline:
+    codes equal, norms and |r| to 1e-5, signs but for <= 0.1 %."""
+    g = gold("ref_prod5")
+    y, want = g[f"x_d{d}"], g[f"rows_d{d}"]
+    mine = O.quantize_rows_qjl(5, y, O.qjl_matrix(d, 42))
+    l = O.row_layout(O.TURBO_PROD, 5, d)
+    cw, aw = l.code_words, l.aux_words
+    assert l.code_bits == 4
+    np.testing.assert_array_equal(turbo_codes(mine, 4, d), turbo_codes(want, 4, d))
+    for w in (cw + aw, cw + aw + 1):
+        np.testing.assert_allclose(mine[..., w].view(np.float32), want[..., w].view(np.float32),
+                                   rtol=1e-5)
+    ms = np.unpackbits(mine[..., cw:cw + aw].copy().view(np.uint8))
+    rs = np.unpackbits(want[..., cw:cw + aw].copy().view(np.uint8))
+    assert (ms != rs).sum() <= max(1, ms.size // 1000)
+
+
+@pytest.mark.parametrize("vbits", [4, 3])
+def test_prod5_decode_vs_reference_fused_kernel(vbits):
+    """The reference's fused decode over TurboProd{5} keys and TurboMse{vbits} values equals
+    float64 attention over the oracle's dequantized rows to 1e-5; the reference CPU path stays
+    within 2e-2."""
+    g = gold("ref_prod5")
+    kd, vd, want = g["kd"], g[f"vd_mse{vbits}"], g[f"out_mse{vbits}"]
+    q, _, _ = widths_inputs()
+    B, Hq, Lq, D = q.shape
+    pk = O.rotation_matrix(D, O.ROT_HADAMARD, 42).astype(np.float64)
+    pv = O.rotation_matrix(D, O.ROT_HADAMARD, 44).astype(np.float64)
+    s = O.qjl_matrix(D, 42)
+    kx = O.dequantize_rows_qjl(5, D, kd, s).astype(np.float64) @ pk
+    vx = O.dequantize_rows(O.TURBO_MSE, vbits, D, vd).astype(np.float64) @ pv
+    scale = float(g["scale"])
+    ex = np.zeros((B, Hq, Lq, D))
+    for b in range(B):
+        for h in range(Hq):
+            sc = q[b, h].astype(np.float64) @ kx[b, h // 4].T * scale
+            p = np.exp(sc - sc.max(1, keepdims=True))
+            ex[b, h] = p @ vx[b, h // 4] / p.sum(1, keepdims=True)
+    assert np.abs(ex - want).max() < 1e-5
+    cpu = O.cache_attention(O.f32_to_bf16_bits(q), kd, vd, (O.TURBO_PROD, 5),
+                            (O.TURBO_MSE, vbits), pk.astype(np.float32), pv.astype(np.float32),
+                            kd.shape[2], scale, threads=8, qjl_k=s)
+    assert np.abs(O.round_bf16(cpu) - want).max() < 2e-2
+
+
 def widths_inputs():
     """The inputs of the ref_decode_widths fixture (tests/golden/make_vectors.py widths_case)."""
     B, Hq, Hkv, D, Lq, Lk = 2, 8, 2, 128, 2, 300
