@@ -127,12 +127,15 @@ static int decode_prepare(DecodeArgs &a, const char *who, const void *q, int32_t
         return fail(CQKV_ERR_ARG, "%s: expected a key side and a value side", who);
     if (k->head_dim != v->head_dim || k->kv_heads != v->kv_heads)
         return fail(CQKV_ERR_ARG, "%s: key / value sides differ in D or heads", who);
-    if (!q || !out || !q_strides || !out_strides)
+    // no query rows (batch or q_len 0): an empty output, as the reference's (rocm_backend/
+    // accel.rs:481); q / out may then be null and the callers launch nothing
+    const bool no_rows = batch == 0 || q_len == 0;
+    if ((!no_rows && (!q || !out)) || !q_strides || !out_strides)
         return fail(CQKV_ERR_ARG, "%s: null q / out / strides", who);
     if (q_dtype < CQKV_BF16 || q_dtype > CQKV_F32 || out_dtype < CQKV_BF16 || out_dtype > CQKV_F32)
         return fail(CQKV_ERR_ARG, "%s: dtypes q %d out %d", who, q_dtype, out_dtype);
     const int hkv = k->kv_heads, d = k->head_dim;
-    if (batch <= 0 || q_heads <= 0 || q_len <= 0 || q_heads % hkv != 0)
+    if (batch < 0 || q_heads <= 0 || q_len < 0 || q_heads % hkv != 0)
         return fail(CQKV_ERR_ARG, "%s: batch %d q_heads %d q_len %d kv_heads %d", who, batch,
                     q_heads, q_len, hkv);
     const int group = q_heads / hkv;
@@ -297,6 +300,7 @@ static int decode_dense(const char *who, const void *q, int32_t q_dtype,
         return fail(CQKV_ERR_ARG, "%s: kv_len %d outside [0, capacity %d]", who, kv_len,
                     k->capacity);
     if (splits < 0) return fail(CQKV_ERR_ARG, "%s: splits %d", who, splits);
+    if (batch == 0 || q_len == 0) return CQKV_OK;
     const int hkv = k->kv_heads, d = k->head_dim;
 
     const int tiles = max(1, tiles_of(kv_len));
@@ -548,6 +552,7 @@ extern "C" int cqkv_decode_attention_paged(const void *q, int32_t q_dtype,
                                 q_heads, q_len, softmax_scale, window_left, window_right, out,
                                 out_dtype, out_strides))
         return rc;
+    if (batch == 0 || q_len == 0) return CQKV_OK;
     std::vector<PagedSeg> segs;
     const int nseg = paged_segments(blocks, n_blocks, batch, &segs);
     int64_t total = 0;

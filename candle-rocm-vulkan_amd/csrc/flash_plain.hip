@@ -282,10 +282,13 @@ extern "C" int cqkv_flash_attn_blocks(const void *q, const int64_t q_strides[3],
                                       size_t workspace_bytes, cqkv_stream_t stream) {
     clear_error();
     static const char *who = "cqkv_flash_attn_blocks";
-    if (!q || !q_strides || !out || !out_strides || !blocks)
+    // no query rows (batch or q_len 0): an empty output once the blocks pass their checks, as
+    // the reference's (rocm_backend/accel.rs:197); q / out may then be null
+    const bool no_rows = batch == 0 || q_len == 0;
+    if ((!no_rows && (!q || !out)) || !q_strides || !out_strides || !blocks)
         return fail(CQKV_ERR_ARG, "%s: null q / out / strides / blocks", who);
     if (n_blocks <= 0) return fail(CQKV_ERR_ARG, "%s: no blocks", who);
-    if (batch <= 0 || q_heads <= 0 || q_len <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0)
+    if (batch < 0 || q_heads <= 0 || q_len < 0 || kv_heads <= 0 || q_heads % kv_heads != 0)
         return fail(CQKV_ERR_ARG, "%s: batch %d q_len %d heads %d / %d", who, batch, q_len,
                     q_heads, kv_heads);
     if (!(softcap >= 0.0f) || softcap == __builtin_inff())
@@ -316,6 +319,7 @@ extern "C" int cqkv_flash_attn_blocks(const void *q, const int64_t q_strides[3],
         return fail(CQKV_ERR_ARG, "%s: K / V row strides must be whole %d-element chunks", who,
                     (int)ce);
     if (int rc = fa_plain_check(who, dtype, kv_dtype, head_dim, k_row, v_row, total)) return rc;
+    if (no_rows) return CQKV_OK;
     const int dmax = fa_dmax(head_dim);
     const int cols = (int)(((int64_t)q_len * (q_heads / kv_heads) + 15) / 16);
     FaPagedPlan p;

@@ -153,6 +153,7 @@ static size_t fp8_stage_bytes(int32_t batch, int32_t kv_len, int32_t kv_heads, i
 extern "C" size_t cqkv_flash_attn_fp8_workspace_bytes(int32_t dtype, int32_t batch, int32_t q_len,
                                                       int32_t kv_len, int32_t q_heads,
                                                       int32_t kv_heads, int32_t head_dim) {
+    // (no query rows or no keys need nothing: see cqkv_flash_attn_fp8)
     if ((dtype != CQKV_BF16 && dtype != CQKV_F16 && dtype != CQKV_F32) || batch <= 0 ||
         q_len <= 0 || kv_len <= 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0 ||
         head_dim <= 0 || head_dim > 256 || head_dim % 8 != 0)
@@ -174,17 +175,23 @@ extern "C" int cqkv_flash_attn_fp8(const void *q, const int64_t q_strides[3], co
                                    void *workspace, size_t workspace_bytes, cqkv_stream_t stream) {
     clear_error();
     static const char *who = "cqkv_flash_attn_fp8";
-    if (!q || !k8 || !v8 || !out || !q_strides || !k_strides || !v_strides || !out_strides)
-        return fail(CQKV_ERR_ARG, "%s: null tensor or strides", who);
+    if (!q_strides || !k_strides || !v_strides || !out_strides)
+        return fail(CQKV_ERR_ARG, "%s: null strides", who);
     if (dtype != CQKV_BF16 && dtype != CQKV_F16 && dtype != CQKV_F32)
         return fail(CQKV_ERR_ARG, "%s: dtype %d (bf16, f16 or f32 q / out)", who, dtype);
     if (head_dim <= 0 || head_dim > 256 || head_dim % 8 != 0)
         return fail(CQKV_ERR_ARG, "%s: head_dim %d (a multiple of 8 up to 256)", who, head_dim);
     // the attention's own limits, checked before the staging pass is launched
-    if (batch <= 0 || q_len <= 0 || kv_len <= 0 || kv_heads <= 0 || q_heads <= 0 ||
+    if (batch < 0 || q_len < 0 || kv_len < 0 || kv_heads <= 0 || q_heads <= 0 ||
         q_heads % kv_heads != 0 || kv_len > (1 << 23))
         return fail(CQKV_ERR_ARG, "%s: batch %d q_len %d kv_len %d heads %d / %d", who, batch,
                     q_len, kv_len, q_heads, kv_heads);
+    // empty inputs as the reference's: no query rows give an empty output, no keys zero rows;
+    // empty tensors may have null data
+    const bool no_rows = batch == 0 || q_len == 0;
+    if (no_rows) return CQKV_OK;
+    if (!q || !out || (kv_len > 0 && (!k8 || !v8)))
+        return fail(CQKV_ERR_ARG, "%s: null tensor", who);
     if (!(k_descale == k_descale) || !(v_descale == v_descale))
         return fail(CQKV_ERR_ARG, "%s: NaN descale", who);
     for (int i = 0; i < 3; ++i)
@@ -192,6 +199,15 @@ extern "C" int cqkv_flash_attn_fp8(const void *q, const int64_t q_strides[3], co
             return fail(CQKV_ERR_ARG, "%s: K / V strides must be multiples of 8 bytes", who);
     if ((uintptr_t)k8 % 8 != 0 || (uintptr_t)v8 % 8 != 0)
         return fail(CQKV_ERR_ARG, "%s: K / V must be 8-byte aligned", who);
+    if (kv_len == 0) {
+        // zero rows from the plain kernel of the query dtype (no K / V is read)
+        const int64_t ss[3] = {0, head_dim, 0};
+        return flash_attn_impl(q, q_strides, nullptr, ss, nullptr, ss, out, out_strides, dtype,
+                               dtype, batch, q_len, 0, q_heads, kv_heads, head_dim, softmax_scale,
+                               window_left, window_right, 0.0f, nullptr, 0, nullptr, nullptr, 0, 0,
+                               nullptr, nullptr, 0, nullptr, 0, stream, 1.0f, nullptr, 1.0f,
+                               nullptr);
+    }
     if (dtype == CQKV_F32) {
         // the f32-query kernel reads the E4M3 codes and widens them exactly, with k_descale in the
         // scores' scale and v_descale in the output, as the reference's fa_row_f32_fp8 does

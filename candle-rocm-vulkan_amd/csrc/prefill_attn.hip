@@ -855,14 +855,15 @@ static size_t pf_vt_bytes(int32_t batch, int32_t kv_len, int32_t kv_heads) {
 
 size_t flash_attn_workspace(int32_t dtype, int32_t batch, int32_t q_len, int32_t kv_len,
                             int32_t q_heads, int32_t kv_heads, int32_t head_dim, bool varlen) {
-    if (batch <= 0 || q_len <= 0 || kv_len <= 0 || q_heads <= 0 || kv_heads <= 0 ||
+    // (no query rows need nothing; no keys run the plain kernel, one split)
+    if (batch <= 0 || q_len <= 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0 ||
         q_heads % kv_heads != 0 || head_dim <= 0 || head_dim > 256)
         return 0;
     const size_t plain =
         fa_plain_workspace_bytes(batch, q_len, kv_len, q_heads, kv_heads, head_dim, varlen);
     // a call of the MFMA prefill's shape whose q / out rows are not aligned for it runs the
     // plain kernel: size for either
-    if (pf_fast_path(dtype, head_dim, q_len))
+    if (kv_len > 0 && pf_fast_path(dtype, head_dim, q_len))
         return std::max(pf_vt_bytes(batch, kv_len, kv_heads), plain);
     return plain;
 }
@@ -878,8 +879,17 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
                     const cqkv_side *k_cache, const cqkv_side *v_cache, int32_t position,
                     void *workspace, size_t workspace_bytes, cqkv_stream_t stream, float q_mul,
                     const float *q_mul_dev, float o_mul, const float *o_mul_dev) {
-    if (!q || !k || !v || !out || !q_strides || !k_strides || !v_strides || !out_strides)
-        return fail(CQKV_ERR_ARG, "cqkv_flash_attn: null tensor or strides");
+    // Empty inputs as the reference: no output rows (batch or q_len 0) give an empty output
+    // (rocm_backend/accel.rs:87) - only a cache append of the K / V rows remains; no keys
+    // (kv_len 0) give zero rows (every key range is empty). Empty tensors may have null data.
+    if (!q_strides || !k_strides || !v_strides || !out_strides)
+        return fail(CQKV_ERR_ARG, "cqkv_flash_attn: null strides");
+    if (batch < 0 || q_len < 0 || kv_len < 0)
+        return fail(CQKV_ERR_ARG, "cqkv_flash_attn: batch %d q_len %d kv_len %d", batch, q_len,
+                    kv_len);
+    const bool no_rows = batch == 0 || q_len == 0, no_keys = batch == 0 || kv_len == 0;
+    if ((!no_rows && (!q || !out)) || (!no_keys && (!k || !v)))
+        return fail(CQKV_ERR_ARG, "cqkv_flash_attn: null tensor");
     // 16-byte row loads of K / V in both kernels, of q in the MFMA prefill (which also stores
     // 8-byte pieces of out rows); a batch stride is unused with variable-length batches
     const bool vl = cu_seqlens_q != nullptr;
@@ -888,19 +898,19 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
         return (uintptr_t)p % bytes == 0 && (vl || s[0] % e == 0) && s[1] % e == 0 && s[2] % e == 0;
     };
     // (the f32-query kernel checks its own, 4-element, alignment)
-    if (dtype != CQKV_F32 && (!aligned(k, k_strides, 16) || !aligned(v, v_strides, 16)))
+    if (dtype != CQKV_F32 && !no_keys && (!aligned(k, k_strides, 16) || !aligned(v, v_strides, 16)))
         return fail(CQKV_ERR_ARG,
                     "cqkv_flash_attn: K / V need 16-byte aligned rows (pointers and strides in "
                     "whole 8-element chunks)");
-    const bool fast = kv_dtype == dtype && pf_fast_path(dtype, head_dim, q_len) &&
-                      aligned(q, q_strides, 16) && aligned(out, out_strides, 8);
+    const bool fast = !no_rows && !no_keys && kv_dtype == dtype &&
+                      pf_fast_path(dtype, head_dim, q_len) && aligned(q, q_strides, 16) &&
+                      aligned(out, out_strides, 8);
     if (!fast) {
         if (int rc = fa_plain_check("cqkv_flash_attn", dtype, kv_dtype, head_dim, k_strides[1],
                                     v_strides[1], kv_len))
             return rc;
     }
-    if (batch <= 0 || q_len <= 0 || kv_len <= 0 || q_heads <= 0 || kv_heads <= 0 ||
-        q_heads % kv_heads != 0)
+    if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0)
         return fail(CQKV_ERR_ARG, "cqkv_flash_attn: batch %d q_len %d kv_len %d heads %d / %d",
                     batch, q_len, kv_len, q_heads, kv_heads);
     if ((k_cache == nullptr) != (v_cache == nullptr))
@@ -978,8 +988,9 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
         f.o_mul = o_mul;
         f.q_mul_dev = q_mul_dev;
         f.o_mul_dev = o_mul_dev;
-        if (int rc = fa_plain_run(f, "cqkv_flash_attn", workspace, workspace_bytes, st)) return rc;
-        if (k_cache) {
+        if (!no_rows)
+            if (int rc = fa_plain_run(f, "cqkv_flash_attn", workspace, workspace_bytes, st)) return rc;
+        if (k_cache && !no_keys) {
             // K / V are (batch, kv_len, kv_heads, D): the append kernel's (batch, head, token)
             const int64_t ks[3] = {k_strides[0], k_strides[2], k_strides[1]};
             const int64_t vs[3] = {v_strides[0], v_strides[2], v_strides[1]};

@@ -87,6 +87,14 @@ enum {
     CQKV_ERR_WORKSPACE = -3 /* workspace too small */
 };
 
+/* Empty inputs (the reference's accelerated attention, candle-core/src/rocm_backend/accel.rs:87,
+ * 197, 481): an attention call with no query rows (batch or q_len 0) returns CQKV_OK after its
+ * argument checks and launches nothing but the cache append of cqkv_flash_attn(_ext) when K / V
+ * rows are given; q / out (and K / V without rows) may then be null. No keys (kv_len 0) in the
+ * dense attention calls give zero output rows (a query with an empty key range, as every masked
+ * row). The paged calls still refuse blocks holding no keys (flash_attn.rs:682), and negative
+ * sizes are errors everywhere. */
+
 /* Cache formats: the reference's kernel mode ids (candle-core/src/accel/formats.rs:41-48).
  * TURBO4 = TurboQuant MSE, Hadamard rotation (QuantFormat::TurboMse{bits}, cqkv_side.bits 1-4,
  * default 4); TURBOPROD = TurboQuant prod (QuantFormat::TurboProd{bits}, bits 2-5, default 4;

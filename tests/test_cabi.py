@@ -189,6 +189,81 @@ def test_flash_attn_ext_argument_errors(cq):
     assert L.cqkv_flash_attn_workspace_bytes(0, 2, 4096, 4096, 32, 7, 128, 0) == 0
 
 
+def test_empty_inputs(cq):
+    """No query rows (batch or q_len 0) are an empty output, as the reference's accelerated
+    attention returns (candle-core/src/rocm_backend/accel.rs:87, 197, 481): the calls return
+    before any launch and take null q / out / K / V; negative sizes stay errors, and the paged
+    forms check their blocks first (no keys is still an error there, flash_attn.rs:682)."""
+    L = cq.lib()
+    x = (ctypes.c_int64 * 3)(8192, 256, 128)
+    one = ctypes.c_void_p(256)
+
+    def dense(batch, ql, kvl, q=None, k=None, dtype=0, kvd=None):
+        kvd = dtype if kvd is None else kvd
+        return L.cqkv_flash_attn_ext(q, x, k, x, k, x, q, x, dtype, kvd, batch, ql, kvl, 8, 2,
+                                     128, 0.1, -1, 0, 0.0, None, 0, None, None, 0, 0, None, None,
+                                     0, None, 0, None)
+    for dt in (0, 1, 2):
+        assert dense(0, 16, 16, dtype=dt) == cq.OK
+        assert dense(2, 0, 16, dtype=dt, k=one) == cq.OK  # K / V rows (for a cache append)
+        assert dense(2, 0, 16, dtype=dt) == cq.ERR_ARG
+        assert dense(0, 0, 0, dtype=dt) == cq.OK
+    assert dense(-1, 16, 16) == cq.ERR_ARG
+    assert dense(2, -1, 16) == cq.ERR_ARG
+    assert dense(2, 16, -1) == cq.ERR_ARG
+    assert dense(2, 16, 16) == cq.ERR_ARG  # rows to write: q / out must be given
+    assert b"null" in L.cqkv_last_error()
+    assert dense(2, 0, 16, dtype=0, kvd=1, k=one) == cq.ERR_ARG  # dtype pairs are still checked
+    assert L.cqkv_flash_attn_workspace_bytes(0, 2, 0, 16, 8, 2, 128, 0) == 0
+    assert L.cqkv_flash_attn_workspace_bytes(0, 2, 16, 0, 8, 2, 128, 0) == 0
+
+    def fp8(batch, ql, kvl, dtype=0):
+        return L.cqkv_flash_attn_fp8(None, x, None, x, None, x, None, x, dtype, batch, ql, kvl,
+                                     8, 8, 128, 0.1, -1, 0, 1.0, 1.0, None, None, None, 0, None)
+    for dt in (0, 1, 2):
+        assert fp8(0, 16, 16, dt) == cq.OK
+        assert fp8(1, 0, 16, dt) == cq.OK
+    assert fp8(1, 16, 0) == cq.ERR_ARG  # zero rows to write need q / out
+    assert fp8(1, -1, 16) == cq.ERR_ARG
+
+    k0 = cq.Side(cq.FP8, 0, 128, 8, 64, 0, 0, 0, 0, 1, 1)
+    v0 = cq.Side(cq.FP8, 1, 128, 8, 64, 0, 0, 0, 0, 1, 1)
+    xs = (ctypes.c_int64 * 3)(1, 1, 1)
+
+    def decode(batch, ql, kvl=10):
+        return L.cqkv_decode_attention(None, 0, xs, ctypes.byref(k0), ctypes.byref(v0), batch, 8,
+                                       ql, None, kvl, 0.1, -1, -1, None, 0, xs, 0, None, 0, None)
+    assert decode(0, 1) == cq.OK
+    assert decode(1, 0) == cq.OK
+    assert decode(1, 0, kvl=65) == cq.ERR_ARG  # kv_len above the capacity
+    assert decode(-1, 1) == cq.ERR_ARG
+    assert decode(1, 1) == cq.ERR_ARG
+
+    def paged(rows, batch, ql):
+        arr = (cq.KvBlock * 1)()
+        arr[0].k, arr[0].v, arr[0].rows = ctypes.pointer(k0), ctypes.pointer(v0), rows
+        return L.cqkv_decode_attention_paged(None, 0, xs, arr, 1, batch, 8, ql, 0.1, -1, -1, None,
+                                             0, xs, None, 0, None)
+    assert paged(10, 0, 1) == cq.OK
+    assert paged(10, 1, 0) == cq.OK
+    assert paged(0, 1, 0) == cq.ERR_ARG
+    assert b"no keys" in L.cqkv_last_error()
+
+    def plain_blocks(rows, batch, ql):
+        arr = (cq.PlainBlock * 1)()
+        arr[0].k = arr[0].v = one
+        arr[0].rows = rows
+        for i, s in enumerate((8192, 128, 128)):
+            arr[0].k_strides[i] = arr[0].v_strides[i] = s
+        return L.cqkv_flash_attn_blocks(None, x, arr, 1, 0, 0, batch, 8, ql, 2, 128, 0.1, -1, 0,
+                                        0.0, None, 0, None, x, None, 0, None)
+    assert plain_blocks(10, 0, 16) == cq.OK
+    assert plain_blocks(10, 2, 0) == cq.OK
+    assert plain_blocks(0, 2, 0) == cq.ERR_ARG
+    assert b"no keys" in L.cqkv_last_error()
+    assert plain_blocks(10, 2, 16) == cq.ERR_ARG
+
+
 def test_paged_argument_errors_and_workspace(cq):
     """cqkv_decode_attention_paged validates its blocks like the reference's check_blocks
     (candle-nn/src/flash_attn.rs:650-686) before any launch, and sizes its scratch."""
