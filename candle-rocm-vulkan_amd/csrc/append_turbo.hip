@@ -4,12 +4,15 @@
 //
 // The row-parallel encoder of append_rows.h spends most of its VALU issue on the sign flip, the
 // seven Walsh-Hadamard stages and a three-step codebook search per element. Here:
-//  * y = x diag(s) H^T (unscaled) is one MFMA product per 16 rows: the rows are the A operand as
-//    they arrive (16-byte loads of bf16 / f16, no conversion), B is the +-1 matrix
-//    B[k][c] = s_k H[pi(c)][k] (exact in bf16 / f16, so every product is exact), built once per
-//    workgroup in LDS and read from there by each product. The output columns are permuted,
-//    pi(16 nb + n) = (D / 16) n + nb, so that lane (n, g) ends with D / 16 consecutive columns of
-//    rows 4 g .. 4 g + 3.
+//  * y = x diag(s) H^T (unscaled) is two MFMA products per 16 rows, one per half of the row
+//    (H = H_2 (x) H_{D/2}: y = (u + v, u - v) with u, v the halves' H_{D/2} transforms, added
+//    and subtracted in f32 by the lane that holds both): the rows are the A operand as they
+//    arrive (16-byte loads of bf16 / f16, no conversion), B is the +-1 matrix
+//    B_h[k][c] = s_{h D/2 + k} H_{D/2}[pi(c)][k] (exact in bf16 / f16, so every product is
+//    exact), built once per workgroup in LDS and read from there by each product. The output
+//    columns are permuted, pi(16 nb + n) = (D / 32) n + nb, so that lane (n, g) ends with D / 32
+//    consecutive columns of each half for rows 4 g .. 4 g + 3. (The whole D x D matrix took
+//    twice the products: keys 39 -> 36 us, values 51 -> 47 us per config-2-shape call.)
 //  * One workgroup of 16 wavefronts per CU shares B and the table: 32 KB of B per wavefront in
 //    registers would have allowed two wavefronts per SIMD, and B per 4-wavefront workgroup would
 //    have limited the CU to two workgroups by LDS. With B shared the kernel runs four wavefronts
@@ -65,15 +68,18 @@ struct TqChunk {
     int b, h, pos, c0, end;
     bool valid;
 };
+// pos0: a.position, read once into a register (a select between it and a.positions[b] as
+// memory reads became one flat load, waited for before the chunk's row loads could issue).
 template <int ROWS>
-__device__ inline TqChunk tq_chunk(const TurboMfmaArgs &p, int ck) {
+__device__ inline TqChunk tq_chunk(const TurboMfmaArgs &p, int ck, int pos0) {
     const AppendArgs &a = p.a;
     TqChunk c = {};
     if (ck >= p.total_chunks) return c;  // valid false: past the last chunk
     const int bx = ck % p.chunks_per_plane, plane = ck / p.chunks_per_plane;
     c.h = plane % a.kv_heads;
     c.b = plane / a.kv_heads;
-    c.pos = a.positions ? a.positions[c.b] : a.position;
+    c.pos = pos0;
+    if (a.positions) c.pos = a.positions[c.b];
     c.c0 = c.pos / 8 * 8 + bx * ROWS;
     c.end = min(c.pos + a.tokens, a.capacity);
     if (a.cs_rows > 0) c.end = min(c.end, a.cs_rows);
@@ -82,26 +88,33 @@ __device__ inline TqChunk tq_chunk(const TurboMfmaArgs &p, int ck) {
 }
 
 // This lane's A operands of 16-row group grp of a chunk: row (group row n), head dims
-// 32 ks + 8 g .. + 7; rows outside [pos, end) read zeros.
+// 32 ks + 8 g .. + 7; rows outside [pos, end) read zeros. Buffer loads from the chunk's first
+// row (its position c0 may precede the first appended row: only rows in [pos, end) are read),
+// with dead rows pointed past the range, so that the loads are unconditional: the compiler can
+// then count them, and wait for them without also waiting for the stores issued after them.
+constexpr uint32_t kTqOOB = 0x80000000u;
 template <int D, int ROWS>
 __device__ inline void tq_load(const AppendArgs &a, const TqChunk &c, int grp, int n, int g,
                                u32x4 (&av)[D / 32]) {
     const int t = c.c0 + 16 * grp + n;
     const bool live = c.valid && t >= c.pos && t < c.end;
-    const uint16_t *row = (const uint16_t *)a.x + (int64_t)c.b * a.sb + (int64_t)c.h * a.sh +
-                          (int64_t)(t - c.pos) * a.st + 8 * g;
+    const uint16_t *base = (const uint16_t *)a.x + (int64_t)c.b * a.sb + (int64_t)c.h * a.sh +
+                           (int64_t)(c.c0 - c.pos) * a.st;
+    const rsrc_t r = make_rsrc(base, kTqOOB);
+    const uint32_t off = live ? (uint32_t)((int64_t)(t - c.c0) * a.st * 2 + 16 * g) : kTqOOB;
 #pragma unroll
-    for (int ks = 0; ks < D / 32; ++ks)
-        av[ks] = live ? *(const u32x4 *)(row + 32 * ks) : u32x4{0u, 0u, 0u, 0u};
+    for (int ks = 0; ks < D / 32; ++ks) av[ks] = ld128(r, off + 64 * ks);
 }
 
 template <int IS_VALUE, int D, bool F16>
 __global__ __launch_bounds__(kTqThreads) void turbo_mfma_kernel(TurboMfmaArgs p) {
     constexpr int NW = kTqThreads / 64;
-    constexpr int NB = D / 16, KS = D / 32, ROWS = kTqRows, GPW = ROWS / (16 * NW);
+    // NBH column blocks and KSH k-steps per half of the row (the H_2 (x) H_{D/2} split)
+    constexpr int NB = D / 16, KS = D / 32, NBH = NB / 2, KSH = KS / 2;
+    constexpr int ROWS = kTqRows, GPW = ROWS / (16 * NW);
     constexpr int kRowBytes = D / 2;
     using op_t = tq_op_t<F16>;
-    __shared__ __attribute__((aligned(16))) u32x4 sm_b[NB * KS * 64];
+    __shared__ __attribute__((aligned(16))) u32x4 sm_b[2 * NBH * KSH * 64];
     __shared__ __attribute__((aligned(16))) u32x2 sm_lut[kLutN * kLutCopies];
     __shared__ __attribute__((aligned(16))) uint8_t sm_codes[IS_VALUE ? ROWS * kRowBytes : 16];
     const AppendArgs &a = p.a;
@@ -109,24 +122,30 @@ __global__ __launch_bounds__(kTqThreads) void turbo_mfma_kernel(TurboMfmaArgs p)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 15, g = lane >> 4;
 
-    // ---- once per workgroup: B (as [nb][ks][lane] operands) and the replicated table; every
-    // read of the kernel arguments here has a workgroup-uniform index (scalar loads) ----
+    // ---- once per workgroup: B (as [half][nb][ks][lane] operands) and the replicated table;
+    // every read of the kernel arguments here has a workgroup-uniform index (scalar loads) ----
+    // The Sylvester matrix is H_2 (x) H_{D/2} (the top index bit): with u = H_{D/2} (s x)[first
+    // half] and v = H_{D/2} (s x)[second half], y = (u + v, u - v). The products take the two
+    // halves' B_h[k][c] = s_{h D/2 + k} H_{D/2}[pi(c)][k], pi(16 nb + n) = NBH n + nb, half the
+    // products of the whole matrix; each lane then adds and subtracts its own u and v.
     const uint32_t sgn[4] = {a.sign_bits[0], a.sign_bits[1], a.sign_bits[2], a.sign_bits[3]};
 #pragma unroll
-    for (int it = 0; it < (NB * KS * 64 + kTqThreads - 1) / kTqThreads; ++it) {
+    for (int it = 0; it < (2 * NBH * KSH * 64 + kTqThreads - 1) / kTqThreads; ++it) {
         const int i = tid + kTqThreads * it;
-        if (i >= NB * KS * 64) break;
-        const int l = i & 63, ks = (i >> 6) % KS, nb = (i >> 6) / KS;
-        const int col = NB * (l & 15) + nb;
+        if (i >= 2 * NBH * KSH * 64) break;
+        const int l = i & 63, ks = (i >> 6) % KSH, nb = ((i >> 6) / KSH) % NBH;
+        const int half = (i >> 6) / (KSH * NBH);
+        const int col = NBH * (l & 15) + nb;
         const uint32_t one = F16 ? 0x3C00u : 0x3F80u;
-        const uint32_t sw = ks == 0 ? sgn[0] : ks == 1 ? sgn[1] : ks == 2 ? sgn[2] : sgn[3];
+        const int kw = half * KSH + ks;  // sign word of the row's elements 32 kw ..
+        const uint32_t sw = kw == 0 ? sgn[0] : kw == 1 ? sgn[1] : kw == 2 ? sgn[2] : sgn[3];
         uint32_t w[4];
 #pragma unroll
         for (int e2 = 0; e2 < 4; ++e2) {
             uint32_t v = 0;
 #pragma unroll
             for (int h2 = 0; h2 < 2; ++h2) {
-                const int k = 32 * ks + 8 * (l >> 4) + 2 * e2 + h2;
+                const int k = 32 * ks + 8 * (l >> 4) + 2 * e2 + h2;  // index in the half
                 const uint32_t par = ((uint32_t)__popc(col & k) + (sw >> (k & 31))) & 1u;
                 v |= (one | (par << 15)) << (16 * h2);
             }
@@ -146,43 +165,70 @@ __global__ __launch_bounds__(kTqThreads) void turbo_mfma_kernel(TurboMfmaArgs p)
         else if (e0 + 1 <= 2 * S) sm_lut[(e0 + 1) * kLutCopies + lane - 32] = hi;
     }
     __syncthreads();
-    const u32x4 *bsm = sm_b + lane;
     // this lane's copy of the entry of bin 0 (bin j is entry j + S)
     const u32x2 *lut0 = sm_lut + S * kLutCopies + (lane & 31);
 
     // ---- the chunks of this workgroup; the next chunk's rows load while this one computes ----
-    int ck = blockIdx.x;
-    TqChunk cur = tq_chunk<ROWS>(p, ck);
-    u32x4 av[GPW][KS], nv[GPW][KS];
+    // The rows are loaded in one place only, into nv, and copied to av at the top of the next
+    // iteration, before that iteration issues its own loads; the first iteration (ck < 0) only
+    // loads. (Loads into av before the loop made the compiler's wait for av at the first product
+    // also wait for the prefetch issued in the loop, serialising every load with the compute.)
+    // Chunk descriptors are formed one iteration ahead of their loads (nn), so that a per-batch
+    // position read is waited for together with the rows, not before them.
+    const int pos0 = a.position;
+    TqChunk nxt = {}, nn = tq_chunk<ROWS>(p, blockIdx.x, pos0);
+    u32x4 av[GPW][KS], nv[GPW][KS] = {};
+    for (int ck = (int)blockIdx.x - (int)gridDim.x; ck < p.total_chunks; ck += gridDim.x) {
+        const TqChunk cur = nxt;
 #pragma unroll
-    for (int grp = 0; grp < GPW; ++grp) tq_load<D, ROWS>(a, cur, wave * GPW + grp, n, g, av[grp]);
-    for (; ck < p.total_chunks; ck += gridDim.x) {
-        const TqChunk nxt = tq_chunk<ROWS>(p, ck + (int)gridDim.x);
+        for (int grp = 0; grp < GPW; ++grp)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) av[grp][ks] = nv[grp][ks];
+        nxt = nn;
+        nn = tq_chunk<ROWS>(p, ck + 2 * (int)gridDim.x, pos0);
 #pragma unroll
         for (int grp = 0; grp < GPW; ++grp) tq_load<D, ROWS>(a, nxt, wave * GPW + grp, n, g, nv[grp]);
-        if (cur.valid) {  // workgroup-uniform
+        // Every iteration computes, also for a chunk that writes nothing (the first iteration,
+        // chunks past the end): its rows are dead and its stores dropped. With a branch around
+        // the compute, the compiler's wait for nv at the top of the iteration counted on the
+        // path without stores and so waited for the stores of the previous chunk as well.
+        {
+            // B is re-read from LDS by each product: an index the compiler cannot see through
+            // keeps it from hoisting the 32 operands out of the loop (and spilling them)
+            int bl = lane;
+            asm volatile("" : "+v"(bl));
+            const u32x4 *bsm = sm_b + bl;
             const int64_t plane = (int64_t)cur.b * a.kv_heads + cur.h;
             uint8_t *codes = a.codes + plane * a.codes_plane;
-            float *norms = (float *)(a.scales + plane * a.scales_plane);
+            // (buffer stores, dead rows past the range: unconditional, as the loads)
+            const rsrc_t code_r = make_rsrc(codes, kTqOOB);
+            const rsrc_t norm_r = make_rsrc(a.scales + plane * a.scales_plane, kTqOOB);
 #pragma unroll
             for (int grp = 0; grp < GPW; ++grp) {
                 const int r0 = 16 * (wave * GPW + grp);  // the group's first row in the chunk
-                // MFMAs in ks-major order: consecutive products update different accumulators
+                // u (acc[0 .. NBH)) and v (acc[NBH ..)), ks-major: consecutive products update
+                // different accumulators
                 f32x4 acc[NB];
 #pragma unroll
-                for (int nb = 0; nb < NB; ++nb)
-                    acc[nb] = mfma16x16x32(__builtin_bit_cast(op_t, av[grp][0]),
-                                           __builtin_bit_cast(op_t, bsm[(nb * KS) * 64]),
-                                           f32x4{0.f, 0.f, 0.f, 0.f});
+                for (int ks = 0; ks < KSH; ++ks)
 #pragma unroll
-                for (int ks = 1; ks < KS; ++ks)
+                    for (int j = 0; j < NB; ++j) {
+                        const int half = j / NBH, nb = j % NBH;
+                        acc[j] = mfma16x16x32(
+                            __builtin_bit_cast(op_t, av[grp][half * KSH + ks]),
+                            __builtin_bit_cast(op_t, bsm[((half * NBH + nb) * KSH + ks) * 64]),
+                            ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[j]);
+                    }
 #pragma unroll
-                    for (int nb = 0; nb < NB; ++nb)
-                        acc[nb] = mfma16x16x32(__builtin_bit_cast(op_t, av[grp][ks]),
-                                               __builtin_bit_cast(op_t, bsm[(nb * KS + ks) * 64]),
-                                               acc[nb]);
-                // lane (n, g): rows r0 + 4 g + i, columns NB n .. NB n + NB - 1 (column NB n + nb
-                // in acc[nb]). Row norms by the hardware square root and reciprocal (1 ulp; the
+                for (int nb = 0; nb < NBH; ++nb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float uu = acc[nb][i], vv = acc[NBH + nb][i];
+                        acc[nb][i] = uu + vv;
+                        acc[NBH + nb][i] = uu - vv;
+                    }
+                // lane (n, g): rows r0 + 4 g + i, columns h D / 2 + NBH n + nb in acc[h NBH + nb]
+                // (h the half). Row norms by the hardware square root and reciprocal (1 ulp; the
                 // rotation itself already leaves the reference's last bits unpinned).
                 float norm[4], inv[4], w[4];
                 bool fin = true;
@@ -224,15 +270,35 @@ __global__ __launch_bounds__(kTqThreads) void turbo_mfma_kernel(TurboMfmaArgs p)
                     }
                 }
                 const int rg = r0 + 4 * g, tg = cur.c0 + rg;  // this lane's first row
-                uint8_t *dst = (IS_VALUE ? sm_codes + rg * kRowBytes
-                                         : codes + (int64_t)tg * kRowBytes) + (NB / 2) * n;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const bool live = tg + i >= cur.pos && tg + i < cur.end;
-                    if (live && n == 0) norms[tg + i] = norm[i] * a.rot_scale;
-                    if (IS_VALUE || live) {
-                        if constexpr (NB == 8) *(uint32_t *)(dst + i * kRowBytes) = word[i];
-                        else *(uint16_t *)(dst + i * kRowBytes) = (uint16_t)word[i];
+                    __builtin_amdgcn_raw_buffer_store_b32(
+                        __float_as_uint(norm[i] * a.rot_scale), norm_r,
+                        live && n == 0 ? (uint32_t)(tg + i) * 4u : kTqOOB, 0, 0);
+                    // the NBH codes of each half: bytes (NBH / 2) n of the first and the second
+                    // half of the row's codes
+                    const uint32_t lo = word[i] & ((1u << (4 * NBH)) - 1u), hi = word[i] >> (4 * NBH);
+                    if constexpr (IS_VALUE != 0) {
+                        uint8_t *dst = sm_codes + (rg + i) * kRowBytes + (NBH / 2) * n;
+                        if constexpr (NBH == 4) {
+                            *(uint16_t *)dst = (uint16_t)lo;
+                            *(uint16_t *)(dst + kRowBytes / 2) = (uint16_t)hi;
+                        } else {
+                            dst[0] = (uint8_t)lo;
+                            dst[kRowBytes / 2] = (uint8_t)hi;
+                        }
+                    } else {
+                        const uint32_t off =
+                            live ? (uint32_t)(tg + i) * kRowBytes + (NBH / 2) * n : kTqOOB;
+                        const uint32_t off2 = live ? off + kRowBytes / 2 : kTqOOB;
+                        if constexpr (NBH == 4) {
+                            __builtin_amdgcn_raw_buffer_store_b16((uint16_t)lo, code_r, off, 0, 0);
+                            __builtin_amdgcn_raw_buffer_store_b16((uint16_t)hi, code_r, off2, 0, 0);
+                        } else {
+                            __builtin_amdgcn_raw_buffer_store_b8((uint8_t)lo, code_r, off, 0, 0);
+                            __builtin_amdgcn_raw_buffer_store_b8((uint8_t)hi, code_r, off2, 0, 0);
+                        }
                     }
                 }
             }
@@ -242,11 +308,6 @@ __global__ __launch_bounds__(kTqThreads) void turbo_mfma_kernel(TurboMfmaArgs p)
                 __syncthreads();  // sm_codes is rewritten by the next chunk
             }
         }
-        cur = nxt;
-#pragma unroll
-        for (int grp = 0; grp < GPW; ++grp)
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) av[grp][ks] = nv[grp][ks];
     }
 }
 
@@ -294,12 +355,19 @@ bool turbo_mfma_launch(const cqkv_side *s, int32_t tokens, int32_t batch, hipStr
     if (a.row_loads != kRowBF16 && a.row_loads != kRowF16) return false;
     const int d = s->head_dim;
     if (d != 64 && d != 128) return false;
+    // 31-bit buffer offsets: rows of a chunk from its first row, codes and norms of a plane
+    if (a.st < 0 || (int64_t)kTqRows * a.st * 2 + 2 * d >= kTqOOB ||
+        (int64_t)s->capacity * (d / 2) >= kTqOOB)
+        return false;
     TurboMfmaArgs p = {};
     p.a = a;
     bool ok = false;
     for (int S = 8; S <= kLutMaxS && !ok; S *= 2) ok = tq_build_lut(a.bnd, S, p);
     if (!ok) return false;
-    p.chunks_per_plane = (int)(((int64_t)tokens + 7 + kTqRows - 1) / kTqRows);
+    // chunks start at the value tile of the first position: with one position for every batch
+    // entry its offset in the tile is known here (no chunk that writes nothing)
+    const int lead = !a.positions && a.position >= 0 ? a.position % 8 : 7;
+    p.chunks_per_plane = (int)(((int64_t)tokens + lead + kTqRows - 1) / kTqRows);
     const int64_t total = (int64_t)p.chunks_per_plane * s->kv_heads * batch;
     if (total <= 0 || total > 0x7fffffff) return false;
     p.total_chunks = (int32_t)total;
