@@ -270,12 +270,18 @@ __global__ __launch_bounds__(kTqThreads) void turbo_mfma_kernel(TurboMfmaArgs p)
                     }
                 }
                 const int rg = r0 + 4 * g, tg = cur.c0 + rg;  // this lane's first row
+                {
+                    // one store of the group's 16 norms: lane (n < 4, g) writes row 4 g + n's
+                    // (every lane of a 16-lane row holds all four of its rows' norms)
+                    const float nm = n == 0 ? norm[0] : n == 1 ? norm[1] : n == 2 ? norm[2] : norm[3];
+                    const bool live = n < 4 && tg + n >= cur.pos && tg + n < cur.end;
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(nm * a.rot_scale), norm_r,
+                                                          live ? (uint32_t)(tg + n) * 4u : kTqOOB,
+                                                          0, 0);
+                }
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const bool live = tg + i >= cur.pos && tg + i < cur.end;
-                    __builtin_amdgcn_raw_buffer_store_b32(
-                        __float_as_uint(norm[i] * a.rot_scale), norm_r,
-                        live && n == 0 ? (uint32_t)(tg + i) * 4u : kTqOOB, 0, 0);
                     // the NBH codes of each half: bytes (NBH / 2) n of the first and the second
                     // half of the row's codes
                     const uint32_t lo = word[i] & ((1u << (4 * NBH)) - 1u), hi = word[i] >> (4 * NBH);
