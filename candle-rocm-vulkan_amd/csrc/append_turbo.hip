@@ -116,7 +116,9 @@ __global__ __launch_bounds__(kTqThreads) void turbo_mfma_kernel(TurboMfmaArgs p)
     using op_t = tq_op_t<F16>;
     __shared__ __attribute__((aligned(16))) u32x4 sm_b[2 * NBH * KSH * 64];
     __shared__ __attribute__((aligned(16))) u32x2 sm_lut[kLutN * kLutCopies];
-    __shared__ __attribute__((aligned(16))) uint8_t sm_codes[IS_VALUE ? ROWS * kRowBytes : 16];
+    // values: the chunk's codes, double-buffered (chunk parity) so that one barrier per chunk
+    // separates their writes from the tile writer's reads
+    __shared__ __attribute__((aligned(16))) uint8_t sm_codes_buf[IS_VALUE ? 2 * ROWS * kRowBytes : 16];
     const AppendArgs &a = p.a;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -188,6 +190,7 @@ __global__ __launch_bounds__(kTqThreads) void turbo_mfma_kernel(TurboMfmaArgs p)
         nn = tq_chunk<ROWS>(p, ck + 2 * (int)gridDim.x, pos0);
 #pragma unroll
         for (int grp = 0; grp < GPW; ++grp) tq_load<D, ROWS>(a, nxt, wave * GPW + grp, n, g, nv[grp]);
+        uint8_t *sm_codes = sm_codes_buf + (IS_VALUE ? (((ck - (int)blockIdx.x) / (int)gridDim.x) & 1) * ROWS * kRowBytes : 0);
         // Every iteration computes, also for a chunk that writes nothing (the first iteration,
         // chunks past the end): its rows are dead and its stores dropped. With a branch around
         // the compute, the compiler's wait for nv at the top of the iteration counted on the
@@ -310,8 +313,9 @@ __global__ __launch_bounds__(kTqThreads) void turbo_mfma_kernel(TurboMfmaArgs p)
             }
             if constexpr (IS_VALUE != 0) {
                 __syncthreads();
+                // (the next chunk writes the other buffer; the one after it this buffer again,
+                // behind the next chunk's barrier)
                 write_value_tiles<false, D, ROWS, kTqThreads>(codes, sm_codes, cur.c0, cur.pos, cur.end, tid);
-                __syncthreads();  // sm_codes is rewritten by the next chunk
             }
         }
     }
