@@ -142,7 +142,7 @@ def side_rows(cq, side, b0, nb, tokens):
     cb, sb = side.codes.numel() // side.batch, side.scales.numel() // side.batch
     view = cq.CacheSide(side.fmt, side.is_value, nb, side.kv_heads, side.head_dim, side.capacity,
                         side.codes[b0 * cb:(b0 + nb) * cb], side.scales[b0 * sb:(b0 + nb) * sb],
-                        side.seed, side.rotation, side.qjl, side.bits)
+                        side.seed, side.rotation, side.qjl, side.bits, side.rot)
     return cq.rows_export(view, tokens).cpu().numpy().view(np.uint32)
 
 

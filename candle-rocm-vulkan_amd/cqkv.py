@@ -24,9 +24,10 @@ TURBO4, TURBOPROD, MXFP4, NVFP4, MXFP8, FP8 = 0, 1, 2, 3, 4, 5
 FORMAT_NAMES = {"fp8": FP8, "mxfp4": MXFP4, "turbo4": TURBO4, "turboprod": TURBOPROD,
                 "nvfp4": NVFP4, "mxfp8": MXFP8}
 BF16, F16, F32 = 0, 1, 2
-# cache-side rotations: DEFAULT rotates TURBO4 sides only; HADAMARD any format (the reference's
-# RotationKind::Hadamard, Auto at power-of-two head dims)
-ROT_DEFAULT, ROT_NONE, ROT_HADAMARD = 0, 1, 2
+# cache-side rotations (RotationKind, candle-core/src/accel/config.rs:104-139): DEFAULT is AUTO for
+# the TurboQuant formats and NONE for the others; AUTO is HADAMARD at power-of-two head dims and
+# DENSE otherwise; HADAMARD at other head dims resolves to DENSE
+ROT_DEFAULT, ROT_NONE, ROT_HADAMARD, ROT_DENSE, ROT_AUTO = 0, 1, 2, 3, 4
 # rotary layouts: rope (halves) and rope_i (interleaved) of candle-nn/src/rotary_emb.rs
 ROPE_HALVES, ROPE_INTERLEAVED = 1, 2
 _DTYPES = {torch.bfloat16: BF16, torch.float16: F16, torch.float32: F32}
@@ -46,7 +47,7 @@ class Side(ctypes.Structure):
                 ("capacity", ctypes.c_int32), ("rotation", ctypes.c_int32),
                 ("bits", ctypes.c_int32), ("reserved", ctypes.c_int32),
                 ("seed", ctypes.c_uint64), ("codes", ctypes.c_void_p),
-                ("scales", ctypes.c_void_p), ("qjl", ctypes.c_void_p)]
+                ("scales", ctypes.c_void_p), ("qjl", ctypes.c_void_p), ("rot", ctypes.c_void_p)]
 
 
 class PlainBlock(ctypes.Structure):
@@ -88,14 +89,15 @@ def lib() -> ctypes.CDLL:
         L.cqkv_decode_splits.argtypes = [i32, i32, i32, i32, i32, i32]
         L.cqkv_decode_splits.restype = i32
         L.cqkv_decode_attention.argtypes = [P, i32, I64P, SP, SP, i32, i32, i32, P, i32, f32,
-                                            i32, i32, P, i32, I64P, i32, P, sz, P]
+                                            i32, i32, f32, P, i32, P, i32, I64P, i32, P, sz, P]
         L.cqkv_decode_attention_noalloc.argtypes = [P, i32, I64P, SP, SP, i32, i32, i32, P, i32,
-                                                    f32, i32, i32, P, i32, I64P, i32, P]
+                                                    f32, i32, i32, f32, P, i32, P, i32, I64P, i32,
+                                                    P]
         BP = ctypes.POINTER(KvBlock)
         L.cqkv_decode_paged_workspace_bytes.argtypes = [BP, i32, i32, i32, i32]
         L.cqkv_decode_paged_workspace_bytes.restype = sz
         L.cqkv_decode_attention_paged.argtypes = [P, i32, I64P, BP, i32, i32, i32, i32, f32, i32,
-                                                  i32, P, i32, I64P, P, sz, P]
+                                                  i32, f32, P, i32, P, i32, I64P, P, sz, P]
         L.cqkv_flash_attn.argtypes = [P, I64P, P, I64P, P, I64P, P, I64P, i32, i32, i32, i32,
                                       i32, i32, i32, f32, i32, i32, SP, SP, i32, P]
         L.cqkv_flash_attn_ext.argtypes = [P, I64P, P, I64P, P, I64P, P, I64P, i32, i32, i32,
@@ -123,6 +125,12 @@ def lib() -> ctypes.CDLL:
         L.cqkv_turbo_codebook.argtypes = [i32, i32, P, P]
         L.cqkv_turbo_signs.argtypes = [i32, ctypes.c_uint64, P]
         L.cqkv_qjl_matrix.argtypes = [i32, ctypes.c_uint64, P]
+        L.cqkv_rotation_matrix.argtypes = [i32, i32, ctypes.c_uint64, P]
+        L.cqkv_resolve_rotation.argtypes = [i32, i32, i32]
+        L.cqkv_resolve_rotation.restype = i32
+        L.cqkv_dequantize_workspace_bytes.argtypes = [SP, i32, i32, i32]
+        L.cqkv_dequantize_workspace_bytes.restype = sz
+        L.cqkv_dequantize_rows.argtypes = [SP, i32, i32, i32, i32, P, i32, I64P, P, sz, P]
         L.cqkv_last_error.restype = ctypes.c_char_p
         L.cqkv_version.restype = ctypes.c_char_p
         _lib = L
@@ -139,7 +147,8 @@ EXPORTED = ["cqkv_codes_plane_bytes", "cqkv_scales_plane_bytes", "cqkv_quant_app
             "cqkv_fp8_quantize_tensor",
             "cqkv_flash_attn_fp8", "cqkv_flash_attn_fp8_workspace_bytes", "cqkv_hadamard_rows", "cqkv_reference_row_words", "cqkv_rows_import",
             "cqkv_rows_export", "cqkv_side_copy", "cqkv_turbo_codebook", "cqkv_turbo_signs",
-            "cqkv_qjl_matrix",
+            "cqkv_qjl_matrix", "cqkv_rotation_matrix", "cqkv_resolve_rotation",
+            "cqkv_dequantize_workspace_bytes", "cqkv_dequantize_rows",
             "cqkv_last_error",
             "cqkv_version"]
 
@@ -186,6 +195,7 @@ class CacheSide:
     qjl: torch.Tensor | None = None  # TURBOPROD: the (D, D) f32 QJL matrix on the device
     # TurboQuant width (TURBO4: TurboMse{bits} 1-4, TURBOPROD: TurboProd{bits} 2-5; 0 = 4)
     bits: int = 0
+    rot: torch.Tensor | None = None  # rotating sides: the (D, D) f32 rotation matrix on the device
 
     @staticmethod
     def empty(fmt: int, is_value: bool, batch: int, kv_heads: int, head_dim: int,
@@ -199,19 +209,27 @@ class CacheSide:
         codes = torch.zeros(batch * kv_heads * cb, dtype=torch.uint8, device=device)
         scales = torch.zeros(batch * kv_heads * sb, dtype=torch.uint8, device=device)
         qjl = qjl_matrix(head_dim, seed).to(device) if fmt == TURBOPROD else None
+        kind = resolve_rotation(fmt, rotation, head_dim)
+        # the rotation matrix, as TurboQuantizer keeps it on the device whenever it rotates
+        rot = (rotation_matrix(head_dim, kind, seed).to(device)
+               if kind in (ROT_HADAMARD, ROT_DENSE) else None)
         return CacheSide(fmt, is_value, batch, kv_heads, head_dim, capacity, codes, scales, seed,
-                         rotation, qjl, bits)
+                         rotation, qjl, bits, rot)
+
+    def rotation_kind(self) -> int:
+        """The resolved rotation: ROT_NONE, ROT_HADAMARD or ROT_DENSE."""
+        return resolve_rotation(self.fmt, self.rotation, self.head_dim)
 
     def rotates(self) -> bool:
-        """Whether rows are stored Hadamard-rotated (seeded by `seed`)."""
-        return self.rotation == ROT_HADAMARD or (self.rotation == ROT_DEFAULT and
-                                                 self.fmt in (TURBO4, TURBOPROD))
+        """Whether rows are stored rotated (by the seeded Hadamard or Dense matrix)."""
+        return self.rotation_kind() in (ROT_HADAMARD, ROT_DENSE)
 
     def struct(self) -> Side:
         return Side(self.fmt, int(self.is_value), self.head_dim, self.kv_heads, self.capacity,
                     self.rotation, self.bits, 0, self.seed, self.codes.data_ptr(),
                     self.scales.data_ptr(),
-                    None if self.qjl is None else self.qjl.data_ptr())
+                    None if self.qjl is None else self.qjl.data_ptr(),
+                    None if self.rot is None else self.rot.data_ptr())
 
     def nbytes(self) -> int:
         return self.codes.numel() + self.scales.numel()
@@ -300,8 +318,10 @@ def decode_attention(q: torch.Tensor, k: CacheSide, v: CacheSide, kv_len: int,
                      softmax_scale: float, kv_lens: torch.Tensor | None = None,
                      window_left: int = -1, window_right: int = -1,
                      out: torch.Tensor | None = None, splits: int = 0,
-                     workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """q (batch, q_heads, q_len, D) -> out of the same shape (dtype of q unless `out` given)."""
+                     workspace: torch.Tensor | None = None, softcap: float = 0.0,
+                     alibi_slopes: torch.Tensor | None = None) -> torch.Tensor:
+    """q (batch, q_heads, q_len, D) -> out of the same shape (dtype of q unless `out` given);
+    softcap / alibi_slopes ((q_heads) or (batch, q_heads) f32) as FlashAttnConfig's."""
     _need_gpu(q, "q")
     b, hq, lq, d = q.shape
     if q.stride(3) != 1:
@@ -315,10 +335,11 @@ def decode_attention(q: torch.Tensor, k: CacheSide, v: CacheSide, kv_len: int,
     elif tuple(out.shape) != tuple(q.shape) or out.stride(3) != 1:
         raise CqkvError(ERR_ARG, f"out {tuple(out.shape)} does not match q")
     ks, vs = k.struct(), v.struct()
+    al, al_bs = _alibi_arg(alibi_slopes, b, hq)
     _check(lib().cqkv_decode_attention(
         _ptr(q), _DTYPES[q.dtype], _strides3(q, (0, 1, 2)), ctypes.byref(ks), ctypes.byref(vs), b,
-        hq, lq, _ptr(kv_lens), kv_len, softmax_scale, window_left, window_right, _ptr(out),
-        _DTYPES[out.dtype], _strides3(out, (0, 1, 2)), splits, _ptr(workspace),
+        hq, lq, _ptr(kv_lens), kv_len, softmax_scale, window_left, window_right, softcap, al,
+        al_bs, _ptr(out), _DTYPES[out.dtype], _strides3(out, (0, 1, 2)), splits, _ptr(workspace),
         0 if workspace is None else workspace.numel() * workspace.element_size(),
         _stream(q.device)))
     return out
@@ -330,7 +351,9 @@ DECODE_SCRATCH_BYTES = 32 << 20  # CQKV_DECODE_SCRATCH_BYTES
 def decode_attention_noalloc(q: torch.Tensor, k: CacheSide, v: CacheSide, kv_len: int,
                              softmax_scale: float, kv_lens: torch.Tensor | None = None,
                              window_left: int = -1, window_right: int = -1,
-                             out: torch.Tensor | None = None, splits: int = 0) -> torch.Tensor:
+                             out: torch.Tensor | None = None, splits: int = 0,
+                             softcap: float = 0.0,
+                             alibi_slopes: torch.Tensor | None = None) -> torch.Tensor:
     """decode_attention through cqkv_decode_attention_noalloc: no device allocation by the
     library (split partials in its per-GPU device scratch array). `out` must be given for a call
     that may not allocate at all (otherwise torch allocates it here)."""
@@ -347,10 +370,12 @@ def decode_attention_noalloc(q: torch.Tensor, k: CacheSide, v: CacheSide, kv_len
     elif tuple(out.shape) != tuple(q.shape) or out.stride(3) != 1:
         raise CqkvError(ERR_ARG, f"out {tuple(out.shape)} does not match q")
     ks, vs = k.struct(), v.struct()
+    al, al_bs = _alibi_arg(alibi_slopes, b, hq)
     _check(lib().cqkv_decode_attention_noalloc(
         _ptr(q), _DTYPES[q.dtype], _strides3(q, (0, 1, 2)), ctypes.byref(ks), ctypes.byref(vs), b,
-        hq, lq, _ptr(kv_lens), kv_len, softmax_scale, window_left, window_right, _ptr(out),
-        _DTYPES[out.dtype], _strides3(out, (0, 1, 2)), splits, _stream(q.device)))
+        hq, lq, _ptr(kv_lens), kv_len, softmax_scale, window_left, window_right, softcap, al,
+        al_bs, _ptr(out), _DTYPES[out.dtype], _strides3(out, (0, 1, 2)), splits,
+        _stream(q.device)))
     return out
 
 
@@ -372,7 +397,8 @@ def decode_paged_workspace_bytes(blocks, batch: int, q_heads: int, q_len: int) -
 
 def decode_attention_paged(q: torch.Tensor, blocks, softmax_scale: float, window_left: int = -1,
                            window_right: int = -1, out: torch.Tensor | None = None,
-                           workspace: torch.Tensor | None = None) -> torch.Tensor:
+                           workspace: torch.Tensor | None = None, softcap: float = 0.0,
+                           alibi_slopes: torch.Tensor | None = None) -> torch.Tensor:
     """Decode over paged cache blocks [(k_side, v_side, rows), ...]: the keys are the blocks'
     first `rows` tokens concatenated (attention_packed_blocks, candle-nn/src/turbo_quant.rs:
     1082-1114). q (batch, q_heads, q_len, D) -> out of the same shape."""
@@ -390,9 +416,10 @@ def decode_attention_paged(q: torch.Tensor, blocks, softmax_scale: float, window
     elif tuple(out.shape) != tuple(q.shape) or out.stride(3) != 1:
         raise CqkvError(ERR_ARG, f"out {tuple(out.shape)} does not match q")
     arr, _sides = _blocks_struct(blocks)
+    al, al_bs = _alibi_arg(alibi_slopes, b, hq)
     _check(lib().cqkv_decode_attention_paged(
         _ptr(q), _DTYPES[q.dtype], _strides3(q, (0, 1, 2)), arr, len(blocks), b, hq, lq,
-        softmax_scale, window_left, window_right, _ptr(out), _DTYPES[out.dtype],
+        softmax_scale, window_left, window_right, softcap, al, al_bs, _ptr(out), _DTYPES[out.dtype],
         _strides3(out, (0, 1, 2)), _ptr(workspace),
         0 if workspace is None else workspace.numel() * workspace.element_size(),
         _stream(q.device)))
@@ -696,6 +723,40 @@ def qjl_matrix(head_dim: int, seed: int) -> torch.Tensor:
     return s
 
 
+def resolve_rotation(fmt: int, rotation: int, head_dim: int) -> int:
+    """RotationKind::resolve of a side's rotation (cqkv_resolve_rotation)."""
+    r = lib().cqkv_resolve_rotation(fmt, rotation, head_dim)
+    if r < 0:
+        raise CqkvError(ERR_ARG, f"rotation {rotation} at head_dim {head_dim}")
+    return r
+
+
+def rotation_matrix(head_dim: int, kind: int, seed: int) -> torch.Tensor:
+    """rotation_matrix(head_dim, kind, seed) (candle-core/src/accel/turbo.rs:180-233), f32 on the
+    host (cqkv_rotation_matrix)."""
+    m = torch.empty((head_dim, head_dim), dtype=torch.float32)
+    _check(lib().cqkv_rotation_matrix(head_dim, kind, seed, ctypes.c_void_p(m.data_ptr())))
+    return m
+
+
+def dequantize(side: CacheSide, tokens: int, position: int = 0, unrotate: bool = True,
+               dtype: torch.dtype = torch.float32, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Cache positions [position, position + tokens) as (batch, kv_heads, tokens, D) values of
+    `dtype` (cqkv_dequantize_rows): TurboQuantizer::dequantize_rows, unrotated when `unrotate`
+    (candle-nn/src/turbo_quant.rs:250-300)."""
+    if out is None:
+        out = torch.empty((side.batch, side.kv_heads, tokens, side.head_dim), dtype=dtype,
+                          device=side.codes.device)
+    elif (tuple(out.shape) != (side.batch, side.kv_heads, tokens, side.head_dim)
+          or out.stride(3) != 1):
+        raise CqkvError(ERR_ARG, f"out {tuple(out.shape)} does not match the cache side")
+    s = side.struct()
+    _check(lib().cqkv_dequantize_rows(ctypes.byref(s), side.batch, position, tokens, int(unrotate),
+                                      _ptr(out), _DTYPES[out.dtype], _strides3(out, (0, 1, 2)),
+                                      None, 0, _stream(out.device)))
+    return out
+
+
 def turbo_signs(head_dim: int, seed: int):
     import numpy as np
     s = np.zeros(head_dim, dtype=np.float32)
@@ -741,6 +802,7 @@ class TurboKvCache:
             new = CacheSide.empty(old.fmt, old.is_value, old.batch, old.kv_heads, old.head_dim,
                                   cap, dev, old.seed, old.rotation, old.bits)
             new.qjl = old.qjl
+            new.rot = old.rot
             if self._len:
                 side_copy(new, old, self._len)
             sides.append(new)
@@ -780,10 +842,20 @@ class TurboKvCache:
         return out
 
     def attention(self, q: torch.Tensor, softmax_scale: float, window_left: int = -1,
-                  window_right: int = -1, splits: int = 0) -> torch.Tensor:
+                  window_right: int = -1, splits: int = 0, softcap: float = 0.0,
+                  alibi_slopes: torch.Tensor | None = None) -> torch.Tensor:
         """q (batch, q_heads, q_len, head_dim), bottom-right aligned over the cached tokens."""
         if self._len == 0:
             raise CqkvError(ERR_ARG, "turbo-quant cache: attention on an empty cache")
         return decode_attention(q, self.k, self.v, self._len, softmax_scale,
                                 window_left=window_left, window_right=window_right,
-                                splits=splits)
+                                splits=splits, softcap=softcap, alibi_slopes=alibi_slopes)
+
+    def keys_values(self, dtype: torch.dtype = torch.float32):
+        """The cached keys and values (batch, kv_heads, seq_len, head_dim), dequantized and
+        unrotated, in `dtype` (TurboKvCache::keys_values, candle-nn/src/turbo_quant.rs:948-966);
+        None on an empty cache."""
+        if self._len == 0:
+            return None
+        return (dequantize(self.k, self._len, dtype=dtype),
+                dequantize(self.v, self._len, dtype=dtype))

@@ -28,13 +28,15 @@ struct AppendArgs {
     uint32_t codes_plane, scales_plane;  // bytes per (batch, head) plane
     const int32_t *positions;            // device, per batch, or null
     int32_t position, tokens, capacity, kv_heads, x_dtype;
-    int32_t rotate;         // Hadamard-rotate each row before encoding (side_rotates)
-    uint32_t sign_bits[4];  // rotation: bit j set -> column j of the rotation has sign -1
+    int32_t rotate;         // Hadamard-rotate each row before encoding (side_fwht)
+    uint32_t sign_bits[8];  // rotation: bit j set -> column j of the rotation has sign -1
     float rot_scale;        // rotation: 1 / sqrt(D) in f32
     float bnd[16];          // TURBO4: the 15 codebook boundaries (+inf padded); TURBOPROD: 7
     int32_t turbo_sym;      // TURBO4: bnd[7] == 0 and bnd[14 - i] == -bnd[i] (a symmetric codebook)
     float cent[16];         // TURBOPROD: the centroids of its (bits - 1)-bit codebook
-    const float *qjl;       // TURBOPROD: device D x D QJL matrix S (row-major)
+    const float *qjl;       // TURBOPROD: device D x D QJL matrix S (row-major, the plane row
+                            // length D; zero rows and columns past the head dim)
+    int32_t dim;            // the head dim (TURBOPROD: residuals past it are zero)
     int32_t pair_loads;     // elements 2l, 2l+1 of every row are one aligned 4 / 8-byte word
     int32_t row_loads;      // rows_block: kRowBF16 / kRowF16 / kRowF32 (16-byte loads) or kRowAny
     const void *cos, *sin;  // rotary tables (cs_rows, D/2) in the dtype of x (fused RoPE only)
@@ -189,22 +191,31 @@ __device__ inline uint32_t quad_xor_u(uint32_t v) {
     constexpr int ctrl = M == 1 ? 0xB1 : 0x4E;
     return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, ctrl, 0xF, 0xF, true);
 }
+// v from the lane `lane ^ 4` (the partner quad of a row of 8 threads at D = 256), by
+// ds_swizzle in bit-mask mode (and 0x1f, xor 4)
+__device__ inline uint32_t xor4_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x101F);
+}
+__device__ inline float xor4(float v) { return __uint_as_float(xor4_u(__float_as_uint(v))); }
 template <int R>
 __device__ inline float row_max(float v) {
     v = fmaxf(v, quad_xor<1>(v));
-    if constexpr (R == 4) v = fmaxf(v, quad_xor<2>(v));
+    if constexpr (R >= 4) v = fmaxf(v, quad_xor<2>(v));
+    if constexpr (R == 8) v = fmaxf(v, xor4(v));
     return v;
 }
 template <int R>
 __device__ inline float row_sum(float v) {
     v += quad_xor<1>(v);
-    if constexpr (R == 4) v += quad_xor<2>(v);
+    if constexpr (R >= 4) v += quad_xor<2>(v);
+    if constexpr (R == 8) v += xor4(v);
     return v;
 }
 template <int R>
 __device__ inline uint32_t row_or(uint32_t v) {
     v |= quad_xor_u<1>(v);
-    if constexpr (R == 4) v |= quad_xor_u<2>(v);
+    if constexpr (R >= 4) v |= quad_xor_u<2>(v);
+    if constexpr (R == 8) v |= xor4_u(v);
     return v;
 }
 
@@ -330,8 +341,8 @@ __device__ inline void rope_row32(const AppendArgs &a, int64_t p, int q, bool li
 // y = H (sign * x) / sqrt(D) of this thread's 32 elements of a row (rotation_matrix(D, Hadamard,
 // seed), candle-core/src/accel/turbo.rs:180-203, applied as TurboQuantizer::rotate does,
 // candle-nn/src/turbo_quant.rs:182-189): the sign flip, the Walsh-Hadamard stages in element-stride
-// order 1, 2, ..., D / 2 (1..16 in the thread, 32 and 64 across the row's threads by DPP), then
-// 1 / sqrt(D).
+// order 1, 2, ..., D / 2 (1..16 in the thread, 32 and 64 across the row's threads by DPP, 128
+// by ds_swizzle), then 1 / sqrt(D).
 template <int D>
 __device__ inline void hadamard_row32(const AppendArgs &a, int q, float (&x)[32]) {
     constexpr int R = D / 32;
@@ -353,10 +364,15 @@ __device__ inline void hadamard_row32(const AppendArgs &a, int q, float (&x)[32]
 #pragma unroll
         for (int i = 0; i < 32; ++i) x[i] = __builtin_fmaf(sg, x[i], quad_xor<1>(x[i]));
     }
-    if constexpr (R == 4) {
+    if constexpr (R >= 4) {
         const float sg = (q & 2) ? -1.0f : 1.0f;  // stride 64: partner thread q ^ 2
 #pragma unroll
         for (int i = 0; i < 32; ++i) x[i] = __builtin_fmaf(sg, x[i], quad_xor<2>(x[i]));
+    }
+    if constexpr (R == 8) {
+        const float sg = (q & 4) ? -1.0f : 1.0f;  // stride 128: partner thread q ^ 4
+#pragma unroll
+        for (int i = 0; i < 32; ++i) x[i] = __builtin_fmaf(sg, x[i], xor4(x[i]));
     }
 #pragma unroll
     for (int i = 0; i < 32; ++i) x[i] *= a.rot_scale;
@@ -396,7 +412,8 @@ __device__ inline void prod_qjl(const AppendArgs &a, const float (&x)[32], float
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
         const uint32_t code = (cw[i / 8] >> (4 * (i % 8))) & 15u;
-        res[i] = live ? x[i] * inv - sm_cent[code] : 0.0f;
+        // elements past the head dim (zero padding) have no residual
+        res[i] = live && 32 * q + i < a.dim ? x[i] * inv - sm_cent[code] : 0.0f;
         rr += res[i] * res[i];
     }
     const float r1 = __builtin_sqrtf(row_sum<R>(rr));
@@ -415,10 +432,67 @@ __device__ inline void prod_qjl(const AppendArgs &a, const float (&x)[32], float
     }
     if (live && q == 0) ((float *)(scales + (int64_t)a.capacity * 4))[t] = r1;
     const int lane = tid & 63, wave = tid >> 6, n = lane & 15, g = lane >> 4;
+    const int o0 = wave * (D / 4);
+    const int pos = a.positions ? a.positions[blockIdx.z] : a.position;
+    int end = min(pos + a.tokens, a.capacity);
+    if (a.cs_rows > 0) end = min(end, a.cs_rows);
+    const int c0 = t - r;  // the block's first cache position
+    uint8_t *signs = scales + (int64_t)a.capacity * 8;
+    if constexpr (D == 256) {
+        // S does not fit the registers whole at D = 256 (256 VGPRs of operands): one 16-output
+        // block of the wavefront's rows at a time, every row block against it; the 64 sign bits
+        // of a row gather in a 64-bit word
+        __syncthreads();
+        uint64_t words[NR / 16];
+#pragma unroll
+        for (int rb = 0; rb < NR / 16; ++rb) words[rb] = 0;
+#pragma unroll 1
+        for (int bo = 0; bo < NB; ++bo) {
+            f16x8 shi[NC], slo[NC];
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const float *src = a.qjl + (int64_t)(o0 + 16 * bo + n) * D + 32 * c + 8 * g;
+                const f32x4 v0 = *(const f32x4 *)src, v1 = *(const f32x4 *)(src + 4);
+                const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+                f16_split8(v, shi[c], slo[c]);
+            }
+#pragma unroll
+            for (int rb = 0; rb < NR / 16; ++rb) {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                const uint16_t *hrow = sm_r + (16 * rb + n) * LD + 8 * g;
+                const uint16_t *lrow = sm_r + (NR + 16 * rb + n) * LD + 8 * g;
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    const f16x8 rhi = *(const f16x8 *)(hrow + 32 * c), rlo = *(const f16x8 *)(lrow + 32 * c);
+                    acc = mfma16x16x32(shi[c], rhi, acc);
+                    acc = mfma16x16x32(shi[c], rlo, acc);
+                    acc = mfma16x16x32(slo[c], rhi, acc);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    words[rb] |= (uint64_t)(acc[i] >= 0.0f ? 1u : 0u) << (16 * bo + 4 * g + i);
+            }
+        }
+#pragma unroll
+        for (int rb = 0; rb < NR / 16; ++rb) {
+            uint32_t lo = (uint32_t)words[rb], hi = (uint32_t)(words[rb] >> 32);
+            lo |= (uint32_t)__shfl_xor((int)lo, 16, 64);
+            hi |= (uint32_t)__shfl_xor((int)hi, 16, 64);
+            lo |= (uint32_t)__shfl_xor((int)lo, 32, 64);
+            hi |= (uint32_t)__shfl_xor((int)hi, 32, 64);
+            // outputs past the head dim (zero rows of the padded S): no sign bits
+            const int valid = a.dim - o0;
+            if (valid < 32) lo &= valid <= 0 ? 0u : (1u << valid) - 1u;
+            if (valid < 64) hi &= valid <= 32 ? 0u : (1u << (valid - 32)) - 1u;
+            const int tr = c0 + 16 * rb + n;
+            if (g == 0 && tr >= pos && tr < end)
+                *(u32x2 *)(signs + (int64_t)tr * (D / 8) + wave * (D / 32)) = u32x2{lo, hi};
+        }
+        return;
+    }
     // this wavefront's rows of S as A operands: lane (m, g) of block bo, chunk c holds
     // S[o0 + 16 bo + m][32 c + 8 g .. + 7]
     f16x8 shi[NB][NC], slo[NB][NC];
-    const int o0 = wave * (D / 4);
 #pragma unroll
     for (int bo = 0; bo < NB; ++bo)
 #pragma unroll
@@ -429,11 +503,6 @@ __device__ inline void prod_qjl(const AppendArgs &a, const float (&x)[32], float
             f16_split8(v, shi[bo][c], slo[bo][c]);
         }
     __syncthreads();
-    const int pos = a.positions ? a.positions[blockIdx.z] : a.position;
-    int end = min(pos + a.tokens, a.capacity);
-    if (a.cs_rows > 0) end = min(end, a.cs_rows);
-    const int c0 = t - r;  // the block's first cache position
-    uint8_t *signs = scales + (int64_t)a.capacity * 8;
 #pragma unroll 1
     for (int rb = 0; rb < NR / 16; ++rb) {
         f32x4 acc[NB];
@@ -459,6 +528,9 @@ __device__ inline void prod_qjl(const AppendArgs &a, const float (&x)[32], float
             for (int i = 0; i < 4; ++i) word |= (acc[bo][i] >= 0.0f ? 1u : 0u) << (16 * bo + 4 * g + i);
         word |= (uint32_t)__shfl_xor((int)word, 16, 64);
         word |= (uint32_t)__shfl_xor((int)word, 32, 64);
+        // outputs past the head dim (zero rows of the padded S): no sign bits
+        const int valid = a.dim - o0;
+        if (valid < D / 4) word &= valid <= 0 ? 0u : (1u << valid) - 1u;
         const int tr = c0 + 16 * rb + n;
         if (g == 0 && tr >= pos && tr < end) {
             uint8_t *dst = signs + (int64_t)tr * (D / 8) + wave * (D / 32);
@@ -695,6 +767,11 @@ __device__ inline void rows_block(const AppendArgs &a, int h, int b, int bx) {
         }
         tok_scale = norm;
         if constexpr (kProd) prod_qjl<D, NR>(a, x, inv, cw, live, t, r, q, scales, sm_resid, sm_cent);
+        if (32 * q + 32 > a.dim) {  // elements past the head dim (zero padding): zero codes
+#pragma unroll
+            for (int i = 0; i < 32; ++i)
+                if (32 * q + i >= a.dim) cw[i / 8] &= ~(15u << (4 * (i % 8)));
+        }
     }
 
     // ---- scales ----
@@ -703,19 +780,25 @@ __device__ inline void rows_block(const AppendArgs &a, int h, int b, int bx) {
         if (live && q == 0) ((float *)(scales + (int64_t)a.capacity * kBlockBytes))[t] = tok_scale;
     }
     if constexpr (FMT == CQKV_FMT_MXFP4 || FMT == CQKV_FMT_MXFP8) {
-        const uint32_t word = row_or<R>(blk << (8 * q));  // block q's byte at byte q
-        if (live && q == 0) {
-            if constexpr (R == 4) *(uint32_t *)(scales + (int64_t)t * 4) = word;
-            else *(uint16_t *)(scales + (int64_t)t * 2) = (uint16_t)word;
+        // block q's byte at byte q of the token's D / 32
+        const uint32_t lo = row_or<R>(q < 4 ? blk << (8 * q) : 0u);
+        if constexpr (R == 8) {
+            const uint32_t hi = row_or<R>(q >= 4 ? blk << (8 * (q - 4)) : 0u);
+            if (live && q == 0) *(u32x2 *)(scales + (int64_t)t * 8) = u32x2{lo, hi};
+        } else if (live && q == 0) {
+            if constexpr (R == 4) *(uint32_t *)(scales + (int64_t)t * 4) = lo;
+            else *(uint16_t *)(scales + (int64_t)t * 2) = (uint16_t)lo;
         }
     }
     if constexpr (FMT == CQKV_FMT_NVFP4) {
-        // blocks 2q, 2q + 1: bytes 2q, 2q + 1 of the token's D / 16
-        const uint32_t lo = row_or<R>(q < 2 ? blk << (16 * q) : 0u);
-        const uint32_t hi = row_or<R>(q >= 2 ? blk << (16 * (q - 2)) : 0u);
+        // blocks 2q, 2q + 1: bytes 2q, 2q + 1 of the token's D / 16; word w from threads 2w, 2w + 1
+        uint32_t w[R / 2];
+#pragma unroll
+        for (int k = 0; k < R / 2; ++k) w[k] = row_or<R>(q / 2 == k ? blk << (16 * (q % 2)) : 0u);
         if (live && q == 0) {
-            if constexpr (R == 4) *(u32x2 *)(scales + (int64_t)t * 8) = u32x2{lo, hi};
-            else *(uint32_t *)(scales + (int64_t)t * 4) = lo;
+            if constexpr (R == 8) *(u32x4 *)(scales + (int64_t)t * 16) = u32x4{w[0], w[1], w[2], w[3]};
+            else if constexpr (R == 4) *(u32x2 *)(scales + (int64_t)t * 8) = u32x2{w[0], w[1]};
+            else *(uint32_t *)(scales + (int64_t)t * 4) = w[0];
         }
     }
 
@@ -769,17 +852,22 @@ inline void launch_rows(const cqkv_side *s, int32_t tokens, int32_t batch, hipSt
     if constexpr (FMT == CQKV_FMT_TURBO4) {
         if (turbo_mfma_launch(s, tokens, batch, st, a)) return;
     }
-    const int rows = 256 / (s->head_dim / 32);
+    const int dk = kernel_dim(s->head_dim);
+    const int rows = 256 / (dk / 32);
     const dim3 grid((unsigned)(((int64_t)tokens + 7 + rows - 1) / rows), s->kv_heads, batch);
     if constexpr (FMT == CQKV_FMT_TURBOPROD) {  // keys only (check_side refuses value sides)
-        if (s->head_dim == 64) launch_rows_d<FMT, 0, 64>(a.row_loads, grid, st, a);
-        else launch_rows_d<FMT, 0, 128>(a.row_loads, grid, st, a);
-    } else if (s->head_dim == 64) {
+        if (dk == 64) launch_rows_d<FMT, 0, 64>(a.row_loads, grid, st, a);
+        else if (dk == 128) launch_rows_d<FMT, 0, 128>(a.row_loads, grid, st, a);
+        else launch_rows_d<FMT, 0, 256>(a.row_loads, grid, st, a);
+    } else if (dk == 64) {
         if (s->is_value) launch_rows_d<FMT, 1, 64>(a.row_loads, grid, st, a);
         else launch_rows_d<FMT, 0, 64>(a.row_loads, grid, st, a);
-    } else {
+    } else if (dk == 128) {
         if (s->is_value) launch_rows_d<FMT, 1, 128>(a.row_loads, grid, st, a);
         else launch_rows_d<FMT, 0, 128>(a.row_loads, grid, st, a);
+    } else {
+        if (s->is_value) launch_rows_d<FMT, 1, 256>(a.row_loads, grid, st, a);
+        else launch_rows_d<FMT, 0, 256>(a.row_loads, grid, st, a);
     }
 }
 

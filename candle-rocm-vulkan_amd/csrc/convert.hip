@@ -26,18 +26,25 @@ struct ConvertArgs {
     uint32_t *rows;  // (batch, kv_heads, tokens, row_words)
     uint8_t *codes, *scales;
     uint32_t codes_plane, scales_plane;
-    int32_t kv_heads, tokens, position, row_words, format, is_value, head_dim;
+    int32_t kv_heads, tokens, position, row_words, format, is_value;
+    int32_t dk;           // plane row length (64, 128, 256)
+    int32_t dim;          // head dim (<= dk): the reference row's elements
     int32_t b8;           // 8-bit codes (FP8, MXFP8), else 4-bit
-    int32_t nblk;         // block scale bytes per token (MX, NVFP4), else 0
+    int32_t nblk;         // block scale bytes per token in the plane (MX, NVFP4), else 0
+    int32_t nblk_ref;     // ... in the reference row (blocks of the head dim)
     int32_t tok_scale;    // an f32 per token (FP8, TURBO4, NVFP4), after the block bytes
     int32_t capacity;
     int32_t cbits;        // TurboQuant codes packed at cbits < 4 per element, or TURBOPROD; else 0
 };
 
+// One workgroup of max(64, dk / 2) threads per 8-token tile of a (batch, head) plane; thread l
+// owns elements 2l, 2l+1 of the plane row, so the value tiles are read and written whole by one
+// thread (no cross-thread read-modify-write). Elements past the head dim are zero codes in the
+// plane and absent from the reference row (whose last code / sign word is zero-filled).
 template <bool EXPORT>
-__global__ __launch_bounds__(64) void convert_kernel(ConvertArgs a) {
+__global__ __launch_bounds__(128) void convert_kernel(ConvertArgs a) {
     const int lane = threadIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int D = a.head_dim;
+    const int D = a.dk, dim = a.dim;
     const int tile = a.position / 8 + (int)blockIdx.x;
     const int t_lo = max(tile * 8, a.position), t_hi = min(tile * 8 + 8, a.position + a.tokens);
     if (t_lo >= t_hi) return;
@@ -46,11 +53,12 @@ __global__ __launch_bounds__(64) void convert_kernel(ConvertArgs a) {
     const int64_t plane = (int64_t)b * a.kv_heads + h;
     uint8_t *codes = a.codes + plane * a.codes_plane;
     uint8_t *scales = a.scales + plane * a.scales_plane;
-    const int code_words = fp8 ? D / 4 : D / 8;
-    const int nb = a.nblk, aux_words = (nb + 3) / 4;
+    const int code_words = fp8 ? (dim + 3) / 4 : (dim + 7) / 8;
+    const int nb = a.nblk, nbr = a.nblk_ref, aux_words = (nbr + 3) / 4;
     float *tscale = (float *)(scales + (int64_t)a.capacity * nb);
+    const bool in0 = 2 * lane < dim, in1 = 2 * lane + 1 < dim;  // real elements of this thread
 
-    // value tile words of this lane (elements 2l, 2l+1)
+    // value tile words of this thread (elements 2l, 2l+1)
     uint64_t vw0 = 0, vw1 = 0;
     uint32_t vn0 = 0, vn1 = 0;
     if (a.is_value && active) {
@@ -66,17 +74,21 @@ __global__ __launch_bounds__(64) void convert_kernel(ConvertArgs a) {
     }
     if (a.cbits) {  // TurboQuant codes of cbits < 4 bits, or TURBOPROD: nibbles <-> packed bits
         __shared__ uint8_t sm_c[256];
-        const int cb = a.cbits, cw = (D * cb + 31) / 32;
+        const int cb = a.cbits, cw = (dim * cb + 31) / 32;
         const bool prod = a.format == CQKV_FMT_TURBOPROD;
-        const int sw = prod ? D / 32 : 0;
+        const int sw = prod ? (dim + 31) / 32 : 0;  // sign words of the reference row
+        // TurboProd: |r| and the sign words follow the norms (TurboMse sides end at the norms)
         const float *r1 = (const float *)(scales + (int64_t)a.capacity * 4);
         uint32_t *signs = (uint32_t *)(scales + (int64_t)a.capacity * 8);
+        const int swp = prod ? D / 32 : 0;  // sign words per token in the plane
         const uint32_t mask = (1u << cb) - 1u;
+        // sign bits of the last reference word past the head dim are zero
+        const uint32_t last_mask = dim % 32 ? (1u << (dim % 32)) - 1u : ~0u;
         for (int t = t_lo; t < t_hi; ++t) {
             uint32_t *row = a.rows + ((plane * a.tokens) + (t - a.position)) * (int64_t)a.row_words;
             const int s = t & 7;
             if (EXPORT) {
-                if (active) {  // this lane's codes of elements 2 lane, 2 lane + 1
+                if (active) {  // this thread's codes of elements 2 lane, 2 lane + 1
                     uint32_t c0, c1;
                     if (!a.is_value) {
                         const uint32_t by = codes[(int64_t)t * (D / 2) + lane];
@@ -92,7 +104,7 @@ __global__ __launch_bounds__(64) void convert_kernel(ConvertArgs a) {
                 __syncthreads();
                 if (lane < cw) {  // word `lane`: bits [32 lane, 32 lane + 32) of the packed codes
                     uint32_t w = 0;
-                    const int j0 = (32 * lane) / cb, j1 = min((32 * lane + 31) / cb, D - 1);
+                    const int j0 = (32 * lane) / cb, j1 = min((32 * lane + 31) / cb, dim - 1);
                     for (int j = j0; j <= j1; ++j) {
                         const uint32_t c = sm_c[j];
                         const int bit = cb * j - 32 * lane;  // -(cb - 1) .. 31
@@ -101,7 +113,10 @@ __global__ __launch_bounds__(64) void convert_kernel(ConvertArgs a) {
                     row[lane] = w;
                 }
                 __syncthreads();
-                if (lane < sw) row[cw + lane] = signs[(int64_t)t * sw + lane];
+                if (lane < sw) {
+                    const uint32_t w = signs[(int64_t)t * swp + lane];
+                    row[cw + lane] = lane == sw - 1 ? w & last_mask : w;
+                }
                 if (lane == 0) {
                     row[cw + sw] = __float_as_uint(tscale[t]);
                     row[cw + sw + 1] = prod ? __float_as_uint(r1[t]) : 0u;
@@ -110,6 +125,8 @@ __global__ __launch_bounds__(64) void convert_kernel(ConvertArgs a) {
                 if (active) {  // elements 2 lane, 2 lane + 1
                     uint32_t c[2];
                     for (int e = 0; e < 2; ++e) {
+                        c[e] = 0;
+                        if (2 * lane + e >= dim) continue;
                         const int pos = cb * (2 * lane + e);
                         const uint64_t two = (uint64_t)row[pos >> 5] |
                                              ((pos >> 5) + 1 < cw ? (uint64_t)row[(pos >> 5) + 1] << 32 : 0ull);
@@ -122,7 +139,10 @@ __global__ __launch_bounds__(64) void convert_kernel(ConvertArgs a) {
                         vn1 = (vn1 & ~(15u << (4 * s))) | (c[1] << (4 * s));
                     }
                 }
-                if (lane < sw) signs[(int64_t)t * sw + lane] = row[cw + lane];
+                if (prod && lane < swp) {  // only TurboProd sides have a sign area
+                    const uint32_t w = lane < sw ? row[cw + lane] : 0u;
+                    signs[(int64_t)t * swp + lane] = lane == sw - 1 ? w & last_mask : w;
+                }
                 if (lane == 0) {
                     tscale[t] = __uint_as_float(row[cw + sw]);
                     if (prod) ((float *)r1)[t] = __uint_as_float(row[cw + sw + 1]);
@@ -159,20 +179,23 @@ __global__ __launch_bounds__(64) void convert_kernel(ConvertArgs a) {
                     c0 = (vn0 >> (4 * s)) & 15u;
                     c1 = (vn1 >> (4 * s)) & 15u;
                 }
+                if (!in0) c0 = 0;  // the zero fill of the last code word
+                if (!in1) c1 = 0;
+                // bytes of the code words only (past them lie the aux and scale words)
                 if (fp8) {
-                    rowb[2 * lane] = (uint8_t)c0;
-                    rowb[2 * lane + 1] = (uint8_t)c1;
-                } else {
+                    if (2 * lane < 4 * code_words) rowb[2 * lane] = (uint8_t)c0;
+                    if (2 * lane + 1 < 4 * code_words) rowb[2 * lane + 1] = (uint8_t)c1;
+                } else if (lane < 4 * code_words) {
                     rowb[lane] = (uint8_t)(c0 | (c1 << 4));
                 }
             } else {
-                uint32_t c0, c1;
+                uint32_t c0 = 0, c1 = 0;
                 if (fp8) {
-                    c0 = rowb[2 * lane];
-                    c1 = rowb[2 * lane + 1];
+                    if (in0) c0 = rowb[2 * lane];
+                    if (in1) c1 = rowb[2 * lane + 1];
                 } else {
-                    c0 = rowb[lane] & 15u;
-                    c1 = rowb[lane] >> 4;
+                    if (in0) c0 = rowb[lane] & 15u;
+                    if (in1) c1 = rowb[lane] >> 4;
                 }
                 if (!a.is_value) {
                     if (fp8) {
@@ -195,13 +218,13 @@ __global__ __launch_bounds__(64) void convert_kernel(ConvertArgs a) {
             uint32_t *rsc = aux + aux_words;
             if (EXPORT) {
                 for (int w = 0; w < aux_words; ++w) aux[w] = 0;
-                for (int k = 0; k < nb; ++k)
+                for (int k = 0; k < nbr; ++k)
                     aux[k >> 2] |= (uint32_t)scales[(int64_t)t * nb + k] << (8 * (k & 3));
                 rsc[0] = a.tok_scale ? __float_as_uint(tscale[t]) : __float_as_uint(1.0f);
                 rsc[1] = 0;
             } else {
-                for (int k = 0; k < nb; ++k)
-                    scales[(int64_t)t * nb + k] = (uint8_t)(aux[k >> 2] >> (8 * (k & 3)));
+                for (int k = 0; k < nb; ++k)  // blocks past the head dim: zero scales
+                    scales[(int64_t)t * nb + k] = k < nbr ? (uint8_t)(aux[k >> 2] >> (8 * (k & 3))) : 0;
                 if (a.tok_scale) tscale[t] = __uint_as_float(rsc[0]);
             }
         }
@@ -240,15 +263,18 @@ static int convert(const cqkv_side *side, uint32_t *rows, int32_t batch, int32_t
     a.row_words = cqkv_reference_row_words(side->format, side->bits, side->head_dim);
     a.format = side->format;
     a.b8 = code_bits(side->format) == 8 ? 1 : 0;
-    a.nblk = block_elems(side->format) ? side->head_dim / block_elems(side->format) : 0;
     a.tok_scale = token_scale(side->format) ? 1 : 0;
     a.capacity = side->capacity;
     a.is_value = side->is_value;
-    a.head_dim = side->head_dim;
+    a.dim = side->head_dim;
+    a.dk = kernel_dim(side->head_dim);
+    a.nblk = block_elems(side->format) ? a.dk / block_elems(side->format) : 0;
+    a.nblk_ref = block_elems(side->format) ? a.dim / block_elems(side->format) : 0;
     a.cbits = side->format == CQKV_FMT_TURBOPROD || turbo_code_bits(side) < 4 ? turbo_code_bits(side) : 0;
     dim3 grid((tokens + 7) / 8 + 1, side->kv_heads, batch);
-    if (to_rows) hipLaunchKernelGGL(convert_kernel<true>, grid, dim3(64), 0, st, a);
-    else hipLaunchKernelGGL(convert_kernel<false>, grid, dim3(64), 0, st, a);
+    const dim3 block(a.dk == 256 ? 128 : 64);
+    if (to_rows) hipLaunchKernelGGL(convert_kernel<true>, grid, block, 0, st, a);
+    else hipLaunchKernelGGL(convert_kernel<false>, grid, block, 0, st, a);
     CQKV_HIP_CHECK(hipGetLastError());
     return CQKV_OK;
 }
@@ -284,7 +310,7 @@ extern "C" int cqkv_side_copy(const cqkv_side *dst, const cqkv_side *src, int32_
     if (int rc = check_side(src, who)) return rc;
     if (dst->format != src->format || dst->is_value != src->is_value ||
         dst->head_dim != src->head_dim || dst->kv_heads != src->kv_heads ||
-        side_rotates(dst) != side_rotates(src) || side_bits(dst) != side_bits(src) ||
+        side_rotation(dst) != side_rotation(src) || side_bits(dst) != side_bits(src) ||
         ((side_rotates(src) || src->format == CQKV_FMT_TURBOPROD) && dst->seed != src->seed))
         return fail(CQKV_ERR_ARG,
                     "%s: sides differ in format, bits, side, head dim, kv heads, rotation or seed", who);
@@ -292,16 +318,16 @@ extern "C" int cqkv_side_copy(const cqkv_side *dst, const cqkv_side *src, int32_
         return fail(CQKV_ERR_ARG, "%s: batch %d, %d tokens for capacities %d -> %d", who, batch,
                     tokens, src->capacity, dst->capacity);
     if (tokens == 0) return CQKV_OK;
-    const int fmt = src->format, d = src->head_dim;
+    const int fmt = src->format, d = kernel_dim(src->head_dim);  // the plane row length
     const size_t planes = (size_t)batch * src->kv_heads;
     const size_t row_bytes = (size_t)d * code_bits(fmt) / 8;
     // values: whole 8-token tiles, at most the smaller capacity (both are multiples of 32)
     const int ctok = src->is_value ? std::min((tokens + 7) / 8 * 8, std::min(src->capacity, dst->capacity))
                                    : tokens;
-    const size_t src_cp = cqkv_codes_plane_bytes(fmt, d, src->capacity);
-    const size_t dst_cp = cqkv_codes_plane_bytes(fmt, d, dst->capacity);
-    const size_t src_sp = cqkv_scales_plane_bytes(fmt, d, src->capacity);
-    const size_t dst_sp = cqkv_scales_plane_bytes(fmt, d, dst->capacity);
+    const size_t src_cp = cqkv_codes_plane_bytes(fmt, src->head_dim, src->capacity);
+    const size_t dst_cp = cqkv_codes_plane_bytes(fmt, src->head_dim, dst->capacity);
+    const size_t src_sp = cqkv_scales_plane_bytes(fmt, src->head_dim, src->capacity);
+    const size_t dst_sp = cqkv_scales_plane_bytes(fmt, src->head_dim, dst->capacity);
     const size_t bb = block_elems(fmt) ? (size_t)d / block_elems(fmt) : 0;  // block bytes per token
     const hipStream_t st = (hipStream_t)stream;
     CQKV_HIP_CHECK(hipMemcpy2DAsync(dst->codes, dst_cp, src->codes, src_cp, row_bytes * ctok,

@@ -244,6 +244,19 @@ __device__ inline bf16x8 fp8x8_scaled_bf16x8(uint32_t w0, uint32_t w1, const flo
 // ---------------------------------------------------------------------------------------------
 // Cross-lane helpers (ds_bpermute based shuffles; wave64)
 // ---------------------------------------------------------------------------------------------
+// The reference's score terms (fa_logit / tq_logit, candle-core/kernels/flash_attn_impl.h:42-47,
+// turbo_quant_impl.h:37-41) on a score x in exp2 units (x = s log2(e)): soft-capping
+// cap tanh(s / cap), as cap2 - 2 cap2 / (2^(2 x log2(e) / cap2) + 1) with cap2 = cap log2(e),
+// then ALiBi -slope |dist| with slope2 = slope log2(e). cap2 = 0 / slope2 = 0 switch them off.
+__device__ inline float fa_logit2(float x, float cap2, float slope2, int dist) {
+    if (cap2 > 0.0f) {
+        const float e = __builtin_amdgcn_exp2f(x * (2.0f * kLog2e / cap2));
+        x = cap2 - 2.0f * cap2 * __builtin_amdgcn_rcpf(e + 1.0f);
+    }
+    if (slope2 != 0.0f) x -= slope2 * (float)(dist < 0 ? -dist : dist);
+    return x;
+}
+
 __device__ inline float shfl_xor(float v, int m) { return __shfl_xor(v, m, kWave); }
 __device__ inline float group16_max(float v) {  // max over lanes sharing lane % 16
     v = fmaxf(v, shfl_xor(v, 16));

@@ -56,7 +56,19 @@ inline bool is_turbo(int32_t format) {
     return format == CQKV_FMT_TURBO4 || format == CQKV_FMT_TURBOPROD;
 }
 
-inline bool supported_dim(int32_t d) { return d == 64 || d == 128; }
+// Plane row length of head dim d: the smallest of 64, 128, 256 that holds it (0 past 256). The
+// kernels are instantiated at these lengths; elements past d are zero codes.
+inline int kernel_dim(int32_t d) { return d < 1 ? 0 : d <= 64 ? 64 : d <= 128 ? 128 : d <= 256 ? 256 : 0; }
+
+// Head dims a cache side of `format` takes: 1-256 (the reference's fused attention bound,
+// FA_MAX_HEAD_DIM), MX formats a multiple of 32 and NVFP4 of 16 (QuantFormat::validate,
+// candle-core/src/accel/formats.rs:166-187).
+inline bool supported_dim(int32_t format, int32_t d) {
+    if (d < 1 || d > 256) return false;
+    if ((format == CQKV_FMT_MXFP4 || format == CQKV_FMT_MXFP8) && d % 32 != 0) return false;
+    if (format == CQKV_FMT_NVFP4 && d % 16 != 0) return false;
+    return true;
+}
 
 // TurboQuant width of a side (QuantFormat::TurboMse{bits} / TurboProd{bits}; 0 selects 4), 0 for
 // the other formats.
@@ -73,10 +85,38 @@ inline int turbo_code_bits(const cqkv_side *s) {
     return s->format == CQKV_FMT_TURBOPROD ? side_bits(s) - 1 : side_bits(s);
 }
 
-// The side's rows are Hadamard-rotated before quantization (CQKV_ROT_DEFAULT: TURBO4 only).
+// RotationKind::resolve (candle-core/src/accel/config.rs:131-138) of a side's rotation at head
+// dim d: CQKV_ROT_NONE, CQKV_ROT_HADAMARD or CQKV_ROT_DENSE; DEFAULT is AUTO for the TurboQuant
+// formats and NONE for the others; -1 for an unknown kind.
+inline int resolve_rotation(int32_t format, int32_t kind, int32_t d) {
+    const bool pow2 = d > 0 && (d & (d - 1)) == 0;
+    switch (kind) {
+    case CQKV_ROT_DEFAULT:
+        return is_turbo(format) ? (pow2 ? CQKV_ROT_HADAMARD : CQKV_ROT_DENSE) : CQKV_ROT_NONE;
+    case CQKV_ROT_NONE: return CQKV_ROT_NONE;
+    case CQKV_ROT_AUTO:
+    case CQKV_ROT_HADAMARD: return pow2 ? CQKV_ROT_HADAMARD : CQKV_ROT_DENSE;
+    case CQKV_ROT_DENSE: return CQKV_ROT_DENSE;
+    default: return -1;
+    }
+}
+inline int side_rotation(const cqkv_side *s) { return resolve_rotation(s->format, s->rotation, s->head_dim); }
+
+// The side's rows are rotated before quantization.
 inline bool side_rotates(const cqkv_side *s) {
-    return s->rotation == CQKV_ROT_HADAMARD ||
-           (s->rotation == CQKV_ROT_DEFAULT && is_turbo(s->format));
+    const int r = side_rotation(s);
+    return r == CQKV_ROT_HADAMARD || r == CQKV_ROT_DENSE;
+}
+// ... by the in-register Walsh-Hadamard transform (a Hadamard side whose head dim is a plane row
+// length); the other rotating sides multiply by their matrix cqkv_side.rot.
+inline bool side_fwht(const cqkv_side *s) {
+    return side_rotation(s) == CQKV_ROT_HADAMARD && s->head_dim == kernel_dim(s->head_dim);
+}
+inline bool side_matrix_rot(const cqkv_side *s) { return side_rotates(s) && !side_fwht(s); }
+// The side's rows reach the encoders through the f32 staging pass (rowmat.hip): rotation by the
+// matrix, or a head dim shorter than the plane row (zero padding).
+inline bool side_staged(const cqkv_side *s) {
+    return side_matrix_rot(s) || s->head_dim != kernel_dim(s->head_dim);
 }
 
 // Validates a cache side; returns CQKV_OK or an error (message set).
@@ -86,6 +126,7 @@ int check_side(const cqkv_side *s, const char *what);
 int turbo_codebook(int dim, int bits, float *centroids, float *boundaries);
 void turbo_signs(int dim, uint64_t seed, float *signs);
 void qjl_matrix(int dim, uint64_t seed, float *out);
+void rotation_matrix(int dim, int kind, uint64_t seed, float *out);
 
 // The dense / variable-length flash attention (prefill_attn.hip) behind cqkv_flash_attn_ext and
 // the FP8 K / V path: dtype is q's and out's, kv_dtype K's and V's (dtype itself, or with f32

@@ -5,6 +5,7 @@
 #include <vector>
 
 #include "decode_kernels.h"
+#include "rowmat.h"
 
 namespace cqkv {
 
@@ -13,71 +14,105 @@ struct CombineArgs {
     int32_t splits, rows, q_heads, q_len, out_dtype, rotate;
     void *out;
     int64_t o_sb, o_sh, o_si;
-    uint32_t vsign_bits[4];
+    uint32_t vsign_bits[8];
     float rot_scale;
+    int32_t head_dim;  // outputs past it (plane row padding) are not written
 };
 
 // Split combine (the formula of tq_combine_impl, candle-core/kernels/turbo_quant_impl.h:659-685,
 // in the log2 domain): o = sum_s w_s o_s / sum_s w_s, w_s = 2^(lse_s - max lse), empty splits
-// skipped; then, for TurboQuant values, x = sign * (H o) / sqrt(D) (the unrotation y Pi).
-// One wavefront per output row (lane l: head dims 2l, 2l+1), four rows per workgroup; the
-// split loop keeps up to 8 splits' loads in flight.
+// skipped; then, for values with the in-register Hadamard rotation, x = sign * (H o) / sqrt(D)
+// (the unrotation y Pi). One wavefront per output row (lane l: head dims 2l, 2l+1, and
+// 128 + 2l, 129 + 2l at D = 256), four rows per workgroup; the split loop keeps up to 8 splits'
+// loads in flight.
 template <int D>
 __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
+    constexpr int NP = D == 256 ? 2 : 1;  // element pairs per lane
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= a.rows) return;
-    const bool active = lane < D / 2;
+    const bool active = lane < D / 2 / NP;
     const float *lse = a.part_lse + row;
     float M = -__builtin_inff();
     for (int s = 0; s < a.splits; ++s) M = fmaxf(M, lse[(int64_t)s * a.rows]);
-    float o0 = 0.0f, o1 = 0.0f;
+    float o[2 * NP] = {};
     if (M != -__builtin_inff()) {
-        float wsum = 0.0f, a0 = 0.0f, a1 = 0.0f;
+        float wsum = 0.0f, acc[2 * NP] = {};
         const float *po = a.part_o + (int64_t)row * D + 2 * (active ? lane : 0);
         const int64_t step = (int64_t)a.rows * D;
 #pragma unroll 8
         for (int s = 0; s < a.splits; ++s) {
             const float e = lse[(int64_t)s * a.rows];
-            const f32x2 v = *(const f32x2 *)(po + s * step);
             const float w = e == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(e - M);
             wsum += w;
-            a0 += w * v.x;
-            a1 += w * v.y;
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                const f32x2 v = *(const f32x2 *)(po + s * step + 128 * p);
+                acc[2 * p] += w * v.x;
+                acc[2 * p + 1] += w * v.y;
+            }
         }
-        o0 = a0 / wsum;
-        o1 = a1 / wsum;
+#pragma unroll
+        for (int k = 0; k < 2 * NP; ++k) o[k] = acc[k] / wsum;
     }
     if (a.rotate) {
-        fwht_pairs_dec<D>(o0, o1, lane);
-        o0 *= a.rot_scale;
-        o1 *= a.rot_scale;
-        if (active && sign_bit(a.vsign_bits, 2 * lane)) o0 = -o0;
-        if (active && sign_bit(a.vsign_bits, 2 * lane + 1)) o1 = -o1;
+        if constexpr (D == 256) fwht_quads_dec(o[0], o[1], o[2], o[3], lane);
+        else fwht_pairs_dec<D>(o[0], o[1], lane);
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                o[2 * p + e] *= a.rot_scale;
+                if (active && sign_bit(a.vsign_bits, 128 * p + 2 * lane + e)) o[2 * p + e] = -o[2 * p + e];
+            }
     }
     if (!active) return;
     const int qi = row % a.q_len, head = (row / a.q_len) % a.q_heads;
     const int b = row / (a.q_len * a.q_heads);
-    const int64_t base = (int64_t)b * a.o_sb + (int64_t)head * a.o_sh + (int64_t)qi * a.o_si + 2 * lane;
-    store_elem(a.out, base, a.out_dtype, o0);
-    store_elem(a.out, base + 1, a.out_dtype, o1);
+    const int64_t base = (int64_t)b * a.o_sb + (int64_t)head * a.o_sh + (int64_t)qi * a.o_si;
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int j = 128 * p + 2 * lane + e;
+            if (j < a.head_dim) store_elem(a.out, base + j, a.out_dtype, o[2 * p + e]);
+        }
 }
 
-void fill_rotation(const cqkv_side *s, uint32_t sign_bits[4], float *rot_scale);
+void fill_rotation(const cqkv_side *s, uint32_t sign_bits[8], float *rot_scale);
 
 static int tiles_of(int kv_len) { return (kv_len + 31) / 32; }
 
-// Key splits per (batch, kv head). One 8-wavefront workgroup per plane fills a CU of the
-// MI355X (256 CUs, two waves per SIMD at this register budget; twice as many workgroups of 4
-// wavefronts): split only when there are fewer planes than that, and then into pieces of at
-// least two tiles per wavefront. Ragged batches (per-sequence lengths) are split into pieces of
-// at most 128 tiles (4096 keys) so long and short sequences even out across CUs.
-constexpr int kCUs = 256;
+// Compute units of the current device (hipDeviceAttributeMultiprocessorCount, cached per device;
+// 256, the MI355X's, when there is no device to ask).
+static int device_cus() {
+    constexpr int kMaxDev = 64;
+    static int cache[kMaxDev];
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    if (!cache[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+            (void)hipGetLastError();
+            n = 256;
+        }
+        cache[dev] = n;
+    }
+    return cache[dev];
+}
 
+// Key splits per (batch, kv head). One 8-wavefront workgroup per plane fills a CU (two waves per
+// SIMD at this register budget; twice as many workgroups of 4 wavefronts): split only when
+// there are fewer planes than the device's CUs take, and then into pieces of at least two tiles
+// per wavefront. Ragged batches (per-sequence lengths) are split into pieces of at most 128 tiles
+// (4096 keys) so long and short sequences even out across CUs.
 static int auto_splits(int batch, int kv_heads, int kv_len, bool ragged, int waves = kWaves) {
     const int planes = batch * kv_heads;
     const int tiles = tiles_of(kv_len);
-    const int wgs = kCUs * (kWaves / waves);  // workgroups that fill the chip
+    const int wgs = device_cus() * (kWaves / waves);  // workgroups that fill the chip
     int s = (wgs + planes - 1) / planes;
     if (ragged) s = max(s, (tiles + 127) / 128);
     s = min(s, max(1, tiles / (2 * waves)));
@@ -89,12 +124,24 @@ static int auto_splits(int batch, int kv_heads, int kv_len, bool ragged, int wav
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Workspace: partial outputs (splits, rows, D) f32 | partial lse (splits, rows) f32.
-static size_t workspace_layout(int32_t batch, int32_t q_heads, int32_t q_len, int32_t head_dim,
-                               int32_t splits, size_t *lse_off) {
-    const size_t rows = (size_t)batch * q_heads * q_len;
-    *lse_off = align256((size_t)splits * rows * head_dim * 4);
-    return *lse_off + align256((size_t)splits * rows * 4);
+// Workspace (D' = the plane row length of head_dim): partial outputs (splits, rows, D') f32 |
+// partial lse (splits, rows) f32 | rotated queries (rows, D') f32 | combined outputs before the
+// matrix unrotation (rows, D') f32 | the padded QJL matrix (D', D') f32. The last three serve the
+// sides that rotate by their matrix and TurboProd keys at a head dim below D'; they are reserved
+// whatever the formats, so the size depends on the shapes only.
+struct DecodeWs {
+    size_t lse, qrot, otmp, qjl, total;
+};
+static DecodeWs workspace_layout(int32_t batch, int32_t q_heads, int32_t q_len, int32_t head_dim,
+                                 int32_t splits) {
+    const size_t rows = (size_t)batch * q_heads * q_len, dk = (size_t)kernel_dim(head_dim);
+    DecodeWs w;
+    w.lse = align256((size_t)splits * rows * dk * 4);
+    w.qrot = w.lse + align256((size_t)splits * rows * 4);
+    w.otmp = w.qrot + align256(rows * dk * 4);
+    w.qjl = w.otmp + align256(rows * dk * 4);
+    w.total = w.qjl + align256(dk * dk * 4);
+    return w;
 }
 
 }  // namespace cqkv
@@ -109,18 +156,29 @@ extern "C" int32_t cqkv_decode_splits(int32_t k_format, int32_t v_format, int32_
 
 extern "C" size_t cqkv_decode_workspace_bytes(int32_t batch, int32_t q_heads, int32_t q_len,
                                               int32_t head_dim, int32_t splits) {
-    if (batch <= 0 || q_heads <= 0 || q_len <= 0 || head_dim <= 0 || splits <= 0) return 0;
-    size_t lse_off;
-    return workspace_layout(batch, q_heads, q_len, head_dim, splits, &lse_off);
+    if (batch <= 0 || q_heads <= 0 || q_len <= 0 || head_dim <= 0 || head_dim > 256 || splits <= 0)
+        return 0;
+    return workspace_layout(batch, q_heads, q_len, head_dim, splits).total;
 }
 
 // Checks and fills what the dense and the paged calls share: queries, output, heads, scale,
 // window, TurboQuant rotation and codebook. k / v give the format, head dim and kv heads.
-static int decode_prepare(DecodeArgs &a, const char *who, const void *q, int32_t q_dtype,
-                          const int64_t q_strides[3], const cqkv_side *k, const cqkv_side *v,
-                          int32_t batch, int32_t q_heads, int32_t q_len, float softmax_scale,
-                          int32_t window_left, int32_t window_right, void *out, int32_t out_dtype,
-                          const int64_t out_strides[3]) {
+// Host-side parts of a decode call beyond the kernel arguments: the matrix rotations.
+struct DecodeHost {
+    const float *k_rot = nullptr;  // rotate the queries by this matrix first (x Pi_k^T)
+    const float *v_rot = nullptr;  // unrotate the combined output by this matrix (y Pi_v)
+    const cqkv_side *k = nullptr;  // the key side (TURBOPROD at a padded head dim: S padded)
+    int32_t head_dim = 0, q_dtype = 0;
+    const void *q = nullptr;
+    int64_t q_strides[3] = {0, 0, 0};
+};
+
+static int decode_prepare(DecodeArgs &a, DecodeHost &h, const char *who, const void *q,
+                          int32_t q_dtype, const int64_t q_strides[3], const cqkv_side *k,
+                          const cqkv_side *v, int32_t batch, int32_t q_heads, int32_t q_len,
+                          float softmax_scale, int32_t window_left, int32_t window_right,
+                          float softcap, const float *alibi_slopes, int32_t alibi_batch_stride,
+                          void *out, int32_t out_dtype, const int64_t out_strides[3]) {
     if (int rc = check_side(k, who)) return rc;
     if (int rc = check_side(v, who)) return rc;
     if (k->is_value != 0 || v->is_value != 1)
@@ -142,7 +200,17 @@ static int decode_prepare(DecodeArgs &a, const char *who, const void *q, int32_t
     if ((int64_t)group * q_len > (1 << 24))
         return fail(CQKV_ERR_ARG, "%s: q_len * q_heads / kv_heads = %lld above 2^24", who,
                     (long long)group * q_len);
+    if (!(softcap >= 0.0f) || softcap == __builtin_inff())
+        return fail(CQKV_ERR_ARG, "%s: softcap %g (finite, >= 0; 0 disables it)", who,
+                    (double)softcap);
+    if (alibi_slopes && alibi_batch_stride != 0 && alibi_batch_stride != q_heads)
+        return fail(CQKV_ERR_ARG, "%s: alibi batch stride %d (0 or q_heads %d)", who,
+                    alibi_batch_stride, q_heads);
     a = DecodeArgs{};
+    h = DecodeHost{};
+    a.cap2 = softcap * kLog2e;
+    a.alibi = alibi_slopes;
+    a.alibi_bs = alibi_batch_stride;
     a.q = q;
     a.q_sb = q_strides[0];
     a.q_sh = q_strides[1];
@@ -160,13 +228,23 @@ static int decode_prepare(DecodeArgs &a, const char *who, const void *q, int32_t
     a.batch = batch;
     a.out = out;
     a.out_dtype = out_dtype;
-    a.rot_k = side_rotates(k) ? 1 : 0;
-    a.rot_v = side_rotates(v) ? 1 : 0;
+    a.rot_k = side_fwht(k) ? 1 : 0;
+    a.rot_v = side_fwht(v) ? 1 : 0;
+    a.head_dim = d;
+    a.qjl_c = -kQjlConst / (float)d;
+    if (side_matrix_rot(k)) h.k_rot = k->rot;
+    if (side_matrix_rot(v)) h.v_rot = v->rot;
+    a.partials = a.rot_v || h.v_rot ? 1 : 0;
+    h.k = k;
+    h.head_dim = d;
+    h.q = q;
+    h.q_dtype = q_dtype;
+    for (int i = 0; i < 3; ++i) h.q_strides[i] = q_strides[i];
     // queries not representable in the operand type get a lo part (f16 / f32 inputs, or rotated
     // queries, for the bf16 key formats); TurboQuant keys take the rotated queries as one f16
     // operand (2^-12 relative rounding: config 5 216-225 -> 208-220 us same-box, its parity tests
     // unchanged)
-    a.q_split = !is_turbo(k->format) && (q_dtype != CQKV_BF16 || a.rot_k) ? 1 : 0;
+    a.q_split = !is_turbo(k->format) && (q_dtype != CQKV_BF16 || a.rot_k || h.k_rot) ? 1 : 0;
     a.o_sb = out_strides[0];
     a.o_sh = out_strides[1];
     a.o_si = out_strides[2];
@@ -206,45 +284,100 @@ static int decode_prepare(DecodeArgs &a, const char *who, const void *q, int32_t
     return CQKV_OK;
 }
 
-// Launches the decode kernel over a.splits splits and, for more than one or a rotated value side,
-// the combine (partials at a.part_o / a.part_lse; the combine unrotates).
-static hipError_t decode_launch(const DecodeArgs &a, int kf, int vf, int d, hipStream_t st) {
+// Launches a decode over a.splits splits: the query rotation by the key side's matrix (into the
+// workspace's rotated-query region), the decode kernel, the combine for more than one split or
+// when a.partials, and the unrotation by the value side's matrix (from the workspace's combined
+// output region). ws: the call's workspace (layout w) when one is needed.
+static hipError_t decode_launch(DecodeArgs a, const DecodeHost &h, int kf, int vf, void *ws,
+                                const DecodeWs &w, hipStream_t st) {
+    const int d = h.head_dim, dk = kernel_dim(d);
+    const int rows = a.batch * a.q_heads * a.q_len;
+    if (h.k_rot) {  // q Pi_k^T, f32, padded to the plane row
+        float *qr = (float *)((char *)ws + w.qrot);
+        const int64_t ys[3] = {(int64_t)a.q_heads * a.q_len * dk, (int64_t)a.q_len * dk, dk};
+        RowMatArgs r = rowmat_args(h.q, h.q_dtype, h.q_strides, a.batch, a.q_heads, a.q_len, d, qr,
+                                   CQKV_F32, ys, dk);
+        r.m = h.k_rot;
+        r.transpose = 1;
+        if (hipError_t e = rowmat_launch(r, st)) return e;
+        a.q = qr;
+        a.q_dtype = CQKV_F32;
+        a.q_sb = ys[0];
+        a.q_sh = ys[1];
+        a.q_si = ys[2];
+    }
+    if (h.k->format == CQKV_FMT_TURBOPROD && d != dk) {  // S padded to the plane row
+        float *sp = (float *)((char *)ws + w.qjl);
+        const int64_t xs[3] = {0, 0, d}, ys[3] = {0, 0, dk};
+        RowMatArgs r = rowmat_args(h.k->qjl, CQKV_F32, xs, 1, 1, dk, d, sp, CQKV_F32, ys, dk);
+        r.xrows = d;
+        if (hipError_t e = rowmat_launch(r, st)) return e;
+        a.qjl = sp;
+    }
     const int64_t wgs = (int64_t)a.splits * a.col_blocks * a.kv_heads * a.batch;
     if (wgs > 0x7fffffff) return hipErrorInvalidConfiguration;
     const dim3 grid((unsigned)wgs);
+    bool ok = false;
     switch (kf) {
-    case CQKV_FMT_FP8: decode_launch_k5(vf, d, grid, st, a); break;
-    case CQKV_FMT_MXFP4: decode_launch_k2(vf, d, grid, st, a); break;
-    case CQKV_FMT_MXFP8: decode_launch_k4(vf, d, grid, st, a); break;
-    case CQKV_FMT_NVFP4: decode_launch_k3(vf, d, grid, st, a); break;
-    case CQKV_FMT_TURBOPROD: decode_launch_k1(vf, d, grid, st, a); break;
-    case kFmtTurboC: decode_launch_k6(vf, d, grid, st, a); break;
-    case kFmtProd4: decode_launch_k7(vf, d, grid, st, a); break;
-    default: decode_launch_k0(vf, d, grid, st, a); break;
+    case CQKV_FMT_FP8: ok = decode_launch_k5(vf, dk, grid, st, a); break;
+    case CQKV_FMT_MXFP4: ok = decode_launch_k2(vf, dk, grid, st, a); break;
+    case CQKV_FMT_MXFP8: ok = decode_launch_k4(vf, dk, grid, st, a); break;
+    case CQKV_FMT_NVFP4: ok = decode_launch_k3(vf, dk, grid, st, a); break;
+    case CQKV_FMT_TURBOPROD: ok = decode_launch_k1(vf, dk, grid, st, a); break;
+    case kFmtTurboC: ok = decode_launch_k6(vf, dk, grid, st, a); break;
+    case kFmtProd4: ok = decode_launch_k7(vf, dk, grid, st, a); break;
+    case CQKV_FMT_TURBO4: ok = decode_launch_k0(vf, dk, grid, st, a); break;
+    default: break;
     }
+    if (!ok) return hipErrorInvalidValue;  // a key / value format pairing without a kernel
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess && (a.splits > 1 || a.rot_v)) {
+    if (e == hipSuccess && (a.splits > 1 || a.partials)) {
         CombineArgs c = {};
         c.part_o = a.part_o;
         c.part_lse = a.part_lse;
         c.splits = a.splits;
-        c.rows = a.batch * a.q_heads * a.q_len;
+        c.rows = rows;
         c.q_heads = a.q_heads;
         c.q_len = a.q_len;
-        c.out_dtype = a.out_dtype;
         c.rotate = a.rot_v;
-        c.out = a.out;
-        c.o_sb = a.o_sb;
-        c.o_sh = a.o_sh;
-        c.o_si = a.o_si;
-        for (int i = 0; i < 4; ++i) c.vsign_bits[i] = a.vsign_bits[i];
+        c.head_dim = d;
+        if (h.v_rot) {  // combined rows to the workspace, f32, for the unrotation below
+            c.out = (char *)ws + w.otmp;
+            c.out_dtype = CQKV_F32;
+            c.o_sb = (int64_t)a.q_heads * a.q_len * d;
+            c.o_sh = (int64_t)a.q_len * d;
+            c.o_si = d;
+        } else {
+            c.out = a.out;
+            c.out_dtype = a.out_dtype;
+            c.o_sb = a.o_sb;
+            c.o_sh = a.o_sh;
+            c.o_si = a.o_si;
+        }
+        for (int i = 0; i < 8; ++i) c.vsign_bits[i] = a.vsign_bits[i];
         c.rot_scale = a.rot_scale;
         const dim3 cg((c.rows + 3) / 4);
-        if (d == 64) hipLaunchKernelGGL(combine_kernel<64>, cg, dim3(256), 0, st, c);
-        else hipLaunchKernelGGL(combine_kernel<128>, cg, dim3(256), 0, st, c);
+        if (dk == 64) hipLaunchKernelGGL(combine_kernel<64>, cg, dim3(256), 0, st, c);
+        else if (dk == 128) hipLaunchKernelGGL(combine_kernel<128>, cg, dim3(256), 0, st, c);
+        else hipLaunchKernelGGL(combine_kernel<256>, cg, dim3(256), 0, st, c);
         e = hipGetLastError();
+        if (e == hipSuccess && h.v_rot) {  // y Pi_v into the output
+            const int64_t xs[3] = {c.o_sb, c.o_sh, c.o_si}, ys[3] = {a.o_sb, a.o_sh, a.o_si};
+            RowMatArgs r = rowmat_args(c.out, CQKV_F32, xs, a.batch, a.q_heads, a.q_len, d, a.out,
+                                       a.out_dtype, ys, d);
+            r.m = h.v_rot;
+            r.transpose = 0;
+            e = rowmat_launch(r, st);
+        }
     }
     return e;
+}
+
+// Whether a decode call needs its workspace: partials, or the matrix rotations' and the padded
+// QJL matrix's regions.
+static bool needs_workspace(const DecodeArgs &a, const DecodeHost &h) {
+    return a.splits > 1 || a.partials || h.k_rot ||
+           (h.k->format == CQKV_FMT_TURBOPROD && h.head_dim != kernel_dim(h.head_dim));
 }
 
 // ---- allocation-free decode: split partials in a library-owned device array ----
@@ -285,13 +418,15 @@ static int decode_dense(const char *who, const void *q, int32_t q_dtype,
                         const int64_t q_strides[3], const cqkv_side *k, const cqkv_side *v,
                         int32_t batch, int32_t q_heads, int32_t q_len, const int32_t *kv_lens,
                         int32_t kv_len, float softmax_scale, int32_t window_left,
-                        int32_t window_right, void *out, int32_t out_dtype,
+                        int32_t window_right, float softcap, const float *alibi_slopes,
+                        int32_t alibi_batch_stride, void *out, int32_t out_dtype,
                         const int64_t out_strides[3], int32_t splits, void *workspace,
                         size_t workspace_bytes, bool noalloc, cqkv_stream_t stream) {
     DecodeArgs a;
-    if (int rc = decode_prepare(a, who, q, q_dtype, q_strides, k, v, batch, q_heads, q_len,
-                                softmax_scale, window_left, window_right, out, out_dtype,
-                                out_strides))
+    DecodeHost h;
+    if (int rc = decode_prepare(a, h, who, q, q_dtype, q_strides, k, v, batch, q_heads, q_len,
+                                softmax_scale, window_left, window_right, softcap, alibi_slopes,
+                                alibi_batch_stride, out, out_dtype, out_strides))
         return rc;
     if (k->capacity != v->capacity)
         return fail(CQKV_ERR_ARG, "%s: key / value capacities %d / %d differ", who, k->capacity,
@@ -307,30 +442,25 @@ static int decode_dense(const char *who, const void *q, int32_t q_dtype,
     int s = splits > 0 ? min(splits, tiles)
                        : auto_splits(batch, hkv, max(kv_len, 1), kv_lens != nullptr,
                                      waves_of(k->format, v->format));
-    size_t lse_off = 0;
-    // partials (and the combine) for more than one split, or for rotated values at any split
-    // count: the combine unrotates
-    const bool partials_any = a.rot_v != 0;
-    if (noalloc) {
-        if (partials_any &&
-            workspace_layout(batch, q_heads, q_len, d, 1, &lse_off) > CQKV_DECODE_SCRATCH_BYTES)
+    if (noalloc) {  // everything the call needs must fit the device scratch
+        auto fits = [&](int n) {
+            a.splits = n;
+            return !needs_workspace(a, h) ||
+                   workspace_layout(batch, q_heads, q_len, d, n).total <= CQKV_DECODE_SCRATCH_BYTES;
+        };
+        if (!fits(s) && splits > 0)
             return fail(CQKV_ERR_WORKSPACE,
-                        "%s: rotated values need %zu bytes of partials, above the %zu-byte "
-                        "device scratch",
-                        who, workspace_layout(batch, q_heads, q_len, d, 1, &lse_off),
+                        "%s: %d splits need %zu bytes of partials, above the %zu-byte device "
+                        "scratch",
+                        who, s, workspace_layout(batch, q_heads, q_len, d, s).total,
                         (size_t)CQKV_DECODE_SCRATCH_BYTES);
-        if (s > 1 &&
-            workspace_layout(batch, q_heads, q_len, d, s, &lse_off) > CQKV_DECODE_SCRATCH_BYTES) {
-            if (splits > 0)
-                return fail(CQKV_ERR_WORKSPACE,
-                            "%s: %d splits need %zu bytes of partials, above the %zu-byte "
-                            "device scratch",
-                            who, s, workspace_layout(batch, q_heads, q_len, d, s, &lse_off),
-                            (size_t)CQKV_DECODE_SCRATCH_BYTES);
-            while (s > 1 && workspace_layout(batch, q_heads, q_len, d, s, &lse_off) >
-                                CQKV_DECODE_SCRATCH_BYTES)
-                --s;
-        }
+        while (s > 1 && !fits(s)) --s;
+        if (!fits(s))
+            return fail(CQKV_ERR_WORKSPACE,
+                        "%s: %zu bytes of partials and rotation buffers exceed the %zu-byte "
+                        "device scratch",
+                        who, workspace_layout(batch, q_heads, q_len, d, s).total,
+                        (size_t)CQKV_DECODE_SCRATCH_BYTES);
     }
     const int tps = (tiles + s - 1) / s;
     s = (tiles + tps - 1) / tps;
@@ -351,21 +481,21 @@ static int decode_dense(const char *who, const void *q, int32_t q_dtype,
     hipStream_t st = (hipStream_t)stream;
     void *ws = workspace;
     bool owned = false;
-    if (s > 1 || partials_any) {
-        const size_t need = workspace_layout(batch, q_heads, q_len, d, s, &lse_off);
+    const DecodeWs w = workspace_layout(batch, q_heads, q_len, d, s);
+    if (needs_workspace(a, h)) {
         if (noalloc) {
             if (int rc = scratch_address(&ws, who)) return rc;
-        } else if (ws && workspace_bytes < need) {
+        } else if (ws && workspace_bytes < w.total) {
             return fail(CQKV_ERR_WORKSPACE, "%s: workspace %zu < %zu bytes", who,
-                        workspace_bytes, need);
+                        workspace_bytes, w.total);
         } else if (!ws) {
-            CQKV_HIP_CHECK(hipMallocAsync(&ws, need, st));
+            CQKV_HIP_CHECK(hipMallocAsync(&ws, w.total, st));
             owned = true;
         }
         a.part_o = (float *)ws;
-        a.part_lse = (float *)((char *)ws + lse_off);
+        a.part_lse = (float *)((char *)ws + w.lse);
     }
-    hipError_t e = decode_launch(a, a.kfmt, a.vfmt, d, st);
+    hipError_t e = decode_launch(a, h, a.kfmt, a.vfmt, ws, w, st);
     if (owned) {
         hipError_t fe = hipFreeAsync(ws, st);
         if (e == hipSuccess) e = fe;
@@ -378,14 +508,16 @@ extern "C" int cqkv_decode_attention(const void *q, int32_t q_dtype, const int64
                                      const cqkv_side *k, const cqkv_side *v, int32_t batch,
                                      int32_t q_heads, int32_t q_len, const int32_t *kv_lens,
                                      int32_t kv_len, float softmax_scale, int32_t window_left,
-                                     int32_t window_right, void *out, int32_t out_dtype,
-                                     const int64_t out_strides[3], int32_t splits,
-                                     void *workspace, size_t workspace_bytes,
+                                     int32_t window_right, float softcap,
+                                     const float *alibi_slopes, int32_t alibi_batch_stride,
+                                     void *out, int32_t out_dtype, const int64_t out_strides[3],
+                                     int32_t splits, void *workspace, size_t workspace_bytes,
                                      cqkv_stream_t stream) {
     clear_error();
     return decode_dense("cqkv_decode_attention", q, q_dtype, q_strides, k, v, batch, q_heads,
-                        q_len, kv_lens, kv_len, softmax_scale, window_left, window_right, out,
-                        out_dtype, out_strides, splits, workspace, workspace_bytes, false, stream);
+                        q_len, kv_lens, kv_len, softmax_scale, window_left, window_right, softcap,
+                        alibi_slopes, alibi_batch_stride, out, out_dtype, out_strides, splits,
+                        workspace, workspace_bytes, false, stream);
 }
 
 extern "C" int cqkv_decode_attention_noalloc(const void *q, int32_t q_dtype,
@@ -394,14 +526,15 @@ extern "C" int cqkv_decode_attention_noalloc(const void *q, int32_t q_dtype,
                                              int32_t q_len, const int32_t *kv_lens,
                                              int32_t kv_len, float softmax_scale,
                                              int32_t window_left, int32_t window_right,
-                                             void *out, int32_t out_dtype,
-                                             const int64_t out_strides[3], int32_t splits,
-                                             cqkv_stream_t stream) {
+                                             float softcap, const float *alibi_slopes,
+                                             int32_t alibi_batch_stride, void *out,
+                                             int32_t out_dtype, const int64_t out_strides[3],
+                                             int32_t splits, cqkv_stream_t stream) {
     clear_error();
     return decode_dense("cqkv_decode_attention_noalloc", q, q_dtype, q_strides, k, v, batch,
                         q_heads, q_len, kv_lens, kv_len, softmax_scale, window_left,
-                        window_right, out, out_dtype, out_strides, splits, nullptr, 0, true,
-                        stream);
+                        window_right, softcap, alibi_slopes, alibi_batch_stride, out, out_dtype,
+                        out_strides, splits, nullptr, 0, true, stream);
 }
 
 // ---- paged decode ----
@@ -479,15 +612,13 @@ static hipError_t write_paged_table(const std::vector<PagedSeg> &segs, PagedSeg 
     return hipSuccess;
 }
 
-// workspace: the segment table, then (more than one segment) the partials
-// The segment table, then partials when there is more than one segment or the values rotate.
-static size_t paged_workspace(int nseg, bool rot_v, int32_t batch, int32_t q_heads, int32_t q_len,
-                              int32_t head_dim, size_t *part_off, size_t *lse_off) {
+// Workspace: the segment table, then the dense decode's workspace (partials, rotation buffers)
+// for the segment count.
+static size_t paged_workspace(int nseg, int32_t batch, int32_t q_heads, int32_t q_len,
+                              int32_t head_dim, size_t *part_off, DecodeWs *w) {
     *part_off = align256((size_t)nseg * sizeof(PagedSeg));
-    size_t parts = 0;
-    *lse_off = 0;
-    if (nseg > 1 || rot_v) parts = workspace_layout(batch, q_heads, q_len, head_dim, nseg, lse_off);
-    return *part_off + parts;
+    *w = workspace_layout(batch, q_heads, q_len, head_dim, nseg);
+    return *part_off + w->total;
 }
 
 static int check_blocks(const cqkv_kv_block *blocks, int32_t n_blocks, int32_t batch,
@@ -506,6 +637,7 @@ static int check_blocks(const cqkv_kv_block *blocks, int32_t n_blocks, int32_t b
             bl.k->kv_heads != b0.k->kv_heads || bl.v->kv_heads != b0.k->kv_heads ||
             bl.k->is_value != 0 || bl.v->is_value != 1 || side_rotates(bl.k) != side_rotates(b0.k) ||
             side_rotates(bl.v) != side_rotates(b0.v) ||
+            side_rotation(bl.k) != side_rotation(b0.k) || side_rotation(bl.v) != side_rotation(b0.v) ||
             (side_rotates(b0.k) && bl.k->seed != b0.k->seed) ||
             (side_rotates(b0.v) && bl.v->seed != b0.v->seed) ||
             (b0.k->format == CQKV_FMT_TURBOPROD && bl.k->qjl != b0.k->qjl))
@@ -532,25 +664,28 @@ extern "C" size_t cqkv_decode_paged_workspace_bytes(const cqkv_kv_block *blocks,
         batch <= 0 || q_heads <= 0 || q_len <= 0)
         return 0;
     const int nseg = paged_segments(blocks, n_blocks, batch, nullptr);
-    size_t part_off, lse_off;
-    return paged_workspace(nseg, side_rotates(blocks[0].v), batch, q_heads, q_len,
-                           blocks[0].k->head_dim, &part_off, &lse_off);
+    size_t part_off;
+    DecodeWs w;
+    return paged_workspace(nseg, batch, q_heads, q_len, blocks[0].k->head_dim, &part_off, &w);
 }
 
 extern "C" int cqkv_decode_attention_paged(const void *q, int32_t q_dtype,
                                            const int64_t q_strides[3], const cqkv_kv_block *blocks,
                                            int32_t n_blocks, int32_t batch, int32_t q_heads,
                                            int32_t q_len, float softmax_scale, int32_t window_left,
-                                           int32_t window_right, void *out, int32_t out_dtype,
+                                           int32_t window_right, float softcap,
+                                           const float *alibi_slopes, int32_t alibi_batch_stride,
+                                           void *out, int32_t out_dtype,
                                            const int64_t out_strides[3], void *workspace,
                                            size_t workspace_bytes, cqkv_stream_t stream) {
     clear_error();
     const char *who = "cqkv_decode_attention_paged";
     if (int rc = check_blocks(blocks, n_blocks, batch, who)) return rc;
     DecodeArgs a;
-    if (int rc = decode_prepare(a, who, q, q_dtype, q_strides, blocks[0].k, blocks[0].v, batch,
-                                q_heads, q_len, softmax_scale, window_left, window_right, out,
-                                out_dtype, out_strides))
+    DecodeHost h;
+    if (int rc = decode_prepare(a, h, who, q, q_dtype, q_strides, blocks[0].k, blocks[0].v, batch,
+                                q_heads, q_len, softmax_scale, window_left, window_right, softcap,
+                                alibi_slopes, alibi_batch_stride, out, out_dtype, out_strides))
         return rc;
     if (batch == 0 || q_len == 0) return CQKV_OK;
     std::vector<PagedSeg> segs;
@@ -562,9 +697,9 @@ extern "C" int cqkv_decode_attention_paged(const void *q, int32_t q_dtype,
     a.splits = nseg;
 
     hipStream_t st = (hipStream_t)stream;
-    size_t part_off, lse_off;
-    const size_t need = paged_workspace(nseg, a.rot_v != 0, batch, q_heads, q_len, d, &part_off,
-                                        &lse_off);
+    size_t part_off;
+    DecodeWs w;
+    const size_t need = paged_workspace(nseg, batch, q_heads, q_len, d, &part_off, &w);
     void *ws = workspace;
     bool owned = false;
     if (ws && workspace_bytes < need)
@@ -575,11 +710,10 @@ extern "C" int cqkv_decode_attention_paged(const void *q, int32_t q_dtype,
     }
     hipError_t e = write_paged_table(segs, (PagedSeg *)ws, st);
     a.segs = (const PagedSeg *)ws;
-    if (nseg > 1 || a.rot_v) {
-        a.part_o = (float *)((char *)ws + part_off);
-        a.part_lse = (float *)((char *)ws + part_off + lse_off);
-    }
-    if (e == hipSuccess) e = decode_launch(a, a.kfmt, a.vfmt, d, st);
+    void *dws = (char *)ws + part_off;
+    a.part_o = (float *)dws;
+    a.part_lse = (float *)((char *)dws + w.lse);
+    if (e == hipSuccess) e = decode_launch(a, h, a.kfmt, a.vfmt, dws, w, st);
     if (owned) {
         hipError_t fe = hipFreeAsync(ws, st);
         if (e == hipSuccess) e = fe;

@@ -11,9 +11,9 @@
 
 namespace cqkv {
 
-void CQKV_CAT(decode_launch_k, CQKV_DECODE_KF)(int vf, int d, dim3 grid, hipStream_t st,
+bool CQKV_CAT(decode_launch_k, CQKV_DECODE_KF)(int vf, int d, dim3 grid, hipStream_t st,
                                                const DecodeArgs &a) {
-    launch_decode_k<CQKV_DECODE_KF>(vf, d, grid, st, a);
+    return launch_decode_k<CQKV_DECODE_KF>(vf, d, grid, st, a);
 }
 
 }  // namespace cqkv

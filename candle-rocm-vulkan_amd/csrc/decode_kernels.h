@@ -72,9 +72,19 @@ struct DecodeArgs {
     void *out;
     int32_t out_dtype, q_split;  // q_split: queries need a lo part (not bf16 inputs)
     int64_t o_sb, o_sh, o_si;
-    int32_t rot_k, rot_v;                   // rotated key / value sides: rotate q, unrotate o
-    uint32_t ksign_bits[4], vsign_bits[4];  // their rotation signs (bit set -> -1)
+    int32_t rot_k, rot_v;  // key / value sides with the in-register Hadamard rotation: rotate q,
+                           // unrotate o (rot_v: partials always, the combine unrotates)
+    uint32_t ksign_bits[8], vsign_bits[8];  // their rotation signs (bit set -> -1)
     float rot_scale;                        // 1 / sqrt(D)
+    int32_t head_dim;      // the head dim d <= D: query elements past it are zero, outputs not
+                           // written
+    float qjl_c;           // TURBOPROD keys: -sqrt(pi / 2) / d
+    int32_t partials;      // write partials at any split count (the combine finishes the rows)
+    // score terms (the TERMS kernels): soft-capping cap * log2(e) (0: off), ALiBi slopes
+    // alibi[b * alibi_bs + head] (device f32, null: off)
+    float cap2;
+    const float *alibi;
+    int32_t alibi_bs;
     float cent[16];  // the TURBO4 code table's codebook (keys', else values'; one per kernel)
     const PagedSeg *segs;  // paged: one segment per split (the planes above are unused)
     const float *qjl;      // TURBOPROD keys: the D x D QJL matrix S (device, row-major)
@@ -106,6 +116,21 @@ __device__ inline void fwht_pairs_dec(float &v0, float &v1, int lane) {
         v0 = upper ? p0 - v0 : v0 + p0;
         v1 = upper ? p1 - v1 : v1 + p1;
     }
+}
+
+// The same transform at D = 256, four elements per lane: (v0, v1) are elements 2 lane, 2 lane + 1
+// and (v2, v3) elements 128 + 2 lane, 129 + 2 lane. H_256 = H_2 x H_128: the transform of each
+// half, then the stride-128 stage inside the lane.
+__device__ inline void fwht_quads_dec(float &v0, float &v1, float &v2, float &v3, int lane) {
+    fwht_pairs_dec<128>(v0, v1, lane);
+    fwht_pairs_dec<128>(v2, v3, lane);
+    float a = v0 + v2, b = v0 - v2;
+    v0 = a;
+    v2 = b;
+    a = v1 + v3;
+    b = v1 - v3;
+    v1 = a;
+    v3 = b;
 }
 
 __device__ inline bool sign_bit(const uint32_t *bits, int j) { return (bits[j >> 5] >> (j & 31)) & 1u; }
@@ -148,21 +173,23 @@ struct Tile {
     uint32_t k[2][is8<KF>() ? D / 16 : D / 32];
     // values: D/32 chunks of 2 head dims x 8 keys (byte codes 4 words, 4-bit 2 words)
     uint32_t v[D / 32][is8<VF>() ? 4 : 2];
-    // per sub-tile, this lane's key: FP8 f32 scale; MXFP4 its E8M0 block byte; MXFP8 all its
-    // E8M0 block bytes; NVFP4 the E4M3 block bytes of its 32 (D=128) / 16 (D=64) head dims
-    uint32_t kscale[2];
+    // per sub-tile, this lane's key: FP8 f32 scale; MXFP4 the E8M0 bytes of its head dims (one,
+    // two at D = 256); MXFP8 all its E8M0 block bytes (kscale2: bytes 4-7 at D = 256); NVFP4 the
+    // E4M3 block bytes of its 64 (D = 256) / 32 (D = 128) / 16 (D = 64) head dims
+    uint32_t kscale[2], kscale2[2];
     uint32_t ktok[2];  // NVFP4: the key's f32 scale
-    // key lane % 32 (broadcast across lanes): the MX formats' value block bytes
-    uint32_t vs;
+    // key lane % 32 (broadcast across lanes): the MX formats' value block bytes (vs2: bytes 4-7
+    // at D = 256)
+    uint32_t vs, vs2;
     // FP8 / TURBO4: the scale words of keys 8 g .. 8 g + 7 of the tile (lane group g), the ones the
     // lane's score and P rows need, read directly instead of broadcast across lanes
     uint32_t ks8[8], vs8[8];
-    // NVFP4: the value block bytes (two words per key at D = 128, one at D = 64) and f32 scales
-    // of keys 8 g .. 8 g + 7, read directly (config-2 shape 100-103 -> 99 us same-box)
-    uint32_t nvb[D == 128 ? 16 : 8], nvg[8];
+    // NVFP4: the value block bytes (D / 64 words per key) and f32 scales of keys 8 g .. 8 g + 7,
+    // read directly (config-2 shape 100-103 -> 99 us same-box)
+    uint32_t nvb[D / 8], nvg[8];
     // TURBOPROD keys: |r| of keys 8 g .. 8 g + 7, and per sub-tile the lane key's sign bits of
-    // its head dims (D / 4 bits: dims (D / 4) g ..)
-    uint32_t kr1[8], ksg[2];
+    // its head dims (D / 4 bits: dims (D / 4) g ..; ksg2: bits 32-63 at D = 256)
+    uint32_t kr1[8], ksg[2], ksg2[2];
 };
 
 // Formats whose per-key scale words are read as ks8 / vs8 (one 32-bit word per key). Same-box
@@ -201,14 +228,30 @@ __device__ inline void load_tile(Tile<KF, VF, D> &r, int tile, bool live, int la
                 r.k[s][4 * i + 2] = w.z;
                 r.k[s][4 * i + 3] = w.w;
             }
-            if constexpr (KF == CQKV_FMT_FP8)
+            if constexpr (KF == CQKV_FMT_FP8) {
                 r.kscale[s] = ld32(ksr, (key * 4) | oob);
-            else if constexpr (D == 128)
+            } else if constexpr (D == 256) {
+                const u32x2 w = ld64(ksr, (key * 8) | oob);
+                r.kscale[s] = w.x;
+                r.kscale2[s] = w.y;
+            } else if constexpr (D == 128) {
                 r.kscale[s] = ld32(ksr, (key * 4) | oob);
-            else
+            } else {
                 r.kscale[s] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(ksr, (key * 2) | oob, 0, 0);
+            }
         } else {
-            if constexpr (D == 128) {
+            if constexpr (D == 256) {  // head dims 64 g .. 64 g + 63: two 16-byte pieces
+                const u32x4 w0 = ld128_stream(kr, (key * 128 + 32 * g) | oob);
+                const u32x4 w1 = ld128_stream(kr, (key * 128 + 32 * g + 16) | oob);
+                r.k[s][0] = w0.x;
+                r.k[s][1] = w0.y;
+                r.k[s][2] = w0.z;
+                r.k[s][3] = w0.w;
+                r.k[s][4] = w1.x;
+                r.k[s][5] = w1.y;
+                r.k[s][6] = w1.z;
+                r.k[s][7] = w1.w;
+            } else if constexpr (D == 128) {
                 const u32x4 w = ld128_stream(kr, (key * 64 + 16 * g) | oob);
                 r.k[s][0] = w.x;
                 r.k[s][1] = w.y;
@@ -219,11 +262,18 @@ __device__ inline void load_tile(Tile<KF, VF, D> &r, int tile, bool live, int la
                 r.k[s][0] = w.x;
                 r.k[s][1] = w.y;
             }
-            if constexpr (KF == CQKV_FMT_MXFP4)
-                r.kscale[s] = __builtin_amdgcn_raw_buffer_load_b8(
-                    ksr, (key * (D / 32) + (D == 128 ? g : g >> 1)) | oob, 0, 0);
+            if constexpr (KF == CQKV_FMT_MXFP4) {
+                if constexpr (D == 256)  // blocks 2 g, 2 g + 1
+                    r.kscale[s] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
+                        ksr, (key * 8 + 2 * g) | oob, 0, 0);
+                else
+                    r.kscale[s] = __builtin_amdgcn_raw_buffer_load_b8(
+                        ksr, (key * (D / 32) + (D == 128 ? g : g >> 1)) | oob, 0, 0);
+            }
             if constexpr (KF == CQKV_FMT_NVFP4) {
-                if constexpr (D == 128)
+                if constexpr (D == 256)  // blocks 4 g .. 4 g + 3
+                    r.kscale[s] = ld32(ksr, (key * 16 + 4 * g) | oob);
+                else if constexpr (D == 128)
                     r.kscale[s] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(
                         ksr, (key * 8 + 2 * g) | oob, 0, 0);
                 else
@@ -256,7 +306,11 @@ __device__ inline void load_tile(Tile<KF, VF, D> &r, int tile, bool live, int la
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
             const uint32_t key = t0 + 8 * (n >> 2) + 4 * s2 + (n & 3);
-            if constexpr (D == 128)
+            if constexpr (D == 256) {
+                const u32x2 w = ld64(ksr, (cap * 8 + key * 32 + 8 * g) | oob);
+                r.ksg[s2] = w.x;
+                r.ksg2[s2] = w.y;
+            } else if constexpr (D == 128)
                 r.ksg[s2] = ld32(ksr, (cap * 8 + key * 16 + 4 * g) | oob);
             else
                 r.ksg[s2] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(ksr, (cap * 8 + key * 8 + 2 * g) | oob, 0, 0);
@@ -265,8 +319,14 @@ __device__ inline void load_tile(Tile<KF, VF, D> &r, int tile, bool live, int la
     if constexpr (direct_scales<VF>()) {
         load_scales8<4>(r.vs8, vsr, t0 + 8 * g, oob);
     } else if constexpr (VF == CQKV_FMT_MXFP4 || VF == CQKV_FMT_MXFP8) {
-        r.vs = D == 128 ? ld32(vsr, (kl * 4) | oob)
-                        : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(vsr, (kl * 2) | oob, 0, 0);
+        if constexpr (D == 256) {
+            const u32x2 w = ld64(vsr, (kl * 8) | oob);
+            r.vs = w.x;
+            r.vs2 = w.y;
+        } else {
+            r.vs = D == 128 ? ld32(vsr, (kl * 4) | oob)
+                            : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(vsr, (kl * 2) | oob, 0, 0);
+        }
     } else if constexpr (VF == CQKV_FMT_NVFP4) {
         const uint32_t kb = t0 + 8 * g;
         constexpr uint32_t kBpk = D / 16;  // block bytes per key
@@ -405,13 +465,13 @@ __device__ inline bf16x8 nvfp4x8_keys_bf16x8(uint32_t w, const float *sg) {
     return __builtin_bit_cast(bf16x8, r);
 }
 
-template <int KF, int VF, int D>
+template <int KF, int VF, int D, bool TERMS>
 __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const DecodeArgs &a,
                                     const op_t<KF> *qhi, const op_t<KF> *qlo, bool q_split, int lane,
                                     int lo, int hi, int lo_max, int hi_min, int L, int koff,
                                     uint32_t tab, float &m_run, float &l_run,
                                     f32x4 *acc, const op_t<KF> *qsop, uint32_t ktab,
-                                    uint32_t vtab) {
+                                    uint32_t vtab, float slope2, int qpos) {
     constexpr int NCH = D / 32;
     const int g = lane >> 4;
     // tile and L are rows of the current block (the whole cache when not paged); keys of the
@@ -431,13 +491,15 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
         } else if constexpr (KF == CQKV_FMT_MXFP8) {
             // chunk j holds head dims 64 (j >> 1) + 16 g + 8 (j & 1) + e: block 2 (j >> 1) + g / 2
             const int bi = 2 * (j >> 1) + (g >> 1);
-            const float sc0 = e8m0_scale((cur.kscale[0] >> (8 * bi)) & 0xffu);
-            const float sc1 = e8m0_scale((cur.kscale[1] >> (8 * bi)) & 0xffu);
+            const uint32_t w0 = bi < 4 ? cur.kscale[0] : cur.kscale2[0];
+            const uint32_t w1 = bi < 4 ? cur.kscale[1] : cur.kscale2[1];
+            const float sc0 = e8m0_scale((w0 >> (8 * (bi & 3))) & 0xffu);
+            const float sc1 = e8m0_scale((w1 >> (8 * (bi & 3))) & 0xffu);
             k0 = fp8x8_scaled_bf16x8(cur.k[0][2 * j], cur.k[0][2 * j + 1], sc0);
             k1 = fp8x8_scaled_bf16x8(cur.k[1][2 * j], cur.k[1][2 * j + 1], sc1);
         } else if constexpr (KF == CQKV_FMT_NVFP4) {
-            // chunk j holds head dims (D/4) g + 8 j + e: the lane's block byte j / 2 (D = 128)
-            const int bi = D == 128 ? (j >> 1) : 0;
+            // chunk j holds head dims (D/4) g + 8 j + e: the lane's block byte j / 2 (D >= 128)
+            const int bi = D >= 128 ? (j >> 1) : 0;
             const float sg0 = __builtin_amdgcn_cvt_f32_fp8(cur.kscale[0] >> (8 * bi), 0) *
                               __uint_as_float(cur.ktok[0]);
             const float sg1 = __builtin_amdgcn_cvt_f32_fp8(cur.kscale[1] >> (8 * bi), 0) *
@@ -447,8 +509,11 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
         } else {
             float sc0 = 1.0f, sc1 = 1.0f;
             if constexpr (KF == CQKV_FMT_MXFP4) {
-                sc0 = cur.kscale[0] ? __uint_as_float(cur.kscale[0] << 23) : 1.0f;
-                sc1 = cur.kscale[1] ? __uint_as_float(cur.kscale[1] << 23) : 1.0f;
+                // D = 256: chunk j holds head dims 64 g + 8 j + e, block byte j / 4 of the two
+                const uint32_t b0 = D == 256 ? (cur.kscale[0] >> (8 * (j >> 2))) & 0xffu : cur.kscale[0];
+                const uint32_t b1 = D == 256 ? (cur.kscale[1] >> (8 * (j >> 2))) & 0xffu : cur.kscale[1];
+                sc0 = b0 ? __uint_as_float(b0 << 23) : 1.0f;
+                sc1 = b1 ? __uint_as_float(b1 << 23) : 1.0f;
             }
             if constexpr (compact_tab<KF>()) {
                 k0 = __builtin_bit_cast(op_t<KF>, u32x4{prod_pair<0>(ktab, cur.k[0][j]),
@@ -467,8 +532,10 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
         s0 = mfma16x16x32(k0, qhi[j], s0);
         s1 = mfma16x16x32(k1, qhi[j], s1);
         if constexpr (is_prod<KF>()) {  // byte j of the lane key's sign bits
-            z0 = mfma16x16x32(signs_f16x8(cur.ksg[0], j), qsop[j], z0);
-            z1 = mfma16x16x32(signs_f16x8(cur.ksg[1], j), qsop[j], z1);
+            const uint32_t sw0 = j < 4 ? cur.ksg[0] : cur.ksg2[0];
+            const uint32_t sw1 = j < 4 ? cur.ksg[1] : cur.ksg2[1];
+            z0 = mfma16x16x32(signs_f16x8(sw0, j & 3), qsop[j], z0);
+            z1 = mfma16x16x32(signs_f16x8(sw1, j & 3), qsop[j], z1);
         }
         if (q_split) {
             s0 = mfma16x16x32(k0, qlo[j], s0);
@@ -481,7 +548,7 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
         // r0 (q . c + r1 sqrt(pi / 2) / D (S q) . z) (turbo_quant_impl.h:268-276); zk holds
         // -(S q) . z (the operands are -1 where the sign bit is set)
         const float zk[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
-        constexpr float kc = -kQjlConst / D;
+        const float kc = a.qjl_c;  // -sqrt(pi / 2) / d
 #pragma unroll
         for (int e = 0; e < 8; ++e)
             x[e] = (x[e] + __uint_as_float(cur.kr1[e]) * kc * zk[e]) *
@@ -493,6 +560,10 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
 #pragma unroll
         for (int e = 0; e < 8; ++e)
             x[e] = x[e] * __uint_as_float(cur.ks8[e]) * a.scale_log2;
+    }
+    if constexpr (TERMS) {  // soft-capping, then ALiBi (tq_logit, turbo_quant_impl.h:37-41)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = fa_logit2(x[e], a.cap2, slope2, qpos - (koff + kbase + e));
     }
     if (!full) {
 #pragma unroll
@@ -545,13 +616,16 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
         // value block u: P scaled by the keys' block-u scales, one bf16 operand (the E2M1 codes
         // and E8M0 scales are exact; P rounds to 8 significant bits, as in a bf16 flash
         // attention). The scale of E8M0 code c is the float with exponent field c (code 0: 0).
-        uint32_t vw[8];
+        uint32_t vw[8], vw2[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) vw[e] = (uint32_t)__shfl((int)cur.vs, 8 * g + e);
+        for (int e = 0; e < 8; ++e) {
+            vw[e] = (uint32_t)__shfl((int)cur.vs, 8 * g + e);
+            vw2[e] = D == 256 ? (uint32_t)__shfl((int)cur.vs2, 8 * g + e) : 0u;
+        }
         if (t0 + 32 > L) {  // uniform: keys past the written length may hold any scale bytes
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-                if (e >= nv) vw[e] = 0u;
+                if (e >= nv) vw[e] = vw2[e] = 0u;
         }
 #pragma unroll
         for (int u = 0; u < NCH; ++u) {
@@ -559,8 +633,9 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
             uint32_t *pwp = (uint32_t *)&pw;
 #pragma unroll
             for (int e = 0; e < 8; e += 2) {
-                const float s0 = __uint_as_float(((vw[e] >> (8 * u)) & 0xffu) << 23);
-                const float s1 = __uint_as_float(((vw[e + 1] >> (8 * u)) & 0xffu) << 23);
+                const uint32_t w0 = u < 4 ? vw[e] : vw2[e], w1 = u < 4 ? vw[e + 1] : vw2[e + 1];
+                const float s0 = __uint_as_float(((w0 >> (8 * (u & 3))) & 0xffu) << 23);
+                const float s1 = __uint_as_float(((w1 >> (8 * (u & 3))) & 0xffu) << 23);
                 pwp[e / 2] = pack_bf16x2(p[e] * s0, p[e + 1] * s1);
             }
             const op_t<VF> pb = __builtin_bit_cast(op_t<VF>, pw);
@@ -575,19 +650,19 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
         // TURBO4: the norm goes into P, which enters as one f16 operand (11 significant bits;
         // the lo part cost 8 more MFMAs per tile: config 5 246-254 -> 236 us same-box).
         float pv[8], sv[8];
-        uint32_t vw[8], vw2[8];  // MX / NVFP4: the keys' block scale bytes
+        uint32_t vw[8], vw2[8];  // MX: the keys' block scale bytes (vw2: bytes 4-7 at D = 256)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             // scales past the written length may be any bits
             if constexpr (direct_scales<VF>())
                 vw[e] = e < nv ? cur.vs8[e] : 0u;
             else if constexpr (VF == CQKV_FMT_NVFP4)
-                vw[e] = e < nv ? cur.nvb[(D == 128 ? 2 : 1) * e] : 0u;
+                vw[e] = e < nv ? cur.nvb[(D / 64) * e] : 0u;
             else
                 vw[e] = e < nv ? (uint32_t)__shfl((int)cur.vs, 8 * g + e) : 0u;
             sv[e] = __uint_as_float(vw[e]);  // FP8 scale, TURBO4 norm
-            if constexpr (VF == CQKV_FMT_NVFP4)
-                vw2[e] = D == 128 && e < nv ? cur.nvb[2 * e + 1] : 0u;
+            if constexpr (VF == CQKV_FMT_MXFP8 && D == 256)
+                vw2[e] = e < nv ? (uint32_t)__shfl((int)cur.vs2, 8 * g + e) : 0u;
             if constexpr (turbo_mse<VF>())
                 pv[e] = (e < nv && p[e] > 0.0f) ? p[e] * sv[e] : 0.0f;
             else
@@ -612,16 +687,17 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
                 float su[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    su[e] = e8m0_scale((vw[e] >> (8 * u)) & 0xffu);
+                    su[e] = e8m0_scale(((u < 4 ? vw[e] : vw2[e]) >> (8 * (u & 3))) & 0xffu);
                 v0 = fp8x8_scaled_bf16x8(cur.v[u][0], cur.v[u][1], su);
                 v1 = fp8x8_scaled_bf16x8(cur.v[u][2], cur.v[u][3], su);
             } else if constexpr (VF == CQKV_FMT_NVFP4) {
-                // this lane's rows 32u + 2n + h lie in block 2u + n / 8 of every key
+                // this lane's rows 32u + 2n + h lie in block 2u + n / 8 of every key: byte bi % 4
+                // of the key's word bi / 4 (D / 64 words per key)
                 const int bi = 2 * u + ((lane & 15) >> 3);
                 float sg[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const uint32_t w = bi < 4 ? vw[e] : vw2[e];
+                    const uint32_t w = e < nv ? cur.nvb[(D / 64) * e + (bi >> 2)] : 0u;
                     sg[e] = __builtin_amdgcn_cvt_f32_fp8(w >> (8 * (bi & 3)), 0) * gk[e];
                     if (e >= nv) sg[e] = 0.0f;
                 }
@@ -643,13 +719,14 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
 
 // Wavefronts per SIMD the register allocation must leave room for with MXFP4 keys and values:
 // 3 at D = 128 (168 VGPRs; at 176 only two fit and BASELINE config 3 runs 30 % slower), 4 at
-// D = 64; other formats take what the allocation gives.
+// D = 64; other formats, and D = 256 (one wavefront per SIMD, VGPRs and AGPRs), take what the
+// allocation gives.
 template <int KF, int VF, int D>
 constexpr int decode_min_waves() {
-    return KF == CQKV_FMT_MXFP4 && VF == CQKV_FMT_MXFP4 ? (D == 128 ? 3 : 4) : 1;
+    return KF == CQKV_FMT_MXFP4 && VF == CQKV_FMT_MXFP4 && D < 256 ? (D == 128 ? 3 : 4) : 1;
 }
 
-template <int KF, int VF, int D, int WAVES>
+template <int KF, int VF, int D, int WAVES, bool TERMS>
 __global__ __launch_bounds__(WAVES * 64)
 __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_kernel(DecodeArgs a) {
     constexpr int NCH = D / 32;
@@ -691,6 +768,15 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
     const bool col_ok = n < ncb;
     int lo, hi, lo_min, hi_max, lo_max, hi_min;
     key_range(col_ok ? (c0col + n) / a.group : 0, a.q_len, L, a.wl, a.wr, lo, hi);
+    // score terms of this lane's column: its ALiBi slope and its query's key position
+    float slope2 = 0.0f;
+    int qpos = 0;
+    if constexpr (TERMS) {
+        const int c = c0col + (col_ok ? n : 0);
+        qpos = c / a.group + L - a.q_len;
+        if (a.alibi && col_ok)
+            slope2 = a.alibi[(int64_t)b * a.alibi_bs + hk * a.group + c % a.group] * kLog2e;
+    }
     if (!col_ok) lo = hi = 0;
     key_range(c0col / a.group, a.q_len, L, a.wl, a.wr, lo_min, hi_min);
     key_range((c0col + ncb - 1) / a.group, a.q_len, L, a.wl, a.wr, lo_max, hi_max);
@@ -723,7 +809,7 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
     for (int idx = threadIdx.x; idx < 16 * D; idx += NT) {
         const int c = idx / D, d = idx % D;
         float v = 0.0f;
-        if (c < ncb) {
+        if (c < ncb && d < a.head_dim) {
             const int head = hk * a.group + (c0col + c) % a.group, qi = (c0col + c) / a.group;
             v = load_elem(a.q, (int64_t)b * a.q_sb + (int64_t)head * a.q_sh + (int64_t)qi * a.q_si + d,
                           a.q_dtype);
@@ -733,14 +819,26 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
     __syncthreads();
     if (a.rot_k) {
         for (int c = wave; c < ncb; c += WAVES) {
-            const bool act = lane < D / 2;
-            float v0 = act ? sm_q[c][2 * lane] : 0.0f, v1 = act ? sm_q[c][2 * lane + 1] : 0.0f;
-            if (act && sign_bit(a.ksign_bits, 2 * lane)) v0 = -v0;
-            if (act && sign_bit(a.ksign_bits, 2 * lane + 1)) v1 = -v1;
-            fwht_pairs_dec<D>(v0, v1, lane);
-            if (act) {
-                sm_q[c][2 * lane] = v0 * a.rot_scale;
-                sm_q[c][2 * lane + 1] = v1 * a.rot_scale;
+            if constexpr (D == 256) {
+                float v[4] = {sm_q[c][2 * lane], sm_q[c][2 * lane + 1], sm_q[c][128 + 2 * lane],
+                              sm_q[c][129 + 2 * lane]};
+                const int j[4] = {2 * lane, 2 * lane + 1, 128 + 2 * lane, 129 + 2 * lane};
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (sign_bit(a.ksign_bits, j[k])) v[k] = -v[k];
+                fwht_quads_dec(v[0], v[1], v[2], v[3], lane);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) sm_q[c][j[k]] = v[k] * a.rot_scale;
+            } else {
+                const bool act = lane < D / 2;
+                float v0 = act ? sm_q[c][2 * lane] : 0.0f, v1 = act ? sm_q[c][2 * lane + 1] : 0.0f;
+                if (act && sign_bit(a.ksign_bits, 2 * lane)) v0 = -v0;
+                if (act && sign_bit(a.ksign_bits, 2 * lane + 1)) v1 = -v1;
+                fwht_pairs_dec<D>(v0, v1, lane);
+                if (act) {
+                    sm_q[c][2 * lane] = v0 * a.rot_scale;
+                    sm_q[c][2 * lane + 1] = v1 * a.rot_scale;
+                }
             }
         }
         __syncthreads();
@@ -827,14 +925,16 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
     load_tile<KF, VF, D>(tb2, t + WAVES, t + WAVES < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
     __builtin_amdgcn_sched_barrier(0);
     for (; t < te; t += 2 * WAVES) {
-        compute_tile<KF, VF, D>(ta, t, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min, Lb, koff, tab,
-                             m_run, l_run, acc, kProd ? qsop : qhi, ktab, vtab);
+        compute_tile<KF, VF, D, TERMS>(ta, t, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min, Lb,
+                                       koff, tab, m_run, l_run, acc, kProd ? qsop : qhi, ktab, vtab,
+                                       slope2, qpos);
         __builtin_amdgcn_sched_barrier(0);
         load_tile<KF, VF, D>(ta, t + 2 * WAVES, t + 2 * WAVES < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
         __builtin_amdgcn_sched_barrier(0);
         if (t + WAVES < te)
-            compute_tile<KF, VF, D>(tb2, t + WAVES, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min,
-                                 Lb, koff, tab, m_run, l_run, acc, kProd ? qsop : qhi, ktab, vtab);
+            compute_tile<KF, VF, D, TERMS>(tb2, t + WAVES, a, qhi, qlo, q_split, lane, lo, hi, lo_max,
+                                           hi_min, Lb, koff, tab, m_run, l_run, acc,
+                                           kProd ? qsop : qhi, ktab, vtab, slope2, qpos);
         __builtin_amdgcn_sched_barrier(0);
         load_tile<KF, VF, D>(tb2, t + 3 * WAVES, t + 3 * WAVES < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
         __builtin_amdgcn_sched_barrier(0);
@@ -857,7 +957,7 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
     const int rows = a.batch * a.q_heads * a.q_len;
     // rotated values always leave partials: the combine unrotates them (an unrotation here costs
     // the MXFP4 kernel three VGPRs and its third wavefront per SIMD)
-    const bool single = a.splits == 1 && !a.rot_v;
+    const bool single = a.splits == 1 && !a.partials;
     for (int idx = threadIdx.x; idx < ncb * D; idx += NT) {
         const int c = idx / D, d = idx % D;
         float M = -__builtin_inff();
@@ -876,6 +976,7 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
             lse = M + __builtin_log2f(wsum);
         }
         const int head = hk * a.group + (c0col + c) % a.group, qi = (c0col + c) / a.group;
+        if (d >= a.head_dim) continue;  // plane row padding
         if (!single) {  // the partial of this split; combine_kernel merges the splits
             const int64_t row = ((int64_t)b * a.q_heads + head) * a.q_len + qi;
             a.part_o[((int64_t)split * rows + row) * D + d] = o;
@@ -890,26 +991,39 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
 // Wavefronts per workgroup: 8 when both formats have byte codes (HBM-bound: one workgroup per
 // plane fills a CU), 4 when either is a 4-bit format (its decode is VALU-heavy; two or three
 // independent workgroups per CU hide each other's latencies better than one of 8 wavefronts: 10 %
-// faster on BASELINE config 3).
+// faster on BASELINE config 3). Plane rows of 256 (d: the plane row length) take 4 wavefronts of
+// one per SIMD: two tiles in flight need more than 256 registers.
 constexpr int kWaves = 8;
-constexpr int waves_of(int kf, int vf) {
-    return (kf == CQKV_FMT_FP8 || kf == CQKV_FMT_MXFP8) && (vf == CQKV_FMT_FP8 || vf == CQKV_FMT_MXFP8)
+constexpr int waves_of(int kf, int vf, int d = 128) {
+    return d < 256 && (kf == CQKV_FMT_FP8 || kf == CQKV_FMT_MXFP8) &&
+                   (vf == CQKV_FMT_FP8 || vf == CQKV_FMT_MXFP8)
                ? kWaves
                : 4;
 }
 
+// d: the plane row length (64, 128 or 256); terms: soft-capping or ALiBi (the TERMS kernels)
+template <int KF, int VF, bool TERMS>
+inline void launch_decode_kvt(int d, dim3 grid, hipStream_t st, const DecodeArgs &a) {
+    constexpr int W = waves_of(KF, VF), W256 = waves_of(KF, VF, 256);
+    if (d == 64)
+        hipLaunchKernelGGL((decode_kernel<KF, VF, 64, W, TERMS>), grid, dim3(W * 64), 0, st, a);
+    else if (d == 128)
+        hipLaunchKernelGGL((decode_kernel<KF, VF, 128, W, TERMS>), grid, dim3(W * 64), 0, st, a);
+    else
+        hipLaunchKernelGGL((decode_kernel<KF, VF, 256, W256, TERMS>), grid, dim3(W256 * 64), 0, st, a);
+}
 template <int KF, int VF>
 inline void launch_decode_kv(int d, dim3 grid, hipStream_t st, const DecodeArgs &a) {
-    constexpr int W = waves_of(KF, VF);
-    if (d == 64)
-        hipLaunchKernelGGL((decode_kernel<KF, VF, 64, W>), grid, dim3(W * 64), 0, st, a);
-    else
-        hipLaunchKernelGGL((decode_kernel<KF, VF, 128, W>), grid, dim3(W * 64), 0, st, a);
+    if (a.cap2 > 0.0f || a.alibi) launch_decode_kvt<KF, VF, true>(d, grid, st, a);
+    else launch_decode_kvt<KF, VF, false>(d, grid, st, a);
 }
 
+// Launches the kernel of key format KF and value format vf; false (nothing launched) for a
+// pairing that has no kernel.
 template <int KF>
-inline void launch_decode_k(int vf, int d, dim3 grid, hipStream_t st, const DecodeArgs &a) {
+inline bool launch_decode_k(int vf, int d, dim3 grid, hipStream_t st, const DecodeArgs &a) {
     if constexpr (KF == kFmtTurboC) {  // compact keys come with TURBO4-table values only
+        if (vf != CQKV_FMT_TURBO4) return false;
         launch_decode_kv<KF, CQKV_FMT_TURBO4>(d, grid, st, a);
     } else {
         switch (vf) {
@@ -918,17 +1032,22 @@ inline void launch_decode_k(int vf, int d, dim3 grid, hipStream_t st, const Deco
         case CQKV_FMT_MXFP8: launch_decode_kv<KF, CQKV_FMT_MXFP8>(d, grid, st, a); break;
         case CQKV_FMT_NVFP4: launch_decode_kv<KF, CQKV_FMT_NVFP4>(d, grid, st, a); break;
         case kFmtTurboC:  // compact values come with 64 KB-table keys only
-            if constexpr (KF == CQKV_FMT_TURBO4 || KF == kFmtProd4)
+            if constexpr (KF == CQKV_FMT_TURBO4 || KF == kFmtProd4) {
                 launch_decode_kv<KF, kFmtTurboC>(d, grid, st, a);
-            break;
-        default: launch_decode_kv<KF, CQKV_FMT_TURBO4>(d, grid, st, a); break;
+                break;
+            } else {
+                return false;
+            }
+        case CQKV_FMT_TURBO4: launch_decode_kv<KF, CQKV_FMT_TURBO4>(d, grid, st, a); break;
+        default: return false;
         }
     }
+    return true;
 }
 
 // Per-key-format launchers, defined in decode_inst.hip (one object per key format).
 #define CQKV_DECODE_LAUNCHER(F) \
-    void decode_launch_k##F(int vf, int d, dim3 grid, hipStream_t st, const DecodeArgs &a);
+    bool decode_launch_k##F(int vf, int d, dim3 grid, hipStream_t st, const DecodeArgs &a);
 CQKV_DECODE_LAUNCHER(0)
 CQKV_DECODE_LAUNCHER(1)
 CQKV_DECODE_LAUNCHER(2)

@@ -161,15 +161,6 @@ using fa_op_t = typename std::conditional<F16, f16x8, bf16x8>::type;
 
 // The score terms of fa_logit (candle-core/kernels/flash_attn_impl.h:42-47) in exp2 units:
 // cap * tanh(s / cap) = cap - 2 cap / (e^(2 s / cap) + 1), then - slope * |pos - key|.
-__device__ inline float fa_logit2(float x, float cap2, float slope2, int dist) {
-    if (cap2 > 0.0f) {
-        const float e = __builtin_amdgcn_exp2f(x * (2.0f * kLog2e / cap2));
-        x = cap2 - 2.0f * cap2 * __builtin_amdgcn_rcpf(e + 1.0f);
-    }
-    if (slope2 != 0.0f) x -= slope2 * (float)(dist < 0 ? -dist : dist);
-    return x;
-}
-
 // Sum of the 8 elements of a bf16 / f16 operand (four dot2 with ones).
 template <bool F16>
 __device__ inline float fa_sum8(fa_op_t<F16> v) {

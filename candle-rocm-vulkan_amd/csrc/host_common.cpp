@@ -31,8 +31,10 @@ int fail(int code, const char *fmt, ...) {
 int check_side(const cqkv_side *s, const char *what) {
     if (!s) return fail(CQKV_ERR_ARG, "%s: null cache side", what);
     if (!code_bits(s->format)) return fail(CQKV_ERR_ARG, "%s: unknown format %d", what, s->format);
-    if (!supported_dim(s->head_dim))
-        return fail(CQKV_ERR_ARG, "%s: head_dim %d not supported (64, 128)", what, s->head_dim);
+    if (!supported_dim(s->format, s->head_dim))
+        return fail(CQKV_ERR_ARG,
+                    "%s: head_dim %d not supported (1-256; MX formats a multiple of 32, NVFP4 of 16)",
+                    what, s->head_dim);
     if (s->kv_heads <= 0) return fail(CQKV_ERR_ARG, "%s: kv_heads %d", what, s->kv_heads);
     if (s->capacity <= 0 || s->capacity % 32 != 0)
         return fail(CQKV_ERR_ARG, "%s: capacity %d is not a positive multiple of 32", what,
@@ -40,8 +42,13 @@ int check_side(const cqkv_side *s, const char *what) {
     if (!s->codes || !s->scales) return fail(CQKV_ERR_ARG, "%s: null codes / scales", what);
     if (s->is_value != 0 && s->is_value != 1)
         return fail(CQKV_ERR_ARG, "%s: is_value must be 0 or 1", what);
-    if (s->rotation < CQKV_ROT_DEFAULT || s->rotation > CQKV_ROT_HADAMARD)
-        return fail(CQKV_ERR_ARG, "%s: rotation %d (default, none or Hadamard)", what, s->rotation);
+    if (s->rotation < CQKV_ROT_DEFAULT || s->rotation > CQKV_ROT_AUTO)
+        return fail(CQKV_ERR_ARG, "%s: rotation %d (default, none, Hadamard, dense or auto)", what,
+                    s->rotation);
+    if (side_matrix_rot(s) && !s->rot)
+        return fail(CQKV_ERR_ARG,
+                    "%s: a %s rotation at head_dim %d needs the side's rotation matrix (rot)", what,
+                    side_rotation(s) == CQKV_ROT_DENSE ? "dense" : "Hadamard", s->head_dim);
     if (s->format == CQKV_FMT_TURBO4 && (s->bits < 0 || s->bits > 4))
         return fail(CQKV_ERR_ARG, "%s: TurboMse bits %d (1-4, 0: 4)", what, s->bits);
     if (s->format == CQKV_FMT_TURBOPROD && (s->bits < 0 || s->bits == 1 || s->bits > 5))
@@ -144,6 +151,58 @@ int turbo_codebook(int dim, int bits, float *centroids, float *boundaries) {
     return 0;
 }
 
+// rotation_matrix (candle-core/src/accel/turbo.rs:180-233) of a resolved kind: the identity, the
+// sign-flipped Sylvester Hadamard matrix / sqrt(dim), or the Dense matrix - dim x dim normals of
+// SplitMix64(seed ^ "ROTATE!!") (Box-Muller in f64), two passes of modified Gram-Schmidt in f64
+// with the dot products and norms summed in index order and no fused multiply-add (this file is
+// built with -ffp-contract=off, as the reference's Rust arithmetic rounds every operation),
+// rounded to f32. Row-major, y = Pi x.
+void rotation_matrix(int dim, int kind, uint64_t seed, float *out) {
+    const size_t n = (size_t)dim * dim;
+    for (size_t i = 0; i < n; ++i) out[i] = 0.0f;
+    if (kind == CQKV_ROT_NONE) {
+        for (int i = 0; i < dim; ++i) out[(size_t)i * dim + i] = 1.0f;
+    } else if (kind == CQKV_ROT_HADAMARD) {
+        std::vector<float> signs(dim);
+        turbo_signs(dim, seed, signs.data());
+        const float sc = 1.0f / sqrtf((float)dim);
+        for (int i = 0; i < dim; ++i)
+            for (int j = 0; j < dim; ++j)
+                out[(size_t)i * dim + j] = (__builtin_popcount((unsigned)(i & j)) & 1 ? -sc : sc) * signs[j];
+    } else {
+        uint64_t state = seed ^ 0x524f544154452121ull;
+        auto next = [&state]() {
+            state += 0x9e3779b97f4a7c15ull;
+            uint64_t z = state;
+            z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+            z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+            return z ^ (z >> 31);
+        };
+        const double two_pi = 2.0 * 3.141592653589793;
+        std::vector<double> rows(n);
+        for (size_t i = 0; i < n; ++i) {
+            const double u1 = ((double)(next() >> 11) + 0.5) / 9007199254740992.0;
+            const double u2 = ((double)(next() >> 11) + 0.5) / 9007199254740992.0;
+            rows[i] = sqrt(-2.0 * log(u1)) * cos(two_pi * u2);
+        }
+        for (int pass = 0; pass < 2; ++pass)
+            for (int i = 0; i < dim; ++i) {
+                double *ri = rows.data() + (size_t)i * dim;
+                for (int j = 0; j < i; ++j) {
+                    const double *rj = rows.data() + (size_t)j * dim;
+                    double dot = 0.0;
+                    for (int t = 0; t < dim; ++t) dot += ri[t] * rj[t];
+                    for (int t = 0; t < dim; ++t) ri[t] -= dot * rj[t];
+                }
+                double nn = 0.0;
+                for (int t = 0; t < dim; ++t) nn += ri[t] * ri[t];
+                nn = sqrt(nn);
+                for (int t = 0; t < dim; ++t) ri[t] /= nn;
+            }
+        for (size_t i = 0; i < n; ++i) out[i] = (float)rows[i];
+    }
+}
+
 // Column signs of the seeded Hadamard rotation: SplitMix64 seeded with seed ^ "HADAMARD"
 // (0x484144414d415244 in ASCII), one draw per column, even draw -> +1
 // (candle-core/src/accel/turbo.rs:150-163, 188-196).
@@ -183,24 +242,26 @@ void qjl_matrix(int dim, uint64_t seed, float *out) {
 
 extern "C" {
 
+// Planes hold rows of the plane row length kernel_dim(head_dim).
 size_t cqkv_codes_plane_bytes(int32_t format, int32_t head_dim, int32_t capacity) {
     const int bits = cqkv::code_bits(format);
-    if (!bits || !cqkv::supported_dim(head_dim) || capacity <= 0) return 0;
-    return (size_t)capacity * (size_t)head_dim * (size_t)bits / 8;
+    if (!bits || !cqkv::supported_dim(format, head_dim) || capacity <= 0) return 0;
+    return (size_t)capacity * (size_t)cqkv::kernel_dim(head_dim) * (size_t)bits / 8;
 }
 
 size_t cqkv_scales_plane_bytes(int32_t format, int32_t head_dim, int32_t capacity) {
-    if (!cqkv::code_bits(format) || !cqkv::supported_dim(head_dim) || capacity <= 0) return 0;
+    if (!cqkv::code_bits(format) || !cqkv::supported_dim(format, head_dim) || capacity <= 0) return 0;
+    const int dk = cqkv::kernel_dim(head_dim);
     if (format == CQKV_FMT_TURBOPROD)  // norms, |r|, sign bits
-        return (size_t)capacity * (8 + (size_t)head_dim / 8);
+        return (size_t)capacity * (8 + (size_t)dk / 8);
     const int be = cqkv::block_elems(format);
-    const size_t blocks = be ? (size_t)capacity * (size_t)(head_dim / be) : 0;
+    const size_t blocks = be ? (size_t)capacity * (size_t)(dk / be) : 0;
     return blocks + (cqkv::token_scale(format) ? (size_t)capacity * 4 : 0);
 }
 
 int32_t cqkv_reference_row_words(int32_t format, int32_t bits, int32_t head_dim) {
     const int cb = cqkv::code_bits(format);
-    if (!cb || !cqkv::supported_dim(head_dim)) return 0;
+    if (!cb || !cqkv::supported_dim(format, head_dim)) return 0;
     if (cqkv::is_turbo(format)) {  // formats.rs:226-240: b-bit (prod: b - 1) codes, prod signs
         const int b = bits ? bits : 4;
         if (format == CQKV_FMT_TURBO4 && (b < 1 || b > 4)) return 0;
@@ -228,6 +289,21 @@ int cqkv_turbo_signs(int32_t head_dim, uint64_t seed, float *signs) {
     if (!signs || head_dim <= 0 || (head_dim & (head_dim - 1)) != 0)
         return cqkv::fail(CQKV_ERR_ARG, "cqkv_turbo_signs: head_dim %d", head_dim);
     cqkv::turbo_signs(head_dim, seed, signs);
+    return CQKV_OK;
+}
+
+int32_t cqkv_resolve_rotation(int32_t format, int32_t kind, int32_t head_dim) {
+    if (head_dim < 1 || head_dim > 1024) return -1;
+    return cqkv::resolve_rotation(format, kind, head_dim);
+}
+
+int cqkv_rotation_matrix(int32_t head_dim, int32_t kind, uint64_t seed, float *out) {
+    if (!out || head_dim < 1 || head_dim > 1024)
+        return cqkv::fail(CQKV_ERR_ARG, "cqkv_rotation_matrix: head_dim %d / null output", head_dim);
+    // DEFAULT as AUTO (the TurboQuant formats' own rotation)
+    const int r = cqkv::resolve_rotation(CQKV_FMT_TURBO4, kind, head_dim);
+    if (r < 0) return cqkv::fail(CQKV_ERR_ARG, "cqkv_rotation_matrix: rotation %d", kind);
+    cqkv::rotation_matrix(head_dim, r, seed, out);
     return CQKV_OK;
 }
 

@@ -44,8 +44,13 @@
  *   cqkv_rows_import /     the reference's packed row layout [codes][aux][rsc0][rsc1]
  *   cqkv_rows_export       (candle-core/src/accel/formats.rs:206-242)
  *   cqkv_side_copy         the grown-buffer copy of Cache::append (candle-nn/src/kv_cache.rs:56-99)
- *   cqkv_qjl_matrix / cqkv_turbo_codebook / cqkv_turbo_signs
- *                          qjl_matrix, Codebook, the Hadamard signs (candle-core/src/accel/turbo.rs)
+ *   cqkv_dequantize_rows   RocmStorage::tq_dequantize + TurboQuantizer::dequantize_rows
+ *                          (candle-core/src/rocm_backend/accel.rs:380-419,
+ *                           candle-nn/src/turbo_quant.rs:250-300, 612-689, 948-966)
+ *   cqkv_qjl_matrix / cqkv_turbo_codebook / cqkv_turbo_signs / cqkv_rotation_matrix /
+ *   cqkv_resolve_rotation  qjl_matrix, Codebook, the Hadamard signs, rotation_matrix
+ *                          (candle-core/src/accel/turbo.rs), RotationKind::resolve
+ *                          (candle-core/src/accel/config.rs:131-138)
  *
  * Cache layout in HBM (one "plane" per (batch, kv head), planes batch-major, `capacity` tokens):
  *   format        codes plane (bytes)                  scales plane (bytes)
@@ -62,6 +67,8 @@
  *   NVFP4 values  capacity * D/2    8-token tiles      the same
  *   TURBOPROD keys capacity * D/2   row-major nibbles  capacity * (8 + D/8): f32 norms, f32 |r|,
  *                  (3-bit codes)                       then D/8 QJL sign-bit bytes per token
+ * D in this table is the plane row length D' = 64, 128 or 256, the smallest that holds the head
+ * dim (elements past the head dim are zero codes with zero block scales).
  * Row-major: token t's codes at t * row_bytes, element j at byte j (FP8) or nibble j (bits 4(j%2)
  * of byte j/2), i.e. the reference's code stream. 8-token tiles (values): token t, element j at
  * tile t/8, offset j*8 + t%8 bytes (FP8) or bits 4(t%8) of the little-endian u32 j (4-bit). The
@@ -127,20 +134,34 @@ enum { CQKV_BF16 = 0, CQKV_F16 = 1, CQKV_F32 = 2 };
 enum { CQKV_ROPE_HALVES = 1, CQKV_ROPE_INTERLEAVED = 2 };
 
 /* Rotation of the rows before quantization (RotationKind of candle-core/src/accel/config.rs:
- * 104-139, TurboQuantizer::rotate, candle-nn/src/turbo_quant.rs:182-189). DEFAULT is the format's
- * own: Hadamard for TURBO4, none for the others. HADAMARD = the sign-flipped Sylvester matrix / sqrt(D)
- * of `seed` (rotation_matrix, candle-core/src/accel/turbo.rs:180-203; what RotationKind::Auto
- * resolves to for the power-of-two head dims here; DEFAULT rotates TURBOPROD sides as well).
- * The cache stores codes of the rotated rows;
- * decode rotates the queries with the key side's rotation and unrotates the output with the
- * value side's. */
-enum { CQKV_ROT_DEFAULT = 0, CQKV_ROT_NONE = 1, CQKV_ROT_HADAMARD = 2 };
+ * 104-139, TurboQuantizer::rotate, candle-nn/src/turbo_quant.rs:182-189). Resolved for the head
+ * dim D as RotationKind::resolve (config.rs:131-138):
+ *   DEFAULT   the format's own: AUTO for the TurboQuant formats, NONE for the others;
+ *   AUTO      HADAMARD when D is a power of two, else DENSE;
+ *   HADAMARD  the sign-flipped Sylvester matrix / sqrt(D) of `seed` (rotation_matrix,
+ *             candle-core/src/accel/turbo.rs:180-203); DENSE when D is not a power of two;
+ *   DENSE     the seeded Gram-Schmidt orthogonal matrix of rotation_matrix (turbo.rs:204-230).
+ * The cache stores codes of the rotated rows x Pi^T; decode rotates the queries with the key
+ * rotation and unrotates the output with the value rotation. A HADAMARD side at D = 64, 128 or
+ * 256 runs the in-register Walsh-Hadamard transform; every other rotating side multiplies by its
+ * matrix cqkv_side.rot (f32, sums in index order). */
+enum {
+    CQKV_ROT_DEFAULT = 0,
+    CQKV_ROT_NONE = 1,
+    CQKV_ROT_HADAMARD = 2,
+    CQKV_ROT_DENSE = 3,
+    CQKV_ROT_AUTO = 4
+};
 
 /* One side (keys or values) of a quantized cache. */
 typedef struct cqkv_side {
     int32_t format;    /* CQKV_FMT_* */
     int32_t is_value;  /* 0 keys (row-major codes), 1 values (8-token tiles) */
-    int32_t head_dim;  /* D: 64 or 128 */
+    int32_t head_dim;  /* D: 1-256 (the reference's fused attention takes D <= FA_MAX_HEAD_DIM =
+                          256, candle-nn/src/turbo_quant.rs:1158); MXFP4 / MXFP8 a multiple of 32
+                          and NVFP4 of 16 (QuantFormat::validate, formats.rs:166-187). Planes hold
+                          rows of D' = 64, 128 or 256 elements (the smallest that holds D); the
+                          elements past D are stored as zeros and never read into a result. */
     int32_t kv_heads;  /* Hkv */
     int32_t capacity;  /* tokens per plane, a multiple of 32 */
     int32_t rotation;  /* CQKV_ROT_* */
@@ -154,12 +175,31 @@ typedef struct cqkv_side {
     void *scales;      /* device, batch * kv_heads planes of cqkv_scales_plane_bytes() */
     const float *qjl;  /* TURBOPROD: device D x D f32 QJL matrix S (row-major, cqkv_qjl_matrix
                           of the side's seed); NULL for the other formats */
+    const float *rot;  /* device D x D f32 rotation matrix Pi of the side (row-major,
+                          cqkv_rotation_matrix(D, rotation, seed)): required when the rotation
+                          resolves to DENSE, or to HADAMARD at a D other than 64, 128 and 256,
+                          and by cqkv_dequantize_rows(unrotate) on any rotating side; may be
+                          NULL otherwise (the reference's TurboQuantizer keeps Pi on the device
+                          whenever it rotates, turbo_quant.rs:57-68) */
 } cqkv_side;
 
 /* The QJL projection S of TurboProd: D x D row-major f32 standard normals from SplitMix64 seeded
  * with (seed + 1) ^ 0x514a4c5f534b4554, Box-Muller in f64 (qjl_matrix,
  * candle-core/src/accel/turbo.rs:236-239). Host memory; upload it for cqkv_side.qjl. */
 int cqkv_qjl_matrix(int32_t head_dim, uint64_t seed, float *out);
+
+/* The rotation a side of `format` with rotation `kind` uses at head dim D (CQKV_ROT_NONE,
+ * CQKV_ROT_HADAMARD or CQKV_ROT_DENSE; RotationKind::resolve, candle-core/src/accel/config.rs:
+ * 131-138, with DEFAULT as the format's own), or -1 for an invalid kind / D. */
+int32_t cqkv_resolve_rotation(int32_t format, int32_t kind, int32_t head_dim);
+
+/* The D x D row-major f32 matrix Pi of rotation `kind` (resolved for D, DEFAULT as AUTO) and
+ * `seed`: rotation_matrix (candle-core/src/accel/turbo.rs:180-233) - the identity, the seeded
+ * sign-flipped Hadamard matrix / sqrt(D), or the Dense matrix: D x D standard normals of
+ * SplitMix64(seed ^ 0x524f544154452121) (Box-Muller in f64), orthonormalised by two passes of
+ * modified Gram-Schmidt in f64 (sums in index order), rounded to f32. Host memory; upload it for
+ * cqkv_side.rot. D 1-1024. */
+int cqkv_rotation_matrix(int32_t head_dim, int32_t kind, uint64_t seed, float *out);
 
 /* Bytes of one (batch, head) plane of codes / scales; 0 for an invalid format or D. */
 size_t cqkv_codes_plane_bytes(int32_t format, int32_t head_dim, int32_t capacity);
@@ -202,15 +242,21 @@ int cqkv_rope_quant_append(const cqkv_side *k_side, const cqkv_side *v_side, con
  *   keys [0, kv_lens[b]) of plane b are attended (device int32 array; NULL: kv_len for all),
  *   kv_len = the largest length (host), used to size the launch;
  *   window_left / window_right: -1 = unbounded (causal = (-1, 0));
+ *   softcap > 0: score = softcap * tanh(score / softcap) (0 disables it); alibi_slopes (device
+ *   f32, NULL: none): score -= slope * |pos - key| with slope = alibi_slopes[b *
+ *   alibi_batch_stride + head], stride 0 (slopes per head) or q_heads - the reference's
+ *   tq_logit (candle-core/kernels/turbo_quant_impl.h:37-41) from FlashAttnConfig's softcap and
+ *   alibi_slopes (TqAttnArgs, candle-core/src/accel/turbo.rs:506-530);
  *   q head h reads kv head h / (q_heads / kv_heads); any q_len (chunked prefill or speculative
  *   decode over the cache: the reference's grid (Lq * Hq / G, splits, B),
  *   candle-core/kernels/turbo_quant_impl.h:621-627).
  *   The key and value sides may differ in format; a side that rotates (CQKV_ROT_*) has the
  *   queries rotated with the key rotation and the output unrotated with the value rotation.
  * splits: key splits per (batch, kv head); 0 = automatic. workspace: device scratch of at least
- * cqkv_decode_workspace_bytes() for the split count used (partials are written for more than
- * one split, and at any split count when the value side rotates); NULL = allocated (and freed)
- * by the call. */
+ * cqkv_decode_workspace_bytes() for the split count used (it is used for more than one split,
+ * for a rotating value side, for a key side that rotates by its matrix and for TURBOPROD keys
+ * below a plane row length; it holds the partials, the rotated queries and the combined rows
+ * before their unrotation); NULL = allocated (and freed) by the call. */
 size_t cqkv_decode_workspace_bytes(int32_t batch, int32_t q_heads, int32_t q_len, int32_t head_dim,
                                    int32_t splits);
 /* The key splits cqkv_decode_attention uses with splits = 0 for a cache of key / value formats
@@ -222,6 +268,7 @@ int cqkv_decode_attention(const void *q, int32_t q_dtype, const int64_t q_stride
                           const cqkv_side *k, const cqkv_side *v, int32_t batch, int32_t q_heads,
                           int32_t q_len, const int32_t *kv_lens, int32_t kv_len,
                           float softmax_scale, int32_t window_left, int32_t window_right,
+                          float softcap, const float *alibi_slopes, int32_t alibi_batch_stride,
                           void *out, int32_t out_dtype, const int64_t out_strides[3],
                           int32_t splits, void *workspace, size_t workspace_bytes,
                           cqkv_stream_t stream);
@@ -241,7 +288,8 @@ int cqkv_decode_attention_noalloc(const void *q, int32_t q_dtype, const int64_t 
                                   const cqkv_side *k, const cqkv_side *v, int32_t batch,
                                   int32_t q_heads, int32_t q_len, const int32_t *kv_lens,
                                   int32_t kv_len, float softmax_scale, int32_t window_left,
-                                  int32_t window_right, void *out, int32_t out_dtype,
+                                  int32_t window_right, float softcap, const float *alibi_slopes,
+                                  int32_t alibi_batch_stride, void *out, int32_t out_dtype,
                                   const int64_t out_strides[3], int32_t splits,
                                   cqkv_stream_t stream);
 
@@ -269,7 +317,8 @@ size_t cqkv_decode_paged_workspace_bytes(const cqkv_kv_block *blocks, int32_t n_
 int cqkv_decode_attention_paged(const void *q, int32_t q_dtype, const int64_t q_strides[3],
                                 const cqkv_kv_block *blocks, int32_t n_blocks, int32_t batch,
                                 int32_t q_heads, int32_t q_len, float softmax_scale,
-                                int32_t window_left, int32_t window_right, void *out,
+                                int32_t window_left, int32_t window_right, float softcap,
+                                const float *alibi_slopes, int32_t alibi_batch_stride, void *out,
                                 int32_t out_dtype, const int64_t out_strides[3], void *workspace,
                                 size_t workspace_bytes, cqkv_stream_t stream);
 
@@ -413,6 +462,28 @@ int cqkv_rows_import(const cqkv_side *side, const uint32_t *rows, int32_t batch,
                      int32_t position, cqkv_stream_t stream);
 int cqkv_rows_export(const cqkv_side *side, uint32_t *rows, int32_t batch, int32_t tokens,
                      int32_t position, cqkv_stream_t stream);
+
+/* Dequantization of cache rows (TqDequant + TurboQuantizer::dequantize_rows, the device half of
+ * TurboKvCache::keys_values: candle-core/src/rocm_backend/accel.rs:380-419,
+ * candle-nn/src/turbo_quant.rs:250-300, 612-689, 948-966): positions [position, position +
+ * tokens) of every (batch, kv head) plane are written to out (batch, kv_heads, tokens, D) with
+ * element strides out_strides {batch, head, token} (D contiguous) in out_dtype (CQKV_BF16 / F16 /
+ * F32, rounded to nearest even from f32). Each element is rsc0 * element_j of
+ * RowCodec::dequantize_row (candle-core/src/accel/turbo.rs:398-424) in f32 - the FP8 scale times
+ * the E4M3 value, E2M1 times its E8M0 / E4M3 block scale (NVFP4: then times the token's scale),
+ * the centroid times the norm - plus, for TURBOPROD keys, the QJL correction
+ * sum_i z_i S[i][j] with z_i = +-rsc0 rsc1 sqrt(pi/2) / D (sums in index order). unrotate != 0
+ * then multiplies the rows by the side's Pi (y Pi, TurboQuantizer::unrotate, sums in index order;
+ * needs cqkv_side.rot when the side rotates), giving the unrotated values keys_values returns
+ * before its dtype cast. Positions past the capacity are an error. workspace: device scratch of
+ * at least cqkv_dequantize_workspace_bytes() (non-zero only for TURBOPROD or unrotate on a
+ * rotating side); NULL = allocated (stream-ordered) and freed by the call. */
+size_t cqkv_dequantize_workspace_bytes(const cqkv_side *side, int32_t batch, int32_t tokens,
+                                       int32_t unrotate);
+int cqkv_dequantize_rows(const cqkv_side *side, int32_t batch, int32_t position, int32_t tokens,
+                         int32_t unrotate, void *out, int32_t out_dtype,
+                         const int64_t out_strides[3], void *workspace, size_t workspace_bytes,
+                         cqkv_stream_t stream);
 
 /* Cache growth (the copy of Cache::append into a grown buffer, candle-nn/src/kv_cache.rs:56-99):
  * the first `tokens` positions of every (batch, kv head) plane of src are copied into dst, a side

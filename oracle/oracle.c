@@ -698,7 +698,7 @@ int orc_cache_attention(const uint16_t *q_bf16, const uint32_t *k_rows, const ui
                         int k_mode, int k_bits, int v_mode, int v_bits, const float *pi_k,
                         const float *pi_v, const float *qjl_k, int b, int hq, int hkv, int lq,
                         int cap, int d, const int32_t *kv_lens, int lk, float scale, int wl, int wr,
-                        float *out, int threads) {
+                        float softcap, const float *alibi, float *out, int threads) {
     deq_ctx kc, vc;
     if (orc_codec_init(&kc.c, k_mode, k_bits, d) != 0 || orc_codec_init(&vc.c, v_mode, v_bits, d) != 0)
         return -1;
@@ -730,8 +730,8 @@ int orc_cache_attention(const uint16_t *q_bf16, const uint32_t *k_rows, const ui
     orc_parallel((size_t)b * hkv, threads, deq_cache_body, &kc);
     orc_parallel((size_t)b * hkv, threads, deq_cache_body, &vc);
     for (size_t i = 0; i < (size_t)b * hq * lq * d; ++i) q[i] = orc_bf16_to_f32(q_bf16[i]);
-    const int rc = orc_attention_unfused(q, k, v, b, hq, hkv, lq, lk, d, kv_lens, scale, 0.0f, wl, wr,
-                                         NULL, out, threads);
+    const int rc = orc_attention_unfused(q, k, v, b, hq, hkv, lq, lk, d, kv_lens, scale, softcap, wl,
+                                         wr, alibi, out, threads);
     free(k);
     free(v);
     free(q);

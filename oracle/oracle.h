@@ -103,12 +103,13 @@ int orc_attention_unfused(const float *q, const float *k, const float *v, int b,
 /* The reference's CPU decode path over packed rows (turbo_quant.rs:948-990 then
  * flash_attn.rs:930-1000): dequantize K/V rows (b, hkv, cap, row_words), unrotate, round to
  * bf16 (the appended dtype), attend with bf16 queries q (b, hq, lq, d) given as bf16 bits.
- * pi_k / pi_v: rotation matrices or NULL. Output f32 (b, hq, lq, d) (round to bf16 to compare). */
+ * pi_k / pi_v: rotation matrices or NULL; softcap / alibi (per-head slopes or NULL) as in
+ * orc_attention_unfused. Output f32 (b, hq, lq, d) (round to bf16 to compare). */
 int orc_cache_attention(const uint16_t *q_bf16, const uint32_t *k_rows, const uint32_t *v_rows,
                         int k_mode, int k_bits, int v_mode, int v_bits, const float *pi_k,
                         const float *pi_v, const float *qjl_k, int b, int hq, int hkv, int lq,
                         int cap, int d, const int32_t *kv_lens, int lk, float scale, int wl, int wr,
-                        float *out, int threads);
+                        float softcap, const float *alibi, float *out, int threads);
 
 /* Split combine (candle-core/kernels/turbo_quant_impl.h:659-685). part_o (splits, rows, d),
  * part_lse (splits, rows). */

@@ -62,7 +62,7 @@ def lib() -> ctypes.CDLL:
         L.orc_attention_unfused.argtypes = [P, P, P, i32, i32, i32, i32, i32, i32, P, f32, f32,
                                             i32, i32, P, P, i32]
         L.orc_cache_attention.argtypes = [P, P, P, i32, i32, i32, i32, P, P, P, i32, i32, i32,
-                                          i32, i32, i32, P, i32, f32, i32, i32, P, i32]
+                                          i32, i32, i32, P, i32, f32, i32, i32, f32, P, P, i32]
         L.orc_qjl_matrix.argtypes = [i32, u64, P]
         L.orc_quantize_rows_qjl.argtypes = [i32, i32, sz, P, P, P, i32]
         L.orc_dequantize_rows_qjl.argtypes = [i32, i32, sz, P, P, P, i32]
@@ -349,10 +349,11 @@ def attention_unfused(q, k, v, scale, kv_lens=None, softcap=0.0, wl=-1, wr=-1, a
 
 
 def cache_attention(q_bf16_bits, k_rows, v_rows, k_fmt, v_fmt, pi_k, pi_v, lk, scale,
-                    kv_lens=None, wl=-1, wr=-1, threads: int = 8, qjl_k=None) -> np.ndarray:
+                    kv_lens=None, wl=-1, wr=-1, threads: int = 8, qjl_k=None, softcap=0.0,
+                    alibi=None) -> np.ndarray:
     """The reference CPU decode path over packed rows. q_bf16_bits (b, hq, lq, d) u16,
     k_rows / v_rows (b, hkv, cap, row_words) u32, formats (mode, bits); qjl_k: the QJL matrix
-    of TurboProd keys. Output f32."""
+    of TurboProd keys; softcap and per-head ALiBi slopes as attention_unfused. Output f32."""
     q = np.ascontiguousarray(q_bf16_bits, dtype=np.uint16)
     k_rows = np.ascontiguousarray(k_rows, dtype=np.uint32)
     v_rows = np.ascontiguousarray(v_rows, dtype=np.uint32)
@@ -363,9 +364,10 @@ def cache_attention(q_bf16_bits, k_rows, v_rows, k_fmt, v_fmt, pi_k, pi_v, lk, s
     pk = None if pi_k is None else np.ascontiguousarray(pi_k, dtype=np.float32)
     pv = None if pi_v is None else np.ascontiguousarray(pi_v, dtype=np.float32)
     sk = None if qjl_k is None else np.ascontiguousarray(qjl_k, dtype=np.float32)
+    al = None if alibi is None else np.ascontiguousarray(alibi, dtype=np.float32)
     rc = lib().orc_cache_attention(_p(q), _p(k_rows), _p(v_rows), k_fmt[0], k_fmt[1], v_fmt[0],
                                    v_fmt[1], _p(pk), _p(pv), _p(sk), b, hq, hkv, lq, cap, d, _p(kl), lk,
-                                   scale, wl, wr, _p(out), threads)
+                                   scale, wl, wr, softcap, _p(al), _p(out), threads)
     if rc != 0:
         raise ValueError(f"cache_attention failed ({rc})")
     return out

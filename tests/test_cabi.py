@@ -40,7 +40,19 @@ def test_plane_sizes(cq):
     assert L.cqkv_scales_plane_bytes(cq.MXFP4, 128, 64) == 64 * 4
     assert L.cqkv_scales_plane_bytes(cq.MXFP4, 64, 64) == 64 * 2
     assert L.cqkv_codes_plane_bytes(cq.TURBO4, 128, 32) == 32 * 64
-    assert L.cqkv_codes_plane_bytes(cq.FP8, 96, 32) == 0
+    # head dims 1-256 (FA_MAX_HEAD_DIM); planes hold rows of 64, 128 or 256 elements
+    assert L.cqkv_codes_plane_bytes(cq.FP8, 96, 32) == 32 * 128
+    assert L.cqkv_codes_plane_bytes(cq.FP8, 80, 32) == 32 * 128
+    assert L.cqkv_codes_plane_bytes(cq.FP8, 48, 32) == 32 * 64
+    assert L.cqkv_codes_plane_bytes(cq.FP8, 256, 32) == 32 * 256
+    assert L.cqkv_scales_plane_bytes(cq.MXFP4, 256, 32) == 32 * 8
+    assert L.cqkv_scales_plane_bytes(cq.NVFP4, 80, 32) == 32 * 8 + 32 * 4
+    assert L.cqkv_codes_plane_bytes(cq.FP8, 257, 32) == 0
+    assert L.cqkv_codes_plane_bytes(cq.FP8, 0, 32) == 0
+    # block formats need whole blocks (QuantFormat::validate, formats.rs:166-187)
+    assert L.cqkv_codes_plane_bytes(cq.MXFP4, 80, 32) == 0
+    assert L.cqkv_codes_plane_bytes(cq.MXFP8, 96, 32) == 32 * 128
+    assert L.cqkv_codes_plane_bytes(cq.NVFP4, 72, 32) == 0
     assert L.cqkv_codes_plane_bytes(7, 128, 32) == 0
     # MXFP8: byte codes + E8M0 per 32; NVFP4: nibbles + E4M3 per 16, then an f32 per token
     assert L.cqkv_codes_plane_bytes(cq.MXFP8, 128, 64) == 64 * 128
@@ -112,10 +124,19 @@ def test_argument_errors_are_status_codes(cq):
     x = (ctypes.c_int64 * 3)(1, 1, 1)
     assert L.cqkv_quant_append(None, None, 0, x, 1, 1, None, 0, None) == cq.ERR_ARG
     assert b"null cache side" in L.cqkv_last_error()
-    side = cq.Side(cq.FP8, 0, 96, 8, 64, 0, 0, 0, 0, 1, 1)
+    side = cq.Side(cq.FP8, 0, 300, 8, 64, 0, 0, 0, 0, 1, 1)
     assert L.cqkv_quant_append(ctypes.byref(side), ctypes.c_void_p(1), 0, x, 1, 1, None, 0,
                                None) == cq.ERR_ARG
-    assert b"head_dim 96" in L.cqkv_last_error()
+    assert b"head_dim 300" in L.cqkv_last_error()
+    side = cq.Side(cq.MXFP4, 0, 80, 8, 64, 0, 0, 0, 0, 1, 1)
+    assert L.cqkv_quant_append(ctypes.byref(side), ctypes.c_void_p(1), 0, x, 1, 1, None, 0,
+                               None) == cq.ERR_ARG
+    assert b"head_dim 80" in L.cqkv_last_error()
+    # a dense rotation (TurboQuant at a head dim that is not a power of two) needs its matrix
+    side = cq.Side(cq.TURBO4, 0, 96, 8, 64, 0, 0, 0, 42, 1, 1)
+    assert L.cqkv_quant_append(ctypes.byref(side), ctypes.c_void_p(1), 0, x, 1, 1, None, 0,
+                               None) == cq.ERR_ARG
+    assert b"rotation matrix" in L.cqkv_last_error()
     side = cq.Side(cq.FP8, 0, 128, 8, 48, 0, 0, 0, 0, 1, 1)
     assert L.cqkv_quant_append(ctypes.byref(side), ctypes.c_void_p(1), 0, x, 1, 1, None, 0,
                                None) == cq.ERR_ARG
@@ -128,13 +149,20 @@ def test_argument_errors_are_status_codes(cq):
     # decode: a key side given twice, more (query, head) columns than 2^24, kv_len past the
     # capacity
     vs = cq.Side(cq.FP8, 1, 128, 8, 64, 0, 0, 0, 0, 1, 1)
-    args = lambda k, v, hq, lq, kvlen: L.cqkv_decode_attention(
+    args = lambda k, v, hq, lq, kvlen, cap=0.0, bs=0: L.cqkv_decode_attention(
         ctypes.c_void_p(1), 0, x, ctypes.byref(k), ctypes.byref(v), 1, hq, lq, None, kvlen,
-        0.1, -1, -1, ctypes.c_void_p(1), 0, x, 0, None, 0, None)
+        0.1, -1, -1, cap, ctypes.c_void_p(1) if bs else None, bs, ctypes.c_void_p(1), 0, x, 0,
+        None, 0, None)
     assert args(side, side, 8, 1, 10) == cq.ERR_ARG
     assert args(side, vs, 8 * 32, 1 << 20, 10) == cq.ERR_ARG
     assert args(side, vs, 8, 1, 65) == cq.ERR_ARG
     assert b"capacity" in L.cqkv_last_error()
+    # score terms: a finite, non-negative soft cap; ALiBi slopes per head or per (batch, head)
+    assert args(side, vs, 8, 1, 10, cap=-1.0) == cq.ERR_ARG
+    assert b"softcap" in L.cqkv_last_error()
+    assert args(side, vs, 8, 1, 10, cap=float("inf")) == cq.ERR_ARG
+    assert args(side, vs, 8, 1, 10, bs=3) == cq.ERR_ARG
+    assert b"alibi" in L.cqkv_last_error()
 
 
 def test_flash_attn_ext_argument_errors(cq):
@@ -232,7 +260,8 @@ def test_empty_inputs(cq):
 
     def decode(batch, ql, kvl=10):
         return L.cqkv_decode_attention(None, 0, xs, ctypes.byref(k0), ctypes.byref(v0), batch, 8,
-                                       ql, None, kvl, 0.1, -1, -1, None, 0, xs, 0, None, 0, None)
+                                       ql, None, kvl, 0.1, -1, -1, 0.0, None, 0, None, 0, xs, 0,
+                                       None, 0, None)
     assert decode(0, 1) == cq.OK
     assert decode(1, 0) == cq.OK
     assert decode(1, 0, kvl=65) == cq.ERR_ARG  # kv_len above the capacity
@@ -242,8 +271,8 @@ def test_empty_inputs(cq):
     def paged(rows, batch, ql):
         arr = (cq.KvBlock * 1)()
         arr[0].k, arr[0].v, arr[0].rows = ctypes.pointer(k0), ctypes.pointer(v0), rows
-        return L.cqkv_decode_attention_paged(None, 0, xs, arr, 1, batch, 8, ql, 0.1, -1, -1, None,
-                                             0, xs, None, 0, None)
+        return L.cqkv_decode_attention_paged(None, 0, xs, arr, 1, batch, 8, ql, 0.1, -1, -1, 0.0,
+                                             None, 0, None, 0, xs, None, 0, None)
     assert paged(10, 0, 1) == cq.OK
     assert paged(10, 1, 0) == cq.OK
     assert paged(0, 1, 0) == cq.ERR_ARG
@@ -283,7 +312,8 @@ def test_paged_argument_errors_and_workspace(cq):
 
     def call(arr, n, hq=8, lq=1):
         return L.cqkv_decode_attention_paged(ctypes.c_void_p(1), 0, x, arr, n, 1, hq, lq, 0.1,
-                                             -1, -1, ctypes.c_void_p(1), 0, x, None, 0, None)
+                                             -1, -1, 0.0, None, 0, ctypes.c_void_p(1), 0, x, None,
+                                             0, None)
     assert call(None, 0) == cq.ERR_ARG
     assert b"no blocks" in L.cqkv_last_error()
     assert call(blocks((k0, v0, 65)), 1) == cq.ERR_ARG  # rows above the capacity
@@ -294,7 +324,7 @@ def test_paged_argument_errors_and_workspace(cq):
     assert b"differs from block 0" in L.cqkv_last_error()
     assert call(blocks((k0, k0, 10)), 1) == cq.ERR_ARG  # a key side in the value slot
     assert call(blocks((k0, v0, 10)), 1, hq=8 * 32, lq=1 << 20) == cq.ERR_ARG  # 2^25 columns
-    # scratch: the block table plus, with several segments, the partials
+    # scratch: the block table, the partials of the segments and the rotation buffers
     one = L.cqkv_decode_paged_workspace_bytes(blocks((k0, v0, 10)), 1, 1, 8, 1)
     many = L.cqkv_decode_paged_workspace_bytes(blocks((k1, v1, 128), (k1, v1, 128)), 2, 1, 8, 1)
     assert 0 < one < many

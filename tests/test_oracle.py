@@ -220,6 +220,71 @@ def test_rotations_orthogonal():
         np.testing.assert_allclose(m @ m.T, np.eye(d), atol=1e-4)
 
 
+def seeded_gaussian_f64(seed: int, d: int) -> np.ndarray:
+    """The d x d f64 normals of SplitMix64(seed) - Box-Muller from two uniforms
+    ((u >> 11) + 0.5) / 2^53 per draw (turbo.rs:150-176) - computed here in numpy from the raw
+    u64 stream."""
+    u = np.array(O.splitmix_u64(seed, 2 * d * d), dtype=np.uint64)
+    f = ((u >> np.uint64(11)).astype(np.float64) + 0.5) / float(1 << 53)
+    u1, u2 = f[0::2], f[1::2]
+    return (np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)).reshape(d, d)
+
+
+def gram_schmidt_by_qr(g: np.ndarray) -> np.ndarray:
+    """The rows of g orthonormalised in order, from LAPACK's Householder QR of g^T: row i of the
+    result spans rows 0..i of g and has a positive component along row i (the sign fixed by
+    diag(R) > 0), which is what Gram-Schmidt of the rows in order computes."""
+    qm, r = np.linalg.qr(g.T)
+    return (qm * np.sign(np.diag(r))[None, :]).T
+
+
+@pytest.mark.parametrize("d,seed", [(96, 42), (80, 44), (48, 7), (24, 0)])
+def test_dense_rotation_is_gram_schmidt_of_seeded_normals(d, seed):
+    """rotation_matrix(d, Dense, seed) (candle-core/src/accel/turbo.rs:204-230): the normals of
+    SplitMix64(seed ^ "ROTATE!!") orthonormalised row by row. Pinned against an independent route
+    (numpy's Box-Muller of the u64 stream, LAPACK QR) to within the f32 rounding of the entries;
+    the transposed matrix, the unseeded stream or a lost row order each fail it."""
+    m = O.rotation_matrix(d, O.ROT_DENSE, seed).astype(np.float64)
+    want = gram_schmidt_by_qr(seeded_gaussian_f64(seed ^ 0x524F544154452121, d))
+    np.testing.assert_allclose(m, want, rtol=0, atol=1e-6)
+    assert np.abs(m.T - want).max() > 1e-2  # not symmetric: the orientation is pinned
+    other = gram_schmidt_by_qr(seeded_gaussian_f64(seed, d))
+    assert np.abs(m - other).max() > 1e-2
+    flipped = gram_schmidt_by_qr(seeded_gaussian_f64(seed ^ 0x524F544154452121, d)[::-1])
+    assert np.abs(m - flipped).max() > 1e-2
+
+
+def test_rotation_resolve_known_answers(cq):
+    """RotationKind::resolve (candle-core/src/accel/config.rs:131-138) and its test
+    (config.rs:535-536): Auto.resolve(128) == Hadamard, Auto.resolve(96) == Dense; Hadamard at a
+    head dim that is not a power of two is Dense. cqkv's DEFAULT is Auto for the TurboQuant
+    formats and None for the others."""
+    R = cq.resolve_rotation
+    assert R(cq.TURBO4, cq.ROT_AUTO, 128) == cq.ROT_HADAMARD
+    assert R(cq.TURBO4, cq.ROT_AUTO, 96) == cq.ROT_DENSE
+    assert R(cq.FP8, cq.ROT_AUTO, 96) == cq.ROT_DENSE
+    assert R(cq.FP8, cq.ROT_HADAMARD, 80) == cq.ROT_DENSE
+    assert R(cq.FP8, cq.ROT_HADAMARD, 64) == cq.ROT_HADAMARD
+    assert R(cq.TURBO4, cq.ROT_DEFAULT, 96) == cq.ROT_DENSE
+    assert R(cq.TURBOPROD, cq.ROT_DEFAULT, 256) == cq.ROT_HADAMARD
+    assert R(cq.FP8, cq.ROT_DEFAULT, 96) == cq.ROT_NONE
+    assert R(cq.MXFP4, cq.ROT_DENSE, 128) == cq.ROT_DENSE
+    assert R(cq.TURBO4, cq.ROT_NONE, 128) == cq.ROT_NONE
+    with pytest.raises(cq.CqkvError):
+        R(cq.FP8, 9, 128)
+
+
+@pytest.mark.parametrize("d,kind,seed", [(96, 3, 42), (80, 3, 44), (256, 2, 42), (128, 2, 44),
+                                         (64, 1, 0), (48, 4, 7)])
+def test_library_rotation_matrix_equals_oracle(cq, d, kind, seed):
+    """cqkv_rotation_matrix (the matrix a caller uploads as cqkv_side.rot) is the oracle's
+    rotation_matrix bit for bit (cqkv kinds: 1 none, 2 Hadamard, 3 dense, 4 auto)."""
+    okind = {1: O.ROT_NONE, 2: O.ROT_HADAMARD, 3: O.ROT_DENSE,
+             4: O.ROT_HADAMARD if d & (d - 1) == 0 else O.ROT_DENSE}[kind]
+    got = cq.rotation_matrix(d, kind, seed).numpy()
+    np.testing.assert_array_equal(got, O.rotation_matrix(d, okind, seed))
+
+
 def test_codebook_reference_bounds():
     # candle-core/src/accel/turbo.rs:584-597
     d = 128
