@@ -81,7 +81,14 @@ def build_cache(cq, fmt, b, hkv, d, ctx, dev, seed, chunk=2048, vfmt=None):
     return cache
 
 
+LAST_MEDIAN_MS = [0.0]  # median per-call time of the last time_calls
+
+
 def time_calls(fn, steps, warmup, stream):
+    """Mean ms per call over exactly `steps` back-to-back calls after `warmup` untimed ones,
+    between two HIP events on the library's stream. A second pass of `steps` calls with an event
+    after each call gives the per-call times, whose median goes to LAST_MEDIAN_MS (kept apart
+    from the first pass, whose calls run back to back with no event between them)."""
     import torch
     for i in range(warmup):
         fn(i)
@@ -93,7 +100,17 @@ def time_calls(fn, steps, warmup, stream):
         fn(i)
     stop.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(stop) / steps  # ms per call
+    mean = start.elapsed_time(stop) / steps
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record(stream)
+    for i in range(steps):
+        fn(i)
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+    LAST_MEDIAN_MS[0] = per[len(per) // 2] if len(per) % 2 else 0.5 * (per[len(per) // 2 - 1] +
+                                                                         per[len(per) // 2])
+    return mean  # ms per call
 
 
 def row_bytes(fmt, d):
@@ -109,14 +126,32 @@ def decode_bytes(b, hq, hkv, d, total_tokens, fmt, vfmt=None):
             + 2 * b * hq * d * 2)
 
 
+def csrc_digest() -> str:
+    """sha256 over the library's kernel sources (csrc/*.hip, *.h, *.cpp and include/cqkv.h, in
+    name order): the counter summaries record the digest of the sources they were taken from."""
+    import hashlib
+    h = hashlib.sha256()
+    src = os.path.join(ROOT, "candle-rocm-vulkan_amd", "csrc")
+    files = sorted(f for f in os.listdir(src) if f.endswith((".hip", ".h", ".cpp")))
+    for name in files + ["../../include/cqkv.h"]:
+        with open(os.path.join(src, name), "rb") as f:
+            h.update(os.path.basename(name).encode() + b"\0" + f.read())
+    return h.hexdigest()
+
+
 def read_traffic():
-    """HBM bytes per decode launch from the committed counter summary, or None."""
+    """HBM bytes per decode launch from the committed counter summary, or None when the summary
+    is missing or was taken from other kernel sources than these (csrc_digest)."""
     try:
         with open(TRAFFIC_SUMMARY) as f:
-            m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", f.read())
-        return int(m.group(1)) if m else None
+            text = f.read()
     except OSError:
         return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", text)
+    d = re.search(r"csrc_sha256:\s*([0-9a-f]{64})", text)
+    if not m or not d or d.group(1) != csrc_digest():
+        return None
+    return int(m.group(1))
 
 
 def cpu_info():
@@ -256,7 +291,8 @@ def prefill_case(cq, dev, stream, steps, warmup):
     tflops = flops / (ms * 1e-3) / 1e12
     return {"workload": "BASELINE config 4: causal bf16 prefill + fused FP8 K/V append",
             "batch": b, "seq_len": s, "q_heads": hq, "kv_heads": hkv, "head_dim": d,
-            "us_per_call": round(ms * 1e3, 2), "flop_per_call": flops,
+            "us_per_call": round(ms * 1e3, 2),
+            "median_us_per_call": round(LAST_MEDIAN_MS[0] * 1e3, 2), "flop_per_call": flops,
             "achieved_tflops": round(tflops, 1), "peak_tflops": BF16_PEAK_TFLOPS,
             "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "bound": "mfma",
             "timed": "whole call: pre-pass (V transpose + fused FP8 K/V append) + prefill kernel"}
@@ -416,7 +452,8 @@ def append_case(cq, dev, stream, steps, warmup, b=32, hkv=8, d=128, t=2048):
 
 def decode_summary(name, ms, nbytes, extra):
     gbs = nbytes / (ms * 1e-3) / 1e9
-    res = {"workload": name, "us_per_call": round(ms * 1e3, 2), "bytes_per_call": nbytes,
+    res = {"workload": name, "us_per_call": round(ms * 1e3, 2),
+           "median_us_per_call": round(LAST_MEDIAN_MS[0] * 1e3, 2), "bytes_per_call": nbytes,
            "achieved_gbs": round(gbs, 1), "peak_gbs": HBM_PEAK_GBS,
            "frac": round(gbs / HBM_PEAK_GBS, 4), "bound": "hbm"}
     res.update(extra)
@@ -495,6 +532,10 @@ def main():
             "warmup": args.warmup,
             "ms_per_step": round(ms, 5),
             "us_per_call": round(ms * 1e3, 2),
+            "median_us_per_call": round(LAST_MEDIAN_MS[0] * 1e3, 2),
+            "timing": "ms_per_step / us_per_call: HIP events on the library's stream around the "
+                      "K back-to-back timed calls (their mean); median_us_per_call: the median "
+                      "of K more calls with an event after each",
             "higher_is_better": True,
             "scaling": "weak",
             "vs_baseline": None,

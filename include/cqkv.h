@@ -7,10 +7,17 @@
  * and returning CQKV_OK or a negative status; cqkv_last_error() gives the message of the last
  * failure of the calling thread. Device memory is allocated (stream-ordered, hipMallocAsync /
  * hipFreeAsync on the call's stream) only by: cqkv_decode_attention,
- * cqkv_decode_attention_paged, cqkv_flash_attn_ext and cqkv_flash_attn_blocks when they are
- * given no workspace (each has a *_workspace_bytes query); cqkv_flash_attn (its workspace);
- * cqkv_flash_attn_fp8 given no workspace (the staged K / V and the attention's workspace).
- * cqkv_decode_attention_noalloc allocates nothing. Nothing here holds torch or candle types.
+ * cqkv_decode_attention_paged, cqkv_flash_attn_ext, cqkv_flash_attn_blocks and
+ * cqkv_dequantize_rows when they are given no workspace (each has a *_workspace_bytes query);
+ * cqkv_flash_attn (its workspace); cqkv_flash_attn_fp8 given no workspace (the staged K / V and
+ * the attention's workspace); cqkv_quant_append, cqkv_rope_quant_append and the cache append of
+ * cqkv_flash_attn(_ext) for a side whose rows are staged (a rotation by its matrix, or a head dim
+ * below the plane row: an f32 copy of the rows, and a padded QJL matrix for TurboProd), and
+ * cqkv_rope_quant_append when it runs as separate launches (plane rows of 256, staged sides: the
+ * rotated keys). cqkv_decode_attention_noalloc allocates nothing; its scratch array is a
+ * 32 MiB (CQKV_DECODE_SCRATCH_BYTES) static device array that every process loading the library
+ * holds on every device it uses, whether or not that entry point is called. Nothing here holds
+ * torch or candle types.
  *
  * Reference interfaces replaced (paths relative to the reference repository root):
  *   cqkv_quant_append      RocmStorage::tq_quantize + Cache::append

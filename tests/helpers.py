@@ -305,3 +305,38 @@ def fp4_thresholds() -> np.ndarray:
                 lo = mid + 1
         thr.append(lo)
     return np.array(thr, dtype=np.uint32)
+
+
+# README.md:301-311 of the reference, produced by turbo_quant::accuracy::attention_error_by_format
+# (candle-nn/src/turbo_quant.rs:1644-1719): (key format, value format) -> relative RMS error of
+# the attention output, mean over seeds 0-5. Oracle (mode, bits).
+PUBLISHED_ERRORS = [((O.FP8, 0), (O.FP8, 0), 0.036), ((O.NVFP4, 0), (O.NVFP4, 0), 0.133),
+                    ((O.TURBO_MSE, 4), (O.TURBO_MSE, 4), 0.137),
+                    ((O.MXFP4, 0), (O.MXFP4, 0), 0.162),
+                    ((O.TURBO_PROD, 4), (O.TURBO_MSE, 4), 0.247),
+                    ((O.TURBO_MSE, 3), (O.TURBO_MSE, 3), 0.253)]
+
+
+def accuracy_inputs(seed: int, d: int = 128):
+    """The reference test's inputs: one SplitMix64(seed * 77 + d) normal stream, as f32, filling
+    k (1, 2, 256, d), then v (1, 2, 256, d), then q (1, 8, 1, d) (turbo_quant.rs:1673-1679)."""
+    n = 2 * 256 * d
+    x = O.normal(seed * 77 + d, (2 * n + 8 * d,))
+    return (x[:n].reshape(1, 2, 256, d), x[n:2 * n].reshape(1, 2, 256, d),
+            x[2 * n:].reshape(1, 8, 1, d))
+
+
+def gqa_attention_f64(q, k, v, scale):
+    """softmax(scale q k^T) v in float64, q (1, hq, 1, d), k / v (1, hkv, lk, d)."""
+    q, k, v = (np.asarray(a, np.float64) for a in (q, k, v))
+    g = q.shape[1] // k.shape[1]
+    out = np.zeros_like(q)
+    for h in range(q.shape[1]):
+        s = k[0, h // g] @ q[0, h, 0] * scale
+        p = np.exp(s - s.max())
+        out[0, h, 0] = p @ v[0, h // g] / p.sum()
+    return out
+
+
+def relative_rms(got, exact) -> float:
+    return float(np.sqrt(((got - exact) ** 2).sum() / (exact ** 2).sum()))

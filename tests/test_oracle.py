@@ -12,6 +12,7 @@ import pytest
 
 from oracle import oracle as O
 from tests.golden import ref_harness as H
+from tests.helpers import PUBLISHED_ERRORS, accuracy_inputs, gqa_attention_f64, relative_rms
 
 GOLD = __import__("os").path.join(__import__("os").path.dirname(__file__), "golden")
 
@@ -1010,3 +1011,34 @@ def test_qjl_matrix_is_standard_normal_from_its_seed():
     np.testing.assert_array_equal(s.ravel(), O.normal((42 + 1) ^ 0x514A4C5F534B4554, (128 * 128,)))
     assert abs(s.mean()) < 0.02 and abs(s.var() - 1) < 0.03
     assert not np.array_equal(s, O.qjl_matrix(128, 43))
+
+
+# ---------------------------------------------------------------------------------------------
+# the reference's published attention-error table
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("kf,vf,want", PUBLISHED_ERRORS)
+def test_published_attention_error_table_on_the_oracle(kf, vf, want):
+    """The reference's own end-to-end accuracy table, recomputed on the oracle: its encoders,
+    codebooks, Hadamard rotation (RotationKind::Auto at d = 128, keys seed s, values s + 2) and
+    QJL stage, dequantized and unrotated in f32 (TurboKvCache::keys_values on the CPU) and
+    attended in float64 against the exact attention of the f32 inputs. Each mean equals the
+    published value to its three decimals; a mistake in a codebook, a rotation seed or the QJL
+    correction moves these well past that."""
+    d = 128
+    errs = []
+    for seed in range(6):
+        k, v, q = accuracy_inputs(seed, d)
+
+        def deq(fmt, x, s):
+            pi = O.rotation_matrix(d, O.ROT_HADAMARD, s)
+            y = O.rotate_rows(pi, x.reshape(-1, d))
+            if fmt[0] == O.TURBO_PROD:
+                sm = O.qjl_matrix(d, s)
+                yd = O.dequantize_rows_qjl(fmt[1], d, O.quantize_rows_qjl(fmt[1], y, sm), sm)
+            else:
+                yd = O.dequantize_rows(fmt[0], fmt[1], d, O.quantize_rows(fmt[0], fmt[1], y))
+            return O.unrotate_rows(pi, yd.reshape(-1, d)).reshape(x.shape)
+
+        got = gqa_attention_f64(q, deq(kf, k, seed), deq(vf, v, seed + 2), d ** -0.5)
+        errs.append(relative_rms(got, gqa_attention_f64(q, k, v, d ** -0.5)))
+    assert abs(np.mean(errs) - want) <= 5e-4, (np.mean(errs), want)
