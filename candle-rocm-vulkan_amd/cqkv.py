@@ -620,7 +620,7 @@ def flash_attn_fp8(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, softmax_sc
     by the same Hadamard matrix first (Q K^T unchanged, outliers spread before the FP8 rounding).
     Nothing waits on the host: the scales stay on the device."""
     d = q.shape[-1]
-    if hadamard and d in (64, 128):
+    if hadamard and d > 1 and d & (d - 1) == 0:  # power-of-two head dims, as the reference
         q, k = hadamard_rows(q), hadamard_rows(k)
     k8, ks = fp8_quantize_tensor(k.contiguous())
     v8, vs = fp8_quantize_tensor(v.contiguous())

@@ -126,21 +126,22 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Workspace (D' = the plane row length of head_dim): partial outputs (splits, rows, D') f32 |
 // partial lse (splits, rows) f32 | rotated queries (rows, D') f32 | combined outputs before the
-// matrix unrotation (rows, D') f32 | the padded QJL matrix (D', D') f32. The last three serve the
-// sides that rotate by their matrix and TurboProd keys at a head dim below D'; they are reserved
-// whatever the formats, so the size depends on the shapes only.
+// matrix unrotation (rows, D') f32 | the padded QJL matrix (D', D') f32. The last three (extras)
+// serve the sides that rotate by their matrix and TurboProd keys at a head dim below D'; the
+// size query reserves them whatever the formats, so its answer depends on the shapes only, and a
+// call that needs none of them uses only the partials.
 struct DecodeWs {
     size_t lse, qrot, otmp, qjl, total;
 };
 static DecodeWs workspace_layout(int32_t batch, int32_t q_heads, int32_t q_len, int32_t head_dim,
-                                 int32_t splits) {
+                                 int32_t splits, bool extras = true) {
     const size_t rows = (size_t)batch * q_heads * q_len, dk = (size_t)kernel_dim(head_dim);
     DecodeWs w;
     w.lse = align256((size_t)splits * rows * dk * 4);
     w.qrot = w.lse + align256((size_t)splits * rows * 4);
-    w.otmp = w.qrot + align256(rows * dk * 4);
-    w.qjl = w.otmp + align256(rows * dk * 4);
-    w.total = w.qjl + align256(dk * dk * 4);
+    w.otmp = w.qrot + (extras ? align256(rows * dk * 4) : 0);
+    w.qjl = w.otmp + (extras ? align256(rows * dk * 4) : 0);
+    w.total = w.qjl + (extras ? align256(dk * dk * 4) : 0);
     return w;
 }
 
@@ -373,11 +374,15 @@ static hipError_t decode_launch(DecodeArgs a, const DecodeHost &h, int kf, int v
     return e;
 }
 
-// Whether a decode call needs its workspace: partials, or the matrix rotations' and the padded
-// QJL matrix's regions.
-static bool needs_workspace(const DecodeArgs &a, const DecodeHost &h) {
-    return a.splits > 1 || a.partials || h.k_rot ||
+// Whether a decode call needs the workspace's extra regions (matrix rotations, padded QJL matrix).
+static bool needs_extras(const DecodeHost &h) {
+    return h.k_rot || h.v_rot ||
            (h.k->format == CQKV_FMT_TURBOPROD && h.head_dim != kernel_dim(h.head_dim));
+}
+
+// Whether a decode call needs its workspace: partials, or the extra regions.
+static bool needs_workspace(const DecodeArgs &a, const DecodeHost &h) {
+    return a.splits > 1 || a.partials || needs_extras(h);
 }
 
 // ---- allocation-free decode: split partials in a library-owned device array ----
@@ -442,24 +447,25 @@ static int decode_dense(const char *who, const void *q, int32_t q_dtype,
     int s = splits > 0 ? min(splits, tiles)
                        : auto_splits(batch, hkv, max(kv_len, 1), kv_lens != nullptr,
                                      waves_of(k->format, v->format));
+    const bool extras = needs_extras(h);
     if (noalloc) {  // everything the call needs must fit the device scratch
         auto fits = [&](int n) {
             a.splits = n;
-            return !needs_workspace(a, h) ||
-                   workspace_layout(batch, q_heads, q_len, d, n).total <= CQKV_DECODE_SCRATCH_BYTES;
+            return !needs_workspace(a, h) || workspace_layout(batch, q_heads, q_len, d, n, extras)
+                                                     .total <= CQKV_DECODE_SCRATCH_BYTES;
         };
         if (!fits(s) && splits > 0)
             return fail(CQKV_ERR_WORKSPACE,
                         "%s: %d splits need %zu bytes of partials, above the %zu-byte device "
                         "scratch",
-                        who, s, workspace_layout(batch, q_heads, q_len, d, s).total,
+                        who, s, workspace_layout(batch, q_heads, q_len, d, s, extras).total,
                         (size_t)CQKV_DECODE_SCRATCH_BYTES);
         while (s > 1 && !fits(s)) --s;
         if (!fits(s))
             return fail(CQKV_ERR_WORKSPACE,
                         "%s: %zu bytes of partials and rotation buffers exceed the %zu-byte "
                         "device scratch",
-                        who, workspace_layout(batch, q_heads, q_len, d, s).total,
+                        who, workspace_layout(batch, q_heads, q_len, d, s, extras).total,
                         (size_t)CQKV_DECODE_SCRATCH_BYTES);
     }
     const int tps = (tiles + s - 1) / s;
@@ -481,7 +487,7 @@ static int decode_dense(const char *who, const void *q, int32_t q_dtype,
     hipStream_t st = (hipStream_t)stream;
     void *ws = workspace;
     bool owned = false;
-    const DecodeWs w = workspace_layout(batch, q_heads, q_len, d, s);
+    const DecodeWs w = workspace_layout(batch, q_heads, q_len, d, s, extras);
     if (needs_workspace(a, h)) {
         if (noalloc) {
             if (int rc = scratch_address(&ws, who)) return rc;

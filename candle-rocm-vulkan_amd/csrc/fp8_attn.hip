@@ -283,28 +283,47 @@ struct HadamardArgs {
     void *out;
     int64_t rows, x_row, out_row;  // element strides between rows
     int32_t dtype;
-    uint32_t sign_bits[4];
+    uint32_t sign_bits[8];
     float scale;
 };
 
+// D a power of two up to 128: lane l holds elements 2l, 2l+1 (lanes past D / 2 idle); D = 256:
+// also 128 + 2l, 129 + 2l, the stride-128 stage in the lane (H_256 = H_2 x H_128).
 template <int D>
 __global__ __launch_bounds__(256) void hadamard_rows_kernel(HadamardArgs a) {
+    constexpr int NP = D == 256 ? 2 : 1;  // element pairs per lane
+    constexpr int DH = D == 256 ? 128 : D;
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= a.rows) return;
-    const bool act = lane < D / 2;
-    const int j0 = 2 * lane, j1 = 2 * lane + 1;
-    float v0 = 0.0f, v1 = 0.0f;
-    if (act) {
-        v0 = load_elem(a.x, row * a.x_row + j0, a.dtype);
-        v1 = load_elem(a.x, row * a.x_row + j1, a.dtype);
-        if ((a.sign_bits[j0 >> 5] >> (j0 & 31)) & 1u) v0 = -v0;
-        if ((a.sign_bits[j1 >> 5] >> (j1 & 31)) & 1u) v1 = -v1;
+    const bool act = lane < DH / 2;
+    float v[2 * NP] = {};
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int j = 128 * p + 2 * lane + e;
+            if (act) {
+                v[2 * p + e] = load_elem(a.x, row * a.x_row + j, a.dtype);
+                if ((a.sign_bits[j >> 5] >> (j & 31)) & 1u) v[2 * p + e] = -v[2 * p + e];
+            }
+        }
+#pragma unroll
+    for (int p = 0; p < NP; ++p) fwht_pairs<DH>(v[2 * p], v[2 * p + 1], lane);
+    if constexpr (NP == 2) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const float s0 = v[e] + v[2 + e], s1 = v[e] - v[2 + e];
+            v[e] = s0;
+            v[2 + e] = s1;
+        }
     }
-    fwht_pairs<D>(v0, v1, lane);
     if (!act) return;
-    store_elem(a.out, row * a.out_row + j0, a.dtype, v0 * a.scale);
-    store_elem(a.out, row * a.out_row + j1, a.dtype, v1 * a.scale);
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+            store_elem(a.out, row * a.out_row + 128 * p + 2 * lane + e, a.dtype, v[2 * p + e] * a.scale);
 }
 
 }  // namespace cqkv
@@ -316,8 +335,9 @@ extern "C" int cqkv_hadamard_rows(const void *x, int32_t dtype, int64_t rows, in
     if (!x || !out) return fail(CQKV_ERR_ARG, "cqkv_hadamard_rows: null pointer");
     if (dtype < CQKV_BF16 || dtype > CQKV_F32)
         return fail(CQKV_ERR_ARG, "cqkv_hadamard_rows: dtype %d", dtype);
-    if (head_dim != 64 && head_dim != 128)
-        return fail(CQKV_ERR_ARG, "cqkv_hadamard_rows: head_dim %d (64 or 128)", head_dim);
+    if (head_dim < 2 || head_dim > 256 || (head_dim & (head_dim - 1)) != 0)
+        return fail(CQKV_ERR_ARG, "cqkv_hadamard_rows: head_dim %d (a power of two, 2-256)",
+                    head_dim);
     // four rows per 256-thread workgroup along x: rows * 64 threads within one launch
     if (rows < 0 || rows > (int64_t)(UINT32_MAX / 64) || x_row_stride < head_dim ||
         out_row_stride < head_dim)
@@ -330,14 +350,23 @@ extern "C" int cqkv_hadamard_rows(const void *x, int32_t dtype, int64_t rows, in
     a.x_row = x_row_stride;
     a.out_row = out_row_stride;
     a.dtype = dtype;
-    float signs[128];
+    float signs[256];
     turbo_signs(head_dim, seed, signs);
     for (int j = 0; j < head_dim; ++j)
         if (signs[j] < 0.0f) a.sign_bits[j >> 5] |= 1u << (j & 31);
     a.scale = 1.0f / sqrtf((float)head_dim);
     const dim3 grid((unsigned)((rows + 3) / 4));
-    if (head_dim == 64) hipLaunchKernelGGL(hadamard_rows_kernel<64>, grid, dim3(256), 0, (hipStream_t)stream, a);
-    else hipLaunchKernelGGL(hadamard_rows_kernel<128>, grid, dim3(256), 0, (hipStream_t)stream, a);
+    const hipStream_t st = (hipStream_t)stream;
+    switch (head_dim) {
+    case 2: hipLaunchKernelGGL(hadamard_rows_kernel<2>, grid, dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL(hadamard_rows_kernel<4>, grid, dim3(256), 0, st, a); break;
+    case 8: hipLaunchKernelGGL(hadamard_rows_kernel<8>, grid, dim3(256), 0, st, a); break;
+    case 16: hipLaunchKernelGGL(hadamard_rows_kernel<16>, grid, dim3(256), 0, st, a); break;
+    case 32: hipLaunchKernelGGL(hadamard_rows_kernel<32>, grid, dim3(256), 0, st, a); break;
+    case 64: hipLaunchKernelGGL(hadamard_rows_kernel<64>, grid, dim3(256), 0, st, a); break;
+    case 128: hipLaunchKernelGGL(hadamard_rows_kernel<128>, grid, dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL(hadamard_rows_kernel<256>, grid, dim3(256), 0, st, a); break;
+    }
     CQKV_HIP_CHECK(hipGetLastError());
     return CQKV_OK;
 }

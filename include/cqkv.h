@@ -453,8 +453,9 @@ int cqkv_flash_attn_fp8(const void *q, const int64_t q_strides[3], const void *k
 /* Hadamard rotation of rows (flash_attn_fp8's incoherent processing, candle-nn/src/flash_attn.rs:
  * 868-880): out_r = x_r * rotation_matrix(D, Hadamard, seed)^T for each of `rows` rows of D
  * contiguous elements (row strides in elements), computed in f32 and rounded to `dtype`
- * (CQKV_BF16 / F16 / F32). D = 64 or 128. The matrix is the sign-flipped Sylvester Hadamard
- * matrix / sqrt(D) of candle-core/src/accel/turbo.rs:180-203. */
+ * (CQKV_BF16 / F16 / F32). D a power of two from 2 to 256 (the reference rotates power-of-two
+ * head dims only). The matrix is the sign-flipped Sylvester Hadamard matrix / sqrt(D) of
+ * candle-core/src/accel/turbo.rs:180-203. */
 int cqkv_hadamard_rows(const void *x, int32_t dtype, int64_t rows, int64_t x_row_stride,
                        int32_t head_dim, uint64_t seed, void *out, int64_t out_row_stride,
                        cqkv_stream_t stream);

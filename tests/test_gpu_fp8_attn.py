@@ -136,7 +136,7 @@ def test_flash_attn_fp8_head_dims_f16_and_workspace(cq, dev, d, dtype, sq):
         cq.flash_attn_fp8_codes(qd, k8d, v8d, scale, True, kd, vd, workspace=ws[:n - 256])
 
 
-@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("d", [2, 8, 32, 64, 128, 256])
 def test_hadamard_rows_vs_oracle_rotation(cq, dev, d):
     """The rotation of flash_attn_fp8's switch: rotation_matrix(d, Hadamard, 0x46413346) in f32.
     The reference multiplies by the dense matrix (its f32 summation order is not pinned, as for
@@ -151,9 +151,18 @@ def test_hadamard_rows_vs_oracle_rotation(cq, dev, d):
     xb = x.to(torch.bfloat16)
     gb = cq.hadamard_rows(xb.to(dev)).float().cpu().numpy()
     wb = O.round_bf16(O.rotate_rows(pi, xb.float().numpy().reshape(-1, d)).reshape(x.shape))
-    ulp = np.abs(wb) * 2.0 ** -7 + 1e-30
+    # one bf16 step of the larger of the two, plus the f32 allowance above for sums that cancel
+    # to (nearly) zero, where the two summation orders differ in the last bits
+    ulp = np.maximum(np.abs(wb), np.abs(gb)) * 2.0 ** -7 + 2e-6
     assert (np.abs(gb - wb) <= ulp).all()
     assert (gb == wb).mean() > 0.99
+
+
+def test_hadamard_rows_refuses_other_head_dims(cq, dev):
+    """The reference rotates power-of-two head dims only (flash_attn.rs:869)."""
+    x = torch.zeros(4, 96, device=dev)
+    with pytest.raises(cq.CqkvError):
+        cq.hadamard_rows(x)
 
 
 def test_flash_attn_fp8_hadamard(cq, dev):

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tests.helpers import kv_source, oracle_rows
+from tests.helpers import assert_turbo_rows_close, kv_source, oracle_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -190,18 +190,21 @@ def test_rope_append_config4_full_size(cq, dev):
     assert torch.equal(vs.codes, vs2.codes) and torch.equal(vs.scales, vs2.scales)
 
 
-def test_rope_append_positions_past_table_skip_keys_and_values(cq, dev):
+@pytest.mark.parametrize("kf,vf", [(5, 5), (5, 0), (2, 5)])
+def test_rope_append_positions_past_table_skip_keys_and_values(cq, dev, kf, vf):
     """Cos / sin tables shorter than the cache: a position past the table is skipped on both
-    sides, so no value row is written without its key row (and rows already there survive)."""
+    sides, so no value row is written without its key row (and rows already there survive).
+    Values of another format than the keys (FP8 keys with TurboQuant-4 values through the MFMA
+    append, MXFP4 keys with FP8 values) take their own launch, clipped at the table's end too."""
     b, hq, hkv, d, t, cap, rows = 3, 4, 2, 128, 4, 64, 40
     qkv = kv_source(5, (b, t, 1, (hq + 2 * hkv) * d))[:, :, 0].to(dev)
     q, k, v = cq.split_qkv(qkv, hq, hkv)
     cos, sin = tables(rows, d, "bf16")
     pos = torch.tensor([0, 37, 50], dtype=torch.int32, device=dev)
-    ks = cq.CacheSide.empty(5, False, b, hkv, d, cap, dev)
-    vs = cq.CacheSide.empty(5, True, b, hkv, d, cap, dev)
-    pre_k = oracle_rows(5, kv_source(93, (b, hkv, cap, d)))
-    pre_v = oracle_rows(5, kv_source(94, (b, hkv, cap, d)))
+    ks = cq.CacheSide.empty(kf, False, b, hkv, d, cap, dev, seed=42)
+    vs = cq.CacheSide.empty(vf, True, b, hkv, d, cap, dev, seed=44)
+    pre_k = oracle_rows(kf, kv_source(93, (b, hkv, cap, d)), 42)
+    pre_v = oracle_rows(vf, kv_source(94, (b, hkv, cap, d)), 44)
     cq.rows_import(ks, torch.from_numpy(pre_k.view(np.int32)).to(dev), 0)
     cq.rows_import(vs, torch.from_numpy(pre_v.view(np.int32)).to(dev), 0)
     cq.rope_quant_append(ks, vs, q, k, v, cos.to(dev), sin.to(dev), 1, positions=pos)
@@ -213,7 +216,14 @@ def test_rope_append_positions_past_table_skip_keys_and_values(cq, dev):
         if n == 0:
             continue
         k_rot = expected_rope(k[bi:bi + 1, :, :n].cpu(), cos, sin, 1, p, "bf16")
-        want_k[bi:bi + 1, :, p:p + n] = O.quantize_rows(5, 0, k_rot)
-        want_v[bi:bi + 1, :, p:p + n] = O.quantize_rows(5, 0, v[bi:bi + 1, :, :n].float().cpu().numpy())
+        want_k[bi:bi + 1, :, p:p + n] = oracle_rows(kf, torch.from_numpy(k_rot), 42)
+        want_v[bi:bi + 1, :, p:p + n] = oracle_rows(vf, v[bi:bi + 1, :, :n].cpu(), 44)
     np.testing.assert_array_equal(got_k, want_k)
-    np.testing.assert_array_equal(got_v, want_v)
+    if vf == 0:  # TurboQuant values: the flip criterion on the written rows, the rest untouched
+        written = np.zeros(cap, bool)
+        for p in pos.tolist():
+            written[p:min(p + t, rows)] = True
+        np.testing.assert_array_equal(got_v[:, :, ~written], want_v[:, :, ~written])
+        assert_turbo_rows_close(got_v[:, :, written], want_v[:, :, written], d)
+    else:
+        np.testing.assert_array_equal(got_v, want_v)

@@ -55,19 +55,26 @@ def test_mfma_append_vs_reference(cq, dev, bits, d, is_value, dtype):
 
 
 @pytest.mark.parametrize("is_value", [False, True])
-def test_mfma_append_per_batch_positions(cq, dev, is_value):
-    b, h, d, t, cap = 3, 2, 128, 37, 96
+@pytest.mark.parametrize("bits,d,dtype", [(4, 128, "bf16"), (3, 64, "f16"), (2, 128, "f16"),
+                                          (1, 64, "bf16"), (4, 64, "f16")])
+def test_mfma_append_per_batch_positions(cq, dev, is_value, bits, d, dtype):
+    """Per-sequence positions: every chunk starts up to 7 tokens early (the first value tile of
+    any position); a position that is not a multiple of 8, and one whose append is cut off at the
+    capacity (positions past it are skipped)."""
+    b, h, t, cap = 4, 2, 37, 96
     seed = 44 if is_value else 42
-    x = kv_source(81, (b, h, t, d))
-    pos = [3, 0, 13]
-    side = cq.CacheSide.empty(TURBO, is_value, b, h, d, cap, dev, seed=seed)
+    x = kv_source(81 + bits + d, (b, h, t, d)).to(DT[dtype])
+    pos = [3, 0, 13, 70]  # 70 + 37 > 96: the last 11 tokens fall past the capacity
+    side = cq.CacheSide.empty(TURBO, is_value, b, h, d, cap, dev, seed=seed, bits=bits)
     cq.quant_append(side, x.to(dev), 0,
                     positions=torch.tensor(pos, dtype=torch.int32, device=dev))
     torch.cuda.synchronize()
     got = export_np(cq, side, cap)
     for i, p in enumerate(pos):
-        assert_rows_match_source(TURBO, got[i:i + 1, :, p:p + t], x[i:i + 1], seed)
-        assert (got[i, :, :p] == 0).all() and (got[i, :, p + t:] == 0).all()
+        n = min(t, cap - p)
+        assert_rows_match_source(TURBO, got[i:i + 1, :, p:p + n], x[i:i + 1, :, :n], seed,
+                                 bits=bits)
+        assert (got[i, :, :p] == 0).all() and (got[i, :, p + n:] == 0).all()
 
 
 @pytest.mark.parametrize("is_value", [False, True])

@@ -5,6 +5,8 @@ Both run the same kernels over the same split count, so their outputs must be eq
 Two calls in a row, the second smaller, show that the array's leftover contents from one call do
 not leak into the next; a third case lowers the automatic split count to fit the array, and an
 explicit split count that does not fit is refused."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -76,3 +78,34 @@ def test_noalloc_lowers_automatic_splits_and_refuses_explicit_ones(cq, dev):
         cq.decode_attention_noalloc(q, cache.k, cache.v, cap, scale, kv_lens=lens, out=got,
                                     splits=16)
     assert e.value.code == cq.ERR_WORKSPACE and "scratch" in str(e.value)
+
+
+def _pool_growth(dev, fn) -> int:
+    """Bytes the device's default memory pool (the one hipMallocAsync draws from) rose above its
+    level before fn(): the used-memory high-water mark, reset to the current use first
+    (hipMemPoolAttrUsedMemHigh = 8, hipMemPoolAttrUsedMemCurrent = 7)."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    pool = ctypes.c_void_p()
+    assert hip.hipDeviceGetDefaultMemPool(ctypes.byref(pool), dev.index or 0) == 0
+    zero, cur, high = ctypes.c_uint64(0), ctypes.c_uint64(0), ctypes.c_uint64(0)
+    torch.cuda.synchronize()
+    assert hip.hipMemPoolSetAttribute(pool, 8, ctypes.byref(zero)) == 0
+    assert hip.hipMemPoolGetAttribute(pool, 7, ctypes.byref(cur)) == 0
+    fn()
+    torch.cuda.synchronize()
+    assert hip.hipMemPoolGetAttribute(pool, 8, ctypes.byref(high)) == 0
+    return high.value - cur.value
+
+
+def test_noalloc_allocates_nothing(cq, dev):
+    """The allocation-free entry point takes nothing from the stream-ordered pool, where the
+    workspace-free cqkv_decode_attention call of the same split count does (the control)."""
+    b, hq, hkv, d, cap = 4, 32, 8, 128, 2048
+    cache = make_cache(cq, dev, 0, b, hkv, d, cap, cap, 41)  # TurboQuant-4: partials + combine
+    q = kv_source(7, (b, hq, 1, d)).to(dev)
+    out = torch.empty_like(q)
+    scale = 1.0 / d ** 0.5
+    assert _pool_growth(dev, lambda: cq.decode_attention(q, cache.k, cache.v, cap, scale, out=out,
+                                                         splits=4)) > 0
+    assert _pool_growth(dev, lambda: cq.decode_attention_noalloc(q, cache.k, cache.v, cap, scale,
+                                                                 out=out, splits=4)) == 0
