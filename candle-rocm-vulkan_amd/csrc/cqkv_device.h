@@ -212,9 +212,21 @@ __device__ inline bf16x8 fp8x8_to_bf16x8(uint32_t w0, uint32_t w1) {
     return __builtin_bit_cast(bf16x8, r);
 }
 
+// 8 E4M3 codes times a power of two (an E8M0 block scale; 0 for an all-zero block), exact in
+// bf16: the conversion applies the scale, one instruction per pair.
+__device__ inline bf16x8 fp8x8_pow2_bf16x8(uint32_t w0, uint32_t w1, float pow2) {
+    u32x4 r;
+    r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, pow2, false));
+    r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, pow2, true));
+    r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, pow2, false));
+    r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, pow2, true));
+    return __builtin_bit_cast(bf16x8, r);
+}
 // 8 E4M3 codes times a scale, rounded to bf16: bf16(scale * e4m3) in f32 arithmetic, the very
 // values of the reference's dequantized bf16 cache (RowCodec::dequantize_row then to_dtype,
-// candle-core/src/accel/turbo.rs:404-409, candle-nn/src/turbo_quant.rs:948-966).
+// candle-core/src/accel/turbo.rs:404-409, candle-nn/src/turbo_quant.rs:948-966). The scaled
+// conversions take only the exponent of their scale operand (measured: any other f32 scale
+// gives other bits than the product), so a general scale is one f32 multiply per code.
 __device__ inline bf16x8 fp8x8_scaled_bf16x8(uint32_t w0, uint32_t w1, float scale) {
     const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(w0, false);
     const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8(w0, true);
@@ -258,14 +270,31 @@ __device__ inline float fa_logit2(float x, float cap2, float slope2, int dist) {
 }
 
 __device__ inline float shfl_xor(float v, int m) { return __shfl_xor(v, m, kWave); }
-__device__ inline float group16_max(float v) {  // max over lanes sharing lane % 16
-    v = fmaxf(v, shfl_xor(v, 16));
-    return fmaxf(v, shfl_xor(v, 32));
+// gfx950 row swaps in the VALU (no LDS round trip): v_permlane16_swap exchanges the odd 16-lane
+// rows of its first operand with the even rows of its second, v_permlane32_swap the upper half
+// of the first with the lower half of the second; with v in both, lane l holds v[l] and
+// v[l ^ 16] (v[l ^ 32]) in the two results.
+__device__ inline float xor16_max(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
-__device__ inline float group16_sum(float v) {
-    v += shfl_xor(v, 16);
-    return v + shfl_xor(v, 32);
+__device__ inline float xor32_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+__device__ inline float xor16_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ inline float xor32_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// over lanes sharing lane % 16 (the 16 columns of an MFMA 16x16 output); the sums add the same
+// pairs as the lane-xor butterfly (v[l] + v[l ^ 16], then + the l ^ 32 partner), so the bits are
+// those of the shuffle form
+__device__ inline float group16_max(float v) { return xor32_max(xor16_max(v)); }
+__device__ inline float group16_sum(float v) { return xor32_sum(xor16_sum(v)); }
 __device__ inline float wave_max(float v) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));

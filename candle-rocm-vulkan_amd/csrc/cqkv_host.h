@@ -145,6 +145,12 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
                     const float *q_mul_dev, float o_mul, const float *o_mul_dev);
 size_t flash_attn_workspace(int32_t dtype, int32_t batch, int32_t q_len, int32_t kv_len,
                             int32_t q_heads, int32_t kv_heads, int32_t head_dim, bool varlen);
+// Whether a dense call of these queries / output takes the MFMA prefill (bf16 / f16, D = 128,
+// more than 16 queries, 16-byte aligned q rows, 8-byte aligned out rows), and the workspace of
+// such a call over E4M3 K / V (V^T and the widened K).
+bool prefill_takes(int32_t dtype, int32_t head_dim, int32_t q_len, const void *q,
+                   const int64_t q_strides[3], const void *out, const int64_t out_strides[3]);
+size_t prefill_e4m3_workspace(int32_t batch, int32_t kv_len, int32_t kv_heads);
 
 // Plain-dtype attention (flash_plain.hip): argument checks, workspace, bytes per K / V element.
 int fa_plain_check(const char *who, int32_t dtype, int32_t kv_dtype, int32_t head_dim,

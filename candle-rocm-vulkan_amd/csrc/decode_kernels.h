@@ -199,6 +199,13 @@ template <int FMT>
 constexpr bool direct_scales() {
     return FMT == CQKV_FMT_FP8 || turbo_mse<FMT>();
 }
+// Key formats whose per-token scale multiplies the score after the dot of the bare codes (the
+// TurboQuant norm), as in the reference's fused kernel (sc = rsc * dot,
+// candle-core/kernels/turbo_quant_impl.h:270-271); they read it as ks8.
+template <int FMT>
+constexpr bool row_scaled_keys() {
+    return turbo_mse<FMT>();
+}
 
 // The 32-bit scale words of keys kb .. kb + 7 (kb a multiple of 8: two aligned 16-byte loads).
 template <int BYTES>
@@ -297,7 +304,7 @@ __device__ inline void load_tile(Tile<KF, VF, D> &r, int tile, bool live, int la
         }
     }
     const uint32_t kl = t0 + (lane & 31);
-    if constexpr (turbo_mse<KF>() || is_prod<KF>())
+    if constexpr (row_scaled_keys<KF>() || is_prod<KF>())
         load_scales8<4>(r.ks8, ksr, t0 + 8 * g, oob);
     if constexpr (is_prod<KF>()) {
         // the scales plane: norms, |r| (at cap * 4), sign bits (at cap * 8, D / 8 per key)
@@ -486,17 +493,21 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
     for (int j = 0; j < NCH; ++j) {
         op_t<KF> k0, k1;
         if constexpr (KF == CQKV_FMT_FP8) {
+            // bf16(scale * code): the reference's bf16 cache values (its CPU path, within whose
+            // 2e-2 the outputs must stay; the fused kernel's f32 products scaled after the dot
+            // move outputs of |x| >= 4 by more than the bf16 ulp leaves)
             k0 = fp8x8_scaled_bf16x8(cur.k[0][2 * j], cur.k[0][2 * j + 1], __uint_as_float(cur.kscale[0]));
             k1 = fp8x8_scaled_bf16x8(cur.k[1][2 * j], cur.k[1][2 * j + 1], __uint_as_float(cur.kscale[1]));
         } else if constexpr (KF == CQKV_FMT_MXFP8) {
-            // chunk j holds head dims 64 (j >> 1) + 16 g + 8 (j & 1) + e: block 2 (j >> 1) + g / 2
+            // chunk j holds head dims 64 (j >> 1) + 16 g + 8 (j & 1) + e: block 2 (j >> 1) + g / 2;
+            // code times the E8M0 power of two is exact in bf16, one conversion per pair
             const int bi = 2 * (j >> 1) + (g >> 1);
             const uint32_t w0 = bi < 4 ? cur.kscale[0] : cur.kscale2[0];
             const uint32_t w1 = bi < 4 ? cur.kscale[1] : cur.kscale2[1];
             const float sc0 = e8m0_scale((w0 >> (8 * (bi & 3))) & 0xffu);
             const float sc1 = e8m0_scale((w1 >> (8 * (bi & 3))) & 0xffu);
-            k0 = fp8x8_scaled_bf16x8(cur.k[0][2 * j], cur.k[0][2 * j + 1], sc0);
-            k1 = fp8x8_scaled_bf16x8(cur.k[1][2 * j], cur.k[1][2 * j + 1], sc1);
+            k0 = fp8x8_pow2_bf16x8(cur.k[0][2 * j], cur.k[0][2 * j + 1], sc0);
+            k1 = fp8x8_pow2_bf16x8(cur.k[1][2 * j], cur.k[1][2 * j + 1], sc1);
         } else if constexpr (KF == CQKV_FMT_NVFP4) {
             // chunk j holds head dims (D/4) g + 8 j + e: the lane's block byte j / 2 (D >= 128)
             const int bi = D >= 128 ? (j >> 1) : 0;
@@ -553,10 +564,10 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
         for (int e = 0; e < 8; ++e)
             x[e] = (x[e] + __uint_as_float(cur.kr1[e]) * kc * zk[e]) *
                    __uint_as_float(cur.ks8[e]) * a.scale_log2;
-    } else if constexpr (!turbo_mse<KF>()) {  // scales are inside the operands
+    } else if constexpr (!row_scaled_keys<KF>()) {  // scales are inside the operands
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] *= a.scale_log2;
-    } else {
+    } else {  // the key's row scale times the dot (TurboQuant norm)
 #pragma unroll
         for (int e = 0; e < 8; ++e)
             x[e] = x[e] * __uint_as_float(cur.ks8[e]) * a.scale_log2;

@@ -10,9 +10,12 @@
 //    cpu_backend/mod.rs:313-315). The scale is written to device memory, so nothing waits on the
 //    host. Three launches: clear the maximum, the maximum (at most 512 workgroups, one atomic
 //    each on the float bits), the codes.
-//  * cqkv_flash_attn_fp8: K and V are E4M3 tensors; one pass writes their values to bf16 into
-//    stream-ordered scratch (E4M3 is exact in bf16), then the bf16 MFMA prefill runs on it with
-//    k_descale folded into the query pre-scale and v_descale into the output normalisation.
+//  * cqkv_flash_attn_fp8: K and V are E4M3 tensors (E4M3 is exact in bf16 and f16). Calls the
+//    MFMA prefill takes (bf16 / f16 queries, D = 128, more than 16 queries) widen the codes in
+//    its V^T pre-pass, K into the workspace and V straight into V^T, one pass over the codes;
+//    other calls first write K and V in the query dtype into the workspace (fp8_stage_kernel)
+//    and run the plain-dtype kernels on that. k_descale is folded into the query pre-scale and
+//    v_descale into the output normalisation. f32 queries read the codes directly.
 #include "cqkv_device.h"
 #include "cqkv_host.h"
 
@@ -145,7 +148,8 @@ extern "C" int cqkv_fp8_quantize_tensor(const void *x, int32_t x_dtype, int64_t 
 }
 
 // Workspace of cqkv_flash_attn_fp8: the staged K / V (dtype copies of the codes), 256-aligned,
-// then the attention's own (flash_attn_workspace); 0 for invalid sizes.
+// then the attention's own (flash_attn_workspace); 0 for invalid sizes. It also covers the MFMA
+// prefill's E4M3 path (V^T and the widened K, prefill_e4m3_workspace), which needs less.
 static size_t fp8_stage_bytes(int32_t batch, int32_t kv_len, int32_t kv_heads, int32_t head_dim) {
     return ((size_t)batch * kv_heads * kv_len * head_dim * 2 * 2 + 255) / 256 * 256;
 }
@@ -211,6 +215,21 @@ extern "C" int cqkv_flash_attn_fp8(const void *q, const int64_t q_strides[3], co
     if (dtype == CQKV_F32) {
         // the f32-query kernel reads the E4M3 codes and widens them exactly, with k_descale in the
         // scores' scale and v_descale in the output, as the reference's fa_row_f32_fp8 does
+        return flash_attn_impl(q, q_strides, k8, k_strides, v8, v_strides, out, out_strides, dtype,
+                               kKvE4M3, batch, q_len, kv_len, q_heads, kv_heads, head_dim,
+                               softmax_scale, window_left, window_right, 0.0f, nullptr, 0, nullptr,
+                               nullptr, 0, 0, nullptr, nullptr, 0, workspace, workspace_bytes,
+                               stream, k_descale, k_scale, v_descale, v_scale);
+    }
+    if (prefill_takes(dtype, head_dim, q_len, q, q_strides, out, out_strides)) {
+        // the MFMA prefill's pre-pass widens the codes itself (K into the workspace, V into its
+        // V^T), so no separate staging pass runs; a caller workspace is still held to the size
+        // cqkv_flash_attn_fp8_workspace_bytes gives, whichever path the call takes
+        const size_t need = cqkv_flash_attn_fp8_workspace_bytes(dtype, batch, q_len, kv_len,
+                                                                q_heads, kv_heads, head_dim);
+        if (workspace && workspace_bytes < need)
+            return fail(CQKV_ERR_WORKSPACE, "%s: workspace %zu bytes, need %zu", who,
+                        workspace_bytes, need);
         return flash_attn_impl(q, q_strides, k8, k_strides, v8, v_strides, out, out_strides, dtype,
                                kKvE4M3, batch, q_len, kv_len, q_heads, kv_heads, head_dim,
                                softmax_scale, window_left, window_right, 0.0f, nullptr, 0, nullptr,

@@ -77,6 +77,13 @@ struct PrefillArgs {
     // pre-scale and the output normalisation
     float q_mul, o_mul;
     const float *q_mul_dev, *o_mul_dev;
+    // E4M3 K / V (e4m3 != 0, dense batches): the pre-pass widens the codes of k8 / v8 (byte
+    // strides) to the dtype (exact in bf16 and f16): K into kst (batch, kv head, kv_len, D),
+    // which the attention kernel then reads as k, V straight into V^T
+    const uint8_t *k8, *v8;
+    int64_t k8_sb, k8_st, k8_sh, v8_sb, v8_st, v8_sh;
+    uint16_t *kst;
+    int32_t e4m3, f16;
 };
 
 // First rows and lengths of sequence b. Variable-length offsets are clamped into the tensors
@@ -711,6 +718,23 @@ PF_INLINE float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
 constexpr int kStRow = 68;  // LDS row stride of the pre-pass tiles in 32-bit words (272 B)
 
+// 8 E4M3 codes (byte order) -> 8 bf16 or f16 values (exact), one conversion per pair
+PF_INLINE u32x4 pf_widen_e4m3(u32x2 c, bool f16) {
+    u32x4 r;
+    if (f16) {
+        r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(c.x, 1.0f, false));
+        r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(c.x, 1.0f, true));
+        r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(c.y, 1.0f, false));
+        r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(c.y, 1.0f, true));
+    } else {
+        r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c.x, 1.0f, false));
+        r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c.x, 1.0f, true));
+        r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c.y, 1.0f, false));
+        r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c.y, 1.0f, true));
+    }
+    return r;
+}
+
 __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t vtile[kPfBK * kStRow];
     __shared__ __attribute__((aligned(16))) uint32_t ktile[kPfBK * kStRow];
@@ -726,7 +750,17 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
         const int id = tid + 256 * i, row = id >> 4, c = id & 15;
         const int key = kt * kPfBK + row;
         u32x4 w = {0u, 0u, 0u, 0u};
-        if (key < kv_len) w = *(const u32x4 *)(vplane + (int64_t)key * a.v_st + 8 * c);
+        if (key < kv_len) {
+            if (a.e4m3) {  // dense batches: the sequence is batch row b
+                const uint8_t *kp = a.k8 + (int64_t)b * a.k8_sb + (int64_t)hk * a.k8_sh;
+                const uint8_t *vp = a.v8 + (int64_t)b * a.v8_sb + (int64_t)hk * a.v8_sh;
+                w = pf_widen_e4m3(*(const u32x2 *)(vp + (int64_t)key * a.v8_st + 8 * c), a.f16);
+                const u32x4 kw = pf_widen_e4m3(*(const u32x2 *)(kp + (int64_t)key * a.k8_st + 8 * c), a.f16);
+                *(u32x4 *)(a.kst + (((int64_t)b * a.kv_heads + hk) * a.kv_len + key) * kPfD + 8 * c) = kw;
+            } else {
+                w = *(const u32x4 *)(vplane + (int64_t)key * a.v_st + 8 * c);
+            }
+        }
         *(u32x4 *)&vtile[row * kStRow + 4 * c] = w;
         if (a.append) {
             u32x4 wk = {0u, 0u, 0u, 0u};
@@ -852,6 +886,25 @@ static bool pf_fast_path(int32_t dtype, int32_t head_dim, int32_t q_len) {
 static size_t pf_vt_bytes(int32_t batch, int32_t kv_len, int32_t kv_heads) {
     return (size_t)batch * kv_heads * kPfD * ((kv_len + kPfBK - 1) / kPfBK * kPfBK) * 2;
 }
+// K widened from E4M3: (batch, kv heads, kv_len, D) of the dtype.
+static size_t pf_kst_bytes(int32_t batch, int32_t kv_len, int32_t kv_heads) {
+    return (size_t)batch * kv_heads * kv_len * kPfD * 2;
+}
+
+bool prefill_takes(int32_t dtype, int32_t head_dim, int32_t q_len, const void *q,
+                   const int64_t q_strides[3], const void *out, const int64_t out_strides[3]) {
+    auto aligned = [](const void *p, const int64_t st[3], int bytes) {
+        const int64_t e = bytes / 2;
+        return (uintptr_t)p % bytes == 0 && st[0] % e == 0 && st[1] % e == 0 && st[2] % e == 0;
+    };
+    return pf_fast_path(dtype, head_dim, q_len) && aligned(q, q_strides, 16) &&
+           aligned(out, out_strides, 8);
+}
+
+size_t prefill_e4m3_workspace(int32_t batch, int32_t kv_len, int32_t kv_heads) {
+    return (pf_vt_bytes(batch, kv_len, kv_heads) + 255) / 256 * 256 +
+           pf_kst_bytes(batch, kv_len, kv_heads);
+}
 
 size_t flash_attn_workspace(int32_t dtype, int32_t batch, int32_t q_len, int32_t kv_len,
                             int32_t q_heads, int32_t kv_heads, int32_t head_dim, bool varlen) {
@@ -897,14 +950,21 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
         const int64_t e = bytes / 2;  // elements per aligned piece
         return (uintptr_t)p % bytes == 0 && (vl || s[0] % e == 0) && s[1] % e == 0 && s[2] % e == 0;
     };
+    // E4M3 K / V under bf16 / f16 queries (cqkv_flash_attn_fp8 passes them only when the MFMA
+    // prefill takes the call; 8-byte aligned code rows, checked there)
+    const bool e4m3 = kv_dtype == kKvE4M3 && dtype != CQKV_F32;
     // (the f32-query kernel checks its own, 4-element, alignment)
-    if (dtype != CQKV_F32 && !no_keys && (!aligned(k, k_strides, 16) || !aligned(v, v_strides, 16)))
+    if (dtype != CQKV_F32 && !e4m3 && !no_keys &&
+        (!aligned(k, k_strides, 16) || !aligned(v, v_strides, 16)))
         return fail(CQKV_ERR_ARG,
                     "cqkv_flash_attn: K / V need 16-byte aligned rows (pointers and strides in "
                     "whole 8-element chunks)");
-    const bool fast = !no_rows && !no_keys && kv_dtype == dtype &&
+    const bool fast = !no_rows && !no_keys && (kv_dtype == dtype || e4m3) &&
                       pf_fast_path(dtype, head_dim, q_len) && aligned(q, q_strides, 16) &&
                       aligned(out, out_strides, 8);
+    if (e4m3 && (!fast || cu_seqlens_q || k_cache))
+        return fail(CQKV_ERR_ARG, "cqkv_flash_attn: E4M3 K / V under %s queries take the MFMA prefill only",
+                    dtype == CQKV_F16 ? "f16" : "bf16");
     if (!fast) {
         if (int rc = fa_plain_check("cqkv_flash_attn", dtype, kv_dtype, head_dim, k_strides[1],
                                     v_strides[1], kv_len))
@@ -1040,16 +1100,38 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
     a.o_mul = o_mul;
     a.q_mul_dev = q_mul_dev;
     a.o_mul_dev = o_mul_dev;
-    // V^T scratch (stream-ordered: freed after the launches that use it)
+    // V^T scratch (stream-ordered: freed after the launches that use it), then, for E4M3 K / V,
+    // the widened K
     a.vt_len = (kv_len + kPfBK - 1) / kPfBK * kPfBK;
     void *vt = workspace;
     const size_t vt_bytes = pf_vt_bytes(batch, kv_len, kv_heads);
-    if (workspace && workspace_bytes < vt_bytes)
+    const size_t kst_off = (vt_bytes + 255) / 256 * 256;
+    const size_t ws_bytes = e4m3 ? kst_off + pf_kst_bytes(batch, kv_len, kv_heads) : vt_bytes;
+    if (workspace && workspace_bytes < ws_bytes)
         return fail(CQKV_ERR_WORKSPACE, "cqkv_flash_attn: workspace %zu < %zu bytes",
-                    workspace_bytes, vt_bytes);
+                    workspace_bytes, ws_bytes);
     const bool vt_owned = workspace == nullptr;
-    if (vt_owned) CQKV_HIP_CHECK(hipMallocAsync(&vt, vt_bytes, st));
+    if (vt_owned) CQKV_HIP_CHECK(hipMallocAsync(&vt, ws_bytes, st));
     a.vt = (const uint16_t *)vt;
+    if (e4m3) {
+        a.e4m3 = 1;
+        a.f16 = dtype == CQKV_F16 ? 1 : 0;
+        a.k8 = (const uint8_t *)k;
+        a.v8 = (const uint8_t *)v;
+        a.k8_sb = k_strides[0];
+        a.k8_st = k_strides[1];
+        a.k8_sh = k_strides[2];
+        a.v8_sb = v_strides[0];
+        a.v8_st = v_strides[1];
+        a.v8_sh = v_strides[2];
+        a.kst = (uint16_t *)((char *)vt + kst_off);
+        // the attention kernel reads the widened K: (batch, kv head, token) strides
+        a.k = a.kst;
+        a.v = a.kst;  // (unread)
+        a.k_st = kPfD;
+        a.k_sh = (int64_t)kv_len * kPfD;
+        a.k_sb = (int64_t)kv_heads * kv_len * kPfD;
+    }
     // an FP8 append runs inside the pre-pass when value tiles line up (position % 8 == 0) and
     // neither side rotates; any other append as two cqkv_quant_append launches after the attention
     const bool fused = k_cache != nullptr && dtype == CQKV_BF16 && position % 8 == 0 &&
