@@ -845,12 +845,19 @@ inline void launch_rows_d(int load, dim3 grid, hipStream_t st, const AppendArgs 
 // one it takes (then the row-parallel encoder runs).
 bool turbo_mfma_launch(const cqkv_side *s, int32_t tokens, int32_t batch, hipStream_t st,
                        const AppendArgs &a);
+// The MFMA form of the TurboProd key append (append_turbo.hip); false when it does not take the
+// case.
+bool prod_mfma_launch(const cqkv_side *s, int32_t tokens, int32_t batch, hipStream_t st,
+                      const AppendArgs &a);
 
 template <int FMT>
 inline void launch_rows(const cqkv_side *s, int32_t tokens, int32_t batch, hipStream_t st,
                         const AppendArgs &a) {
     if constexpr (FMT == CQKV_FMT_TURBO4) {
         if (turbo_mfma_launch(s, tokens, batch, st, a)) return;
+    }
+    if constexpr (FMT == CQKV_FMT_TURBOPROD) {
+        if (prod_mfma_launch(s, tokens, batch, st, a)) return;
     }
     const int dk = kernel_dim(s->head_dim);
     const int rows = 256 / (dk / 32);

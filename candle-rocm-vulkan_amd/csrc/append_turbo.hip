@@ -394,4 +394,319 @@ bool turbo_mfma_launch(const cqkv_side *s, int32_t tokens, int32_t batch, hipStr
     return true;
 }
 
+// ---------------------------------------------------------------------------------------------
+// TurboProd keys (RowCodec::quantize_row, candle-core/src/accel/turbo.rs:299-323): the MSE codes
+// of the rotated unit row u = y / |y| in the (bits - 1)-bit codebook, the residual
+// r = u - centroid[code], |r|, and the sign bits of p = S r (S the D x D QJL matrix).
+//
+// The rows enter as the B operand of v_mfma_f32_32x32x16 (32 tokens per wavefront), so the
+// products leave each lane with one token:
+//  * rotation: U_h^T = A_h X_h^T per half h of the row (the H_2 (x) H_{D/2} split of the
+//    turbo_mfma_kernel), A_h[f][k] = s_{h D/2 + k} H_{D/2}[f][k] with the feature rows permuted
+//    so that lane (token n, half l) receives features (D/4) l + q, q < D/4, of u and v; then
+//    y = (u + v, u - v) gives the lane the features (D/4) l + q and D/2 + (D/4) l + q: two
+//    contiguous runs of D/4 codes (one 16- or 8-byte store each);
+//  * norm and |r|: lane sums plus the partner lane l ^ 32 (v_permlane32_swap);
+//  * codes by the bin table of the TurboMse kernel, centroids from a per-lane LDS copy;
+//  * S r: P^T = S' R^T with R^T straight from the registers (B operand of k-step c = the lane's
+//    residuals 8 c .. 8 c + 7, in the order of its two runs), S' = S with its columns in that
+//    order and its output rows permuted so that lane l receives outputs (D/2) l .. + D/2 - 1
+//    (one store of D/2 sign bits). The residual is scaled by 64 (exact) and split into f16
+//    hi + lo, S likewise: p = S_hi r_hi + S_hi r_lo + S_lo r_hi on the f16 MFMA (products
+//    exact, f32 sums; the dropped S_lo r_lo is 2^-22 of a term), as in the row-parallel form.
+// S' (hi and lo) and the rotation operands are built once per workgroup in LDS.
+constexpr int kPqThreads = 512;  // 8 wavefronts, two per SIMD
+constexpr int kPqTok = 32;       // tokens per wavefront and chunk
+constexpr int kPqRows = kPqTok * (kPqThreads / 64);
+constexpr int kCentCopies = 32;
+typedef float pq_f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ inline pq_f32x16 pq_mfma(f16x8 a, f16x8 b, pq_f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ inline pq_f32x16 pq_mfma(bf16x8 a, bf16x8 b, pq_f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+// the 32x32 MFMA output / operand row m = 8 j + 4 hm + i as (j, hm, i)
+__device__ inline int pq_perm(int m, int quarter, int blk) {
+    // row m of output block blk -> index quarter * hm + 16 blk + 4 j + i
+    return quarter * ((m >> 2) & 1) + 16 * blk + 4 * (m >> 3) + (m & 3);
+}
+
+template <int D, bool F16>
+__global__ __launch_bounds__(kPqThreads) void prod_mfma_kernel(TurboMfmaArgs p) {
+    constexpr int NW = kPqThreads / 64;
+    constexpr int H = D / 2;           // half row
+    constexpr int FB = H / 32;         // 32-feature blocks of a half's transform
+    constexpr int KH = H / 16;         // 16-wide k-steps of a half
+    constexpr int Q = H / 2;           // features per lane and run
+    constexpr int OB = D / 32;         // 32-output blocks of S r
+    constexpr int KC = D / 16;         // k-steps of S r
+    constexpr int ROWS = kPqRows;
+    using op_t = tq_op_t<F16>;
+    // rotation operands [half][fb][ks][lane], S' operands [ob][c][hi / lo][lane]
+    __shared__ __attribute__((aligned(16))) u32x4 sm_h[2 * FB * KH * 64];
+    __shared__ __attribute__((aligned(16))) u32x4 sm_s[OB * KC * 2 * 64];
+    __shared__ __attribute__((aligned(16))) u32x2 sm_lut[kLutN * kLutCopies];
+    __shared__ float sm_cent[16 * kCentCopies];
+    const AppendArgs &a = p.a;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 31, l = lane >> 5;
+
+    // ---- once per workgroup ----
+    const uint32_t one = F16 ? 0x3C00u : 0x3F80u;
+    for (int i = tid; i < 2 * FB * KH * 64; i += kPqThreads) {
+        const int ln = i & 63, ks = (i >> 6) % KH, fb = ((i >> 6) / KH) % FB, half = (i >> 6) / (KH * FB);
+        const int f = pq_perm(ln & 31, Q, fb);  // feature of operand row ln % 32 (in the half)
+        uint32_t w[4];
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+            uint32_t v = 0;
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+                const int k = 16 * ks + 8 * (ln >> 5) + 2 * e2 + h2;  // index in the half
+                const int el = half * H + k;
+                const uint32_t par = ((uint32_t)__popc(f & k) + (a.sign_bits[el >> 5] >> (el & 31))) & 1u;
+                v |= (one | (par << 15)) << (16 * h2);
+            }
+            w[e2] = v;
+        }
+        sm_h[i] = u32x4{w[0], w[1], w[2], w[3]};
+    }
+    for (int i = tid; i < OB * KC * 64; i += kPqThreads) {
+        const int ln = i & 63, c = (i >> 6) % KC, ob = (i >> 6) / KC;
+        const int o = pq_perm(ln & 31, H, ob);  // output row of operand row ln % 32
+        const int hl = ln >> 5;
+        // slots 8 hl .. + 7 of k-step c: the residuals 8 c' .. 8 c' + 7 of lane half hl's runs
+        const int c2 = c % (KC / 2);
+        const int f0 = (c < KC / 2 ? 0 : H) + Q * hl + 8 * c2;
+        uint32_t hi[4], lo[4];
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+            const float s0 = a.qjl[(int64_t)o * D + f0 + 2 * e2];
+            const float s1 = a.qjl[(int64_t)o * D + f0 + 2 * e2 + 1];
+            const float h0 = (float)(_Float16)s0, h1 = (float)(_Float16)s1;
+            hi[e2] = pack_f16x2(h0, h1);
+            lo[e2] = pack_f16x2(s0 - h0, s1 - h1);
+        }
+        sm_s[((ob * KC + c) * 2 + 0) * 64 + ln] = u32x4{hi[0], hi[1], hi[2], hi[3]};
+        sm_s[((ob * KC + c) * 2 + 1) * 64 + ln] = u32x4{lo[0], lo[1], lo[2], lo[3]};
+    }
+    const int S = p.lut_s;
+    for (int i = tid; i <= 2 * S; i += kPqThreads) {
+        const u32x2 e = u32x2{__float_as_uint(p.lut_b[i]), p.lut_c[i]};
+#pragma unroll 4
+        for (int c = 0; c < kLutCopies; ++c) sm_lut[i * kLutCopies + c] = e;
+    }
+    for (int i = tid; i < 16 * kCentCopies; i += kPqThreads) sm_cent[i] = a.cent[i / kCentCopies];
+    __syncthreads();
+    const u32x2 *lut0 = sm_lut + S * kLutCopies + (lane & 31);
+    const float *cent = sm_cent + (lane & 31);
+
+    // ---- chunks: ROWS tokens of one plane per workgroup, 32 per wavefront; the next chunk's
+    // rows load while this one computes ----
+    const int pos0 = a.position;
+    TqChunk nxt = {}, nn = tq_chunk<ROWS>(p, blockIdx.x, pos0);
+    u32x4 xv[2][KH], nv[2][KH] = {};
+    for (int ck = (int)blockIdx.x - (int)gridDim.x; ck < p.total_chunks; ck += gridDim.x) {
+        const TqChunk cur = nxt;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int ks = 0; ks < KH; ++ks) xv[h][ks] = nv[h][ks];
+        nxt = nn;
+        nn = tq_chunk<ROWS>(p, ck + 2 * (int)gridDim.x, pos0);
+        {
+            // lane (n, l): token c0 + 32 wave + n, elements h H + 16 ks + 8 l .. + 7
+            const int t = nxt.c0 + kPqTok * wave + n;
+            const bool live = nxt.valid && t >= nxt.pos && t < nxt.end;
+            const uint16_t *base = (const uint16_t *)a.x + (int64_t)nxt.b * a.sb +
+                                   (int64_t)nxt.h * a.sh + (int64_t)(nxt.c0 - nxt.pos) * a.st;
+            const rsrc_t r = make_rsrc(base, kTqOOB);
+            const uint32_t off = live ? (uint32_t)((int64_t)(t - nxt.c0) * a.st * 2 + 16 * l) : kTqOOB;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int ks = 0; ks < KH; ++ks) nv[h][ks] = ld128(r, off + 2 * (h * H + 16 * ks));
+        }
+        // (every iteration computes; dead tokens read zeros and store nothing)
+        int bl = lane;  // keeps the operand reads from being hoisted out of the loop
+        asm volatile("" : "+v"(bl));
+        const u32x4 *hsm = sm_h + bl;
+        const u32x4 *ssm = sm_s + bl;
+        // rotation: u in ya[fb], v in yb[fb]
+        pq_f32x16 ya[FB], yb[FB];
+#pragma unroll
+        for (int fb = 0; fb < FB; ++fb) {
+            ya[fb] = pq_f32x16{};
+            yb[fb] = pq_f32x16{};
+        }
+#pragma unroll
+        for (int ks = 0; ks < KH; ++ks)
+#pragma unroll
+            for (int fb = 0; fb < FB; ++fb) {
+                ya[fb] = pq_mfma(__builtin_bit_cast(op_t, hsm[((0 * FB + fb) * KH + ks) * 64]),
+                                 __builtin_bit_cast(op_t, xv[0][ks]), ya[fb]);
+                yb[fb] = pq_mfma(__builtin_bit_cast(op_t, hsm[((1 * FB + fb) * KH + ks) * 64]),
+                                 __builtin_bit_cast(op_t, xv[1][ks]), yb[fb]);
+            }
+        // y = (u + v, u - v): lane features Q l + q (ya) and H + Q l + q (yb), q = 16 fb + j
+        float ss = 0.0f;
+#pragma unroll
+        for (int fb = 0; fb < FB; ++fb)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const float u = ya[fb][j], v = yb[fb][j];
+                ya[fb][j] = u + v;
+                yb[fb][j] = u - v;
+                ss = __builtin_fmaf(ya[fb][j], ya[fb][j], ss);
+                ss = __builtin_fmaf(yb[fb][j], yb[fb][j], ss);
+            }
+        const float norm = __builtin_amdgcn_sqrtf(xor32_sum(ss));
+        const float inv = norm > 0.0f ? __builtin_amdgcn_rcpf(norm) : 0.0f;
+        const float w = (float)S * inv;
+        const bool fin = norm <= 3.0e38f && w <= 3.0e38f;
+        // codes: nibble q of run 0, then of run 1 (the plain count where a norm is not finite:
+        // NaN -> 0, infinities)
+        uint32_t cw[2][Q / 8];
+        if (__all(fin)) {
+#pragma unroll
+            for (int run = 0; run < 2; ++run)
+#pragma unroll
+                for (int wd = 0; wd < Q / 8; ++wd) {
+                    uint32_t word = 0;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int q = 8 * wd + e;
+                        const float us = (run == 0 ? ya[q / 16][q % 16] : yb[q / 16][q % 16]) * w;
+                        const u32x2 ent = lut0[(int)us * kLutCopies];
+                        word |= (ent.y + (us >= __uint_as_float(ent.x) ? 1u : 0u)) << (4 * e);
+                    }
+                    cw[run][wd] = word;
+                }
+        } else {
+#pragma unroll
+            for (int run = 0; run < 2; ++run)
+#pragma unroll
+                for (int wd = 0; wd < Q / 8; ++wd) {
+                    uint32_t word = 0;
+                    for (int e = 0; e < 8; ++e) {
+                        const int q = 8 * wd + e;
+                        const float u = (run == 0 ? ya[q / 16][q % 16] : yb[q / 16][q % 16]) * inv;
+                        uint32_t code = 0;
+                        for (int kk = 0; kk < 15; ++kk) code += u >= a.bnd[kk] ? 1u : 0u;
+                        word |= code << (4 * e);
+                    }
+                    cw[run][wd] = word;
+                }
+        }
+        // residuals r = u - centroid[code], scaled by 64, as f16 hi / lo B operands (k-step c:
+        // word c of run 0, then of run 1)
+        f16x8 rhi[KC], rlo[KC];
+        float rr = 0.0f;
+#pragma unroll
+        for (int run = 0; run < 2; ++run)
+#pragma unroll
+            for (int wd = 0; wd < Q / 8; ++wd) {
+                float rv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int q = 8 * wd + e;
+                    const float y = run == 0 ? ya[q / 16][q % 16] : yb[q / 16][q % 16];
+                    const uint32_t code = (cw[run][wd] >> (4 * e)) & 15u;
+                    const float r = y * inv - cent[code * kCentCopies];
+                    rr = __builtin_fmaf(r, r, rr);
+                    rv[e] = 64.0f * r;
+                }
+                split8(rv, rhi[run * (KC / 2) + wd], rlo[run * (KC / 2) + wd]);
+            }
+        const float r1 = __builtin_amdgcn_sqrtf(xor32_sum(rr));
+        // p = S r for the lane's outputs (D/2) l + 16 ob + j
+        pq_f32x16 pp[OB];
+#pragma unroll
+        for (int ob = 0; ob < OB; ++ob) pp[ob] = pq_f32x16{};
+#pragma unroll
+        for (int c = 0; c < KC; ++c)
+#pragma unroll
+            for (int ob = 0; ob < OB; ++ob) {
+                const f16x8 shi = __builtin_bit_cast(f16x8, ssm[((ob * KC + c) * 2 + 0) * 64]);
+                const f16x8 slo = __builtin_bit_cast(f16x8, ssm[((ob * KC + c) * 2 + 1) * 64]);
+                pp[ob] = pq_mfma(shi, rhi[c], pp[ob]);
+                pp[ob] = pq_mfma(shi, rlo[c], pp[ob]);
+                pp[ob] = pq_mfma(slo, rhi[c], pp[ob]);
+            }
+        uint32_t sg[OB / 2];
+#pragma unroll
+        for (int i = 0; i < OB / 2; ++i) sg[i] = 0;
+#pragma unroll
+        for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) sg[ob / 2] |= (pp[ob][j] >= 0.0f ? 1u : 0u) << (16 * (ob & 1) + j);
+
+        // ---- stores (dead tokens: offsets past the range, dropped) ----
+        const int t = cur.c0 + kPqTok * wave + n;
+        const bool live = cur.valid && t >= cur.pos && t < cur.end;
+        const int64_t plane = (int64_t)cur.b * a.kv_heads + cur.h;
+        const rsrc_t code_r = make_rsrc(a.codes + plane * a.codes_plane, kTqOOB);
+        const rsrc_t sc_r = make_rsrc(a.scales + plane * a.scales_plane, kTqOOB);
+        const uint32_t crow = live ? (uint32_t)t * (D / 2) : kTqOOB;
+        // run 0 at byte (D/8) l of the row, run 1 at D/4 + (D/8) l
+        if constexpr (Q / 8 == 4) {
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{cw[0][0], cw[0][1], cw[0][2], cw[0][3]}, code_r,
+                                                   live ? crow + (D / 8) * l : kTqOOB, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{cw[1][0], cw[1][1], cw[1][2], cw[1][3]}, code_r,
+                                                   live ? crow + D / 4 + (D / 8) * l : kTqOOB, 0, 0);
+        } else {
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{cw[0][0], cw[0][1]}, code_r,
+                                                  live ? crow + (D / 8) * l : kTqOOB, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{cw[1][0], cw[1][1]}, code_r,
+                                                  live ? crow + D / 4 + (D / 8) * l : kTqOOB, 0, 0);
+        }
+        const uint32_t cap = (uint32_t)a.capacity;
+        // norm (lane half 0) and |r| (lane half 1) of the token
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l == 0 ? norm * a.rot_scale : r1), sc_r,
+                                              live ? (uint32_t)t * 4u + 4u * cap * (uint32_t)l : kTqOOB,
+                                              0, 0);
+        // sign bits of outputs (D/2) l .. : bytes (D/16) l of the token's D/8
+        const uint32_t soff = live ? 8u * cap + (uint32_t)t * (D / 8) + (D / 16) * l : kTqOOB;
+        if constexpr (OB == 4) __builtin_amdgcn_raw_buffer_store_b64(u32x2{sg[0], sg[1]}, sc_r, soff, 0, 0);
+        else __builtin_amdgcn_raw_buffer_store_b32(sg[0], sc_r, soff, 0, 0);
+    }
+}
+
+template <int D>
+static void pq_launch_d(bool f16, dim3 grid, hipStream_t st, const TurboMfmaArgs &p) {
+    if (f16) hipLaunchKernelGGL((prod_mfma_kernel<D, true>), grid, dim3(kPqThreads), 0, st, p);
+    else hipLaunchKernelGGL((prod_mfma_kernel<D, false>), grid, dim3(kPqThreads), 0, st, p);
+}
+
+// Launches the MFMA form for a TurboProd key side appended from 16-byte aligned bf16 / f16 rows
+// with the Hadamard rotation at D = 64 / 128; false (nothing launched) for any other case.
+bool prod_mfma_launch(const cqkv_side *s, int32_t tokens, int32_t batch, hipStream_t st,
+                      const AppendArgs &a) {
+    if (s->format != CQKV_FMT_TURBOPROD || s->is_value || !a.rotate || !a.qjl) return false;
+    if (a.row_loads != kRowBF16 && a.row_loads != kRowF16) return false;
+    const int d = s->head_dim;
+    if ((d != 64 && d != 128) || a.dim != d) return false;
+    if (a.st < 0 || (int64_t)kPqRows * a.st * 2 + 2 * d >= kTqOOB ||
+        (int64_t)s->capacity * (8 + d / 8) >= kTqOOB || (int64_t)s->capacity * (d / 2) >= kTqOOB)
+        return false;
+    TurboMfmaArgs p = {};
+    p.a = a;
+    bool ok = false;
+    for (int S = 8; S <= kLutMaxS && !ok; S *= 2) ok = tq_build_lut(a.bnd, S, p);
+    if (!ok) return false;
+    const int lead = !a.positions && a.position >= 0 ? a.position % 8 : 7;
+    p.chunks_per_plane = (int)(((int64_t)tokens + lead + kPqRows - 1) / kPqRows);
+    const int64_t total = (int64_t)p.chunks_per_plane * s->kv_heads * batch;
+    if (total <= 0 || total > 0x7fffffff) return false;
+    p.total_chunks = (int32_t)total;
+    const dim3 grid((unsigned)std::min<int64_t>(total, 256));
+    const bool f16 = a.row_loads == kRowF16;
+    if (d == 128) pq_launch_d<128>(f16, grid, st, p);
+    else pq_launch_d<64>(f16, grid, st, p);
+    return true;
+}
+
 }  // namespace cqkv

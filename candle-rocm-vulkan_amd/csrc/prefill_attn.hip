@@ -265,24 +265,26 @@ PF_INLINE void pf_addr_opaque(PfAddr &ad) {
     for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(ad.v[i]));
 }
 
-// S^T (64 keys x 32 queries) = K Q^T for the tile at k_lds, key block 0 first.
+// S^T (64 keys x 32 queries) = K Q^T for the tile at k_lds.
 template <bool F16>
 PF_INLINE void pf_qk(f32x16 (&s)[2], const PfState &st, const uint8_t *k_lds, const PfAddr &ad) {
     using op_t = pf_op_t<F16>;
     op_t kop[16];
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks)
+        for (int mb = 0; mb < 2; ++mb)
             kop[8 * mb + ks] = __builtin_bit_cast(
                 op_t, *(const u32x4 *)(k_lds + ad.k[ks] + 32 * mb * kPfRow));
+    // the two key blocks' chains alternate, so consecutive products are independent
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
+    for (int mb = 0; mb < 2; ++mb)
         s[mb] = mfma32x32x16(kop[8 * mb], __builtin_bit_cast(op_t, st.qop[0]), f32x16{});
 #pragma unroll
-        for (int ks = 1; ks < 8; ++ks)
+    for (int ks = 1; ks < 8; ++ks)
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
             s[mb] = mfma32x32x16(kop[8 * mb + ks], __builtin_bit_cast(op_t, st.qop[ks]), s[mb]);
-    }
 }
 
 // Soft-capping and ALiBi of the raw scores of a tile whose first key is k0 (exp2 units, in the
