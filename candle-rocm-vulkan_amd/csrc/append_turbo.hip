@@ -28,6 +28,7 @@
 //    half in LDS, so the lookups do not conflict on banks.
 // Rows whose norm or 1 / norm is not finite take the plain count, as in rows_block.
 #include <algorithm>
+#include <cstring>
 
 #include "append_rows.h"
 
@@ -70,8 +71,8 @@ struct TqChunk {
 };
 // pos0: a.position, read once into a register (a select between it and a.positions[b] as
 // memory reads became one flat load, waited for before the chunk's row loads could issue).
-template <int ROWS>
-__device__ inline TqChunk tq_chunk(const TurboMfmaArgs &p, int ck, int pos0) {
+template <int ROWS, typename Args>
+__device__ inline TqChunk tq_chunk(const Args &p, int ck, int pos0) {
     const AppendArgs &a = p.a;
     TqChunk c = {};
     if (ck >= p.total_chunks) return c;  // valid false: past the last chunk
@@ -415,10 +416,8 @@ bool turbo_mfma_launch(const cqkv_side *s, int32_t tokens, int32_t batch, hipStr
 //    hi + lo, S likewise: p = S_hi r_hi + S_hi r_lo + S_lo r_hi on the f16 MFMA (products
 //    exact, f32 sums; the dropped S_lo r_lo is 2^-22 of a term), as in the row-parallel form.
 // S' (hi and lo) and the rotation operands are built once per workgroup in LDS.
-constexpr int kPqThreads = 512;  // 8 wavefronts, two per SIMD
-constexpr int kPqTok = 32;       // tokens per wavefront and chunk
-constexpr int kPqRows = kPqTok * (kPqThreads / 64);
-constexpr int kCentCopies = 32;
+constexpr int kPqThreads = 768;  // 12 wavefronts, three per SIMD (at most 168 VGPRs)
+constexpr int kPqTok = 32;       // tokens per chunk: one wavefront's
 typedef float pq_f32x16 __attribute__((ext_vector_type(16)));
 
 __device__ inline pq_f32x16 pq_mfma(f16x8 a, f16x8 b, pq_f32x16 c) {
@@ -442,13 +441,13 @@ __global__ __launch_bounds__(kPqThreads) void prod_mfma_kernel(TurboMfmaArgs p) 
     constexpr int Q = H / 2;           // features per lane and run
     constexpr int OB = D / 32;         // 32-output blocks of S r
     constexpr int KC = D / 16;         // k-steps of S r
-    constexpr int ROWS = kPqRows;
     using op_t = tq_op_t<F16>;
     // rotation operands [half][fb][ks][lane], S' operands [ob][c][hi / lo][lane]
     __shared__ __attribute__((aligned(16))) u32x4 sm_h[2 * FB * KH * 64];
     __shared__ __attribute__((aligned(16))) u32x4 sm_s[OB * KC * 2 * 64];
-    __shared__ __attribute__((aligned(16))) u32x2 sm_lut[kLutN * kLutCopies];
-    __shared__ float sm_cent[16 * kCentCopies];
+    // bin table entries with the two centroids a code of the bin can take, times -64:
+    // (inner boundary, count below, -64 centroid[count], -64 centroid[count + 1])
+    __shared__ __attribute__((aligned(16))) u32x4 sm_lut[kLutN * kLutCopies];
     const AppendArgs &a = p.a;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -474,61 +473,72 @@ __global__ __launch_bounds__(kPqThreads) void prod_mfma_kernel(TurboMfmaArgs p) 
         }
         sm_h[i] = u32x4{w[0], w[1], w[2], w[3]};
     }
-    for (int i = tid; i < OB * KC * 64; i += kPqThreads) {
-        const int ln = i & 63, c = (i >> 6) % KC, ob = (i >> 6) / KC;
-        const int o = pq_perm(ln & 31, H, ob);  // output row of operand row ln % 32
-        const int hl = ln >> 5;
-        // slots 8 hl .. + 7 of k-step c: the residuals 8 c' .. 8 c' + 7 of lane half hl's runs
-        const int c2 = c % (KC / 2);
-        const int f0 = (c < KC / 2 ? 0 : H) + Q * hl + 8 * c2;
-        uint32_t hi[4], lo[4];
+    {
+        // S' operands: each thread's rows of S (two 16-byte loads per operand lane) are loaded
+        // before any is converted
+        constexpr int NS = OB * KC * 64, IT = (NS + kPqThreads - 1) / kPqThreads;
+        f32x4 sv[IT][2];
 #pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) {
-            const float s0 = a.qjl[(int64_t)o * D + f0 + 2 * e2];
-            const float s1 = a.qjl[(int64_t)o * D + f0 + 2 * e2 + 1];
-            const float h0 = (float)(_Float16)s0, h1 = (float)(_Float16)s1;
-            hi[e2] = pack_f16x2(h0, h1);
-            lo[e2] = pack_f16x2(s0 - h0, s1 - h1);
+        for (int it = 0; it < IT; ++it) {
+            const int i = tid + it * kPqThreads;
+            if (i < NS) {
+                const int ln = i & 63, c = (i >> 6) % KC, ob = (i >> 6) / KC;
+                const int o = pq_perm(ln & 31, H, ob);  // output row of operand row ln % 32
+                // slots 8 hl .. + 7 of k-step c: residuals 8 c' .. 8 c' + 7 of lane half hl's runs
+                const int f0 = (c < KC / 2 ? 0 : H) + Q * (ln >> 5) + 8 * (c % (KC / 2));
+                const f32x4 *src = (const f32x4 *)(a.qjl + (int64_t)o * D + f0);
+                sv[it][0] = src[0];
+                sv[it][1] = src[1];
+            }
         }
-        sm_s[((ob * KC + c) * 2 + 0) * 64 + ln] = u32x4{hi[0], hi[1], hi[2], hi[3]};
-        sm_s[((ob * KC + c) * 2 + 1) * 64 + ln] = u32x4{lo[0], lo[1], lo[2], lo[3]};
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            const int i = tid + it * kPqThreads;
+            if (i < NS) {
+                const int ln = i & 63, c = (i >> 6) % KC, ob = (i >> 6) / KC;
+                const float v[8] = {sv[it][0].x, sv[it][0].y, sv[it][0].z, sv[it][0].w,
+                                    sv[it][1].x, sv[it][1].y, sv[it][1].z, sv[it][1].w};
+                uint32_t hi[4], lo[4];
+#pragma unroll
+                for (int e2 = 0; e2 < 4; ++e2) {
+                    const float h0 = (float)(_Float16)v[2 * e2], h1 = (float)(_Float16)v[2 * e2 + 1];
+                    hi[e2] = pack_f16x2(h0, h1);
+                    lo[e2] = pack_f16x2(v[2 * e2] - h0, v[2 * e2 + 1] - h1);
+                }
+                sm_s[((ob * KC + c) * 2 + 0) * 64 + ln] = u32x4{hi[0], hi[1], hi[2], hi[3]};
+                sm_s[((ob * KC + c) * 2 + 1) * 64 + ln] = u32x4{lo[0], lo[1], lo[2], lo[3]};
+            }
+        }
     }
     const int S = p.lut_s;
-    for (int i = tid; i <= 2 * S; i += kPqThreads) {
-        const u32x2 e = u32x2{__float_as_uint(p.lut_b[i]), p.lut_c[i]};
-#pragma unroll 4
-        for (int c = 0; c < kLutCopies; ++c) sm_lut[i * kLutCopies + c] = e;
+    for (int i = tid; i < (2 * S + 1) * kLutCopies; i += kPqThreads) {
+        const int j = i / kLutCopies, c = p.lut_c[j];
+        sm_lut[i] = u32x4{__float_as_uint(p.lut_b[j]), (uint32_t)c, __float_as_uint(-64.0f * a.cent[c]),
+                          __float_as_uint(-64.0f * a.cent[min(c + 1, 15)])};
     }
-    for (int i = tid; i < 16 * kCentCopies; i += kPqThreads) sm_cent[i] = a.cent[i / kCentCopies];
     __syncthreads();
-    const u32x2 *lut0 = sm_lut + S * kLutCopies + (lane & 31);
-    const float *cent = sm_cent + (lane & 31);
+    const int lut0 = S * kLutCopies + (lane & 31);  // this lane's copy of bin 0's entry
 
-    // ---- chunks: ROWS tokens of one plane per workgroup, 32 per wavefront; the next chunk's
-    // rows load while this one computes ----
+    // ---- chunks of 32 tokens of one plane, one per wavefront at a time (the wavefronts of a
+    // workgroup take consecutive chunks); three wavefronts per SIMD cover each other's row loads
+    // (a prefetch of the next chunk's rows would need 32 more registers) ----
     const int pos0 = a.position;
-    TqChunk nxt = {}, nn = tq_chunk<ROWS>(p, blockIdx.x, pos0);
-    u32x4 xv[2][KH], nv[2][KH] = {};
-    for (int ck = (int)blockIdx.x - (int)gridDim.x; ck < p.total_chunks; ck += gridDim.x) {
-        const TqChunk cur = nxt;
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int ks = 0; ks < KH; ++ks) xv[h][ks] = nv[h][ks];
-        nxt = nn;
-        nn = tq_chunk<ROWS>(p, ck + 2 * (int)gridDim.x, pos0);
+    const int gw = (int)blockIdx.x * NW + wave, gstride = (int)gridDim.x * NW;
+    for (int ck = gw; ck < p.total_chunks; ck += gstride) {
+        const TqChunk cur = tq_chunk<kPqTok>(p, ck, pos0);
+        u32x4 xv[2][KH];
         {
-            // lane (n, l): token c0 + 32 wave + n, elements h H + 16 ks + 8 l .. + 7
-            const int t = nxt.c0 + kPqTok * wave + n;
-            const bool live = nxt.valid && t >= nxt.pos && t < nxt.end;
-            const uint16_t *base = (const uint16_t *)a.x + (int64_t)nxt.b * a.sb +
-                                   (int64_t)nxt.h * a.sh + (int64_t)(nxt.c0 - nxt.pos) * a.st;
+            // lane (n, l): token c0 + n, elements h H + 16 ks + 8 l .. + 7
+            const int t = cur.c0 + n;
+            const bool live = cur.valid && t >= cur.pos && t < cur.end;
+            const uint16_t *base = (const uint16_t *)a.x + (int64_t)cur.b * a.sb +
+                                   (int64_t)cur.h * a.sh + (int64_t)(cur.c0 - cur.pos) * a.st;
             const rsrc_t r = make_rsrc(base, kTqOOB);
-            const uint32_t off = live ? (uint32_t)((int64_t)(t - nxt.c0) * a.st * 2 + 16 * l) : kTqOOB;
+            const uint32_t off = live ? (uint32_t)((int64_t)(t - cur.c0) * a.st * 2 + 16 * l) : kTqOOB;
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
-                for (int ks = 0; ks < KH; ++ks) nv[h][ks] = ld128(r, off + 2 * (h * H + 16 * ks));
+                for (int ks = 0; ks < KH; ++ks) xv[h][ks] = ld128(r, off + 2 * (h * H + 16 * ks));
         }
         // (every iteration computes; dead tokens read zeros and store nothing)
         int bl = lane;  // keeps the operand reads from being hoisted out of the loop
@@ -567,85 +577,113 @@ __global__ __launch_bounds__(kPqThreads) void prod_mfma_kernel(TurboMfmaArgs p) 
         const float inv = norm > 0.0f ? __builtin_amdgcn_rcpf(norm) : 0.0f;
         const float w = (float)S * inv;
         const bool fin = norm <= 3.0e38f && w <= 3.0e38f;
-        // codes: nibble q of run 0, then of run 1 (the plain count where a norm is not finite:
-        // NaN -> 0, infinities)
+        // codes (nibble q of run 0, then of run 1) and the residuals r = u - centroid[code],
+        // scaled by 64, as f16 hi / lo B operands (k-step c: word c of run 0, then of run 1);
+        // where a norm is not finite, the plain count (NaN -> 0, infinities) and the centroid
+        // from the kernel arguments
         uint32_t cw[2][Q / 8];
-        if (__all(fin)) {
-#pragma unroll
-            for (int run = 0; run < 2; ++run)
-#pragma unroll
-                for (int wd = 0; wd < Q / 8; ++wd) {
-                    uint32_t word = 0;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const int q = 8 * wd + e;
-                        const float us = (run == 0 ? ya[q / 16][q % 16] : yb[q / 16][q % 16]) * w;
-                        const u32x2 ent = lut0[(int)us * kLutCopies];
-                        word |= (ent.y + (us >= __uint_as_float(ent.x) ? 1u : 0u)) << (4 * e);
-                    }
-                    cw[run][wd] = word;
-                }
-        } else {
-#pragma unroll
-            for (int run = 0; run < 2; ++run)
-#pragma unroll
-                for (int wd = 0; wd < Q / 8; ++wd) {
-                    uint32_t word = 0;
-                    for (int e = 0; e < 8; ++e) {
-                        const int q = 8 * wd + e;
-                        const float u = (run == 0 ? ya[q / 16][q % 16] : yb[q / 16][q % 16]) * inv;
-                        uint32_t code = 0;
-                        for (int kk = 0; kk < 15; ++kk) code += u >= a.bnd[kk] ? 1u : 0u;
-                        word |= code << (4 * e);
-                    }
-                    cw[run][wd] = word;
-                }
-        }
-        // residuals r = u - centroid[code], scaled by 64, as f16 hi / lo B operands (k-step c:
-        // word c of run 0, then of run 1)
         f16x8 rhi[KC], rlo[KC];
         float rr = 0.0f;
+        const float inv64 = 64.0f * inv;
+        const bool fast = __all(fin);
 #pragma unroll
         for (int run = 0; run < 2; ++run)
 #pragma unroll
             for (int wd = 0; wd < Q / 8; ++wd) {
+                uint32_t word = 0;
                 float rv[8];
+                if (fast) {
+                    // four lookups at a time in flight together, then their use
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int q = 8 * wd + e;
-                    const float y = run == 0 ? ya[q / 16][q % 16] : yb[q / 16][q % 16];
-                    const uint32_t code = (cw[run][wd] >> (4 * e)) & 15u;
-                    const float r = y * inv - cent[code * kCentCopies];
-                    rr = __builtin_fmaf(r, r, rr);
-                    rv[e] = 64.0f * r;
+                    for (int e0 = 0; e0 < 8; e0 += 4) {
+                        float us[4];
+                        u32x4 ent[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int q = 8 * wd + e0 + e;
+                            us[e] = (run == 0 ? ya[q / 16][q % 16] : yb[q / 16][q % 16]) * w;
+                            ent[e] = sm_lut[lut0 + (int)us[e] * kLutCopies];
+                        }
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int q = 8 * wd + e0 + e;
+                            const float y = run == 0 ? ya[q / 16][q % 16] : yb[q / 16][q % 16];
+                            const bool up = us[e] >= __uint_as_float(ent[e].x);
+                            word |= (ent[e].y + (up ? 1u : 0u)) << (4 * (e0 + e));
+                            rv[e0 + e] = __builtin_fmaf(y, inv64, __uint_as_float(up ? ent[e].w : ent[e].z));
+                        }
+                    }
+                } else {
+                    for (int e = 0; e < 8; ++e) {
+                        const int q = 8 * wd + e;
+                        const float y = run == 0 ? ya[q / 16][q % 16] : yb[q / 16][q % 16];
+                        const float u = y * inv;
+                        uint32_t code = 0;
+                        for (int kk = 0; kk < 15; ++kk) code += u >= a.bnd[kk] ? 1u : 0u;
+                        word |= code << (4 * e);
+                        rv[e] = 64.0f * (u - a.cent[code]);
+                    }
                 }
-                split8(rv, rhi[run * (KC / 2) + wd], rlo[run * (KC / 2) + wd]);
+                // f16 hi (round to nearest) and lo = v - hi rounded once to f16: one
+                // v_cvt_pk_f16_f32 per pair, one mixed-precision FMA per element
+                u32x4 hw, lw;
+#pragma unroll
+                for (int e2 = 0; e2 < 4; ++e2) {
+                    rr = __builtin_fmaf(rv[2 * e2], rv[2 * e2], rr);
+                    rr = __builtin_fmaf(rv[2 * e2 + 1], rv[2 * e2 + 1], rr);
+                    const uint32_t h2 = pack_f16x2(rv[2 * e2], rv[2 * e2 + 1]);
+                    uint32_t l2;
+                    asm("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,1]"
+                        : "=v"(l2) : "v"(rv[2 * e2]), "v"(h2));
+                    asm("v_fma_mixhi_f16 %0, %1, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+                        : "+v"(l2) : "v"(rv[2 * e2 + 1]), "v"(h2));
+                    hw[e2] = h2;
+                    lw[e2] = l2;
+                }
+                const f16x8 hi = __builtin_bit_cast(f16x8, hw), lo = __builtin_bit_cast(f16x8, lw);
+                cw[run][wd] = word;
+                rhi[run * (KC / 2) + wd] = hi;
+                rlo[run * (KC / 2) + wd] = lo;
             }
-        const float r1 = __builtin_amdgcn_sqrtf(xor32_sum(rr));
+        const float r1 = __builtin_amdgcn_sqrtf(xor32_sum(rr)) * (1.0f / 64.0f);
         // p = S r for the lane's outputs (D/2) l + 16 ob + j
-        pq_f32x16 pp[OB];
-#pragma unroll
-        for (int ob = 0; ob < OB; ++ob) pp[ob] = pq_f32x16{};
-#pragma unroll
-        for (int c = 0; c < KC; ++c)
-#pragma unroll
-            for (int ob = 0; ob < OB; ++ob) {
-                const f16x8 shi = __builtin_bit_cast(f16x8, ssm[((ob * KC + c) * 2 + 0) * 64]);
-                const f16x8 slo = __builtin_bit_cast(f16x8, ssm[((ob * KC + c) * 2 + 1) * 64]);
-                pp[ob] = pq_mfma(shi, rhi[c], pp[ob]);
-                pp[ob] = pq_mfma(shi, rlo[c], pp[ob]);
-                pp[ob] = pq_mfma(slo, rhi[c], pp[ob]);
-            }
+        // two passes of half the output blocks each (half the accumulators live)
         uint32_t sg[OB / 2];
 #pragma unroll
         for (int i = 0; i < OB / 2; ++i) sg[i] = 0;
 #pragma unroll
-        for (int ob = 0; ob < OB; ++ob)
+        for (int ph = 0; ph < 2; ++ph) {
+            pq_f32x16 pp[OB / 2];
 #pragma unroll
-            for (int j = 0; j < 16; ++j) sg[ob / 2] |= (pp[ob][j] >= 0.0f ? 1u : 0u) << (16 * (ob & 1) + j);
+            for (int o2 = 0; o2 < OB / 2; ++o2) pp[o2] = pq_f32x16{};
+#pragma unroll
+            for (int c = 0; c < KC; ++c)
+#pragma unroll
+                for (int o2 = 0; o2 < OB / 2; ++o2) {
+                    const int ob = ph * (OB / 2) + o2;
+                    const f16x8 shi = __builtin_bit_cast(f16x8, ssm[((ob * KC + c) * 2 + 0) * 64]);
+                    const f16x8 slo = __builtin_bit_cast(f16x8, ssm[((ob * KC + c) * 2 + 1) * 64]);
+                    pp[o2] = pq_mfma(shi, rhi[c], pp[o2]);
+                    pp[o2] = pq_mfma(shi, rlo[c], pp[o2]);
+                    pp[o2] = pq_mfma(slo, rhi[c], pp[o2]);
+                }
+#pragma unroll
+            for (int o2 = 0; o2 < OB / 2; ++o2) {
+                const int ob = ph * (OB / 2) + o2;
+                // bit j of the block's 16 = (p_j >= 0), shifted in from the top (one add with
+                // carry per bit)
+                uint32_t g = 0;
+#pragma unroll
+                for (int j = 15; j >= 0; --j) g = 2u * g + (pp[o2][j] >= 0.0f ? 1u : 0u);
+                sg[ob / 2] |= g << (16 * (ob & 1));
+            }
+        }
 
-        // ---- stores (dead tokens: offsets past the range, dropped) ----
-        const int t = cur.c0 + kPqTok * wave + n;
+        // ---- stores (dead tokens: offsets past the range, dropped); the lane's token and half
+        // are recomputed here, so that their store offsets are not held across the loop ----
+        int sl = lane;
+        asm volatile("" : "+v"(sl));
+        const int t = cur.c0 + (sl & 31), l = sl >> 5;
         const bool live = cur.valid && t >= cur.pos && t < cur.end;
         const int64_t plane = (int64_t)cur.b * a.kv_heads + cur.h;
         const rsrc_t code_r = make_rsrc(a.codes + plane * a.codes_plane, kTqOOB);
@@ -689,7 +727,7 @@ bool prod_mfma_launch(const cqkv_side *s, int32_t tokens, int32_t batch, hipStre
     if (a.row_loads != kRowBF16 && a.row_loads != kRowF16) return false;
     const int d = s->head_dim;
     if ((d != 64 && d != 128) || a.dim != d) return false;
-    if (a.st < 0 || (int64_t)kPqRows * a.st * 2 + 2 * d >= kTqOOB ||
+    if (a.st < 0 || (int64_t)kPqTok * a.st * 2 + 2 * d >= kTqOOB ||
         (int64_t)s->capacity * (8 + d / 8) >= kTqOOB || (int64_t)s->capacity * (d / 2) >= kTqOOB)
         return false;
     TurboMfmaArgs p = {};
@@ -698,11 +736,12 @@ bool prod_mfma_launch(const cqkv_side *s, int32_t tokens, int32_t batch, hipStre
     for (int S = 8; S <= kLutMaxS && !ok; S *= 2) ok = tq_build_lut(a.bnd, S, p);
     if (!ok) return false;
     const int lead = !a.positions && a.position >= 0 ? a.position % 8 : 7;
-    p.chunks_per_plane = (int)(((int64_t)tokens + lead + kPqRows - 1) / kPqRows);
+    p.chunks_per_plane = (int)(((int64_t)tokens + lead + kPqTok - 1) / kPqTok);
     const int64_t total = (int64_t)p.chunks_per_plane * s->kv_heads * batch;
     if (total <= 0 || total > 0x7fffffff) return false;
     p.total_chunks = (int32_t)total;
-    const dim3 grid((unsigned)std::min<int64_t>(total, 256));
+    // one workgroup per CU (the LDS tables), enough of them for every chunk
+    const dim3 grid((unsigned)std::min<int64_t>((total + kPqThreads / 64 - 1) / (kPqThreads / 64), 256));
     const bool f16 = a.row_loads == kRowF16;
     if (d == 128) pq_launch_d<128>(f16, grid, st, p);
     else pq_launch_d<64>(f16, grid, st, p);
