@@ -510,18 +510,24 @@ __global__ __launch_bounds__(kPqThreads) void prod_mfma_kernel(TurboMfmaArgs p) 
             }
         }
     }
+    // the bin table: one thread per entry writes copy 0 (two dependent argument reads), then
+    // every thread fills the other copies from it
     const int S = p.lut_s;
-    for (int i = tid; i < (2 * S + 1) * kLutCopies; i += kPqThreads) {
-        const int j = i / kLutCopies, c = p.lut_c[j];
-        sm_lut[i] = u32x4{__float_as_uint(p.lut_b[j]), (uint32_t)c, __float_as_uint(-64.0f * a.cent[c]),
-                          __float_as_uint(-64.0f * a.cent[min(c + 1, 15)])};
+    if (tid <= 2 * S) {
+        const int c = p.lut_c[tid];
+        sm_lut[tid * kLutCopies] =
+            u32x4{__float_as_uint(p.lut_b[tid]), (uint32_t)c, __float_as_uint(-64.0f * a.cent[c]),
+                  __float_as_uint(-64.0f * a.cent[min(c + 1, 15)])};
     }
+    __syncthreads();
+    for (int i = tid; i < (2 * S + 1) * kLutCopies; i += kPqThreads)
+        if (i % kLutCopies != 0) sm_lut[i] = sm_lut[i / kLutCopies * kLutCopies];
     __syncthreads();
     const int lut0 = S * kLutCopies + (lane & 31);  // this lane's copy of bin 0's entry
 
     // ---- chunks of 32 tokens of one plane, one per wavefront at a time (the wavefronts of a
     // workgroup take consecutive chunks); three wavefronts per SIMD cover each other's row loads
-    // (a prefetch of the next chunk's rows would need 32 more registers) ----
+    // (a prefetch of the next chunk's rows would need 32 more registers: it spilled) ----
     const int pos0 = a.position;
     const int gw = (int)blockIdx.x * NW + wave, gstride = (int)gridDim.x * NW;
     for (int ck = gw; ck < p.total_chunks; ck += gstride) {
