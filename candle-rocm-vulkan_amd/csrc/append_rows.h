@@ -219,15 +219,22 @@ __device__ inline uint32_t row_or(uint32_t v) {
     return v;
 }
 
-// The 32 elements of this thread (row offset `off`, element 32 q first), issued as one batch of
-// loads before any conversion.
+// The 32 elements of this thread: element offset `base` (the block's first row, uniform across the
+// workgroup) plus `lane` (this thread's row and element 32 q first), issued as one batch of loads
+// before any conversion. The 16-byte forms are buffer loads from `base`, with dead rows pointed
+// past the buffer range (the hardware returns zeros): no branch around a load, so the loads of a
+// batch are in flight together (the host takes these forms only when a block's rows lie within
+// 2^31 bytes of `base`).
+constexpr uint32_t kRowOOB = 0x80000000u;
 template <int LOAD>
-__device__ inline void load_row32(const AppendArgs &a, int64_t off, bool live, float (&x)[32]) {
+__device__ inline void load_row32(const AppendArgs &a, int64_t base, int64_t lane, bool live,
+                                  float (&x)[32]) {
     if constexpr (LOAD == kRowBF16 || LOAD == kRowF16) {
+        const rsrc_t r = make_rsrc((const uint16_t *)a.x + base, kRowOOB);
+        const uint32_t off = live ? (uint32_t)lane * 2u : kRowOOB;
         u32x4 w[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            w[i] = live ? *(const u32x4 *)((const uint16_t *)a.x + off + 8 * i) : u32x4{0u, 0u, 0u, 0u};
+        for (int i = 0; i < 4; ++i) w[i] = ld128(r, off + 16 * i);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -242,17 +249,18 @@ __device__ inline void load_row32(const AppendArgs &a, int64_t off, bool live, f
                 }
             }
     } else if constexpr (LOAD == kRowF32) {
+        const rsrc_t r = make_rsrc((const float *)a.x + base, kRowOOB);
+        const uint32_t off = live ? (uint32_t)lane * 4u : kRowOOB;
         u32x4 w[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            w[i] = live ? *(const u32x4 *)((const float *)a.x + off + 4 * i) : u32x4{0u, 0u, 0u, 0u};
+        for (int i = 0; i < 8; ++i) w[i] = ld128(r, off + 16 * i);
 #pragma unroll
         for (int i = 0; i < 8; ++i)
 #pragma unroll
             for (int e = 0; e < 4; ++e) x[4 * i + e] = __uint_as_float(w[i][e]);
     } else {
 #pragma unroll
-        for (int i = 0; i < 32; ++i) x[i] = live ? load_elem(a.x, off + i, a.x_dtype) : 0.0f;
+        for (int i = 0; i < 32; ++i) x[i] = live ? load_elem(a.x, base + lane + i, a.x_dtype) : 0.0f;
     }
 }
 
@@ -625,8 +633,8 @@ __device__ inline void rows_block(const AppendArgs &a, int h, int b, int bx) {
     uint8_t *scales = a.scales + plane * a.scales_plane;
 
     float x[32];
-    load_row32<LOAD>(a, (int64_t)b * a.sb + (int64_t)h * a.sh + (int64_t)(t - pos) * a.st + 32 * q,
-                     live, x);
+    load_row32<LOAD>(a, (int64_t)b * a.sb + (int64_t)h * a.sh + (int64_t)(c0 - pos) * a.st,
+                     (int64_t)r * a.st + 32 * q, live, x);
     if constexpr (ROPE != 0) rope_row32<D, ROPE>(a, t, q, live, x);
     if (a.rotate) hadamard_row32<D>(a, q, x);
 

@@ -68,9 +68,11 @@ static int fill_append_args(AppendArgs &a, const cqkv_side *side, const void *x,
     a.capacity = side->capacity;
     a.kv_heads = side->kv_heads;
     {
-        // 16-byte row loads when every thread's 32 elements start 16-byte aligned
+        // 16-byte row loads when every thread's 32 elements start 16-byte aligned and the rows of
+        // a workgroup (at most 256, token stride xs[2]) lie within 2^31 bytes of its first row
         const int64_t v = x_dtype == CQKV_F32 ? 4 : 8;
-        const bool al = (uintptr_t)x % 16 == 0 && xs[0] % v == 0 && xs[1] % v == 0 && xs[2] % v == 0;
+        const bool al = (uintptr_t)x % 16 == 0 && xs[0] % v == 0 && xs[1] % v == 0 && xs[2] % v == 0 &&
+                        xs[2] >= 0 && (256 * xs[2] + 256) * (x_dtype == CQKV_F32 ? 4 : 2) < (int64_t)1 << 31;
         a.row_loads = !al                     ? kRowAny
                       : x_dtype == CQKV_F32   ? kRowF32
                       : x_dtype == CQKV_BF16  ? kRowBF16
