@@ -177,7 +177,6 @@ struct Tile {
     // two at D = 256); MXFP8 all its E8M0 block bytes (kscale2: bytes 4-7 at D = 256); NVFP4 the
     // E4M3 block bytes of its 64 (D = 256) / 32 (D = 128) / 16 (D = 64) head dims
     uint32_t kscale[2], kscale2[2];
-    uint32_t ktok[2];  // NVFP4: the key's f32 scale
     // key lane % 32 (broadcast across lanes): the MX formats' value block bytes (vs2: bytes 4-7
     // at D = 256)
     uint32_t vs, vs2;
@@ -200,11 +199,11 @@ constexpr bool direct_scales() {
     return FMT == CQKV_FMT_FP8 || turbo_mse<FMT>();
 }
 // Key formats whose per-token scale multiplies the score after the dot of the bare codes (the
-// TurboQuant norm), as in the reference's fused kernel (sc = rsc * dot,
+// TurboQuant norm, the NVFP4 token scale), as in the reference's fused kernel (sc = rsc * dot,
 // candle-core/kernels/turbo_quant_impl.h:270-271); they read it as ks8.
 template <int FMT>
 constexpr bool row_scaled_keys() {
-    return turbo_mse<FMT>();
+    return turbo_mse<FMT>() || FMT == CQKV_FMT_NVFP4;
 }
 
 // The 32-bit scale words of keys kb .. kb + 7 (kb a multiple of 8: two aligned 16-byte loads).
@@ -285,7 +284,6 @@ __device__ inline void load_tile(Tile<KF, VF, D> &r, int tile, bool live, int la
                         ksr, (key * 8 + 2 * g) | oob, 0, 0);
                 else
                     r.kscale[s] = __builtin_amdgcn_raw_buffer_load_b8(ksr, (key * 4 + g) | oob, 0, 0);
-                r.ktok[s] = ld32(ksr, (ktok_off + key * 4) | oob);
             }
         }
     }
@@ -304,7 +302,9 @@ __device__ inline void load_tile(Tile<KF, VF, D> &r, int tile, bool live, int la
         }
     }
     const uint32_t kl = t0 + (lane & 31);
-    if constexpr (row_scaled_keys<KF>() || is_prod<KF>())
+    if constexpr (KF == CQKV_FMT_NVFP4)  // the token scales follow the block bytes
+        load_scales8<4>(r.ks8, ksr, ktok_off / 4 + t0 + 8 * g, oob);
+    else if constexpr (row_scaled_keys<KF>() || is_prod<KF>())
         load_scales8<4>(r.ks8, ksr, t0 + 8 * g, oob);
     if constexpr (is_prod<KF>()) {
         // the scales plane: norms, |r| (at cap * 4), sign bits (at cap * 8, D / 8 per key)
@@ -365,6 +365,11 @@ __device__ inline uint32_t fp4x2_to_bf16x2(uint32_t w, int byte_sel, float scale
 template <int FMT>
 using op_t = typename std::conditional<turbo_mse<FMT>() || is_prod<FMT>(), f16x8,
                                       bf16x8>::type;
+// Key-side operand type (keys and queries): as op_t, except NVFP4 keys, whose E2M1 code times its
+// E4M3 block scale is exact in f16 (at most 6 significant bits, magnitudes 2^-10 .. 2688); their
+// f32 token scale then multiplies the score after the dot, as a TurboQuant norm does.
+template <int FMT>
+using kop_t = typename std::conditional<FMT == CQKV_FMT_NVFP4, f16x8, op_t<FMT>>::type;
 
 typedef __attribute__((address_space(3))) const uint32_t lds_u32;
 
@@ -430,31 +435,26 @@ __device__ inline float e8m0_scale(uint32_t code) {  // code 0 marks an all-zero
     return code == 0 ? 0.0f : __uint_as_float(code << 23);
 }
 
-// NVFP4: 8 E2M1 codes of one word times the scale sg = fl(cs * gs) of their (token, block):
-// the E4M3 block scale cs times the token's f32 scale gs, rounded once per block, then one
-// multiply per element before the bf16 rounding. The reference's dequantized cache rounds
-// fl(fl(fp4 * cs) * gs) instead (RowCodec::elem times rsc0, turbo.rs:383-395): the two agree
-// except where the f32 values straddle a bf16 rounding boundary (one bf16 ulp, rarely). The codes
-// are converted unscaled: the conversion's own scale operand is meant for the E8M0 powers of
-// two of the MX formats, not for E4M3 values.
-__device__ inline bf16x8 nvfp4x8_bf16x8(uint32_t w, float sg) {
-    u32x4 r;
-    uint32_t *rp = (uint32_t *)&r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        f32x2 f;
-        switch (i) {  // the selector must be an immediate
-        case 0: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0); break;
-        case 1: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1); break;
-        case 2: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2); break;
-        default: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3); break;
-        }
-        rp[i] = pack_bf16x2(f.x * sg, f.y * sg);
-    }
-    return __builtin_bit_cast(bf16x8, r);
+// NVFP4 key operand: 8 E2M1 codes of one word times the E4M3 block scale in byte `bi` of `cs`, in
+// f16 (exact): one conversion per code pair, one packed f16 multiply.
+__device__ inline f16x8 nvfp4x8_f16x8(uint32_t w, uint32_t cs, int bi) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 c2 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(cs >> (8 * (bi & 2)), 1.0f, false));
+    const h2 sc = (bi & 1) ? h2{c2.y, c2.y} : h2{c2.x, c2.x};
+    h2 r[4];
+    r[0] = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0)) * sc;
+    r[1] = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 1)) * sc;
+    r[2] = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 2)) * sc;
+    r[3] = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 3)) * sc;
+    return __builtin_bit_cast(f16x8, r);
 }
 
-// The same for 8 codes of 8 keys, key e scaled by sg[e].
+// NVFP4 value operand: 8 E2M1 codes of 8 keys, key e's code times its scale sg[e] = fl(cs * gs)
+// (the E4M3 block scale times the token's f32 scale, rounded once per block), then rounded to
+// bf16. The reference's dequantized cache rounds fl(fl(fp4 * cs) * gs) instead (RowCodec::elem
+// times rsc0, turbo.rs:383-395): the two agree except where the f32 values straddle a bf16
+// rounding boundary (one bf16 ulp, rarely). The codes are converted unscaled: the conversion's
+// own scale operand takes only the exponent (E8M0 powers of two), not E4M3 values.
 __device__ inline bf16x8 nvfp4x8_keys_bf16x8(uint32_t w, const float *sg) {
     u32x4 r;
     uint32_t *rp = (uint32_t *)&r;
@@ -474,11 +474,11 @@ __device__ inline bf16x8 nvfp4x8_keys_bf16x8(uint32_t w, const float *sg) {
 
 template <int KF, int VF, int D, bool TERMS>
 __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const DecodeArgs &a,
-                                    const op_t<KF> *qhi, const op_t<KF> *qlo, bool q_split, int lane,
+                                    const kop_t<KF> *qhi, const kop_t<KF> *qlo, bool q_split, int lane,
                                     int lo, int hi, int lo_max, int hi_min, int L, int koff,
                                     uint32_t tab, float &m_run, float &l_run,
-                                    f32x4 *acc, const op_t<KF> *qsop, uint32_t ktab,
-                                    uint32_t vtab, float slope2, int qpos) {
+                                    f32x4 *acc, const kop_t<KF> *qsop, uint32_t ktab,
+                                    uint32_t vtab, float slope2, int qpos, float kscale2) {
     constexpr int NCH = D / 32;
     const int g = lane >> 4;
     // tile and L are rows of the current block (the whole cache when not paged); keys of the
@@ -491,7 +491,7 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
     f32x4 z0 = {0.f, 0.f, 0.f, 0.f}, z1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
-        op_t<KF> k0, k1;
+        kop_t<KF> k0, k1;
         if constexpr (KF == CQKV_FMT_FP8) {
             // bf16(scale * code): the reference's bf16 cache values (its CPU path, within whose
             // 2e-2 the outputs must stay; the fused kernel's f32 products scaled after the dot
@@ -509,14 +509,11 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
             k0 = fp8x8_pow2_bf16x8(cur.k[0][2 * j], cur.k[0][2 * j + 1], sc0);
             k1 = fp8x8_pow2_bf16x8(cur.k[1][2 * j], cur.k[1][2 * j + 1], sc1);
         } else if constexpr (KF == CQKV_FMT_NVFP4) {
-            // chunk j holds head dims (D/4) g + 8 j + e: the lane's block byte j / 2 (D >= 128)
+            // chunk j holds head dims (D/4) g + 8 j + e: the lane's block byte j / 2 (D >= 128);
+            // code times block scale in f16 (exact), the token scale goes on the score
             const int bi = D >= 128 ? (j >> 1) : 0;
-            const float sg0 = __builtin_amdgcn_cvt_f32_fp8(cur.kscale[0] >> (8 * bi), 0) *
-                              __uint_as_float(cur.ktok[0]);
-            const float sg1 = __builtin_amdgcn_cvt_f32_fp8(cur.kscale[1] >> (8 * bi), 0) *
-                              __uint_as_float(cur.ktok[1]);
-            k0 = nvfp4x8_bf16x8(cur.k[0][j], sg0);
-            k1 = nvfp4x8_bf16x8(cur.k[1][j], sg1);
+            k0 = nvfp4x8_f16x8(cur.k[0][j], cur.kscale[0], bi);
+            k1 = nvfp4x8_f16x8(cur.k[1][j], cur.kscale[1], bi);
         } else {
             float sc0 = 1.0f, sc1 = 1.0f;
             if constexpr (KF == CQKV_FMT_MXFP4) {
@@ -563,14 +560,14 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
 #pragma unroll
         for (int e = 0; e < 8; ++e)
             x[e] = (x[e] + __uint_as_float(cur.kr1[e]) * kc * zk[e]) *
-                   __uint_as_float(cur.ks8[e]) * a.scale_log2;
+                   __uint_as_float(cur.ks8[e]) * kscale2;
     } else if constexpr (!row_scaled_keys<KF>()) {  // scales are inside the operands
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] *= a.scale_log2;
+        for (int e = 0; e < 8; ++e) x[e] *= kscale2;
     } else {  // the key's row scale times the dot (TurboQuant norm)
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-            x[e] = x[e] * __uint_as_float(cur.ks8[e]) * a.scale_log2;
+            x[e] = x[e] * __uint_as_float(cur.ks8[e]) * kscale2;
     }
     if constexpr (TERMS) {  // soft-capping, then ALiBi (tq_logit, turbo_quant_impl.h:37-41)
 #pragma unroll
@@ -854,12 +851,28 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
         }
         __syncthreads();
     }
-    op_t<KF> qhi[NCH], qlo[NCH], qsop[kProd ? NCH : 1];
+    kop_t<KF> qhi[NCH], qlo[NCH], qsop[kProd ? NCH : 1];
+    // the scores' factor: scale * log2(e), times 2^qe for queries scaled by 2^-qe into f16 range
+    float kscale2 = a.scale_log2;
+    int qe = 0;
+    if constexpr (KF == CQKV_FMT_NVFP4) {
+        // f16 queries: 2^-qe brings the largest |q| of the workgroup's columns below 2^15 (every
+        // wavefront reads all of them, so each finds the same qe); exact scaling both ways
+        float m = 0.0f;
+        for (int i = lane; i < 16 * D; i += 64) m = fmaxf(m, __builtin_fabsf(sm_q[i / D][i % D]));
+        m = wave_max(m);
+        qe = m < 16384.0f ? 0 : max(__builtin_amdgcn_frexp_expf(m) - 14, 0);  // m < 2^(qe + 14)
+        kscale2 = __builtin_ldexpf(a.scale_log2, qe);
+    }
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
         float qv[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) qv[e] = sm_q[n][qdim<KF, D>(j, g, e)];
+        if constexpr (KF == CQKV_FMT_NVFP4) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qv[e] = __builtin_ldexpf(qv[e], -qe);
+        }
         split8(qv, qhi[j], qlo[j]);
     }
     if constexpr (kProd) {
@@ -938,14 +951,14 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
     for (; t < te; t += 2 * WAVES) {
         compute_tile<KF, VF, D, TERMS>(ta, t, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min, Lb,
                                        koff, tab, m_run, l_run, acc, kProd ? qsop : qhi, ktab, vtab,
-                                       slope2, qpos);
+                                       slope2, qpos, kscale2);
         __builtin_amdgcn_sched_barrier(0);
         load_tile<KF, VF, D>(ta, t + 2 * WAVES, t + 2 * WAVES < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
         __builtin_amdgcn_sched_barrier(0);
         if (t + WAVES < te)
             compute_tile<KF, VF, D, TERMS>(tb2, t + WAVES, a, qhi, qlo, q_split, lane, lo, hi, lo_max,
                                            hi_min, Lb, koff, tab, m_run, l_run, acc,
-                                           kProd ? qsop : qhi, ktab, vtab, slope2, qpos);
+                                           kProd ? qsop : qhi, ktab, vtab, slope2, qpos, kscale2);
         __builtin_amdgcn_sched_barrier(0);
         load_tile<KF, VF, D>(tb2, t + 3 * WAVES, t + 3 * WAVES < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
         __builtin_amdgcn_sched_barrier(0);

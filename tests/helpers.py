@@ -135,6 +135,14 @@ def exact_decode(fmt: int, q: torch.Tensor, k_rows: np.ndarray, v_rows: np.ndarr
     return out
 
 
+def exact_scores(fmt: int) -> bool:
+    """Key formats whose decode scores are the exact value of the codes, as in the reference's
+    fused kernel: TurboQuant (f16 codebook values times the f32 norm) and NVFP4 (E2M1 code times
+    E4M3 block scale, exact in f16, times the f32 token scale). Their outputs are held to
+    assert_decode_parity's exact-value criterion."""
+    return fmt in (0, 3)
+
+
 def assert_decode_parity(fmt: int, got: np.ndarray, ref: np.ndarray, exact: np.ndarray | None,
                          rotated: bool | None = None, value_bf16: bool = False):
     """FP8 / MX / NVFP4: the BASELINE tolerance against the reference path. TurboQuant: the same
@@ -143,14 +151,17 @@ def assert_decode_parity(fmt: int, got: np.ndarray, ref: np.ndarray, exact: np.n
     alone moves outputs by up to ~4e-2 on outlier-heavy inputs) plus the tolerance. The exact
     value is what the reference's own fused kernel computes: on the committed fixture
     tests/golden/ref_decode_turbo4.npz it agrees with the exact value to 4e-6, and the
-    reference's CPU path differs from it by 3.0e-2. `rotated` (default: fmt is TurboQuant)
-    selects the second criterion for any cache whose key or value side rotates: the reference
-    path then unrotates in f32 and rounds to bf16 as for TurboQuant. `value_bf16`: the kernel
+    reference's CPU path differs from it by 3.0e-2. NVFP4 keys take the same criterion: their
+    scores are exact too (E2M1 code times E4M3 block scale is exact in f16, the f32 token scale
+    multiplies the score), where the reference path rounds the dequantized keys to bf16 first,
+    so outputs of |x| >= 4 can sit one bf16 step (0.031) from it. `rotated` (default: fmt is
+    TurboQuant or NVFP4) selects the second criterion for any cache whose key or value side
+    rotates: the reference path then unrotates in f32 and rounds to bf16 as for TurboQuant. `value_bf16`: the kernel
     rounds the dequantized (rotated) values to bf16 as the reference path rounds the unrotated
     ones, each a bf16 rounding at the value's magnitude (outlier channels reach |v| ~ 25, where
     one rounding is up to 6e-2): the exact value is then met within the tolerance plus 2^-8 of
     its magnitude, elementwise."""
-    rotated = fmt == 0 if rotated is None else rotated
+    rotated = exact_scores(fmt) if rotated is None else rotated
     if not rotated or exact is None:
         return assert_close_bf16(got, ref)
     tol = 2e-2 + (2.0 ** -8 * np.abs(exact) if value_bf16 else 0.0)

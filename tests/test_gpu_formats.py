@@ -18,8 +18,8 @@ import torch
 
 from oracle import oracle as O
 from tests.helpers import (assert_close_bf16, assert_decode_parity, assert_rotated_rows_close,
-                           assert_turbo_rows_close, exact_decode, kv_source, oracle_decode,
-                           oracle_rows, rotates)
+                           assert_turbo_rows_close, exact_decode, exact_scores, kv_source,
+                           oracle_decode, oracle_rows, rotates)
 
 pytestmark = pytest.mark.gpu
 
@@ -95,7 +95,7 @@ def run_cache_decode(cq, dev, kf, vf, rotation, b=2, hq=8, hkv=2, d=128, ctx=700
     want = oracle_decode(k_fmt, q, kr, vr, ctx, scale, **kw)
     exact = exact_decode(k_fmt, q, kr, vr, ctx, scale, **kw)
     got = got.float().cpu().numpy()
-    rotated = rotates(k_fmt, rotation) or rotates(v_fmt, rotation)
+    rotated = rotates(k_fmt, rotation) or rotates(v_fmt, rotation) or exact_scores(k_fmt)
     assert_decode_parity(k_fmt, got, want, exact, rotated=rotated, value_bf16=v_fmt != 0)
     return got
 

@@ -18,7 +18,8 @@ import torch
 
 from oracle import oracle as O
 from tests.helpers import (assert_decode_parity, assert_rotated_rows_close, exact_decode,
-                           kv_source, obits, oracle_decode, oracle_rows, rotates, side_pi)
+                           exact_scores, kv_source, obits, oracle_decode, oracle_rows, rotates,
+                           side_pi)
 
 pytestmark = pytest.mark.gpu
 
@@ -88,7 +89,7 @@ def run_decode(cq, dev, kf, vf, d, rotation=ROT_DEFAULT, b=2, hq=8, hkv=2, ctx=3
               alibi=None if alibi is None else np.array(alibi, np.float32))
     want = oracle_decode(k_fmt, q, kr, vr, ctx, scale, **kw)
     exact = exact_decode(k_fmt, q, kr, vr, ctx, scale, **kw)
-    rotated = rotates(k_fmt, rotation, d) or rotates(v_fmt, rotation, d)
+    rotated = rotates(k_fmt, rotation, d) or rotates(v_fmt, rotation, d) or exact_scores(k_fmt)
     assert_decode_parity(k_fmt, got.float().cpu().numpy(), want, exact, rotated=rotated,
                          value_bf16=v_fmt != 0)
     return got, cache, q

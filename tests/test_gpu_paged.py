@@ -12,8 +12,8 @@ import numpy as np
 import pytest
 import torch
 
-from tests.helpers import (assert_close_bf16, assert_decode_parity, exact_decode, kv_source,
-                           oracle_decode, oracle_rows)
+from tests.helpers import (assert_close_bf16, assert_decode_parity, exact_decode, exact_scores,
+                           kv_source, oracle_decode, oracle_rows)
 
 pytestmark = pytest.mark.gpu
 
@@ -66,7 +66,7 @@ def paged_case(cq, dev, fmt, b, hq, hkv, d, sizes, caps, lq=1, wl=-1, wr=-1, see
     # one-operand P (MXFP4 bf16, TurboQuant-4 f16): segments round P against other maxima
     atol, rtol = (2e-3, 4e-3) if fmt in ("mxfp4", "turbo4") else (1e-5, 1e-4)
     np.testing.assert_allclose(got, want_dense.cpu().numpy(), atol=atol, rtol=rtol)
-    if f == 0:
+    if exact_scores(f):
         exact = exact_decode(f, q, kr, vr, total, scale, wl=wl, wr=wr)
         assert_decode_parity(f, got, want, exact)
     else:

@@ -12,8 +12,8 @@ import torch
 
 from oracle import oracle as O
 from tests.helpers import (assert_close_bf16, assert_decode_parity, assert_rows_match_source,
-                           assert_turbo_rows_close, exact_decode, kv_source, oracle_decode,
-                           oracle_rows)
+                           assert_turbo_rows_close, exact_decode, exact_scores, kv_source,
+                           oracle_decode, oracle_rows)
 
 pytestmark = pytest.mark.gpu
 
@@ -138,7 +138,7 @@ def run_decode(cq, dev, fmt, b, hq, hkv, d, ctx, lq=1, splits=0, kv_lens=None, w
     lens_np = None if kv_lens is None else np.array(kv_lens, np.int32)
     want = oracle_decode(f, q, kr, vr, ctx, scale, kv_lens=lens_np, wl=wl, wr=wr)
     got = got.float().cpu().numpy()
-    if f == 0:
+    if exact_scores(f):
         exact = exact_decode(f, q, kr, vr, ctx, scale, kv_lens=lens_np, wl=wl, wr=wr)
         assert_decode_parity(f, got, want, exact)
         want = exact
@@ -294,7 +294,7 @@ def full_size_case(cq, dev, fmt, b, hq, hkv, d, ctx, lens=None, check=(0,), spli
         # TurboQuant-4: the exact value of the codes (what the reference's fused kernel computes)
         # at the tolerance, the reference CPU path within its own deviation from it plus the
         # tolerance (assert_decode_parity); one sequence at a time to bound host memory
-        exact = exact_decode(f, qb, kb, vb, n, 1.0 / d ** 0.5) if f == 0 else None
+        exact = exact_decode(f, qb, kb, vb, n, 1.0 / d ** 0.5) if exact_scores(f) else None
         if exact is not None:
             print(f"seq {bi}: max|o| {np.abs(exact).max():.3f}, gpu-exact "
                   f"{np.abs(got[bi:bi + 1] - exact).max():.3e}, cpu path-exact "
