@@ -9,8 +9,8 @@
 // windows (causal = (-1, 0), candle-core/src/accel/attention.rs:80-92), bf16 in / out, f32
 // accumulation; rows with no visible key give zeros.
 //
-// Kernel shape (one workgroup = 8 wavefronts = 64 queries x 4 query heads sharing a kv head, 32
-// queries per wavefront):
+// Kernel shape (head dim D = 128 or 64; one workgroup = 8 wavefronts = 64 queries x 4 query heads
+// sharing a kv head, 32 queries per wavefront):
 //  * Both products run on v_mfma_f32_32x32x16_bf16. S^T = K Q^T: K (32 keys x 16 dims) comes
 //    from LDS with ds_read_b128, Q^T (pre-scaled by scale * log2(e), rounded to bf16) stays in
 //    registers for the whole key loop. The S^T accumulator of a lane holds one query column, so
@@ -41,7 +41,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-constexpr int kPfD = 128;          // head dim
+constexpr int kPfD = 128;          // head dim of the fused FP8 append and the E4M3 K / V path
 constexpr int kPfBQ = 64;          // queries per workgroup (two wavefronts of 32 per head)
 constexpr int kPfBK = 64;          // keys per tile
 
@@ -137,20 +137,35 @@ __device__ inline void pf_key_range(int i, int lq, int lk, int wl, int wr, int &
     hi = max(hi, lo);
 }
 
-// LDS tile layout: 64 rows (keys) x 256 B (128 bf16 dims), no padding; the 16-byte chunk c of
-// row r sits at chunk position c ^ swz(r). swz takes 16 distinct values over any 16 consecutive
-// rows (the 16 rows of one ds_read_b128 pass) and 4 distinct even offsets over 4 consecutive
-// rows (the 4 rows x 2 chunks of one ds_read_b64_tr_b16 group), so both read patterns are
-// conflict-free.
-__device__ inline int swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+// LDS K tile layout: 64 rows (keys) x 2 D bytes, no padding; the 16-byte chunk c of row r sits at
+// chunk position c ^ swz(r). At D = 128 (16 chunks a row) swz takes 16 distinct values over any 16
+// consecutive rows (the 16 rows of one ds_read_b128 pass); at D = 64 (8 chunks a row, two rows per
+// 256 bytes of banks) (r % 2, c ^ swz(r)) takes 16 distinct values over them: either way the
+// reads are conflict-free.
+template <int D>
+__device__ inline int swz(int r) {
+    if constexpr (D == 128) return ((r & 7) << 1) | ((r >> 3) & 1);
+    else return (r >> 1) & 7;
+}
 // V^T tile layout in LDS: 128 rows (head dims) x 128 B (64 keys); the 16-byte chunk j (8 keys) of
 // row d sits at position j ^ swz_vt(d). Over any 16 consecutive rows, (d % 2, position) takes 16
 // distinct values, so a ds_read_b128 of one chunk across 16 rows is conflict-free.
 __device__ inline int swz_vt(int d) { return (d >> 1) & 7; }
 constexpr int kPfVtRow = 128;
 constexpr int kPfWaves = 8;               // 4 query heads x 2 halves of the 64 queries
-constexpr int kPfRow = 256;
-constexpr int kPfHalf = kPfBK * kPfRow;   // one K or V tile: 16 KB
+// Per head dim: 16-dim k-steps of S = K Q^T, 32-dim blocks of O^T, bytes of a K row and tile, of a
+// V^T tile (D rows of 64 keys), and each wavefront's 1 KB copies of a tile: K rows 8 w .. 8 w + 7,
+// V^T rows (D / 8) w .. in pieces of 8 rows. The V^T stages follow the four K stages in LDS:
+// VBIAS shifts V^T read offsets so that (stage - VBIAS) + block offset fits the 16-bit DS offset.
+template <int D>
+struct PfGeom {
+    static constexpr int KS = D / 16, MD = D / 32;
+    static constexpr int ROW = 2 * D, KTILE = kPfBK * ROW, VTILE = D * kPfVtRow;
+    static constexpr int RPC = 1024 / ROW;  // K rows per copy
+    static constexpr int KCP = KTILE / 1024 / kPfWaves, VCP = VTILE / 1024 / kPfWaves;
+    static constexpr int CP = KCP + VCP;    // copies per wavefront and tile
+    static constexpr uint32_t VBIAS = 4 * KTILE;
+};
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -165,54 +180,59 @@ PF_INLINE rsrc_t pf_rsrc(const void *base, uint32_t bytes) {
     return make_rsrc((const void *)(((uint64_t)hi << 32) | lo), __builtin_amdgcn_readfirstlane(bytes));
 }
 // Asynchronous global -> LDS copy of key tile kt into the stages kstage / vstage: K rows (keys)
-// and V^T rows (head dims), one buffer_load_dwordx4 ... lds (1 KB) per 4 K rows / 8 V^T rows.
-// Wavefront w copies K rows 8w .. 8w+7 and V^T rows 16w .. 16w+15. K: lane l writes chunk
-// position l % 16 of row l / 16, so it loads logical chunk (l % 16) ^ swz(row); the buffer
-// range ends at the last key, so rows past it read zeros. V^T: lane l writes chunk position
-// l % 8 of row l / 8 (the pre-pass zero-fills keys past the end). Tiles past the last one
+// and V^T rows (head dims), one buffer_load_dwordx4 ... lds (1 KB) per 1024 / (2 D) K rows / 8
+// V^T rows. Wavefront w copies K rows 8w .. 8w+7 and V^T rows (D / 8) w .. K: lane l writes
+// chunk position l % (D / 8) of its row, so it loads logical chunk (l % (D / 8)) ^ swz(row); the
+// buffer range ends at the last key, so rows past it read zeros. V^T: lane l writes chunk
+// position l % 8 of row l / 8 (the pre-pass zero-fills keys past the end). Tiles past the last one
 // (valid false) get a zero-size resource: no memory access, zeros into a stage nobody reads
 // again. Buffer loads count on vmcnt only, so the LDS reads of other stages need no wait on
 // these copies.
+template <int D>
 PF_INLINE void pf_issue_tile(uint8_t *kstage, uint8_t *vstage, const uint16_t *kplane,
                              const uint16_t *vtplane, int64_t k_st, int vt_len,
-                             const uint32_t (&koff)[2], const uint32_t (&voff)[2], int kt,
-                             int kv_len, int wave, bool valid) {
+                             const uint32_t *koff, const uint32_t *voff, int kt, int kv_len,
+                             int wave, bool valid) {
+    using G = PfGeom<D>;
     const int row0 = valid ? kt * kPfBK : 0;
     const int nvalid = min(kPfBK, kv_len - row0);
     const rsrc_t kr = pf_rsrc(kplane + (int64_t)row0 * k_st,
-                              valid ? (uint32_t)((int64_t)(nvalid - 1) * k_st * 2 + kPfRow) : 0u);
+                              valid ? (uint32_t)((int64_t)(nvalid - 1) * k_st * 2 + G::ROW) : 0u);
 #pragma unroll
-    for (int r4 = 0; r4 < 2; ++r4)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void *)(kstage + (8 * wave + 4 * r4) * kPfRow),
-                                                 16, koff[r4], 0, 0, 0);
-    const rsrc_t vr = pf_rsrc(vtplane + row0, valid ? (uint32_t)(((int64_t)kPfD * vt_len - row0) * 2) : 0u);
+    for (int r = 0; r < G::KCP; ++r)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            kr, (lds_void *)(kstage + (8 * wave + G::RPC * r) * G::ROW), 16, koff[r], 0, 0, 0);
+    const rsrc_t vr = pf_rsrc(vtplane + row0, valid ? (uint32_t)(((int64_t)D * vt_len - row0) * 2) : 0u);
 #pragma unroll
-    for (int r8 = 0; r8 < 2; ++r8)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_void *)(vstage + (16 * wave + 8 * r8) * kPfVtRow),
-                                                 16, voff[r8], 0, 0, 0);
+    for (int r8 = 0; r8 < G::VCP; ++r8)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            vr, (lds_void *)(vstage + ((D / 8) * wave + 8 * r8) * kPfVtRow), 16, voff[r8], 0, 0, 0);
 }
 // byte offsets of this lane's copy sources from a tile's first K row / first V^T key
-PF_INLINE void pf_copy_offsets(uint32_t (&koff)[2], uint32_t (&voff)[2], int64_t k_st, int vt_len,
-                               int wave, int lane) {
+template <int D>
+PF_INLINE void pf_copy_offsets(uint32_t *koff, uint32_t *voff, int64_t k_st, int vt_len, int wave,
+                               int lane) {
+    using G = PfGeom<D>;
+    constexpr int CPR = G::ROW / 16;  // 16-byte chunks per K row
 #pragma unroll
-    for (int r4 = 0; r4 < 2; ++r4) {
-        const int row = 8 * wave + 4 * r4 + (lane >> 4);
-        koff[r4] = (uint32_t)(((int64_t)row * k_st + 8 * ((lane & 15) ^ swz(row))) * 2);
+    for (int r = 0; r < G::KCP; ++r) {
+        const int row = 8 * wave + G::RPC * r + lane / CPR;
+        koff[r] = (uint32_t)(((int64_t)row * k_st + 8 * ((lane % CPR) ^ swz<D>(row))) * 2);
     }
 #pragma unroll
-    for (int r8 = 0; r8 < 2; ++r8) {
-        const int d = 16 * wave + 8 * r8 + (lane >> 3);
+    for (int r8 = 0; r8 < G::VCP; ++r8) {
+        const int d = (D / 8) * wave + 8 * r8 + (lane >> 3);
         voff[r8] = (uint32_t)(((int64_t)d * vt_len + 8 * ((lane & 7) ^ swz_vt(d))) * 2);
     }
 }
-constexpr int kPfCopiesPerTile = 4;  // global_load_lds per wavefront per tile
 
 // s_waitcnt vmcnt(n) (gfx9 encoding; expcnt and lgkmcnt left at their maxima)
 #define PF_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | 0x0f70)
 
+template <int D>
 struct PfState {
-    u32x4 qop[8];    // Q^T operands (16-dim steps ks) of this wavefront's 32 queries, raw bits
-    f32x16 acc[4];   // O^T: 32-dim block md
+    u32x4 qop[D / 16];  // Q^T operands (16-dim steps ks) of this wavefront's 32 queries, raw bits
+    f32x16 acc[D / 32]; // O^T: 32-dim block md
     float negm;      // -m_run (0 before the first key), added to the raw scores
     float m_run, l_run;
     float thr;       // the row maximum moves when a tile's maximum exceeds thr: -inf before the
@@ -222,18 +242,18 @@ struct PfState {
 
 constexpr int kDsRead = 0x100, kMfma = 0x008, kValu = 0x402;  // sched_group_barrier classes (VALU + TRANS)
 
-// Orders a block of 16 MFMAs with its 16 LDS operand reads, VALU VALU instructions per MFMA
+// Orders a block of NM MFMAs with its NM LDS operand reads, VALU VALU instructions per MFMA
 // and the VMEM (tile copy) instructions: four reads first, then MFMA, read, copy, VALU x VALU,
 // so each MFMA's operand was requested four MFMAs earlier and the VALU work fills the MFMA
 // pipe's busy cycles.
-template <int VALU, int VMEM = 0>
+template <int VALU, int VMEM = 0, int NM = 16>
 PF_INLINE void pf_block_schedule() {
 #pragma unroll
     for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < NM; ++i) {
         __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-        if (i < 12) __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+        if (i < NM - 4) __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
         if (i < VMEM) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
         if (VALU > 0) __builtin_amdgcn_sched_group_barrier(kValu, VALU, 0);
     }
@@ -243,48 +263,53 @@ PF_INLINE void pf_block_schedule() {
 // at every step, so each read is one register plus a constant that fits the 16-bit DS offset
 // field (stage, key block, head-dim block); left alone, the compiler keeps a register per
 // (stage, offset) pair.
+template <int D>
 struct PfAddr {
-    uint32_t k[8];  // K row qr, chunk 2 ks + h (swizzled), of key block 0
-    uint32_t v[4];  // kPfVBias + V^T row qr, chunk 2 kk + h (swizzled), of head-dim block 0
+    uint32_t k[D / 16];  // K row qr, chunk 2 ks + h (swizzled), of key block 0
+    uint32_t v[4];       // VBIAS + V^T row qr, chunk 2 kk + h (swizzled), of head-dim block 0
 };
-// The V^T stages follow the four 16 KB K stages; biasing the V^T offsets by 64 KB leaves
-// (stage address - 64 KB) + head-dim block offset, below 64 KB, as the constant part.
-constexpr uint32_t kPfVBias = 4 * kPfHalf;
-PF_INLINE void pf_addr_init(PfAddr &ad, int lane) {
+// The V^T stages follow the four K stages; biasing the V^T offsets by their size (64 KB at
+// D = 128) leaves (stage address - bias) + head-dim block offset, below 64 KB, as the constant
+// part.
+template <int D>
+PF_INLINE void pf_addr_init(PfAddr<D> &ad, int lane) {
     const int qr = lane & 31, h = lane >> 5;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) ad.k[ks] = qr * kPfRow + (((2 * ks + h) ^ swz(qr)) << 4);
+    for (int ks = 0; ks < D / 16; ++ks)
+        ad.k[ks] = qr * PfGeom<D>::ROW + (((2 * ks + h) ^ swz<D>(qr)) << 4);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
-        ad.v[kk] = kPfVBias + qr * kPfVtRow + (((2 * kk + h) ^ swz_vt(qr)) << 4);
+        ad.v[kk] = PfGeom<D>::VBIAS + qr * kPfVtRow + (((2 * kk + h) ^ swz_vt(qr)) << 4);
 }
-PF_INLINE void pf_addr_opaque(PfAddr &ad) {
+template <int D>
+PF_INLINE void pf_addr_opaque(PfAddr<D> &ad) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(ad.k[i]));
+    for (int i = 0; i < D / 16; ++i) asm volatile("" : "+v"(ad.k[i]));
 #pragma unroll
     for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(ad.v[i]));
 }
 
 // S^T (64 keys x 32 queries) = K Q^T for the tile at k_lds.
-template <bool F16>
-PF_INLINE void pf_qk(f32x16 (&s)[2], const PfState &st, const uint8_t *k_lds, const PfAddr &ad) {
+template <bool F16, int D>
+PF_INLINE void pf_qk(f32x16 (&s)[2], const PfState<D> &st, const uint8_t *k_lds, const PfAddr<D> &ad) {
     using op_t = pf_op_t<F16>;
-    op_t kop[16];
+    constexpr int KS = D / 16;
+    op_t kop[2 * KS];
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
+    for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb)
-            kop[8 * mb + ks] = __builtin_bit_cast(
-                op_t, *(const u32x4 *)(k_lds + ad.k[ks] + 32 * mb * kPfRow));
+            kop[KS * mb + ks] = __builtin_bit_cast(
+                op_t, *(const u32x4 *)(k_lds + ad.k[ks] + 32 * mb * PfGeom<D>::ROW));
     // the two key blocks' chains alternate, so consecutive products are independent
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
-        s[mb] = mfma32x32x16(kop[8 * mb], __builtin_bit_cast(op_t, st.qop[0]), f32x16{});
+        s[mb] = mfma32x32x16(kop[KS * mb], __builtin_bit_cast(op_t, st.qop[0]), f32x16{});
 #pragma unroll
-    for (int ks = 1; ks < 8; ++ks)
+    for (int ks = 1; ks < KS; ++ks)
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb)
-            s[mb] = mfma32x32x16(kop[8 * mb + ks], __builtin_bit_cast(op_t, st.qop[ks]), s[mb]);
+            s[mb] = mfma32x32x16(kop[KS * mb + ks], __builtin_bit_cast(op_t, st.qop[ks]), s[mb]);
 }
 
 // Soft-capping and ALiBi of the raw scores of a tile whose first key is k0 (exp2 units, in the
@@ -323,7 +348,8 @@ PF_INLINE void pf_logit(f32x16 (&s)[2], const PfLogit &lg, int k0, int lane) {
 }
 
 // masks scores of keys outside the lane's visible range (tiles that cross a range end only)
-PF_INLINE void pf_mask(f32x16 (&s)[2], const PfState &st, int k0, int lane) {
+template <int D>
+PF_INLINE void pf_mask(f32x16 (&s)[2], const PfState<D> &st, int k0, int lane) {
     const int h = lane >> 5;
     // key - qlo of register 0, made opaque so the per-register offsets stay immediates
     int u = k0 + 4 * h - st.qlo;
@@ -367,7 +393,8 @@ PF_INLINE float pf_rowmax(const f32x16 (&s)[2]) {
 // The row maximum moves (rare): s is shifted to the new maximum, O and the row sum rescaled.
 // Q carries scale * log2(e) and pf_shift adds -m_run, so s is the exponent of p = exp2(s)
 // relative to m_run.
-PF_INLINE void pf_rescale(f32x16 (&s)[2], PfState &st, float mx, bool need) {
+template <int D>
+PF_INLINE void pf_rescale(f32x16 (&s)[2], PfState<D> &st, float mx, bool need) {
     const bool fresh = st.m_run == -__builtin_inff();
     const float shift = need ? mx : 0.0f;
     const float m_new = need ? (fresh ? 0.0f : st.m_run) + mx : st.m_run;
@@ -377,7 +404,7 @@ PF_INLINE void pf_rescale(f32x16 (&s)[2], PfState &st, float mx, bool need) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) s[mb][j] -= shift;
 #pragma unroll
-    for (int md = 0; md < 4; ++md) st.acc[md] *= alpha;
+    for (int md = 0; md < D / 32; ++md) st.acc[md] *= alpha;
     st.l_run *= alpha;
     st.m_run = m_new;
     st.thr = m_new == -__builtin_inff() ? -__builtin_inff() : 8.0f;
@@ -421,8 +448,8 @@ PF_INLINE float pf_dot2_ones(uint32_t w, float acc) {
         return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), ones, acc, false);
     }
 }
-template <bool F16>
-PF_INLINE void pf_psum(PfState &st, const u32x4 (&pop)[4]) {
+template <bool F16, int D>
+PF_INLINE void pf_psum(PfState<D> &st, const u32x4 (&pop)[4]) {
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -440,21 +467,22 @@ PF_INLINE void pf_psum(PfState &st, const u32x4 (&pop)[4]) {
 // operand holds S^T registers 8 (kk % 2) .. +7 of key block kk / 2, i.e. lane half h holds keys
 // 16 kk + 8 (e / 4) + 4 h + e % 4 in k-slot 8 h + e; the pre-pass stores V^T keys in that order
 // (bits 2 and 3 of the key swapped), so the A operand of lane (d, h) is chunk 2 kk + h of row d.
-template <bool F16>
-PF_INLINE void pf_pv(PfState &st, const u32x4 (&pop)[4], const uint8_t *v_lds, const PfAddr &ad) {
+template <bool F16, int D>
+PF_INLINE void pf_pv(PfState<D> &st, const u32x4 (&pop)[4], const uint8_t *v_lds, const PfAddr<D> &ad) {
     using op_t = pf_op_t<F16>;
-    op_t vt[16];
+    constexpr int MD = D / 32;
+    op_t vt[4 * MD];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-        for (int md = 0; md < 4; ++md)
-            vt[4 * kk + md] =
-                __builtin_bit_cast(op_t, *(const u32x4 *)(v_lds + (ad.v[kk] - kPfVBias) + md * 32 * kPfVtRow));
+        for (int md = 0; md < MD; ++md)
+            vt[MD * kk + md] = __builtin_bit_cast(
+                op_t, *(const u32x4 *)(v_lds + (ad.v[kk] - PfGeom<D>::VBIAS) + md * 32 * kPfVtRow));
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-        for (int md = 0; md < 4; ++md)
-            st.acc[md] = mfma32x32x16(vt[4 * kk + md], __builtin_bit_cast(op_t, pop[kk]), st.acc[md]);
+        for (int md = 0; md < MD; ++md)
+            st.acc[md] = mfma32x32x16(vt[MD * kk + md], __builtin_bit_cast(op_t, pop[kk]), st.acc[md]);
 }
 
 // One key tile t of a wavefront (not the last), with S(t) in `cur`:
@@ -465,13 +493,16 @@ PF_INLINE void pf_pv(PfState &st, const u32x4 (&pop)[4], const uint8_t *v_lds, c
 //    shifts S(t + 1) by -m_run and takes its row maximum; the copies of a later tile
 //    (issue_copies) are issued among its first MFMAs;
 //  * then, rarely, the row maximum moves (pf_rescale).
-template <bool LOGIT, bool F16, typename IssueCopies>
-PF_INLINE void pf_tile(f32x16 (&cur)[2], f32x16 (&nxt)[2], u32x4 (&pop)[4], PfState &st,
-                       const uint8_t *k_next, const uint8_t *v_cur, const PfAddr &ad,
+// At D = 64 each block has half the MFMAs of D = 128 for the same softmax work: twice the VALU
+// instructions go between consecutive MFMAs.
+template <bool LOGIT, bool F16, int D, typename IssueCopies>
+PF_INLINE void pf_tile(f32x16 (&cur)[2], f32x16 (&nxt)[2], u32x4 (&pop)[4], PfState<D> &st,
+                       const uint8_t *k_next, const uint8_t *v_cur, const PfAddr<D> &ad,
                        bool masked, int k1, int lane, const PfLogit &lg, IssueCopies &&issue_copies) {
-    pf_qk<F16>(nxt, st, k_next, ad);
+    constexpr int NM = D / 8, R = 128 / D;  // MFMAs per block, VALU ratio to D = 128
+    pf_qk<F16, D>(nxt, st, k_next, ad);
     pf_exp<F16>(pop, cur);
-    pf_block_schedule<3>();
+    pf_block_schedule<3 * R, 0, NM>();
     __builtin_amdgcn_sched_barrier(0);
     // P(t) is used only after the branch below: pin its computation to block 1
 #pragma unroll
@@ -479,11 +510,11 @@ PF_INLINE void pf_tile(f32x16 (&cur)[2], f32x16 (&nxt)[2], u32x4 (&pop)[4], PfSt
     if (LOGIT) pf_logit(nxt, lg, k1, lane);
     if (masked) pf_mask(nxt, st, k1, lane);
     issue_copies();
-    pf_pv<F16>(st, pop, v_cur, ad);
-    pf_psum<F16>(st, pop);
+    pf_pv<F16, D>(st, pop, v_cur, ad);
+    pf_psum<F16, D>(st, pop);
     pf_shift(nxt, st.negm);
     float mx = pf_rowmax(nxt);
-    pf_block_schedule<4, 4>();
+    pf_block_schedule<4 * R, PfGeom<D>::CP, NM>();
     __builtin_amdgcn_sched_barrier(0);
     mx = pf_max_halves(mx);
     const bool need = mx > st.thr;
@@ -491,31 +522,32 @@ PF_INLINE void pf_tile(f32x16 (&cur)[2], f32x16 (&nxt)[2], u32x4 (&pop)[4], PfSt
 }
 
 // The last key tile: P(t) and O += V(t)^T P(t).
-template <bool F16>
-PF_INLINE void pf_last_tile(const f32x16 (&cur)[2], u32x4 (&pop)[4], PfState &st,
-                            const uint8_t *v_cur, const PfAddr &ad) {
+template <bool F16, int D>
+PF_INLINE void pf_last_tile(const f32x16 (&cur)[2], u32x4 (&pop)[4], PfState<D> &st,
+                            const uint8_t *v_cur, const PfAddr<D> &ad) {
     pf_exp<F16>(pop, cur);
-    pf_pv<F16>(st, pop, v_cur, ad);
-    pf_psum<F16>(st, pop);
-    pf_block_schedule<1>();
+    pf_pv<F16, D>(st, pop, v_cur, ad);
+    pf_psum<F16, D>(st, pop);
+    pf_block_schedule<128 / D, 0, D / 8>();
 }
 
-// Two wavefronts per SIMD (8 per workgroup, ~240 registers each).
+// Two wavefronts per SIMD (8 per workgroup, ~240 registers each at D = 128).
 // LOGIT: soft-capping and / or ALiBi (a separate instantiation keeps them off the plain path)
-template <bool LOGIT, bool F16>
+template <bool LOGIT, bool F16, int D>
 __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a) {
+    using G = PfGeom<D>;
     // the K and V^T rings: four stages each, as distinct arrays named statically below, so the
     // compiler can tell the asynchronous copy into one stage from the reads of another (a
     // dynamically selected stage makes it wait for every copy before every LDS read); K stages
     // first, so a K read address plus any stage offset fits the 16-bit LDS offset field
-    __shared__ __attribute__((aligned(1024))) uint8_t ks0[kPfHalf];
-    __shared__ __attribute__((aligned(1024))) uint8_t ks1[kPfHalf];
-    __shared__ __attribute__((aligned(1024))) uint8_t ks2[kPfHalf];
-    __shared__ __attribute__((aligned(1024))) uint8_t ks3[kPfHalf];
-    __shared__ __attribute__((aligned(1024))) uint8_t vs0[kPfHalf];
-    __shared__ __attribute__((aligned(1024))) uint8_t vs1[kPfHalf];
-    __shared__ __attribute__((aligned(1024))) uint8_t vs2[kPfHalf];
-    __shared__ __attribute__((aligned(1024))) uint8_t vs3[kPfHalf];
+    __shared__ __attribute__((aligned(1024))) uint8_t ks0[G::KTILE];
+    __shared__ __attribute__((aligned(1024))) uint8_t ks1[G::KTILE];
+    __shared__ __attribute__((aligned(1024))) uint8_t ks2[G::KTILE];
+    __shared__ __attribute__((aligned(1024))) uint8_t ks3[G::KTILE];
+    __shared__ __attribute__((aligned(1024))) uint8_t vs0[G::VTILE];
+    __shared__ __attribute__((aligned(1024))) uint8_t vs1[G::VTILE];
+    __shared__ __attribute__((aligned(1024))) uint8_t vs2[G::VTILE];
+    __shared__ __attribute__((aligned(1024))) uint8_t vs3[G::VTILE];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int qr = lane & 31, h = lane >> 5;
@@ -546,7 +578,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     const int kt_begin = lo_first / kPfBK;
     const int ntiles = (hi_last + kPfBK - 1) / kPfBK - kt_begin;
 
-    PfState st;
+    PfState<D> st;
     {
         const int qi = q0 + 32 * qhalf + qr;
         const bool ok = wave_live && qi < lq;
@@ -554,7 +586,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
                               (int64_t)min(qi, lq - 1) * a.q_st;
         const float qs = a.scale_log2 * a.q_mul * (a.q_mul_dev ? a.q_mul_dev[0] : 1.0f);
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
+        for (int ks = 0; ks < G::KS; ++ks) {
             u32x4 w = ok ? ldg128(row + 16 * ks + 8 * h) : u32x4{0u, 0u, 0u, 0u};
             // q * scale * log2(e) (* k_descale), rounded to the dtype
 #pragma unroll
@@ -575,11 +607,11 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
         st.l_run = 0.0f;
         st.negm = 0.0f;
 #pragma unroll
-        for (int md = 0; md < 4; ++md) st.acc[md] = f32x16{};
+        for (int md = 0; md < G::MD; ++md) st.acc[md] = f32x16{};
     }
 
     const uint16_t *kplane = a.k + sq.k0 + (int64_t)hk * a.k_sh;
-    const uint16_t *vtplane = a.vt + ((int64_t)b * a.kv_heads + hk) * kPfD * a.vt_len;
+    const uint16_t *vtplane = a.vt + ((int64_t)b * a.kv_heads + hk) * D * a.vt_len;
     PfLogit lg = {};
     if (LOGIT) {
         lg.cap2 = a.softcap2;
@@ -596,25 +628,25 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     // V(t - 1) in step t - 1.
 #define PF_KS(k) ((k) == 0 ? ks0 : (k) == 1 ? ks1 : (k) == 2 ? ks2 : ks3)
 #define PF_VS(k) ((k) == 0 ? vs0 : (k) == 1 ? vs1 : (k) == 2 ? vs2 : vs3)
-    uint32_t koff[2], voff[2];
-    pf_copy_offsets(koff, voff, a.k_st, a.vt_len, wave, lane);
+    uint32_t koff[G::KCP], voff[G::VCP];
+    pf_copy_offsets<D>(koff, voff, a.k_st, a.vt_len, wave, lane);
     // Every step issues the copies of one tile; past the last tile they are dummies with a
     // zero-size resource (no memory access; zeros land in a stage nobody reads again), so each
     // wavefront always has the copies of exactly the next two tiles in flight at a barrier.
 #define PF_ISSUE(k, t)                                                                       \
-    pf_issue_tile(PF_KS(k), PF_VS(k), kplane, vtplane, a.k_st, a.vt_len, koff, voff,         \
+    pf_issue_tile<D>(PF_KS(k), PF_VS(k), kplane, vtplane, a.k_st, a.vt_len, koff, voff,      \
                   kt_begin + (t), lk, wave, (t) < ntiles)
     PF_ISSUE(0, 0);
     PF_ISSUE(1, 1);
     PF_ISSUE(2, 2);
-    PF_WAIT_VMCNT(2 * kPfCopiesPerTile);
+    PF_WAIT_VMCNT(2 * G::CP);
     __builtin_amdgcn_s_barrier();
 
     // Barrier t: this wavefront's copies of tile t + 1 have landed (those of tile t + 2 may be
     // in flight); the copies of tile t + 3 follow within the step.
 #define PF_SYNC(k, t)                                                                        \
     {                                                                                        \
-        PF_WAIT_VMCNT(kPfCopiesPerTile);                                                     \
+        PF_WAIT_VMCNT(G::CP);                                                                \
         __builtin_amdgcn_s_barrier();                                                        \
     }
     if (!wave_live) {  // heads past the group: copies and barriers only
@@ -634,10 +666,10 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     };
     f32x16 sa[2], sb[2];
     u32x4 pop[4];
-    PfAddr ad;
-    pf_addr_init(ad, lane);
+    PfAddr<D> ad;
+    pf_addr_init<D>(ad, lane);
     if (ntiles > 0) {
-        pf_qk<F16>(sa, st, ks0, ad);
+        pf_qk<F16, D>(sa, st, ks0, ad);
         if (LOGIT) pf_logit(sa, lg, kt_begin * kPfBK, lane);
         pf_shift(sa, st.negm);
         if (tile_masked(0)) pf_mask(sa, st, kt_begin * kPfBK, lane);
@@ -656,7 +688,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
             last = k;                                                                        \
             break;                                                                           \
         }                                                                                    \
-        pf_tile<LOGIT, F16>(CUR, NXT, pop, st, PF_KS(((k) + 1) & 3), PF_VS(k), ad,           \
+        pf_tile<LOGIT, F16, D>(CUR, NXT, pop, st, PF_KS(((k) + 1) & 3), PF_VS(k), ad,        \
                        tile_masked(t + 1), (kt_begin + t + 1) * kPfBK, lane, lg, [&] {       \
                     PF_ISSUE(((k) + 3) & 3, t + 3);                                          \
                 });                                                                          \
@@ -673,10 +705,10 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
         PF_WAIT_VMCNT(0);  // the dummy copies past the end
         pf_addr_opaque(ad);
         switch (last) {
-            case 0: pf_last_tile<F16>(sa, pop, st, vs0, ad); break;
-            case 1: pf_last_tile<F16>(sb, pop, st, vs1, ad); break;
-            case 2: pf_last_tile<F16>(sa, pop, st, vs2, ad); break;
-            default: pf_last_tile<F16>(sb, pop, st, vs3, ad); break;
+            case 0: pf_last_tile<F16, D>(sa, pop, st, vs0, ad); break;
+            case 1: pf_last_tile<F16, D>(sb, pop, st, vs1, ad); break;
+            case 2: pf_last_tile<F16, D>(sa, pop, st, vs2, ad); break;
+            default: pf_last_tile<F16, D>(sb, pop, st, vs3, ad); break;
         }
     }
 #undef PF_STEP
@@ -693,7 +725,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     if (qi >= lq) return;
     uint16_t *orow = a.out + sq.o0 + (int64_t)qi * a.o_st + (int64_t)head * a.o_sh;
 #pragma unroll
-    for (int md = 0; md < 4; ++md)
+    for (int md = 0; md < G::MD; ++md)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             u32x2 w;
@@ -718,7 +750,9 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
 PF_INLINE float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 PF_INLINE float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-constexpr int kStRow = 68;  // LDS row stride of the pre-pass tiles in 32-bit words (272 B)
+// LDS row stride of the pre-pass tiles in 32-bit words: the row plus 16 bytes (272 B at D = 128)
+template <int D>
+constexpr int st_row() { return D / 2 + 4; }
 
 // 8 E4M3 codes (byte order) -> 8 bf16 or f16 values (exact), one conversion per pair
 PF_INLINE u32x4 pf_widen_e4m3(u32x2 c, bool f16) {
@@ -737,7 +771,12 @@ PF_INLINE u32x4 pf_widen_e4m3(u32x2 c, bool f16) {
     return r;
 }
 
+template <int D>
 __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
+    constexpr int kStRow = st_row<D>(), CPR = D / 8;  // 16-byte chunks per row
+    // (the fused FP8 append and the E4M3 widening are D = 128 only: the host passes neither
+    // at D = 64)
+    constexpr bool kFull = D == kPfD;
     __shared__ __attribute__((aligned(16))) uint32_t vtile[kPfBK * kStRow];
     __shared__ __attribute__((aligned(16))) uint32_t ktile[kPfBK * kStRow];
     __shared__ float vscale[kPfBK], vrcp[kPfBK];
@@ -748,12 +787,12 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
     const uint16_t *vplane = a.v + sq.v0 + (int64_t)hk * a.v_sh;
     const uint16_t *kplane = a.k + sq.k0 + (int64_t)hk * a.k_sh;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int id = tid + 256 * i, row = id >> 4, c = id & 15;
+    for (int i = 0; i < D / 32; ++i) {
+        const int id = tid + 256 * i, row = id / CPR, c = id % CPR;
         const int key = kt * kPfBK + row;
         u32x4 w = {0u, 0u, 0u, 0u};
         if (key < kv_len) {
-            if (a.e4m3) {  // dense batches: the sequence is batch row b
+            if (kFull && a.e4m3) {  // dense batches: the sequence is batch row b
                 const uint8_t *kp = a.k8 + (int64_t)b * a.k8_sb + (int64_t)hk * a.k8_sh;
                 const uint8_t *vp = a.v8 + (int64_t)b * a.v8_sb + (int64_t)hk * a.v8_sh;
                 w = pf_widen_e4m3(*(const u32x2 *)(vp + (int64_t)key * a.v8_st + 8 * c), a.f16);
@@ -764,7 +803,7 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
             }
         }
         *(u32x4 *)&vtile[row * kStRow + 4 * c] = w;
-        if (a.append) {
+        if (kFull && a.append) {
             u32x4 wk = {0u, 0u, 0u, 0u};
             if (key < kv_len) wk = *(const u32x4 *)(kplane + (int64_t)key * a.k_st + 8 * c);
             *(u32x4 *)&ktile[row * kStRow + 4 * c] = wk;
@@ -772,9 +811,9 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
     }
     __syncthreads();
     // V^T: thread (d, j) writes keys 8j .. 8j+7 (in register order) of head dim d
-    uint16_t *out = (uint16_t *)a.vt + ((int64_t)b * a.kv_heads + hk) * kPfD * a.vt_len;
+    uint16_t *out = (uint16_t *)a.vt + ((int64_t)b * a.kv_heads + hk) * D * a.vt_len;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < D / 32; ++i) {
         const int id = tid + 256 * i, d = id >> 3, j = id & 7;
         uint32_t w[4];
 #pragma unroll
@@ -787,7 +826,7 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
         }
         *(u32x4 *)(out + (int64_t)d * a.vt_len + kt * kPfBK + 8 * j) = u32x4{w[0], w[1], w[2], w[3]};
     }
-    if (!a.append) return;
+    if (!kFull || !a.append) return;
     const int64_t plane = (int64_t)b * a.kv_heads + hk;
     // ---- per-token scales: 4 threads per token, 32 head dims each ----
     const int r = tid >> 2, qd = tid & 3, t = kt * kPfBK + r;
@@ -881,12 +920,13 @@ namespace cqkv {
 // Whether a call takes the MFMA prefill kernel (bf16, head dim 128, more than 16 queries);
 // every other call runs the plain-dtype kernel of flash_plain.h.
 static bool pf_fast_path(int32_t dtype, int32_t head_dim, int32_t q_len) {
-    return (dtype == CQKV_BF16 || dtype == CQKV_F16) && head_dim == kPfD && q_len > 16;
+    return (dtype == CQKV_BF16 || dtype == CQKV_F16) && (head_dim == 128 || head_dim == 64) &&
+           q_len > 16;
 }
 
 // V^T scratch of the MFMA prefill: (batch, kv heads, D, kv_len rounded up to the key tile) bf16.
-static size_t pf_vt_bytes(int32_t batch, int32_t kv_len, int32_t kv_heads) {
-    return (size_t)batch * kv_heads * kPfD * ((kv_len + kPfBK - 1) / kPfBK * kPfBK) * 2;
+static size_t pf_vt_bytes(int32_t batch, int32_t kv_len, int32_t kv_heads, int32_t head_dim) {
+    return (size_t)batch * kv_heads * head_dim * ((kv_len + kPfBK - 1) / kPfBK * kPfBK) * 2;
 }
 // K widened from E4M3: (batch, kv heads, kv_len, D) of the dtype.
 static size_t pf_kst_bytes(int32_t batch, int32_t kv_len, int32_t kv_heads) {
@@ -899,12 +939,13 @@ bool prefill_takes(int32_t dtype, int32_t head_dim, int32_t q_len, const void *q
         const int64_t e = bytes / 2;
         return (uintptr_t)p % bytes == 0 && st[0] % e == 0 && st[1] % e == 0 && st[2] % e == 0;
     };
-    return pf_fast_path(dtype, head_dim, q_len) && aligned(q, q_strides, 16) &&
+    // (the E4M3 widening of the pre-pass is written for head dim 128)
+    return head_dim == kPfD && pf_fast_path(dtype, head_dim, q_len) && aligned(q, q_strides, 16) &&
            aligned(out, out_strides, 8);
 }
 
 size_t prefill_e4m3_workspace(int32_t batch, int32_t kv_len, int32_t kv_heads) {
-    return (pf_vt_bytes(batch, kv_len, kv_heads) + 255) / 256 * 256 +
+    return (pf_vt_bytes(batch, kv_len, kv_heads, kPfD) + 255) / 256 * 256 +
            pf_kst_bytes(batch, kv_len, kv_heads);
 }
 
@@ -919,8 +960,20 @@ size_t flash_attn_workspace(int32_t dtype, int32_t batch, int32_t q_len, int32_t
     // a call of the MFMA prefill's shape whose q / out rows are not aligned for it runs the
     // plain kernel: size for either
     if (kv_len > 0 && pf_fast_path(dtype, head_dim, q_len))
-        return std::max(pf_vt_bytes(batch, kv_len, kv_heads), plain);
+        return std::max(pf_vt_bytes(batch, kv_len, kv_heads, head_dim), plain);
     return plain;
+}
+
+template <int D>
+static void pf_launch(bool f16, bool terms, dim3 grid, hipStream_t st, const PrefillArgs &a) {
+    const dim3 block(kPfWaves * 64);
+    if (f16) {
+        if (terms) hipLaunchKernelGGL((prefill_kernel<true, true, D>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((prefill_kernel<false, true, D>), grid, block, 0, st, a);
+    } else {
+        if (terms) hipLaunchKernelGGL((prefill_kernel<true, false, D>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((prefill_kernel<false, false, D>), grid, block, 0, st, a);
+    }
 }
 
 int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
@@ -964,7 +1017,7 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
     const bool fast = !no_rows && !no_keys && (kv_dtype == dtype || e4m3) &&
                       pf_fast_path(dtype, head_dim, q_len) && aligned(q, q_strides, 16) &&
                       aligned(out, out_strides, 8);
-    if (e4m3 && (!fast || cu_seqlens_q || k_cache))
+    if (e4m3 && (!fast || head_dim != kPfD || cu_seqlens_q || k_cache))
         return fail(CQKV_ERR_ARG, "cqkv_flash_attn: E4M3 K / V under %s queries take the MFMA prefill only",
                     dtype == CQKV_F16 ? "f16" : "bf16");
     if (!fast) {
@@ -1106,7 +1159,7 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
     // the widened K
     a.vt_len = (kv_len + kPfBK - 1) / kPfBK * kPfBK;
     void *vt = workspace;
-    const size_t vt_bytes = pf_vt_bytes(batch, kv_len, kv_heads);
+    const size_t vt_bytes = pf_vt_bytes(batch, kv_len, kv_heads, head_dim);
     const size_t kst_off = (vt_bytes + 255) / 256 * 256;
     const size_t ws_bytes = e4m3 ? kst_off + pf_kst_bytes(batch, kv_len, kv_heads) : vt_bytes;
     if (workspace && workspace_bytes < ws_bytes)
@@ -1136,7 +1189,7 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
     }
     // an FP8 append runs inside the pre-pass when value tiles line up (position % 8 == 0) and
     // neither side rotates; any other append as two cqkv_quant_append launches after the attention
-    const bool fused = k_cache != nullptr && dtype == CQKV_BF16 && position % 8 == 0 &&
+    const bool fused = k_cache != nullptr && dtype == CQKV_BF16 && head_dim == kPfD && position % 8 == 0 &&
                        k_cache->format == CQKV_FMT_FP8 &&
                        v_cache->format == CQKV_FMT_FP8 && !side_rotates(k_cache) &&
                        !side_rotates(v_cache);
@@ -1152,17 +1205,13 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
         a.vc_plane = (uint32_t)cqkv_codes_plane_bytes(CQKV_FMT_FP8, kPfD, v_cache->capacity);
         a.vs_plane = (uint32_t)cqkv_scales_plane_bytes(CQKV_FMT_FP8, kPfD, v_cache->capacity);
     }
-    hipLaunchKernelGGL(prefill_stage_kernel, dim3(a.vt_len / kPfBK, kv_heads, batch), dim3(256),
-                       0, st, a);
+    const dim3 sgrid(a.vt_len / kPfBK, kv_heads, batch);
+    if (head_dim == 64) hipLaunchKernelGGL(prefill_stage_kernel<64>, sgrid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(prefill_stage_kernel<128>, sgrid, dim3(256), 0, st, a);
     const dim3 grid(a.q_blocks * kv_heads * ((a.group + a.heads_per_wg - 1) / a.heads_per_wg) * batch);
     const bool terms = softcap > 0.0f || alibi_slopes;
-    if (dtype == CQKV_F16) {
-        if (terms) hipLaunchKernelGGL((prefill_kernel<true, true>), grid, dim3(kPfWaves * 64), 0, st, a);
-        else hipLaunchKernelGGL((prefill_kernel<false, true>), grid, dim3(kPfWaves * 64), 0, st, a);
-    } else {
-        if (terms) hipLaunchKernelGGL((prefill_kernel<true, false>), grid, dim3(kPfWaves * 64), 0, st, a);
-        else hipLaunchKernelGGL((prefill_kernel<false, false>), grid, dim3(kPfWaves * 64), 0, st, a);
-    }
+    if (head_dim == 64) pf_launch<64>(dtype == CQKV_F16, terms, grid, st, a);
+    else pf_launch<128>(dtype == CQKV_F16, terms, grid, st, a);
     hipError_t le = hipGetLastError();
     hipError_t fe = vt_owned ? hipFreeAsync(vt, st) : hipSuccess;
     if (le != hipSuccess) return fail(CQKV_ERR_HIP, "cqkv_flash_attn: launch: %s", hipGetErrorString(le));
