@@ -439,8 +439,9 @@ __device__ inline float e8m0_scale(uint32_t code) {  // code 0 marks an all-zero
 // f16 (exact): one conversion per code pair, one packed f16 multiply.
 __device__ inline f16x8 nvfp4x8_f16x8(uint32_t w, uint32_t cs, int bi) {
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    const h2 c2 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(cs >> (8 * (bi & 2)), 1.0f, false));
-    const h2 sc = (bi & 1) ? h2{c2.y, c2.y} : h2{c2.x, c2.x};
+    const uint32_t c2 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(cs >> (8 * (bi & 2)), 1.0f, false));
+    // the block's f16 scale in both halves (one byte permute)
+    const h2 sc = __builtin_bit_cast(h2, __builtin_amdgcn_perm(c2, c2, (bi & 1) ? 0x03020302u : 0x01000100u));
     h2 r[4];
     r[0] = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0)) * sc;
     r[1] = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 1)) * sc;
@@ -449,27 +450,18 @@ __device__ inline f16x8 nvfp4x8_f16x8(uint32_t w, uint32_t cs, int bi) {
     return __builtin_bit_cast(f16x8, r);
 }
 
-// NVFP4 value operand: 8 E2M1 codes of 8 keys, key e's code times its scale sg[e] = fl(cs * gs)
-// (the E4M3 block scale times the token's f32 scale, rounded once per block), then rounded to
-// bf16. The reference's dequantized cache rounds fl(fl(fp4 * cs) * gs) instead (RowCodec::elem
-// times rsc0, turbo.rs:383-395): the two agree except where the f32 values straddle a bf16
-// rounding boundary (one bf16 ulp, rarely). The codes are converted unscaled: the conversion's
-// own scale operand takes only the exponent (E8M0 powers of two), not E4M3 values.
-__device__ inline bf16x8 nvfp4x8_keys_bf16x8(uint32_t w, const float *sg) {
-    u32x4 r;
-    uint32_t *rp = (uint32_t *)&r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        f32x2 f;
-        switch (i) {
-        case 0: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0); break;
-        case 1: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1); break;
-        case 2: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2); break;
-        default: f = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3); break;
-        }
-        rp[i] = pack_bf16x2(f.x * sg[2 * i], f.y * sg[2 * i + 1]);
-    }
-    return __builtin_bit_cast(bf16x8, r);
+// NVFP4 value operand: 8 E2M1 codes of 8 keys (one head dim), key pair i's codes times the f16
+// pair cs[i] of their E4M3 block scales: exact in f16, one conversion and one packed multiply per
+// pair. The reference's dequantized value is fl(fl(fp4 * cs) * gs) (RowCodec::elem times rsc0,
+// turbo.rs:383-395); fp4 * cs is exact here and gs goes into P.
+__device__ inline f16x8 nvfp4_codes_f16x8(uint32_t w, const uint32_t *cs) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    h2 r[4];
+    r[0] = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0)) * __builtin_bit_cast(h2, cs[0]);
+    r[1] = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 1)) * __builtin_bit_cast(h2, cs[1]);
+    r[2] = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 2)) * __builtin_bit_cast(h2, cs[2]);
+    r[3] = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 3)) * __builtin_bit_cast(h2, cs[3]);
+    return __builtin_bit_cast(f16x8, r);
 }
 
 template <int KF, int VF, int D, bool TERMS>
@@ -478,7 +470,8 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
                                     int lo, int hi, int lo_max, int hi_min, int L, int koff,
                                     uint32_t tab, float &m_run, float &l_run,
                                     f32x4 *acc, const kop_t<KF> *qsop, uint32_t ktab,
-                                    uint32_t vtab, float slope2, int qpos, float kscale2) {
+                                    uint32_t vtab, float slope2, int qpos, float kscale2,
+                                    int &e_run) {
     constexpr int NCH = D / 32;
     const int g = lane >> 4;
     // tile and L are rows of the current block (the whole cache when not paged); keys of the
@@ -587,6 +580,36 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
     const float m_new = fmaxf(m_run, mx);
     const bool none = m_new == -__builtin_inff();
     const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+    float alpha_o = alpha;  // O's factor (NVFP4 values: times 2^(old e_run - new e_run))
+    // keys past the written length may hold any bytes: keep them out of PV
+    const int nv = min(max(L - kbase, 0), 8);
+    float gsw[8];  // NVFP4 values: the keys' f32 token scales times 2^(14 - e_run)
+    if constexpr (VF == CQKV_FMT_NVFP4) {
+        if (t0 + 32 > L) {  // uniform: only the tile holding the end of the keys
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (e >= nv) {
+                    cur.nvg[e] = 0u;
+#pragma unroll
+                    for (int i = 0; i < D / 64; ++i) cur.nvb[(D / 64) * e + i] = 0u;
+                }
+        }
+        // O is accumulated in units of 2^(e_run - 14), with e_run the largest binary exponent of
+        // the token scales seen so far (uniform: every lane group reads 8 of the tile's 32 keys),
+        // so the f16 operand P * g * 2^(14 - e_run) stays below 2^14 and products down to 2^-28 of
+        // the largest remain normal f16 numbers; a larger exponent rescales O exactly.
+        float gm = __uint_as_float(cur.nvg[0]);
+#pragma unroll
+        for (int e = 1; e < 8; ++e) gm = fmaxf(gm, __uint_as_float(cur.nvg[e]));
+        gm = group16_max(gm);
+        const int e_new = gm > 0.0f ? max(e_run, __builtin_amdgcn_frexp_expf(gm)) : e_run;
+        if (e_new != e_run) {
+            alpha_o = __builtin_ldexpf(alpha, e_run - e_new);
+            e_run = e_new;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) gsw[e] = __builtin_ldexpf(__uint_as_float(cur.nvg[e]), 14 - e_run);
+    }
     float p[8], psum = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -595,12 +618,10 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
     }
     l_run = l_run * alpha + psum;
     m_run = m_new;
-    if (__any(alpha != 1.0f)) {
+    if (__any(alpha_o != 1.0f)) {
 #pragma unroll
-        for (int t = 0; t < 2 * NCH; ++t) acc[t] *= alpha;
+        for (int t = 0; t < 2 * NCH; ++t) acc[t] *= alpha_o;
     }
-    // keys past the written length may hold any bytes: keep them out of PV
-    const int nv = min(max(L - kbase, 0), 8);
     if (t0 + 32 > L) {  // uniform: only the tile holding the end of the keys
 #pragma unroll
         for (int u = 0; u < NCH; ++u) {
@@ -620,7 +641,37 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
         }
     }
     // O^T += V^T P^T: d-tile 2u + h, row r <-> head dim 32u + 2r + h
-    if constexpr (VF == CQKV_FMT_MXFP4) {
+    if constexpr (VF == CQKV_FMT_NVFP4) {
+        // V: E2M1 code times its E4M3 block scale, exact in f16 (at most 6 significant bits,
+        // 2^-10 .. 2688); the key's f32 token scale goes into P, one f16 operand
+        // p * g * 2^(14 - e_run) (11 significant bits), as TurboQuant's norm does. Keys past the
+        // length have zero codes and scales.
+        float pv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pv[e] = p[e] * gsw[e];
+        const f16x8 pf = __builtin_bit_cast(
+            f16x8, u32x4{pack_f16x2(pv[0], pv[1]), pack_f16x2(pv[2], pv[3]), pack_f16x2(pv[4], pv[5]),
+                         pack_f16x2(pv[6], pv[7])});
+#pragma unroll
+        for (int u = 0; u < NCH; ++u) {
+            // rows 32u + 2n + h lie in block bi = 2u + n / 8 of every key: byte bi % 4 of the key's
+            // word bi / 4; the pair (keys 2i, 2i + 1) gathered into bytes 0-1 by one byte permute
+            const int bi = 2 * u + ((lane & 15) >> 3);
+            const uint32_t sel = (uint32_t)(bi & 3) | ((uint32_t)(4 + (bi & 3)) << 8) | 0x0c0c0000u;
+            uint32_t cs[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                cs[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(
+                                                         __builtin_amdgcn_perm(cur.nvb[(D / 64) * (2 * i + 1) + (bi >> 2)],
+                                                                               cur.nvb[(D / 64) * (2 * i) + (bi >> 2)], sel),
+                                                         1.0f, false));
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const f16x8 v = nvfp4_codes_f16x8(cur.v[u][h], cs);
+                acc[2 * u + h] = mfma16x16x32(v, pf, acc[2 * u + h]);
+            }
+        }
+    } else if constexpr (VF == CQKV_FMT_MXFP4) {
         // value block u: P scaled by the keys' block-u scales, one bf16 operand (the E2M1 codes
         // and E8M0 scales are exact; P rounds to 8 significant bits, as in a bf16 flash
         // attention). The scale of E8M0 code c is the float with exponent field c (code 0: 0).
@@ -653,7 +704,7 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
             acc[2 * u + 1] = mfma16x16x32(v1, pb, acc[2 * u + 1]);
         }
     } else {
-        // FP8 / MXFP8 / NVFP4: the value scales are inside the V operand (rounded to bf16 as the
+        // FP8 / MXFP8: the value scales are inside the V operand (rounded to bf16 as the
         // reference's dequantized cache), P goes in full precision as a bf16 hi + lo pair.
         // TURBO4: the norm goes into P, which enters as one f16 operand (11 significant bits;
         // the lo part cost 8 more MFMAs per tile: config 5 246-254 -> 236 us same-box).
@@ -664,8 +715,6 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
             // scales past the written length may be any bits
             if constexpr (direct_scales<VF>())
                 vw[e] = e < nv ? cur.vs8[e] : 0u;
-            else if constexpr (VF == CQKV_FMT_NVFP4)
-                vw[e] = e < nv ? cur.nvb[(D / 64) * e] : 0u;
             else
                 vw[e] = e < nv ? (uint32_t)__shfl((int)cur.vs, 8 * g + e) : 0u;
             sv[e] = __uint_as_float(vw[e]);  // FP8 scale, TURBO4 norm
@@ -675,12 +724,6 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
                 pv[e] = (e < nv && p[e] > 0.0f) ? p[e] * sv[e] : 0.0f;
             else
                 pv[e] = (e < nv && p[e] > 0.0f) ? p[e] : 0.0f;
-        }
-        float gk[8];  // NVFP4: the keys' f32 scales
-        if constexpr (VF == CQKV_FMT_NVFP4) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                gk[e] = e < nv ? __uint_as_float(cur.nvg[e]) : 0.0f;
         }
         op_t<VF> phi, plo;
         split8(pv, phi, plo);
@@ -698,19 +741,6 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
                     su[e] = e8m0_scale(((u < 4 ? vw[e] : vw2[e]) >> (8 * (u & 3))) & 0xffu);
                 v0 = fp8x8_scaled_bf16x8(cur.v[u][0], cur.v[u][1], su);
                 v1 = fp8x8_scaled_bf16x8(cur.v[u][2], cur.v[u][3], su);
-            } else if constexpr (VF == CQKV_FMT_NVFP4) {
-                // this lane's rows 32u + 2n + h lie in block 2u + n / 8 of every key: byte bi % 4
-                // of the key's word bi / 4 (D / 64 words per key)
-                const int bi = 2 * u + ((lane & 15) >> 3);
-                float sg[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const uint32_t w = e < nv ? cur.nvb[(D / 64) * e + (bi >> 2)] : 0u;
-                    sg[e] = __builtin_amdgcn_cvt_f32_fp8(w >> (8 * (bi & 3)), 0) * gk[e];
-                    if (e >= nv) sg[e] = 0.0f;
-                }
-                v0 = nvfp4x8_keys_bf16x8(cur.v[u][0], sg);
-                v1 = nvfp4x8_keys_bf16x8(cur.v[u][1], sg);
             } else {
                 v0 = decode8<VF>(cur.v[u][0], 0, 1.0f, compact_tab<VF>() ? vtab : tab);
                 v1 = decode8<VF>(cur.v[u][1], 0, 1.0f, compact_tab<VF>() ? vtab : tab);
@@ -939,6 +969,8 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
     const uint32_t ktab = (uint32_t)(size_t)sm_ktab + 4 * (lane & 31);
     const uint32_t vtab = (uint32_t)(size_t)sm_vtab + 4 * (lane & 31);
     float m_run = -__builtin_inff(), l_run = 0.0f;
+    // NVFP4 values: O in units of 2^(e_run - 14) (below any f32 exponent until a scale is seen)
+    int e_run = -1024;
 
     // Register sets A and B alternate; the scheduling barriers keep every load of one set
     // issued before the next set's, so each wait only covers the set about to be used.
@@ -951,20 +983,26 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
     for (; t < te; t += 2 * WAVES) {
         compute_tile<KF, VF, D, TERMS>(ta, t, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min, Lb,
                                        koff, tab, m_run, l_run, acc, kProd ? qsop : qhi, ktab, vtab,
-                                       slope2, qpos, kscale2);
+                                       slope2, qpos, kscale2, e_run);
         __builtin_amdgcn_sched_barrier(0);
         load_tile<KF, VF, D>(ta, t + 2 * WAVES, t + 2 * WAVES < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
         __builtin_amdgcn_sched_barrier(0);
         if (t + WAVES < te)
             compute_tile<KF, VF, D, TERMS>(tb2, t + WAVES, a, qhi, qlo, q_split, lane, lo, hi, lo_max,
                                            hi_min, Lb, koff, tab, m_run, l_run, acc,
-                                           kProd ? qsop : qhi, ktab, vtab, slope2, qpos, kscale2);
+                                           kProd ? qsop : qhi, ktab, vtab, slope2, qpos, kscale2, e_run);
         __builtin_amdgcn_sched_barrier(0);
         load_tile<KF, VF, D>(tb2, t + 3 * WAVES, t + 3 * WAVES < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
         __builtin_amdgcn_sched_barrier(0);
     }
 
     // ---- merge the wavefronts ----
+    if constexpr (VF == CQKV_FMT_NVFP4) {
+#pragma unroll
+        for (int t = 0; t < 2 * NCH; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[t][i] = __builtin_ldexpf(acc[t][i], e_run - 14);
+    }
     if constexpr (kTurbo) __syncthreads();  // every wavefront is done with the code table
     const float l_col = group16_sum(l_run);
 #pragma unroll
