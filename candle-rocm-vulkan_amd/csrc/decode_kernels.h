@@ -538,7 +538,9 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
             z0 = mfma16x16x32(signs_f16x8(sw0, j & 3), qsop[j], z0);
             z1 = mfma16x16x32(signs_f16x8(sw1, j & 3), qsop[j], z1);
         }
-        if (q_split) {
+        // (TurboQuant keys never take a query lo part: no branch, so the chunks' code lookups
+        // and products schedule as one block)
+        if (!turbo_mse<KF>() && !is_prod<KF>() && q_split) {
             s0 = mfma16x16x32(k0, qlo[j], s0);
             s1 = mfma16x16x32(k1, qlo[j], s1);
         }
