@@ -459,17 +459,19 @@ __device__ inline void fa_issue_shared(uint8_t *stage, int t, int te, const uint
 
 // Prefill-shaped calls: one workgroup = 4 wavefronts on 4 consecutive 16-column blocks (64
 // columns of a kv head) over one split of the keys. The wavefronts share every K / V tile: each
-// issues a quarter of a tile's copies into a three-stage LDS ring, one barrier per tile, and
-// computes its own columns; no merge across wavefronts.
+// issues a quarter of a tile's copies into a three-stage LDS ring (two at D = 256, so that two
+// workgroups share a CU), one barrier per tile, and computes its own columns; no merge across
+// wavefronts.
 template <bool F16, int D>
 __global__ __launch_bounds__(256) void fa_tile_kernel(FaArgs a) {
     using op_t = fa_op_t<F16>;
     using G = FaTileGeom<D>;
     constexpr int NJ = D / 32, NU = D / 16, W = 4, NCPW = G::NCP / W;
+    constexpr int NST = D == 256 ? 2 : 3;  // ring stages (96 KB of three at D = 256: one workgroup per CU)
     static_assert(G::NCP % W == 0, "copies per wavefront");
     __shared__ __attribute__((aligned(1024))) uint8_t st0[2 * G::TILE];
     __shared__ __attribute__((aligned(1024))) uint8_t st1[2 * G::TILE];
-    __shared__ __attribute__((aligned(1024))) uint8_t st2[2 * G::TILE];
+    __shared__ __attribute__((aligned(1024))) uint8_t st2[NST == 3 ? 2 * G::TILE : 1024];
 
     const int planes = a.batch * a.kv_heads;
     const int rest = (int)blockIdx.x / planes, plane_id = (int)blockIdx.x % planes;
@@ -566,16 +568,18 @@ __global__ __launch_bounds__(256) void fa_tile_kernel(FaArgs a) {
 
     fa_issue_shared<D, NCPW>(st0, tb, te, kplane, vplane, a.k_st, a.v_st, Lb, a.head_dim, wave,
                              koffs, voffs);
-    fa_issue_shared<D, NCPW>(st1, tb + 1, te, kplane, vplane, a.k_st, a.v_st, Lb, a.head_dim,
-                             wave, koffs, voffs);
-    // step t: stage t % 3 holds tile t; after the barrier every copy of tile t has landed and
-    // every wavefront is done with tile t - 1, whose stage takes tile t + 2
-#define FA_TSTEP(CUR, NEXT2)                                                                    \
+    if constexpr (NST == 3)
+        fa_issue_shared<D, NCPW>(st1, tb + 1, te, kplane, vplane, a.k_st, a.v_st, Lb, a.head_dim,
+                                 wave, koffs, voffs);
+    // step t: stage t % NST holds tile t; after the barrier every copy of tile t has landed and
+    // every wavefront is done with tile t - 1, whose stage takes tile t + NST - 1 (with two
+    // stages the wait covers every copy in flight: the next tile's are issued after the barrier)
+#define FA_TSTEP(CUR, NEXT)                                                                     \
     {                                                                                          \
         if (t >= te) break;                                                                    \
-        FA_WAIT_VMCNT(2 * NCPW);                                                               \
+        FA_WAIT_VMCNT(NST == 3 ? 2 * NCPW : 0);                                                \
         __syncthreads();                                                                       \
-        fa_issue_shared<D, NCPW>(NEXT2, t + 2, te, kplane, vplane, a.k_st, a.v_st, Lb,          \
+        fa_issue_shared<D, NCPW>(NEXT, t + NST - 1, te, kplane, vplane, a.k_st, a.v_st, Lb,     \
                                  a.head_dim, wave, koffs, voffs);                              \
         if (wave_live)                                                                         \
             fa_tile<F16, D, false>(CUR, CUR + G::TILE, qop, t, lane, lo, hi, wlo_max, whi_min,  \
@@ -584,10 +588,17 @@ __global__ __launch_bounds__(256) void fa_tile_kernel(FaArgs a) {
         __builtin_amdgcn_sched_barrier(0);                                                     \
         ++t;                                                                                   \
     }
-    for (int t = tb;;) {
-        FA_TSTEP(st0, st2)
-        FA_TSTEP(st1, st0)
-        FA_TSTEP(st2, st1)
+    if constexpr (NST == 3) {
+        for (int t = tb;;) {
+            FA_TSTEP(st0, st2)
+            FA_TSTEP(st1, st0)
+            FA_TSTEP(st2, st1)
+        }
+    } else {
+        for (int t = tb;;) {
+            FA_TSTEP(st0, st1)
+            FA_TSTEP(st1, st0)
+        }
     }
 #undef FA_TSTEP
     FA_WAIT_VMCNT(0);
