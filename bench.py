@@ -13,7 +13,8 @@ timed with HIP events on the stream the library launches on (torch's current str
 roofline.achieved = the same bytes / the decode kernel's average duration (the same figure, as
 one call is one launch). roofline.traffic = HBM bytes per launch read by rocprofv3's FETCH_SIZE
 and WRITE_SIZE counters, scaled by what they read for a plain copy of known size; it is taken
-from the committed counter summary when that file is present. cpu_baseline = the oracle's
+from the committed counter summary only while that summary's kernel-source digest equals these
+sources' (csrc_digest), and is null otherwise. cpu_baseline = the oracle's
 restatement of the reference CPU path (dequantize -> bf16 -> f32 unfused attention), timed on the
 host on a bounded sample of the same workload.
 
@@ -582,6 +583,9 @@ def main():
             "BASELINE config 3: MXFP4-KV ragged decode", ms, nbytes,
             {"batch": 64, "q_heads": 32, "kv_heads": 8, "head_dim": 128,
              "lens": "uniform [1024, 32768], random.Random(3)", "sum_len": int(sum(lens)),
+             "dtype": "e2m1 codes with e8m0 block scales; bf16 MFMA operands: keys exact, "
+                      "bf16 queries exact, P times each key's value block scale as one bf16 "
+                      "operand (8 significant bits); f32 accumulate",
              "timed": "whole call (split-K decode + combine)"})
         log(f"config 3: {ms * 1e3:.2f} us/call")
         if not args.no_cpu:
@@ -602,6 +606,10 @@ def main():
         other["c5_turbo4"] = decode_summary(
             "BASELINE config 5: TurboQuant-4 KV decode", ms, nbytes,
             {"batch": 8, "q_heads": 64, "kv_heads": 8, "head_dim": 128, "context": 131072,
+             "dtype": "4-bit codebook codes with f32 norms; f16 MFMA operands: codebook values "
+                      "(f16-rounded f32 centroids), the rotated queries as one f16 operand and P "
+                      "times the norms as one f16 operand (11 significant bits each); f32 "
+                      "accumulate",
              "timed": "whole call (split-K decode + combine with unrotation)"})
         log(f"config 5: {ms * 1e3:.2f} us/call")
         if not args.no_cpu:
@@ -625,6 +633,9 @@ def main():
             "TurboProd (QJL) keys + TurboQuant-4 values decode at the BASELINE config-5 shape",
             ms, nbytes,
             {"batch": 8, "q_heads": 64, "kv_heads": 8, "head_dim": 128, "context": 131072,
+             "dtype": "keys: 3-bit codebook codes, f32 norm and |r|, QJL sign bits as exact +-1 "
+                      "operands; f16 MFMA operands: codebook values, rotated queries and S q as "
+                      "one f16 operand each; values as TurboQuant-4; f32 accumulate",
              "timed": "whole call (split-K decode + combine with unrotation)"})
         log(f"turboprod: {ms * 1e3:.2f} us/call")
         if not args.no_cpu:
@@ -653,10 +664,15 @@ def main():
             caches, _, ms, nbytes = decode_case(cq, dev, stream, fmt, 32, 32, 8, 128, 8192,
                                                 steps_x, warm_x)
             del caches
+            dt = ("e4m3 codes with e8m0 block scales, exact in bf16; bf16 queries; P as bf16 "
+                  "hi + lo operands; f32 accumulate" if fmt == cq.MXFP8 else
+                  "e2m1 codes times e4m3 block scales, exact in f16, on both sides; queries as "
+                  "f16 (scaled by a power of two into range), the f32 token scales on the scores "
+                  "and, for values, in one f16 P operand (11 significant bits); f32 accumulate")
             other[f"c2_shape_{name}"] = decode_summary(
                 f"{name.upper()}-KV decode at the BASELINE config-2 shape", ms, nbytes,
                 {"batch": 32, "q_heads": 32, "kv_heads": 8, "head_dim": 128, "context": 8192,
-                 "timed": "whole call (split-K decode + combine)"})
+                 "dtype": dt, "timed": "whole call (split-K decode + combine)"})
             log(f"{name}: {ms * 1e3:.2f} us/call")
             torch.cuda.empty_cache()
     if want("pd"):
