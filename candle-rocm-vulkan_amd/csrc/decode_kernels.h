@@ -464,9 +464,10 @@ __device__ inline f16x8 nvfp4_codes_f16x8(uint32_t w, const uint32_t *cs) {
     return __builtin_bit_cast(f16x8, r);
 }
 
-template <int KF, int VF, int D, bool TERMS>
+// QS: the queries carry a lo part (their own instantiation: no branch inside the key products)
+template <int KF, int VF, int D, bool TERMS, bool QS>
 __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const DecodeArgs &a,
-                                    const kop_t<KF> *qhi, const kop_t<KF> *qlo, bool q_split, int lane,
+                                    const kop_t<KF> *qhi, const kop_t<KF> *qlo, int lane,
                                     int lo, int hi, int lo_max, int hi_min, int L, int koff,
                                     uint32_t tab, float &m_run, float &l_run,
                                     f32x4 *acc, const kop_t<KF> *qsop, uint32_t ktab,
@@ -538,9 +539,7 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
             z0 = mfma16x16x32(signs_f16x8(sw0, j & 3), qsop[j], z0);
             z1 = mfma16x16x32(signs_f16x8(sw1, j & 3), qsop[j], z1);
         }
-        // (TurboQuant keys never take a query lo part: no branch, so the chunks' code lookups
-        // and products schedule as one block)
-        if (!turbo_mse<KF>() && !is_prod<KF>() && q_split) {
+        if constexpr (QS) {
             s0 = mfma16x16x32(k0, qlo[j], s0);
             s1 = mfma16x16x32(k1, qlo[j], s1);
         }
@@ -766,7 +765,7 @@ constexpr int decode_min_waves() {
     return KF == CQKV_FMT_MXFP4 && VF == CQKV_FMT_MXFP4 && D < 256 ? (D == 128 ? 3 : 4) : 1;
 }
 
-template <int KF, int VF, int D, int WAVES, bool TERMS>
+template <int KF, int VF, int D, int WAVES, bool TERMS, bool QS>
 __global__ __launch_bounds__(WAVES * 64)
 __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_kernel(DecodeArgs a) {
     constexpr int NCH = D / 32;
@@ -944,7 +943,6 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
         for (int i = threadIdx.x; i < kProdTabWords; i += NT)
             sm_vtab[i] = pack_f16x2(a.vcent[(i >> 5) & 7], a.vcent[(i >> 9) & 7]);
     }
-    const bool q_split = a.q_split != 0;
     __syncthreads();
     if constexpr (kTurbo) {  // entry (b, l) at word 64 b + l: code pair (b & 15, b >> 4)
         for (int i = threadIdx.x; i < 256 * 64; i += NT)
@@ -983,14 +981,14 @@ __attribute__((amdgpu_waves_per_eu(decode_min_waves<KF, VF, D>()))) void decode_
     load_tile<KF, VF, D>(tb2, t + WAVES, t + WAVES < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
     __builtin_amdgcn_sched_barrier(0);
     for (; t < te; t += 2 * WAVES) {
-        compute_tile<KF, VF, D, TERMS>(ta, t, a, qhi, qlo, q_split, lane, lo, hi, lo_max, hi_min, Lb,
+        compute_tile<KF, VF, D, TERMS, QS>(ta, t, a, qhi, qlo, lane, lo, hi, lo_max, hi_min, Lb,
                                        koff, tab, m_run, l_run, acc, kProd ? qsop : qhi, ktab, vtab,
                                        slope2, qpos, kscale2, e_run);
         __builtin_amdgcn_sched_barrier(0);
         load_tile<KF, VF, D>(ta, t + 2 * WAVES, t + 2 * WAVES < te, lane, kr, ksr, vr, vsr, ktok_off, vtok_off);
         __builtin_amdgcn_sched_barrier(0);
         if (t + WAVES < te)
-            compute_tile<KF, VF, D, TERMS>(tb2, t + WAVES, a, qhi, qlo, q_split, lane, lo, hi, lo_max,
+            compute_tile<KF, VF, D, TERMS, QS>(tb2, t + WAVES, a, qhi, qlo, lane, lo, hi, lo_max,
                                            hi_min, Lb, koff, tab, m_run, l_run, acc,
                                            kProd ? qsop : qhi, ktab, vtab, slope2, qpos, kscale2, e_run);
         __builtin_amdgcn_sched_barrier(0);
@@ -1066,15 +1064,28 @@ constexpr int waves_of(int kf, int vf, int d = 128) {
 }
 
 // d: the plane row length (64, 128 or 256); terms: soft-capping or ALiBi (the TERMS kernels)
-template <int KF, int VF, bool TERMS>
-inline void launch_decode_kvt(int d, dim3 grid, hipStream_t st, const DecodeArgs &a) {
+template <int KF, int VF, bool TERMS, bool QS>
+inline void launch_decode_kvtq(int d, dim3 grid, hipStream_t st, const DecodeArgs &a) {
     constexpr int W = waves_of(KF, VF), W256 = waves_of(KF, VF, 256);
     if (d == 64)
-        hipLaunchKernelGGL((decode_kernel<KF, VF, 64, W, TERMS>), grid, dim3(W * 64), 0, st, a);
+        hipLaunchKernelGGL((decode_kernel<KF, VF, 64, W, TERMS, QS>), grid, dim3(W * 64), 0, st, a);
     else if (d == 128)
-        hipLaunchKernelGGL((decode_kernel<KF, VF, 128, W, TERMS>), grid, dim3(W * 64), 0, st, a);
+        hipLaunchKernelGGL((decode_kernel<KF, VF, 128, W, TERMS, QS>), grid, dim3(W * 64), 0, st, a);
     else
-        hipLaunchKernelGGL((decode_kernel<KF, VF, 256, W256, TERMS>), grid, dim3(W256 * 64), 0, st, a);
+        hipLaunchKernelGGL((decode_kernel<KF, VF, 256, W256, TERMS, QS>), grid, dim3(W256 * 64), 0, st, a);
+}
+// Queries with a lo part (f32 or rotated queries over non-TurboQuant keys; TurboQuant keys take
+// one f16 query operand) get their own kernels, so the common bf16-query kernels have no branch
+// inside the key products.
+template <int KF, int VF, bool TERMS>
+inline void launch_decode_kvt(int d, dim3 grid, hipStream_t st, const DecodeArgs &a) {
+    if constexpr (!turbo_mse<KF>() && !is_prod<KF>()) {
+        if (a.q_split) {
+            launch_decode_kvtq<KF, VF, TERMS, true>(d, grid, st, a);
+            return;
+        }
+    }
+    launch_decode_kvtq<KF, VF, TERMS, false>(d, grid, st, a);
 }
 template <int KF, int VF>
 inline void launch_decode_kv(int d, dim3 grid, hipStream_t st, const DecodeArgs &a) {
