@@ -43,7 +43,7 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 constexpr int kPfD = 128;          // head dim of the fused FP8 append and the E4M3 K / V path
 constexpr int kPfBQ = 64;          // queries per workgroup (two wavefronts of 32 per head)
-constexpr int kPfBK = 64;          // keys per tile
+constexpr int kPfBK = 64;          // keys per tile of the pre-pass and of the attention at D <= 128
 
 struct PrefillArgs {
     const uint16_t *q, *k, *v;
@@ -144,27 +144,48 @@ __device__ inline void pf_key_range(int i, int lq, int lk, int wl, int wr, int &
 // reads are conflict-free.
 template <int D>
 __device__ inline int swz(int r) {
-    if constexpr (D == 128) return ((r & 7) << 1) | ((r >> 3) & 1);
+    if constexpr (D >= 128) return ((r & 7) << 1) | ((r >> 3) & 1);  // rows of 16 or 32 chunks
     else return (r >> 1) & 7;
 }
-// V^T tile layout in LDS: 128 rows (head dims) x 128 B (64 keys); the 16-byte chunk j (8 keys) of
-// row d sits at position j ^ swz_vt(d). Over any 16 consecutive rows, (d % 2, position) takes 16
-// distinct values, so a ds_read_b128 of one chunk across 16 rows is conflict-free.
-__device__ inline int swz_vt(int d) { return (d >> 1) & 7; }
-constexpr int kPfVtRow = 128;
-constexpr int kPfWaves = 8;               // 4 query heads x 2 halves of the 64 queries
-// Per head dim: 16-dim k-steps of S = K Q^T, 32-dim blocks of O^T, bytes of a K row and tile, of a
-// V^T tile (D rows of 64 keys), and each wavefront's 1 KB copies of a tile: K rows 8 w .. 8 w + 7,
-// V^T rows (D / 8) w .. in pieces of 8 rows. The V^T stages follow the four K stages in LDS:
-// VBIAS shifts V^T read offsets so that (stage - VBIAS) + block offset fits the 16-bit DS offset.
+// V^T tile layout in LDS: D rows (head dims) x VTROW bytes (keys of the tile); the 16-byte chunk j
+// (8 keys) of row d sits at position j ^ swz_vt(d). With 128-byte rows, over any 16 consecutive
+// rows (d % 2, position) takes 16 distinct values; with 64-byte rows, (d % 4, position) does: a
+// ds_read_b128 of one chunk across 16 rows is conflict-free either way.
+template <int VTROW>
+__device__ inline int swz_vt(int d) {
+    if constexpr (VTROW == 128) return (d >> 1) & 7;
+    else return (d >> 2) & 3;
+}
+// Per head dim:
+//  * the workgroup: W wavefronts, W / 2 query heads x 2 halves of the 64 queries (8 at D <= 128,
+//    two per SIMD; 4 at D = 256, one per SIMD with VGPRs and AGPRs, as the 32 x 256 accumulator,
+//    the queries and the scores take more than 256 registers);
+//  * key tiles of BK keys (64; 32 at D = 256, so that four ring stages of K and V^T fit in LDS):
+//    MB 32-key blocks of S, KK 16-key steps of O^T += V^T P^T;
+//  * 16-dim k-steps of S = K Q^T, 32-dim blocks of O^T, bytes of a K row and tile, of a V^T row
+//    (BK keys) and tile, and each wavefront's 1 KB copies of a tile: K rows (BK / W) w .., V^T rows
+//    (D / W) w .. in pieces of 1024 / VTROW rows.
+//  * The V^T stages follow the four K stages in LDS: VBIAS shifts V^T read offsets so that
+//    (stage - VBIAS) + block offset fits the 16-bit DS offset.
+//  * VALU instructions per MFMA of the two blocks of a tile step (scores: exponentials and
+//    conversions; then row sums, shift and row maximum).
 template <int D>
 struct PfGeom {
+    static constexpr int W = D == 256 ? 4 : 8;
+    static constexpr int BK = D == 256 ? 32 : 64, MB = BK / 32, KK = BK / 16, VTROW = 2 * BK;
     static constexpr int KS = D / 16, MD = D / 32;
-    static constexpr int ROW = 2 * D, KTILE = kPfBK * ROW, VTILE = D * kPfVtRow;
+    static constexpr int ROW = 2 * D, KTILE = BK * ROW, VTILE = D * VTROW;
     static constexpr int RPC = 1024 / ROW;  // K rows per copy
-    static constexpr int KCP = KTILE / 1024 / kPfWaves, VCP = VTILE / 1024 / kPfWaves;
+    static constexpr int KCP = KTILE / 1024 / W, VCP = VTILE / 1024 / W;
     static constexpr int CP = KCP + VCP;    // copies per wavefront and tile
     static constexpr uint32_t VBIAS = 4 * KTILE;
+    static constexpr int NM = MB * KS;      // MFMAs per block (S(t + 1); O^T += V^T P^T)
+    static constexpr int V1 = (24 * MB + NM - 1) / NM, V2 = (32 * MB + NM - 1) / NM;
+    // D = 256: the queries enter the MFMA as given and the scores are scaled in f32 (the shift
+    // becomes one FMA); with sums over 256 dims the rounding of pre-scaled queries to the dtype
+    // moved outputs by up to 3 bf16 ulps
+    static constexpr bool QRAW = D == 256;
+    static_assert(NM == MD * KK, "both blocks of a step have NM products");
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -194,19 +215,20 @@ PF_INLINE void pf_issue_tile(uint8_t *kstage, uint8_t *vstage, const uint16_t *k
                              const uint32_t *koff, const uint32_t *voff, int kt, int kv_len,
                              int wave, bool valid) {
     using G = PfGeom<D>;
-    const int row0 = valid ? kt * kPfBK : 0;
-    const int nvalid = min(kPfBK, kv_len - row0);
+    const int row0 = valid ? kt * G::BK : 0;
+    const int nvalid = min(G::BK, kv_len - row0);
     const rsrc_t kr = pf_rsrc(kplane + (int64_t)row0 * k_st,
                               valid ? (uint32_t)((int64_t)(nvalid - 1) * k_st * 2 + G::ROW) : 0u);
 #pragma unroll
     for (int r = 0; r < G::KCP; ++r)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            kr, (lds_void *)(kstage + (8 * wave + G::RPC * r) * G::ROW), 16, koff[r], 0, 0, 0);
+            kr, (lds_void *)(kstage + ((G::BK / G::W) * wave + G::RPC * r) * G::ROW), 16, koff[r], 0, 0, 0);
     const rsrc_t vr = pf_rsrc(vtplane + row0, valid ? (uint32_t)(((int64_t)D * vt_len - row0) * 2) : 0u);
 #pragma unroll
     for (int r8 = 0; r8 < G::VCP; ++r8)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            vr, (lds_void *)(vstage + ((D / 8) * wave + 8 * r8) * kPfVtRow), 16, voff[r8], 0, 0, 0);
+            vr, (lds_void *)(vstage + ((D / G::W) * wave + (1024 / G::VTROW) * r8) * G::VTROW), 16,
+            voff[r8], 0, 0, 0);
 }
 // byte offsets of this lane's copy sources from a tile's first K row / first V^T key
 template <int D>
@@ -216,13 +238,14 @@ PF_INLINE void pf_copy_offsets(uint32_t *koff, uint32_t *voff, int64_t k_st, int
     constexpr int CPR = G::ROW / 16;  // 16-byte chunks per K row
 #pragma unroll
     for (int r = 0; r < G::KCP; ++r) {
-        const int row = 8 * wave + G::RPC * r + lane / CPR;
+        const int row = (G::BK / G::W) * wave + G::RPC * r + lane / CPR;
         koff[r] = (uint32_t)(((int64_t)row * k_st + 8 * ((lane % CPR) ^ swz<D>(row))) * 2);
     }
+    constexpr int VCPR = G::VTROW / 16;  // 16-byte chunks per V^T row
 #pragma unroll
     for (int r8 = 0; r8 < G::VCP; ++r8) {
-        const int d = (D / 8) * wave + 8 * r8 + (lane >> 3);
-        voff[r8] = (uint32_t)(((int64_t)d * vt_len + 8 * ((lane & 7) ^ swz_vt(d))) * 2);
+        const int d = (D / G::W) * wave + (1024 / G::VTROW) * r8 + lane / VCPR;
+        voff[r8] = (uint32_t)(((int64_t)d * vt_len + 8 * ((lane % VCPR) ^ swz_vt<G::VTROW>(d))) * 2);
     }
 }
 
@@ -235,6 +258,8 @@ struct PfState {
     f32x16 acc[D / 32]; // O^T: 32-dim block md
     float negm;      // -m_run (0 before the first key), added to the raw scores
     float m_run, l_run;
+    float c2;        // scores' factor when the queries enter unscaled (QRAW): scale * log2(e)
+    float mraw;      // the mask value of unscaled scores: -inf times the sign of c2
     float thr;       // the row maximum moves when a tile's maximum exceeds thr: -inf before the
                      // row's first key, then 8 (p stays below 2^8)
     int qlo, qhi;    // visible keys of this lane's query
@@ -265,8 +290,8 @@ PF_INLINE void pf_block_schedule() {
 // (stage, offset) pair.
 template <int D>
 struct PfAddr {
-    uint32_t k[D / 16];  // K row qr, chunk 2 ks + h (swizzled), of key block 0
-    uint32_t v[4];       // VBIAS + V^T row qr, chunk 2 kk + h (swizzled), of head-dim block 0
+    uint32_t k[D / 16];           // K row qr, chunk 2 ks + h (swizzled), of key block 0
+    uint32_t v[PfGeom<D>::KK];    // VBIAS + V^T row qr, chunk 2 kk + h (swizzled), of head-dim block 0
 };
 // The V^T stages follow the four K stages; biasing the V^T offsets by their size (64 KB at
 // D = 128) leaves (stage address - bias) + head-dim block offset, below 64 KB, as the constant
@@ -278,37 +303,38 @@ PF_INLINE void pf_addr_init(PfAddr<D> &ad, int lane) {
     for (int ks = 0; ks < D / 16; ++ks)
         ad.k[ks] = qr * PfGeom<D>::ROW + (((2 * ks + h) ^ swz<D>(qr)) << 4);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-        ad.v[kk] = PfGeom<D>::VBIAS + qr * kPfVtRow + (((2 * kk + h) ^ swz_vt(qr)) << 4);
+    for (int kk = 0; kk < PfGeom<D>::KK; ++kk)
+        ad.v[kk] = PfGeom<D>::VBIAS + qr * PfGeom<D>::VTROW +
+                   (((2 * kk + h) ^ swz_vt<PfGeom<D>::VTROW>(qr)) << 4);
 }
 template <int D>
 PF_INLINE void pf_addr_opaque(PfAddr<D> &ad) {
 #pragma unroll
     for (int i = 0; i < D / 16; ++i) asm volatile("" : "+v"(ad.k[i]));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(ad.v[i]));
+    for (int i = 0; i < PfGeom<D>::KK; ++i) asm volatile("" : "+v"(ad.v[i]));
 }
 
-// S^T (64 keys x 32 queries) = K Q^T for the tile at k_lds.
+// S^T (BK keys x 32 queries) = K Q^T for the tile at k_lds: MB 32-key blocks.
 template <bool F16, int D>
-PF_INLINE void pf_qk(f32x16 (&s)[2], const PfState<D> &st, const uint8_t *k_lds, const PfAddr<D> &ad) {
+PF_INLINE void pf_qk(f32x16 *s, const PfState<D> &st, const uint8_t *k_lds, const PfAddr<D> &ad) {
     using op_t = pf_op_t<F16>;
-    constexpr int KS = D / 16;
-    op_t kop[2 * KS];
+    constexpr int KS = D / 16, MB = PfGeom<D>::MB;
+    op_t kop[MB * KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
+        for (int mb = 0; mb < MB; ++mb)
             kop[KS * mb + ks] = __builtin_bit_cast(
                 op_t, *(const u32x4 *)(k_lds + ad.k[ks] + 32 * mb * PfGeom<D>::ROW));
-    // the two key blocks' chains alternate, so consecutive products are independent
+    // with two key blocks their chains alternate, so consecutive products are independent
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int mb = 0; mb < MB; ++mb)
         s[mb] = mfma32x32x16(kop[KS * mb], __builtin_bit_cast(op_t, st.qop[0]), f32x16{});
 #pragma unroll
     for (int ks = 1; ks < KS; ++ks)
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
+        for (int mb = 0; mb < MB; ++mb)
             s[mb] = mfma32x32x16(kop[KS * mb + ks], __builtin_bit_cast(op_t, st.qop[ks]), s[mb]);
 }
 
@@ -324,11 +350,12 @@ struct PfLogit {
 };
 // cap * tanh(x / cap) = cap - 2 cap / (e^(2x / cap) + 1): one exp2 and one reciprocal, exact
 // limits at both ends (e -> inf: cap; e -> 0: -cap), absolute error ~1e-7 cap
-PF_INLINE void pf_logit(f32x16 (&s)[2], const PfLogit &lg, int k0, int lane) {
+template <int MB>
+PF_INLINE void pf_logit(f32x16 *s, const PfLogit &lg, int k0, int lane) {
     if (lg.cap2 > 0.0f) {
         const float two_cap = 2.0f * lg.cap2;
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
+        for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
                 const float e = __builtin_amdgcn_exp2f(s[mb][j] * lg.e2);
@@ -338,7 +365,7 @@ PF_INLINE void pf_logit(f32x16 (&s)[2], const PfLogit &lg, int k0, int lane) {
     if (lg.slope2 != 0.0f) {
         const int d0 = lg.pos - (k0 + 4 * (lane >> 5));  // pos - key of register 0
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
+        for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
                 const int dist = d0 - (32 * mb + 8 * (j >> 2) + (j & 3));
@@ -349,17 +376,18 @@ PF_INLINE void pf_logit(f32x16 (&s)[2], const PfLogit &lg, int k0, int lane) {
 
 // masks scores of keys outside the lane's visible range (tiles that cross a range end only)
 template <int D>
-PF_INLINE void pf_mask(f32x16 (&s)[2], const PfState<D> &st, int k0, int lane) {
+PF_INLINE void pf_mask(f32x16 *s, const PfState<D> &st, int k0, int lane,
+                       float mval = -__builtin_inff()) {
     const int h = lane >> 5;
     // key - qlo of register 0, made opaque so the per-register offsets stay immediates
     int u = k0 + 4 * h - st.qlo;
     asm volatile("" : "+v"(u));
     const uint32_t w = (uint32_t)(st.qhi - st.qlo);
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int mb = 0; mb < PfGeom<D>::MB; ++mb)
 #pragma unroll
         for (int j = 0; j < 16; ++j)
-            if ((uint32_t)(u + 32 * mb + 8 * (j >> 2) + (j & 3)) >= w) s[mb][j] = -__builtin_inff();
+            if ((uint32_t)(u + 32 * mb + 8 * (j >> 2) + (j & 3)) >= w) s[mb][j] = mval;
 }
 
 PF_INLINE float pf_max_halves(float x) {  // max of lanes l and l ^ 32
@@ -372,35 +400,63 @@ PF_INLINE float pf_sum_halves(float x) {  // sum of lanes l and l ^ 32
 }
 
 // scores relative to the running maximum
-PF_INLINE void pf_shift(f32x16 (&s)[2], float negm) {
+template <int MB>
+PF_INLINE void pf_scale(f32x16 *s, float c) {
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s[mb][j] *= c;
+}
+// unscaled scores to the exponent: s * c - m_run, one FMA each
+template <int MB>
+PF_INLINE void pf_shift_scaled(f32x16 *s, float c, float negm) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s[mb][j] = __builtin_fmaf(s[mb][j], c, negm);
+}
+template <int MB>
+PF_INLINE void pf_shift(f32x16 *s, float negm) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int j = 0; j < 16; ++j) s[mb][j] += negm;
 }
 
-// this lane's maximum over the tile (two chains, block 0 first)
-PF_INLINE float pf_rowmax(const f32x16 (&s)[2]) {
-    float m0 = s[0][0], m1 = s[1][0];
+// this lane's maximum over the tile (two chains: the two key blocks, or the even and odd
+// registers of one)
+template <int MB>
+PF_INLINE float pf_rowmax(const f32x16 *s) {
+    if constexpr (MB == 2) {
+        float m0 = s[0][0], m1 = s[1][0];
 #pragma unroll
-    for (int j = 1; j < 16; ++j) {
-        m0 = fmaxf(m0, s[0][j]);
-        m1 = fmaxf(m1, s[1][j]);
+        for (int j = 1; j < 16; ++j) {
+            m0 = fmaxf(m0, s[0][j]);
+            m1 = fmaxf(m1, s[1][j]);
+        }
+        return fmaxf(m0, m1);
+    } else {
+        float m0 = s[0][0], m1 = s[0][1];
+#pragma unroll
+        for (int j = 2; j < 16; j += 2) {
+            m0 = fmaxf(m0, s[0][j]);
+            m1 = fmaxf(m1, s[0][j + 1]);
+        }
+        return fmaxf(m0, m1);
     }
-    return fmaxf(m0, m1);
 }
 
 // The row maximum moves (rare): s is shifted to the new maximum, O and the row sum rescaled.
 // Q carries scale * log2(e) and pf_shift adds -m_run, so s is the exponent of p = exp2(s)
 // relative to m_run.
 template <int D>
-PF_INLINE void pf_rescale(f32x16 (&s)[2], PfState<D> &st, float mx, bool need) {
+PF_INLINE void pf_rescale(f32x16 *s, PfState<D> &st, float mx, bool need) {
     const bool fresh = st.m_run == -__builtin_inff();
     const float shift = need ? mx : 0.0f;
     const float m_new = need ? (fresh ? 0.0f : st.m_run) + mx : st.m_run;
     const float alpha = need ? __builtin_amdgcn_exp2f(st.m_run - m_new) : 1.0f;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int mb = 0; mb < PfGeom<D>::MB; ++mb)
 #pragma unroll
         for (int j = 0; j < 16; ++j) s[mb][j] -= shift;
 #pragma unroll
@@ -412,10 +468,10 @@ PF_INLINE void pf_rescale(f32x16 (&s)[2], PfState<D> &st, float mx, bool need) {
 }
 
 // p = exp2(s), packed to the P^T operands of the dtype (raw bits)
-template <bool F16>
-PF_INLINE void pf_exp(u32x4 (&pop)[4], const f32x16 (&s)[2]) {
+template <bool F16, int MB>
+PF_INLINE void pf_exp(u32x4 *pop, const f32x16 *s) {
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
             uint32_t w[4];
@@ -449,10 +505,10 @@ PF_INLINE float pf_dot2_ones(uint32_t w, float acc) {
     }
 }
 template <bool F16, int D>
-PF_INLINE void pf_psum(PfState<D> &st, const u32x4 (&pop)[4]) {
+PF_INLINE void pf_psum(PfState<D> &st, const u32x4 *pop) {
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2 * PfGeom<D>::MB; ++i) {
         const u32x4 w = pop[i];
         const uint32_t w0 = w.x, w1 = w.y, w2 = w.z, w3 = w.w;
         a0 = pf_dot2_ones<F16>(w0, a0);
@@ -468,18 +524,18 @@ PF_INLINE void pf_psum(PfState<D> &st, const u32x4 (&pop)[4]) {
 // 16 kk + 8 (e / 4) + 4 h + e % 4 in k-slot 8 h + e; the pre-pass stores V^T keys in that order
 // (bits 2 and 3 of the key swapped), so the A operand of lane (d, h) is chunk 2 kk + h of row d.
 template <bool F16, int D>
-PF_INLINE void pf_pv(PfState<D> &st, const u32x4 (&pop)[4], const uint8_t *v_lds, const PfAddr<D> &ad) {
+PF_INLINE void pf_pv(PfState<D> &st, const u32x4 *pop, const uint8_t *v_lds, const PfAddr<D> &ad) {
     using op_t = pf_op_t<F16>;
-    constexpr int MD = D / 32;
-    op_t vt[4 * MD];
+    constexpr int MD = D / 32, KK = PfGeom<D>::KK;
+    op_t vt[KK * MD];
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
+    for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
         for (int md = 0; md < MD; ++md)
             vt[MD * kk + md] = __builtin_bit_cast(
-                op_t, *(const u32x4 *)(v_lds + (ad.v[kk] - PfGeom<D>::VBIAS) + md * 32 * kPfVtRow));
+                op_t, *(const u32x4 *)(v_lds + (ad.v[kk] - PfGeom<D>::VBIAS) + md * 32 * PfGeom<D>::VTROW));
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
+    for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
         for (int md = 0; md < MD; ++md)
             st.acc[md] = mfma32x32x16(vt[MD * kk + md], __builtin_bit_cast(op_t, pop[kk]), st.acc[md]);
@@ -496,25 +552,31 @@ PF_INLINE void pf_pv(PfState<D> &st, const u32x4 (&pop)[4], const uint8_t *v_lds
 // At D = 64 each block has half the MFMAs of D = 128 for the same softmax work: twice the VALU
 // instructions go between consecutive MFMAs.
 template <bool LOGIT, bool F16, int D, typename IssueCopies>
-PF_INLINE void pf_tile(f32x16 (&cur)[2], f32x16 (&nxt)[2], u32x4 (&pop)[4], PfState<D> &st,
+PF_INLINE void pf_tile(f32x16 *cur, f32x16 *nxt, u32x4 *pop, PfState<D> &st,
                        const uint8_t *k_next, const uint8_t *v_cur, const PfAddr<D> &ad,
                        bool masked, int k1, int lane, const PfLogit &lg, IssueCopies &&issue_copies) {
-    constexpr int NM = D / 8, R = 128 / D;  // MFMAs per block, VALU ratio to D = 128
+    using G = PfGeom<D>;
+    constexpr int NM = G::NM;  // MFMAs per block
     pf_qk<F16, D>(nxt, st, k_next, ad);
-    pf_exp<F16>(pop, cur);
-    pf_block_schedule<3 * R, 0, NM>();
+    pf_exp<F16, G::MB>(pop, cur);
+    pf_block_schedule<G::V1, 0, NM>();
     __builtin_amdgcn_sched_barrier(0);
     // P(t) is used only after the branch below: pin its computation to block 1
 #pragma unroll
-    for (int i = 0; i < 4; ++i) asm volatile("" ::"v"(pop[i]));
-    if (LOGIT) pf_logit(nxt, lg, k1, lane);
-    if (masked) pf_mask(nxt, st, k1, lane);
+    for (int i = 0; i < 2 * G::MB; ++i) asm volatile("" ::"v"(pop[i]));
+    if (LOGIT) {
+        if constexpr (G::QRAW) pf_scale<G::MB>(nxt, st.c2);
+        pf_logit<G::MB>(nxt, lg, k1, lane);
+    }
+    // (unscaled scores of the QRAW form take the mask value that their scaling turns into -inf)
+    if (masked) pf_mask(nxt, st, k1, lane, G::QRAW && !LOGIT ? st.mraw : -__builtin_inff());
     issue_copies();
     pf_pv<F16, D>(st, pop, v_cur, ad);
     pf_psum<F16, D>(st, pop);
-    pf_shift(nxt, st.negm);
-    float mx = pf_rowmax(nxt);
-    pf_block_schedule<4 * R, PfGeom<D>::CP, NM>();
+    if (G::QRAW && !LOGIT) pf_shift_scaled<G::MB>(nxt, st.c2, st.negm);
+    else pf_shift<G::MB>(nxt, st.negm);
+    float mx = pf_rowmax<G::MB>(nxt);
+    pf_block_schedule<G::V2, G::CP, NM>();
     __builtin_amdgcn_sched_barrier(0);
     mx = pf_max_halves(mx);
     const bool need = mx > st.thr;
@@ -523,18 +585,18 @@ PF_INLINE void pf_tile(f32x16 (&cur)[2], f32x16 (&nxt)[2], u32x4 (&pop)[4], PfSt
 
 // The last key tile: P(t) and O += V(t)^T P(t).
 template <bool F16, int D>
-PF_INLINE void pf_last_tile(const f32x16 (&cur)[2], u32x4 (&pop)[4], PfState<D> &st,
+PF_INLINE void pf_last_tile(const f32x16 *cur, u32x4 *pop, PfState<D> &st,
                             const uint8_t *v_cur, const PfAddr<D> &ad) {
-    pf_exp<F16>(pop, cur);
+    pf_exp<F16, PfGeom<D>::MB>(pop, cur);
     pf_pv<F16, D>(st, pop, v_cur, ad);
     pf_psum<F16, D>(st, pop);
-    pf_block_schedule<128 / D, 0, D / 8>();
+    pf_block_schedule<(D == 256 ? PfGeom<D>::V1 : 128 / D), 0, PfGeom<D>::NM>();
 }
 
 // Two wavefronts per SIMD (8 per workgroup, ~240 registers each at D = 128).
 // LOGIT: soft-capping and / or ALiBi (a separate instantiation keeps them off the plain path)
 template <bool LOGIT, bool F16, int D>
-__global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(PfGeom<D>::W * 64, 1) void prefill_kernel(PrefillArgs a) {
     using G = PfGeom<D>;
     // the K and V^T rings: four stages each, as distinct arrays named statically below, so the
     // compiler can tell the asynchronous copy into one stage from the reads of another (a
@@ -564,7 +626,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     const int b = plane / (a.kv_heads * hgroups);
     const int rem = plane % (a.kv_heads * hgroups);
     const int hk = rem % a.kv_heads, hgrp = rem / a.kv_heads;
-    const int hslot = wave & 3, qhalf = wave >> 2;
+    const int hslot = wave % (G::W / 2), qhalf = wave / (G::W / 2);
     const int head = hk * a.group + hgrp * a.heads_per_wg + hslot;
     const bool wave_live = hslot < a.heads_per_wg && hgrp * a.heads_per_wg + hslot < a.group;
     const int q0 = qb * kPfBQ;
@@ -575,8 +637,8 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     int lo_first, hi_first, lo_last, hi_last;
     pf_key_range(q0, lq, lk, a.wl, a.wr, lo_first, hi_first);
     pf_key_range(min(q0 + kPfBQ, lq) - 1, lq, lk, a.wl, a.wr, lo_last, hi_last);
-    const int kt_begin = lo_first / kPfBK;
-    const int ntiles = (hi_last + kPfBK - 1) / kPfBK - kt_begin;
+    const int kt_begin = lo_first / G::BK;
+    const int ntiles = (hi_last + G::BK - 1) / G::BK - kt_begin;
 
     PfState<D> st;
     {
@@ -585,12 +647,15 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
         const uint16_t *row = a.q + sq.q0 + (int64_t)min(head, a.q_heads - 1) * a.q_sh +
                               (int64_t)min(qi, lq - 1) * a.q_st;
         const float qs = a.scale_log2 * a.q_mul * (a.q_mul_dev ? a.q_mul_dev[0] : 1.0f);
+        // (QRAW: a zero factor is made the smallest normal one, so masked scores stay -inf)
+        st.c2 = qs == 0.0f ? 1.17549435e-38f : qs;
+        st.mraw = st.c2 > 0.0f ? -__builtin_inff() : __builtin_inff();
 #pragma unroll
         for (int ks = 0; ks < G::KS; ++ks) {
             u32x4 w = ok ? ldg128(row + 16 * ks + 8 * h) : u32x4{0u, 0u, 0u, 0u};
             // q * scale * log2(e) (* k_descale), rounded to the dtype
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
+            for (int e = 0; e < 4 && !G::QRAW; ++e) {
                 if constexpr (F16)
                     w[e] = pack_f16x2(f16_bits_to_f32(w[e] & 0xffffu) * qs,
                                       f16_bits_to_f32(w[e] >> 16) * qs);
@@ -661,19 +726,23 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
     }
 
     const auto tile_masked = [&](int kt) {
-        const int k0 = (kt_begin + kt) * kPfBK;
-        return !(k0 >= lo_last && k0 + kPfBK <= hi_first);
+        const int k0 = (kt_begin + kt) * G::BK;
+        return !(k0 >= lo_last && k0 + G::BK <= hi_first);
     };
-    f32x16 sa[2], sb[2];
-    u32x4 pop[4];
+    f32x16 sa[G::MB], sb[G::MB];
+    u32x4 pop[2 * G::MB];
     PfAddr<D> ad;
     pf_addr_init<D>(ad, lane);
     if (ntiles > 0) {
         pf_qk<F16, D>(sa, st, ks0, ad);
-        if (LOGIT) pf_logit(sa, lg, kt_begin * kPfBK, lane);
-        pf_shift(sa, st.negm);
-        if (tile_masked(0)) pf_mask(sa, st, kt_begin * kPfBK, lane);
-        const float mx = pf_max_halves(pf_rowmax(sa));
+        if (LOGIT) {
+            if constexpr (G::QRAW) pf_scale<G::MB>(sa, st.c2);
+            pf_logit<G::MB>(sa, lg, kt_begin * G::BK, lane);
+        }
+        if (G::QRAW && !LOGIT) pf_shift_scaled<G::MB>(sa, st.c2, st.negm);
+        else pf_shift<G::MB>(sa, st.negm);
+        if (tile_masked(0)) pf_mask(sa, st, kt_begin * G::BK, lane);
+        const float mx = pf_max_halves(pf_rowmax<G::MB>(sa));
         const bool need = mx > st.thr;
         if (__any(need)) pf_rescale(sa, st, mx, need);
     }
@@ -689,7 +758,7 @@ __global__ __launch_bounds__(kPfWaves * 64, 1) void prefill_kernel(PrefillArgs a
             break;                                                                           \
         }                                                                                    \
         pf_tile<LOGIT, F16, D>(CUR, NXT, pop, st, PF_KS(((k) + 1) & 3), PF_VS(k), ad,        \
-                       tile_masked(t + 1), (kt_begin + t + 1) * kPfBK, lane, lg, [&] {       \
+                       tile_masked(t + 1), (kt_begin + t + 1) * G::BK, lane, lg, [&] {       \
                     PF_ISSUE(((k) + 3) & 3, t + 3);                                          \
                 });                                                                          \
         ++t;                                                                                 \
@@ -917,11 +986,11 @@ namespace cqkv {
 
 // The whole prefill call; descales (q_mul / o_mul and their device factors) are those of the FP8
 // K / V path (fp8_attn.hip), 1 / null for bf16 K / V.
-// Whether a call takes the MFMA prefill kernel (bf16, head dim 128, more than 16 queries);
-// every other call runs the plain-dtype kernel of flash_plain.h.
+// Whether a call takes the MFMA prefill kernel (bf16 / f16, head dim 64, 128 or 256, more than 16
+// queries); every other call runs the plain-dtype kernel of flash_plain.h.
 static bool pf_fast_path(int32_t dtype, int32_t head_dim, int32_t q_len) {
-    return (dtype == CQKV_BF16 || dtype == CQKV_F16) && (head_dim == 128 || head_dim == 64) &&
-           q_len > 16;
+    return (dtype == CQKV_BF16 || dtype == CQKV_F16) &&
+           (head_dim == 128 || head_dim == 64 || head_dim == 256) && q_len > 16;
 }
 
 // V^T scratch of the MFMA prefill: (batch, kv heads, D, kv_len rounded up to the key tile) bf16.
@@ -966,7 +1035,7 @@ size_t flash_attn_workspace(int32_t dtype, int32_t batch, int32_t q_len, int32_t
 
 template <int D>
 static void pf_launch(bool f16, bool terms, dim3 grid, hipStream_t st, const PrefillArgs &a) {
-    const dim3 block(kPfWaves * 64);
+    const dim3 block(PfGeom<D>::W * 64);
     if (f16) {
         if (terms) hipLaunchKernelGGL((prefill_kernel<true, true, D>), grid, block, 0, st, a);
         else hipLaunchKernelGGL((prefill_kernel<false, true, D>), grid, block, 0, st, a);
@@ -1138,7 +1207,8 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
     a.q_heads = q_heads;
     a.kv_heads = kv_heads;
     a.group = q_heads / kv_heads;
-    a.heads_per_wg = a.group < 4 ? a.group : 4;
+    const int hpw = head_dim == 256 ? PfGeom<256>::W / 2 : PfGeom<128>::W / 2;  // heads per workgroup
+    a.heads_per_wg = a.group < hpw ? a.group : hpw;
     a.q_blocks = (q_len + kPfBQ - 1) / kPfBQ;
     a.wl = window_left;
     a.wr = window_right;
@@ -1207,10 +1277,12 @@ int flash_attn_impl(const void *q, const int64_t q_strides[3], const void *k,
     }
     const dim3 sgrid(a.vt_len / kPfBK, kv_heads, batch);
     if (head_dim == 64) hipLaunchKernelGGL(prefill_stage_kernel<64>, sgrid, dim3(256), 0, st, a);
+    else if (head_dim == 256) hipLaunchKernelGGL(prefill_stage_kernel<256>, sgrid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL(prefill_stage_kernel<128>, sgrid, dim3(256), 0, st, a);
     const dim3 grid(a.q_blocks * kv_heads * ((a.group + a.heads_per_wg - 1) / a.heads_per_wg) * batch);
     const bool terms = softcap > 0.0f || alibi_slopes;
     if (head_dim == 64) pf_launch<64>(dtype == CQKV_F16, terms, grid, st, a);
+    else if (head_dim == 256) pf_launch<256>(dtype == CQKV_F16, terms, grid, st, a);
     else pf_launch<128>(dtype == CQKV_F16, terms, grid, st, a);
     hipError_t le = hipGetLastError();
     hipError_t fe = vt_owned ? hipFreeAsync(vt, st) : hipSuccess;

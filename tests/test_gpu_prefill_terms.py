@@ -35,8 +35,10 @@ def oracle_terms(q, k, v, scale, wl, wr, softcap=0.0, slopes=None):
 @pytest.mark.parametrize("softcap,per_batch,wl,wr", [(5.0, False, -1, 0), (0.0, False, -1, 0),
                                                      (2.0, True, 30, 0), (3.0, False, 40, 5),
                                                      (0.0, True, -1, -1)])
-def test_prefill_softcap_alibi(cq, dev, softcap, per_batch, wl, wr):
-    b, sq, sk, hq, hkv, d = 2, 150, 190, 8, 2, 128
+@pytest.mark.parametrize("d", [128, 256])
+def test_prefill_softcap_alibi(cq, dev, softcap, per_batch, wl, wr, d):
+    """D = 256 runs the MFMA prefill's 32-key-tile, four-wavefront form."""
+    b, sq, sk, hq, hkv = 2, 150, 190, 8, 2
     q = bf16_randn(31, (b, sq, hq, d), 3.0)  # large enough scores for tanh to bite
     k = bf16_randn(32, (b, sk, hkv, d))
     v = bf16_randn(33, (b, sk, hkv, d))
@@ -72,12 +74,13 @@ def varlen_inputs(seed, lens_q, lens_k, hq, hkv, d=128):
 
 @pytest.mark.parametrize("causal,wl,softcap,alibi", [(True, -1, 0.0, False), (False, -1, 0.0, False),
                                                      (True, 70, 0.0, False), (True, -1, 3.0, True)])
-def test_prefill_varlen(cq, dev, causal, wl, softcap, alibi):
+@pytest.mark.parametrize("d", [128, 256])
+def test_prefill_varlen(cq, dev, causal, wl, softcap, alibi, d):
     """Ragged sequences (an empty one, single-token ones, more queries than keys) against the
     oracle per sequence and against the dense call on each sequence."""
     lens_q = [100, 0, 1, 257, 64, 30]
     lens_k = [130, 60, 1, 257, 200, 20]
-    hq, hkv, d = 8, 2, 128
+    hq, hkv = 8, 2
     q, k, v, cu_q, cu_k = varlen_inputs(51, lens_q, lens_k, hq, hkv, d)
     slopes = (0.03 * (1 + torch.arange(hq, dtype=torch.float32))) if alibi else None
     scale = 1.0 / d ** 0.5
