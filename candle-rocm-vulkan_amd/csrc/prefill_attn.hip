@@ -181,6 +181,7 @@ struct PfGeom {
     static constexpr uint32_t VBIAS = 4 * KTILE;
     static constexpr int NM = MB * KS;      // MFMAs per block (S(t + 1); O^T += V^T P^T)
     static constexpr int V1 = (24 * MB + NM - 1) / NM, V2 = (32 * MB + NM - 1) / NM;
+    static constexpr int V2C = (16 * MB + NM - 1) / NM;  // block 2 when the MFMA adds -m_run
     // D = 256: the queries enter the MFMA as given and the scores are scaled in f32 (the shift
     // becomes one FMA); with sums over 256 dims the rounding of pre-scaled queries to the dtype
     // moved outputs by up to 3 bf16 ulps
@@ -257,6 +258,8 @@ struct PfState {
     u32x4 qop[D / 16];  // Q^T operands (16-dim steps ks) of this wavefront's 32 queries, raw bits
     f32x16 acc[D / 32]; // O^T: 32-dim block md
     float negm;      // -m_run (0 before the first key), added to the raw scores
+    f32x16 negv;     // negm in every register: the initial value of the score products when
+                     // the scores need no f32 scaling or terms before the shift
     float m_run, l_run;
     float c2;        // scores' factor when the queries enter unscaled (QRAW): scale * log2(e)
     float mraw;      // the mask value of unscaled scores: -inf times the sign of c2
@@ -317,7 +320,8 @@ PF_INLINE void pf_addr_opaque(PfAddr<D> &ad) {
 
 // S^T (BK keys x 32 queries) = K Q^T for the tile at k_lds: MB 32-key blocks.
 template <bool F16, int D>
-PF_INLINE void pf_qk(f32x16 *s, const PfState<D> &st, const uint8_t *k_lds, const PfAddr<D> &ad) {
+PF_INLINE void pf_qk(f32x16 *s, const PfState<D> &st, const uint8_t *k_lds, const PfAddr<D> &ad,
+                     const f32x16 &c0) {
     using op_t = pf_op_t<F16>;
     constexpr int KS = D / 16, MB = PfGeom<D>::MB;
     op_t kop[MB * KS];
@@ -330,7 +334,7 @@ PF_INLINE void pf_qk(f32x16 *s, const PfState<D> &st, const uint8_t *k_lds, cons
     // with two key blocks their chains alternate, so consecutive products are independent
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
-        s[mb] = mfma32x32x16(kop[KS * mb], __builtin_bit_cast(op_t, st.qop[0]), f32x16{});
+        s[mb] = mfma32x32x16(kop[KS * mb], __builtin_bit_cast(op_t, st.qop[0]), c0);
 #pragma unroll
     for (int ks = 1; ks < KS; ++ks)
 #pragma unroll
@@ -465,6 +469,8 @@ PF_INLINE void pf_rescale(f32x16 *s, PfState<D> &st, float mx, bool need) {
     st.m_run = m_new;
     st.thr = m_new == -__builtin_inff() ? -__builtin_inff() : 8.0f;
     st.negm -= shift;  // -m_new: 0 - mx for a row's first keys, -m_run - mx after
+#pragma unroll
+    for (int j = 0; j < 16; ++j) st.negv[j] = st.negm;
 }
 
 // p = exp2(s), packed to the P^T operands of the dtype (raw bits)
@@ -557,7 +563,10 @@ PF_INLINE void pf_tile(f32x16 *cur, f32x16 *nxt, u32x4 *pop, PfState<D> &st,
                        bool masked, int k1, int lane, const PfLogit &lg, IssueCopies &&issue_copies) {
     using G = PfGeom<D>;
     constexpr int NM = G::NM;  // MFMAs per block
-    pf_qk<F16, D>(nxt, st, k_next, ad);
+    // scores that need no f32 scaling or terms start from -m_run in the MFMA: no shift
+    constexpr bool CM = !G::QRAW && !LOGIT;
+    if constexpr (CM) pf_qk<F16, D>(nxt, st, k_next, ad, st.negv);
+    else pf_qk<F16, D>(nxt, st, k_next, ad, f32x16{});
     pf_exp<F16, G::MB>(pop, cur);
     pf_block_schedule<G::V1, 0, NM>();
     __builtin_amdgcn_sched_barrier(0);
@@ -574,9 +583,9 @@ PF_INLINE void pf_tile(f32x16 *cur, f32x16 *nxt, u32x4 *pop, PfState<D> &st,
     pf_pv<F16, D>(st, pop, v_cur, ad);
     pf_psum<F16, D>(st, pop);
     if (G::QRAW && !LOGIT) pf_shift_scaled<G::MB>(nxt, st.c2, st.negm);
-    else pf_shift<G::MB>(nxt, st.negm);
+    else if (!CM) pf_shift<G::MB>(nxt, st.negm);
     float mx = pf_rowmax<G::MB>(nxt);
-    pf_block_schedule<G::V2, G::CP, NM>();
+    pf_block_schedule<CM ? G::V2C : G::V2, G::CP, NM>();
     __builtin_amdgcn_sched_barrier(0);
     mx = pf_max_halves(mx);
     const bool need = mx > st.thr;
@@ -671,6 +680,7 @@ __global__ __launch_bounds__(PfGeom<D>::W * 64, 1) void prefill_kernel(PrefillAr
         st.thr = -__builtin_inff();
         st.l_run = 0.0f;
         st.negm = 0.0f;
+        st.negv = f32x16{};
 #pragma unroll
         for (int md = 0; md < G::MD; ++md) st.acc[md] = f32x16{};
     }
@@ -734,7 +744,7 @@ __global__ __launch_bounds__(PfGeom<D>::W * 64, 1) void prefill_kernel(PrefillAr
     PfAddr<D> ad;
     pf_addr_init<D>(ad, lane);
     if (ntiles > 0) {
-        pf_qk<F16, D>(sa, st, ks0, ad);
+        pf_qk<F16, D>(sa, st, ks0, ad, f32x16{});  // (negm is 0 here)
         if (LOGIT) {
             if constexpr (G::QRAW) pf_scale<G::MB>(sa, st.c2);
             pf_logit<G::MB>(sa, lg, kt_begin * G::BK, lane);
