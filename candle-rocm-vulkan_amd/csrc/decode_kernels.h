@@ -675,7 +675,17 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
     } else if constexpr (VF == CQKV_FMT_MXFP4) {
         // value block u: P scaled by the keys' block-u scales, one bf16 operand (the E2M1 codes
         // and E8M0 scales are exact; P rounds to 8 significant bits, as in a bf16 flash
-        // attention). The scale of E8M0 code c is the float with exponent field c (code 0: 0).
+        // attention). E8M0 code c is the scale 2^(c - 127). Each key pair's P is rounded to bf16
+        // once, its exponent fields biased by -127; block u then adds the two keys' codes to the
+        // exponent fields (a byte permute, a packed multiply-add and a packed clamp per pair and
+        // block): the bits of rounding p * 2^(c - 127) wherever that is a normal bf16 number.
+        // Results below the normal range clamp to zero. P is floored at 2^-100 (masked keys, exp
+        // underflow), so no zero p meets a large code; such a key's operand stays below 2^-100
+        // times the row's largest, and a column with no visible key is dropped by the rescale
+        // (alpha 0) or the epilogue (m -inf). Code 0 marks an all-zero block: its zero codes
+        // make any operand vanish.
+        typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+        typedef short i16x2 __attribute__((ext_vector_type(2)));
         uint32_t vw[8], vw2[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -687,16 +697,29 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
             for (int e = 0; e < 8; ++e)
                 if (e >= nv) vw[e] = vw2[e] = 0u;
         }
+        u16x2 pb[4];  // bf16 P of keys 2i, 2i + 1, exponent fields minus 127
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // (the word made opaque: otherwise the compiler splits the pair conversion in two)
+            uint32_t w = pack_bf16x2(fmaxf(p[2 * i], 0x1p-100f), fmaxf(p[2 * i + 1], 0x1p-100f));
+            asm volatile("" : "+v"(w));
+            pb[i] = __builtin_bit_cast(u16x2, w) - u16x2{0x3f80, 0x3f80};
+        }
+        const uint32_t k128 = 0x00800080u;  // 128 in both halves: c << 7 by the multiply-add
 #pragma unroll
         for (int u = 0; u < NCH; ++u) {
             u32x4 pw;
             uint32_t *pwp = (uint32_t *)&pw;
+            // byte u % 4 of the even key's word into byte 0, of the odd key's into byte 2
+            const uint32_t sel = (uint32_t)(u & 3) | 0x0c00u | ((uint32_t)(4 + (u & 3)) << 16) | 0x0c000000u;
 #pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-                const uint32_t w0 = u < 4 ? vw[e] : vw2[e], w1 = u < 4 ? vw[e + 1] : vw2[e + 1];
-                const float s0 = __uint_as_float(((w0 >> (8 * (u & 3))) & 0xffu) << 23);
-                const float s1 = __uint_as_float(((w1 >> (8 * (u & 3))) & 0xffu) << 23);
-                pwp[e / 2] = pack_bf16x2(p[e] * s0, p[e + 1] * s1);
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t w0 = u < 4 ? vw[2 * i] : vw2[2 * i];
+                const uint32_t w1 = u < 4 ? vw[2 * i + 1] : vw2[2 * i + 1];
+                const uint32_t c = __builtin_amdgcn_perm(w1, w0, sel);
+                uint32_t r;  // c * 128 + pb per half, one v_pk_mad_u16 (the compiler emits a shift and an add)
+                asm("v_pk_mad_u16 %0, %1, %2, %3" : "=v"(r) : "v"(c), "v"(k128), "v"(pb[i]));
+                pwp[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(i16x2, r), i16x2{0, 0}));
             }
             const op_t<VF> pb = __builtin_bit_cast(op_t<VF>, pw);
             const op_t<VF> v0 = decode8<VF>(cur.v[u][0], 0, 1.0f, tab);
