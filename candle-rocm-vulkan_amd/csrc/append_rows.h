@@ -1042,6 +1042,72 @@ __device__ inline void rope_query_rows16(const RopeAppendArgs &r, int g, int b, 
     }
 }
 
+// Query rows of the halves layout with 16-byte lanes (16-bit dtype, rows and tables 16-byte
+// aligned), the same head groups as rope_query_rows16 (64 / (D/8) heads): lane l holds elements
+// 8c..8c+7 and D/2 + 8c..+7 (c = l % (D/16)) of head g * (64 / (D/8)) + (l / (D/16)) % (64 / (D/8))
+// of token 2s + l / 32 of the pair s, so each pair of elements is in one lane (no exchange across
+// lanes) and a lane's 16-byte cos / sin chunks serve 16 outputs. A wave takes its 8 tokens as four
+// token pairs, every load issued before the first conversion. Products are rounded before the sum,
+// as in rope_query_rows16.
+template <int D>
+__device__ inline void rope_query_rows16h(const RopeAppendArgs &r, int g, int b, int bx, int wave,
+                                          int lane) {
+#pragma clang fp contract(off)
+    const AppendArgs &a = r.k;
+    constexpr int LPH = D / 16, RPW = 64 / (D / 8), HALF = D / 2;  // lanes per head, heads per group
+    static_assert(LPH * RPW == 32, "a token's heads of the group take half the wave");
+    const int pos = a.positions ? a.positions[b] : a.position;
+    if (pos < 0) return;
+    const int h = g * RPW + (lane / LPH) % RPW, c = lane % LPH, ts = lane >> 5;
+    const bool live = h < r.q_heads;
+    const int i_lo = (bx * 4 + wave) * 8, i_end = min(min(i_lo + 8, a.tokens), a.cs_rows - pos);
+    if (i_lo >= i_end) return;
+    const uint16_t *qp = (const uint16_t *)r.q + (int64_t)b * r.qsb + (int64_t)h * r.qsh + 8 * c;
+    uint16_t *op = (uint16_t *)r.q_out + (int64_t)b * r.osb + (int64_t)h * r.osh + 8 * c;
+    const bool bf = a.x_dtype == CQKV_BF16;
+    auto f32_of = [bf](uint32_t bits16) {
+        return bf ? bf16_bits_to_f32(bits16) : f16_bits_to_f32(bits16);
+    };
+    u32x4 xl[4], xh[4], cv[4], sv[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int i = i_lo + 2 * s + ts;
+        xl[s] = xh[s] = cv[s] = sv[s] = u32x4{0u, 0u, 0u, 0u};
+        if (i < i_end) {
+            const int64_t trow = (int64_t)(pos + i) * HALF + 8 * c;
+            cv[s] = *(const u32x4 *)((const uint16_t *)a.cos + trow);
+            sv[s] = *(const u32x4 *)((const uint16_t *)a.sin + trow);
+            if (live) {
+                xl[s] = *(const u32x4 *)(qp + (int64_t)i * r.qst);
+                xh[s] = *(const u32x4 *)(qp + (int64_t)i * r.qst + HALF);
+            }
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int i = i_lo + 2 * s + ts;
+        if (i >= i_end || !live) continue;
+        u32x4 ol, oh;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            float lo[2], hi[2];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const float cc = f32_of(k ? cv[s][w] >> 16 : cv[s][w] & 0xffffu);
+                const float ss = f32_of(k ? sv[s][w] >> 16 : sv[s][w] & 0xffffu);
+                const float x0 = f32_of(k ? xl[s][w] >> 16 : xl[s][w] & 0xffffu);
+                const float x1 = f32_of(k ? xh[s][w] >> 16 : xh[s][w] & 0xffffu);
+                lo[k] = x0 * cc - x1 * ss;
+                hi[k] = x0 * ss + x1 * cc;
+            }
+            ol[w] = bf ? pack_bf16x2(lo[0], lo[1]) : pack_f16x2(lo[0], lo[1]);
+            oh[w] = bf ? pack_bf16x2(hi[0], hi[1]) : pack_f16x2(hi[0], hi[1]);
+        }
+        *(u32x4 *)(op + (int64_t)i * r.ost) = ol;
+        *(u32x4 *)(op + (int64_t)i * r.ost + HALF) = oh;
+    }
+}
+
 // Blocks of 64 tokens: key and value planes by the row-parallel encoder (the keys rotated after
 // their load), query head groups as two 32-token halves.
 constexpr int kRopeBlockTokens = 64;
@@ -1062,7 +1128,10 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendArgs r) {
     } else {
 #pragma unroll
         for (int k = 0; k < 2; ++k) {  // rope_query_rows* cover 32 tokens per block index
-            if (LOAD != kRowF32 && r.q_vec16) rope_query_rows16<D, ROPE>(r, y - qy, b, 2 * bx + k, wave, lane);
+            if (LOAD != kRowF32 && r.q_vec16 && ROPE == CQKV_ROPE_HALVES)
+                rope_query_rows16h<D>(r, y - qy, b, 2 * bx + k, wave, lane);
+            else if (LOAD != kRowF32 && r.q_vec16)
+                rope_query_rows16<D, ROPE>(r, y - qy, b, 2 * bx + k, wave, lane);
             else rope_query_rows<D, ROPE, false>(r, y - qy, b, 2 * bx + k, wave, lane);
         }
     }
