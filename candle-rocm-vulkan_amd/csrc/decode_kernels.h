@@ -679,11 +679,12 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
         // once, its exponent fields biased by -127; block u then adds the two keys' codes to the
         // exponent fields (a byte permute, a packed multiply-add and a packed clamp per pair and
         // block): the bits of rounding p * 2^(c - 127) wherever that is a normal bf16 number.
-        // Results below the normal range clamp to zero. P is floored at 2^-100 (masked keys, exp
-        // underflow), so no zero p meets a large code; such a key's operand stays below 2^-100
-        // times the row's largest, and a column with no visible key is dropped by the rescale
-        // (alpha 0) or the epilogue (m -inf). Code 0 marks an all-zero block: its zero codes
-        // make any operand vanish.
+        // Results below the normal range clamp to zero. Masked keys (tiles across a range end)
+        // take code 0, and p floored at 2^-100 then clamps to exactly zero; the floor keeps a p
+        // that underflows in exp2 from meeting a large code, its operand then at most 2^-100 of
+        // its value where the row's largest p is at least 1. A column with no visible key is
+        // dropped by the rescale (alpha 0) or the epilogue (m -inf). Code 0 also marks an
+        // all-zero block: its zero codes make any operand vanish.
         typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
         typedef short i16x2 __attribute__((ext_vector_type(2)));
         uint32_t vw[8], vw2[8];
@@ -696,6 +697,11 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
 #pragma unroll
             for (int e = 0; e < 8; ++e)
                 if (e >= nv) vw[e] = vw2[e] = 0u;
+        }
+        if (!full) {  // uniform: masked keys take code 0, so their operands clamp to exactly 0
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (x[e] == -__builtin_inff()) vw[e] = vw2[e] = 0u;
         }
         u16x2 pb[4];  // bf16 P of keys 2i, 2i + 1, exponent fields minus 127
 #pragma unroll

@@ -196,6 +196,36 @@ def test_decode_multi_query_windows(cq, dev, fmt, wl, wr):
     assert_close_bf16(got, want)
 
 
+@pytest.mark.parametrize("splits", [1, 0])
+def test_decode_mxfp4_masked_keys_with_huge_value_scales(cq, dev, splits):
+    """Keys a window masks contribute nothing, whatever their value block scales. MXFP4 values
+    enter P by adding their E8M0 codes to P's exponent fields; keys 250-258 carry values of
+    magnitude 2^100 (codes near 227) and every other key 2^-20, and a causal window of 40 keys
+    leaves keys 257 and 258 visible to the first query, 258 to the second and neither to the
+    third. A masked key's operand has to be exactly zero here: any remnant of 2^100 weighed
+    against 2^-20 values would dominate the third query's output. Checked against the oracle
+    per output row, relative to the row's largest value."""
+    b, hq, hkv, d, ctx, lq = 1, 8, 2, 128, 300, 3
+    q = kv_source(11, (b, hq, lq, d))
+    k = kv_source(12, (b, hkv, ctx, d))
+    vf = kv_source(13, (b, hkv, ctx, d)).float() * 2.0 ** -20
+    vf[:, :, 250:259] *= 2.0 ** 120
+    v = vf.to(torch.bfloat16)
+    cache = cq.TurboKvCache(2, 2, b, hkv, d, ctx, device=dev)
+    cache.append(k.to(dev), v.to(dev))
+    scale = 1.0 / d ** 0.5
+    got = cq.decode_attention(q.to(dev), cache.k, cache.v, ctx, scale, window_left=40,
+                              window_right=0, splits=splits,
+                              out=torch.empty((b, hq, lq, d), dtype=torch.float32, device=dev))
+    torch.cuda.synchronize()
+    got = got.cpu().numpy()
+    want = oracle_decode(2, q, oracle_rows(2, k, 42), oracle_rows(2, v, 44), ctx, scale, wl=40, wr=0)
+    peak = np.abs(want).max(axis=-1, keepdims=True)
+    assert (peak[..., 2, :] < 1e-3).all() and (peak[..., 0, :] > 1e20).all()
+    ratio = (np.abs(got - want) / peak).max(axis=(0, 1, 3))  # per query
+    assert (ratio < 2e-2).all(), ratio
+
+
 def test_decode_f32_queries(cq, dev):
     """f32 queries (not bf16-representable) take the hi + lo query operands."""
     b, hq, hkv, d, ctx = 2, 8, 2, 128, 700
