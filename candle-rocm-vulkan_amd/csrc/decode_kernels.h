@@ -684,7 +684,9 @@ __device__ inline void compute_tile(Tile<KF, VF, D> &cur, int tile, const Decode
         // that underflows in exp2 from meeting a large code, its operand then at most 2^-100 of
         // its value where the row's largest p is at least 1. A column with no visible key is
         // dropped by the rescale (alpha 0) or the epilogue (m -inf). Code 0 also marks an
-        // all-zero block: its zero codes make any operand vanish.
+        // all-zero block: its zero codes make any operand vanish. Above the bf16 range (p 2^(c -
+        // 127) >= 2^128, blocks with |x| >= 2^122) the clamp gives zero too, where the
+        // reference's dequantized f32 values already overflow to infinity.
         typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
         typedef short i16x2 __attribute__((ext_vector_type(2)));
         uint32_t vw[8], vw2[8];
