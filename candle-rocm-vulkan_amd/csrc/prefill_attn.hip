@@ -857,7 +857,6 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
     // at D = 64)
     constexpr bool kFull = D == kPfD;
     __shared__ __attribute__((aligned(16))) uint32_t vtile[kPfBK * kStRow];
-    __shared__ __attribute__((aligned(16))) uint32_t ktile[kPfBK * kStRow];
     __shared__ float vscale[kPfBK], vrcp[kPfBK];
     const int kt = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x;
@@ -865,6 +864,7 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
     const int kv_len = sq.lk;  // this sequence's keys (the V^T row is zero-filled past them)
     const uint16_t *vplane = a.v + sq.v0 + (int64_t)hk * a.v_sh;
     const uint16_t *kplane = a.k + sq.k0 + (int64_t)hk * a.k_sh;
+    u32x4 vreg[D / 32], kreg[D / 32];  // every load of the tile is issued before the first use
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) {
         const int id = tid + 256 * i, row = id / CPR, c = id % CPR;
@@ -881,11 +881,55 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
                 w = *(const u32x4 *)(vplane + (int64_t)key * a.v_st + 8 * c);
             }
         }
-        *(u32x4 *)&vtile[row * kStRow + 4 * c] = w;
+        vreg[i] = w;
         if (kFull && a.append) {
             u32x4 wk = {0u, 0u, 0u, 0u};
             if (key < kv_len) wk = *(const u32x4 *)(kplane + (int64_t)key * a.k_st + 8 * c);
-            *(u32x4 *)&ktile[row * kStRow + 4 * c] = wk;
+            kreg[i] = wk;
+        }
+    }
+    const int64_t plane = (int64_t)b * a.kv_heads + hk;
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) {
+        const int id = tid + 256 * i, row = id / CPR, c = id % CPR;
+        *(u32x4 *)&vtile[row * kStRow + 4 * c] = vreg[i];
+        if (kFull && a.append) {
+            // ---- the row's scales from the CPR consecutive lanes that hold it, and its key
+            // codes straight from the registers (8 per lane, row-major) ----
+            const int t = kt * kPfBK + row;
+            const uint32_t kw[4] = {kreg[i].x, kreg[i].y, kreg[i].z, kreg[i].w};
+            const uint32_t vw[4] = {vreg[i].x, vreg[i].y, vreg[i].z, vreg[i].w};
+            float kmax = 0.0f, vmax = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                kmax = fmaxf(kmax, fmaxf(__builtin_fabsf(bf16_lo(kw[e])), __builtin_fabsf(bf16_hi(kw[e]))));
+                vmax = fmaxf(vmax, fmaxf(__builtin_fabsf(bf16_lo(vw[e])), __builtin_fabsf(bf16_hi(vw[e]))));
+            }
+#pragma unroll
+            for (int o = 1; o < CPR; o <<= 1) {
+                kmax = fmaxf(kmax, __shfl_xor(kmax, o, 64));
+                vmax = fmaxf(vmax, __shfl_xor(vmax, o, 64));
+            }
+            const float ksc = kmax > 0.0f ? kmax / 448.0f : 1.0f;
+            const float vsc = vmax > 0.0f ? vmax / 448.0f : 1.0f;
+            const bool live = t < kv_len;
+            if (c == 0) {
+                vscale[row] = vsc;
+                vrcp[row] = 1.0f / vsc;
+                if (live) {
+                    ((float *)(a.ks + plane * a.ks_plane))[a.position + t] = ksc;
+                    ((float *)(a.vs + plane * a.vs_plane))[a.position + t] = vsc;
+                }
+            }
+            if (live) {
+                const float kr = 1.0f / ksc;
+                u32x2 cw;
+                cw.x = fp8_row_codes(bf16_lo(kw[0]), bf16_hi(kw[0]), ksc, kr) |
+                       (fp8_row_codes(bf16_lo(kw[1]), bf16_hi(kw[1]), ksc, kr) << 16);
+                cw.y = fp8_row_codes(bf16_lo(kw[2]), bf16_hi(kw[2]), ksc, kr) |
+                       (fp8_row_codes(bf16_lo(kw[3]), bf16_hi(kw[3]), ksc, kr) << 16);
+                *(u32x2 *)(a.kc + plane * a.kc_plane + (int64_t)(a.position + t) * kPfD + 8 * c) = cw;
+            }
         }
     }
     __syncthreads();
@@ -906,48 +950,8 @@ __global__ __launch_bounds__(256) void prefill_stage_kernel(PrefillArgs a) {
         *(u32x4 *)(out + (int64_t)d * a.vt_len + kt * kPfBK + 8 * j) = u32x4{w[0], w[1], w[2], w[3]};
     }
     if (!kFull || !a.append) return;
-    const int64_t plane = (int64_t)b * a.kv_heads + hk;
-    // ---- per-token scales: 4 threads per token, 32 head dims each ----
-    const int r = tid >> 2, qd = tid & 3, t = kt * kPfBK + r;
-    const bool live = t < kv_len;
-    float kmax = 0.0f, vmax = 0.0f;
-#pragma unroll
-    for (int w = 0; w < 16; ++w) {
-        const uint32_t kw = ktile[r * kStRow + 16 * qd + w], vw = vtile[r * kStRow + 16 * qd + w];
-        kmax = fmaxf(kmax, fmaxf(__builtin_fabsf(bf16_lo(kw)), __builtin_fabsf(bf16_hi(kw))));
-        vmax = fmaxf(vmax, fmaxf(__builtin_fabsf(bf16_lo(vw)), __builtin_fabsf(bf16_hi(vw))));
-    }
-    kmax = fmaxf(kmax, __shfl_xor(kmax, 1, 64));
-    kmax = fmaxf(kmax, __shfl_xor(kmax, 2, 64));
-    vmax = fmaxf(vmax, __shfl_xor(vmax, 1, 64));
-    vmax = fmaxf(vmax, __shfl_xor(vmax, 2, 64));
-    const float ksc = kmax > 0.0f ? kmax / 448.0f : 1.0f;
-    const float vsc = vmax > 0.0f ? vmax / 448.0f : 1.0f;
-    if (qd == 0) {
-        vscale[r] = vsc;
-        vrcp[r] = 1.0f / vsc;
-        if (live) {
-            ((float *)(a.ks + plane * a.ks_plane))[a.position + t] = ksc;
-            ((float *)(a.vs + plane * a.vs_plane))[a.position + t] = vsc;
-        }
-    }
-    // ---- key codes: the thread's 32 dims of its token, row-major ----
-    if (live) {
-        const float kr = 1.0f / ksc;
-        uint32_t cw[8];
-#pragma unroll
-        for (int w = 0; w < 8; ++w) {
-            const uint32_t x01 = ktile[r * kStRow + 16 * qd + 2 * w];
-            const uint32_t x23 = ktile[r * kStRow + 16 * qd + 2 * w + 1];
-            cw[w] = fp8_row_codes(bf16_lo(x01), bf16_hi(x01), ksc, kr) |
-                    (fp8_row_codes(bf16_lo(x23), bf16_hi(x23), ksc, kr) << 16);
-        }
-        uint8_t *dst = a.kc + plane * a.kc_plane + (int64_t)(a.position + t) * kPfD + 32 * qd;
-        *(u32x4 *)dst = u32x4{cw[0], cw[1], cw[2], cw[3]};
-        *(u32x4 *)(dst + 16) = u32x4{cw[4], cw[5], cw[6], cw[7]};
-    }
-    __syncthreads();
-    // ---- value codes: thread (dim pair dp, groups g, g + 4) of 8 tokens, 8-token tiles ----
+    // ---- value codes: thread (dim pair dp, groups g, g + 4) of 8 tokens, 8-token tiles (the
+    // row scales were written before the barrier above) ----
     const int dp = tid & 63;
     uint8_t *vc = a.vc + plane * a.vc_plane;
 #pragma unroll
